@@ -1,0 +1,303 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 backend on the quantized projection path.
+
+A step is one pass of the small-lane GEMV sweep (gate/up shape N=8192,K=2048
+and down shape N=2048,K=8192, int4 group 32, M in {1,2,4,8} lanes of fp32
+activations, seed 0): eight products, each on its own copy of the weights,
+rotated through more copies than the 256 MiB Infinity Cache holds, so every
+byte is read from HBM.  `value` is the step's algorithmic bytes over its time.
+
+Beside it, on the same run: the decode GEMV alone (M=1, 8192x2048, the
+dominant kernel) against the HBM roofline, the batched prefill GEMM against
+the bf16/f16 MFMA peak, the decode attention over a 16384-position byte ring,
+and the reference's own CPU float path (oracle/_ref, AVX2+FMA build, the
+host's cores) on a bounded sample of the same sweep.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
+SHAPES = [(8192, 2048), (2048, 8192)]
+LANES = [1, 2, 4, 8]
+COPIES = 48                     # 48 x 10.5 MB per shape: past the 256 MiB MALL
+
+
+def gemv_bytes(N, K, M, group=32):
+    return N * K // 2 + N * (K // group) * 4 + M * (K + N) * 4
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    return ap.parse_args()
+
+
+class Rotation:
+    """COPIES device copies of one weight set, each bound as its own plane."""
+
+    def __init__(self, backend, N, K, seed=0):
+        from igllm_amd.backend import make_plane, synth_projection
+
+        codes, gains, _ = synth_projection(N, K, 1, seed=seed)
+        self.host = (codes, gains)
+        self.N, self.K = N, K
+        cbytes, gbytes = codes.nbytes, gains.nbytes
+        self.cstride = (cbytes + 255) // 256 * 256
+        self.gstride = (gbytes + 255) // 256 * 256
+        self.codes = backend.alloc(self.cstride * COPIES)
+        self.gains = backend.alloc(self.gstride * COPIES)
+        self.planes = []
+        for c in range(COPIES):
+            self.codes.put(codes, c * self.cstride)
+            self.gains.put(gains, c * self.gstride)
+            cp = make_plane(codes, gains, K)
+            backend.bind_dev(cp, self.codes, self.gains, c * self.cstride, c * self.gstride)
+            self.planes.append(cp)
+
+
+def cpu_baseline(budget_s=12.0):
+    """The reference's float back_mat_mat over the same sweep, on this host."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import ctypes
+    import oracle_lib as ol
+    from igllm_amd.backend import synth_projection
+
+    cores = min(16, os.cpu_count() or 1)
+    lib = ol.ref("tuned")
+    kind = "reference"
+    flags = ""
+    try:
+        flags = open("/proc/cpuinfo").read()
+    except OSError:
+        pass
+    if lib is None or " avx2" not in flags or " fma" not in flags:
+        lib, kind = None, "port"
+    cases = []
+    for (N, K) in SHAPES:
+        for M in LANES:
+            codes, gains, act = synth_projection(N, K, M, seed=0)
+            cases.append((N, K, M, codes, gains, act))
+    total_bytes = 0
+    t0 = time.perf_counter()
+    passes = 0
+    if kind == "reference":
+        desk = lib.ref_desk_open(cores, 256, 8192)
+        try:
+            while True:
+                for (N, K, M, codes, gains, act) in cases:
+                    d = ol.plane_desc(codes, gains, K)
+                    out = np.empty((M, N), dtype=np.float32)
+                    lib.ref_desk_mat_mat(desk, ctypes.byref(d), ol.p(act), K, M, ol.p(out), N)
+                    total_bytes += gemv_bytes(N, K, M)
+                passes += 1
+                if time.perf_counter() - t0 > budget_s:
+                    break
+        finally:
+            lib.ref_desk_close(desk)
+    else:
+        while True:
+            for (N, K, M, codes, gains, act) in cases:
+                ol.oracle_mat_mat(codes, gains, act, K, threads=cores)
+                total_bytes += gemv_bytes(N, K, M)
+            passes += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+    secs = time.perf_counter() - t0
+    model = ""
+    for line in flags.splitlines():
+        if line.startswith("model name"):
+            model = line.split(":", 1)[1].strip()
+            break
+    return {
+        "value": round(total_bytes / secs / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": kind,
+        "sample": f"{passes} passes of the 8-product sweep (both shapes, M=1,2,4,8), "
+                  f"{secs:.1f} s, {'ref back_mat_mat AVX2+FMA float path, pool' if kind == 'reference' else 'C restatement'}"
+                  f" of {cores} threads on {model}",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this backend runs on one GPU; multi-GPU sharding is "
+                                   "described in DESIGN.md, not built"}))
+        sys.exit(2)
+    from igllm_amd.backend import Backend, make_plane, synth_projection
+
+    be = Backend(device=0, sum_limit=256, col_limit=8192, lane_limit=16)
+    rot = {shape: Rotation(be, *shape) for shape in SHAPES}
+    acts = {}
+    outs = {}
+    for (N, K) in SHAPES:
+        for M in LANES:
+            _, _, act = synth_projection(N, K, M, seed=0)
+            acts[(N, K, M)] = be.upload(act)
+            outs[(N, K, M)] = be.alloc(M * N * 4)
+    step_bytes = sum(gemv_bytes(N, K, M) for (N, K) in SHAPES for M in LANES)
+
+    counter = [0]
+
+    def step():
+        for (N, K) in SHAPES:
+            r = rot[(N, K)]
+            for M in LANES:
+                cp = r.planes[counter[0] % COPIES]
+                counter[0] += 1
+                be.gemv_dev(cp, acts[(N, K, M)], K, M, outs[(N, K, M)], N)
+
+    for _ in range(args.warmup):
+        step()
+    be.sync()
+    be.mark()
+    for _ in range(args.steps):
+        step()
+    be.mark()
+    ms_total = be.marks_ms()
+    ms_per_step = ms_total / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # ---- dominant kernel: decode GEMV M=1, 8192 x 2048, on rotating copies.
+    N, K = SHAPES[0]
+    r = rot[(N, K)]
+    launches = 400
+    for i in range(20):
+        be.gemv_dev(r.planes[i % COPIES], acts[(N, K, 1)], K, 1, outs[(N, K, 1)], N)
+    be.sync()
+    be.mark()
+    for i in range(launches):
+        be.gemv_dev(r.planes[i % COPIES], acts[(N, K, 1)], K, 1, outs[(N, K, 1)], N)
+    be.mark()
+    gemv_us = be.marks_ms() * 1e3 / launches
+    gemv_algo = gemv_bytes(N, K, 1)
+    gemv_gbps = gemv_algo / (gemv_us * 1e-6) / 1e9
+
+    # ---- per-config GEMV rates (same rotation), for the record.
+    sweep = {}
+    for (N, K) in SHAPES:
+        for M in LANES:
+            rr = rot[(N, K)]
+            be.sync()
+            be.mark()
+            for i in range(100):
+                be.gemv_dev(rr.planes[i % COPIES], acts[(N, K, M)], K, M, outs[(N, K, M)], N)
+            be.mark()
+            us = be.marks_ms() * 1e3 / 100
+            sweep[f"{N}x{K}_M{M}"] = {"us": round(us, 3),
+                                      "GBps": round(gemv_bytes(N, K, M) / (us * 1e-6) / 1e9, 1)}
+
+    # ---- prefill GEMM, bf16 in/out, M = 2048 lanes (both shapes).
+    prefill = {}
+    for (N, K) in SHAPES:
+        M = 2048
+        a = be.alloc(M * K * 2)
+        c = be.alloc(M * N * 2)
+        rng = np.random.default_rng(0)
+        a.put((rng.normal(size=M * K).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))
+        cp = rot[(N, K)].planes[0]
+        for _ in range(3):
+            be.gemm_bf16_dev(cp, a, K, M, c, N)
+        be.sync()
+        be.mark()
+        reps = 20
+        for i in range(reps):
+            be.gemm_bf16_dev(rot[(N, K)].planes[i % COPIES], a, K, M, c, N)
+        be.mark()
+        us = be.marks_ms() * 1e3 / reps
+        tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        prefill[f"{N}x{K}_M{M}"] = {"us": round(us, 2), "TFLOPs": round(tflops, 1),
+                                    "frac_of_mfma_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+        a.free()
+        c.free()
+
+    # ---- decode attention, 8 q heads / 1 KV head / d=256, L=16384, int8 bytes.
+    L, head, rings = 16384, 256, 40
+    rng = np.random.default_rng(1)
+    ring_bytes = L * head
+    kb = be.alloc(ring_bytes * rings)
+    vb = be.alloc(ring_bytes * rings)
+    block = rng.integers(0, 256, size=ring_bytes, dtype=np.uint8)
+    for i in range(rings):
+        kb.put(block, i * ring_bytes)
+        vb.put(block[::-1].copy(), i * ring_bytes)
+    q = be.upload(rng.normal(size=(8, head)).astype(np.float32))
+    o = be.alloc(8 * head * 4)
+    lib, desk = be.lib, be.desk
+    import ctypes
+
+    def attend(i):
+        code = lib.igl_attend_dev(ctypes.byref(desk), kb.ptr + (i % rings) * ring_bytes,
+                                  vb.ptr + (i % rings) * ring_bytes, 1, 4.0 / 127, 4.0 / 127, L, 1,
+                                  8, head, q.ptr, 0, L, 1.0 / 16, o.ptr)
+        if code != 0:
+            raise RuntimeError(f"attend: {code}")
+
+    for i in range(5):
+        attend(i)
+    be.sync()
+    be.mark()
+    reps = 100
+    for i in range(reps):
+        attend(i)
+    be.mark()
+    att_us = be.marks_ms() * 1e3 / reps
+    att_bytes = 2 * L * head + 2 * 8 * head * 4
+    attention = {"L": L, "us": round(att_us, 2),
+                 "GBps": round(att_bytes / (att_us * 1e-6) / 1e9, 1),
+                 "frac_of_hbm_peak": round(att_bytes / (att_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                 "note": f"int8 K/V rings rotated over {rings} copies (past the MALL); "
+                         "includes the chunk-merge launch"}
+
+    cpu = None if args.no_cpu else cpu_baseline()
+
+    line = {
+        "metric": "decode tok/s + int4 GEMV HBM GB/s (% of peak) + prefill GEMM % MFMA, 1 GPU",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4xfp32",
+        "data": "synthetic (seeded splitmix64/xoshiro256**, int4 uniform -8..7, |N(0,0.02)| gains, "
+                "N(0,1) activations)",
+        "config": {"workload": "small-lane int4 g32 GEMV sweep: N=8192,K=2048 and N=2048,K=8192, "
+                               "M in {1,2,4,8}, fp32 activations, weights rotated over "
+                               f"{COPIES} copies per shape",
+                   "step_bytes": step_bytes},
+        "roofline": {"bound": "hbm", "kernel": "gemv_q4_kernel<1,4> 8192x2048 M=1",
+                     "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes": gemv_algo, "avg_launch_us": round(gemv_us, 3)},
+        "cpu_baseline": cpu,
+        "gemv_sweep": sweep,
+        "prefill_gemm": prefill,
+        "decode_attention": attention,
+        "decode_tok_s": None,
+    }
+    print(json.dumps(line))
+    be.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,646 @@
+/* back_hip.c - the C11 shim that fills igllm's backend table with the gfx950
+ * kernels.
+ *
+ * It owns what back_open owned on the CPU (app_core.c:5415-5443): the scratch
+ * a product needs, allocated once, so nothing is allocated in the token loop.
+ * Here that is device staging, a HIP stream (default priority), two timing
+ * events and the sticky error the void entries report through.  Every entry
+ * checks shapes, strides and alignment on the host before anything is
+ * launched; an entry that cannot run records IGL_FAIL_SUPPORT or
+ * IGL_FAIL_ARGUMENT and leaves its output unwritten.  There is no CPU path.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include "igl_backend.h"
+#include "igl_launch.h"
+
+#define IGL_GEMV_LANES 8  /* lanes one GEMV launch carries */
+#define IGL_GEMM_FLOOR 64 /* lanes from which mat_mat takes the MFMA GEMM */
+
+struct igl_device_plane {
+  const void  *codes;
+  const float *gains;
+  int          owned; /* allocated by igl_plane_attach */
+};
+
+struct igl_desk_state {
+  int         device;
+  hipStream_t stream;
+  hipEvent_t  mark[2];
+  int         mark_turn;
+  int         marks_made;
+  int         error;
+  int         lane_limit;
+  int         col_limit;
+  int         sum_limit;
+  int         lds_limit;  /* LDS bytes a workgroup may hold on this device */
+  /* device and pinned staging for the host-pointer table entries */
+  float *act_dev;
+  float *act_pin;
+  float *out_dev;
+  float *out_pin;
+  size_t out_floats;
+  /* GEMV K-chunk partials and attention split partials */
+  float *part_dev;
+  size_t part_floats;
+  float *work_dev;
+  size_t work_floats;
+  /* staging for the elementwise host entries */
+  float *elem_dev;
+  size_t elem_floats;
+};
+
+static void desk_fail(igl_desk_state *st, int code) {
+  if (st && st->error == IGL_OKAY) st->error = code;
+}
+
+static int hip_check(igl_desk_state *st, hipError_t e) {
+  if (e == hipSuccess) return IGL_OKAY;
+  desk_fail(st, e == hipErrorOutOfMemory ? IGL_FAIL_MEMORY : IGL_FAIL_DEVICE);
+  return e == hipErrorOutOfMemory ? IGL_FAIL_MEMORY : IGL_FAIL_DEVICE;
+}
+
+const char *igl_code_text(int code) {
+  switch (code) {
+    case IGL_OKAY: return "okay";
+    case IGL_FAIL_ARGUMENT: return "bad argument";
+    case IGL_FAIL_MEMORY: return "out of memory";
+    case IGL_FAIL_FILE: return "file error";
+    case IGL_FAIL_FORMAT: return "bad format";
+    case IGL_FAIL_MISSING: return "missing";
+    case IGL_FAIL_SUPPORT: return "unsupported by the gfx950 backend";
+    case IGL_FAIL_STATE: return "bad state";
+    case IGL_FAIL_DEVICE: return "device error";
+    default: return "unknown";
+  }
+}
+
+int igl_desk_error_take(igl_desk *desk) {
+  int code;
+  if (!desk || !desk->state) return IGL_FAIL_STATE;
+  code = desk->state->error;
+  desk->state->error = IGL_OKAY;
+  return code;
+}
+
+/* Grows a device buffer to at least `floats`; used only at load time or on
+ * the first call that needs more room. */
+static int grow_dev(igl_desk_state *st, float **buf, size_t *have, size_t floats) {
+  void *fresh = NULL;
+  if (*have >= floats) return IGL_OKAY;
+  if (hipMalloc(&fresh, floats * sizeof(float)) != hipSuccess) {
+    desk_fail(st, IGL_FAIL_MEMORY);
+    return IGL_FAIL_MEMORY;
+  }
+  if (*buf) (void)hipFree(*buf);
+  *buf = (float *)fresh;
+  *have = floats;
+  return IGL_OKAY;
+}
+
+static int grow_out(igl_desk_state *st, size_t floats) {
+  void *dev = NULL, *pin = NULL;
+  if (st->out_floats >= floats) return IGL_OKAY;
+  if (hipMalloc(&dev, floats * sizeof(float)) != hipSuccess) goto fail;
+  if (hipHostMalloc(&pin, floats * sizeof(float), hipHostMallocDefault) != hipSuccess) goto fail;
+  if (st->out_dev) (void)hipFree(st->out_dev);
+  if (st->out_pin) (void)hipHostFree(st->out_pin);
+  st->out_dev = (float *)dev;
+  st->out_pin = (float *)pin;
+  st->out_floats = floats;
+  return IGL_OKAY;
+fail:
+  if (dev) (void)hipFree(dev);
+  desk_fail(st, IGL_FAIL_MEMORY);
+  return IGL_FAIL_MEMORY;
+}
+
+/* ---- plane checks -------------------------------------------------------- */
+
+static int is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+/* The code planes the kernels take (the BASELINE int4 group-32 planes and
+ * their group-size relatives); everything else is refused, not emulated. */
+static int plane_supported(const igl_plane *sheet) {
+  if (!sheet || sheet->form != IGL_PLANE_CODE) return IGL_FAIL_SUPPORT;
+  if (sheet->bit_count != 4 || sheet->code_flip != 0 || sheet->bias_data) return IGL_FAIL_SUPPORT;
+  if (sheet->gain_type != IGL_STORE_F32) return IGL_FAIL_SUPPORT;
+  if (sheet->row_count < 1 || sheet->col_count < 32 || (sheet->col_count & 31)) return IGL_FAIL_SUPPORT;
+  if (sheet->group_size < 32 || (sheet->group_size & 31) || !is_pow2(sheet->group_size / 32))
+    return IGL_FAIL_SUPPORT;
+  if (sheet->group_count * sheet->group_size < sheet->col_count ||
+      (sheet->group_count - 1) * sheet->group_size >= sheet->col_count)
+    return IGL_FAIL_SUPPORT;
+  if ((sheet->row_stride & 15u) || sheet->row_stride < (size_t)sheet->col_count / 2u)
+    return IGL_FAIL_SUPPORT;
+  return IGL_OKAY;
+}
+
+/* Room the GEMV's K-chunk partials need for this plane, over every lane count
+ * a launch can carry. */
+static size_t plane_part_floats(const igl_desk_state *st, const igl_plane *sheet) {
+  size_t most = 0;
+  for (int lanes = 1; lanes <= IGL_GEMV_LANES; ++lanes) {
+    int cols = igl_gemv_chunk_cols(lanes, sheet->col_count, st->lds_limit);
+    size_t chunks = (size_t)((sheet->col_count + cols - 1) / cols);
+    size_t need = chunks > 1 ? chunks * (size_t)lanes * (size_t)sheet->row_count : 0;
+    if (need > most) most = need;
+  }
+  return most;
+}
+
+static int plane_reserve(igl_desk_state *st, const igl_plane *sheet) {
+  size_t part = plane_part_floats(st, sheet);
+  size_t out = (size_t)st->lane_limit * (size_t)sheet->row_count;
+  if (part && grow_dev(st, &st->part_dev, &st->part_floats, part) != IGL_OKAY) return IGL_FAIL_MEMORY;
+  return grow_out(st, out);
+}
+
+int igl_plane_attach(igl_desk *desk, igl_plane *sheet) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  igl_device_plane *dp;
+  size_t code_bytes, gain_bytes;
+  void *codes = NULL, *gains = NULL;
+  int code;
+  if (!st) return IGL_FAIL_STATE;
+  if ((code = plane_supported(sheet)) != IGL_OKAY) return code;
+  if (!sheet->code_data || !sheet->gain_data) return IGL_FAIL_ARGUMENT;
+  code_bytes = (size_t)sheet->row_count * sheet->row_stride;
+  gain_bytes = (size_t)sheet->row_count * (size_t)sheet->group_count * sizeof(float);
+  dp = (igl_device_plane *)calloc(1, sizeof(*dp));
+  if (!dp) return IGL_FAIL_MEMORY;
+  if (hipMalloc(&codes, code_bytes) != hipSuccess || hipMalloc(&gains, gain_bytes) != hipSuccess) {
+    if (codes) (void)hipFree(codes);
+    free(dp);
+    return IGL_FAIL_MEMORY;
+  }
+  if (hipMemcpy(codes, sheet->code_data, code_bytes, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(gains, sheet->gain_data, gain_bytes, hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipFree(codes);
+    (void)hipFree(gains);
+    free(dp);
+    return IGL_FAIL_DEVICE;
+  }
+  dp->codes = codes;
+  dp->gains = (const float *)gains;
+  dp->owned = 1;
+  if ((code = plane_reserve(st, sheet)) != IGL_OKAY) {
+    (void)hipFree(codes);
+    (void)hipFree(gains);
+    free(dp);
+    return code;
+  }
+  sheet->device = dp;
+  return IGL_OKAY;
+}
+
+int igl_plane_bind_dev(igl_desk *desk, igl_plane *sheet, const void *code_dev, const float *gain_dev) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  igl_device_plane *dp;
+  int code;
+  if (!st) return IGL_FAIL_STATE;
+  if ((code = plane_supported(sheet)) != IGL_OKAY) return code;
+  if (!code_dev || !gain_dev || ((uintptr_t)code_dev & 15u) || ((uintptr_t)gain_dev & 3u))
+    return IGL_FAIL_ARGUMENT;
+  dp = (igl_device_plane *)calloc(1, sizeof(*dp));
+  if (!dp) return IGL_FAIL_MEMORY;
+  dp->codes = code_dev;
+  dp->gains = gain_dev;
+  dp->owned = 0;
+  if ((code = plane_reserve(st, sheet)) != IGL_OKAY) {
+    free(dp);
+    return code;
+  }
+  sheet->device = dp;
+  return IGL_OKAY;
+}
+
+void igl_plane_detach(igl_desk *desk, igl_plane *sheet) {
+  igl_device_plane *dp;
+  (void)desk;
+  if (!sheet || !sheet->device) return;
+  dp = sheet->device;
+  if (dp->owned) {
+    (void)hipFree((void *)dp->codes);
+    (void)hipFree((void *)dp->gains);
+  }
+  free(dp);
+  sheet->device = NULL;
+}
+
+/* ---- device-resident projection ------------------------------------------ */
+
+static int check_lanes(const igl_plane *sheet, const void *act, int act_stride, int lanes,
+                       const void *out, int out_stride) {
+  if (!act || !out || lanes < 1) return IGL_FAIL_ARGUMENT;
+  if (lanes > 1 && (act_stride < sheet->col_count || out_stride < sheet->row_count))
+    return IGL_FAIL_ARGUMENT;
+  return IGL_OKAY;
+}
+
+int igl_gemv_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev, int act_stride,
+                 int lane_count, float *out_dev, int out_stride) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  const igl_device_plane *dp;
+  int code, done;
+  if (!st) return IGL_FAIL_STATE;
+  if ((code = plane_supported(sheet)) != IGL_OKAY || !sheet->device) {
+    code = code != IGL_OKAY ? code : IGL_FAIL_STATE;
+    desk_fail(st, code);
+    return code;
+  }
+  if ((code = check_lanes(sheet, act_dev, act_stride, lane_count, out_dev, out_stride)) != IGL_OKAY) {
+    desk_fail(st, code);
+    return code;
+  }
+  if (plane_part_floats(st, sheet) > st->part_floats) {
+    desk_fail(st, IGL_FAIL_STATE);
+    return IGL_FAIL_STATE;
+  }
+  dp = sheet->device;
+  for (done = 0; done < lane_count; done += IGL_GEMV_LANES) {
+    int lanes = lane_count - done < IGL_GEMV_LANES ? lane_count - done : IGL_GEMV_LANES;
+    hipError_t e = igl_launch_gemv_q4(
+        (const uint8_t *)dp->codes, (long long)sheet->row_stride, dp->gains, sheet->group_count,
+        sheet->group_size, sheet->code_bias, act_dev + (size_t)done * (size_t)act_stride,
+        act_stride, lanes, out_dev + (size_t)done * (size_t)out_stride, out_stride,
+        sheet->row_count, sheet->col_count, st->part_dev, st->lds_limit, st->stream);
+    if ((code = hip_check(st, e)) != IGL_OKAY) return code;
+  }
+  return IGL_OKAY;
+}
+
+static int gemm_run(igl_desk *desk, const igl_plane *sheet, const void *act_dev, int act_bf16,
+                    int act_stride, int lane_count, void *out_dev, int out_bf16, int out_stride) {
+  igl_desk_state *st = desk->state;
+  const igl_device_plane *dp = sheet->device;
+  const int align = act_bf16 ? 8 : 4;
+  int code;
+  if ((code = check_lanes(sheet, act_dev, act_stride, lane_count, out_dev, out_stride)) != IGL_OKAY ||
+      ((uintptr_t)act_dev & 15u) || (act_stride % align) ||
+      (lane_count == 1 && act_stride % align)) {
+    code = code != IGL_OKAY ? code : IGL_FAIL_ARGUMENT;
+    desk_fail(st, code);
+    return code;
+  }
+  return hip_check(st, igl_launch_gemm_q4(act_dev, act_bf16, act_stride, (const uint8_t *)dp->codes,
+                                          (long long)sheet->row_stride, dp->gains,
+                                          sheet->group_count, sheet->group_size, sheet->code_bias,
+                                          out_dev, out_bf16, out_stride, lane_count,
+                                          sheet->row_count, sheet->col_count, st->stream));
+}
+
+int igl_gemm_lane_floor(void) { return IGL_GEMM_FLOOR; }
+
+int igl_mat_mat_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev, int act_stride,
+                    int lane_count, float *out_dev, int out_stride) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  int code;
+  if (!st) return IGL_FAIL_STATE;
+  if (lane_count < IGL_GEMM_FLOOR)
+    return igl_gemv_dev(desk, sheet, act_dev, act_stride, lane_count, out_dev, out_stride);
+  if ((code = plane_supported(sheet)) != IGL_OKAY || !sheet->device) {
+    code = code != IGL_OKAY ? code : IGL_FAIL_STATE;
+    desk_fail(st, code);
+    return code;
+  }
+  return gemm_run(desk, sheet, act_dev, 0, act_stride, lane_count, out_dev, 0, out_stride);
+}
+
+int igl_gemm_bf16_dev(igl_desk *desk, const igl_plane *sheet, const uint16_t *act_dev,
+                      int act_stride, int lane_count, uint16_t *out_dev, int out_stride) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  int code;
+  if (!st) return IGL_FAIL_STATE;
+  if ((code = plane_supported(sheet)) != IGL_OKAY || !sheet->device) {
+    code = code != IGL_OKAY ? code : IGL_FAIL_STATE;
+    desk_fail(st, code);
+    return code;
+  }
+  return gemm_run(desk, sheet, act_dev, 1, act_stride, lane_count, out_dev, 1, out_stride);
+}
+
+/* ---- attention and cache ------------------------------------------------- */
+
+int igl_attend_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t *value_store,
+                   int format, float key_scale, float value_scale, int cache_span,
+                   int kv_count, int group_share, int head_size, const float *query_dev,
+                   int place_start, int span_count, float score_scale, float *blend_out_dev) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  size_t need;
+  int kv_width;
+  if (!st) return IGL_FAIL_STATE;
+  if (!key_store || !value_store || !query_dev || !blend_out_dev || kv_count < 1 ||
+      cache_span < 1 || span_count < 1 || span_count > cache_span || place_start < 0 ||
+      (format != IGL_CACHE_E4M3 && format != IGL_CACHE_INT8)) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return IGL_FAIL_ARGUMENT;
+  }
+  if ((head_size != 256 && head_size != 512) || group_share != 8) {
+    desk_fail(st, IGL_FAIL_SUPPORT);
+    return IGL_FAIL_SUPPORT;
+  }
+  kv_width = kv_count * head_size;
+  if (((uintptr_t)key_store & 15u) || ((uintptr_t)value_store & 15u)) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return IGL_FAIL_ARGUMENT;
+  }
+  need = igl_attend_work_floats(span_count, kv_count * group_share, head_size);
+  if (grow_dev(st, &st->work_dev, &st->work_floats, need) != IGL_OKAY) return IGL_FAIL_MEMORY;
+  return hip_check(st, igl_launch_attend(key_store, value_store, format, key_scale, value_scale,
+                                         cache_span, kv_width, kv_count, group_share, head_size,
+                                         query_dev, place_start, span_count, score_scale,
+                                         blend_out_dev, st->work_dev, st->stream));
+}
+
+int igl_cache_lay_dev(igl_desk *desk, const float *row_dev, int width, float scale, int format,
+                      uint8_t *store_dev, size_t slot_first) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  if (!row_dev || !store_dev || width < 1 || !(scale > 0.0f) ||
+      (format != IGL_CACHE_E4M3 && format != IGL_CACHE_INT8)) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return IGL_FAIL_ARGUMENT;
+  }
+  return hip_check(st, igl_launch_cache_lay(row_dev, width, scale, format, store_dev, slot_first,
+                                            st->stream));
+}
+
+int igl_norm_rms_dev(igl_desk *desk, const float *in_dev, const float *gain_dev, int n, int rows,
+                     int stride, float eps, float *out_dev) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  if (!in_dev || !out_dev || n < 1 || rows < 1 || (rows > 1 && stride < n)) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return IGL_FAIL_ARGUMENT;
+  }
+  return hip_check(st, igl_launch_norm_rms(in_dev, gain_dev, n, rows, stride, eps, out_dev, st->stream));
+}
+
+int igl_soft_max_dev(igl_desk *desk, float *v_dev, int n, int rows, int stride) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  if (!v_dev || n < 1 || rows < 1 || (rows > 1 && stride < n)) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return IGL_FAIL_ARGUMENT;
+  }
+  return hip_check(st, igl_launch_soft_max(v_dev, n, rows, stride, st->stream));
+}
+
+int igl_gelu_gate_dev(igl_desk *desk, float *gate_dev, const float *rise_dev, int n) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  if (!gate_dev || !rise_dev || n < 1) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return IGL_FAIL_ARGUMENT;
+  }
+  return hip_check(st, igl_launch_gelu_gate(gate_dev, rise_dev, n, st->stream));
+}
+
+int igl_rope_turn_dev(igl_desk *desk, float *v_dev, int heads, int head_size, const float *cos_dev,
+                      const float *sin_dev) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  if (!v_dev || !cos_dev || !sin_dev || heads < 1 || head_size < 2 || (head_size & 1)) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return IGL_FAIL_ARGUMENT;
+  }
+  return hip_check(st, igl_launch_rope_turn(v_dev, heads, head_size, cos_dev, sin_dev, st->stream));
+}
+
+/* ---- the table entries (host pointers, synchronous) ---------------------- */
+
+static void table_mat_mat(igl_desk *desk, const igl_plane *sheet, const float *act_data,
+                          int act_stride, int lane_count, float *out_data, int out_stride) {
+  igl_desk_state *st = desk->state;
+  int done = 0;
+  if (!sheet || !sheet->device || !act_data || !out_data || lane_count < 1) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return;
+  }
+  if (lane_count == 1) act_stride = sheet->col_count, out_stride = sheet->row_count;
+  if (sheet->col_count > st->col_limit || (size_t)sheet->row_count * st->lane_limit > st->out_floats) {
+    desk_fail(st, IGL_FAIL_STATE);
+    return;
+  }
+  while (done < lane_count) {
+    int lanes = lane_count - done < st->lane_limit ? lane_count - done : st->lane_limit;
+    size_t K = (size_t)sheet->col_count, N = (size_t)sheet->row_count;
+    if (hip_check(st, hipMemcpy2DAsync(st->act_dev, K * sizeof(float),
+                                       act_data + (size_t)done * (size_t)act_stride,
+                                       (size_t)act_stride * sizeof(float), K * sizeof(float),
+                                       (size_t)lanes, hipMemcpyHostToDevice, st->stream)) != IGL_OKAY)
+      return;
+    if (igl_mat_mat_dev(desk, sheet, st->act_dev, (int)K, lanes, st->out_dev, (int)N) != IGL_OKAY)
+      return;
+    if (hip_check(st, hipMemcpy2DAsync(out_data + (size_t)done * (size_t)out_stride,
+                                       (size_t)out_stride * sizeof(float), st->out_dev,
+                                       N * sizeof(float), N * sizeof(float), (size_t)lanes,
+                                       hipMemcpyDeviceToHost, st->stream)) != IGL_OKAY)
+      return;
+    if (hip_check(st, hipStreamSynchronize(st->stream)) != IGL_OKAY) return;
+    done += lanes;
+  }
+}
+
+static void table_mat_vec(igl_desk *desk, const igl_plane *sheet, const float *act_data,
+                          float *out_data) {
+  table_mat_mat(desk, sheet, act_data, 0, 1, out_data, 0);
+}
+
+/* The elementwise entries stage their vectors through the device. */
+static float *elem_stage(igl_desk_state *st, size_t floats) {
+  if (grow_dev(st, &st->elem_dev, &st->elem_floats, floats) != IGL_OKAY) return NULL;
+  return st->elem_dev;
+}
+
+static int elem_put(igl_desk_state *st, float *dst, const float *src, int n) {
+  return hip_check(st, hipMemcpyAsync(dst, src, (size_t)n * sizeof(float), hipMemcpyHostToDevice,
+                                      st->stream));
+}
+
+static void elem_get(igl_desk_state *st, float *dst, const float *src, int n) {
+  if (hip_check(st, hipMemcpyAsync(dst, src, (size_t)n * sizeof(float), hipMemcpyDeviceToHost,
+                                   st->stream)) == IGL_OKAY)
+    (void)hip_check(st, hipStreamSynchronize(st->stream));
+}
+
+static void table_norm_rms(igl_desk *desk, const float *value_list, const float *gain_list,
+                           int value_count, float eps_value, float *value_out) {
+  igl_desk_state *st = desk->state;
+  float *room = elem_stage(st, 3 * (size_t)value_count);
+  if (!room || value_count < 1) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return;
+  }
+  if (elem_put(st, room, value_list, value_count) != IGL_OKAY) return;
+  if (gain_list && elem_put(st, room + value_count, gain_list, value_count) != IGL_OKAY) return;
+  if (igl_norm_rms_dev(desk, room, gain_list ? room + value_count : NULL, value_count, 1,
+                       value_count, eps_value, room + 2 * (size_t)value_count) != IGL_OKAY)
+    return;
+  elem_get(st, value_out, room + 2 * (size_t)value_count, value_count);
+}
+
+static void table_soft_max(igl_desk *desk, float *value_list, int value_count) {
+  igl_desk_state *st = desk->state;
+  float *room = elem_stage(st, (size_t)value_count);
+  if (!room || value_count < 1) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return;
+  }
+  if (elem_put(st, room, value_list, value_count) != IGL_OKAY) return;
+  if (igl_soft_max_dev(desk, room, value_count, 1, value_count) != IGL_OKAY) return;
+  elem_get(st, value_list, room, value_count);
+}
+
+static void table_gelu_gate(igl_desk *desk, float *gate_list, const float *rise_list,
+                            int value_count) {
+  igl_desk_state *st = desk->state;
+  float *room = elem_stage(st, 2 * (size_t)value_count);
+  if (!room || value_count < 1) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return;
+  }
+  if (elem_put(st, room, gate_list, value_count) != IGL_OKAY) return;
+  if (elem_put(st, room + value_count, rise_list, value_count) != IGL_OKAY) return;
+  if (igl_gelu_gate_dev(desk, room, room + value_count, value_count) != IGL_OKAY) return;
+  elem_get(st, gate_list, room, value_count);
+}
+
+static void table_rope_turn(igl_desk *desk, float *value_list, int head_size, const float *cos_list,
+                            const float *sin_list) {
+  igl_desk_state *st = desk->state;
+  int half = head_size / 2;
+  float *room = elem_stage(st, 2 * (size_t)head_size);
+  if (!room || head_size < 2) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return;
+  }
+  if (elem_put(st, room, value_list, head_size) != IGL_OKAY) return;
+  if (elem_put(st, room + head_size, cos_list, half) != IGL_OKAY) return;
+  if (elem_put(st, room + head_size + half, sin_list, half) != IGL_OKAY) return;
+  if (igl_rope_turn_dev(desk, room, 1, head_size, room + head_size, room + head_size + half) != IGL_OKAY)
+    return;
+  elem_get(st, value_list, room, head_size);
+}
+
+/* ---- open / close --------------------------------------------------------- */
+
+int igl_back_open(igl_desk *desk, int device_index, int sum_limit, int col_limit, int lane_limit) {
+  igl_desk_state *st;
+  int count = 0;
+  if (!desk) return IGL_FAIL_ARGUMENT;
+  memset(desk, 0, sizeof(*desk));
+  if (hipGetDeviceCount(&count) != hipSuccess || count < 1) return IGL_FAIL_DEVICE;
+  if (device_index < 0 || device_index >= count) return IGL_FAIL_ARGUMENT;
+  if (hipSetDevice(device_index) != hipSuccess) return IGL_FAIL_DEVICE;
+  st = (igl_desk_state *)calloc(1, sizeof(*st));
+  if (!st) return IGL_FAIL_MEMORY;
+  st->device = device_index;
+  st->lane_limit = lane_limit > 0 ? lane_limit : 16;
+  st->col_limit = col_limit > 0 ? col_limit : 1;
+  st->sum_limit = sum_limit > 0 ? sum_limit : 1;
+  if (hipDeviceGetAttribute(&st->lds_limit, hipDeviceAttributeMaxSharedMemoryPerBlock,
+                            device_index) != hipSuccess || st->lds_limit < 16384)
+    st->lds_limit = 65536;
+  if (hipStreamCreateWithFlags(&st->stream, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreate(&st->mark[0]) != hipSuccess || hipEventCreate(&st->mark[1]) != hipSuccess ||
+      hipMalloc((void **)&st->act_dev, (size_t)st->lane_limit * st->col_limit * sizeof(float)) != hipSuccess ||
+      hipHostMalloc((void **)&st->act_pin, (size_t)st->lane_limit * st->col_limit * sizeof(float),
+                    hipHostMallocDefault) != hipSuccess) {
+    desk->state = st;
+    igl_back_close(desk);
+    return IGL_FAIL_DEVICE;
+  }
+  desk->state = st;
+  desk->name_text = "hip/gfx950";
+  desk->mat_vec = table_mat_vec;
+  desk->mat_mat = table_mat_mat;
+  desk->norm_rms = table_norm_rms;
+  desk->soft_max = table_soft_max;
+  desk->gelu_gate = table_gelu_gate;
+  desk->rope_turn = table_rope_turn;
+  return IGL_OKAY;
+}
+
+void igl_back_close(igl_desk *desk) {
+  igl_desk_state *st;
+  if (!desk || !desk->state) return;
+  st = desk->state;
+  if (st->stream) (void)hipStreamSynchronize(st->stream);
+  if (st->act_dev) (void)hipFree(st->act_dev);
+  if (st->act_pin) (void)hipHostFree(st->act_pin);
+  if (st->out_dev) (void)hipFree(st->out_dev);
+  if (st->out_pin) (void)hipHostFree(st->out_pin);
+  if (st->part_dev) (void)hipFree(st->part_dev);
+  if (st->work_dev) (void)hipFree(st->work_dev);
+  if (st->elem_dev) (void)hipFree(st->elem_dev);
+  if (st->mark[0]) (void)hipEventDestroy(st->mark[0]);
+  if (st->mark[1]) (void)hipEventDestroy(st->mark[1]);
+  if (st->stream) (void)hipStreamDestroy(st->stream);
+  free(st);
+  memset(desk, 0, sizeof(*desk));
+}
+
+/* ---- plumbing ------------------------------------------------------------ */
+
+void *igl_dev_alloc(igl_desk *desk, size_t bytes) {
+  void *p = NULL;
+  (void)desk;
+  if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) return NULL;
+  return p;
+}
+
+void igl_dev_free(igl_desk *desk, void *ptr) {
+  (void)desk;
+  if (ptr) (void)hipFree(ptr);
+}
+
+int igl_copy_to_dev(igl_desk *desk, void *dst_dev, const void *src_host, size_t bytes) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  if (hip_check(st, hipMemcpyAsync(dst_dev, src_host, bytes, hipMemcpyHostToDevice, st->stream)) != IGL_OKAY)
+    return IGL_FAIL_DEVICE;
+  return hip_check(st, hipStreamSynchronize(st->stream));
+}
+
+int igl_copy_to_host(igl_desk *desk, void *dst_host, const void *src_dev, size_t bytes) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  if (hip_check(st, hipMemcpyAsync(dst_host, src_dev, bytes, hipMemcpyDeviceToHost, st->stream)) != IGL_OKAY)
+    return IGL_FAIL_DEVICE;
+  return hip_check(st, hipStreamSynchronize(st->stream));
+}
+
+int igl_fill_dev(igl_desk *desk, void *dst_dev, int byte_value, size_t bytes) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  return hip_check(st, hipMemsetAsync(dst_dev, byte_value, bytes, st->stream));
+}
+
+int igl_sync(igl_desk *desk) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  return hip_check(st, hipStreamSynchronize(st->stream));
+}
+
+int igl_mark(igl_desk *desk) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  st->mark_turn ^= 1;
+  st->marks_made += 1;
+  return hip_check(st, hipEventRecord(st->mark[st->mark_turn], st->stream));
+}
+
+float igl_marks_ms(igl_desk *desk) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  float ms = -1.0f;
+  if (!st || st->marks_made < 2) return -1.0f;
+  if (hip_check(st, hipEventSynchronize(st->mark[st->mark_turn])) != IGL_OKAY) return -1.0f;
+  if (hip_check(st, hipEventElapsedTime(&ms, st->mark[st->mark_turn ^ 1], st->mark[st->mark_turn])) != IGL_OKAY)
+    return -1.0f;
+  return ms;
+}

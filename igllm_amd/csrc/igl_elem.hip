@@ -1,0 +1,172 @@
+// igl_elem.hip - the backend table's elementwise entries and the cache
+// writer, gfx950.
+//
+// These are the entries of back_desk that are not projections (norm_rms,
+// soft_max, gelu_gate, rope_turn; app_core.c:5223-5245) plus the key/value
+// ring writer that the reference keeps outside the table (cache_lay,
+// app_core.c:11205-11236).  They read no weights; each is one small launch.
+#include "igl_device.h"
+
+namespace igl {
+
+// RMS norm of one vector per workgroup: sum of squares in double (the
+// reference accumulates in double, kern_norm_rms app_core.c:4667-4684), then
+// x * (mean + eps)^-1/2 * gain.
+__global__ void norm_rms_kernel(const float *in, const float *gain, int n, int stride, float eps,
+                                float *out) {
+  __shared__ double part[256];
+  const float *x = in + (size_t)blockIdx.x * stride;
+  float *y = out + (size_t)blockIdx.x * stride;
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) acc += (double)x[i] * (double)x[i];
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+    __syncthreads();
+  }
+  const float shrink = (float)pow(part[0] / (double)n + (double)eps, -0.5);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const float v = x[i] * shrink;
+    y[i] = gain ? v * gain[i] : v;
+  }
+}
+
+// Softmax of one vector per workgroup: peak, e^(v - peak), total, scale.
+__global__ void soft_max_kernel(float *v, int n, int stride) {
+  __shared__ float part[256];
+  float *x = v + (size_t)blockIdx.x * stride;
+  float peak = -INFINITY;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) peak = fmaxf(peak, x[i]);
+  part[threadIdx.x] = peak;
+  __syncthreads();
+  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) part[threadIdx.x] = fmaxf(part[threadIdx.x], part[threadIdx.x + w]);
+    __syncthreads();
+  }
+  peak = part[0];
+  __syncthreads();
+  float total = 0.0f;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const float e = __expf(x[i] - peak);
+    x[i] = e;
+    total += e;
+  }
+  part[threadIdx.x] = total;
+  __syncthreads();
+  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+    __syncthreads();
+  }
+  const float shrink = part[0] > 0.0f ? 1.0f / part[0] : 0.0f;
+  if (part[0] > 0.0f)
+    for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] *= shrink;
+}
+
+// gate <- gelu_tanh(gate) * rise, with gelu_tanh(x) = x t / (t + 1),
+// t = e^(2 sqrt(2/pi) (x + 0.044715 x^3)), zero where 2y <= -30 and t
+// clamped at 2y = 30 (kern_gelu_tanh, app_core.c:5105-5118).
+__global__ void gelu_gate_kernel(float *gate, const float *rise, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float x = gate[i];
+  const float turn = 2.0f * 0.7978845608028654f * (x + 0.044715f * (x * x * x));
+  float g;
+  if (!(turn > -30.0f)) {
+    g = x * 0.0f;
+  } else {
+    const float t = __expf(fminf(turn, 30.0f));
+    g = x * (t / (t + 1.0f));
+  }
+  gate[i] = g * rise[i];
+}
+
+// Rotate-half RoPE on `heads` heads of `head_size` (kern_rope_turn,
+// app_core.c:5196-5207).
+__global__ void rope_turn_kernel(float *v, int heads, int head_size, const float *cosv,
+                                 const float *sinv) {
+  const int half = head_size / 2;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= heads * half) return;
+  const int h = i / half;
+  const int j = i - h * half;
+  float *x = v + (size_t)h * head_size;
+  const float lo = x[j], hi = x[j + half];
+  x[j] = lo * cosv[j] - hi * sinv[j];
+  x[j + half] = hi * cosv[j] + lo * sinv[j];
+}
+
+// e4m3 grid rounding of value/scale: nearest, ties to even, saturating at
+// +-448; below 2^-6 steps of 2^-9 (cache_pack8/cache_code8,
+// app_core.c:10980-11016).
+__device__ __forceinline__ uint8_t code8(float value) {
+  const float top = 448.0f, norm = 1.0f / 64.0f, step = 1.0f / 512.0f;
+  uint8_t sign = 0;
+  float mag = value;
+  if (value < 0.0f) { sign = 0x80u; mag = -value; }
+  if (!(mag < top)) return (uint8_t)(sign | 0x7Eu);  // 448 (and NaN) saturate
+  if (mag < norm) {
+    const float lv = __builtin_rintf(mag / step);
+    if (lv == 0.0f) return 0x00u;  // a negative that rounds to zero is stored as +0
+    if (lv >= 8.0f) return (uint8_t)(sign | 0x08u);  // rounded up to 2^-6
+    return (uint8_t)(sign | (uint8_t)lv);
+  }
+  int power;
+  (void)frexpf(mag, &power);  // mag in [2^(power-1), 2^power)
+  const float unit = ldexpf(1.0f, power - 4);
+  float r = __builtin_rintf(mag / unit) * unit;
+  if (r > top) r = top;
+  (void)frexpf(r, &power);
+  const int mant = (int)(ldexpf(r, 4 - power) + 0.5f) - 8;
+  return (uint8_t)(sign | (uint8_t)((power + 6) << 3) | (uint8_t)mant);
+}
+
+__device__ __forceinline__ uint8_t code_i8(float value, float scale) {
+  float level = __builtin_rintf(value / scale);
+  if (!(level > -127.0f)) level = -127.0f;
+  if (level > 127.0f) level = 127.0f;
+  return (uint8_t)(int8_t)level;
+}
+
+// Writes `width` values of `row` into ring slot `slot` of a byte store.
+__global__ void cache_lay_kernel(const float *row, int width, float scale, int fmt, uint8_t *store,
+                                 size_t slot_first) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= width) return;
+  store[slot_first + i] = fmt == 0 ? code8(row[i] / scale) : code_i8(row[i], scale);
+}
+
+}  // namespace igl
+
+using namespace igl;
+
+extern "C" hipError_t igl_launch_norm_rms(const float *in, const float *gain, int n, int rows,
+                                          int stride, float eps, float *out, hipStream_t stream) {
+  hipLaunchKernelGGL(norm_rms_kernel, dim3(rows), dim3(256), 0, stream, in, gain, n, stride, eps, out);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_soft_max(float *v, int n, int rows, int stride, hipStream_t stream) {
+  hipLaunchKernelGGL(soft_max_kernel, dim3(rows), dim3(256), 0, stream, v, n, stride);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_gelu_gate(float *gate, const float *rise, int n, hipStream_t stream) {
+  hipLaunchKernelGGL(gelu_gate_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, gate, rise, n);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_rope_turn(float *v, int heads, int head_size, const float *cosv,
+                                           const float *sinv, hipStream_t stream) {
+  const int total = heads * (head_size / 2);
+  hipLaunchKernelGGL(rope_turn_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, v, heads,
+                     head_size, cosv, sinv);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_cache_lay(const float *row, int width, float scale, int fmt,
+                                           uint8_t *store, size_t slot_first, hipStream_t stream) {
+  hipLaunchKernelGGL(cache_lay_kernel, dim3((width + 255) / 256), dim3(256), 0, stream, row, width,
+                     scale, fmt, store, slot_first);
+  return hipGetLastError();
+}

@@ -1,0 +1,48 @@
+/* igl_launch.h - launchers the HIP kernel files export to the C11 shim.
+ * Each returns the launch's hipError_t; none validates its arguments (the shim
+ * does, before calling). */
+#ifndef IGL_LAUNCH_H
+#define IGL_LAUNCH_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int igl_gemv_rows_per_tile(int lanes);
+int igl_gemv_chunk_cols(int lanes, int K, int lds_limit);
+hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_stride, const float *gains,
+                              int gain_stride, int group_size, int code_bias, const float *act,
+                              int act_stride, int lanes, float *out, int out_stride, int N, int K,
+                              float *part, int lds_limit, hipStream_t stream);
+
+hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride, const uint8_t *codes,
+                              long long row_stride, const float *gains, int gain_stride,
+                              int group_size, int code_bias, void *out, int out_bf16,
+                              int out_stride, int M, int N, int K, hipStream_t stream);
+
+int igl_attend_chunk_size(void);
+size_t igl_attend_work_floats(int span_count, int head_count, int head_size);
+hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t *value_store, int fmt,
+                             float key_scale, float value_scale, int cache_span, int kv_width,
+                             int kv_count, int group_share, int head_size, const float *query,
+                             int place_start, int span_count, float score_scale, float *blend_out,
+                             float *work, hipStream_t stream);
+
+hipError_t igl_launch_norm_rms(const float *in, const float *gain, int n, int rows, int stride,
+                               float eps, float *out, hipStream_t stream);
+hipError_t igl_launch_soft_max(float *v, int n, int rows, int stride, hipStream_t stream);
+hipError_t igl_launch_gelu_gate(float *gate, const float *rise, int n, hipStream_t stream);
+hipError_t igl_launch_rope_turn(float *v, int heads, int head_size, const float *cosv,
+                                const float *sinv, hipStream_t stream);
+hipError_t igl_launch_cache_lay(const float *row, int width, float scale, int fmt, uint8_t *store,
+                                size_t slot_first, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,213 @@
+/* igl_backend.h - C ABI of the MI355X (gfx950) backend for igllm's quantized
+ * projection path.
+ *
+ * The reference engine reaches every projection through `back_desk`, a table
+ * of function pointers filled by `back_open` (app_core.c:5223-5245,
+ * 5415-5443).  This header is that table's drop-in: the same six entries with
+ * the same signatures and meanings, filled by `igl_back_open`, plus the pieces
+ * the reference names as missing for an accelerator (GUIDE.md:567-577,
+ * TODO.md:134-137): a device buffer handle beside each plane, device-resident
+ * forms of the entries, a decode-attention entry and a cache writer, and a
+ * sticky error, because the table's entries return void and must not fail
+ * (app_core.c:5236-5244).
+ *
+ * Plain C11: pointers, sizes and enums only.  Two groups of entries:
+ *   - the table entries take host pointers, exactly as the reference's do, and
+ *     stage through the device (synchronous: the result is in `out` on return);
+ *   - the `_dev` entries take device pointers, enqueue on the desk's stream
+ *     and return at once; `igl_sync` waits.
+ * Results of an entry that fails are left unwritten and the error is kept in
+ * the desk until `igl_desk_error_take` reads it.
+ */
+#ifndef IGL_BACKEND_H
+#define IGL_BACKEND_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Result codes: the reference's `app_code` values (app_core.c:40-49), plus one
+ * for a failure the device itself reported. */
+typedef enum igl_code {
+  IGL_OKAY = 0,
+  IGL_FAIL_ARGUMENT = -1,
+  IGL_FAIL_MEMORY = -2,
+  IGL_FAIL_FILE = -3,
+  IGL_FAIL_FORMAT = -4,
+  IGL_FAIL_MISSING = -5,
+  IGL_FAIL_SUPPORT = -6,
+  IGL_FAIL_STATE = -7,
+  IGL_FAIL_DEVICE = -8
+} igl_code;
+
+/* `store_type` (app_core.c:1412-1424), same values. */
+typedef enum igl_store_type {
+  IGL_STORE_VOID = 0,
+  IGL_STORE_F32,
+  IGL_STORE_F16,
+  IGL_STORE_BF16,
+  IGL_STORE_F64,
+  IGL_STORE_I8,
+  IGL_STORE_U8,
+  IGL_STORE_I16,
+  IGL_STORE_I32,
+  IGL_STORE_I64,
+  IGL_STORE_BOOL
+} igl_store_type;
+
+/* `plane_form` (app_core.c:1772), same values. */
+typedef enum igl_plane_form { IGL_PLANE_VOID = 0, IGL_PLANE_REAL, IGL_PLANE_CODE } igl_plane_form;
+
+typedef struct igl_device_plane igl_device_plane;
+
+/* A weight, field for field the reference's `plane` (app_core.c:1775-1795),
+ * with the device handle `igl_plane_attach` sets beside it.  The code bytes
+ * are the checkpoint's own rows (`row_stride` bytes apart, a dense
+ * little-endian bit stream, low field first); nothing is repacked. */
+typedef struct igl_plane {
+  int            form;        /* igl_plane_form */
+  int            row_count;   /* N, output features */
+  int            col_count;   /* K, input features */
+  const void    *real_data;
+  int            real_type;   /* igl_store_type */
+  const uint8_t *code_data;
+  size_t         row_stride;
+  const void    *gain_data;   /* [row_count * group_count] */
+  int            gain_type;   /* igl_store_type; F32 is supported */
+  const int8_t  *bias_data;   /* zero points, NULL when symmetric */
+  int            bit_count;
+  int            code_bias;
+  int            code_flip;
+  int            group_size;
+  int            group_count;
+  float          enter_gain;
+  float          leave_gain;
+  void          *own_block;
+  igl_device_plane *device;   /* set by igl_plane_attach / igl_plane_bind_dev */
+} igl_plane;
+
+typedef struct igl_desk_state igl_desk_state;
+
+/* The backend table: `back_desk`'s entries (app_core.c:5236-5244) with the
+ * same argument meanings.  `state` replaces the reference's CPU scratch. */
+typedef struct igl_desk {
+  const char     *name_text;
+  igl_desk_state *state;
+  void (*mat_vec)(struct igl_desk *desk, const igl_plane *sheet, const float *act_data,
+                  float *out_data);
+  void (*mat_mat)(struct igl_desk *desk, const igl_plane *sheet, const float *act_data,
+                  int act_stride, int lane_count, float *out_data, int out_stride);
+  void (*norm_rms)(struct igl_desk *desk, const float *value_list, const float *gain_list,
+                   int value_count, float eps_value, float *value_out);
+  void (*soft_max)(struct igl_desk *desk, float *value_list, int value_count);
+  void (*gelu_gate)(struct igl_desk *desk, float *gate_list, const float *rise_list,
+                    int value_count);
+  void (*rope_turn)(struct igl_desk *desk, float *value_list, int head_size,
+                    const float *cos_list, const float *sin_list);
+} igl_desk;
+
+/* ---- opening and closing ------------------------------------------------ */
+
+/* Replaces back_open (app_core.c:5415-5443).  `sum_limit` and `col_limit` are
+ * the widest group count and column count the model binds, as the reference
+ * passes them (app_core.c:12585); `lane_limit` sizes the host staging (0
+ * selects the reference's 16, KERN_LANE_LIMIT app_core.c:1980).  Allocates
+ * everything the token loop needs, on device `device_index`. */
+int  igl_back_open(igl_desk *desk, int device_index, int sum_limit, int col_limit, int lane_limit);
+/* Replaces back_close (app_core.c:5445-5453). */
+void igl_back_close(igl_desk *desk);
+
+/* The first failure since the last call, and clears it (IGL_OKAY if none). */
+int  igl_desk_error_take(igl_desk *desk);
+const char *igl_code_text(int code);
+
+/* ---- weights ------------------------------------------------------------ */
+
+/* Copies a code plane's bytes and gains to the device unchanged and sets
+ * `sheet->device`.  Supported: 4-bit codes, code_flip 0, F32 gains, no zero
+ * points, group_size a power-of-two multiple of 32, col_count a multiple of
+ * 32, row_stride a multiple of 16.  Anything else is IGL_FAIL_SUPPORT. */
+int  igl_plane_attach(igl_desk *desk, igl_plane *sheet);
+/* The same for bytes and gains already on the device (no copy; the caller
+ * keeps ownership). */
+int  igl_plane_bind_dev(igl_desk *desk, igl_plane *sheet, const void *code_dev,
+                        const float *gain_dev);
+void igl_plane_detach(igl_desk *desk, igl_plane *sheet);
+
+/* ---- device-resident entries (enqueue on the desk's stream) -------------- */
+
+/* y = W x for `lane_count` lanes of fp32 activations: 1..8 lanes a launch
+ * take the HBM-streaming GEMV (more lanes run in chunks of 8); from
+ * `igl_gemm_lane_floor()` lanes on, the MFMA GEMM. */
+int igl_mat_mat_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev, int act_stride,
+                    int lane_count, float *out_dev, int out_stride);
+/* Always the GEMV path (lanes in chunks of 8), whatever the lane count. */
+int igl_gemv_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev, int act_stride,
+                 int lane_count, float *out_dev, int out_stride);
+/* Batched prefill: bf16 activations [lanes][act_stride] -> bf16 [lanes][out_stride],
+ * fp32 accumulate, on the MFMA GEMM. */
+int igl_gemm_bf16_dev(igl_desk *desk, const igl_plane *sheet, const uint16_t *act_dev,
+                      int act_stride, int lane_count, uint16_t *out_dev, int out_stride);
+int igl_gemm_lane_floor(void);
+
+/* Byte formats of the key/value ring. */
+typedef enum igl_cache_format { IGL_CACHE_E4M3 = 0, IGL_CACHE_INT8 = 1 } igl_cache_format;
+
+/* Decode attention for one lane: for every key/value head, the `group_share`
+ * query heads that read it attend over positions place_start ..
+ * place_start + span_count - 1, stored in ring slot p % cache_span, each row
+ * kv_count * head_size bytes.  A byte decodes to real8(byte) * scale (e4m3, the
+ * reference's cache_real8) or (int8)byte * scale.  Scores are multiplied by
+ * `score_scale` (1.0 in the reference graph, whose q/k norms absorb it).
+ * query/blend_out: [kv_count * group_share][head_size] fp32.
+ * Supported: head_size 256 or 512, group_share 8. */
+int igl_attend_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t *value_store,
+                   int format, float key_scale, float value_scale, int cache_span,
+                   int kv_count, int group_share, int head_size, const float *query_dev,
+                   int place_start, int span_count, float score_scale, float *blend_out_dev);
+/* cache_lay (app_core.c:11205-11236) for a byte store: row / scale to the ring
+ * at byte offset slot_first. */
+int igl_cache_lay_dev(igl_desk *desk, const float *row_dev, int width, float scale, int format,
+                      uint8_t *store_dev, size_t slot_first);
+
+int igl_norm_rms_dev(igl_desk *desk, const float *in_dev, const float *gain_dev, int n, int rows,
+                     int stride, float eps, float *out_dev);
+int igl_soft_max_dev(igl_desk *desk, float *v_dev, int n, int rows, int stride);
+int igl_gelu_gate_dev(igl_desk *desk, float *gate_dev, const float *rise_dev, int n);
+int igl_rope_turn_dev(igl_desk *desk, float *v_dev, int heads, int head_size, const float *cos_dev,
+                      const float *sin_dev);
+
+/* ---- device memory and timing (plumbing) --------------------------------- */
+
+void *igl_dev_alloc(igl_desk *desk, size_t bytes);
+void  igl_dev_free(igl_desk *desk, void *ptr);
+int   igl_copy_to_dev(igl_desk *desk, void *dst_dev, const void *src_host, size_t bytes);
+int   igl_copy_to_host(igl_desk *desk, void *dst_host, const void *src_dev, size_t bytes);
+int   igl_fill_dev(igl_desk *desk, void *dst_dev, int byte_value, size_t bytes);
+int   igl_sync(igl_desk *desk);
+/* Events on the desk's stream around enqueued work: mark, then read the
+ * milliseconds between the last two marks after they complete. */
+int   igl_mark(igl_desk *desk);
+float igl_marks_ms(igl_desk *desk);
+
+/* ---- synthetic inputs (seeded, shared by the CPU and GPU hosts) ----------- */
+
+/* splitmix64-seeded xoshiro256**; normals by Box-Muller in double. */
+typedef struct igl_rng { uint64_t s[4]; } igl_rng;
+void     igl_rng_seed(igl_rng *rng, uint64_t seed);
+uint64_t igl_rng_next(igl_rng *rng);
+void     igl_rng_normal(igl_rng *rng, float *out, size_t count, float mean, float stddev);
+/* N rows of K int4 codes uniform in -8..7, stored as value + 8, two a byte,
+ * low nibble first, rows `row_stride` bytes apart (row_stride >= K/2). */
+void     igl_rng_codes4(igl_rng *rng, uint8_t *codes, int N, int K, size_t row_stride);
+/* |N(0, stddev)| gains. */
+void     igl_rng_gains(igl_rng *rng, float *gains, size_t count, float stddev);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

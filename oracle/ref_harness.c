@@ -1,0 +1,164 @@
+/* ref_harness.c - exports the reference engine's own projection, codec and
+ * attention functions under a flat C ABI, for the parity tests and the CPU
+ * baseline.
+ *
+ * TEST INFRASTRUCTURE ONLY.  It is built by oracle/Makefile straight from the
+ * reference's single translation unit where it lies (app_core.c, included
+ * below through -I), into oracle/_ref/, which git ignores.  No reference source
+ * is copied into this repository; nothing in igllm_amd/ links this.
+ *
+ * Two builds are made: a plain one (SSE2 tier, the float path the oracle
+ * restates to the bit) and a tuned one (-mavx2 -mfma, the reference's fastest
+ * float path on x86, used as the CPU baseline).  Neither enables the VNNI
+ * integer grid, which rounds activations and is not the fp32 oracle.
+ */
+#include "app_core.c"
+
+#if defined(APP_SIMD_AVX512VNNI)
+#  error "the harness must not be built on the integer-grid tier"
+#endif
+
+/* Flat description of a code plane; the fields of `plane` (app_core.c:1775)
+ * a code plane uses, gains fp32. */
+typedef struct ref_plane_desc {
+  int            row_count;
+  int            col_count;
+  const uint8_t *code_data;
+  size_t         row_stride;
+  const float   *gain_data;
+  const int8_t  *bias_data;
+  int            bit_count;
+  int            code_bias;
+  int            code_flip;
+  int            group_size;
+  int            group_count;
+} ref_plane_desc;
+
+static void ref_plane_fill(const ref_plane_desc *desc, plane *sheet) {
+  memset(sheet, 0, sizeof(*sheet));
+  sheet->form = PLANE_CODE;
+  sheet->row_count = desc->row_count;
+  sheet->col_count = desc->col_count;
+  sheet->code_data = desc->code_data;
+  sheet->row_stride = desc->row_stride;
+  sheet->gain_data = desc->gain_data;
+  sheet->gain_type = STORE_F32;
+  sheet->bias_data = desc->bias_data;
+  sheet->bit_count = desc->bit_count;
+  sheet->code_bias = desc->code_bias;
+  sheet->code_flip = desc->code_flip;
+  sheet->group_size = desc->group_size;
+  sheet->group_count = desc->group_count;
+}
+
+const char *ref_flavor(void) { return back_flavor(); }
+
+uint32_t ref_pack_read(const uint8_t *code_data, size_t element_index, int bit_count) {
+  return pack_read(code_data, element_index, bit_count);
+}
+
+void ref_plane_row(const ref_plane_desc *desc, int row_index, float *row_out) {
+  plane sheet;
+  ref_plane_fill(desc, &sheet);
+  plane_row(&sheet, row_index, row_out);
+}
+
+/* A desk and its pool, held open so the CPU baseline times products and not
+ * thread creation. */
+typedef struct ref_desk {
+  back_desk  desk;
+  pool_group pool;
+} ref_desk;
+
+void *ref_desk_open(int thread_count, int sum_limit, int col_limit) {
+  ref_desk *box = (ref_desk *)calloc(1, sizeof(ref_desk));
+  if (!box) return NULL;
+  if (pool_open(&box->pool, thread_count) != APP_OKAY ||
+      back_open(&box->desk, &box->pool, sum_limit, col_limit) != APP_OKAY) {
+    free(box);
+    return NULL;
+  }
+  return box;
+}
+
+void ref_desk_close(void *handle) {
+  ref_desk *box = (ref_desk *)handle;
+  if (!box) return;
+  back_close(&box->desk);
+  pool_close(&box->pool);
+  free(box);
+}
+
+void ref_desk_mat_mat(void *handle, const ref_plane_desc *desc, const float *act, int act_stride,
+                      int lane_count, float *out, int out_stride) {
+  ref_desk *box = (ref_desk *)handle;
+  plane sheet;
+  ref_plane_fill(desc, &sheet);
+  box->desk.mat_mat(&box->desk, &sheet, act, act_stride, lane_count, out, out_stride);
+}
+
+float ref_cache_pack8(float value) { return cache_pack8(value); }
+uint8_t ref_cache_code8(float value) { return cache_code8(value); }
+float ref_cache_real8(uint8_t code) { return cache_real8(code); }
+void ref_cache_grid_fill(float *grid, float scale) { cache_grid_fill(grid, scale); }
+float ref_exp_near(float value) { return kern_exp_near(value); }
+void ref_soft_max(float *value_list, int value_count) { kern_soft_max(value_list, value_count); }
+float ref_quant_step(float value, float step) {
+  quant_step(&value, 1, step);
+  return value;
+}
+
+/* One lane's grouped decode attention through the reference's own two jobs
+ * (attend_score_band / attend_blend_band, app_core.c:11296-11365), forked over
+ * the desk's pool exactly as session_attend_group forks them (11415-11453).
+ * Only the session and model fields those jobs read are set. */
+void ref_attend(void *handle, const uint8_t *key_store, const uint8_t *value_store,
+                const float *key_grid, const float *value_grid, int cache_span, int kv_width,
+                int kv_index, const float *query, int head_first, int group_share, int head_size,
+                int place_start, int span_count, float *blend_out) {
+  ref_desk *box = (ref_desk *)handle;
+  app_model *model = (app_model *)calloc(1, sizeof(app_model));
+  app_session *session = (app_session *)calloc(1, sizeof(app_session));
+  int bands = pool_bands(&box->pool);
+  attend_job job;
+  if (!model || !session) {
+    free(model);
+    free(session);
+    return;
+  }
+  model->desk = box->desk;
+  session->model = model;
+  session->score_stride = span_count;
+  session->block_room = cache_block_rows(head_size) * head_size;
+  session->score_room = (float *)calloc((size_t)group_share * (size_t)span_count, sizeof(float));
+  session->cache_room = (float *)calloc((size_t)bands * (size_t)session->block_room, sizeof(float));
+  memset(&job, 0, sizeof(job));
+  job.session = session;
+  job.key_store = key_store;
+  job.value_store = value_store;
+  job.key_grid = key_grid;
+  job.value_grid = value_grid;
+  job.query_lane = query;
+  job.blend_lane = blend_out;
+  job.cache_span = cache_span;
+  job.place_start = place_start;
+  job.span_count = span_count;
+  job.block_rows = cache_block_rows(head_size);
+  job.block_room = session->block_room;
+  job.kv_index = kv_index;
+  job.head_first = head_first;
+  job.group_share = group_share;
+  job.head_size = head_size;
+  job.kv_width = kv_width;
+  if (box->pool.worker_count > 0 && span_count >= ATTEND_BAND_SPAN) {
+    pool_run(&box->pool, attend_score_band, &job);
+    pool_run(&box->pool, attend_blend_band, &job);
+  } else {
+    attend_score_band(&job, 0, 1);
+    attend_blend_band(&job, 0, 1);
+  }
+  free(session->score_room);
+  free(session->cache_room);
+  free(session);
+  free(model);
+}

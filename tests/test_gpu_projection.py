@@ -1,0 +1,170 @@
+"""GPU parity of the packed int4 projection: decode GEMV, small-lane verify
+GEMV and batched prefill GEMM, against the oracle on the same seeded inputs.
+
+Bars:
+  * GEMV (fp32 in/out): every output within relative error 1e-3 of the oracle,
+    relative to max(|y_ref|, rms(y_ref)) so that outputs near zero are judged
+    against the scale of the row set rather than against themselves.
+  * GEMM (bf16 in/out): bf16 output rounding alone is up to 2^-9 relative, so
+    |C - y_ref| <= 2^-8 |y_ref| + 2e-3 rms(y_ref), y_ref the oracle (or the
+    float64 closed form at the largest sizes) on the bf16-rounded activations.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from igllm_amd.backend import make_plane, synth_projection
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_err(got, want):
+    want = want.astype(np.float64)
+    floor = np.sqrt(np.mean(want ** 2))
+    return float(np.max(np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want), floor)))
+
+
+def run_gemv_dev(backend, cp, act, lanes, path="gemv"):
+    K, N = cp.K, cp.N
+    dev_act = backend.upload(act)
+    dev_out = backend.alloc(lanes * N * 4)
+    fn = backend.gemv_dev if path == "gemv" else backend.mat_mat_dev
+    fn(cp, dev_act, K, lanes, dev_out, N)
+    backend.sync()
+    out = dev_out.get(np.float32, lanes * N).reshape(lanes, N)
+    dev_act.free()
+    dev_out.free()
+    return out
+
+
+def print_case(**kw):
+    print("case", " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def test_decode_gemv_config0(backend):
+    """W [8192, 2048] int4 g32, x [2048] ~ N(0,1), seed 0 (the decode projection)."""
+    print_case(test="config0", N=8192, K=2048, lanes=1, seed=0)
+    codes, gains, act = synth_projection(8192, 2048, 1, seed=0)
+    cp = backend.attach(make_plane(codes, gains, 2048))
+    got = run_gemv_dev(backend, cp, act, 1)
+    want = ol.oracle_mat_mat(codes, gains, act, 2048, threads=8)
+    err = rel_err(got, want)
+    print("rel_err", err)
+    assert err <= 1e-3
+    # the table entry (host pointers) is the same launch behind staging
+    host = backend.mat_vec(cp, act[0])
+    assert np.array_equal(host, got[0])
+    backend.detach(cp)
+
+
+@pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 8192)])
+@pytest.mark.parametrize("lanes", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_small_lane_sweep(backend, N, K, lanes):
+    print_case(test="sweep", N=N, K=K, lanes=lanes)
+    codes, gains, act = synth_projection(N, K, lanes, seed=lanes)
+    cp = backend.attach(make_plane(codes, gains, K))
+    got = run_gemv_dev(backend, cp, act, lanes)
+    want = ol.oracle_mat_mat(codes, gains, act, K, threads=8)
+    err = rel_err(got, want)
+    print("rel_err", err)
+    assert err <= 1e-3
+    backend.detach(cp)
+
+
+@pytest.mark.parametrize("N,K,lanes,group", [
+    (70, 128, 1, 32), (130, 96, 3, 32), (1, 32, 1, 32), (257, 1536, 2, 32), (64, 12288, 1, 32),
+    (33, 12288, 8, 32), (100, 2048, 8, 64), (100, 4096, 4, 128), (512, 256, 16, 32),
+    (300, 6144, 12, 32), (40, 8192, 5, 32),
+])
+def test_gemv_edges(backend, N, K, lanes, group):
+    """Ragged rows, narrow and odd unit counts, K-chunked launches, wider groups,
+    lane counts past one launch."""
+    print_case(test="gemv_edges", N=N, K=K, lanes=lanes, group=group)
+    codes, gains, act = synth_projection(N, K, lanes, seed=N + K, group_size=group)
+    cp = backend.attach(make_plane(codes, gains, K, group_size=group))
+    got = run_gemv_dev(backend, cp, act, lanes)
+    want = ol.oracle_mat_mat(codes, gains, act, K, group_size=group, threads=8)
+    assert rel_err(got, want) <= 1e-3
+    host = backend.mat_mat(cp, act)
+    assert rel_err(host, want) <= 1e-3
+    backend.detach(cp)
+
+
+def test_gemv_unaligned_activations(backend):
+    """An activation stride that is not a multiple of four floats takes the
+    scalar staging path."""
+    N, K, lanes = 96, 256, 3
+    codes, gains, act = synth_projection(N, K, lanes, seed=9)
+    padded = np.zeros((lanes, K + 1), dtype=np.float32)
+    padded[:, :K] = act
+    cp = backend.attach(make_plane(codes, gains, K))
+    dev_act = backend.upload(padded)
+    dev_out = backend.alloc(lanes * N * 4)
+    backend.gemv_dev(cp, dev_act, K + 1, lanes, dev_out, N)
+    backend.sync()
+    got = dev_out.get(np.float32, lanes * N).reshape(lanes, N)
+    want = ol.oracle_mat_mat(codes, gains, act, K)
+    assert rel_err(got, want) <= 1e-3
+    backend.detach(cp)
+
+
+def test_unsupported_plane_is_refused(backend):
+    from igllm_amd.backend import BackendError
+
+    codes, gains, act = synth_projection(16, 48, 1, seed=3, group_size=16)
+    with pytest.raises(BackendError):
+        backend.attach(make_plane(codes, gains, 48, group_size=16))
+
+
+def bf16_round(x):
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return u.astype(np.uint16)
+
+
+def bf16_to_f32(raw):
+    return (raw.astype(np.uint32) << 16).view(np.float32)
+
+
+def closed_form64(codes, gains, act64, K, group=32):
+    nib = np.stack([codes & 15, codes >> 4], axis=-1).reshape(codes.shape[0], -1)[:, :K]
+    w = (nib.astype(np.float64) - 8.0) * np.repeat(gains.astype(np.float64), group, axis=1)[:, :K]
+    return act64 @ w.T
+
+
+@pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 8192)])
+@pytest.mark.parametrize("M", [64, 256, 1024, 2048])
+def test_prefill_gemm(backend, N, K, M):
+    print_case(test="prefill", N=N, K=K, M=M)
+    codes, gains, act = synth_projection(N, K, M, seed=M)
+    a16 = bf16_round(act).reshape(M, K)
+    cp = backend.attach(make_plane(codes, gains, K))
+    dev_a = backend.upload(a16)
+    dev_c = backend.alloc(M * N * 2)
+    backend.gemm_bf16_dev(cp, dev_a, K, M, dev_c, N)
+    backend.sync()
+    got = bf16_to_f32(dev_c.get(np.uint16, M * N)).reshape(M, N)
+    a32 = bf16_to_f32(a16)
+    if M <= 64:
+        want = ol.oracle_mat_mat(codes, gains, a32, K, threads=8).astype(np.float64)
+    else:
+        want = closed_form64(codes, gains, a32.astype(np.float64), K)
+    rms = math.sqrt(float(np.mean(want ** 2)))
+    excess = np.abs(got - want) - (2.0 ** -8 * np.abs(want) + 2e-3 * rms)
+    print("max_excess", float(excess.max()), "rms", rms)
+    assert float(excess.max()) <= 0.0
+    backend.detach(cp)
+
+
+def test_mat_mat_many_lanes_takes_gemm(backend):
+    """fp32 activations with >= 64 lanes go to the MFMA GEMM through mat_mat_dev."""
+    N, K, M = 384, 1024, 96
+    codes, gains, act = synth_projection(N, K, M, seed=5)
+    cp = backend.attach(make_plane(codes, gains, K))
+    got = run_gemv_dev(backend, cp, act, M, path="mat_mat")
+    want = ol.oracle_mat_mat(codes, gains, act, K, threads=8)
+    # binary16 activations and dequantized weights: 2^-11 relative each
+    assert rel_err(got, want) <= 2e-3
+    backend.detach(cp)
