@@ -1,35 +1,48 @@
 // igl_attend.hip - decode attention over the byte-quantized key/value ring,
 // gfx950.
 //
-// For one lane (one query position) and one key/value head shared by GROUP
+// For one lane (one query position) and each key/value head shared by 8
 // query heads, computes
 //     o_h = sum_t softmax_t(score_scale * q_h . k_t) v_t
 // over the visible positions t = place_start .. place_start + span - 1, whose
 // rows sit in ring slot t % cache_span (session_attend_group with
 // attend_score_band and attend_blend_band, app_core.c:11296-11453; ring and
 // span rules 11500, 11516-11526).  A stored byte decodes to
-//     e4m3:  cache_real8(byte) * scale  (cache_real8, app_core.c:11018-11030)
+//     e4m3:  cache_real8(byte) * scale   (cache_real8, app_core.c:11018-11030)
 //     int8:  (int8_t)byte * scale
-// The reference computes every score against `grid[byte] = real8 * scale`;
-// here the scale is applied to the finished dot product instead, which is the
-// same value up to fp32 rounding.
+// The reference scores every row against `grid[byte] = real8 * scale`; here
+// the scale multiplies the finished dot product, the same value up to fp32
+// rounding.
 //
-// e4m3 bytes are decoded without a table: moving the byte's exponent and
-// mantissa to bits [7,14) of a binary16 and its sign to bit 15 gives exactly
-// real8(byte) / 256 for all 256 codes, including 0x7F/0xFF, which the
-// reference reads as +-480 and which this mapping also reads as +-480 (no NaN
-// code exists on either side).
+// Why MFMA: with 8 query heads on one key/value head every key and value
+// byte feeds 8 multiply-adds, 8 MAC per byte of HBM traffic, above the ~5
+// fp32 MAC per byte the vector ALU can sustain at the HBM rate.  Both
+// products therefore run on v_mfma_f32_16x16x32_f16:
+//   scores  S[16 x 32 positions] = [q_hi; q_lo] (16 x d) . K^T (d x 32)
+//   blend   O[16 x d]            = [p_hi; p_lo] (16 x 32) . V (32 x d)
+// The 16 MFMA rows hold each head twice, as an exact two-term binary16 split
+// (x = hi + lo, |lo| <= 2^-11 |x|), so the products keep ~22 significant
+// bits and accumulate in fp32; the two rows are added at the end.  Bytes
+// decode to binary16 exactly:
+//   e4m3: move bit 7 to bit 8 and shift the byte up by 7, giving
+//         real8(byte) / 256 for all 256 codes (0x7F/0xFF read +-480, as the
+//         reference reads them);
+//   int8: (byte ^ 0x80) in the mantissa of 1024.0, minus 1152.
 //
-// Split over the span (flash-decoding): a workgroup takes CHUNK positions,
-// computes the chunk's scores, its running maximum, exponentials and their
-// sum, and its unnormalized blend; a second kernel merges the chunks in chunk
-// order.  v1 runs the dot products on the vector ALU.
+// Work layout: a workgroup owns 128 positions (4 waves x 32).  A wave loads
+// its 32 key rows straight into MFMA operand order (each lane a contiguous
+// d/4-byte run of a row), its 32 value rows into LDS (transposed on read), runs
+// the scores, the tile softmax, and the blend; the four waves' (max, total,
+// output) are merged in LDS and written as the chunk's partial.  A second
+// kernel merges the chunks in chunk order (flash-decoding).
 #include "igl_device.h"
 
 namespace igl {
 
 constexpr int kAttendThreads = 256;
-constexpr int kAttendChunk = 128;
+constexpr int kAttendTile = 32;                    // positions per wave
+constexpr int kAttendChunk = 4 * kAttendTile;      // positions per workgroup
+constexpr int kAttendGroup = 8;                    // query heads per key/value head
 
 struct AttendArgs {
   const uint8_t *key_store;    // [cache_span][kv_width]
@@ -41,163 +54,273 @@ struct AttendArgs {
   const float *query;          // [head_count][HEAD]
   float key_scale;             // decoded-byte multiplier, score_scale folded in
   float value_scale;
-  int fmt;                     // 0 = e4m3, 1 = int8
   float *part_out;             // [chunks][head_count][HEAD]
   float *part_peak;            // [chunks][head_count]
   float *part_total;           // [chunks][head_count]
   int head_count;
 };
 
-__device__ __forceinline__ float decode_byte(uint32_t b, int fmt) {
-  if (fmt == 0) {
-    const uint32_t h = ((b & 0x7Fu) << 7) | ((b & 0x80u) << 8);
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+// Two bytes held in bits [0,8) and [16,24) of `x`, as two exact binary16.
+template <int FMT>
+__device__ __forceinline__ uint32_t decode_pair(uint32_t x) {
+  if (FMT == 0) {
+    return (x + (x & 0x00800080u)) << 7;  // e4m3 -> real8 / 256
+  } else {
+    half2_t h = as_half2(x ^ 0x64806480u);  // 1152 + (int8)byte
+    h = h + half2_t{(_Float16)-1152.0f, (_Float16)-1152.0f};
+    return __builtin_bit_cast(uint32_t, h);
   }
-  return (float)(int8_t)(uint8_t)b;
 }
 
-template <int HEAD, int GROUP>
-__global__ __launch_bounds__(kAttendThreads) void attend_chunk_kernel(AttendArgs a) {
-  constexpr int kPosHalves = kAttendChunk / 64;  // position blocks of 64 in a chunk
-  constexpr int kDimSplit = 4 / kPosHalves;      // waves sharing one position block
-  constexpr int kDimsPerWave = HEAD / kDimSplit;
-  constexpr int kBlendDims = HEAD / kAttendThreads;  // dims a thread blends (1 or 2)
+// Eight bytes (two dwords, low byte first) as eight binary16 operand values.
+template <int FMT>
+__device__ __forceinline__ half8_t decode8(uint32_t lo, uint32_t hi) {
+  uint32_t w[4];
+  w[0] = decode_pair<FMT>(__builtin_amdgcn_perm(0u, lo, 0x0C010C00u));
+  w[1] = decode_pair<FMT>(__builtin_amdgcn_perm(0u, lo, 0x0C030C02u));
+  w[2] = decode_pair<FMT>(__builtin_amdgcn_perm(0u, hi, 0x0C010C00u));
+  w[3] = decode_pair<FMT>(__builtin_amdgcn_perm(0u, hi, 0x0C030C02u));
+  return __builtin_bit_cast(half8_t, w);
+}
 
-  __shared__ float ps[4][GROUP][64];               // partial scores per wave
-  __shared__ float pt[kAttendChunk][GROUP];        // probabilities, position-major
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
+
+template <int HEAD, int FMT>
+__global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs a) {
+  constexpr int S = HEAD / 32;        // k-steps of the score product
+  constexpr int QD = HEAD / 4;        // bytes of a key row one lane group reads
+  constexpr int TILES = HEAD / 16;    // 16-wide dim tiles of the blend
+  constexpr int QUADS = TILES / 4;    // four tiles share one LDS read
+  constexpr int VPITCH = HEAD + 8;    // staged value row: (HEAD/4 + 2) dwords, conflict-free reads
+  constexpr int kWaveV = kAttendTile * VPITCH;
+
+  __shared__ __attribute__((aligned(16))) uint8_t vs[4 * kWaveV];
+  __shared__ float ps[4][kAttendGroup][kAttendTile];
+  __shared__ float wm[4][kAttendGroup];
+  __shared__ float wl[4][kAttendGroup];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int chunk = blockIdx.x;
+  const int g = lane >> 4;        // lane group
+  const int n = lane & 15;        // MFMA row (A) / column (B, D)
   const int kv = blockIdx.y;
-  const int head0 = kv * GROUP;
-  const int t_base = chunk * kAttendChunk;
+  const int head0 = kv * kAttendGroup;
+  const int chunk = blockIdx.x;
+  const int t0 = chunk * kAttendChunk + wave * kAttendTile;
+  const bool live = t0 < a.span_count;
   const size_t kv_off = (size_t)kv * HEAD;
 
-  // ---- scores: lane = position, waves split (position block, dim range).
+  // ---- query operands: row n is head (n & 7), hi part (n < 8) or lo part.
+  half8_t qa[S];
   {
-    const int pblk = wave / kDimSplit;
-    const int dpart = wave % kDimSplit;
-    const int t = t_base + pblk * 64 + lane;
-    float sc[GROUP];
+    const float *q = a.query + (size_t)(head0 + (n & 7)) * HEAD + QD * g;
+    const bool lo_part = n >= 8;
 #pragma unroll
-    for (int h = 0; h < GROUP; ++h) sc[h] = 0.0f;
-    if (t < a.span_count) {
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = q[8 * s + e];
+        const _Float16 hi = (_Float16)v;
+        qa[s][e] = lo_part ? (_Float16)(v - (float)hi) : hi;
+      }
+  }
+
+  // ---- key rows in operand order, value rows into LDS.
+  float4_t sacc[2] = {float4_t{0, 0, 0, 0}, float4_t{0, 0, 0, 0}};
+  uint8_t *vw = vs + wave * kWaveV;
+  if (live) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int t = min(t0 + n + 16 * j, a.span_count - 1);
       const int slot = (a.place_start + t) % a.cache_span;
       const uint4_t *row = reinterpret_cast<const uint4_t *>(
-          a.key_store + (size_t)slot * a.kv_width + kv_off + dpart * kDimsPerWave);
-      const float *q = a.query + (size_t)head0 * HEAD + dpart * kDimsPerWave;
-      for (int d16 = 0; d16 < kDimsPerWave / 16; ++d16) {
-        const uint4_t w = __builtin_nontemporal_load(row + d16);
-        float kf[16];
+          a.key_store + (size_t)slot * a.kv_width + kv_off + QD * g);
+      uint4_t kr[QD / 16];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+      for (int c = 0; c < QD / 16; ++c) kr[c] = __builtin_nontemporal_load(row + c);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) kf[4 * j + i] = decode_byte((w[j] >> (8 * i)) & 0xFFu, a.fmt);
+      for (int s = 0; s < S; ++s) {
+        const uint4_t w = kr[s >> 1];
+        const half8_t kb = (s & 1) ? decode8<FMT>(w[2], w[3]) : decode8<FMT>(w[0], w[1]);
+        sacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kb, sacc[j], 0, 0, 0);
+      }
+    }
+    // value rows: lane -> row lane/2, half lane&1
+    {
+      const int r = lane >> 1;
+      const int t = min(t0 + r, a.span_count - 1);
+      const int slot = (a.place_start + t) % a.cache_span;
+      const uint2_t *src = reinterpret_cast<const uint2_t *>(
+          a.value_store + (size_t)slot * a.kv_width + kv_off + (lane & 1) * (HEAD / 2));
+      uint2_t *dst = reinterpret_cast<uint2_t *>(vw + r * VPITCH + (lane & 1) * (HEAD / 2));
 #pragma unroll
-        for (int h = 0; h < GROUP; ++h) {
-          float s = sc[h];
+      for (int c = 0; c < HEAD / 16; ++c) dst[c] = __builtin_nontemporal_load(src + c);
+    }
+  }
+
+  // ---- tile softmax.  After the xor-32 sum, lane groups 0/2 hold heads 0-3
+  // and 1/3 heads 4-7 (row r of the group is head 4 (g & 1) + r), position
+  // n + 16 j.
+  float m_run[4], l_run[4];
+  float p[2][4];
 #pragma unroll
-          for (int i = 0; i < 16; ++i) s = __builtin_fmaf(kf[i], q[h * HEAD + d16 * 16 + i], s);
-          sc[h] = s;
-        }
+  for (int r = 0; r < 4; ++r) {
+    float s0 = sacc[0][r] + xor32(sacc[0][r]);
+    float s1 = sacc[1][r] + xor32(sacc[1][r]);
+    s0 = (t0 + n < a.span_count) ? s0 * a.key_scale : -INFINITY;
+    s1 = (t0 + n + 16 < a.span_count) ? s1 * a.key_scale : -INFINITY;
+    float m = row16_max(fmaxf(s0, s1));
+    if (!live) m = -INFINITY;
+    const float p0 = live ? __expf(s0 - m) : 0.0f;
+    const float p1 = live ? __expf(s1 - m) : 0.0f;
+    p[0][r] = p0;
+    p[1][r] = p1;
+    m_run[r] = m;
+    l_run[r] = row16_sum(p0 + p1);
+  }
+  if (g < 2) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ps[wave][4 * g + r][n] = p[0][r];
+      ps[wave][4 * g + r][n + 16] = p[1][r];
+    }
+    if (n == 0)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        wm[wave][4 * g + r] = m_run[r];
+        wl[wave][4 * g + r] = l_run[r];
+      }
+  }
+  __syncthreads();
+
+  // ---- blend: A = probabilities (row n: head n & 7, hi/lo), k = positions 8g..8g+7.
+  float4_t o[TILES];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) o[t] = float4_t{0, 0, 0, 0};
+  if (live) {
+    half8_t pa;
+    {
+      const float *src = &ps[wave][n & 7][8 * g];
+      const bool lo_part = n >= 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = src[e];
+        const _Float16 hi = (_Float16)v;
+        pa[e] = lo_part ? (_Float16)(v - (float)hi) : hi;
       }
     }
 #pragma unroll
-    for (int h = 0; h < GROUP; ++h) ps[wave][h][lane] = sc[h];
-  }
-  __syncthreads();
-
-  // ---- chunk softmax: wave w takes heads w, w+4; lane = position in a block.
-  for (int h = wave; h < GROUP; h += 4) {
-    float s[kPosHalves];
-    float m = -INFINITY;
+    for (int qd = 0; qd < QUADS; ++qd) {
+      uint32_t dw[8];
 #pragma unroll
-    for (int pb = 0; pb < kPosHalves; ++pb) {
-      const int t = t_base + pb * 64 + lane;
-      float v = 0.0f;
+      for (int e = 0; e < 8; ++e)
+        dw[e] = *reinterpret_cast<const uint32_t *>(vw + (8 * g + e) * VPITCH + 64 * qd + 4 * n);
 #pragma unroll
-      for (int dp = 0; dp < kDimSplit; ++dp) v += ps[pb * kDimSplit + dp][h][lane];
-      v = (t < a.span_count) ? v * a.key_scale : -INFINITY;
-      s[pb] = v;
-      m = fmaxf(m, v);
-    }
-    // wave max
-    m = row16_max(m);
-    m = fmaxf(fmaxf(lane_read(m, 0), lane_read(m, 16)), fmaxf(lane_read(m, 32), lane_read(m, 48)));
-    float l = 0.0f;
+      for (int t = 0; t < 4; ++t) {
+        uint32_t w[4];
+        const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + t) << 16) | (uint32_t)t;
 #pragma unroll
-    for (int pb = 0; pb < kPosHalves; ++pb) {
-      const float p = s[pb] == -INFINITY ? 0.0f : __expf(s[pb] - m);
-      pt[pb * 64 + lane][h] = p;
-      l += p;
-    }
-    l = wave_sum_to_last(l);
-    if (lane == 63) {
-      a.part_peak[(size_t)chunk * a.head_count + head0 + h] = m;
-      a.part_total[(size_t)chunk * a.head_count + head0 + h] = l;
+        for (int pr = 0; pr < 4; ++pr)
+          w[pr] = decode_pair<FMT>(__builtin_amdgcn_perm(dw[2 * pr + 1], dw[2 * pr], sel));
+        o[4 * qd + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, __builtin_bit_cast(half8_t, w),
+                                                               o[4 * qd + t], 0, 0, 0);
+      }
     }
   }
-  __syncthreads();
+  // hi + lo rows
+#pragma unroll
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[t][r] += xor32(o[t][r]);
 
-  // ---- blend: thread = dims [kBlendDims*tid, +kBlendDims), every position of
-  // the chunk in order; a wave's row read is 64 (or 128) contiguous bytes.
+  // ---- merge the four waves: scale each by e^(m_w - M) per head.
+  __syncthreads();  // every wave is done reading its value tile; reuse vs as float[4][8][HEAD]
+  float *ob = reinterpret_cast<float *>(vs);
   {
-    float o[GROUP][kBlendDims];
+    float scale[4];
 #pragma unroll
-    for (int h = 0; h < GROUP; ++h)
-#pragma unroll
-      for (int i = 0; i < kBlendDims; ++i) o[h][i] = 0.0f;
-    const int d0 = tid * kBlendDims;
-    const int t_end = min(kAttendChunk, a.span_count - t_base);
-    for (int tl = 0; tl < t_end; ++tl) {
-      const int slot = (a.place_start + t_base + tl) % a.cache_span;
-      const uint8_t *row = a.value_store + (size_t)slot * a.kv_width + kv_off + d0;
-      float vf[kBlendDims];
-      if (kBlendDims == 1) {
-        vf[0] = decode_byte(row[0], a.fmt);
-      } else {
-        const uint32_t w = *reinterpret_cast<const uint16_t *>(row);
-#pragma unroll
-        for (int i = 0; i < kBlendDims; ++i) vf[i] = decode_byte((w >> (8 * i)) & 0xFFu, a.fmt);
-      }
-#pragma unroll
-      for (int h = 0; h < GROUP; ++h) {
-        const float p = pt[tl][h];
-#pragma unroll
-        for (int i = 0; i < kBlendDims; ++i) o[h][i] = __builtin_fmaf(p, vf[i], o[h][i]);
-      }
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * (g & 1) + r;
+      float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+      scale[r] = live ? __expf(m_run[r] - M) : 0.0f;
     }
+    if (g < 2) {
 #pragma unroll
-    for (int h = 0; h < GROUP; ++h)
+      for (int qd = 0; qd < QUADS; ++qd)
 #pragma unroll
-      for (int i = 0; i < kBlendDims; ++i)
-        a.part_out[((size_t)chunk * a.head_count + head0 + h) * HEAD + d0 + i] = o[h][i] * a.value_scale;
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            ob[(wave * kAttendGroup + 4 * g + r) * HEAD + 64 * qd + 4 * n + t] = o[4 * qd + t][r] * scale[r];
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < kAttendGroup * HEAD; i += kAttendThreads) {
+    const int h = i / HEAD;
+    const int d = i - h * HEAD;
+    const float v = ((ob[(0 * kAttendGroup + h) * HEAD + d] + ob[(1 * kAttendGroup + h) * HEAD + d]) +
+                     ob[(2 * kAttendGroup + h) * HEAD + d]) + ob[(3 * kAttendGroup + h) * HEAD + d];
+    a.part_out[((size_t)chunk * a.head_count + head0 + h) * HEAD + d] = v * a.value_scale;
+  }
+  if (tid < kAttendGroup) {
+    const int h = tid;
+    const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      if (wm[w][h] != -INFINITY) L += wl[w][h] * __expf(wm[w][h] - M);
+    a.part_peak[(size_t)chunk * a.head_count + head0 + h] = M;
+    a.part_total[(size_t)chunk * a.head_count + head0 + h] = L;
   }
 }
 
-// Merges chunk partials in chunk order: one workgroup per head.
-__global__ void attend_merge_kernel(const float *part_out, const float *part_peak,
-                                    const float *part_total, int chunks, int head_count,
-                                    int head_size, float *blend_out) {
+// Merges chunk partials: one workgroup per head; chunk weights once in LDS,
+// then every thread sums its dims over the chunks in chunk order.
+__global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out,
+                                                           const float *part_peak,
+                                                           const float *part_total, int chunks,
+                                                           int head_count, int head_size,
+                                                           float *blend_out) {
+  extern __shared__ float wgt[];  // [chunks]
+  __shared__ float red[256];
   const int h = blockIdx.x;
   float peak = -INFINITY;
-  for (int c = 0; c < chunks; ++c) peak = fmaxf(peak, part_peak[(size_t)c * head_count + h]);
-  float total = 0.0f;
-  for (int c = 0; c < chunks; ++c) {
-    const float m = part_peak[(size_t)c * head_count + h];
-    if (m != -INFINITY) total += part_total[(size_t)c * head_count + h] * __expf(m - peak);
+  for (int c = threadIdx.x; c < chunks; c += blockDim.x)
+    peak = fmaxf(peak, part_peak[(size_t)c * head_count + h]);
+  red[threadIdx.x] = peak;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + w]);
+    __syncthreads();
   }
-  const float inv = total > 0.0f ? 1.0f / total : 0.0f;
+  peak = red[0];
+  __syncthreads();
+  float total = 0.0f;
+  for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
+    const float m = part_peak[(size_t)c * head_count + h];
+    const float wv = m == -INFINITY ? 0.0f : __expf(m - peak);
+    wgt[c] = wv;
+    total += wv * part_total[(size_t)c * head_count + h];
+  }
+  red[threadIdx.x] = total;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  const float inv = red[0] > 0.0f ? 1.0f / red[0] : 0.0f;
   for (int d = threadIdx.x; d < head_size; d += blockDim.x) {
-    float acc = 0.0f;
-    for (int c = 0; c < chunks; ++c) {
-      const float m = part_peak[(size_t)c * head_count + h];
-      if (m != -INFINITY)
-        acc += part_out[((size_t)c * head_count + h) * head_size + d] * __expf(m - peak);
+    float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
+    int c = 0;
+    for (; c + 4 <= chunks; c += 4) {
+      acc0 += wgt[c] * part_out[((size_t)c * head_count + h) * head_size + d];
+      acc1 += wgt[c + 1] * part_out[((size_t)(c + 1) * head_count + h) * head_size + d];
+      acc2 += wgt[c + 2] * part_out[((size_t)(c + 2) * head_count + h) * head_size + d];
+      acc3 += wgt[c + 3] * part_out[((size_t)(c + 3) * head_count + h) * head_size + d];
     }
-    blend_out[(size_t)h * head_size + d] = acc * inv;
+    for (; c < chunks; ++c) acc0 += wgt[c] * part_out[((size_t)c * head_count + h) * head_size + d];
+    blend_out[(size_t)h * head_size + d] = ((acc0 + acc1) + (acc2 + acc3)) * inv;
   }
 }
 
@@ -216,6 +339,7 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
   AttendArgs a;
   const int chunks = (span_count + kAttendChunk - 1) / kAttendChunk;
   const int head_count = kv_count * group_share;
+  if (group_share != kAttendGroup) return hipErrorInvalidValue;
   a.key_store = key_store;
   a.value_store = value_store;
   a.kv_width = kv_width;
@@ -227,22 +351,26 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
   const float unit = fmt == 0 ? 256.0f : 1.0f;
   a.key_scale = key_scale * unit * score_scale;
   a.value_scale = value_scale * unit;
-  a.fmt = fmt;
   a.head_count = head_count;
   a.part_out = work;
   a.part_peak = work + (size_t)chunks * head_count * head_size;
   a.part_total = a.part_peak + (size_t)chunks * head_count;
   dim3 grid(chunks, kv_count);
-  if (head_size == 256 && group_share == 8)
-    hipLaunchKernelGGL((attend_chunk_kernel<256, 8>), grid, dim3(kAttendThreads), 0, stream, a);
-  else if (head_size == 512 && group_share == 8)
-    hipLaunchKernelGGL((attend_chunk_kernel<512, 8>), grid, dim3(kAttendThreads), 0, stream, a);
+  if (head_size == 256 && fmt == 0)
+    hipLaunchKernelGGL((attend_mfma_kernel<256, 0>), grid, dim3(kAttendThreads), 0, stream, a);
+  else if (head_size == 256 && fmt == 1)
+    hipLaunchKernelGGL((attend_mfma_kernel<256, 1>), grid, dim3(kAttendThreads), 0, stream, a);
+  else if (head_size == 512 && fmt == 0)
+    hipLaunchKernelGGL((attend_mfma_kernel<512, 0>), grid, dim3(kAttendThreads), 0, stream, a);
+  else if (head_size == 512 && fmt == 1)
+    hipLaunchKernelGGL((attend_mfma_kernel<512, 1>), grid, dim3(kAttendThreads), 0, stream, a);
   else
     return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attend_merge_kernel, dim3(head_count), dim3(256), 0, stream, a.part_out,
-                     a.part_peak, a.part_total, chunks, head_count, head_size, blend_out);
+  hipLaunchKernelGGL(attend_merge_kernel, dim3(head_count), dim3(256), chunks * sizeof(float),
+                     stream, a.part_out, a.part_peak, a.part_total, chunks, head_count, head_size,
+                     blend_out);
   return hipGetLastError();
 }
 

@@ -219,6 +219,142 @@ __global__ void gemv_chunk_sum_kernel(const float *part, int chunks, int M, int 
   out[(size_t)m * out_stride + n] = total;
 }
 
+// The one- and two-lane form, for planes whose units fit one per lane of the
+// waves sharing a row tile (K <= 8192).  A lane's 32 activations per lane of
+// the batch live in VGPRs for the rows the wave owns, so there is no LDS
+// staging and no barrier before the arithmetic: the row loads, the gains and
+// the activations are all requested first and the launch pays one memory
+// round trip.  The arithmetic is gemv_q4_kernel's, term for term.
+template <int M, int R>
+__global__ __launch_bounds__(kGemvThreads) void gemv_q4_reg_kernel(GemvArgs a) {
+  __shared__ float red[4][R][M];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int tiles_per_block = 4 / a.ksplit;
+  const int tile = blockIdx.x * tiles_per_block + wave / a.ksplit;
+  const int ks = wave % a.ksplit;
+  const int row0 = tile * R;
+  const int units = a.K >> 5;
+  const int u = (units * ks) / a.ksplit + lane;
+  const bool has = row0 < a.N && u < (units * (ks + 1)) / a.ksplit;
+
+  uint4_t w[R];
+  float s[R];
+  float4_t x[M][8];
+  if (has) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min(row0 + r, a.N - 1);  // tail rows are computed, never stored
+      w[r] = __builtin_nontemporal_load(
+          reinterpret_cast<const uint4_t *>(a.codes + (size_t)row * (size_t)a.row_stride) + u);
+      s[r] = a.gains[(size_t)row * (size_t)a.gain_stride + ((unsigned)u >> a.group_shift)];
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float *src = a.act + (size_t)m * a.act_stride + u * 32;
+      if (a.act_vec) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) x[m][q] = *reinterpret_cast<const float4_t *>(src + 4 * q);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          x[m][q] = float4_t{src[4 * q], src[4 * q + 1], src[4 * q + 2], src[4 * q + 3]};
+      }
+    }
+  }
+
+  float acc[R][M];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+  if (has) {
+    const uint32_t exp16 = 0x4C004C00u;
+    float part[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) part[r][m] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      half2_t p[R][4];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t d = w[r][j];
+        p[r][0] = nibble_pair16<0>(d, exp16);
+        p[r][1] = nibble_pair16<1>(d, exp16);
+        p[r][2] = nibble_pair16<2>(d, exp16);
+        p[r][3] = nibble_pair16<3>(d, exp16);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int m = 0; m < M; ++m)
+            part[r][m] = __builtin_fmaf((float)p[r][i].x, x[m][2 * j][i], part[r][m]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int m = 0; m < M; ++m)
+            part[r][m] = __builtin_fmaf((float)p[r][i].y, x[m][2 * j + 1][i], part[r][m]);
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float total = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        total += x[m][q].x; total += x[m][q].y; total += x[m][q].z; total += x[m][q].w;
+      }
+      const float c = a.unit_bias * total;
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r][m] = s[r] * (part[r][m] - c);
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = wave_sum_to_last(acc[r][m]);
+
+  if (a.ksplit == 1) {
+    if (lane == 63) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (row0 + r < a.N)
+#pragma unroll
+          for (int m = 0; m < M; ++m) a.out[(size_t)m * a.out_stride + row0 + r] = acc[r][m];
+    }
+    return;
+  }
+  if (lane == 63) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) red[wave][r][m] = acc[r][m];
+  }
+  __syncthreads();
+  if (ks == 0 && lane < R * M) {
+    const int r = lane / M;
+    const int m = lane - r * M;
+    float total = 0.0f;
+    for (int k = 0; k < a.ksplit; ++k) total += red[wave + k][r][m];
+    if (row0 + r < a.N) a.out[(size_t)m * a.out_stride + row0 + r] = total;
+  }
+}
+
+template <int M, int R>
+static hipError_t gemv_reg_launch(const GemvArgs &a, hipStream_t stream) {
+  const int tiles = (a.N + R - 1) / R;
+  const int tiles_per_block = 4 / a.ksplit;
+  dim3 grid((tiles + tiles_per_block - 1) / tiles_per_block);
+  hipLaunchKernelGGL((gemv_q4_reg_kernel<M, R>), grid, dim3(kGemvThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
 template <int M, int R>
 static size_t gemv_lds_bytes(int units) {
   return (size_t)M * units * (8 * sizeof(float4_t) + sizeof(float)) + sizeof(float) * 4 * R * M;
@@ -280,6 +416,21 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
   a.K = K;
   a.unit_bias = 16.0f + (float)code_bias;
   a.act_vec = ((((uintptr_t)act) & 15u) == 0 && (act_stride & 3) == 0) ? 1 : 0;
+  // One and two lanes with at most 256 units a row: the register form, with
+  // enough waves on a row tile that each lane holds one unit.
+  if (lanes <= 2 && K / 32 <= 4 * kWave) {
+    const int units = K / 32;
+    const int R = 4;
+    const int tiles = (N + R - 1) / R;
+    int ksplit = 1;
+    while (ksplit < 4 && (units > ksplit * kWave || (tiles * ksplit < 2048 && units / (ksplit * 2) >= 32)))
+      ksplit *= 2;
+    a.ksplit = ksplit;
+    a.chunk_cols = K;
+    a.out = out;
+    a.out_stride = out_stride;
+    return lanes == 1 ? gemv_reg_launch<1, 4>(a, stream) : gemv_reg_launch<2, 4>(a, stream);
+  }
   a.chunk_cols = igl_gemv_chunk_cols(lanes, K, lds_limit);
   const int chunks = (K + a.chunk_cols - 1) / a.chunk_cols;
   const int R = igl_gemv_rows_per_tile(lanes);
