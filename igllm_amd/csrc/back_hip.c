@@ -78,6 +78,10 @@ const char *igl_code_text(int code) {
   }
 }
 
+void *igl_desk_stream(igl_desk *desk) {
+  return desk && desk->state ? (void *)desk->state->stream : NULL;
+}
+
 int igl_desk_error_take(igl_desk *desk) {
   int code;
   if (!desk || !desk->state) return IGL_FAIL_STATE;
@@ -325,16 +329,19 @@ int igl_gemm_bf16_dev(igl_desk *desk, const igl_plane *sheet, const uint16_t *ac
 
 /* ---- attention and cache ------------------------------------------------- */
 
-int igl_attend_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t *value_store,
-                   int format, float key_scale, float value_scale, int cache_span,
-                   int kv_count, int group_share, int head_size, const float *query_dev,
-                   int place_start, int span_count, float score_scale, float *blend_out_dev) {
+int igl_attend_lanes_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t *value_store,
+                         int format, float key_scale, float value_scale, int cache_span,
+                         int kv_count, int group_share, int head_size, const float *query_dev,
+                         int lane_stride, int place_first, int window, int lane_count,
+                         float score_scale, float *blend_out_dev) {
   igl_desk_state *st = desk ? desk->state : NULL;
   size_t need;
-  int kv_width;
+  int kv_width, widest;
   if (!st) return IGL_FAIL_STATE;
+  widest = window > 0 && window < place_first + lane_count ? window : place_first + lane_count;
   if (!key_store || !value_store || !query_dev || !blend_out_dev || kv_count < 1 ||
-      cache_span < 1 || span_count < 1 || span_count > cache_span || place_start < 0 ||
+      cache_span < 1 || lane_count < 1 || place_first < 0 || window < 0 || widest > cache_span ||
+      (lane_count > 1 && lane_stride < kv_count * group_share * head_size) ||
       (format != IGL_CACHE_E4M3 && format != IGL_CACHE_INT8)) {
     desk_fail(st, IGL_FAIL_ARGUMENT);
     return IGL_FAIL_ARGUMENT;
@@ -348,12 +355,27 @@ int igl_attend_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t *valu
     desk_fail(st, IGL_FAIL_ARGUMENT);
     return IGL_FAIL_ARGUMENT;
   }
-  need = igl_attend_work_floats(span_count, kv_count * group_share, head_size);
+  need = igl_attend_work_floats(place_first, window, lane_count, kv_count * group_share, head_size);
   if (grow_dev(st, &st->work_dev, &st->work_floats, need) != IGL_OKAY) return IGL_FAIL_MEMORY;
   return hip_check(st, igl_launch_attend(key_store, value_store, format, key_scale, value_scale,
                                          cache_span, kv_width, kv_count, group_share, head_size,
-                                         query_dev, place_start, span_count, score_scale,
-                                         blend_out_dev, st->work_dev, st->stream));
+                                         query_dev, lane_stride, place_first, window, lane_count,
+                                         score_scale, blend_out_dev, st->work_dev, st->stream));
+}
+
+int igl_attend_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t *value_store,
+                   int format, float key_scale, float value_scale, int cache_span,
+                   int kv_count, int group_share, int head_size, const float *query_dev,
+                   int place_start, int span_count, float score_scale, float *blend_out_dev) {
+  if (desk && desk->state && (span_count < 1 || place_start < 0)) {
+    desk_fail(desk->state, IGL_FAIL_ARGUMENT);
+    return IGL_FAIL_ARGUMENT;
+  }
+  /* One lane whose window is exactly its span: it sits at place_start + span - 1. */
+  return igl_attend_lanes_dev(desk, key_store, value_store, format, key_scale, value_scale,
+                              cache_span, kv_count, group_share, head_size, query_dev, 0,
+                              place_start + span_count - 1, span_count, 1, score_scale,
+                              blend_out_dev);
 }
 
 int igl_cache_lay_dev(igl_desk *desk, const float *row_dev, int width, float scale, int format,

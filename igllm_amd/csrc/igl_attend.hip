@@ -49,9 +49,11 @@ struct AttendArgs {
   const uint8_t *value_store;
   int kv_width;
   int cache_span;
-  int place_start;
-  int span_count;
-  const float *query;          // [head_count][HEAD]
+  int place0;                  // position of lane 0; lane l is at place0 + l
+  int window;                  // positions a lane sees (0: all from position 0)
+  int chunks;                  // chunk slots per lane in the partial buffers
+  int q_stride;                // floats between lanes of query / blend
+  const float *query;          // [lanes][head_count][HEAD]
   float key_scale;             // decoded-byte multiplier, score_scale folded in
   float value_scale;
   float *part_out;             // [chunks][head_count][HEAD]
@@ -107,14 +109,22 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
   const int kv = blockIdx.y;
   const int head0 = kv * kAttendGroup;
   const int chunk = blockIdx.x;
+  const int lane_id = blockIdx.z;
+  // The lane's visible positions: the last `window` up to and including its
+  // own (session_attend 11516-11526); `start` is the first, ring slot p % span.
+  const int pos = a.place0 + lane_id;
+  const int span_count = a.window > 0 ? min(pos + 1, a.window) : pos + 1;
+  const int place_start = pos - span_count + 1;
+  if (chunk * kAttendChunk >= span_count) return;  // the whole block is past this lane's span
+  const int pc = lane_id * a.chunks + chunk;
   const int t0 = chunk * kAttendChunk + wave * kAttendTile;
-  const bool live = t0 < a.span_count;
+  const bool live = t0 < span_count;
   const size_t kv_off = (size_t)kv * HEAD;
 
   // ---- query operands: row n is head (n & 7), hi part (n < 8) or lo part.
   half8_t qa[S];
   {
-    const float *q = a.query + (size_t)(head0 + (n & 7)) * HEAD + QD * g;
+    const float *q = a.query + (size_t)lane_id * a.q_stride + (size_t)(head0 + (n & 7)) * HEAD + QD * g;
     const bool lo_part = n >= 8;
 #pragma unroll
     for (int s = 0; s < S; ++s)
@@ -132,8 +142,8 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
   if (live) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int t = min(t0 + n + 16 * j, a.span_count - 1);
-      const int slot = (a.place_start + t) % a.cache_span;
+      const int t = min(t0 + n + 16 * j, span_count - 1);
+      const int slot = (place_start + t) % a.cache_span;
       const uint4_t *row = reinterpret_cast<const uint4_t *>(
           a.key_store + (size_t)slot * a.kv_width + kv_off + QD * g);
       uint4_t kr[QD / 16];
@@ -149,8 +159,8 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
     // value rows: lane -> row lane/2, half lane&1
     {
       const int r = lane >> 1;
-      const int t = min(t0 + r, a.span_count - 1);
-      const int slot = (a.place_start + t) % a.cache_span;
+      const int t = min(t0 + r, span_count - 1);
+      const int slot = (place_start + t) % a.cache_span;
       const uint2_t *src = reinterpret_cast<const uint2_t *>(
           a.value_store + (size_t)slot * a.kv_width + kv_off + (lane & 1) * (HEAD / 2));
       uint2_t *dst = reinterpret_cast<uint2_t *>(vw + r * VPITCH + (lane & 1) * (HEAD / 2));
@@ -168,8 +178,8 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
   for (int r = 0; r < 4; ++r) {
     float s0 = sacc[0][r] + xor32(sacc[0][r]);
     float s1 = sacc[1][r] + xor32(sacc[1][r]);
-    s0 = (t0 + n < a.span_count) ? s0 * a.key_scale : -INFINITY;
-    s1 = (t0 + n + 16 < a.span_count) ? s1 * a.key_scale : -INFINITY;
+    s0 = (t0 + n < span_count) ? s0 * a.key_scale : -INFINITY;
+    s1 = (t0 + n + 16 < span_count) ? s1 * a.key_scale : -INFINITY;
     float m = row16_max(fmaxf(s0, s1));
     if (!live) m = -INFINITY;
     const float p0 = live ? __expf(s0 - m) : 0.0f;
@@ -261,7 +271,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
     const int d = i - h * HEAD;
     const float v = ((ob[(0 * kAttendGroup + h) * HEAD + d] + ob[(1 * kAttendGroup + h) * HEAD + d]) +
                      ob[(2 * kAttendGroup + h) * HEAD + d]) + ob[(3 * kAttendGroup + h) * HEAD + d];
-    a.part_out[((size_t)chunk * a.head_count + head0 + h) * HEAD + d] = v * a.value_scale;
+    a.part_out[((size_t)pc * a.head_count + head0 + h) * HEAD + d] = v * a.value_scale;
   }
   if (tid < kAttendGroup) {
     const int h = tid;
@@ -270,21 +280,31 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
 #pragma unroll
     for (int w = 0; w < 4; ++w)
       if (wm[w][h] != -INFINITY) L += wl[w][h] * __expf(wm[w][h] - M);
-    a.part_peak[(size_t)chunk * a.head_count + head0 + h] = M;
-    a.part_total[(size_t)chunk * a.head_count + head0 + h] = L;
+    a.part_peak[(size_t)pc * a.head_count + head0 + h] = M;
+    a.part_total[(size_t)pc * a.head_count + head0 + h] = L;
   }
 }
 
-// Merges chunk partials: one workgroup per head; chunk weights once in LDS,
-// then every thread sums its dims over the chunks in chunk order.
-__global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out,
-                                                           const float *part_peak,
-                                                           const float *part_total, int chunks,
+// Merges chunk partials: one workgroup per (head, lane); chunk weights once in
+// LDS, then every thread sums its dims over the chunks in chunk order.
+__global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out_all,
+                                                           const float *part_peak_all,
+                                                           const float *part_total_all,
+                                                           int chunk_slots, int place0, int window,
                                                            int head_count, int head_size,
-                                                           float *blend_out) {
+                                                           float *blend_all, int o_stride) {
   extern __shared__ float wgt[];  // [chunks]
   __shared__ float red[256];
   const int h = blockIdx.x;
+  const int lane = blockIdx.y;
+  const int pos = place0 + lane;
+  const int span = window > 0 ? min(pos + 1, window) : pos + 1;
+  const int chunks = (span + kAttendChunk - 1) / kAttendChunk;
+  const size_t base = (size_t)lane * chunk_slots;
+  const float *part_out = part_out_all + base * head_count * head_size;
+  const float *part_peak = part_peak_all + base * head_count;
+  const float *part_total = part_total_all + base * head_count;
+  float *blend_out = blend_all + (size_t)lane * o_stride;
   float peak = -INFINITY;
   for (int c = threadIdx.x; c < chunks; c += blockDim.x)
     peak = fmaxf(peak, part_peak[(size_t)c * head_count + h]);
@@ -330,32 +350,44 @@ using namespace igl;
 
 extern "C" int igl_attend_chunk_size(void) { return kAttendChunk; }
 
+static int attend_max_span(int place0, int window, int lanes) {
+  const int last = place0 + lanes;  // span of the last lane when unwindowed
+  return window > 0 ? (last < window ? last : window) : last;
+}
+
+// `lanes` query lanes at positions place0 .. place0 + lanes - 1, each seeing
+// the last `window` positions up to its own (0: every position from 0).  Lane
+// l's query and output are `q_stride` floats after lane l - 1's.
 extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t *value_store,
                                         int fmt, float key_scale, float value_scale,
                                         int cache_span, int kv_width, int kv_count,
                                         int group_share, int head_size, const float *query,
-                                        int place_start, int span_count, float score_scale,
-                                        float *blend_out, float *work, hipStream_t stream) {
+                                        int q_stride, int place0, int window, int lanes,
+                                        float score_scale, float *blend_out, float *work,
+                                        hipStream_t stream) {
   AttendArgs a;
-  const int chunks = (span_count + kAttendChunk - 1) / kAttendChunk;
+  const int chunks = (attend_max_span(place0, window, lanes) + kAttendChunk - 1) / kAttendChunk;
   const int head_count = kv_count * group_share;
-  if (group_share != kAttendGroup) return hipErrorInvalidValue;
+  if (group_share != kAttendGroup || lanes < 1) return hipErrorInvalidValue;
   a.key_store = key_store;
   a.value_store = value_store;
   a.kv_width = kv_width;
   a.cache_span = cache_span;
-  a.place_start = place_start;
-  a.span_count = span_count;
+  a.place0 = place0;
+  a.window = window;
+  a.chunks = chunks;
+  a.q_stride = q_stride;
   a.query = query;
   // e4m3 decodes to real8 / 256; the 256 goes back in with the scale.
   const float unit = fmt == 0 ? 256.0f : 1.0f;
   a.key_scale = key_scale * unit * score_scale;
   a.value_scale = value_scale * unit;
   a.head_count = head_count;
+  const size_t slots = (size_t)lanes * chunks;
   a.part_out = work;
-  a.part_peak = work + (size_t)chunks * head_count * head_size;
-  a.part_total = a.part_peak + (size_t)chunks * head_count;
-  dim3 grid(chunks, kv_count);
+  a.part_peak = work + slots * head_count * head_size;
+  a.part_total = a.part_peak + slots * head_count;
+  dim3 grid(chunks, kv_count, lanes);
   if (head_size == 256 && fmt == 0)
     hipLaunchKernelGGL((attend_mfma_kernel<256, 0>), grid, dim3(kAttendThreads), 0, stream, a);
   else if (head_size == 256 && fmt == 1)
@@ -368,14 +400,16 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
     return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attend_merge_kernel, dim3(head_count), dim3(256), chunks * sizeof(float),
-                     stream, a.part_out, a.part_peak, a.part_total, chunks, head_count, head_size,
-                     blend_out);
+  hipLaunchKernelGGL(attend_merge_kernel, dim3(head_count, lanes), dim3(256),
+                     chunks * sizeof(float), stream, a.part_out, a.part_peak, a.part_total, chunks,
+                     place0, window, head_count, head_size, blend_out, q_stride);
   return hipGetLastError();
 }
 
-// Floats of workspace igl_launch_attend needs.
-extern "C" size_t igl_attend_work_floats(int span_count, int head_count, int head_size) {
-  const size_t chunks = (size_t)((span_count + kAttendChunk - 1) / kAttendChunk);
-  return chunks * (size_t)head_count * ((size_t)head_size + 2);
+// Floats of workspace igl_launch_attend needs for the same arguments.
+extern "C" size_t igl_attend_work_floats(int place0, int window, int lanes, int head_count,
+                                         int head_size) {
+  const size_t chunks =
+      (size_t)((attend_max_span(place0, window, lanes) + kAttendChunk - 1) / kAttendChunk);
+  return (size_t)lanes * chunks * (size_t)head_count * ((size_t)head_size + 2);
 }

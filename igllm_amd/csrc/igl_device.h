@@ -82,4 +82,69 @@ __device__ __forceinline__ half2_t nibble_pair16(uint32_t d, uint32_t exp16) {
   return as_half2(and_or_b32(moved, 0x03C003C0u, exp16));
 }
 
+// e4m3 grid rounding of a value already divided by its scale: nearest, ties
+// to even, saturating at +-448 (and NaN to +448); below 2^-6 steps of 2^-9; a
+// negative that rounds to zero is +0 (cache_pack8/cache_code8,
+// app_core.c:10980-11016).
+__device__ __forceinline__ uint8_t e4m3_code(float value) {
+  const float top = 448.0f, norm = 1.0f / 64.0f, step = 1.0f / 512.0f;
+  uint8_t sign = 0;
+  float mag = value;
+  if (value < 0.0f) { sign = 0x80u; mag = -value; }
+  if (!(mag < top)) return (uint8_t)(sign | 0x7Eu);
+  if (mag < norm) {
+    const float lv = __builtin_rintf(mag / step);
+    if (lv == 0.0f) return 0x00u;
+    if (lv >= 8.0f) return (uint8_t)(sign | 0x08u);  // rounded up to 2^-6
+    return (uint8_t)(sign | (uint8_t)lv);
+  }
+  int power;
+  (void)frexpf(mag, &power);  // mag in [2^(power-1), 2^power)
+  const float unit = ldexpf(1.0f, power - 4);
+  float r = __builtin_rintf(mag / unit) * unit;
+  if (r > top) r = top;
+  (void)frexpf(r, &power);
+  const int mant = (int)(ldexpf(r, 4 - power) + 0.5f) - 8;
+  return (uint8_t)(sign | (uint8_t)((power + 6) << 3) | (uint8_t)mant);
+}
+
+// int8 bytes: rint(value / scale) clamped to +-127, two's complement.
+__device__ __forceinline__ uint8_t int8_code(float value, float scale) {
+  float level = __builtin_rintf(value / scale);
+  if (!(level > -127.0f)) level = -127.0f;
+  if (level > 127.0f) level = 127.0f;
+  return (uint8_t)(int8_t)level;
+}
+
+// The reference's series exponential (kern_exp_near, app_core.c:4739-4777):
+// 2^k e^r, k the nearest integer to x / ln 2, r reduced in two pieces of ln 2,
+// e^r by its Taylor series to the seventh term, arguments below -87 floored.
+__device__ __forceinline__ float exp_near(float x) {
+  if (x < -87.0f) x = -87.0f;
+  const float stepped = x * 1.4426950408889634f + 0.5f;
+  float whole = (float)(int)stepped;
+  if (whole > stepped) whole -= 1.0f;
+  float rest = x - whole * 0.693359375f;
+  rest -= whole * -2.1219444005469057e-4f;
+  float poly = 1.0f / 5040.0f;
+  poly = poly * rest + 1.0f / 720.0f;
+  poly = poly * rest + 1.0f / 120.0f;
+  poly = poly * rest + 1.0f / 24.0f;
+  poly = poly * rest + 1.0f / 6.0f;
+  poly = poly * rest + 1.0f / 2.0f;
+  poly = poly * rest + 1.0f;
+  poly = poly * rest + 1.0f;
+  return poly * __builtin_bit_cast(float, (uint32_t)((int)whole + 127) << 23);
+}
+
+// gelu_tanh(x) = x t / (t + 1), t = e^(2 sqrt(2/pi)(x + 0.044715 x^3)); zero
+// at or below 2y = -30, t clamped at 2y = 30 (kern_gelu_tanh, 5105-5118).
+__device__ __forceinline__ float gelu_near(float x) {
+  const float cube = x * x * x;
+  const float turn = 2.0f * 0.7978845608028654f * (x + 0.044715f * cube);
+  if (!(turn > -30.0f)) return x * 0.0f;
+  const float t = exp_near(turn > 30.0f ? 30.0f : turn);
+  return x * (t / (t + 1.0f));
+}
+
 }  // namespace igl

@@ -69,16 +69,7 @@ __global__ void soft_max_kernel(float *v, int n, int stride) {
 __global__ void gelu_gate_kernel(float *gate, const float *rise, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const float x = gate[i];
-  const float turn = 2.0f * 0.7978845608028654f * (x + 0.044715f * (x * x * x));
-  float g;
-  if (!(turn > -30.0f)) {
-    g = x * 0.0f;
-  } else {
-    const float t = __expf(fminf(turn, 30.0f));
-    g = x * (t / (t + 1.0f));
-  }
-  gate[i] = g * rise[i];
+  gate[i] = gelu_near(gate[i]) * rise[i];
 }
 
 // Rotate-half RoPE on `heads` heads of `head_size` (kern_rope_turn,
@@ -96,44 +87,12 @@ __global__ void rope_turn_kernel(float *v, int heads, int head_size, const float
   x[j + half] = hi * cosv[j] + lo * sinv[j];
 }
 
-// e4m3 grid rounding of value/scale: nearest, ties to even, saturating at
-// +-448; below 2^-6 steps of 2^-9 (cache_pack8/cache_code8,
-// app_core.c:10980-11016).
-__device__ __forceinline__ uint8_t code8(float value) {
-  const float top = 448.0f, norm = 1.0f / 64.0f, step = 1.0f / 512.0f;
-  uint8_t sign = 0;
-  float mag = value;
-  if (value < 0.0f) { sign = 0x80u; mag = -value; }
-  if (!(mag < top)) return (uint8_t)(sign | 0x7Eu);  // 448 (and NaN) saturate
-  if (mag < norm) {
-    const float lv = __builtin_rintf(mag / step);
-    if (lv == 0.0f) return 0x00u;  // a negative that rounds to zero is stored as +0
-    if (lv >= 8.0f) return (uint8_t)(sign | 0x08u);  // rounded up to 2^-6
-    return (uint8_t)(sign | (uint8_t)lv);
-  }
-  int power;
-  (void)frexpf(mag, &power);  // mag in [2^(power-1), 2^power)
-  const float unit = ldexpf(1.0f, power - 4);
-  float r = __builtin_rintf(mag / unit) * unit;
-  if (r > top) r = top;
-  (void)frexpf(r, &power);
-  const int mant = (int)(ldexpf(r, 4 - power) + 0.5f) - 8;
-  return (uint8_t)(sign | (uint8_t)((power + 6) << 3) | (uint8_t)mant);
-}
-
-__device__ __forceinline__ uint8_t code_i8(float value, float scale) {
-  float level = __builtin_rintf(value / scale);
-  if (!(level > -127.0f)) level = -127.0f;
-  if (level > 127.0f) level = 127.0f;
-  return (uint8_t)(int8_t)level;
-}
-
 // Writes `width` values of `row` into ring slot `slot` of a byte store.
 __global__ void cache_lay_kernel(const float *row, int width, float scale, int fmt, uint8_t *store,
                                  size_t slot_first) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= width) return;
-  store[slot_first + i] = fmt == 0 ? code8(row[i] / scale) : code_i8(row[i], scale);
+  store[slot_first + i] = fmt == 0 ? e4m3_code(row[i] / scale) : int8_code(row[i], scale);
 }
 
 }  // namespace igl

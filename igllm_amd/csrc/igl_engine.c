@@ -1,0 +1,728 @@
+/* igl_engine.c - a device-resident decode session for the Gemma 4 text stack
+ * on this backend.
+ *
+ * It restates the reference's session graph (session_pass app_core.c:11843-
+ * 11975, session_layer 11637-11743, session_attend 11455-11580) with every
+ * activation and the key/value cache held in HBM, so a decode step crosses
+ * the host boundary twice: the token id in, the greedy pick out.  The weights
+ * are the checkpoint's payload copied to the device unchanged; every plane is
+ * a view into that copy (the reference's plane_bind_gemma layout, 7886-7955).
+ *
+ * What it reads: config.json (the text_config fields config_read reads,
+ * 8325-8475) and model.safetensors (U8 code planes with F32 group scales, F32
+ * norm gains and scalars).  What it supports is what the kernels take: 4-bit
+ * planes, one key/value head per 8 query heads, heads of 256 or 512, a byte
+ * key/value cache (every owning layer ships k/v_cache_scale).  Anything else is
+ * refused at open with IGL_FAIL_SUPPORT.
+ *
+ * Differences of arrangement, none of arithmetic: a batch of lanes writes all
+ * its keys and values before any of them attends (the reference interleaves
+ * lane by lane, 11481-11483), so a sliding layer's ring is `window + lanes`
+ * rows deep instead of `window`, which keeps every row a lane can see; the
+ * attention and norms reduce in their own order.
+ */
+#define _POSIX_C_SOURCE 200809L
+#include <ctype.h>
+#include <fcntl.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include "igl_backend.h"
+#include "igl_launch.h"
+
+#define ENG_LAYER_LIMIT 128
+#define ENG_TENSOR_LIMIT 4096
+
+typedef struct eng_tensor {
+  char      name[160];
+  int       dtype;     /* 0 U8, 1 F32, -1 other */
+  int       rank;
+  long long shape[3];
+  size_t    begin, end;
+} eng_tensor;
+
+typedef struct eng_layer {
+  int full, shared, source, keep, head_size, inner, cache_span;
+  igl_plane q, k, v, o, gate, up, down, ple_gate, ple_proj;
+  const float *q_norm, *k_norm, *enter_norm, *after_attn, *before_ff, *after_ff, *after_ple;
+  float layer_gain, k_scale, v_scale;
+  uint8_t *k_store, *v_store;
+} eng_layer;
+
+struct igl_engine {
+  igl_desk   *desk;
+  hipStream_t stream;
+  int vocab, hidden, layers, heads, kv_heads, window, ple, share_count;
+  float eps, cap;
+  int window_limit, lane_limit, fill, precise;
+  int turns[2], halves[2];
+  float *steps_dev[2];
+  /* the checkpoint */
+  void   *map;
+  size_t  map_bytes;
+  size_t  payload_at;
+  eng_tensor *tensor;
+  int     tensor_count;
+  uint8_t *payload_dev;
+  size_t   payload_bytes;
+  igl_plane embed, ple_embed, ple_lift, head;
+  const float *ple_norm, *final_norm;
+  eng_layer layer[ENG_LAYER_LIMIT];
+  /* device rooms, lane_limit lanes each */
+  int32_t *ids_dev;
+  float *state, *scrap, *lift, *q, *k, *v, *blend, *gate, *rise, *ple_seed, *ple_room, *logits;
+  int q_stride, kv_stride, inner_max, ple_stride;
+  void *pick_work;
+  int32_t *pick_dev;
+  float *margin_dev;
+};
+
+/* ---- a little JSON, enough for config.json and a safetensors header ------ */
+
+static const char *skip_ws(const char *p) {
+  while (*p && isspace((unsigned char)*p)) ++p;
+  return p;
+}
+
+/* End of the JSON value starting at p (string, number, literal, object or list). */
+static const char *value_end(const char *p) {
+  int depth = 0;
+  p = skip_ws(p);
+  if (*p == '"') {
+    for (++p; *p && *p != '"'; ++p)
+      if (*p == '\\' && p[1]) ++p;
+    return *p ? p + 1 : p;
+  }
+  if (*p != '{' && *p != '[') {
+    while (*p && *p != ',' && *p != '}' && *p != ']') ++p;
+    return p;
+  }
+  for (; *p; ++p) {
+    if (*p == '"') {
+      for (++p; *p && *p != '"'; ++p)
+        if (*p == '\\' && p[1]) ++p;
+      if (!*p) return p;
+    } else if (*p == '{' || *p == '[') {
+      ++depth;
+    } else if (*p == '}' || *p == ']') {
+      if (--depth == 0) return p + 1;
+    }
+  }
+  return p;
+}
+
+/* The value of member `key` directly inside the object [obj, obj_end). */
+static const char *member(const char *obj, const char *obj_end, const char *key) {
+  const char *p = skip_ws(obj);
+  size_t klen = strlen(key);
+  if (*p != '{') return NULL;
+  ++p;
+  while (p < obj_end) {
+    const char *name;
+    p = skip_ws(p);
+    if (*p != '"') return NULL;
+    name = p + 1;
+    p = value_end(p);
+    p = skip_ws(p);
+    if (*p != ':') return NULL;
+    p = skip_ws(p + 1);
+    if ((size_t)(p - name) >= klen + 2 && strncmp(name, key, klen) == 0 && name[klen] == '"') return p;
+    p = skip_ws(value_end(p));
+    if (*p == ',') ++p;
+    else return NULL;
+  }
+  return NULL;
+}
+
+static double member_number(const char *obj, const char *key, double spare) {
+  const char *v = member(obj, value_end(obj), key);
+  if (!v) return spare;
+  if (*v == 't') return 1.0;
+  if (*v == 'f') return 0.0;
+  if (*v == '[') v = skip_ws(v + 1);
+  return strtod(v, NULL);
+}
+
+static char *read_text(const char *path) {
+  FILE *f = fopen(path, "rb");
+  long n;
+  char *text;
+  if (!f) return NULL;
+  fseek(f, 0, SEEK_END);
+  n = ftell(f);
+  fseek(f, 0, SEEK_SET);
+  text = (char *)malloc((size_t)n + 1);
+  if (text && fread(text, 1, (size_t)n, f) != (size_t)n) {
+    free(text);
+    text = NULL;
+  }
+  if (text) text[n] = '\0';
+  fclose(f);
+  return text;
+}
+
+/* ---- the checkpoint ------------------------------------------------------ */
+
+static int parse_header(igl_engine *e, const char *h, size_t len) {
+  const char *p = skip_ws(h), *end = h + len;
+  if (*p != '{') return IGL_FAIL_FORMAT;
+  ++p;
+  e->tensor = (eng_tensor *)calloc(ENG_TENSOR_LIMIT, sizeof(eng_tensor));
+  if (!e->tensor) return IGL_FAIL_MEMORY;
+  while (p < end) {
+    const char *name, *obj, *obj_end, *v;
+    size_t nlen;
+    p = skip_ws(p);
+    if (*p == '}') break;
+    if (*p != '"') return IGL_FAIL_FORMAT;
+    name = p + 1;
+    p = value_end(p);
+    nlen = (size_t)(p - 1 - name);
+    p = skip_ws(p);
+    if (*p != ':') return IGL_FAIL_FORMAT;
+    obj = skip_ws(p + 1);
+    obj_end = value_end(obj);
+    if (!(nlen == 12 && strncmp(name, "__metadata__", 12) == 0)) {
+      eng_tensor *t;
+      if (e->tensor_count >= ENG_TENSOR_LIMIT || nlen >= sizeof(t->name)) return IGL_FAIL_SUPPORT;
+      t = &e->tensor[e->tensor_count++];
+      memcpy(t->name, name, nlen);
+      t->name[nlen] = '\0';
+      v = member(obj, obj_end, "dtype");
+      t->dtype = !v ? -1 : strncmp(v, "\"U8\"", 4) == 0 ? 0 : strncmp(v, "\"F32\"", 5) == 0 ? 1 : -1;
+      v = member(obj, obj_end, "shape");
+      if (!v || *v != '[') return IGL_FAIL_FORMAT;
+      ++v;
+      while (1) {
+        v = skip_ws(v);
+        if (*v == ']') break;
+        if (t->rank >= 3) return IGL_FAIL_SUPPORT;
+        t->shape[t->rank++] = strtoll(v, (char **)&v, 10);
+        v = skip_ws(v);
+        if (*v == ',') ++v;
+      }
+      v = member(obj, obj_end, "data_offsets");
+      if (!v || *v != '[') return IGL_FAIL_FORMAT;
+      t->begin = (size_t)strtoull(v + 1, (char **)&v, 10);
+      v = skip_ws(v);
+      if (*v == ',') ++v;
+      t->end = (size_t)strtoull(v, NULL, 10);
+    }
+    p = skip_ws(obj_end);
+    if (*p == ',') ++p;
+  }
+  return IGL_OKAY;
+}
+
+static const eng_tensor *find_tensor(const igl_engine *e, const char *name) {
+  for (int i = 0; i < e->tensor_count; ++i)
+    if (strcmp(e->tensor[i].name, name) == 0) return &e->tensor[i];
+  return NULL;
+}
+
+static const char *k_prefix[] = {"model.language_model.", "language_model.model.", "model.", ""};
+
+static const eng_tensor *find_stem(const igl_engine *e, const char *stem, const char *leaf) {
+  char name[256];
+  snprintf(name, sizeof(name), "%s.%s", stem, leaf);
+  return find_tensor(e, name);
+}
+
+/* A 4-bit code plane in the export's layout (plane_bind_gemma, 7886-7955):
+ * `weight` (or `embedding_quantized`) U8 [rows, cols/2] + its F32 scale
+ * [rows, groups]; bound in place on the device copy of the payload. */
+static int bind_plane(igl_engine *e, const char *stem, int col_hint, igl_plane *out) {
+  const eng_tensor *w = find_stem(e, stem, "embedding_quantized");
+  const eng_tensor *s = w ? find_stem(e, stem, "embedding_scale") : NULL;
+  if (!w) {
+    w = find_stem(e, stem, "weight");
+    s = find_stem(e, stem, "weight_scale");
+  }
+  if (!w || !s) return IGL_FAIL_MISSING;
+  if (w->dtype != 0 || s->dtype != 1 || w->rank != 2 || s->rank != 2) return IGL_FAIL_SUPPORT;
+  if (w->shape[1] * 2 != col_hint) return IGL_FAIL_SUPPORT; /* 4 bits a code only */
+  memset(out, 0, sizeof(*out));
+  out->form = IGL_PLANE_CODE;
+  out->row_count = (int)w->shape[0];
+  out->col_count = col_hint;
+  out->code_data = (const uint8_t *)e->map + e->payload_at + w->begin;
+  out->row_stride = (size_t)w->shape[1];
+  out->gain_data = (const uint8_t *)e->map + e->payload_at + s->begin;
+  out->gain_type = IGL_STORE_F32;
+  out->bit_count = 4;
+  out->code_bias = 8;
+  out->group_count = (int)s->shape[1];
+  out->group_size = col_hint / out->group_count;
+  return igl_plane_bind_dev(e->desk, out, e->payload_dev + w->begin,
+                            (const float *)(e->payload_dev + s->begin));
+}
+
+static const float *bind_vector(igl_engine *e, const char *stem, int n) {
+  const eng_tensor *t = find_stem(e, stem, "weight");
+  if (!t) t = find_tensor(e, stem);
+  if (!t || t->dtype != 1 || (long long)(t->end - t->begin) != 4LL * n) return NULL;
+  return (const float *)(e->payload_dev + t->begin);
+}
+
+static float read_scalar(const igl_engine *e, const char *name, float spare) {
+  const eng_tensor *t = find_tensor(e, name);
+  float v;
+  if (!t || t->dtype != 1 || t->end - t->begin != 4) return spare;
+  memcpy(&v, (const uint8_t *)e->map + e->payload_at + t->begin, 4);
+  return v;
+}
+
+/* rope_build (8121-8145): inverse frequencies 1/theta^(2i/d) in double, as
+ * float; "proportional" rotates only partial * d / 2 pairs. */
+static int rope_table(igl_engine *e, int kind, int head_size, double theta, double part, int proportional) {
+  int half = head_size / 2, turns = half;
+  float *steps = (float *)calloc((size_t)half, sizeof(float));
+  if (!steps) return IGL_FAIL_MEMORY;
+  if (proportional) {
+    turns = (int)(part * head_size / 2.0);
+    if (turns > half) turns = half;
+    if (turns < 0) turns = 0;
+  }
+  for (int i = 0; i < turns; ++i) steps[i] = (float)(1.0 / pow(theta, (double)(2 * i) / (double)head_size));
+  e->turns[kind] = turns;
+  e->halves[kind] = half;
+  if (hipMalloc((void **)&e->steps_dev[kind], (size_t)half * sizeof(float)) != hipSuccess ||
+      hipMemcpy(e->steps_dev[kind], steps, (size_t)half * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+    free(steps);
+    return IGL_FAIL_DEVICE;
+  }
+  free(steps);
+  return IGL_OKAY;
+}
+
+static int dev_alloc(void **p, size_t bytes) {
+  return hipMalloc(p, bytes ? bytes : 16) == hipSuccess ? IGL_OKAY : IGL_FAIL_MEMORY;
+}
+
+/* ---- open / close ---------------------------------------------------------- */
+
+int igl_engine_open(igl_engine **out, igl_desk *desk, const char *folder, int window_limit,
+                    int lane_limit, int precise) {
+  char path[1024], stem[256];
+  char *config = NULL;
+  const char *text, *rope, *kinds;
+  igl_engine *e;
+  int fd = -1, code = IGL_OKAY;
+  struct stat st;
+  uint64_t header_len = 0;
+  const char *prefix = NULL;
+  double theta[2], part[2];
+  int proportional[2];
+  if (!out || !desk || !desk->state || !folder) return IGL_FAIL_ARGUMENT;
+  *out = NULL;
+  e = (igl_engine *)calloc(1, sizeof(*e));
+  if (!e) return IGL_FAIL_MEMORY;
+  e->desk = desk;
+  e->stream = (hipStream_t)igl_desk_stream(desk);
+  e->lane_limit = lane_limit > 0 ? lane_limit : 16;
+  e->precise = precise;
+
+  /* config.json */
+  snprintf(path, sizeof(path), "%s/config.json", folder);
+  config = read_text(path);
+  if (!config) { code = IGL_FAIL_MISSING; goto fail; }
+  text = member(config, config + strlen(config), "text_config");
+  if (!text) text = skip_ws(config);
+  e->vocab = (int)member_number(text, "vocab_size", 262144);
+  e->hidden = (int)member_number(text, "hidden_size", 2304);
+  e->layers = (int)member_number(text, "num_hidden_layers", 30);
+  e->heads = (int)member_number(text, "num_attention_heads", 8);
+  e->kv_heads = (int)member_number(text, "num_key_value_heads", 4);
+  e->window = (int)member_number(text, "sliding_window", 512);
+  e->ple = (int)member_number(text, "hidden_size_per_layer_input", 256);
+  e->share_count = (int)member_number(text, "num_kv_shared_layers", 0);
+  e->eps = (float)member_number(text, "rms_norm_eps", 1e-6);
+  e->cap = (float)member_number(text, "final_logit_softcapping", 0.0);
+  e->window_limit = (int)member_number(text, "max_position_embeddings", 131072);
+  if (window_limit > 0 && window_limit < e->window_limit) e->window_limit = window_limit;
+  if (e->layers < 1 || e->layers > ENG_LAYER_LIMIT || e->kv_heads != 1 || e->heads != 8) {
+    code = IGL_FAIL_SUPPORT;
+    goto fail;
+  }
+  kinds = member(text, value_end(text), "layer_types");
+  for (int i = 0; i < e->layers; ++i) {
+    int full = ((i + 1) % 6) == 0;
+    if (kinds && *kinds == '[') {
+      const char *p = kinds + 1;
+      for (int j = 0; j <= i && p; ++j) {
+        p = skip_ws(p);
+        if (*p != '"') { p = NULL; break; }
+        if (j == i) full = strncmp(p, "\"sliding_attention\"", 19) != 0;
+        p = skip_ws(value_end(p));
+        if (*p == ',') ++p;
+      }
+    }
+    e->layer[i].full = full;
+  }
+  e->layer[e->layers - 1].full = 1;
+  rope = member(text, value_end(text), "rope_parameters");
+  for (int kind = 0; kind < 2; ++kind) {
+    const char *r = rope ? member(rope, value_end(rope), kind ? "full_attention" : "sliding_attention") : NULL;
+    const char *type = r ? member(r, value_end(r), "rope_type") : NULL;
+    theta[kind] = r ? member_number(r, "rope_theta", kind ? 1e6 : 1e4) : (kind ? 1e6 : 1e4);
+    part[kind] = r ? member_number(r, "partial_rotary_factor", 1.0) : (kind ? 0.25 : 1.0);
+    proportional[kind] = type ? strncmp(type, "\"proportional\"", 14) == 0 : kind == 1;
+  }
+
+  /* model.safetensors, mapped; the payload copied to the device as it lies */
+  snprintf(path, sizeof(path), "%s/model.safetensors", folder);
+  fd = open(path, O_RDONLY);
+  if (fd < 0 || fstat(fd, &st) != 0 || st.st_size < 8) { code = IGL_FAIL_FILE; goto fail; }
+  e->map_bytes = (size_t)st.st_size;
+  e->map = mmap(NULL, e->map_bytes, PROT_READ, MAP_PRIVATE, fd, 0);
+  if (e->map == MAP_FAILED) { e->map = NULL; code = IGL_FAIL_FILE; goto fail; }
+  for (int b = 0; b < 8; ++b) header_len |= (uint64_t)((const uint8_t *)e->map)[b] << (8 * b);
+  if (8 + header_len > e->map_bytes) { code = IGL_FAIL_FORMAT; goto fail; }
+  {
+    char *header = (char *)malloc(header_len + 1);
+    if (!header) { code = IGL_FAIL_MEMORY; goto fail; }
+    memcpy(header, (const uint8_t *)e->map + 8, header_len);
+    header[header_len] = '\0';
+    code = parse_header(e, header, header_len);
+    free(header);
+    if (code != IGL_OKAY) goto fail;
+  }
+  e->payload_at = 8 + header_len;
+  e->payload_bytes = e->map_bytes - e->payload_at;
+  if ((code = dev_alloc((void **)&e->payload_dev, e->payload_bytes)) != IGL_OKAY) goto fail;
+  if (hipMemcpy(e->payload_dev, (const uint8_t *)e->map + e->payload_at, e->payload_bytes,
+                hipMemcpyHostToDevice) != hipSuccess) { code = IGL_FAIL_DEVICE; goto fail; }
+
+  for (size_t c = 0; c < sizeof(k_prefix) / sizeof(k_prefix[0]) && !prefix; ++c) {
+    snprintf(stem, sizeof(stem), "%sembed_tokens", k_prefix[c]);
+    if (find_stem(e, stem, "embedding_quantized") || find_stem(e, stem, "weight")) prefix = k_prefix[c];
+  }
+  if (!prefix) { code = IGL_FAIL_MISSING; goto fail; }
+#define STEM(...) (snprintf(stem, sizeof(stem), __VA_ARGS__), stem)
+  if ((code = bind_plane(e, STEM("%sembed_tokens", prefix), e->hidden, &e->embed)) != IGL_OKAY ||
+      (code = bind_plane(e, STEM("%sembed_tokens_per_layer", prefix), e->layers * e->ple, &e->ple_embed)) != IGL_OKAY ||
+      (code = bind_plane(e, STEM("%sper_layer_model_projection", prefix), e->hidden, &e->ple_lift)) != IGL_OKAY)
+    goto fail;
+  if (bind_plane(e, "lm_head", e->hidden, &e->head) != IGL_OKAY &&
+      bind_plane(e, STEM("%slm_head", prefix), e->hidden, &e->head) != IGL_OKAY)
+    e->head = e->embed;
+  e->vocab = e->head.row_count;
+  e->ple_norm = bind_vector(e, STEM("%sper_layer_projection_norm", prefix), e->ple);
+  e->final_norm = bind_vector(e, STEM("%snorm", prefix), e->hidden);
+  if (!e->ple_norm || !e->final_norm) { code = IGL_FAIL_MISSING; goto fail; }
+
+  {
+    int first_share = e->layers - e->share_count;
+    e->inner_max = 0;
+    e->q_stride = 0;
+    for (int i = 0; i < e->layers; ++i) {
+      eng_layer *L = &e->layer[i];
+      const eng_tensor *t;
+      L->shared = e->share_count > 0 && i >= first_share;
+      L->source = i;
+      if (L->shared) {
+        L->source = -1;
+        for (int j = first_share - 1; j >= 0; --j)
+          if (e->layer[j].full == L->full) { L->source = j; break; }
+        if (L->source < 0) { code = IGL_FAIL_FORMAT; goto fail; }
+      } else {
+        int last = -1;
+        for (int j = 0; j < first_share; ++j)
+          if (e->layer[j].full == L->full) last = j;
+        L->keep = e->share_count > 0 && last == i;
+      }
+      t = find_tensor(e, STEM("%slayers.%d.self_attn.q_proj.weight", prefix, i));
+      if (!t) { code = IGL_FAIL_MISSING; goto fail; }
+      L->head_size = (int)t->shape[0] / e->heads;
+      if (L->head_size != 256 && L->head_size != 512) { code = IGL_FAIL_SUPPORT; goto fail; }
+      t = find_tensor(e, STEM("%slayers.%d.mlp.gate_proj.weight", prefix, i));
+      if (!t) { code = IGL_FAIL_MISSING; goto fail; }
+      L->inner = (int)t->shape[0];
+      if (L->inner > e->inner_max) e->inner_max = L->inner;
+      if (e->heads * L->head_size > e->q_stride) e->q_stride = e->heads * L->head_size;
+      if ((code = bind_plane(e, STEM("%slayers.%d.self_attn.q_proj", prefix, i), e->hidden, &L->q)) ||
+          (code = bind_plane(e, STEM("%slayers.%d.self_attn.o_proj", prefix, i), e->heads * L->head_size, &L->o)) ||
+          (code = bind_plane(e, STEM("%slayers.%d.mlp.gate_proj", prefix, i), e->hidden, &L->gate)) ||
+          (code = bind_plane(e, STEM("%slayers.%d.mlp.up_proj", prefix, i), e->hidden, &L->up)) ||
+          (code = bind_plane(e, STEM("%slayers.%d.mlp.down_proj", prefix, i), L->inner, &L->down)) ||
+          (code = bind_plane(e, STEM("%slayers.%d.per_layer_input_gate", prefix, i), e->hidden, &L->ple_gate)) ||
+          (code = bind_plane(e, STEM("%slayers.%d.per_layer_projection", prefix, i), e->ple, &L->ple_proj)))
+        goto fail;
+      L->q_norm = bind_vector(e, STEM("%slayers.%d.self_attn.q_norm", prefix, i), L->head_size);
+      L->enter_norm = bind_vector(e, STEM("%slayers.%d.input_layernorm", prefix, i), e->hidden);
+      L->after_attn = bind_vector(e, STEM("%slayers.%d.post_attention_layernorm", prefix, i), e->hidden);
+      L->before_ff = bind_vector(e, STEM("%slayers.%d.pre_feedforward_layernorm", prefix, i), e->hidden);
+      L->after_ff = bind_vector(e, STEM("%slayers.%d.post_feedforward_layernorm", prefix, i), e->hidden);
+      L->after_ple = bind_vector(e, STEM("%slayers.%d.post_per_layer_input_norm", prefix, i), e->hidden);
+      if (!L->q_norm || !L->enter_norm || !L->after_attn || !L->before_ff || !L->after_ff || !L->after_ple) {
+        code = IGL_FAIL_MISSING;
+        goto fail;
+      }
+      L->layer_gain = read_scalar(e, STEM("%slayers.%d.layer_scalar", prefix, i), 1.0f);
+      if (!L->shared) {
+        if ((code = bind_plane(e, STEM("%slayers.%d.self_attn.k_proj", prefix, i), e->hidden, &L->k)) ||
+            (code = bind_plane(e, STEM("%slayers.%d.self_attn.v_proj", prefix, i), e->hidden, &L->v)))
+          goto fail;
+        if (L->k.row_count != L->head_size) { code = IGL_FAIL_SUPPORT; goto fail; }
+        L->k_norm = bind_vector(e, STEM("%slayers.%d.self_attn.k_norm", prefix, i), L->head_size);
+        if (!L->k_norm) { code = IGL_FAIL_MISSING; goto fail; }
+        L->k_scale = read_scalar(e, STEM("%slayers.%d.self_attn.k_cache_scale", prefix, i), 0.0f);
+        L->v_scale = read_scalar(e, STEM("%slayers.%d.self_attn.v_cache_scale", prefix, i), 0.0f);
+        if (!(L->k_scale > 0.0f) || !(L->v_scale > 0.0f)) { code = IGL_FAIL_SUPPORT; goto fail; }
+        /* full depth where sharers or the full rule need it; a sliding ring
+         * otherwise, widened by a batch so a batch can write before it reads */
+        L->cache_span = (L->full || L->keep) ? e->window_limit : e->window + e->lane_limit;
+        if (L->cache_span > e->window_limit) L->cache_span = e->window_limit;
+        if ((code = dev_alloc((void **)&L->k_store, (size_t)L->cache_span * L->head_size)) ||
+            (code = dev_alloc((void **)&L->v_store, (size_t)L->cache_span * L->head_size)))
+          goto fail;
+      } else {
+        const eng_layer *S = &e->layer[L->source];
+        if (S->head_size != L->head_size) { code = IGL_FAIL_FORMAT; goto fail; }
+      }
+    }
+  }
+#undef STEM
+  for (int kind = 0; kind < 2; ++kind) {
+    int hs = 0;
+    for (int i = 0; i < e->layers; ++i)
+      if (e->layer[i].full == kind) hs = e->layer[i].head_size;
+    if (hs && (code = rope_table(e, kind, hs, theta[kind], part[kind], proportional[kind])) != IGL_OKAY)
+      goto fail;
+  }
+
+  /* rooms */
+  {
+    size_t lanes = (size_t)e->lane_limit;
+    e->kv_stride = e->q_stride / e->heads;
+    e->ple_stride = e->layers * e->ple;
+    if ((code = dev_alloc((void **)&e->ids_dev, lanes * sizeof(int32_t))) ||
+        (code = dev_alloc((void **)&e->state, lanes * e->hidden * 4)) ||
+        (code = dev_alloc((void **)&e->scrap, lanes * e->hidden * 4)) ||
+        (code = dev_alloc((void **)&e->lift, lanes * e->hidden * 4)) ||
+        (code = dev_alloc((void **)&e->q, lanes * e->q_stride * 4)) ||
+        (code = dev_alloc((void **)&e->blend, lanes * e->q_stride * 4)) ||
+        (code = dev_alloc((void **)&e->k, lanes * e->kv_stride * 4)) ||
+        (code = dev_alloc((void **)&e->v, lanes * e->kv_stride * 4)) ||
+        (code = dev_alloc((void **)&e->gate, lanes * e->inner_max * 4)) ||
+        (code = dev_alloc((void **)&e->rise, lanes * e->inner_max * 4)) ||
+        (code = dev_alloc((void **)&e->ple_seed, lanes * e->ple_stride * 4)) ||
+        (code = dev_alloc((void **)&e->ple_room, lanes * e->ple_stride * 4)) ||
+        (code = dev_alloc((void **)&e->logits, lanes * (size_t)e->vocab * 4)) ||
+        (code = dev_alloc(&e->pick_work, igl_pick_work_bytes())) ||
+        (code = dev_alloc((void **)&e->pick_dev, sizeof(int32_t))) ||
+        (code = dev_alloc((void **)&e->margin_dev, sizeof(float))))
+      goto fail;
+  }
+  free(config);
+  close(fd);
+  *out = e;
+  return IGL_OKAY;
+fail:
+  free(config);
+  if (fd >= 0) close(fd);
+  igl_engine_close(e);
+  return code;
+}
+
+void igl_engine_close(igl_engine *e) {
+  if (!e) return;
+  (void)hipStreamSynchronize(e->stream);
+  for (int i = 0; i < e->layers && i < ENG_LAYER_LIMIT; ++i) {
+    eng_layer *L = &e->layer[i];
+    igl_plane *pl[] = {&L->q, &L->k, &L->v, &L->o, &L->gate, &L->up, &L->down, &L->ple_gate, &L->ple_proj};
+    for (size_t j = 0; j < sizeof(pl) / sizeof(pl[0]); ++j) igl_plane_detach(e->desk, pl[j]);
+    if (L->k_store) (void)hipFree(L->k_store);
+    if (L->v_store) (void)hipFree(L->v_store);
+  }
+  if (e->head.device == e->embed.device) e->head.device = NULL;
+  igl_plane_detach(e->desk, &e->embed);
+  igl_plane_detach(e->desk, &e->ple_embed);
+  igl_plane_detach(e->desk, &e->ple_lift);
+  igl_plane_detach(e->desk, &e->head);
+  {
+    void *bufs[] = {e->payload_dev, e->ids_dev, e->state, e->scrap, e->lift, e->q, e->blend, e->k, e->v,
+                    e->gate, e->rise, e->ple_seed, e->ple_room, e->logits, e->pick_work, e->pick_dev,
+                    e->margin_dev, e->steps_dev[0], e->steps_dev[1]};
+    for (size_t j = 0; j < sizeof(bufs) / sizeof(bufs[0]); ++j)
+      if (bufs[j]) (void)hipFree(bufs[j]);
+  }
+  if (e->map) munmap(e->map, e->map_bytes);
+  free(e->tensor);
+  free(e);
+}
+
+/* ---- the pass ------------------------------------------------------------- */
+
+#define RUN(x)                                            \
+  do {                                                    \
+    hipError_t run_e = (x);                               \
+    if (run_e != hipSuccess) return IGL_FAIL_DEVICE;      \
+  } while (0)
+#define OKAY(x)                                           \
+  do {                                                    \
+    int okay_c = (x);                                     \
+    if (okay_c != IGL_OKAY) return okay_c;                \
+  } while (0)
+
+/* Device addresses of a plane's codes and gains: the same offsets into the
+ * device copy of the payload as into the mapped file. */
+static const uint8_t *dev_codes(const igl_engine *e, const igl_plane *p) {
+  return e->payload_dev + ((const uint8_t *)p->code_data - ((const uint8_t *)e->map + e->payload_at));
+}
+
+static const float *dev_gains(const igl_engine *e, const igl_plane *p) {
+  return (const float *)(e->payload_dev +
+                         ((const uint8_t *)p->gain_data - ((const uint8_t *)e->map + e->payload_at)));
+}
+
+static int project(igl_engine *e, const igl_plane *p, const float *act, int act_stride, int lanes,
+                   float *out, int out_stride) {
+  if (e->precise) return igl_gemv_dev(e->desk, p, act, act_stride, lanes, out, out_stride);
+  return igl_mat_mat_dev(e->desk, p, act, act_stride, lanes, out, out_stride);
+}
+
+static int norm_rows(igl_engine *e, const float *in, const float *gain, int n, int lanes, int stride,
+                     float *out) {
+  return igl_norm_rms_dev(e->desk, in, gain, n, lanes, stride, e->eps, out);
+}
+
+/* One layer for `lanes` lanes at positions place .. place + lanes - 1
+ * (session_layer 11637-11743 with session_attend 11455-11580). */
+static int run_layer(igl_engine *e, int li, int place, int lanes) {
+  eng_layer *L = &e->layer[li];
+  const eng_layer *S = &e->layer[L->source];
+  const int H = e->hidden, hs = L->head_size, qw = e->heads * hs;
+  const int kind = L->full ? 1 : 0;
+  hipStream_t st = e->stream;
+
+  OKAY(norm_rows(e, e->state, L->enter_norm, H, lanes, H, e->scrap));
+  OKAY(project(e, &L->q, e->scrap, H, lanes, e->q, e->q_stride));
+  RUN(igl_launch_head_prep(e->q, e->q_stride, e->heads, hs, lanes, L->q_norm, e->eps,
+                           e->steps_dev[kind], 1, place, st));
+  if (!L->shared) {
+    OKAY(project(e, &L->k, e->scrap, H, lanes, e->k, e->kv_stride));
+    OKAY(project(e, &L->v, e->scrap, H, lanes, e->v, e->kv_stride));
+    RUN(igl_launch_head_prep(e->k, e->kv_stride, 1, hs, lanes, L->k_norm, e->eps,
+                             e->steps_dev[kind], 1, place, st));
+    RUN(igl_launch_head_prep(e->v, e->kv_stride, 1, hs, lanes, NULL, e->eps, e->steps_dev[kind], 0,
+                             place, st));
+    RUN(igl_launch_cache_lay_rows(e->k, e->kv_stride, hs, L->k_scale, L->k_store, L->cache_span,
+                                  place, lanes, st));
+    RUN(igl_launch_cache_lay_rows(e->v, e->kv_stride, hs, L->v_scale, L->v_store, L->cache_span,
+                                  place, lanes, st));
+  }
+  OKAY(igl_attend_lanes_dev(e->desk, S->k_store, S->v_store, IGL_CACHE_E4M3, S->k_scale, S->v_scale,
+                            S->cache_span, 1, e->heads, hs, e->q, e->q_stride, place,
+                            L->full ? 0 : e->window, lanes, 1.0f, e->blend));
+  OKAY(project(e, &L->o, e->blend, e->q_stride, lanes, e->lift, H));
+  (void)qw;
+  OKAY(norm_rows(e, e->lift, L->after_attn, H, lanes, H, e->lift));
+  RUN(igl_launch_add_rows(e->state, H, e->lift, H, H, lanes, 1.0f, 0, st));
+  OKAY(norm_rows(e, e->state, L->before_ff, H, lanes, H, e->scrap));
+  OKAY(project(e, &L->gate, e->scrap, H, lanes, e->gate, e->inner_max));
+  OKAY(project(e, &L->up, e->scrap, H, lanes, e->rise, e->inner_max));
+  RUN(igl_launch_gelu_gate_rows(e->gate, e->inner_max, e->rise, e->inner_max, L->inner, lanes, st));
+  OKAY(project(e, &L->down, e->gate, e->inner_max, lanes, e->lift, H));
+  OKAY(norm_rows(e, e->lift, L->after_ff, H, lanes, H, e->lift));
+  RUN(igl_launch_add_rows(e->state, H, e->lift, H, H, lanes, 1.0f, 0, st));
+  /* per-layer input */
+  OKAY(project(e, &L->ple_gate, e->state, H, lanes, e->gate, e->inner_max));
+  RUN(igl_launch_gelu_mul(e->gate, e->inner_max, e->ple_room + (size_t)li * e->ple, e->ple_stride,
+                          e->ple, lanes, st));
+  OKAY(project(e, &L->ple_proj, e->gate, e->inner_max, lanes, e->lift, H));
+  OKAY(norm_rows(e, e->lift, L->after_ple, H, lanes, H, e->lift));
+  RUN(igl_launch_add_rows(e->state, H, e->lift, H, H, lanes, L->layer_gain,
+                          L->layer_gain != 1.0f, st));
+  return IGL_OKAY;
+}
+
+/* session_pass (11843-11975) for `lanes` ids; with `logits`, the head runs on
+ * the last lane (1) or every lane (2). */
+static int run_pass(igl_engine *e, const int32_t *ids, int lanes, int logits) {
+  hipStream_t st = e->stream;
+  const int H = e->hidden, place = e->fill;
+  if (lanes < 1 || lanes > e->lane_limit || place + lanes > e->window_limit) return IGL_FAIL_STATE;
+  for (int l = 0; l < lanes; ++l)
+    if (ids[l] < 0 || ids[l] >= e->embed.row_count) return IGL_FAIL_ARGUMENT;
+  RUN(hipMemcpyAsync(e->ids_dev, ids, (size_t)lanes * sizeof(int32_t), hipMemcpyHostToDevice, st));
+  /* embedding row times sqrt(hidden) */
+  {
+    const igl_plane *p = &e->embed;
+    RUN(igl_launch_gather_rows(dev_codes(e, p), (long long)p->row_stride, dev_gains(e, p),
+                               p->group_count, p->group_size, p->code_bias, H, p->row_count,
+                               e->ids_dev, lanes, (float)sqrt((double)H), e->state, H, st));
+  }
+  /* per-layer inputs */
+  {
+    const igl_plane *p = &e->ple_embed;
+    const int chunk_all = e->layers * e->ple;
+    OKAY(project(e, &e->ple_lift, e->state, H, lanes, e->ple_room, e->ple_stride));
+    RUN(igl_launch_gather_rows(dev_codes(e, p), (long long)p->row_stride, dev_gains(e, p),
+                               p->group_count, p->group_size, p->code_bias, chunk_all, p->row_count,
+                               e->ids_dev, lanes, (float)sqrt((double)e->ple), e->ple_seed,
+                               e->ple_stride, st));
+    RUN(igl_launch_ple_mix(e->ple_room, e->ple_stride, e->ple_seed, e->ple_stride, e->ple_norm,
+                           e->ple, e->layers, lanes, e->eps, (float)(1.0 / sqrt((double)H)),
+                           (float)(1.0 / sqrt(2.0)), st));
+  }
+  for (int li = 0; li < e->layers; ++li) OKAY(run_layer(e, li, place, lanes));
+  e->fill += lanes;
+  if (logits) {
+    const int from = logits == 2 ? 0 : lanes - 1;
+    const int span = lanes - from;
+    OKAY(norm_rows(e, e->state + (size_t)from * H, e->final_norm, H, span, H, e->scrap));
+    OKAY(project(e, &e->head, e->scrap, H, span, e->logits, e->vocab));
+    if (e->cap > 0.0f) RUN(igl_launch_logit_cap(e->logits, (size_t)span * e->vocab, e->cap, st));
+  }
+  return IGL_OKAY;
+}
+
+int igl_engine_prime(igl_engine *e, const int32_t *ids, int count) {
+  if (!e || !ids || count < 1) return IGL_FAIL_ARGUMENT;
+  /* every id but the last, in chunks of the lane limit (session_prime_media 14443-14467) */
+  for (int at = 0; at + 1 < count;) {
+    int lanes = count - 1 - at < e->lane_limit ? count - 1 - at : e->lane_limit;
+    OKAY(run_pass(e, ids + at, lanes, 0));
+    at += lanes;
+  }
+  return igl_desk_error_take(e->desk);
+}
+
+int igl_engine_step(igl_engine *e, int32_t id, int32_t *pick_out, float *margin_out) {
+  int32_t pick = -1;
+  float margin = 0.0f;
+  if (!e) return IGL_FAIL_ARGUMENT;
+  OKAY(run_pass(e, &id, 1, 1));
+  RUN(igl_launch_pick(e->logits, e->vocab, e->pick_work, e->pick_dev, e->margin_dev, e->stream));
+  RUN(hipMemcpyAsync(&pick, e->pick_dev, sizeof(pick), hipMemcpyDeviceToHost, e->stream));
+  RUN(hipMemcpyAsync(&margin, e->margin_dev, sizeof(margin), hipMemcpyDeviceToHost, e->stream));
+  RUN(hipStreamSynchronize(e->stream));
+  if (pick_out) *pick_out = pick;
+  if (margin_out) *margin_out = margin;
+  return igl_desk_error_take(e->desk);
+}
+
+int igl_engine_logits(igl_engine *e, float *out, int lane) {
+  if (!e || !out || lane < 0 || lane >= e->lane_limit) return IGL_FAIL_ARGUMENT;
+  RUN(hipMemcpyAsync(out, e->logits + (size_t)lane * e->vocab, (size_t)e->vocab * sizeof(float),
+                     hipMemcpyDeviceToHost, e->stream));
+  RUN(hipStreamSynchronize(e->stream));
+  return IGL_OKAY;
+}
+
+int igl_engine_fill(const igl_engine *e) { return e ? e->fill : 0; }
+int igl_engine_vocab(const igl_engine *e) { return e ? e->vocab : 0; }
+
+int igl_engine_reset(igl_engine *e) {
+  if (!e) return IGL_FAIL_ARGUMENT;
+  e->fill = 0;
+  return IGL_OKAY;
+}

@@ -8,6 +8,8 @@
 #include <stdint.h>
 #include <hip/hip_runtime_api.h>
 
+#include "igl_backend.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -25,12 +27,42 @@ hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride, con
                               int out_stride, int M, int N, int K, hipStream_t stream);
 
 int igl_attend_chunk_size(void);
-size_t igl_attend_work_floats(int span_count, int head_count, int head_size);
+size_t igl_attend_work_floats(int place0, int window, int lanes, int head_count, int head_size);
 hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t *value_store, int fmt,
                              float key_scale, float value_scale, int cache_span, int kv_width,
                              int kv_count, int group_share, int head_size, const float *query,
-                             int place_start, int span_count, float score_scale, float *blend_out,
-                             float *work, hipStream_t stream);
+                             int q_stride, int place0, int window, int lanes, float score_scale,
+                             float *blend_out, float *work, hipStream_t stream);
+
+/* The desk's HIP stream, for the engine's own launches (back_hip.c). */
+void *igl_desk_stream(igl_desk *desk);
+
+/* session kernels (igl_session.hip) */
+hipError_t igl_launch_gather_rows(const uint8_t *codes, long long row_stride, const float *gains,
+                                  int group_count, int group_size, int code_bias, int cols,
+                                  int rows, const int32_t *ids, int lanes, float factor,
+                                  float *out, int out_stride, hipStream_t stream);
+hipError_t igl_launch_ple_mix(float *room, int room_stride, const float *seed, int seed_stride,
+                              const float *gain, int ple, int chunks, int lanes, float eps,
+                              float lift_scale, float blend, hipStream_t stream);
+hipError_t igl_launch_head_prep(float *v, int lane_stride, int heads, int head_size, int lanes,
+                                const float *gain, float eps, const float *step, int turn,
+                                int place_first, hipStream_t stream);
+hipError_t igl_launch_add_rows(float *into, int into_stride, const float *from, int from_stride,
+                               int n, int lanes, float gain, int apply_gain, hipStream_t stream);
+hipError_t igl_launch_scale_rows(float *v, int stride, int n, int lanes, float gain,
+                                 hipStream_t stream);
+hipError_t igl_launch_gelu_mul(float *gate, int gate_stride, const float *ple, int ple_stride,
+                               int n, int lanes, hipStream_t stream);
+hipError_t igl_launch_gelu_gate_rows(float *gate, int gate_stride, const float *rise,
+                                     int rise_stride, int n, int lanes, hipStream_t stream);
+hipError_t igl_launch_cache_lay_rows(const float *rows, int row_stride, int width, float scale,
+                                     uint8_t *store, int span, int place_first, int lanes,
+                                     hipStream_t stream);
+hipError_t igl_launch_logit_cap(float *v, size_t n, float cap, hipStream_t stream);
+size_t igl_pick_work_bytes(void);
+hipError_t igl_launch_pick(const float *v, int n, void *work, int32_t *index_out,
+                           float *margin_out, hipStream_t stream);
 
 hipError_t igl_launch_norm_rms(const float *in, const float *gain, int n, int rows, int stride,
                                float eps, float *out, hipStream_t stream);

@@ -1,0 +1,316 @@
+// igl_session.hip - the device side of a decode pass besides the projections
+// and attention: embedding gathers, the per-layer-embedding mix, head norms
+// with the rotary turn, residual updates, the cache writer for a batch of
+// lanes, the logit cap and the greedy pick.  gfx950.
+//
+// Each restates a step of the reference's session graph (session_pass
+// app_core.c:11843-11975, session_layer 11637-11743, session_attend
+// 11455-11580) in the same order of float operations where the reference has
+// one; reductions the reference does in double (norms) are done in double.
+#include "igl_device.h"
+
+namespace igl {
+
+// Rows `ids[l]` of a 4-bit code plane as floats times `factor`:
+// ((code - code_bias) * gain) * factor (plane_row 1826-1856, then kern_scale).
+__global__ void gather_rows_kernel(const uint8_t *codes, long long row_stride, const float *gains,
+                                   int group_count, int group_shift, int code_bias, int cols,
+                                   int rows, const int32_t *ids, float factor, float *out,
+                                   int out_stride) {
+  const int lane = blockIdx.y;
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= cols) return;
+  int id = ids[lane];
+  if (id < 0) id = 0;
+  id %= rows;
+  const uint8_t b = codes[(size_t)id * row_stride + (k >> 1)];
+  const int c = (k & 1) ? (b >> 4) : (b & 15);
+  const float gain = gains[(size_t)id * group_count + ((unsigned)(k >> 5) >> group_shift)];
+  const float v = (float)(c - code_bias) * gain;
+  out[(size_t)lane * out_stride + k] = v * factor;
+}
+
+__device__ __forceinline__ double block_sum_double(double v, double *red) {
+  red[threadIdx.x] = v;
+  __syncthreads();
+  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  const double total = red[0];
+  __syncthreads();
+  return total;
+}
+
+// The per-layer inputs of one lane (session_pass 11877-11902): the projected
+// chunk scaled by 1/sqrt(hidden), RMS-normed with the shared gain, plus the
+// token's per-layer embedding row scaled by sqrt(ple), times 1/sqrt(2).
+// One workgroup per (chunk, lane); `seed` is already scaled by sqrt(ple).
+__global__ __launch_bounds__(256) void ple_mix_kernel(float *room, int room_stride,
+                                                      const float *seed, int seed_stride,
+                                                      const float *gain, int ple, float eps,
+                                                      float lift_scale, float blend) {
+  __shared__ double red[256];
+  const int chunk = blockIdx.x;
+  const int lane = blockIdx.y;
+  float *x = room + (size_t)lane * room_stride + (size_t)chunk * ple;
+  const float *s = seed + (size_t)lane * seed_stride + (size_t)chunk * ple;
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < ple; i += blockDim.x) {
+    const float v = x[i] * lift_scale;
+    acc += (double)v * (double)v;
+  }
+  const double total = block_sum_double(acc, red);
+  const float shrink = (float)pow(total / (double)ple + (double)eps, -0.5);
+  for (int i = threadIdx.x; i < ple; i += blockDim.x) {
+    const float v = x[i] * lift_scale;
+    const float normed = v * shrink * gain[i];
+    x[i] = (normed + s[i]) * blend;
+  }
+}
+
+// Head norms and the rotary turn for a batch of lanes (session_attend
+// 11487-11514).  One workgroup per (head, lane).  `gain` NULL normalizes
+// without a gain (the value heads); `turn` 0 skips the rotation.  The angle of
+// pair j at position p is p * step[j] in double, its cos and sin rounded to
+// float (rope_wave 8147-8154); pairs past `turns` have step 0 (identity).
+__global__ __launch_bounds__(256) void head_prep_kernel(float *v, int lane_stride, int head_size,
+                                                        const float *gain, float eps,
+                                                        const float *step, int turn,
+                                                        int place_first) {
+  __shared__ double red[256];
+  const int head = blockIdx.x;
+  const int lane = blockIdx.y;
+  float *x = v + (size_t)lane * lane_stride + (size_t)head * head_size;
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < head_size; i += blockDim.x) acc += (double)x[i] * (double)x[i];
+  const double total = block_sum_double(acc, red);
+  const float shrink = (float)pow(total / (double)head_size + (double)eps, -0.5);
+  const int half = head_size / 2;
+  const double place = (double)(place_first + lane);
+  for (int j = threadIdx.x; j < half; j += blockDim.x) {
+    float lo = x[j] * shrink;
+    float hi = x[j + half] * shrink;
+    if (gain) {
+      lo = lo * gain[j];
+      hi = hi * gain[j + half];
+    }
+    if (turn) {
+      const double angle = place * (double)step[j];
+      const float c = (float)cos(angle);
+      const float s = (float)sin(angle);
+      x[j] = lo * c - hi * s;
+      x[j + half] = hi * c + lo * s;
+    } else {
+      x[j] = lo;
+      x[j + half] = hi;
+    }
+  }
+}
+
+// into[l][i] += from[l][i] (kern_add), optionally then times `gain` (kern_scale).
+__global__ void add_rows_kernel(float *into, int into_stride, const float *from, int from_stride,
+                                int n, float gain, int apply_gain) {
+  const int lane = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float v = into[(size_t)lane * into_stride + i] + from[(size_t)lane * from_stride + i];
+  if (apply_gain) v *= gain;
+  into[(size_t)lane * into_stride + i] = v;
+}
+
+__global__ void scale_rows_kernel(float *v, int stride, int n, float gain) {
+  const int lane = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  v[(size_t)lane * stride + i] *= gain;
+}
+
+// The per-layer-input gate of a layer: gate[l][i] = gelu(gate[l][i]) * ple[l][i]
+// (session_layer 11718-11723).
+__global__ void gelu_mul_kernel(float *gate, int gate_stride, const float *ple, int ple_stride, int n) {
+  const int lane = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float *g = gate + (size_t)lane * gate_stride + i;
+  *g = gelu_near(*g) * ple[(size_t)lane * ple_stride + i];
+}
+
+// The feed-forward gate over a batch: gate = gelu(gate) * rise (kern_gelu_gate).
+__global__ void gelu_gate_rows_kernel(float *gate, int gate_stride, const float *rise,
+                                      int rise_stride, int n) {
+  const int lane = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float *g = gate + (size_t)lane * gate_stride + i;
+  *g = gelu_near(*g) * rise[(size_t)lane * rise_stride + i];
+}
+
+// Byte cache rows for a batch of lanes: lane l at position place_first + l
+// goes to slot (place_first + l) % span (cache_lay 11205-11236).
+__global__ void cache_lay_rows_kernel(const float *rows, int row_stride, int width, float scale,
+                                      uint8_t *store, int span, int place_first) {
+  const int lane = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= width) return;
+  const size_t slot = (size_t)((place_first + lane) % span);
+  store[slot * width + i] = e4m3_code(rows[(size_t)lane * row_stride + i] / scale);
+}
+
+// cap * (1 - 2 / (e^(2y) + 1)), y = x / cap clamped to +-10 (kern_logit_cap_one, 5009-5014).
+__global__ void logit_cap_kernel(float *v, size_t n, float cap) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float back = 1.0f / cap;
+  float y = v[i] * back;
+  if (y > 10.0f) y = 10.0f;
+  if (y < -10.0f) y = -10.0f;
+  v[i] = cap * (1.0f - 2.0f / (exp_near(y + y) + 1.0f));
+}
+
+// Greedy pick: the first index of the largest logit (session_pick_at
+// 14672-14677), and the gap to the second largest value.  Stage one: per-block
+// (best, index, second); stage two in one block.
+struct Top2 {
+  float best;
+  int index;
+  float second;
+};
+
+__device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
+  Top2 r;
+  if (b.best > a.best || (b.best == a.best && b.index < a.index)) {
+    r.best = b.best;
+    r.index = b.index;
+    r.second = fmaxf(a.best, b.second);
+  } else {
+    r.best = a.best;
+    r.index = a.index;
+    r.second = fmaxf(a.second, b.best);
+  }
+  return r;
+}
+
+__global__ __launch_bounds__(256) void pick_stage_kernel(const float *v, int n, Top2 *part) {
+  __shared__ Top2 red[256];
+  Top2 t{-INFINITY, 0x7FFFFFFF, -INFINITY};
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    Top2 one{v[i], i, -INFINITY};
+    t = top2_merge(t, one);
+  }
+  red[threadIdx.x] = t;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] = top2_merge(red[threadIdx.x], red[threadIdx.x + w]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[blockIdx.x] = red[0];
+}
+
+__global__ __launch_bounds__(256) void pick_final_kernel(const Top2 *part, int parts, int32_t *index_out,
+                                                         float *margin_out) {
+  __shared__ Top2 red[256];
+  Top2 t{-INFINITY, 0x7FFFFFFF, -INFINITY};
+  for (int i = threadIdx.x; i < parts; i += blockDim.x) t = top2_merge(t, part[i]);
+  red[threadIdx.x] = t;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] = top2_merge(red[threadIdx.x], red[threadIdx.x + w]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    *index_out = red[0].index;
+    *margin_out = red[0].best - red[0].second;
+  }
+}
+
+}  // namespace igl
+
+using namespace igl;
+
+static const int kPickBlocks = 256;
+
+extern "C" hipError_t igl_launch_gather_rows(const uint8_t *codes, long long row_stride,
+                                             const float *gains, int group_count, int group_size,
+                                             int code_bias, int cols, int rows, const int32_t *ids,
+                                             int lanes, float factor, float *out, int out_stride,
+                                             hipStream_t stream) {
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((cols + 255) / 256, lanes), dim3(256), 0, stream, codes,
+                     row_stride, gains, group_count, __builtin_ctz((unsigned)(group_size / 32)),
+                     code_bias, cols, rows, ids, factor, out, out_stride);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_ple_mix(float *room, int room_stride, const float *seed,
+                                         int seed_stride, const float *gain, int ple, int chunks,
+                                         int lanes, float eps, float lift_scale, float blend,
+                                         hipStream_t stream) {
+  hipLaunchKernelGGL(ple_mix_kernel, dim3(chunks, lanes), dim3(256), 0, stream, room, room_stride,
+                     seed, seed_stride, gain, ple, eps, lift_scale, blend);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_head_prep(float *v, int lane_stride, int heads, int head_size,
+                                           int lanes, const float *gain, float eps,
+                                           const float *step, int turn, int place_first,
+                                           hipStream_t stream) {
+  hipLaunchKernelGGL(head_prep_kernel, dim3(heads, lanes), dim3(256), 0, stream, v, lane_stride,
+                     head_size, gain, eps, step, turn, place_first);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_add_rows(float *into, int into_stride, const float *from,
+                                          int from_stride, int n, int lanes, float gain,
+                                          int apply_gain, hipStream_t stream) {
+  hipLaunchKernelGGL(add_rows_kernel, dim3((n + 255) / 256, lanes), dim3(256), 0, stream, into,
+                     into_stride, from, from_stride, n, gain, apply_gain);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_scale_rows(float *v, int stride, int n, int lanes, float gain,
+                                            hipStream_t stream) {
+  hipLaunchKernelGGL(scale_rows_kernel, dim3((n + 255) / 256, lanes), dim3(256), 0, stream, v,
+                     stride, n, gain);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_gelu_mul(float *gate, int gate_stride, const float *ple,
+                                          int ple_stride, int n, int lanes, hipStream_t stream) {
+  hipLaunchKernelGGL(gelu_mul_kernel, dim3((n + 255) / 256, lanes), dim3(256), 0, stream, gate,
+                     gate_stride, ple, ple_stride, n);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_gelu_gate_rows(float *gate, int gate_stride, const float *rise,
+                                                int rise_stride, int n, int lanes,
+                                                hipStream_t stream) {
+  hipLaunchKernelGGL(gelu_gate_rows_kernel, dim3((n + 255) / 256, lanes), dim3(256), 0, stream,
+                     gate, gate_stride, rise, rise_stride, n);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_cache_lay_rows(const float *rows, int row_stride, int width,
+                                                float scale, uint8_t *store, int span,
+                                                int place_first, int lanes, hipStream_t stream) {
+  hipLaunchKernelGGL(cache_lay_rows_kernel, dim3((width + 255) / 256, lanes), dim3(256), 0, stream,
+                     rows, row_stride, width, scale, store, span, place_first);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_logit_cap(float *v, size_t n, float cap, hipStream_t stream) {
+  hipLaunchKernelGGL(logit_cap_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, v, n, cap);
+  return hipGetLastError();
+}
+
+extern "C" size_t igl_pick_work_bytes(void) { return sizeof(Top2) * kPickBlocks; }
+
+extern "C" hipError_t igl_launch_pick(const float *v, int n, void *work, int32_t *index_out,
+                                      float *margin_out, hipStream_t stream) {
+  hipLaunchKernelGGL(pick_stage_kernel, dim3(kPickBlocks), dim3(256), 0, stream, v, n,
+                     reinterpret_cast<Top2 *>(work));
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(pick_final_kernel, dim3(1), dim3(256), 0, stream,
+                     reinterpret_cast<const Top2 *>(work), kPickBlocks, index_out, margin_out);
+  return hipGetLastError();
+}

@@ -74,6 +74,16 @@ class Rng(ctypes.Structure):
     _fields_ = [("s", ctypes.c_uint64 * 4)]
 
 
+class GemmaShape(ctypes.Structure):
+    """`igl_gemma_shape`: the synthetic checkpoint's text-stack dimensions."""
+
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "vocab", "hidden", "inner", "layers", "heads", "kv_heads", "head_dim", "full_head_dim",
+        "window", "ple_size", "shared_layers", "double_wide", "full_every", "max_positions",
+        "cache_scales")] + [(n, ctypes.c_float) for n in (
+            "norm_eps", "logit_cap", "rope_local", "rope_global", "partial_rotary")]
+
+
 MAT_VEC_FN = ctypes.CFUNCTYPE(None, ctypes.POINTER(Desk), ctypes.POINTER(Plane), c_float_p, c_float_p)
 MAT_MAT_FN = ctypes.CFUNCTYPE(None, ctypes.POINTER(Desk), ctypes.POINTER(Plane), c_float_p,
                               ctypes.c_int, ctypes.c_int, c_float_p, ctypes.c_int)
@@ -104,6 +114,20 @@ SIGNATURES = {
     "igl_gemm_lane_floor": (_I, []),
     "igl_attend_dev": (_I, [ctypes.POINTER(Desk), _P, _P, _I, _F, _F, _I, _I, _I, _I, _P, _I, _I,
                             _F, _P]),
+    "igl_attend_lanes_dev": (_I, [ctypes.POINTER(Desk), _P, _P, _I, _F, _F, _I, _I, _I, _I, _P,
+                                  _I, _I, _I, _I, _F, _P]),
+    "igl_gemma_shape_e2b": (None, [ctypes.POINTER(GemmaShape)]),
+    "igl_gemma_full_layer": (_I, [ctypes.POINTER(GemmaShape), _I]),
+    "igl_gemma_write": (_I, [ctypes.c_char_p, ctypes.POINTER(GemmaShape), ctypes.c_uint64]),
+    "igl_engine_open": (_I, [ctypes.POINTER(_P), ctypes.POINTER(Desk), ctypes.c_char_p, _I, _I, _I]),
+    "igl_engine_close": (None, [_P]),
+    "igl_engine_prime": (_I, [_P, _P, _I]),
+    "igl_engine_step": (_I, [_P, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32),
+                             ctypes.POINTER(ctypes.c_float)]),
+    "igl_engine_logits": (_I, [_P, _P, _I]),
+    "igl_engine_fill": (_I, [_P]),
+    "igl_engine_vocab": (_I, [_P]),
+    "igl_engine_reset": (_I, [_P]),
     "igl_cache_lay_dev": (_I, [ctypes.POINTER(Desk), _P, _I, _F, _I, _P, _Z]),
     "igl_norm_rms_dev": (_I, [ctypes.POINTER(Desk), _P, _P, _I, _I, _I, _F, _P]),
     "igl_soft_max_dev": (_I, [ctypes.POINTER(Desk), _P, _I, _I, _I]),

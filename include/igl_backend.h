@@ -168,6 +168,17 @@ int igl_attend_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t *valu
                    int format, float key_scale, float value_scale, int cache_span,
                    int kv_count, int group_share, int head_size, const float *query_dev,
                    int place_start, int span_count, float score_scale, float *blend_out_dev);
+/* The same for `lane_count` lanes at positions place_first .. + lane_count - 1
+ * (a prefill chunk or a speculative block), one launch: lane l sees the last
+ * `window` positions up to and including its own (0: all from position 0),
+ * its query and output `lane_stride` floats after lane l - 1's.  Every lane's
+ * keys and values must already be in the ring, which must be deep enough
+ * that no lane's visible rows were overwritten by a later lane's. */
+int igl_attend_lanes_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t *value_store,
+                         int format, float key_scale, float value_scale, int cache_span,
+                         int kv_count, int group_share, int head_size, const float *query_dev,
+                         int lane_stride, int place_first, int window, int lane_count,
+                         float score_scale, float *blend_out_dev);
 /* cache_lay (app_core.c:11205-11236) for a byte store: row / scale to the ring
  * at byte offset slot_first. */
 int igl_cache_lay_dev(igl_desk *desk, const float *row_dev, int width, float scale, int format,
@@ -205,6 +216,47 @@ void     igl_rng_normal(igl_rng *rng, float *out, size_t count, float mean, floa
 void     igl_rng_codes4(igl_rng *rng, uint8_t *codes, int N, int K, size_t row_stride);
 /* |N(0, stddev)| gains. */
 void     igl_rng_gains(igl_rng *rng, float *gains, size_t count, float stddev);
+
+/* ---- synthetic Gemma 4 E2B-shaped checkpoint ------------------------------ */
+
+/* The text stack's dimensions (model/config.json of the reference's export). */
+typedef struct igl_gemma_shape {
+  int   vocab, hidden, inner, layers, heads, kv_heads, head_dim, full_head_dim;
+  int   window, ple_size, shared_layers, double_wide, full_every, max_positions;
+  int   cache_scales;  /* write k/v_cache_scale so a byte cache is used */
+  float norm_eps, logit_cap, rope_local, rope_global, partial_rotary;
+} igl_gemma_shape;
+
+/* config.json's dimensions: 35 layers, hidden 1536, FFN 6144 (12288 on the 20
+ * key/value-sharing layers), 8 heads, 1 KV head, head 256 / 512, window 512,
+ * vocab 262144. */
+void igl_gemma_shape_e2b(igl_gemma_shape *shape);
+int  igl_gemma_full_layer(const igl_gemma_shape *shape, int layer);
+/* Writes config.json, tokenizer.json and model.safetensors (int4 group-32
+ * planes in the export's U8 + F32-scale layout) into `folder`, seeded. */
+int  igl_gemma_write(const char *folder, const igl_gemma_shape *shape, uint64_t seed);
+
+/* ---- a device-resident decode session ------------------------------------- */
+
+/* The reference's session graph (session_pass app_core.c:11843-11975) with
+ * activations and the byte key/value cache in HBM: ids in, greedy picks out.
+ * Loads config.json + model.safetensors from `folder` (4-bit planes, one KV
+ * head per 8 query heads, byte cache scales).  `lane_limit` lanes run per pass
+ * (the reference's is 16); `precise` keeps every projection on the fp32
+ * activation GEMV, otherwise batches of 64+ lanes take the MFMA GEMM. */
+typedef struct igl_engine igl_engine;
+int  igl_engine_open(igl_engine **engine_out, igl_desk *desk, const char *folder,
+                     int window_limit, int lane_limit, int precise);
+void igl_engine_close(igl_engine *engine);
+/* session_prime (app_core.c:14469): every id but the last. */
+int  igl_engine_prime(igl_engine *engine, const int32_t *ids, int count);
+/* session_step + the greedy pick (first maximum, 14672-14677); margin_out
+ * receives the gap to the runner-up logit. */
+int  igl_engine_step(igl_engine *engine, int32_t id, int32_t *pick_out, float *margin_out);
+int  igl_engine_logits(igl_engine *engine, float *out, int lane);
+int  igl_engine_fill(const igl_engine *engine);
+int  igl_engine_vocab(const igl_engine *engine);
+int  igl_engine_reset(igl_engine *engine);
 
 #ifdef __cplusplus
 }

@@ -108,6 +108,55 @@ float ref_quant_step(float value, float step) {
   return value;
 }
 
+/* The reference engine end to end: load the checkpoint in `folder`, prime the
+ * prompt (all but its last id, app_core.c:14443-14471), then step and take the
+ * greedy pick `gen_count` times, the way the CLI's answer loop does
+ * (app_main.c:600-611) but without stopping at the close id.  The pick is the
+ * first maximum (session_pick_at, app_core.c:14672-14677).  `margin_out`, when
+ * given, receives each step's gap between the best and second-best logit.
+ * Returns 0 or the app_code that stopped it. */
+int ref_engine_greedy(const char *folder, int thread_count, int cache_bits, int window_limit,
+                      const int32_t *prompt, int prompt_count, int gen_count, int32_t *out_ids,
+                      float *margin_out) {
+  app_setup setup = app_setup_plain();
+  app_model *model = NULL;
+  app_session *session = NULL;
+  app_code code;
+  int32_t id;
+  setup.thread_count = thread_count;
+  setup.cache_bits = cache_bits;
+  setup.window_limit = window_limit;
+  code = model_load(folder, &setup, &model);
+  if (code != APP_OKAY) return (int)code;
+  code = session_open(model, &session);
+  if (code != APP_OKAY) {
+    model_free(model);
+    return (int)code;
+  }
+  code = session_prime(session, prompt, prompt_count);
+  id = prompt[prompt_count - 1];
+  for (int step = 0; code == APP_OKAY && step < gen_count; ++step) {
+    const float *logits = session_step(session, id);
+    int vocab = model_vocab_count(model);
+    int best = 0;
+    float second = -FLT_MAX;
+    if (!logits) {
+      code = APP_FAIL_STATE;
+      break;
+    }
+    for (int v = 1; v < vocab; ++v)
+      if (logits[v] > logits[best]) best = v;
+    for (int v = 0; v < vocab; ++v)
+      if (v != best && logits[v] > second) second = logits[v];
+    out_ids[step] = best;
+    if (margin_out) margin_out[step] = logits[best] - second;
+    id = best;
+  }
+  session_close(session);
+  model_free(model);
+  return (int)code;
+}
+
 /* One lane's grouped decode attention through the reference's own two jobs
  * (attend_score_band / attend_blend_band, app_core.c:11296-11365), forked over
  * the desk's pool exactly as session_attend_group forks them (11415-11453).

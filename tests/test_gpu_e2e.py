@@ -1,0 +1,52 @@
+"""End-to-end greedy parity: the device-resident engine against the reference
+engine's own greedy stream on the same seeded synthetic checkpoint
+(tests/golden/e2e_small.json, written by tests/golden/make_e2e_golden.py from
+the reference compiled out of app_core.c).
+
+Bar: the greedy token stream is identical over the fixture's 128 tokens.  The
+fixture records each step's top-1/top-2 margin in the reference; the smallest
+is printed, since a tie closer than fp32 reassociation could flip a pick.
+"""
+import json
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+from igllm_amd.engine import SMALL, Engine, prompt_ids, write_gemma
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def load_fixture(name):
+    with open(os.path.join(HERE, "golden", f"e2e_{name}.json")) as f:
+        return json.load(f)
+
+
+@pytest.fixture(scope="module")
+def small_model():
+    fx = load_fixture("small")
+    folder = os.path.join(tempfile.gettempdir(), f"igl_gemma_small_{os.getpid()}")
+    write_gemma(folder, seed=fx["seed"], **SMALL)
+    return folder, fx
+
+
+@pytest.mark.parametrize("lane_limit", [16, 64])
+def test_small_greedy_stream_matches_reference(backend, small_model, lane_limit):
+    folder, fx = small_model
+    prompt = prompt_ids(fx["prompt_count"], fx["shape"]["vocab"], seed=fx["prompt_seed"])
+    eng = Engine(backend, folder, window_limit=fx["window_limit"], lane_limit=lane_limit, precise=True)
+    try:
+        ids, margins = eng.greedy(prompt, fx["gen"])
+    finally:
+        eng.close()
+    want = np.array(fx["plain"]["ids"], dtype=np.int32)
+    ref_margin = np.array(fx["plain"]["margin"])
+    print("min reference margin", float(ref_margin.min()), "min engine margin", float(margins.min()))
+    if not np.array_equal(ids, want):
+        first = int(np.nonzero(ids != want)[0][0])
+        print("first divergence at step", first, "reference margin there", ref_margin[first])
+    assert np.array_equal(ids, want)
