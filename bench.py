@@ -44,7 +44,62 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decode leg")
     return ap.parse_args()
+
+
+def e2e_decode(be, prompt_count=2048, gen=256):
+    """Synthetic Gemma-4-E2B-shaped decode (model/config.json dimensions, every
+    plane int4 group 32, FP8 key/value cache): write the seeded checkpoint,
+    prime a 2048-id seeded prompt, then 256 greedy steps."""
+    import tempfile
+    from igllm_amd.engine import Engine, prompt_ids, write_gemma
+
+    root = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
+    folder = os.path.join(root, f"igl_gemma_e2b_{os.getpid()}")
+    t0 = time.perf_counter()
+    shape = write_gemma(folder, seed=0)
+    write_s = time.perf_counter() - t0
+    prompt = prompt_ids(prompt_count, shape.vocab, seed=0)
+    out = {"model": "synthetic Gemma-4-E2B text stack (model/config.json dims), int4 g32, "
+                    "FP8 KV cache", "prompt": prompt_count, "gen": gen,
+           "checkpoint_write_s": round(write_s, 1)}
+    try:
+        for precise in (False, True):
+            t0 = time.perf_counter()
+            eng = Engine(be, folder, window_limit=prompt_count + gen + 64,
+                         lane_limit=16 if precise else 256, precise=precise)
+            load_s = time.perf_counter() - t0
+            try:
+                t0 = time.perf_counter()
+                eng.prime(prompt)
+                be.sync()
+                prime_s = time.perf_counter() - t0
+                token = int(prompt[-1])
+                picks, margins = [], []
+                t0 = time.perf_counter()
+                for _ in range(gen):
+                    token, margin = eng.step(token)
+                    picks.append(token)
+                    margins.append(margin)
+                decode_s = time.perf_counter() - t0
+            finally:
+                eng.close()
+            key = "precise" if precise else "fast_prefill"
+            out[key] = {"load_s": round(load_s, 2),
+                        "prefill_tok_s": round((prompt_count - 1) / prime_s, 1),
+                        "decode_tok_s": round(gen / decode_s, 1),
+                        "decode_ms_per_token": round(decode_s * 1e3 / gen, 3),
+                        "min_margin": round(float(min(margins)), 5),
+                        "first_ids": picks[:16],
+                        "lane_limit": 16 if precise else 256}
+            out.setdefault("streams", []).append(picks)
+        out["prefill_modes_agree"] = out["streams"][0] == out["streams"][1]
+        out.pop("streams")
+    finally:
+        import shutil
+        shutil.rmtree(folder, ignore_errors=True)
+    return out
 
 
 class Rotation:
@@ -265,6 +320,7 @@ def main():
                  "note": f"int8 K/V rings rotated over {rings} copies (past the MALL); "
                          "includes the chunk-merge launch"}
 
+    e2e = None if args.no_e2e else e2e_decode(be)
     cpu = None if args.no_cpu else cpu_baseline()
 
     line = {
@@ -293,7 +349,8 @@ def main():
         "gemv_sweep": sweep,
         "prefill_gemm": prefill,
         "decode_attention": attention,
-        "decode_tok_s": None,
+        "decode_tok_s": None if not e2e else e2e["precise"]["decode_tok_s"],
+        "e2e": e2e,
     }
     print(json.dumps(line))
     be.close()
