@@ -32,6 +32,11 @@ MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
 SHAPES = [(8192, 2048), (2048, 8192)]
 LANES = [1, 2, 4, 8]
 COPIES = 48                     # 48 x 10.5 MB per shape: past the 256 MiB MALL
+# HBM bytes per dispatch of the decode GEMV (M=1, 8192x2048), from two rocprofv3
+# --pmc runs of `bench.py --kernel gemv` (profiles/gemv_q4_m1_8192x2048.md):
+# FETCH_SIZE 5191.2 KiB x 2.0 + WRITE_SIZE 32.0 KiB x 1.0, the factors a 256 MiB
+# device copy gives (profiles/copy_256mib_calibration.md).
+GEMV_M1_TRAFFIC_BYTES = int((5191.2 * 2.0 + 32.0) * 1024)
 
 
 def gemv_bytes(N, K, M, group=32):
@@ -45,7 +50,80 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decode leg")
+    ap.add_argument("--kernel", choices=["gemv", "gemv8", "gemm", "attend", "copy"],
+                    help="run one kernel's workload alone in a loop (for rocprofv3) and exit")
     return ap.parse_args()
+
+
+def kernel_loop(be, name, reps):
+    """One kernel's workload alone, for counter runs: the decode GEMV (M=1,
+    8192x2048, rotated copies), the M=8 GEMV, the M=2048 prefill GEMM, the
+    L=16384 attention, or a 256 MiB device copy that calibrates FETCH_SIZE and
+    WRITE_SIZE against a known byte count."""
+    import ctypes
+    from igllm_amd.backend import synth_projection
+
+    if name == "copy":
+        nbytes = 256 << 20
+        src, dst = be.alloc(nbytes), be.alloc(nbytes)
+        lib = be.lib
+        hip = ctypes.CDLL("libamdhip64.so")
+        hip.hipMemcpyDtoD.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+        for _ in range(reps):
+            if hip.hipMemcpyDtoD(dst.ptr, src.ptr, nbytes) != 0:
+                raise RuntimeError("hipMemcpyDtoD failed")
+        be.sync()
+        print(json.dumps({"kernel": "copy", "bytes_each": nbytes, "reps": reps}))
+        del lib
+        return
+    if name in ("gemv", "gemv8"):
+        N, K = SHAPES[0]
+        M = 1 if name == "gemv" else 8
+        rot = Rotation(be, N, K)
+        _, _, act = synth_projection(N, K, M, seed=0)
+        a = be.upload(act)
+        o = be.alloc(M * N * 4)
+        be.sync()
+        be.mark()
+        for i in range(reps):
+            be.gemv_dev(rot.planes[i % COPIES], a, K, M, o, N)
+        be.mark()
+        us = be.marks_ms() * 1e3 / reps
+        print(json.dumps({"kernel": name, "N": N, "K": K, "M": M, "avg_us": round(us, 3),
+                          "algorithmic_bytes": gemv_bytes(N, K, M),
+                          "GBps": round(gemv_bytes(N, K, M) / (us * 1e-6) / 1e9, 1)}))
+        return
+    if name == "gemm":
+        N, K = SHAPES[0]
+        M = 2048
+        rot = Rotation(be, N, K)
+        a = be.alloc(M * K * 2)
+        c = be.alloc(M * N * 2)
+        rng = np.random.default_rng(0)
+        a.put((rng.normal(size=M * K).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))
+        be.sync()
+        be.mark()
+        for i in range(reps):
+            be.gemm_bf16_dev(rot.planes[i % COPIES], a, K, M, c, N)
+        be.mark()
+        us = be.marks_ms() * 1e3 / reps
+        print(json.dumps({"kernel": "gemm", "M": M, "N": N, "K": K, "avg_us": round(us, 2),
+                          "TFLOPs": round(2.0 * M * N * K / (us * 1e-6) / 1e12, 1)}))
+        return
+    if name == "attend":
+        L, head = 16384, 256
+        rng = np.random.default_rng(1)
+        kb = be.upload(rng.integers(0, 256, size=(L, head), dtype=np.uint8))
+        vb = be.upload(rng.integers(0, 256, size=(L, head), dtype=np.uint8))
+        q = be.upload(rng.normal(size=(8, head)).astype(np.float32))
+        o = be.alloc(8 * head * 4)
+        be.sync()
+        be.mark()
+        for _ in range(reps):
+            be.attend_dev(kb, vb, 1, 4.0 / 127, 4.0 / 127, L, 1, 8, head, q, 0, L, 1.0 / 16, o)
+        be.mark()
+        us = be.marks_ms() * 1e3 / reps
+        print(json.dumps({"kernel": "attend", "L": L, "avg_us": round(us, 2)}))
 
 
 def e2e_decode(be, prompt_count=2048, gen=256):
@@ -198,6 +276,10 @@ def main():
     from igllm_amd.backend import Backend, make_plane, synth_projection
 
     be = Backend(device=0, sum_limit=256, col_limit=8192, lane_limit=16)
+    if args.kernel:
+        kernel_loop(be, args.kernel, args.steps)
+        be.close()
+        return
     rot = {shape: Rotation(be, *shape) for shape in SHAPES}
     acts = {}
     outs = {}
@@ -341,9 +423,10 @@ def main():
                                "M in {1,2,4,8}, fp32 activations, weights rotated over "
                                f"{COPIES} copies per shape",
                    "step_bytes": step_bytes},
-        "roofline": {"bound": "hbm", "kernel": "gemv_q4_kernel<1,4> 8192x2048 M=1",
+        "roofline": {"bound": "hbm", "kernel": "gemv_q4_reg_kernel<1,4> 8192x2048 M=1",
                      "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": GEMV_M1_TRAFFIC_BYTES,
                      "algorithmic_bytes": gemv_algo, "avg_launch_us": round(gemv_us, 3)},
         "cpu_baseline": cpu,
         "gemv_sweep": sweep,
