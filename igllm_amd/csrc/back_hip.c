@@ -148,9 +148,7 @@ static int plane_supported(const igl_plane *sheet) {
 static size_t plane_part_floats(const igl_desk_state *st, const igl_plane *sheet) {
   size_t most = 0;
   for (int lanes = 1; lanes <= IGL_GEMV_LANES; ++lanes) {
-    int cols = igl_gemv_chunk_cols(lanes, sheet->col_count, st->lds_limit);
-    size_t chunks = (size_t)((sheet->col_count + cols - 1) / cols);
-    size_t need = chunks > 1 ? chunks * (size_t)lanes * (size_t)sheet->row_count : 0;
+    size_t need = igl_gemv_part_floats(lanes, sheet->row_count, sheet->col_count, st->lds_limit);
     if (need > most) most = need;
   }
   return most;

@@ -346,6 +346,389 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_reg_kernel(GemvArgs a) {
   }
 }
 
+// ---- the small-lane form on the matrix cores (1..8 lanes) -----------------
+//
+// One v_mfma_f32_16x16x32_f16 per (16 rows, unit):
+//   * A (16 rows x 32 codes) is c - code_bias, exact in binary16.  A lane
+//     loads one row's whole unit (16 bytes); four units sit across the four
+//     16-lane groups of a wave and a 4 x 4 exchange of dwords between the
+//     groups (two permlane32 and two permlane16 swaps) leaves in group q the
+//     q-th eight codes of each unit, the layout the instruction reads.
+//   * B (32 codes x 16 columns): column m < 8 is lane m's activations times
+//     2^e rounded to binary16 (the high part), column m + 8 the remainder
+//     rounded again (the low part), so hi + lo carries x to 22 bits.  e is
+//     chosen per (unit, lane) to put the unit's largest |x| in [2^14, 2^15):
+//     neither part overflows, and the low part stays normal.
+//   * D columns m and m + 8 hold 2^e sum (c - bias) x_hi and ... x_lo, each a
+//     sum of exact products in fp32; 2^-e and the gain multiply them into
+//     the fp32 accumulator, and row_shr:8 adds the pair at the end.
+// A workgroup owns `tiles_per_block` 16-row tiles over a chunk of
+// `chunk_units` units; its four waves split that as tiles x K-parts and build
+// the chunk's B tiles and gains in LDS once while their code loads are in
+// flight.  K-parts add in a fixed order through LDS; K-chunks (blockIdx.y)
+// write partials that gemv_chunk_sum_kernel adds in chunk order.
+struct GemvMfmaArgs {
+  const uint8_t *codes;
+  long long row_stride;
+  const float *gains;
+  int gain_stride;
+  int group_shift;
+  const float *act;
+  int act_stride;
+  int act_vec;
+  float *out;             // [M][out_stride], or partials [chunk][M][N]
+  int out_stride;
+  int M, N, K;
+  int tiles_per_block;    // 1, 2 or 4
+  int chunk_units;        // units of K one workgroup covers
+  float code_bias;
+  int gain_vec;           // one gain a unit, rows 16-byte aligned: float4 gain loads
+};
+
+__device__ __forceinline__ void lane_group_exchange(uint32_t &d0, uint32_t &d1, uint32_t &d2,
+                                                    uint32_t &d3) {
+  // Group g's dword j goes to group j's register g.
+  auto s02 = __builtin_amdgcn_permlane32_swap(d0, d2, false, false);
+  auto s13 = __builtin_amdgcn_permlane32_swap(d1, d3, false, false);
+  auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+  auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+  d0 = s01[0];
+  d1 = s01[1];
+  d2 = s23[0];
+  d3 = s23[1];
+}
+
+// Eight codes of a dword as binary16 (c - bias), in the order 0,4,1,5,2,6,3,7.
+__device__ __forceinline__ half8_t codes_less_bias(uint32_t d, uint32_t exp16, half2_t shift) {
+  const half2_t p0 = nibble_pair16<0>(d, exp16) - shift;
+  const half2_t p1 = nibble_pair16<1>(d, exp16) - shift;
+  const half2_t p2 = nibble_pair16<2>(d, exp16) - shift;
+  const half2_t p3 = nibble_pair16<3>(d, exp16) - shift;
+  return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+constexpr int kMfmaGains = 4;  // pad of the gain rows in LDS (keeps 16-byte reads aligned)
+
+template <int NG, bool VEC>
+__global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
+  extern __shared__ uint4_t lds_u4[];
+  const int RTB = a.tiles_per_block;
+  const int parts = 4 / RTB;
+  const int CU = a.chunk_units;
+  const int rows_b = RTB * 16;
+  const int pitch = rows_b + kMfmaGains;
+  uint4_t *bt = lds_u4;                                       // [CU][4 groups][16 columns]
+  float *gs = reinterpret_cast<float *>(bt + CU * 64);        // [CU][pitch]
+  float *sc = gs + CU * pitch;                                // [CU][8]
+  float *red = sc + CU * 8;                                   // [parts][RTB][16][8]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int t = wave % RTB;
+  const int part = wave / RTB;
+  const int r = lane & 15;
+  const int q = lane >> 4;
+  const int chunk = blockIdx.y;
+  const int unit_c0 = chunk * CU;
+  const int row_b0 = blockIdx.x * rows_b;
+  const int u_w0 = part * (NG * 4);
+
+  // Staging loads go out first and unconditionally (indices past the end are
+  // clamped and their values dropped), then the code loads, so the block
+  // waits one round trip for its gains and activations while the codes are
+  // still in flight.
+  // Gains: float4 runs of each row's chunk (at most 4 a thread: 64 rows x 16).
+  const int gain_runs = rows_b * (CU >> 2);
+  float4_t gv[4];
+  if (VEC) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = min(tid + 256 * k, gain_runs - 1);
+      const int rr = i / (CU >> 2);
+      const int c4 = i - rr * (CU >> 2);
+      const int row = min(row_b0 + rr, a.N - 1);
+      gv[k] = *reinterpret_cast<const float4_t *>(a.gains + (size_t)row * (size_t)a.gain_stride +
+                                                 unit_c0 + 4 * c4);
+    }
+  }
+  // Activations: item (unit, lane m, group g) is x[m][32 u + 8 g .. + 7] (at
+  // most 8 a thread: 64 units x 8 lanes x 4 groups).
+  const int items = CU * a.M * 4;
+  float4_t xa[8], xb[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int i = min(tid + 256 * k, items - 1);
+    const int um = i >> 2;
+    const int u = um / a.M;
+    const int m = um - u * a.M;
+    const float *src =
+        a.act + (size_t)m * (size_t)a.act_stride + (size_t)(unit_c0 + u) * 32 + 8 * (i & 3);
+    if (VEC) {
+      xa[k] = *reinterpret_cast<const float4_t *>(src);
+      xb[k] = *reinterpret_cast<const float4_t *>(src + 4);
+    } else {
+      xa[k] = float4_t{src[0], src[1], src[2], src[3]};
+      xb[k] = float4_t{src[4], src[5], src[6], src[7]};
+    }
+  }
+
+  // Codes: lane (r, q) takes unit u_w0 + 4 g + q of its row.
+  uint4_t w[NG];
+  {
+    const int row = min(row_b0 + 16 * t + r, a.N - 1);  // tail rows are computed, never stored
+    const uint4_t *src =
+        reinterpret_cast<const uint4_t *>(a.codes + (size_t)row * (size_t)a.row_stride) + unit_c0 +
+        u_w0 + q;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) w[g] = __builtin_nontemporal_load(src + 4 * g);
+  }
+
+  // Gains stored [unit][row].
+  if (VEC) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = tid + 256 * k;
+      if (i < gain_runs) {
+        const int rr = i / (CU >> 2);
+        const int u = 4 * (i - rr * (CU >> 2));
+        gs[(u + 0) * pitch + rr] = gv[k].x;
+        gs[(u + 1) * pitch + rr] = gv[k].y;
+        gs[(u + 2) * pitch + rr] = gv[k].z;
+        gs[(u + 3) * pitch + rr] = gv[k].w;
+      }
+    }
+  } else {
+    for (int i = tid; i < CU * rows_b; i += 256) {
+      const int rr = i / CU;
+      const int u = i - rr * CU;
+      const int row = min(row_b0 + rr, a.N - 1);
+      gs[u * pitch + rr] =
+          a.gains[(size_t)row * (size_t)a.gain_stride + ((unsigned)(unit_c0 + u) >> a.group_shift)];
+    }
+  }
+
+  // B tiles; the four items of a (unit, lane) sit in one quad and agree on e.
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int i = tid + 256 * k;
+    if (i >= items) break;
+    const int g = i & 3;
+    const int um = i >> 2;
+    const int u = um / a.M;
+    const int m = um - u * a.M;
+    const float v[8] = {xa[k].x, xa[k].y, xa[k].z, xa[k].w, xb[k].x, xb[k].y, xb[k].z, xb[k].w};
+    float peak = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) peak = fmaxf(peak, fabsf(v[j]));
+    peak = fmaxf(peak, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, peak), 0xB1, 0xF, 0xF, false)));
+    peak = fmaxf(peak, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, peak), 0x4E, 0xF, 0xF, false)));
+    int e = 0;
+    if (peak > 0.0f && peak <= 3.4e38f) {
+      int power;
+      (void)frexpf(peak, &power);  // peak in [2^(power-1), 2^power)
+      e = min(max(15 - power, -126), 126);
+    }
+    const float up = __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
+    if (g == 0) sc[u * 8 + m] = __builtin_bit_cast(float, (uint32_t)(127 - e) << 23);
+    half8_t hi, lo;
+    constexpr int kOrder[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float s = v[kOrder[j]] * up;
+      const _Float16 h = (_Float16)s;
+      hi[j] = h;
+      lo[j] = (_Float16)(s - (float)h);
+    }
+    bt[(u * 4 + g) * 16 + m] = __builtin_bit_cast(uint4_t, hi);
+    bt[(u * 4 + g) * 16 + m + 8] = __builtin_bit_cast(uint4_t, lo);
+  }
+  __syncthreads();
+
+  const uint32_t exp16 = 0x4C004C00u;
+  const _Float16 lift = (_Float16)(16.0f + a.code_bias);
+  const half2_t shift = half2_t{lift, lift};
+  const int m_col = r & 7;
+  float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  // A group is four units: its B tiles, gains and scales are read from LDS
+  // one group ahead, its four products issue back to back, then the gains.
+  const float *gbase = gs + 16 * t + 4 * q;
+  uint4_t bq[2][4];
+  float4_t gq[2][4];
+  float sq[2][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int u = u_w0 + j;
+    bq[0][j] = bt[u * 64 + lane];
+    gq[0][j] = *reinterpret_cast<const float4_t *>(gbase + u * pitch);
+    sq[0][j] = sc[u * 8 + m_col];
+  }
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const int cur = g & 1;
+    if (g + 1 < NG) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int u = u_w0 + 4 * (g + 1) + j;
+        bq[cur ^ 1][j] = bt[u * 64 + lane];
+        gq[cur ^ 1][j] = *reinterpret_cast<const float4_t *>(gbase + u * pitch);
+        sq[cur ^ 1][j] = sc[u * 8 + m_col];
+      }
+    }
+    uint32_t d[4] = {w[g].x, w[g].y, w[g].z, w[g].w};
+    lane_group_exchange(d[0], d[1], d[2], d[3]);
+    float4_t D[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      D[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_less_bias(d[j], exp16, shift),
+                                                    __builtin_bit_cast(half8_t, bq[cur][j]),
+                                                    float4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float s = sq[cur][j];
+      acc.x = __builtin_fmaf(gq[cur][j].x * s, D[j].x, acc.x);
+      acc.y = __builtin_fmaf(gq[cur][j].y * s, D[j].y, acc.y);
+      acc.z = __builtin_fmaf(gq[cur][j].z * s, D[j].z, acc.z);
+      acc.w = __builtin_fmaf(gq[cur][j].w * s, D[j].w, acc.w);
+    }
+  }
+  // Low columns into their high partners: lane r >= 8 holds lane m = r - 8.
+  acc.x += dpp_move<0x118>(acc.x);
+  acc.y += dpp_move<0x118>(acc.y);
+  acc.z += dpp_move<0x118>(acc.z);
+  acc.w += dpp_move<0x118>(acc.w);
+
+  const int m = r - 8;
+  const bool owner = r >= 8 && m < a.M;
+  float *dst;
+  int dst_stride;
+  if (gridDim.y > 1) {
+    dst = a.out + (size_t)chunk * (size_t)a.M * (size_t)a.N;
+    dst_stride = a.N;
+  } else {
+    dst = a.out;
+    dst_stride = a.out_stride;
+  }
+  const int row0 = row_b0 + 16 * t + 4 * q;
+  if (parts == 1) {
+    if (owner) {
+      float *o = dst + (size_t)m * (size_t)dst_stride;
+      if (row0 + 0 < a.N) o[row0 + 0] = acc.x;
+      if (row0 + 1 < a.N) o[row0 + 1] = acc.y;
+      if (row0 + 2 < a.N) o[row0 + 2] = acc.z;
+      if (row0 + 3 < a.N) o[row0 + 3] = acc.w;
+    }
+    return;
+  }
+  if (owner) {
+    float *slot = red + ((part * RTB + t) * 16 + 4 * q) * 8 + m;
+    slot[0] = acc.x;
+    slot[8] = acc.y;
+    slot[16] = acc.z;
+    slot[24] = acc.w;
+  }
+  __syncthreads();
+  if (part == 0 && owner) {
+    float *o = dst + (size_t)m * (size_t)dst_stride;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float total = 0.0f;
+      for (int k = 0; k < parts; ++k) total += red[((k * RTB + t) * 16 + 4 * q + i) * 8 + m];
+      if (row0 + i < a.N) o[row0 + i] = total;
+    }
+  }
+}
+
+// Work split of the matrix-core form for `lanes` lanes of an N x K plane, or 0
+// when the form does not apply (K not a multiple of 128, or more than 8 lanes).
+struct GemvMfmaPlan {
+  int tiles_per_block, chunk_units, chunks, groups_per_wave;
+};
+
+static int gemv_mfma_plan(int lanes, int N, int K, GemvMfmaPlan *plan) {
+  if (lanes < 1 || lanes > 8 || K % 128 || N < 1) return 0;
+  const int units = K / 32;
+  const int groups = units / 4;
+  const int tiles = (N + 15) / 16;
+  if (units <= 64) {
+    int rtb = 0;
+    for (int c = 4; c >= 1; c /= 2)
+      if ((tiles + c - 1) / c >= 256 && groups % (4 / c) == 0) { rtb = c; break; }
+    if (!rtb)
+      for (int c = 1; c <= 4; c *= 2)
+        if (groups % (4 / c) == 0) { rtb = c; break; }
+    plan->tiles_per_block = rtb;
+    plan->chunk_units = units;
+    plan->chunks = 1;
+    plan->groups_per_wave = groups / (4 / rtb);
+  } else {
+    // The fewest chunks that give 256 workgroups, keeping two groups a wave.
+    int kb = 0;
+    for (int c = (units + 63) / 64; c <= groups; ++c) {
+      if (groups % c || groups / c > 16) continue;
+      kb = c;
+      if ((tiles + 3) / 4 * c >= 256 || groups / c <= 2) break;
+    }
+    if (!kb) return 0;
+    plan->tiles_per_block = 4;
+    plan->chunk_units = units / kb;
+    plan->chunks = kb;
+    plan->groups_per_wave = groups / kb;
+  }
+  return plan->groups_per_wave >= 1 && plan->groups_per_wave <= 16;
+}
+
+static size_t gemv_mfma_lds(const GemvMfmaPlan &p) {
+  const int rows_b = p.tiles_per_block * 16;
+  return (size_t)p.chunk_units * 1024 + (size_t)p.chunk_units * (rows_b + kMfmaGains) * 4 +
+         (size_t)p.chunk_units * 32 + (size_t)4 * 16 * 8 * 4;
+}
+
+template <int NG, bool VEC>
+static hipError_t gemv_mfma_launch_form(const GemvMfmaArgs &a, const GemvMfmaPlan &p,
+                                        hipStream_t stream) {
+  const size_t lds = gemv_mfma_lds(p);
+  static size_t lds_granted = 65536;  // launches above 64 KiB ask once
+  if (lds > lds_granted) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q4_mfma_kernel<NG, VEC>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    lds_granted = lds;
+  }
+  const int tiles = (a.N + 15) / 16;
+  dim3 grid((tiles + p.tiles_per_block - 1) / p.tiles_per_block, p.chunks);
+  hipLaunchKernelGGL((gemv_q4_mfma_kernel<NG, VEC>), grid, dim3(256), lds, stream, a);
+  return hipGetLastError();
+}
+
+template <int NG>
+static hipError_t gemv_mfma_launch(const GemvMfmaArgs &a, const GemvMfmaPlan &p, hipStream_t stream) {
+  return a.act_vec && a.gain_vec ? gemv_mfma_launch_form<NG, true>(a, p, stream)
+                                 : gemv_mfma_launch_form<NG, false>(a, p, stream);
+}
+
+static hipError_t gemv_mfma_dispatch(const GemvMfmaArgs &a, const GemvMfmaPlan &p, hipStream_t stream) {
+  switch (p.groups_per_wave) {
+    case 1: return gemv_mfma_launch<1>(a, p, stream);
+    case 2: return gemv_mfma_launch<2>(a, p, stream);
+    case 3: return gemv_mfma_launch<3>(a, p, stream);
+    case 4: return gemv_mfma_launch<4>(a, p, stream);
+    case 5: return gemv_mfma_launch<5>(a, p, stream);
+    case 6: return gemv_mfma_launch<6>(a, p, stream);
+    case 7: return gemv_mfma_launch<7>(a, p, stream);
+    case 8: return gemv_mfma_launch<8>(a, p, stream);
+    case 9: return gemv_mfma_launch<9>(a, p, stream);
+    case 10: return gemv_mfma_launch<10>(a, p, stream);
+    case 11: return gemv_mfma_launch<11>(a, p, stream);
+    case 12: return gemv_mfma_launch<12>(a, p, stream);
+    case 13: return gemv_mfma_launch<13>(a, p, stream);
+    case 14: return gemv_mfma_launch<14>(a, p, stream);
+    case 15: return gemv_mfma_launch<15>(a, p, stream);
+    case 16: return gemv_mfma_launch<16>(a, p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 template <int M, int R>
 static hipError_t gemv_reg_launch(const GemvArgs &a, hipStream_t stream) {
   const int tiles = (a.N + R - 1) / R;
@@ -396,6 +779,18 @@ extern "C" int igl_gemv_chunk_cols(int lanes, int K, int lds_limit) {
   return per * 32;
 }
 
+// Floats of K-chunk partials a launch of `lanes` lanes over an N x K plane
+// writes (0 when it needs none).
+extern "C" size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit) {
+  GemvMfmaPlan plan;
+  if (lanes >= 3 && gemv_mfma_plan(lanes, N, K, &plan))
+    return plan.chunks > 1 ? (size_t)plan.chunks * (size_t)lanes * (size_t)N : 0;
+  if (lanes <= 2 && K / 32 <= 4 * kWave) return 0;
+  const int cols = igl_gemv_chunk_cols(lanes, K, lds_limit);
+  const size_t chunks = (size_t)((K + cols - 1) / cols);
+  return chunks > 1 ? chunks * (size_t)lanes * (size_t)N : 0;
+}
+
 // Launches y = W x for 1..8 lanes.  `part` must hold chunks * lanes * N floats
 // when the plane needs more than one K-chunk, and may be NULL otherwise;
 // `lds_limit` is the device's LDS bytes per workgroup.
@@ -416,6 +811,40 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
   a.K = K;
   a.unit_bias = 16.0f + (float)code_bias;
   a.act_vec = ((((uintptr_t)act) & 15u) == 0 && (act_stride & 3) == 0) ? 1 : 0;
+  // Three to eight lanes on the matrix cores where the plane's width allows.
+  GemvMfmaPlan plan;
+  if (lanes >= 3 && gemv_mfma_plan(lanes, N, K, &plan)) {
+    GemvMfmaArgs b;
+    b.codes = codes;
+    b.row_stride = row_stride;
+    b.gains = gains;
+    b.gain_stride = gain_stride;
+    b.group_shift = a.group_shift;
+    b.act = act;
+    b.act_stride = act_stride;
+    b.act_vec = a.act_vec;
+    b.M = lanes;
+    b.N = N;
+    b.K = K;
+    b.tiles_per_block = plan.tiles_per_block;
+    b.chunk_units = plan.chunk_units;
+    b.code_bias = (float)code_bias;
+    b.gain_vec = (a.group_shift == 0 && (((uintptr_t)gains) & 15u) == 0 && (gain_stride & 3) == 0) ? 1 : 0;
+    if (plan.chunks > 1) {
+      if (!part) return hipErrorInvalidValue;
+      b.out = part;
+      b.out_stride = N;
+    } else {
+      b.out = out;
+      b.out_stride = out_stride;
+    }
+    hipError_t e = gemv_mfma_dispatch(b, plan, stream);
+    if (e != hipSuccess || plan.chunks == 1) return e;
+    const int total = lanes * N;
+    hipLaunchKernelGGL(gemv_chunk_sum_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, part,
+                       plan.chunks, lanes, N, out, out_stride);
+    return hipGetLastError();
+  }
   // One and two lanes with at most 256 units a row: the register form, with
   // enough waves on a row tile that each lane holds one unit.
   if (lanes <= 2 && K / 32 <= 4 * kWave) {

@@ -16,6 +16,7 @@ extern "C" {
 
 int igl_gemv_rows_per_tile(int lanes);
 int igl_gemv_chunk_cols(int lanes, int K, int lds_limit);
+size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit);
 hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_stride, const float *gains,
                               int gain_stride, int group_size, int code_bias, const float *act,
                               int act_stride, int lanes, float *out, int out_stride, int N, int K,
