@@ -357,8 +357,9 @@ int igl_attend_lanes_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t
   if (grow_dev(st, &st->work_dev, &st->work_floats, need) != IGL_OKAY) return IGL_FAIL_MEMORY;
   return hip_check(st, igl_launch_attend(key_store, value_store, format, key_scale, value_scale,
                                          cache_span, kv_width, kv_count, group_share, head_size,
-                                         query_dev, lane_stride, place_first, window, lane_count,
-                                         score_scale, blend_out_dev, st->work_dev, st->stream));
+                                         query_dev, lane_stride, place_first, NULL, window,
+                                         lane_count, score_scale, blend_out_dev, st->work_dev,
+                                         st->stream));
 }
 
 int igl_attend_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t *value_store,

@@ -50,6 +50,7 @@ struct AttendArgs {
   int kv_width;
   int cache_span;
   int place0;                  // position of lane 0; lane l is at place0 + l
+  const int *place_dev;        // when set, lane 0's position is read here instead
   int window;                  // positions a lane sees (0: all from position 0)
   int chunks;                  // chunk slots per lane in the partial buffers
   int q_stride;                // floats between lanes of query / blend
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
   const int lane_id = blockIdx.z;
   // The lane's visible positions: the last `window` up to and including its
   // own (session_attend 11516-11526); `start` is the first, ring slot p % span.
-  const int pos = a.place0 + lane_id;
+  const int pos = (a.place_dev ? *a.place_dev : a.place0) + lane_id;
   const int span_count = a.window > 0 ? min(pos + 1, a.window) : pos + 1;
   const int place_start = pos - span_count + 1;
   if (chunk * kAttendChunk >= span_count) return;  // the whole block is past this lane's span
@@ -290,14 +291,15 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
 __global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out_all,
                                                            const float *part_peak_all,
                                                            const float *part_total_all,
-                                                           int chunk_slots, int place0, int window,
+                                                           int chunk_slots, int place0,
+                                                           const int *place_dev, int window,
                                                            int head_count, int head_size,
                                                            float *blend_all, int o_stride) {
   extern __shared__ float wgt[];  // [chunks]
   __shared__ float red[256];
   const int h = blockIdx.x;
   const int lane = blockIdx.y;
-  const int pos = place0 + lane;
+  const int pos = (place_dev ? *place_dev : place0) + lane;
   const int span = window > 0 ? min(pos + 1, window) : pos + 1;
   const int chunks = (span + kAttendChunk - 1) / kAttendChunk;
   const size_t base = (size_t)lane * chunk_slots;
@@ -357,14 +359,17 @@ static int attend_max_span(int place0, int window, int lanes) {
 
 // `lanes` query lanes at positions place0 .. place0 + lanes - 1, each seeing
 // the last `window` positions up to its own (0: every position from 0).  Lane
-// l's query and output are `q_stride` floats after lane l - 1's.
+// l's query and output are `q_stride` floats after lane l - 1's.  With
+// `place_dev`, lane 0's position is read from device memory when the kernels
+// run and `place0` is only its upper bound, which sizes the grid (a launch
+// that a graph replays at every step).
 extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t *value_store,
                                         int fmt, float key_scale, float value_scale,
                                         int cache_span, int kv_width, int kv_count,
                                         int group_share, int head_size, const float *query,
-                                        int q_stride, int place0, int window, int lanes,
-                                        float score_scale, float *blend_out, float *work,
-                                        hipStream_t stream) {
+                                        int q_stride, int place0, const int *place_dev,
+                                        int window, int lanes, float score_scale,
+                                        float *blend_out, float *work, hipStream_t stream) {
   AttendArgs a;
   const int chunks = (attend_max_span(place0, window, lanes) + kAttendChunk - 1) / kAttendChunk;
   const int head_count = kv_count * group_share;
@@ -374,6 +379,7 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
   a.kv_width = kv_width;
   a.cache_span = cache_span;
   a.place0 = place0;
+  a.place_dev = place_dev;
   a.window = window;
   a.chunks = chunks;
   a.q_stride = q_stride;
@@ -402,7 +408,7 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(attend_merge_kernel, dim3(head_count, lanes), dim3(256),
                      chunks * sizeof(float), stream, a.part_out, a.part_peak, a.part_total, chunks,
-                     place0, window, head_count, head_size, blend_out, q_stride);
+                     place0, place_dev, window, head_count, head_size, blend_out, q_stride);
   return hipGetLastError();
 }
 

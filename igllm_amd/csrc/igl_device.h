@@ -38,6 +38,56 @@ __device__ __forceinline__ float wave_sum_to_last(float v) {
   return v;
 }
 
+// The same six DPP steps on a double (two 32-bit moves a step).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double dpp_move_f64(double v) {
+  const uint64_t bits = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)bits, CTRL, ROW_MASK, 0xF, true);
+  const uint32_t hi =
+      (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(bits >> 32), CTRL, ROW_MASK, 0xF, true);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ double wave_sum_f64_to_last(double v) {
+  v += dpp_move_f64<0xB1>(v);
+  v += dpp_move_f64<0x4E>(v);
+  v += dpp_move_f64<0x141>(v);
+  v += dpp_move_f64<0x140>(v);
+  v += dpp_move_f64<0x142, 0xA>(v);
+  v += dpp_move_f64<0x143, 0xC>(v);
+  return v;
+}
+
+__device__ __forceinline__ double lane_read_f64(double v, int lane) {
+  const uint64_t bits = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)bits, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(bits >> 32), lane);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Sum of one double per thread over a workgroup of up to 16 waves, the same
+// total in every thread: DPP within each wave, then the wave sums in wave
+// order.  `red` holds one double a wave; the trailing barrier lets the caller
+// reuse it.
+__device__ __forceinline__ double block_sum_f64(double v, double *red) {
+  const int waves = (blockDim.x + 63) >> 6;
+  v = wave_sum_f64_to_last(v);
+  if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double total = red[0];
+  for (int w = 1; w < waves; ++w) total += red[w];
+  __syncthreads();
+  return total;
+}
+
+// The reference's RMS step (kern_norm_rms, app_core.c:4667-4684):
+// (float)pow(square_total / n + eps, -0.5), as 1 / sqrt in double.  The two
+// doubles differ by at most an ulp, so the floats they round to are equal
+// unless the double lies within an ulp of a float rounding boundary.
+__device__ __forceinline__ float rms_shrink(double square_total, int n, float eps) {
+  return (float)(1.0 / __builtin_sqrt(square_total / (double)n + (double)eps));
+}
+
 // Sum over each 16-lane row; every lane of the row holds the row total.
 __device__ __forceinline__ float row16_sum(float v) {
   v += dpp_move<0xB1>(v);

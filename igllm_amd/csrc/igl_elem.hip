@@ -14,18 +14,12 @@ namespace igl {
 // x * (mean + eps)^-1/2 * gain.
 __global__ void norm_rms_kernel(const float *in, const float *gain, int n, int stride, float eps,
                                 float *out) {
-  __shared__ double part[256];
+  __shared__ double part[16];
   const float *x = in + (size_t)blockIdx.x * stride;
   float *y = out + (size_t)blockIdx.x * stride;
   double acc = 0.0;
   for (int i = threadIdx.x; i < n; i += blockDim.x) acc += (double)x[i] * (double)x[i];
-  part[threadIdx.x] = acc;
-  __syncthreads();
-  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
-    __syncthreads();
-  }
-  const float shrink = (float)pow(part[0] / (double)n + (double)eps, -0.5);
+  const float shrink = rms_shrink(block_sum_f64(acc, part), n, eps);
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
     const float v = x[i] * shrink;
     y[i] = gain ? v * gain[i] : v;

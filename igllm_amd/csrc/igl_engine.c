@@ -48,6 +48,14 @@ typedef struct eng_tensor {
   size_t    begin, end;
 } eng_tensor;
 
+/* Host side of a decode step, in pinned memory so a captured graph's copies
+ * read and write it at every replay. */
+typedef struct igl_step_io {
+  int32_t place, id;   /* copied to ctl_dev[0..1] */
+  int32_t pick;        /* copied back from pick_dev[0..1] */
+  float margin;
+} igl_step_io;
+
 typedef struct eng_layer {
   int full, shared, source, keep, head_size, inner, cache_span;
   igl_plane q, k, v, o, gate, up, down, ple_gate, ple_proj;
@@ -76,12 +84,18 @@ struct igl_engine {
   const float *ple_norm, *final_norm;
   eng_layer layer[ENG_LAYER_LIMIT];
   /* device rooms, lane_limit lanes each */
-  int32_t *ids_dev;
+  int32_t *ctl_dev;   /* [0] position of lane 0, [1 ..] the lanes' token ids */
+  int32_t *ids_dev;   /* ctl_dev + 1 */
   float *state, *scrap, *lift, *q, *k, *v, *blend, *gate, *rise, *ple_seed, *ple_room, *logits;
+  float *attend_work;
+  size_t attend_floats;
   int q_stride, kv_stride, inner_max, ple_stride;
   void *pick_work;
-  int32_t *pick_dev;
-  float *margin_dev;
+  int32_t *pick_dev;  /* [0] the pick, [1] its margin (as float bits) */
+  /* the decode step as one captured graph */
+  igl_step_io *io;    /* pinned: what the step reads and writes on the host */
+  int graph_on, graph_ready, graph_tried;
+  hipGraphExec_t graph;
 };
 
 /* ---- a little JSON, enough for config.json and a safetensors header ------ */
@@ -347,7 +361,9 @@ int igl_engine_open(igl_engine **out, igl_desk *desk, const char *folder, int wi
   e->cap = (float)member_number(text, "final_logit_softcapping", 0.0);
   e->window_limit = (int)member_number(text, "max_position_embeddings", 131072);
   if (window_limit > 0 && window_limit < e->window_limit) e->window_limit = window_limit;
-  if (e->layers < 1 || e->layers > ENG_LAYER_LIMIT || e->kv_heads != 1 || e->heads != 8) {
+  /* norm_add holds a row of up to 4096 per workgroup */
+  if (e->layers < 1 || e->layers > ENG_LAYER_LIMIT || e->kv_heads != 1 || e->heads != 8 ||
+      e->hidden > 4096) {
     code = IGL_FAIL_SUPPORT;
     goto fail;
   }
@@ -503,7 +519,17 @@ int igl_engine_open(igl_engine **out, igl_desk *desk, const char *folder, int wi
     size_t lanes = (size_t)e->lane_limit;
     e->kv_stride = e->q_stride / e->heads;
     e->ple_stride = e->layers * e->ple;
-    if ((code = dev_alloc((void **)&e->ids_dev, lanes * sizeof(int32_t))) ||
+    int widest = 0;
+    size_t one, many;
+    for (int i = 0; i < e->layers; ++i)
+      if (e->layer[i].head_size > widest) widest = e->layer[i].head_size;
+    /* attention partials: a decode step at the last position, or a batch */
+    one = igl_attend_work_floats(e->window_limit - 1, 0, 1, e->heads, widest);
+    many = igl_attend_work_floats(e->window_limit - e->lane_limit > 0 ? e->window_limit - e->lane_limit : 0,
+                                  0, e->lane_limit, e->heads, widest);
+    e->attend_floats = one > many ? one : many;
+    if ((code = dev_alloc((void **)&e->ctl_dev, (lanes + 1) * sizeof(int32_t))) ||
+        (code = dev_alloc((void **)&e->attend_work, e->attend_floats * sizeof(float))) ||
         (code = dev_alloc((void **)&e->state, lanes * e->hidden * 4)) ||
         (code = dev_alloc((void **)&e->scrap, lanes * e->hidden * 4)) ||
         (code = dev_alloc((void **)&e->lift, lanes * e->hidden * 4)) ||
@@ -517,9 +543,15 @@ int igl_engine_open(igl_engine **out, igl_desk *desk, const char *folder, int wi
         (code = dev_alloc((void **)&e->ple_room, lanes * e->ple_stride * 4)) ||
         (code = dev_alloc((void **)&e->logits, lanes * (size_t)e->vocab * 4)) ||
         (code = dev_alloc(&e->pick_work, igl_pick_work_bytes())) ||
-        (code = dev_alloc((void **)&e->pick_dev, sizeof(int32_t))) ||
-        (code = dev_alloc((void **)&e->margin_dev, sizeof(float))))
+        (code = dev_alloc((void **)&e->pick_dev, 2 * sizeof(int32_t))))
       goto fail;
+    e->ids_dev = e->ctl_dev + 1;
+    if (hipHostMalloc((void **)&e->io, sizeof(igl_step_io), hipHostMallocDefault) != hipSuccess) {
+      e->io = NULL;
+      code = IGL_FAIL_MEMORY;
+      goto fail;
+    }
+    e->graph_on = 1;
   }
   free(config);
   close(fd);
@@ -547,13 +579,15 @@ void igl_engine_close(igl_engine *e) {
   igl_plane_detach(e->desk, &e->ple_embed);
   igl_plane_detach(e->desk, &e->ple_lift);
   igl_plane_detach(e->desk, &e->head);
+  if (e->graph_ready) (void)hipGraphExecDestroy(e->graph);
   {
-    void *bufs[] = {e->payload_dev, e->ids_dev, e->state, e->scrap, e->lift, e->q, e->blend, e->k, e->v,
-                    e->gate, e->rise, e->ple_seed, e->ple_room, e->logits, e->pick_work, e->pick_dev,
-                    e->margin_dev, e->steps_dev[0], e->steps_dev[1]};
+    void *bufs[] = {e->payload_dev, e->ctl_dev, e->attend_work, e->state, e->scrap, e->lift, e->q,
+                    e->blend, e->k, e->v, e->gate, e->rise, e->ple_seed, e->ple_room, e->logits,
+                    e->pick_work, e->pick_dev, e->steps_dev[0], e->steps_dev[1]};
     for (size_t j = 0; j < sizeof(bufs) / sizeof(bufs[0]); ++j)
       if (bufs[j]) (void)hipFree(bufs[j]);
   }
+  if (e->io) (void)hipHostFree(e->io);
   if (e->map) munmap(e->map, e->map_bytes);
   free(e->tensor);
   free(e);
@@ -594,65 +628,133 @@ static int norm_rows(igl_engine *e, const float *in, const float *gain, int n, i
   return igl_norm_rms_dev(e->desk, in, gain, n, lanes, stride, e->eps, out);
 }
 
-/* One layer for `lanes` lanes at positions place .. place + lanes - 1
- * (session_layer 11637-11743 with session_attend 11455-11580). */
-static int run_layer(igl_engine *e, int li, int place, int lanes) {
-  eng_layer *L = &e->layer[li];
-  const eng_layer *S = &e->layer[L->source];
-  const int H = e->hidden, hs = L->head_size, qw = e->heads * hs;
-  const int kind = L->full ? 1 : 0;
-  hipStream_t st = e->stream;
+/* One plane of a one-lane group launch. */
+typedef struct eng_group {
+  int count;
+  const uint8_t *codes[3];
+  long long row_stride[3];
+  const float *gains[3];
+  int gain_stride[3], rows[3];
+  float *out[3];
+} eng_group;
 
-  OKAY(norm_rows(e, e->state, L->enter_norm, H, lanes, H, e->scrap));
-  OKAY(project(e, &L->q, e->scrap, H, lanes, e->q, e->q_stride));
-  RUN(igl_launch_head_prep(e->q, e->q_stride, e->heads, hs, lanes, L->q_norm, e->eps,
-                           e->steps_dev[kind], 1, place, st));
-  if (!L->shared) {
-    OKAY(project(e, &L->k, e->scrap, H, lanes, e->k, e->kv_stride));
-    OKAY(project(e, &L->v, e->scrap, H, lanes, e->v, e->kv_stride));
-    RUN(igl_launch_head_prep(e->k, e->kv_stride, 1, hs, lanes, L->k_norm, e->eps,
-                             e->steps_dev[kind], 1, place, st));
-    RUN(igl_launch_head_prep(e->v, e->kv_stride, 1, hs, lanes, NULL, e->eps, e->steps_dev[kind], 0,
-                             place, st));
-    RUN(igl_launch_cache_lay_rows(e->k, e->kv_stride, hs, L->k_scale, L->k_store, L->cache_span,
-                                  place, lanes, st));
-    RUN(igl_launch_cache_lay_rows(e->v, e->kv_stride, hs, L->v_scale, L->v_store, L->cache_span,
-                                  place, lanes, st));
+static void group_add(igl_engine *e, eng_group *g, const igl_plane *p, float *out) {
+  g->codes[g->count] = dev_codes(e, p);
+  g->row_stride[g->count] = (long long)p->row_stride;
+  g->gains[g->count] = dev_gains(e, p);
+  g->gain_stride[g->count] = p->group_count;
+  g->rows[g->count] = p->row_count;
+  g->out[g->count] = out;
+  g->count++;
+}
+
+/* Planes that can share one launch: the same width and group size, K within
+ * the register form, 4-row multiples between segments. */
+static int group_fits(const eng_group *g, const igl_plane *const *p, int mode) {
+  for (int i = 0; i < g->count; ++i) {
+    if (p[i]->col_count != p[0]->col_count || p[i]->group_size != p[0]->group_size ||
+        p[i]->code_bias != p[0]->code_bias || p[i]->col_count > 8192)
+      return 0;
+    if (mode == IGL_GEMV_SEGMENTS && i + 1 < g->count && p[i]->row_count % 4) return 0;
   }
-  OKAY(igl_attend_lanes_dev(e->desk, S->k_store, S->v_store, IGL_CACHE_E4M3, S->k_scale, S->v_scale,
-                            S->cache_span, 1, e->heads, hs, e->q, e->q_stride, place,
-                            L->full ? 0 : e->window, lanes, 1.0f, e->blend));
-  OKAY(project(e, &L->o, e->blend, e->q_stride, lanes, e->lift, H));
-  (void)qw;
-  OKAY(norm_rows(e, e->lift, L->after_attn, H, lanes, H, e->lift));
-  RUN(igl_launch_add_rows(e->state, H, e->lift, H, H, lanes, 1.0f, 0, st));
-  OKAY(norm_rows(e, e->state, L->before_ff, H, lanes, H, e->scrap));
-  OKAY(project(e, &L->gate, e->scrap, H, lanes, e->gate, e->inner_max));
-  OKAY(project(e, &L->up, e->scrap, H, lanes, e->rise, e->inner_max));
-  RUN(igl_launch_gelu_gate_rows(e->gate, e->inner_max, e->rise, e->inner_max, L->inner, lanes, st));
-  OKAY(project(e, &L->down, e->gate, e->inner_max, lanes, e->lift, H));
-  OKAY(norm_rows(e, e->lift, L->after_ff, H, lanes, H, e->lift));
-  RUN(igl_launch_add_rows(e->state, H, e->lift, H, H, lanes, 1.0f, 0, st));
-  /* per-layer input */
-  OKAY(project(e, &L->ple_gate, e->state, H, lanes, e->gate, e->inner_max));
-  RUN(igl_launch_gelu_mul(e->gate, e->inner_max, e->ple_room + (size_t)li * e->ple, e->ple_stride,
-                          e->ple, lanes, st));
-  OKAY(project(e, &L->ple_proj, e->gate, e->inner_max, lanes, e->lift, H));
-  OKAY(norm_rows(e, e->lift, L->after_ple, H, lanes, H, e->lift));
-  RUN(igl_launch_add_rows(e->state, H, e->lift, H, H, lanes, L->layer_gain,
-                          L->layer_gain != 1.0f, st));
+  return mode != IGL_GEMV_GELU_PAIR || p[0]->row_count == p[1]->row_count;
+}
+
+static int group_run(igl_engine *e, const eng_group *g, const igl_plane *first, int mode,
+                     const float *act, const float *mul) {
+  RUN(igl_launch_gemv_group(mode, g->count, g->codes, g->row_stride, g->gains, g->gain_stride,
+                            g->rows, g->out, first->group_size, first->code_bias, act,
+                            first->col_count, mul, e->stream));
   return IGL_OKAY;
 }
 
-/* session_pass (11843-11975) for `lanes` ids; with `logits`, the head runs on
- * the last lane (1) or every lane (2). */
-static int run_pass(igl_engine *e, const int32_t *ids, int lanes, int logits) {
+/* One layer for `lanes` lanes at positions place .. place + lanes - 1 (the
+ * position is read from ctl_dev[0] when the kernels run; `bound` is its
+ * largest value, which sizes the attention grid) - session_layer
+ * 11637-11743 with session_attend 11455-11580.  On entry scrap holds
+ * norm(state) * enter_norm; on return, for a layer that is not the last, the
+ * next layer's. */
+static int run_layer(igl_engine *e, int li, int bound, int lanes) {
+  eng_layer *L = &e->layer[li];
+  const eng_layer *S = &e->layer[L->source];
+  const int H = e->hidden, hs = L->head_size;
+  const int kind = L->full ? 1 : 0;
+  const float *next_norm = li + 1 < e->layers ? e->layer[li + 1].enter_norm : NULL;
   hipStream_t st = e->stream;
-  const int H = e->hidden, place = e->fill;
-  if (lanes < 1 || lanes > e->lane_limit || place + lanes > e->window_limit) return IGL_FAIL_STATE;
-  for (int l = 0; l < lanes; ++l)
-    if (ids[l] < 0 || ids[l] >= e->embed.row_count) return IGL_FAIL_ARGUMENT;
-  RUN(hipMemcpyAsync(e->ids_dev, ids, (size_t)lanes * sizeof(int32_t), hipMemcpyHostToDevice, st));
+
+  /* query, key, value projections; then their norms and turns and the cache rows */
+  {
+    eng_group g = {0};
+    const igl_plane *p[3] = {&L->q, &L->k, &L->v};
+    group_add(e, &g, &L->q, e->q);
+    if (!L->shared) {
+      group_add(e, &g, &L->k, e->k);
+      group_add(e, &g, &L->v, e->v);
+    }
+    if (lanes == 1 && group_fits(&g, p, IGL_GEMV_SEGMENTS)) {
+      OKAY(group_run(e, &g, &L->q, IGL_GEMV_SEGMENTS, e->scrap, NULL));
+    } else {
+      OKAY(project(e, &L->q, e->scrap, H, lanes, e->q, e->q_stride));
+      if (!L->shared) {
+        OKAY(project(e, &L->k, e->scrap, H, lanes, e->k, e->kv_stride));
+        OKAY(project(e, &L->v, e->scrap, H, lanes, e->v, e->kv_stride));
+      }
+    }
+  }
+  RUN(igl_launch_qkv_prep(e->q, e->q_stride, L->shared ? NULL : e->k, e->v, e->kv_stride, e->heads,
+                          hs, lanes, L->q_norm, L->k_norm, e->eps, e->steps_dev[kind], e->ctl_dev,
+                          L->k_store, L->v_store, L->k_scale, L->v_scale, L->cache_span, st));
+  RUN(igl_launch_attend(S->k_store, S->v_store, IGL_CACHE_E4M3, S->k_scale, S->v_scale,
+                        S->cache_span, hs, 1, e->heads, hs, e->q, e->q_stride, bound, e->ctl_dev,
+                        L->full ? 0 : e->window, lanes, 1.0f, e->blend, e->attend_work, st));
+  OKAY(project(e, &L->o, e->blend, e->q_stride, lanes, e->lift, H));
+  /* state += norm(o) * after_attn; scrap = norm(state) * before_ff */
+  RUN(igl_launch_norm_add(e->state, H, e->lift, H, L->after_attn, H, lanes, e->eps, 1.0f, 0,
+                          L->before_ff, e->scrap, H, st));
+  /* gate = gelu(gate proj) * up proj; down */
+  {
+    eng_group g = {0};
+    const igl_plane *p[2] = {&L->gate, &L->up};
+    group_add(e, &g, &L->gate, e->gate);
+    group_add(e, &g, &L->up, e->rise);
+    if (lanes == 1 && group_fits(&g, p, IGL_GEMV_GELU_PAIR)) {
+      OKAY(group_run(e, &g, &L->gate, IGL_GEMV_GELU_PAIR, e->scrap, NULL));
+    } else {
+      OKAY(project(e, &L->gate, e->scrap, H, lanes, e->gate, e->inner_max));
+      OKAY(project(e, &L->up, e->scrap, H, lanes, e->rise, e->inner_max));
+      RUN(igl_launch_gelu_gate_rows(e->gate, e->inner_max, e->rise, e->inner_max, L->inner, lanes,
+                                    st));
+    }
+  }
+  OKAY(project(e, &L->down, e->gate, e->inner_max, lanes, e->lift, H));
+  RUN(igl_launch_norm_add(e->state, H, e->lift, H, L->after_ff, H, lanes, e->eps, 1.0f, 0, NULL,
+                          NULL, 0, st));
+  /* per-layer input: gelu(gate proj of state) * this layer's slice, projected back */
+  {
+    eng_group g = {0};
+    const igl_plane *p[1] = {&L->ple_gate};
+    const float *slice = e->ple_room + (size_t)li * e->ple;
+    group_add(e, &g, &L->ple_gate, e->gate);
+    if (lanes == 1 && group_fits(&g, p, IGL_GEMV_GELU_MUL)) {
+      OKAY(group_run(e, &g, &L->ple_gate, IGL_GEMV_GELU_MUL, e->state, slice));
+    } else {
+      OKAY(project(e, &L->ple_gate, e->state, H, lanes, e->gate, e->inner_max));
+      RUN(igl_launch_gelu_mul(e->gate, e->inner_max, slice, e->ple_stride, e->ple, lanes, st));
+    }
+  }
+  OKAY(project(e, &L->ple_proj, e->gate, e->inner_max, lanes, e->lift, H));
+  /* state = (state + norm(ple) * after_ple) * layer_scalar; scrap = next layer's input */
+  RUN(igl_launch_norm_add(e->state, H, e->lift, H, L->after_ple, H, lanes, e->eps, L->layer_gain,
+                          L->layer_gain != 1.0f, next_norm, e->scrap, H, st));
+  return IGL_OKAY;
+}
+
+/* session_pass (11843-11975) for `lanes` ids already in ids_dev, lane 0 at
+ * the position in ctl_dev[0] (at most `bound`); with `logits`, the head runs
+ * on the last lane (1) or every lane (2). */
+static int run_pass(igl_engine *e, int bound, int lanes, int logits) {
+  hipStream_t st = e->stream;
+  const int H = e->hidden;
   /* embedding row times sqrt(hidden) */
   {
     const igl_plane *p = &e->embed;
@@ -673,8 +775,8 @@ static int run_pass(igl_engine *e, const int32_t *ids, int lanes, int logits) {
                            e->ple, e->layers, lanes, e->eps, (float)(1.0 / sqrt((double)H)),
                            (float)(1.0 / sqrt(2.0)), st));
   }
-  for (int li = 0; li < e->layers; ++li) OKAY(run_layer(e, li, place, lanes));
-  e->fill += lanes;
+  OKAY(norm_rows(e, e->state, e->layer[0].enter_norm, H, lanes, H, e->scrap));
+  for (int li = 0; li < e->layers; ++li) OKAY(run_layer(e, li, bound, lanes));
   if (logits) {
     const int from = logits == 2 ? 0 : lanes - 1;
     const int span = lanes - from;
@@ -687,27 +789,84 @@ static int run_pass(igl_engine *e, const int32_t *ids, int lanes, int logits) {
 
 int igl_engine_prime(igl_engine *e, const int32_t *ids, int count) {
   if (!e || !ids || count < 1) return IGL_FAIL_ARGUMENT;
+  if (e->fill + count > e->window_limit) return IGL_FAIL_STATE;
+  for (int l = 0; l < count; ++l)
+    if (ids[l] < 0 || ids[l] >= e->embed.row_count) return IGL_FAIL_ARGUMENT;
   /* every id but the last, in chunks of the lane limit (session_prime_media 14443-14467) */
   for (int at = 0; at + 1 < count;) {
     int lanes = count - 1 - at < e->lane_limit ? count - 1 - at : e->lane_limit;
-    OKAY(run_pass(e, ids + at, lanes, 0));
+    RUN(igl_launch_put_int(e->ctl_dev, e->fill, e->stream));
+    RUN(hipMemcpyAsync(e->ids_dev, ids + at, (size_t)lanes * sizeof(int32_t), hipMemcpyHostToDevice,
+                       e->stream));
+    OKAY(run_pass(e, e->fill, lanes, 0));
+    e->fill += lanes;
     at += lanes;
   }
   return igl_desk_error_take(e->desk);
 }
 
+/* One decode step as the graph replays it: the position and id in from the
+ * pinned io block, the pass at any position up to the last, the greedy pick,
+ * the pick and its margin out to the io block. */
+static int step_body(igl_engine *e) {
+  RUN(hipMemcpyAsync(e->ctl_dev, &e->io->place, 2 * sizeof(int32_t), hipMemcpyHostToDevice,
+                     e->stream));
+  OKAY(run_pass(e, e->window_limit - 1, 1, 1));
+  RUN(igl_launch_pick(e->logits, e->vocab, e->pick_work, e->pick_dev, (float *)(e->pick_dev + 1),
+                      e->stream));
+  RUN(hipMemcpyAsync(&e->io->pick, e->pick_dev, 2 * sizeof(int32_t), hipMemcpyDeviceToHost,
+                     e->stream));
+  return IGL_OKAY;
+}
+
+static int capture_step(igl_engine *e) {
+  hipGraph_t graph = NULL;
+  int code;
+  hipError_t end;
+  if (hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
+    return IGL_FAIL_DEVICE;
+  code = step_body(e);
+  end = hipStreamEndCapture(e->stream, &graph);
+  if (code == IGL_OKAY && end != hipSuccess) code = IGL_FAIL_DEVICE;
+  if (code == IGL_OKAY && hipGraphInstantiate(&e->graph, graph, NULL, NULL, 0) != hipSuccess)
+    code = IGL_FAIL_DEVICE;
+  if (graph) (void)hipGraphDestroy(graph);
+  if (code == IGL_OKAY) e->graph_ready = 1;
+  return code;
+}
+
 int igl_engine_step(igl_engine *e, int32_t id, int32_t *pick_out, float *margin_out) {
-  int32_t pick = -1;
-  float margin = 0.0f;
   if (!e) return IGL_FAIL_ARGUMENT;
-  OKAY(run_pass(e, &id, 1, 1));
-  RUN(igl_launch_pick(e->logits, e->vocab, e->pick_work, e->pick_dev, e->margin_dev, e->stream));
-  RUN(hipMemcpyAsync(&pick, e->pick_dev, sizeof(pick), hipMemcpyDeviceToHost, e->stream));
-  RUN(hipMemcpyAsync(&margin, e->margin_dev, sizeof(margin), hipMemcpyDeviceToHost, e->stream));
+  if (e->fill + 1 > e->window_limit) return IGL_FAIL_STATE;
+  if (id < 0 || id >= e->embed.row_count) return IGL_FAIL_ARGUMENT;
+  e->io->place = e->fill;
+  e->io->id = id;
+  e->io->pick = -1;
+  e->io->margin = 0.0f;
+  /* the first step runs as it is enqueued (every kernel's first launch
+   * happens outside a capture); later ones replay its capture */
+  if (e->graph_on && !e->graph_ready && !e->graph_tried) {
+    e->graph_tried = 1;
+    OKAY(step_body(e));
+    RUN(hipStreamSynchronize(e->stream));
+    OKAY(igl_desk_error_take(e->desk));
+    OKAY(capture_step(e));
+  } else if (e->graph_on && e->graph_ready) {
+    RUN(hipGraphLaunch(e->graph, e->stream));
+  } else {
+    OKAY(step_body(e));
+  }
   RUN(hipStreamSynchronize(e->stream));
-  if (pick_out) *pick_out = pick;
-  if (margin_out) *margin_out = margin;
+  e->fill += 1;
+  if (pick_out) *pick_out = e->io->pick;
+  if (margin_out) *margin_out = e->io->margin;
   return igl_desk_error_take(e->desk);
+}
+
+int igl_engine_set_graph(igl_engine *e, int on) {
+  if (!e) return IGL_FAIL_ARGUMENT;
+  e->graph_on = on ? 1 : 0;
+  return IGL_OKAY;
 }
 
 int igl_engine_logits(igl_engine *e, float *out, int lane) {

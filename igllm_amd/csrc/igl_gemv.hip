@@ -225,7 +225,7 @@ __global__ void gemv_chunk_sum_kernel(const float *part, int chunks, int M, int 
 // staging and no barrier before the arithmetic: the row loads, the gains and
 // the activations are all requested first and the launch pays one memory
 // round trip.  The arithmetic is gemv_q4_kernel's, term for term.
-template <int M, int R>
+template <int M, int R, int UPL>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q4_reg_kernel(GemvArgs a) {
   __shared__ float red[4][R][M];
   const int tid = threadIdx.x;
@@ -236,30 +236,35 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_reg_kernel(GemvArgs a) {
   const int ks = wave % a.ksplit;
   const int row0 = tile * R;
   const int units = a.K >> 5;
-  const int u = (units * ks) / a.ksplit + lane;
-  const bool has = row0 < a.N && u < (units * (ks + 1)) / a.ksplit;
+  const int u_end = (units * (ks + 1)) / a.ksplit;
+  // A lane's units: u_first + 64 j for j < UPL, those before u_end.
+  const int u_first = (units * ks) / a.ksplit + lane;
 
-  uint4_t w[R];
-  float s[R];
-  float4_t x[M][8];
-  if (has) {
+  uint4_t w[UPL][R];
+  float s[UPL][R];
+  float4_t x[UPL][M][8];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = min(row0 + r, a.N - 1);  // tail rows are computed, never stored
-      w[r] = __builtin_nontemporal_load(
-          reinterpret_cast<const uint4_t *>(a.codes + (size_t)row * (size_t)a.row_stride) + u);
-      s[r] = a.gains[(size_t)row * (size_t)a.gain_stride + ((unsigned)u >> a.group_shift)];
-    }
+  for (int j = 0; j < UPL; ++j) {
+    const int u = u_first + kWave * j;
+    if (row0 < a.N && u < u_end) {
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const float *src = a.act + (size_t)m * a.act_stride + u * 32;
-      if (a.act_vec) {
+      for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, a.N - 1);  // tail rows are computed, never stored
+        w[j][r] = __builtin_nontemporal_load(
+            reinterpret_cast<const uint4_t *>(a.codes + (size_t)row * (size_t)a.row_stride) + u);
+        s[j][r] = a.gains[(size_t)row * (size_t)a.gain_stride + ((unsigned)u >> a.group_shift)];
+      }
 #pragma unroll
-        for (int q = 0; q < 8; ++q) x[m][q] = *reinterpret_cast<const float4_t *>(src + 4 * q);
-      } else {
+      for (int m = 0; m < M; ++m) {
+        const float *src = a.act + (size_t)m * a.act_stride + u * 32;
+        if (a.act_vec) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
-          x[m][q] = float4_t{src[4 * q], src[4 * q + 1], src[4 * q + 2], src[4 * q + 3]};
+          for (int q = 0; q < 8; ++q) x[j][m][q] = *reinterpret_cast<const float4_t *>(src + 4 * q);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            x[j][m][q] = float4_t{src[4 * q], src[4 * q + 1], src[4 * q + 2], src[4 * q + 3]};
+        }
       }
     }
   }
@@ -269,7 +274,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_reg_kernel(GemvArgs a) {
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
-  if (has) {
+#pragma unroll
+  for (int uj = 0; uj < UPL; ++uj) {
+    if (!(row0 < a.N && u_first + kWave * uj < u_end)) continue;
     const uint32_t exp16 = 0x4C004C00u;
     float part[R][M];
 #pragma unroll
@@ -281,7 +288,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_reg_kernel(GemvArgs a) {
       half2_t p[R][4];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const uint32_t d = w[r][j];
+        const uint32_t d = w[uj][r][j];
         p[r][0] = nibble_pair16<0>(d, exp16);
         p[r][1] = nibble_pair16<1>(d, exp16);
         p[r][2] = nibble_pair16<2>(d, exp16);
@@ -293,25 +300,25 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_reg_kernel(GemvArgs a) {
         for (int r = 0; r < R; ++r)
 #pragma unroll
           for (int m = 0; m < M; ++m)
-            part[r][m] = __builtin_fmaf((float)p[r][i].x, x[m][2 * j][i], part[r][m]);
+            part[r][m] = __builtin_fmaf((float)p[r][i].x, x[uj][m][2 * j][i], part[r][m]);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
           for (int m = 0; m < M; ++m)
-            part[r][m] = __builtin_fmaf((float)p[r][i].y, x[m][2 * j + 1][i], part[r][m]);
+            part[r][m] = __builtin_fmaf((float)p[r][i].y, x[uj][m][2 * j + 1][i], part[r][m]);
     }
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       float total = 0.0f;
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        total += x[m][q].x; total += x[m][q].y; total += x[m][q].z; total += x[m][q].w;
+        total += x[uj][m][q].x; total += x[uj][m][q].y; total += x[uj][m][q].z; total += x[uj][m][q].w;
       }
       const float c = a.unit_bias * total;
 #pragma unroll
-      for (int r = 0; r < R; ++r) acc[r][m] = s[r] * (part[r][m] - c);
+      for (int r = 0; r < R; ++r) acc[r][m] = __builtin_fmaf(s[uj][r], part[r][m] - c, acc[r][m]);
     }
   }
 
@@ -343,6 +350,171 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_reg_kernel(GemvArgs a) {
     float total = 0.0f;
     for (int k = 0; k < a.ksplit; ++k) total += red[wave + k][r][m];
     if (row0 + r < a.N) a.out[(size_t)m * a.out_stride + row0 + r] = total;
+  }
+}
+
+// ---- one activation row against several planes in one launch (decode) -----
+//
+// The register form for one lane and four rows a wave, over up to three planes
+// that read the same activations (the query, key and value projections; the
+// gate and up projections), with the epilogue the decode step applies next:
+//   GEMV_SEGMENTS  the planes' rows one after another, each stored as it is;
+//   GEMV_GELU_PAIR planes 0 and 1 have the same rows: a wave takes rows n, n+1
+//                  of both and stores gelu(plane 0) * plane 1 (kern_gelu_gate,
+//                  app_core.c:5105-5190);
+//   GEMV_GELU_MUL  one plane, stored as gelu(y[n]) * mul[n] (the per-layer
+//                  input gate, session_layer 11718-11723).
+// Each row's sum is formed as gemv_q4_reg_kernel forms it; with the same
+// K-split the results are those of separate launches followed by the
+// elementwise kernel, bit for bit.
+enum { GEMV_SEGMENTS = 0, GEMV_GELU_PAIR = 1, GEMV_GELU_MUL = 2 };
+
+struct GemvGroupArgs {
+  const uint8_t *codes[3];
+  long long row_stride[3];
+  const float *gains[3];
+  int gain_stride[3];
+  int rows[3];            // rows of each plane
+  float *out[3];          // GEMV_SEGMENTS: one output row per plane; otherwise out[0]
+  int segments;
+  int tiles;              // four-row tiles over all planes
+  int group_shift;
+  const float *act;
+  int act_vec;
+  int K;
+  int ksplit;
+  float unit_bias;
+  const float *mul;       // GEMV_GELU_MUL
+};
+
+template <int MODE>
+__global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupArgs a) {
+  constexpr int R = 4;
+  __shared__ float red[4][R];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int tiles_per_block = 4 / a.ksplit;
+  const int tile = blockIdx.x * tiles_per_block + wave / a.ksplit;
+  const int ks = wave % a.ksplit;
+  const int units = a.K >> 5;
+  const int u = (units * ks) / a.ksplit + lane;
+  const bool has = tile < a.tiles && u < (units * (ks + 1)) / a.ksplit;
+
+  // Row r of the tile: which plane, which row of it.
+  int plane[R], prow[R];
+  if (MODE == GEMV_GELU_PAIR) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      plane[r] = r >> 1;
+      prow[r] = min(2 * tile + (r & 1), a.rows[0] - 1);
+    }
+  } else {
+    int seg = 0, first = 0;
+    const int row0 = tile * R;
+    if (a.segments > 1 && row0 >= a.rows[0]) { seg = 1; first = a.rows[0]; }
+    if (a.segments > 2 && row0 >= a.rows[0] + a.rows[1]) { seg = 2; first = a.rows[0] + a.rows[1]; }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      plane[r] = seg;
+      prow[r] = min(row0 - first + r, a.rows[seg] - 1);
+    }
+  }
+
+  uint4_t w[R];
+  float s[R];
+  float4_t x[8];
+  if (has) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int p = plane[r];
+      w[r] = __builtin_nontemporal_load(
+          reinterpret_cast<const uint4_t *>(a.codes[p] + (size_t)prow[r] * (size_t)a.row_stride[p]) + u);
+      s[r] = a.gains[p][(size_t)prow[r] * (size_t)a.gain_stride[p] + ((unsigned)u >> a.group_shift)];
+    }
+    const float *src = a.act + u * 32;
+    if (a.act_vec) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) x[q] = *reinterpret_cast<const float4_t *>(src + 4 * q);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) x[q] = float4_t{src[4 * q], src[4 * q + 1], src[4 * q + 2], src[4 * q + 3]};
+    }
+  }
+
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  if (has) {
+    const uint32_t exp16 = 0x4C004C00u;
+    float part[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) part[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      half2_t p[R][4];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t d = w[r][j];
+        p[r][0] = nibble_pair16<0>(d, exp16);
+        p[r][1] = nibble_pair16<1>(d, exp16);
+        p[r][2] = nibble_pair16<2>(d, exp16);
+        p[r][3] = nibble_pair16<3>(d, exp16);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < R; ++r) part[r] = __builtin_fmaf((float)p[r][i].x, x[2 * j][i], part[r]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < R; ++r) part[r] = __builtin_fmaf((float)p[r][i].y, x[2 * j + 1][i], part[r]);
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      total += x[q].x; total += x[q].y; total += x[q].z; total += x[q].w;
+    }
+    const float c = a.unit_bias * total;
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = s[r] * (part[r] - c);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum_to_last(acc[r]);
+
+  if (a.ksplit > 1) {
+    if (lane == 63) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) red[wave][r] = acc[r];
+    }
+    __syncthreads();
+    if (ks != 0 || lane != 63) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float total = 0.0f;
+      for (int k = 0; k < a.ksplit; ++k) total += red[wave + k][r];
+      acc[r] = total;
+    }
+  } else if (lane != 63) {
+    return;
+  }
+  if (tile >= a.tiles) return;
+  if (MODE == GEMV_GELU_PAIR) {
+    const int n0 = 2 * tile;
+    if (n0 < a.rows[0]) a.out[0][n0] = gelu_near(acc[0]) * acc[2];
+    if (n0 + 1 < a.rows[0]) a.out[0][n0 + 1] = gelu_near(acc[1]) * acc[3];
+  } else {
+    const int row0 = tile * R;
+    const int first = plane[0] == 0 ? 0 : plane[0] == 1 ? a.rows[0] : a.rows[0] + a.rows[1];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int n = row0 - first + r;
+      if (n >= a.rows[plane[0]]) break;
+      if (MODE == GEMV_GELU_MUL)
+        a.out[0][n] = gelu_near(acc[r]) * a.mul[n];
+      else
+        a.out[plane[0]][n] = acc[r];
+    }
   }
 }
 
@@ -729,12 +901,12 @@ static hipError_t gemv_mfma_dispatch(const GemvMfmaArgs &a, const GemvMfmaPlan &
   }
 }
 
-template <int M, int R>
+template <int M, int R, int UPL>
 static hipError_t gemv_reg_launch(const GemvArgs &a, hipStream_t stream) {
   const int tiles = (a.N + R - 1) / R;
   const int tiles_per_block = 4 / a.ksplit;
   dim3 grid((tiles + tiles_per_block - 1) / tiles_per_block);
-  hipLaunchKernelGGL((gemv_q4_reg_kernel<M, R>), grid, dim3(kGemvThreads), 0, stream, a);
+  hipLaunchKernelGGL((gemv_q4_reg_kernel<M, R, UPL>), grid, dim3(kGemvThreads), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -779,13 +951,74 @@ extern "C" int igl_gemv_chunk_cols(int lanes, int K, int lds_limit) {
   return per * 32;
 }
 
+// One activation row against `segments` planes of the same width and group
+// size (see gemv_q4_group_kernel for the modes).  Every plane but the last of
+// a GEMV_SEGMENTS launch has a multiple of four rows; a GEMV_GELU_PAIR launch
+// takes two planes of equal rows.  K / 32 must fit the waves of a row tile
+// (K <= 8192).
+extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_t *const *codes,
+                                            const long long *row_stride,
+                                            const float *const *gains, const int *gain_stride,
+                                            const int *rows, float *const *out, int group_size,
+                                            int code_bias, const float *act, int K,
+                                            const float *mul, hipStream_t stream) {
+  GemvGroupArgs a;
+  const int units = K / 32;
+  if (segments < 1 || segments > 3 || K % 32 || units > 4 * kWave || group_size < 32)
+    return hipErrorInvalidValue;
+  if ((mode == GEMV_GELU_PAIR && (segments != 2 || rows[0] != rows[1])) ||
+      (mode == GEMV_GELU_MUL && (segments != 1 || !mul)))
+    return hipErrorInvalidValue;
+  int total = 0;
+  for (int s = 0; s < 3; ++s) {
+    const int live = s < segments;
+    if (live && (rows[s] < 1 || (mode == GEMV_SEGMENTS && s + 1 < segments && rows[s] % 4)))
+      return hipErrorInvalidValue;
+    a.codes[s] = live ? codes[s] : nullptr;
+    a.row_stride[s] = live ? row_stride[s] : 0;
+    a.gains[s] = live ? gains[s] : nullptr;
+    a.gain_stride[s] = live ? gain_stride[s] : 0;
+    a.rows[s] = live ? rows[s] : 0;
+    a.out[s] = live ? out[s] : nullptr;
+    total += a.rows[s];
+  }
+  a.segments = segments;
+  a.tiles = mode == GEMV_GELU_PAIR ? (rows[0] + 1) / 2 : (total + 3) / 4;
+  a.group_shift = __builtin_ctz((unsigned)(group_size / 32));
+  a.act = act;
+  a.act_vec = (((uintptr_t)act) & 15u) == 0 ? 1 : 0;
+  a.K = K;
+  a.unit_bias = 16.0f + (float)code_bias;
+  a.mul = mul;
+  int ksplit = 1;
+  while (ksplit < 4 && (units > ksplit * kWave || (a.tiles * ksplit < 2048 && units / (ksplit * 2) >= 32)))
+    ksplit *= 2;
+  a.ksplit = ksplit;
+  const int tiles_per_block = 4 / ksplit;
+  dim3 grid((a.tiles + tiles_per_block - 1) / tiles_per_block);
+  switch (mode) {
+    case GEMV_SEGMENTS:
+      hipLaunchKernelGGL((gemv_q4_group_kernel<GEMV_SEGMENTS>), grid, dim3(kGemvThreads), 0, stream, a);
+      break;
+    case GEMV_GELU_PAIR:
+      hipLaunchKernelGGL((gemv_q4_group_kernel<GEMV_GELU_PAIR>), grid, dim3(kGemvThreads), 0, stream, a);
+      break;
+    case GEMV_GELU_MUL:
+      hipLaunchKernelGGL((gemv_q4_group_kernel<GEMV_GELU_MUL>), grid, dim3(kGemvThreads), 0, stream, a);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 // Floats of K-chunk partials a launch of `lanes` lanes over an N x K plane
 // writes (0 when it needs none).
 extern "C" size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit) {
   GemvMfmaPlan plan;
   if (lanes >= 3 && gemv_mfma_plan(lanes, N, K, &plan))
     return plan.chunks > 1 ? (size_t)plan.chunks * (size_t)lanes * (size_t)N : 0;
-  if (lanes <= 2 && K / 32 <= 4 * kWave) return 0;
+  if (lanes <= 2 && K / 32 <= 8 * kWave) return 0;
   const int cols = igl_gemv_chunk_cols(lanes, K, lds_limit);
   const size_t chunks = (size_t)((K + cols - 1) / cols);
   return chunks > 1 ? chunks * (size_t)lanes * (size_t)N : 0;
@@ -845,20 +1078,24 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
                        plan.chunks, lanes, N, out, out_stride);
     return hipGetLastError();
   }
-  // One and two lanes with at most 256 units a row: the register form, with
-  // enough waves on a row tile that each lane holds one unit.
-  if (lanes <= 2 && K / 32 <= 4 * kWave) {
+  // One and two lanes with at most 512 units a row: the register form, with
+  // enough waves on a row tile that each lane holds one unit (two past 256).
+  if (lanes <= 2 && K / 32 <= 8 * kWave) {
     const int units = K / 32;
     const int R = 4;
     const int tiles = (N + R - 1) / R;
+    const int upl = units > 4 * kWave ? 2 : 1;
     int ksplit = 1;
-    while (ksplit < 4 && (units > ksplit * kWave || (tiles * ksplit < 2048 && units / (ksplit * 2) >= 32)))
+    while (ksplit < 4 && (units > ksplit * kWave * upl ||
+                          (tiles * ksplit < 2048 && units / (ksplit * 2) >= 32 * upl)))
       ksplit *= 2;
     a.ksplit = ksplit;
     a.chunk_cols = K;
     a.out = out;
     a.out_stride = out_stride;
-    return lanes == 1 ? gemv_reg_launch<1, 4>(a, stream) : gemv_reg_launch<2, 4>(a, stream);
+    if (upl == 2)
+      return lanes == 1 ? gemv_reg_launch<1, 4, 2>(a, stream) : gemv_reg_launch<2, 4, 2>(a, stream);
+    return lanes == 1 ? gemv_reg_launch<1, 4, 1>(a, stream) : gemv_reg_launch<2, 4, 1>(a, stream);
   }
   a.chunk_cols = igl_gemv_chunk_cols(lanes, K, lds_limit);
   const int chunks = (K + a.chunk_cols - 1) / a.chunk_cols;

@@ -17,6 +17,15 @@ extern "C" {
 int igl_gemv_rows_per_tile(int lanes);
 int igl_gemv_chunk_cols(int lanes, int K, int lds_limit);
 size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit);
+/* modes of igl_launch_gemv_group */
+#define IGL_GEMV_SEGMENTS 0
+#define IGL_GEMV_GELU_PAIR 1
+#define IGL_GEMV_GELU_MUL 2
+hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_t *const *codes,
+                                 const long long *row_stride, const float *const *gains,
+                                 const int *gain_stride, const int *rows, float *const *out,
+                                 int group_size, int code_bias, const float *act, int K,
+                                 const float *mul, hipStream_t stream);
 hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_stride, const float *gains,
                               int gain_stride, int group_size, int code_bias, const float *act,
                               int act_stride, int lanes, float *out, int out_stride, int N, int K,
@@ -32,8 +41,9 @@ size_t igl_attend_work_floats(int place0, int window, int lanes, int head_count,
 hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t *value_store, int fmt,
                              float key_scale, float value_scale, int cache_span, int kv_width,
                              int kv_count, int group_share, int head_size, const float *query,
-                             int q_stride, int place0, int window, int lanes, float score_scale,
-                             float *blend_out, float *work, hipStream_t stream);
+                             int q_stride, int place0, const int *place_dev, int window,
+                             int lanes, float score_scale, float *blend_out, float *work,
+                             hipStream_t stream);
 
 /* The desk's HIP stream, for the engine's own launches (back_hip.c). */
 void *igl_desk_stream(igl_desk *desk);
@@ -49,6 +59,17 @@ hipError_t igl_launch_ple_mix(float *room, int room_stride, const float *seed, i
 hipError_t igl_launch_head_prep(float *v, int lane_stride, int heads, int head_size, int lanes,
                                 const float *gain, float eps, const float *step, int turn,
                                 int place_first, hipStream_t stream);
+hipError_t igl_launch_put_int(int32_t *dst, int value, hipStream_t stream);
+hipError_t igl_launch_qkv_prep(float *q, int q_stride, const float *k, const float *v,
+                               int kv_stride, int heads, int head_size, int lanes,
+                               const float *q_gain, const float *k_gain, float eps,
+                               const float *step, const int *place_dev, uint8_t *k_store,
+                               uint8_t *v_store, float k_scale, float v_scale, int span,
+                               hipStream_t stream);
+hipError_t igl_launch_norm_add(float *state, int state_stride, const float *lift, int lift_stride,
+                               const float *after_gain, int n, int lanes, float eps, float scale,
+                               int apply_scale, const float *next_gain, float *out,
+                               int out_stride, hipStream_t stream);
 hipError_t igl_launch_add_rows(float *into, int into_stride, const float *from, int from_stride,
                                int n, int lanes, float gain, int apply_gain, hipStream_t stream);
 hipError_t igl_launch_scale_rows(float *v, int stride, int n, int lanes, float gain,

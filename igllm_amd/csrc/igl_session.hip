@@ -30,18 +30,6 @@ __global__ void gather_rows_kernel(const uint8_t *codes, long long row_stride, c
   out[(size_t)lane * out_stride + k] = v * factor;
 }
 
-__device__ __forceinline__ double block_sum_double(double v, double *red) {
-  red[threadIdx.x] = v;
-  __syncthreads();
-  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-    __syncthreads();
-  }
-  const double total = red[0];
-  __syncthreads();
-  return total;
-}
-
 // The per-layer inputs of one lane (session_pass 11877-11902): the projected
 // chunk scaled by 1/sqrt(hidden), RMS-normed with the shared gain, plus the
 // token's per-layer embedding row scaled by sqrt(ple), times 1/sqrt(2).
@@ -60,8 +48,8 @@ __global__ __launch_bounds__(256) void ple_mix_kernel(float *room, int room_stri
     const float v = x[i] * lift_scale;
     acc += (double)v * (double)v;
   }
-  const double total = block_sum_double(acc, red);
-  const float shrink = (float)pow(total / (double)ple + (double)eps, -0.5);
+  const double total = block_sum_f64(acc, red);
+  const float shrink = rms_shrink(total, ple, eps);
   for (int i = threadIdx.x; i < ple; i += blockDim.x) {
     const float v = x[i] * lift_scale;
     const float normed = v * shrink * gain[i];
@@ -84,8 +72,8 @@ __global__ __launch_bounds__(256) void head_prep_kernel(float *v, int lane_strid
   float *x = v + (size_t)lane * lane_stride + (size_t)head * head_size;
   double acc = 0.0;
   for (int i = threadIdx.x; i < head_size; i += blockDim.x) acc += (double)x[i] * (double)x[i];
-  const double total = block_sum_double(acc, red);
-  const float shrink = (float)pow(total / (double)head_size + (double)eps, -0.5);
+  const double total = block_sum_f64(acc, red);
+  const float shrink = rms_shrink(total, head_size, eps);
   const int half = head_size / 2;
   const double place = (double)(place_first + lane);
   for (int j = threadIdx.x; j < half; j += blockDim.x) {
@@ -105,6 +93,122 @@ __global__ __launch_bounds__(256) void head_prep_kernel(float *v, int lane_strid
       x[j] = lo;
       x[j + half] = hi;
     }
+  }
+}
+
+// One head of head_prep_kernel's arithmetic, returned through `put(j, value)`
+// for every dim j instead of written back.
+template <typename Put>
+__device__ __forceinline__ void head_turn(const float *x, int head_size, const float *gain,
+                                          float eps, const float *step, int turn, double place,
+                                          double *red, Put put) {
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < head_size; i += blockDim.x) acc += (double)x[i] * (double)x[i];
+  const double total = block_sum_f64(acc, red);
+  const float shrink = rms_shrink(total, head_size, eps);
+  const int half = head_size / 2;
+  for (int j = threadIdx.x; j < half; j += blockDim.x) {
+    float lo = x[j] * shrink;
+    float hi = x[j + half] * shrink;
+    if (gain) {
+      lo = lo * gain[j];
+      hi = hi * gain[j + half];
+    }
+    if (turn) {
+      const double angle = place * (double)step[j];
+      const float c = (float)cos(angle);
+      const float s = (float)sin(angle);
+      put(j, lo * c - hi * s);
+      put(j + half, hi * c + lo * s);
+    } else {
+      put(j, lo);
+      put(j + half, hi);
+    }
+  }
+}
+
+// The query, key and value heads of a batch of lanes in one launch
+// (session_attend 11487-11514, then cache_lay 11205-11236 for the key and
+// value rows).  Workgroup (b, lane): b < heads is query head b (norm, gain,
+// turn, written back in place); b == heads the key head (norm, gain, turn,
+// then its e4m3 bytes into ring slot (place + lane) % span); b == heads + 1
+// the value head (norm without gain, no turn, into the value ring).  Lane 0's
+// position is read from `place_dev`, so a captured launch serves every step.
+// The arithmetic is head_prep_kernel's and cache_lay_rows_kernel's.
+__global__ __launch_bounds__(256) void qkv_prep_kernel(
+    float *q, int q_stride, const float *k, const float *v, int kv_stride, int heads,
+    int head_size, const float *q_gain, const float *k_gain, float eps, const float *step,
+    const int *place_dev, uint8_t *k_store, uint8_t *v_store, float k_scale, float v_scale,
+    int span) {
+  __shared__ double red[256];
+  const int b = blockIdx.x;
+  const int lane = blockIdx.y;
+  const int place = *place_dev + lane;
+  if (b < heads) {
+    float *x = q + (size_t)lane * q_stride + (size_t)b * head_size;
+    // Every read of x finishes (block_sum_f64's barriers) before a write.
+    head_turn(x, head_size, q_gain, eps, step, 1, (double)place, red,
+              [&](int j, float value) { x[j] = value; });
+    return;
+  }
+  const bool key = b == heads;
+  const float *x = (key ? k : v) + (size_t)lane * kv_stride;
+  uint8_t *row = (key ? k_store : v_store) + (size_t)(place % span) * head_size;
+  const float scale = key ? k_scale : v_scale;
+  head_turn(x, head_size, key ? k_gain : nullptr, eps, step, key ? 1 : 0, (double)place, red,
+            [&](int j, float value) { row[j] = e4m3_code(value / scale); });
+}
+
+// A residual update with the norms on either side of it (session_layer
+// 11660-11737), one workgroup a lane: state <- state + norm(lift) *
+// after_gain, times `scale` when `apply_scale` (the layer scalar); then, with
+// `next_gain`, out <- norm(state) * next_gain, the next sub-block's input.
+// The same float operations as norm_rms_kernel, add_rows_kernel and
+// norm_rms_kernel in turn.
+__global__ __launch_bounds__(256) void norm_add_kernel(float *state, int state_stride,
+                                                       const float *lift, int lift_stride,
+                                                       const float *after_gain,
+                                                       int n, float eps, float scale,
+                                                       int apply_scale, const float *next_gain,
+                                                       float *out, int out_stride) {
+  constexpr int kHeld = 16;  // values a thread holds: rows up to 4096
+  __shared__ double red[16];
+  const int lane = blockIdx.x;
+  float *s = state + (size_t)lane * state_stride;
+  const float *x = lift + (size_t)lane * lift_stride;
+  // Every load is issued before the first use (one round trip, not one per value).
+  float xv[kHeld], sv[kHeld], gv[kHeld];
+#pragma unroll
+  for (int k = 0; k < kHeld; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    xv[k] = i < n ? x[i] : 0.0f;
+    sv[k] = i < n ? s[i] : 0.0f;
+    gv[k] = i < n ? after_gain[i] : 0.0f;
+  }
+  double acc = 0.0;
+#pragma unroll
+  for (int k = 0; k < kHeld; ++k) acc += (double)xv[k] * (double)xv[k];
+  const float shrink = rms_shrink(block_sum_f64(acc, red), n, eps);
+  double acc2 = 0.0;
+#pragma unroll
+  for (int k = 0; k < kHeld; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    const float normed = xv[k] * shrink * gv[k];
+    float sum = sv[k] + normed;
+    if (apply_scale) sum *= scale;
+    sv[k] = sum;
+    if (i < n) {
+      s[i] = sum;
+      acc2 += (double)sum * (double)sum;
+    }
+  }
+  if (!next_gain) return;
+  const float shrink2 = rms_shrink(block_sum_f64(acc2, red), n, eps);
+  float *y = out + (size_t)lane * out_stride;
+#pragma unroll
+  for (int k = 0; k < kHeld; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    if (i < n) y[i] = sv[k] * shrink2 * next_gain[i];
   }
 }
 
@@ -256,6 +360,39 @@ extern "C" hipError_t igl_launch_head_prep(float *v, int lane_stride, int heads,
                                            hipStream_t stream) {
   hipLaunchKernelGGL(head_prep_kernel, dim3(heads, lanes), dim3(256), 0, stream, v, lane_stride,
                      head_size, gain, eps, step, turn, place_first);
+  return hipGetLastError();
+}
+
+__global__ void put_int_kernel(int32_t *dst, int value) { *dst = value; }
+
+// One int written on the stream (a batch's position, ahead of its kernels).
+extern "C" hipError_t igl_launch_put_int(int32_t *dst, int value, hipStream_t stream) {
+  hipLaunchKernelGGL(put_int_kernel, dim3(1), dim3(1), 0, stream, dst, value);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_qkv_prep(float *q, int q_stride, const float *k, const float *v,
+                                          int kv_stride, int heads, int head_size, int lanes,
+                                          const float *q_gain, const float *k_gain, float eps,
+                                          const float *step, const int *place_dev,
+                                          uint8_t *k_store, uint8_t *v_store, float k_scale,
+                                          float v_scale, int span, hipStream_t stream) {
+  const int blocks = heads + (k ? 2 : 0);
+  hipLaunchKernelGGL(qkv_prep_kernel, dim3(blocks, lanes), dim3(256), 0, stream, q, q_stride, k, v,
+                     kv_stride, heads, head_size, q_gain, k_gain, eps, step, place_dev, k_store,
+                     v_store, k_scale, v_scale, span);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_norm_add(float *state, int state_stride, const float *lift,
+                                          int lift_stride, const float *after_gain, int n,
+                                          int lanes, float eps, float scale, int apply_scale,
+                                          const float *next_gain, float *out, int out_stride,
+                                          hipStream_t stream) {
+  if (n > 4096) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(norm_add_kernel, dim3(lanes), dim3(256), 0, stream, state, state_stride, lift,
+                     lift_stride, after_gain, n, eps, scale, apply_scale, next_gain, out,
+                     out_stride);
   return hipGetLastError();
 }
 

@@ -92,6 +92,9 @@ class Engine:
     def reset(self):
         self._check(self.lib.igl_engine_reset(self.handle), "reset")
 
+    def set_graph(self, on: bool):
+        self._check(self.lib.igl_engine_set_graph(self.handle, int(on)), "set_graph")
+
     def close(self):
         if self.handle:
             self.lib.igl_engine_close(self.handle)

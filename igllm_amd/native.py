@@ -128,6 +128,7 @@ SIGNATURES = {
     "igl_engine_fill": (_I, [_P]),
     "igl_engine_vocab": (_I, [_P]),
     "igl_engine_reset": (_I, [_P]),
+    "igl_engine_set_graph": (_I, [_P, _I]),
     "igl_cache_lay_dev": (_I, [ctypes.POINTER(Desk), _P, _I, _F, _I, _P, _Z]),
     "igl_norm_rms_dev": (_I, [ctypes.POINTER(Desk), _P, _P, _I, _I, _I, _F, _P]),
     "igl_soft_max_dev": (_I, [ctypes.POINTER(Desk), _P, _I, _I, _I]),

@@ -257,6 +257,10 @@ int  igl_engine_logits(igl_engine *engine, float *out, int lane);
 int  igl_engine_fill(const igl_engine *engine);
 int  igl_engine_vocab(const igl_engine *engine);
 int  igl_engine_reset(igl_engine *engine);
+/* Whether decode steps replay one captured HIP graph (on by default): the
+ * first step runs as enqueued and is captured; later steps launch the capture,
+ * whose kernels read the position and id from device memory. */
+int  igl_engine_set_graph(igl_engine *engine, int on);
 
 #ifdef __cplusplus
 }
