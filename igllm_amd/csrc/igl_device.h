@@ -128,7 +128,11 @@ __device__ __forceinline__ uint32_t and_or_b32(uint32_t a, uint32_t mask, uint32
 template <int I>
 __device__ __forceinline__ half2_t nibble_pair16(uint32_t d, uint32_t exp16) {
   constexpr int kShift = 6 - 4 * I;
-  uint32_t moved = kShift >= 0 ? (d << kShift) : (d >> (-kShift));
+  uint32_t moved;
+  if constexpr (kShift >= 0)
+    moved = d << kShift;
+  else
+    moved = d >> (-kShift);
   return as_half2(and_or_b32(moved, 0x03C003C0u, exp16));
 }
 

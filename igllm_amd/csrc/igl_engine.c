@@ -87,6 +87,10 @@ struct igl_engine {
   int32_t *ctl_dev;   /* [0] position of lane 0, [1 ..] the lanes' token ids */
   int32_t *ids_dev;   /* ctl_dev + 1 */
   float *state, *scrap, *lift, *q, *k, *v, *blend, *gate, *rise, *ple_seed, *ple_room, *logits;
+  float *state_buf[2];  /* the residual row and its other half of a pair (fused updates) */
+  int cur, pending;
+  const float *pending_gain;
+  float pending_scale;
   float *attend_work;
   size_t attend_floats;
   int q_stride, kv_stride, inner_max, ple_stride;
@@ -530,7 +534,8 @@ int igl_engine_open(igl_engine **out, igl_desk *desk, const char *folder, int wi
     e->attend_floats = one > many ? one : many;
     if ((code = dev_alloc((void **)&e->ctl_dev, (lanes + 1) * sizeof(int32_t))) ||
         (code = dev_alloc((void **)&e->attend_work, e->attend_floats * sizeof(float))) ||
-        (code = dev_alloc((void **)&e->state, lanes * e->hidden * 4)) ||
+        (code = dev_alloc((void **)&e->state_buf[0], lanes * e->hidden * 4)) ||
+        (code = dev_alloc((void **)&e->state_buf[1], lanes * e->hidden * 4)) ||
         (code = dev_alloc((void **)&e->scrap, lanes * e->hidden * 4)) ||
         (code = dev_alloc((void **)&e->lift, lanes * e->hidden * 4)) ||
         (code = dev_alloc((void **)&e->q, lanes * e->q_stride * 4)) ||
@@ -546,6 +551,7 @@ int igl_engine_open(igl_engine **out, igl_desk *desk, const char *folder, int wi
         (code = dev_alloc((void **)&e->pick_dev, 2 * sizeof(int32_t))))
       goto fail;
     e->ids_dev = e->ctl_dev + 1;
+    e->state = e->state_buf[0];
     if (hipHostMalloc((void **)&e->io, sizeof(igl_step_io), hipHostMallocDefault) != hipSuccess) {
       e->io = NULL;
       code = IGL_FAIL_MEMORY;
@@ -581,7 +587,7 @@ void igl_engine_close(igl_engine *e) {
   igl_plane_detach(e->desk, &e->head);
   if (e->graph_ready) (void)hipGraphExecDestroy(e->graph);
   {
-    void *bufs[] = {e->payload_dev, e->ctl_dev, e->attend_work, e->state, e->scrap, e->lift, e->q,
+    void *bufs[] = {e->payload_dev, e->ctl_dev, e->attend_work, e->state_buf[0], e->state_buf[1], e->scrap, e->lift, e->q,
                     e->blend, e->k, e->v, e->gate, e->rise, e->ple_seed, e->ple_room, e->logits,
                     e->pick_work, e->pick_dev, e->steps_dev[0], e->steps_dev[1]};
     for (size_t j = 0; j < sizeof(bufs) / sizeof(bufs[0]); ++j)
@@ -661,38 +667,93 @@ static int group_fits(const eng_group *g, const igl_plane *const *p, int mode) {
 }
 
 static int group_run(igl_engine *e, const eng_group *g, const igl_plane *first, int mode,
-                     const float *act, const float *mul) {
+                     const float *act, const float *mul, const igl_gemv_prologue *pro) {
   RUN(igl_launch_gemv_group(mode, g->count, g->codes, g->row_stride, g->gains, g->gain_stride,
                             g->rows, g->out, first->group_size, first->code_bias, act,
-                            first->col_count, mul, e->stream));
+                            first->col_count, mul, pro, e->stream));
+  return IGL_OKAY;
+}
+
+/* A residual update formed in the next grouped launch's prologue: state
+ * moves to the other buffer of the pair. */
+static igl_gemv_prologue state_update(igl_engine *e, const float *lift, const float *lift_gain,
+                                      float scale, const float *norm_gain) {
+  igl_gemv_prologue pro;
+  pro.state_in = e->state;
+  pro.state_out = e->state_buf[e->cur ^ 1];
+  pro.lift = lift;
+  pro.lift_gain = lift_gain;
+  pro.scale = scale;
+  pro.apply_scale = scale != 1.0f;
+  pro.norm_gain = norm_gain;
+  pro.eps = e->eps;
+  return pro;
+}
+
+static void state_flip(igl_engine *e) {
+  e->cur ^= 1;
+  e->state = e->state_buf[e->cur];
+}
+
+/* The previous layer's last update, if a fused step left it for this layer's
+ * first launch and that launch cannot take it: applied in place, with the
+ * next input norm into scrap (`next_norm` NULL: none). */
+static int settle(igl_engine *e, int lanes, const float *next_norm) {
+  if (!e->pending) return IGL_OKAY;
+  e->pending = 0;
+  RUN(igl_launch_norm_add(e->state, e->hidden, e->lift, e->hidden, e->pending_gain, e->hidden,
+                          lanes, e->eps, e->pending_scale, e->pending_scale != 1.0f, next_norm,
+                          e->scrap, e->hidden, e->stream));
   return IGL_OKAY;
 }
 
 /* One layer for `lanes` lanes at positions place .. place + lanes - 1 (the
  * position is read from ctl_dev[0] when the kernels run; `bound` is its
  * largest value, which sizes the attention grid) - session_layer
- * 11637-11743 with session_attend 11455-11580.  On entry scrap holds
- * norm(state) * enter_norm; on return, for a layer that is not the last, the
- * next layer's. */
+ * 11637-11743 with session_attend 11455-11580.
+ *
+ * A batch runs every residual update as its own launch, with scrap holding
+ * the next sub-block's normed input.  One lane (a decode step) folds each
+ * update into the prologue of the grouped launch that consumes it - the
+ * post-attention update into the gate/up launch, the post-feed-forward one
+ * into the per-layer-input gate, and this layer's last (per-layer-input)
+ * update into the next layer's query/key/value launch - so a layer is eight
+ * launches. */
 static int run_layer(igl_engine *e, int li, int bound, int lanes) {
   eng_layer *L = &e->layer[li];
   const eng_layer *S = &e->layer[L->source];
   const int H = e->hidden, hs = L->head_size;
   const int kind = L->full ? 1 : 0;
-  const float *next_norm = li + 1 < e->layers ? e->layer[li + 1].enter_norm : NULL;
   hipStream_t st = e->stream;
+  eng_group gq = {0}, gf = {0}, gp = {0};
+  const igl_plane *pq[3] = {&L->q, &L->k, &L->v};
+  const igl_plane *pf[2] = {&L->gate, &L->up};
+  const igl_plane *pp[1] = {&L->ple_gate};
+  const float *slice = e->ple_room + (size_t)li * e->ple;
+  int fused;
+
+  group_add(e, &gq, &L->q, e->q);
+  if (!L->shared) {
+    group_add(e, &gq, &L->k, e->k);
+    group_add(e, &gq, &L->v, e->v);
+  }
+  group_add(e, &gf, &L->gate, e->gate);
+  group_add(e, &gf, &L->up, e->rise);
+  group_add(e, &gp, &L->ple_gate, e->gate);
+  fused = lanes == 1 && H <= 4096 && group_fits(&gq, pq, IGL_GEMV_SEGMENTS) &&
+          group_fits(&gf, pf, IGL_GEMV_GELU_PAIR) && group_fits(&gp, pp, IGL_GEMV_GELU_MUL) &&
+          L->q.col_count == H && L->gate.col_count == H && L->ple_gate.col_count == H;
 
   /* query, key, value projections; then their norms and turns and the cache rows */
-  {
-    eng_group g = {0};
-    const igl_plane *p[3] = {&L->q, &L->k, &L->v};
-    group_add(e, &g, &L->q, e->q);
-    if (!L->shared) {
-      group_add(e, &g, &L->k, e->k);
-      group_add(e, &g, &L->v, e->v);
-    }
-    if (lanes == 1 && group_fits(&g, p, IGL_GEMV_SEGMENTS)) {
-      OKAY(group_run(e, &g, &L->q, IGL_GEMV_SEGMENTS, e->scrap, NULL));
+  if (fused && e->pending) {
+    igl_gemv_prologue pro = state_update(e, e->lift, e->pending_gain, e->pending_scale, L->enter_norm);
+    e->pending = 0;
+    OKAY(group_run(e, &gq, &L->q, IGL_GEMV_SEGMENTS, NULL, NULL, &pro));
+    state_flip(e);
+  } else {
+    OKAY(settle(e, lanes, L->enter_norm));
+    if (fused) {
+      OKAY(group_run(e, &gq, &L->q, IGL_GEMV_SEGMENTS, e->scrap, NULL, NULL));
     } else {
       OKAY(project(e, &L->q, e->scrap, H, lanes, e->q, e->q_stride));
       if (!L->shared) {
@@ -708,44 +769,36 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
                         S->cache_span, hs, 1, e->heads, hs, e->q, e->q_stride, bound, e->ctl_dev,
                         L->full ? 0 : e->window, lanes, 1.0f, e->blend, e->attend_work, st));
   OKAY(project(e, &L->o, e->blend, e->q_stride, lanes, e->lift, H));
-  /* state += norm(o) * after_attn; scrap = norm(state) * before_ff */
-  RUN(igl_launch_norm_add(e->state, H, e->lift, H, L->after_attn, H, lanes, e->eps, 1.0f, 0,
-                          L->before_ff, e->scrap, H, st));
-  /* gate = gelu(gate proj) * up proj; down */
-  {
-    eng_group g = {0};
-    const igl_plane *p[2] = {&L->gate, &L->up};
-    group_add(e, &g, &L->gate, e->gate);
-    group_add(e, &g, &L->up, e->rise);
-    if (lanes == 1 && group_fits(&g, p, IGL_GEMV_GELU_PAIR)) {
-      OKAY(group_run(e, &g, &L->gate, IGL_GEMV_GELU_PAIR, e->scrap, NULL));
-    } else {
-      OKAY(project(e, &L->gate, e->scrap, H, lanes, e->gate, e->inner_max));
-      OKAY(project(e, &L->up, e->scrap, H, lanes, e->rise, e->inner_max));
-      RUN(igl_launch_gelu_gate_rows(e->gate, e->inner_max, e->rise, e->inner_max, L->inner, lanes,
-                                    st));
-    }
+  /* state += norm(o) * after_attn; gate = gelu(gate proj) * up proj of norm(state) * before_ff */
+  if (fused) {
+    igl_gemv_prologue pro = state_update(e, e->lift, L->after_attn, 1.0f, L->before_ff);
+    OKAY(group_run(e, &gf, &L->gate, IGL_GEMV_GELU_PAIR, NULL, NULL, &pro));
+    state_flip(e);
+  } else {
+    RUN(igl_launch_norm_add(e->state, H, e->lift, H, L->after_attn, H, lanes, e->eps, 1.0f, 0,
+                            L->before_ff, e->scrap, H, st));
+    OKAY(project(e, &L->gate, e->scrap, H, lanes, e->gate, e->inner_max));
+    OKAY(project(e, &L->up, e->scrap, H, lanes, e->rise, e->inner_max));
+    RUN(igl_launch_gelu_gate_rows(e->gate, e->inner_max, e->rise, e->inner_max, L->inner, lanes, st));
   }
   OKAY(project(e, &L->down, e->gate, e->inner_max, lanes, e->lift, H));
-  RUN(igl_launch_norm_add(e->state, H, e->lift, H, L->after_ff, H, lanes, e->eps, 1.0f, 0, NULL,
-                          NULL, 0, st));
-  /* per-layer input: gelu(gate proj of state) * this layer's slice, projected back */
-  {
-    eng_group g = {0};
-    const igl_plane *p[1] = {&L->ple_gate};
-    const float *slice = e->ple_room + (size_t)li * e->ple;
-    group_add(e, &g, &L->ple_gate, e->gate);
-    if (lanes == 1 && group_fits(&g, p, IGL_GEMV_GELU_MUL)) {
-      OKAY(group_run(e, &g, &L->ple_gate, IGL_GEMV_GELU_MUL, e->state, slice));
-    } else {
-      OKAY(project(e, &L->ple_gate, e->state, H, lanes, e->gate, e->inner_max));
-      RUN(igl_launch_gelu_mul(e->gate, e->inner_max, slice, e->ple_stride, e->ple, lanes, st));
-    }
+  /* state += norm(down) * after_ff; gate = gelu(per-layer gate proj of state) * slice */
+  if (fused) {
+    igl_gemv_prologue pro = state_update(e, e->lift, L->after_ff, 1.0f, NULL);
+    OKAY(group_run(e, &gp, &L->ple_gate, IGL_GEMV_GELU_MUL, NULL, slice, &pro));
+    state_flip(e);
+  } else {
+    RUN(igl_launch_norm_add(e->state, H, e->lift, H, L->after_ff, H, lanes, e->eps, 1.0f, 0, NULL,
+                            NULL, 0, st));
+    OKAY(project(e, &L->ple_gate, e->state, H, lanes, e->gate, e->inner_max));
+    RUN(igl_launch_gelu_mul(e->gate, e->inner_max, slice, e->ple_stride, e->ple, lanes, st));
   }
   OKAY(project(e, &L->ple_proj, e->gate, e->inner_max, lanes, e->lift, H));
-  /* state = (state + norm(ple) * after_ple) * layer_scalar; scrap = next layer's input */
-  RUN(igl_launch_norm_add(e->state, H, e->lift, H, L->after_ple, H, lanes, e->eps, L->layer_gain,
-                          L->layer_gain != 1.0f, next_norm, e->scrap, H, st));
+  /* state = (state + norm(ple) * after_ple) * layer_scalar: applied by the
+   * next launch that reads state (settle, or a fused prologue) */
+  e->pending = 1;
+  e->pending_gain = L->after_ple;
+  e->pending_scale = L->layer_gain;
   return IGL_OKAY;
 }
 
@@ -755,6 +808,9 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
 static int run_pass(igl_engine *e, int bound, int lanes, int logits) {
   hipStream_t st = e->stream;
   const int H = e->hidden;
+  e->cur = 0;
+  e->state = e->state_buf[0];
+  e->pending = 0;
   /* embedding row times sqrt(hidden) */
   {
     const igl_plane *p = &e->embed;
@@ -777,10 +833,17 @@ static int run_pass(igl_engine *e, int bound, int lanes, int logits) {
   }
   OKAY(norm_rows(e, e->state, e->layer[0].enter_norm, H, lanes, H, e->scrap));
   for (int li = 0; li < e->layers; ++li) OKAY(run_layer(e, li, bound, lanes));
+  if (logits == 1 && lanes == 1) {
+    /* the last update with the final norm in one launch */
+    OKAY(settle(e, lanes, e->final_norm));
+  } else {
+    OKAY(settle(e, lanes, NULL));
+  }
   if (logits) {
     const int from = logits == 2 ? 0 : lanes - 1;
     const int span = lanes - from;
-    OKAY(norm_rows(e, e->state + (size_t)from * H, e->final_norm, H, span, H, e->scrap));
+    if (!(logits == 1 && lanes == 1))
+      OKAY(norm_rows(e, e->state + (size_t)from * H, e->final_norm, H, span, H, e->scrap));
     OKAY(project(e, &e->head, e->scrap, H, span, e->logits, e->vocab));
     if (e->cap > 0.0f) RUN(igl_launch_logit_cap(e->logits, (size_t)span * e->vocab, e->cap, st));
   }

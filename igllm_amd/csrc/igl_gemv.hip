@@ -26,6 +26,7 @@
 //     gain * (sum (16 + c) x - (16 + code_bias) X).
 //   * Row sums close with six DPP adds across the wave.
 #include "igl_device.h"
+#include "igl_launch.h"
 
 namespace igl {
 
@@ -385,12 +386,83 @@ struct GemvGroupArgs {
   int ksplit;
   float unit_bias;
   const float *mul;       // GEMV_GELU_MUL
+  // The residual update in front of the product (with `state_in` set): the
+  // activations are not read from `act` but formed in every workgroup as
+  //   s = (state_in + norm(lift) * lift_gain) * scale   (lift NULL: s = state_in)
+  //   x = norm(s) * norm_gain                           (norm_gain NULL: x = s)
+  // with the float operations of norm_add_kernel; workgroup 0 writes s to
+  // `state_out`, which must not alias `state_in`.
+  const float *state_in;
+  float *state_out;
+  const float *lift;
+  const float *lift_gain;
+  float scale;
+  int apply_scale;
+  const float *norm_gain;
+  float eps;
 };
 
-template <int MODE>
+// The update above for K <= 256 HELD, into `xs` (K floats of LDS).  Thread t
+// holds elements t + 256 k, as norm_add_kernel does.
+template <int HELD>
+__device__ __forceinline__ void group_prologue(const GemvGroupArgs &a, float *xs, double *red) {
+  constexpr int kHeld = HELD;
+  const int n = a.K;
+  float sv[kHeld], lv[kHeld], gv[kHeld], nv[kHeld];
+#pragma unroll
+  for (int k = 0; k < kHeld; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    const bool in = i < n;
+    sv[k] = in ? a.state_in[i] : 0.0f;
+    lv[k] = in && a.lift ? a.lift[i] : 0.0f;
+    gv[k] = in && a.lift ? a.lift_gain[i] : 0.0f;
+    nv[k] = in && a.norm_gain ? a.norm_gain[i] : 0.0f;
+  }
+  if (a.lift) {
+    double acc = 0.0;
+#pragma unroll
+    for (int k = 0; k < kHeld; ++k) acc += (double)lv[k] * (double)lv[k];
+    const float shrink = rms_shrink(block_sum_f64(acc, red), n, a.eps);
+#pragma unroll
+    for (int k = 0; k < kHeld; ++k) {
+      const float normed = lv[k] * shrink * gv[k];
+      float sum = sv[k] + normed;
+      if (a.apply_scale) sum *= a.scale;
+      sv[k] = sum;
+    }
+    if (blockIdx.x == 0) {
+#pragma unroll
+      for (int k = 0; k < kHeld; ++k) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < n) a.state_out[i] = sv[k];
+      }
+    }
+  }
+  float shrink2 = 1.0f;
+  if (a.norm_gain) {
+    double acc2 = 0.0;
+#pragma unroll
+    for (int k = 0; k < kHeld; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      if (i < n) acc2 += (double)sv[k] * (double)sv[k];
+    }
+    shrink2 = rms_shrink(block_sum_f64(acc2, red), n, a.eps);
+  }
+#pragma unroll
+  for (int k = 0; k < kHeld; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    if (i < n) xs[i] = a.norm_gain ? sv[k] * shrink2 * nv[k] : sv[k];
+  }
+  __syncthreads();
+}
+
+// PRO: 0, or the elements a thread holds in the prologue (K <= 256 PRO).
+template <int MODE, int PRO>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupArgs a) {
   constexpr int R = 4;
   __shared__ float red[4][R];
+  __shared__ double pro_red[16];
+  __shared__ __attribute__((aligned(16))) float xs[PRO ? 256 * PRO : 4];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -432,13 +504,23 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
           reinterpret_cast<const uint4_t *>(a.codes[p] + (size_t)prow[r] * (size_t)a.row_stride[p]) + u);
       s[r] = a.gains[p][(size_t)prow[r] * (size_t)a.gain_stride[p] + ((unsigned)u >> a.group_shift)];
     }
-    const float *src = a.act + u * 32;
-    if (a.act_vec) {
+    if (!PRO) {
+      const float *src = a.act + u * 32;
+      if (a.act_vec) {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) x[q] = *reinterpret_cast<const float4_t *>(src + 4 * q);
-    } else {
+        for (int q = 0; q < 8; ++q) x[q] = *reinterpret_cast<const float4_t *>(src + 4 * q);
+      } else {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) x[q] = float4_t{src[4 * q], src[4 * q + 1], src[4 * q + 2], src[4 * q + 3]};
+        for (int q = 0; q < 8; ++q) x[q] = float4_t{src[4 * q], src[4 * q + 1], src[4 * q + 2], src[4 * q + 3]};
+      }
+    }
+  }
+  if (PRO) {
+    // The weight loads above are in flight while the block forms x.
+    group_prologue<PRO ? PRO : 1>(a, xs, pro_red);
+    if (has) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) x[q] = *reinterpret_cast<const float4_t *>(xs + u * 32 + 4 * q);
     }
   }
 
@@ -961,11 +1043,23 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
                                             const float *const *gains, const int *gain_stride,
                                             const int *rows, float *const *out, int group_size,
                                             int code_bias, const float *act, int K,
-                                            const float *mul, hipStream_t stream) {
+                                            const float *mul, const igl_gemv_prologue *pro,
+                                            hipStream_t stream) {
   GemvGroupArgs a;
   const int units = K / 32;
   if (segments < 1 || segments > 3 || K % 32 || units > 4 * kWave || group_size < 32)
     return hipErrorInvalidValue;
+  if (pro && (K > 4096 || !pro->state_in || (pro->lift && (!pro->state_out || !pro->lift_gain ||
+                                                            pro->state_out == pro->state_in))))
+    return hipErrorInvalidValue;
+  a.state_in = pro ? pro->state_in : nullptr;
+  a.state_out = pro ? pro->state_out : nullptr;
+  a.lift = pro ? pro->lift : nullptr;
+  a.lift_gain = pro ? pro->lift_gain : nullptr;
+  a.scale = pro ? pro->scale : 1.0f;
+  a.apply_scale = pro ? pro->apply_scale : 0;
+  a.norm_gain = pro ? pro->norm_gain : nullptr;
+  a.eps = pro ? pro->eps : 0.0f;
   if ((mode == GEMV_GELU_PAIR && (segments != 2 || rows[0] != rows[1])) ||
       (mode == GEMV_GELU_MUL && (segments != 1 || !mul)))
     return hipErrorInvalidValue;
@@ -996,19 +1090,26 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
   a.ksplit = ksplit;
   const int tiles_per_block = 4 / ksplit;
   dim3 grid((a.tiles + tiles_per_block - 1) / tiles_per_block);
-  switch (mode) {
-    case GEMV_SEGMENTS:
-      hipLaunchKernelGGL((gemv_q4_group_kernel<GEMV_SEGMENTS>), grid, dim3(kGemvThreads), 0, stream, a);
-      break;
-    case GEMV_GELU_PAIR:
-      hipLaunchKernelGGL((gemv_q4_group_kernel<GEMV_GELU_PAIR>), grid, dim3(kGemvThreads), 0, stream, a);
-      break;
-    case GEMV_GELU_MUL:
-      hipLaunchKernelGGL((gemv_q4_group_kernel<GEMV_GELU_MUL>), grid, dim3(kGemvThreads), 0, stream, a);
-      break;
-    default:
-      return hipErrorInvalidValue;
+#define IGL_GROUP_LAUNCH(M_, P_) \
+  hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_>), grid, dim3(kGemvThreads), 0, stream, a)
+  // registers the prologue holds: the fewest of 6, 8, 16 a thread that cover K
+  const int held = !pro ? 0 : K <= 6 * 256 ? 6 : K <= 8 * 256 ? 8 : 16;
+  switch (mode * 4 + (held == 0 ? 0 : held == 6 ? 1 : held == 8 ? 2 : 3)) {
+    case 0: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 0); break;
+    case 1: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 6); break;
+    case 2: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 8); break;
+    case 3: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 16); break;
+    case 4: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 0); break;
+    case 5: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 6); break;
+    case 6: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 8); break;
+    case 7: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 16); break;
+    case 8: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 0); break;
+    case 9: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 6); break;
+    case 10: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 8); break;
+    case 11: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 16); break;
+    default: return hipErrorInvalidValue;
   }
+#undef IGL_GROUP_LAUNCH
   return hipGetLastError();
 }
 

@@ -21,11 +21,26 @@ size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit);
 #define IGL_GEMV_SEGMENTS 0
 #define IGL_GEMV_GELU_PAIR 1
 #define IGL_GEMV_GELU_MUL 2
+/* The residual update a grouped launch can form in front of its product, in
+ * place of reading `act`: s = (state_in + norm(lift) * lift_gain) * scale
+ * (lift NULL: s = state_in), written to state_out by one workgroup; the
+ * activations are norm(s) * norm_gain (norm_gain NULL: s).  K <= 4096. */
+typedef struct igl_gemv_prologue {
+  const float *state_in;
+  float *state_out;
+  const float *lift;
+  const float *lift_gain;
+  float scale;
+  int apply_scale;
+  const float *norm_gain;
+  float eps;
+} igl_gemv_prologue;
 hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_t *const *codes,
                                  const long long *row_stride, const float *const *gains,
                                  const int *gain_stride, const int *rows, float *const *out,
                                  int group_size, int code_bias, const float *act, int K,
-                                 const float *mul, hipStream_t stream);
+                                 const float *mul, const igl_gemv_prologue *pro,
+                                 hipStream_t stream);
 hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_stride, const float *gains,
                               int gain_stride, int group_size, int code_bias, const float *act,
                               int act_stride, int lanes, float *out, int out_stride, int N, int K,
