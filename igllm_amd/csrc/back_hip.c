@@ -51,6 +51,9 @@ struct igl_desk_state {
   /* staging for the elementwise host entries */
   float *elem_dev;
   size_t elem_floats;
+  /* the GEMM's binary16 copy of its activations */
+  float *gemm_dev;
+  size_t gemm_floats;
 };
 
 static void desk_fail(igl_desk_state *st, int code) {
@@ -288,11 +291,17 @@ static int gemm_run(igl_desk *desk, const igl_plane *sheet, const void *act_dev,
     desk_fail(st, code);
     return code;
   }
+  {
+    size_t bytes = igl_gemm_work_bytes(lane_count, sheet->row_count, sheet->col_count);
+    if (bytes && grow_dev(st, &st->gemm_dev, &st->gemm_floats, (bytes + 3) / 4) != IGL_OKAY)
+      return IGL_FAIL_MEMORY;
+  }
   return hip_check(st, igl_launch_gemm_q4(act_dev, act_bf16, act_stride, (const uint8_t *)dp->codes,
                                           (long long)sheet->row_stride, dp->gains,
                                           sheet->group_count, sheet->group_size, sheet->code_bias,
                                           out_dev, out_bf16, out_stride, lane_count,
-                                          sheet->row_count, sheet->col_count, st->stream));
+                                          sheet->row_count, sheet->col_count, st->gemm_dev,
+                                          st->stream));
 }
 
 int igl_gemm_lane_floor(void) { return IGL_GEMM_FLOOR; }
@@ -599,6 +608,7 @@ void igl_back_close(igl_desk *desk) {
   if (st->part_dev) (void)hipFree(st->part_dev);
   if (st->work_dev) (void)hipFree(st->work_dev);
   if (st->elem_dev) (void)hipFree(st->elem_dev);
+  if (st->gemm_dev) (void)hipFree(st->gemm_dev);
   if (st->mark[0]) (void)hipEventDestroy(st->mark[0]);
   if (st->mark[1]) (void)hipEventDestroy(st->mark[1]);
   if (st->stream) (void)hipStreamDestroy(st->stream);

@@ -46,10 +46,13 @@ hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_stride, const 
                               int act_stride, int lanes, float *out, int out_stride, int N, int K,
                               float *part, int lds_limit, hipStream_t stream);
 
+/* `work`: igl_gemm_work_bytes(M, N, K) bytes (NULL takes the small-tile form). */
+size_t igl_gemm_work_bytes(int M, int N, int K);
 hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride, const uint8_t *codes,
                               long long row_stride, const float *gains, int gain_stride,
                               int group_size, int code_bias, void *out, int out_bf16,
-                              int out_stride, int M, int N, int K, hipStream_t stream);
+                              int out_stride, int M, int N, int K, void *work,
+                              hipStream_t stream);
 
 int igl_attend_chunk_size(void);
 size_t igl_attend_work_floats(int place0, int window, int lanes, int head_count, int head_size);

@@ -81,4 +81,6 @@ def test_e2b_greedy_stream_matches_reference(backend, precise):
     gap = float(np.max(np.abs(margins - ref_margin)))
     print("precise", precise, "max margin difference", gap)
     assert np.array_equal(ids, want)
-    assert gap <= 2e-3
+    # The fast mode primes through binary16 GEMM operands, which moves some
+    # cached FP8 key/value bytes by one step; the gaps then move by ~1e-3.
+    assert gap <= (2e-3 if precise else 5e-3)
