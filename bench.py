@@ -180,10 +180,45 @@ def e2e_decode(be, prompt_count=2048, gen=256):
             out.setdefault("streams", []).append(picks)
         out["prefill_modes_agree"] = out["streams"][0] == out["streams"][1]
         out.pop("streams")
+        out["guess"] = e2e_guess(be, folder, shape, prompt_count, gen)
     finally:
         import shutil
         shutil.rmtree(folder, ignore_errors=True)
     return out
+
+
+def e2e_guess(be, folder, shape, prompt_count, gen, span=4, repeat=512):
+    """--guess 4 against plain greedy decode on a prompt that repeats its first
+    512 ids, on one engine: plain decode, then the same prompt again under the
+    prompt-lookup loop.  The two streams must agree."""
+    from igllm_amd.engine import Engine, Scout, guess_loop, prompt_ids
+
+    prompt = prompt_ids(prompt_count, shape.vocab, seed=0, repeat_span=repeat)
+    eng = Engine(be, folder, window_limit=prompt_count + gen + 64, lane_limit=16, precise=True)
+    try:
+        eng.prime(prompt)
+        be.sync()
+        token, plain = int(prompt[-1]), []
+        t0 = time.perf_counter()
+        for _ in range(gen):
+            token, _ = eng.step(token)
+            plain.append(token)
+        plain_s = time.perf_counter() - t0
+        eng.reset()
+        eng.prime(prompt)
+        be.sync()
+        t0 = time.perf_counter()
+        ids, (rounds, drawn, taken) = guess_loop(
+            Scout(eng.lib), prompt, gen, span, lambda t: eng.step(t)[0],
+            lambda b: eng.guess(b)[0], eng.keep)
+        guess_s = time.perf_counter() - t0
+    finally:
+        eng.close()
+    return {"prompt": f"{prompt_count} ids repeating the first {repeat}", "span": span,
+            "gen": gen, "decode_tok_s": round(gen / guess_s, 1),
+            "plain_decode_tok_s": round(gen / plain_s, 1),
+            "rounds": rounds, "drawn": drawn, "taken": taken,
+            "streams_agree": bool(np.array_equal(ids, plain)), "first_ids": ids[:16].tolist()}
 
 
 class Rotation:

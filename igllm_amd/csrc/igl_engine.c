@@ -95,7 +95,9 @@ struct igl_engine {
   size_t attend_floats;
   int q_stride, kv_stride, inner_max, ple_stride;
   void *pick_work;
-  int32_t *pick_dev;  /* [0] the pick, [1] its margin (as float bits) */
+  int32_t *pick_dev;  /* per lane: the pick, its margin (as float bits) */
+  int32_t *pairs_host; /* pinned: a block's picks and margins */
+  int guess_from, guess_count; /* a block in flight (igl_engine_guess) */
   /* the decode step as one captured graph */
   igl_step_io *io;    /* pinned: what the step reads and writes on the host */
   int graph_on, graph_ready, graph_tried;
@@ -547,13 +549,13 @@ int igl_engine_open(igl_engine **out, igl_desk *desk, const char *folder, int wi
         (code = dev_alloc((void **)&e->ple_seed, lanes * e->ple_stride * 4)) ||
         (code = dev_alloc((void **)&e->ple_room, lanes * e->ple_stride * 4)) ||
         (code = dev_alloc((void **)&e->logits, lanes * (size_t)e->vocab * 4)) ||
-        (code = dev_alloc(&e->pick_work, igl_pick_work_bytes())) ||
-        (code = dev_alloc((void **)&e->pick_dev, 2 * sizeof(int32_t))))
+        (code = dev_alloc(&e->pick_work, igl_pick_work_bytes(e->lane_limit))) ||
+        (code = dev_alloc((void **)&e->pick_dev, 2 * lanes * sizeof(int32_t))))
       goto fail;
     e->ids_dev = e->ctl_dev + 1;
     e->state = e->state_buf[0];
-    if (hipHostMalloc((void **)&e->io, sizeof(igl_step_io), hipHostMallocDefault) != hipSuccess) {
-      e->io = NULL;
+    if (hipHostMalloc((void **)&e->io, sizeof(igl_step_io), hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc((void **)&e->pairs_host, 2 * lanes * sizeof(int32_t), hipHostMallocDefault) != hipSuccess) {
       code = IGL_FAIL_MEMORY;
       goto fail;
     }
@@ -594,6 +596,7 @@ void igl_engine_close(igl_engine *e) {
       if (bufs[j]) (void)hipFree(bufs[j]);
   }
   if (e->io) (void)hipHostFree(e->io);
+  if (e->pairs_host) (void)hipHostFree(e->pairs_host);
   if (e->map) munmap(e->map, e->map_bytes);
   free(e->tensor);
   free(e);
@@ -852,7 +855,7 @@ static int run_pass(igl_engine *e, int bound, int lanes, int logits) {
 
 int igl_engine_prime(igl_engine *e, const int32_t *ids, int count) {
   if (!e || !ids || count < 1) return IGL_FAIL_ARGUMENT;
-  if (e->fill + count > e->window_limit) return IGL_FAIL_STATE;
+  if (e->guess_count || e->fill + count > e->window_limit) return IGL_FAIL_STATE;
   for (int l = 0; l < count; ++l)
     if (ids[l] < 0 || ids[l] >= e->embed.row_count) return IGL_FAIL_ARGUMENT;
   /* every id but the last, in chunks of the lane limit (session_prime_media 14443-14467) */
@@ -875,7 +878,7 @@ static int step_body(igl_engine *e) {
   RUN(hipMemcpyAsync(e->ctl_dev, &e->io->place, 2 * sizeof(int32_t), hipMemcpyHostToDevice,
                      e->stream));
   OKAY(run_pass(e, e->window_limit - 1, 1, 1));
-  RUN(igl_launch_pick(e->logits, e->vocab, e->pick_work, e->pick_dev, (float *)(e->pick_dev + 1),
+  RUN(igl_launch_pick(e->logits, e->vocab, (size_t)e->vocab, 1, e->pick_work, e->pick_dev,
                       e->stream));
   RUN(hipMemcpyAsync(&e->io->pick, e->pick_dev, 2 * sizeof(int32_t), hipMemcpyDeviceToHost,
                      e->stream));
@@ -900,7 +903,7 @@ static int capture_step(igl_engine *e) {
 
 int igl_engine_step(igl_engine *e, int32_t id, int32_t *pick_out, float *margin_out) {
   if (!e) return IGL_FAIL_ARGUMENT;
-  if (e->fill + 1 > e->window_limit) return IGL_FAIL_STATE;
+  if (e->guess_count || e->fill + 1 > e->window_limit) return IGL_FAIL_STATE;
   if (id < 0 || id >= e->embed.row_count) return IGL_FAIL_ARGUMENT;
   e->io->place = e->fill;
   e->io->id = id;
@@ -930,6 +933,115 @@ int igl_engine_set_graph(igl_engine *e, int on) {
   if (!e) return IGL_FAIL_ARGUMENT;
   e->graph_on = on ? 1 : 0;
   return IGL_OKAY;
+}
+
+/* ---- a speculative block (session_guess / session_guess_keep) ------------ */
+
+/* session_guess (app_core.c:12139-12203): ids[0] is the next input and
+ * ids[1 ..] the proposed continuation; one pass over all of them, with the
+ * greedy pick (and its top-1/top-2 gap) of every lane's row of logits.  The
+ * cache keeps the block's rows until igl_engine_keep.  Nothing needs saving
+ * first: a sliding ring here is window + lane_limit rows deep, so the rows a
+ * block overwrites are past every window a later position can reach, and a
+ * full-depth ring only gains rows past the kept positions, which later
+ * steps overwrite before any query reads them. */
+int igl_engine_guess(igl_engine *e, const int32_t *ids, int count, int32_t *picks_out,
+                     float *margins_out) {
+  if (!e || !ids || count < 1 || count > e->lane_limit) return IGL_FAIL_ARGUMENT;
+  if (e->guess_count || e->fill + count > e->window_limit) return IGL_FAIL_STATE;
+  for (int l = 0; l < count; ++l)
+    if (ids[l] < 0 || ids[l] >= e->embed.row_count) return IGL_FAIL_ARGUMENT;
+  RUN(igl_launch_put_int(e->ctl_dev, e->fill, e->stream));
+  RUN(hipMemcpyAsync(e->ids_dev, ids, (size_t)count * sizeof(int32_t), hipMemcpyHostToDevice,
+                     e->stream));
+  OKAY(run_pass(e, e->fill, count, 2));
+  RUN(igl_launch_pick(e->logits, e->vocab, (size_t)e->vocab, count, e->pick_work, e->pick_dev,
+                      e->stream));
+  RUN(hipMemcpyAsync(e->pairs_host, e->pick_dev, 2 * (size_t)count * sizeof(int32_t),
+                     hipMemcpyDeviceToHost, e->stream));
+  RUN(hipStreamSynchronize(e->stream));
+  OKAY(igl_desk_error_take(e->desk));
+  for (int l = 0; l < count; ++l) {
+    if (picks_out) picks_out[l] = e->pairs_host[2 * l];
+    if (margins_out) memcpy(&margins_out[l], &e->pairs_host[2 * l + 1], sizeof(float));
+  }
+  e->guess_from = e->fill;
+  e->guess_count = count;
+  return IGL_OKAY;
+}
+
+/* session_guess_keep (12207-12223): the first `keep` lanes of the block stay
+ * in the session; 0 leaves it as it was before the block. */
+int igl_engine_keep(igl_engine *e, int keep) {
+  if (!e) return IGL_FAIL_ARGUMENT;
+  if (!e->guess_count) return IGL_FAIL_STATE;
+  if (keep < 0 || keep > e->guess_count) return IGL_FAIL_ARGUMENT;
+  e->fill = e->guess_from + keep;
+  e->guess_count = 0;
+  return IGL_OKAY;
+}
+
+/* ---- the prompt-lookup proposer (the reference's scout, 12225-12361) ---- */
+
+#define IGL_SCOUT_REACH 3
+#define IGL_SCOUT_REACH_LEAST 2
+
+struct igl_scout {
+  int32_t *ids;
+  int count, room;
+};
+
+int igl_scout_open(igl_scout **out) {
+  if (!out) return IGL_FAIL_ARGUMENT;
+  *out = (igl_scout *)calloc(1, sizeof(igl_scout));
+  return *out ? IGL_OKAY : IGL_FAIL_MEMORY;
+}
+
+void igl_scout_close(igl_scout *scout) {
+  if (!scout) return;
+  free(scout->ids);
+  free(scout);
+}
+
+/* Ids the stream has committed to, in order (scout_note, 12311-12328). */
+int igl_scout_note(igl_scout *scout, const int32_t *ids, int count) {
+  if (!scout || (!ids && count > 0) || count < 0) return IGL_FAIL_ARGUMENT;
+  if (scout->count + count > scout->room) {
+    int room = scout->room ? scout->room : 1024;
+    int32_t *fresh;
+    while (room < scout->count + count) room *= 2;
+    fresh = (int32_t *)realloc(scout->ids, sizeof(int32_t) * (size_t)room);
+    if (!fresh) return IGL_FAIL_MEMORY;
+    scout->ids = fresh;
+    scout->room = room;
+  }
+  if (count) memcpy(scout->ids + scout->count, ids, sizeof(int32_t) * (size_t)count);
+  scout->count += count;
+  return IGL_OKAY;
+}
+
+/* Up to `want` ids that followed the latest earlier occurrence of the
+ * stream's last `reach` ids, the longest reach (3, then 2) that matches
+ * anywhere; 0 when none does (scout_draw, 12341-12361). */
+int igl_scout_draw(const igl_scout *scout, int32_t *out, int want) {
+  if (!scout || !out || want < 1) return 0;
+  for (int reach = IGL_SCOUT_REACH; reach >= IGL_SCOUT_REACH_LEAST; --reach) {
+    const int32_t *tail;
+    if (scout->count < reach + 1) continue;
+    tail = scout->ids + scout->count - reach;
+    for (int place = scout->count - reach - 1; place >= 0; --place) {
+      int slot, take;
+      for (slot = 0; slot < reach; ++slot)
+        if (scout->ids[place + slot] != tail[slot]) break;
+      if (slot < reach) continue;
+      take = scout->count - (place + reach);
+      if (take < 1) continue;
+      if (take > want) take = want;
+      memcpy(out, scout->ids + place + reach, sizeof(int32_t) * (size_t)take);
+      return take;
+    }
+  }
+  return 0;
 }
 
 int igl_engine_logits(igl_engine *e, float *out, int lane) {

@@ -100,9 +100,9 @@ hipError_t igl_launch_cache_lay_rows(const float *rows, int row_stride, int widt
                                      uint8_t *store, int span, int place_first, int lanes,
                                      hipStream_t stream);
 hipError_t igl_launch_logit_cap(float *v, size_t n, float cap, hipStream_t stream);
-size_t igl_pick_work_bytes(void);
-hipError_t igl_launch_pick(const float *v, int n, void *work, int32_t *index_out,
-                           float *margin_out, hipStream_t stream);
+size_t igl_pick_work_bytes(int lanes);
+hipError_t igl_launch_pick(const float *v, int n, size_t stride, int lanes, void *work,
+                           int32_t *pairs, hipStream_t stream);
 
 hipError_t igl_launch_norm_rms(const float *in, const float *gain, int n, int rows, int stride,
                                float eps, float *out, hipStream_t stream);

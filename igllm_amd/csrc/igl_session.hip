@@ -295,8 +295,12 @@ __device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
   return r;
 }
 
-__global__ __launch_bounds__(256) void pick_stage_kernel(const float *v, int n, Top2 *part) {
+// One lane of logits a grid row (blockIdx.y), `stride` floats apart.
+__global__ __launch_bounds__(256) void pick_stage_kernel(const float *v, int n, size_t stride,
+                                                         Top2 *part) {
   __shared__ Top2 red[256];
+  v += (size_t)blockIdx.y * stride;
+  part += (size_t)blockIdx.y * gridDim.x;
   Top2 t{-INFINITY, 0x7FFFFFFF, -INFINITY};
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
     Top2 one{v[i], i, -INFINITY};
@@ -311,9 +315,13 @@ __global__ __launch_bounds__(256) void pick_stage_kernel(const float *v, int n, 
   if (threadIdx.x == 0) part[blockIdx.x] = red[0];
 }
 
-__global__ __launch_bounds__(256) void pick_final_kernel(const Top2 *part, int parts, int32_t *index_out,
-                                                         float *margin_out) {
+// Workgroup l closes lane l: pairs[2 l] = its pick, pairs[2 l + 1] = the
+// margin's float bits.
+__global__ __launch_bounds__(256) void pick_final_kernel(const Top2 *part, int parts, int32_t *pairs) {
   __shared__ Top2 red[256];
+  part += (size_t)blockIdx.x * parts;
+  int32_t *index_out = pairs + 2 * blockIdx.x;
+  float *margin_out = reinterpret_cast<float *>(pairs + 2 * blockIdx.x + 1);
   Top2 t{-INFINITY, 0x7FFFFFFF, -INFINITY};
   for (int i = threadIdx.x; i < parts; i += blockDim.x) t = top2_merge(t, part[i]);
   red[threadIdx.x] = t;
@@ -439,15 +447,18 @@ extern "C" hipError_t igl_launch_logit_cap(float *v, size_t n, float cap, hipStr
   return hipGetLastError();
 }
 
-extern "C" size_t igl_pick_work_bytes(void) { return sizeof(Top2) * kPickBlocks; }
+// Workspace for `lanes` lanes of igl_launch_pick.
+extern "C" size_t igl_pick_work_bytes(int lanes) { return sizeof(Top2) * kPickBlocks * (size_t)lanes; }
 
-extern "C" hipError_t igl_launch_pick(const float *v, int n, void *work, int32_t *index_out,
-                                      float *margin_out, hipStream_t stream) {
-  hipLaunchKernelGGL(pick_stage_kernel, dim3(kPickBlocks), dim3(256), 0, stream, v, n,
-                     reinterpret_cast<Top2 *>(work));
+// The greedy pick of `lanes` rows of n logits, `stride` floats apart, into
+// pairs[2 l] (index) and pairs[2 l + 1] (the top-1/top-2 gap's float bits).
+extern "C" hipError_t igl_launch_pick(const float *v, int n, size_t stride, int lanes, void *work,
+                                      int32_t *pairs, hipStream_t stream) {
+  hipLaunchKernelGGL(pick_stage_kernel, dim3(kPickBlocks, lanes), dim3(256), 0, stream, v, n,
+                     stride, reinterpret_cast<Top2 *>(work));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(pick_final_kernel, dim3(1), dim3(256), 0, stream,
-                     reinterpret_cast<const Top2 *>(work), kPickBlocks, index_out, margin_out);
+  hipLaunchKernelGGL(pick_final_kernel, dim3(lanes), dim3(256), 0, stream,
+                     reinterpret_cast<const Top2 *>(work), kPickBlocks, pairs);
   return hipGetLastError();
 }

@@ -47,6 +47,7 @@ class Engine:
                  precise: bool = True):
         self.backend = backend
         self.lib = backend.lib
+        self.lane_limit = lane_limit
         self.handle = ctypes.c_void_p()
         code = self.lib.igl_engine_open(ctypes.byref(self.handle), ctypes.byref(backend.desk),
                                         folder.encode(), window_limit, lane_limit, int(precise))
@@ -98,4 +99,89 @@ class Engine:
     def close(self):
         if self.handle:
             self.lib.igl_engine_close(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def guess(self, ids: np.ndarray):
+        """One block pass (session_guess): the greedy pick and gap of every lane."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        picks = np.empty(ids.size, dtype=np.int32)
+        margins = np.empty(ids.size, dtype=np.float32)
+        self._check(self.lib.igl_engine_guess(self.handle, ids.ctypes.data, ids.size,
+                                              picks.ctypes.data, margins.ctypes.data), "guess")
+        return picks, margins
+
+    def keep(self, count: int):
+        self._check(self.lib.igl_engine_keep(self.handle, int(count)), "keep")
+
+    def guess_greedy(self, prompt: np.ndarray, count: int, span: int = 4):
+        """The CLI's greedy --guess loop (main_answer_guess, app_main.c:520-598)
+        without the stop-id check: the scout proposes up to span - 1 ids, the
+        block keeps the prefix the model agrees with plus its next pick; with
+        nothing proposed, an ordinary step.  Returns the ids and (rounds, ids
+        proposed, ids taken)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        self.prime(prompt)
+        return guess_loop(Scout(self.lib), prompt, count, min(span, self.lane_limit),
+                          lambda t: self.step(t)[0], lambda b: self.guess(b)[0], self.keep)
+
+
+def guess_loop(scout, prompt, count, span, step, guess, keep):
+    """main_answer_guess's greedy loop over a primed session: `step(id)` is
+    one ordinary step's pick, `guess(block)` the picks of a block's lanes and
+    `keep(n)` session_guess_keep.  Owns and closes `scout`."""
+    span = max(1, min(span, 16))
+    try:
+        scout.note(prompt)
+        token = int(prompt[-1])
+        out, rounds, drawn, taken = [], 0, 0, 0
+        while len(out) < count:
+            want = max(0, min(span - 1, count - len(out) - 1))
+            drafts = scout.draw(want)
+            rounds += 1
+            if drafts.size == 0:
+                token = int(step(token))
+                out.append(token)
+                scout.note(np.array([token], dtype=np.int32))
+                continue
+            block = np.concatenate([np.array([token], dtype=np.int32), drafts])
+            picks = guess(block)
+            drawn += drafts.size
+            take = 0
+            while take + 1 < block.size and picks[take] == block[take + 1]:
+                take += 1
+            taken += take
+            made = [int(t) for t in block[1:take + 1]] + [int(picks[take])]
+            out.extend(made)
+            scout.note(np.array(made, dtype=np.int32))
+            token = made[-1]
+            keep(take + 1)
+        return np.array(out, dtype=np.int32), (rounds, drawn, taken)
+    finally:
+        scout.close()
+
+
+class Scout:
+    """The prompt-lookup proposer (igl_scout_*)."""
+
+    def __init__(self, lib):
+        self.lib = lib
+        self.handle = ctypes.c_void_p()
+        if lib.igl_scout_open(ctypes.byref(self.handle)) != native.IGL_OKAY:
+            raise BackendError("igl_scout_open")
+
+    def note(self, ids: np.ndarray):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        if self.lib.igl_scout_note(self.handle, ids.ctypes.data, ids.size) != native.IGL_OKAY:
+            raise BackendError("igl_scout_note")
+
+    def draw(self, want: int) -> np.ndarray:
+        if want < 1:
+            return np.empty(0, dtype=np.int32)
+        out = np.empty(want, dtype=np.int32)
+        got = self.lib.igl_scout_draw(self.handle, out.ctypes.data, want)
+        return out[:got].copy()
+
+    def close(self):
+        if self.handle:
+            self.lib.igl_scout_close(self.handle)
             self.handle = ctypes.c_void_p()

@@ -129,6 +129,12 @@ SIGNATURES = {
     "igl_engine_vocab": (_I, [_P]),
     "igl_engine_reset": (_I, [_P]),
     "igl_engine_set_graph": (_I, [_P, _I]),
+    "igl_engine_guess": (_I, [_P, _P, _I, _P, _P]),
+    "igl_engine_keep": (_I, [_P, _I]),
+    "igl_scout_open": (_I, [ctypes.POINTER(_P)]),
+    "igl_scout_close": (None, [_P]),
+    "igl_scout_note": (_I, [_P, _P, _I]),
+    "igl_scout_draw": (_I, [_P, _P, _I]),
     "igl_cache_lay_dev": (_I, [ctypes.POINTER(Desk), _P, _I, _F, _I, _P, _Z]),
     "igl_norm_rms_dev": (_I, [ctypes.POINTER(Desk), _P, _P, _I, _I, _I, _F, _P]),
     "igl_soft_max_dev": (_I, [ctypes.POINTER(Desk), _P, _I, _I, _I]),

@@ -261,6 +261,23 @@ int  igl_engine_reset(igl_engine *engine);
  * first step runs as enqueued and is captured; later steps launch the capture,
  * whose kernels read the position and id from device memory. */
 int  igl_engine_set_graph(igl_engine *engine, int on);
+/* session_guess (app_core.c:12139-12203): one pass over ids[0 .. count) (the
+ * next input, then a proposed continuation) with the greedy pick and top-1 /
+ * top-2 gap of every lane; the block stays open until igl_engine_keep, and
+ * step / prime / guess refuse meanwhile.  count <= lane_limit. */
+int  igl_engine_guess(igl_engine *engine, const int32_t *ids, int count, int32_t *picks_out,
+                      float *margins_out);
+/* session_guess_keep (12207-12223): keep the block's first `keep` lanes. */
+int  igl_engine_keep(igl_engine *engine, int keep);
+
+/* The prompt-lookup proposer (the reference's scout, app_core.c:12225-12361):
+ * the committed ids in order, and what followed the latest earlier occurrence
+ * of the last 3 (else 2) of them. */
+typedef struct igl_scout igl_scout;
+int  igl_scout_open(igl_scout **scout_out);
+void igl_scout_close(igl_scout *scout);
+int  igl_scout_note(igl_scout *scout, const int32_t *ids, int count);
+int  igl_scout_draw(const igl_scout *scout, int32_t *out, int want);
 
 #ifdef __cplusplus
 }

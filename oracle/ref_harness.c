@@ -157,6 +157,85 @@ int ref_engine_greedy(const char *folder, int thread_count, int cache_bits, int 
   return (int)code;
 }
 
+static int32_t ref_top(const float *logits, int vocab) {
+  int32_t best = 0;
+  for (int v = 1; v < vocab; ++v)
+    if (logits[v] > logits[best]) best = v;
+  return best;
+}
+
+/* The CLI's greedy --guess loop (main_answer_guess, app_main.c:520-598) on
+ * the reference engine, without the stop-id check: the scout proposes up to
+ * span - 1 ids (scout_draw), session_guess runs the block, the argmax rows
+ * keep the agreed prefix plus the next id, session_guess_keep commits them;
+ * with nothing proposed, an ordinary step.  stats_out: rounds, ids proposed,
+ * ids taken. */
+int ref_engine_guess(const char *folder, int thread_count, int cache_bits, int window_limit,
+                     const int32_t *prompt, int prompt_count, int gen_count, int span,
+                     int32_t *out_ids, long *stats_out) {
+  app_setup setup = app_setup_plain();
+  app_model *model = NULL;
+  app_session *session = NULL;
+  app_scout *scout = NULL;
+  app_code code;
+  int32_t block[16];
+  int32_t id_value;
+  int made = 0, vocab;
+  long rounds = 0, drawn = 0, taken = 0;
+  setup.thread_count = thread_count;
+  setup.cache_bits = cache_bits;
+  setup.window_limit = window_limit;
+  code = model_load(folder, &setup, &model);
+  if (code != APP_OKAY) return (int)code;
+  code = session_open(model, &session);
+  if (code == APP_OKAY) code = scout_open(&scout);
+  if (code == APP_OKAY) code = session_prime(session, prompt, prompt_count);
+  if (code == APP_OKAY) code = scout_note(scout, prompt, prompt_count);
+  vocab = model_vocab_count(model);
+  if (span > session_guess_limit(session)) span = session_guess_limit(session);
+  if (span < 1) span = 1;
+  id_value = prompt[prompt_count - 1];
+  while (code == APP_OKAY && made < gen_count) {
+    int want = span - 1, count, take = 0;
+    const float *rows;
+    int32_t after;
+    if (want > gen_count - made - 1) want = gen_count - made - 1;
+    if (want < 0) want = 0;
+    block[0] = id_value;
+    count = 1 + scout_draw(scout, block + 1, want);
+    rounds += 1;
+    if (count == 1) {
+      const float *logits = session_step(session, id_value);
+      if (!logits) { code = APP_FAIL_STATE; break; }
+      id_value = ref_top(logits, vocab);
+      out_ids[made++] = id_value;
+      code = scout_note(scout, &id_value, 1);
+      continue;
+    }
+    rows = session_guess(session, block, count);
+    if (!rows) { code = APP_FAIL_STATE; break; }
+    drawn += count - 1;
+    while (take + 1 < count && ref_top(rows + (size_t)take * vocab, vocab) == block[take + 1]) take += 1;
+    after = ref_top(rows + (size_t)take * vocab, vocab);
+    taken += take;
+    for (int slot = 0; slot <= take && made < gen_count; ++slot) {
+      id_value = slot < take ? block[slot + 1] : after;
+      out_ids[made++] = id_value;
+      if (scout_note(scout, &id_value, 1) != APP_OKAY) code = APP_FAIL_MEMORY;
+    }
+    if (code == APP_OKAY) code = session_guess_keep(session, take + 1);
+  }
+  if (stats_out) {
+    stats_out[0] = rounds;
+    stats_out[1] = drawn;
+    stats_out[2] = taken;
+  }
+  if (scout) scout_close(scout);
+  if (session) session_close(session);
+  model_free(model);
+  return (int)code;
+}
+
 /* One lane's grouped decode attention through the reference's own two jobs
  * (attend_score_band / attend_blend_band, app_core.c:11296-11365), forked over
  * the desk's pool exactly as session_attend_group forks them (11415-11453).

@@ -5,6 +5,7 @@ by oracle/Makefile), run on this repository's seeded synthetic checkpoint.
 
     python tests/golden/make_e2e_golden.py small   # 10 layers, vocab 4096
     python tests/golden/make_e2e_golden.py e2b     # config.json dimensions
+    python tests/golden/make_e2e_golden.py small_guess   # --guess 4, repeating prompt
 
 For each, the checkpoint is written with igl_gemma_write (seed 0) into a
 scratch folder, the prompt is drawn by igllm_amd.engine.prompt_ids, and the
@@ -32,6 +33,9 @@ import oracle_lib  # noqa: E402
 CASES = {
     "small": dict(shape=SMALL, prompt=600, gen=128, window=1024),
     "e2b": dict(shape={}, prompt=2048, gen=256, window=2560),
+    # --guess 4 on a prompt that repeats its first `repeat` ids
+    "small_guess": dict(shape=SMALL, prompt=600, gen=128, window=1024, repeat=128, span=4),
+    "e2b_guess": dict(shape={}, prompt=2048, gen=256, window=2560, repeat=512, span=4),
 }
 
 
@@ -50,16 +54,49 @@ def ref_stream(kind, folder, prompt, gen, window, threads):
     return out, margin, time.time() - t0
 
 
+def ref_guess(kind, folder, prompt, gen, window, threads, span):
+    lib = ctypes.CDLL(oracle_lib.REF_PLAIN_PATH if kind == "plain" else oracle_lib.REF_TUNED_PATH)
+    fn = lib.ref_engine_guess
+    fn.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                   ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    out = np.zeros(gen, np.int32)
+    stats = np.zeros(3, np.int64)
+    t0 = time.time()
+    code = fn(folder.encode(), threads, 8, window, prompt.ctypes.data, prompt.size, gen, span,
+              out.ctypes.data, stats.ctypes.data)
+    if code != 0:
+        raise SystemExit(f"ref_engine_guess({kind}) returned {code}")
+    return out, stats, time.time() - t0
+
+
 def main():
     name = sys.argv[1] if len(sys.argv) > 1 else "small"
     case = CASES[name]
     threads = int(os.environ.get("IGL_THREADS", os.cpu_count() or 4))
     folder = os.path.join(tempfile.gettempdir(), f"igl_gemma_{name}")
     shape = write_gemma(folder, seed=0, **case["shape"])
-    prompt = prompt_ids(case["prompt"], shape.vocab, seed=0)
+    prompt = prompt_ids(case["prompt"], shape.vocab, seed=0, repeat_span=case.get("repeat", 0))
     result = {"case": name, "seed": 0, "prompt_seed": 0, "prompt_count": case["prompt"],
               "gen": case["gen"], "window_limit": case["window"], "cache_bits": 8,
+              "repeat_span": case.get("repeat", 0), "guess_span": case.get("span", 0),
               "shape": {k: getattr(shape, k) for k, _ in shape._fields_}}
+    if case.get("span"):
+        for kind in ("plain", "tuned"):
+            ids, stats, secs = ref_guess(kind, folder, prompt, case["gen"], case["window"], threads,
+                                         case["span"])
+            result[kind] = {"ids": ids.tolist(), "rounds": int(stats[0]), "drawn": int(stats[1]),
+                            "taken": int(stats[2]), "seconds": secs, "threads": threads}
+            print(kind, f"{secs:.1f}s", "rounds", int(stats[0]), "drawn", int(stats[1]),
+                  "taken", int(stats[2]), flush=True)
+        # the same prompt without guessing: the streams must agree
+        ids, margin, secs = ref_stream("plain", folder, prompt, case["gen"], case["window"], threads)
+        result["greedy"] = {"ids": ids.tolist(), "margin": [float(m) for m in margin], "seconds": secs}
+        result["streams_agree"] = result["plain"]["ids"] == result["tuned"]["ids"]
+        result["guess_equals_greedy"] = result["plain"]["ids"] == result["greedy"]["ids"]
+        with open(os.path.join(HERE, f"e2e_{name}.json"), "w") as f:
+            json.dump(result, f, indent=1)
+        print("agree", result["streams_agree"], "guess == greedy", result["guess_equals_greedy"])
+        return
     for kind in ("plain", "tuned"):
         ids, margin, secs = ref_stream(kind, folder, prompt, case["gen"], case["window"], threads)
         result[kind] = {"ids": ids.tolist(), "margin": [float(m) for m in margin], "seconds": secs,

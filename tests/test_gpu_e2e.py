@@ -84,3 +84,54 @@ def test_e2b_greedy_stream_matches_reference(backend, precise):
     # The fast mode primes through binary16 GEMM operands, which moves some
     # cached FP8 key/value bytes by one step; the gaps then move by ~1e-3.
     assert gap <= (2e-3 if precise else 5e-3)
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_small_guess_stream_matches_reference(backend, small_model, graph):
+    """--guess 4 on a prompt that repeats its first 128 ids
+    (tests/golden/e2e_small_guess.json): the engine's blocks (igl_engine_guess /
+    igl_engine_keep) under the product's loop give the reference's stream and
+    the reference's round, proposed and kept counts; every committed id's
+    top-1/top-2 gap, from a block lane or an ordinary step, is the reference
+    greedy run's gap for that id."""
+    from igllm_amd.engine import Scout, guess_loop
+
+    folder, small = small_model
+    fx = load_fixture("small_guess")
+    assert fx["seed"] == small["seed"] and fx["shape"]["vocab"] == small["shape"]["vocab"]
+    prompt = prompt_ids(fx["prompt_count"], fx["shape"]["vocab"], seed=fx["prompt_seed"],
+                        repeat_span=fx["repeat_span"])
+    eng = Engine(backend, folder, window_limit=fx["window_limit"], lane_limit=16, precise=True)
+    gaps, held = [], {}
+    try:
+        eng.set_graph(graph)
+        eng.prime(prompt)
+
+        def step(token):
+            pick, gap = eng.step(token)
+            gaps.append(gap)
+            return pick
+
+        def guess(block):
+            picks, held["gaps"] = eng.guess(block)
+            return picks
+
+        def keep(count):
+            gaps.extend(float(x) for x in held.pop("gaps")[:count])
+            eng.keep(count)
+
+        ids, counts = guess_loop(Scout(eng.lib), prompt, fx["gen"], fx["guess_span"], step, guess,
+                                 keep)
+        fill = eng.fill
+    finally:
+        eng.close()
+    want = np.array(fx["greedy"]["ids"], dtype=np.int32)
+    print("counts", counts, "reference", (fx["plain"]["rounds"], fx["plain"]["drawn"],
+                                          fx["plain"]["taken"]))
+    assert np.array_equal(ids, want)
+    assert counts == (fx["plain"]["rounds"], fx["plain"]["drawn"], fx["plain"]["taken"])
+    # the session holds the prompt and every committed id but the last
+    assert fill == fx["prompt_count"] - 1 + fx["gen"]
+    gap = float(np.max(np.abs(np.array(gaps) - np.array(fx["greedy"]["margin"]))))
+    print("max gap difference", gap)
+    assert len(gaps) == fx["gen"] and gap <= 2e-3
