@@ -34,9 +34,9 @@ LANES = [1, 2, 4, 8]
 COPIES = 48                     # 48 x 10.5 MB per shape: past the 256 MiB MALL
 # HBM bytes per dispatch of the decode GEMV (M=1, 8192x2048), from two rocprofv3
 # --pmc runs of `bench.py --kernel gemv` (profiles/gemv_q4_m1_8192x2048.md):
-# FETCH_SIZE 5191.2 KiB x 2.0 + WRITE_SIZE 32.0 KiB x 1.0, the factors a 256 MiB
+# FETCH_SIZE 5182.1 KiB x 2.0 + WRITE_SIZE 32.0 KiB x 1.0, the factors a 256 MiB
 # device copy gives (profiles/copy_256mib_calibration.md).
-GEMV_M1_TRAFFIC_BYTES = int((5191.2 * 2.0 + 32.0) * 1024)
+GEMV_M1_TRAFFIC_BYTES = int((5182.1 * 2.0 + 32.0) * 1024)
 
 
 def gemv_bytes(N, K, M, group=32):
@@ -464,7 +464,7 @@ def main():
                                "M in {1,2,4,8}, fp32 activations, weights rotated over "
                                f"{COPIES} copies per shape",
                    "step_bytes": step_bytes},
-        "roofline": {"bound": "hbm", "kernel": "gemv_q4_reg_kernel<1,4> 8192x2048 M=1",
+        "roofline": {"bound": "hbm", "kernel": "gemv_q4_dot_kernel<1,4,1,1,true,1> 8192x2048 M=1",
                      "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": GEMV_M1_TRAFFIC_BYTES,

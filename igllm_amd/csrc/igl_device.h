@@ -201,4 +201,147 @@ __device__ __forceinline__ float gelu_near(float x) {
   return x * (t / (t + 1.0f));
 }
 
+// ---- activations as signed base-16 digits (the integer-dot GEMV form) -----
+//
+// A 32-element unit of x is scaled by 2^(P - E), E the frexp exponent of its
+// largest |x| and P = 4 DIG - 2 (v_ldexp_f32: exact at any exponent), and
+// rounded to the nearest integer q (ties to even), so |q| <= 2^P.  q + B,
+// B = 0x888888 cut to DIG hex digits, is then a DIG-digit unsigned number
+// whose digits d_j give q = sum_j (d_j - 8) 16^j, and d_j - 8 as a 4-bit
+// two's complement value is d_j ^ 8.  A dword of codes c (eight of them, low
+// nibble first) xor 0x88888888 is likewise the signed values c - 8, so
+// v_dot8_i32_i4 of it against the dword that holds digit j of the same eight
+// elements is sum (c - 8)(d_j - 8), exactly, and the DIG of them weighted by
+// 16^j give sum (c - 8) q exactly.  The unit's product is that sum, rounded
+// once to float, times 2^(E - P) (ldexp again): the only other rounding is
+// q's, half a unit in the P-th bit below the unit's largest |x|.  x must be
+// finite; a unit of zeros has E = 0 and q = 0.
+
+template <int DIG>
+struct DigitForm {
+  static_assert(DIG == 5 || DIG == 6, "five or six digits");
+  static constexpr int kP = 4 * DIG - 2;
+  static constexpr uint32_t kBias = 0x888888u >> (4 * (6 - DIG));
+  // bits(x 2^(P - E) + 1.5 * 2^23) = 0x4B400000 + q, as |q| <= 2^22
+  static constexpr uint32_t kLess = 0x4B400000u - kBias;
+};
+
+// Digits 0 .. DIG-1 of eight elements that share `scale`: nibble e of d[j] is
+// digit j of element e.  Three rounds of block swaps (halves between rows
+// four apart, bytes two apart, nibbles one apart) transpose the 8 x 8 nibble
+// matrix whose row e is element e's biased q.
+template <int DIG>
+__device__ __forceinline__ void digits_of_eight(const float (&x)[8], int up, uint32_t (&d)[DIG]) {
+  uint32_t v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    v[e] = __float_as_uint(__builtin_amdgcn_ldexpf(x[e], up) + 12582912.0f) - DigitForm<DIG>::kLess;
+  uint32_t w[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    w[e] = __builtin_amdgcn_perm(v[e + 4], v[e], 0x05040100u);      // a.lo, b.lo
+    w[e + 4] = __builtin_amdgcn_perm(v[e + 4], v[e], 0x07060302u);  // a.hi, b.hi
+  }
+  uint32_t z[8];
+#pragma unroll
+  for (int h = 0; h < 8; h += 4)
+#pragma unroll
+    for (int e = h; e < h + 2; ++e) {
+      z[e] = __builtin_amdgcn_perm(w[e + 2], w[e], 0x06020400u);      // a0 b0 a2 b2
+      z[e + 2] = __builtin_amdgcn_perm(w[e + 2], w[e], 0x07030501u);  // a1 b1 a3 b3
+    }
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const uint32_t a = z[e], b = z[e + 1];
+    if (e < DIG) d[e] = ((a & 0x0F0F0F0Fu) | ((b << 4) & 0xF0F0F0F0u)) ^ 0x88888888u;
+    if (e + 1 < DIG) d[e + 1] = (((a >> 4) & 0x0F0F0F0Fu) | (b & 0xF0F0F0F0u)) ^ 0x88888888u;
+  }
+}
+
+// sum_j t[j] 16^j as a float, with one rounding: each |t[j]| <= 32 * 64, so
+// the two halves are exact in 24 bits.
+template <int DIG>
+__device__ __forceinline__ float digit_sum(const int (&t)[DIG]) {
+  const int lo = t[0] + 16 * t[1] + 256 * t[2];
+  int hi = t[3] + 16 * t[4];
+  if constexpr (DIG == 6) hi += 256 * t[5];
+  return __builtin_fmaf((float)hi, 4096.0f, (float)lo);
+}
+
+// Staging x in digit form, for a workgroup of 256 threads.  Eight-element
+// group g of lane m (g < K / 8) is thread (m K / 8 + g) % 256's item
+// (m K / 8 + g) / 256; a thread holds GPT items.  The LDS form: uint4
+// dig[(m DIG + j) units + u] holds digit j of unit u's four dwords of eight
+// elements, and down[m units + u] = E - P.  K % 32 == 0, so the four
+// groups of a unit sit in one quad of threads, and a quad is wholly inside
+// or wholly past the end.
+//
+// The loads are a step of their own so that a kernel issues them before its
+// weight loads: vmcnt retires loads in order, so activations requested after
+// the weights could not be converted until every weight had arrived.
+template <int GPT>
+struct DigitLoads {
+  float x[GPT][8];
+};
+
+// An item past the end stands for the same quarter of the last unit, so a
+// quad past the end recomputes that unit exactly and its LDS writes repeat
+// the owner's values: nothing on the way from the loads to the stores
+// branches, and the compiler's wait counts (exact only in straight-line
+// code) let the conversion start as soon as the activations arrive.
+__device__ __forceinline__ int digit_item(int i, int groups) {
+  const int g = (int)threadIdx.x + 256 * i;
+  return g < groups ? g : groups - 4 + (g & 3);
+}
+
+// VEC: x 16-byte aligned and act_stride % 4 == 0.
+template <int M, int GPT, bool VEC>
+__device__ __forceinline__ void digit_loads(DigitLoads<GPT> &h, const float *act, int act_stride,
+                                            int K) {
+  const int per_lane = K >> 3;
+#pragma unroll
+  for (int i = 0; i < GPT; ++i) {
+    const int g = digit_item(i, M * per_lane);
+    const int m = M == 1 ? 0 : M == 2 ? (g >= per_lane ? 1 : 0) : g / per_lane;
+    const float *src = act + (size_t)m * act_stride + 8 * (g - m * per_lane);
+    if (VEC) {
+      const float4_t p = *reinterpret_cast<const float4_t *>(src);
+      const float4_t q = *reinterpret_cast<const float4_t *>(src + 4);
+      h.x[i][0] = p.x; h.x[i][1] = p.y; h.x[i][2] = p.z; h.x[i][3] = p.w;
+      h.x[i][4] = q.x; h.x[i][5] = q.y; h.x[i][6] = q.z; h.x[i][7] = q.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h.x[i][e] = src[e];
+    }
+  }
+}
+
+// The held groups into LDS; ends with a barrier every thread reaches.
+template <int M, int GPT, int DIG>
+__device__ __forceinline__ void digit_store(const DigitLoads<GPT> &h, int K, uint4_t *dig,
+                                            int *down) {
+  const int units = K >> 5;
+  const int per_lane = K >> 3;
+  uint32_t *base = reinterpret_cast<uint32_t *>(dig);
+#pragma unroll
+  for (int i = 0; i < GPT; ++i) {
+    const int g = digit_item(i, M * per_lane);
+    const int m = M == 1 ? 0 : M == 2 ? (g >= per_lane ? 1 : 0) : g / per_lane;
+    const int gg = g - m * per_lane;
+    float peak = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) peak = fmaxf(peak, fabsf(h.x[i][e]));
+    peak = fmaxf(peak, dpp_move<0xB1>(peak));  // quad_perm [1,0,3,2]
+    peak = fmaxf(peak, dpp_move<0x4E>(peak));  // quad_perm [2,3,0,1]
+    const int E = __builtin_amdgcn_frexp_expf(peak);
+    uint32_t d[DIG];
+    digits_of_eight<DIG>(h.x[i], DigitForm<DIG>::kP - E, d);
+    const int u = gg >> 2, dw = gg & 3;
+#pragma unroll
+    for (int j = 0; j < DIG; ++j) base[((m * DIG + j) * units + u) * 4 + dw] = d[j];
+    if (dw == 0) down[m * units + u] = E - DigitForm<DIG>::kP;
+  }
+  __syncthreads();
+}
+
 }  // namespace igl

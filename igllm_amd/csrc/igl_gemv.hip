@@ -354,6 +354,136 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_reg_kernel(GemvArgs a) {
   }
 }
 
+// ---- the integer-dot form (one and two lanes) ------------------------------
+//
+// The register form's layout (a lane holds one unit of R rows; `ksplit` waves
+// share a row tile), with the unit's product taken on the integer dot path:
+// the workgroup stages x in digit form (stage_digits) while the row loads
+// are in flight, and a lane then spends, per row and unit, four xors and
+// 4 DIG v_dot8_i32_i4 on exact integer sums where the float form spends
+// 32 conversions and 32 FMAs.  y = sum_units gain 2^(E - P) sum (c - 8) q.
+constexpr int kDigits = 6;
+
+__host__ __device__ constexpr size_t gemv_dot_lds_bytes(int M, int units) {
+  return (size_t)M * units * (kDigits * 16 + 4);
+}
+
+template <int M, int R, int UPL, int GPT, bool VEC, int KS>
+__global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
+  extern __shared__ uint4_t lds_dig[];
+  __shared__ float red[4][R][M];
+  constexpr int kTilesPerBlock = 4 / KS;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile = blockIdx.x * kTilesPerBlock + wave / KS;
+  const int ks = wave % KS;
+  const int row0 = tile * R;
+  const int units = a.K >> 5;
+  const int u_end = (units * (ks + 1)) / KS;
+  const int u_first = (units * ks) / KS + lane;
+  uint4_t *dig = lds_dig;
+  int *down = reinterpret_cast<int *>(dig + M * kDigits * units);
+
+  // Activations first, then the weights, all unconditionally: rows and
+  // units past the end reload valid ones and get gain 0, so the arithmetic
+  // needs no branch either (tail rows of a tile are computed, never stored).
+  DigitLoads<GPT> held;
+  digit_loads<M, GPT, VEC>(held, a.act, a.act_stride, a.K);
+  // Gains before codes, and each row's codes in row order: the row loop
+  // below waits for one row at a time.
+  uint4_t w[UPL][R];
+  float s[UPL][R];
+  bool live[UPL];
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    live[j] = row0 < a.N && u_first + kWave * j < u_end;
+    const int u = min(u_first + kWave * j, units - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min(row0 + r, a.N - 1);
+      s[j][r] = a.gains[(size_t)row * (size_t)a.gain_stride + ((unsigned)u >> a.group_shift)];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const int u = min(u_first + kWave * j, units - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min(row0 + r, a.N - 1);
+      w[j][r] = __builtin_nontemporal_load(
+          reinterpret_cast<const uint4_t *>(a.codes + (size_t)row * (size_t)a.row_stride) + u);
+    }
+  }
+  digit_store<M, GPT, kDigits>(held, a.K, dig, down);
+
+  float acc[R][M];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+#pragma unroll
+  for (int uj = 0; uj < UPL; ++uj) {
+    const int u = min(u_first + kWave * uj, units - 1);
+    uint4_t dd[M][kDigits];
+    int shift[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+#pragma unroll
+      for (int j = 0; j < kDigits; ++j) dd[m][j] = dig[(m * kDigits + j) * units + u];
+      shift[m] = down[m * units + u];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint4_t c = w[uj][r] ^ 0x88888888u;
+      const float gain = live[uj] ? s[uj][r] : 0.0f;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        int t[kDigits];
+#pragma unroll
+        for (int j = 0; j < kDigits; ++j) t[j] = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int j = 0; j < kDigits; ++j)
+            t[j] = __builtin_amdgcn_sdot8((int)c[q], (int)dd[m][j][q], t[j], false);
+        acc[r][m] = __builtin_fmaf(gain, __builtin_amdgcn_ldexpf(digit_sum<kDigits>(t), shift[m]),
+                                   acc[r][m]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = wave_sum_to_last(acc[r][m]);
+
+  if (KS == 1) {
+    if (lane == 63) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (row0 + r < a.N)
+#pragma unroll
+          for (int m = 0; m < M; ++m) a.out[(size_t)m * a.out_stride + row0 + r] = acc[r][m];
+    }
+    return;
+  }
+  if (lane == 63) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) red[wave][r][m] = acc[r][m];
+  }
+  __syncthreads();
+  if (ks == 0 && lane < R * M) {
+    const int r = lane / M;
+    const int m = lane - r * M;
+    float total = 0.0f;
+    for (int k = 0; k < KS; ++k) total += red[wave + k][r][m];
+    if (row0 + r < a.N) a.out[(size_t)m * a.out_stride + row0 + r] = total;
+  }
+}
+
 // ---- one activation row against several planes in one launch (decode) -----
 //
 // The register form for one lane and four rows a wave, over up to three planes
@@ -983,6 +1113,51 @@ static hipError_t gemv_mfma_dispatch(const GemvMfmaArgs &a, const GemvMfmaPlan &
   }
 }
 
+template <int M, int R, int UPL, int GPT, int KS>
+static hipError_t gemv_dot_launch_ks(const GemvArgs &a, hipStream_t stream) {
+  const int tiles = (a.N + R - 1) / R;
+  constexpr int kTilesPerBlock = 4 / KS;
+  dim3 grid((tiles + kTilesPerBlock - 1) / kTilesPerBlock);
+  const size_t lds = gemv_dot_lds_bytes(M, a.K >> 5);
+  static size_t lds_granted = 65536;  // launches above 64 KiB ask once
+  if (lds > lds_granted) {
+    hipError_t e =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q4_dot_kernel<M, R, UPL, GPT, true, KS>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    lds_granted = lds;
+  }
+  hipLaunchKernelGGL((gemv_q4_dot_kernel<M, R, UPL, GPT, true, KS>), grid, dim3(kGemvThreads), lds,
+                     stream, a);
+  return hipGetLastError();
+}
+
+template <int M, int R, int UPL, int GPT>
+static hipError_t gemv_dot_launch_gpt(const GemvArgs &a, hipStream_t stream) {
+  switch (a.ksplit) {
+    case 1: return gemv_dot_launch_ks<M, R, UPL, GPT, 1>(a, stream);
+    case 2: return gemv_dot_launch_ks<M, R, UPL, GPT, 2>(a, stream);
+    case 4: return gemv_dot_launch_ks<M, R, UPL, GPT, 4>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Items a thread stages: M K / 8 groups over 256 threads, at most 8.
+constexpr int kDotMaxItems = 8;
+
+// The integer-dot form for M <= 2 lanes with 16-byte aligned activations:
+// M K <= 16384 (a thread stages at most eight groups of eight).
+template <int M, int R, int UPL>
+static hipError_t gemv_dot_launch(const GemvArgs &a, hipStream_t stream) {
+  const int items = (M * (a.K >> 3) + kGemvThreads - 1) / kGemvThreads;
+  if (!a.act_vec) return hipErrorInvalidValue;
+  if (items <= 1) return gemv_dot_launch_gpt<M, R, UPL, 1>(a, stream);
+  if (items <= 2) return gemv_dot_launch_gpt<M, R, UPL, 2>(a, stream);
+  if (items <= 4) return gemv_dot_launch_gpt<M, R, UPL, 4>(a, stream);
+  if (items <= kDotMaxItems) return gemv_dot_launch_gpt<M, R, UPL, kDotMaxItems>(a, stream);
+  return hipErrorInvalidValue;
+}
+
 template <int M, int R, int UPL>
 static hipError_t gemv_reg_launch(const GemvArgs &a, hipStream_t stream) {
   const int tiles = (a.N + R - 1) / R;
@@ -1194,6 +1369,11 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
     a.chunk_cols = K;
     a.out = out;
     a.out_stride = out_stride;
+    if (a.act_vec && lanes * K <= kDotMaxItems * kGemvThreads * 8) {
+      if (upl == 2)
+        return lanes == 1 ? gemv_dot_launch<1, 4, 2>(a, stream) : gemv_dot_launch<2, 4, 2>(a, stream);
+      return lanes == 1 ? gemv_dot_launch<1, 4, 1>(a, stream) : gemv_dot_launch<2, 4, 1>(a, stream);
+    }
     if (upl == 2)
       return lanes == 1 ? gemv_reg_launch<1, 4, 2>(a, stream) : gemv_reg_launch<2, 4, 2>(a, stream);
     return lanes == 1 ? gemv_reg_launch<1, 4, 1>(a, stream) : gemv_reg_launch<2, 4, 1>(a, stream);

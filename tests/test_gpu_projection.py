@@ -92,10 +92,11 @@ def test_gemv_edges(backend, N, K, lanes, group):
     backend.detach(cp)
 
 
-def test_gemv_unaligned_activations(backend):
+@pytest.mark.parametrize("lanes", [1, 3])
+def test_gemv_unaligned_activations(backend, lanes):
     """An activation stride that is not a multiple of four floats takes the
-    scalar staging path."""
-    N, K, lanes = 96, 256, 3
+    scalar staging path (one lane: the float register form)."""
+    N, K = 96, 256
     codes, gains, act = synth_projection(N, K, lanes, seed=9)
     padded = np.zeros((lanes, K + 1), dtype=np.float32)
     padded[:, :K] = act
@@ -107,6 +108,43 @@ def test_gemv_unaligned_activations(backend):
     got = dev_out.get(np.float32, lanes * N).reshape(lanes, N)
     want = ol.oracle_mat_mat(codes, gains, act, K)
     assert rel_err(got, want) <= 1e-3
+    backend.detach(cp)
+
+
+@pytest.mark.parametrize("case", ["zeros", "tiny", "subnormal", "huge", "mixed"])
+@pytest.mark.parametrize("lanes", [1, 2])
+def test_gemv_activation_range(backend, lanes, case):
+    """The one- and two-lane products quantize each 32-element unit of x to 24
+    bits against the unit's largest |x|, scaling by exact powers of two: a
+    unit of zeros, x at 1e-30, subnormal x, x at 1e30, and units mixing 1e-6
+    with 1e3, against the float64 closed form."""
+    print_case(test="activation_range", lanes=lanes, case=case)
+    N, K = 300, 2048
+    codes, gains, act = synth_projection(N, K, lanes, seed=21)
+    act = act.astype(np.float64)
+    if case == "zeros":
+        act[:, 32:96] = 0.0
+        act[:, 200] = 0.0
+    elif case == "tiny":
+        act *= 1e-30
+    elif case == "subnormal":
+        act *= 1e-40
+    elif case == "huge":
+        act *= 1e30
+    else:
+        act[:, 0::2] *= 1e-6
+        act[:, 1::64] *= 1e3
+    act = act.astype(np.float32)
+    cp = backend.attach(make_plane(codes, gains, K))
+    got = run_gemv_dev(backend, cp, act, lanes)
+    vals = ((codes[:, :, None] >> np.array([0, 4], dtype=np.uint8)) & 15).reshape(N, K).astype(np.float64) - 8
+    scale = np.repeat(gains.astype(np.float64), 32, axis=1)
+    want = act.astype(np.float64) @ (vals * scale).T
+    err = rel_err(got, want)
+    print("rel_err", err)
+    assert np.all(np.isfinite(got))
+    # subnormal x: the closed form's own inputs carry only ~17 bits
+    assert err <= (1e-3 if case == "subnormal" else 1e-5)
     backend.detach(cp)
 
 
