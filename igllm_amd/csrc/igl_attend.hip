@@ -54,7 +54,6 @@ struct AttendArgs {
   const int *place_dev;        // when set, lane 0's position is read here instead
   int window;                  // positions a lane sees (0: all from position 0)
   int chunks;                  // workgroup slots per lane in the partial buffers
-  int chunks_per_block;        // 128-position chunks one workgroup walks
   float *final_out;            // when one workgroup covers a lane: the blend, [lanes][q_stride]
   int q_stride;                // floats between lanes of query / blend
   const float *query;          // [lanes][head_count][HEAD]
@@ -100,13 +99,18 @@ __device__ __forceinline__ float xsum32(float v) {
   return lo + hi;
 }
 
-// One workgroup walks CPB consecutive 128-position chunks of one lane.  Each
-// wave owns 32 positions of every chunk and makes two passes over them: the
-// scores of all its chunks first (held in registers) and their peak, then the
-// probabilities against that peak and the blend, so nothing already summed
-// is ever rescaled.  The next chunk's rows are loaded while the current one
-// computes.
-template <int HEAD, int FMT, int CPB>
+// One workgroup takes one 128-position chunk of one lane; each wave owns 32
+// positions of it.  The query, key and value loads all go out first, so the
+// launch pays one memory round trip; then the scores, the wave's softmax
+// against its own peak, and the blend.  The four waves merge in LDS.  A
+// workgroup that covers the lane's whole span writes the blend; otherwise it
+// writes a partial (blend, peak, total) for attend_merge_kernel.
+//
+// (Measured: the last workgroup to finish merging the partials itself, after
+// an agent-scope release/acquire ticket, was slower than the merge launch at
+// every span tried, 15 vs 13 us at a 512 window and 52 vs 29 us at 2300
+// positions of 512 dims: one CU then reads every partial.)
+template <int HEAD, int FMT, bool QVEC>
 __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs a) {
   constexpr int S = HEAD / 32;        // k-steps of the score product
   constexpr int QD = HEAD / 4;        // bytes of a key row one lane group reads
@@ -119,6 +123,8 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
   __shared__ float ps[4][kAttendGroup][kAttendTile];
   __shared__ float wm[4][kAttendGroup];
   __shared__ float wl[4][kAttendGroup];
+  __shared__ float head_peak[kAttendGroup];
+  __shared__ float head_norm[kAttendGroup];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -134,162 +140,156 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
   const int pos = (a.place_dev ? *a.place_dev : a.place0) + lane_id;
   const int span_count = a.window > 0 ? min(pos + 1, a.window) : pos + 1;
   const int place_start = pos - span_count + 1;
-  const int c_first = block * CPB;
-  if (c_first * kAttendChunk >= span_count) return;  // the whole block is past this lane's span
-  const int c_count = min(CPB, (span_count + kAttendChunk - 1) / kAttendChunk - c_first);
+  const int blocks_seen = (span_count + kAttendChunk - 1) / kAttendChunk;
+  if (block >= blocks_seen) return;  // past this lane's span
   const int pc = lane_id * a.chunks + block;
   const size_t kv_off = (size_t)kv * HEAD;
+  const int t0 = block * kAttendChunk + wave * kAttendTile;
+  const bool live = t0 < span_count;
 
-  // ---- query operands: row n is head (n & 7), hi part (n < 8) or lo part.
-  half8_t qa[S];
+  // ---- loads.  Query row n is head (n & 7), floats QD g + 8 s .. + 7.  Key
+  // rows n and n + 16 of the wave's 32, bytes QD g .. QD g + QD - 1 (operand
+  // order); value rows lane / 2, half lane & 1.  Rows past the span repeat
+  // the last one.
+  float qf[S][8];
   {
     const float *q = a.query + (size_t)lane_id * a.q_stride + (size_t)(head0 + (n & 7)) * HEAD + QD * g;
-    const bool lo_part = n >= 8;
 #pragma unroll
-    for (int s = 0; s < S; ++s)
+    for (int s = 0; s < S; ++s) {
+      if (QVEC) {
+        const float4_t u = *reinterpret_cast<const float4_t *>(q + 8 * s);
+        const float4_t v = *reinterpret_cast<const float4_t *>(q + 8 * s + 4);
+        qf[s][0] = u.x; qf[s][1] = u.y; qf[s][2] = u.z; qf[s][3] = u.w;
+        qf[s][4] = v.x; qf[s][5] = v.y; qf[s][6] = v.z; qf[s][7] = v.w;
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float v = q[8 * s + e];
-        const _Float16 hi = (_Float16)v;
-        qa[s][e] = lo_part ? (_Float16)(v - (float)hi) : hi;
+        for (int e = 0; e < 8; ++e) qf[s][e] = q[8 * s + e];
       }
-  }
-
-  // Loads of chunk c for this wave.  Key rows n and n + 16 of the wave's 32,
-  // bytes QD g .. QD g + QD - 1 (operand order); value rows lane / 2, half
-  // lane & 1.  Rows past the span repeat the last one.
-  auto key_rows = [&](int c, uint4_t (&kr)[2][QD / 16]) {
-    const int t0 = (c_first + c) * kAttendChunk + wave * kAttendTile;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int t = min(t0 + n + 16 * j, span_count - 1);
-      const int slot = (place_start + t) % a.cache_span;
-      const uint4_t *row = reinterpret_cast<const uint4_t *>(
-          a.key_store + (size_t)slot * a.kv_width + kv_off + QD * g);
-#pragma unroll
-      for (int q = 0; q < QD / 16; ++q) kr[j][q] = __builtin_nontemporal_load(row + q);
     }
-  };
-  auto value_rows = [&](int c, uint2_t (&vr)[HEAD / 16]) {
-    const int t0 = (c_first + c) * kAttendChunk + wave * kAttendTile;
+  }
+  uint4_t kr[2][QD / 16];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int t = min(t0 + n + 16 * j, span_count - 1);
+    const int slot = (place_start + t) % a.cache_span;
+    const uint4_t *row =
+        reinterpret_cast<const uint4_t *>(a.key_store + (size_t)slot * a.kv_width + kv_off + QD * g);
+#pragma unroll
+    for (int q = 0; q < QD / 16; ++q) kr[j][q] = __builtin_nontemporal_load(row + q);
+  }
+  uint2_t vr[HEAD / 16];
+  {
     const int t = min(t0 + (lane >> 1), span_count - 1);
     const int slot = (place_start + t) % a.cache_span;
     const uint2_t *src = reinterpret_cast<const uint2_t *>(
         a.value_store + (size_t)slot * a.kv_width + kv_off + (lane & 1) * (HEAD / 2));
 #pragma unroll
     for (int q = 0; q < HEAD / 16; ++q) vr[q] = __builtin_nontemporal_load(src + q);
-  };
+  }
 
-  // ---- pass 1: scores.  After the half-wave sum, lane groups 0/2 hold heads
-  // 0-3 and 1/3 heads 4-7 (row r of the group is head 4 (g & 1) + r), for
-  // positions n and n + 16 of the wave's 32.
-  float sc[CPB][2][4];
-  float m_w[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  uint4_t kn[2][QD / 16];
-  key_rows(0, kn);
+  // query operands: the hi part (rows n < 8) or the lo part of each head
+  half8_t qa[S];
+  {
+    const bool lo_part = n >= 8;
 #pragma unroll
-  for (int c = 0; c < CPB; ++c) {
-    if (c < c_count) {
-      uint4_t kc[2][QD / 16];
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = qf[s][e];
+        const _Float16 hi = (_Float16)v;
+        qa[s][e] = lo_part ? (_Float16)(v - (float)hi) : hi;
+      }
+  }
+
+  // ---- scores.  After the half-wave sum, lane groups 0/2 hold heads 0-3 and
+  // 1/3 heads 4-7 (row r of the group is head 4 (g & 1) + r), for positions
+  // n and n + 16 of the wave's 32.
+  float sc[2][4];
+  float m_w[4];
+  {
+    float4_t sacc[2] = {float4_t{0, 0, 0, 0}, float4_t{0, 0, 0, 0}};
+    if (live) {
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int q = 0; q < QD / 16; ++q) kc[j][q] = kn[j][q];
-      if (c + 1 < CPB && c + 1 < c_count) key_rows(c + 1, kn);
-      const int t0 = (c_first + c) * kAttendChunk + wave * kAttendTile;
-      float4_t sacc[2] = {float4_t{0, 0, 0, 0}, float4_t{0, 0, 0, 0}};
-      if (t0 < span_count) {
+        for (int s = 0; s < S; ++s) {
+          const uint4_t w = kr[j][s >> 1];
+          const half8_t kb = (s & 1) ? decode8<FMT>(w[2], w[3]) : decode8<FMT>(w[0], w[1]);
+          sacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kb, sacc[j], 0, 0, 0);
+        }
+    }
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int s = 0; s < S; ++s) {
-            const uint4_t w = kc[j][s >> 1];
-            const half8_t kb = (s & 1) ? decode8<FMT>(w[2], w[3]) : decode8<FMT>(w[0], w[1]);
-            sacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kb, sacc[j], 0, 0, 0);
-          }
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float s0 = xsum32(sacc[0][r]);
-        float s1 = xsum32(sacc[1][r]);
-        s0 = (t0 + n < span_count) ? s0 * a.key_scale : -INFINITY;
-        s1 = (t0 + n + 16 < span_count) ? s1 * a.key_scale : -INFINITY;
-        sc[c][0][r] = s0;
-        sc[c][1][r] = s1;
-        m_w[r] = fmaxf(m_w[r], row16_max(fmaxf(s0, s1)));
-      }
+    for (int r = 0; r < 4; ++r) {
+      float s0 = xsum32(sacc[0][r]);
+      float s1 = xsum32(sacc[1][r]);
+      s0 = (t0 + n < span_count) ? s0 * a.key_scale : -INFINITY;
+      s1 = (t0 + n + 16 < span_count) ? s1 * a.key_scale : -INFINITY;
+      sc[0][r] = s0;
+      sc[1][r] = s1;
+      m_w[r] = row16_max(fmaxf(s0, s1));
     }
   }
 
-  // ---- pass 2: probabilities against the wave's peak; the blend with
-  // A = probabilities (row n: head n & 7, hi/lo), k = positions 8g..8g+7.
-  float l_w[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  // ---- probabilities against the wave's peak; the blend with A =
+  // probabilities (row n: head n & 7, hi/lo), k = positions 8g .. 8g+7.
+  float l_w[4];
   float4_t o[TILES];
 #pragma unroll
   for (int t = 0; t < TILES; ++t) o[t] = float4_t{0, 0, 0, 0};
   uint8_t *vw = vs + wave * kWaveV;
-  uint2_t vn[HEAD / 16];
-  value_rows(0, vn);
+  {
+    float p[2][4];
 #pragma unroll
-  for (int c = 0; c < CPB; ++c) {
-    if (c < c_count) {
-      uint2_t vc[HEAD / 16];
-#pragma unroll
-      for (int q = 0; q < HEAD / 16; ++q) vc[q] = vn[q];
-      if (c + 1 < CPB && c + 1 < c_count) value_rows(c + 1, vn);
-      const int t0 = (c_first + c) * kAttendChunk + wave * kAttendTile;
-      const bool live = t0 < span_count;
-      float p[2][4];
+    for (int r = 0; r < 4; ++r) {
+      p[0][r] = live ? __expf(sc[0][r] - m_w[r]) : 0.0f;
+      p[1][r] = live ? __expf(sc[1][r] - m_w[r]) : 0.0f;
+      l_w[r] = row16_sum(p[0][r] + p[1][r]);
+    }
+    if (g < 2) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        p[0][r] = live ? __expf(sc[c][0][r] - m_w[r]) : 0.0f;
-        p[1][r] = live ? __expf(sc[c][1][r] - m_w[r]) : 0.0f;
-        l_w[r] += row16_sum(p[0][r] + p[1][r]);
+        ps[wave][4 * g + r][n] = p[0][r];
+        ps[wave][4 * g + r][n + 16] = p[1][r];
       }
-      if (g < 2) {
+    }
+    if (live) {
+      uint2_t *dst = reinterpret_cast<uint2_t *>(vw + (lane >> 1) * VPITCH + (lane & 1) * (HEAD / 2));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          ps[wave][4 * g + r][n] = p[0][r];
-          ps[wave][4 * g + r][n + 16] = p[1][r];
+      for (int q = 0; q < HEAD / 16; ++q) dst[q] = vr[q];
+    }
+    // Only this wave's rows of `ps` and `vs` are read below: a wave barrier.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (live) {
+      half8_t pa;
+      {
+        const float *src = &ps[wave][n & 7][8 * g];
+        const bool lo_part = n >= 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float v = src[e];
+          const _Float16 hi = (_Float16)v;
+          pa[e] = lo_part ? (_Float16)(v - (float)hi) : hi;
         }
       }
-      if (live) {
-        uint2_t *dst = reinterpret_cast<uint2_t *>(vw + (lane >> 1) * VPITCH + (lane & 1) * (HEAD / 2));
 #pragma unroll
-        for (int q = 0; q < HEAD / 16; ++q) dst[q] = vc[q];
-      }
-      __syncthreads();
-      if (live) {
-        half8_t pa;
-        {
-          const float *src = &ps[wave][n & 7][8 * g];
-          const bool lo_part = n >= 8;
+      for (int qd = 0; qd < QUADS; ++qd) {
+        uint32_t dw[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float v = src[e];
-            const _Float16 hi = (_Float16)v;
-            pa[e] = lo_part ? (_Float16)(v - (float)hi) : hi;
-          }
-        }
+        for (int e = 0; e < 8; ++e)
+          dw[e] = *reinterpret_cast<const uint32_t *>(vw + (8 * g + e) * VPITCH + 64 * qd + 4 * n);
 #pragma unroll
-        for (int qd = 0; qd < QUADS; ++qd) {
-          uint32_t dw[8];
+        for (int t = 0; t < 4; ++t) {
+          uint32_t w[4];
+          const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + t) << 16) | (uint32_t)t;
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            dw[e] = *reinterpret_cast<const uint32_t *>(vw + (8 * g + e) * VPITCH + 64 * qd + 4 * n);
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            uint32_t w[4];
-            const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + t) << 16) | (uint32_t)t;
-#pragma unroll
-            for (int pr = 0; pr < 4; ++pr)
-              w[pr] = decode_pair<FMT>(__builtin_amdgcn_perm(dw[2 * pr + 1], dw[2 * pr], sel));
-            o[4 * qd + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, __builtin_bit_cast(half8_t, w),
-                                                                   o[4 * qd + t], 0, 0, 0);
-          }
+          for (int pr = 0; pr < 4; ++pr)
+            w[pr] = decode_pair<FMT>(__builtin_amdgcn_perm(dw[2 * pr + 1], dw[2 * pr], sel));
+          o[4 * qd + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, __builtin_bit_cast(half8_t, w),
+                                                                 o[4 * qd + t], 0, 0, 0);
         }
       }
-      __syncthreads();  // the value tile and probabilities are free for the next chunk
     }
   }
   // hi + lo rows
@@ -306,14 +306,24 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
   }
 
   // ---- merge the four waves: scale each by e^(m_w - M) per head.
-  __syncthreads();  // wm, wl written; vs is reused as float[4][8][HEAD]
+  __syncthreads();  // wm, wl written and every wave done with vs, reused as float[4][8][HEAD]
+  if (tid < kAttendGroup) {
+    const int h = tid;
+    const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      if (wm[w][h] != -INFINITY) L += wl[w][h] * __expf(wm[w][h] - M);
+    head_peak[h] = M;
+    head_norm[h] = L;
+  }
   float *ob = reinterpret_cast<float *>(vs);
   {
     float scale[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int h = 4 * (g & 1) + r;
-      float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+      const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
       scale[r] = m_w[r] != -INFINITY ? __expf(m_w[r] - M) : 0.0f;
     }
     if (g < 2) {
@@ -333,11 +343,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
     for (int i = tid; i < kAttendGroup * HEAD; i += kAttendThreads) {
       const int h = i / HEAD;
       const int d = i - h * HEAD;
-      const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
-      float L = 0.0f;
-#pragma unroll
-      for (int w = 0; w < 4; ++w)
-        if (wm[w][h] != -INFINITY) L += wl[w][h] * __expf(wm[w][h] - M);
+      const float L = head_norm[h];
       const float v = ((ob[(0 * kAttendGroup + h) * HEAD + d] + ob[(1 * kAttendGroup + h) * HEAD + d]) +
                        ob[(2 * kAttendGroup + h) * HEAD + d]) + ob[(3 * kAttendGroup + h) * HEAD + d];
       out[(size_t)h * HEAD + d] = L > 0.0f ? v * a.value_scale * (1.0f / L) : 0.0f;
@@ -352,14 +358,8 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
     a.part_out[((size_t)pc * a.head_count + head0 + h) * HEAD + d] = v * a.value_scale;
   }
   if (tid < kAttendGroup) {
-    const int h = tid;
-    const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
-    float L = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w)
-      if (wm[w][h] != -INFINITY) L += wl[w][h] * __expf(wm[w][h] - M);
-    a.part_peak[(size_t)pc * a.head_count + head0 + h] = M;
-    a.part_total[(size_t)pc * a.head_count + head0 + h] = L;
+    a.part_peak[(size_t)pc * a.head_count + head0 + tid] = head_peak[tid];
+    a.part_total[(size_t)pc * a.head_count + head0 + tid] = head_norm[tid];
   }
 }
 
@@ -368,7 +368,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
 __global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out_all,
                                                            const float *part_peak_all,
                                                            const float *part_total_all,
-                                                           int chunk_slots, int chunks_per_block,
+                                                           int chunk_slots,
                                                            int place0, const int *place_dev,
                                                            int window, int head_count,
                                                            int head_size, float *blend_all,
@@ -380,7 +380,7 @@ __global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out
   const int pos = (place_dev ? *place_dev : place0) + lane;
   const int span = window > 0 ? min(pos + 1, window) : pos + 1;
   // the workgroups that saw part of this lane's span
-  const int chunks = ((span + kAttendChunk - 1) / kAttendChunk + chunks_per_block - 1) / chunks_per_block;
+  const int chunks = (span + kAttendChunk - 1) / kAttendChunk;
   const size_t base = (size_t)lane * chunk_slots;
   const float *part_out = part_out_all + base * head_count * head_size;
   const float *part_peak = part_peak_all + base * head_count;
@@ -436,20 +436,16 @@ static int attend_max_span(int place0, int window, int lanes) {
   return window > 0 ? (last < window ? last : window) : last;
 }
 
-// Chunks a workgroup walks (the kernel takes 1 or 4); a workgroup that covers
-// a lane's whole span writes the blend itself, with no merge launch.
-static int attend_chunks_per_block(int lanes, int head_size) {
-  // Measured on a 512-position window: four parallel workgroups and the merge
-  // (16 us) beat one workgroup walking four chunks (26 us), so one chunk each.
-  (void)lanes;
-  (void)head_size;
-  return 1;
+static int attend_blocks(int place0, int window, int lanes) {
+  return (attend_max_span(place0, window, lanes) + kAttendChunk - 1) / kAttendChunk;
 }
 
-static int attend_blocks(int place0, int window, int lanes, int head_size) {
-  const int chunks = (attend_max_span(place0, window, lanes) + kAttendChunk - 1) / kAttendChunk;
-  const int cpb = attend_chunks_per_block(lanes, head_size);
-  return (chunks + cpb - 1) / cpb;
+template <int HEAD, int FMT>
+static void attend_launch(const AttendArgs &a, dim3 grid, bool qvec, hipStream_t stream) {
+  if (qvec)
+    hipLaunchKernelGGL((attend_mfma_kernel<HEAD, FMT, true>), grid, dim3(kAttendThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((attend_mfma_kernel<HEAD, FMT, false>), grid, dim3(kAttendThreads), 0, stream, a);
 }
 
 // `lanes` query lanes at positions place0 .. place0 + lanes - 1, each seeing
@@ -466,7 +462,7 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
                                         int window, int lanes, float score_scale,
                                         float *blend_out, float *work, hipStream_t stream) {
   AttendArgs a;
-  const int chunks = attend_blocks(place0, window, lanes, head_size);  // workgroups a lane
+  const int chunks = attend_blocks(place0, window, lanes);  // workgroups a lane
   const int head_count = kv_count * group_share;
   if (group_share != kAttendGroup || lanes < 1) return hipErrorInvalidValue;
   a.key_store = key_store;
@@ -477,7 +473,6 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
   a.place_dev = place_dev;
   a.window = window;
   a.chunks = chunks;
-  a.chunks_per_block = attend_chunks_per_block(lanes, head_size);
   a.final_out = chunks == 1 ? blend_out : nullptr;
   a.q_stride = q_stride;
   a.query = query;
@@ -491,33 +486,28 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
   a.part_peak = work + slots * head_count * head_size;
   a.part_total = a.part_peak + slots * head_count;
   dim3 grid(chunks, kv_count, lanes);
-  const int four = a.chunks_per_block == 4;
-  if (head_size == 256 && fmt == 0 && four)
-    hipLaunchKernelGGL((attend_mfma_kernel<256, 0, 4>), grid, dim3(kAttendThreads), 0, stream, a);
-  else if (head_size == 256 && fmt == 1 && four)
-    hipLaunchKernelGGL((attend_mfma_kernel<256, 1, 4>), grid, dim3(kAttendThreads), 0, stream, a);
-  else if (head_size == 256 && fmt == 0)
-    hipLaunchKernelGGL((attend_mfma_kernel<256, 0, 1>), grid, dim3(kAttendThreads), 0, stream, a);
+  const bool qvec = (((uintptr_t)query) & 15u) == 0 && (q_stride & 3) == 0;
+  if (head_size == 256 && fmt == 0)
+    attend_launch<256, 0>(a, grid, qvec, stream);
   else if (head_size == 256 && fmt == 1)
-    hipLaunchKernelGGL((attend_mfma_kernel<256, 1, 1>), grid, dim3(kAttendThreads), 0, stream, a);
+    attend_launch<256, 1>(a, grid, qvec, stream);
   else if (head_size == 512 && fmt == 0)
-    hipLaunchKernelGGL((attend_mfma_kernel<512, 0, 1>), grid, dim3(kAttendThreads), 0, stream, a);
+    attend_launch<512, 0>(a, grid, qvec, stream);
   else if (head_size == 512 && fmt == 1)
-    hipLaunchKernelGGL((attend_mfma_kernel<512, 1, 1>), grid, dim3(kAttendThreads), 0, stream, a);
+    attend_launch<512, 1>(a, grid, qvec, stream);
   else
     return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || chunks == 1) return e;
   hipLaunchKernelGGL(attend_merge_kernel, dim3(head_count, lanes), dim3(256),
                      chunks * sizeof(float), stream, a.part_out, a.part_peak, a.part_total, chunks,
-                     a.chunks_per_block, place0, place_dev, window, head_count, head_size,
-                     blend_out, q_stride);
+                     place0, place_dev, window, head_count, head_size, blend_out, q_stride);
   return hipGetLastError();
 }
 
 // Floats of workspace igl_launch_attend needs for the same arguments.
 extern "C" size_t igl_attend_work_floats(int place0, int window, int lanes, int head_count,
                                          int head_size) {
-  const size_t blocks = (size_t)attend_blocks(place0, window, lanes, head_size);
+  const size_t blocks = (size_t)attend_blocks(place0, window, lanes);
   return (size_t)lanes * blocks * (size_t)head_count * ((size_t)head_size + 2);
 }

@@ -316,30 +316,53 @@ __device__ __forceinline__ void digit_loads(DigitLoads<GPT> &h, const float *act
   }
 }
 
+// One eight-element group (lane m, group gg of K / 8) into LDS.  The four
+// threads of a quad hold one unit's four groups and all four must run it.
+template <int DIG>
+__device__ __forceinline__ void digit_group_store(const float (&x)[8], int m, int gg, int units,
+                                                  uint4_t *dig, int *down) {
+  float peak = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) peak = fmaxf(peak, fabsf(x[e]));
+  peak = fmaxf(peak, dpp_move<0xB1>(peak));  // quad_perm [1,0,3,2]
+  peak = fmaxf(peak, dpp_move<0x4E>(peak));  // quad_perm [2,3,0,1]
+  const int E = __builtin_amdgcn_frexp_expf(peak);
+  uint32_t d[DIG];
+  digits_of_eight<DIG>(x, DigitForm<DIG>::kP - E, d);
+  const int u = gg >> 2, dw = gg & 3;
+  uint32_t *base = reinterpret_cast<uint32_t *>(dig);
+#pragma unroll
+  for (int j = 0; j < DIG; ++j) base[((m * DIG + j) * units + u) * 4 + dw] = d[j];
+  if (dw == 0) down[m * units + u] = E - DigitForm<DIG>::kP;
+}
+
 // The held groups into LDS; ends with a barrier every thread reaches.
 template <int M, int GPT, int DIG>
 __device__ __forceinline__ void digit_store(const DigitLoads<GPT> &h, int K, uint4_t *dig,
                                             int *down) {
   const int units = K >> 5;
   const int per_lane = K >> 3;
-  uint32_t *base = reinterpret_cast<uint32_t *>(dig);
 #pragma unroll
   for (int i = 0; i < GPT; ++i) {
     const int g = digit_item(i, M * per_lane);
     const int m = M == 1 ? 0 : M == 2 ? (g >= per_lane ? 1 : 0) : g / per_lane;
-    const int gg = g - m * per_lane;
-    float peak = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) peak = fmaxf(peak, fabsf(h.x[i][e]));
-    peak = fmaxf(peak, dpp_move<0xB1>(peak));  // quad_perm [1,0,3,2]
-    peak = fmaxf(peak, dpp_move<0x4E>(peak));  // quad_perm [2,3,0,1]
-    const int E = __builtin_amdgcn_frexp_expf(peak);
-    uint32_t d[DIG];
-    digits_of_eight<DIG>(h.x[i], DigitForm<DIG>::kP - E, d);
-    const int u = gg >> 2, dw = gg & 3;
-#pragma unroll
-    for (int j = 0; j < DIG; ++j) base[((m * DIG + j) * units + u) * 4 + dw] = d[j];
-    if (dw == 0) down[m * units + u] = E - DigitForm<DIG>::kP;
+    digit_group_store<DIG>(h.x[i], m, g - m * per_lane, units, dig, down);
+  }
+  __syncthreads();
+}
+
+// One lane of x already in LDS (`xs`, K floats, 16-byte aligned) into digit
+// form; ends with a barrier every thread reaches.
+template <int DIG>
+__device__ __forceinline__ void digit_store_lds(const float *xs, int K, uint4_t *dig, int *down) {
+  const int units = K >> 5;
+  const int groups = K >> 3;
+  for (int i = 0; i * 256 < groups; ++i) {
+    const int g = digit_item(i, groups);
+    const float4_t p = *reinterpret_cast<const float4_t *>(xs + 8 * g);
+    const float4_t q = *reinterpret_cast<const float4_t *>(xs + 8 * g + 4);
+    const float x[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
+    digit_group_store<DIG>(x, 0, g, units, dig, down);
   }
   __syncthreads();
 }

@@ -589,7 +589,8 @@ void igl_engine_close(igl_engine *e) {
   igl_plane_detach(e->desk, &e->head);
   if (e->graph_ready) (void)hipGraphExecDestroy(e->graph);
   {
-    void *bufs[] = {e->payload_dev, e->ctl_dev, e->attend_work, e->state_buf[0], e->state_buf[1], e->scrap, e->lift, e->q,
+    void *bufs[] = {e->payload_dev, e->ctl_dev, e->attend_work, e->state_buf[0],
+                    e->state_buf[1], e->scrap, e->lift, e->q,
                     e->blend, e->k, e->v, e->gate, e->rise, e->ple_seed, e->ple_room, e->logits,
                     e->pick_work, e->pick_dev, e->steps_dev[0], e->steps_dev[1]};
     for (size_t j = 0; j < sizeof(bufs) / sizeof(bufs[0]); ++j)

@@ -44,6 +44,7 @@ struct GemvArgs {
   int K;                  // columns of the whole plane
   int chunk_cols;         // columns per grid K-chunk (blockIdx.y)
   int ksplit;             // waves of a workgroup sharing one row tile: 1, 2 or 4
+  int ks_log;             // log2(ksplit)
   float unit_bias;        // 16 + code_bias
   int act_vec;            // activations 16-byte aligned with act_stride % 4 == 0
 };
@@ -368,20 +369,21 @@ __host__ __device__ constexpr size_t gemv_dot_lds_bytes(int M, int units) {
   return (size_t)M * units * (kDigits * 16 + 4);
 }
 
-template <int M, int R, int UPL, int GPT, bool VEC, int KS>
+template <int M, int R, int UPL, int GPT>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
   extern __shared__ uint4_t lds_dig[];
   __shared__ float red[4][R][M];
-  constexpr int kTilesPerBlock = 4 / KS;
+  // wave-uniform indices in scalar registers; ksplit a power of two
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tile = blockIdx.x * kTilesPerBlock + wave / KS;
-  const int ks = wave % KS;
+  const int ks_log = __builtin_amdgcn_readfirstlane(a.ks_log);
+  const int tile = blockIdx.x * (4 >> ks_log) + (wave >> ks_log);
+  const int ks = wave & ((1 << ks_log) - 1);
   const int row0 = tile * R;
   const int units = a.K >> 5;
-  const int u_end = (units * (ks + 1)) / KS;
-  const int u_first = (units * ks) / KS + lane;
+  const int u_end = (units * (ks + 1)) >> ks_log;
+  const int u_first = ((units * ks) >> ks_log) + lane;
   uint4_t *dig = lds_dig;
   int *down = reinterpret_cast<int *>(dig + M * kDigits * units);
 
@@ -389,7 +391,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
   // units past the end reload valid ones and get gain 0, so the arithmetic
   // needs no branch either (tail rows of a tile are computed, never stored).
   DigitLoads<GPT> held;
-  digit_loads<M, GPT, VEC>(held, a.act, a.act_stride, a.K);
+  digit_loads<M, GPT, true>(held, a.act, a.act_stride, a.K);
   // Gains before codes, and each row's codes in row order: the row loop
   // below waits for one row at a time.
   uint4_t w[UPL][R];
@@ -425,30 +427,62 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
 #pragma unroll
   for (int uj = 0; uj < UPL; ++uj) {
     const int u = min(u_first + kWave * uj, units - 1);
-    uint4_t dd[M][kDigits];
-    int shift[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-#pragma unroll
-      for (int j = 0; j < kDigits; ++j) dd[m][j] = dig[(m * kDigits + j) * units + u];
-      shift[m] = down[m * units + u];
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const uint4_t c = w[uj][r] ^ 0x88888888u;
-      const float gain = live[uj] ? s[uj][r] : 0.0f;
+    if constexpr (M <= 2) {
+      // every lane's digits held across the rows; a row waits for its own codes
+      uint4_t dd[M][kDigits];
+      int shift[M];
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        int t[kDigits];
 #pragma unroll
-        for (int j = 0; j < kDigits; ++j) t[j] = 0;
+        for (int j = 0; j < kDigits; ++j) dd[m][j] = dig[(m * kDigits + j) * units + u];
+        shift[m] = down[m * units + u];
+      }
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+      for (int r = 0; r < R; ++r) {
+        const uint4_t c = w[uj][r] ^ 0x88888888u;
+        const float gain = live[uj] ? s[uj][r] : 0.0f;
 #pragma unroll
-          for (int j = 0; j < kDigits; ++j)
-            t[j] = __builtin_amdgcn_sdot8((int)c[q], (int)dd[m][j][q], t[j], false);
-        acc[r][m] = __builtin_fmaf(gain, __builtin_amdgcn_ldexpf(digit_sum<kDigits>(t), shift[m]),
-                                   acc[r][m]);
+        for (int m = 0; m < M; ++m) {
+          int t[kDigits];
+#pragma unroll
+          for (int j = 0; j < kDigits; ++j) t[j] = 0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < kDigits; ++j)
+              t[j] = __builtin_amdgcn_sdot8((int)c[q], (int)dd[m][j][q], t[j], false);
+          acc[r][m] = __builtin_fmaf(gain, __builtin_amdgcn_ldexpf(digit_sum<kDigits>(t), shift[m]),
+                                     acc[r][m]);
+        }
+      }
+    } else {
+      // one lane's digits at a time
+      uint4_t c[R];
+      float gain[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        c[r] = w[uj][r] ^ 0x88888888u;
+        gain[r] = live[uj] ? s[uj][r] : 0.0f;
+      }
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        uint4_t dd[kDigits];
+#pragma unroll
+        for (int j = 0; j < kDigits; ++j) dd[j] = dig[(m * kDigits + j) * units + u];
+        const int shift = down[m * units + u];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          int t[kDigits];
+#pragma unroll
+          for (int j = 0; j < kDigits; ++j) t[j] = 0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < kDigits; ++j)
+              t[j] = __builtin_amdgcn_sdot8((int)c[r][q], (int)dd[j][q], t[j], false);
+          acc[r][m] = __builtin_fmaf(gain[r], __builtin_amdgcn_ldexpf(digit_sum<kDigits>(t), shift),
+                                     acc[r][m]);
+        }
       }
     }
   }
@@ -458,7 +492,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[r][m] = wave_sum_to_last(acc[r][m]);
 
-  if (KS == 1) {
+  if (ks_log == 0) {
     if (lane == 63) {
 #pragma unroll
       for (int r = 0; r < R; ++r)
@@ -479,7 +513,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
     const int r = lane / M;
     const int m = lane - r * M;
     float total = 0.0f;
-    for (int k = 0; k < KS; ++k) total += red[wave + k][r][m];
+    for (int k = 0; k < (1 << ks_log); ++k) total += red[wave + k][r][m];
     if (row0 + r < a.N) a.out[(size_t)m * a.out_stride + row0 + r] = total;
   }
 }
@@ -532,88 +566,117 @@ struct GemvGroupArgs {
   float eps;
 };
 
-// The update above for K <= 256 HELD, into `xs` (K floats of LDS).  Thread t
-// holds elements t + 256 k, as norm_add_kernel does.
+// The update above for K <= 256 HELD, into `xs` (K floats of LDS), in two
+// steps so that a kernel can issue the loads ahead of its weight loads.
+// Thread t holds elements t + 256 k, as norm_add_kernel does.  Every load is
+// issued: an absent vector reads state_in in its place and elements past K
+// reread element K - 1, and the values are then masked.
 template <int HELD>
-__device__ __forceinline__ void group_prologue(const GemvGroupArgs &a, float *xs, double *red) {
+struct PrologueLoads {
+  float sv[HELD], lv[HELD], gv[HELD], nv[HELD];
+};
+
+template <int HELD>
+__device__ __forceinline__ void prologue_loads(const GemvGroupArgs &a, PrologueLoads<HELD> &p) {
+  const float *lift = a.lift ? a.lift : a.state_in;
+  const float *lift_gain = a.lift ? a.lift_gain : a.state_in;
+  const float *norm_gain = a.norm_gain ? a.norm_gain : a.state_in;
+#pragma unroll
+  for (int k = 0; k < HELD; ++k) {
+    const int i = min((int)threadIdx.x + 256 * k, a.K - 1);
+    p.sv[k] = a.state_in[i];
+    p.lv[k] = lift[i];
+    p.gv[k] = lift_gain[i];
+    p.nv[k] = norm_gain[i];
+  }
+}
+
+// Branch-free up to the stores (both reductions always run, absent vectors
+// are masked), so that the compiler keeps the loads where they were issued.
+template <int HELD>
+__device__ __forceinline__ void group_prologue(const GemvGroupArgs &a, const PrologueLoads<HELD> &p,
+                                               float *xs, double *red) {
   constexpr int kHeld = HELD;
   const int n = a.K;
+  const bool lift = a.lift != nullptr;
+  const bool normed = a.norm_gain != nullptr;
   float sv[kHeld], lv[kHeld], gv[kHeld], nv[kHeld];
 #pragma unroll
   for (int k = 0; k < kHeld; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    const bool in = i < n;
-    sv[k] = in ? a.state_in[i] : 0.0f;
-    lv[k] = in && a.lift ? a.lift[i] : 0.0f;
-    gv[k] = in && a.lift ? a.lift_gain[i] : 0.0f;
-    nv[k] = in && a.norm_gain ? a.norm_gain[i] : 0.0f;
+    const bool in = (int)threadIdx.x + 256 * k < n;
+    sv[k] = in ? p.sv[k] : 0.0f;
+    lv[k] = in && lift ? p.lv[k] : 0.0f;
+    gv[k] = in && lift ? p.gv[k] : 0.0f;
+    nv[k] = in && normed ? p.nv[k] : 0.0f;
   }
-  if (a.lift) {
-    double acc = 0.0;
+  double acc = 0.0;
 #pragma unroll
-    for (int k = 0; k < kHeld; ++k) acc += (double)lv[k] * (double)lv[k];
-    const float shrink = rms_shrink(block_sum_f64(acc, red), n, a.eps);
+  for (int k = 0; k < kHeld; ++k) acc += (double)lv[k] * (double)lv[k];
+  const float shrink = rms_shrink(block_sum_f64(acc, red), n, a.eps);
 #pragma unroll
-    for (int k = 0; k < kHeld; ++k) {
-      const float normed = lv[k] * shrink * gv[k];
-      float sum = sv[k] + normed;
-      if (a.apply_scale) sum *= a.scale;
-      sv[k] = sum;
-    }
-    if (blockIdx.x == 0) {
-#pragma unroll
-      for (int k = 0; k < kHeld; ++k) {
-        const int i = threadIdx.x + 256 * k;
-        if (i < n) a.state_out[i] = sv[k];
-      }
-    }
+  for (int k = 0; k < kHeld; ++k) {
+    float sum = sv[k] + lv[k] * shrink * gv[k];
+    if (a.apply_scale) sum *= a.scale;
+    sv[k] = lift ? sum : sv[k];
   }
-  float shrink2 = 1.0f;
-  if (a.norm_gain) {
-    double acc2 = 0.0;
+  if (lift && blockIdx.x == 0) {
 #pragma unroll
     for (int k = 0; k < kHeld; ++k) {
       const int i = threadIdx.x + 256 * k;
-      if (i < n) acc2 += (double)sv[k] * (double)sv[k];
+      if (i < n) a.state_out[i] = sv[k];
     }
-    shrink2 = rms_shrink(block_sum_f64(acc2, red), n, a.eps);
   }
+  double acc2 = 0.0;
+#pragma unroll
+  for (int k = 0; k < kHeld; ++k) acc2 += (double)sv[k] * (double)sv[k];
+  const float shrink2 = rms_shrink(block_sum_f64(acc2, red), n, a.eps);
 #pragma unroll
   for (int k = 0; k < kHeld; ++k) {
     const int i = threadIdx.x + 256 * k;
-    if (i < n) xs[i] = a.norm_gain ? sv[k] * shrink2 * nv[k] : sv[k];
+    if (i < n) xs[i] = normed ? sv[k] * shrink2 * nv[k] : sv[k];
   }
   __syncthreads();
 }
 
+// Digit-form LDS of the grouped launch: K <= 8192.
+constexpr int kGroupMaxUnits = 256;
+
 // PRO: 0, or the elements a thread holds in the prologue (K <= 256 PRO).
-template <int MODE, int PRO>
+// GPT (PRO 0): the eight-element groups of x a thread stages, K <= 2048 GPT.
+// Each row's sum is formed as gemv_q4_dot_kernel forms it.
+template <int MODE, int PRO, int GPT, int KS>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupArgs a) {
   constexpr int R = 4;
+  constexpr int kTilesPerBlock = 4 / KS;
+  constexpr int kItems = GPT;
   __shared__ float red[4][R];
   __shared__ double pro_red[16];
   __shared__ __attribute__((aligned(16))) float xs[PRO ? 256 * PRO : 4];
+  __shared__ uint4_t dig[kDigits * kGroupMaxUnits];
+  __shared__ int down[kGroupMaxUnits];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int tiles_per_block = 4 / a.ksplit;
-  const int tile = blockIdx.x * tiles_per_block + wave / a.ksplit;
-  const int ks = wave % a.ksplit;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile = blockIdx.x * kTilesPerBlock + wave / KS;
+  const int ks = wave % KS;
   const int units = a.K >> 5;
-  const int u = (units * ks) / a.ksplit + lane;
-  const bool has = tile < a.tiles && u < (units * (ks + 1)) / a.ksplit;
+  const int u_raw = (units * ks) / KS + lane;
+  const bool has = tile < a.tiles && u_raw < (units * (ks + 1)) / KS;
+  const int u = min(u_raw, units - 1);
 
-  // Row r of the tile: which plane, which row of it.
+  // Row r of the tile: which plane, which row of it (tiles past the end
+  // reread the last row; their sums are dropped).
+  const int tile_c = min(tile, a.tiles - 1);
   int plane[R], prow[R];
   if (MODE == GEMV_GELU_PAIR) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       plane[r] = r >> 1;
-      prow[r] = min(2 * tile + (r & 1), a.rows[0] - 1);
+      prow[r] = min(2 * tile_c + (r & 1), a.rows[0] - 1);
     }
   } else {
     int seg = 0, first = 0;
-    const int row0 = tile * R;
+    const int row0 = tile_c * R;
     if (a.segments > 1 && row0 >= a.rows[0]) { seg = 1; first = a.rows[0]; }
     if (a.segments > 2 && row0 >= a.rows[0] + a.rows[1]) { seg = 2; first = a.rows[0] + a.rows[1]; }
 #pragma unroll
@@ -623,78 +686,61 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
     }
   }
 
-  uint4_t w[R];
+  // The activation side first (the prologue's vectors, or x itself), then the
+  // weights, gains before codes: vmcnt retires loads in order, so the block
+  // forms x while the weights are in flight, and each row waits only for its
+  // own codes.
+  PrologueLoads<PRO ? PRO : 1> pl;
+  DigitLoads<kItems> held;
+  if (PRO)
+    prologue_loads<PRO ? PRO : 1>(a, pl);
+  else if (a.act_vec)
+    digit_loads<1, kItems, true>(held, a.act, 0, a.K);
+  else
+    digit_loads<1, kItems, false>(held, a.act, 0, a.K);
   float s[R];
-  float4_t x[8];
-  if (has) {
+  uint4_t w[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int p = plane[r];
-      w[r] = __builtin_nontemporal_load(
-          reinterpret_cast<const uint4_t *>(a.codes[p] + (size_t)prow[r] * (size_t)a.row_stride[p]) + u);
-      s[r] = a.gains[p][(size_t)prow[r] * (size_t)a.gain_stride[p] + ((unsigned)u >> a.group_shift)];
-    }
-    if (!PRO) {
-      const float *src = a.act + u * 32;
-      if (a.act_vec) {
+  for (int r = 0; r < R; ++r) {
+    const int p = plane[r];
+    s[r] = a.gains[p][(size_t)prow[r] * (size_t)a.gain_stride[p] + ((unsigned)u >> a.group_shift)];
+  }
 #pragma unroll
-        for (int q = 0; q < 8; ++q) x[q] = *reinterpret_cast<const float4_t *>(src + 4 * q);
-      } else {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) x[q] = float4_t{src[4 * q], src[4 * q + 1], src[4 * q + 2], src[4 * q + 3]};
-      }
-    }
+  for (int r = 0; r < R; ++r) {
+    const int p = plane[r];
+    w[r] = __builtin_nontemporal_load(
+        reinterpret_cast<const uint4_t *>(a.codes[p] + (size_t)prow[r] * (size_t)a.row_stride[p]) + u);
   }
   if (PRO) {
-    // The weight loads above are in flight while the block forms x.
-    group_prologue<PRO ? PRO : 1>(a, xs, pro_red);
-    if (has) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) x[q] = *reinterpret_cast<const float4_t *>(xs + u * 32 + 4 * q);
-    }
+    group_prologue<PRO ? PRO : 1>(a, pl, xs, pro_red);
+    digit_store_lds<kDigits>(xs, a.K, dig, down);
+  } else {
+    digit_store<1, kItems, kDigits>(held, a.K, dig, down);
   }
 
   float acc[R];
+  {
+    uint4_t dd[kDigits];
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-  if (has) {
-    const uint32_t exp16 = 0x4C004C00u;
-    float part[R];
+    for (int j = 0; j < kDigits; ++j) dd[j] = dig[j * units + u];
+    const int shift = down[u];
 #pragma unroll
-    for (int r = 0; r < R; ++r) part[r] = 0.0f;
+    for (int r = 0; r < R; ++r) {
+      const uint4_t c = w[r] ^ 0x88888888u;
+      int t[kDigits];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      half2_t p[R][4];
+      for (int j = 0; j < kDigits; ++j) t[j] = 0;
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const uint32_t d = w[r][j];
-        p[r][0] = nibble_pair16<0>(d, exp16);
-        p[r][1] = nibble_pair16<1>(d, exp16);
-        p[r][2] = nibble_pair16<2>(d, exp16);
-        p[r][3] = nibble_pair16<3>(d, exp16);
-      }
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int r = 0; r < R; ++r) part[r] = __builtin_fmaf((float)p[r][i].x, x[2 * j][i], part[r]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int r = 0; r < R; ++r) part[r] = __builtin_fmaf((float)p[r][i].y, x[2 * j + 1][i], part[r]);
+        for (int j = 0; j < kDigits; ++j)
+          t[j] = __builtin_amdgcn_sdot8((int)c[q], (int)dd[j][q], t[j], false);
+      const float gain = has ? s[r] : 0.0f;
+      acc[r] = wave_sum_to_last(gain * __builtin_amdgcn_ldexpf(digit_sum<kDigits>(t), shift));
     }
-    float total = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      total += x[q].x; total += x[q].y; total += x[q].z; total += x[q].w;
-    }
-    const float c = a.unit_bias * total;
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = s[r] * (part[r] - c);
   }
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = wave_sum_to_last(acc[r]);
 
-  if (a.ksplit > 1) {
+  if (KS > 1) {
     if (lane == 63) {
 #pragma unroll
       for (int r = 0; r < R; ++r) red[wave][r] = acc[r];
@@ -704,7 +750,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       float total = 0.0f;
-      for (int k = 0; k < a.ksplit; ++k) total += red[wave + k][r];
+      for (int k = 0; k < KS; ++k) total += red[wave + k][r];
       acc[r] = total;
     }
   } else if (lane != 63) {
@@ -1113,44 +1159,34 @@ static hipError_t gemv_mfma_dispatch(const GemvMfmaArgs &a, const GemvMfmaPlan &
   }
 }
 
-template <int M, int R, int UPL, int GPT, int KS>
-static hipError_t gemv_dot_launch_ks(const GemvArgs &a, hipStream_t stream) {
+template <int M, int R, int UPL, int GPT>
+static hipError_t gemv_dot_launch_gpt(const GemvArgs &a, hipStream_t stream) {
   const int tiles = (a.N + R - 1) / R;
-  constexpr int kTilesPerBlock = 4 / KS;
-  dim3 grid((tiles + kTilesPerBlock - 1) / kTilesPerBlock);
+  const int tiles_per_block = 4 / a.ksplit;
+  dim3 grid((tiles + tiles_per_block - 1) / tiles_per_block);
   const size_t lds = gemv_dot_lds_bytes(M, a.K >> 5);
   static size_t lds_granted = 65536;  // launches above 64 KiB ask once
   if (lds > lds_granted) {
-    hipError_t e =
-        hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q4_dot_kernel<M, R, UPL, GPT, true, KS>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q4_dot_kernel<M, R, UPL, GPT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     lds_granted = lds;
   }
-  hipLaunchKernelGGL((gemv_q4_dot_kernel<M, R, UPL, GPT, true, KS>), grid, dim3(kGemvThreads), lds,
-                     stream, a);
+  hipLaunchKernelGGL((gemv_q4_dot_kernel<M, R, UPL, GPT>), grid, dim3(kGemvThreads), lds, stream, a);
   return hipGetLastError();
-}
-
-template <int M, int R, int UPL, int GPT>
-static hipError_t gemv_dot_launch_gpt(const GemvArgs &a, hipStream_t stream) {
-  switch (a.ksplit) {
-    case 1: return gemv_dot_launch_ks<M, R, UPL, GPT, 1>(a, stream);
-    case 2: return gemv_dot_launch_ks<M, R, UPL, GPT, 2>(a, stream);
-    case 4: return gemv_dot_launch_ks<M, R, UPL, GPT, 4>(a, stream);
-    default: return hipErrorInvalidValue;
-  }
 }
 
 // Items a thread stages: M K / 8 groups over 256 threads, at most 8.
 constexpr int kDotMaxItems = 8;
 
-// The integer-dot form for M <= 2 lanes with 16-byte aligned activations:
-// M K <= 16384 (a thread stages at most eight groups of eight).
+// The integer-dot form with 16-byte aligned activations and M K <= 16384 (a
+// thread stages at most eight groups of eight); `a.ksplit` a power of two.
 template <int M, int R, int UPL>
-static hipError_t gemv_dot_launch(const GemvArgs &a, hipStream_t stream) {
+static hipError_t gemv_dot_launch(GemvArgs a, hipStream_t stream) {
   const int items = (M * (a.K >> 3) + kGemvThreads - 1) / kGemvThreads;
   if (!a.act_vec) return hipErrorInvalidValue;
+  a.ks_log = a.ksplit == 1 ? 0 : a.ksplit == 2 ? 1 : a.ksplit == 4 ? 2 : -1;
+  if (a.ks_log < 0) return hipErrorInvalidValue;
   if (items <= 1) return gemv_dot_launch_gpt<M, R, UPL, 1>(a, stream);
   if (items <= 2) return gemv_dot_launch_gpt<M, R, UPL, 2>(a, stream);
   if (items <= 4) return gemv_dot_launch_gpt<M, R, UPL, 4>(a, stream);
@@ -1265,8 +1301,23 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
   a.ksplit = ksplit;
   const int tiles_per_block = 4 / ksplit;
   dim3 grid((a.tiles + tiles_per_block - 1) / tiles_per_block);
-#define IGL_GROUP_LAUNCH(M_, P_) \
-  hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_>), grid, dim3(kGemvThreads), 0, stream, a)
+  // eight-element groups of x a thread stages without a prologue
+  const int gpt = K <= 2048 ? 1 : K <= 4096 ? 2 : 4;
+#define IGL_GROUP_KS(M_, P_, G_)                                                                    \
+  do {                                                                                              \
+    if (ksplit == 1)                                                                                \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 1>), grid, dim3(kGemvThreads), 0, stream, a); \
+    else if (ksplit == 2)                                                                           \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 2>), grid, dim3(kGemvThreads), 0, stream, a); \
+    else                                                                                            \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 4>), grid, dim3(kGemvThreads), 0, stream, a); \
+  } while (0)
+#define IGL_GROUP_LAUNCH(M_, P_)                                  \
+  do {                                                            \
+    if (P_ != 0 || gpt == 1) IGL_GROUP_KS(M_, P_, 1);             \
+    else if (gpt == 2) IGL_GROUP_KS(M_, P_, 2);                   \
+    else IGL_GROUP_KS(M_, P_, 4);                                 \
+  } while (0)
   // registers the prologue holds: the fewest of 6, 8, 16 a thread that cover K
   const int held = !pro ? 0 : K <= 6 * 256 ? 6 : K <= 8 * 256 ? 8 : 16;
   switch (mode * 4 + (held == 0 ? 0 : held == 6 ? 1 : held == 8 ? 2 : 3)) {
@@ -1285,6 +1336,7 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
     default: return hipErrorInvalidValue;
   }
 #undef IGL_GROUP_LAUNCH
+#undef IGL_GROUP_KS
   return hipGetLastError();
 }
 
@@ -1320,6 +1372,33 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
   a.K = K;
   a.unit_bias = 16.0f + (float)code_bias;
   a.act_vec = ((((uintptr_t)act) & 15u) == 0 && (act_stride & 3) == 0) ? 1 : 0;
+  // One to four lanes on the integer dot path (aligned activations, M K <=
+  // 16384): eight-row tiles from 128 units up for one and two lanes, so the
+  // staging of x is shared by more rows; enough waves on a row tile that each
+  // lane holds one unit (two past 256).
+  if (a.act_vec && lanes <= 4 && lanes * K <= kDotMaxItems * kGemvThreads * 8 &&
+      K / 32 <= 8 * kWave) {
+    const int units = K / 32;
+    const int R = lanes <= 2 && units >= 128 ? 8 : 4;
+    const int tiles = (N + R - 1) / R;
+    const int upl = units > 4 * kWave ? 2 : 1;
+    int ksplit = 1;
+    while (ksplit < 4 && (units > ksplit * kWave * upl ||
+                          (tiles * ksplit < 2048 && units / (ksplit * 2) >= 32 * upl)))
+      ksplit *= 2;
+    a.ksplit = ksplit;
+    a.chunk_cols = K;
+    a.out = out;
+    a.out_stride = out_stride;
+    switch (lanes) {
+      case 1:
+        if (R == 4) return gemv_dot_launch<1, 4, 1>(a, stream);
+        return upl == 2 ? gemv_dot_launch<1, 8, 2>(a, stream) : gemv_dot_launch<1, 8, 1>(a, stream);
+      case 2: return R == 4 ? gemv_dot_launch<2, 4, 1>(a, stream) : gemv_dot_launch<2, 8, 1>(a, stream);
+      case 3: return gemv_dot_launch<3, 4, 1>(a, stream);
+      default: return gemv_dot_launch<4, 4, 1>(a, stream);
+    }
+  }
   // Three to eight lanes on the matrix cores where the plane's width allows.
   GemvMfmaPlan plan;
   if (lanes >= 3 && gemv_mfma_plan(lanes, N, K, &plan)) {
@@ -1354,8 +1433,8 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
                        plan.chunks, lanes, N, out, out_stride);
     return hipGetLastError();
   }
-  // One and two lanes with at most 512 units a row: the register form, with
-  // enough waves on a row tile that each lane holds one unit (two past 256).
+  // One and two lanes with unaligned activations and at most 512 units a
+  // row: the float register form, the integer form's layout.
   if (lanes <= 2 && K / 32 <= 8 * kWave) {
     const int units = K / 32;
     const int R = 4;
@@ -1369,11 +1448,6 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
     a.chunk_cols = K;
     a.out = out;
     a.out_stride = out_stride;
-    if (a.act_vec && lanes * K <= kDotMaxItems * kGemvThreads * 8) {
-      if (upl == 2)
-        return lanes == 1 ? gemv_dot_launch<1, 4, 2>(a, stream) : gemv_dot_launch<2, 4, 2>(a, stream);
-      return lanes == 1 ? gemv_dot_launch<1, 4, 1>(a, stream) : gemv_dot_launch<2, 4, 1>(a, stream);
-    }
     if (upl == 2)
       return lanes == 1 ? gemv_reg_launch<1, 4, 2>(a, stream) : gemv_reg_launch<2, 4, 2>(a, stream);
     return lanes == 1 ? gemv_reg_launch<1, 4, 1>(a, stream) : gemv_reg_launch<2, 4, 1>(a, stream);
