@@ -220,6 +220,16 @@ class Backend:
                                           act.ptr + act_off, act_stride, lanes, out.ptr + out_off,
                                           out_stride), "gemv_dev")
 
+    def plane_lift_dev(self, cp, act: DevBuf, act_stride, lanes, out: DevBuf, out_stride):
+        """plane_lift_many on device: enter_gain grid, product, leave_gain grid."""
+        self._check(self.lib.igl_plane_lift_dev(ctypes.byref(self.desk), ctypes.byref(cp.plane),
+                                                act.ptr, act_stride, lanes, out.ptr, out_stride),
+                    "plane_lift_dev")
+
+    def quant_step_dev(self, src: DevBuf, src_stride, dst: DevBuf, dst_stride, n, lanes, step):
+        self._check(self.lib.igl_quant_step_dev(ctypes.byref(self.desk), src.ptr, src_stride, dst.ptr,
+                                                dst_stride, n, lanes, float(step)), "quant_step_dev")
+
     def gemm_bf16_dev(self, cp, act: DevBuf, act_stride, lanes, out: DevBuf, out_stride):
         self._check(self.lib.igl_gemm_bf16_dev(ctypes.byref(self.desk), ctypes.byref(cp.plane),
                                                act.ptr, act_stride, lanes, out.ptr, out_stride),

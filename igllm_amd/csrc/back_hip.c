@@ -48,6 +48,8 @@ struct igl_desk_state {
   size_t part_floats;
   float *work_dev;
   size_t work_floats;
+  float *quant_dev;   /* plane_lift: the activations on the plane's entry grid */
+  size_t quant_floats;
   /* staging for the elementwise host entries */
   float *elem_dev;
   size_t elem_floats;
@@ -334,6 +336,53 @@ int igl_gemm_bf16_dev(igl_desk *desk, const igl_plane *sheet, const uint16_t *ac
   return gemm_run(desk, sheet, act_dev, 1, act_stride, lane_count, out_dev, 1, out_stride);
 }
 
+/* ---- the static activation grid around a product --------------------------- */
+
+int igl_quant_step_dev(igl_desk *desk, const float *src_dev, int src_stride, float *dst_dev,
+                       int dst_stride, int n, int lanes, float step) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  if (!src_dev || !dst_dev || n < 1 || lanes < 1 ||
+      (lanes > 1 && (src_stride < n || dst_stride < n))) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return IGL_FAIL_ARGUMENT;
+  }
+  return hip_check(st, igl_launch_quant_step(src_dev, src_stride, dst_dev, dst_stride, n, lanes,
+                                             step, st->stream));
+}
+
+/* plane_lift_many (app_core.c:7814-7843) without the model-wide input rule:
+ * with enter_gain > 0 the lanes are put on that grid (in desk scratch) before
+ * the product, and with leave_gain > 0 the outputs after it.  The product is
+ * igl_mat_mat_dev's.  The table's mat_mat does neither: its caller does. */
+int igl_plane_lift_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev,
+                       int act_stride, int lane_count, float *out_dev, int out_stride) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  int code;
+  if (!st) return IGL_FAIL_STATE;
+  if (!sheet || !act_dev || !out_dev || lane_count < 1 ||
+      (lane_count > 1 && (act_stride < sheet->col_count || out_stride < sheet->row_count))) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return IGL_FAIL_ARGUMENT;
+  }
+  if (sheet->enter_gain > 0.0f) {
+    const int cols = sheet->col_count;
+    if (grow_dev(st, &st->quant_dev, &st->quant_floats, (size_t)lane_count * (size_t)cols) != IGL_OKAY)
+      return IGL_FAIL_MEMORY;
+    if ((code = hip_check(st, igl_launch_quant_step(act_dev, act_stride, st->quant_dev, cols, cols,
+                                                    lane_count, sheet->enter_gain, st->stream))) !=
+        IGL_OKAY)
+      return code;
+    code = igl_mat_mat_dev(desk, sheet, st->quant_dev, cols, lane_count, out_dev, out_stride);
+  } else {
+    code = igl_mat_mat_dev(desk, sheet, act_dev, act_stride, lane_count, out_dev, out_stride);
+  }
+  if (code != IGL_OKAY || !(sheet->leave_gain > 0.0f)) return code;
+  return hip_check(st, igl_launch_quant_step(out_dev, out_stride, out_dev, out_stride,
+                                             sheet->row_count, lane_count, sheet->leave_gain,
+                                             st->stream));
+}
+
 /* ---- attention and cache ------------------------------------------------- */
 
 int igl_attend_lanes_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t *value_store,
@@ -607,6 +656,7 @@ void igl_back_close(igl_desk *desk) {
   if (st->out_pin) (void)hipHostFree(st->out_pin);
   if (st->part_dev) (void)hipFree(st->part_dev);
   if (st->work_dev) (void)hipFree(st->work_dev);
+  if (st->quant_dev) (void)hipFree(st->quant_dev);
   if (st->elem_dev) (void)hipFree(st->elem_dev);
   if (st->gemm_dev) (void)hipFree(st->gemm_dev);
   if (st->mark[0]) (void)hipEventDestroy(st->mark[0]);

@@ -89,9 +89,41 @@ __global__ void cache_lay_kernel(const float *row, int width, float scale, int f
   store[slot_first + i] = fmt == 0 ? e4m3_code(row[i] / scale) : int8_code(row[i], scale);
 }
 
+// The static activation grid on `lanes` rows of n (quant_step,
+// app_core.c:1930-1940): rint(x / step) with the division correctly rounded,
+// clamped to [-128, 127] by the reference's two comparisons (a NaN passes
+// through), times step.  A step that is not positive copies x unchanged.
+// src may be dst.
+__global__ void quant_step_kernel(const float *src, int src_stride, float *dst, int dst_stride,
+                                  int n, float step) {
+  const int lane = blockIdx.y;
+  const float *in = src + (size_t)lane * src_stride;
+  float *out = dst + (size_t)lane * dst_stride;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const float x = in[i];
+    if (!(step > 0.0f)) {
+      out[i] = x;
+      continue;
+    }
+    float level = __builtin_rintf(x / step);
+    if (level < -128.0f) level = -128.0f;
+    if (level > 127.0f) level = 127.0f;
+    out[i] = level * step;
+  }
+}
+
 }  // namespace igl
 
 using namespace igl;
+
+extern "C" hipError_t igl_launch_quant_step(const float *src, int src_stride, float *dst,
+                                            int dst_stride, int n, int lanes, float step,
+                                            hipStream_t stream) {
+  const int blocks = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+  hipLaunchKernelGGL(quant_step_kernel, dim3(blocks, lanes), dim3(256), 0, stream, src, src_stride, dst,
+                     dst_stride, n, step);
+  return hipGetLastError();
+}
 
 extern "C" hipError_t igl_launch_norm_rms(const float *in, const float *gain, int n, int rows,
                                           int stride, float eps, float *out, hipStream_t stream) {

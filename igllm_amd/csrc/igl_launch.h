@@ -104,6 +104,8 @@ size_t igl_pick_work_bytes(int lanes);
 hipError_t igl_launch_pick(const float *v, int n, size_t stride, int lanes, void *work,
                            int32_t *pairs, hipStream_t stream);
 
+hipError_t igl_launch_quant_step(const float *src, int src_stride, float *dst, int dst_stride,
+                                 int n, int lanes, float step, hipStream_t stream);
 hipError_t igl_launch_norm_rms(const float *in, const float *gain, int n, int rows, int stride,
                                float eps, float *out, hipStream_t stream);
 hipError_t igl_launch_soft_max(float *v, int n, int rows, int stride, hipStream_t stream);

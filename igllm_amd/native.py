@@ -112,6 +112,8 @@ SIGNATURES = {
     "igl_gemv_dev": (_I, [ctypes.POINTER(Desk), ctypes.POINTER(Plane), _P, _I, _I, _P, _I]),
     "igl_gemm_bf16_dev": (_I, [ctypes.POINTER(Desk), ctypes.POINTER(Plane), _P, _I, _I, _P, _I]),
     "igl_gemm_lane_floor": (_I, []),
+    "igl_quant_step_dev": (_I, [ctypes.POINTER(Desk), _P, _I, _P, _I, _I, _I, _F]),
+    "igl_plane_lift_dev": (_I, [ctypes.POINTER(Desk), ctypes.POINTER(Plane), _P, _I, _I, _P, _I]),
     "igl_attend_dev": (_I, [ctypes.POINTER(Desk), _P, _P, _I, _F, _F, _I, _I, _I, _I, _P, _I, _I,
                             _F, _P]),
     "igl_attend_lanes_dev": (_I, [ctypes.POINTER(Desk), _P, _P, _I, _F, _F, _I, _I, _I, _I, _P,

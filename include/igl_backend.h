@@ -153,6 +153,19 @@ int igl_gemm_bf16_dev(igl_desk *desk, const igl_plane *sheet, const uint16_t *ac
                       int act_stride, int lane_count, uint16_t *out_dev, int out_stride);
 int igl_gemm_lane_floor(void);
 
+/* quant_step (app_core.c:1930-1940) on `lanes` rows of n floats: rint(x / step)
+ * clamped to [-128, 127], times step; a step that is not positive copies.  src
+ * may be dst. */
+int igl_quant_step_dev(igl_desk *desk, const float *src_dev, int src_stride, float *dst_dev,
+                       int dst_stride, int n, int lanes, float step);
+/* plane_lift_many (app_core.c:7814-7843), the caller-side wrapper of the
+ * table's mat_mat: the lanes on the plane's enter_gain grid before the
+ * product (igl_mat_mat_dev's), the outputs on its leave_gain grid after;
+ * either step is skipped when its gain is not positive.  The model-wide
+ * input rule (quant_act) is not applied. */
+int igl_plane_lift_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev,
+                       int act_stride, int lane_count, float *out_dev, int out_stride);
+
 /* Byte formats of the key/value ring. */
 typedef enum igl_cache_format { IGL_CACHE_E4M3 = 0, IGL_CACHE_INT8 = 1 } igl_cache_format;
 

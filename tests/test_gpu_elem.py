@@ -49,3 +49,66 @@ def test_rope_turn(backend):
         want = v.copy()
         ol.oracle().oracle_rope_turn(ol.p(want), head, ol.p(c), ol.p(s))
         assert np.max(np.abs(got - want)) <= 1e-6
+
+
+@pytest.mark.parametrize("step", [0.0625, 0.1, 3.7, 0.0])
+def test_quant_step_dev(backend, step):
+    """igl_quant_step_dev against the pinned float32 closed form, bit for bit:
+    three lanes at a stride, out of place and in place."""
+    from test_oracle import quant_step_closed, quant_step_inputs
+
+    x = quant_step_inputs()
+    n, lanes, stride = x.size, 3, x.size + 5
+    host = np.zeros((lanes, stride), dtype=np.float32)
+    for l in range(lanes):
+        host[l, :n] = np.roll(x, 17 * l)
+    src = backend.upload(host)
+    dst = backend.alloc(host.nbytes)
+    backend.quant_step_dev(src, stride, dst, stride, n, lanes, step)
+    backend.quant_step_dev(src, stride, src, stride, n, lanes, step)
+    backend.sync()
+    out = dst.get(np.float32, lanes * stride).reshape(lanes, stride)
+    inplace = src.get(np.float32, lanes * stride).reshape(lanes, stride)
+    for l in range(lanes):
+        want = quant_step_closed(host[l, :n], step)
+        assert np.array_equal(out[l, :n].view(np.uint32), want.view(np.uint32))
+        assert np.array_equal(inplace[l, :n].view(np.uint32), want.view(np.uint32))
+    src.free()
+    dst.free()
+
+
+@pytest.mark.parametrize("lanes", [1, 3, 64])
+def test_plane_lift_dev(backend, lanes):
+    """plane_lift_many on device (app_core.c:7814-7843): the lanes on the
+    enter_gain grid, the product, the outputs on the leave_gain grid.  The
+    composition is checked to the bit against the same steps taken one by one
+    (the closed-form grid, then igl_mat_mat_dev), and the product against the
+    oracle on the gridded activations."""
+    from igllm_amd.backend import make_plane, synth_projection
+    from test_oracle import quant_step_closed
+
+    N, K = 640, 2048
+    codes, gains, act = synth_projection(N, K, lanes, seed=31)
+    act = (act * 3).astype(np.float32)
+    cp = backend.attach(make_plane(codes, gains, K))
+    cp.plane.enter_gain = 0.05
+    cp.plane.leave_gain = 0.01
+    entered = np.stack([quant_step_closed(a, 0.05) for a in act])
+    dev_act = backend.upload(act)
+    dev_entered = backend.upload(entered)
+    out = backend.alloc(lanes * N * 4)
+    plain = backend.alloc(lanes * N * 4)
+    backend.plane_lift_dev(cp, dev_act, K, lanes, out, N)
+    backend.mat_mat_dev(cp, dev_entered, K, lanes, plain, N)
+    backend.sync()
+    got = out.get(np.float32, lanes * N).reshape(lanes, N)
+    product = plain.get(np.float32, lanes * N).reshape(lanes, N)
+    want = np.stack([quant_step_closed(y, 0.01) for y in product])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    ref = ol.oracle_mat_mat(codes, gains, entered, K, threads=8)
+    floor = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    tol = 2e-3 if lanes >= 64 else 1e-3  # 64 lanes take the binary16-operand MFMA GEMM
+    assert np.max(np.abs(product - ref) / np.maximum(np.abs(ref), floor)) <= tol
+    for b in (dev_act, dev_entered, out, plain):
+        b.free()
+    backend.detach(cp)

@@ -33,6 +33,48 @@ def pack_fields(values, bits):
 
 # ---- quant layer --------------------------------------------------------------
 
+def quant_step_inputs():
+    """Values for the activation grid: normals at several scales, exact ties
+    (k + 1/2) step for a power-of-two step, values past both clamps, signed
+    zeros, infinities and NaN."""
+    rng = np.random.default_rng(5)
+    vals = [rng.normal(size=400) * s for s in (0.01, 1.0, 30.0)]
+    vals.append((np.arange(-140, 140) + 0.5) * 0.0625)
+    vals.append(np.array([-1e9, 1e9, -8.03, 7.97, 0.0, -0.0, np.inf, -np.inf, np.nan]))
+    return np.concatenate(vals).astype(np.float32)
+
+
+def quant_step_closed(x, step):
+    """rint(x / step) in float32, clamped by comparisons (NaN passes), times step."""
+    x = np.asarray(x, dtype=np.float32)
+    if not step > 0:
+        return x.copy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        level = np.rint(x / np.float32(step)).astype(np.float32)
+    level = np.where(level < -128, np.float32(-128), level)
+    level = np.where(level > 127, np.float32(127), level)
+    return (level * np.float32(step)).astype(np.float32)
+
+
+@pytest.mark.parametrize("step", [0.0625, 0.1, 3.7, 1e-30, 0.0, -1.0, float("nan")])
+def test_quant_step_pinned(step):
+    """oracle_quant_step (app_core.c:1930-1940) against numpy's float32 closed
+    form (ties to even, both clamps, NaN through, non-positive steps inert) and,
+    where it was built, the reference's own quant_step."""
+    x = quant_step_inputs()
+    want = quant_step_closed(x, step)
+    got = np.array([ol.oracle().oracle_quant_step(float(v), step) for v in x], dtype=np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    ref = ol.ref("plain")
+    if ref is not None:
+        got_ref = np.array([ref.ref_quant_step(float(v), step) for v in x], dtype=np.float32)
+        assert np.array_equal(got_ref.view(np.uint32), want.view(np.uint32))
+    if step == 0.0625:
+        # the ties went to even levels
+        ties = x[1200:1480]
+        assert np.all(np.rint(ties / np.float32(step)) % 2 == 0)
+
+
 def test_nibble_kat():
     """app_test.c:593-594: {0x98,0xBA,0x21,0x0F} are 0,1,2,3,-7,-6,7,-8 (code - 8)."""
     row = np.array([0x98, 0xBA, 0x21, 0x0F], dtype=np.uint8)
