@@ -186,38 +186,54 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_q4_kernel(GemmArgs g) {
 
 // ---- the large-tile form ---------------------------------------------------
 //
-// For M and N of 256 and up.  The activations are first converted once to a
-// binary16 copy (act_half_kernel), so the tile loop moves them into LDS
-// unchanged instead of converting every element once per column tile.  Each
-// workgroup owns a 256 x 256 tile of C; its four waves (2 x 2) each hold a
-// 128 x 128 block as 8 x 8 v_mfma_f32_16x16x32_f16 accumulators, four times
-// the products per byte of LDS read of a 64 x 64 block.  K advances one 32-code
-// group a step through two LDS buffers: the next step's global loads are in
-// flight while the current step's 64 products a wave run, then it is
-// dequantized into the other buffer, one barrier a step.  The dequantized
-// weight is (c - code_bias) * gain in packed binary16: exact code times the
-// gain rounded to binary16, rounded once more (both within 2^-11).
+// For M and N of 256 and up, K a multiple of 64.  The activations are first
+// converted once to a binary16 copy (act_half_kernel) in the operand order
+// the weights are decoded in (below), so the tile loop only moves them.
+//
+// A workgroup owns a 256 x 256 tile of C; its eight waves (2 x 4) each hold a
+// 128 x 64 block as 8 x 4 v_mfma_f32_16x16x32_f16 accumulators.  K advances
+// 64 a step through three LDS stages that only the LDS DMA writes
+// (global_load_lds: no registers held for loads in flight, two steps ahead):
+//   * the step's 256 x 64 binary16 activations, 16-byte chunks of a row
+//     XOR-swizzled by the row's low three bits (no padding, no conflicts);
+//   * the 256 rows' 64 codes as they are packed (32 bytes a row), and
+//   * their two fp32 gains.
+// A wave turns its 64 columns' codes into binary16 operands in registers as
+// it consumes them: one v_and_or_b32 puts a nibble in the mantissa of 1024.0
+// (ulp 1: 1024 + c) or, four bits up, of 1024.0 with ulp 16 (1024 + 16 c), so
+// a dword of eight codes takes one shift; subtracting 1024 + bias (or
+// 1024 + 16 bias) is exact, and one multiply by the gain rounded to binary16
+// gives (c - bias) gain or 16 (c - bias) gain, rounded once.  The activation
+// copy holds x / 16 where the weight holds 16 (c - bias) gain, and each eight
+// consecutive k appear in the order 0 4 1 5 2 6 3 7 the pairs come in.
+// Every wave's step is its activation reads for both 32-k halves, the eight
+// weight operands, then 64 products.
 constexpr int kBigM = 256;
 constexpr int kBigN = 256;
 constexpr int kBigK = 64;
-constexpr int kBigPitch = kBigK + 8;          // halves per LDS row
-constexpr int kBigTile = kBigM * kBigPitch;   // halves per LDS tile (A or B)
+constexpr int kBigStages = 3;
+constexpr int kBigA = kBigM * kBigK;          // halves of a stage's activations
+constexpr int kBigB = kBigN * kBigK / 2;      // bytes of a stage's codes
+constexpr int kBigG = kBigN * kBigK / 32;     // floats of a stage's gains
+constexpr int kBigStage = kBigA * 2 + kBigB + kBigG * 4;
 
-// a16[m][k] = binary16(a[m][k]), saturating at +-65504.
+// a16 = binary16(a), saturating at +-65504, in the large-tile form's operand
+// order: within each eight k, positions 0 4 1 5 2 6 3 7, and k = 1, 5, 3, 7
+// divided by 16 (exact for every normal binary16).
 template <bool A_BF16>
 __global__ void act_half_kernel(const void *act, int act_stride, int M, int K, _Float16 *a16) {
   const int k8 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
   const int m = blockIdx.y;
   if (k8 >= K || m >= M) return;
-  half8_t h;
+  float x[8];
   if (A_BF16) {
     // rows are 16-byte aligned (act_stride % 8 == 0): one load for 8 values
     const uint4_t raw = *reinterpret_cast<const uint4_t *>(
         reinterpret_cast<const uint16_t *>(act) + (size_t)m * act_stride + k8);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      h[2 * i] = sat_half(__builtin_bit_cast(float, raw[i] << 16));
-      h[2 * i + 1] = sat_half(__builtin_bit_cast(float, raw[i] & 0xFFFF0000u));
+      x[2 * i] = __builtin_bit_cast(float, raw[i] << 16);
+      x[2 * i + 1] = __builtin_bit_cast(float, raw[i] & 0xFFFF0000u);
     }
   } else {
     const float4_t *src = reinterpret_cast<const float4_t *>(
@@ -225,80 +241,82 @@ __global__ void act_half_kernel(const void *act, int act_stride, int M, int K, _
     const float4_t lo = src[0], hi = src[1];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      h[i] = sat_half(lo[i]);
-      h[4 + i] = sat_half(hi[i]);
+      x[i] = lo[i];
+      x[4 + i] = hi[i];
     }
+  }
+  const _Float16 sixteenth = (_Float16)0.0625f;
+  half8_t h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool up = i & 1;  // k = 1, 3 and their partners 5, 7
+    const _Float16 a = sat_half(x[i]), b = sat_half(x[i + 4]);
+    h[2 * i] = up ? a * sixteenth : a;
+    h[2 * i + 1] = up ? b * sixteenth : b;
   }
   *reinterpret_cast<half8_t *>(a16 + (size_t)m * K + k8) = h;
 }
 
 struct GemmBigArgs {
-  const _Float16 *a16;    // [M][K]
+  const _Float16 *a16;    // [M][K], act_half_kernel's form
   const uint8_t *codes;
   long long row_stride;
   const float *gains;
   int gain_stride;
   int group_shift;
   float code_bias;
-  void *out;
+  void *out;              // C, or with K slices fp32 partials [slice][M][N]
   int out_stride;
-  int M, N, K;
+  int M, N, K;            // K: the whole plane's columns
+  int k_steps;            // 64-wide steps of one K slice (blockIdx.z)
+  size_t slice_floats;    // floats between slices' partials (0: no split)
 };
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
 
 template <bool C_BF16>
 __global__ __launch_bounds__(512) void gemm_q4_big_kernel(GemmBigArgs g) {
-  extern __shared__ __attribute__((aligned(16))) _Float16 lds_h[];  // A[2], B[2]
-  constexpr int G = kBigK / 32;  // groups a step
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds_b[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2;      // 2 wave rows of 128
   const int wn = wave & 3;       // 4 wave columns of 64
   const int m0 = blockIdx.y * kBigM;
   const int n0 = blockIdx.x * kBigN;
+  const int steps = g.k_steps;
+  const int k_first = blockIdx.z * g.k_steps * kBigK;
 
-  // Thread t stages half (t & 1) of row t / 2 of the A tile (32 halves) and
-  // group (t & 1) of row t / 2 of the weight tile (16 bytes and its gain).
-  const int row = tid >> 1;
-  const int part = tid & 1;
-  const int am = min(m0 + row, g.M - 1);
-  const int bn = min(n0 + row, g.N - 1);
-  const bool a_live = m0 + row < g.M;
-  const bool b_live = n0 + row < g.N;
-  const uint4_t *a_src = reinterpret_cast<const uint4_t *>(g.a16 + (size_t)am * g.K + 32 * part);
-  const uint4_t *b_src =
-      reinterpret_cast<const uint4_t *>(g.codes + (size_t)bn * (size_t)g.row_stride) + part;
-  const float *gain_row = g.gains + (size_t)bn * g.gain_stride;
-  uint4_t ra[4], rb;
-  float rs;
-  auto fetch = [&](int k) {
+  // DMA sources (a lane's 16 bytes land at the wave's LDS address + 16 lane).
+  // Activations: wave w's instruction i fills rows 8 (4 w + i) .. +7, lane l
+  // row R0 + l / 8 at physical chunk l % 8, logical chunk (l % 8) ^ (row & 7).
+  const _Float16 *a_src[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ra[i] = a_src[(k >> 3) + i];
-    rb = __builtin_nontemporal_load(b_src + (k >> 5));
-    rs = gain_row[(unsigned)((k >> 5) + part) >> g.group_shift];
-  };
-  const uint32_t exp16 = 0x4C004C00u;
-  const _Float16 lift = (_Float16)(16.0f + g.code_bias);
-  auto stage = [&](int buf) {
-    _Float16 *as = lds_h + buf * kBigTile + row * kBigPitch + 32 * part;
-    _Float16 *bs = lds_h + (2 + buf) * kBigTile + row * kBigPitch + 32 * part;
-    const uint4_t zero = {0u, 0u, 0u, 0u};
+  for (int i = 0; i < 4; ++i) {
+    const int r = 8 * (4 * wave + i) + (lane >> 3);
+    const int c = (lane & 7) ^ (r & 7);
+    a_src[i] = g.a16 + (size_t)min(m0 + r, g.M - 1) * g.K + k_first + 8 * c;
+  }
+  // codes: wave w fills rows 32 w .. +31, lane l row 32 w + l / 2, half l & 1;
+  // gains (4 bytes a lane): the same rows, group l & 1
+  const int br = min(n0 + 32 * wave + (lane >> 1), g.N - 1);
+  const uint8_t *b_src = g.codes + (size_t)br * (size_t)g.row_stride + k_first / 2 + 16 * (lane & 1);
+  const float *s_src = g.gains + (size_t)br * g.gain_stride;
+  const int s_first = k_first / 32;
+  const int s_grp = lane & 1;
+  auto issue = [&](int step) {
+    uint8_t *st = lds_b + (step % kBigStages) * kBigStage;
+    const int k0 = step * kBigK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4_t *>(as + 8 * i) = a_live ? ra[i] : zero;
-    const half2_t shift = half2_t{lift, lift};
-    const _Float16 sh = (_Float16)rs;
-    const half2_t scale = b_live ? half2_t{sh, sh} : half2_t{(_Float16)0.0f, (_Float16)0.0f};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // codes 8j .. 8j+7, pairs (i, i + 4) in the halves of nibble_pair16<i>
-      const uint32_t d = rb[j];
-      const half2_t p0 = (nibble_pair16<0>(d, exp16) - shift) * scale;
-      const half2_t p1 = (nibble_pair16<1>(d, exp16) - shift) * scale;
-      const half2_t p2 = (nibble_pair16<2>(d, exp16) - shift) * scale;
-      const half2_t p3 = (nibble_pair16<3>(d, exp16) - shift) * scale;
-      const half8_t h = {p0.x, p1.x, p2.x, p3.x, p0.y, p1.y, p2.y, p3.y};
-      *reinterpret_cast<half8_t *>(bs + 8 * j) = h;
-    }
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds((global_void_t *)(a_src[i] + k0),
+                                       (lds_void_t *)(st + (4 * wave + i) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((global_void_t *)(b_src + k0 / 2),
+                                     (lds_void_t *)(st + kBigA * 2 + wave * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(
+        (global_void_t *)(s_src + (((unsigned)(s_first + k0 / 32 + s_grp)) >> g.group_shift)),
+        (lds_void_t *)(st + kBigA * 2 + kBigB + wave * 256), 4, 0, 0);
   };
 
   float4_t acc[8][4];
@@ -306,62 +324,147 @@ __global__ __launch_bounds__(512) void gemm_q4_big_kernel(GemmBigArgs g) {
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t exp10 = 0x64006400u;  // 1024.0 in both halves
+  const _Float16 lo_bias = (_Float16)(1024.0f + g.code_bias);
+  const _Float16 hi_bias = (_Float16)(1024.0f + 16.0f * g.code_bias);
+  const half2_t bias_lo = half2_t{lo_bias, lo_bias};
+  const half2_t bias_hi = half2_t{hi_bias, hi_bias};
+  const int gq = lane >> 4;     // lane group: k 16 gq .. 16 gq + 15 of a step
+  const int n = lane & 15;
 
-  fetch(0);
-  stage(0);
-  __syncthreads();
-  const int steps = g.K / kBigK;
-  const int koff = 8 * (lane >> 4);
+  issue(0);
+  if (steps > 1) issue(1);
   for (int s = 0; s < steps; ++s) {
-    const int cur = s & 1;
-    if (s + 1 < steps) fetch((s + 1) * kBigK);
+    // this wave's six loads of step s are in LDS (those of s + 1 may not be)
+    if (s + 1 < steps)
+      __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // ... and every wave's, and every wave has consumed the stage the next
+    // issue overwrites (its reads fed the previous step's products); no
+    // fence, which would also wait for the loads two steps ahead
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (s + 2 < steps) issue(s + 2);
+    const uint8_t *st = lds_b + (s % kBigStages) * kBigStage;
+    const _Float16 *as = reinterpret_cast<const _Float16 *>(st);
+    const uint8_t *bs = st + kBigA * 2;
+    const float *gs = reinterpret_cast<const float *>(st + kBigA * 2 + kBigB);
+    uint2_t braw[4];
+    half2_t bscale[4];
 #pragma unroll
-    for (int q = 0; q < G; ++q) {
-      const _Float16 *as = lds_h + cur * kBigTile + (wm * 128 + (lane & 15)) * kBigPitch + 32 * q + koff;
-      const _Float16 *bs = lds_h + (2 + cur) * kBigTile + (wn * 64 + (lane & 15)) * kBigPitch + 32 * q + koff;
-      half8_t af[8], bf[4];
+    for (int j = 0; j < 4; ++j) {
+      const int row = wn * 64 + 16 * j + n;
+      braw[j] = *reinterpret_cast<const uint2_t *>(bs + row * 32 + 8 * gq);
+      const _Float16 sh = (_Float16)gs[row * 2 + (gq >> 1)];
+      bscale[j] = half2_t{sh, sh};
+    }
+    // k-half q of lane group gq is k 16 gq + 8 q .. + 7: its activations are
+    // logical chunk 2 gq + q of the row, its codes dword q of the eight bytes
+    half8_t af[2][8], bf[2][4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) af[i] = *reinterpret_cast<const half8_t *>(as + i * 16 * kBigPitch);
+    for (int q = 0; q < 2; ++q)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const half8_t *>(bs + j * 16 * kBigPitch);
+      for (int i = 0; i < 8; ++i) {
+        const int r = wm * 128 + 16 * i + n;
+        const int p = (2 * gq + q) ^ (r & 7);
+        af[q][i] = *reinterpret_cast<const half8_t *>(as + r * kBigK + 8 * p);
+      }
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t d = braw[j][q];
+        const uint32_t e = d >> 8;
+        const half2_t p0 = (as_half2(and_or_b32(d, 0x000F000Fu, exp10)) - bias_lo) * bscale[j];
+        const half2_t p1 = (as_half2(and_or_b32(d, 0x00F000F0u, exp10)) - bias_hi) * bscale[j];
+        const half2_t p2 = (as_half2(and_or_b32(e, 0x000F000Fu, exp10)) - bias_lo) * bscale[j];
+        const half2_t p3 = (as_half2(and_or_b32(e, 0x00F000F0u, exp10)) - bias_hi) * bscale[j];
+        bf[q][j] = __builtin_bit_cast(
+            half8_t, uint4_t{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                             __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)});
+      }
+    // keep the reads and the decoding ahead of the products
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
 #pragma unroll
       for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    if (s + 1 < steps) stage(cur ^ 1);
-    __syncthreads();
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[q][i], bf[q][j], acc[i][j], 0, 0, 0);
   }
 
   // D layout of a 16x16 tile: lane l holds rows 4*(l/16) + r, column l % 16.
+  float *part = reinterpret_cast<float *>(g.out) + blockIdx.z * g.slice_floats;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int n = n0 + wn * 64 + j * 16 + (lane & 15);
-      if (n >= g.N) continue;
+      const int nn = n0 + wn * 64 + j * 16 + n;
+      if (nn >= g.N) continue;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 128 + i * 16 + 4 * (lane >> 4) + r;
+        const int m = m0 + wm * 128 + i * 16 + 4 * gq + r;
         if (m >= g.M) continue;
-        if (C_BF16)
-          reinterpret_cast<uint16_t *>(g.out)[(size_t)m * g.out_stride + n] = float_to_bf16(acc[i][j][r]);
+        if (g.slice_floats)
+          part[(size_t)m * g.N + nn] = acc[i][j][r];
+        else if (C_BF16)
+          reinterpret_cast<uint16_t *>(g.out)[(size_t)m * g.out_stride + nn] = float_to_bf16(acc[i][j][r]);
         else
-          reinterpret_cast<float *>(g.out)[(size_t)m * g.out_stride + n] = acc[i][j][r];
+          reinterpret_cast<float *>(g.out)[(size_t)m * g.out_stride + nn] = acc[i][j][r];
       }
     }
+}
+
+// C = the K slices' partials added in slice order (four columns a thread).
+template <bool C_BF16>
+__global__ void gemm_slice_sum_kernel(const float *part, int slices, size_t slice_floats, int M,
+                                      int N, void *out, int out_stride) {
+  const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  const int m = blockIdx.y;
+  if (n >= N) return;
+  const float *src = part + (size_t)m * N + n;
+  float4_t t = *reinterpret_cast<const float4_t *>(src);
+  for (int z = 1; z < slices; ++z) t += *reinterpret_cast<const float4_t *>(src + z * slice_floats);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (n + e >= N) break;
+    if (C_BF16)
+      reinterpret_cast<uint16_t *>(out)[(size_t)m * out_stride + n + e] = float_to_bf16(t[e]);
+    else
+      reinterpret_cast<float *>(out)[(size_t)m * out_stride + n + e] = t[e];
+  }
 }
 
 }  // namespace igl
 
 using namespace igl;
 
-// Bytes of workspace igl_launch_gemm_q4 needs for an M x K product (the
-// binary16 activations of the large-tile form), 0 when it takes the small one.
+// K slices of a large-tile launch: while the tiles fill fewer than 256
+// workgroups (one a CU) and every slice keeps four 64-wide steps, K is cut in
+// two again; N % 4 == 0 for the slice sum's four-column reads.
+static int gemm_slices(int M, int N, int K) {
+  const int tiles = ((M + kBigM - 1) / kBigM) * ((N + kBigN - 1) / kBigN);
+  int slices = 1;
+  while (slices < 8 && tiles * slices < 256 && N % 4 == 0 && K % (2 * slices * kBigK) == 0 &&
+         K / (2 * slices) >= 4 * kBigK)
+    slices *= 2;
+  return slices;
+}
+
+static size_t gemm_half_bytes(int M, int K) {
+  return ((size_t)M * (size_t)K * sizeof(_Float16) + 255) & ~(size_t)255;
+}
+
+// Bytes of workspace igl_launch_gemm_q4 needs for an M x N x K product (the
+// binary16 activations of the large-tile form, then any K slices' fp32
+// partials), 0 when it takes the small form.
 extern "C" size_t igl_gemm_work_bytes(int M, int N, int K) {
   if (M < kBigM || N < kBigN || K % kBigK) return 0;
-  return (size_t)M * (size_t)K * sizeof(_Float16);
+  const int slices = gemm_slices(M, N, K);
+  return gemm_half_bytes(M, K) + (slices > 1 ? (size_t)slices * M * N * sizeof(float) : 0);
 }
 
 extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride,
@@ -371,6 +474,8 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
                                          int M, int N, int K, void *work, hipStream_t stream) {
   if (igl_gemm_work_bytes(M, N, K) && work) {
     _Float16 *a16 = reinterpret_cast<_Float16 *>(work);
+    const int slices = gemm_slices(M, N, K);
+    float *part = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(work) + gemm_half_bytes(M, K));
     dim3 cgrid((K / 8 + 255) / 256, M);
     if (act_bf16)
       hipLaunchKernelGGL((act_half_kernel<true>), cgrid, dim3(256), 0, stream, act, act_stride, M, K, a16);
@@ -386,12 +491,14 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
     b.gain_stride = gain_stride;
     b.group_shift = __builtin_ctz((unsigned)(group_size / 32));
     b.code_bias = (float)code_bias;
-    b.out = out;
+    b.out = slices > 1 ? static_cast<void *>(part) : out;
     b.out_stride = out_stride;
     b.M = M;
     b.N = N;
     b.K = K;
-    const size_t lds = 4 * (size_t)kBigTile * sizeof(_Float16);
+    b.k_steps = K / kBigK / slices;
+    b.slice_floats = slices > 1 ? (size_t)M * N : 0;
+    const size_t lds = (size_t)kBigStages * kBigStage;
     static int granted[2];
     const void *fn = out_bf16 ? reinterpret_cast<const void *>(&gemm_q4_big_kernel<true>)
                               : reinterpret_cast<const void *>(&gemm_q4_big_kernel<false>);
@@ -400,11 +507,20 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
       if (e != hipSuccess) return e;
       granted[out_bf16 ? 1 : 0] = 1;
     }
-    dim3 grid((N + kBigN - 1) / kBigN, (M + kBigM - 1) / kBigM);
+    dim3 grid((N + kBigN - 1) / kBigN, (M + kBigM - 1) / kBigM, slices);
     if (out_bf16)
       hipLaunchKernelGGL((gemm_q4_big_kernel<true>), grid, dim3(512), lds, stream, b);
     else
       hipLaunchKernelGGL((gemm_q4_big_kernel<false>), grid, dim3(512), lds, stream, b);
+    e = hipGetLastError();
+    if (e != hipSuccess || slices == 1) return e;
+    dim3 sgrid((N / 4 + 255) / 256, M);
+    if (out_bf16)
+      hipLaunchKernelGGL((gemm_slice_sum_kernel<true>), sgrid, dim3(256), 0, stream, part, slices,
+                         b.slice_floats, M, N, out, out_stride);
+    else
+      hipLaunchKernelGGL((gemm_slice_sum_kernel<false>), sgrid, dim3(256), 0, stream, part, slices,
+                         b.slice_floats, M, N, out, out_stride);
     return hipGetLastError();
   }
   GemmArgs g;
