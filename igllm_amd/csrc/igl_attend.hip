@@ -363,8 +363,10 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
   }
 }
 
-// Merges chunk partials: one workgroup per (head, lane); chunk weights once in
-// LDS, then every thread sums its dims over the chunks in chunk order.
+// Merges chunk partials.  One workgroup per (head, lane, 64 dims): the
+// chunk weights e^(peak_c - peak) once in LDS, then thread (d, slice) sums
+// chunks c = slice (mod 4) of dim d with eight loads in flight, and the four
+// slices are added in a fixed order, so the result does not depend on timing.
 __global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out_all,
                                                            const float *part_peak_all,
                                                            const float *part_total_all,
@@ -374,55 +376,59 @@ __global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out
                                                            int head_size, float *blend_all,
                                                            int o_stride) {
   extern __shared__ float wgt[];  // [chunks]
-  __shared__ float red[256];
+  __shared__ float red[4];
+  __shared__ float slice_sum[4][64];
   const int h = blockIdx.x;
-  const int lane = blockIdx.y;
-  const int pos = (place_dev ? *place_dev : place0) + lane;
+  const int lane_id = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int pos = (place_dev ? *place_dev : place0) + lane_id;
   const int span = window > 0 ? min(pos + 1, window) : pos + 1;
   // the workgroups that saw part of this lane's span
   const int chunks = (span + kAttendChunk - 1) / kAttendChunk;
-  const size_t base = (size_t)lane * chunk_slots;
+  const size_t base = (size_t)lane_id * chunk_slots;
   const float *part_out = part_out_all + base * head_count * head_size;
   const float *part_peak = part_peak_all + base * head_count;
   const float *part_total = part_total_all + base * head_count;
-  float *blend_out = blend_all + (size_t)lane * o_stride;
+  float *blend_out = blend_all + (size_t)lane_id * o_stride;
   float peak = -INFINITY;
-  for (int c = threadIdx.x; c < chunks; c += blockDim.x)
-    peak = fmaxf(peak, part_peak[(size_t)c * head_count + h]);
-  red[threadIdx.x] = peak;
+  for (int c = tid; c < chunks; c += 256) peak = fmaxf(peak, part_peak[(size_t)c * head_count + h]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) peak = fmaxf(peak, __shfl_xor(peak, o));
+  if ((tid & 63) == 0) red[wave] = peak;
   __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + w]);
-    __syncthreads();
-  }
-  peak = red[0];
+  peak = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   __syncthreads();
   float total = 0.0f;
-  for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
+  for (int c = tid; c < chunks; c += 256) {
     const float m = part_peak[(size_t)c * head_count + h];
     const float wv = m == -INFINITY ? 0.0f : __expf(m - peak);
     wgt[c] = wv;
     total += wv * part_total[(size_t)c * head_count + h];
   }
-  red[threadIdx.x] = total;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) total += __shfl_xor(total, o);
+  if ((tid & 63) == 0) red[wave] = total;
+  __syncthreads();  // also: wgt complete
+  total = ((red[0] + red[1]) + red[2]) + red[3];
+  const float inv = total > 0.0f ? 1.0f / total : 0.0f;
+  const int d = blockIdx.z * 64 + (tid & 63);
+  const int slice = wave;
+  const float *col = part_out + (size_t)h * head_size + d;
+  const size_t step = (size_t)head_count * head_size;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int c = slice;
+  for (; c + 28 < chunks; c += 32) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[u] += wgt[c + 4 * u] * col[(size_t)(c + 4 * u) * step];
+  }
+  for (int u = 0; c < chunks; c += 4, ++u) acc[u & 7] += wgt[c] * col[(size_t)c * step];
+  slice_sum[slice][tid & 63] =
+      ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-    __syncthreads();
-  }
-  const float inv = red[0] > 0.0f ? 1.0f / red[0] : 0.0f;
-  for (int d = threadIdx.x; d < head_size; d += blockDim.x) {
-    float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
-    int c = 0;
-    for (; c + 4 <= chunks; c += 4) {
-      acc0 += wgt[c] * part_out[((size_t)c * head_count + h) * head_size + d];
-      acc1 += wgt[c + 1] * part_out[((size_t)(c + 1) * head_count + h) * head_size + d];
-      acc2 += wgt[c + 2] * part_out[((size_t)(c + 2) * head_count + h) * head_size + d];
-      acc3 += wgt[c + 3] * part_out[((size_t)(c + 3) * head_count + h) * head_size + d];
-    }
-    for (; c < chunks; ++c) acc0 += wgt[c] * part_out[((size_t)c * head_count + h) * head_size + d];
-    blend_out[(size_t)h * head_size + d] = ((acc0 + acc1) + (acc2 + acc3)) * inv;
-  }
+  if (slice == 0 && d < head_size)
+    blend_out[(size_t)h * head_size + d] =
+        (((slice_sum[0][tid] + slice_sum[1][tid]) + slice_sum[2][tid]) + slice_sum[3][tid]) * inv;
 }
 
 }  // namespace igl
@@ -499,7 +505,7 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
     return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || chunks == 1) return e;
-  hipLaunchKernelGGL(attend_merge_kernel, dim3(head_count, lanes), dim3(256),
+  hipLaunchKernelGGL(attend_merge_kernel, dim3(head_count, lanes, (head_size + 63) / 64), dim3(256),
                      chunks * sizeof(float), stream, a.part_out, a.part_peak, a.part_total, chunks,
                      place0, place_dev, window, head_count, head_size, blend_out, q_stride);
   return hipGetLastError();

@@ -298,10 +298,13 @@ __global__ __launch_bounds__(512) void gemm_q4_big_kernel(GemmBigArgs g) {
     const int c = (lane & 7) ^ (r & 7);
     a_src[i] = g.a16 + (size_t)min(m0 + r, g.M - 1) * g.K + k_first + 8 * c;
   }
-  // codes: wave w fills rows 32 w .. +31, lane l row 32 w + l / 2, half l & 1;
-  // gains (4 bytes a lane): the same rows, group l & 1
+  // codes: wave w fills rows 32 w .. +31, lane l row 32 w + l / 2, physical
+  // half l & 1, which holds logical half (l & 1) ^ (bit 3 of the row): rows
+  // n and n + 8 then read their eight bytes from different banks.  Gains
+  // (4 bytes a lane): the same rows, group l & 1.
   const int br = min(n0 + 32 * wave + (lane >> 1), g.N - 1);
-  const uint8_t *b_src = g.codes + (size_t)br * (size_t)g.row_stride + k_first / 2 + 16 * (lane & 1);
+  const uint8_t *b_src = g.codes + (size_t)br * (size_t)g.row_stride + k_first / 2 +
+                         16 * ((lane & 1) ^ ((lane >> 4) & 1));
   const float *s_src = g.gains + (size_t)br * g.gain_stride;
   const int s_first = k_first / 32;
   const int s_grp = lane & 1;
@@ -356,7 +359,8 @@ __global__ __launch_bounds__(512) void gemm_q4_big_kernel(GemmBigArgs g) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = wn * 64 + 16 * j + n;
-      braw[j] = *reinterpret_cast<const uint2_t *>(bs + row * 32 + 8 * gq);
+      const int half = (gq >> 1) ^ ((n >> 3) & 1);
+      braw[j] = *reinterpret_cast<const uint2_t *>(bs + row * 32 + 16 * half + 8 * (gq & 1));
       const _Float16 sh = (_Float16)gs[row * 2 + (gq >> 1)];
       bscale[j] = half2_t{sh, sh};
     }
