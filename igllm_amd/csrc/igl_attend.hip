@@ -125,6 +125,8 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
   __shared__ float wl[4][kAttendGroup];
   __shared__ float head_peak[kAttendGroup];
   __shared__ float head_norm[kAttendGroup];
+  // the query block as binary16 operands: [part hi / lo][head][HEAD / 8]
+  __shared__ half8_t qs[2][kAttendGroup][HEAD / 8];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -147,23 +149,25 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
   const int t0 = block * kAttendChunk + wave * kAttendTile;
   const bool live = t0 < span_count;
 
-  // ---- loads.  Query row n is head (n & 7), floats QD g + 8 s .. + 7.  Key
-  // rows n and n + 16 of the wave's 32, bytes QD g .. QD g + QD - 1 (operand
-  // order); value rows lane / 2, half lane & 1.  Rows past the span repeat
-  // the last one.
-  float qf[S][8];
+  // ---- loads.  The query block (8 heads x HEAD floats) is split among the
+  // workgroup's threads, eight floats each, to be converted once; key rows n
+  // and n + 16 of the wave's 32, bytes QD g .. QD g + QD - 1 (operand order);
+  // value rows lane / 2, half lane & 1.  Rows past the span repeat the last.
+  constexpr int kQItems = kAttendGroup * HEAD / 8 / kAttendThreads;  // 1 or 2
+  float qf[kQItems][8];
   {
-    const float *q = a.query + (size_t)lane_id * a.q_stride + (size_t)(head0 + (n & 7)) * HEAD + QD * g;
+    const float *qb = a.query + (size_t)lane_id * a.q_stride + (size_t)head0 * HEAD;
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
+    for (int i = 0; i < kQItems; ++i) {
+      const float *q = qb + 8 * (tid + kAttendThreads * i);
       if (QVEC) {
-        const float4_t u = *reinterpret_cast<const float4_t *>(q + 8 * s);
-        const float4_t v = *reinterpret_cast<const float4_t *>(q + 8 * s + 4);
-        qf[s][0] = u.x; qf[s][1] = u.y; qf[s][2] = u.z; qf[s][3] = u.w;
-        qf[s][4] = v.x; qf[s][5] = v.y; qf[s][6] = v.z; qf[s][7] = v.w;
+        const float4_t u = *reinterpret_cast<const float4_t *>(q);
+        const float4_t v = *reinterpret_cast<const float4_t *>(q + 4);
+        qf[i][0] = u.x; qf[i][1] = u.y; qf[i][2] = u.z; qf[i][3] = u.w;
+        qf[i][4] = v.x; qf[i][5] = v.y; qf[i][6] = v.z; qf[i][7] = v.w;
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qf[s][e] = q[8 * s + e];
+        for (int e = 0; e < 8; ++e) qf[i][e] = q[e];
       }
     }
   }
@@ -187,19 +191,25 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
     for (int q = 0; q < HEAD / 16; ++q) vr[q] = __builtin_nontemporal_load(src + q);
   }
 
-  // query operands: the hi part (rows n < 8) or the lo part of each head
-  half8_t qa[S];
-  {
-    const bool lo_part = n >= 8;
+  // query operands: x = hi + lo, each rounded to binary16 (|lo| <= 2^-11 |x|);
+  // row n of the score product is head n & 7, its hi part (n < 8) or lo part
 #pragma unroll
-    for (int s = 0; s < S; ++s)
+  for (int i = 0; i < kQItems; ++i) {
+    half8_t hi8, lo8;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float v = qf[s][e];
-        const _Float16 hi = (_Float16)v;
-        qa[s][e] = lo_part ? (_Float16)(v - (float)hi) : hi;
-      }
+    for (int e = 0; e < 8; ++e) {
+      const _Float16 hi = (_Float16)qf[i][e];
+      hi8[e] = hi;
+      lo8[e] = (_Float16)(qf[i][e] - (float)hi);
+    }
+    const int item = tid + kAttendThreads * i;  // head item / (HEAD / 8), chunk item % (HEAD / 8)
+    qs[0][item / (HEAD / 8)][item % (HEAD / 8)] = hi8;
+    qs[1][item / (HEAD / 8)][item % (HEAD / 8)] = lo8;
   }
+  __syncthreads();
+  half8_t qa[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) qa[s] = qs[n >> 3][n & 7][QD * g / 8 + s];
 
   // ---- scores.  After the half-wave sum, lane groups 0/2 hold heads 0-3 and
   // 1/3 heads 4-7 (row r of the group is head 4 (g & 1) + r), for positions
