@@ -375,8 +375,8 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
 
 // Merges chunk partials.  One workgroup per (head, lane, 64 dims): the
 // chunk weights e^(peak_c - peak) once in LDS, then thread (d, slice) sums
-// chunks c = slice (mod 4) of dim d with eight loads in flight, and the four
-// slices are added in a fixed order, so the result does not depend on timing.
+// chunks c = slice (mod 4) of dim d, 32 loads in flight, and the four slices
+// are added in a fixed order, so the result does not depend on timing.
 __global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out_all,
                                                            const float *part_peak_all,
                                                            const float *part_total_all,
@@ -426,13 +426,19 @@ __global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out
   const int slice = wave;
   const float *col = part_out + (size_t)h * head_size + d;
   const size_t step = (size_t)head_count * head_size;
+  // 32 chunks of the slice at a time, every load issued before the sums
+  // (past the end: the last chunk again, weight 0)
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  int c = slice;
-  for (; c + 28 < chunks; c += 32) {
+  for (int c0 = slice; c0 < chunks; c0 += 128) {
+    float v[32];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc[u] += wgt[c + 4 * u] * col[(size_t)(c + 4 * u) * step];
+    for (int u = 0; u < 32; ++u) v[u] = col[(size_t)min(c0 + 4 * u, chunks - 1) * step];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+      const int c = c0 + 4 * u;
+      acc[u & 7] += (c < chunks ? wgt[c] : 0.0f) * v[u];
+    }
   }
-  for (int u = 0; c < chunks; c += 4, ++u) acc[u & 7] += wgt[c] * col[(size_t)c * step];
   slice_sum[slice][tid & 63] =
       ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
