@@ -372,6 +372,8 @@ def main():
     for (N, K) in SHAPES:
         for M in LANES:
             rr = rot[(N, K)]
+            for i in range(10):
+                be.gemv_dev(rr.planes[i % COPIES], acts[(N, K, M)], K, M, outs[(N, K, M)], N)
             be.sync()
             be.mark()
             for i in range(100):
