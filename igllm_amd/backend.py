@@ -81,7 +81,10 @@ class CodePlane:
 
 
 def make_plane(codes: np.ndarray, gains: np.ndarray, K: int, group_size: int = 32,
-               code_bias: int = 8) -> CodePlane:
+               code_bias: int | None = None, bits: int = 4, code_flip: int = 0) -> CodePlane:
+    """A code plane over `codes` [N, row_stride] (bits-wide fields, low bits
+    first) and F32 `gains` [N, groups]; code_bias defaults to 2^(bits-1), the
+    export's offset (plane_bind_gemma, app_core.c:7931-7935)."""
     codes = np.ascontiguousarray(codes, dtype=np.uint8)
     gains = np.ascontiguousarray(gains, dtype=np.float32)
     N = codes.shape[0]
@@ -94,9 +97,9 @@ def make_plane(codes: np.ndarray, gains: np.ndarray, K: int, group_size: int = 3
     p.gain_data = _ptr(gains)
     p.gain_type = native.IGL_STORE_F32
     p.bias_data = None
-    p.bit_count = 4
-    p.code_bias = code_bias
-    p.code_flip = 0
+    p.bit_count = bits
+    p.code_bias = (1 << (bits - 1)) if code_bias is None else code_bias
+    p.code_flip = code_flip
     p.group_size = group_size
     p.group_count = gains.shape[1]
     return CodePlane(p, codes, gains)

@@ -131,27 +131,46 @@ fail:
 
 static int is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
-/* The code planes the kernels take (the BASELINE int4 group-32 planes and
- * their group-size relatives); everything else is refused, not emulated. */
+/* The code planes the kernels take: 2, 4 or 8-bit codes with the offset of
+ * half their range (code_bias = 2^(bits-1)) and any flip (the signed I8
+ * planes flip 128), F32 gains over groups of 32 times a power of two columns
+ * or one group a row; everything else is refused, not emulated. */
 static int plane_supported(const igl_plane *sheet) {
   if (!sheet || sheet->form != IGL_PLANE_CODE) return IGL_FAIL_SUPPORT;
-  if (sheet->bit_count != 4 || sheet->code_flip != 0 || sheet->bias_data) return IGL_FAIL_SUPPORT;
+  if (sheet->bit_count != 2 && sheet->bit_count != 4 && sheet->bit_count != 8) return IGL_FAIL_SUPPORT;
+  if (sheet->code_bias != 1 << (sheet->bit_count - 1) || sheet->code_flip < 0 ||
+      sheet->code_flip >= 1 << sheet->bit_count || sheet->bias_data)
+    return IGL_FAIL_SUPPORT;
   if (sheet->gain_type != IGL_STORE_F32) return IGL_FAIL_SUPPORT;
   if (sheet->row_count < 1 || sheet->col_count < 32 || (sheet->col_count & 31)) return IGL_FAIL_SUPPORT;
-  if (sheet->group_size < 32 || (sheet->group_size & 31) || !is_pow2(sheet->group_size / 32))
-    return IGL_FAIL_SUPPORT;
-  if (sheet->group_count * sheet->group_size < sheet->col_count ||
-      (sheet->group_count - 1) * sheet->group_size >= sheet->col_count)
-    return IGL_FAIL_SUPPORT;
-  if ((sheet->row_stride & 15u) || sheet->row_stride < (size_t)sheet->col_count / 2u)
+  if (sheet->group_count == 1) {
+    if (sheet->group_size < sheet->col_count) return IGL_FAIL_SUPPORT;
+  } else {
+    if (sheet->group_size < 32 || (sheet->group_size & 31) || !is_pow2(sheet->group_size / 32))
+      return IGL_FAIL_SUPPORT;
+    if (sheet->group_count * sheet->group_size < sheet->col_count ||
+        (sheet->group_count - 1) * sheet->group_size >= sheet->col_count)
+      return IGL_FAIL_SUPPORT;
+  }
+  if ((sheet->row_stride & 15u) ||
+      sheet->row_stride < ((size_t)sheet->col_count * (size_t)sheet->bit_count + 7u) / 8u)
     return IGL_FAIL_SUPPORT;
   return IGL_OKAY;
+}
+
+/* The tuned 4-bit kernels take codes stored value + 8 with no flip; every
+ * other code plane goes through the every-width form. */
+static int plane_is_q4(const igl_plane *sheet) {
+  return sheet->bit_count == 4 && sheet->code_flip == 0;
 }
 
 /* Room the GEMV's K-chunk partials need for this plane, over every lane count
  * a launch can carry. */
 static size_t plane_part_floats(const igl_desk_state *st, const igl_plane *sheet) {
   size_t most = 0;
+  if (!plane_is_q4(sheet))
+    return igl_gemv_code_part_floats(sheet->bit_count, IGL_GEMV_LANES, sheet->row_count,
+                                     sheet->col_count);
   for (int lanes = 1; lanes <= IGL_GEMV_LANES; ++lanes) {
     size_t need = igl_gemv_part_floats(lanes, sheet->row_count, sheet->col_count, st->lds_limit);
     if (need > most) most = need;
@@ -268,11 +287,21 @@ int igl_gemv_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev, i
     return IGL_FAIL_STATE;
   }
   dp = sheet->device;
+  if (!plane_is_q4(sheet)) {
+    igl_code_view view = igl_plane_view(sheet, dp->codes, dp->gains);
+    if (((uintptr_t)act_dev & 15u) || (lane_count > 1 && (act_stride & 3))) {
+      desk_fail(st, IGL_FAIL_ARGUMENT);
+      return IGL_FAIL_ARGUMENT;
+    }
+    return hip_check(st, igl_launch_gemv_codes(&view, act_dev, act_stride, lane_count, out_dev,
+                                               out_stride, sheet->row_count, sheet->col_count,
+                                               st->part_dev, st->stream));
+  }
   for (done = 0; done < lane_count; done += IGL_GEMV_LANES) {
     int lanes = lane_count - done < IGL_GEMV_LANES ? lane_count - done : IGL_GEMV_LANES;
     hipError_t e = igl_launch_gemv_q4(
         (const uint8_t *)dp->codes, (long long)sheet->row_stride, dp->gains, sheet->group_count,
-        sheet->group_size, sheet->code_bias, act_dev + (size_t)done * (size_t)act_stride,
+        igl_plane_group_shift(sheet), sheet->code_bias, act_dev + (size_t)done * (size_t)act_stride,
         act_stride, lanes, out_dev + (size_t)done * (size_t)out_stride, out_stride,
         sheet->row_count, sheet->col_count, st->part_dev, st->lds_limit, st->stream);
     if ((code = hip_check(st, e)) != IGL_OKAY) return code;
@@ -300,7 +329,8 @@ static int gemm_run(igl_desk *desk, const igl_plane *sheet, const void *act_dev,
   }
   return hip_check(st, igl_launch_gemm_q4(act_dev, act_bf16, act_stride, (const uint8_t *)dp->codes,
                                           (long long)sheet->row_stride, dp->gains,
-                                          sheet->group_count, sheet->group_size, sheet->code_bias,
+                                          sheet->group_count, igl_plane_group_shift(sheet),
+                                          sheet->code_bias,
                                           out_dev, out_bf16, out_stride, lane_count,
                                           sheet->row_count, sheet->col_count, st->gemm_dev,
                                           st->stream));
@@ -313,7 +343,7 @@ int igl_mat_mat_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev
   igl_desk_state *st = desk ? desk->state : NULL;
   int code;
   if (!st) return IGL_FAIL_STATE;
-  if (lane_count < IGL_GEMM_FLOOR)
+  if (lane_count < IGL_GEMM_FLOOR || (sheet && sheet->form == IGL_PLANE_CODE && !plane_is_q4(sheet)))
     return igl_gemv_dev(desk, sheet, act_dev, act_stride, lane_count, out_dev, out_stride);
   if ((code = plane_supported(sheet)) != IGL_OKAY || !sheet->device) {
     code = code != IGL_OKAY ? code : IGL_FAIL_STATE;

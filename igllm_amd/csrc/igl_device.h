@@ -268,6 +268,127 @@ __device__ __forceinline__ float digit_sum(const int (&t)[DIG]) {
   return __builtin_fmaf((float)hi, 4096.0f, (float)lo);
 }
 
+// ---- the other code widths on the same digit form -------------------------
+//
+// The staged q is the same 23-bit integer for every code width (P = 22); how
+// its digits are laid out in LDS follows the codes it meets:
+//   DIGITS_NIBBLE  4-bit codes: six hex digits, nibble e of a dword element e
+//                  of its eight (the codes' own order);
+//   DIGITS_PAIRS   2-bit codes: the same six hex digits, but the dwords of a
+//                  unit hold elements 0,2,..,14 / 1,3,..,15 / 16,18,..,30 /
+//                  17,19,..,31, the order in which `w & 0x33333333` and
+//                  `(w >> 2) & 0x33333333` spread a dword of sixteen 2-bit
+//                  codes into two dwords of nibbles;
+//   DIGITS_BYTE    8-bit codes: three base-256 digits, q + 0x808080, byte e
+//                  of a dword element e of its four, for v_dot4_i32_i8.
+// Every form fills six 16-byte slots a unit: uint4 dig[(m 6 + s) units + u].
+// Nibble forms: slot s = digit j, dword k = the k-th eight elements.  Byte
+// form: slot 2 j + h = digit j of elements 16 h .. 16 h + 15, four a dword.
+// The pair form also stores qsum[m units + u] = sum_e q_e, which takes the
+// code bias out of a dot against unsigned codes: sum (c - b) q = sum c q - b qsum.
+enum { DIGITS_NIBBLE = 0, DIGITS_PAIRS = 1, DIGITS_BYTE = 2 };
+
+template <int BITS>
+struct CodeForm {
+  static_assert(BITS == 2 || BITS == 4 || BITS == 8, "2, 4 or 8-bit codes");
+  static constexpr int kDigits = BITS == 2 ? DIGITS_PAIRS : BITS == 8 ? DIGITS_BYTE : DIGITS_NIBBLE;
+  static constexpr int kUnitsPerSlot2 = 256 / (32 * BITS);  // twice the units a 16-byte slot holds
+};
+
+constexpr int kDigitP = 22;  // |q| <= 2^22 for every form
+constexpr uint32_t kByteBias = 0x808080u;
+
+// Digits 0..2 of four elements in byte form: byte e of d[j] is base-256
+// digit j of element e, as a signed byte (d - 128).
+__device__ __forceinline__ void bytes_of_four(uint32_t v0, uint32_t v1, uint32_t v2, uint32_t v3,
+                                              uint32_t (&d)[3]) {
+  const uint32_t t01 = __builtin_amdgcn_perm(v1, v0, 0x05010400u);   // v0.b0 v1.b0 v0.b1 v1.b1
+  const uint32_t t23 = __builtin_amdgcn_perm(v3, v2, 0x05010400u);
+  const uint32_t t01h = __builtin_amdgcn_perm(v1, v0, 0x07030602u);  // v0.b2 v1.b2 v0.b3 v1.b3
+  const uint32_t t23h = __builtin_amdgcn_perm(v3, v2, 0x07030602u);
+  d[0] = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
+  d[1] = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
+  d[2] = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u) ^ 0x80808080u;
+}
+
+// sum_j t[j] 256^j: |t[j]| <= 16 * 128 * 128 per half unit, so t0 + 256 t1
+// is an exact int, and the float is formed with two roundings.
+__device__ __forceinline__ float byte_digit_sum(int t0, int t1, int t2) {
+  return __builtin_fmaf((float)t2, 65536.0f, (float)(t0 + 256 * t1));
+}
+
+// sum_j t[j] 16^j - bias qsum as an exact int (|sum c q| <= 3 * 2^22 * 32 and
+// |bias qsum| <= 2 * 2^27 for 2-bit codes), rounded once to float.
+__device__ __forceinline__ float pair_digit_sum(const int (&t)[6], int bias_qsum) {
+  uint32_t v = (uint32_t)t[5];
+#pragma unroll
+  for (int j = 4; j >= 0; --j) v = (v << 4) + (uint32_t)t[j];
+  return (float)(int)(v - (uint32_t)bias_qsum);
+}
+
+// One eight-element group (lane m, group gg of K / 8) into LDS in form FORM.
+// The four threads of a quad hold one unit's four groups and all four must
+// run it (the pair form also trades elements between threads 0-1 and 2-3).
+template <int FORM>
+__device__ __forceinline__ void digit_group_store_form(const float (&xin)[8], int m, int gg, int units,
+                                                       uint4_t *dig, int *down, int *qsum) {
+  float peak = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) peak = fmaxf(peak, fabsf(xin[e]));
+  peak = fmaxf(peak, dpp_move<0xB1>(peak));  // quad_perm [1,0,3,2]
+  peak = fmaxf(peak, dpp_move<0x4E>(peak));  // quad_perm [2,3,0,1]
+  const int E = __builtin_amdgcn_frexp_expf(peak);
+  const int up = kDigitP - E;
+  const int u = gg >> 2, dw = gg & 3;
+  uint32_t *base = reinterpret_cast<uint32_t *>(dig);
+  float x[8];
+  if constexpr (FORM == DIGITS_PAIRS) {
+    // Thread dw even holds elements 16h + 0..7 and wants the even ones of
+    // 16h + 0..15; its partner (dw + 1) holds 16h + 8..15 and wants the odd.
+    const bool odd = dw & 1;
+    float recv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) recv[i] = dpp_move<0xB1>(odd ? xin[2 * i] : xin[2 * i + 1]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = odd ? recv[i] : xin[2 * i];
+      x[4 + i] = odd ? xin[2 * i + 1] : recv[i];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = xin[e];
+  }
+  if constexpr (FORM == DIGITS_BYTE) {
+    uint32_t v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      v[e] = __float_as_uint(__builtin_amdgcn_ldexpf(x[e], up) + 12582912.0f) - (0x4B400000u - kByteBias);
+    uint32_t lo[3], hi[3];
+    bytes_of_four(v[0], v[1], v[2], v[3], lo);
+    bytes_of_four(v[4], v[5], v[6], v[7], hi);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      uint32_t *slot = base + ((m * 6 + 2 * j + (dw >> 1)) * units + u) * 4 + 2 * (dw & 1);
+      *reinterpret_cast<uint2_t *>(slot) = uint2_t{lo[j], hi[j]};
+    }
+  } else {
+    uint32_t d[6];
+    digits_of_eight<6>(x, up, d);
+#pragma unroll
+    for (int j = 0; j < 6; ++j) base[((m * 6 + j) * units + u) * 4 + dw] = d[j];
+    if constexpr (FORM == DIGITS_PAIRS) {
+      int s = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        s += (int)(__float_as_uint(__builtin_amdgcn_ldexpf(x[e], up) + 12582912.0f) - 0x4B400000u);
+      s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, true);
+      s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, true);
+      if (dw == 0) qsum[m * units + u] = s;
+    }
+  }
+  if (dw == 0) down[m * units + u] = E - kDigitP;
+}
+
 // Staging x in digit form, for a workgroup of 256 threads.  Eight-element
 // group g of lane m (g < K / 8) is thread (m K / 8 + g) % 256's item
 // (m K / 8 + g) / 256; a thread holds GPT items.  The LDS form: uint4
@@ -363,6 +484,39 @@ __device__ __forceinline__ void digit_store_lds(const float *xs, int K, uint4_t 
     const float4_t q = *reinterpret_cast<const float4_t *>(xs + 8 * g + 4);
     const float x[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
     digit_group_store<DIG>(x, 0, g, units, dig, down);
+  }
+  __syncthreads();
+}
+
+// Items of M lanes into LDS in form FORM; ends with a barrier every thread
+// reaches.  Item i of a thread: digit_item.
+template <int M, int GPT, int FORM>
+__device__ __forceinline__ void digit_store_form(const DigitLoads<GPT> &h, int K, uint4_t *dig,
+                                                 int *down, int *qsum) {
+  const int units = K >> 5;
+  const int per_lane = K >> 3;
+#pragma unroll
+  for (int i = 0; i < GPT; ++i) {
+    const int g = digit_item(i, M * per_lane);
+    const int m = M == 1 ? 0 : M == 2 ? (g >= per_lane ? 1 : 0) : g / per_lane;
+    digit_group_store_form<FORM>(h.x[i], m, g - m * per_lane, units, dig, down, qsum);
+  }
+  __syncthreads();
+}
+
+// One lane of x already in LDS (`xs`, K floats, 16-byte aligned) into form
+// FORM; ends with a barrier every thread reaches.
+template <int FORM>
+__device__ __forceinline__ void digit_store_lds_form(const float *xs, int K, uint4_t *dig, int *down,
+                                                     int *qsum) {
+  const int units = K >> 5;
+  const int groups = K >> 3;
+  for (int i = 0; i * 256 < groups; ++i) {
+    const int g = digit_item(i, groups);
+    const float4_t p = *reinterpret_cast<const float4_t *>(xs + 8 * g);
+    const float4_t q = *reinterpret_cast<const float4_t *>(xs + 8 * g + 4);
+    const float x[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
+    digit_group_store_form<FORM>(x, 0, g, units, dig, down, qsum);
   }
   __syncthreads();
 }

@@ -658,12 +658,13 @@ static void group_add(igl_engine *e, eng_group *g, const igl_plane *p, float *ou
   g->count++;
 }
 
-/* Planes that can share one launch: the same width and group size, K within
- * the register form, 4-row multiples between segments. */
+/* Planes that can share one launch: 4-bit, the same width and groups, K
+ * within the register form, 4-row multiples between segments. */
 static int group_fits(const eng_group *g, const igl_plane *const *p, int mode) {
   for (int i = 0; i < g->count; ++i) {
     if (p[i]->col_count != p[0]->col_count || p[i]->group_size != p[0]->group_size ||
-        p[i]->code_bias != p[0]->code_bias || p[i]->col_count > 8192)
+        p[i]->group_count != p[0]->group_count || p[i]->code_bias != p[0]->code_bias ||
+        p[i]->bit_count != 4 || p[i]->code_flip != 0 || p[i]->col_count > 8192)
       return 0;
     if (mode == IGL_GEMV_SEGMENTS && i + 1 < g->count && p[i]->row_count % 4) return 0;
   }
@@ -673,7 +674,7 @@ static int group_fits(const eng_group *g, const igl_plane *const *p, int mode) {
 static int group_run(igl_engine *e, const eng_group *g, const igl_plane *first, int mode,
                      const float *act, const float *mul, const igl_gemv_prologue *pro) {
   RUN(igl_launch_gemv_group(mode, g->count, g->codes, g->row_stride, g->gains, g->gain_stride,
-                            g->rows, g->out, first->group_size, first->code_bias, act,
+                            g->rows, g->out, igl_plane_group_shift(first), first->code_bias, act,
                             first->col_count, mul, pro, e->stream));
   return IGL_OKAY;
 }
@@ -819,7 +820,7 @@ static int run_pass(igl_engine *e, int bound, int lanes, int logits) {
   {
     const igl_plane *p = &e->embed;
     RUN(igl_launch_gather_rows(dev_codes(e, p), (long long)p->row_stride, dev_gains(e, p),
-                               p->group_count, p->group_size, p->code_bias, H, p->row_count,
+                               p->group_count, igl_plane_group_shift(p), p->code_bias, H, p->row_count,
                                e->ids_dev, lanes, (float)sqrt((double)H), e->state, H, st));
   }
   /* per-layer inputs */
@@ -828,7 +829,7 @@ static int run_pass(igl_engine *e, int bound, int lanes, int logits) {
     const int chunk_all = e->layers * e->ple;
     OKAY(project(e, &e->ple_lift, e->state, H, lanes, e->ple_room, e->ple_stride));
     RUN(igl_launch_gather_rows(dev_codes(e, p), (long long)p->row_stride, dev_gains(e, p),
-                               p->group_count, p->group_size, p->code_bias, chunk_all, p->row_count,
+                               p->group_count, igl_plane_group_shift(p), p->code_bias, chunk_all, p->row_count,
                                e->ids_dev, lanes, (float)sqrt((double)e->ple), e->ple_seed,
                                e->ple_stride, st));
     RUN(igl_launch_ple_mix(e->ple_room, e->ple_stride, e->ple_seed, e->ple_stride, e->ple_norm,

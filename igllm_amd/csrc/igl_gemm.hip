@@ -36,7 +36,7 @@ struct GemmArgs {
   long long row_stride;
   const float *gains;
   int gain_stride;
-  int group_shift;        // log2(group_size / 32)
+  int group_shift;        // gain of unit u: u >> group_shift (31: one gain a row)
   float code_bias;
   void *out;              // [M][out_stride] of bf16 or fp32
   int out_stride;
@@ -473,7 +473,7 @@ extern "C" size_t igl_gemm_work_bytes(int M, int N, int K) {
 
 extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride,
                                          const uint8_t *codes, long long row_stride,
-                                         const float *gains, int gain_stride, int group_size,
+                                         const float *gains, int gain_stride, int group_shift,
                                          int code_bias, void *out, int out_bf16, int out_stride,
                                          int M, int N, int K, void *work, hipStream_t stream) {
   if (igl_gemm_work_bytes(M, N, K) && work) {
@@ -493,7 +493,7 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
     b.row_stride = row_stride;
     b.gains = gains;
     b.gain_stride = gain_stride;
-    b.group_shift = __builtin_ctz((unsigned)(group_size / 32));
+    b.group_shift = group_shift;
     b.code_bias = (float)code_bias;
     b.out = slices > 1 ? static_cast<void *>(part) : out;
     b.out_stride = out_stride;
@@ -534,7 +534,7 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
   g.row_stride = row_stride;
   g.gains = gains;
   g.gain_stride = gain_stride;
-  g.group_shift = __builtin_ctz((unsigned)(group_size / 32));
+  g.group_shift = group_shift;
   g.code_bias = (float)code_bias;
   g.out = out;
   g.out_stride = out_stride;

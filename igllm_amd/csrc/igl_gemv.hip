@@ -35,7 +35,7 @@ struct GemvArgs {
   long long row_stride;   // bytes between rows of codes
   const float *gains;     // [N][gain_stride]
   int gain_stride;        // groups per row
-  int group_shift;        // log2(group_size / 32)
+  int group_shift;        // gain of unit u: u >> group_shift (31: one gain a row)
   const float *act;       // lanes of K floats, act_stride apart
   int act_stride;
   float *out;             // lanes of N floats, out_stride apart (grid K-split: partials)
@@ -515,6 +515,233 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
     float total = 0.0f;
     for (int k = 0; k < (1 << ks_log); ++k) total += red[wave + k][r][m];
     if (row0 + r < a.N) a.out[(size_t)m * a.out_stride + row0 + r] = total;
+  }
+}
+
+// ---- the integer-dot form for every code width (2, 4, 8 bits) --------------
+//
+// The shipped export's other planes: 2-bit (four codes a byte, low bits
+// first, value + 2), 8-bit signed I8 (code_flip 128: the byte itself is the
+// value) and one gain a row (group_shift 31).  The same layout as
+// gemv_q4_dot_kernel, over 16-byte slots of codes instead of units: a slot
+// is two units of 2-bit codes, one of 4-bit codes, half of one of 8-bit codes.
+// Per row and slot a lane spends
+//   2-bit: 8 and/shift ops to spread 64 codes into nibbles, 48 v_dot8_i32_i4;
+//   4-bit: 4 xors, 24 v_dot8_i32_i4;
+//   8-bit: 4 xors, 12 v_dot4_i32_i8,
+// on exact integer sums, then as before one float per unit (half unit at 8
+// bits), times 2^(E - P) and the gain.  2-bit codes are dotted unsigned and
+// their bias leaves through the staged activation sum (qsum); 4- and 8-bit
+// codes are made signed by one xor with (code_flip ^ code_bias) replicated.
+// `blockIdx.y` takes a K-chunk of `chunk_cols` columns (a multiple of 128);
+// chunks write partials [chunk][M][N] that gemv_chunk_sum_kernel adds.
+// `lanes` <= M: lanes past it reread the last lane and are not stored.
+struct GemvCodeArgs {
+  const uint8_t *codes;
+  long long row_stride;
+  const float *gains;
+  int gain_stride;
+  int group_shift;        // gain of unit u: u >> group_shift (31: one gain a row)
+  const float *act;       // 16-byte aligned, act_stride % 4 == 0
+  int act_stride;
+  float *out;             // [lanes][out_stride], or partials [chunk][M][N]
+  int out_stride;
+  int lanes;
+  int N, K;
+  int chunk_cols;
+  int ks_log;             // log2 of the waves that share a row tile
+  uint32_t code_xor;      // 4, 8-bit: makes a dword of codes signed values; 2-bit: undoes the flip
+  int code_bias;          // 2-bit: taken off through qsum
+};
+
+__host__ __device__ constexpr size_t gemv_code_lds_bytes(int M, int units) {
+  return (size_t)M * units * (6 * 16 + 8);
+}
+
+template <int BITS, int M, int R, int UPL, int GPT>
+__global__ __launch_bounds__(kGemvThreads) void gemv_code_dot_kernel(GemvCodeArgs a) {
+  constexpr int FORM = CodeForm<BITS>::kDigits;
+  extern __shared__ uint4_t lds_dig[];
+  __shared__ float red[4][R][M];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ks_log = __builtin_amdgcn_readfirstlane(a.ks_log);
+  const int tile = blockIdx.x * (4 >> ks_log) + (wave >> ks_log);
+  const int ks = wave & ((1 << ks_log) - 1);
+  const int row0 = tile * R;
+  const int col0 = blockIdx.y * a.chunk_cols;
+  const int cols = min(a.chunk_cols, a.K - col0);
+  const int units = cols >> 5;
+  const int slots = (cols * BITS + 127) >> 7;
+  const int s_end = (slots * (ks + 1)) >> ks_log;
+  const int s_first = ((slots * ks) >> ks_log) + lane;
+  const int unit0 = col0 >> 5;
+  uint4_t *dig = lds_dig;
+  int *down = reinterpret_cast<int *>(dig + M * 6 * units);
+  int *qsum = down + M * units;
+  constexpr int kSub = BITS == 2 ? 2 : 1;  // units a slot's gains cover
+
+  // Activations first, then gains, then codes, all unconditional (clamped).
+  DigitLoads<GPT> held;
+  {
+    const int last = a.lanes - 1;
+    const int per_lane = cols >> 3;
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int g = digit_item(i, M * per_lane);
+      const int m = M == 1 ? 0 : g / per_lane;
+      const float *src = a.act + (size_t)min(m, last) * a.act_stride + col0 + 8 * (g - m * per_lane);
+      const float4_t p = *reinterpret_cast<const float4_t *>(src);
+      const float4_t q = *reinterpret_cast<const float4_t *>(src + 4);
+      held.x[i][0] = p.x; held.x[i][1] = p.y; held.x[i][2] = p.z; held.x[i][3] = p.w;
+      held.x[i][4] = q.x; held.x[i][5] = q.y; held.x[i][6] = q.z; held.x[i][7] = q.w;
+    }
+  }
+  uint4_t w[UPL][R];
+  float s[UPL][R][kSub];
+  bool live[UPL][kSub];
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const int sl = min(s_first + kWave * j, slots - 1);
+#pragma unroll
+    for (int h = 0; h < kSub; ++h) {
+      const int u_raw = BITS == 2 ? 2 * sl + h : BITS == 8 ? sl >> 1 : sl;
+      live[j][h] = row0 < a.N && s_first + kWave * j < s_end && u_raw < units;
+      const int u = min(u_raw, units - 1);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, a.N - 1);
+        s[j][r][h] = a.gains[(size_t)row * (size_t)a.gain_stride + ((unsigned)(unit0 + u) >> a.group_shift)];
+      }
+    }
+  }
+  const uint8_t *code0 = a.codes + (size_t)(col0 / 8) * BITS;
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const int sl = min(s_first + kWave * j, slots - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min(row0 + r, a.N - 1);
+      w[j][r] = __builtin_nontemporal_load(
+          reinterpret_cast<const uint4_t *>(code0 + (size_t)row * (size_t)a.row_stride) + sl);
+    }
+  }
+  digit_store_form<M, GPT, FORM>(held, cols, dig, down, qsum);
+
+  float acc[R][M];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+  const uint32_t cx = a.code_xor;
+#pragma unroll
+  for (int uj = 0; uj < UPL; ++uj) {
+    const int sl = min(s_first + kWave * uj, slots - 1);
+    if constexpr (BITS == 4) {
+      const int u = sl;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        uint4_t dd[6];
+#pragma unroll
+        for (int j = 0; j < 6; ++j) dd[j] = dig[(m * 6 + j) * units + u];
+        const int shift = down[m * units + u];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint4_t c = w[uj][r] ^ cx;
+          int t[6];
+#pragma unroll
+          for (int j = 0; j < 6; ++j) t[j] = 0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < 6; ++j) t[j] = __builtin_amdgcn_sdot8((int)c[q], (int)dd[j][q], t[j], false);
+          const float gain = live[uj][0] ? s[uj][r][0] : 0.0f;
+          acc[r][m] = __builtin_fmaf(gain, __builtin_amdgcn_ldexpf(digit_sum<6>(t), shift), acc[r][m]);
+        }
+      }
+    } else if constexpr (BITS == 2) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int u = min(2 * sl + h, units - 1);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          uint4_t dd[6];
+#pragma unroll
+          for (int j = 0; j < 6; ++j) dd[j] = dig[(m * 6 + j) * units + u];
+          const int shift = down[m * units + u];
+          const int bq = a.code_bias * qsum[m * units + u];
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const uint32_t c0 = w[uj][r][2 * h] ^ cx, c1 = w[uj][r][2 * h + 1] ^ cx;
+            const uint32_t n[4] = {c0 & 0x33333333u, (c0 >> 2) & 0x33333333u, c1 & 0x33333333u,
+                                   (c1 >> 2) & 0x33333333u};
+            int t[6];
+#pragma unroll
+            for (int j = 0; j < 6; ++j) t[j] = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+              for (int j = 0; j < 6; ++j) t[j] = __builtin_amdgcn_sdot8((int)n[q], (int)dd[j][q], t[j], false);
+            const float gain = live[uj][h] ? s[uj][r][h] : 0.0f;
+            acc[r][m] = __builtin_fmaf(gain, __builtin_amdgcn_ldexpf(pair_digit_sum(t, bq), shift), acc[r][m]);
+          }
+        }
+      }
+    } else {
+      const int u = sl >> 1, hf = sl & 1;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        uint4_t dd[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) dd[j] = dig[(m * 6 + 2 * j + hf) * units + u];
+        const int shift = down[m * units + u];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint4_t c = w[uj][r] ^ cx;
+          int t[3] = {0, 0, 0};
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) t[j] = __builtin_amdgcn_sdot4((int)c[q], (int)dd[j][q], t[j], false);
+          const float gain = live[uj][0] ? s[uj][r][0] : 0.0f;
+          acc[r][m] = __builtin_fmaf(gain, __builtin_amdgcn_ldexpf(byte_digit_sum(t[0], t[1], t[2]), shift),
+                                     acc[r][m]);
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = wave_sum_to_last(acc[r][m]);
+
+  float *dst = a.out + (size_t)blockIdx.y * (size_t)a.lanes * (size_t)a.out_stride;
+  if (ks_log == 0) {
+    if (lane == 63) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (row0 + r < a.N)
+#pragma unroll
+          for (int m = 0; m < M; ++m)
+            if (m < a.lanes) dst[(size_t)m * a.out_stride + row0 + r] = acc[r][m];
+    }
+    return;
+  }
+  if (lane == 63) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) red[wave][r][m] = acc[r][m];
+  }
+  __syncthreads();
+  if (ks == 0 && lane < R * M) {
+    const int r = lane / M;
+    const int m = lane - r * M;
+    float total = 0.0f;
+    for (int k = 0; k < (1 << ks_log); ++k) total += red[wave + k][r][m];
+    if (row0 + r < a.N && m < a.lanes) dst[(size_t)m * a.out_stride + row0 + r] = total;
   }
 }
 
@@ -1252,13 +1479,13 @@ extern "C" int igl_gemv_chunk_cols(int lanes, int K, int lds_limit) {
 extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_t *const *codes,
                                             const long long *row_stride,
                                             const float *const *gains, const int *gain_stride,
-                                            const int *rows, float *const *out, int group_size,
+                                            const int *rows, float *const *out, int group_shift,
                                             int code_bias, const float *act, int K,
                                             const float *mul, const igl_gemv_prologue *pro,
                                             hipStream_t stream) {
   GemvGroupArgs a;
   const int units = K / 32;
-  if (segments < 1 || segments > 3 || K % 32 || units > 4 * kWave || group_size < 32)
+  if (segments < 1 || segments > 3 || K % 32 || units > 4 * kWave || group_shift < 0)
     return hipErrorInvalidValue;
   if (pro && (K > 4096 || !pro->state_in || (pro->lift && (!pro->state_out || !pro->lift_gain ||
                                                             pro->state_out == pro->state_in))))
@@ -1289,7 +1516,7 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
   }
   a.segments = segments;
   a.tiles = mode == GEMV_GELU_PAIR ? (rows[0] + 1) / 2 : (total + 3) / 4;
-  a.group_shift = __builtin_ctz((unsigned)(group_size / 32));
+  a.group_shift = group_shift;
   a.act = act;
   a.act_vec = (((uintptr_t)act) & 15u) == 0 ? 1 : 0;
   a.K = K;
@@ -1340,6 +1567,137 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
   return hipGetLastError();
 }
 
+// ---- every code width: gemv_code_dot_kernel --------------------------------
+
+namespace igl {
+
+// Lanes a launch of the every-width form carries (template M).
+static int code_launch_lanes(int lanes) { return lanes <= 2 ? lanes : 4; }
+
+// Columns of one K-chunk: a multiple of 128 with M cols <= 16384 (eight
+// staged groups a thread) and at most 512 slots a row.
+static int code_chunk_cols(int bits, int M, int K) {
+  int most = (16384 / M < 65536 / bits ? 16384 / M : 65536 / bits) / 128 * 128;
+  const int chunks = (K + most - 1) / most;
+  const int per = (K + chunks - 1) / chunks;
+  return (per + 127) / 128 * 128;
+}
+
+template <int BITS, int M, int UPL, int GPT>
+static hipError_t gemv_code_launch4(const GemvCodeArgs &a, dim3 grid, size_t lds, hipStream_t stream) {
+  hipLaunchKernelGGL((gemv_code_dot_kernel<BITS, M, 4, UPL, GPT>), grid, dim3(kGemvThreads), lds, stream, a);
+  return hipGetLastError();
+}
+
+template <int BITS, int M>
+static hipError_t gemv_code_launch_m(const GemvCodeArgs &a, int upl, int gpt, dim3 grid, size_t lds,
+                                     hipStream_t stream) {
+  if (upl == 1) {
+    switch (gpt) {
+      case 1: return gemv_code_launch4<BITS, M, 1, 1>(a, grid, lds, stream);
+      case 2: return gemv_code_launch4<BITS, M, 1, 2>(a, grid, lds, stream);
+      case 4: return gemv_code_launch4<BITS, M, 1, 4>(a, grid, lds, stream);
+      default: return gemv_code_launch4<BITS, M, 1, 8>(a, grid, lds, stream);
+    }
+  }
+  switch (gpt) {
+    case 1: return gemv_code_launch4<BITS, M, 2, 1>(a, grid, lds, stream);
+    case 2: return gemv_code_launch4<BITS, M, 2, 2>(a, grid, lds, stream);
+    case 4: return gemv_code_launch4<BITS, M, 2, 4>(a, grid, lds, stream);
+    default: return gemv_code_launch4<BITS, M, 2, 8>(a, grid, lds, stream);
+  }
+}
+
+template <int BITS>
+static hipError_t gemv_code_launch_bits(const GemvCodeArgs &a, int M, int upl, int gpt, dim3 grid,
+                                        size_t lds, hipStream_t stream) {
+  switch (M) {
+    case 1: return gemv_code_launch_m<BITS, 1>(a, upl, gpt, grid, lds, stream);
+    case 2: return gemv_code_launch_m<BITS, 2>(a, upl, gpt, grid, lds, stream);
+    default: return gemv_code_launch_m<BITS, 4>(a, upl, gpt, grid, lds, stream);
+  }
+}
+
+}  // namespace igl
+
+extern "C" size_t igl_gemv_code_part_floats(int bit_count, int lanes, int N, int K) {
+  size_t most = 0;
+  for (int l = 1; l <= (lanes < 4 ? lanes : 4); ++l) {
+    const int M = code_launch_lanes(l);
+    const int cols = code_chunk_cols(bit_count, M, K);
+    const size_t chunks = (size_t)((K + cols - 1) / cols);
+    const size_t need = chunks > 1 ? chunks * (size_t)l * (size_t)N : 0;
+    if (need > most) most = need;
+  }
+  return most;
+}
+
+// y = W x for any number of lanes over a 2, 4 or 8-bit code plane, four
+// lanes a launch.  Activations 16-byte aligned with act_stride % 4 == 0;
+// `part` holds igl_gemv_code_part_floats(bits, lanes, N, K) floats.
+extern "C" hipError_t igl_launch_gemv_codes(const igl_code_view *v, const float *act, int act_stride,
+                                            int lanes, float *out, int out_stride, int N, int K,
+                                            float *part, hipStream_t stream) {
+  const int bits = v->bit_count;
+  if ((bits != 2 && bits != 4 && bits != 8) || K % 32 || (((uintptr_t)act) & 15u) ||
+      (lanes > 1 && (act_stride & 3)))
+    return hipErrorInvalidValue;
+  GemvCodeArgs a;
+  a.codes = v->codes;
+  a.row_stride = v->row_stride;
+  a.gains = v->gains;
+  a.gain_stride = v->gain_stride;
+  a.group_shift = v->group_shift;
+  a.N = N;
+  a.K = K;
+  a.code_bias = v->code_bias;
+  const uint32_t field = bits == 2 ? (uint32_t)(v->code_flip & 3)
+                                   : (uint32_t)((v->code_flip ^ v->code_bias) & ((1 << bits) - 1));
+  a.code_xor = field * (bits == 2 ? 0x55555555u : bits == 4 ? 0x11111111u : 0x01010101u);
+  for (int done = 0; done < lanes; done += 4) {
+    const int l = lanes - done < 4 ? lanes - done : 4;
+    const int M = code_launch_lanes(l);
+    const int cols = code_chunk_cols(bits, M, K);
+    const int chunks = (K + cols - 1) / cols;
+    const int slots = cols * bits / 128;
+    const int upl = slots > 4 * kWave ? 2 : 1;
+    const int tiles = (N + 3) / 4;
+    int ksplit = 1;
+    while (ksplit < 4 && (slots > ksplit * kWave * upl ||
+                          (tiles * ksplit * chunks < 2048 && slots / (ksplit * 2) >= 32 * upl)))
+      ksplit *= 2;
+    const int items = (M * (cols >> 3) + kGemvThreads - 1) / kGemvThreads;
+    const int gpt = items <= 1 ? 1 : items <= 2 ? 2 : items <= 4 ? 4 : 8;
+    a.act = act + (size_t)done * (size_t)act_stride;
+    a.act_stride = act_stride;
+    a.lanes = l;
+    a.chunk_cols = cols;
+    a.ks_log = ksplit == 1 ? 0 : ksplit == 2 ? 1 : 2;
+    if (chunks > 1) {
+      if (!part) return hipErrorInvalidValue;
+      a.out = part;
+      a.out_stride = N;
+    } else {
+      a.out = out + (size_t)done * (size_t)out_stride;
+      a.out_stride = out_stride;
+    }
+    const int per_block = 4 / ksplit;
+    const dim3 grid((tiles + per_block - 1) / per_block, chunks);
+    const size_t lds = gemv_code_lds_bytes(M, cols / 32);
+    hipError_t e = bits == 2   ? gemv_code_launch_bits<2>(a, M, upl, gpt, grid, lds, stream)
+                   : bits == 4 ? gemv_code_launch_bits<4>(a, M, upl, gpt, grid, lds, stream)
+                               : gemv_code_launch_bits<8>(a, M, upl, gpt, grid, lds, stream);
+    if (e != hipSuccess) return e;
+    if (chunks > 1) {
+      const int total = l * N;
+      hipLaunchKernelGGL(gemv_chunk_sum_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, part,
+                         chunks, l, N, out + (size_t)done * (size_t)out_stride, out_stride);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+  }
+  return hipSuccess;
+}
+
 // Floats of K-chunk partials a launch of `lanes` lanes over an N x K plane
 // writes (0 when it needs none).
 extern "C" size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit) {
@@ -1356,7 +1714,7 @@ extern "C" size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit) {
 // when the plane needs more than one K-chunk, and may be NULL otherwise;
 // `lds_limit` is the device's LDS bytes per workgroup.
 extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_stride,
-                                         const float *gains, int gain_stride, int group_size,
+                                         const float *gains, int gain_stride, int group_shift,
                                          int code_bias, const float *act, int act_stride,
                                          int lanes, float *out, int out_stride, int N, int K,
                                          float *part, int lds_limit, hipStream_t stream) {
@@ -1365,7 +1723,7 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
   a.row_stride = row_stride;
   a.gains = gains;
   a.gain_stride = gain_stride;
-  a.group_shift = __builtin_ctz((unsigned)(group_size / 32));
+  a.group_shift = group_shift;
   a.act = act;
   a.act_stride = act_stride;
   a.N = N;

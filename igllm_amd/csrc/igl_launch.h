@@ -14,6 +14,48 @@
 extern "C" {
 #endif
 
+/* A code plane as the kernels read it: 32-column unit u of a row takes gain
+ * u >> group_shift of that row (group_shift 31: one gain a row); a code's
+ * value is (code ^ code_flip) - code_bias. */
+typedef struct igl_code_view {
+  const uint8_t *codes;
+  long long row_stride;
+  const float *gains;
+  int gain_stride;
+  int group_shift;
+  int bit_count;
+  int code_bias;
+  int code_flip;
+} igl_code_view;
+
+/* The group_shift of a plane whose group size is 32 times a power of two, or
+ * that has one group a row. */
+static inline int igl_plane_group_shift(const igl_plane *sheet) {
+  int shift = 0;
+  if (sheet->group_count == 1) return 31;
+  while ((32 << shift) < sheet->group_size) ++shift;
+  return shift;
+}
+
+static inline igl_code_view igl_plane_view(const igl_plane *sheet, const void *codes,
+                                           const float *gains) {
+  igl_code_view v;
+  v.codes = (const uint8_t *)codes;
+  v.row_stride = (long long)sheet->row_stride;
+  v.gains = gains;
+  v.gain_stride = sheet->group_count;
+  v.group_shift = igl_plane_group_shift(sheet);
+  v.bit_count = sheet->bit_count;
+  v.code_bias = sheet->code_bias;
+  v.code_flip = sheet->code_flip;
+  return v;
+}
+
+size_t igl_gemv_code_part_floats(int bit_count, int lanes, int N, int K);
+hipError_t igl_launch_gemv_codes(const igl_code_view *v, const float *act, int act_stride,
+                                 int lanes, float *out, int out_stride, int N, int K,
+                                 float *part, hipStream_t stream);
+
 int igl_gemv_rows_per_tile(int lanes);
 int igl_gemv_chunk_cols(int lanes, int K, int lds_limit);
 size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit);
@@ -38,11 +80,11 @@ typedef struct igl_gemv_prologue {
 hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_t *const *codes,
                                  const long long *row_stride, const float *const *gains,
                                  const int *gain_stride, const int *rows, float *const *out,
-                                 int group_size, int code_bias, const float *act, int K,
+                                 int group_shift, int code_bias, const float *act, int K,
                                  const float *mul, const igl_gemv_prologue *pro,
                                  hipStream_t stream);
 hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_stride, const float *gains,
-                              int gain_stride, int group_size, int code_bias, const float *act,
+                              int gain_stride, int group_shift, int code_bias, const float *act,
                               int act_stride, int lanes, float *out, int out_stride, int N, int K,
                               float *part, int lds_limit, hipStream_t stream);
 
@@ -50,7 +92,7 @@ hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_stride, const 
 size_t igl_gemm_work_bytes(int M, int N, int K);
 hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride, const uint8_t *codes,
                               long long row_stride, const float *gains, int gain_stride,
-                              int group_size, int code_bias, void *out, int out_bf16,
+                              int group_shift, int code_bias, void *out, int out_bf16,
                               int out_stride, int M, int N, int K, void *work,
                               hipStream_t stream);
 
@@ -68,7 +110,7 @@ void *igl_desk_stream(igl_desk *desk);
 
 /* session kernels (igl_session.hip) */
 hipError_t igl_launch_gather_rows(const uint8_t *codes, long long row_stride, const float *gains,
-                                  int group_count, int group_size, int code_bias, int cols,
+                                  int group_count, int group_shift, int code_bias, int cols,
                                   int rows, const int32_t *ids, int lanes, float factor,
                                   float *out, int out_stride, hipStream_t stream);
 hipError_t igl_launch_ple_mix(float *room, int room_stride, const float *seed, int seed_stride,

@@ -343,12 +343,12 @@ using namespace igl;
 static const int kPickBlocks = 256;
 
 extern "C" hipError_t igl_launch_gather_rows(const uint8_t *codes, long long row_stride,
-                                             const float *gains, int group_count, int group_size,
+                                             const float *gains, int group_count, int group_shift,
                                              int code_bias, int cols, int rows, const int32_t *ids,
                                              int lanes, float factor, float *out, int out_stride,
                                              hipStream_t stream) {
   hipLaunchKernelGGL(gather_rows_kernel, dim3((cols + 255) / 256, lanes), dim3(256), 0, stream, codes,
-                     row_stride, gains, group_count, __builtin_ctz((unsigned)(group_size / 32)),
+                     row_stride, gains, group_count, group_shift,
                      code_bias, cols, rows, ids, factor, out, out_stride);
   return hipGetLastError();
 }

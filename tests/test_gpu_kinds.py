@@ -1,0 +1,152 @@
+"""GPU parity of the shipped export's other plane kinds against the oracle:
+2-bit planes (value + 2, four codes a byte), signed I8 planes (code_flip 128,
+code_bias 128), unsigned 8-bit planes, 4-bit planes with a flip, and one gain
+a row (per-channel scales, G = 1), at the widths the export has them
+(model/config.json module_quant_configs: MLP of layers 15-34, lm_head and
+embed_tokens 2-bit; per_layer_input_gate and per_layer_projection 8-bit).
+
+Bar: every output within relative error 1e-3 of the oracle, relative to
+max(|y_ref|, rms(y_ref)), as for the 4-bit GEMV.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from igllm_amd.backend import BackendError, make_plane
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_err(got, want):
+    want = want.astype(np.float64)
+    floor = np.sqrt(np.mean(want ** 2))
+    return float(np.max(np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want), floor)))
+
+
+def print_case(**kw):
+    print("case", " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def synth_kind(N, K, bits, group, lanes, seed, stride=None):
+    """Uniform codes of any width (uniform bytes), |N(0, 0.02)| gains, N(0,1) x."""
+    rng = np.random.default_rng(seed)
+    stride = stride or ((K * bits + 7) // 8 + 15) // 16 * 16
+    codes = rng.integers(0, 256, size=(N, stride), dtype=np.uint8)
+    G = (K + group - 1) // group
+    gains = np.abs(rng.normal(0, 0.02, size=(N, G))).astype(np.float32)
+    act = rng.normal(size=(lanes, K)).astype(np.float32)
+    return codes, gains, act
+
+
+def run_dev(backend, cp, act, lanes, path="gemv"):
+    K, N = cp.K, cp.N
+    dev_act = backend.upload(act)
+    dev_out = backend.alloc(lanes * N * 4)
+    fn = backend.gemv_dev if path == "gemv" else backend.mat_mat_dev
+    fn(cp, dev_act, K, lanes, dev_out, N)
+    backend.sync()
+    out = dev_out.get(np.float32, lanes * N).reshape(lanes, N)
+    dev_act.free()
+    dev_out.free()
+    return out
+
+
+KINDS = {
+    "u2": dict(bits=2, code_flip=0),
+    "i8": dict(bits=8, code_flip=128),
+    "u8": dict(bits=8, code_flip=0),
+    "u4flip": dict(bits=4, code_flip=5),
+}
+
+
+@pytest.mark.parametrize("kind", list(KINDS))
+@pytest.mark.parametrize("N,K,group,lanes", [
+    (6144, 1536, 1536, 1),   # gate/up of a 2-bit MLP layer, per-channel
+    (1536, 6144, 6144, 1),   # its down projection
+    (256, 1536, 1536, 1),    # per_layer_input_gate
+    (1536, 256, 256, 1),     # per_layer_projection
+    (1536, 256, 256, 3),
+    (2048, 1536, 32, 2),     # group-32 scales
+    (1000, 2048, 128, 4),
+    (300, 1536, 1536, 5),
+    (129, 6144, 6144, 8),
+    (70, 96, 96, 1),         # K not a multiple of 64
+    (33, 20480, 20480, 2),   # two K-chunks
+    (64, 4096, 32, 16),
+])
+def test_kind_gemv(backend, kind, N, K, group, lanes):
+    kw = KINDS[kind]
+    print_case(test="kind_gemv", kind=kind, N=N, K=K, group=group, lanes=lanes)
+    codes, gains, act = synth_kind(N, K, kw["bits"], group, lanes, seed=N + K + lanes)
+    cp = backend.attach(make_plane(codes, gains, K, group_size=group, **kw))
+    got = run_dev(backend, cp, act, lanes)
+    want = ol.oracle_mat_mat(codes, gains, act, K, group, threads=8, bits=kw["bits"],
+                             code_bias=1 << (kw["bits"] - 1), code_flip=kw["code_flip"])
+    err = rel_err(got, want)
+    print("rel_err", err)
+    assert err <= 1e-3
+    backend.detach(cp)
+
+
+@pytest.mark.parametrize("kind", ["u2", "i8"])
+def test_kind_table_entries(backend, kind):
+    """mat_vec / mat_mat through the table (host pointers), 70 lanes."""
+    kw = KINDS[kind]
+    N, K, lanes = 512, 1536, 70
+    print_case(test="kind_table", kind=kind, N=N, K=K, lanes=lanes)
+    codes, gains, act = synth_kind(N, K, kw["bits"], K, lanes, seed=7)
+    cp = backend.attach(make_plane(codes, gains, K, group_size=K, **kw))
+    want = ol.oracle_mat_mat(codes, gains, act, K, K, threads=8, bits=kw["bits"],
+                             code_bias=1 << (kw["bits"] - 1), code_flip=kw["code_flip"])
+    got = backend.mat_mat(cp, act)
+    assert rel_err(got, want) <= 1e-3
+    one = backend.mat_vec(cp, act[0])
+    assert np.array_equal(one, got[0])
+    backend.detach(cp)
+
+
+@pytest.mark.parametrize("kind", ["u2", "i8"])
+@pytest.mark.parametrize("fill", ["zeros", "tiny", "subnormal", "huge", "mixed"])
+def test_kind_activation_range(backend, kind, fill):
+    """The digit form over units of zeros, 1e-30, subnormal and 1e30 activations."""
+    kw = KINDS[kind]
+    N, K = 512, 1536
+    print_case(test="kind_range", kind=kind, fill=fill)
+    codes, gains, act = synth_kind(N, K, kw["bits"], 32, 1, seed=11)
+    if fill == "zeros":
+        act[:] = 0.0
+        act[0, 64:96] = np.linspace(-1, 1, 32)
+    elif fill == "tiny":
+        act *= 1e-30
+    elif fill == "subnormal":
+        act = (act * 1e-39).astype(np.float32)
+    elif fill == "huge":
+        act *= 1e30
+    else:
+        act[0, ::3] *= 1e20
+        act[0, 1::7] = 0.0
+    cp = backend.attach(make_plane(codes, gains, K, group_size=32, **kw))
+    got = run_dev(backend, cp, act, 1)
+    want = ol.oracle_mat_mat(codes, gains, act, K, 32, threads=8, bits=kw["bits"],
+                             code_bias=1 << (kw["bits"] - 1), code_flip=kw["code_flip"])
+    assert np.all(np.isfinite(got))
+    bar = 1e-3 if fill == "subnormal" else 1e-5
+    err = rel_err(got, want)
+    print("rel_err", err)
+    assert err <= bar
+    backend.detach(cp)
+
+
+def test_kind_refusals(backend):
+    """Kinds the kernels do not compute are refused at attach, not emulated."""
+    codes, gains, act = synth_kind(64, 96, 3, 32, 1, seed=1)
+    with pytest.raises(BackendError):
+        backend.attach(make_plane(codes, gains, 96, bits=3))
+    codes, gains, act = synth_kind(64, 96, 8, 48, 1, seed=1)
+    with pytest.raises(BackendError):
+        backend.attach(make_plane(codes, gains, 96, group_size=48, bits=8))
+    codes, gains, act = synth_kind(64, 96, 8, 96, 1, seed=1)
+    with pytest.raises(BackendError):
+        backend.attach(make_plane(codes, gains, 96, group_size=96, bits=8, code_bias=0))
+    with pytest.raises(BackendError):
+        backend.attach(make_plane(codes, gains, 96, group_size=96, bits=8, code_flip=256))

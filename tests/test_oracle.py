@@ -184,6 +184,50 @@ def test_mat_mat_bitexact_vs_reference(ref_plain, N, K, group, bits, lanes, thre
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+# The shipped export's kinds: one gain a row (group = K), signed I8 (flip 128),
+# 2-bit MLP / head planes, 4-bit per-channel attention planes.
+SHIPPED_KINDS = [
+    (70, 1536, 1536, 8, 128, 3), (40, 256, 256, 8, 128, 1), (64, 1536, 1536, 2, 0, 2),
+    (33, 6144, 6144, 2, 0, 1), (50, 1536, 1536, 4, 0, 4), (24, 8960, 256, 4, 0, 2),
+    (20, 96, 96, 2, 1, 3), (20, 96, 32, 8, 0, 2), (20, 96, 96, 4, 5, 1),
+]
+
+
+@pytest.mark.parametrize("N,K,group,bits,flip,lanes", SHIPPED_KINDS)
+def test_shipped_kinds_closed_form(N, K, group, bits, flip, lanes):
+    """y = sum_g s[n,g] sum_{k in g} ((c ^ flip) - bias) x in float64."""
+    stride = (K * bits + 7) // 8
+    codes = rng.integers(0, 256, size=(N, stride), dtype=np.uint8)
+    G = (K + group - 1) // group
+    gains = np.abs(rng.normal(0, 0.02, size=(N, G))).astype(np.float32)
+    act = rng.normal(size=(lanes, K)).astype(np.float32)
+    bias = 1 << (bits - 1)
+    got = ol.oracle_mat_mat(codes, gains, act, K, group, threads=2, bits=bits, code_bias=bias,
+                            code_flip=flip)
+    fields = np.unpackbits(codes, axis=1, bitorder="little")[:, :K * bits].reshape(N, K, bits)
+    c = (fields.astype(np.int64) << np.arange(bits)).sum(axis=2) ^ flip
+    w = (c - bias).astype(np.float64) * np.repeat(gains.astype(np.float64), group, axis=1)[:, :K]
+    want = act.astype(np.float64) @ w.T
+    scale = np.sqrt(np.mean(want ** 2))
+    assert np.max(np.abs(got - want)) <= 2e-6 * scale * math.sqrt(K / 32) + 1e-7
+    if flip:  # a restatement that dropped the flip misses the closed form
+        wrong = ol.oracle_mat_mat(codes, gains, act, K, group, bits=bits, code_bias=bias)
+        assert np.max(np.abs(wrong - want)) > 1e-3 * scale
+
+
+@pytest.mark.parametrize("N,K,group,bits,flip,lanes", SHIPPED_KINDS)
+def test_shipped_kinds_bitexact_vs_reference(ref_plain, N, K, group, bits, flip, lanes):
+    stride = (K * bits + 7) // 8
+    codes = rng.integers(0, 256, size=(N, stride), dtype=np.uint8)
+    G = (K + group - 1) // group
+    gains = np.abs(rng.normal(0, 0.02, size=(N, G))).astype(np.float32)
+    act = rng.normal(size=(lanes, K)).astype(np.float32)
+    kw = dict(bits=bits, code_bias=1 << (bits - 1), code_flip=flip)
+    got = ol.oracle_mat_mat(codes, gains, act, K, group, threads=2, **kw)
+    want = ol.ref_mat_mat(ref_plain, codes, gains, act, K, group, threads=2, **kw)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 # ---- FP8 codec ----------------------------------------------------------------
 
 def e4m3_definition(code):
