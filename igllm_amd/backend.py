@@ -65,7 +65,7 @@ class DevBuf:
 
 @dataclass
 class CodePlane:
-    """A 4-bit code plane: the numpy arrays it points into and its igl_plane."""
+    """A plane (code or real): the numpy arrays it points into and its igl_plane."""
 
     plane: Plane
     codes: np.ndarray  # uint8 [N, row_stride]
@@ -103,6 +103,22 @@ def make_plane(codes: np.ndarray, gains: np.ndarray, K: int, group_size: int = 3
     p.group_size = group_size
     p.group_count = gains.shape[1]
     return CodePlane(p, codes, gains)
+
+
+def make_real_plane(rows: np.ndarray, real_type: int) -> CodePlane:
+    """A real plane over `rows` [N, K]: float32, or the uint16 bits of binary16
+    (IGL_STORE_F16) or bf16 (IGL_STORE_BF16) values."""
+    rows = np.ascontiguousarray(rows)
+    want = np.float32 if real_type == native.IGL_STORE_F32 else np.uint16
+    if rows.dtype != want:
+        raise ValueError(f"real_type {real_type} takes {want.__name__} rows")
+    p = Plane()
+    p.form = native.IGL_PLANE_REAL
+    p.row_count = rows.shape[0]
+    p.col_count = rows.shape[1]
+    p.real_data = _ptr(rows)
+    p.real_type = real_type
+    return CodePlane(p, rows, np.zeros((0,), dtype=np.float32))
 
 
 class Backend:

@@ -131,11 +131,22 @@ fail:
 
 static int is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
-/* The code planes the kernels take: 2, 4 or 8-bit codes with the offset of
- * half their range (code_bias = 2^(bits-1)) and any flip (the signed I8
- * planes flip 128), F32 gains over groups of 32 times a power of two columns
- * or one group a row; everything else is refused, not emulated. */
+/* Bytes of one value of a real plane the kernels read, 0 for other types. */
+static int real_bytes_of(int real_type) {
+  return real_type == IGL_STORE_F32 ? 4 : real_type == IGL_STORE_F16 || real_type == IGL_STORE_BF16 ? 2 : 0;
+}
+
+/* The planes the kernels take: real planes of F32, F16 or BF16 rows, K a
+ * multiple of 8; code planes of 2, 4 or 8-bit codes with the offset of half
+ * their range (code_bias = 2^(bits-1)) and any flip (the signed I8 planes flip
+ * 128), F32 gains over groups of 32 times a power of two columns or one group
+ * a row.  Everything else is refused, not emulated. */
 static int plane_supported(const igl_plane *sheet) {
+  if (sheet && sheet->form == IGL_PLANE_REAL)
+    return real_bytes_of(sheet->real_type) && sheet->row_count >= 1 && sheet->col_count >= 8 &&
+                   (sheet->col_count & 7) == 0
+               ? IGL_OKAY
+               : IGL_FAIL_SUPPORT;
   if (!sheet || sheet->form != IGL_PLANE_CODE) return IGL_FAIL_SUPPORT;
   if (sheet->bit_count != 2 && sheet->bit_count != 4 && sheet->bit_count != 8) return IGL_FAIL_SUPPORT;
   if (sheet->code_bias != 1 << (sheet->bit_count - 1) || sheet->code_flip < 0 ||
@@ -161,13 +172,15 @@ static int plane_supported(const igl_plane *sheet) {
 /* The tuned 4-bit kernels take codes stored value + 8 with no flip; every
  * other code plane goes through the every-width form. */
 static int plane_is_q4(const igl_plane *sheet) {
-  return sheet->bit_count == 4 && sheet->code_flip == 0;
+  return sheet->form == IGL_PLANE_CODE && sheet->bit_count == 4 && sheet->code_flip == 0;
 }
 
 /* Room the GEMV's K-chunk partials need for this plane, over every lane count
  * a launch can carry. */
 static size_t plane_part_floats(const igl_desk_state *st, const igl_plane *sheet) {
   size_t most = 0;
+  if (sheet->form == IGL_PLANE_REAL)
+    return igl_gemv_real_part_floats(IGL_GEMV_LANES, sheet->row_count, sheet->col_count);
   if (!plane_is_q4(sheet))
     return igl_gemv_code_part_floats(sheet->bit_count, IGL_GEMV_LANES, sheet->row_count,
                                      sheet->col_count);
@@ -192,19 +205,32 @@ int igl_plane_attach(igl_desk *desk, igl_plane *sheet) {
   void *codes = NULL, *gains = NULL;
   int code;
   if (!st) return IGL_FAIL_STATE;
+  const void *code_src, *gain_src;
   if ((code = plane_supported(sheet)) != IGL_OKAY) return code;
-  if (!sheet->code_data || !sheet->gain_data) return IGL_FAIL_ARGUMENT;
-  code_bytes = (size_t)sheet->row_count * sheet->row_stride;
-  gain_bytes = (size_t)sheet->row_count * (size_t)sheet->group_count * sizeof(float);
+  if (sheet->form == IGL_PLANE_REAL) {
+    /* a real plane's rows travel as the codes, with no gains */
+    code_src = sheet->real_data;
+    gain_src = NULL;
+    code_bytes = (size_t)sheet->row_count * (size_t)sheet->col_count * (size_t)real_bytes_of(sheet->real_type);
+    gain_bytes = 0;
+    if (!code_src) return IGL_FAIL_ARGUMENT;
+  } else {
+    code_src = sheet->code_data;
+    gain_src = sheet->gain_data;
+    code_bytes = (size_t)sheet->row_count * sheet->row_stride;
+    gain_bytes = (size_t)sheet->row_count * (size_t)sheet->group_count * sizeof(float);
+    if (!code_src || !gain_src) return IGL_FAIL_ARGUMENT;
+  }
   dp = (igl_device_plane *)calloc(1, sizeof(*dp));
   if (!dp) return IGL_FAIL_MEMORY;
-  if (hipMalloc(&codes, code_bytes) != hipSuccess || hipMalloc(&gains, gain_bytes) != hipSuccess) {
+  if (hipMalloc(&codes, code_bytes) != hipSuccess ||
+      (gain_bytes && hipMalloc(&gains, gain_bytes) != hipSuccess)) {
     if (codes) (void)hipFree(codes);
     free(dp);
     return IGL_FAIL_MEMORY;
   }
-  if (hipMemcpy(codes, sheet->code_data, code_bytes, hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemcpy(gains, sheet->gain_data, gain_bytes, hipMemcpyHostToDevice) != hipSuccess) {
+  if (hipMemcpy(codes, code_src, code_bytes, hipMemcpyHostToDevice) != hipSuccess ||
+      (gain_bytes && hipMemcpy(gains, gain_src, gain_bytes, hipMemcpyHostToDevice) != hipSuccess)) {
     (void)hipFree(codes);
     (void)hipFree(gains);
     free(dp);
@@ -229,7 +255,8 @@ int igl_plane_bind_dev(igl_desk *desk, igl_plane *sheet, const void *code_dev, c
   int code;
   if (!st) return IGL_FAIL_STATE;
   if ((code = plane_supported(sheet)) != IGL_OKAY) return code;
-  if (!code_dev || !gain_dev || ((uintptr_t)code_dev & 15u) || ((uintptr_t)gain_dev & 3u))
+  if (!code_dev || ((uintptr_t)code_dev & 15u) ||
+      (sheet->form == IGL_PLANE_CODE && (!gain_dev || ((uintptr_t)gain_dev & 3u))))
     return IGL_FAIL_ARGUMENT;
   dp = (igl_device_plane *)calloc(1, sizeof(*dp));
   if (!dp) return IGL_FAIL_MEMORY;
@@ -287,6 +314,15 @@ int igl_gemv_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev, i
     return IGL_FAIL_STATE;
   }
   dp = sheet->device;
+  if (sheet->form == IGL_PLANE_REAL) {
+    if (((uintptr_t)act_dev & 15u) || (lane_count > 1 && (act_stride & 3))) {
+      desk_fail(st, IGL_FAIL_ARGUMENT);
+      return IGL_FAIL_ARGUMENT;
+    }
+    return hip_check(st, igl_launch_gemv_real(dp->codes, sheet->real_type, act_dev, act_stride,
+                                              lane_count, out_dev, out_stride, sheet->row_count,
+                                              sheet->col_count, st->part_dev, st->stream));
+  }
   if (!plane_is_q4(sheet)) {
     igl_code_view view = igl_plane_view(sheet, dp->codes, dp->gains);
     if (((uintptr_t)act_dev & 15u) || (lane_count > 1 && (act_stride & 3))) {
@@ -343,7 +379,7 @@ int igl_mat_mat_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev
   igl_desk_state *st = desk ? desk->state : NULL;
   int code;
   if (!st) return IGL_FAIL_STATE;
-  if (lane_count < IGL_GEMM_FLOOR || (sheet && sheet->form == IGL_PLANE_CODE && !plane_is_q4(sheet)))
+  if (lane_count < IGL_GEMM_FLOOR || (sheet && !plane_is_q4(sheet)))
     return igl_gemv_dev(desk, sheet, act_dev, act_stride, lane_count, out_dev, out_stride);
   if ((code = plane_supported(sheet)) != IGL_OKAY || !sheet->device) {
     code = code != IGL_OKAY ? code : IGL_FAIL_STATE;
@@ -362,6 +398,10 @@ int igl_gemm_bf16_dev(igl_desk *desk, const igl_plane *sheet, const uint16_t *ac
     code = code != IGL_OKAY ? code : IGL_FAIL_STATE;
     desk_fail(st, code);
     return code;
+  }
+  if (!plane_is_q4(sheet)) {
+    desk_fail(st, IGL_FAIL_SUPPORT);
+    return IGL_FAIL_SUPPORT;
   }
   return gemm_run(desk, sheet, act_dev, 1, act_stride, lane_count, out_dev, 1, out_stride);
 }

@@ -745,6 +745,134 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_code_dot_kernel(GemvCodeArg
   }
 }
 
+// ---- real planes: F32, F16 or BF16 rows -------------------------------------
+//
+// kern_mat_vec_band's PLANE_REAL arm (app_core.c:4239-4248): every row dotted
+// with every lane in fp32.  The export keeps one such plane,
+// per_layer_model_projection (8960 x 1536 bf16, 26.25 MiB a decode step).
+// A wave owns R rows; a lane streams 16-byte slots of them (eight bf16/f16
+// or four f32 values), converts each value exactly to fp32 (bf16: a shift;
+// f16: the conversion) and multiplies it into per-lane fp32 accumulators
+// against x, which the workgroup stages once in LDS.  `blockIdx.y` takes a
+// K-chunk; chunks write partials [chunk][lanes][N] for gemv_chunk_sum_kernel.
+struct GemvRealArgs {
+  const uint8_t *rows;
+  long long row_bytes;
+  const float *act;       // 16-byte aligned, act_stride % 4 == 0
+  int act_stride;
+  int lanes;              // <= M
+  float *out;
+  int out_stride;
+  int N, K;
+  int chunk_cols;         // a multiple of 64
+};
+
+template <int TYPE>
+struct RealSlot {
+  static constexpr int kValues = TYPE == IGL_STORE_F32 ? 4 : 8;
+  static constexpr int kBytes = TYPE == IGL_STORE_F32 ? 4 : 2;
+};
+
+template <int TYPE>
+__device__ __forceinline__ void real_values(const uint4_t w, float (&v)[RealSlot<TYPE>::kValues]) {
+  if constexpr (TYPE == IGL_STORE_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(w[i]);
+  } else if constexpr (TYPE == IGL_STORE_BF16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const half2_t h = as_half2(w[i]);
+      v[2 * i] = (float)h.x;
+      v[2 * i + 1] = (float)h.y;
+    }
+  }
+}
+
+constexpr int kRealRows = 4;
+
+template <int TYPE, int M>
+__global__ __launch_bounds__(kGemvThreads) void gemv_real_kernel(GemvRealArgs a) {
+  extern __shared__ float4_t real_xs[];  // [M][cols / 4]
+  constexpr int R = kRealRows;
+  constexpr int kPer = RealSlot<TYPE>::kValues;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col0 = blockIdx.y * a.chunk_cols;
+  const int cols = min(a.chunk_cols, a.K - col0);
+  const int quads = cols >> 2;
+  const int slots = cols / kPer;
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+
+  const uint8_t *base[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    base[r] = a.rows + (size_t)min(row0 + r, a.N - 1) * (size_t)a.row_bytes +
+              (size_t)col0 * RealSlot<TYPE>::kBytes;
+  // the first slot's rows go out before the staging loads
+  uint4_t w[R];
+  const int s0 = min(lane, slots - 1);
+#pragma unroll
+  for (int r = 0; r < R; ++r) w[r] = __builtin_nontemporal_load(reinterpret_cast<const uint4_t *>(base[r]) + s0);
+  for (int i = tid; i < M * quads; i += kGemvThreads) {
+    const int m = i / quads;
+    const int q = i - m * quads;
+    real_xs[i] = *reinterpret_cast<const float4_t *>(a.act + (size_t)min(m, a.lanes - 1) * a.act_stride +
+                                                     col0 + 4 * q);
+  }
+  __syncthreads();
+
+  float acc[R][M];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+  for (int s = lane; s < slots; s += kWave) {
+    uint4_t next[R];
+    const int sn = min(s + kWave, slots - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) next[r] = __builtin_nontemporal_load(reinterpret_cast<const uint4_t *>(base[r]) + sn);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float x[kPer];
+      const float4_t xa = real_xs[m * quads + s * (kPer / 4)];
+      x[0] = xa.x; x[1] = xa.y; x[2] = xa.z; x[3] = xa.w;
+      if constexpr (kPer == 8) {
+        const float4_t xb = real_xs[m * quads + s * 2 + 1];
+        x[4] = xb.x; x[5] = xb.y; x[6] = xb.z; x[7] = xb.w;
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float v[kPer];
+        real_values<TYPE>(w[r], v);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) acc[r][m] = __builtin_fmaf(v[i], x[i], acc[r][m]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) w[r] = next[r];
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = wave_sum_to_last(acc[r][m]);
+  if (lane != 63) return;
+  float *dst = a.out + (size_t)blockIdx.y * (size_t)a.lanes * (size_t)a.out_stride;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (row0 + r < a.N)
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+        if (m < a.lanes) dst[(size_t)m * a.out_stride + row0 + r] = acc[r][m];
+}
+
 // ---- one activation row against several planes in one launch (decode) -----
 //
 // The register form for one lane and four rows a wave, over up to three planes
@@ -1687,6 +1815,93 @@ extern "C" hipError_t igl_launch_gemv_codes(const igl_code_view *v, const float 
     hipError_t e = bits == 2   ? gemv_code_launch_bits<2>(a, M, upl, gpt, grid, lds, stream)
                    : bits == 4 ? gemv_code_launch_bits<4>(a, M, upl, gpt, grid, lds, stream)
                                : gemv_code_launch_bits<8>(a, M, upl, gpt, grid, lds, stream);
+    if (e != hipSuccess) return e;
+    if (chunks > 1) {
+      const int total = l * N;
+      hipLaunchKernelGGL(gemv_chunk_sum_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, part,
+                         chunks, l, N, out + (size_t)done * (size_t)out_stride, out_stride);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+  }
+  return hipSuccess;
+}
+
+// ---- real planes: gemv_real_kernel -----------------------------------------
+
+namespace igl {
+
+static int real_launch_lanes(int lanes) { return lanes <= 1 ? 1 : lanes <= 2 ? 2 : lanes <= 4 ? 4 : 8; }
+
+// Columns of one K-chunk: a multiple of 64 with M cols floats <= 32 KiB.
+static int real_chunk_cols(int M, int K) {
+  const int most = 8192 / M;
+  const int chunks = (K + most - 1) / most;
+  const int per = (K + chunks - 1) / chunks;
+  return (per + 63) / 64 * 64;
+}
+
+template <int TYPE>
+static hipError_t gemv_real_launch_type(const GemvRealArgs &a, int M, dim3 grid, size_t lds,
+                                        hipStream_t stream) {
+  switch (M) {
+    case 1: hipLaunchKernelGGL((gemv_real_kernel<TYPE, 1>), grid, dim3(kGemvThreads), lds, stream, a); break;
+    case 2: hipLaunchKernelGGL((gemv_real_kernel<TYPE, 2>), grid, dim3(kGemvThreads), lds, stream, a); break;
+    case 4: hipLaunchKernelGGL((gemv_real_kernel<TYPE, 4>), grid, dim3(kGemvThreads), lds, stream, a); break;
+    default: hipLaunchKernelGGL((gemv_real_kernel<TYPE, 8>), grid, dim3(kGemvThreads), lds, stream, a); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace igl
+
+extern "C" size_t igl_gemv_real_part_floats(int lanes, int N, int K) {
+  size_t most = 0;
+  for (int l = 1; l <= (lanes < 8 ? lanes : 8); ++l) {
+    const int cols = real_chunk_cols(real_launch_lanes(l), K);
+    const size_t chunks = (size_t)((K + cols - 1) / cols);
+    const size_t need = chunks > 1 ? chunks * (size_t)l * (size_t)N : 0;
+    if (need > most) most = need;
+  }
+  return most;
+}
+
+// y = W x for any number of lanes over a real plane (F32, F16 or BF16 rows of
+// K values, K % 8 == 0), eight lanes a launch.  Activations 16-byte aligned
+// with act_stride % 4 == 0; `part` holds igl_gemv_real_part_floats floats.
+extern "C" hipError_t igl_launch_gemv_real(const void *rows, int real_type, const float *act,
+                                           int act_stride, int lanes, float *out, int out_stride,
+                                           int N, int K, float *part, hipStream_t stream) {
+  if ((real_type != IGL_STORE_F32 && real_type != IGL_STORE_F16 && real_type != IGL_STORE_BF16) ||
+      K % 8 || N < 1 || (((uintptr_t)act) & 15u) || (((uintptr_t)rows) & 15u) ||
+      (lanes > 1 && (act_stride & 3)))
+    return hipErrorInvalidValue;
+  GemvRealArgs a;
+  a.rows = static_cast<const uint8_t *>(rows);
+  a.row_bytes = (long long)K * (real_type == IGL_STORE_F32 ? 4 : 2);
+  a.N = N;
+  a.K = K;
+  for (int done = 0; done < lanes; done += 8) {
+    const int l = lanes - done < 8 ? lanes - done : 8;
+    const int M = real_launch_lanes(l);
+    const int cols = real_chunk_cols(M, K);
+    const int chunks = (K + cols - 1) / cols;
+    a.act = act + (size_t)done * (size_t)act_stride;
+    a.act_stride = act_stride;
+    a.lanes = l;
+    a.chunk_cols = cols;
+    if (chunks > 1) {
+      if (!part) return hipErrorInvalidValue;
+      a.out = part;
+      a.out_stride = N;
+    } else {
+      a.out = out + (size_t)done * (size_t)out_stride;
+      a.out_stride = out_stride;
+    }
+    const dim3 grid((N + 4 * kRealRows - 1) / (4 * kRealRows), chunks);
+    const size_t lds = (size_t)M * (size_t)cols * sizeof(float);
+    hipError_t e = real_type == IGL_STORE_F32    ? gemv_real_launch_type<IGL_STORE_F32>(a, M, grid, lds, stream)
+                   : real_type == IGL_STORE_F16 ? gemv_real_launch_type<IGL_STORE_F16>(a, M, grid, lds, stream)
+                                                : gemv_real_launch_type<IGL_STORE_BF16>(a, M, grid, lds, stream);
     if (e != hipSuccess) return e;
     if (chunks > 1) {
       const int total = l * N;

@@ -56,6 +56,11 @@ hipError_t igl_launch_gemv_codes(const igl_code_view *v, const float *act, int a
                                  int lanes, float *out, int out_stride, int N, int K,
                                  float *part, hipStream_t stream);
 
+size_t igl_gemv_real_part_floats(int lanes, int N, int K);
+hipError_t igl_launch_gemv_real(const void *rows, int real_type, const float *act, int act_stride,
+                                int lanes, float *out, int out_stride, int N, int K, float *part,
+                                hipStream_t stream);
+
 int igl_gemv_rows_per_tile(int lanes);
 int igl_gemv_chunk_cols(int lanes, int K, int lds_limit);
 size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit);

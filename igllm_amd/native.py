@@ -22,6 +22,9 @@ IGL_FAIL_DEVICE = -8
 
 IGL_PLANE_CODE = 2
 IGL_STORE_F32 = 1
+IGL_STORE_F16 = 2
+IGL_STORE_BF16 = 3
+IGL_PLANE_REAL = 1
 IGL_CACHE_E4M3 = 0
 IGL_CACHE_INT8 = 1
 

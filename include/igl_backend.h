@@ -126,13 +126,17 @@ const char *igl_code_text(int code);
 
 /* ---- weights ------------------------------------------------------------ */
 
-/* Copies a code plane's bytes and gains to the device unchanged and sets
- * `sheet->device`.  Supported: 4-bit codes, code_flip 0, F32 gains, no zero
- * points, group_size a power-of-two multiple of 32, col_count a multiple of
- * 32, row_stride a multiple of 16.  Anything else is IGL_FAIL_SUPPORT. */
+/* Copies a plane's bytes (and gains) to the device unchanged and sets
+ * `sheet->device`.  Supported code planes: 2, 4 or 8-bit codes with
+ * code_bias 2^(bits-1) and any code_flip (the export's signed I8 planes flip
+ * 128), F32 gains, no zero points, group_size a power-of-two multiple of 32 or
+ * one group a row, col_count a multiple of 32, row_stride a multiple of 16.
+ * Supported real planes (plane_bind_part's `weight` of a float type,
+ * app_core.c:7985-7998): F32, F16 or BF16 rows, col_count a multiple of 8.
+ * Anything else is IGL_FAIL_SUPPORT. */
 int  igl_plane_attach(igl_desk *desk, igl_plane *sheet);
 /* The same for bytes and gains already on the device (no copy; the caller
- * keeps ownership). */
+ * keeps ownership).  A real plane passes its rows as `code_dev` and no gains. */
 int  igl_plane_bind_dev(igl_desk *desk, igl_plane *sheet, const void *code_dev,
                         const float *gain_dev);
 void igl_plane_detach(igl_desk *desk, igl_plane *sheet);

@@ -301,6 +301,52 @@ int oracle_mat_mat(const oracle_plane *sheet, const float *act, int act_stride, 
   return 0;
 }
 
+/* A real plane's product (kern_mat_vec_band's PLANE_REAL arm,
+ * app_core.c:4239-4248): every row against every lane with kern_dot_real.
+ * fp32 and bf16 rows take its SSE2 blocks (2048-2066 and 2102-2112: a bf16
+ * value widens exactly, so the bf16 arm is the fp32 arm on the widened row);
+ * any other type the sequential walk (2137-2139), here binary16.
+ * `real_type`: ORACLE_REAL_F32, ORACLE_REAL_F16 or ORACLE_REAL_BF16. */
+static float oracle_real_read(const void *row, int real_type, int slot) {
+  uint32_t bits;
+  float value;
+  if (real_type == ORACLE_REAL_F32) return ((const float *)row)[slot];
+  if (real_type == ORACLE_REAL_BF16) {
+    bits = (uint32_t)((const uint16_t *)row)[slot] << 16;
+    memcpy(&value, &bits, 4);
+    return value;
+  }
+  {
+    uint16_t h = ((const uint16_t *)row)[slot];
+    int e = (h >> 10) & 31, m = h & 1023;
+    value = e == 0 ? ldexpf((float)m, -24) : e == 31 ? (m ? NAN : INFINITY) : ldexpf((float)(m + 1024), e - 25);
+    return (h & 0x8000) ? -value : value;
+  }
+}
+
+int oracle_mat_mat_real(const void *real_data, int real_type, int row_count, int col_count,
+                        const float *act, int act_stride, int lane_count, float *out,
+                        int out_stride) {
+  size_t row_bytes = (size_t)col_count * (real_type == ORACLE_REAL_F32 ? 4u : 2u);
+  float *wide = (float *)malloc(sizeof(float) * (size_t)col_count);
+  if (!wide) return -2;
+  for (int n = 0; n < row_count; ++n) {
+    const void *row = (const uint8_t *)real_data + (size_t)n * row_bytes;
+    for (int k = 0; k < col_count; ++k) wide[k] = oracle_real_read(row, real_type, k);
+    for (int l = 0; l < lane_count; ++l) {
+      const float *x = act + (size_t)l * (size_t)act_stride;
+      float total = 0.0f;
+      if (real_type == ORACLE_REAL_F16)
+        for (int k = 0; k < col_count; ++k) total += wide[k] * x[k];
+      else
+        total = oracle_dot_real(wide, x, col_count);
+      out[(size_t)l * (size_t)out_stride + (size_t)n] = total;
+    }
+  }
+  free(wide);
+  return 0;
+}
+
 /* ------------------------------------------------------------------------ */
 /* FP8 E4M3 cache codec (app_core.c:7488-7490, 10980-11036)                  */
 /* ------------------------------------------------------------------------ */

@@ -63,6 +63,12 @@ void  oracle_row_code_many(const oracle_plane *sheet, int row_index, const float
                            int sum_stride, float *out, int out_stride);
 /* back_mat_mat on a plain build: chunks of 16 lanes, group sums, then rows
  * banded over `thread_count` threads (1 = serial). */
+#define ORACLE_REAL_F32  1  /* STORE_F32, app_core.c:1414 */
+#define ORACLE_REAL_F16  2
+#define ORACLE_REAL_BF16 3
+int   oracle_mat_mat_real(const void *real_data, int real_type, int row_count, int col_count,
+                          const float *act, int act_stride, int lane_count, float *out,
+                          int out_stride);
 int   oracle_mat_mat(const oracle_plane *sheet, const float *act, int act_stride,
                      int lane_count, float *out, int out_stride, int thread_count);
 

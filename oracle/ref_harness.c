@@ -97,6 +97,22 @@ void ref_desk_mat_mat(void *handle, const ref_plane_desc *desc, const float *act
   box->desk.mat_mat(&box->desk, &sheet, act, act_stride, lane_count, out, out_stride);
 }
 
+/* The same desk entry on a real plane: `real_type` is the reference's
+ * store_type (STORE_F32, STORE_F16, STORE_BF16). */
+void ref_desk_mat_mat_real(void *handle, const void *real_data, int real_type, int row_count,
+                           int col_count, const float *act, int act_stride, int lane_count,
+                           float *out, int out_stride) {
+  ref_desk *box = (ref_desk *)handle;
+  plane sheet;
+  memset(&sheet, 0, sizeof(sheet));
+  sheet.form = PLANE_REAL;
+  sheet.row_count = row_count;
+  sheet.col_count = col_count;
+  sheet.real_data = real_data;
+  sheet.real_type = (store_type)real_type;
+  box->desk.mat_mat(&box->desk, &sheet, act, act_stride, lane_count, out, out_stride);
+}
+
 float ref_cache_pack8(float value) { return cache_pack8(value); }
 uint8_t ref_cache_code8(float value) { return cache_code8(value); }
 float ref_cache_real8(uint8_t code) { return cache_real8(code); }

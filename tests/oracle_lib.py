@@ -47,6 +47,7 @@ ORACLE_SIGS = {
     "oracle_dot_code": (_F, [_P, _I, _I, _P, _I, _I]),
     "oracle_row_code": (_F, [ctypes.POINTER(PlaneDesc), _I, _P, _P]),
     "oracle_mat_mat": (_I, [ctypes.POINTER(PlaneDesc), _P, _I, _I, _P, _I, _I]),
+    "oracle_mat_mat_real": (_I, [_P, _I, _I, _I, _P, _I, _I, _P, _I]),
     "oracle_pack8": (_F, [_F]),
     "oracle_code8": (ctypes.c_uint8, [_F]),
     "oracle_real8": (_F, [ctypes.c_uint8]),
@@ -71,6 +72,7 @@ REF_SIGS = {
     "ref_desk_open": (_P, [_I, _I, _I]),
     "ref_desk_close": (None, [_P]),
     "ref_desk_mat_mat": (None, [_P, ctypes.POINTER(PlaneDesc), _P, _I, _I, _P, _I]),
+    "ref_desk_mat_mat_real": (None, [_P, _P, _I, _I, _I, _P, _I, _I, _P, _I]),
     "ref_cache_pack8": (_F, [_F]),
     "ref_cache_code8": (ctypes.c_uint8, [_F]),
     "ref_cache_real8": (_F, [ctypes.c_uint8]),
@@ -156,6 +158,34 @@ def ref_mat_mat(lib, codes, gains, act, K, group_size=32, threads=1, **kw) -> np
     assert desk
     try:
         lib.ref_desk_mat_mat(desk, ctypes.byref(d), p(act), act.shape[1], lanes, p(out), codes.shape[0])
+    finally:
+        lib.ref_desk_close(desk)
+    return out
+
+
+REAL_F32, REAL_F16, REAL_BF16 = 1, 2, 3  # the reference's store_type values
+
+
+def oracle_mat_mat_real(real, real_type, act) -> np.ndarray:
+    """A real plane [N, K] (float32, or uint16 bits of binary16 / bf16) times lanes of x."""
+    real = np.ascontiguousarray(real)
+    act = np.ascontiguousarray(act, dtype=np.float32)
+    N, K = real.shape
+    out = np.empty((act.shape[0], N), dtype=np.float32)
+    rc = oracle().oracle_mat_mat_real(p(real), real_type, N, K, p(act), K, act.shape[0], p(out), N)
+    assert rc == 0
+    return out
+
+
+def ref_mat_mat_real(lib, real, real_type, act, threads=1) -> np.ndarray:
+    real = np.ascontiguousarray(real)
+    act = np.ascontiguousarray(act, dtype=np.float32)
+    N, K = real.shape
+    out = np.empty((act.shape[0], N), dtype=np.float32)
+    desk = lib.ref_desk_open(threads, 1, K)
+    assert desk
+    try:
+        lib.ref_desk_mat_mat_real(desk, p(real), real_type, N, K, p(act), K, act.shape[0], p(out), N)
     finally:
         lib.ref_desk_close(desk)
     return out

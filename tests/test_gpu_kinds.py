@@ -3,7 +3,8 @@
 code_bias 128), unsigned 8-bit planes, 4-bit planes with a flip, and one gain
 a row (per-channel scales, G = 1), at the widths the export has them
 (model/config.json module_quant_configs: MLP of layers 15-34, lm_head and
-embed_tokens 2-bit; per_layer_input_gate and per_layer_projection 8-bit).
+embed_tokens 2-bit; per_layer_input_gate and per_layer_projection 8-bit),
+and real planes of bf16, binary16 or fp32 rows (per_layer_model_projection).
 
 Bar: every output within relative error 1e-3 of the oracle, relative to
 max(|y_ref|, rms(y_ref)), as for the 4-bit GEMV.
@@ -150,3 +151,51 @@ def test_kind_refusals(backend):
         backend.attach(make_plane(codes, gains, 96, group_size=96, bits=8, code_bias=0))
     with pytest.raises(BackendError):
         backend.attach(make_plane(codes, gains, 96, group_size=96, bits=8, code_flip=256))
+
+
+# ---- real planes (per_layer_model_projection: 8960 x 1536 bf16) --------------
+
+def real_rows(N, K, real_type, seed):
+    rng = np.random.default_rng(seed)
+    w = rng.normal(0, 0.05, size=(N, K)).astype(np.float32)
+    if real_type == ol.REAL_F32:
+        return w
+    if real_type == ol.REAL_F16:
+        return w.astype(np.float16).view(np.uint16)
+    return (w.view(np.uint32) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("real_type", [ol.REAL_BF16, ol.REAL_F16, ol.REAL_F32])
+@pytest.mark.parametrize("N,K,lanes", [
+    (8960, 1536, 1), (8960, 1536, 2), (8960, 1536, 5), (1000, 1536, 8), (300, 1536, 16),
+    (3, 8, 1), (70, 72, 3), (100, 12288, 8), (77, 20000, 1),
+])
+def test_real_gemv(backend, real_type, N, K, lanes):
+    from igllm_amd.backend import make_real_plane
+
+    print_case(test="real_gemv", real_type=real_type, N=N, K=K, lanes=lanes)
+    rows = real_rows(N, K, real_type, seed=N + K)
+    act = np.random.default_rng(lanes).normal(size=(lanes, K)).astype(np.float32)
+    cp = backend.attach(make_real_plane(rows, real_type))
+    got = run_dev(backend, cp, act, lanes)
+    want = ol.oracle_mat_mat_real(rows, real_type, act)
+    err = rel_err(got, want)
+    print("rel_err", err)
+    assert err <= 1e-3
+    backend.detach(cp)
+
+
+def test_real_table_entries(backend):
+    from igllm_amd.backend import make_real_plane
+
+    N, K, lanes = 8960, 1536, 70
+    print_case(test="real_table", N=N, K=K, lanes=lanes)
+    rows = real_rows(N, K, ol.REAL_BF16, seed=3)
+    act = np.random.default_rng(3).normal(size=(lanes, K)).astype(np.float32)
+    cp = backend.attach(make_real_plane(rows, ol.REAL_BF16))
+    want = ol.oracle_mat_mat_real(rows, ol.REAL_BF16, act)
+    got = backend.mat_mat(cp, act)
+    assert rel_err(got, want) <= 1e-3
+    # one lane takes the whole row in one K-chunk, eight lanes two: not bit-equal
+    assert rel_err(backend.mat_vec(cp, act[0])[None], want[:1]) <= 1e-3
+    backend.detach(cp)

@@ -228,6 +228,42 @@ def test_shipped_kinds_bitexact_vs_reference(ref_plain, N, K, group, bits, flip,
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+def real_rows(N, K, real_type):
+    """Rows of a real plane and their values in float64."""
+    w = rng.normal(0, 0.05, size=(N, K)).astype(np.float32)
+    if real_type == ol.REAL_F32:
+        return w, w.astype(np.float64)
+    if real_type == ol.REAL_F16:
+        h = w.astype(np.float16)
+        return h.view(np.uint16), h.astype(np.float64)
+    b = (w.view(np.uint32) >> 16).astype(np.uint16)
+    return b, (b.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+@pytest.mark.parametrize("real_type", [ol.REAL_F32, ol.REAL_F16, ol.REAL_BF16])
+@pytest.mark.parametrize("N,K,lanes", [(70, 1536, 1), (33, 1541, 3), (20, 7, 2)])
+def test_real_plane_closed_form(real_type, N, K, lanes):
+    raw, w64 = real_rows(N, K, real_type)
+    act = rng.normal(size=(lanes, K)).astype(np.float32)
+    got = ol.oracle_mat_mat_real(raw, real_type, act)
+    want = act.astype(np.float64) @ w64.T
+    scale = np.sqrt(np.mean(want ** 2))
+    assert np.max(np.abs(got - want)) <= 2e-6 * scale * math.sqrt(K)
+    if real_type == ol.REAL_BF16:  # reading the bits as binary16 misses it
+        wrong = ol.oracle_mat_mat_real(raw, ol.REAL_F16, act)
+        assert not np.allclose(wrong, want, rtol=1e-2)
+
+
+@pytest.mark.parametrize("real_type", [ol.REAL_F32, ol.REAL_F16, ol.REAL_BF16])
+@pytest.mark.parametrize("N,K,lanes", [(70, 1536, 1), (33, 1541, 3), (96, 8960, 2)])
+def test_real_plane_bitexact_vs_reference(ref_plain, real_type, N, K, lanes):
+    raw, _ = real_rows(N, K, real_type)
+    act = rng.normal(size=(lanes, K)).astype(np.float32)
+    got = ol.oracle_mat_mat_real(raw, real_type, act)
+    want = ol.ref_mat_mat_real(ref_plain, raw, real_type, act, threads=2)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 # ---- FP8 codec ----------------------------------------------------------------
 
 def e4m3_definition(code):
