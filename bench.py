@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decode leg")
-    ap.add_argument("--kernel", choices=["gemv", "gemv8", "gemm", "attend", "copy"],
+    ap.add_argument("--kernel", choices=["gemv", "gemv8", "gemm", "attend", "copy", "head2", "real"],
                     help="run one kernel's workload alone in a loop (for rocprofv3) and exit")
     return ap.parse_args()
 
@@ -75,6 +75,23 @@ def kernel_loop(be, name, reps):
         be.sync()
         print(json.dumps({"kernel": "copy", "bytes_each": nbytes, "reps": reps}))
         del lib
+        return
+    if name in ("head2", "real"):
+        key = "u2_head_262144x1536" if name == "head2" else "bf16_ple_model_8960x1536"
+        rot = KindRotation(be, KIND_CASES[key])
+        N, K = rot.N, rot.K
+        x = be.upload(np.random.default_rng(1).normal(size=(1, K)).astype(np.float32))
+        y = be.alloc(N * 4)
+        for i in range(3):  # first launches load the code objects
+            be.gemv_dev(rot.planes[i % rot.copies], x, K, 1, y, N)
+        be.sync()
+        be.mark()
+        for i in range(reps):
+            be.gemv_dev(rot.planes[i % rot.copies], x, K, 1, y, N)
+        be.mark()
+        us = be.marks_ms() * 1e3 / reps
+        print(json.dumps({"kernel": key, "avg_us": round(us, 3), "algorithmic_bytes": rot.algo,
+                          "GBps": round(rot.algo / (us * 1e-6) / 1e9, 1)}))
         return
     if name in ("gemv", "gemv8"):
         N, K = SHAPES[0]
@@ -219,6 +236,92 @@ def e2e_guess(be, folder, shape, prompt_count, gen, span=4, repeat=512):
             "plain_decode_tok_s": round(gen / plain_s, 1),
             "rounds": rounds, "drawn": drawn, "taken": taken,
             "streams_agree": bool(np.array_equal(ids, plain)), "first_ids": ids[:16].tolist()}
+
+
+# The shipped export's other decode products (model/config.json
+# module_quant_configs; one gain a row): name -> (N, K, bits, flip) for code
+# planes, (N, K, "bf16") for the real plane.
+KIND_CASES = {
+    "u2_mlp_gate_6144x1536": (6144, 1536, 2, 0),
+    "u2_mlp_down_1536x6144": (1536, 6144, 2, 0),
+    "u2_head_262144x1536": (262144, 1536, 2, 0),
+    "i8_ple_gate_256x1536": (256, 1536, 8, 128),
+    "i8_ple_proj_1536x256": (1536, 256, 8, 128),
+    "u4_q_proj_2048x1536": (2048, 1536, 4, 0),
+    "bf16_ple_model_8960x1536": (8960, 1536, "bf16"),
+}
+
+
+class KindRotation:
+    """Device copies of one plane of another kind (enough to pass the 256 MiB
+    MALL), each bound as its own plane; `algo` is one M=1 product's
+    algorithmic bytes."""
+
+    def __init__(self, backend, case, seed=0):
+        import ctypes
+        from igllm_amd import native
+        from igllm_amd.backend import make_plane, make_real_plane
+
+        rng = np.random.default_rng(seed)
+        N, K = case[0], case[1]
+        if case[2] == "bf16":
+            w = rng.normal(0, 0.05, size=(N, K)).astype(np.float32)
+            rows = (w.view(np.uint32) >> 16).astype(np.uint16)
+            payload, gains = rows, None
+            maker = lambda: make_real_plane(rows, native.IGL_STORE_BF16)  # noqa: E731
+            self.algo = N * K * 2 + (K + N) * 4
+        else:
+            bits, flip = case[2], case[3]
+            stride = ((K * bits + 7) // 8 + 15) // 16 * 16
+            codes = rng.integers(0, 256, size=(N, stride), dtype=np.uint8)
+            gains = np.abs(rng.normal(0, 0.02, size=(N, 1))).astype(np.float32)
+            payload = codes
+            maker = lambda: make_plane(codes, gains, K, group_size=K, bits=bits, code_flip=flip)  # noqa: E731
+            self.algo = N * stride + N * 4 + (K + N) * 4
+        pstride = (payload.nbytes + 255) // 256 * 256
+        self.copies = max(2, -(-(320 << 20) // pstride))
+        self.payload = backend.alloc(pstride * self.copies)
+        self.gains = backend.upload(gains) if gains is not None else None
+        self.planes = []
+        for c in range(self.copies):
+            self.payload.put(payload, c * pstride)
+            cp = maker()
+            code = backend.lib.igl_plane_bind_dev(
+                ctypes.byref(backend.desk), ctypes.byref(cp.plane), self.payload.ptr + c * pstride,
+                self.gains.ptr if self.gains is not None else None)
+            if code != native.IGL_OKAY:
+                raise RuntimeError(f"bind_dev: {code}")
+            self.planes.append(cp)
+        self.N, self.K = N, K
+
+
+def kinds_leg(be, reps=100):
+    """M=1 GEMV of each KIND_CASES plane, rotated copies, HIP events."""
+    out = {}
+    for name, case in KIND_CASES.items():
+        rot = KindRotation(be, case)
+        N, K = rot.N, rot.K
+        x = be.upload(np.random.default_rng(1).normal(size=(1, K)).astype(np.float32))
+        y = be.alloc(N * 4)
+        for i in range(10):
+            be.gemv_dev(rot.planes[i % rot.copies], x, K, 1, y, N)
+        be.sync()
+        be.mark()
+        for i in range(reps):
+            be.gemv_dev(rot.planes[i % rot.copies], x, K, 1, y, N)
+        be.mark()
+        us = be.marks_ms() * 1e3 / reps
+        gbps = rot.algo / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 3), "algorithmic_bytes": rot.algo, "GBps": round(gbps, 1),
+                     "frac_of_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4), "copies": rot.copies}
+        for cp in rot.planes:
+            be.detach(cp)
+        rot.payload.free()
+        if rot.gains is not None:
+            rot.gains.free()
+        x.free()
+        y.free()
+    return out
 
 
 class Rotation:
@@ -445,6 +548,7 @@ def main():
                  "note": f"int8 K/V rings rotated over {rings} copies (past the MALL); "
                          "includes the chunk-merge launch"}
 
+    kinds = kinds_leg(be)
     e2e = None if args.no_e2e else e2e_decode(be)
     cpu = None if args.no_cpu else cpu_baseline()
 
@@ -475,6 +579,7 @@ def main():
         "gemv_sweep": sweep,
         "prefill_gemm": prefill,
         "decode_attention": attention,
+        "other_plane_kinds_m1": kinds,
         "decode_tok_s": None if not e2e else e2e["precise"]["decode_tok_s"],
         "e2e": e2e,
     }

@@ -522,7 +522,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
 //
 // The shipped export's other planes: 2-bit (four codes a byte, low bits
 // first, value + 2), 8-bit signed I8 (code_flip 128: the byte itself is the
-// value) and one gain a row (group_shift 31).  The same layout as
+// value) and one gain a row (group_shift 31).  The same arithmetic as
 // gemv_q4_dot_kernel, over 16-byte slots of codes instead of units: a slot
 // is two units of 2-bit codes, one of 4-bit codes, half of one of 8-bit codes.
 // Per row and slot a lane spends
@@ -533,9 +533,17 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
 // bits), times 2^(E - P) and the gain.  2-bit codes are dotted unsigned and
 // their bias leaves through the staged activation sum (qsum); 4- and 8-bit
 // codes are made signed by one xor with (code_flip ^ code_bias) replicated.
-// `blockIdx.y` takes a K-chunk of `chunk_cols` columns (a multiple of 128);
-// chunks write partials [chunk][M][N] that gemv_chunk_sum_kernel adds.
-// `lanes` <= M: lanes past it reread the last lane and are not stored.
+//
+// Layout: a wave's 64 lanes are 2^subs_log sub-waves of 64 >> subs_log lanes,
+// each over R rows of its own (short rows: a 2-bit row of 1536 codes is 24
+// slots, so two sub-waves of 32 lanes keep 48 lanes busy instead of 24); a
+// lane takes slots sl, sl + 64, ... of its rows; `ksplit` waves may share a
+// row tile.  After the one staging of x, a workgroup walks `tile_iters` row
+// tiles, gridDim.x tile groups apart, with the next tile's gains and codes
+// requested before the current tile's arithmetic.  `blockIdx.y` takes a
+// K-chunk of `chunk_cols` columns (a multiple of 128); chunks write partials
+// [chunk][lanes][N] that gemv_chunk_sum_kernel adds.  `lanes` <= M: lanes past
+// it reread the last lane and are not stored.
 struct GemvCodeArgs {
   const uint8_t *codes;
   long long row_stride;
@@ -544,12 +552,14 @@ struct GemvCodeArgs {
   int group_shift;        // gain of unit u: u >> group_shift (31: one gain a row)
   const float *act;       // 16-byte aligned, act_stride % 4 == 0
   int act_stride;
-  float *out;             // [lanes][out_stride], or partials [chunk][M][N]
+  float *out;             // [lanes][out_stride], or partials [chunk][lanes][N]
   int out_stride;
   int lanes;
   int N, K;
   int chunk_cols;
   int ks_log;             // log2 of the waves that share a row tile
+  int subs_log;           // log2 of the sub-waves (0 unless ks_log == 0 and UPL == 1)
+  int tile_iters;         // row tiles a wave walks
   uint32_t code_xor;      // 4, 8-bit: makes a dword of codes signed values; 2-bit: undoes the flip
   int code_bias;          // 2-bit: taken off through qsum
 };
@@ -558,31 +568,89 @@ __host__ __device__ constexpr size_t gemv_code_lds_bytes(int M, int units) {
   return (size_t)M * units * (6 * 16 + 8);
 }
 
-template <int BITS, int M, int R, int UPL, int GPT>
+// Sum over each sub-wave of 64 >> subs_log lanes; the total lands in the
+// sub-wave's last lane.
+__device__ __forceinline__ float sub_sum_to_last(float v, int subs_log) {
+  v += dpp_move<0xB1>(v);
+  v += dpp_move<0x4E>(v);
+  v += dpp_move<0x141>(v);
+  v += dpp_move<0x140>(v);
+  if (subs_log >= 2) return v;
+  v += dpp_move<0x142, 0xA>(v);
+  if (subs_log == 1) return v;
+  v += dpp_move<0x143, 0xC>(v);
+  return v;
+}
+
+template <int BITS, int R, int UPL>
+struct CodeTile {
+  static constexpr int kSub = BITS == 2 ? 2 : 1;  // units a slot's gains cover
+  uint4_t w[UPL][R];
+  float s[UPL][R][kSub];
+};
+
+// TILED: the workgroup walks a.tile_iters tiles; otherwise exactly one.
+template <int BITS, int M, int R, int UPL, int GPT, bool TILED>
 __global__ __launch_bounds__(kGemvThreads) void gemv_code_dot_kernel(GemvCodeArgs a) {
   constexpr int FORM = CodeForm<BITS>::kDigits;
+  constexpr int kSub = CodeTile<BITS, R, UPL>::kSub;
   extern __shared__ uint4_t lds_dig[];
   __shared__ float red[4][R][M];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ks_log = __builtin_amdgcn_readfirstlane(a.ks_log);
-  const int tile = blockIdx.x * (4 >> ks_log) + (wave >> ks_log);
+  const int subs_log = __builtin_amdgcn_readfirstlane(a.subs_log);
   const int ks = wave & ((1 << ks_log) - 1);
-  const int row0 = tile * R;
+  const int sub = lane >> (6 - subs_log);
+  const int sub_lane = lane & ((64 >> subs_log) - 1);
+  const int rows_per_tile = R << subs_log;
+  const int tile_step = gridDim.x * (4 >> ks_log);
   const int col0 = blockIdx.y * a.chunk_cols;
   const int cols = min(a.chunk_cols, a.K - col0);
   const int units = cols >> 5;
   const int slots = (cols * BITS + 127) >> 7;
   const int s_end = (slots * (ks + 1)) >> ks_log;
-  const int s_first = ((slots * ks) >> ks_log) + lane;
+  const int s_first = ((slots * ks) >> ks_log) + sub_lane;
   const int unit0 = col0 >> 5;
+  const uint8_t *code0 = a.codes + (size_t)(col0 / 8) * BITS;
   uint4_t *dig = lds_dig;
   int *down = reinterpret_cast<int *>(dig + M * 6 * units);
   int *qsum = down + M * units;
-  constexpr int kSub = BITS == 2 ? 2 : 1;  // units a slot's gains cover
 
-  // Activations first, then gains, then codes, all unconditional (clamped).
+  // Every load unconditional (clamped rows, slots and units), gains before
+  // codes; rows past N and slots past the part get gain 0.
+  auto load_tile = [&](int tile, CodeTile<BITS, R, UPL> &t) {
+    const int row0 = tile * rows_per_tile + sub * R;
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) {
+      const int sl = min(s_first + 64 * j, slots - 1);
+      const bool in = s_first + 64 * j < s_end;
+#pragma unroll
+      for (int h = 0; h < kSub; ++h) {
+        const int u_raw = BITS == 2 ? 2 * sl + h : BITS == 8 ? sl >> 1 : sl;
+        const int u = min(u_raw, units - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int row = min(row0 + r, a.N - 1);
+          const float g = a.gains[(size_t)row * (size_t)a.gain_stride + ((unsigned)(unit0 + u) >> a.group_shift)];
+          t.s[j][r][h] = in && u_raw < units && row0 + r < a.N ? g : 0.0f;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) {
+      const int sl = min(s_first + 64 * j, slots - 1);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, a.N - 1);
+        t.w[j][r] = __builtin_nontemporal_load(
+            reinterpret_cast<const uint4_t *>(code0 + (size_t)row * (size_t)a.row_stride) + sl);
+      }
+    }
+  };
+
+  // Activations first, then the first tile's weights.
   DigitLoads<GPT> held;
   {
     const int last = a.lanes - 1;
@@ -598,150 +666,135 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_code_dot_kernel(GemvCodeArg
       held.x[i][4] = q.x; held.x[i][5] = q.y; held.x[i][6] = q.z; held.x[i][7] = q.w;
     }
   }
-  uint4_t w[UPL][R];
-  float s[UPL][R][kSub];
-  bool live[UPL][kSub];
-#pragma unroll
-  for (int j = 0; j < UPL; ++j) {
-    const int sl = min(s_first + kWave * j, slots - 1);
-#pragma unroll
-    for (int h = 0; h < kSub; ++h) {
-      const int u_raw = BITS == 2 ? 2 * sl + h : BITS == 8 ? sl >> 1 : sl;
-      live[j][h] = row0 < a.N && s_first + kWave * j < s_end && u_raw < units;
-      const int u = min(u_raw, units - 1);
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int row = min(row0 + r, a.N - 1);
-        s[j][r][h] = a.gains[(size_t)row * (size_t)a.gain_stride + ((unsigned)(unit0 + u) >> a.group_shift)];
-      }
-    }
-  }
-  const uint8_t *code0 = a.codes + (size_t)(col0 / 8) * BITS;
-#pragma unroll
-  for (int j = 0; j < UPL; ++j) {
-    const int sl = min(s_first + kWave * j, slots - 1);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = min(row0 + r, a.N - 1);
-      w[j][r] = __builtin_nontemporal_load(
-          reinterpret_cast<const uint4_t *>(code0 + (size_t)row * (size_t)a.row_stride) + sl);
-    }
-  }
+  int tile = blockIdx.x * (4 >> ks_log) + (wave >> ks_log);
+  CodeTile<BITS, R, UPL> cur;
+  load_tile(tile, cur);
   digit_store_form<M, GPT, FORM>(held, cols, dig, down, qsum);
 
-  float acc[R][M];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
   const uint32_t cx = a.code_xor;
+  const int tiles_total = (a.N + rows_per_tile - 1) / rows_per_tile;
+  const int iters = TILED ? a.tile_iters : 1;
+  for (int it = 0; it < iters; ++it) {
+    CodeTile<BITS, R, UPL> nxt;
+    if constexpr (TILED) load_tile(min(tile + tile_step, tiles_total - 1), nxt);
+
+    float acc[R][M];
 #pragma unroll
-  for (int uj = 0; uj < UPL; ++uj) {
-    const int sl = min(s_first + kWave * uj, slots - 1);
-    if constexpr (BITS == 4) {
-      const int u = sl;
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int m = 0; m < M; ++m) {
-        uint4_t dd[6];
+      for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 6; ++j) dd[j] = dig[(m * 6 + j) * units + u];
-        const int shift = down[m * units + u];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const uint4_t c = w[uj][r] ^ cx;
-          int t[6];
-#pragma unroll
-          for (int j = 0; j < 6; ++j) t[j] = 0;
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int j = 0; j < 6; ++j) t[j] = __builtin_amdgcn_sdot8((int)c[q], (int)dd[j][q], t[j], false);
-          const float gain = live[uj][0] ? s[uj][r][0] : 0.0f;
-          acc[r][m] = __builtin_fmaf(gain, __builtin_amdgcn_ldexpf(digit_sum<6>(t), shift), acc[r][m]);
-        }
-      }
-    } else if constexpr (BITS == 2) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int u = min(2 * sl + h, units - 1);
+    for (int uj = 0; uj < UPL; ++uj) {
+      const int sl = min(s_first + 64 * uj, slots - 1);
+      if constexpr (BITS == 4) {
+        const int u = sl;
 #pragma unroll
         for (int m = 0; m < M; ++m) {
           uint4_t dd[6];
 #pragma unroll
           for (int j = 0; j < 6; ++j) dd[j] = dig[(m * 6 + j) * units + u];
           const int shift = down[m * units + u];
-          const int bq = a.code_bias * qsum[m * units + u];
 #pragma unroll
           for (int r = 0; r < R; ++r) {
-            const uint32_t c0 = w[uj][r][2 * h] ^ cx, c1 = w[uj][r][2 * h + 1] ^ cx;
-            const uint32_t n[4] = {c0 & 0x33333333u, (c0 >> 2) & 0x33333333u, c1 & 0x33333333u,
-                                   (c1 >> 2) & 0x33333333u};
+            const uint4_t c = cur.w[uj][r] ^ cx;
             int t[6];
 #pragma unroll
             for (int j = 0; j < 6; ++j) t[j] = 0;
 #pragma unroll
             for (int q = 0; q < 4; ++q)
 #pragma unroll
-              for (int j = 0; j < 6; ++j) t[j] = __builtin_amdgcn_sdot8((int)n[q], (int)dd[j][q], t[j], false);
-            const float gain = live[uj][h] ? s[uj][r][h] : 0.0f;
-            acc[r][m] = __builtin_fmaf(gain, __builtin_amdgcn_ldexpf(pair_digit_sum(t, bq), shift), acc[r][m]);
+              for (int j = 0; j < 6; ++j) t[j] = __builtin_amdgcn_sdot8((int)c[q], (int)dd[j][q], t[j], false);
+            acc[r][m] = __builtin_fmaf(cur.s[uj][r][0], __builtin_amdgcn_ldexpf(digit_sum<6>(t), shift), acc[r][m]);
+          }
+        }
+      } else if constexpr (BITS == 2) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int u = min(2 * sl + h, units - 1);
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            uint4_t dd[6];
+#pragma unroll
+            for (int j = 0; j < 6; ++j) dd[j] = dig[(m * 6 + j) * units + u];
+            const int shift = down[m * units + u];
+            const int bq = a.code_bias * qsum[m * units + u];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              const uint32_t c0 = cur.w[uj][r][2 * h] ^ cx, c1 = cur.w[uj][r][2 * h + 1] ^ cx;
+              const uint32_t n[4] = {c0 & 0x33333333u, (c0 >> 2) & 0x33333333u, c1 & 0x33333333u,
+                                     (c1 >> 2) & 0x33333333u};
+              int t[6];
+#pragma unroll
+              for (int j = 0; j < 6; ++j) t[j] = 0;
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int j = 0; j < 6; ++j) t[j] = __builtin_amdgcn_sdot8((int)n[q], (int)dd[j][q], t[j], false);
+              acc[r][m] = __builtin_fmaf(cur.s[uj][r][h], __builtin_amdgcn_ldexpf(pair_digit_sum(t, bq), shift),
+                                         acc[r][m]);
+            }
+          }
+        }
+      } else {
+        const int u = sl >> 1, hf = sl & 1;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          uint4_t dd[3];
+#pragma unroll
+          for (int j = 0; j < 3; ++j) dd[j] = dig[(m * 6 + 2 * j + hf) * units + u];
+          const int shift = down[m * units + u];
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const uint4_t c = cur.w[uj][r] ^ cx;
+            int t[3] = {0, 0, 0};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+              for (int j = 0; j < 3; ++j) t[j] = __builtin_amdgcn_sdot4((int)c[q], (int)dd[j][q], t[j], false);
+            acc[r][m] = __builtin_fmaf(cur.s[uj][r][0],
+                                       __builtin_amdgcn_ldexpf(byte_digit_sum(t[0], t[1], t[2]), shift), acc[r][m]);
           }
         }
       }
-    } else {
-      const int u = sl >> 1, hf = sl & 1;
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        uint4_t dd[3];
-#pragma unroll
-        for (int j = 0; j < 3; ++j) dd[j] = dig[(m * 6 + 2 * j + hf) * units + u];
-        const int shift = down[m * units + u];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const uint4_t c = w[uj][r] ^ cx;
-          int t[3] = {0, 0, 0};
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int j = 0; j < 3; ++j) t[j] = __builtin_amdgcn_sdot4((int)c[q], (int)dd[j][q], t[j], false);
-          const float gain = live[uj][0] ? s[uj][r][0] : 0.0f;
-          acc[r][m] = __builtin_fmaf(gain, __builtin_amdgcn_ldexpf(byte_digit_sum(t[0], t[1], t[2]), shift),
-                                     acc[r][m]);
-        }
-      }
     }
-  }
 
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int m = 0; m < M; ++m) acc[r][m] = wave_sum_to_last(acc[r][m]);
-
-  float *dst = a.out + (size_t)blockIdx.y * (size_t)a.lanes * (size_t)a.out_stride;
-  if (ks_log == 0) {
-    if (lane == 63) {
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (row0 + r < a.N)
-#pragma unroll
-          for (int m = 0; m < M; ++m)
-            if (m < a.lanes) dst[(size_t)m * a.out_stride + row0 + r] = acc[r][m];
-    }
-    return;
-  }
-  if (lane == 63) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int m = 0; m < M; ++m) red[wave][r][m] = acc[r][m];
-  }
-  __syncthreads();
-  if (ks == 0 && lane < R * M) {
-    const int r = lane / M;
-    const int m = lane - r * M;
-    float total = 0.0f;
-    for (int k = 0; k < (1 << ks_log); ++k) total += red[wave + k][r][m];
-    if (row0 + r < a.N && m < a.lanes) dst[(size_t)m * a.out_stride + row0 + r] = total;
+      for (int m = 0; m < M; ++m) acc[r][m] = sub_sum_to_last(acc[r][m], subs_log);
+
+    const int row0 = tile * rows_per_tile + sub * R;
+    float *dst = a.out + (size_t)blockIdx.y * (size_t)a.lanes * (size_t)a.out_stride;
+    if (ks_log == 0) {
+      if (sub_lane == (64 >> subs_log) - 1) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (row0 + r < a.N)
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+              if (m < a.lanes) dst[(size_t)m * a.out_stride + row0 + r] = acc[r][m];
+      }
+    } else {
+      // one tile a wave group (tile_iters == 1, subs_log == 0)
+      if (lane == 63) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int m = 0; m < M; ++m) red[wave][r][m] = acc[r][m];
+      }
+      __syncthreads();
+      if (ks == 0 && lane < R * M) {
+        const int r = lane / M;
+        const int m = lane - r * M;
+        float total = 0.0f;
+        for (int k = 0; k < (1 << ks_log); ++k) total += red[wave + k][r][m];
+        if (row0 + r < a.N && m < a.lanes) dst[(size_t)m * a.out_stride + row0 + r] = total;
+      }
+    }
+    if constexpr (TILED) {
+      tile += tile_step;
+      cur = nxt;
+    }
   }
 }
 
@@ -1711,16 +1764,32 @@ static int code_chunk_cols(int bits, int M, int K) {
   return (per + 127) / 128 * 128;
 }
 
+// Workgroups a tiled launch keeps: eight a CU.
+constexpr int kCodeTiledBlocks = 2048;
+
 template <int BITS, int M, int UPL, int GPT>
 static hipError_t gemv_code_launch4(const GemvCodeArgs &a, dim3 grid, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((gemv_code_dot_kernel<BITS, M, 4, UPL, GPT>), grid, dim3(kGemvThreads), lds, stream, a);
+  // the tiled walk only for one lane and one slot a lane (tall decode planes)
+  if constexpr (M == 1 && UPL == 1) {
+    if (a.tile_iters > 1) {
+      hipLaunchKernelGGL((gemv_code_dot_kernel<BITS, M, 4, UPL, GPT, true>), grid, dim3(kGemvThreads), lds,
+                         stream, a);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((gemv_code_dot_kernel<BITS, M, 4, UPL, GPT, false>), grid, dim3(kGemvThreads), lds, stream,
+                     a);
   return hipGetLastError();
 }
 
 template <int BITS, int M>
 static hipError_t gemv_code_launch_m(const GemvCodeArgs &a, int upl, int gpt, dim3 grid, size_t lds,
                                      hipStream_t stream) {
-  if (upl == 1) {
+  // more than 256 slots a row happen only for one lane of 4- or 8-bit codes and
+  // two lanes of 8-bit codes (code_chunk_cols)
+  constexpr bool kTwoSlots = (M == 1 && BITS >= 4) || (M == 2 && BITS == 8);
+  if (upl == 1 || !kTwoSlots) {
+    if (upl != 1) return hipErrorInvalidValue;
     switch (gpt) {
       case 1: return gemv_code_launch4<BITS, M, 1, 1>(a, grid, lds, stream);
       case 2: return gemv_code_launch4<BITS, M, 1, 2>(a, grid, lds, stream);
@@ -1728,12 +1797,15 @@ static hipError_t gemv_code_launch_m(const GemvCodeArgs &a, int upl, int gpt, di
       default: return gemv_code_launch4<BITS, M, 1, 8>(a, grid, lds, stream);
     }
   }
-  switch (gpt) {
-    case 1: return gemv_code_launch4<BITS, M, 2, 1>(a, grid, lds, stream);
-    case 2: return gemv_code_launch4<BITS, M, 2, 2>(a, grid, lds, stream);
-    case 4: return gemv_code_launch4<BITS, M, 2, 4>(a, grid, lds, stream);
-    default: return gemv_code_launch4<BITS, M, 2, 8>(a, grid, lds, stream);
+  if constexpr (kTwoSlots) {
+    switch (gpt) {
+      case 1: return gemv_code_launch4<BITS, M, 2, 1>(a, grid, lds, stream);
+      case 2: return gemv_code_launch4<BITS, M, 2, 2>(a, grid, lds, stream);
+      case 4: return gemv_code_launch4<BITS, M, 2, 4>(a, grid, lds, stream);
+      default: return gemv_code_launch4<BITS, M, 2, 8>(a, grid, lds, stream);
+    }
   }
+  return hipErrorInvalidValue;
 }
 
 template <int BITS>
@@ -1787,12 +1859,14 @@ extern "C" hipError_t igl_launch_gemv_codes(const igl_code_view *v, const float 
     const int M = code_launch_lanes(l);
     const int cols = code_chunk_cols(bits, M, K);
     const int chunks = (K + cols - 1) / cols;
-    const int slots = cols * bits / 128;
+    const int slots = (cols * bits + 127) / 128;
     const int upl = slots > 4 * kWave ? 2 : 1;
-    const int tiles = (N + 3) / 4;
+    // short rows: sub-waves of 16 or 32 lanes, each over its own rows
+    const int subs_log = upl == 1 && slots <= 16 ? 2 : upl == 1 && slots <= 32 ? 1 : 0;
+    const int tiles = (N + (4 << subs_log) - 1) / (4 << subs_log);
     int ksplit = 1;
-    while (ksplit < 4 && (slots > ksplit * kWave * upl ||
-                          (tiles * ksplit * chunks < 2048 && slots / (ksplit * 2) >= 32 * upl)))
+    while (subs_log == 0 && ksplit < 4 &&
+           (slots > ksplit * kWave * upl || (tiles * ksplit * chunks < 2048 && slots / (ksplit * 2) >= 32 * upl)))
       ksplit *= 2;
     const int items = (M * (cols >> 3) + kGemvThreads - 1) / kGemvThreads;
     const int gpt = items <= 1 ? 1 : items <= 2 ? 2 : items <= 4 ? 4 : 8;
@@ -1801,6 +1875,7 @@ extern "C" hipError_t igl_launch_gemv_codes(const igl_code_view *v, const float 
     a.lanes = l;
     a.chunk_cols = cols;
     a.ks_log = ksplit == 1 ? 0 : ksplit == 2 ? 1 : 2;
+    a.subs_log = subs_log;
     if (chunks > 1) {
       if (!part) return hipErrorInvalidValue;
       a.out = part;
@@ -1810,7 +1885,12 @@ extern "C" hipError_t igl_launch_gemv_codes(const igl_code_view *v, const float 
       a.out_stride = out_stride;
     }
     const int per_block = 4 / ksplit;
-    const dim3 grid((tiles + per_block - 1) / per_block, chunks);
+    const int blocks = (tiles + per_block - 1) / per_block;
+    // a tall one-lane plane: fewer workgroups, each walking several row tiles
+    // after one staging of x
+    const bool tiled = M == 1 && upl == 1 && ksplit == 1 && chunks == 1 && blocks > kCodeTiledBlocks;
+    a.tile_iters = tiled ? (blocks + kCodeTiledBlocks - 1) / kCodeTiledBlocks : 1;
+    const dim3 grid(tiled ? kCodeTiledBlocks : blocks, chunks);
     const size_t lds = gemv_code_lds_bytes(M, cols / 32);
     hipError_t e = bits == 2   ? gemv_code_launch_bits<2>(a, M, upl, gpt, grid, lds, stream)
                    : bits == 4 ? gemv_code_launch_bits<4>(a, M, upl, gpt, grid, lds, stream)
