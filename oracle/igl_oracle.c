@@ -301,6 +301,93 @@ int oracle_mat_mat(const oracle_plane *sheet, const float *act, int act_stride, 
   return 0;
 }
 
+/* The product of a plane the export calibrated (enter_gain = step > 0) on the
+ * integer grid, the reference's level path (back_mat_mat 5283-5306 with
+ * exact_flag; kern_level_stage 2924-2963, kern_row_code_level 3272-3296 and
+ * kern_row_code_level_many 4204-4229): each activation is its quant_step
+ * level L = rint(x / step) clamped to [-128, 127] (kern_level_of reads the
+ * same level back off quant_step's output), and per group
+ *     part = sum ((code ^ flip) L) - bias sum L        (exact, 64-bit)
+ *     total += gain * step * (float)part               (in group order).
+ * The reference takes this path only where kern_level_ready holds (2, 4 or 8
+ * bits; one group, or groups a multiple of 64 columns) and every value of every
+ * lane of the 16-lane chunk is on the grid; otherwise the chunk goes to the
+ * float path on the quant_step values, and so does this function (a NaN is
+ * what puts a value off the grid here).  Returns 0. */
+static int oracle_level_ready(const oracle_plane *sheet) {
+  int span;
+  if (sheet->bit_count != 2 && sheet->bit_count != 4 && sheet->bit_count != 8) return 0;
+  if (sheet->group_count > 1 && sheet->group_size % 64) return 0;
+  span = sheet->group_count > 1 ? sheet->group_size : sheet->col_count;
+  return (int64_t)span * (int64_t)((1 << sheet->bit_count) - 1) * 128 <= (int64_t)INT32_MAX;
+}
+
+int oracle_mat_mat_level(const oracle_plane *sheet, const float *act, int act_stride,
+                         int lane_count, float step, float *out, int out_stride) {
+  int K = sheet->col_count;
+  int8_t *levels = (int8_t *)malloc((size_t)K * ORACLE_LANE_LIMIT);
+  float *grid = (float *)malloc(sizeof(float) * (size_t)K * ORACLE_LANE_LIMIT);
+  int64_t *lsum = (int64_t *)malloc(sizeof(int64_t) * (size_t)sheet->group_count * ORACLE_LANE_LIMIT);
+  int done = 0, rc = 0;
+  if (!levels || !grid || !lsum) {
+    rc = -2;
+    goto out;
+  }
+  while (done < lane_count) {
+    int chunk = lane_count - done < ORACLE_LANE_LIMIT ? lane_count - done : ORACLE_LANE_LIMIT;
+    int on_grid = oracle_level_ready(sheet);
+    for (int l = 0; l < chunk; ++l)
+      for (int k = 0; k < K; ++k) {
+        float v = act[(size_t)(done + l) * (size_t)act_stride + (size_t)k];
+        float level = rintf(v / step);
+        if (level < -128.0f) level = -128.0f;
+        if (level > 127.0f) level = 127.0f;
+        grid[(size_t)l * (size_t)K + (size_t)k] = level * step;
+        if (level != level) on_grid = 0;
+        else levels[(size_t)l * (size_t)K + (size_t)k] = (int8_t)level;
+      }
+    if (!on_grid) {
+      rc = oracle_mat_mat(sheet, grid, K, chunk, out + (size_t)done * (size_t)out_stride, out_stride, 1);
+      if (rc) goto out;
+      done += chunk;
+      continue;
+    }
+    for (int l = 0; l < chunk; ++l)
+      for (int g = 0; g < sheet->group_count; ++g) {
+        int lo = g * sheet->group_size;
+        int hi = lo + sheet->group_size < K ? lo + sheet->group_size : K;
+        int64_t s = 0;
+        for (int k = lo; k < hi; ++k) s += levels[(size_t)l * (size_t)K + (size_t)k];
+        lsum[(size_t)l * (size_t)sheet->group_count + (size_t)g] = s;
+      }
+    for (int n = 0; n < sheet->row_count; ++n) {
+      const uint8_t *row = sheet->code_data + (size_t)n * sheet->row_stride;
+      for (int l = 0; l < chunk; ++l) {
+        float total = 0.0f;
+        for (int g = 0; g < sheet->group_count; ++g) {
+          size_t at = (size_t)n * (size_t)sheet->group_count + (size_t)g;
+          int lo = g * sheet->group_size;
+          int hi = lo + sheet->group_size < K ? lo + sheet->group_size : K;
+          int64_t bias = sheet->code_bias + (sheet->bias_data ? sheet->bias_data[at] : 0);
+          int64_t part = 0;
+          for (int k = lo; k < hi; ++k)
+            part += (int64_t)(oracle_pack_read(row, (size_t)k, sheet->bit_count) ^ (uint32_t)sheet->code_flip) *
+                    (int64_t)levels[(size_t)l * (size_t)K + (size_t)k];
+          part -= bias * lsum[(size_t)l * (size_t)sheet->group_count + (size_t)g];
+          total += sheet->gain_data[at] * step * (float)part;
+        }
+        out[(size_t)(done + l) * (size_t)out_stride + (size_t)n] = total;
+      }
+    }
+    done += chunk;
+  }
+out:
+  free(levels);
+  free(grid);
+  free(lsum);
+  return rc;
+}
+
 /* A real plane's product (kern_mat_vec_band's PLANE_REAL arm,
  * app_core.c:4239-4248): every row against every lane with kern_dot_real.
  * fp32 and bf16 rows take its SSE2 blocks (2048-2066 and 2102-2112: a bf16

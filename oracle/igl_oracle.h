@@ -16,6 +16,9 @@
  *   pack_read / plane_row  - the reference's nibble KAT (app_test.c:593-594,
  *                            651-658) and an independent bit writer
  *   row_code / mat_mat     - closed form in double; bit-exact vs oracle/_ref
+ *   mat_mat_level          - closed form in double; bit-exact vs the level
+ *                            (AVX-512 VNNI) build of oracle/_ref
+ *   mat_mat_real           - closed form in double; bit-exact vs oracle/_ref
  *   FP8 codec              - all 256 codes against the e4m3 definition and
  *                            torch.float8_e4m3fn; round trip; bit-exact vs _ref
  *   exp_near / soft_max    - libm exp and the softmax definition; vs _ref
@@ -63,14 +66,19 @@ void  oracle_row_code_many(const oracle_plane *sheet, int row_index, const float
                            int sum_stride, float *out, int out_stride);
 /* back_mat_mat on a plain build: chunks of 16 lanes, group sums, then rows
  * banded over `thread_count` threads (1 = serial). */
+int   oracle_mat_mat(const oracle_plane *sheet, const float *act, int act_stride,
+                     int lane_count, float *out, int out_stride, int thread_count);
+/* back_mat_mat on a calibrated plane (enter_gain = step) on the level tier:
+ * activations as their quant_step levels, exact integer sums per group. */
+int   oracle_mat_mat_level(const oracle_plane *sheet, const float *act, int act_stride,
+                           int lane_count, float step, float *out, int out_stride);
+/* back_mat_mat on a real plane (kern_dot_real per row and lane). */
 #define ORACLE_REAL_F32  1  /* STORE_F32, app_core.c:1414 */
 #define ORACLE_REAL_F16  2
 #define ORACLE_REAL_BF16 3
 int   oracle_mat_mat_real(const void *real_data, int real_type, int row_count, int col_count,
                           const float *act, int act_stride, int lane_count, float *out,
                           int out_stride);
-int   oracle_mat_mat(const oracle_plane *sheet, const float *act, int act_stride,
-                     int lane_count, float *out, int out_stride, int thread_count);
 
 /* FP8 E4M3 cache codec and its decode table */
 float   oracle_pack8(float value);

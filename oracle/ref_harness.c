@@ -7,15 +7,17 @@
  * below through -I), into oracle/_ref/, which git ignores.  No reference source
  * is copied into this repository; nothing in igllm_amd/ links this.
  *
- * Two builds are made: a plain one (SSE2 tier, the float path the oracle
- * restates to the bit) and a tuned one (-mavx2 -mfma, the reference's fastest
- * float path on x86, used as the CPU baseline).  Neither enables the VNNI
- * integer grid, which rounds activations and is not the fp32 oracle.
+ * Three builds are made: a plain one (SSE2 tier, the float path the oracle
+ * restates to the bit), a tuned one (-mavx2 -mfma, the reference's fastest
+ * float path on x86, used as the CPU baseline), and a level one
+ * (REF_LEVEL_TIER: AVX-512 VNNI), whose products take the integer grid: the
+ * calibrated-plane path oracle_mat_mat_level restates.  The float builds
+ * refuse the VNNI tier, whose uncalibrated products round activations.
  */
 #include "app_core.c"
 
-#if defined(APP_SIMD_AVX512VNNI)
-#  error "the harness must not be built on the integer-grid tier"
+#if defined(APP_SIMD_AVX512VNNI) && !defined(REF_LEVEL_TIER)
+#  error "the float builds of the harness must not take the integer-grid tier"
 #endif
 
 /* Flat description of a code plane; the fields of `plane` (app_core.c:1775)
@@ -96,6 +98,20 @@ void ref_desk_mat_mat(void *handle, const ref_plane_desc *desc, const float *act
   ref_plane_fill(desc, &sheet);
   box->desk.mat_mat(&box->desk, &sheet, act, act_stride, lane_count, out, out_stride);
 }
+
+/* The desk entry on a calibrated plane (enter_gain = step): on the level
+ * build (REF_LEVEL_TIER, AVX-512 VNNI) a chunk whose values all sit on the
+ * step's grid takes the integer level path (back_mat_mat 5283-5306). */
+void ref_desk_mat_mat_step(void *handle, const ref_plane_desc *desc, float step, const float *act,
+                           int act_stride, int lane_count, float *out, int out_stride) {
+  ref_desk *box = (ref_desk *)handle;
+  plane sheet;
+  ref_plane_fill(desc, &sheet);
+  sheet.enter_gain = step;
+  box->desk.mat_mat(&box->desk, &sheet, act, act_stride, lane_count, out, out_stride);
+}
+
+int ref_level_live(void *handle) { return ((ref_desk *)handle)->desk.level_live; }
 
 /* The same desk entry on a real plane: `real_type` is the reference's
  * store_type (STORE_F32, STORE_F16, STORE_BF16). */

@@ -14,6 +14,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_PATH = os.path.join(ROOT, "oracle", "liboracle.so")
 REF_PLAIN_PATH = os.path.join(ROOT, "oracle", "_ref", "libigl_ref_plain.so")
 REF_TUNED_PATH = os.path.join(ROOT, "oracle", "_ref", "libigl_ref_tuned.so")
+REF_LEVEL_PATH = os.path.join(ROOT, "oracle", "_ref", "libigl_ref_level.so")
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -48,6 +49,7 @@ ORACLE_SIGS = {
     "oracle_row_code": (_F, [ctypes.POINTER(PlaneDesc), _I, _P, _P]),
     "oracle_mat_mat": (_I, [ctypes.POINTER(PlaneDesc), _P, _I, _I, _P, _I, _I]),
     "oracle_mat_mat_real": (_I, [_P, _I, _I, _I, _P, _I, _I, _P, _I]),
+    "oracle_mat_mat_level": (_I, [ctypes.POINTER(PlaneDesc), _P, _I, _I, _F, _P, _I]),
     "oracle_pack8": (_F, [_F]),
     "oracle_code8": (ctypes.c_uint8, [_F]),
     "oracle_real8": (_F, [ctypes.c_uint8]),
@@ -73,6 +75,8 @@ REF_SIGS = {
     "ref_desk_close": (None, [_P]),
     "ref_desk_mat_mat": (None, [_P, ctypes.POINTER(PlaneDesc), _P, _I, _I, _P, _I]),
     "ref_desk_mat_mat_real": (None, [_P, _P, _I, _I, _I, _P, _I, _I, _P, _I]),
+    "ref_desk_mat_mat_step": (None, [_P, ctypes.POINTER(PlaneDesc), _F, _P, _I, _I, _P, _I]),
+    "ref_level_live": (_I, [_P]),
     "ref_cache_pack8": (_F, [_F]),
     "ref_cache_code8": (ctypes.c_uint8, [_F]),
     "ref_cache_real8": (_F, [ctypes.c_uint8]),
@@ -102,10 +106,20 @@ def oracle():
     return _cache["oracle"]
 
 
+def host_has_vnni() -> bool:
+    try:
+        flags = open("/proc/cpuinfo").read()
+    except OSError:
+        return False
+    return all(f" {f}" in flags for f in ("avx512f", "avx512bw", "avx512dq", "avx512vl", "avx512_vnni",
+                                          "gfni"))
+
+
 def ref(kind: str = "plain"):
-    """The compiled reference harness, or None where it was not built."""
-    path = REF_PLAIN_PATH if kind == "plain" else REF_TUNED_PATH
-    if not os.path.exists(path):
+    """The compiled reference harness (plain, tuned or level), or None where it
+    was not built, or for the level build, where this host lacks AVX-512 VNNI."""
+    path = {"plain": REF_PLAIN_PATH, "tuned": REF_TUNED_PATH, "level": REF_LEVEL_PATH}[kind]
+    if not os.path.exists(path) or (kind == "level" and not host_has_vnni()):
         return None
     key = "ref_" + kind
     if key not in _cache:
@@ -164,6 +178,42 @@ def ref_mat_mat(lib, codes, gains, act, K, group_size=32, threads=1, **kw) -> np
 
 
 REAL_F32, REAL_F16, REAL_BF16 = 1, 2, 3  # the reference's store_type values
+
+
+def quant_step(x, step):
+    """quant_step (app_core.c:1930-1940) through the oracle, element by element."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    f = oracle().oracle_quant_step
+    return np.array([f(float(v), step) for v in x.ravel()], dtype=np.float32).reshape(x.shape)
+
+
+def oracle_mat_mat_level(codes, gains, act, K, group_size, step, **kw) -> np.ndarray:
+    codes = np.ascontiguousarray(codes)
+    gains = np.ascontiguousarray(gains, dtype=np.float32)
+    act = np.ascontiguousarray(act, dtype=np.float32)
+    out = np.empty((act.shape[0], codes.shape[0]), dtype=np.float32)
+    d = plane_desc(codes, gains, K, group_size, **kw)
+    rc = oracle().oracle_mat_mat_level(ctypes.byref(d), p(act), act.shape[1], act.shape[0], step, p(out),
+                                       codes.shape[0])
+    assert rc == 0
+    return out
+
+
+def ref_mat_mat_step(lib, codes, gains, act, K, group_size, step, threads=1, **kw) -> np.ndarray:
+    codes = np.ascontiguousarray(codes)
+    gains = np.ascontiguousarray(gains, dtype=np.float32)
+    act = np.ascontiguousarray(act, dtype=np.float32)
+    out = np.empty((act.shape[0], codes.shape[0]), dtype=np.float32)
+    d = plane_desc(codes, gains, K, group_size, **kw)
+    desk = lib.ref_desk_open(threads, gains.shape[1], K)
+    assert desk
+    try:
+        assert lib.ref_level_live(desk) == 1
+        lib.ref_desk_mat_mat_step(desk, ctypes.byref(d), step, p(act), act.shape[1], act.shape[0], p(out),
+                                  codes.shape[0])
+    finally:
+        lib.ref_desk_close(desk)
+    return out
 
 
 def oracle_mat_mat_real(real, real_type, act) -> np.ndarray:

@@ -228,6 +228,92 @@ def test_shipped_kinds_bitexact_vs_reference(ref_plain, N, K, group, bits, flip,
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+# ---- calibrated planes: the integer level path --------------------------------
+
+LEVEL_CASES = [
+    (70, 1536, 1536, 4, 0, 1), (70, 1536, 1536, 4, 0, 3), (40, 1536, 1536, 2, 0, 2),
+    (40, 256, 256, 8, 128, 5), (33, 6144, 6144, 2, 0, 1), (20, 512, 128, 4, 0, 2),
+    (24, 1536, 1536, 8, 0, 17), (20, 96, 32, 4, 0, 1),
+]
+
+
+def level_inputs(N, K, group, bits, lanes, seed=5):
+    r = np.random.default_rng(seed)
+    stride = (K * bits + 7) // 8
+    codes = r.integers(0, 256, size=(N, stride), dtype=np.uint8)
+    gains = np.abs(r.normal(0, 0.02, size=(N, (K + group - 1) // group))).astype(np.float32)
+    act = r.normal(size=(lanes, K)).astype(np.float32)
+    return codes, gains, act, np.float32(2.5 / 127)  # values past 2.5 clip to the ends
+
+
+def level_closed(codes, gains, act, K, group, bits, flip, step):
+    """sum over groups of gain * step * sum ((c ^ flip) - bias) L in float64,
+    L the numpy float32 quant_step level."""
+    N = codes.shape[0]
+    fields = np.unpackbits(codes, axis=1, bitorder="little")[:, :K * bits].reshape(N, K, bits)
+    c = (fields.astype(np.int64) << np.arange(bits)).sum(axis=2) ^ flip
+    L = np.clip(np.rint(act / step), -128, 127).astype(np.float64)
+    w = (c - (1 << (bits - 1))).astype(np.float64) * np.repeat(gains.astype(np.float64), group, axis=1)[:, :K]
+    return (L * float(step)) @ w.T
+
+
+@pytest.mark.parametrize("N,K,group,bits,flip,lanes", LEVEL_CASES)
+def test_level_closed_form(N, K, group, bits, flip, lanes):
+    codes, gains, act, step = level_inputs(N, K, group, bits, lanes)
+    kw = dict(bits=bits, code_bias=1 << (bits - 1), code_flip=flip)
+    got = ol.oracle_mat_mat_level(codes, gains, act, K, group, float(step), **kw)
+    want = level_closed(codes, gains, act, K, group, bits, flip, step)
+    scale = np.sqrt(np.mean(want ** 2))
+    assert np.max(np.abs(got - want)) <= 1e-6 * scale * math.sqrt(K / group)
+    # a restatement that took x instead of its level misses it
+    plain = ol.oracle_mat_mat(codes, gains, act, K, group, **kw)
+    assert np.max(np.abs(plain - want)) > 1e-4 * scale
+
+
+def test_level_one_group_is_one_rounding():
+    """One gain a row: y = fl(fl(gain * step) * fl(part)), part the exact integer sum."""
+    N, K, bits = 50, 1536, 4
+    codes, gains, act, step = level_inputs(N, K, K, bits, 2)
+    got = ol.oracle_mat_mat_level(codes, gains, act, K, K, float(step), bits=bits, code_bias=8)
+    fields = np.unpackbits(codes, axis=1, bitorder="little")[:, :K * bits].reshape(N, K, bits)
+    c = (fields.astype(np.int64) << np.arange(bits)).sum(axis=2) - 8
+    L = np.clip(np.rint(act / step), -128, 127).astype(np.int64)
+    part = L @ c.T
+    want = (gains[:, 0] * step)[None, :] * part.astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+
+
+def test_level_off_grid_takes_float_path():
+    """Groups of 32 are not level-ready, and a NaN puts a chunk off the grid:
+    both go to the float path on the quant_step values."""
+    codes, gains, act, step = level_inputs(20, 96, 32, 4, 2)
+    want = ol.oracle_mat_mat(codes, gains, ol.quant_step(act, float(step)), 96, 32)
+    got = ol.oracle_mat_mat_level(codes, gains, act, 96, 32, float(step))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    codes, gains, act, step = level_inputs(20, 1536, 1536, 4, 3)
+    act[1, 7] = np.nan
+    want = ol.oracle_mat_mat(codes, gains, ol.quant_step(act, float(step)), 1536, 1536)
+    got = ol.oracle_mat_mat_level(codes, gains, act, 1536, 1536, float(step))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.all(np.isnan(got[1]))
+
+
+@pytest.mark.parametrize("N,K,group,bits,flip,lanes", [c for c in LEVEL_CASES if c[2] % 64 == 0])
+def test_level_bitexact_vs_reference(N, K, group, bits, flip, lanes):
+    """The oracle against the reference's own VNNI build on quant_step'd lanes
+    (level-ready planes: off the grid, that build's float path is its AVX-512
+    one, not the SSE2 order the oracle restates)."""
+    lib = ol.ref("level")
+    if lib is None:
+        pytest.skip("level build of oracle/_ref absent, or this host has no AVX-512 VNNI")
+    codes, gains, act, step = level_inputs(N, K, group, bits, lanes)
+    kw = dict(bits=bits, code_bias=1 << (bits - 1), code_flip=flip)
+    got = ol.oracle_mat_mat_level(codes, gains, act, K, group, float(step), **kw)
+    want = ol.ref_mat_mat_step(lib, codes, gains, ol.quant_step(act, float(step)), K, group, float(step),
+                               threads=2, **kw)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def real_rows(N, K, real_type):
     """Rows of a real plane and their values in float64."""
     w = rng.normal(0, 0.05, size=(N, K)).astype(np.float32)
