@@ -435,6 +435,18 @@ int igl_plane_lift_dev(igl_desk *desk, const igl_plane *sheet, const float *act_
     desk_fail(st, IGL_FAIL_ARGUMENT);
     return IGL_FAIL_ARGUMENT;
   }
+  /* A calibrated code plane below the GEMM's lane floor: one launch on the
+   * activation grid, entry and leave grids fused, the reference's level path
+   * (exact integer sums) rather than the float path on quant_step values. */
+  if (sheet->enter_gain > 0.0f && sheet->form == IGL_PLANE_CODE && lane_count < IGL_GEMM_FLOOR &&
+      plane_supported(sheet) == IGL_OKAY && sheet->device &&
+      igl_gemv_level_fits(sheet->bit_count, sheet->col_count) && ((uintptr_t)act_dev & 15u) == 0 &&
+      (lane_count == 1 || (act_stride & 3) == 0)) {
+    igl_code_view view = igl_plane_view(sheet, sheet->device->codes, sheet->device->gains);
+    return hip_check(st, igl_launch_gemv_level(&view, sheet->enter_gain, sheet->leave_gain, act_dev,
+                                               act_stride, lane_count, out_dev, out_stride,
+                                               sheet->row_count, sheet->col_count, st->stream));
+  }
   if (sheet->enter_gain > 0.0f) {
     const int cols = sheet->col_count;
     if (grow_dev(st, &st->quant_dev, &st->quant_floats, (size_t)lane_count * (size_t)cols) != IGL_OKAY)

@@ -488,6 +488,79 @@ __device__ __forceinline__ void digit_store_lds(const float *xs, int K, uint4_t 
   __syncthreads();
 }
 
+// ---- activations as grid levels (a plane the export calibrated) -----------
+//
+// L = rint(x / step) clamped to [-128, 127], quant_step's level (the division
+// correctly rounded, as quant_step's).  Nibble forms store two dwords a group
+// of eight: `lo` holds L & 15 (unsigned), `hi` holds L >> 4 (a signed
+// nibble), so L = 16 hi + lo and a dot against codes splits into one signed
+// and one unsigned v_dot8; the byte form stores L itself, four a dword.  The
+// element order is the digit form's (DIGITS_PAIRS for 2-bit codes).  LDS:
+// uint4 lv[(m 2 + s) units + u], s = 0 / 1 the lo / hi dwords (bytes: elements
+// 0..15 / 16..31); corr[m units + u] = the bias correction of the unit
+// (4-bit: 8 sum lo; 2-bit: code_bias sum L; 8-bit: 0); nanu[m units + u] != 0
+// where the unit holds a NaN (its level is no level; the lane's outputs are NaN).
+template <int FORM>
+__device__ __forceinline__ void level_group_store(const float (&xin)[8], float step, int code_bias, int m,
+                                                  int gg, int units, uint4_t *lv, int *corr, int *nanu) {
+  const int u = gg >> 2, dw = gg & 3;
+  float x[8];
+  if constexpr (FORM == DIGITS_PAIRS) {
+    const bool odd = dw & 1;
+    float recv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) recv[i] = dpp_move<0xB1>(odd ? xin[2 * i] : xin[2 * i + 1]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = odd ? recv[i] : xin[2 * i];
+      x[4 + i] = odd ? xin[2 * i + 1] : recv[i];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = xin[e];
+  }
+  int L[8];
+  int bad = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float q = __builtin_rintf(x[e] / step);
+    bad |= q != q;
+    q = q < -128.0f ? -128.0f : q;
+    q = q > 127.0f ? 127.0f : q;
+    L[e] = q == q ? (int)q : 0;
+  }
+  uint32_t *base = reinterpret_cast<uint32_t *>(lv);
+  int c = 0;
+  if constexpr (FORM == DIGITS_BYTE) {
+    uint32_t b0 = 0, b1 = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      b0 |= ((uint32_t)L[e] & 0xFFu) << (8 * e);
+      b1 |= ((uint32_t)L[e + 4] & 0xFFu) << (8 * e);
+    }
+    *reinterpret_cast<uint2_t *>(base + ((m * 2 + (dw >> 1)) * units + u) * 4 + 2 * (dw & 1)) = uint2_t{b0, b1};
+  } else {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      lo |= ((uint32_t)L[e] & 15u) << (4 * e);
+      hi |= ((uint32_t)(L[e] >> 4) & 15u) << (4 * e);
+      c += FORM == DIGITS_PAIRS ? L[e] : (L[e] & 15);
+    }
+    base[((m * 2 + 0) * units + u) * 4 + dw] = lo;
+    base[((m * 2 + 1) * units + u) * 4 + dw] = hi;
+    c *= FORM == DIGITS_PAIRS ? code_bias : 8;
+  }
+  c += __builtin_amdgcn_update_dpp(0, c, 0xB1, 0xF, 0xF, true);
+  c += __builtin_amdgcn_update_dpp(0, c, 0x4E, 0xF, 0xF, true);
+  bad += __builtin_amdgcn_update_dpp(0, bad, 0xB1, 0xF, 0xF, true);
+  bad += __builtin_amdgcn_update_dpp(0, bad, 0x4E, 0xF, 0xF, true);
+  if (dw == 0) {
+    corr[m * units + u] = c;
+    nanu[m * units + u] = bad;
+  }
+}
+
 // Items of M lanes into LDS in form FORM; ends with a barrier every thread
 // reaches.  Item i of a thread: digit_item.
 template <int M, int GPT, int FORM>
@@ -500,6 +573,22 @@ __device__ __forceinline__ void digit_store_form(const DigitLoads<GPT> &h, int K
     const int g = digit_item(i, M * per_lane);
     const int m = M == 1 ? 0 : M == 2 ? (g >= per_lane ? 1 : 0) : g / per_lane;
     digit_group_store_form<FORM>(h.x[i], m, g - m * per_lane, units, dig, down, qsum);
+  }
+  __syncthreads();
+}
+
+// Items of M lanes into LDS as grid levels; ends with a barrier every thread
+// reaches.
+template <int M, int GPT, int FORM>
+__device__ __forceinline__ void level_store_form(const DigitLoads<GPT> &h, int K, float step, int code_bias,
+                                                 uint4_t *lv, int *corr, int *nanu) {
+  const int units = K >> 5;
+  const int per_lane = K >> 3;
+#pragma unroll
+  for (int i = 0; i < GPT; ++i) {
+    const int g = digit_item(i, M * per_lane);
+    const int m = M == 1 ? 0 : g / per_lane;
+    level_group_store<FORM>(h.x[i], step, code_bias, m, g - m * per_lane, units, lv, corr, nanu);
   }
   __syncthreads();
 }

@@ -798,6 +798,279 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_code_dot_kernel(GemvCodeArg
   }
 }
 
+// ---- calibrated planes: the product on the activation grid ------------------
+//
+// A plane whose export carries input_activation_scale (enter_gain = step > 0)
+// is multiplied on quant_step's grid: each activation is its level L, an
+// integer in [-128, 127] (level_group_store), so a row's sum
+//     part = sum ((c ^ flip) - bias) L
+// is an exact integer (the reference's level path, kern_row_code_level,
+// app_core.c:3272-3296) and costs, per row and unit, a third of the digit
+// form's dots: 4-bit codes 4 v_dot8_i32_i4 (c - 8 against L >> 4) and 4
+// v_dot8_u32_u4 (c against L & 15); 2-bit codes the same on the spread
+// nibbles; 8-bit codes 8 v_dot4_i32_i8 against L.  With one gain a row the
+// row's integer parts add exactly across lanes and waves and the row closes
+// as the reference closes it, gain * step * (float)part, one rounding each;
+// with several groups each unit closes on its own group's gain.  The output
+// then goes on the plane's leave grid (quant_step with leave_gain), fused.
+// One K-chunk (M K <= 16384); layout as gemv_code_dot_kernel.
+struct GemvLevelArgs {
+  const uint8_t *codes;
+  long long row_stride;
+  const float *gains;
+  int gain_stride;
+  int group_shift;
+  const float *act;
+  int act_stride;
+  float *out;
+  int out_stride;
+  int lanes;
+  int N, K;
+  int ks_log;
+  int subs_log;
+  uint32_t code_xor;      // 4-bit: undoes the flip; 8-bit: makes the bytes signed values; 2-bit: undoes the flip
+  int code_bias;
+  float step;             // enter_gain
+  float leave;            // leave_gain (<= 0: none)
+};
+
+__host__ __device__ constexpr size_t gemv_level_lds_bytes(int M, int units) {
+  return (size_t)M * units * (2 * 16 + 8);
+}
+
+__device__ __forceinline__ int sub_sum_to_last_int(int v, int subs_log) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, true);
+  if (subs_log >= 2) return v;
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, true);
+  if (subs_log == 1) return v;
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, true);
+  return v;
+}
+
+// quant_step of one value (app_core.c:1930-1940); a step that is not positive
+// leaves it.
+__device__ __forceinline__ float grid_value(float v, float step) {
+  if (!(step > 0.0f)) return v;
+  float level = __builtin_rintf(v / step);
+  if (level < -128.0f) level = -128.0f;
+  if (level > 127.0f) level = 127.0f;
+  return level * step;
+}
+
+template <int BITS, int M, int R, int UPL, int GPT>
+__global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs a) {
+  constexpr int FORM = CodeForm<BITS>::kDigits;
+  constexpr int kSub = BITS == 2 ? 2 : 1;
+  extern __shared__ uint4_t lds_lv[];
+  __shared__ int ired[4][R][M];
+  __shared__ float fred[4][R][M];
+  __shared__ int bred[4][M];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ks_log = __builtin_amdgcn_readfirstlane(a.ks_log);
+  const int subs_log = __builtin_amdgcn_readfirstlane(a.subs_log);
+  const bool one_group = a.group_shift == 31;
+  const int ks = wave & ((1 << ks_log) - 1);
+  const int sub = lane >> (6 - subs_log);
+  const int sub_lane = lane & ((64 >> subs_log) - 1);
+  const int tile = blockIdx.x * (4 >> ks_log) + (wave >> ks_log);
+  const int row0 = tile * (R << subs_log) + sub * R;
+  const int units = a.K >> 5;
+  const int slots = (a.K * BITS + 127) >> 7;
+  const int s_end = (slots * (ks + 1)) >> ks_log;
+  const int s_first = ((slots * ks) >> ks_log) + sub_lane;
+  uint4_t *lv = lds_lv;
+  int *corr = reinterpret_cast<int *>(lv + M * 2 * units);
+  int *nanu = corr + M * units;
+
+  DigitLoads<GPT> held;
+  {
+    const int last = a.lanes - 1;
+    const int per_lane = a.K >> 3;
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int g = digit_item(i, M * per_lane);
+      const int m = M == 1 ? 0 : g / per_lane;
+      const float *src = a.act + (size_t)min(m, last) * a.act_stride + 8 * (g - m * per_lane);
+      const float4_t p = *reinterpret_cast<const float4_t *>(src);
+      const float4_t q = *reinterpret_cast<const float4_t *>(src + 4);
+      held.x[i][0] = p.x; held.x[i][1] = p.y; held.x[i][2] = p.z; held.x[i][3] = p.w;
+      held.x[i][4] = q.x; held.x[i][5] = q.y; held.x[i][6] = q.z; held.x[i][7] = q.w;
+    }
+  }
+  // gains (one a row, or one a unit and row) before codes, all clamped
+  uint4_t w[UPL][R];
+  float s[UPL][R][kSub];
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const int sl = min(s_first + 64 * j, slots - 1);
+    const bool in = s_first + 64 * j < s_end;
+#pragma unroll
+    for (int h = 0; h < kSub; ++h) {
+      const int u_raw = BITS == 2 ? 2 * sl + h : BITS == 8 ? sl >> 1 : sl;
+      const int u = min(u_raw, units - 1);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, a.N - 1);
+        const float g = a.gains[(size_t)row * (size_t)a.gain_stride + ((unsigned)u >> a.group_shift)];
+        s[j][r][h] = in && u_raw < units && row0 + r < a.N ? g : 0.0f;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const int sl = min(s_first + 64 * j, slots - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min(row0 + r, a.N - 1);
+      w[j][r] = __builtin_nontemporal_load(reinterpret_cast<const uint4_t *>(a.codes + (size_t)row * (size_t)a.row_stride) + sl);
+    }
+  }
+  level_store_form<M, GPT, FORM>(held, a.K, a.step, a.code_bias, lv, corr, nanu);
+
+  // one gain a row: exact integer parts (a slot past the part or the row adds
+  // nothing: its gain is 0, so it is masked by that); several groups: floats
+  int ip[R][M];
+  float fp[R][M];
+  int bad[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) bad[m] = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      ip[r][m] = 0;
+      fp[r][m] = 0.0f;
+    }
+  const uint32_t cx = a.code_xor;
+#pragma unroll
+  for (int uj = 0; uj < UPL; ++uj) {
+    const int sl = min(s_first + 64 * uj, slots - 1);
+    const bool in = s_first + 64 * uj < s_end;
+#pragma unroll
+    for (int h = 0; h < kSub; ++h) {
+      const int u_raw = BITS == 2 ? 2 * sl + h : BITS == 8 ? sl >> 1 : sl;
+      const int u = min(u_raw, units - 1);
+      const bool live = in && u_raw < units;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const int cu = corr[m * units + u];
+        bad[m] |= live && nanu[m * units + u] != 0;
+        uint4_t lo, hi;
+        if constexpr (BITS == 8) {
+          lo = lv[(m * 2 + (sl & 1)) * units + u];
+        } else {
+          lo = lv[(m * 2 + 0) * units + u];
+          hi = lv[(m * 2 + 1) * units + u];
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          int part;
+          if constexpr (BITS == 8) {
+            const uint4_t c = w[uj][r] ^ cx;
+            part = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) part = __builtin_amdgcn_sdot4((int)c[q], (int)lo[q], part, false);
+          } else {
+            uint32_t n[4];
+            if constexpr (BITS == 4) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) n[q] = w[uj][r][q] ^ cx;
+            } else {
+              const uint32_t c0 = w[uj][r][2 * h] ^ cx, c1 = w[uj][r][2 * h + 1] ^ cx;
+              n[0] = c0 & 0x33333333u;
+              n[1] = (c0 >> 2) & 0x33333333u;
+              n[2] = c1 & 0x33333333u;
+              n[3] = (c1 >> 2) & 0x33333333u;
+            }
+            int th = 0;
+            uint32_t tl = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              // 4-bit: c - 8 (signed) against the high nibbles; 2-bit: c itself
+              const uint32_t sc = BITS == 4 ? n[q] ^ 0x88888888u : n[q];
+              th = __builtin_amdgcn_sdot8((int)sc, (int)hi[q], th, false);
+              tl = __builtin_amdgcn_udot8(n[q], lo[q], tl, false);
+            }
+            part = 16 * th + (int)tl - cu;
+          }
+          const float g = s[uj][r][h];
+          if (one_group) {
+            ip[r][m] += g != 0.0f ? part : 0;
+          } else {
+            fp[r][m] += g * a.step * (float)part;
+          }
+        }
+      }
+    }
+  }
+
+  // sums over the sub-wave, then over the waves that share the tile
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      if (one_group)
+        ip[r][m] = sub_sum_to_last_int(ip[r][m], subs_log);
+      else
+        fp[r][m] = sub_sum_to_last(fp[r][m], subs_log);
+    }
+#pragma unroll
+  for (int m = 0; m < M; ++m) bad[m] = sub_sum_to_last_int(bad[m], subs_log);
+  const bool owner = sub_lane == (64 >> subs_log) - 1;
+  if (ks_log > 0) {
+    // one tile a wave group (subs_log == 0): the waves' sums meet in LDS
+    if (owner) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        bred[wave][m] = bad[m];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          ired[wave][r][m] = ip[r][m];
+          fred[wave][r][m] = fp[r][m];
+        }
+      }
+    }
+    __syncthreads();
+    if (ks != 0) return;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      int b = 0;
+      for (int k = 0; k < (1 << ks_log); ++k) b += bred[wave + k][m];
+      bad[m] = b;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        int it = 0;
+        float ft = 0.0f;
+        for (int k = 0; k < (1 << ks_log); ++k) {
+          it += ired[wave + k][r][m];
+          ft += fred[wave + k][r][m];
+        }
+        ip[r][m] = it;
+        fp[r][m] = ft;
+      }
+    }
+  }
+  if (!owner) return;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = row0 + r;
+    if (row >= a.N) continue;
+    const float gain_step = one_group ? a.gains[(size_t)row * (size_t)a.gain_stride] * a.step : 0.0f;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      if (m >= a.lanes) continue;
+      float y = one_group ? gain_step * (float)ip[r][m] : fp[r][m];
+      if (bad[m]) y = __builtin_nanf("");
+      a.out[(size_t)m * a.out_stride + row] = grid_value(y, a.leave);
+    }
+  }
+}
+
 // ---- real planes: F32, F16 or BF16 rows -------------------------------------
 //
 // kern_mat_vec_band's PLANE_REAL arm (app_core.c:4239-4248): every row dotted
@@ -1902,6 +2175,116 @@ extern "C" hipError_t igl_launch_gemv_codes(const igl_code_view *v, const float 
                          chunks, l, N, out + (size_t)done * (size_t)out_stride, out_stride);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
+  }
+  return hipSuccess;
+}
+
+// ---- calibrated planes: gemv_level_kernel ----------------------------------
+
+namespace igl {
+
+template <int BITS, int M, int UPL, int GPT>
+static hipError_t gemv_level_launch4(const GemvLevelArgs &a, dim3 grid, size_t lds, hipStream_t stream) {
+  hipLaunchKernelGGL((gemv_level_kernel<BITS, M, 4, UPL, GPT>), grid, dim3(kGemvThreads), lds, stream, a);
+  return hipGetLastError();
+}
+
+template <int BITS, int M>
+static hipError_t gemv_level_launch_m(const GemvLevelArgs &a, int upl, int gpt, dim3 grid, size_t lds,
+                                      hipStream_t stream) {
+  // more than 256 slots a row: one lane of 4-bit codes, one or two of 8-bit codes
+  constexpr bool kTwoSlots = (M == 1 && BITS >= 4) || (M == 2 && BITS == 8);
+  if (upl == 1) {
+    switch (gpt) {
+      case 1: return gemv_level_launch4<BITS, M, 1, 1>(a, grid, lds, stream);
+      case 2: return gemv_level_launch4<BITS, M, 1, 2>(a, grid, lds, stream);
+      case 4: return gemv_level_launch4<BITS, M, 1, 4>(a, grid, lds, stream);
+      default: return gemv_level_launch4<BITS, M, 1, 8>(a, grid, lds, stream);
+    }
+  }
+  if constexpr (kTwoSlots) {
+    switch (gpt) {
+      case 1: return gemv_level_launch4<BITS, M, 2, 1>(a, grid, lds, stream);
+      case 2: return gemv_level_launch4<BITS, M, 2, 2>(a, grid, lds, stream);
+      case 4: return gemv_level_launch4<BITS, M, 2, 4>(a, grid, lds, stream);
+      default: return gemv_level_launch4<BITS, M, 2, 8>(a, grid, lds, stream);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int BITS>
+static hipError_t gemv_level_launch_bits(const GemvLevelArgs &a, int M, int upl, int gpt, dim3 grid,
+                                         size_t lds, hipStream_t stream) {
+  switch (M) {
+    case 1: return gemv_level_launch_m<BITS, 1>(a, upl, gpt, grid, lds, stream);
+    case 2: return gemv_level_launch_m<BITS, 2>(a, upl, gpt, grid, lds, stream);
+    default: return gemv_level_launch_m<BITS, 4>(a, upl, gpt, grid, lds, stream);
+  }
+}
+
+}  // namespace igl
+
+// Whether igl_launch_gemv_level takes this plane's shape.
+extern "C" int igl_gemv_level_fits(int bit_count, int K) {
+  return (bit_count == 2 || bit_count == 4 || bit_count == 8) && K >= 32 && K % 32 == 0 && K <= 16384 &&
+         (K * bit_count + 127) / 128 <= 512;
+}
+
+// y = quant_step(W quant_step(x, step), leave) for any number of lanes of a
+// 2, 4 or 8-bit code plane, on the activation grid (gemv_level_kernel).
+// Activations 16-byte aligned with act_stride % 4 == 0; every condition is
+// checked before anything is launched.
+extern "C" hipError_t igl_launch_gemv_level(const igl_code_view *v, float step, float leave,
+                                            const float *act, int act_stride, int lanes, float *out,
+                                            int out_stride, int N, int K, hipStream_t stream) {
+  const int bits = v->bit_count;
+  if (!(step > 0.0f) || !igl_gemv_level_fits(bits, K) || (((uintptr_t)act) & 15u) ||
+      (lanes > 1 && (act_stride & 3)) || lanes < 1 || N < 1)
+    return hipErrorInvalidValue;
+  GemvLevelArgs a;
+  a.codes = v->codes;
+  a.row_stride = v->row_stride;
+  a.gains = v->gains;
+  a.gain_stride = v->gain_stride;
+  a.group_shift = v->group_shift;
+  a.N = N;
+  a.K = K;
+  a.code_bias = v->code_bias;
+  a.step = step;
+  a.leave = leave;
+  const uint32_t field = bits == 8 ? (uint32_t)((v->code_flip ^ v->code_bias) & 255)
+                                   : (uint32_t)(v->code_flip & ((1 << bits) - 1));
+  a.code_xor = field * (bits == 2 ? 0x55555555u : bits == 4 ? 0x11111111u : 0x01010101u);
+  // lanes a launch: M K <= 16384 (eight staged groups a thread), at most four
+  const int most = 16384 / K >= 4 ? 4 : 16384 / K >= 2 ? 2 : 1;
+  for (int done = 0; done < lanes; done += most) {
+    const int l = lanes - done < most ? lanes - done : most;
+    const int M = l <= 2 ? l : 4;
+    const int slots = (K * bits + 127) / 128;
+    const int upl = slots > 4 * kWave ? 2 : 1;
+    const int subs_log = upl == 1 && slots <= 16 ? 2 : upl == 1 && slots <= 32 ? 1 : 0;
+    const int tiles = (N + (4 << subs_log) - 1) / (4 << subs_log);
+    int ksplit = 1;
+    while (subs_log == 0 && ksplit < 4 &&
+           (slots > ksplit * kWave * upl || (tiles * ksplit < 2048 && slots / (ksplit * 2) >= 32 * upl)))
+      ksplit *= 2;
+    const int items = (M * (K >> 3) + kGemvThreads - 1) / kGemvThreads;
+    const int gpt = items <= 1 ? 1 : items <= 2 ? 2 : items <= 4 ? 4 : 8;
+    a.act = act + (size_t)done * (size_t)act_stride;
+    a.act_stride = act_stride;
+    a.lanes = l;
+    a.out = out + (size_t)done * (size_t)out_stride;
+    a.out_stride = out_stride;
+    a.ks_log = ksplit == 1 ? 0 : ksplit == 2 ? 1 : 2;
+    a.subs_log = subs_log;
+    const int per_block = 4 / ksplit;
+    const dim3 grid((tiles + per_block - 1) / per_block);
+    const size_t lds = gemv_level_lds_bytes(M, K / 32);
+    hipError_t e = bits == 2   ? gemv_level_launch_bits<2>(a, M, upl, gpt, grid, lds, stream)
+                   : bits == 4 ? gemv_level_launch_bits<4>(a, M, upl, gpt, grid, lds, stream)
+                               : gemv_level_launch_bits<8>(a, M, upl, gpt, grid, lds, stream);
+    if (e != hipSuccess) return e;
   }
   return hipSuccess;
 }

@@ -56,6 +56,10 @@ hipError_t igl_launch_gemv_codes(const igl_code_view *v, const float *act, int a
                                  int lanes, float *out, int out_stride, int N, int K,
                                  float *part, hipStream_t stream);
 
+int igl_gemv_level_fits(int bit_count, int K);
+hipError_t igl_launch_gemv_level(const igl_code_view *v, float step, float leave, const float *act,
+                                 int act_stride, int lanes, float *out, int out_stride, int N, int K,
+                                 hipStream_t stream);
 size_t igl_gemv_real_part_floats(int lanes, int N, int K);
 hipError_t igl_launch_gemv_real(const void *rows, int real_type, const float *act, int act_stride,
                                 int lanes, float *out, int out_stride, int N, int K, float *part,

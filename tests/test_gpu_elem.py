@@ -80,10 +80,11 @@ def test_quant_step_dev(backend, step):
 @pytest.mark.parametrize("lanes", [1, 3, 64])
 def test_plane_lift_dev(backend, lanes):
     """plane_lift_many on device (app_core.c:7814-7843): the lanes on the
-    enter_gain grid, the product, the outputs on the leave_gain grid.  The
-    composition is checked to the bit against the same steps taken one by one
-    (the closed-form grid, then igl_mat_mat_dev), and the product against the
-    oracle on the gridded activations."""
+    enter_gain grid, the product, the outputs on the leave_gain grid.  Below 64
+    lanes the product is the fused one on the activation grid (exact integer
+    sums), from 64 the steps one by one (grid, MFMA GEMM, grid).  Checked: the
+    product against the oracle on the gridded activations, and the leave grid
+    to the bit against the closed form applied to that product."""
     from igllm_amd.backend import make_plane, synth_projection
     from test_oracle import quant_step_closed
 
@@ -92,23 +93,95 @@ def test_plane_lift_dev(backend, lanes):
     act = (act * 3).astype(np.float32)
     cp = backend.attach(make_plane(codes, gains, K))
     cp.plane.enter_gain = 0.05
-    cp.plane.leave_gain = 0.01
     entered = np.stack([quant_step_closed(a, 0.05) for a in act])
     dev_act = backend.upload(act)
-    dev_entered = backend.upload(entered)
     out = backend.alloc(lanes * N * 4)
-    plain = backend.alloc(lanes * N * 4)
+    cp.plane.leave_gain = 0.0
     backend.plane_lift_dev(cp, dev_act, K, lanes, out, N)
-    backend.mat_mat_dev(cp, dev_entered, K, lanes, plain, N)
+    backend.sync()
+    product = out.get(np.float32, lanes * N).reshape(lanes, N)
+    cp.plane.leave_gain = 0.01
+    backend.plane_lift_dev(cp, dev_act, K, lanes, out, N)
     backend.sync()
     got = out.get(np.float32, lanes * N).reshape(lanes, N)
-    product = plain.get(np.float32, lanes * N).reshape(lanes, N)
     want = np.stack([quant_step_closed(y, 0.01) for y in product])
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     ref = ol.oracle_mat_mat(codes, gains, entered, K, threads=8)
     floor = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
-    tol = 2e-3 if lanes >= 64 else 1e-3  # 64 lanes take the binary16-operand MFMA GEMM
+    tol = 2e-3 if lanes >= 64 else 1e-5  # 64 lanes take the binary16-operand MFMA GEMM
     assert np.max(np.abs(product - ref) / np.maximum(np.abs(ref), floor)) <= tol
-    for b in (dev_act, dev_entered, out, plain):
+    for b in (dev_act, out):
         b.free()
+    backend.detach(cp)
+
+
+LEVEL_KINDS = [
+    (2048, 1536, 4, 0, 1), (2048, 1536, 4, 0, 3), (6144, 1536, 2, 0, 1), (1536, 6144, 2, 0, 2),
+    (256, 1536, 8, 128, 1), (1536, 256, 8, 128, 4), (1536, 2048, 4, 0, 5), (300, 16384, 4, 0, 1),
+    (100, 8192, 8, 128, 2), (70, 96, 2, 1, 1),
+]
+
+
+@pytest.mark.parametrize("N,K,bits,flip,lanes", LEVEL_KINDS)
+def test_plane_lift_level_bitexact(backend, N, K, bits, flip, lanes):
+    """Calibrated per-channel planes (the export's kinds, one gain a row): the
+    fused product on the activation grid equals the oracle's level path (the
+    reference's VNNI-tier kern_row_code_level, pinned to the bit against that
+    build) to the bit, and so does the leave grid after it."""
+    from igllm_amd.backend import make_plane
+    from test_oracle import quant_step_closed
+
+    print("case level N=%d K=%d bits=%d flip=%d lanes=%d" % (N, K, bits, flip, lanes), flush=True)
+    r = np.random.default_rng(N + K + bits)
+    stride = ((K * bits + 7) // 8 + 15) // 16 * 16
+    codes = r.integers(0, 256, size=(N, stride), dtype=np.uint8)
+    gains = np.abs(r.normal(0, 0.02, size=(N, 1))).astype(np.float32)
+    act = r.normal(size=(lanes, K)).astype(np.float32)
+    step, leave = float(np.float32(2.5 / 127)), float(np.float32(0.02))
+    cp = backend.attach(make_plane(codes, gains, K, group_size=K, bits=bits, code_flip=flip))
+    cp.plane.enter_gain = step
+    kw = dict(bits=bits, code_bias=1 << (bits - 1), code_flip=flip)
+    want = ol.oracle_mat_mat_level(codes, gains, act, K, K, step, **kw)
+    dev_act = backend.upload(act)
+    out = backend.alloc(lanes * N * 4)
+    backend.plane_lift_dev(cp, dev_act, K, lanes, out, N)
+    backend.sync()
+    got = out.get(np.float32, lanes * N).reshape(lanes, N)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    cp.plane.leave_gain = leave
+    backend.plane_lift_dev(cp, dev_act, K, lanes, out, N)
+    backend.sync()
+    got = out.get(np.float32, lanes * N).reshape(lanes, N)
+    assert np.array_equal(got.view(np.uint32), np.stack([quant_step_closed(y, leave) for y in want]).view(np.uint32))
+    dev_act.free()
+    out.free()
+    backend.detach(cp)
+
+
+def test_plane_lift_level_nan_lane(backend):
+    """A NaN activation puts its lane's outputs at NaN and leaves the others on
+    the grid.  (The reference sends the whole 16-lane chunk to the float path
+    when one lane is off the grid, so its other lanes would carry float-path
+    roundings; here each lane keeps the level path.)"""
+    from igllm_amd.backend import make_plane
+
+    N, K = 512, 1536
+    r = np.random.default_rng(9)
+    codes = r.integers(0, 256, size=(N, K // 2), dtype=np.uint8)
+    gains = np.abs(r.normal(0, 0.02, size=(N, 1))).astype(np.float32)
+    act = r.normal(size=(2, K)).astype(np.float32)
+    act[1, 100] = np.nan
+    step = float(np.float32(2.5 / 127))
+    cp = backend.attach(make_plane(codes, gains, K, group_size=K))
+    cp.plane.enter_gain = step
+    dev_act = backend.upload(act)
+    out = backend.alloc(2 * N * 4)
+    backend.plane_lift_dev(cp, dev_act, K, 2, out, N)
+    backend.sync()
+    got = out.get(np.float32, 2 * N).reshape(2, N)
+    assert np.all(np.isnan(got[1])) and np.all(np.isfinite(got[0]))
+    want = ol.oracle_mat_mat_level(codes, gains, act[:1], K, K, step)
+    assert np.array_equal(got[0].view(np.uint32), want[0].view(np.uint32))
+    dev_act.free()
+    out.free()
     backend.detach(cp)
