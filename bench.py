@@ -249,6 +249,9 @@ KIND_CASES = {
     "i8_ple_proj_1536x256": (1536, 256, 8, 128),
     "u4_q_proj_2048x1536": (2048, 1536, 4, 0),
     "bf16_ple_model_8960x1536": (8960, 1536, "bf16"),
+    # calibrated (enter_gain): the product on the activation grid, igl_plane_lift_dev
+    "u4_calibrated_8192x2048": (8192, 2048, 4, 0, 2.5 / 127),
+    "u2_calibrated_mlp_gate_6144x1536": (6144, 1536, 2, 0, 2.5 / 127),
 }
 
 
@@ -269,6 +272,7 @@ class KindRotation:
             rows = (w.view(np.uint32) >> 16).astype(np.uint16)
             payload, gains = rows, None
             maker = lambda: make_real_plane(rows, native.IGL_STORE_BF16)  # noqa: E731
+            self.lift = False
             self.algo = N * K * 2 + (K + N) * 4
         else:
             bits, flip = case[2], case[3]
@@ -276,7 +280,13 @@ class KindRotation:
             codes = rng.integers(0, 256, size=(N, stride), dtype=np.uint8)
             gains = np.abs(rng.normal(0, 0.02, size=(N, 1))).astype(np.float32)
             payload = codes
-            maker = lambda: make_plane(codes, gains, K, group_size=K, bits=bits, code_flip=flip)  # noqa: E731
+            step = case[4] if len(case) > 4 else 0.0
+
+            def maker():
+                cp = make_plane(codes, gains, K, group_size=K, bits=bits, code_flip=flip)
+                cp.plane.enter_gain = step
+                return cp
+            self.lift = step > 0
             self.algo = N * stride + N * 4 + (K + N) * 4
         pstride = (payload.nbytes + 255) // 256 * 256
         self.copies = max(2, -(-(320 << 20) // pstride))
@@ -303,12 +313,13 @@ def kinds_leg(be, reps=100):
         N, K = rot.N, rot.K
         x = be.upload(np.random.default_rng(1).normal(size=(1, K)).astype(np.float32))
         y = be.alloc(N * 4)
+        run = be.plane_lift_dev if rot.lift else be.gemv_dev
         for i in range(10):
-            be.gemv_dev(rot.planes[i % rot.copies], x, K, 1, y, N)
+            run(rot.planes[i % rot.copies], x, K, 1, y, N)
         be.sync()
         be.mark()
         for i in range(reps):
-            be.gemv_dev(rot.planes[i % rot.copies], x, K, 1, y, N)
+            run(rot.planes[i % rot.copies], x, K, 1, y, N)
         be.mark()
         us = be.marks_ms() * 1e3 / reps
         gbps = rot.algo / (us * 1e-6) / 1e9

@@ -50,6 +50,16 @@ struct igl_desk_state {
   size_t work_floats;
   float *quant_dev;   /* plane_lift: the activations on the plane's entry grid */
   size_t quant_floats;
+  /* plane_lift's prefill on the grid: widened codes, unit gains, level sums,
+   * the two planes' products of an 8-bit plane */
+  float *wide_dev;
+  size_t wide_floats;
+  float *ones_dev;
+  size_t ones_floats;
+  float *lsum_dev;
+  size_t lsum_floats;
+  float *prod_dev;
+  size_t prod_floats;
   /* staging for the elementwise host entries */
   float *elem_dev;
   size_t elem_floats;
@@ -425,6 +435,66 @@ int igl_quant_step_dev(igl_desk *desk, const float *src_dev, int src_stride, flo
  * with enter_gain > 0 the lanes are put on that grid (in desk scratch) before
  * the product, and with leave_gain > 0 the outputs after it.  The product is
  * igl_mat_mat_dev's.  The table's mat_mat does neither: its caller does. */
+/* The prefill of a calibrated plane with one gain a row on the activation
+ * grid: the lanes as levels, the codes as 4-bit planes of unit gain, the MFMA
+ * GEMM on those integer-valued operands (exact: every partial sum an integer
+ * below 2^24), then gain * step * part and the leave grid, as the reference's
+ * level path closes a row (kern_row_code_level, app_core.c:3272-3296). */
+static int lift_levels_gemm(igl_desk_state *st, const igl_plane *sheet, const float *act_dev,
+                            int act_stride, int lanes, float *out_dev, int out_stride) {
+  const int N = sheet->row_count, K = sheet->col_count, bits = sheet->bit_count;
+  const int two = bits == 8;
+  const int widen = !(bits == 4 && sheet->code_flip == 0);
+  const size_t plane_bytes = (size_t)N * (size_t)(K / 2);
+  const uint8_t *hi_plane = (const uint8_t *)sheet->device->codes;
+  const uint8_t *lo_plane = NULL;
+  long long row_stride = (long long)sheet->row_stride;
+  size_t work = igl_gemm_work_bytes(lanes, N, K);
+  float *a_out = two ? NULL : out_dev;
+  int a_stride = two ? N : out_stride;
+  int code;
+  if (grow_dev(st, &st->quant_dev, &st->quant_floats, (size_t)lanes * (size_t)K) != IGL_OKAY ||
+      (widen && grow_dev(st, &st->wide_dev, &st->wide_floats, (two ? 2 : 1) * plane_bytes / 4) != IGL_OKAY) ||
+      (two && grow_dev(st, &st->lsum_dev, &st->lsum_floats, (size_t)lanes) != IGL_OKAY) ||
+      (two && grow_dev(st, &st->prod_dev, &st->prod_floats, 2 * (size_t)lanes * (size_t)N) != IGL_OKAY) ||
+      (work && grow_dev(st, &st->gemm_dev, &st->gemm_floats, (work + 3) / 4) != IGL_OKAY))
+    return IGL_FAIL_MEMORY;
+  if (st->ones_floats < (size_t)N) {
+    if (grow_dev(st, &st->ones_dev, &st->ones_floats, (size_t)N) != IGL_OKAY) return IGL_FAIL_MEMORY;
+    if ((code = hip_check(st, igl_launch_fill(st->ones_dev, st->ones_floats, 1.0f, st->stream))) != IGL_OKAY)
+      return code;
+  }
+  if (two) a_out = st->prod_dev;
+  if ((code = hip_check(st, igl_launch_quant_level(act_dev, act_stride, st->quant_dev, K, K, lanes,
+                                                   sheet->enter_gain, two ? st->lsum_dev : NULL,
+                                                   st->stream))) != IGL_OKAY)
+    return code;
+  if (widen) {
+    hi_plane = (const uint8_t *)st->wide_dev;
+    lo_plane = two ? hi_plane + plane_bytes : NULL;
+    row_stride = K / 2;
+    if ((code = hip_check(st, igl_launch_code_widen((const uint8_t *)sheet->device->codes,
+                                                    (long long)sheet->row_stride, N, K, bits,
+                                                    sheet->code_flip, sheet->code_bias,
+                                                    (uint8_t *)hi_plane, (uint8_t *)lo_plane,
+                                                    st->stream))) != IGL_OKAY)
+      return code;
+  }
+  if ((code = hip_check(st, igl_launch_gemm_q4(st->quant_dev, 0, K, hi_plane, row_stride, st->ones_dev, 1, 31,
+                                               8, a_out, 0, a_stride, lanes, N, K, st->gemm_dev,
+                                               st->stream))) != IGL_OKAY)
+    return code;
+  if (two &&
+      (code = hip_check(st, igl_launch_gemm_q4(st->quant_dev, 0, K, lo_plane, row_stride, st->ones_dev, 1, 31,
+                                               8, st->prod_dev + (size_t)lanes * (size_t)N, 0, N, lanes,
+                                               N, K, st->gemm_dev, st->stream))) != IGL_OKAY)
+    return code;
+  return hip_check(st, igl_launch_grid_close(a_out, two ? st->prod_dev + (size_t)lanes * (size_t)N : NULL,
+                                             two ? st->lsum_dev : NULL, a_stride,
+                                             sheet->device->gains, sheet->enter_gain, sheet->leave_gain, N,
+                                             lanes, out_dev, out_stride, st->stream));
+}
+
 int igl_plane_lift_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev,
                        int act_stride, int lane_count, float *out_dev, int out_stride) {
   igl_desk_state *st = desk ? desk->state : NULL;
@@ -447,6 +517,10 @@ int igl_plane_lift_dev(igl_desk *desk, const igl_plane *sheet, const float *act_
                                                act_stride, lane_count, out_dev, out_stride,
                                                sheet->row_count, sheet->col_count, st->stream));
   }
+  if (sheet->enter_gain > 0.0f && sheet->form == IGL_PLANE_CODE && lane_count >= IGL_GEMM_FLOOR &&
+      plane_supported(sheet) == IGL_OKAY && sheet->device && sheet->group_count == 1 &&
+      ((uintptr_t)act_dev & 15u) == 0 && (act_stride & 3) == 0)
+    return lift_levels_gemm(st, sheet, act_dev, act_stride, lane_count, out_dev, out_stride);
   if (sheet->enter_gain > 0.0f) {
     const int cols = sheet->col_count;
     if (grow_dev(st, &st->quant_dev, &st->quant_floats, (size_t)lane_count * (size_t)cols) != IGL_OKAY)
@@ -739,6 +813,10 @@ void igl_back_close(igl_desk *desk) {
   if (st->part_dev) (void)hipFree(st->part_dev);
   if (st->work_dev) (void)hipFree(st->work_dev);
   if (st->quant_dev) (void)hipFree(st->quant_dev);
+  if (st->wide_dev) (void)hipFree(st->wide_dev);
+  if (st->ones_dev) (void)hipFree(st->ones_dev);
+  if (st->lsum_dev) (void)hipFree(st->lsum_dev);
+  if (st->prod_dev) (void)hipFree(st->prod_dev);
   if (st->elem_dev) (void)hipFree(st->elem_dev);
   if (st->gemm_dev) (void)hipFree(st->gemm_dev);
   if (st->mark[0]) (void)hipEventDestroy(st->mark[0]);

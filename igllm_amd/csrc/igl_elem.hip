@@ -112,9 +112,124 @@ __global__ void quant_step_kernel(const float *src, int src_stride, float *dst, 
   }
 }
 
+// ---- the prefill of a calibrated plane on the activation grid -------------
+//
+// With one gain a row, y = gain * step * sum ((c ^ flip) - bias) L is taken as
+// an MFMA product of integer-valued operands: the lanes as their levels L
+// (quant_level_kernel), the codes as 4-bit planes with unit gains (widened by
+// code_widen_kernel), so every product and partial sum is an integer below
+// 2^24 that binary16 operands and fp32 accumulation carry exactly; then
+// grid_close_kernel closes each row as the reference's level path does.
+
+// L = rint(x / step) clamped to [-128, 127], as a float; also sum L per lane
+// into `lsum` (which must start at zero: integers below 2^24, exact in fp32).
+__global__ void quant_level_kernel(const float *src, int src_stride, float *dst, int dst_stride, int n,
+                                   float step, float *lsum) {
+  const int lane = blockIdx.y;
+  const float *in = src + (size_t)lane * src_stride;
+  float *out = dst + (size_t)lane * dst_stride;
+  float total = 0.0f;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    float level = __builtin_rintf(in[i] / step);
+    if (level < -128.0f) level = -128.0f;
+    if (level > 127.0f) level = 127.0f;
+    out[i] = level;
+    total += level;
+  }
+  if (lsum) {
+    total = wave_sum_to_last(total);
+    if ((threadIdx.x & 63) == 63) atomicAdd(lsum + lane, total);
+  }
+}
+
+// Codes of any width as 4-bit planes of value + 8, two a byte, low nibble
+// first, rows of K / 2 bytes:
+//   2-bit and 4-bit codes: one plane, (c ^ flip) - bias + 8;
+//   8-bit codes (bias 128): two planes, hi = c' >> 4 and lo = c' & 15 with
+//   c' = c ^ flip, so c' - 128 = 16 (hi - 8) + (lo - 8) + 8.
+// One thread writes one byte (two codes) of each plane.
+__global__ void code_widen_kernel(const uint8_t *codes, long long row_stride, int N, int K, int bits,
+                                  int flip, int bias, uint8_t *hi_plane, uint8_t *lo_plane) {
+  const int half = K >> 1;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)N * half) return;
+  const int n = (int)(i / half);
+  const int k = 2 * (int)(i - (size_t)n * half);
+  const uint8_t *row = codes + (size_t)n * row_stride;
+  int c[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int at = (k + j) * bits;
+    c[j] = ((row[at >> 3] >> (at & 7)) & ((1 << bits) - 1)) ^ flip;
+  }
+  if (bits == 8) {
+    hi_plane[i] = (uint8_t)((c[0] >> 4) | ((c[1] >> 4) << 4));
+    lo_plane[i] = (uint8_t)((c[0] & 15) | ((c[1] & 15) << 4));
+  } else {
+    hi_plane[i] = (uint8_t)((c[0] - bias + 8) | ((c[1] - bias + 8) << 4));
+  }
+}
+
+// out = quant_step(gain[n] * step * part, leave): part = a, the widened
+// plane's product, or for an 8-bit plane part = 16 a + b + 8 lsum[m], a and b
+// the hi and lo planes' products.  In place on `a` allowed.
+__global__ void grid_close_kernel(const float *a, const float *b, const float *lsum, int in_stride,
+                                  const float *gains, float step, float leave, int N, float *out,
+                                  int out_stride) {
+  const int m = blockIdx.y;
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  float part = a[(size_t)m * in_stride + n];
+  if (b) part = (16.0f * part + b[(size_t)m * in_stride + n]) + 8.0f * lsum[m];
+  float y = gains[n] * step * part;
+  if (leave > 0.0f) {
+    float level = __builtin_rintf(y / leave);
+    if (level < -128.0f) level = -128.0f;
+    if (level > 127.0f) level = 127.0f;
+    y = level * leave;
+  }
+  out[(size_t)m * out_stride + n] = y;
+}
+
+__global__ void fill_kernel(float *dst, size_t n, float value) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = value;
+}
+
 }  // namespace igl
 
 using namespace igl;
+
+extern "C" hipError_t igl_launch_quant_level(const float *src, int src_stride, float *dst, int dst_stride,
+                                             int n, int lanes, float step, float *lsum, hipStream_t stream) {
+  const int blocks = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+  if (lsum) hipLaunchKernelGGL(fill_kernel, dim3((lanes + 255) / 256), dim3(256), 0, stream, lsum, (size_t)lanes, 0.0f);
+  hipLaunchKernelGGL(quant_level_kernel, dim3(blocks, lanes), dim3(256), 0, stream, src, src_stride, dst,
+                     dst_stride, n, step, lsum);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_code_widen(const uint8_t *codes, long long row_stride, int N, int K, int bits,
+                                            int flip, int bias, uint8_t *hi_plane, uint8_t *lo_plane,
+                                            hipStream_t stream) {
+  const size_t total = (size_t)N * (size_t)(K / 2);
+  hipLaunchKernelGGL(code_widen_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, codes,
+                     row_stride, N, K, bits, flip, bias, hi_plane, lo_plane);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_grid_close(const float *a, const float *b, const float *lsum, int in_stride,
+                                            const float *gains, float step, float leave, int N, int lanes,
+                                            float *out, int out_stride, hipStream_t stream) {
+  hipLaunchKernelGGL(grid_close_kernel, dim3((N + 255) / 256, lanes), dim3(256), 0, stream, a, b, lsum, in_stride,
+                     gains, step, leave, N, out, out_stride);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_fill(float *dst, size_t n, float value, hipStream_t stream) {
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, dst, n, value);
+  return hipGetLastError();
+}
 
 extern "C" hipError_t igl_launch_quant_step(const float *src, int src_stride, float *dst,
                                             int dst_stride, int n, int lanes, float step,

@@ -157,6 +157,16 @@ hipError_t igl_launch_pick(const float *v, int n, size_t stride, int lanes, void
 
 hipError_t igl_launch_quant_step(const float *src, int src_stride, float *dst, int dst_stride,
                                  int n, int lanes, float step, hipStream_t stream);
+/* the prefill of a calibrated plane (igl_elem.hip) */
+hipError_t igl_launch_quant_level(const float *src, int src_stride, float *dst, int dst_stride,
+                                  int n, int lanes, float step, float *lsum, hipStream_t stream);
+hipError_t igl_launch_code_widen(const uint8_t *codes, long long row_stride, int N, int K, int bits,
+                                 int flip, int bias, uint8_t *hi_plane, uint8_t *lo_plane,
+                                 hipStream_t stream);
+hipError_t igl_launch_grid_close(const float *a, const float *b, const float *lsum, int in_stride,
+                                 const float *gains, float step, float leave, int N, int lanes,
+                                 float *out, int out_stride, hipStream_t stream);
+hipError_t igl_launch_fill(float *dst, size_t n, float value, hipStream_t stream);
 hipError_t igl_launch_norm_rms(const float *in, const float *gain, int n, int rows, int stride,
                                float eps, float *out, hipStream_t stream);
 hipError_t igl_launch_soft_max(float *v, int n, int rows, int stride, hipStream_t stream);
