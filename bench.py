@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decode leg")
-    ap.add_argument("--kernel", choices=["gemv", "gemv8", "gemm", "attend", "copy", "head2", "real"],
+    ap.add_argument("--kernel", choices=["gemv", "gemv8", "gemm", "attend", "copy", "head2", "real", "calib"],
                     help="run one kernel's workload alone in a loop (for rocprofv3) and exit")
     return ap.parse_args()
 
@@ -58,8 +58,10 @@ def parse():
 def kernel_loop(be, name, reps):
     """One kernel's workload alone, for counter runs: the decode GEMV (M=1,
     8192x2048, rotated copies), the M=8 GEMV, the M=2048 prefill GEMM, the
-    L=16384 attention, or a 256 MiB device copy that calibrates FETCH_SIZE and
-    WRITE_SIZE against a known byte count."""
+    L=16384 attention, a 256 MiB device copy that calibrates FETCH_SIZE and
+    WRITE_SIZE against a known byte count, the 2-bit 262144x1536 head and the
+    bf16 8960x1536 real plane at M=1 (rotated copies), or the calibrated
+    prefill (M=2048, 8192x2048 4-bit, one gain a row)."""
     import ctypes
     from igllm_amd.backend import synth_projection
 
@@ -92,6 +94,27 @@ def kernel_loop(be, name, reps):
         us = be.marks_ms() * 1e3 / reps
         print(json.dumps({"kernel": key, "avg_us": round(us, 3), "algorithmic_bytes": rot.algo,
                           "GBps": round(rot.algo / (us * 1e-6) / 1e9, 1)}))
+        return
+    if name == "calib":
+        from igllm_amd.backend import make_plane
+        N, K, M = 8192, 2048, 2048
+        rng = np.random.default_rng(2)
+        codes = rng.integers(0, 256, size=(N, K // 2), dtype=np.uint8)
+        gains = np.abs(rng.normal(0, 0.02, size=(N, 1))).astype(np.float32)
+        cp = be.attach(make_plane(codes, gains, K, group_size=K))
+        cp.plane.enter_gain = 2.5 / 127
+        cp.plane.leave_gain = 0.02
+        a = be.upload(rng.normal(size=(M, K)).astype(np.float32))
+        c = be.alloc(M * N * 4)
+        for _ in range(3):  # first launches load the code objects
+            be.plane_lift_dev(cp, a, K, M, c, N)
+        be.sync()
+        be.mark()
+        for _ in range(reps):
+            be.plane_lift_dev(cp, a, K, M, c, N)
+        be.mark()
+        us = be.marks_ms() * 1e3 / reps
+        print(json.dumps({"kernel": "calib", "M": M, "N": N, "K": K, "avg_us": round(us, 2)}))
         return
     if name in ("gemv", "gemv8"):
         N, K = SHAPES[0]
@@ -520,6 +543,37 @@ def main():
                                     "frac_of_mfma_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
         a.free()
         c.free()
+
+    # ---- calibrated prefill (enter_gain, one gain a row): fp32 lanes through
+    # plane_lift_dev, the MFMA GEMM on levels and unit gains plus the row close.
+    from igllm_amd.backend import make_plane as _make_plane
+    for name, (N, K, bits) in {"calibrated_u4_8192x2048_M2048": (8192, 2048, 4),
+                               "calibrated_u2_6144x1536_M2048": (6144, 1536, 2)}.items():
+        M = 2048
+        rng = np.random.default_rng(2)
+        codes = rng.integers(0, 256, size=(N, K * bits // 8), dtype=np.uint8)
+        gains = np.abs(rng.normal(0, 0.02, size=(N, 1))).astype(np.float32)
+        cp = be.attach(_make_plane(codes, gains, K, group_size=K, bits=bits))
+        cp.plane.enter_gain = 2.5 / 127
+        cp.plane.leave_gain = 0.02
+        a = be.upload(rng.normal(size=(M, K)).astype(np.float32))
+        c = be.alloc(M * N * 4)
+        for _ in range(3):
+            be.plane_lift_dev(cp, a, K, M, c, N)
+        be.sync()
+        be.mark()
+        reps = 20
+        for _ in range(reps):
+            be.plane_lift_dev(cp, a, K, M, c, N)
+        be.mark()
+        us = be.marks_ms() * 1e3 / reps
+        tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        prefill[name] = {"us": round(us, 2), "TFLOPs": round(tflops, 1),
+                         "frac_of_mfma_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                         "note": "fp32 in/out, includes the level pass, code widening and row close"}
+        a.free()
+        c.free()
+        be.detach(cp)
 
     # ---- decode attention, 8 q heads / 1 KV head / d=256, L=16384, int8 bytes.
     L, head, rings = 16384, 256, 40

@@ -379,7 +379,7 @@ static int gemm_run(igl_desk *desk, const igl_plane *sheet, const void *act_dev,
                                           sheet->code_bias,
                                           out_dev, out_bf16, out_stride, lane_count,
                                           sheet->row_count, sheet->col_count, st->gemm_dev,
-                                          st->stream));
+                                          NULL, st->stream));
 }
 
 int igl_gemm_lane_floor(void) { return IGL_GEMM_FLOOR; }
@@ -453,7 +453,7 @@ static int lift_levels_gemm(igl_desk_state *st, const igl_plane *sheet, const fl
   float *a_out = two ? NULL : out_dev;
   int a_stride = two ? N : out_stride;
   int code;
-  if (grow_dev(st, &st->quant_dev, &st->quant_floats, (size_t)lanes * (size_t)K) != IGL_OKAY ||
+  if (((two || !work) && grow_dev(st, &st->quant_dev, &st->quant_floats, (size_t)lanes * (size_t)K) != IGL_OKAY) ||
       (widen && grow_dev(st, &st->wide_dev, &st->wide_floats, (two ? 2 : 1) * plane_bytes / 4) != IGL_OKAY) ||
       (two && grow_dev(st, &st->lsum_dev, &st->lsum_floats, (size_t)lanes) != IGL_OKAY) ||
       (two && grow_dev(st, &st->prod_dev, &st->prod_floats, 2 * (size_t)lanes * (size_t)N) != IGL_OKAY) ||
@@ -465,10 +465,6 @@ static int lift_levels_gemm(igl_desk_state *st, const igl_plane *sheet, const fl
       return code;
   }
   if (two) a_out = st->prod_dev;
-  if ((code = hip_check(st, igl_launch_quant_level(act_dev, act_stride, st->quant_dev, K, K, lanes,
-                                                   sheet->enter_gain, two ? st->lsum_dev : NULL,
-                                                   st->stream))) != IGL_OKAY)
-    return code;
   if (widen) {
     hi_plane = (const uint8_t *)st->wide_dev;
     lo_plane = two ? hi_plane + plane_bytes : NULL;
@@ -480,14 +476,26 @@ static int lift_levels_gemm(igl_desk_state *st, const igl_plane *sheet, const fl
                                                     st->stream))) != IGL_OKAY)
       return code;
   }
+  if (!two && work) {
+    /* the large-tile form takes the levels and the row close in its own
+     * conversion and store */
+    const igl_gemm_close close = {sheet->device->gains, sheet->enter_gain, sheet->leave_gain};
+    return hip_check(st, igl_launch_gemm_q4(act_dev, 0, act_stride, hi_plane, row_stride, st->ones_dev, 1, 31,
+                                            8, out_dev, 0, out_stride, lanes, N, K, st->gemm_dev, &close,
+                                            st->stream));
+  }
+  if ((code = hip_check(st, igl_launch_quant_level(act_dev, act_stride, st->quant_dev, K, K, lanes,
+                                                   sheet->enter_gain, two ? st->lsum_dev : NULL,
+                                                   st->stream))) != IGL_OKAY)
+    return code;
   if ((code = hip_check(st, igl_launch_gemm_q4(st->quant_dev, 0, K, hi_plane, row_stride, st->ones_dev, 1, 31,
-                                               8, a_out, 0, a_stride, lanes, N, K, st->gemm_dev,
+                                               8, a_out, 0, a_stride, lanes, N, K, st->gemm_dev, NULL,
                                                st->stream))) != IGL_OKAY)
     return code;
   if (two &&
       (code = hip_check(st, igl_launch_gemm_q4(st->quant_dev, 0, K, lo_plane, row_stride, st->ones_dev, 1, 31,
                                                8, st->prod_dev + (size_t)lanes * (size_t)N, 0, N, lanes,
-                                               N, K, st->gemm_dev, st->stream))) != IGL_OKAY)
+                                               N, K, st->gemm_dev, NULL, st->stream))) != IGL_OKAY)
     return code;
   return hip_check(st, igl_launch_grid_close(a_out, two ? st->prod_dev + (size_t)lanes * (size_t)N : NULL,
                                              two ? st->lsum_dev : NULL, a_stride,

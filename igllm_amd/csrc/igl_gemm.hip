@@ -20,6 +20,7 @@
 // significant bits instead of eight, and bf16 activations convert exactly to
 // binary16 over its normal range (|a| < 65504; larger values saturate).
 #include "igl_device.h"
+#include "igl_launch.h"
 
 namespace igl {
 
@@ -220,8 +221,12 @@ constexpr int kBigStage = kBigA * 2 + kBigB + kBigG * 4;
 // a16 = binary16(a), saturating at +-65504, in the large-tile form's operand
 // order: within each eight k, positions 0 4 1 5 2 6 3 7, and k = 1, 5, 3, 7
 // divided by 16 (exact for every normal binary16).
+// With level_step > 0 (a calibrated plane's prefill), each x is first its
+// quant_step level rint(x / level_step) clamped to [-128, 127]: an integer the
+// binary16 operand holds exactly (and so does a level / 16).
 template <bool A_BF16>
-__global__ void act_half_kernel(const void *act, int act_stride, int M, int K, _Float16 *a16) {
+__global__ void act_half_kernel(const void *act, int act_stride, int M, int K, _Float16 *a16,
+                                float level_step) {
   const int k8 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
   const int m = blockIdx.y;
   if (k8 >= K || m >= M) return;
@@ -243,6 +248,14 @@ __global__ void act_half_kernel(const void *act, int act_stride, int M, int K, _
     for (int i = 0; i < 4; ++i) {
       x[i] = lo[i];
       x[4 + i] = hi[i];
+    }
+  }
+  if (level_step > 0.0f) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float level = __builtin_rintf(x[i] / level_step);
+      level = level < -128.0f ? -128.0f : level;
+      x[i] = level > 127.0f ? 127.0f : level;
     }
   }
   const _Float16 sixteenth = (_Float16)0.0625f;
@@ -270,7 +283,22 @@ struct GemmBigArgs {
   int M, N, K;            // K: the whole plane's columns
   int k_steps;            // 64-wide steps of one K slice (blockIdx.z)
   size_t slice_floats;    // floats between slices' partials (0: no split)
+  igl_gemm_close close;   // fp32 C only: C = grid(close.gains[n] step acc, leave)
 };
+
+// The row close of a calibrated plane's product on levels and unit gains:
+// gain * step * part (one rounding each, as the reference's level path), then
+// the leave grid (quant_step).
+__device__ __forceinline__ float close_value(const igl_gemm_close &c, int n, float part) {
+  float y = c.gains[n] * c.step * part;
+  if (c.leave > 0.0f) {
+    float level = __builtin_rintf(y / c.leave);
+    level = level < -128.0f ? -128.0f : level;
+    level = level > 127.0f ? 127.0f : level;
+    y = level * c.leave;
+  }
+  return y;
+}
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void global_void_t;
@@ -417,7 +445,8 @@ __global__ __launch_bounds__(512) void gemm_q4_big_kernel(GemmBigArgs g) {
         else if (C_BF16)
           reinterpret_cast<uint16_t *>(g.out)[(size_t)m * g.out_stride + nn] = float_to_bf16(acc[i][j][r]);
         else
-          reinterpret_cast<float *>(g.out)[(size_t)m * g.out_stride + nn] = acc[i][j][r];
+          reinterpret_cast<float *>(g.out)[(size_t)m * g.out_stride + nn] =
+              g.close.gains ? close_value(g.close, nn, acc[i][j][r]) : acc[i][j][r];
       }
     }
 }
@@ -425,7 +454,7 @@ __global__ __launch_bounds__(512) void gemm_q4_big_kernel(GemmBigArgs g) {
 // C = the K slices' partials added in slice order (four columns a thread).
 template <bool C_BF16>
 __global__ void gemm_slice_sum_kernel(const float *part, int slices, size_t slice_floats, int M,
-                                      int N, void *out, int out_stride) {
+                                      int N, void *out, int out_stride, igl_gemm_close close) {
   const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
   const int m = blockIdx.y;
   if (n >= N) return;
@@ -438,7 +467,8 @@ __global__ void gemm_slice_sum_kernel(const float *part, int slices, size_t slic
     if (C_BF16)
       reinterpret_cast<uint16_t *>(out)[(size_t)m * out_stride + n + e] = float_to_bf16(t[e]);
     else
-      reinterpret_cast<float *>(out)[(size_t)m * out_stride + n + e] = t[e];
+      reinterpret_cast<float *>(out)[(size_t)m * out_stride + n + e] =
+          close.gains ? close_value(close, n + e, t[e]) : t[e];
   }
 }
 
@@ -475,16 +505,22 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
                                          const uint8_t *codes, long long row_stride,
                                          const float *gains, int gain_stride, int group_shift,
                                          int code_bias, void *out, int out_bf16, int out_stride,
-                                         int M, int N, int K, void *work, hipStream_t stream) {
+                                         int M, int N, int K, void *work,
+                                         const igl_gemm_close *close, hipStream_t stream) {
+  const igl_gemm_close no_close = {nullptr, 0.0f, 0.0f};
+  const igl_gemm_close cl = close ? *close : no_close;
+  if (cl.gains && (out_bf16 || act_bf16 || !igl_gemm_work_bytes(M, N, K) || !work))
+    return hipErrorInvalidValue;  // the close rides only on the large-tile form's fp32 C
   if (igl_gemm_work_bytes(M, N, K) && work) {
     _Float16 *a16 = reinterpret_cast<_Float16 *>(work);
     const int slices = gemm_slices(M, N, K);
     float *part = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(work) + gemm_half_bytes(M, K));
     dim3 cgrid((K / 8 + 255) / 256, M);
     if (act_bf16)
-      hipLaunchKernelGGL((act_half_kernel<true>), cgrid, dim3(256), 0, stream, act, act_stride, M, K, a16);
+      hipLaunchKernelGGL((act_half_kernel<true>), cgrid, dim3(256), 0, stream, act, act_stride, M, K, a16, 0.0f);
     else
-      hipLaunchKernelGGL((act_half_kernel<false>), cgrid, dim3(256), 0, stream, act, act_stride, M, K, a16);
+      hipLaunchKernelGGL((act_half_kernel<false>), cgrid, dim3(256), 0, stream, act, act_stride, M, K, a16,
+                         cl.gains ? cl.step : 0.0f);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     GemmBigArgs b;
@@ -502,6 +538,7 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
     b.K = K;
     b.k_steps = K / kBigK / slices;
     b.slice_floats = slices > 1 ? (size_t)M * N : 0;
+    b.close = cl;
     const size_t lds = (size_t)kBigStages * kBigStage;
     static int granted[2];
     const void *fn = out_bf16 ? reinterpret_cast<const void *>(&gemm_q4_big_kernel<true>)
@@ -521,10 +558,10 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
     dim3 sgrid((N / 4 + 255) / 256, M);
     if (out_bf16)
       hipLaunchKernelGGL((gemm_slice_sum_kernel<true>), sgrid, dim3(256), 0, stream, part, slices,
-                         b.slice_floats, M, N, out, out_stride);
+                         b.slice_floats, M, N, out, out_stride, cl);
     else
       hipLaunchKernelGGL((gemm_slice_sum_kernel<false>), sgrid, dim3(256), 0, stream, part, slices,
-                         b.slice_floats, M, N, out, out_stride);
+                         b.slice_floats, M, N, out, out_stride, cl);
     return hipGetLastError();
   }
   GemmArgs g;

@@ -97,13 +97,24 @@ hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_stride, const 
                               int act_stride, int lanes, float *out, int out_stride, int N, int K,
                               float *part, int lds_limit, hipStream_t stream);
 
-/* `work`: igl_gemm_work_bytes(M, N, K) bytes (NULL takes the small-tile form). */
+/* The row close of a calibrated plane's product taken on levels and unit gains:
+ * C = quant_step(gains[n] * step * acc, leave) (fp32 C).  With `gains` set the
+ * activations are also put on the grid of `step` (their levels) as they are
+ * converted.  Only on the large-tile form with fp32 activations and output. */
+typedef struct igl_gemm_close {
+  const float *gains;
+  float step;
+  float leave;
+} igl_gemm_close;
+
+/* `work`: igl_gemm_work_bytes(M, N, K) bytes (NULL takes the small-tile form);
+ * `close` NULL for a plain product. */
 size_t igl_gemm_work_bytes(int M, int N, int K);
 hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride, const uint8_t *codes,
                               long long row_stride, const float *gains, int gain_stride,
                               int group_shift, int code_bias, void *out, int out_bf16,
                               int out_stride, int M, int N, int K, void *work,
-                              hipStream_t stream);
+                              const igl_gemm_close *close, hipStream_t stream);
 
 int igl_attend_chunk_size(void);
 size_t igl_attend_work_floats(int place0, int window, int lanes, int head_count, int head_size);
