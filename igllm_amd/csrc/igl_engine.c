@@ -42,7 +42,7 @@
 
 typedef struct eng_tensor {
   char      name[160];
-  int       dtype;     /* 0 U8, 1 F32, -1 other */
+  int       dtype;     /* 0 U8, 1 F32, 2 I8, 3 BF16, -1 other */
   int       rank;
   long long shape[3];
   size_t    begin, end;
@@ -216,7 +216,12 @@ static int parse_header(igl_engine *e, const char *h, size_t len) {
       memcpy(t->name, name, nlen);
       t->name[nlen] = '\0';
       v = member(obj, obj_end, "dtype");
-      t->dtype = !v ? -1 : strncmp(v, "\"U8\"", 4) == 0 ? 0 : strncmp(v, "\"F32\"", 5) == 0 ? 1 : -1;
+      t->dtype = !v                                   ? -1
+                 : strncmp(v, "\"U8\"", 4) == 0   ? 0
+                 : strncmp(v, "\"F32\"", 5) == 0  ? 1
+                 : strncmp(v, "\"I8\"", 4) == 0   ? 2
+                 : strncmp(v, "\"BF16\"", 6) == 0 ? 3
+                                                  : -1;
       v = member(obj, obj_end, "shape");
       if (!v || *v != '[') return IGL_FAIL_FORMAT;
       ++v;
@@ -255,20 +260,55 @@ static const eng_tensor *find_stem(const igl_engine *e, const char *stem, const 
   return find_tensor(e, name);
 }
 
-/* A 4-bit code plane in the export's layout (plane_bind_gemma, 7886-7955):
- * `weight` (or `embedding_quantized`) U8 [rows, cols/2] + its F32 scale
- * [rows, groups]; bound in place on the device copy of the payload. */
+static float read_scalar(const igl_engine *e, const char *name, float spare) {
+  const eng_tensor *t = find_tensor(e, name);
+  float v;
+  if (!t || t->dtype != 1 || t->end - t->begin != 4) return spare;
+  memcpy(&v, (const uint8_t *)e->map + e->payload_at + t->begin, 4);
+  return v;
+}
+
+/* A plane in the export's layout (plane_bind_gemma, 7886-7955, and
+ * plane_bind_part's real arm, 7985-7998), bound in place on the device copy of
+ * the payload:
+ *   `weight` (or `embedding_quantized`) U8 [rows, cols * bits / 8], the width
+ *   the one that makes the byte count come out for `col_hint` (8, 4, 2 bits),
+ *   or I8 [rows, cols] (8 bits, code_flip 128), with an F32 scale [rows, G];
+ *   `input_activation_scale` / `output_activation_scale`, where present, are
+ *   the plane's enter and leave grids (7946-7953);
+ *   a BF16 or F32 `weight` [rows, col_hint] with no scale is a real plane. */
 static int bind_plane(igl_engine *e, const char *stem, int col_hint, igl_plane *out) {
+  static const int widths[] = {8, 4, 2};
   const eng_tensor *w = find_stem(e, stem, "embedding_quantized");
   const eng_tensor *s = w ? find_stem(e, stem, "embedding_scale") : NULL;
+  char name[320];
+  int bits = 0, groups;
   if (!w) {
     w = find_stem(e, stem, "weight");
     s = find_stem(e, stem, "weight_scale");
   }
-  if (!w || !s) return IGL_FAIL_MISSING;
-  if (w->dtype != 0 || s->dtype != 1 || w->rank != 2 || s->rank != 2) return IGL_FAIL_SUPPORT;
-  if (w->shape[1] * 2 != col_hint) return IGL_FAIL_SUPPORT; /* 4 bits a code only */
+  if (!w) return IGL_FAIL_MISSING;
   memset(out, 0, sizeof(*out));
+  if (!s && (w->dtype == 1 || w->dtype == 3)) {
+    if (w->rank != 2 || w->shape[1] != col_hint) return IGL_FAIL_FORMAT;
+    out->form = IGL_PLANE_REAL;
+    out->row_count = (int)w->shape[0];
+    out->col_count = col_hint;
+    out->real_data = (const uint8_t *)e->map + e->payload_at + w->begin;
+    out->real_type = w->dtype == 3 ? IGL_STORE_BF16 : IGL_STORE_F32;
+    return igl_plane_bind_dev(e->desk, out, e->payload_dev + w->begin, NULL);
+  }
+  if (!s) return IGL_FAIL_MISSING;
+  if ((w->dtype != 0 && w->dtype != 2) || s->dtype != 1 || w->rank != 2 || s->rank < 1 || s->rank > 2)
+    return IGL_FAIL_SUPPORT;
+  if (w->dtype == 2) {
+    bits = w->shape[1] == col_hint ? 8 : 0;
+  } else {
+    for (size_t i = 0; i < sizeof(widths) / sizeof(widths[0]) && !bits; ++i)
+      if (((long long)col_hint * widths[i] + 7) / 8 == w->shape[1]) bits = widths[i];
+  }
+  groups = s->rank == 2 ? (int)s->shape[1] : 1;
+  if (!bits || groups < 1 || col_hint % groups) return IGL_FAIL_FORMAT;
   out->form = IGL_PLANE_CODE;
   out->row_count = (int)w->shape[0];
   out->col_count = col_hint;
@@ -276,10 +316,15 @@ static int bind_plane(igl_engine *e, const char *stem, int col_hint, igl_plane *
   out->row_stride = (size_t)w->shape[1];
   out->gain_data = (const uint8_t *)e->map + e->payload_at + s->begin;
   out->gain_type = IGL_STORE_F32;
-  out->bit_count = 4;
-  out->code_bias = 8;
-  out->group_count = (int)s->shape[1];
-  out->group_size = col_hint / out->group_count;
+  out->bit_count = bits;
+  out->code_bias = 1 << (bits - 1);
+  out->code_flip = w->dtype == 2 ? out->code_bias : 0;
+  out->group_count = groups;
+  out->group_size = col_hint / groups;
+  snprintf(name, sizeof(name), "%s.input_activation_scale", stem);
+  out->enter_gain = read_scalar(e, name, 0.0f);
+  snprintf(name, sizeof(name), "%s.output_activation_scale", stem);
+  out->leave_gain = read_scalar(e, name, 0.0f);
   return igl_plane_bind_dev(e->desk, out, e->payload_dev + w->begin,
                             (const float *)(e->payload_dev + s->begin));
 }
@@ -291,13 +336,6 @@ static const float *bind_vector(igl_engine *e, const char *stem, int n) {
   return (const float *)(e->payload_dev + t->begin);
 }
 
-static float read_scalar(const igl_engine *e, const char *name, float spare) {
-  const eng_tensor *t = find_tensor(e, name);
-  float v;
-  if (!t || t->dtype != 1 || t->end - t->begin != 4) return spare;
-  memcpy(&v, (const uint8_t *)e->map + e->payload_at + t->begin, 4);
-  return v;
-}
 
 /* rope_build (8121-8145): inverse frequencies 1/theta^(2i/d) in double, as
  * float; "proportional" rotates only partial * d / 2 pairs. */
@@ -629,6 +667,9 @@ static const float *dev_gains(const igl_engine *e, const igl_plane *p) {
 
 static int project(igl_engine *e, const igl_plane *p, const float *act, int act_stride, int lanes,
                    float *out, int out_stride) {
+  /* plane_lift_many (7814-7843): a calibrated plane's product on its grids */
+  if (p->form == IGL_PLANE_CODE && (p->enter_gain > 0.0f || p->leave_gain > 0.0f))
+    return igl_plane_lift_dev(e->desk, p, act, act_stride, lanes, out, out_stride);
   if (e->precise) return igl_gemv_dev(e->desk, p, act, act_stride, lanes, out, out_stride);
   return igl_mat_mat_dev(e->desk, p, act, act_stride, lanes, out, out_stride);
 }
@@ -658,13 +699,14 @@ static void group_add(igl_engine *e, eng_group *g, const igl_plane *p, float *ou
   g->count++;
 }
 
-/* Planes that can share one launch: 4-bit, the same width and groups, K
- * within the register form, 4-row multiples between segments. */
+/* Planes that can share one launch: 4-bit and uncalibrated, the same width
+ * and groups, K within the register form, 4-row multiples between segments. */
 static int group_fits(const eng_group *g, const igl_plane *const *p, int mode) {
   for (int i = 0; i < g->count; ++i) {
     if (p[i]->col_count != p[0]->col_count || p[i]->group_size != p[0]->group_size ||
         p[i]->group_count != p[0]->group_count || p[i]->code_bias != p[0]->code_bias ||
-        p[i]->bit_count != 4 || p[i]->code_flip != 0 || p[i]->col_count > 8192)
+        p[i]->bit_count != 4 || p[i]->code_flip != 0 || p[i]->col_count > 8192 ||
+        p[i]->enter_gain > 0.0f || p[i]->leave_gain > 0.0f)
       return 0;
     if (mode == IGL_GEMV_SEGMENTS && i + 1 < g->count && p[i]->row_count % 4) return 0;
   }
@@ -819,19 +861,18 @@ static int run_pass(igl_engine *e, int bound, int lanes, int logits) {
   /* embedding row times sqrt(hidden) */
   {
     const igl_plane *p = &e->embed;
-    RUN(igl_launch_gather_rows(dev_codes(e, p), (long long)p->row_stride, dev_gains(e, p),
-                               p->group_count, igl_plane_group_shift(p), p->code_bias, H, p->row_count,
-                               e->ids_dev, lanes, (float)sqrt((double)H), e->state, H, st));
+    const igl_code_view view = igl_plane_view(p, dev_codes(e, p), dev_gains(e, p));
+    RUN(igl_launch_gather_rows(&view, H, p->row_count, e->ids_dev, lanes, (float)sqrt((double)H),
+                               e->state, H, st));
   }
   /* per-layer inputs */
   {
     const igl_plane *p = &e->ple_embed;
     const int chunk_all = e->layers * e->ple;
     OKAY(project(e, &e->ple_lift, e->state, H, lanes, e->ple_room, e->ple_stride));
-    RUN(igl_launch_gather_rows(dev_codes(e, p), (long long)p->row_stride, dev_gains(e, p),
-                               p->group_count, igl_plane_group_shift(p), p->code_bias, chunk_all, p->row_count,
-                               e->ids_dev, lanes, (float)sqrt((double)e->ple), e->ple_seed,
-                               e->ple_stride, st));
+    const igl_code_view view = igl_plane_view(p, dev_codes(e, p), dev_gains(e, p));
+    RUN(igl_launch_gather_rows(&view, chunk_all, p->row_count, e->ids_dev, lanes,
+                               (float)sqrt((double)e->ple), e->ple_seed, e->ple_stride, st));
     RUN(igl_launch_ple_mix(e->ple_room, e->ple_stride, e->ple_seed, e->ple_stride, e->ple_norm,
                            e->ple, e->layers, lanes, e->eps, (float)(1.0 / sqrt((double)H)),
                            (float)(1.0 / sqrt(2.0)), st));

@@ -32,13 +32,18 @@
 
 typedef struct gemma_tensor {
   char   name[160];
-  int    dtype;       /* 0 = U8, 1 = F32 */
+  int    dtype;       /* 0 = U8, 1 = F32, 2 = I8, 3 = BF16 */
   int    rank;
   long long shape[2];
   size_t offset;      /* within the payload */
   size_t bytes;
-  int    fill;        /* 0 codes, 1 scales, 2 norm gain, 3 layer scalar, 4 cache scale */
+  int    fill;        /* 0 codes, 1 scales, 2 norm gain, 3 layer scalar, 4 cache scale,
+                         5 the constant `value`, 6 scales value * U(0.75, 1.25), 7 bf16 N(0, value),
+                         8 scales value * U(0.99, 1.01), 9 2-bit codes of mean value 0 */
+  float  value;
 } gemma_tensor;
+
+static const char *const k_dtype_name[] = {"U8", "F32", "I8", "BF16"};
 
 typedef struct gemma_list {
   gemma_tensor item[GEMMA_TENSOR_LIMIT];
@@ -86,7 +91,7 @@ static int add_tensor(gemma_list *list, const char *name, int dtype, int rank, l
   t->rank = rank;
   t->shape[0] = d0;
   t->shape[1] = d1;
-  t->bytes = elems * (dtype == 0 ? 1u : 4u);
+  t->bytes = elems * (dtype == 1 ? 4u : dtype == 3 ? 2u : 1u);
   t->offset = list->payload;
   t->fill = fill;
   list->payload += (t->bytes + GEMMA_ALIGN - 1) / GEMMA_ALIGN * GEMMA_ALIGN;
@@ -104,6 +109,32 @@ static int add_plane(gemma_list *list, const char *stem, long long rows, long lo
   return add_tensor(list, name, 1, 2, rows, cols / 32, 1);
 }
 
+/* A plane in the export's own kinds (plane_bind_gemma, app_core.c:7886-7955):
+ * `bits`-wide codes (U8, or I8 for signed bytes), `groups` scale columns of
+ * gain_std * U(0.75, 1.25) (one a row, as a per-channel export's absmax scales
+ * sit close together), and where `enter` > 0 the calibrated activation steps
+ * `input_activation_scale` / `output_activation_scale` (7946-7953). */
+static int add_plane_kind(gemma_list *list, const char *stem, long long rows, long long cols, int embed,
+                          int bits, int i8, long long groups, float gain_std, float enter, float leave) {
+  char name[200];
+  int code;
+  snprintf(name, sizeof(name), "%s.%s", stem, embed ? "embedding_quantized" : "weight");
+  if ((code = add_tensor(list, name, i8 ? 2 : 0, 2, rows, cols * bits / 8, bits == 2 ? 9 : 0)) != IGL_OKAY)
+    return code;
+  snprintf(name, sizeof(name), "%s.%s", stem, embed ? "embedding_scale" : "weight_scale");
+  if ((code = add_tensor(list, name, 1, 2, rows, groups, 6)) != IGL_OKAY) return code;
+  list->item[list->count - 1].value = gain_std;
+  if (enter > 0.0f) {
+    snprintf(name, sizeof(name), "%s.input_activation_scale", stem);
+    if ((code = add_tensor(list, name, 1, 1, 1, 0, 5)) != IGL_OKAY) return code;
+    list->item[list->count - 1].value = enter;
+    snprintf(name, sizeof(name), "%s.output_activation_scale", stem);
+    if ((code = add_tensor(list, name, 1, 1, 1, 0, 5)) != IGL_OKAY) return code;
+    list->item[list->count - 1].value = leave;
+  }
+  return IGL_OKAY;
+}
+
 static int add_vector(gemma_list *list, const char *stem, long long n, int fill) {
   char name[200];
   snprintf(name, sizeof(name), "%s.weight", stem);
@@ -119,10 +150,25 @@ static int igl_gemma_layout(const igl_gemma_shape *s, gemma_list *list) {
   memset(list, 0, sizeof(*list));
   if (s->hidden % 32 || s->inner % 32 || s->ple_size % 32 || s->head_dim % 32 || s->full_head_dim % 32)
     return IGL_FAIL_ARGUMENT;
-  if (add_plane(list, P "embed_tokens", s->vocab, s->hidden, 1) ||
-      add_plane(list, P "embed_tokens_per_layer", s->vocab, ple_all, 1) ||
-      add_plane(list, P "per_layer_model_projection", ple_all, s->hidden, 0) ||
-      add_vector(list, P "per_layer_projection_norm", s->ple_size, 2) ||
+  if (s->kinds) {
+    /* the export's kinds: 2-bit embedding (the head, tied), 4-bit per-layer
+     * embedding with a scale column per layer, bf16 per_layer_model_projection */
+    /* the tied head's rows: 2-bit values average -0.5, so scales that differ
+     * from row to row would put a row-dependent bias into every logit; the
+     * embedding's scales sit within 1% of each other */
+    if (add_plane_kind(list, P "embed_tokens", s->vocab, s->hidden, 1, 2, 0, 1, 0.05f, 0.0f, 0.0f) ||
+        add_plane_kind(list, P "embed_tokens_per_layer", s->vocab, ple_all, 1, 4, 0, s->layers, 0.02f, 0.0f,
+                       0.0f) ||
+        add_tensor(list, P "per_layer_model_projection.weight", 3, 2, ple_all, s->hidden, 7))
+      return IGL_FAIL_SUPPORT;
+    list->item[1].fill = 8;
+    list->item[list->count - 1].value = 0.02f;
+  } else if (add_plane(list, P "embed_tokens", s->vocab, s->hidden, 1) ||
+             add_plane(list, P "embed_tokens_per_layer", s->vocab, ple_all, 1) ||
+             add_plane(list, P "per_layer_model_projection", ple_all, s->hidden, 0)) {
+    return IGL_FAIL_SUPPORT;
+  }
+  if (add_vector(list, P "per_layer_projection_norm", s->ple_size, 2) ||
       add_vector(list, P "norm", s->hidden, 2))
     return IGL_FAIL_SUPPORT;
   for (int i = 0; i < s->layers; ++i) {
@@ -131,34 +177,44 @@ static int igl_gemma_layout(const igl_gemma_shape *s, gemma_list *list) {
     int shared = i >= first_share;
     long long inner = (long long)s->inner * (shared && s->double_wide ? 2 : 1);
     int code = 0;
+    /* the export's kinds: 4-bit attention, MLPs of layers 0-14 4-bit and the
+     * rest 2-bit, signed-byte per-layer planes; one scale a row, every
+     * projection calibrated (module_quant_configs, model/config.json) */
+    const int mlp_bits = i < 15 ? 4 : 2;
+    const float mlp_std = mlp_bits == 4 ? 0.02f : 0.05f;
 #define L(fmt) (snprintf(stem, sizeof(stem), P "layers.%d." fmt, i), stem)
-    code |= add_plane(list, L("self_attn.q_proj"), (long long)s->heads * hd, s->hidden, 0);
+#define PLANE(name, rows, cols, bits, i8, std, enter, leave)                                       \
+  (s->kinds ? add_plane_kind(list, L(name), rows, cols, 0, bits, i8, 1, std, enter, leave)         \
+            : add_plane(list, L(name), rows, cols, 0))
+    code |= PLANE("self_attn.q_proj", (long long)s->heads * hd, s->hidden, 4, 0, 0.02f, 0.04f, 0.04f);
     if (!shared) {
-      code |= add_plane(list, L("self_attn.k_proj"), (long long)s->kv_heads * hd, s->hidden, 0);
-      code |= add_plane(list, L("self_attn.v_proj"), (long long)s->kv_heads * hd, s->hidden, 0);
+      code |= PLANE("self_attn.k_proj", (long long)s->kv_heads * hd, s->hidden, 4, 0, 0.02f, 0.04f, 0.04f);
+      code |= PLANE("self_attn.v_proj", (long long)s->kv_heads * hd, s->hidden, 4, 0, 0.02f, 0.04f, 0.04f);
       code |= add_vector(list, L("self_attn.k_norm"), hd, 2);
       if (s->cache_scales) {
         code |= add_tensor(list, L("self_attn.k_cache_scale"), 1, 0, 1, 0, 4);
         code |= add_tensor(list, L("self_attn.v_cache_scale"), 1, 0, 1, 0, 4);
       }
     }
-    code |= add_plane(list, L("self_attn.o_proj"), s->hidden, (long long)s->heads * hd, 0);
+    code |= PLANE("self_attn.o_proj", s->hidden, (long long)s->heads * hd, 4, 0, 0.02f, 0.04f, 0.04f);
     code |= add_vector(list, L("self_attn.q_norm"), hd, 2);
     code |= add_vector(list, L("input_layernorm"), s->hidden, 2);
     code |= add_vector(list, L("post_attention_layernorm"), s->hidden, 2);
     code |= add_vector(list, L("pre_feedforward_layernorm"), s->hidden, 2);
     code |= add_vector(list, L("post_feedforward_layernorm"), s->hidden, 2);
-    code |= add_plane(list, L("mlp.gate_proj"), inner, s->hidden, 0);
-    code |= add_plane(list, L("mlp.up_proj"), inner, s->hidden, 0);
-    code |= add_plane(list, L("mlp.down_proj"), s->hidden, inner, 0);
-    code |= add_plane(list, L("per_layer_input_gate"), s->ple_size, s->hidden, 0);
-    code |= add_plane(list, L("per_layer_projection"), s->hidden, s->ple_size, 0);
+    code |= PLANE("mlp.gate_proj", inner, s->hidden, mlp_bits, 0, mlp_std, 0.04f, mlp_bits == 4 ? 0.04f : 0.02f);
+    code |= PLANE("mlp.up_proj", inner, s->hidden, mlp_bits, 0, mlp_std, 0.04f, mlp_bits == 4 ? 0.04f : 0.02f);
+    code |= PLANE("mlp.down_proj", s->hidden, inner, mlp_bits, 0, mlp_std, mlp_bits == 4 ? 0.1f : 0.02f,
+                  mlp_bits == 4 ? 0.1f : 0.02f);
+    code |= PLANE("per_layer_input_gate", s->ple_size, s->hidden, 8, 1, 0.0012f, 0.1f, 0.05f);
+    code |= PLANE("per_layer_projection", s->hidden, s->ple_size, 8, 1, 0.0012f, 0.05f, 0.05f);
+#undef PLANE
     code |= add_vector(list, L("post_per_layer_input_norm"), s->hidden, 2);
     code |= add_tensor(list, L("layer_scalar"), 1, 0, 1, 0, 3);
 #undef L
     if (code) return IGL_FAIL_SUPPORT;
   }
-  if (add_plane(list, "lm_head", s->vocab, s->hidden, 0)) return IGL_FAIL_SUPPORT;
+  if (!s->kinds && add_plane(list, "lm_head", s->vocab, s->hidden, 0)) return IGL_FAIL_SUPPORT;
   return IGL_OKAY;
 }
 
@@ -223,6 +279,23 @@ static int write_config(const char *folder, const igl_gemma_shape *s) {
   return code;
 }
 
+/* 2-bit codes whose values c - 2 average zero, as a trained plane's do (a
+ * uniform draw would put a mean of -0.5 a code into every row and every
+ * activation it touches): P(c) = 2/16, 3/16, 4/16, 7/16 for c = 0..3, one
+ * nibble of a draw a code, four codes a byte, low bits first. */
+static void fill_codes2(igl_rng *rng, uint8_t *dst, size_t count) {
+  static const uint8_t k_code[16] = {0, 0, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 3, 3, 3, 3};
+  size_t i = 0;
+  while (i < count) {
+    uint64_t bits = igl_rng_next(rng);
+    for (int b = 0; b < 4 && i < count; ++b, ++i) {
+      uint8_t v = 0;
+      for (int f = 0; f < 4; ++f) v |= (uint8_t)(k_code[(bits >> (16 * b + 4 * f)) & 15] << (2 * f));
+      dst[i] = v;
+    }
+  }
+}
+
 /* Fills `count` bytes of codes: 16 nibbles a draw, low nibble first. */
 static void fill_codes(igl_rng *rng, uint8_t *dst, size_t count) {
   size_t i = 0;
@@ -263,7 +336,7 @@ int igl_gemma_write(const char *folder, const igl_gemma_shape *shape, uint64_t s
     else snprintf(shape_text, sizeof(shape_text), "[%lld,%lld]", x->shape[0], x->shape[1]);
     at += (size_t)snprintf(header + at, header_cap - at,
                            ",\"%s\":{\"dtype\":\"%s\",\"shape\":%s,\"data_offsets\":[%zu,%zu]}",
-                           x->name, x->dtype == 0 ? "U8" : "F32", shape_text, x->offset,
+                           x->name, k_dtype_name[x->dtype], shape_text, x->offset,
                            x->offset + x->bytes);
     if (at + 512 > header_cap) {
       code = IGL_FAIL_SUPPORT;
@@ -308,6 +381,8 @@ int igl_gemma_write(const char *folder, const igl_gemma_shape *shape, uint64_t s
         size_t take = left < buf_cap ? left : buf_cap;
         if (x->fill == 0) {
           fill_codes(&rng, buf, take);
+        } else if (x->fill == 9) {
+          fill_codes2(&rng, buf, take);
         } else {
           float *v = (float *)buf;
           size_t n = take / 4;
@@ -318,8 +393,29 @@ int igl_gemma_write(const char *folder, const igl_gemma_shape *shape, uint64_t s
           } else if (x->fill == 3) {
             for (size_t i = 0; i < n; ++i)
               v[i] = 0.85f + 0.3f * (float)((igl_rng_next(&rng) >> 11) * 0x1.0p-53);
-          } else {
+          } else if (x->fill == 4) {
             for (size_t i = 0; i < n; ++i) v[i] = 6.0f / 448.0f;
+          } else if (x->fill == 5) {
+            for (size_t i = 0; i < n; ++i) v[i] = x->value;
+          } else if (x->fill == 6 || x->fill == 8) {
+            const float spread = x->fill == 6 ? 0.5f : 0.02f;
+            for (size_t i = 0; i < n; ++i)
+              v[i] = x->value * (1.0f - 0.5f * spread +
+                                 spread * (float)((igl_rng_next(&rng) >> 11) * 0x1.0p-53));
+          } else {
+            /* bf16: the top halves of N(0, value) floats, two a word */
+            uint16_t *h = (uint16_t *)buf;
+            size_t count = take / 2;
+            float tmp[256];
+            for (size_t i = 0; i < count; i += 256) {
+              size_t m = count - i < 256 ? count - i : 256;
+              igl_rng_normal(&rng, tmp, m, 0.0f, x->value);
+              for (size_t j = 0; j < m; ++j) {
+                uint32_t bits;
+                memcpy(&bits, &tmp[j], 4);
+                h[i + j] = (uint16_t)(bits >> 16);
+              }
+            }
           }
         }
         if (fwrite(buf, 1, take, f) != take) { code = IGL_FAIL_FILE; goto done; }

@@ -129,10 +129,9 @@ hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t *value_stor
 void *igl_desk_stream(igl_desk *desk);
 
 /* session kernels (igl_session.hip) */
-hipError_t igl_launch_gather_rows(const uint8_t *codes, long long row_stride, const float *gains,
-                                  int group_count, int group_shift, int code_bias, int cols,
-                                  int rows, const int32_t *ids, int lanes, float factor,
-                                  float *out, int out_stride, hipStream_t stream);
+hipError_t igl_launch_gather_rows(const igl_code_view *v, int cols, int rows, const int32_t *ids,
+                                  int lanes, float factor, float *out, int out_stride,
+                                  hipStream_t stream);
 hipError_t igl_launch_ple_mix(float *room, int room_stride, const float *seed, int seed_stride,
                               const float *gain, int ple, int chunks, int lanes, float eps,
                               float lift_scale, float blend, hipStream_t stream);

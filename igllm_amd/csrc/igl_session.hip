@@ -8,23 +8,26 @@
 // 11455-11580) in the same order of float operations where the reference has
 // one; reductions the reference does in double (norms) are done in double.
 #include "igl_device.h"
+#include "igl_launch.h"
 
 namespace igl {
 
-// Rows `ids[l]` of a 4-bit code plane as floats times `factor`:
-// ((code - code_bias) * gain) * factor (plane_row 1826-1856, then kern_scale).
+// Rows `ids[l]` of a 2, 4 or 8-bit code plane as floats times `factor`:
+// (((code ^ flip) - code_bias) * gain) * factor (plane_row 1826-1856, then
+// kern_scale).
 __global__ void gather_rows_kernel(const uint8_t *codes, long long row_stride, const float *gains,
-                                   int group_count, int group_shift, int code_bias, int cols,
-                                   int rows, const int32_t *ids, float factor, float *out,
-                                   int out_stride) {
+                                   int group_count, int group_shift, int code_bias, int code_flip,
+                                   int bits, int cols, int rows, const int32_t *ids, float factor,
+                                   float *out, int out_stride) {
   const int lane = blockIdx.y;
   const int k = blockIdx.x * blockDim.x + threadIdx.x;
   if (k >= cols) return;
   int id = ids[lane];
   if (id < 0) id = 0;
   id %= rows;
-  const uint8_t b = codes[(size_t)id * row_stride + (k >> 1)];
-  const int c = (k & 1) ? (b >> 4) : (b & 15);
+  const int at = k * bits;
+  const uint8_t b = codes[(size_t)id * row_stride + (at >> 3)];
+  const int c = ((b >> (at & 7)) & ((1 << bits) - 1)) ^ code_flip;
   const float gain = gains[(size_t)id * group_count + ((unsigned)(k >> 5) >> group_shift)];
   const float v = (float)(c - code_bias) * gain;
   out[(size_t)lane * out_stride + k] = v * factor;
@@ -342,14 +345,12 @@ using namespace igl;
 
 static const int kPickBlocks = 256;
 
-extern "C" hipError_t igl_launch_gather_rows(const uint8_t *codes, long long row_stride,
-                                             const float *gains, int group_count, int group_shift,
-                                             int code_bias, int cols, int rows, const int32_t *ids,
-                                             int lanes, float factor, float *out, int out_stride,
-                                             hipStream_t stream) {
-  hipLaunchKernelGGL(gather_rows_kernel, dim3((cols + 255) / 256, lanes), dim3(256), 0, stream, codes,
-                     row_stride, gains, group_count, group_shift,
-                     code_bias, cols, rows, ids, factor, out, out_stride);
+extern "C" hipError_t igl_launch_gather_rows(const igl_code_view *v, int cols, int rows,
+                                             const int32_t *ids, int lanes, float factor, float *out,
+                                             int out_stride, hipStream_t stream) {
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((cols + 255) / 256, lanes), dim3(256), 0, stream, v->codes,
+                     v->row_stride, v->gains, v->gain_stride, v->group_shift, v->code_bias, v->code_flip,
+                     v->bit_count, cols, rows, ids, factor, out, out_stride);
   return hipGetLastError();
 }
 

@@ -241,6 +241,7 @@ typedef struct igl_gemma_shape {
   int   vocab, hidden, inner, layers, heads, kv_heads, head_dim, full_head_dim;
   int   window, ple_size, shared_layers, double_wide, full_every, max_positions;
   int   cache_scales;  /* write k/v_cache_scale so a byte cache is used */
+  int   kinds;         /* 0: int4 group-32 planes everywhere; 1: the export's own kinds */
   float norm_eps, logit_cap, rope_local, rope_global, partial_rotary;
 } igl_gemma_shape;
 

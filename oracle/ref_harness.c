@@ -189,6 +189,48 @@ int ref_engine_greedy(const char *folder, int thread_count, int cache_bits, int 
   return (int)code;
 }
 
+/* The same, but the step inputs are `forced` (not the picks): each step's
+ * pick and margin against a given token sequence, so a stream that a random
+ * model would collapse onto one id still walks many inputs. */
+int ref_engine_forced(const char *folder, int thread_count, int cache_bits, int window_limit,
+                      const int32_t *prompt, int prompt_count, const int32_t *forced, int gen_count,
+                      int32_t *out_ids, float *margin_out) {
+  app_setup setup = app_setup_plain();
+  app_model *model = NULL;
+  app_session *session = NULL;
+  app_code code;
+  setup.thread_count = thread_count;
+  setup.cache_bits = cache_bits;
+  setup.window_limit = window_limit;
+  code = model_load(folder, &setup, &model);
+  if (code != APP_OKAY) return (int)code;
+  code = session_open(model, &session);
+  if (code != APP_OKAY) {
+    model_free(model);
+    return (int)code;
+  }
+  code = session_prime(session, prompt, prompt_count);
+  for (int step = 0; code == APP_OKAY && step < gen_count; ++step) {
+    const float *logits = session_step(session, step == 0 ? prompt[prompt_count - 1] : forced[step - 1]);
+    int vocab = model_vocab_count(model);
+    int best = 0;
+    float second = -FLT_MAX;
+    if (!logits) {
+      code = APP_FAIL_STATE;
+      break;
+    }
+    for (int v = 1; v < vocab; ++v)
+      if (logits[v] > logits[best]) best = v;
+    for (int v = 0; v < vocab; ++v)
+      if (v != best && logits[v] > second) second = logits[v];
+    out_ids[step] = best;
+    margin_out[step] = logits[best] - second;
+  }
+  session_close(session);
+  model_free(model);
+  return (int)code;
+}
+
 static int32_t ref_top(const float *logits, int vocab) {
   int32_t best = 0;
   for (int v = 1; v < vocab; ++v)

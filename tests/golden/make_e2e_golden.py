@@ -6,12 +6,15 @@ by oracle/Makefile), run on this repository's seeded synthetic checkpoint.
     python tests/golden/make_e2e_golden.py small   # 10 layers, vocab 4096
     python tests/golden/make_e2e_golden.py e2b     # config.json dimensions
     python tests/golden/make_e2e_golden.py small_guess   # --guess 4, repeating prompt
+    python tests/golden/make_e2e_golden.py small_kinds   # the export's plane kinds, 20 layers
 
 For each, the checkpoint is written with igl_gemma_write (seed 0) into a
 scratch folder, the prompt is drawn by igllm_amd.engine.prompt_ids, and the
 reference's plain (SSE2) and tuned (AVX2+FMA) float builds each prime it and
 take `gen` greedy steps with an FP8 key/value cache (--cache 8).  The fixture
-keeps the prompt seed, both streams and every step's top-1/top-2 margin.
+keeps the prompt seed, both streams and every step's top-1/top-2 margin.  For
+the export's kinds (calibrated planes) the level build (AVX-512 VNNI, where
+this host has it) is run too: its products take the integer grid.
 """
 import ctypes
 import json
@@ -36,11 +39,18 @@ CASES = {
     # --guess 4 on a prompt that repeats its first `repeat` ids
     "small_guess": dict(shape=SMALL, prompt=600, gen=128, window=1024, repeat=128, span=4),
     "e2b_guess": dict(shape={}, prompt=2048, gen=256, window=2560, repeat=512, span=4),
+    # 2-bit MLPs from layer 15, I8 per-layer planes, bf16 per_layer_model_projection,
+    # one scale a row, every projection but the head calibrated
+    "small_kinds": dict(shape=dict(vocab=4096, hidden=512, inner=1024, layers=20, shared_layers=8, kinds=1),
+                        prompt=600, gen=128, window=1024),
 }
+
+PATHS = {"plain": oracle_lib.REF_PLAIN_PATH, "tuned": oracle_lib.REF_TUNED_PATH,
+         "level": oracle_lib.REF_LEVEL_PATH}
 
 
 def ref_stream(kind, folder, prompt, gen, window, threads):
-    lib = ctypes.CDLL(oracle_lib.REF_PLAIN_PATH if kind == "plain" else oracle_lib.REF_TUNED_PATH)
+    lib = ctypes.CDLL(PATHS[kind])
     fn = lib.ref_engine_greedy
     fn.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                    ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
@@ -52,6 +62,22 @@ def ref_stream(kind, folder, prompt, gen, window, threads):
     if code != 0:
         raise SystemExit(f"ref_engine_greedy({kind}) returned {code}")
     return out, margin, time.time() - t0
+
+
+def ref_forced(kind, folder, prompt, forced, window, threads):
+    """Each step's pick and margin with the inputs `forced` (after the prompt's
+    last id) instead of the picks."""
+    lib = ctypes.CDLL(PATHS[kind])
+    fn = lib.ref_engine_forced
+    fn.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                   ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    out = np.zeros(forced.size, np.int32)
+    margin = np.zeros(forced.size, np.float32)
+    code = fn(folder.encode(), threads, 8, window, prompt.ctypes.data, prompt.size, forced.ctypes.data,
+              forced.size, out.ctypes.data, margin.ctypes.data)
+    if code != 0:
+        raise SystemExit(f"ref_engine_forced({kind}) returned {code}")
+    return out, margin
 
 
 def ref_guess(kind, folder, prompt, gen, window, threads, span):
@@ -97,15 +123,32 @@ def main():
             json.dump(result, f, indent=1)
         print("agree", result["streams_agree"], "guess == greedy", result["guess_equals_greedy"])
         return
-    for kind in ("plain", "tuned"):
+    kinds = ("plain", "tuned")
+    if case["shape"].get("kinds") and oracle_lib.ref("level") is not None:
+        kinds += ("level",)
+    for kind in kinds:
         ids, margin, secs = ref_stream(kind, folder, prompt, case["gen"], case["window"], threads)
         result[kind] = {"ids": ids.tolist(), "margin": [float(m) for m in margin], "seconds": secs,
                         "threads": threads}
         print(kind, f"{secs:.1f}s", "min margin", float(margin.min()), flush=True)
     result["streams_agree"] = result["plain"]["ids"] == result["tuned"]["ids"]
+    if case["shape"].get("kinds"):
+        # a random model settles on one id; forced inputs (seed 1) walk many
+        forced = prompt_ids(case["gen"], shape.vocab, seed=1)
+        result["forced_seed"] = 1
+        for kind in kinds:
+            ids, margin = ref_forced(kind, folder, prompt, forced, case["window"], threads)
+            result[kind]["forced_ids"] = ids.tolist()
+            result[kind]["forced_margin"] = [float(m) for m in margin]
+            print(kind, "forced: distinct picks", len(set(ids.tolist())), "min margin", float(margin.min()),
+                  flush=True)
+    if "level" in result:
+        a, b = np.array(result["plain"]["ids"]), np.array(result["level"]["ids"])
+        result["plain_level_first_difference"] = int(np.argmax(a != b)) if np.any(a != b) else None
     with open(os.path.join(HERE, f"e2e_{name}.json"), "w") as f:
         json.dump(result, f, indent=1)
-    print("agree", result["streams_agree"])
+    print("agree", result["streams_agree"], "plain/level first difference",
+          result.get("plain_level_first_difference"))
 
 
 if __name__ == "__main__":

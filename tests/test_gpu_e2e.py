@@ -135,3 +135,78 @@ def test_small_guess_stream_matches_reference(backend, small_model, graph):
     gap = float(np.max(np.abs(np.array(gaps) - np.array(fx["greedy"]["margin"]))))
     print("max gap difference", gap)
     assert len(gaps) == fx["gen"] and gap <= 2e-3
+
+
+# ---- the export's plane kinds ------------------------------------------------
+
+KINDS_SHAPE = dict(vocab=4096, hidden=512, inner=1024, layers=20, shared_layers=8, kinds=1)
+
+
+@pytest.fixture(scope="module")
+def kinds_model():
+    fx = load_fixture("small_kinds")
+    folder = os.path.join(tempfile.gettempdir(), f"igl_gemma_kinds_{os.getpid()}")
+    write_gemma(folder, seed=fx["seed"], **KINDS_SHAPE)
+    return folder, fx
+
+
+@pytest.mark.parametrize("lane_limit,precise", [(16, True), (64, False)])
+def test_kinds_greedy_and_forced_match_reference(backend, kinds_model, lane_limit, precise):
+    """A checkpoint in the export's own kinds (2-bit MLPs from layer 15 and a
+    2-bit tied head, I8 per-layer planes, bf16 per_layer_model_projection, one
+    scale a row, every projection but the head calibrated), against the
+    reference engine (tests/golden/e2e_small_kinds.json).  Calibrated products
+    take the activation grid here, exact integer sums (the reference's level
+    path); the fixture's plain (SSE2 float) and level (VNNI) streams agree.
+
+    Greedy: the stream settles on one id, so the per-step top-1/top-2 gaps are
+    compared too.  Forced inputs (seed 1, so many inputs are walked): picks and
+    gaps against the plain build.  The activation grids make a quantized model
+    sensitive to the last bit: a product that lands near a level's edge moves a
+    whole level on a different rounding, so the reference's own builds part
+    too.  The bars come from that spread, recorded in the fixture: gaps within
+    1.5 times the largest gap difference between the reference's float,
+    tuned and level builds, and picks equal wherever the reference's gap
+    exceeds 1.5 times the largest gap at which those builds pick differently.
+    """
+    folder, fx = kinds_model
+    prompt = prompt_ids(fx["prompt_count"], fx["shape"]["vocab"], seed=fx["prompt_seed"])
+    forced = prompt_ids(fx["gen"], fx["shape"]["vocab"], seed=fx["forced_seed"])
+    eng = Engine(backend, folder, window_limit=fx["window_limit"], lane_limit=lane_limit, precise=precise)
+    try:
+        ids, margins = eng.greedy(prompt, fx["gen"])
+        eng.reset()
+        eng.prime(prompt)
+        picks, gaps = [], []
+        token = int(prompt[-1])
+        for t in forced:
+            pick, gap = eng.step(token)
+            picks.append(pick)
+            gaps.append(gap)
+            token = int(t)
+    finally:
+        eng.close()
+    want = np.array(fx["plain"]["ids"], dtype=np.int32)
+    ref_margin = np.array(fx["plain"]["margin"])
+    print("greedy: max gap difference", float(np.max(np.abs(margins - ref_margin))))
+    assert np.array_equal(ids, want)
+    assert np.max(np.abs(margins - ref_margin)) <= 2e-2
+    picks = np.array(picks)
+    gaps = np.array(gaps)
+    fwant = np.array(fx["plain"]["forced_ids"])
+    fgap = np.array(fx["plain"]["forced_margin"])
+    spread, parted = 0.0, 0.0
+    for kind in ("tuned", "level"):
+        if kind in fx:
+            other_gap = np.array(fx[kind]["forced_margin"])
+            other_ids = np.array(fx[kind]["forced_ids"])
+            spread = max(spread, float(np.max(np.abs(other_gap - fgap))))
+            if np.any(other_ids != fwant):
+                parted = max(parted, float(np.max(fgap[other_ids != fwant])))
+    decided = fgap > 1.5 * parted
+    print("reference builds: gap spread", spread, "largest gap where they part", parted)
+    print("forced: distinct picks", len(set(picks.tolist())), "mismatches", int((picks != fwant).sum()),
+          "of which decided", int(((picks != fwant) & decided).sum()), "of", int(decided.sum()),
+          "max gap difference", float(np.max(np.abs(gaps - fgap))))
+    assert np.array_equal(picks[decided], fwant[decided])
+    assert np.max(np.abs(gaps - fgap)) <= 1.5 * spread
