@@ -224,7 +224,45 @@ def e2e_decode(be, prompt_count=2048, gen=256):
     finally:
         import shutil
         shutil.rmtree(folder, ignore_errors=True)
+    out["export_kinds"] = e2e_kinds(be, prompt_count, gen)
     return out
+
+
+def e2e_kinds(be, prompt_count, gen):
+    """The same dimensions in the export's own kinds: 2-bit MLPs from layer 15
+    and a 2-bit tied head, I8 per-layer planes, bf16 per_layer_model_projection,
+    one scale a row, every projection but the head calibrated (activation
+    grids, the product on integer levels)."""
+    import shutil
+    import tempfile
+    from igllm_amd.engine import Engine, prompt_ids, write_gemma
+
+    root = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
+    folder = os.path.join(root, f"igl_gemma_e2b_kinds_{os.getpid()}")
+    try:
+        shape = write_gemma(folder, seed=0, kinds=1)
+        prompt = prompt_ids(prompt_count, shape.vocab, seed=0)
+        eng = Engine(be, folder, window_limit=prompt_count + gen + 64, lane_limit=256, precise=False)
+        try:
+            t0 = time.perf_counter()
+            eng.prime(prompt)
+            be.sync()
+            prime_s = time.perf_counter() - t0
+            token = int(prompt[-1])
+            margins = []
+            t0 = time.perf_counter()
+            for _ in range(gen):
+                token, margin = eng.step(token)
+                margins.append(margin)
+            decode_s = time.perf_counter() - t0
+        finally:
+            eng.close()
+        return {"prefill_tok_s": round((prompt_count - 1) / prime_s, 1),
+                "decode_tok_s": round(gen / decode_s, 1),
+                "decode_ms_per_token": round(decode_s * 1e3 / gen, 3),
+                "min_margin": round(float(min(margins)), 5), "lane_limit": 256}
+    finally:
+        shutil.rmtree(folder, ignore_errors=True)
 
 
 def e2e_guess(be, folder, shape, prompt_count, gen, span=4, repeat=512):

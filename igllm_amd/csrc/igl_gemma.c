@@ -27,7 +27,7 @@
 
 #include "igl_backend.h"
 
-#define GEMMA_TENSOR_LIMIT 1024
+#define GEMMA_TENSOR_LIMIT 4096
 #define GEMMA_ALIGN 256u
 
 typedef struct gemma_tensor {
@@ -309,7 +309,7 @@ int igl_gemma_write(const char *folder, const igl_gemma_shape *shape, uint64_t s
   gemma_list *list;
   igl_rng rng;
   char path[1024], *header = NULL;
-  size_t header_cap = 256 * 1024, at = 0, pad;
+  size_t header_cap = 1024 * 1024, at = 0, pad;
   FILE *f = NULL;
   uint8_t *buf = NULL;
   const size_t buf_cap = 64u << 20;
