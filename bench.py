@@ -172,7 +172,34 @@ def kernel_loop(be, name, reps):
         print(json.dumps({"kernel": "attend", "L": L, "avg_us": round(us, 2)}))
 
 
-def e2e_decode(be, prompt_count=2048, gen=256):
+def cpu_e2e(folder, prompt, gen=8, prime=64):
+    """The reference engine itself (oracle/_ref, AVX2+FMA build) on the same
+    checkpoint, on this host's cores: a bounded sample, the first `prime` ids of
+    the prompt then `gen` greedy steps, each phase timed by the reference."""
+    import ctypes
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as ol
+
+    if ol.ref("tuned") is None:
+        return None
+    lib = ctypes.CDLL(ol.REF_TUNED_PATH)
+    fn = lib.ref_engine_clock
+    fn.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                   ctypes.c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
+    cores = min(16, os.cpu_count() or 1)
+    ids = np.ascontiguousarray(prompt[:prime], dtype=np.int32)
+    prime_s, step_s = ctypes.c_double(), ctypes.c_double()
+    code = fn(folder.encode(), cores, 8, prime + gen + 16, ids.ctypes.data, ids.size, gen,
+              ctypes.byref(prime_s), ctypes.byref(step_s))
+    if code != 0:
+        return {"error": f"ref_engine_clock returned {code}"}
+    return {"decode_tok_s": round(gen / step_s.value, 2), "prefill_tok_s": round((prime - 1) / prime_s.value, 1),
+            "cores": cores, "kind": "reference",
+            "sample": f"reference engine (app_core.c, AVX2+FMA build), {prime}-id prompt then {gen} greedy "
+                      f"steps on the same checkpoint, {cores} threads"}
+
+
+def e2e_decode(be, prompt_count=2048, gen=256, cpu=True):
     """Synthetic Gemma-4-E2B-shaped decode (model/config.json dimensions, every
     plane int4 group 32, FP8 key/value cache): write the seeded checkpoint,
     prime a 2048-id seeded prompt, then 256 greedy steps."""
@@ -221,6 +248,8 @@ def e2e_decode(be, prompt_count=2048, gen=256):
         out["prefill_modes_agree"] = out["streams"][0] == out["streams"][1]
         out.pop("streams")
         out["guess"] = e2e_guess(be, folder, shape, prompt_count, gen)
+        if cpu:
+            out["cpu_baseline"] = cpu_e2e(folder, prompt)
     finally:
         import shutil
         shutil.rmtree(folder, ignore_errors=True)
@@ -652,7 +681,7 @@ def main():
                          "includes the chunk-merge launch"}
 
     kinds = kinds_leg(be)
-    e2e = None if args.no_e2e else e2e_decode(be)
+    e2e = None if args.no_e2e else e2e_decode(be, cpu=not args.no_cpu)
     cpu = None if args.no_cpu else cpu_baseline()
 
     line = {

@@ -189,6 +189,51 @@ int ref_engine_greedy(const char *folder, int thread_count, int cache_bits, int 
   return (int)code;
 }
 
+/* The reference engine's own timing of a bounded run: prime `prompt`, then
+ * `gen_count` greedy steps; the wall seconds of each phase (the CPU baseline of
+ * the end-to-end decode).  Returns 0 or the app_code that stopped it. */
+int ref_engine_clock(const char *folder, int thread_count, int cache_bits, int window_limit,
+                     const int32_t *prompt, int prompt_count, int gen_count, double *prime_s,
+                     double *step_s) {
+  app_setup setup = app_setup_plain();
+  app_model *model = NULL;
+  app_session *session = NULL;
+  app_code code;
+  struct timespec t0, t1, t2;
+  int32_t id;
+  setup.thread_count = thread_count;
+  setup.cache_bits = cache_bits;
+  setup.window_limit = window_limit;
+  code = model_load(folder, &setup, &model);
+  if (code != APP_OKAY) return (int)code;
+  code = session_open(model, &session);
+  if (code != APP_OKAY) {
+    model_free(model);
+    return (int)code;
+  }
+  clock_gettime(CLOCK_MONOTONIC, &t0);
+  code = session_prime(session, prompt, prompt_count);
+  clock_gettime(CLOCK_MONOTONIC, &t1);
+  id = prompt[prompt_count - 1];
+  for (int step = 0; code == APP_OKAY && step < gen_count; ++step) {
+    const float *logits = session_step(session, id);
+    int vocab = model_vocab_count(model), best = 0;
+    if (!logits) {
+      code = APP_FAIL_STATE;
+      break;
+    }
+    for (int v = 1; v < vocab; ++v)
+      if (logits[v] > logits[best]) best = v;
+    id = best;
+  }
+  clock_gettime(CLOCK_MONOTONIC, &t2);
+  *prime_s = (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+  *step_s = (double)(t2.tv_sec - t1.tv_sec) + 1e-9 * (double)(t2.tv_nsec - t1.tv_nsec);
+  session_close(session);
+  model_free(model);
+  return (int)code;
+}
+
 /* The same, but the step inputs are `forced` (not the picks): each step's
  * pick and margin against a given token sequence, so a stream that a random
  * model would collapse onto one id still walks many inputs. */
