@@ -193,12 +193,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_q4_kernel(GemmArgs g) {
 //
 // A workgroup owns a 256 x 256 tile of C; its eight waves (2 x 4) each hold a
 // 128 x 64 block as 8 x 4 v_mfma_f32_16x16x32_f16 accumulators.  K advances
-// 64 a step through three LDS stages that only the LDS DMA writes
-// (global_load_lds: no registers held for loads in flight, two steps ahead):
-//   * the step's 256 x 64 binary16 activations, 16-byte chunks of a row
-//     XOR-swizzled by the row's low three bits (no padding, no conflicts);
-//   * the 256 rows' 64 codes as they are packed (32 bytes a row), and
-//   * their two fp32 gains.
+// 64 a step through LDS stages that only the LDS DMA writes (global_load_lds:
+// no registers held for loads in flight):
+//   * three stages of the step's 256 x 64 binary16 activations (two steps
+//     ahead), 16-byte chunks of a row XOR-swizzled by the row's low three
+//     bits (no padding, no conflicts);
+//   * four stages (three steps ahead) of the 256 rows' 64 codes as they are
+//     packed (32 bytes a row) and their two fp32 gains.
 // A wave turns its 64 columns' codes into binary16 operands in registers as
 // it consumes them: one v_and_or_b32 puts a nibble in the mantissa of 1024.0
 // (ulp 1: 1024 + c) or, four bits up, of 1024.0 with ulp 16 (1024 + 16 c), so
@@ -207,16 +208,26 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_q4_kernel(GemmArgs g) {
 // gives (c - bias) gain or 16 (c - bias) gain, rounded once.  The activation
 // copy holds x / 16 where the weight holds 16 (c - bias) gain, and each eight
 // consecutive k appear in the order 0 4 1 5 2 6 3 7 the pairs come in.
-// Every wave's step is its activation reads for both 32-k halves, the eight
-// weight operands, then 64 products.
+// A wave's step runs 64 products in eight blocks of eight, reading the next
+// block's activations and decoding one of the next step's eight weight
+// operands beside each block.  The weights are the products' first operand,
+// so each accumulator holds C transposed: four consecutive columns of one row,
+// stored as one vector.
+//
+// Measured on this tile (M = 2048, 8192 x 2048): the same loop with only its
+// products (no decode, no activation reads, no DMA) takes ~70% of the whole
+// kernel, and the final 32 MB of output drains in ~15 us with every CU
+// finishing its one tile at once.
 constexpr int kBigM = 256;
 constexpr int kBigN = 256;
 constexpr int kBigK = 64;
-constexpr int kBigStages = 3;
+constexpr int kBigStages = 3;                 // activation stages (DMA two steps ahead)
+constexpr int kBigCodeStages = 4;             // code stages (decoded a step early)
 constexpr int kBigA = kBigM * kBigK;          // halves of a stage's activations
 constexpr int kBigB = kBigN * kBigK / 2;      // bytes of a stage's codes
 constexpr int kBigG = kBigN * kBigK / 32;     // floats of a stage's gains
-constexpr int kBigStage = kBigA * 2 + kBigB + kBigG * 4;
+constexpr int kBigCodeStage = kBigB + kBigG * 4;
+constexpr int kBigLds = kBigStages * kBigA * 2 + kBigCodeStages * kBigCodeStage;
 
 // a16 = binary16(a), saturating at +-65504, in the large-tile form's operand
 // order: within each eight k, positions 0 4 1 5 2 6 3 7, and k = 1, 5, 3, 7
@@ -336,18 +347,24 @@ __global__ __launch_bounds__(512) void gemm_q4_big_kernel(GemmBigArgs g) {
   const float *s_src = g.gains + (size_t)br * g.gain_stride;
   const int s_first = k_first / 32;
   const int s_grp = lane & 1;
-  auto issue = [&](int step) {
-    uint8_t *st = lds_b + (step % kBigStages) * kBigStage;
+  // Activation stages first, then the code stages.
+  auto a_stage = [&](int step) { return lds_b + (step % kBigStages) * (kBigA * 2); };
+  auto b_stage = [&](int step) { return lds_b + kBigStages * kBigA * 2 + (step % kBigCodeStages) * kBigCodeStage; };
+  auto issue_a = [&](int step) {
+    uint8_t *st = a_stage(step);
     const int k0 = step * kBigK;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       __builtin_amdgcn_global_load_lds((global_void_t *)(a_src[i] + k0),
                                        (lds_void_t *)(st + (4 * wave + i) * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((global_void_t *)(b_src + k0 / 2),
-                                     (lds_void_t *)(st + kBigA * 2 + wave * 1024), 16, 0, 0);
+  };
+  auto issue_b = [&](int step) {
+    uint8_t *st = b_stage(step);
+    const int k0 = step * kBigK;
+    __builtin_amdgcn_global_load_lds((global_void_t *)(b_src + k0 / 2), (lds_void_t *)(st + wave * 1024), 16, 0, 0);
     __builtin_amdgcn_global_load_lds(
         (global_void_t *)(s_src + (((unsigned)(s_first + k0 / 32 + s_grp)) >> g.group_shift)),
-        (lds_void_t *)(st + kBigA * 2 + kBigB + wave * 256), 4, 0, 0);
+        (lds_void_t *)(st + kBigB + wave * 256), 4, 0, 0);
   };
 
   float4_t acc[8][4];
@@ -363,92 +380,160 @@ __global__ __launch_bounds__(512) void gemm_q4_big_kernel(GemmBigArgs g) {
   const int gq = lane >> 4;     // lane group: k 16 gq .. 16 gq + 15 of a step
   const int n = lane & 15;
 
-  issue(0);
-  if (steps > 1) issue(1);
-  for (int s = 0; s < steps; ++s) {
-    // this wave's six loads of step s are in LDS (those of s + 1 may not be)
-    if (s + 1 < steps)
-      __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
-    else
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    // ... and every wave's, and every wave has consumed the stage the next
-    // issue overwrites (its reads fed the previous step's products); no
-    // fence, which would also wait for the loads two steps ahead
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    if (s + 2 < steps) issue(s + 2);
-    const uint8_t *st = lds_b + (s % kBigStages) * kBigStage;
-    const _Float16 *as = reinterpret_cast<const _Float16 *>(st);
-    const uint8_t *bs = st + kBigA * 2;
-    const float *gs = reinterpret_cast<const float *>(st + kBigA * 2 + kBigB);
-    uint2_t braw[4];
-    half2_t bscale[4];
+  // The codes of a step are read and decoded into binary16 operands a step
+  // ahead, eight fragments a step: one v_and_or_b32 puts a nibble pair in the
+  // mantissas of 1024.0 (ulp 1, or four bits up ulp 16); subtracting
+  // 1024 + bias (or 1024 + 16 bias) is exact; one multiply by the gain rounds
+  // once.  k-half q of lane group gq is k 16 gq + 8 q .. + 7: its activations
+  // are logical chunk 2 gq + q of the row, its codes dword q of the eight bytes.
+  auto read_codes = [&](const uint8_t *st, uint2_t (&braw)[4], half2_t (&bscale)[4]) {
+    const float *gs = reinterpret_cast<const float *>(st + kBigB);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = wn * 64 + 16 * j + n;
       const int half = (gq >> 1) ^ ((n >> 3) & 1);
-      braw[j] = *reinterpret_cast<const uint2_t *>(bs + row * 32 + 16 * half + 8 * (gq & 1));
+      braw[j] = *reinterpret_cast<const uint2_t *>(st + row * 32 + 16 * half + 8 * (gq & 1));
       const _Float16 sh = (_Float16)gs[row * 2 + (gq >> 1)];
       bscale[j] = half2_t{sh, sh};
     }
-    // k-half q of lane group gq is k 16 gq + 8 q .. + 7: its activations are
-    // logical chunk 2 gq + q of the row, its codes dword q of the eight bytes
-    half8_t af[2][8], bf[2][4];
+  };
+  auto read_rows = [&](const uint8_t *st, int i, half8_t (&a)[2]) {
+    const _Float16 *as = reinterpret_cast<const _Float16 *>(st);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int r = wm * 128 + 16 * i + n;
+      const int p = (2 * gq + q) ^ (r & 7);
+      a[q] = *reinterpret_cast<const half8_t *>(as + r * kBigK + 8 * p);
+    }
+  };
+  auto decode = [&](uint32_t d, half2_t scale) {
+    const uint32_t e = d >> 8;
+    const half2_t p0 = (as_half2(and_or_b32(d, 0x000F000Fu, exp10)) - bias_lo) * scale;
+    const half2_t p1 = (as_half2(and_or_b32(d, 0x00F000F0u, exp10)) - bias_hi) * scale;
+    const half2_t p2 = (as_half2(and_or_b32(e, 0x000F000Fu, exp10)) - bias_lo) * scale;
+    const half2_t p3 = (as_half2(and_or_b32(e, 0x00F000F0u, exp10)) - bias_hi) * scale;
+    return __builtin_bit_cast(half8_t, uint4_t{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                                               __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)});
+  };
+  // Waits until this wave's loads but the last `after` are in (vmcnt retires
+  // them in order) and its LDS reads have landed (the stages they read are
+  // refilled after the next barrier), then meets every wave at a bare barrier
+  // (a fence would also wait for the loads still in flight for later steps).
+  auto wait_meet = [&](int after) {
+    if (after >= 12)
+      __builtin_amdgcn_s_waitcnt(0x007C);  // vmcnt(12) lgkmcnt(0)
+    else if (after >= 6)
+      __builtin_amdgcn_s_waitcnt(0x0076);  // vmcnt(6) lgkmcnt(0)
+    else if (after >= 4)
+      __builtin_amdgcn_s_waitcnt(0x0074);  // vmcnt(4) lgkmcnt(0)
+    else
+      __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // Software pipeline.  Iteration s issues the activations of step s + 2 and
+  // the codes of step s + 3, and runs step s's 64 products in eight blocks of
+  // eight; between the blocks it reads step s's next row tile of activations
+  // (one block ahead) and decodes one of step s + 1's eight code fragments, so
+  // the decoding runs beside the matrix cores instead of between steps.  A
+  // wave's loads retire in issue order: before iteration s they are ...,
+  // [A s, B s+1], [A s+1, B s+2] (4 + 2 each), so A s and B s+1 are in when
+  // all but the last 4 [s+1 < steps] + 2 [s+2 < steps] are.
+  issue_b(0);
+  issue_a(0);
+  if (steps > 1) issue_b(1);
+  if (steps > 1) issue_a(1);
+  if (steps > 2) issue_b(2);
+  wait_meet((steps > 1 ? 10 : 0) + (steps > 2 ? 2 : 0) >= 12 ? 12 : 0);
+  half8_t bf[2][4];
+  {
+    uint2_t braw[4];
+    half2_t bscale[4];
+    read_codes(b_stage(0), braw, bscale);
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int r = wm * 128 + 16 * i + n;
-        const int p = (2 * gq + q) ^ (r & 7);
-        af[q][i] = *reinterpret_cast<const half8_t *>(as + r * kBigK + 8 * p);
-      }
+      for (int j = 0; j < 4; ++j) bf[q][j] = decode(braw[j][q], bscale[j]);
+  }
+  for (int s = 0; s < steps; ++s) {
+    wait_meet(4 * (s + 1 < steps) + 2 * (s + 2 < steps));
+    if (s + 2 < steps) issue_a(s + 2);
+    if (s + 3 < steps) issue_b(s + 3);
+    const bool more = s + 1 < steps;
+    const uint8_t *ast = a_stage(s);
+    half8_t bn[2][4];
+    uint2_t braw[4];
+    half2_t bscale[4];
+    read_codes(b_stage(more ? s + 1 : s), braw, bscale);
+    half8_t a_cur[2], a_next[2];
+    read_rows(ast, 0, a_cur);
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
+    for (int i = 0; i < 8; ++i) {
+      if (i + 1 < 8) read_rows(ast, i + 1, a_next);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t d = braw[j][q];
-        const uint32_t e = d >> 8;
-        const half2_t p0 = (as_half2(and_or_b32(d, 0x000F000Fu, exp10)) - bias_lo) * bscale[j];
-        const half2_t p1 = (as_half2(and_or_b32(d, 0x00F000F0u, exp10)) - bias_hi) * bscale[j];
-        const half2_t p2 = (as_half2(and_or_b32(e, 0x000F000Fu, exp10)) - bias_lo) * bscale[j];
-        const half2_t p3 = (as_half2(and_or_b32(e, 0x00F000F0u, exp10)) - bias_hi) * bscale[j];
-        bf[q][j] = __builtin_bit_cast(
-            half8_t, uint4_t{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
-                             __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)});
-      }
-    // keep the reads and the decoding ahead of the products
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int q = 0; q < 2; ++q)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[q][i], bf[q][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[q][j], a_cur[q], acc[i][j], 0, 0, 0);
+      bn[i >> 2][i & 3] = decode(braw[i & 3][i >> 2], bscale[i & 3]);
+      __builtin_amdgcn_sched_barrier(0);
+      a_cur[0] = a_next[0];
+      a_cur[1] = a_next[1];
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bf[q][j] = bn[q][j];
   }
 
-  // D layout of a 16x16 tile: lane l holds rows 4*(l/16) + r, column l % 16.
+  // The products take the codes as the first operand, so a 16x16 tile of D is
+  // C transposed: lane l holds row l % 16 of its row tile and the four
+  // consecutive columns 4 (l / 16) .. + 3, stored as one 8- or 16-byte vector.
   float *part = reinterpret_cast<float *>(g.out) + blockIdx.z * g.slice_floats;
+  const bool vec_ok = g.slice_floats ? (g.N % 4 == 0)
+                                     : (g.out_stride % 4 == 0 &&
+                                        ((uintptr_t)g.out & (C_BF16 ? 7u : 15u)) == 0);
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 8; ++i) {
+    const int m = m0 + wm * 128 + i * 16 + n;
+    if (m >= g.M) continue;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int nn = n0 + wn * 64 + j * 16 + n;
-      if (nn >= g.N) continue;
+      const int nb = n0 + wn * 64 + j * 16 + 4 * gq;
+      float4_t v = acc[i][j];
+      if (!g.slice_floats && !C_BF16 && g.close.gains) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (nb + r < g.N) v[r] = close_value(g.close, nb + r, v[r]);
+      }
+      if (vec_ok && nb + 3 < g.N) {
+        if (g.slice_floats) {
+          *reinterpret_cast<float4_t *>(part + (size_t)m * g.N + nb) = v;
+        } else if (C_BF16) {
+          const uint32_t lo = (uint32_t)float_to_bf16(v[0]) | ((uint32_t)float_to_bf16(v[1]) << 16);
+          const uint32_t hi = (uint32_t)float_to_bf16(v[2]) | ((uint32_t)float_to_bf16(v[3]) << 16);
+          *reinterpret_cast<uint2_t *>(reinterpret_cast<uint16_t *>(g.out) + (size_t)m * g.out_stride + nb) =
+              uint2_t{lo, hi};
+        } else {
+          *reinterpret_cast<float4_t *>(reinterpret_cast<float *>(g.out) + (size_t)m * g.out_stride + nb) = v;
+        }
+        continue;
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 128 + i * 16 + 4 * gq + r;
-        if (m >= g.M) continue;
+        const int nn = nb + r;
+        if (nn >= g.N) continue;
         if (g.slice_floats)
-          part[(size_t)m * g.N + nn] = acc[i][j][r];
+          part[(size_t)m * g.N + nn] = v[r];
         else if (C_BF16)
-          reinterpret_cast<uint16_t *>(g.out)[(size_t)m * g.out_stride + nn] = float_to_bf16(acc[i][j][r]);
+          reinterpret_cast<uint16_t *>(g.out)[(size_t)m * g.out_stride + nn] = float_to_bf16(v[r]);
         else
-          reinterpret_cast<float *>(g.out)[(size_t)m * g.out_stride + nn] =
-              g.close.gains ? close_value(g.close, nn, acc[i][j][r]) : acc[i][j][r];
+          reinterpret_cast<float *>(g.out)[(size_t)m * g.out_stride + nn] = v[r];
       }
     }
+  }
 }
 
 // C = the K slices' partials added in slice order (four columns a thread).
@@ -539,7 +624,7 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
     b.k_steps = K / kBigK / slices;
     b.slice_floats = slices > 1 ? (size_t)M * N : 0;
     b.close = cl;
-    const size_t lds = (size_t)kBigStages * kBigStage;
+    const size_t lds = (size_t)kBigLds;
     static int granted[2];
     const void *fn = out_bf16 ? reinterpret_cast<const void *>(&gemm_q4_big_kernel<true>)
                               : reinterpret_cast<const void *>(&gemm_q4_big_kernel<false>);
