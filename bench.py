@@ -50,7 +50,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decode leg")
-    ap.add_argument("--kernel", choices=["gemv", "gemv8", "gemm", "attend", "copy", "head2", "real", "calib"],
+    ap.add_argument("--kernel", choices=["gemv", "gemv8", "gemm", "attend", "copy", "head2", "real", "calib",
+                                         "readfloor"],
                     help="run one kernel's workload alone in a loop (for rocprofv3) and exit")
     return ap.parse_args()
 
@@ -60,8 +61,9 @@ def kernel_loop(be, name, reps):
     8192x2048, rotated copies), the M=8 GEMV, the M=2048 prefill GEMM, the
     L=16384 attention, a 256 MiB device copy that calibrates FETCH_SIZE and
     WRITE_SIZE against a known byte count, the 2-bit 262144x1536 head and the
-    bf16 8960x1536 real plane at M=1 (rotated copies), or the calibrated
-    prefill (M=2048, 8192x2048 4-bit, one gain a row)."""
+    bf16 8960x1536 real plane at M=1 (rotated copies), the calibrated
+    prefill (M=2048, 8192x2048 4-bit, one gain a row), or the read floor (the
+    M=1 GEMV's byte count read once, rotated buffers)."""
     import ctypes
     from igllm_amd.backend import synth_projection
 
@@ -77,6 +79,21 @@ def kernel_loop(be, name, reps):
         be.sync()
         print(json.dumps({"kernel": "copy", "bytes_each": nbytes, "reps": reps}))
         del lib
+        return
+    if name == "readfloor":
+        N, K = SHAPES[0]
+        nbytes = gemv_bytes(N, K, 1)
+        bufs = [be.alloc(nbytes) for _ in range(COPIES)]
+        for i in range(20):
+            be.read_floor_dev(bufs[i % COPIES], nbytes)
+        be.sync()
+        be.mark()
+        for i in range(reps):
+            be.read_floor_dev(bufs[i % COPIES], nbytes)
+        be.mark()
+        us = be.marks_ms() * 1e3 / reps
+        print(json.dumps({"kernel": "read_floor", "bytes": nbytes, "avg_us": round(us, 3),
+                          "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}))
         return
     if name in ("head2", "real"):
         key = "u2_head_262144x1536" if name == "head2" else "bf16_ple_model_8960x1536"
@@ -571,6 +588,51 @@ def main():
     gemv_algo = gemv_bytes(N, K, 1)
     gemv_gbps = gemv_algo / (gemv_us * 1e-6) / 1e9
 
+    # ---- the read floor: a kernel that only reads the same bytes once (16-byte
+    # loads, two a thread), over as many rotated buffers, launched the same way.
+    floor_bufs = [be.alloc(gemv_algo) for _ in range(COPIES)]
+    for i in range(20):
+        be.read_floor_dev(floor_bufs[i % COPIES], gemv_algo)
+    be.sync()
+    be.mark()
+    for i in range(launches):
+        be.read_floor_dev(floor_bufs[i % COPIES], gemv_algo)
+    be.mark()
+    floor_us = be.marks_ms() * 1e3 / launches
+
+    # Each launch above is enqueued by one ctypes call (~4 us of host time), so
+    # both rates are partly the host's.  The same launches recorded once and
+    # replayed (igl_record_*: no host launch each) time the kernels themselves.
+    def replayed(enqueue, count=2 * COPIES):
+        be.record_begin()
+        for i in range(count):
+            enqueue(i)
+        handle = be.record_end()
+        try:
+            be.replay_run(handle)
+            be.sync()
+            be.mark()
+            be.replay_run(handle)
+            be.mark()
+            return be.marks_ms() * 1e3 / count
+        finally:
+            be.replay_free(handle)
+
+    gemv_replayed_us = replayed(lambda i: be.gemv_dev(r.planes[i % COPIES], acts[(N, K, 1)], K, 1,
+                                                      outs[(N, K, 1)], N))
+    floor_replayed_us = replayed(lambda i: be.read_floor_dev(floor_bufs[i % COPIES], gemv_algo))
+    for b in floor_bufs:
+        b.free()
+    read_floor = {"enqueued_us": round(floor_us, 3), "replayed_us": round(floor_replayed_us, 3),
+                  "replayed_GBps": round(gemv_algo / (floor_replayed_us * 1e-6) / 1e9, 1),
+                  "replayed_frac_of_peak": round(gemv_algo / (floor_replayed_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                  "gemv_replayed_us": round(gemv_replayed_us, 3),
+                  "gemv_replayed_frac_of_peak": round(gemv_algo / (gemv_replayed_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                  "gemv_frac_of_floor": round(floor_replayed_us / gemv_replayed_us, 4),
+                  "note": "read_floor_kernel: the same byte count read once and nothing else (16-byte "
+                          f"loads, two a thread), rotated over {COPIES} buffers; 'replayed' = "
+                          f"{2 * COPIES} launches recorded once and replayed, no host launch each"}
+
     # ---- per-config GEMV rates (same rotation), for the record.
     sweep = {}
     for (N, K) in SHAPES:
@@ -702,11 +764,12 @@ def main():
                                "M in {1,2,4,8}, fp32 activations, weights rotated over "
                                f"{COPIES} copies per shape",
                    "step_bytes": step_bytes},
-        "roofline": {"bound": "hbm", "kernel": "gemv_q4_dot_kernel<1,4,1,1,true,1> 8192x2048 M=1",
+        "roofline": {"bound": "hbm", "kernel": "gemv_q4_dot_kernel<1, 2, 1, 1> 8192x2048 M=1",
                      "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": GEMV_M1_TRAFFIC_BYTES,
-                     "algorithmic_bytes": gemv_algo, "avg_launch_us": round(gemv_us, 3)},
+                     "algorithmic_bytes": gemv_algo, "avg_launch_us": round(gemv_us, 3),
+                     "read_floor": read_floor},
         "cpu_baseline": cpu,
         "gemv_sweep": sweep,
         "prefill_gemm": prefill,

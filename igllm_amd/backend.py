@@ -279,6 +279,29 @@ class Backend:
         self._check(native.IGL_OKAY, "marks_ms")
         return ms
 
+    def record_begin(self):
+        """Starts recording the device entries called next (igl_record_begin)."""
+        self._check(self.lib.igl_record_begin(ctypes.byref(self.desk)), "record_begin")
+
+    def record_end(self) -> int:
+        """Ends the recording; returns the replay handle (igl_record_end)."""
+        handle = ctypes.c_void_p()
+        code = self.lib.igl_record_end(ctypes.byref(self.desk), ctypes.byref(handle))
+        if code != native.IGL_OKAY:
+            raise BackendError(f"record_end: {self.lib.igl_code_text(code).decode()} ({code})")
+        return handle.value
+
+    def replay_run(self, handle: int):
+        self._check(self.lib.igl_replay_run(ctypes.byref(self.desk), handle), "replay_run")
+
+    def replay_free(self, handle: int):
+        self.lib.igl_replay_free(ctypes.byref(self.desk), handle)
+
+    def read_floor_dev(self, src: DevBuf, nbytes: int):
+        """Reads nbytes of a device buffer once and keeps nothing (the HBM read
+        floor the GEMV's rate is judged against)."""
+        self._check(self.lib.igl_read_floor_dev(ctypes.byref(self.desk), src.ptr, nbytes), "read_floor_dev")
+
 
 # -- synthetic inputs -----------------------------------------------------------
 

@@ -66,10 +66,28 @@ struct igl_desk_state {
   /* the GEMM's binary16 copy of its activations */
   float *gemm_dev;
   size_t gemm_floats;
+  /* a recording in progress on the stream, and replays not yet freed (both
+   * freeze the scratch above: a replay keeps the addresses it recorded) */
+  int recording;
+  int record_error;  /* the first failure while recording (error_take keeps it) */
+  int replays_live;
+};
+
+struct igl_replay {
+  hipGraphExec_t exec;
+  igl_desk_state *owner;
 };
 
 static void desk_fail(igl_desk_state *st, int code) {
   if (st && st->error == IGL_OKAY) st->error = code;
+  if (st && st->recording && st->record_error == IGL_OKAY) st->record_error = code;
+}
+
+/* Entries that touch host memory, synchronize or allocate cannot be recorded. */
+static int refuse_recording(igl_desk_state *st) {
+  if (!st->recording) return 0;
+  desk_fail(st, IGL_FAIL_STATE);
+  return 1;
 }
 
 static int hip_check(igl_desk_state *st, hipError_t e) {
@@ -110,6 +128,10 @@ int igl_desk_error_take(igl_desk *desk) {
 static int grow_dev(igl_desk_state *st, float **buf, size_t *have, size_t floats) {
   void *fresh = NULL;
   if (*have >= floats) return IGL_OKAY;
+  if (st->recording || st->replays_live) {
+    desk_fail(st, IGL_FAIL_STATE);
+    return IGL_FAIL_STATE;
+  }
   if (hipMalloc(&fresh, floats * sizeof(float)) != hipSuccess) {
     desk_fail(st, IGL_FAIL_MEMORY);
     return IGL_FAIL_MEMORY;
@@ -123,6 +145,10 @@ static int grow_dev(igl_desk_state *st, float **buf, size_t *have, size_t floats
 static int grow_out(igl_desk_state *st, size_t floats) {
   void *dev = NULL, *pin = NULL;
   if (st->out_floats >= floats) return IGL_OKAY;
+  if (st->recording || st->replays_live) {
+    desk_fail(st, IGL_FAIL_STATE);
+    return IGL_FAIL_STATE;
+  }
   if (hipMalloc(&dev, floats * sizeof(float)) != hipSuccess) goto fail;
   if (hipHostMalloc(&pin, floats * sizeof(float), hipHostMallocDefault) != hipSuccess) goto fail;
   if (st->out_dev) (void)hipFree(st->out_dev);
@@ -633,6 +659,17 @@ int igl_soft_max_dev(igl_desk *desk, float *v_dev, int n, int rows, int stride) 
   return hip_check(st, igl_launch_soft_max(v_dev, n, rows, stride, st->stream));
 }
 
+int igl_read_floor_dev(igl_desk *desk, const void *src_dev, size_t bytes) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  if (!src_dev || bytes < 16 || bytes % 16 || ((uintptr_t)src_dev & 15u) || !st->act_dev) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return IGL_FAIL_ARGUMENT;
+  }
+  /* the sink: a word of the table's activation staging, scratch between calls */
+  return hip_check(st, igl_launch_read_floor(src_dev, bytes, (uint32_t *)st->act_dev, st->stream));
+}
+
 int igl_gelu_gate_dev(igl_desk *desk, float *gate_dev, const float *rise_dev, int n) {
   igl_desk_state *st = desk ? desk->state : NULL;
   if (!st) return IGL_FAIL_STATE;
@@ -660,6 +697,7 @@ static void table_mat_mat(igl_desk *desk, const igl_plane *sheet, const float *a
                           int act_stride, int lane_count, float *out_data, int out_stride) {
   igl_desk_state *st = desk->state;
   int done = 0;
+  if (refuse_recording(st)) return;
   if (!sheet || !sheet->device || !act_data || !out_data || lane_count < 1) {
     desk_fail(st, IGL_FAIL_ARGUMENT);
     return;
@@ -696,6 +734,7 @@ static void table_mat_vec(igl_desk *desk, const igl_plane *sheet, const float *a
 
 /* The elementwise entries stage their vectors through the device. */
 static float *elem_stage(igl_desk_state *st, size_t floats) {
+  if (refuse_recording(st)) return NULL;
   if (grow_dev(st, &st->elem_dev, &st->elem_floats, floats) != IGL_OKAY) return NULL;
   return st->elem_dev;
 }
@@ -851,6 +890,7 @@ void igl_dev_free(igl_desk *desk, void *ptr) {
 int igl_copy_to_dev(igl_desk *desk, void *dst_dev, const void *src_host, size_t bytes) {
   igl_desk_state *st = desk ? desk->state : NULL;
   if (!st) return IGL_FAIL_STATE;
+  if (refuse_recording(st)) return IGL_FAIL_STATE;
   if (hip_check(st, hipMemcpyAsync(dst_dev, src_host, bytes, hipMemcpyHostToDevice, st->stream)) != IGL_OKAY)
     return IGL_FAIL_DEVICE;
   return hip_check(st, hipStreamSynchronize(st->stream));
@@ -859,6 +899,7 @@ int igl_copy_to_dev(igl_desk *desk, void *dst_dev, const void *src_host, size_t 
 int igl_copy_to_host(igl_desk *desk, void *dst_host, const void *src_dev, size_t bytes) {
   igl_desk_state *st = desk ? desk->state : NULL;
   if (!st) return IGL_FAIL_STATE;
+  if (refuse_recording(st)) return IGL_FAIL_STATE;
   if (hip_check(st, hipMemcpyAsync(dst_host, src_dev, bytes, hipMemcpyDeviceToHost, st->stream)) != IGL_OKAY)
     return IGL_FAIL_DEVICE;
   return hip_check(st, hipStreamSynchronize(st->stream));
@@ -867,18 +908,22 @@ int igl_copy_to_host(igl_desk *desk, void *dst_host, const void *src_dev, size_t
 int igl_fill_dev(igl_desk *desk, void *dst_dev, int byte_value, size_t bytes) {
   igl_desk_state *st = desk ? desk->state : NULL;
   if (!st) return IGL_FAIL_STATE;
+  /* a memset node is not recorded: replays after the first have gone wrong */
+  if (refuse_recording(st)) return IGL_FAIL_STATE;
   return hip_check(st, hipMemsetAsync(dst_dev, byte_value, bytes, st->stream));
 }
 
 int igl_sync(igl_desk *desk) {
   igl_desk_state *st = desk ? desk->state : NULL;
   if (!st) return IGL_FAIL_STATE;
+  if (refuse_recording(st)) return IGL_FAIL_STATE;
   return hip_check(st, hipStreamSynchronize(st->stream));
 }
 
 int igl_mark(igl_desk *desk) {
   igl_desk_state *st = desk ? desk->state : NULL;
   if (!st) return IGL_FAIL_STATE;
+  if (refuse_recording(st)) return IGL_FAIL_STATE;
   st->mark_turn ^= 1;
   st->marks_made += 1;
   return hip_check(st, hipEventRecord(st->mark[st->mark_turn], st->stream));
@@ -887,9 +932,86 @@ int igl_mark(igl_desk *desk) {
 float igl_marks_ms(igl_desk *desk) {
   igl_desk_state *st = desk ? desk->state : NULL;
   float ms = -1.0f;
-  if (!st || st->marks_made < 2) return -1.0f;
+  if (!st || st->marks_made < 2 || refuse_recording(st)) return -1.0f;
   if (hip_check(st, hipEventSynchronize(st->mark[st->mark_turn])) != IGL_OKAY) return -1.0f;
   if (hip_check(st, hipEventElapsedTime(&ms, st->mark[st->mark_turn ^ 1], st->mark[st->mark_turn])) != IGL_OKAY)
     return -1.0f;
   return ms;
+}
+
+/* ---- recording and replay (HIP graphs) ----------------------------------- */
+
+int igl_record_begin(igl_desk *desk) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  if (st->recording) {
+    desk_fail(st, IGL_FAIL_STATE);
+    return IGL_FAIL_STATE;
+  }
+  if (hip_check(st, hipStreamBeginCapture(st->stream, hipStreamCaptureModeThreadLocal)) != IGL_OKAY)
+    return IGL_FAIL_DEVICE;
+  st->recording = 1;
+  st->record_error = IGL_OKAY;
+  return IGL_OKAY;
+}
+
+int igl_record_end(igl_desk *desk, igl_replay **replay_out) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  hipGraph_t graph = NULL;
+  hipGraphExec_t exec = NULL;
+  igl_replay *replay;
+  hipError_t e;
+  int code;
+  if (replay_out) *replay_out = NULL;
+  if (!st) return IGL_FAIL_STATE;
+  if (!st->recording) {
+    desk_fail(st, IGL_FAIL_STATE);
+    return IGL_FAIL_STATE;
+  }
+  st->recording = 0;
+  e = hipStreamEndCapture(st->stream, &graph);
+  /* an entry refused or failed while recording: no replay, the code returned */
+  code = st->record_error != IGL_OKAY ? st->record_error : st->error;
+  st->record_error = IGL_OKAY;
+  st->error = IGL_OKAY;
+  if (code == IGL_OKAY && e != hipSuccess) code = IGL_FAIL_DEVICE;
+  if (code == IGL_OKAY && !replay_out) code = IGL_FAIL_ARGUMENT;
+  if (code == IGL_OKAY && hipGraphInstantiate(&exec, graph, NULL, NULL, 0) != hipSuccess)
+    code = IGL_FAIL_DEVICE;
+  if (graph) (void)hipGraphDestroy(graph);
+  if (code != IGL_OKAY) {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    return code;
+  }
+  replay = (igl_replay *)malloc(sizeof(*replay));
+  if (!replay) {
+    (void)hipGraphExecDestroy(exec);
+    return IGL_FAIL_MEMORY;
+  }
+  replay->exec = exec;
+  replay->owner = st;
+  st->replays_live += 1;
+  *replay_out = replay;
+  return IGL_OKAY;
+}
+
+int igl_replay_run(igl_desk *desk, igl_replay *replay) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  if (!st) return IGL_FAIL_STATE;
+  if (!replay || replay->owner != st) {
+    desk_fail(st, IGL_FAIL_ARGUMENT);
+    return IGL_FAIL_ARGUMENT;
+  }
+  if (refuse_recording(st)) return IGL_FAIL_STATE;
+  return hip_check(st, hipGraphLaunch(replay->exec, st->stream));
+}
+
+void igl_replay_free(igl_desk *desk, igl_replay *replay) {
+  (void)desk;
+  if (!replay) return;
+  /* the replay's own desk (open until its replays are freed) */
+  (void)hipStreamSynchronize(replay->owner->stream);
+  replay->owner->replays_live -= 1;
+  (void)hipGraphExecDestroy(replay->exec);
+  free(replay);
 }

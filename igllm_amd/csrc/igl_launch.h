@@ -177,6 +177,9 @@ hipError_t igl_launch_grid_close(const float *a, const float *b, const float *ls
                                  const float *gains, float step, float leave, int N, int lanes,
                                  float *out, int out_stride, hipStream_t stream);
 hipError_t igl_launch_fill(float *dst, size_t n, float value, hipStream_t stream);
+/* Reads `bytes` (a multiple of 16) of src once and keeps nothing (sink: one
+ * word, written only on an improbable fold). */
+hipError_t igl_launch_read_floor(const void *src, size_t bytes, uint32_t *sink, hipStream_t stream);
 hipError_t igl_launch_norm_rms(const float *in, const float *gain, int n, int rows, int stride,
                                float eps, float *out, hipStream_t stream);
 hipError_t igl_launch_soft_max(float *v, int n, int rows, int stride, hipStream_t stream);

@@ -153,6 +153,11 @@ SIGNATURES = {
     "igl_sync": (_I, [ctypes.POINTER(Desk)]),
     "igl_mark": (_I, [ctypes.POINTER(Desk)]),
     "igl_marks_ms": (_F, [ctypes.POINTER(Desk)]),
+    "igl_read_floor_dev": (_I, [ctypes.POINTER(Desk), _P, _Z]),
+    "igl_record_begin": (_I, [ctypes.POINTER(Desk)]),
+    "igl_record_end": (_I, [ctypes.POINTER(Desk), ctypes.POINTER(_P)]),
+    "igl_replay_run": (_I, [ctypes.POINTER(Desk), _P]),
+    "igl_replay_free": (None, [ctypes.POINTER(Desk), _P]),
     "igl_rng_seed": (None, [ctypes.POINTER(Rng), ctypes.c_uint64]),
     "igl_rng_next": (ctypes.c_uint64, [ctypes.POINTER(Rng)]),
     "igl_rng_normal": (None, [ctypes.POINTER(Rng), _P, _Z, _F, _F]),

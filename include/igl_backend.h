@@ -220,6 +220,33 @@ int   igl_sync(igl_desk *desk);
  * milliseconds between the last two marks after they complete. */
 int   igl_mark(igl_desk *desk);
 float igl_marks_ms(igl_desk *desk);
+/* No counterpart in the reference (a calibration for the benchmark): reads
+ * `bytes` (a multiple of 16, 16-byte aligned) of src_dev once with 16-byte
+ * loads, two a thread, and keeps nothing.  Its time is the floor of any kernel
+ * that must read those bytes once, the yardstick of the GEMV's rate. */
+int   igl_read_floor_dev(igl_desk *desk, const void *src_dev, size_t bytes);
+
+/* ---- recording and replay (HIP graphs) ------------------------------------ */
+
+/* No counterpart in the reference; for callers that replay a fixed sequence of
+ * device entries (a decode step, a benchmark loop) without paying a host launch
+ * for each.  igl_record_begin starts recording the desk's stream: the device
+ * entries called until igl_record_end (the *_dev products and lifts,
+ * attention, the elementwise *_dev entries) are recorded, not run, and
+ * igl_record_end returns them as one replay; igl_replay_run enqueues it.
+ * While recording, every entry that touches host memory, synchronizes,
+ * allocates or fills (the table entries, copies, igl_sync, marks,
+ * igl_fill_dev) is refused with IGL_FAIL_STATE, and igl_record_end then
+ * returns that code and no replay.  A replay keeps the addresses it recorded:
+ * the buffers and planes it names must outlive it, and while any replay of a
+ * desk is alive the desk's scratch cannot grow (a call that would need more
+ * room fails with IGL_FAIL_STATE), so call each entry once before recording.
+ * Free every replay before igl_back_close. */
+typedef struct igl_replay igl_replay;
+int  igl_record_begin(igl_desk *desk);
+int  igl_record_end(igl_desk *desk, igl_replay **replay_out);
+int  igl_replay_run(igl_desk *desk, igl_replay *replay);
+void igl_replay_free(igl_desk *desk, igl_replay *replay);
 
 /* ---- synthetic inputs (seeded, shared by the CPU and GPU hosts) ----------- */
 
