@@ -34,9 +34,9 @@ LANES = [1, 2, 4, 8]
 COPIES = 48                     # 48 x 10.5 MB per shape: past the 256 MiB MALL
 # HBM bytes per dispatch of the decode GEMV (M=1, 8192x2048), from two rocprofv3
 # --pmc runs of `bench.py --kernel gemv` (profiles/gemv_q4_m1_8192x2048.md):
-# FETCH_SIZE 5182.1 KiB x 2.0 + WRITE_SIZE 32.0 KiB x 1.0, the factors a 256 MiB
+# FETCH_SIZE 5179.6 KiB x 2.0 + WRITE_SIZE 32.0 KiB x 1.0, the factors a 256 MiB
 # device copy gives (profiles/copy_256mib_calibration.md).
-GEMV_M1_TRAFFIC_BYTES = int((5182.1 * 2.0 + 32.0) * 1024)
+GEMV_M1_TRAFFIC_BYTES = int((5179.6 * 2.0 + 32.0) * 1024)
 
 
 def gemv_bytes(N, K, M, group=32):
