@@ -462,13 +462,25 @@ int igl_quant_step_dev(igl_desk *desk, const float *src_dev, int src_stride, flo
  * the product, and with leave_gain > 0 the outputs after it.  The product is
  * igl_mat_mat_dev's.  The table's mat_mat does neither: its caller does. */
 /* The prefill of a calibrated plane with one gain a row on the activation
- * grid: the lanes as levels, the codes as 4-bit planes of unit gain, the MFMA
- * GEMM on those integer-valued operands (exact: every partial sum an integer
- * below 2^24), then gain * step * part and the leave grid, as the reference's
- * level path closes a row (kern_row_code_level, app_core.c:3272-3296). */
+ * grid, closed as the reference's level path closes a row
+ * (kern_row_code_level, app_core.c:3272-3296): on the int8 matrix cores where
+ * the plane's width fits (igl_launch_gemm_level: exact int32 sums); otherwise
+ * the lanes as levels, the codes as 4-bit planes of unit gain, the binary16
+ * MFMA GEMM on those integer-valued operands (exact: every partial sum an
+ * integer below 2^24), then gain * step * part and the leave grid. */
 static int lift_levels_gemm(igl_desk_state *st, const igl_plane *sheet, const float *act_dev,
                             int act_stride, int lanes, float *out_dev, int out_stride) {
   const int N = sheet->row_count, K = sheet->col_count, bits = sheet->bit_count;
+  if (igl_gemm_level_fits(bits, sheet->code_bias, K) && sheet->row_stride % 16 == 0) {
+    /* the integer matrix cores: int8 levels against the codes as int8 */
+    const igl_gemm_close close = {sheet->device->gains, sheet->enter_gain, sheet->leave_gain};
+    const size_t need = igl_gemm_level_work_bytes(lanes, N, K, bits);
+    if (grow_dev(st, &st->gemm_dev, &st->gemm_floats, (need + 3) / 4) != IGL_OKAY) return IGL_FAIL_MEMORY;
+    return hip_check(st, igl_launch_gemm_level(act_dev, act_stride, (const uint8_t *)sheet->device->codes,
+                                               (long long)sheet->row_stride, bits, sheet->code_flip,
+                                               sheet->code_bias, &close, out_dev, out_stride, lanes, N, K,
+                                               st->gemm_dev, st->stream));
+  }
   const int two = bits == 8;
   const int widen = !(bits == 4 && sheet->code_flip == 0);
   const size_t plane_bytes = (size_t)N * (size_t)(K / 2);

@@ -177,6 +177,18 @@ hipError_t igl_launch_grid_close(const float *a, const float *b, const float *ls
                                  const float *gains, float step, float leave, int N, int lanes,
                                  float *out, int out_stride, hipStream_t stream);
 hipError_t igl_launch_fill(float *dst, size_t n, float value, hipStream_t stream);
+/* The prefill of a calibrated plane with one gain a row on the integer matrix
+ * cores (igl_gemm_level.hip): levels of act on close->step, exact int32 sums
+ * against the codes, then gain * step * part and the leave grid; a lane with a
+ * NaN gives NaN outputs.  Fits: 2-, 4- or 8-bit codes with code_bias
+ * 2^(bits-1), K a multiple of 128 (64 for 8-bit); row_stride a multiple of 16;
+ * act 16-byte aligned with act_stride % 4 == 0.  `work` holds
+ * igl_gemm_level_work_bytes(M, N, K, bits) bytes. */
+int igl_gemm_level_fits(int bits, int code_bias, int K);
+size_t igl_gemm_level_work_bytes(int M, int N, int K, int bits);
+hipError_t igl_launch_gemm_level(const float *act, int act_stride, const uint8_t *codes, long long row_stride,
+                                 int bits, int code_flip, int code_bias, const igl_gemm_close *close, float *out,
+                                 int out_stride, int M, int N, int K, void *work, hipStream_t stream);
 /* Reads `bytes` (a multiple of 16) of src once and keeps nothing (sink: one
  * word, written only on an improbable fold). */
 hipError_t igl_launch_read_floor(const void *src, size_t bytes, uint32_t *sink, hipStream_t stream);
