@@ -81,10 +81,22 @@ struct LevelArgs {
   int k_steps;            // steps of one slice (blockIdx.z)
 };
 
-__device__ __forceinline__ float level_close(const float *gains, float step, float leave, int n, int32_t part) {
-  float y = gains[n] * step * (float)part;
+// fl(y / leave) from leave_rcp = fl(1 / leave): q = fl(y * leave_rcp) is
+// within an ulp of the quotient, the fma gives the remainder y - q leave
+// exactly, and one more fma rounds q to the correctly rounded quotient
+// (Markstein's correction step).  Finite y only; others divide.
+__device__ __forceinline__ float div_leave(float y, float leave, float leave_rcp) {
+  if (!(__builtin_fabsf(y) <= 3.0e38f)) return y / leave;
+  const float q = y * leave_rcp;
+  const float e = __builtin_fmaf(-q, leave, y);
+  return __builtin_fmaf(e, leave_rcp, q);
+}
+
+// The leave grid (quant_step) on y = fl(gain * step) * part.
+__device__ __forceinline__ float level_grid(float gain_step, int32_t part, float leave, float leave_rcp) {
+  float y = gain_step * (float)part;
   if (leave > 0.0f) {
-    float level = __builtin_rintf(y / leave);
+    float level = __builtin_rintf(div_leave(y, leave, leave_rcp));
     level = level < -128.0f ? -128.0f : level;
     level = level > 127.0f ? 127.0f : level;
     y = level * leave;
@@ -228,6 +240,14 @@ __global__ __launch_bounds__(kLvThreads) void gemm_level_kernel(LevelArgs g) {
   // row l % 16 of its row tile and columns 4 (l / 16) .. + 3.
   const bool vec_ok = g.part ? (g.N % 4 == 0) : (g.out_stride % 4 == 0 && ((uintptr_t)g.out & 15u) == 0);
   int32_t *part = g.part ? g.part + (size_t)blockIdx.z * (size_t)g.M * (size_t)g.N : nullptr;
+  // fl(gain * step) of the lane's sixteen columns, loaded before any store
+  // (the outputs could alias the gains as far as the compiler knows)
+  float gs[4][4];
+  const float leave_rcp = g.leave > 0.0f ? 1.0f / g.leave : 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) gs[j][r] = g.gains[min(n0 + wn * 64 + j * 16 + 4 * gq + r, g.N - 1)] * g.step;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int m = m0 + wm * 128 + i * 16 + n;
@@ -249,8 +269,7 @@ __global__ __launch_bounds__(kLvThreads) void gemm_level_kernel(LevelArgs g) {
       float4_t v;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        v[r] = nan_row ? __builtin_nanf("")
-                       : level_close(g.gains, g.step, g.leave, min(nb + r, g.N - 1), acc[i][j][r] >> F::SHIFT);
+        v[r] = nan_row ? __builtin_nanf("") : level_grid(gs[j][r], acc[i][j][r] >> F::SHIFT, g.leave, leave_rcp);
       if (vec_ok && nb + 3 < g.N) {
         *reinterpret_cast<float4_t *>(g.out + (size_t)m * g.out_stride + nb) = v;
       } else {
@@ -272,7 +291,9 @@ __global__ void level_close_kernel(const int32_t *part, int slices, int M, int N
   if (n >= N) return;
   int32_t t = 0;
   for (int z = 0; z < slices; ++z) t += part[((size_t)z * M + m) * N + n];
-  out[(size_t)m * out_stride + n] = nan_rows[m] ? __builtin_nanf("") : level_close(gains, step, leave, n, t >> shift);
+  const float leave_rcp = leave > 0.0f ? 1.0f / leave : 0.0f;
+  out[(size_t)m * out_stride + n] =
+      nan_rows[m] ? __builtin_nanf("") : level_grid(gains[n] * step, t >> shift, leave, leave_rcp);
 }
 
 // One block a row: levels rint(x / step) clamped to [-128, 127] (quant_step,
