@@ -53,12 +53,15 @@ __device__ __forceinline__ float bf16_to_float(uint16_t raw) {
   return __builtin_bit_cast(float, (uint32_t)raw << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
-__device__ __forceinline__ uint16_t float_to_bf16(float v) {
-  uint32_t bits = __builtin_bit_cast(uint32_t, v);
-  if ((bits & 0x7F800000u) == 0x7F800000u && (bits & 0x7FFFFFu)) return (uint16_t)((bits >> 16) | 0x40u);
-  bits += 0x7FFFu + ((bits >> 16) & 1u);
-  return (uint16_t)(bits >> 16);
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet): the conversion
+// instruction, two values at a time where a pair is stored together.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint16_t float_to_bf16(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+  bf16x2_t p;
+  p[0] = (__bf16)lo;
+  p[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, p);
 }
 
 template <bool A_BF16, bool C_BF16>
@@ -512,8 +515,8 @@ __global__ __launch_bounds__(512) void gemm_q4_big_kernel(GemmBigArgs g) {
         if (g.slice_floats) {
           *reinterpret_cast<float4_t *>(part + (size_t)m * g.N + nb) = v;
         } else if (C_BF16) {
-          const uint32_t lo = (uint32_t)float_to_bf16(v[0]) | ((uint32_t)float_to_bf16(v[1]) << 16);
-          const uint32_t hi = (uint32_t)float_to_bf16(v[2]) | ((uint32_t)float_to_bf16(v[3]) << 16);
+          const uint32_t lo = bf16_pair(v[0], v[1]);
+          const uint32_t hi = bf16_pair(v[2], v[3]);
           *reinterpret_cast<uint2_t *>(reinterpret_cast<uint16_t *>(g.out) + (size_t)m * g.out_stride + nb) =
               uint2_t{lo, hi};
         } else {
