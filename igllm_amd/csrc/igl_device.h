@@ -610,4 +610,22 @@ __device__ __forceinline__ void digit_store_lds_form(const float *xs, int K, uin
   __syncthreads();
 }
 
+
+// The tile (x, y) a workgroup of a 2-D grid computes, so that each of the
+// eight XCDs (workgroups go to them round-robin by linear id, each with its
+// own L2) owns one compact block of the tile grid: XCD k takes tile rows
+// (k / 4) of two and tile columns (k % 4) of four.  Its workgroups then share
+// the rows of one operand and the columns of the other in their L2 instead of
+// each reading all of one.  Grids whose sides do not divide keep the plain map.
+__device__ __forceinline__ void xcd_tile(int &tx, int &ty) {
+  const int gx = gridDim.x, gy = gridDim.y;
+  tx = blockIdx.x;
+  ty = blockIdx.y;
+  if (gx % 4 || gy % 2) return;
+  const int id = blockIdx.x + blockIdx.y * gx;
+  const int k = id & 7, q = id >> 3;
+  const int sx = gx / 4, sy = gy / 2;
+  tx = (k & 3) * sx + q % sx;
+  ty = (k >> 2) * sy + q / sx;
+}
 }  // namespace igl

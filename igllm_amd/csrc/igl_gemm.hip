@@ -325,8 +325,10 @@ __global__ __launch_bounds__(512) void gemm_q4_big_kernel(GemmBigArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2;      // 2 wave rows of 128
   const int wn = wave & 3;       // 4 wave columns of 64
-  const int m0 = blockIdx.y * kBigM;
-  const int n0 = blockIdx.x * kBigN;
+  int tile_x, tile_y;
+  xcd_tile(tile_x, tile_y);
+  const int m0 = tile_y * kBigM;
+  const int n0 = tile_x * kBigN;
   const int steps = g.k_steps;
   const int k_first = blockIdx.z * g.k_steps * kBigK;
 

@@ -132,8 +132,10 @@ __global__ __launch_bounds__(kLvThreads) void gemm_level_kernel(LevelArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2;      // 2 wave rows of 128
   const int wn = wave & 3;       // 4 wave columns of 64
-  const int m0 = blockIdx.y * kLvM;
-  const int n0 = blockIdx.x * kLvN;
+  int tile_x, tile_y;
+  xcd_tile(tile_x, tile_y);
+  const int m0 = tile_y * kLvM;
+  const int n0 = tile_x * kLvN;
   const int steps = g.k_steps;
   const int k_first = blockIdx.z * g.k_steps * F::K;
 
