@@ -674,6 +674,23 @@ static int project(igl_engine *e, const igl_plane *p, const float *act, int act_
   return igl_mat_mat_dev(e->desk, p, act, act_stride, lanes, out, out_stride);
 }
 
+/* One lane through a calibrated plane on the level GEMV (the route
+ * igl_plane_lift_dev takes for it) with the elementwise step that follows
+ * fused into the store: the same kernel and the same arithmetic, one launch
+ * fewer.  0 where that route does not take the plane. */
+static int level_epi_fits(const igl_plane *p, const float *act, int lanes) {
+  return lanes == 1 && p->form == IGL_PLANE_CODE && p->enter_gain > 0.0f && p->device &&
+         igl_gemv_level_fits(p->bit_count, p->col_count) && ((uintptr_t)act & 15u) == 0;
+}
+
+static int project_level_epi(igl_engine *e, const igl_plane *p, const float *act, float *out, int epi,
+                             const float *epi_in) {
+  const igl_code_view view = igl_plane_view(p, dev_codes(e, p), dev_gains(e, p));
+  RUN(igl_launch_gemv_level_epi(&view, p->enter_gain, p->leave_gain, act, p->col_count, 1, out, p->row_count,
+                                p->row_count, p->col_count, epi, epi_in, 0, e->stream));
+  return IGL_OKAY;
+}
+
 static int norm_rows(igl_engine *e, const float *in, const float *gain, int n, int lanes, int stride,
                      float *out) {
   return igl_norm_rms_dev(e->desk, in, gain, n, lanes, stride, e->eps, out);
@@ -825,8 +842,13 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
     RUN(igl_launch_norm_add(e->state, H, e->lift, H, L->after_attn, H, lanes, e->eps, 1.0f, 0,
                             L->before_ff, e->scrap, H, st));
     OKAY(project(e, &L->gate, e->scrap, H, lanes, e->gate, e->inner_max));
-    OKAY(project(e, &L->up, e->scrap, H, lanes, e->rise, e->inner_max));
-    RUN(igl_launch_gelu_gate_rows(e->gate, e->inner_max, e->rise, e->inner_max, L->inner, lanes, st));
+    if (level_epi_fits(&L->up, e->scrap, lanes) && L->up.row_count == L->inner) {
+      /* gate = gelu(gate) * up proj, in the up projection's store */
+      OKAY(project_level_epi(e, &L->up, e->scrap, e->gate, IGL_LEVEL_EPI_GELU_RISE, e->gate));
+    } else {
+      OKAY(project(e, &L->up, e->scrap, H, lanes, e->rise, e->inner_max));
+      RUN(igl_launch_gelu_gate_rows(e->gate, e->inner_max, e->rise, e->inner_max, L->inner, lanes, st));
+    }
   }
   OKAY(project(e, &L->down, e->gate, e->inner_max, lanes, e->lift, H));
   /* state += norm(down) * after_ff; gate = gelu(per-layer gate proj of state) * slice */
@@ -837,8 +859,13 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
   } else {
     RUN(igl_launch_norm_add(e->state, H, e->lift, H, L->after_ff, H, lanes, e->eps, 1.0f, 0, NULL,
                             NULL, 0, st));
-    OKAY(project(e, &L->ple_gate, e->state, H, lanes, e->gate, e->inner_max));
-    RUN(igl_launch_gelu_mul(e->gate, e->inner_max, slice, e->ple_stride, e->ple, lanes, st));
+    if (level_epi_fits(&L->ple_gate, e->state, lanes) && L->ple_gate.row_count == e->ple) {
+      /* gate = gelu(per-layer gate proj) * slice, in the projection's store */
+      OKAY(project_level_epi(e, &L->ple_gate, e->state, e->gate, IGL_LEVEL_EPI_GELU_MUL, slice));
+    } else {
+      OKAY(project(e, &L->ple_gate, e->state, H, lanes, e->gate, e->inner_max));
+      RUN(igl_launch_gelu_mul(e->gate, e->inner_max, slice, e->ple_stride, e->ple, lanes, st));
+    }
   }
   OKAY(project(e, &L->ple_proj, e->gate, e->inner_max, lanes, e->lift, H));
   /* state = (state + norm(ple) * after_ple) * layer_scalar: applied by the

@@ -832,6 +832,9 @@ struct GemvLevelArgs {
   int code_bias;
   float step;             // enter_gain
   float leave;            // leave_gain (<= 0: none)
+  int epi;                // IGL_LEVEL_EPI_*: the elementwise step that follows, fused
+  const float *epi_in;    // its other operand, lane m at epi_in + m * epi_stride
+  int epi_stride;
 };
 
 __host__ __device__ constexpr size_t gemv_level_lds_bytes(int M, int units) {
@@ -1066,7 +1069,14 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
       if (m >= a.lanes) continue;
       float y = one_group ? gain_step * (float)ip[r][m] : fp[r][m];
       if (bad[m]) y = __builtin_nanf("");
-      a.out[(size_t)m * a.out_stride + row] = grid_value(y, a.leave);
+      y = grid_value(y, a.leave);
+      // the reference's next step on this output (kern_gelu_gate): with the gate
+      // projection's output, gelu(gate) * y; with the per-layer input, gelu(y) * it
+      if (a.epi == IGL_LEVEL_EPI_GELU_RISE)
+        y = gelu_near(a.epi_in[(size_t)m * a.epi_stride + row]) * y;
+      else if (a.epi == IGL_LEVEL_EPI_GELU_MUL)
+        y = gelu_near(y) * a.epi_in[(size_t)m * a.epi_stride + row];
+      a.out[(size_t)m * a.out_stride + row] = y;
     }
   }
 }
@@ -2238,11 +2248,25 @@ extern "C" int igl_gemv_level_fits(int bit_count, int K) {
 extern "C" hipError_t igl_launch_gemv_level(const igl_code_view *v, float step, float leave,
                                             const float *act, int act_stride, int lanes, float *out,
                                             int out_stride, int N, int K, hipStream_t stream) {
+  return igl_launch_gemv_level_epi(v, step, leave, act, act_stride, lanes, out, out_stride, N, K,
+                                   IGL_LEVEL_EPI_NONE, nullptr, 0, stream);
+}
+
+// The same, with the elementwise step that follows the product fused into its
+// store (IGL_LEVEL_EPI_*; epi_in may be `out` itself: each output reads its
+// own element first).
+extern "C" hipError_t igl_launch_gemv_level_epi(const igl_code_view *v, float step, float leave,
+                                                const float *act, int act_stride, int lanes, float *out,
+                                                int out_stride, int N, int K, int epi, const float *epi_in,
+                                                int epi_stride, hipStream_t stream) {
   const int bits = v->bit_count;
   if (!(step > 0.0f) || !igl_gemv_level_fits(bits, K) || (((uintptr_t)act) & 15u) ||
-      (lanes > 1 && (act_stride & 3)) || lanes < 1 || N < 1)
+      (lanes > 1 && (act_stride & 3)) || lanes < 1 || N < 1 || epi < IGL_LEVEL_EPI_NONE ||
+      epi > IGL_LEVEL_EPI_GELU_MUL || (epi != IGL_LEVEL_EPI_NONE && !epi_in))
     return hipErrorInvalidValue;
   GemvLevelArgs a;
+  a.epi = epi;
+  a.epi_stride = epi_stride;
   a.codes = v->codes;
   a.row_stride = v->row_stride;
   a.gains = v->gains;
@@ -2276,6 +2300,7 @@ extern "C" hipError_t igl_launch_gemv_level(const igl_code_view *v, float step, 
     a.lanes = l;
     a.out = out + (size_t)done * (size_t)out_stride;
     a.out_stride = out_stride;
+    a.epi_in = epi_in ? epi_in + (size_t)done * (size_t)epi_stride : nullptr;
     a.ks_log = ksplit == 1 ? 0 : ksplit == 2 ? 1 : 2;
     a.subs_log = subs_log;
     const int per_block = 4 / ksplit;

@@ -60,6 +60,13 @@ int igl_gemv_level_fits(int bit_count, int K);
 hipError_t igl_launch_gemv_level(const igl_code_view *v, float step, float leave, const float *act,
                                  int act_stride, int lanes, float *out, int out_stride, int N, int K,
                                  hipStream_t stream);
+/* The step after a product, fused into its store: none; out = gelu(epi_in) * y
+ * (the up projection after the gate's, kern_gelu_gate); out = gelu(y) * epi_in
+ * (the per-layer-input gate). */
+enum { IGL_LEVEL_EPI_NONE = 0, IGL_LEVEL_EPI_GELU_RISE = 1, IGL_LEVEL_EPI_GELU_MUL = 2 };
+hipError_t igl_launch_gemv_level_epi(const igl_code_view *v, float step, float leave, const float *act,
+                                     int act_stride, int lanes, float *out, int out_stride, int N, int K,
+                                     int epi, const float *epi_in, int epi_stride, hipStream_t stream);
 size_t igl_gemv_real_part_floats(int lanes, int N, int K);
 hipError_t igl_launch_gemv_real(const void *rows, int real_type, const float *act, int act_stride,
                                 int lanes, float *out, int out_stride, int N, int K, float *part,
