@@ -29,20 +29,26 @@
 //         reference reads them);
 //   int8: (byte ^ 0x80) in the mantissa of 1024.0, minus 1152.
 //
-// Work layout: a workgroup owns 128-position chunks (4 waves x 32).  A wave
+// Work layout: a workgroup owns W waves of 32 positions, W = 1 for spans up
+// to kAttendShortSpan (the most workgroups and the shortest chain each: at a
+// 2048-position decode context one wave measured 3% faster a token than four,
+// the merge launch costing little in the replayed step) and 4 beyond.  A wave
 // loads its 32 key rows straight into MFMA operand order (each lane a
 // contiguous d/4-byte run of a row), its 32 value rows into LDS (transposed on
 // read), runs the scores, the softmax against its peak, and the blend; the
-// four waves' (max, total, output) are merged in LDS and written as the
+// waves' (max, total, output) are merged in LDS and written as the
 // workgroup's partial.  A second kernel merges the partials in order
 // (flash-decoding); a span of one chunk is written directly.
 #include "igl_device.h"
 
 namespace igl {
 
-constexpr int kAttendThreads = 256;
 constexpr int kAttendTile = 32;                    // positions per wave
-constexpr int kAttendChunk = 4 * kAttendTile;      // positions per workgroup
+// Waves a workgroup (its chunk: 32 positions a wave), by the longest span a
+// launch covers: one up to kAttendShortSpan positions (the most workgroups,
+// the shortest chain each), four beyond (fewer partials to write and merge: at
+// 16384 positions four measured 14.7 us against 20.4 us for one).
+constexpr int kAttendShortSpan = 4096;
 constexpr int kAttendGroup = 8;                    // query heads per key/value head
 
 struct AttendArgs {
@@ -99,10 +105,10 @@ __device__ __forceinline__ float xsum32(float v) {
   return lo + hi;
 }
 
-// One workgroup takes one 128-position chunk of one lane; each wave owns 32
-// positions of it.  The query, key and value loads all go out first, so the
+// One workgroup takes one chunk of kChunk positions of one lane; each wave
+// owns 32 positions of it.  The query, key and value loads all go out first, so the
 // launch pays one memory round trip; then the scores, the wave's softmax
-// against its own peak, and the blend.  The four waves merge in LDS.  A
+// against its own peak, and the blend.  The waves merge in LDS.  A
 // workgroup that covers the lane's whole span writes the blend; otherwise it
 // writes a partial (blend, peak, total) for attend_merge_kernel.
 //
@@ -110,8 +116,10 @@ __device__ __forceinline__ float xsum32(float v) {
 // an agent-scope release/acquire ticket, was slower than the merge launch at
 // every span tried, 15 vs 13 us at a 512 window and 52 vs 29 us at 2300
 // positions of 512 dims: one CU then reads every partial.)
-template <int HEAD, int FMT, bool QVEC>
-__global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs a) {
+template <int HEAD, int FMT, bool QVEC, int W>
+__global__ __launch_bounds__(64 * W) void attend_mfma_kernel(AttendArgs a) {
+  constexpr int kThreads = 64 * W;            // W waves
+  constexpr int kChunk = kAttendTile * W;     // positions a workgroup
   constexpr int S = HEAD / 32;        // k-steps of the score product
   constexpr int QD = HEAD / 4;        // bytes of a key row one lane group reads
   constexpr int TILES = HEAD / 16;    // 16-wide dim tiles of the blend
@@ -119,10 +127,10 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
   constexpr int VPITCH = HEAD + 8;    // staged value row: (HEAD/4 + 2) dwords, conflict-free reads
   constexpr int kWaveV = kAttendTile * VPITCH;
 
-  __shared__ __attribute__((aligned(16))) uint8_t vs[4 * kWaveV];
-  __shared__ float ps[4][kAttendGroup][kAttendTile];
-  __shared__ float wm[4][kAttendGroup];
-  __shared__ float wl[4][kAttendGroup];
+  __shared__ __attribute__((aligned(16))) uint8_t vs[W * kWaveV];
+  __shared__ float ps[W][kAttendGroup][kAttendTile];
+  __shared__ float wm[W][kAttendGroup];
+  __shared__ float wl[W][kAttendGroup];
   __shared__ float head_peak[kAttendGroup];
   __shared__ float head_norm[kAttendGroup];
   // the query block as binary16 operands: [part hi / lo][head][HEAD / 8]
@@ -142,24 +150,26 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
   const int pos = (a.place_dev ? *a.place_dev : a.place0) + lane_id;
   const int span_count = a.window > 0 ? min(pos + 1, a.window) : pos + 1;
   const int place_start = pos - span_count + 1;
-  const int blocks_seen = (span_count + kAttendChunk - 1) / kAttendChunk;
+  const int blocks_seen = (span_count + kChunk - 1) / kChunk;
   if (block >= blocks_seen) return;  // past this lane's span
   const int pc = lane_id * a.chunks + block;
   const size_t kv_off = (size_t)kv * HEAD;
-  const int t0 = block * kAttendChunk + wave * kAttendTile;
+  const int t0 = block * kChunk + wave * kAttendTile;
   const bool live = t0 < span_count;
 
   // ---- loads.  The query block (8 heads x HEAD floats) is split among the
   // workgroup's threads, eight floats each, to be converted once; key rows n
   // and n + 16 of the wave's 32, bytes QD g .. QD g + QD - 1 (operand order);
   // value rows lane / 2, half lane & 1.  Rows past the span repeat the last.
-  constexpr int kQItems = kAttendGroup * HEAD / 8 / kAttendThreads;  // 1 or 2
+  constexpr int kQTotal = kAttendGroup * HEAD / 8;                 // eight-float items
+  constexpr int kQItems = (kQTotal + kThreads - 1) / kThreads;
   float qf[kQItems][8];
   {
     const float *qb = a.query + (size_t)lane_id * a.q_stride + (size_t)head0 * HEAD;
 #pragma unroll
     for (int i = 0; i < kQItems; ++i) {
-      const float *q = qb + 8 * (tid + kAttendThreads * i);
+      const int item = tid + kThreads * i;
+      const float *q = qb + 8 * (kQTotal % kThreads == 0 ? item : min(item, kQTotal - 1));
       if (QVEC) {
         const float4_t u = *reinterpret_cast<const float4_t *>(q);
         const float4_t v = *reinterpret_cast<const float4_t *>(q + 4);
@@ -202,9 +212,11 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
       hi8[e] = hi;
       lo8[e] = (_Float16)(qf[i][e] - (float)hi);
     }
-    const int item = tid + kAttendThreads * i;  // head item / (HEAD / 8), chunk item % (HEAD / 8)
-    qs[0][item / (HEAD / 8)][item % (HEAD / 8)] = hi8;
-    qs[1][item / (HEAD / 8)][item % (HEAD / 8)] = lo8;
+    const int item = tid + kThreads * i;  // head item / (HEAD / 8), chunk item % (HEAD / 8)
+    if (kQTotal % kThreads == 0 || item < kQTotal) {
+      qs[0][item / (HEAD / 8)][item % (HEAD / 8)] = hi8;
+      qs[1][item / (HEAD / 8)][item % (HEAD / 8)] = lo8;
+    }
   }
   __syncthreads();
   half8_t qa[S];
@@ -315,14 +327,20 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
     }
   }
 
-  // ---- merge the four waves: scale each by e^(m_w - M) per head.
-  __syncthreads();  // wm, wl written and every wave done with vs, reused as float[4][8][HEAD]
+  // ---- merge the W waves: scale each by e^(m_w - M) per head.
+  __syncthreads();  // wm, wl written and every wave done with vs, reused as float[W][8][HEAD]
+  auto peak_of = [&](int h) {
+    float M = wm[0][h];
+#pragma unroll
+    for (int w = 1; w < W; ++w) M = fmaxf(M, wm[w][h]);
+    return M;
+  };
   if (tid < kAttendGroup) {
     const int h = tid;
-    const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+    const float M = peak_of(h);
     float L = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
+    for (int w = 0; w < W; ++w)
       if (wm[w][h] != -INFINITY) L += wl[w][h] * __expf(wm[w][h] - M);
     head_peak[h] = M;
     head_norm[h] = L;
@@ -333,7 +351,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int h = 4 * (g & 1) + r;
-      const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+      const float M = peak_of(h);
       scale[r] = m_w[r] != -INFINITY ? __expf(m_w[r] - M) : 0.0f;
     }
     if (g < 2) {
@@ -350,21 +368,23 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
   if (a.final_out) {
     // The block saw every visible position: normalize and write the blend.
     float *out = a.final_out + (size_t)lane_id * a.q_stride + (size_t)head0 * HEAD;
-    for (int i = tid; i < kAttendGroup * HEAD; i += kAttendThreads) {
+    for (int i = tid; i < kAttendGroup * HEAD; i += kThreads) {
       const int h = i / HEAD;
       const int d = i - h * HEAD;
       const float L = head_norm[h];
-      const float v = ((ob[(0 * kAttendGroup + h) * HEAD + d] + ob[(1 * kAttendGroup + h) * HEAD + d]) +
-                       ob[(2 * kAttendGroup + h) * HEAD + d]) + ob[(3 * kAttendGroup + h) * HEAD + d];
+      float v = ob[h * HEAD + d];
+#pragma unroll
+      for (int w = 1; w < W; ++w) v += ob[(w * kAttendGroup + h) * HEAD + d];
       out[(size_t)h * HEAD + d] = L > 0.0f ? v * a.value_scale * (1.0f / L) : 0.0f;
     }
     return;
   }
-  for (int i = tid; i < kAttendGroup * HEAD; i += kAttendThreads) {
+  for (int i = tid; i < kAttendGroup * HEAD; i += kThreads) {
     const int h = i / HEAD;
     const int d = i - h * HEAD;
-    const float v = ((ob[(0 * kAttendGroup + h) * HEAD + d] + ob[(1 * kAttendGroup + h) * HEAD + d]) +
-                     ob[(2 * kAttendGroup + h) * HEAD + d]) + ob[(3 * kAttendGroup + h) * HEAD + d];
+    float v = ob[h * HEAD + d];
+#pragma unroll
+    for (int w = 1; w < W; ++w) v += ob[(w * kAttendGroup + h) * HEAD + d];
     a.part_out[((size_t)pc * a.head_count + head0 + h) * HEAD + d] = v * a.value_scale;
   }
   if (tid < kAttendGroup) {
@@ -380,7 +400,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_mfma_kernel(AttendArgs 
 __global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out_all,
                                                            const float *part_peak_all,
                                                            const float *part_total_all,
-                                                           int chunk_slots,
+                                                           int chunk_slots, int chunk,
                                                            int place0, const int *place_dev,
                                                            int window, int head_count,
                                                            int head_size, float *blend_all,
@@ -395,7 +415,7 @@ __global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out
   const int pos = (place_dev ? *place_dev : place0) + lane_id;
   const int span = window > 0 ? min(pos + 1, window) : pos + 1;
   // the workgroups that saw part of this lane's span
-  const int chunks = (span + kAttendChunk - 1) / kAttendChunk;
+  const int chunks = (span + chunk - 1) / chunk;
   const size_t base = (size_t)lane_id * chunk_slots;
   const float *part_out = part_out_all + base * head_count * head_size;
   const float *part_peak = part_peak_all + base * head_count;
@@ -451,23 +471,26 @@ __global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out
 
 using namespace igl;
 
-extern "C" int igl_attend_chunk_size(void) { return kAttendChunk; }
-
 static int attend_max_span(int place0, int window, int lanes) {
   const int last = place0 + lanes;  // span of the last lane when unwindowed
   return window > 0 ? (last < window ? last : window) : last;
 }
 
-static int attend_blocks(int place0, int window, int lanes) {
-  return (attend_max_span(place0, window, lanes) + kAttendChunk - 1) / kAttendChunk;
+static int attend_waves(int place0, int window, int lanes) {
+  return attend_max_span(place0, window, lanes) <= kAttendShortSpan ? 1 : 4;
 }
 
-template <int HEAD, int FMT>
+static int attend_blocks(int place0, int window, int lanes) {
+  const int chunk = attend_waves(place0, window, lanes) * kAttendTile;
+  return (attend_max_span(place0, window, lanes) + chunk - 1) / chunk;
+}
+
+template <int HEAD, int FMT, int W>
 static void attend_launch(const AttendArgs &a, dim3 grid, bool qvec, hipStream_t stream) {
   if (qvec)
-    hipLaunchKernelGGL((attend_mfma_kernel<HEAD, FMT, true>), grid, dim3(kAttendThreads), 0, stream, a);
+    hipLaunchKernelGGL((attend_mfma_kernel<HEAD, FMT, true, W>), grid, dim3(64 * W), 0, stream, a);
   else
-    hipLaunchKernelGGL((attend_mfma_kernel<HEAD, FMT, false>), grid, dim3(kAttendThreads), 0, stream, a);
+    hipLaunchKernelGGL((attend_mfma_kernel<HEAD, FMT, false, W>), grid, dim3(64 * W), 0, stream, a);
 }
 
 // `lanes` query lanes at positions place0 .. place0 + lanes - 1, each seeing
@@ -484,6 +507,7 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
                                         int window, int lanes, float score_scale,
                                         float *blend_out, float *work, hipStream_t stream) {
   AttendArgs a;
+  const int waves = attend_waves(place0, window, lanes);
   const int chunks = attend_blocks(place0, window, lanes);  // workgroups a lane
   const int head_count = kv_count * group_share;
   if (group_share != kAttendGroup || lanes < 1) return hipErrorInvalidValue;
@@ -510,20 +534,21 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
   dim3 grid(chunks, kv_count, lanes);
   const bool qvec = (((uintptr_t)query) & 15u) == 0 && (q_stride & 3) == 0;
   if (head_size == 256 && fmt == 0)
-    attend_launch<256, 0>(a, grid, qvec, stream);
+    waves == 1 ? attend_launch<256, 0, 1>(a, grid, qvec, stream) : attend_launch<256, 0, 4>(a, grid, qvec, stream);
   else if (head_size == 256 && fmt == 1)
-    attend_launch<256, 1>(a, grid, qvec, stream);
+    waves == 1 ? attend_launch<256, 1, 1>(a, grid, qvec, stream) : attend_launch<256, 1, 4>(a, grid, qvec, stream);
   else if (head_size == 512 && fmt == 0)
-    attend_launch<512, 0>(a, grid, qvec, stream);
+    waves == 1 ? attend_launch<512, 0, 1>(a, grid, qvec, stream) : attend_launch<512, 0, 4>(a, grid, qvec, stream);
   else if (head_size == 512 && fmt == 1)
-    attend_launch<512, 1>(a, grid, qvec, stream);
+    waves == 1 ? attend_launch<512, 1, 1>(a, grid, qvec, stream) : attend_launch<512, 1, 4>(a, grid, qvec, stream);
   else
     return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || chunks == 1) return e;
   hipLaunchKernelGGL(attend_merge_kernel, dim3(head_count, lanes, (head_size + 63) / 64), dim3(256),
                      chunks * sizeof(float), stream, a.part_out, a.part_peak, a.part_total, chunks,
-                     place0, place_dev, window, head_count, head_size, blend_out, q_stride);
+                     waves * kAttendTile, place0, place_dev, window, head_count, head_size, blend_out,
+                     q_stride);
   return hipGetLastError();
 }
 

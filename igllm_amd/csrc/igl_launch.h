@@ -123,7 +123,6 @@ hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride, con
                               int out_stride, int M, int N, int K, void *work,
                               const igl_gemm_close *close, hipStream_t stream);
 
-int igl_attend_chunk_size(void);
 size_t igl_attend_work_floats(int place0, int window, int lanes, int head_count, int head_size);
 hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t *value_store, int fmt,
                              float key_scale, float value_scale, int cache_span, int kv_width,
