@@ -533,7 +533,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend runs on one GPU; multi-GPU sharding is "
-                                   "described in DESIGN.md, not built"}))
+                                   "not built (rows of a plane would be split across GPUs, one all-gather "
+                                   "of the outputs a product)"}))
         sys.exit(2)
     from igllm_amd.backend import Backend, make_plane, synth_projection
 
