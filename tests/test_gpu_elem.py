@@ -119,17 +119,21 @@ LEVEL_KINDS = [
     (2048, 1536, 4, 0, 1), (2048, 1536, 4, 0, 3), (6144, 1536, 2, 0, 1), (1536, 6144, 2, 0, 2),
     (256, 1536, 8, 128, 1), (1536, 256, 8, 128, 4), (1536, 2048, 4, 0, 5), (300, 16384, 4, 0, 1),
     (100, 8192, 8, 128, 2), (70, 96, 2, 1, 1),
-    # from 64 lanes: the MFMA GEMM on levels and widened codes
+    # from 64 lanes: the int8 MFMA GEMM (levels against codes as int8 operands)
     (2048, 1536, 4, 0, 64), (6144, 1536, 2, 0, 300), (256, 1536, 8, 128, 70), (1536, 256, 8, 128, 256),
     (1536, 6144, 2, 0, 100), (512, 2048, 4, 3, 64),
+    # K off that kernel's step (128; 64 for 8-bit codes): the binary16 MFMA on
+    # levels and widened codes
+    (512, 1056, 4, 0, 64), (384, 1056, 8, 128, 64), (640, 1056, 2, 0, 96),
 ]
 
 
 @pytest.mark.parametrize("N,K,bits,flip,lanes", LEVEL_KINDS)
 def test_plane_lift_level_bitexact(backend, N, K, bits, flip, lanes):
     """Calibrated per-channel planes (the export's kinds, one gain a row): the
-    product on the activation grid (the fused GEMV below 64 lanes, the MFMA
-    GEMM on integer-valued operands from 64) equals the oracle's level path
+    product on the activation grid (the fused GEMV below 64 lanes; from 64 the
+    int8 MFMA GEMM, or the binary16 MFMA on integer-valued operands where K does
+    not fit it) equals the oracle's level path
     (the reference's VNNI-tier kern_row_code_level, pinned to the bit against
     that build) to the bit, and so does the leave grid after it."""
     from igllm_amd.backend import make_plane
