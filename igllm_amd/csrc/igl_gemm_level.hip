@@ -273,7 +273,9 @@ __global__ __launch_bounds__(kLvThreads) void gemm_level_kernel(LevelArgs g) {
       for (int r = 0; r < 4; ++r)
         v[r] = nan_row ? __builtin_nanf("") : level_grid(gs[j][r], acc[i][j][r] >> F::SHIFT, g.leave, leave_rcp);
       if (vec_ok && nb + 3 < g.N) {
-        *reinterpret_cast<float4_t *>(g.out + (size_t)m * g.out_stride + nb) = v;
+        // streamed past L2: the fp32 tile outgrows the L2s, whose half-filled
+        // lines were otherwise written back twice (WRITE_SIZE 1.5x the output)
+        __builtin_nontemporal_store(v, reinterpret_cast<float4_t *>(g.out + (size_t)m * g.out_stride + nb));
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
