@@ -353,11 +353,15 @@ __global__ void act_level_kernel(const float *act, int act_stride, int K, float 
 
 static int level_step_k(int bits) { return bits == 8 ? 64 : 128; }
 
+// K slices while the tiles fill under half the CUs: a slice's int32 partials
+// are M x N words each way, and at M = 2048 they cost more than idle CUs do
+// (6144 x 1536, 192 tiles: 47 us unsplit, 86 us in two slices; 2048 x 1536,
+// 64 tiles: 44.6 us in two, 46.2 us unsplit).
 static int level_slices(int M, int N, int K, int bits) {
   const int tiles = ((M + kLvM - 1) / kLvM) * ((N + kLvN - 1) / kLvN);
   const int steps = K / level_step_k(bits);
   int slices = 1;
-  while (slices < 16 && tiles * slices < 256 && steps % (2 * slices) == 0 && steps / (2 * slices) >= 2)
+  while (slices < 16 && tiles * slices < 128 && steps % (2 * slices) == 0 && steps / (2 * slices) >= 2)
     slices *= 2;
   return slices;
 }
