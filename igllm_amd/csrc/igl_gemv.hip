@@ -2195,7 +2195,10 @@ namespace igl {
 
 template <int BITS, int M, int UPL, int GPT>
 static hipError_t gemv_level_launch4(const GemvLevelArgs &a, dim3 grid, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((gemv_level_kernel<BITS, M, 4, UPL, GPT>), grid, dim3(kGemvThreads), lds, stream, a);
+  // one lane: two-row tiles, twice the workgroups (the export-kinds decode
+  // measured 2.52 against 2.68 ms a token with four)
+  hipLaunchKernelGGL((gemv_level_kernel<BITS, M, (M == 1 ? 2 : 4), UPL, GPT>), grid, dim3(kGemvThreads), lds, stream,
+                     a);
   return hipGetLastError();
 }
 
@@ -2288,7 +2291,8 @@ extern "C" hipError_t igl_launch_gemv_level_epi(const igl_code_view *v, float st
     const int slots = (K * bits + 127) / 128;
     const int upl = slots > 4 * kWave ? 2 : 1;
     const int subs_log = upl == 1 && slots <= 16 ? 2 : upl == 1 && slots <= 32 ? 1 : 0;
-    const int tiles = (N + (4 << subs_log) - 1) / (4 << subs_log);
+    const int rows_t = M == 1 ? 2 : 4;  // rows a sub-wave (the kernel's R)
+    const int tiles = (N + (rows_t << subs_log) - 1) / (rows_t << subs_log);
     int ksplit = 1;
     while (subs_log == 0 && ksplit < 4 &&
            (slots > ksplit * kWave * upl || (tiles * ksplit < 2048 && slots / (ksplit * 2) >= 32 * upl)))
