@@ -9,6 +9,7 @@
  * launched; an entry that cannot run records IGL_FAIL_SUPPORT or
  * IGL_FAIL_ARGUMENT and leaves its output unwritten.  There is no CPU path.
  */
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -37,6 +38,11 @@ struct igl_desk_state {
   int         col_limit;
   int         sum_limit;
   int         lds_limit;  /* LDS bytes a workgroup may hold on this device */
+  /* The table entries share the staging below, and the reference calls one of
+   * them (soft_max, from attend_blend_band app_core.c:11333-11346) from every
+   * worker of its pool at once: the entries take this lock. */
+  pthread_mutex_t table_lock;
+  int             table_lock_live;
   /* device and pinned staging for the host-pointer table entries */
   float *act_dev;
   float *act_pin;
@@ -705,7 +711,7 @@ int igl_rope_turn_dev(igl_desk *desk, float *v_dev, int heads, int head_size, co
 
 /* ---- the table entries (host pointers, synchronous) ---------------------- */
 
-static void table_mat_mat(igl_desk *desk, const igl_plane *sheet, const float *act_data,
+static void table_mat_mat_body(igl_desk *desk, const igl_plane *sheet, const float *act_data,
                           int act_stride, int lane_count, float *out_data, int out_stride) {
   igl_desk_state *st = desk->state;
   int done = 0;
@@ -739,11 +745,6 @@ static void table_mat_mat(igl_desk *desk, const igl_plane *sheet, const float *a
   }
 }
 
-static void table_mat_vec(igl_desk *desk, const igl_plane *sheet, const float *act_data,
-                          float *out_data) {
-  table_mat_mat(desk, sheet, act_data, 0, 1, out_data, 0);
-}
-
 /* The elementwise entries stage their vectors through the device. */
 static float *elem_stage(igl_desk_state *st, size_t floats) {
   if (refuse_recording(st)) return NULL;
@@ -762,7 +763,7 @@ static void elem_get(igl_desk_state *st, float *dst, const float *src, int n) {
     (void)hip_check(st, hipStreamSynchronize(st->stream));
 }
 
-static void table_norm_rms(igl_desk *desk, const float *value_list, const float *gain_list,
+static void table_norm_rms_body(igl_desk *desk, const float *value_list, const float *gain_list,
                            int value_count, float eps_value, float *value_out) {
   igl_desk_state *st = desk->state;
   float *room = elem_stage(st, 3 * (size_t)value_count);
@@ -778,7 +779,7 @@ static void table_norm_rms(igl_desk *desk, const float *value_list, const float 
   elem_get(st, value_out, room + 2 * (size_t)value_count, value_count);
 }
 
-static void table_soft_max(igl_desk *desk, float *value_list, int value_count) {
+static void table_soft_max_body(igl_desk *desk, float *value_list, int value_count) {
   igl_desk_state *st = desk->state;
   float *room = elem_stage(st, (size_t)value_count);
   if (!room || value_count < 1) {
@@ -790,7 +791,7 @@ static void table_soft_max(igl_desk *desk, float *value_list, int value_count) {
   elem_get(st, value_list, room, value_count);
 }
 
-static void table_gelu_gate(igl_desk *desk, float *gate_list, const float *rise_list,
+static void table_gelu_gate_body(igl_desk *desk, float *gate_list, const float *rise_list,
                             int value_count) {
   igl_desk_state *st = desk->state;
   float *room = elem_stage(st, 2 * (size_t)value_count);
@@ -804,7 +805,7 @@ static void table_gelu_gate(igl_desk *desk, float *gate_list, const float *rise_
   elem_get(st, gate_list, room, value_count);
 }
 
-static void table_rope_turn(igl_desk *desk, float *value_list, int head_size, const float *cos_list,
+static void table_rope_turn_body(igl_desk *desk, float *value_list, int head_size, const float *cos_list,
                             const float *sin_list) {
   igl_desk_state *st = desk->state;
   int half = head_size / 2;
@@ -821,6 +822,46 @@ static void table_rope_turn(igl_desk *desk, float *value_list, int head_size, co
   elem_get(st, value_list, room, head_size);
 }
 
+/* The entries the table holds: each body under the desk's lock. */
+static void table_mat_mat(igl_desk *desk, const igl_plane *sheet, const float *act_data,
+                          int act_stride, int lane_count, float *out_data, int out_stride) {
+  pthread_mutex_lock(&desk->state->table_lock);
+  table_mat_mat_body(desk, sheet, act_data, act_stride, lane_count, out_data, out_stride);
+  pthread_mutex_unlock(&desk->state->table_lock);
+}
+
+static void table_mat_vec(igl_desk *desk, const igl_plane *sheet, const float *act_data,
+                          float *out_data) {
+  table_mat_mat(desk, sheet, act_data, 0, 1, out_data, 0);
+}
+
+static void table_norm_rms(igl_desk *desk, const float *value_list, const float *gain_list,
+                           int value_count, float eps_value, float *value_out) {
+  pthread_mutex_lock(&desk->state->table_lock);
+  table_norm_rms_body(desk, value_list, gain_list, value_count, eps_value, value_out);
+  pthread_mutex_unlock(&desk->state->table_lock);
+}
+
+static void table_soft_max(igl_desk *desk, float *value_list, int value_count) {
+  pthread_mutex_lock(&desk->state->table_lock);
+  table_soft_max_body(desk, value_list, value_count);
+  pthread_mutex_unlock(&desk->state->table_lock);
+}
+
+static void table_gelu_gate(igl_desk *desk, float *gate_list, const float *rise_list,
+                            int value_count) {
+  pthread_mutex_lock(&desk->state->table_lock);
+  table_gelu_gate_body(desk, gate_list, rise_list, value_count);
+  pthread_mutex_unlock(&desk->state->table_lock);
+}
+
+static void table_rope_turn(igl_desk *desk, float *value_list, int head_size, const float *cos_list,
+                            const float *sin_list) {
+  pthread_mutex_lock(&desk->state->table_lock);
+  table_rope_turn_body(desk, value_list, head_size, cos_list, sin_list);
+  pthread_mutex_unlock(&desk->state->table_lock);
+}
+
 /* ---- open / close --------------------------------------------------------- */
 
 int igl_back_open(igl_desk *desk, int device_index, int sum_limit, int col_limit, int lane_limit) {
@@ -834,6 +875,11 @@ int igl_back_open(igl_desk *desk, int device_index, int sum_limit, int col_limit
   st = (igl_desk_state *)calloc(1, sizeof(*st));
   if (!st) return IGL_FAIL_MEMORY;
   st->device = device_index;
+  if (pthread_mutex_init(&st->table_lock, NULL) != 0) {
+    free(st);
+    return IGL_FAIL_MEMORY;
+  }
+  st->table_lock_live = 1;
   st->lane_limit = lane_limit > 0 ? lane_limit : 16;
   st->col_limit = col_limit > 0 ? col_limit : 1;
   st->sum_limit = sum_limit > 0 ? sum_limit : 1;
@@ -881,6 +927,7 @@ void igl_back_close(igl_desk *desk) {
   if (st->mark[0]) (void)hipEventDestroy(st->mark[0]);
   if (st->mark[1]) (void)hipEventDestroy(st->mark[1]);
   if (st->stream) (void)hipStreamDestroy(st->stream);
+  if (st->table_lock_live) pthread_mutex_destroy(&st->table_lock);
   free(st);
   memset(desk, 0, sizeof(*desk));
 }

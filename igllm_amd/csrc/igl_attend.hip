@@ -558,3 +558,19 @@ extern "C" size_t igl_attend_work_floats(int place0, int window, int lanes, int 
   const size_t blocks = (size_t)attend_blocks(place0, window, lanes);
   return (size_t)lanes * blocks * (size_t)head_count * ((size_t)head_size + 2);
 }
+
+// Floats of workspace enough for every igl_launch_attend call of at most
+// `lanes` lanes whose spans stay within `span_limit` positions.  The chunk
+// count is not monotonic in the span: chunks are kAttendTile positions up to
+// kAttendShortSpan and four times that beyond, so a span just under
+// kAttendShortSpan has more chunks than one just over it.  The largest count
+// of each regime is taken.
+extern "C" size_t igl_attend_work_floats_limit(int span_limit, int lanes, int head_count,
+                                               int head_size) {
+  if (span_limit < 1 || lanes < 1) return 0;
+  const int short_top = span_limit < kAttendShortSpan ? span_limit : kAttendShortSpan;
+  const int b_short = attend_blocks(short_top - 1, 0, 1);
+  const int b_long = attend_blocks(span_limit - 1, 0, 1);
+  const size_t blocks = (size_t)(b_short > b_long ? b_short : b_long);
+  return (size_t)lanes * blocks * (size_t)head_count * ((size_t)head_size + 2);
+}

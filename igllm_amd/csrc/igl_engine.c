@@ -38,6 +38,11 @@
 #include "igl_launch.h"
 
 #define ENG_LAYER_LIMIT 128
+/* Lanes a speculative block may carry: the only pass that takes logits on
+ * more than one lane (a prime takes none), so the 262144-wide logit rows are
+ * sized by this and not by the prime's lane limit.  The reference's blocks
+ * carry at most KERN_LANE_LIMIT = 16 (app_core.c:1980). */
+#define ENG_GUESS_LIMIT 64
 #define ENG_TENSOR_LIMIT 4096
 
 typedef struct eng_tensor {
@@ -69,7 +74,7 @@ struct igl_engine {
   hipStream_t stream;
   int vocab, hidden, layers, heads, kv_heads, window, ple, share_count;
   float eps, cap;
-  int window_limit, lane_limit, fill, precise;
+  int window_limit, lane_limit, guess_limit, fill, precise;
   int turns[2], halves[2];
   float *steps_dev[2];
   /* the checkpoint */
@@ -385,6 +390,7 @@ int igl_engine_open(igl_engine **out, igl_desk *desk, const char *folder, int wi
   e->desk = desk;
   e->stream = (hipStream_t)igl_desk_stream(desk);
   e->lane_limit = lane_limit > 0 ? lane_limit : 16;
+  e->guess_limit = e->lane_limit < ENG_GUESS_LIMIT ? e->lane_limit : ENG_GUESS_LIMIT;
   e->precise = precise;
 
   /* config.json */
@@ -564,14 +570,11 @@ int igl_engine_open(igl_engine **out, igl_desk *desk, const char *folder, int wi
     e->kv_stride = e->q_stride / e->heads;
     e->ple_stride = e->layers * e->ple;
     int widest = 0;
-    size_t one, many;
     for (int i = 0; i < e->layers; ++i)
       if (e->layer[i].head_size > widest) widest = e->layer[i].head_size;
-    /* attention partials: a decode step at the last position, or a batch */
-    one = igl_attend_work_floats(e->window_limit - 1, 0, 1, e->heads, widest);
-    many = igl_attend_work_floats(e->window_limit - e->lane_limit > 0 ? e->window_limit - e->lane_limit : 0,
-                                  0, e->lane_limit, e->heads, widest);
-    e->attend_floats = one > many ? one : many;
+    /* attention partials: every launch has at most lane_limit lanes, each
+     * seeing at most window_limit positions */
+    e->attend_floats = igl_attend_work_floats_limit(e->window_limit, e->lane_limit, e->heads, widest);
     if ((code = dev_alloc((void **)&e->ctl_dev, (lanes + 1) * sizeof(int32_t))) ||
         (code = dev_alloc((void **)&e->attend_work, e->attend_floats * sizeof(float))) ||
         (code = dev_alloc((void **)&e->state_buf[0], lanes * e->hidden * 4)) ||
@@ -586,14 +589,15 @@ int igl_engine_open(igl_engine **out, igl_desk *desk, const char *folder, int wi
         (code = dev_alloc((void **)&e->rise, lanes * e->inner_max * 4)) ||
         (code = dev_alloc((void **)&e->ple_seed, lanes * e->ple_stride * 4)) ||
         (code = dev_alloc((void **)&e->ple_room, lanes * e->ple_stride * 4)) ||
-        (code = dev_alloc((void **)&e->logits, lanes * (size_t)e->vocab * 4)) ||
-        (code = dev_alloc(&e->pick_work, igl_pick_work_bytes(e->lane_limit))) ||
-        (code = dev_alloc((void **)&e->pick_dev, 2 * lanes * sizeof(int32_t))))
+        (code = dev_alloc((void **)&e->logits, (size_t)e->guess_limit * (size_t)e->vocab * 4)) ||
+        (code = dev_alloc(&e->pick_work, igl_pick_work_bytes(e->guess_limit))) ||
+        (code = dev_alloc((void **)&e->pick_dev, 2 * (size_t)e->guess_limit * sizeof(int32_t))))
       goto fail;
     e->ids_dev = e->ctl_dev + 1;
     e->state = e->state_buf[0];
     if (hipHostMalloc((void **)&e->io, sizeof(igl_step_io), hipHostMallocDefault) != hipSuccess ||
-        hipHostMalloc((void **)&e->pairs_host, 2 * lanes * sizeof(int32_t), hipHostMallocDefault) != hipSuccess) {
+        hipHostMalloc((void **)&e->pairs_host, 2 * (size_t)e->guess_limit * sizeof(int32_t),
+                      hipHostMallocDefault) != hipSuccess) {
       code = IGL_FAIL_MEMORY;
       goto fail;
     }
@@ -1017,7 +1021,7 @@ int igl_engine_set_graph(igl_engine *e, int on) {
  * steps overwrite before any query reads them. */
 int igl_engine_guess(igl_engine *e, const int32_t *ids, int count, int32_t *picks_out,
                      float *margins_out) {
-  if (!e || !ids || count < 1 || count > e->lane_limit) return IGL_FAIL_ARGUMENT;
+  if (!e || !ids || count < 1 || count > e->guess_limit) return IGL_FAIL_ARGUMENT;
   if (e->guess_count || e->fill + count > e->window_limit) return IGL_FAIL_STATE;
   for (int l = 0; l < count; ++l)
     if (ids[l] < 0 || ids[l] >= e->embed.row_count) return IGL_FAIL_ARGUMENT;
@@ -1115,7 +1119,7 @@ int igl_scout_draw(const igl_scout *scout, int32_t *out, int want) {
 }
 
 int igl_engine_logits(igl_engine *e, float *out, int lane) {
-  if (!e || !out || lane < 0 || lane >= e->lane_limit) return IGL_FAIL_ARGUMENT;
+  if (!e || !out || lane < 0 || lane >= e->guess_limit) return IGL_FAIL_ARGUMENT;
   RUN(hipMemcpyAsync(out, e->logits + (size_t)lane * e->vocab, (size_t)e->vocab * sizeof(float),
                      hipMemcpyDeviceToHost, e->stream));
   RUN(hipStreamSynchronize(e->stream));

@@ -124,6 +124,9 @@ hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride, con
                               const igl_gemm_close *close, hipStream_t stream);
 
 size_t igl_attend_work_floats(int place0, int window, int lanes, int head_count, int head_size);
+/* Enough for every call of at most `lanes` lanes whose spans stay within
+ * `span_limit` positions (the chunk count is not monotonic in the span). */
+size_t igl_attend_work_floats_limit(int span_limit, int lanes, int head_count, int head_size);
 hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t *value_store, int fmt,
                              float key_scale, float value_scale, int cache_span, int kv_width,
                              int kv_count, int group_share, int head_size, const float *query,

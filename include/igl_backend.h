@@ -298,6 +298,7 @@ int  igl_engine_prime(igl_engine *engine, const int32_t *ids, int count);
 /* session_step + the greedy pick (first maximum, 14672-14677); margin_out
  * receives the gap to the runner-up logit. */
 int  igl_engine_step(igl_engine *engine, int32_t id, int32_t *pick_out, float *margin_out);
+/* The last pass's logits of `lane` (below min(lane_limit, 64)). */
 int  igl_engine_logits(igl_engine *engine, float *out, int lane);
 int  igl_engine_fill(const igl_engine *engine);
 int  igl_engine_vocab(const igl_engine *engine);
@@ -309,7 +310,9 @@ int  igl_engine_set_graph(igl_engine *engine, int on);
 /* session_guess (app_core.c:12139-12203): one pass over ids[0 .. count) (the
  * next input, then a proposed continuation) with the greedy pick and top-1 /
  * top-2 gap of every lane; the block stays open until igl_engine_keep, and
- * step / prime / guess refuse meanwhile.  count <= lane_limit. */
+ * step / prime / guess refuse meanwhile.  count <= min(lane_limit, 64): the
+ * logit rows are held for that many lanes (the reference's blocks carry at
+ * most 16). */
 int  igl_engine_guess(igl_engine *engine, const int32_t *ids, int count, int32_t *picks_out,
                       float *margins_out);
 /* session_guess_keep (12207-12223): keep the block's first `keep` lanes. */

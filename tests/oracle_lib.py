@@ -15,6 +15,7 @@ ORACLE_PATH = os.path.join(ROOT, "oracle", "liboracle.so")
 REF_PLAIN_PATH = os.path.join(ROOT, "oracle", "_ref", "libigl_ref_plain.so")
 REF_TUNED_PATH = os.path.join(ROOT, "oracle", "_ref", "libigl_ref_tuned.so")
 REF_LEVEL_PATH = os.path.join(ROOT, "oracle", "_ref", "libigl_ref_level.so")
+REF_DROPIN_PATH = os.path.join(ROOT, "oracle", "_ref", "libigl_ref_dropin.so")
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
