@@ -593,16 +593,12 @@ int igl_plane_lift_dev(igl_desk *desk, const igl_plane *sheet, const float *act_
 
 /* ---- attention and cache ------------------------------------------------- */
 
-int igl_attend_lanes_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t *value_store,
-                         int format, float key_scale, float value_scale, int cache_span,
-                         int kv_count, int group_share, int head_size, const float *query_dev,
-                         int lane_stride, int place_first, int window, int lane_count,
-                         float score_scale, float *blend_out_dev) {
-  igl_desk_state *st = desk ? desk->state : NULL;
-  size_t need;
-  int kv_width, widest;
-  if (!st) return IGL_FAIL_STATE;
-  widest = window > 0 && window < place_first + lane_count ? window : place_first + lane_count;
+/* The checks both lane entries make before anything is launched. */
+static int attend_check(igl_desk_state *st, const uint8_t *key_store, const uint8_t *value_store,
+                        int format, int cache_span, int kv_count, int group_share, int head_size,
+                        const float *query_dev, int lane_stride, int place_first, int window,
+                        int lane_count, const float *blend_out_dev) {
+  int widest = window > 0 && window < place_first + lane_count ? window : place_first + lane_count;
   if (!key_store || !value_store || !query_dev || !blend_out_dev || kv_count < 1 ||
       cache_span < 1 || lane_count < 1 || place_first < 0 || window < 0 || widest > cache_span ||
       (lane_count > 1 && lane_stride < kv_count * group_share * head_size) ||
@@ -614,17 +610,64 @@ int igl_attend_lanes_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t
     desk_fail(st, IGL_FAIL_SUPPORT);
     return IGL_FAIL_SUPPORT;
   }
-  kv_width = kv_count * head_size;
   if (((uintptr_t)key_store & 15u) || ((uintptr_t)value_store & 15u)) {
     desk_fail(st, IGL_FAIL_ARGUMENT);
     return IGL_FAIL_ARGUMENT;
   }
+  return IGL_OKAY;
+}
+
+int igl_attend_lanes_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t *value_store,
+                         int format, float key_scale, float value_scale, int cache_span,
+                         int kv_count, int group_share, int head_size, const float *query_dev,
+                         int lane_stride, int place_first, int window, int lane_count,
+                         float score_scale, float *blend_out_dev) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  size_t need;
+  int code;
+  if (!st) return IGL_FAIL_STATE;
+  if ((code = attend_check(st, key_store, value_store, format, cache_span, kv_count, group_share,
+                           head_size, query_dev, lane_stride, place_first, window, lane_count,
+                           blend_out_dev)) != IGL_OKAY)
+    return code;
   need = igl_attend_work_floats(place_first, window, lane_count, kv_count * group_share, head_size);
   if (grow_dev(st, &st->work_dev, &st->work_floats, need) != IGL_OKAY) return IGL_FAIL_MEMORY;
   return hip_check(st, igl_launch_attend(key_store, value_store, format, key_scale, value_scale,
-                                         cache_span, kv_width, kv_count, group_share, head_size,
-                                         query_dev, lane_stride, place_first, NULL, window,
-                                         lane_count, score_scale, blend_out_dev, st->work_dev,
+                                         cache_span, kv_count * head_size, kv_count, group_share,
+                                         head_size, query_dev, lane_stride, place_first, NULL,
+                                         window, lane_count, score_scale, blend_out_dev,
+                                         st->work_dev, st->stream));
+}
+
+/* The same kernels with the partials in the fixed per-device array
+ * (igl_attend.hip); nothing is allocated or freed. */
+int igl_attend_lanes_fixed_dev(igl_desk *desk, const uint8_t *key_store,
+                               const uint8_t *value_store, int format, float key_scale,
+                               float value_scale, int cache_span, int kv_count, int group_share,
+                               int head_size, const float *query_dev, int lane_stride,
+                               int place_first, int window, int lane_count, float score_scale,
+                               float *blend_out_dev) {
+  igl_desk_state *st = desk ? desk->state : NULL;
+  float *work;
+  int code;
+  if (!st) return IGL_FAIL_STATE;
+  if ((code = attend_check(st, key_store, value_store, format, cache_span, kv_count, group_share,
+                           head_size, query_dev, lane_stride, place_first, window, lane_count,
+                           blend_out_dev)) != IGL_OKAY)
+    return code;
+  if (igl_attend_work_floats(place_first, window, lane_count, kv_count * group_share, head_size) >
+      (size_t)IGL_ATTEND_FIXED_FLOATS) {
+    desk_fail(st, IGL_FAIL_SUPPORT);
+    return IGL_FAIL_SUPPORT;
+  }
+  if (!(work = igl_attend_fixed_ptr(st->device))) {
+    desk_fail(st, IGL_FAIL_STATE);
+    return IGL_FAIL_STATE;
+  }
+  return hip_check(st, igl_launch_attend(key_store, value_store, format, key_scale, value_scale,
+                                         cache_span, kv_count * head_size, kv_count, group_share,
+                                         head_size, query_dev, lane_stride, place_first, NULL,
+                                         window, lane_count, score_scale, blend_out_dev, work,
                                          st->stream));
 }
 
@@ -872,6 +915,8 @@ int igl_back_open(igl_desk *desk, int device_index, int sum_limit, int col_limit
   if (hipGetDeviceCount(&count) != hipSuccess || count < 1) return IGL_FAIL_DEVICE;
   if (device_index < 0 || device_index >= count) return IGL_FAIL_ARGUMENT;
   if (hipSetDevice(device_index) != hipSuccess) return IGL_FAIL_DEVICE;
+  /* the fixed attention workspace's address on this device, once */
+  if (igl_attend_fixed_resolve(device_index) != hipSuccess) return IGL_FAIL_DEVICE;
   st = (igl_desk_state *)calloc(1, sizeof(*st));
   if (!st) return IGL_FAIL_MEMORY;
   st->device = device_index;

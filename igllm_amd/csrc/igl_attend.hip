@@ -39,6 +39,9 @@
 // waves' (max, total, output) are merged in LDS and written as the
 // workgroup's partial.  A second kernel merges the partials in order
 // (flash-decoding); a span of one chunk is written directly.
+#include <mutex>
+
+#include "igl_backend.h"
 #include "igl_device.h"
 
 namespace igl {
@@ -573,4 +576,37 @@ extern "C" size_t igl_attend_work_floats_limit(int span_limit, int lanes, int he
   const int b_long = attend_blocks(span_limit - 1, 0, 1);
   const size_t blocks = (size_t)(b_short > b_long ? b_short : b_long);
   return (size_t)lanes * blocks * (size_t)head_count * ((size_t)head_size + 2);
+}
+
+// ---- the workspace of the entry that allocates nothing ---------------------
+//
+// igl_attend_lanes_fixed_dev writes its chunk partials here instead of into
+// the desk's grow-only workspace.  One copy of the array lives on each GPU the
+// library runs on, until the process ends.  On the host, `scratch` names a
+// stand-in, not device memory: host code passes the address that
+// hipGetSymbolAddress gives for the current device, resolved once per device
+// (igl_attend_fixed_resolve, called by igl_back_open with that device current).
+static __device__ __align__(256) float scratch[IGL_ATTEND_FIXED_FLOATS];
+
+namespace {
+constexpr int kFixedDevices = 64;
+std::mutex fixed_lock;
+float *fixed_ptr[kFixedDevices];
+}  // namespace
+
+extern "C" hipError_t igl_attend_fixed_resolve(int device) {
+  if (device < 0 || device >= kFixedDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> hold(fixed_lock);
+  if (fixed_ptr[device]) return hipSuccess;
+  void *ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  fixed_ptr[device] = static_cast<float *>(ptr);
+  return hipSuccess;
+}
+
+extern "C" float *igl_attend_fixed_ptr(int device) {
+  if (device < 0 || device >= kFixedDevices) return nullptr;
+  std::lock_guard<std::mutex> hold(fixed_lock);
+  return fixed_ptr[device];
 }

@@ -124,6 +124,11 @@ hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride, con
                               const igl_gemm_close *close, hipStream_t stream);
 
 size_t igl_attend_work_floats(int place0, int window, int lanes, int head_count, int head_size);
+/* The device address of the fixed attention workspace on `device`
+ * (IGL_ATTEND_FIXED_FLOATS floats), resolved once per device with it current
+ * (igl_back_open); NULL before. */
+hipError_t igl_attend_fixed_resolve(int device);
+float *igl_attend_fixed_ptr(int device);
 /* Enough for every call of at most `lanes` lanes whose spans stay within
  * `span_limit` positions (the chunk count is not monotonic in the span). */
 size_t igl_attend_work_floats_limit(int span_limit, int lanes, int head_count, int head_size);

@@ -121,6 +121,8 @@ SIGNATURES = {
                             _F, _P]),
     "igl_attend_lanes_dev": (_I, [ctypes.POINTER(Desk), _P, _P, _I, _F, _F, _I, _I, _I, _I, _P,
                                   _I, _I, _I, _I, _F, _P]),
+    "igl_attend_lanes_fixed_dev": (_I, [ctypes.POINTER(Desk), _P, _P, _I, _F, _F, _I, _I, _I, _I,
+                                        _P, _I, _I, _I, _I, _F, _P]),
     "igl_gemma_shape_e2b": (None, [ctypes.POINTER(GemmaShape)]),
     "igl_gemma_full_layer": (_I, [ctypes.POINTER(GemmaShape), _I]),
     "igl_gemma_write": (_I, [ctypes.c_char_p, ctypes.POINTER(GemmaShape), ctypes.c_uint64]),

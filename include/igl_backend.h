@@ -196,6 +196,25 @@ int igl_attend_lanes_dev(igl_desk *desk, const uint8_t *key_store, const uint8_t
                          int kv_count, int group_share, int head_size, const float *query_dev,
                          int lane_stride, int place_first, int window, int lane_count,
                          float score_scale, float *blend_out_dev);
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): igl_attend_lanes_dev with the same arguments and results,
+ * whose chunk partials live in a fixed array of IGL_ATTEND_FIXED_FLOATS floats
+ * (8 MiB) that each GPU holds from the library's load until the process ends,
+ * instead of in the desk's grow-only workspace.  It allocates and frees
+ * nothing.  A call whose partials exceed the array (at most
+ * lane_count * kv_count * group_share * (head_size + 2) * ceil(span / 32)
+ * floats, span the longest lane's) is refused with IGL_FAIL_SUPPORT before
+ * anything is launched.  Every call on one GPU shares that GPU's array and
+ * nothing in it needs to start at zero (each partial is written before it is
+ * read); calls that overlap on one GPU (two desks, or two streams) race. */
+#define IGL_ATTEND_FIXED_FLOATS (1u << 21)
+int igl_attend_lanes_fixed_dev(igl_desk *desk, const uint8_t *key_store,
+                               const uint8_t *value_store, int format, float key_scale,
+                               float value_scale, int cache_span, int kv_count, int group_share,
+                               int head_size, const float *query_dev, int lane_stride,
+                               int place_first, int window, int lane_count, float score_scale,
+                               float *blend_out_dev);
 /* cache_lay (app_core.c:11205-11236) for a byte store: row / scale to the ring
  * at byte offset slot_first. */
 int igl_cache_lay_dev(igl_desk *desk, const float *row_dev, int width, float scale, int format,
