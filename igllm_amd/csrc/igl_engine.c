@@ -1059,11 +1059,55 @@ int igl_engine_keep(igl_engine *e, int keep) {
 
 #define IGL_SCOUT_REACH 3
 #define IGL_SCOUT_REACH_LEAST 2
+#define IGL_SCOUT_GRAMS (IGL_SCOUT_REACH - IGL_SCOUT_REACH_LEAST + 1)
+
+/* The committed stream, and for each reach an index from an n-gram of the
+ * stream to the latest position it starts at among the positions a draw may
+ * use: those with at least one committed id after the n-gram.  A draw is then
+ * one lookup a reach instead of a scan of the stream.  Index slots hold start
+ * positions (-1 empty); a slot's key is the n-gram the stream holds there. */
+typedef struct scout_index {
+  int32_t *slot;
+  size_t   room;  /* a power of two */
+  size_t   used;
+} scout_index;
 
 struct igl_scout {
-  int32_t *ids;
-  int count, room;
+  int32_t    *ids;
+  size_t      count, room;
+  scout_index gram[IGL_SCOUT_GRAMS];  /* [r]: reach IGL_SCOUT_REACH - r */
 };
+
+static uint32_t scout_hash(const int32_t *g, int reach) {
+  uint32_t h = 0x811C9DC5u ^ (uint32_t)reach;
+  for (int i = 0; i < reach; ++i) {
+    h = (h ^ (uint32_t)g[i]) * 0x01000193u;
+    h ^= h >> 15;
+  }
+  return h;
+}
+
+/* The slot that holds `g` (its start is the latest occurrence), or the empty
+ * slot where it would go. */
+static size_t scout_probe(const igl_scout *sc, const scout_index *ix, const int32_t *g, int reach) {
+  size_t at = scout_hash(g, reach) & (ix->room - 1);
+  for (;; at = (at + 1) & (ix->room - 1)) {
+    const int32_t start = ix->slot[at];
+    if (start < 0 || memcmp(sc->ids + start, g, sizeof(int32_t) * (size_t)reach) == 0) return at;
+  }
+}
+
+static int scout_index_grow(igl_scout *sc, scout_index *ix, int reach) {
+  const size_t room = ix->room ? 2 * ix->room : 256;
+  scout_index fresh = {(int32_t *)malloc(sizeof(int32_t) * room), room, ix->used};
+  if (!fresh.slot) return IGL_FAIL_MEMORY;
+  memset(fresh.slot, 0xFF, sizeof(int32_t) * room);
+  for (size_t i = 0; i < ix->room; ++i)
+    if (ix->slot[i] >= 0) fresh.slot[scout_probe(sc, &fresh, sc->ids + ix->slot[i], reach)] = ix->slot[i];
+  free(ix->slot);
+  *ix = fresh;
+  return IGL_OKAY;
+}
 
 int igl_scout_open(igl_scout **out) {
   if (!out) return IGL_FAIL_ARGUMENT;
@@ -1073,24 +1117,43 @@ int igl_scout_open(igl_scout **out) {
 
 void igl_scout_close(igl_scout *scout) {
   if (!scout) return;
+  for (int r = 0; r < IGL_SCOUT_GRAMS; ++r) free(scout->gram[r].slot);
   free(scout->ids);
   free(scout);
 }
 
-/* Ids the stream has committed to, in order (scout_note, 12311-12328). */
+/* Appends ids the stream has committed to (scout_note, app_core.c:12311-12328).
+ * Each id appended at position c makes the n-grams starting at c - reach
+ * usable (they now have an id after them); each is recorded as its gram's
+ * latest start. */
 int igl_scout_note(igl_scout *scout, const int32_t *ids, int count) {
   if (!scout || (!ids && count > 0) || count < 0) return IGL_FAIL_ARGUMENT;
-  if (scout->count + count > scout->room) {
-    int room = scout->room ? scout->room : 1024;
+  if (scout->count + (size_t)count > (size_t)INT32_MAX) return IGL_FAIL_ARGUMENT;
+  if (scout->count + (size_t)count > scout->room) {
+    size_t room = scout->room + scout->room / 2 + 256;
     int32_t *fresh;
-    while (room < scout->count + count) room *= 2;
-    fresh = (int32_t *)realloc(scout->ids, sizeof(int32_t) * (size_t)room);
+    if (room < scout->count + (size_t)count) room = scout->count + (size_t)count;
+    fresh = (int32_t *)realloc(scout->ids, sizeof(int32_t) * room);
     if (!fresh) return IGL_FAIL_MEMORY;
     scout->ids = fresh;
     scout->room = room;
   }
-  if (count) memcpy(scout->ids + scout->count, ids, sizeof(int32_t) * (size_t)count);
-  scout->count += count;
+  for (int i = 0; i < count; ++i) {
+    const size_t c = scout->count;
+    scout->ids[c] = ids[i];
+    scout->count = c + 1;
+    for (int r = 0; r < IGL_SCOUT_GRAMS; ++r) {
+      const int reach = IGL_SCOUT_REACH - r;
+      scout_index *ix = &scout->gram[r];
+      size_t at;
+      if (c < (size_t)reach) continue;
+      if (2 * (ix->used + 1) > ix->room && scout_index_grow(scout, ix, reach) != IGL_OKAY)
+        return IGL_FAIL_MEMORY;
+      at = scout_probe(scout, ix, scout->ids + c - reach, reach);
+      if (ix->slot[at] < 0) ix->used++;
+      ix->slot[at] = (int32_t)(c - reach);
+    }
+  }
   return IGL_OKAY;
 }
 
@@ -1099,21 +1162,20 @@ int igl_scout_note(igl_scout *scout, const int32_t *ids, int count) {
  * anywhere; 0 when none does (scout_draw, 12341-12361). */
 int igl_scout_draw(const igl_scout *scout, int32_t *out, int want) {
   if (!scout || !out || want < 1) return 0;
-  for (int reach = IGL_SCOUT_REACH; reach >= IGL_SCOUT_REACH_LEAST; --reach) {
+  for (int r = 0; r < IGL_SCOUT_GRAMS; ++r) {
+    const int reach = IGL_SCOUT_REACH - r;
+    const scout_index *ix = &scout->gram[r];
     const int32_t *tail;
-    if (scout->count < reach + 1) continue;
+    size_t at, from, take;
+    if (scout->count < (size_t)reach + 1 || !ix->room) continue;
     tail = scout->ids + scout->count - reach;
-    for (int place = scout->count - reach - 1; place >= 0; --place) {
-      int slot, take;
-      for (slot = 0; slot < reach; ++slot)
-        if (scout->ids[place + slot] != tail[slot]) break;
-      if (slot < reach) continue;
-      take = scout->count - (place + reach);
-      if (take < 1) continue;
-      if (take > want) take = want;
-      memcpy(out, scout->ids + place + reach, sizeof(int32_t) * (size_t)take);
-      return take;
-    }
+    at = scout_probe(scout, ix, tail, reach);
+    if (ix->slot[at] < 0) continue;
+    from = (size_t)ix->slot[at] + (size_t)reach;
+    take = scout->count - from;
+    if (take > (size_t)want) take = (size_t)want;
+    memcpy(out, scout->ids + from, sizeof(int32_t) * take);
+    return (int)take;
   }
   return 0;
 }

@@ -73,6 +73,34 @@ def test_scout_against_brute_force(lib):
         assert draw(lib, ids, want) == expect, (trial, ids, want)
 
 
+def test_scout_incremental_against_brute_force(lib):
+    """One long stream noted a few ids at a time (the index rehashes many
+    times), drawn after every note, against the definition."""
+    rng = np.random.default_rng(11)
+    ids = rng.integers(0, 12, size=3000).tolist()
+    s = Scout(lib)
+    try:
+        n = 0
+        while n < len(ids):
+            k = int(rng.integers(1, 5))
+            s.note(np.array(ids[n:n + k], dtype=np.int32))
+            n = min(n + k, len(ids))
+            seen = ids[:n]
+            expect = []
+            for reach in (3, 2):
+                if n < reach + 1:
+                    continue
+                tail = seen[n - reach:]
+                places = [p for p in range(n - reach) if seen[p:p + reach] == tail]
+                if places:
+                    p = max(places)
+                    expect = seen[p + reach:p + reach + 3]
+                    break
+            assert list(s.draw(3)) == expect, n
+    finally:
+        s.close()
+
+
 def test_scout_grows(lib):
     s = Scout(lib)
     try:
