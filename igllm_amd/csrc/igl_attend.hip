@@ -29,16 +29,22 @@
 //         reference reads them);
 //   int8: (byte ^ 0x80) in the mantissa of 1024.0, minus 1152.
 //
-// Work layout: a workgroup owns W waves of 32 positions, W = 1 for spans up
-// to kAttendShortSpan (the most workgroups and the shortest chain each: at a
-// 2048-position decode context one wave measured 3% faster a token than four,
-// the merge launch costing little in the replayed step) and 4 beyond.  A wave
-// loads its 32 key rows straight into MFMA operand order (each lane a
-// contiguous d/4-byte run of a row), its 32 value rows into LDS (transposed on
-// read), runs the scores, the softmax against its peak, and the blend; the
-// waves' (max, total, output) are merged in LDS and written as the
-// workgroup's partial.  A second kernel merges the partials in order
-// (flash-decoding); a span of one chunk is written directly.
+// Work layout (flash-decoding): a lane's span is cut into chunks of C
+// positions (32 up to kAttendShortSpan, 64 beyond), one workgroup of four
+// waves a chunk.  The two products split the chunk differently among the
+// waves, so each wave's dependent chain is a quarter of the chunk's work:
+// scores by positions (wave w: C/4 positions over every dim), the blend by
+// dims (wave w: a quarter of the dims over every position).  A span of one
+// chunk is written directly; otherwise each chunk writes a partial (blend,
+// peak, total) and attend_fold_kernel folds them in one memory round trip.
+//
+// (Measured on the box, one launch pair inside a graph: a 512-position
+// sliding window of 256-dim heads takes 9.5 us, of which 4.9 us is the chunk
+// kernel and 1.55 us the bare cost of each dependent launch; the former form,
+// one wave per 32 positions over every dim with a cross-wave merge, took 6.9
+// us for the same chunks.  A last-workgroup fold in the same kernel, after an
+// agent-scope release/acquire ticket, was slower at every chunk count tried:
+// 10.5 us at 8 chunks, over 100 us at 256.)
 #include <mutex>
 
 #include "igl_backend.h"
@@ -46,12 +52,10 @@
 
 namespace igl {
 
-constexpr int kAttendTile = 32;                    // positions per wave
-// Waves a workgroup (its chunk: 32 positions a wave), by the longest span a
-// launch covers: one up to kAttendShortSpan positions (the most workgroups,
-// the shortest chain each), four beyond (fewer partials to write and merge: at
-// 16384 positions four measured 14.7 us against 20.4 us for one).
-constexpr int kAttendShortSpan = 4096;
+// Positions a chunk, by the longest span a launch covers: 32 up to
+// kAttendShortSpan (the most workgroups, the shortest chain each), 64 beyond
+// (half the partials: at 16384 positions 11.4 us against 13.0 us for 32).
+constexpr int kAttendShortSpan = 8192;
 constexpr int kAttendGroup = 8;                    // query heads per key/value head
 
 struct AttendArgs {
@@ -108,71 +112,63 @@ __device__ __forceinline__ float xsum32(float v) {
   return lo + hi;
 }
 
-// One workgroup takes one chunk of kChunk positions of one lane; each wave
-// owns 32 positions of it.  The query, key and value loads all go out first, so the
-// launch pays one memory round trip; then the scores, the wave's softmax
-// against its own peak, and the blend.  The waves merge in LDS.  A
-// workgroup that covers the lane's whole span writes the blend; otherwise it
-// writes a partial (blend, peak, total) for attend_merge_kernel.
-//
-// (Measured: the last workgroup to finish merging the partials itself, after
-// an agent-scope release/acquire ticket, was slower than the merge launch at
-// every span tried, 15 vs 13 us at a 512 window and 52 vs 29 us at 2300
-// positions of 512 dims: one CU then reads every partial.)
-template <int HEAD, int FMT, bool QVEC, int W>
-__global__ __launch_bounds__(64 * W) void attend_mfma_kernel(AttendArgs a) {
-  constexpr int kThreads = 64 * W;            // W waves
-  constexpr int kChunk = kAttendTile * W;     // positions a workgroup
+// The split form.  A workgroup of four waves takes a chunk of C positions
+// (32 or 64) of one lane.  The two products are split differently among the
+// waves, so that each wave's dependent chain is a quarter of the chunk's work:
+//   scores: wave w takes positions w*C/4 .. (w+1)*C/4 - 1 over every dim (its
+//           key rows straight into MFMA operand order, as above);
+//   blend:  wave w takes dims w*HEAD/4 .. (w+1)*HEAD/4 - 1 over every position
+//           of the chunk (its slice of each value row staged in its own LDS).
+// Between the two, the probabilities (against each wave's own peak) and the
+// waves' peaks and sums go through LDS: one barrier.  Each wave then owns its
+// dims of the output outright, so nothing is merged across waves.
+template <int HEAD, int FMT, int C, bool QVEC>
+__global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
+  constexpr int W = 4;                // waves
+  constexpr int PW = C / W;           // positions a wave scores: 8 or 16
+  constexpr int DS = HEAD / W;        // dims a wave blends: 64 or 128
   constexpr int S = HEAD / 32;        // k-steps of the score product
   constexpr int QD = HEAD / 4;        // bytes of a key row one lane group reads
-  constexpr int TILES = HEAD / 16;    // 16-wide dim tiles of the blend
-  constexpr int QUADS = TILES / 4;    // four tiles share one LDS read
-  constexpr int VPITCH = HEAD + 8;    // staged value row: (HEAD/4 + 2) dwords, conflict-free reads
-  constexpr int kWaveV = kAttendTile * VPITCH;
+  constexpr int QUADS = DS / 64;      // 64-dim groups of a wave's blend
+  constexpr int KS = C / 32;          // k-steps of the blend (32 positions each)
+  constexpr int VP = DS + 8;          // staged value row pitch in bytes (8-byte aligned rows)
+  constexpr int LPR = DS / 16;        // lanes that load one value row (16 bytes each)
+  constexpr int RPI = 64 / LPR;       // value rows one load instruction covers
+  constexpr int VL = C / RPI;         // value loads a lane issues
+  static_assert(PW == 8 || PW == 16, "chunk of 32 or 64 positions");
 
-  __shared__ __attribute__((aligned(16))) uint8_t vs[W * kWaveV];
-  __shared__ float ps[W][kAttendGroup][kAttendTile];
+  __shared__ half8_t qs[2][kAttendGroup][HEAD / 8];
+  __shared__ float ps[kAttendGroup][C];
   __shared__ float wm[W][kAttendGroup];
   __shared__ float wl[W][kAttendGroup];
-  __shared__ float head_peak[kAttendGroup];
-  __shared__ float head_norm[kAttendGroup];
-  // the query block as binary16 operands: [part hi / lo][head][HEAD / 8]
-  __shared__ half8_t qs[2][kAttendGroup][HEAD / 8];
+  __shared__ __attribute__((aligned(16))) uint8_t vs[W][C * VP];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int g = lane >> 4;        // lane group
-  const int n = lane & 15;        // MFMA row (A) / column (B, D)
+  const int g = lane >> 4;
+  const int n = lane & 15;
   const int kv = blockIdx.y;
   const int head0 = kv * kAttendGroup;
   const int block = blockIdx.x;
   const int lane_id = blockIdx.z;
-  // The lane's visible positions: the last `window` up to and including its
-  // own (session_attend 11516-11526); `start` is the first, ring slot p % span.
   const int pos = (a.place_dev ? *a.place_dev : a.place0) + lane_id;
   const int span_count = a.window > 0 ? min(pos + 1, a.window) : pos + 1;
   const int place_start = pos - span_count + 1;
-  const int blocks_seen = (span_count + kChunk - 1) / kChunk;
-  if (block >= blocks_seen) return;  // past this lane's span
+  if (block >= (span_count + C - 1) / C) return;  // past this lane's span: the whole workgroup
   const int pc = lane_id * a.chunks + block;
   const size_t kv_off = (size_t)kv * HEAD;
-  const int t0 = block * kChunk + wave * kAttendTile;
-  const bool live = t0 < span_count;
+  const int c0 = block * C;  // the chunk's first position (relative to place_start)
 
-  // ---- loads.  The query block (8 heads x HEAD floats) is split among the
-  // workgroup's threads, eight floats each, to be converted once; key rows n
-  // and n + 16 of the wave's 32, bytes QD g .. QD g + QD - 1 (operand order);
-  // value rows lane / 2, half lane & 1.  Rows past the span repeat the last.
-  constexpr int kQTotal = kAttendGroup * HEAD / 8;                 // eight-float items
-  constexpr int kQItems = (kQTotal + kThreads - 1) / kThreads;
+  // ---- loads, all issued before the first wait
+  constexpr int kQTotal = kAttendGroup * HEAD / 8;
+  constexpr int kQItems = kQTotal / 256;
   float qf[kQItems][8];
   {
     const float *qb = a.query + (size_t)lane_id * a.q_stride + (size_t)head0 * HEAD;
 #pragma unroll
     for (int i = 0; i < kQItems; ++i) {
-      const int item = tid + kThreads * i;
-      const float *q = qb + 8 * (kQTotal % kThreads == 0 ? item : min(item, kQTotal - 1));
+      const float *q = qb + 8 * (tid + 256 * i);
       if (QVEC) {
         const float4_t u = *reinterpret_cast<const float4_t *>(q);
         const float4_t v = *reinterpret_cast<const float4_t *>(q + 4);
@@ -184,28 +180,29 @@ __global__ __launch_bounds__(64 * W) void attend_mfma_kernel(AttendArgs a) {
       }
     }
   }
-  uint4_t kr[2][QD / 16];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int t = min(t0 + n + 16 * j, span_count - 1);
+  // key row: position c0 + wave*PW + (n % PW), bytes QD*g .. QD*g + QD - 1
+  const int tk = c0 + wave * PW + (n % PW);
+  uint4_t kr[QD / 16];
+  {
+    const int t = min(tk, span_count - 1);
     const int slot = (place_start + t) % a.cache_span;
     const uint4_t *row =
         reinterpret_cast<const uint4_t *>(a.key_store + (size_t)slot * a.kv_width + kv_off + QD * g);
 #pragma unroll
-    for (int q = 0; q < QD / 16; ++q) kr[j][q] = __builtin_nontemporal_load(row + q);
+    for (int q = 0; q < QD / 16; ++q) kr[q] = __builtin_nontemporal_load(row + q);
   }
-  uint2_t vr[HEAD / 16];
-  {
-    const int t = min(t0 + (lane >> 1), span_count - 1);
-    const int slot = (place_start + t) % a.cache_span;
-    const uint2_t *src = reinterpret_cast<const uint2_t *>(
-        a.value_store + (size_t)slot * a.kv_width + kv_off + (lane & 1) * (HEAD / 2));
+  // value rows: row (lane / LPR) + RPI*i of the chunk, bytes of dims
+  // wave*DS + 16*(lane % LPR) .. + 15
+  uint4_t vr[VL];
 #pragma unroll
-    for (int q = 0; q < HEAD / 16; ++q) vr[q] = __builtin_nontemporal_load(src + q);
+  for (int i = 0; i < VL; ++i) {
+    const int t = min(c0 + lane / LPR + RPI * i, span_count - 1);
+    const int slot = (place_start + t) % a.cache_span;
+    vr[i] = __builtin_nontemporal_load(reinterpret_cast<const uint4_t *>(
+        a.value_store + (size_t)slot * a.kv_width + kv_off + wave * DS + 16 * (lane % LPR)));
   }
 
-  // query operands: x = hi + lo, each rounded to binary16 (|lo| <= 2^-11 |x|);
-  // row n of the score product is head n & 7, its hi part (n < 8) or lo part
+  // query operands, x = hi + lo in binary16
 #pragma unroll
   for (int i = 0; i < kQItems; ++i) {
     half8_t hi8, lo8;
@@ -215,259 +212,218 @@ __global__ __launch_bounds__(64 * W) void attend_mfma_kernel(AttendArgs a) {
       hi8[e] = hi;
       lo8[e] = (_Float16)(qf[i][e] - (float)hi);
     }
-    const int item = tid + kThreads * i;  // head item / (HEAD / 8), chunk item % (HEAD / 8)
-    if (kQTotal % kThreads == 0 || item < kQTotal) {
-      qs[0][item / (HEAD / 8)][item % (HEAD / 8)] = hi8;
-      qs[1][item / (HEAD / 8)][item % (HEAD / 8)] = lo8;
+    const int item = tid + 256 * i;
+    qs[0][item / (HEAD / 8)][item % (HEAD / 8)] = hi8;
+    qs[1][item / (HEAD / 8)][item % (HEAD / 8)] = lo8;
+  }
+  __syncthreads();
+
+  // ---- scores of the wave's PW positions for the 8 heads, all dims
+  float sc[4];
+  float m_w[4];
+  {
+    float4_t sacc = float4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const half8_t qa = qs[n >> 3][n & 7][QD * g / 8 + s];
+      const uint4_t w = kr[s >> 1];
+      const half8_t kb = (s & 1) ? decode8<FMT>(w[2], w[3]) : decode8<FMT>(w[0], w[1]);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, kb, sacc, 0, 0, 0);
+    }
+    const bool valid = n < PW && tk < span_count;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float v = xsum32(sacc[r]);
+      sc[r] = valid ? v * a.key_scale : -INFINITY;
+      m_w[r] = row16_max(sc[r]);
+    }
+  }
+  // probabilities against the wave's peak, and the wave's sums
+  {
+    float l_w[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float p = m_w[r] != -INFINITY && sc[r] != -INFINITY ? __expf(sc[r] - m_w[r]) : 0.0f;
+      l_w[r] = row16_sum(p);
+      if (g < 2 && n < PW) ps[4 * g + r][wave * PW + n] = p;
+    }
+    if (g < 2 && n == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        wm[wave][4 * g + r] = m_w[r];
+        wl[wave][4 * g + r] = l_w[r];
+      }
+    }
+  }
+  // the wave's value slice into its own LDS rows
+  {
+    uint8_t *vw = vs[wave];
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      uint2_t *dst = reinterpret_cast<uint2_t *>(vw + (lane / LPR + RPI * i) * VP + 16 * (lane % LPR));
+      dst[0] = uint2_t{vr[i][0], vr[i][1]};
+      dst[1] = uint2_t{vr[i][2], vr[i][3]};
     }
   }
   __syncthreads();
-  half8_t qa[S];
-#pragma unroll
-  for (int s = 0; s < S; ++s) qa[s] = qs[n >> 3][n & 7][QD * g / 8 + s];
 
-  // ---- scores.  After the half-wave sum, lane groups 0/2 hold heads 0-3 and
-  // 1/3 heads 4-7 (row r of the group is head 4 (g & 1) + r), for positions
-  // n and n + 16 of the wave's 32.
-  float sc[2][4];
-  float m_w[4];
-  {
-    float4_t sacc[2] = {float4_t{0, 0, 0, 0}, float4_t{0, 0, 0, 0}};
-    if (live) {
+  // ---- blend of the wave's dims over the chunk's positions.  A = the
+  // probabilities (row n: head n & 7, hi part for n < 8, lo part otherwise;
+  // k = positions 8g .. 8g + 7 of the k-step), each scaled by e^(m_w - M),
+  // M the chunk's peak of the head.
+  const int hh = n & 7;
+  float M = wm[0][hh];
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+  for (int w = 1; w < W; ++w) M = fmaxf(M, wm[w][hh]);
+  float4_t o[4 * QUADS];
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-          const uint4_t w = kr[j][s >> 1];
-          const half8_t kb = (s & 1) ? decode8<FMT>(w[2], w[3]) : decode8<FMT>(w[0], w[1]);
-          sacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kb, sacc[j], 0, 0, 0);
-        }
-    }
+  for (int t = 0; t < 4 * QUADS; ++t) o[t] = float4_t{0, 0, 0, 0};
+  const uint8_t *vw = vs[wave];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float s0 = xsum32(sacc[0][r]);
-      float s1 = xsum32(sacc[1][r]);
-      s0 = (t0 + n < span_count) ? s0 * a.key_scale : -INFINITY;
-      s1 = (t0 + n + 16 < span_count) ? s1 * a.key_scale : -INFINITY;
-      sc[0][r] = s0;
-      sc[1][r] = s1;
-      m_w[r] = row16_max(fmaxf(s0, s1));
-    }
-  }
-
-  // ---- probabilities against the wave's peak; the blend with A =
-  // probabilities (row n: head n & 7, hi/lo), k = positions 8g .. 8g+7.
-  float l_w[4];
-  float4_t o[TILES];
+  for (int ks = 0; ks < KS; ++ks) {
+    const int p0 = 32 * ks + 8 * g;  // the lane's first position of the k-step
+    const float mw = wm[p0 / PW][hh];
+    const float f = mw != -INFINITY ? __expf(mw - M) : 0.0f;
+    half8_t pa;
+    {
+      const float *src = &ps[hh][p0];
 #pragma unroll
-  for (int t = 0; t < TILES; ++t) o[t] = float4_t{0, 0, 0, 0};
-  uint8_t *vw = vs + wave * kWaveV;
-  {
-    float p[2][4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[0][r] = live ? __expf(sc[0][r] - m_w[r]) : 0.0f;
-      p[1][r] = live ? __expf(sc[1][r] - m_w[r]) : 0.0f;
-      l_w[r] = row16_sum(p[0][r] + p[1][r]);
-    }
-    if (g < 2) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        ps[wave][4 * g + r][n] = p[0][r];
-        ps[wave][4 * g + r][n + 16] = p[1][r];
+      for (int e = 0; e < 8; ++e) {
+        const float v = src[e] * f;
+        const _Float16 hi = (_Float16)v;
+        pa[e] = n >= 8 ? (_Float16)(v - (float)hi) : hi;
       }
     }
-    if (live) {
-      uint2_t *dst = reinterpret_cast<uint2_t *>(vw + (lane >> 1) * VPITCH + (lane & 1) * (HEAD / 2));
 #pragma unroll
-      for (int q = 0; q < HEAD / 16; ++q) dst[q] = vr[q];
-    }
-    // Only this wave's rows of `ps` and `vs` are read below: a wave barrier.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (live) {
-      half8_t pa;
-      {
-        const float *src = &ps[wave][n & 7][8 * g];
-        const bool lo_part = n >= 8;
+    for (int qd = 0; qd < QUADS; ++qd) {
+      uint32_t dw[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float v = src[e];
-          const _Float16 hi = (_Float16)v;
-          pa[e] = lo_part ? (_Float16)(v - (float)hi) : hi;
-        }
-      }
+      for (int e = 0; e < 8; ++e)
+        dw[e] = *reinterpret_cast<const uint32_t *>(vw + (p0 + e) * VP + 64 * qd + 4 * n);
 #pragma unroll
-      for (int qd = 0; qd < QUADS; ++qd) {
-        uint32_t dw[8];
+      for (int t = 0; t < 4; ++t) {
+        uint32_t w[4];
+        const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + t) << 16) | (uint32_t)t;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          dw[e] = *reinterpret_cast<const uint32_t *>(vw + (8 * g + e) * VPITCH + 64 * qd + 4 * n);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          uint32_t w[4];
-          const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + t) << 16) | (uint32_t)t;
-#pragma unroll
-          for (int pr = 0; pr < 4; ++pr)
-            w[pr] = decode_pair<FMT>(__builtin_amdgcn_perm(dw[2 * pr + 1], dw[2 * pr], sel));
-          o[4 * qd + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, __builtin_bit_cast(half8_t, w),
-                                                                 o[4 * qd + t], 0, 0, 0);
-        }
+        for (int pr = 0; pr < 4; ++pr)
+          w[pr] = decode_pair<FMT>(__builtin_amdgcn_perm(dw[2 * pr + 1], dw[2 * pr], sel));
+        o[4 * qd + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, __builtin_bit_cast(half8_t, w),
+                                                               o[4 * qd + t], 0, 0, 0);
       }
     }
   }
-  // hi + lo rows
+  // hi + lo rows; lanes g < 2 hold head 4g + r, dims wave*DS + 64qd + 4n + t
 #pragma unroll
-  for (int t = 0; t < TILES; ++t)
+  for (int t = 0; t < 4 * QUADS; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) o[t][r] = xsum32(o[t][r]);
-  if (g < 2 && n == 0) {
+  if (g >= 2) return;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      wm[wave][4 * g + r] = m_w[r];
-      wl[wave][4 * g + r] = l_w[r];
-    }
-  }
-
-  // ---- merge the W waves: scale each by e^(m_w - M) per head.
-  __syncthreads();  // wm, wl written and every wave done with vs, reused as float[W][8][HEAD]
-  auto peak_of = [&](int h) {
-    float M = wm[0][h];
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * g + r;
+    float Mh = wm[0][h];
 #pragma unroll
-    for (int w = 1; w < W; ++w) M = fmaxf(M, wm[w][h]);
-    return M;
-  };
-  if (tid < kAttendGroup) {
-    const int h = tid;
-    const float M = peak_of(h);
+    for (int w = 1; w < W; ++w) Mh = fmaxf(Mh, wm[w][h]);
     float L = 0.0f;
 #pragma unroll
     for (int w = 0; w < W; ++w)
-      if (wm[w][h] != -INFINITY) L += wl[w][h] * __expf(wm[w][h] - M);
-    head_peak[h] = M;
-    head_norm[h] = L;
-  }
-  float *ob = reinterpret_cast<float *>(vs);
-  {
-    float scale[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int h = 4 * (g & 1) + r;
-      const float M = peak_of(h);
-      scale[r] = m_w[r] != -INFINITY ? __expf(m_w[r] - M) : 0.0f;
+      if (wm[w][h] != -INFINITY) L += wl[w][h] * __expf(wm[w][h] - Mh);
+    float *dst;
+    float mul;
+    if (a.final_out) {
+      dst = a.final_out + (size_t)lane_id * a.q_stride + (size_t)(head0 + h) * HEAD + wave * DS + 4 * n;
+      mul = L > 0.0f ? a.value_scale * (1.0f / L) : 0.0f;
+    } else {
+      dst = a.part_out + ((size_t)pc * a.head_count + head0 + h) * HEAD + wave * DS + 4 * n;
+      mul = a.value_scale;
+      if (wave == 0 && n == 0) {
+        a.part_peak[(size_t)pc * a.head_count + head0 + h] = Mh;
+        a.part_total[(size_t)pc * a.head_count + head0 + h] = L;
+      }
     }
-    if (g < 2) {
 #pragma unroll
-      for (int qd = 0; qd < QUADS; ++qd)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            ob[(wave * kAttendGroup + 4 * g + r) * HEAD + 64 * qd + 4 * n + t] = o[4 * qd + t][r] * scale[r];
-    }
-  }
-  __syncthreads();
-  if (a.final_out) {
-    // The block saw every visible position: normalize and write the blend.
-    float *out = a.final_out + (size_t)lane_id * a.q_stride + (size_t)head0 * HEAD;
-    for (int i = tid; i < kAttendGroup * HEAD; i += kThreads) {
-      const int h = i / HEAD;
-      const int d = i - h * HEAD;
-      const float L = head_norm[h];
-      float v = ob[h * HEAD + d];
-#pragma unroll
-      for (int w = 1; w < W; ++w) v += ob[(w * kAttendGroup + h) * HEAD + d];
-      out[(size_t)h * HEAD + d] = L > 0.0f ? v * a.value_scale * (1.0f / L) : 0.0f;
-    }
-    return;
-  }
-  for (int i = tid; i < kAttendGroup * HEAD; i += kThreads) {
-    const int h = i / HEAD;
-    const int d = i - h * HEAD;
-    float v = ob[h * HEAD + d];
-#pragma unroll
-    for (int w = 1; w < W; ++w) v += ob[(w * kAttendGroup + h) * HEAD + d];
-    a.part_out[((size_t)pc * a.head_count + head0 + h) * HEAD + d] = v * a.value_scale;
-  }
-  if (tid < kAttendGroup) {
-    a.part_peak[(size_t)pc * a.head_count + head0 + tid] = head_peak[tid];
-    a.part_total[(size_t)pc * a.head_count + head0 + tid] = head_norm[tid];
+    for (int qd = 0; qd < QUADS; ++qd)
+      *reinterpret_cast<float4_t *>(dst + 64 * qd) =
+          float4_t{o[4 * qd][r] * mul, o[4 * qd + 1][r] * mul, o[4 * qd + 2][r] * mul, o[4 * qd + 3][r] * mul};
   }
 }
 
-// Merges chunk partials.  One workgroup per (head, lane, 64 dims): the
-// chunk weights e^(peak_c - peak) once in LDS, then thread (d, slice) sums
-// chunks c = slice (mod 4) of dim d, 32 loads in flight, and the four slices
-// are added in a fixed order, so the result does not depend on timing.
-__global__ __launch_bounds__(256) void attend_merge_kernel(const float *part_out_all,
-                                                           const float *part_peak_all,
-                                                           const float *part_total_all,
-                                                           int chunk_slots, int chunk,
-                                                           int place0, const int *place_dev,
-                                                           int window, int head_count,
-                                                           int head_size, float *blend_all,
-                                                           int o_stride) {
-  extern __shared__ float wgt[];  // [chunks]
-  __shared__ float red[4];
-  __shared__ float slice_sum[4][64];
-  const int h = blockIdx.x;
-  const int lane_id = blockIdx.y;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+// Folds chunk partials in one memory round trip.  A workgroup per (head, lane,
+// DIMS dims) of 256 threads: thread (d, s) loads, for up to PER chunks
+// c = s, s + 256/DIMS, ..., its dim's partial and the chunk's peak and total
+// together; the slices' peaks meet in LDS (the head's peak M), each thread
+// weights its chunks by e^(peak_c - M), and the slices' sums meet in LDS in a
+// fixed order.  Spans of more chunks than one pass holds take further passes,
+// each rescaled to the running peak.
+template <int DIMS, int PER>
+__global__ __launch_bounds__(256) void attend_fold_kernel(const float *part_out_all,
+                                                          const float *part_peak_all,
+                                                          const float *part_total_all,
+                                                          int chunk_slots, int chunk, int place0,
+                                                          const int *place_dev, int window,
+                                                          int head_count, int head_size,
+                                                          float *blend_all, int o_stride) {
+  constexpr int SL = 256 / DIMS;
+  __shared__ float red_m[SL];
+  __shared__ float red_a[SL][DIMS];
+  __shared__ float red_l[SL];
+  const int h = blockIdx.x, lane_id = blockIdx.y, tid = threadIdx.x;
+  const int d = tid % DIMS, sl = tid / DIMS;
   const int pos = (place_dev ? *place_dev : place0) + lane_id;
   const int span = window > 0 ? min(pos + 1, window) : pos + 1;
-  // the workgroups that saw part of this lane's span
   const int chunks = (span + chunk - 1) / chunk;
   const size_t base = (size_t)lane_id * chunk_slots;
-  const float *part_out = part_out_all + base * head_count * head_size;
-  const float *part_peak = part_peak_all + base * head_count;
-  const float *part_total = part_total_all + base * head_count;
-  float *blend_out = blend_all + (size_t)lane_id * o_stride;
-  float peak = -INFINITY;
-  for (int c = tid; c < chunks; c += 256) peak = fmaxf(peak, part_peak[(size_t)c * head_count + h]);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) peak = fmaxf(peak, __shfl_xor(peak, o));
-  if ((tid & 63) == 0) red[wave] = peak;
-  __syncthreads();
-  peak = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-  float total = 0.0f;
-  for (int c = tid; c < chunks; c += 256) {
-    const float m = part_peak[(size_t)c * head_count + h];
-    const float wv = m == -INFINITY ? 0.0f : __expf(m - peak);
-    wgt[c] = wv;
-    total += wv * part_total[(size_t)c * head_count + h];
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) total += __shfl_xor(total, o);
-  if ((tid & 63) == 0) red[wave] = total;
-  __syncthreads();  // also: wgt complete
-  total = ((red[0] + red[1]) + red[2]) + red[3];
-  const float inv = total > 0.0f ? 1.0f / total : 0.0f;
-  const int d = blockIdx.z * 64 + (tid & 63);
-  const int slice = wave;
-  const float *col = part_out + (size_t)h * head_size + d;
   const size_t step = (size_t)head_count * head_size;
-  // 32 chunks of the slice at a time, every load issued before the sums
-  // (past the end: the last chunk again, weight 0)
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int c0 = slice; c0 < chunks; c0 += 128) {
-    float v[32];
+  const float *pout = part_out_all + base * step + (size_t)h * head_size + blockIdx.z * DIMS + d;
+  const float *ppk = part_peak_all + base * head_count + h;
+  const float *ptt = part_total_all + base * head_count + h;
+  float run_m = -INFINITY, acc = 0.0f, tot = 0.0f;
+  for (int c0 = 0; c0 < chunks; c0 += SL * PER) {
+    float v[PER], m[PER], l[PER];
 #pragma unroll
-    for (int u = 0; u < 32; ++u) v[u] = col[(size_t)min(c0 + 4 * u, chunks - 1) * step];
+    for (int u = 0; u < PER; ++u) {
+      const int c = min(c0 + sl + SL * u, chunks - 1);
+      v[u] = pout[(size_t)c * step];
+      m[u] = ppk[(size_t)c * head_count];
+      l[u] = ptt[(size_t)c * head_count];
+    }
+    float mx = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < 32; ++u) {
-      const int c = c0 + 4 * u;
-      acc[u & 7] += (c < chunks ? wgt[c] : 0.0f) * v[u];
+    for (int u = 0; u < PER; ++u)
+      if (c0 + sl + SL * u < chunks) mx = fmaxf(mx, m[u]);
+    __syncthreads();  // red_m of the previous pass read by every thread
+    if (d == 0) red_m[sl] = mx;
+    __syncthreads();
+    float M = run_m;
+#pragma unroll
+    for (int i = 0; i < SL; ++i) M = fmaxf(M, red_m[i]);
+    if (M != -INFINITY && run_m != -INFINITY && M != run_m) {
+      const float f = __expf(run_m - M);
+      acc *= f;
+      tot *= f;
+    }
+    run_m = M;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const bool in = c0 + sl + SL * u < chunks && m[u] != -INFINITY;
+      const float w = in ? __expf(m[u] - M) : 0.0f;
+      acc += w * v[u];
+      tot += w * l[u];
     }
   }
-  slice_sum[slice][tid & 63] =
-      ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  red_a[sl][d] = acc;
+  if (d == 0) red_l[sl] = tot;
   __syncthreads();
-  if (slice == 0 && d < head_size)
-    blend_out[(size_t)h * head_size + d] =
-        (((slice_sum[0][tid] + slice_sum[1][tid]) + slice_sum[2][tid]) + slice_sum[3][tid]) * inv;
+  if (sl == 0) {
+    float A = 0.0f, T = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+      A += red_a[i][d];
+      T += red_l[i];
+    }
+    blend_all[(size_t)lane_id * o_stride + (size_t)h * head_size + blockIdx.z * DIMS + d] =
+        T > 0.0f ? A * (1.0f / T) : 0.0f;
+  }
 }
 
 }  // namespace igl
@@ -479,21 +435,29 @@ static int attend_max_span(int place0, int window, int lanes) {
   return window > 0 ? (last < window ? last : window) : last;
 }
 
-static int attend_waves(int place0, int window, int lanes) {
-  return attend_max_span(place0, window, lanes) <= kAttendShortSpan ? 1 : 4;
+static int attend_chunk(int place0, int window, int lanes) {
+  return attend_max_span(place0, window, lanes) <= kAttendShortSpan ? 32 : 64;
 }
 
 static int attend_blocks(int place0, int window, int lanes) {
-  const int chunk = attend_waves(place0, window, lanes) * kAttendTile;
+  const int chunk = attend_chunk(place0, window, lanes);
   return (attend_max_span(place0, window, lanes) + chunk - 1) / chunk;
 }
 
-template <int HEAD, int FMT, int W>
+template <int HEAD, int FMT, int C>
 static void attend_launch(const AttendArgs &a, dim3 grid, bool qvec, hipStream_t stream) {
   if (qvec)
-    hipLaunchKernelGGL((attend_mfma_kernel<HEAD, FMT, true, W>), grid, dim3(64 * W), 0, stream, a);
+    hipLaunchKernelGGL((attend_split_kernel<HEAD, FMT, C, true>), grid, dim3(256), 0, stream, a);
   else
-    hipLaunchKernelGGL((attend_mfma_kernel<HEAD, FMT, false, W>), grid, dim3(64 * W), 0, stream, a);
+    hipLaunchKernelGGL((attend_split_kernel<HEAD, FMT, C, false>), grid, dim3(256), 0, stream, a);
+}
+
+template <int HEAD, int FMT>
+static void attend_launch_chunk(const AttendArgs &a, dim3 grid, int chunk, bool qvec, hipStream_t stream) {
+  if (chunk == 32)
+    attend_launch<HEAD, FMT, 32>(a, grid, qvec, stream);
+  else
+    attend_launch<HEAD, FMT, 64>(a, grid, qvec, stream);
 }
 
 // `lanes` query lanes at positions place0 .. place0 + lanes - 1, each seeing
@@ -510,7 +474,7 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
                                         int window, int lanes, float score_scale,
                                         float *blend_out, float *work, hipStream_t stream) {
   AttendArgs a;
-  const int waves = attend_waves(place0, window, lanes);
+  const int chunk = attend_chunk(place0, window, lanes);
   const int chunks = attend_blocks(place0, window, lanes);  // workgroups a lane
   const int head_count = kv_count * group_share;
   if (group_share != kAttendGroup || lanes < 1) return hipErrorInvalidValue;
@@ -537,21 +501,44 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
   dim3 grid(chunks, kv_count, lanes);
   const bool qvec = (((uintptr_t)query) & 15u) == 0 && (q_stride & 3) == 0;
   if (head_size == 256 && fmt == 0)
-    waves == 1 ? attend_launch<256, 0, 1>(a, grid, qvec, stream) : attend_launch<256, 0, 4>(a, grid, qvec, stream);
+    attend_launch_chunk<256, 0>(a, grid, chunk, qvec, stream);
   else if (head_size == 256 && fmt == 1)
-    waves == 1 ? attend_launch<256, 1, 1>(a, grid, qvec, stream) : attend_launch<256, 1, 4>(a, grid, qvec, stream);
+    attend_launch_chunk<256, 1>(a, grid, chunk, qvec, stream);
   else if (head_size == 512 && fmt == 0)
-    waves == 1 ? attend_launch<512, 0, 1>(a, grid, qvec, stream) : attend_launch<512, 0, 4>(a, grid, qvec, stream);
+    attend_launch_chunk<512, 0>(a, grid, chunk, qvec, stream);
   else if (head_size == 512 && fmt == 1)
-    waves == 1 ? attend_launch<512, 1, 1>(a, grid, qvec, stream) : attend_launch<512, 1, 4>(a, grid, qvec, stream);
+    attend_launch_chunk<512, 1>(a, grid, chunk, qvec, stream);
   else
     return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || chunks == 1) return e;
-  hipLaunchKernelGGL(attend_merge_kernel, dim3(head_count, lanes, (head_size + 63) / 64), dim3(256),
-                     chunks * sizeof(float), stream, a.part_out, a.part_peak, a.part_total, chunks,
-                     waves * kAttendTile, place0, place_dev, window, head_count, head_size, blend_out,
-                     q_stride);
+  // One lane: 16 dims a fold workgroup (the most workgroups); many lanes
+  // (a prime or a block): 64.  Chunks a thread loads: enough for one pass.
+  const int dims = lanes == 1 ? 16 : 64;
+  const int slices = 256 / dims;
+  int per = 1;
+  while (per < 32 && per * slices < chunks) per *= 2;
+  const dim3 fgrid(head_count, lanes, head_size / dims);
+#define IGL_FOLD(D, P)                                                                             \
+  hipLaunchKernelGGL((attend_fold_kernel<D, P>), fgrid, dim3(256), 0, stream, a.part_out,         \
+                     a.part_peak, a.part_total, chunks, chunk, place0, place_dev, window,          \
+                     head_count, head_size, blend_out, q_stride)
+#define IGL_FOLD_PER(D)                                                                            \
+  switch (per) {                                                                                   \
+    case 1: IGL_FOLD(D, 1); break;                                                                 \
+    case 2: IGL_FOLD(D, 2); break;                                                                 \
+    case 4: IGL_FOLD(D, 4); break;                                                                 \
+    case 8: IGL_FOLD(D, 8); break;                                                                 \
+    case 16: IGL_FOLD(D, 16); break;                                                               \
+    default: IGL_FOLD(D, 32); break;                                                               \
+  }
+  if (dims == 16) {
+    IGL_FOLD_PER(16)
+  } else {
+    IGL_FOLD_PER(64)
+  }
+#undef IGL_FOLD_PER
+#undef IGL_FOLD
   return hipGetLastError();
 }
 
@@ -564,10 +551,10 @@ extern "C" size_t igl_attend_work_floats(int place0, int window, int lanes, int 
 
 // Floats of workspace enough for every igl_launch_attend call of at most
 // `lanes` lanes whose spans stay within `span_limit` positions.  The chunk
-// count is not monotonic in the span: chunks are kAttendTile positions up to
-// kAttendShortSpan and four times that beyond, so a span just under
-// kAttendShortSpan has more chunks than one just over it.  The largest count
-// of each regime is taken.
+// count is not monotonic in the span: chunks are 32 positions up to
+// kAttendShortSpan and 64 beyond, so a span just under kAttendShortSpan has
+// more chunks than one just over it.  The largest count of each regime is
+// taken.
 extern "C" size_t igl_attend_work_floats_limit(int span_limit, int lanes, int head_count,
                                                int head_size) {
   if (span_limit < 1 || lanes < 1) return 0;

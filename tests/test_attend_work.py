@@ -1,9 +1,9 @@
 """CPU check of the attention workspace the engine allocates at open.
 
 The decode attention writes one partial per (lane, chunk, head).  Its chunk
-count is not monotonic in the span (32-position chunks up to 4096 positions,
-128-position chunks beyond), so a batch whose last position lands just under
-4096 needs more partials than a decode step at the last position of a longer
+count is not monotonic in the span (32-position chunks up to 8192 positions,
+64-position chunks beyond), so a batch whose last position lands just under
+8192 needs more partials than a decode step at the last position of a longer
 window.  The engine sizes the buffer with igl_attend_work_floats_limit; this
 replays every (position, lanes) pair a prime, a speculative block or a decode
 step can launch with, and checks each launch's need against that size.  Pure
@@ -28,7 +28,7 @@ def lib():
     return lib
 
 
-@pytest.mark.parametrize("window_limit", [4097, 8192, 16000])
+@pytest.mark.parametrize("window_limit", [4097, 8192, 8193, 12000, 16000])
 @pytest.mark.parametrize("lane_limit", [16, 2048])
 def test_every_launch_fits_the_engine_allocation(lib, window_limit, lane_limit):
     have = lib.igl_attend_work_floats_limit(window_limit, lane_limit, HEADS, HEAD)
@@ -43,13 +43,13 @@ def test_every_launch_fits_the_engine_allocation(lib, window_limit, lane_limit):
     assert worst <= have, (worst, have)
 
 
-def test_former_sizing_fell_short(lib):
-    """The sizing the engine used before (a decode step at the last position, or
-    a full batch ending there) is smaller than a 16-lane batch ending just under
-    4096 positions in an 8192-position window: the case the limit covers."""
-    W, lanes = 8192, 16
+def test_longest_span_alone_falls_short(lib):
+    """Sizing by a decode step at the last position, or by a full batch ending
+    there, is smaller than a 16-lane batch ending at position 8191 of a
+    12000-position window: the case the limit covers."""
+    W, lanes = 12000, 16
     one = lib.igl_attend_work_floats(W - 1, 0, 1, HEADS, HEAD)
     many = lib.igl_attend_work_floats(W - lanes, 0, lanes, HEADS, HEAD)
-    need = lib.igl_attend_work_floats(4096 - lanes, 0, lanes, HEADS, HEAD)
+    need = lib.igl_attend_work_floats(8192 - lanes, 0, lanes, HEADS, HEAD)
     assert need > max(one, many)
     assert need <= lib.igl_attend_work_floats_limit(W, lanes, HEADS, HEAD)
