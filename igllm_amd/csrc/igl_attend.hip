@@ -76,6 +76,23 @@ struct AttendArgs {
   float *part_peak;            // [chunks][head_count]
   float *part_total;           // [chunks][head_count]
   int head_count;
+  // The decode step's heads prepared here (attend_split_kernel's PREP form):
+  // `query` holds the query heads before their norm; q_gain their gain; turn
+  // the (cos, sin) of the lane's position times each rotation step, HEAD / 2
+  // pairs.  With k_raw set, the workgroup whose chunk holds the lane's
+  // position also prepares its key and value heads (norm and gain and turn;
+  // norm) and writes their bytes into ring slot position % cache_span of
+  // k_ring / v_ring (the rings read here), code = e4m3(value / scale).
+  const float *q_gain;
+  const float *turn;           // [HEAD / 2][2]
+  const float *k_raw;
+  const float *v_raw;
+  const float *k_gain;
+  uint8_t *k_ring;
+  uint8_t *v_ring;
+  float k_code_scale;
+  float v_code_scale;
+  float eps;
 };
 
 // Two bytes held in bits [0,8) and [16,24) of `x`, as two exact binary16.
@@ -122,7 +139,7 @@ __device__ __forceinline__ float xsum32(float v) {
 // Between the two, the probabilities (against each wave's own peak) and the
 // waves' peaks and sums go through LDS: one barrier.  Each wave then owns its
 // dims of the output outright, so nothing is merged across waves.
-template <int HEAD, int FMT, int C, bool QVEC>
+template <int HEAD, int FMT, int C, bool QVEC, bool PREP>
 __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
   constexpr int W = 4;                // waves
   constexpr int PW = C / W;           // positions a wave scores: 8 or 16
@@ -136,6 +153,8 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
   constexpr int RPI = 64 / LPR;       // value rows one load instruction covers
   constexpr int VL = C / RPI;         // value loads a lane issues
   static_assert(PW == 8 || PW == 16, "chunk of 32 or 64 positions");
+  static_assert(!PREP || (FMT == 0 && QVEC), "prepared heads: e4m3 rings, aligned queries");
+  constexpr int HALF = HEAD / 2;
 
   __shared__ half8_t qs[2][kAttendGroup][HEAD / 8];
   __shared__ float ps[kAttendGroup][C];
@@ -155,8 +174,24 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
   const int pos = (a.place_dev ? *a.place_dev : a.place0) + lane_id;
   const int span_count = a.window > 0 ? min(pos + 1, a.window) : pos + 1;
   const int place_start = pos - span_count + 1;
-  if (block >= (span_count + C - 1) / C) return;  // past this lane's span: the whole workgroup
+  const int blocks_seen = (span_count + C - 1) / C;
+  if (block >= blocks_seen) return;  // past this lane's span: the whole workgroup
   const int pc = lane_id * a.chunks + block;
+  // PREP: this workgroup's chunk holds the lane's position, whose key and
+  // value rows it prepares (one key pair j, j + HALF and one value pair a
+  // thread, threads below HALF)
+  const bool row_here = PREP && a.k_raw != nullptr && block == blocks_seen - 1;
+  float kx[2] = {0.0f, 0.0f}, vx[2] = {0.0f, 0.0f}, kg[2] = {0.0f, 0.0f}, kt[2] = {0.0f, 0.0f};
+  if (row_here && tid < HALF) {
+    kx[0] = a.k_raw[tid];
+    kx[1] = a.k_raw[tid + HALF];
+    vx[0] = a.v_raw[tid];
+    vx[1] = a.v_raw[tid + HALF];
+    kg[0] = a.k_gain[tid];
+    kg[1] = a.k_gain[tid + HALF];
+    kt[0] = a.turn[2 * tid];
+    kt[1] = a.turn[2 * tid + 1];
+  }
   const size_t kv_off = (size_t)kv * HEAD;
   const int c0 = block * C;  // the chunk's first position (relative to place_start)
 
@@ -202,6 +237,83 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
         a.value_store + (size_t)slot * a.kv_width + kv_off + wave * DS + 16 * (lane % LPR)));
   }
 
+  __shared__ double kv_red[2][W];
+  __shared__ __attribute__((aligned(16))) uint8_t row_bytes[2][HEAD];
+  if (PREP) {
+    // Each head's items are 32 (HEAD 256) or 64 (HEAD 512) consecutive
+    // threads; the pair (j, j + HALF) of a dim sits HALF / 8 items apart.
+    constexpr int kHeadItems = HEAD / 8;
+#pragma unroll
+    for (int i = 0; i < kQItems; ++i) {
+      const int item = tid + 256 * i;
+      const int d0 = 8 * (item % kHeadItems);
+      double ss = 0.0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += (double)qf[i][e] * (double)qf[i][e];
+#pragma unroll
+      for (int off = kHeadItems / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+      const float shrink = rms_shrink(ss, HEAD, a.eps);
+      float own[8], other[8];
+      const float4_t g0 = *reinterpret_cast<const float4_t *>(a.q_gain + d0);
+      const float4_t g1 = *reinterpret_cast<const float4_t *>(a.q_gain + d0 + 4);
+      const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        own[e] = qf[i][e] * shrink;
+        own[e] = own[e] * gg[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) other[e] = __shfl_xor(own[e], kHeadItems / 2);
+      const bool low = d0 < HALF;
+      const int j0 = low ? d0 : d0 - HALF;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float c = a.turn[2 * (j0 + e)];
+        const float sn = a.turn[2 * (j0 + e) + 1];
+        qf[i][e] = low ? own[e] * c - other[e] * sn : own[e] * c + other[e] * sn;
+      }
+    }
+    if (row_here) {
+      // key: norm, gain, turn; value: norm (session_attend 11504-11510)
+      double ks = (double)kx[0] * (double)kx[0] + (double)kx[1] * (double)kx[1];
+      double vs2 = (double)vx[0] * (double)vx[0] + (double)vx[1] * (double)vx[1];
+      ks = wave_sum_f64_to_last(ks);
+      vs2 = wave_sum_f64_to_last(vs2);
+      if (lane == 63) {
+        kv_red[0][wave] = ks;
+        kv_red[1][wave] = vs2;
+      }
+      __syncthreads();
+      double kt_sum = kv_red[0][0], vt_sum = kv_red[1][0];
+#pragma unroll
+      for (int w = 1; w < W; ++w) {
+        kt_sum += kv_red[0][w];
+        vt_sum += kv_red[1][w];
+      }
+      if (tid < HALF) {
+        const float ksh = rms_shrink(kt_sum, HEAD, a.eps);
+        const float vsh = rms_shrink(vt_sum, HEAD, a.eps);
+        float lo = kx[0] * ksh, hi = kx[1] * ksh;
+        lo = lo * kg[0];
+        hi = hi * kg[1];
+        const float k0 = lo * kt[0] - hi * kt[1];
+        const float k1 = hi * kt[0] + lo * kt[1];
+        const uint8_t b0 = e4m3_code(k0 / a.k_code_scale), b1 = e4m3_code(k1 / a.k_code_scale);
+        const uint8_t c0b = e4m3_code(vx[0] * vsh / a.v_code_scale);
+        const uint8_t c1b = e4m3_code(vx[1] * vsh / a.v_code_scale);
+        const size_t row = (size_t)(pos % a.cache_span) * a.kv_width + kv_off;
+        a.k_ring[row + tid] = b0;
+        a.k_ring[row + tid + HALF] = b1;
+        a.v_ring[row + tid] = c0b;
+        a.v_ring[row + tid + HALF] = c1b;
+        row_bytes[0][tid] = b0;
+        row_bytes[0][tid + HALF] = b1;
+        row_bytes[1][tid] = c0b;
+        row_bytes[1][tid + HALF] = c1b;
+      }
+    }
+  }
+
   // query operands, x = hi + lo in binary16
 #pragma unroll
   for (int i = 0; i < kQItems; ++i) {
@@ -218,6 +330,11 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
   }
   __syncthreads();
 
+  // the lane's own new key row (PREP): the bytes just written, not the stale ones loaded
+  if (row_here && tk == span_count - 1) {
+#pragma unroll
+    for (int q = 0; q < QD / 16; ++q) kr[q] = *reinterpret_cast<const uint4_t *>(&row_bytes[0][QD * g + 16 * q]);
+  }
   // ---- scores of the wave's PW positions for the 8 heads, all dims
   float sc[4];
   float m_w[4];
@@ -263,6 +380,15 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
       uint2_t *dst = reinterpret_cast<uint2_t *>(vw + (lane / LPR + RPI * i) * VP + 16 * (lane % LPR));
       dst[0] = uint2_t{vr[i][0], vr[i][1]};
       dst[1] = uint2_t{vr[i][2], vr[i][3]};
+    }
+    if (row_here) {
+      // the new value row's slice replaces the stale one staged above (the
+      // staging wrote whole 8-byte words; every lane of the wave is past it)
+      __builtin_amdgcn_wave_barrier();
+      const int r = span_count - 1 - c0;
+      if (lane < DS / 8)
+        *reinterpret_cast<uint2_t *>(vw + r * VP + 8 * lane) =
+            *reinterpret_cast<const uint2_t *>(&row_bytes[1][wave * DS + 8 * lane]);
     }
   }
   __syncthreads();
@@ -447,9 +573,9 @@ static int attend_blocks(int place0, int window, int lanes) {
 template <int HEAD, int FMT, int C>
 static void attend_launch(const AttendArgs &a, dim3 grid, bool qvec, hipStream_t stream) {
   if (qvec)
-    hipLaunchKernelGGL((attend_split_kernel<HEAD, FMT, C, true>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((attend_split_kernel<HEAD, FMT, C, true, false>), grid, dim3(256), 0, stream, a);
   else
-    hipLaunchKernelGGL((attend_split_kernel<HEAD, FMT, C, false>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((attend_split_kernel<HEAD, FMT, C, false, false>), grid, dim3(256), 0, stream, a);
 }
 
 template <int HEAD, int FMT>
@@ -459,6 +585,10 @@ static void attend_launch_chunk(const AttendArgs &a, dim3 grid, int chunk, bool 
   else
     attend_launch<HEAD, FMT, 64>(a, grid, qvec, stream);
 }
+
+static hipError_t attend_fold(const AttendArgs &a, int chunks, int chunk, int place0,
+                              const int *place_dev, int window, int lanes, int head_size,
+                              float *blend_out, hipStream_t stream);
 
 // `lanes` query lanes at positions place0 .. place0 + lanes - 1, each seeing
 // the last `window` positions up to its own (0: every position from 0).  Lane
@@ -498,6 +628,9 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
   a.part_out = work;
   a.part_peak = work + slots * head_count * head_size;
   a.part_total = a.part_peak + slots * head_count;
+  a.q_gain = a.turn = a.k_raw = a.v_raw = a.k_gain = nullptr;
+  a.k_ring = a.v_ring = nullptr;
+  a.k_code_scale = a.v_code_scale = a.eps = 0.0f;
   dim3 grid(chunks, kv_count, lanes);
   const bool qvec = (((uintptr_t)query) & 15u) == 0 && (q_stride & 3) == 0;
   if (head_size == 256 && fmt == 0)
@@ -512,6 +645,16 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
     return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || chunks == 1) return e;
+  return attend_fold(a, chunks, chunk, place0, place_dev, window, lanes, head_size, blend_out,
+                     stream);
+}
+
+// The fold of a launch's chunk partials into `blend_out`.
+static hipError_t attend_fold(const AttendArgs &a, int chunks, int chunk, int place0,
+                              const int *place_dev, int window, int lanes, int head_size,
+                              float *blend_out, hipStream_t stream) {
+  const int head_count = a.head_count;
+  const int q_stride = a.q_stride;
   // One lane: 16 dims a fold workgroup (the most workgroups); many lanes
   // (a prime or a block): 64.  Chunks a thread loads: enough for one pass.
   const int dims = lanes == 1 ? 16 : 64;
@@ -540,6 +683,72 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
 #undef IGL_FOLD_PER
 #undef IGL_FOLD
   return hipGetLastError();
+}
+
+// The decode step's attention with the heads prepared in the same launch
+// (attend_split_kernel's PREP form): one lane at the position in *place_dev
+// (place_bound its upper bound, which sizes the grid), e4m3 rings, one
+// key/value head.  query: the query heads before their norm, 16-byte aligned;
+// turn: (cos, sin) pairs of the position times each step, head_size / 2 of
+// them; k_raw, v_raw, k_gain: the key and value heads before their norms and
+// the key gain, whose bytes go to ring slot position % cache_span (NULL for a
+// layer that reads another layer's rings and writes none).
+extern "C" hipError_t igl_launch_attend_prep(const uint8_t *key_store, const uint8_t *value_store,
+                                             float key_scale, float value_scale, int cache_span,
+                                             int head_size, const float *query, const float *q_gain,
+                                             const float *turn, const float *k_raw,
+                                             const float *v_raw, const float *k_gain,
+                                             uint8_t *k_ring, uint8_t *v_ring, float eps,
+                                             int place_bound, const int *place_dev, int window,
+                                             float score_scale, float *blend_out, float *work,
+                                             hipStream_t stream) {
+  AttendArgs a;
+  const int chunk = attend_chunk(place_bound, window, 1);
+  const int chunks = attend_blocks(place_bound, window, 1);
+  if ((((uintptr_t)query) & 15u) || (((uintptr_t)q_gain) & 15u) || !place_dev || !turn)
+    return hipErrorInvalidValue;
+  if (k_raw && (!v_raw || !k_gain || !k_ring || !v_ring)) return hipErrorInvalidValue;
+  a.key_store = key_store;
+  a.value_store = value_store;
+  a.kv_width = head_size;
+  a.cache_span = cache_span;
+  a.place0 = place_bound;
+  a.place_dev = place_dev;
+  a.window = window;
+  a.chunks = chunks;
+  a.final_out = chunks == 1 ? blend_out : nullptr;
+  a.q_stride = kAttendGroup * head_size;
+  a.query = query;
+  a.key_scale = key_scale * 256.0f * score_scale;
+  a.value_scale = value_scale * 256.0f;
+  a.head_count = kAttendGroup;
+  a.part_out = work;
+  a.part_peak = work + (size_t)chunks * kAttendGroup * head_size;
+  a.part_total = a.part_peak + (size_t)chunks * kAttendGroup;
+  a.q_gain = q_gain;
+  a.turn = turn;
+  a.k_raw = k_raw;
+  a.v_raw = v_raw;
+  a.k_gain = k_gain;
+  a.k_ring = k_ring;
+  a.v_ring = v_ring;
+  a.k_code_scale = key_scale;
+  a.v_code_scale = value_scale;
+  a.eps = eps;
+  const dim3 grid(chunks, 1, 1);
+  if (head_size == 256 && chunk == 32)
+    hipLaunchKernelGGL((attend_split_kernel<256, 0, 32, true, true>), grid, dim3(256), 0, stream, a);
+  else if (head_size == 256)
+    hipLaunchKernelGGL((attend_split_kernel<256, 0, 64, true, true>), grid, dim3(256), 0, stream, a);
+  else if (head_size == 512 && chunk == 32)
+    hipLaunchKernelGGL((attend_split_kernel<512, 0, 32, true, true>), grid, dim3(256), 0, stream, a);
+  else if (head_size == 512)
+    hipLaunchKernelGGL((attend_split_kernel<512, 0, 64, true, true>), grid, dim3(256), 0, stream, a);
+  else
+    return hipErrorInvalidValue;
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || chunks == 1) return e;
+  return attend_fold(a, chunks, chunk, place_bound, place_dev, window, 1, head_size, blend_out, stream);
 }
 
 // Floats of workspace igl_launch_attend needs for the same arguments.

@@ -77,6 +77,7 @@ struct igl_engine {
   int window_limit, lane_limit, guess_limit, fill, precise;
   int turns[2], halves[2];
   float *steps_dev[2];
+  float *turn_dev[2];  /* a one-lane pass's rotation row of each kind: [half][cos, sin] */
   /* the checkpoint */
   void   *map;
   size_t  map_bytes;
@@ -357,6 +358,7 @@ static int rope_table(igl_engine *e, int kind, int head_size, double theta, doub
   e->turns[kind] = turns;
   e->halves[kind] = half;
   if (hipMalloc((void **)&e->steps_dev[kind], (size_t)half * sizeof(float)) != hipSuccess ||
+      hipMalloc((void **)&e->turn_dev[kind], (size_t)half * 2 * sizeof(float)) != hipSuccess ||
       hipMemcpy(e->steps_dev[kind], steps, (size_t)half * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
     free(steps);
     return IGL_FAIL_DEVICE;
@@ -634,7 +636,8 @@ void igl_engine_close(igl_engine *e) {
     void *bufs[] = {e->payload_dev, e->ctl_dev, e->attend_work, e->state_buf[0],
                     e->state_buf[1], e->scrap, e->lift, e->q,
                     e->blend, e->k, e->v, e->gate, e->rise, e->ple_seed, e->ple_room, e->logits,
-                    e->pick_work, e->pick_dev, e->steps_dev[0], e->steps_dev[1]};
+                    e->pick_work, e->pick_dev, e->steps_dev[0], e->steps_dev[1],
+                    e->turn_dev[0], e->turn_dev[1]};
     for (size_t j = 0; j < sizeof(bufs) / sizeof(bufs[0]); ++j)
       if (bufs[j]) (void)hipFree(bufs[j]);
   }
@@ -830,12 +833,21 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
       }
     }
   }
-  RUN(igl_launch_qkv_prep(e->q, e->q_stride, L->shared ? NULL : e->k, e->v, e->kv_stride, e->heads,
-                          hs, lanes, L->q_norm, L->k_norm, e->eps, e->steps_dev[kind], e->ctl_dev,
-                          L->k_store, L->v_store, L->k_scale, L->v_scale, L->cache_span, st));
-  RUN(igl_launch_attend(S->k_store, S->v_store, IGL_CACHE_E4M3, S->k_scale, S->v_scale,
-                        S->cache_span, hs, 1, e->heads, hs, e->q, e->q_stride, bound, e->ctl_dev,
-                        L->full ? 0 : e->window, lanes, 1.0f, e->blend, e->attend_work, st));
+  if (lanes == 1) {
+    /* one lane: the heads' norms and turns and the new ring row in the
+     * attention launch (the pass's rotation rows are already on device) */
+    RUN(igl_launch_attend_prep(S->k_store, S->v_store, S->k_scale, S->v_scale, S->cache_span, hs, e->q,
+                               L->q_norm, e->turn_dev[kind], L->shared ? NULL : e->k, e->v, L->k_norm,
+                               L->k_store, L->v_store, e->eps, bound, e->ctl_dev, L->full ? 0 : e->window,
+                               1.0f, e->blend, e->attend_work, st));
+  } else {
+    RUN(igl_launch_qkv_prep(e->q, e->q_stride, L->shared ? NULL : e->k, e->v, e->kv_stride, e->heads,
+                            hs, lanes, L->q_norm, L->k_norm, e->eps, e->steps_dev[kind], e->ctl_dev,
+                            L->k_store, L->v_store, L->k_scale, L->v_scale, L->cache_span, st));
+    RUN(igl_launch_attend(S->k_store, S->v_store, IGL_CACHE_E4M3, S->k_scale, S->v_scale,
+                          S->cache_span, hs, 1, e->heads, hs, e->q, e->q_stride, bound, e->ctl_dev,
+                          L->full ? 0 : e->window, lanes, 1.0f, e->blend, e->attend_work, st));
+  }
   OKAY(project(e, &L->o, e->blend, e->q_stride, lanes, e->lift, H));
   /* state += norm(o) * after_attn; gate = gelu(gate proj) * up proj of norm(state) * before_ff */
   if (fused) {
@@ -909,6 +921,10 @@ static int run_pass(igl_engine *e, int bound, int lanes, int logits) {
                            (float)(1.0 / sqrt(2.0)), st));
   }
   OKAY(norm_rows(e, e->state, e->layer[0].enter_norm, H, lanes, H, e->scrap));
+  if (lanes == 1)
+    RUN(igl_launch_turn_row(e->steps_dev[0], e->steps_dev[0] ? e->halves[0] : 0, e->steps_dev[1],
+                            e->steps_dev[1] ? e->halves[1] : 0, e->ctl_dev, e->turn_dev[0],
+                            e->turn_dev[1], st));
   for (int li = 0; li < e->layers; ++li) OKAY(run_layer(e, li, bound, lanes));
   if (logits == 1 && lanes == 1) {
     /* the last update with the final norm in one launch */

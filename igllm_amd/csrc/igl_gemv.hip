@@ -1329,9 +1329,6 @@ __device__ __forceinline__ void group_prologue(const GemvGroupArgs &a, const Pro
   __syncthreads();
 }
 
-// Digit-form LDS of the grouped launch: K <= 8192.
-constexpr int kGroupMaxUnits = 256;
-
 // PRO: 0, or the elements a thread holds in the prologue (K <= 256 PRO).
 // GPT (PRO 0): the eight-element groups of x a thread stages, K <= 2048 GPT.
 // Each row's sum is formed as gemv_q4_dot_kernel forms it.
@@ -1343,8 +1340,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
   __shared__ float red[4][R];
   __shared__ double pro_red[16];
   __shared__ __attribute__((aligned(16))) float xs[PRO ? 256 * PRO : 4];
-  __shared__ uint4_t dig[kDigits * kGroupMaxUnits];
-  __shared__ int down[kGroupMaxUnits];
+  // the digit form of x, sized at launch (gemv_dot_lds_bytes(1, K / 32)):
+  // the LDS a workgroup holds bounds how many share a CU
+  extern __shared__ uint4_t lds_grp[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1354,6 +1352,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
   const int u_raw = (units * ks) / KS + lane;
   const bool has = tile < a.tiles && u_raw < (units * (ks + 1)) / KS;
   const int u = min(u_raw, units - 1);
+  uint4_t *dig = lds_grp;
+  int *down = reinterpret_cast<int *>(lds_grp + kDigits * units);
 
   // Row r of the tile: which plane, which row of it (tiles past the end
   // reread the last row; their sums are dropped).
@@ -1992,16 +1992,17 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
   a.ksplit = ksplit;
   const int tiles_per_block = 4 / ksplit;
   dim3 grid((a.tiles + tiles_per_block - 1) / tiles_per_block);
+  const size_t lds = gemv_dot_lds_bytes(1, units);  // at most 25 KiB (K <= 8192)
   // eight-element groups of x a thread stages without a prologue
   const int gpt = K <= 2048 ? 1 : K <= 4096 ? 2 : 4;
 #define IGL_GROUP_KS(M_, P_, G_)                                                                    \
   do {                                                                                              \
     if (ksplit == 1)                                                                                \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 1>), grid, dim3(kGemvThreads), 0, stream, a); \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
     else if (ksplit == 2)                                                                           \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 2>), grid, dim3(kGemvThreads), 0, stream, a); \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 2>), grid, dim3(kGemvThreads), lds, stream, a); \
     else                                                                                            \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 4>), grid, dim3(kGemvThreads), 0, stream, a); \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 4>), grid, dim3(kGemvThreads), lds, stream, a); \
   } while (0)
 #define IGL_GROUP_LAUNCH(M_, P_)                                  \
   do {                                                            \

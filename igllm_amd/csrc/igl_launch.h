@@ -139,6 +139,18 @@ hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t *value_stor
                              int lanes, float score_scale, float *blend_out, float *work,
                              hipStream_t stream);
 
+/* The decode step's attention with the query, key and value heads prepared in
+ * the same launch (norms, gains, turns, the new ring row): one lane, e4m3 rings,
+ * one key/value head; k_raw NULL for a layer that writes no row. */
+hipError_t igl_launch_attend_prep(const uint8_t *key_store, const uint8_t *value_store,
+                                  float key_scale, float value_scale, int cache_span,
+                                  int head_size, const float *query, const float *q_gain,
+                                  const float *turn, const float *k_raw, const float *v_raw,
+                                  const float *k_gain, uint8_t *k_ring, uint8_t *v_ring,
+                                  float eps, int place_bound, const int *place_dev, int window,
+                                  float score_scale, float *blend_out, float *work,
+                                  hipStream_t stream);
+
 /* The desk's HIP stream, for the engine's own launches (back_hip.c). */
 void *igl_desk_stream(igl_desk *desk);
 
@@ -153,6 +165,11 @@ hipError_t igl_launch_head_prep(float *v, int lane_stride, int heads, int head_s
                                 const float *gain, float eps, const float *step, int turn,
                                 int place_first, hipStream_t stream);
 hipError_t igl_launch_put_int(int32_t *dst, int value, hipStream_t stream);
+/* (cos, sin) of the position in *place_dev times each step of both kinds of
+ * layer, as float pairs [half][2]. */
+hipError_t igl_launch_turn_row(const float *step0, int half0, const float *step1, int half1,
+                               const int *place_dev, float *turn0, float *turn1,
+                               hipStream_t stream);
 hipError_t igl_launch_qkv_prep(float *q, int q_stride, const float *k, const float *v,
                                int kv_stride, int heads, int head_size, int lanes,
                                const float *q_gain, const float *k_gain, float eps,

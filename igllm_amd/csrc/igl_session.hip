@@ -380,6 +380,33 @@ extern "C" hipError_t igl_launch_put_int(int32_t *dst, int value, hipStream_t st
   return hipGetLastError();
 }
 
+// The rotation row of one position, for each kind of layer: turn[j] =
+// ((float)cos(p * step[j]), (float)sin(p * step[j])) in double, as head_turn
+// forms them (the reference's cos_room / sin_room at that position), p read
+// from place_dev.  Computed once a decode step for every layer's attention.
+__global__ __launch_bounds__(256) void turn_row_kernel(const float *step0, int half0,
+                                                       const float *step1, int half1,
+                                                       const int *place_dev, float *turn0,
+                                                       float *turn1) {
+  const double place = (double)*place_dev;
+  for (int j = threadIdx.x; j < half0 + half1; j += blockDim.x) {
+    const bool first = j < half0;
+    const int i = first ? j : j - half0;
+    const double angle = place * (double)(first ? step0 : step1)[i];
+    float *t = first ? turn0 : turn1;
+    t[2 * i] = (float)cos(angle);
+    t[2 * i + 1] = (float)sin(angle);
+  }
+}
+
+extern "C" hipError_t igl_launch_turn_row(const float *step0, int half0, const float *step1,
+                                          int half1, const int *place_dev, float *turn0,
+                                          float *turn1, hipStream_t stream) {
+  hipLaunchKernelGGL(turn_row_kernel, dim3(1), dim3(256), 0, stream, step0, half0, step1, half1,
+                     place_dev, turn0, turn1);
+  return hipGetLastError();
+}
+
 extern "C" hipError_t igl_launch_qkv_prep(float *q, int q_stride, const float *k, const float *v,
                                           int kv_stride, int heads, int head_size, int lanes,
                                           const float *q_gain, const float *k_gain, float eps,
