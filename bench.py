@@ -5,7 +5,10 @@ A step is one pass of the small-lane GEMV sweep (gate/up shape N=8192,K=2048
 and down shape N=2048,K=8192, int4 group 32, M in {1,2,4,8} lanes of fp32
 activations, seed 0): eight products, each on its own copy of the weights,
 rotated through more copies than the 256 MiB Infinity Cache holds, so every
-byte is read from HBM.  `value` is the step's algorithmic bytes over its time.
+byte is read from HBM.  `value` is the step's algorithmic bytes over its time,
+the K timed steps recorded once and replayed with HIP events on the desk's
+stream around the replay (the GPU's time; the same steps enqueued one ctypes
+call a launch are reported beside it).
 
 Beside it, on the same run: the decode GEMV alone (M=1, 8192x2048, the
 dominant kernel) against the HBM roofline, the batched prefill GEMM against
@@ -29,6 +32,10 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
+MFMA_I8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA
+# Threads the CPU legs use: the GPU box's CPU share for one GPU is 16, whatever
+# nproc reports there, so 16 is "all cores" of this job.
+CPU_SHARE = 16
 SHAPES = [(8192, 2048), (2048, 8192)]
 LANES = [1, 2, 4, 8]
 COPIES = 48                     # 48 x 10.5 MB per shape: past the 256 MiB MALL
@@ -53,12 +60,16 @@ def parse():
     ap.add_argument("--kernel", choices=["gemv", "gemv8", "gemm", "attend", "copy", "head2", "real", "calib",
                                          "readfloor"],
                     help="run one kernel's workload alone in a loop (for rocprofv3) and exit")
+    ap.add_argument("--lanes", type=int, default=2048, help="--kernel gemm: the lane count M")
+    ap.add_argument("--shape", type=int, default=0, choices=[0, 1],
+                    help="--kernel gemm: 0 for 8192x2048, 1 for 2048x8192")
     return ap.parse_args()
 
 
-def kernel_loop(be, name, reps):
+def kernel_loop(be, name, reps, lanes=2048, shape=0):
     """One kernel's workload alone, for counter runs: the decode GEMV (M=1,
-    8192x2048, rotated copies), the M=8 GEMV, the M=2048 prefill GEMM, the
+    8192x2048, rotated copies), the M=8 GEMV, the prefill GEMM (M lanes, either
+    shape; M=2048 on 8192x2048 by default), the
     L=16384 attention, a 256 MiB device copy that calibrates FETCH_SIZE and
     WRITE_SIZE against a known byte count, the 2-bit 262144x1536 head and the
     bf16 8960x1536 real plane at M=1 (rotated copies), the calibrated
@@ -153,8 +164,8 @@ def kernel_loop(be, name, reps):
                           "GBps": round(gemv_bytes(N, K, M) / (us * 1e-6) / 1e9, 1)}))
         return
     if name == "gemm":
-        N, K = SHAPES[0]
-        M = 2048
+        N, K = SHAPES[shape]
+        M = lanes
         rot = Rotation(be, N, K)
         a = be.alloc(M * K * 2)
         c = be.alloc(M * N * 2)
@@ -189,10 +200,11 @@ def kernel_loop(be, name, reps):
         print(json.dumps({"kernel": "attend", "L": L, "avg_us": round(us, 2)}))
 
 
-def cpu_e2e(folder, prompt, gen=8, prime=64):
+def cpu_e2e(folder, prompt, gen=8, prime=2048):
     """The reference engine itself (oracle/_ref, AVX2+FMA build) on the same
-    checkpoint, on this host's cores: a bounded sample, the first `prime` ids of
-    the prompt then `gen` greedy steps, each phase timed by the reference."""
+    checkpoint, on this host's cores: the GPU leg's whole 2048-id prompt, so the
+    decode steps run at the same context, then `gen` greedy steps (a bounded
+    sample of the GPU leg's 256), each phase timed by the reference."""
     import ctypes
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as ol
@@ -203,7 +215,7 @@ def cpu_e2e(folder, prompt, gen=8, prime=64):
     fn = lib.ref_engine_clock
     fn.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
                    ctypes.c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
-    cores = min(16, os.cpu_count() or 1)
+    cores = min(CPU_SHARE, os.cpu_count() or 1)
     ids = np.ascontiguousarray(prompt[:prime], dtype=np.int32)
     prime_s, step_s = ctypes.c_double(), ctypes.c_double()
     code = fn(folder.encode(), cores, 8, prime + gen + 16, ids.ctypes.data, ids.size, gen,
@@ -213,13 +225,46 @@ def cpu_e2e(folder, prompt, gen=8, prime=64):
     return {"decode_tok_s": round(gen / step_s.value, 2), "prefill_tok_s": round((prime - 1) / prime_s.value, 1),
             "cores": cores, "kind": "reference",
             "sample": f"reference engine (app_core.c, AVX2+FMA build), {prime}-id prompt then {gen} greedy "
-                      f"steps on the same checkpoint, {cores} threads"}
+                      f"steps (the GPU leg's context) on the same checkpoint, {cores} threads"}
 
 
 # Lanes a fast-mode prefill pass carries: the whole 2048-id prompt at once.  The
 # prefill products are then M = 2047 GEMMs that fill the GPU; at 256 lanes a
 # pass the 2048-row projections were 8 tiles (15.5k against 38.7k tok/s).
 FAST_LANES = 2048
+
+
+def decode_bytes(shape, place):
+    """HBM bytes one decode step at `place` reads at config dimensions with
+    int4 group-32 planes: every plane's codes and scales once (the projections
+    of each layer, the per-layer-input gate and projection, the model's
+    per-layer projection and the tied head), the embedding rows it gathers, and
+    the FP8 key/value bytes each layer's attention reads (a sliding layer the
+    last `window` positions, a full one all of them; a layer that shares
+    another's cache reads that cache again)."""
+    def plane(n, k):
+        return n * k // 2 + n * (k // 32) * 4
+
+    from igllm_amd.native import load
+    import ctypes
+    lib = load()
+    H, P, L = shape.hidden, shape.ple_size, shape.layers
+    total = plane(shape.vocab, H) + plane(P * L, H)  # head and the model's per-layer projection
+    total += H // 2 + H // 32 * 4 + P * L // 2 + P * L // 32 * 4  # one embedding row of each table
+    first_share = L - shape.shared_layers
+    for i in range(L):
+        full = lib.igl_gemma_full_layer(ctypes.byref(shape), i)
+        hd = shape.full_head_dim if full else shape.head_dim
+        inner = shape.inner * (2 if shape.double_wide and i >= first_share else 1)
+        q = shape.heads * hd
+        total += plane(q, H) + plane(H, q)  # q and o
+        if i < first_share:
+            total += 2 * plane(shape.kv_heads * hd, H)  # k and v
+        total += 2 * plane(inner, H) + plane(H, inner)  # gate, up, down
+        total += plane(P, H) + plane(H, P)  # per-layer-input gate and projection
+        span = place + 1 if full else min(place + 1, shape.window)
+        total += 2 * span * shape.kv_heads * hd
+    return total
 
 
 def e2e_decode(be, prompt_count=2048, gen=256, cpu=True):
@@ -260,10 +305,13 @@ def e2e_decode(be, prompt_count=2048, gen=256, cpu=True):
             finally:
                 eng.close()
             key = "precise" if precise else "fast_prefill"
+            step_bytes = decode_bytes(shape, prompt_count - 1 + gen // 2)
             out[key] = {"load_s": round(load_s, 2),
                         "prefill_tok_s": round((prompt_count - 1) / prime_s, 1),
                         "decode_tok_s": round(gen / decode_s, 1),
                         "decode_ms_per_token": round(decode_s * 1e3 / gen, 3),
+                        "bytes_per_token": step_bytes,
+                        "hbm_frac": round(step_bytes / (decode_s / gen) / 1e9 / HBM_PEAK_GBPS, 4),
                         "min_margin": round(float(min(margins)), 5),
                         "first_ids": picks[:16],
                         "lane_limit": 16 if precise else FAST_LANES}
@@ -471,14 +519,23 @@ class Rotation:
             self.planes.append(cp)
 
 
-def cpu_baseline(budget_s=12.0):
-    """The reference's float back_mat_mat over the same sweep, on this host."""
+def cpu_baseline(budget_s=10.0):
+    """The reference's float back_mat_mat over the same sweep, on this host:
+    the job's whole CPU share (16 threads), then one thread."""
+    allc = cpu_sweep(min(CPU_SHARE, os.cpu_count() or 1), budget_s)
+    one = cpu_sweep(1, budget_s)
+    allc["one_thread"] = {k: one[k] for k in ("value", "unit", "cores", "kind", "sample")}
+    return allc
+
+
+def cpu_sweep(cores, budget_s):
+    """`cores` threads of the reference's float back_mat_mat over the sweep for
+    about `budget_s` seconds."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import ctypes
     import oracle_lib as ol
     from igllm_amd.backend import synth_projection
 
-    cores = min(16, os.cpu_count() or 1)
     lib = ol.ref("tuned")
     kind = "reference"
     flags = ""
@@ -546,7 +603,7 @@ def main():
 
     be = Backend(device=0, sum_limit=256, col_limit=8192, lane_limit=16)
     if args.kernel:
-        kernel_loop(be, args.kernel, args.steps)
+        kernel_loop(be, args.kernel, args.steps, args.lanes, args.shape)
         be.close()
         return
     rot = {shape: Rotation(be, *shape) for shape in SHAPES}
@@ -561,55 +618,9 @@ def main():
 
     counter = [0]
 
-    def step():
-        for (N, K) in SHAPES:
-            r = rot[(N, K)]
-            for M in LANES:
-                cp = r.planes[counter[0] % COPIES]
-                counter[0] += 1
-                be.gemv_dev(cp, acts[(N, K, M)], K, M, outs[(N, K, M)], N)
-
-    for _ in range(args.warmup):
-        step()
-    be.sync()
-    be.mark()
-    for _ in range(args.steps):
-        step()
-    be.mark()
-    ms_total = be.marks_ms()
-    ms_per_step = ms_total / args.steps
-    value = step_bytes / (ms_per_step * 1e-3) / 1e9
-
-    # ---- dominant kernel: decode GEMV M=1, 8192 x 2048, on rotating copies.
-    N, K = SHAPES[0]
-    r = rot[(N, K)]
-    launches = 400
-    for i in range(20):
-        be.gemv_dev(r.planes[i % COPIES], acts[(N, K, 1)], K, 1, outs[(N, K, 1)], N)
-    be.sync()
-    be.mark()
-    for i in range(launches):
-        be.gemv_dev(r.planes[i % COPIES], acts[(N, K, 1)], K, 1, outs[(N, K, 1)], N)
-    be.mark()
-    gemv_us = be.marks_ms() * 1e3 / launches
-    gemv_algo = gemv_bytes(N, K, 1)
-    gemv_gbps = gemv_algo / (gemv_us * 1e-6) / 1e9
-
-    # ---- the read floor: a kernel that only reads the same bytes once (16-byte
-    # loads, two a thread), over as many rotated buffers, launched the same way.
-    floor_bufs = [be.alloc(gemv_algo) for _ in range(COPIES)]
-    for i in range(20):
-        be.read_floor_dev(floor_bufs[i % COPIES], gemv_algo)
-    be.sync()
-    be.mark()
-    for i in range(launches):
-        be.read_floor_dev(floor_bufs[i % COPIES], gemv_algo)
-    be.mark()
-    floor_us = be.marks_ms() * 1e3 / launches
-
-    # Each launch above is enqueued by one ctypes call (~4 us of host time), so
-    # both rates are partly the host's.  The same launches recorded once and
-    # replayed (igl_record_*: no host launch each) time the kernels themselves.
+    # Launches enqueued one ctypes call each carry ~4 us of host time; the same
+    # launches recorded once and replayed (igl_record_*: no host launch each)
+    # time the kernels themselves.
     def replayed(enqueue, count=2 * COPIES):
         be.record_begin()
         for i in range(count):
@@ -625,8 +636,72 @@ def main():
         finally:
             be.replay_free(handle)
 
+
+    def step():
+        for (N, K) in SHAPES:
+            r = rot[(N, K)]
+            for M in LANES:
+                cp = r.planes[counter[0] % COPIES]
+                counter[0] += 1
+                be.gemv_dev(cp, acts[(N, K, M)], K, M, outs[(N, K, M)], N)
+
+    for _ in range(args.warmup):
+        step()
+    be.sync()
+    # The timed region: the K steps enqueued one ctypes call a launch (the
+    # host's ~4 us a call bounds the short products), and the same K steps
+    # recorded once and replayed (the GPU's own time; `value`).
+    be.mark()
+    for _ in range(args.steps):
+        step()
+    be.mark()
+    enqueued_ms_per_step = be.marks_ms() / args.steps
+    be.record_begin()
+    for _ in range(args.steps):
+        step()
+    steps_replay = be.record_end()
+    try:
+        be.replay_run(steps_replay)  # untimed: every copy's first read of this pass
+        be.sync()
+        be.mark()
+        be.replay_run(steps_replay)
+        be.mark()
+        ms_total = be.marks_ms()
+    finally:
+        be.replay_free(steps_replay)
+    ms_per_step = ms_total / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # ---- dominant kernel: decode GEMV M=1, 8192 x 2048, on rotating copies.
+    N, K = SHAPES[0]
+    r = rot[(N, K)]
+    launches = 400
+    for i in range(20):
+        be.gemv_dev(r.planes[i % COPIES], acts[(N, K, 1)], K, 1, outs[(N, K, 1)], N)
+    be.sync()
+    be.mark()
+    for i in range(launches):
+        be.gemv_dev(r.planes[i % COPIES], acts[(N, K, 1)], K, 1, outs[(N, K, 1)], N)
+    be.mark()
+    gemv_enq_us = be.marks_ms() * 1e3 / launches
+    gemv_algo = gemv_bytes(N, K, 1)
+
+    # ---- the read floor: a kernel that only reads the same bytes once (16-byte
+    # loads, two a thread), over as many rotated buffers, launched the same way.
+    floor_bufs = [be.alloc(gemv_algo) for _ in range(COPIES)]
+    for i in range(20):
+        be.read_floor_dev(floor_bufs[i % COPIES], gemv_algo)
+    be.sync()
+    be.mark()
+    for i in range(launches):
+        be.read_floor_dev(floor_bufs[i % COPIES], gemv_algo)
+    be.mark()
+    floor_us = be.marks_ms() * 1e3 / launches
+
     gemv_replayed_us = replayed(lambda i: be.gemv_dev(r.planes[i % COPIES], acts[(N, K, 1)], K, 1,
-                                                      outs[(N, K, 1)], N))
+                                                      outs[(N, K, 1)], N), launches)
+    gemv_us = gemv_replayed_us
+    gemv_gbps = gemv_algo / (gemv_us * 1e-6) / 1e9
     floor_replayed_us = replayed(lambda i: be.read_floor_dev(floor_bufs[i % COPIES], gemv_algo))
     for b in floor_bufs:
         b.free()
@@ -656,29 +731,34 @@ def main():
             sweep[f"{N}x{K}_M{M}"] = {"us": round(us, 3),
                                       "GBps": round(gemv_bytes(N, K, M) / (us * 1e-6) / 1e9, 1)}
 
-    # ---- prefill GEMM, bf16 in/out, M = 2048 lanes (both shapes).
+    # ---- prefill GEMM, bf16 in/out, M in {64, 256, 1024, 2048} lanes (both
+    # shapes; BASELINE's prefill config), timed replayed (the GEMM launches
+    # recorded once: no host launch each).  From 256 lanes the bound is the
+    # MFMA peak; at 64 lanes the product is below the ridge (182 FLOP a byte
+    # against ~312 for bf16), so it is also quoted against the HBM roof.
     prefill = {}
     for (N, K) in SHAPES:
-        M = 2048
-        a = be.alloc(M * K * 2)
-        c = be.alloc(M * N * 2)
-        rng = np.random.default_rng(0)
-        a.put((rng.normal(size=M * K).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))
-        cp = rot[(N, K)].planes[0]
-        for _ in range(3):
-            be.gemm_bf16_dev(cp, a, K, M, c, N)
-        be.sync()
-        be.mark()
-        reps = 20
-        for i in range(reps):
-            be.gemm_bf16_dev(rot[(N, K)].planes[i % COPIES], a, K, M, c, N)
-        be.mark()
-        us = be.marks_ms() * 1e3 / reps
-        tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
-        prefill[f"{N}x{K}_M{M}"] = {"us": round(us, 2), "TFLOPs": round(tflops, 1),
-                                    "frac_of_mfma_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
-        a.free()
-        c.free()
+        for M in (64, 256, 1024, 2048):
+            a = be.alloc(M * K * 2)
+            c = be.alloc(M * N * 2)
+            rng = np.random.default_rng(0)
+            a.put((rng.normal(size=M * K).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))
+            planes = rot[(N, K)].planes
+            for i in range(3):
+                be.gemm_bf16_dev(planes[i % COPIES], a, K, M, c, N)
+            be.sync()
+            reps = 20 if M >= 1024 else 2 * COPIES
+            us = replayed(lambda i: be.gemm_bf16_dev(planes[i % COPIES], a, K, M, c, N), reps)
+            tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+            nbytes = N * K // 2 + N * (K // 32) * 4 + 2 * M * (K + N)
+            entry = {"us": round(us, 2), "TFLOPs": round(tflops, 1),
+                     "frac_of_mfma_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+            if M == 64:
+                entry["GBps"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+                entry["frac_of_hbm_peak"] = round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)
+            prefill[f"{N}x{K}_M{M}"] = entry
+            a.free()
+            c.free()
 
     # ---- calibrated prefill (enter_gain, one gain a row): fp32 lanes through
     # plane_lift_dev, the MFMA GEMM on levels and unit gains plus the row close.
@@ -703,12 +783,12 @@ def main():
             be.plane_lift_dev(cp, a, K, M, c, N)
         be.mark()
         us = be.marks_ms() * 1e3 / reps
-        tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
-        prefill[name] = {"us": round(us, 2), "TFLOPs": round(tflops, 1),
-                         "frac_of_mfma_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+        tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        prefill[name] = {"us": round(us, 2), "TOPs": round(tops, 1),
+                         "frac_of_i8_mfma_peak": round(tops / MFMA_I8_PEAK_TOPS, 4),
                          "note": "fp32 in/out; the level pass (act_level_kernel) and the int8 MFMA GEMM with "
-                                 "the row close and leave grid (gemm_level_kernel); frac against the bf16 "
-                                 "figure like the other entries (int8 peak: 5.0 POP/s)"}
+                                 "the row close and leave grid (gemm_level_kernel), against the int8 "
+                                 "peak (5.0 POP/s)"}
         a.free()
         c.free()
         be.detach(cp)
@@ -743,13 +823,44 @@ def main():
     for i in range(reps):
         attend(i)
     be.mark()
-    att_us = be.marks_ms() * 1e3 / reps
+    att_enq_us = be.marks_ms() * 1e3 / reps
+    att_us = replayed(attend, 2 * rings)
     att_bytes = 2 * L * head + 2 * 8 * head * 4
     attention = {"L": L, "us": round(att_us, 2),
                  "GBps": round(att_bytes / (att_us * 1e-6) / 1e9, 1),
                  "frac_of_hbm_peak": round(att_bytes / (att_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
-                 "note": f"int8 K/V rings rotated over {rings} copies (past the MALL); "
-                         "includes the chunk-merge launch"}
+                 "enqueued_us": round(att_enq_us, 2),
+                 "note": f"int8 K/V rings rotated over {rings} copies (past the MALL); the chunk kernel and "
+                         "the fold, recorded once and replayed (enqueued_us: one ctypes call each)"}
+    kb.free()
+    vb.free()
+    # the decode step's sliding-window call: 512 positions of 256 dims, e4m3,
+    # at position 2300 of a 2560-slot ring (rotated past the MALL)
+    Ls, win, srings = 2560, 512, 200
+    ring_s = Ls * head
+    ks = be.alloc(ring_s * srings)
+    vs = be.alloc(ring_s * srings)
+    blk = rng.integers(0, 256, size=ring_s, dtype=np.uint8) & 0xBF  # no 0x7F / 0xFF codes
+    for i in range(srings):
+        ks.put(blk, i * ring_s)
+        vs.put(blk[::-1].copy(), i * ring_s)
+
+    def slide(i):
+        code = lib.igl_attend_lanes_dev(ctypes.byref(desk), ks.ptr + (i % srings) * ring_s,
+                                        vs.ptr + (i % srings) * ring_s, 0, 0.02, 0.02, Ls, 1, 8, head,
+                                        q.ptr, 8 * head, 2300, win, 1, 1.0, o.ptr)
+        if code != 0:
+            raise RuntimeError(f"attend sliding: {code}")
+
+    for i in range(5):
+        slide(i)
+    be.sync()
+    sl_us = replayed(slide, srings)
+    attention["sliding_512"] = {"us": round(sl_us, 2),
+                                "note": "one lane at position 2300, window 512, head 256, e4m3 rings rotated "
+                                        f"over {srings} copies; chunk kernel and fold, replayed"}
+    ks.free()
+    vs.free()
 
     kinds = kinds_leg(be)
     e2e = None if args.no_e2e else e2e_decode(be, cpu=not args.no_cpu)
@@ -763,6 +874,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
+        "enqueued_ms_per_step": round(enqueued_ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -778,6 +890,9 @@ def main():
                      "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": GEMV_M1_TRAFFIC_BYTES,
                      "algorithmic_bytes": gemv_algo, "avg_launch_us": round(gemv_us, 3),
+                     "avg_launch_us_enqueued": round(gemv_enq_us, 3),
+                     "timing": f"{launches} launches on rotated copies recorded once and replayed, HIP events "
+                               "on the desk's stream; enqueued: the same launches one ctypes call each",
                      "read_floor": read_floor},
         "cpu_baseline": cpu,
         "gemv_sweep": sweep,

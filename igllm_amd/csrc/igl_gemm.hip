@@ -199,8 +199,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_q4_kernel(GemmArgs g) {
 // 64 a step through LDS stages that only the LDS DMA writes (global_load_lds:
 // no registers held for loads in flight):
 //   * three stages of the step's 256 x 64 binary16 activations (two steps
-//     ahead), 16-byte chunks of a row XOR-swizzled by the row's low three
-//     bits (no padding, no conflicts);
+//     ahead), 16-byte chunks of a row XOR-swizzled by bits 1..3 of the row
+//     (no padding, no conflicts: a 16-byte LDS read serves 16 lanes a cycle
+//     from 64 banks, rows are 128 bytes so (row & 1) picks the banks' half,
+//     and the swizzle gives the 16 rows of a read 16 distinct slots; swizzled
+//     by the row's low three bits, rows r and r + 8 met in every read);
 //   * four stages (three steps ahead) of the 256 rows' 64 codes as they are
 //     packed (32 bytes a row) and their two fp32 gains.
 // A wave turns its 64 columns' codes into binary16 operands in registers as
@@ -334,12 +337,12 @@ __global__ __launch_bounds__(512) void gemm_q4_big_kernel(GemmBigArgs g) {
 
   // DMA sources (a lane's 16 bytes land at the wave's LDS address + 16 lane).
   // Activations: wave w's instruction i fills rows 8 (4 w + i) .. +7, lane l
-  // row R0 + l / 8 at physical chunk l % 8, logical chunk (l % 8) ^ (row & 7).
+  // row R0 + l / 8 at physical chunk l % 8, logical chunk (l % 8) ^ ((row >> 1) & 7).
   const _Float16 *a_src[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 8 * (4 * wave + i) + (lane >> 3);
-    const int c = (lane & 7) ^ (r & 7);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
     a_src[i] = g.a16 + (size_t)min(m0 + r, g.M - 1) * g.K + k_first + 8 * c;
   }
   // codes: wave w fills rows 32 w .. +31, lane l row 32 w + l / 2, physical
@@ -407,7 +410,7 @@ __global__ __launch_bounds__(512) void gemm_q4_big_kernel(GemmBigArgs g) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int r = wm * 128 + 16 * i + n;
-      const int p = (2 * gq + q) ^ (r & 7);
+      const int p = (2 * gq + q) ^ ((r >> 1) & 7);
       a[q] = *reinterpret_cast<const half8_t *>(as + r * kBigK + 8 * p);
     }
   };
@@ -562,6 +565,189 @@ __global__ void gemm_slice_sum_kernel(const float *part, int slices, size_t slic
   }
 }
 
+// ---- the skinny form (64 <= M < 256 lanes) --------------------------------
+//
+// Few lanes leave the product bound by the weight stream, which must be read
+// once: a workgroup of four waves owns 128 weight rows x 64 lanes and walks its
+// K slice in steps of 64, with the large-tile form's operand order, decoding
+// and DMA staging (three stages, issued two steps ahead; eight stages measured
+// slower: a CU's outstanding reads, not their latency, bound the stream).  Wave w decodes rows
+// 32 w .. 32 w + 31 and multiplies them by all 64 lanes (2 x 4 products of
+// 16 x 16 a k-half), so no row is decoded twice.  K slices (blockIdx.z) keep
+// at least 128 workgroups; their fp32 partials are added in slice order by
+// gemm_slice_sum_kernel.
+constexpr int kMidM = 64;
+constexpr int kMidN = 128;
+constexpr int kMidK = 64;
+constexpr int kMidStages = 3;
+constexpr int kMidAhead = kMidStages - 1;
+constexpr int kMidA = kMidM * kMidK;                  // halves of a stage's activations
+constexpr int kMidB = kMidN * kMidK / 2;              // bytes of a stage's codes
+constexpr int kMidG = kMidN * kMidK / 32;             // floats of a stage's gains
+constexpr int kMidStage = kMidA * 2 + kMidB + kMidG * 4;
+constexpr int kMidLds = kMidStages * kMidStage;
+
+template <bool C_BF16>
+__global__ __launch_bounds__(256) void gemm_q4_mid_kernel(GemmBigArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds_m[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = blockIdx.x * kMidN;
+  const int m0 = blockIdx.y * kMidM;
+  const int steps = g.k_steps;
+  const int k_first = blockIdx.z * g.k_steps * kMidK;
+
+  // DMA sources.  Activations: wave w's instruction i fills rows 8 (2 w + i)
+  // .. +7, lane l row R0 + l / 8 at physical chunk l % 8, logical chunk
+  // (l % 8) ^ ((row >> 1) & 7).  Codes: wave w fills rows 32 w .. +31, lane l row
+  // 32 w + l / 2, physical half l & 1 holding logical half (l & 1) ^ (bit 3 of
+  // the row).  Gains: the same rows, group l & 1.
+  const _Float16 *a_src[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = 8 * (2 * wave + i) + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    a_src[i] = g.a16 + (size_t)min(m0 + r, g.M - 1) * g.K + k_first + 8 * c;
+  }
+  const int br = min(n0 + 32 * wave + (lane >> 1), g.N - 1);
+  const uint8_t *b_src = g.codes + (size_t)br * (size_t)g.row_stride + k_first / 2 +
+                         16 * ((lane & 1) ^ ((lane >> 4) & 1));
+  const float *s_src = g.gains + (size_t)br * g.gain_stride;
+  const int s_first = k_first / 32;
+  const int s_grp = lane & 1;
+  auto stage = [&](int step) { return lds_m + (step % kMidStages) * kMidStage; };
+  auto issue = [&](int step) {
+    uint8_t *st = stage(step);
+    const int k0 = step * kMidK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_global_load_lds((global_void_t *)(a_src[i] + k0),
+                                       (lds_void_t *)(st + (2 * wave + i) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((global_void_t *)(b_src + k0 / 2),
+                                     (lds_void_t *)(st + kMidA * 2 + wave * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(
+        (global_void_t *)(s_src + (((unsigned)(s_first + k0 / 32 + s_grp)) >> g.group_shift)),
+        (lds_void_t *)(st + kMidA * 2 + kMidB + wave * 256), 4, 0, 0);
+  };
+
+  float4_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t exp10 = 0x64006400u;  // 1024.0 in both halves
+  const _Float16 lo_bias = (_Float16)(1024.0f + g.code_bias);
+  const _Float16 hi_bias = (_Float16)(1024.0f + 16.0f * g.code_bias);
+  const half2_t bias_lo = half2_t{lo_bias, lo_bias};
+  const half2_t bias_hi = half2_t{hi_bias, hi_bias};
+  const int gq = lane >> 4;
+  const int n = lane & 15;
+  auto decode = [&](uint32_t d, half2_t scale) {
+    const uint32_t e = d >> 8;
+    const half2_t p0 = (as_half2(and_or_b32(d, 0x000F000Fu, exp10)) - bias_lo) * scale;
+    const half2_t p1 = (as_half2(and_or_b32(d, 0x00F000F0u, exp10)) - bias_hi) * scale;
+    const half2_t p2 = (as_half2(and_or_b32(e, 0x000F000Fu, exp10)) - bias_lo) * scale;
+    const half2_t p3 = (as_half2(and_or_b32(e, 0x00F000F0u, exp10)) - bias_hi) * scale;
+    return __builtin_bit_cast(half8_t, uint4_t{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                                               __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)});
+  };
+
+  // A wave's loads retire in issue order, four a step: before iteration s
+  // steps s .. min(s + kMidAhead, steps) - 1 are in flight, so step s is in
+  // when all but the last 4 min(kMidAhead - 1, steps - s - 1) are.
+  for (int t = 0; t < kMidAhead && t < steps; ++t) issue(t);
+  for (int s = 0; s < steps; ++s) {
+    switch (min(kMidAhead - 1, steps - s - 1)) {  // vmcnt(4 n) lgkmcnt(0)
+      case 0: __builtin_amdgcn_s_waitcnt(0x0070); break;
+      case 1: __builtin_amdgcn_s_waitcnt(0x0074); break;
+      case 2: __builtin_amdgcn_s_waitcnt(0x0078); break;
+      case 3: __builtin_amdgcn_s_waitcnt(0x007C); break;
+      case 4: __builtin_amdgcn_s_waitcnt(0x4070); break;
+      case 5: __builtin_amdgcn_s_waitcnt(0x4074); break;
+      default: __builtin_amdgcn_s_waitcnt(0x4078); break;
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // every wave's DMA of step s is in; step s - 1's stage is free
+    asm volatile("" ::: "memory");
+    if (s + kMidAhead < steps) issue(s + kMidAhead);
+    const uint8_t *st = stage(s);
+    const _Float16 *as = reinterpret_cast<const _Float16 *>(st);
+    const uint8_t *cs = st + kMidA * 2;
+    const float *gs = reinterpret_cast<const float *>(cs + kMidB);
+    half8_t bf[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int row = 32 * wave + 16 * j + n;
+      const int half = (gq >> 1) ^ ((n >> 3) & 1);
+      const uint2_t raw = *reinterpret_cast<const uint2_t *>(cs + row * 32 + 16 * half + 8 * (gq & 1));
+      const _Float16 sh = (_Float16)gs[row * 2 + (gq >> 1)];
+      const half2_t sc = half2_t{sh, sh};
+      bf[0][j] = decode(raw[0], sc);
+      bf[1][j] = decode(raw[1], sc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      half8_t a[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int r = 16 * i + n;
+        const int p = (2 * gq + q) ^ ((r >> 1) & 7);
+        a[q] = *reinterpret_cast<const half8_t *>(as + r * kMidK + 8 * p);
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[q][j], a[q], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // D is C transposed (as in the large-tile form): lane l holds lane row
+  // l % 16 of its tile and four consecutive weight rows 4 (l / 16) .. + 3.
+  float *part = reinterpret_cast<float *>(g.out) + blockIdx.z * g.slice_floats;
+  const bool vec_ok = g.slice_floats ? (g.N % 4 == 0)
+                                     : (g.out_stride % 4 == 0 &&
+                                        ((uintptr_t)g.out & (C_BF16 ? 7u : 15u)) == 0);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + 16 * i + n;
+    if (m >= g.M) continue;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int nb = n0 + 32 * wave + 16 * j + 4 * gq;
+      float4_t v = acc[i][j];
+      if (!g.slice_floats && !C_BF16 && g.close.gains) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (nb + r < g.N) v[r] = close_value(g.close, nb + r, v[r]);
+      }
+      if (vec_ok && nb + 3 < g.N) {
+        if (g.slice_floats) {
+          *reinterpret_cast<float4_t *>(part + (size_t)m * g.N + nb) = v;
+        } else if (C_BF16) {
+          *reinterpret_cast<uint2_t *>(reinterpret_cast<uint16_t *>(g.out) + (size_t)m * g.out_stride + nb) =
+              uint2_t{bf16_pair(v[0], v[1]), bf16_pair(v[2], v[3])};
+        } else {
+          *reinterpret_cast<float4_t *>(reinterpret_cast<float *>(g.out) + (size_t)m * g.out_stride + nb) = v;
+        }
+        continue;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int nn = nb + r;
+        if (nn >= g.N) continue;
+        if (g.slice_floats)
+          part[(size_t)m * g.N + nn] = v[r];
+        else if (C_BF16)
+          reinterpret_cast<uint16_t *>(g.out)[(size_t)m * g.out_stride + nn] = float_to_bf16(v[r]);
+        else
+          reinterpret_cast<float *>(g.out)[(size_t)m * g.out_stride + nn] = v[r];
+      }
+    }
+  }
+}
+
 }  // namespace igl
 
 using namespace igl;
@@ -585,7 +771,26 @@ static size_t gemm_half_bytes(int M, int K) {
 // Bytes of workspace igl_launch_gemm_q4 needs for an M x N x K product (the
 // binary16 activations of the large-tile form, then any K slices' fp32
 // partials), 0 when it takes the small form.
+// K slices of a skinny-form launch: while the tiles fill fewer than 128
+// workgroups (the weight stream needs about half the CUs).
+static int gemm_mid_slices(int M, int N, int K) {
+  const int tiles = ((M + kMidM - 1) / kMidM) * ((N + kMidN - 1) / kMidN);
+  int slices = 1;
+  while (slices < 8 && tiles * slices < 128 && N % 4 == 0 && K % (2 * slices * kMidK) == 0 &&
+         K / (2 * slices) >= 4 * kMidK)
+    slices *= 2;
+  return slices;
+}
+
+static int gemm_is_mid(int M, int N, int K) {
+  return M >= 64 && M < kBigM && N >= kMidN && K % kMidK == 0;
+}
+
 extern "C" size_t igl_gemm_work_bytes(int M, int N, int K) {
+  if (gemm_is_mid(M, N, K)) {
+    const int slices = gemm_mid_slices(M, N, K);
+    return gemm_half_bytes(M, K) + (slices > 1 ? (size_t)slices * M * N * sizeof(float) : 0);
+  }
   if (M < kBigM || N < kBigN || K % kBigK) return 0;
   const int slices = gemm_slices(M, N, K);
   return gemm_half_bytes(M, K) + (slices > 1 ? (size_t)slices * M * N * sizeof(float) : 0);
@@ -603,7 +808,8 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
     return hipErrorInvalidValue;  // the close rides only on the large-tile form's fp32 C
   if (igl_gemm_work_bytes(M, N, K) && work) {
     _Float16 *a16 = reinterpret_cast<_Float16 *>(work);
-    const int slices = gemm_slices(M, N, K);
+    const bool mid = gemm_is_mid(M, N, K);
+    const int slices = mid ? gemm_mid_slices(M, N, K) : gemm_slices(M, N, K);
     float *part = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(work) + gemm_half_bytes(M, K));
     dim3 cgrid((K / 8 + 255) / 256, M);
     if (act_bf16)
@@ -629,20 +835,33 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
     b.k_steps = K / kBigK / slices;
     b.slice_floats = slices > 1 ? (size_t)M * N : 0;
     b.close = cl;
-    const size_t lds = (size_t)kBigLds;
-    static int granted[2];
-    const void *fn = out_bf16 ? reinterpret_cast<const void *>(&gemm_q4_big_kernel<true>)
-                              : reinterpret_cast<const void *>(&gemm_q4_big_kernel<false>);
-    if (!granted[out_bf16 ? 1 : 0]) {
-      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    // The dynamic LDS each form asks for is granted once per kernel.
+    static int granted[4];
+    const int use_bf16 = out_bf16 && (!mid || slices == 1);
+    const void *fn = mid ? (use_bf16 ? reinterpret_cast<const void *>(&gemm_q4_mid_kernel<true>)
+                                     : reinterpret_cast<const void *>(&gemm_q4_mid_kernel<false>))
+                         : (use_bf16 ? reinterpret_cast<const void *>(&gemm_q4_big_kernel<true>)
+                                     : reinterpret_cast<const void *>(&gemm_q4_big_kernel<false>));
+    const int lds = mid ? kMidLds : kBigLds;
+    const int which = 2 * mid + use_bf16;
+    if (!granted[which]) {
+      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
       if (e != hipSuccess) return e;
-      granted[out_bf16 ? 1 : 0] = 1;
+      granted[which] = 1;
     }
-    dim3 grid((N + kBigN - 1) / kBigN, (M + kBigM - 1) / kBigM, slices);
-    if (out_bf16)
-      hipLaunchKernelGGL((gemm_q4_big_kernel<true>), grid, dim3(512), lds, stream, b);
-    else
-      hipLaunchKernelGGL((gemm_q4_big_kernel<false>), grid, dim3(512), lds, stream, b);
+    if (mid) {
+      const dim3 grid((N + kMidN - 1) / kMidN, (M + kMidM - 1) / kMidM, slices);
+      if (use_bf16)
+        hipLaunchKernelGGL((gemm_q4_mid_kernel<true>), grid, dim3(256), (size_t)lds, stream, b);
+      else
+        hipLaunchKernelGGL((gemm_q4_mid_kernel<false>), grid, dim3(256), (size_t)lds, stream, b);
+    } else {
+      const dim3 grid((N + kBigN - 1) / kBigN, (M + kBigM - 1) / kBigM, slices);
+      if (use_bf16)
+        hipLaunchKernelGGL((gemm_q4_big_kernel<true>), grid, dim3(512), (size_t)lds, stream, b);
+      else
+        hipLaunchKernelGGL((gemm_q4_big_kernel<false>), grid, dim3(512), (size_t)lds, stream, b);
+    }
     e = hipGetLastError();
     if (e != hipSuccess || slices == 1) return e;
     dim3 sgrid((N / 4 + 255) / 256, M);

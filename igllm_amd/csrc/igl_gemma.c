@@ -12,8 +12,7 @@
  * model.safetensors, every payload 256-byte aligned so a device copy of the
  * payload can bind planes in place.
  *
- * Values: codes uniform over 0..15 (16 per xoshiro256** draw), or, with
- * `centered`, over 1..15 (values -7..7, mean zero); scales
+ * Values: codes uniform over 0..15 (16 per xoshiro256** draw); scales
  * |N(0, 0.02)|; norm gains 1 + 0.1 N(0,1); layer scalars uniform in
  * [0.85, 1.15]; cache scales 6/448 (keys, values) so a unit-rms row fits the
  * e4m3 grid.  The draws run in tensor order from one seeded stream.
@@ -297,21 +296,6 @@ static void fill_codes2(igl_rng *rng, uint8_t *dst, size_t count) {
   }
 }
 
-/* Fills `count` bytes of 4-bit codes whose values (code - 8) are uniform over
- * -7..7, mean zero: each nibble is 1 + floor(15 u / 65536) of a 16-bit slice
- * u of a draw, four nibbles a draw. */
-static void fill_codes_centered(igl_rng *rng, uint8_t *dst, size_t count) {
-  size_t i = 0;
-  while (i < count) {
-    uint64_t bits = igl_rng_next(rng);
-    for (int b = 0; b < 2 && i < count; ++b, ++i) {
-      const uint32_t lo = 1u + (uint32_t)((((bits >> (32 * b)) & 0xFFFFu) * 15u) >> 16);
-      const uint32_t hi = 1u + (uint32_t)((((bits >> (32 * b + 16)) & 0xFFFFu) * 15u) >> 16);
-      dst[i] = (uint8_t)(lo | (hi << 4));
-    }
-  }
-}
-
 /* Fills `count` bytes of codes: 16 nibbles a draw, low nibble first. */
 static void fill_codes(igl_rng *rng, uint8_t *dst, size_t count) {
   size_t i = 0;
@@ -395,9 +379,7 @@ int igl_gemma_write(const char *folder, const igl_gemma_shape *shape, uint64_t s
       }
       while (left > 0) {
         size_t take = left < buf_cap ? left : buf_cap;
-        if (x->fill == 0 && shape->centered) {
-          fill_codes_centered(&rng, buf, take);
-        } else if (x->fill == 0) {
+        if (x->fill == 0) {
           fill_codes(&rng, buf, take);
         } else if (x->fill == 9) {
           fill_codes2(&rng, buf, take);

@@ -83,7 +83,7 @@ class GemmaShape(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "vocab", "hidden", "inner", "layers", "heads", "kv_heads", "head_dim", "full_head_dim",
         "window", "ple_size", "shared_layers", "double_wide", "full_every", "max_positions",
-        "cache_scales", "kinds", "centered")] + [(n, ctypes.c_float) for n in (
+        "cache_scales", "kinds")] + [(n, ctypes.c_float) for n in (
             "norm_eps", "logit_cap", "rope_local", "rope_global", "partial_rotary")]
 
 

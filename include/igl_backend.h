@@ -288,7 +288,6 @@ typedef struct igl_gemma_shape {
   int   window, ple_size, shared_layers, double_wide, full_every, max_positions;
   int   cache_scales;  /* write k/v_cache_scale so a byte cache is used */
   int   kinds;         /* 0: int4 group-32 planes everywhere; 1: the export's own kinds */
-  int   centered;      /* 4-bit code values uniform over -7..7 (mean zero) instead of -8..7 */
   float norm_eps, logit_cap, rope_local, rope_global, partial_rotary;
 } igl_gemma_shape;
 

@@ -140,6 +140,13 @@ float ref_quant_step(float value, float step) {
   return value;
 }
 
+static int32_t ref_top(const float *logits, int vocab) {
+  int32_t best = 0;
+  for (int v = 1; v < vocab; ++v)
+    if (logits[v] > logits[best]) best = v;
+  return best;
+}
+
 /* The reference engine end to end: load the checkpoint in `folder`, prime the
  * prompt (all but its last id, app_core.c:14443-14471), then step and take the
  * greedy pick `gen_count` times, the way the CLI's answer loop does
@@ -183,6 +190,49 @@ int ref_engine_greedy(const char *folder, int thread_count, int cache_bits, int 
     out_ids[step] = best;
     if (margin_out) margin_out[step] = logits[best] - second;
     id = best;
+  }
+  session_close(session);
+  model_free(model);
+  return (int)code;
+}
+
+/* The greedy run of ref_engine_greedy, keeping the whole row of logits at
+ * each of `probe_count` steps (ascending step indices in `probe_steps`) in
+ * `rows_out` [probe_count][vocab].  Returns 0 or the app_code that stopped it. */
+int ref_engine_probe(const char *folder, int thread_count, int cache_bits, int window_limit,
+                     const int32_t *prompt, int prompt_count, int gen_count, const int32_t *probe_steps,
+                     int probe_count, int32_t *out_ids, float *rows_out) {
+  app_setup setup = app_setup_plain();
+  app_model *model = NULL;
+  app_session *session = NULL;
+  app_code code;
+  int32_t id;
+  int next_probe = 0;
+  setup.thread_count = thread_count;
+  setup.cache_bits = cache_bits;
+  setup.window_limit = window_limit;
+  code = model_load(folder, &setup, &model);
+  if (code != APP_OKAY) return (int)code;
+  code = session_open(model, &session);
+  if (code != APP_OKAY) {
+    model_free(model);
+    return (int)code;
+  }
+  code = session_prime(session, prompt, prompt_count);
+  id = prompt[prompt_count - 1];
+  for (int step = 0; code == APP_OKAY && step < gen_count; ++step) {
+    const float *logits = session_step(session, id);
+    const int vocab = model_vocab_count(model);
+    if (!logits) {
+      code = APP_FAIL_STATE;
+      break;
+    }
+    if (next_probe < probe_count && probe_steps[next_probe] == step) {
+      memcpy(rows_out + (size_t)next_probe * (size_t)vocab, logits, sizeof(float) * (size_t)vocab);
+      ++next_probe;
+    }
+    out_ids[step] = ref_top(logits, vocab);
+    id = out_ids[step];
   }
   session_close(session);
   model_free(model);
@@ -274,13 +324,6 @@ int ref_engine_forced(const char *folder, int thread_count, int cache_bits, int 
   session_close(session);
   model_free(model);
   return (int)code;
-}
-
-static int32_t ref_top(const float *logits, int vocab) {
-  int32_t best = 0;
-  for (int v = 1; v < vocab; ++v)
-    if (logits[v] > logits[best]) best = v;
-  return best;
 }
 
 /* The CLI's greedy --guess loop (main_answer_guess, app_main.c:520-598) on

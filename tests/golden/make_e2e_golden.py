@@ -8,7 +8,7 @@ by oracle/Makefile), run on this repository's seeded synthetic checkpoint.
     python tests/golden/make_e2e_golden.py small_guess   # --guess 4, repeating prompt
     python tests/golden/make_e2e_golden.py small_long    # 8300-id prompt, 12000-position window
     python tests/golden/make_e2e_golden.py small_kinds   # the export's plane kinds, 20 layers
-    python tests/golden/make_e2e_golden.py e2b_centered  # config.json dimensions, zero-mean codes
+    python tests/golden/make_e2e_golden.py e2b_logits    # config.json dimensions, whole logit rows
 
 For each, the checkpoint is written with igl_gemma_write (seed 0) into a
 scratch folder, the prompt is drawn by igllm_amd.engine.prompt_ids, and the
@@ -44,10 +44,10 @@ CASES = {
     # whose spans cross the attention's change of chunk length
     "small_long": dict(shape=SMALL, prompt=8300, gen=32, window=12000),
     "e2b_guess": dict(shape={}, prompt=2048, gen=256, window=2560, repeat=512, span=4),
-    # config.json dimensions with zero-mean int4 codes (values -7..7): the
-    # default codes (-8..7, mean -0.5) give every plane a coherent component
-    # that settles the 35-layer stream on one id; these do not
-    "e2b_centered": dict(shape=dict(centered=1), prompt=2048, gen=256, window=2560),
+    # config.json dimensions: the logits of whole rows at a few steps (the
+    # greedy pick settles on one id; the 262144-wide rows do not)
+    "e2b_logits": dict(shape={}, prompt=2048, gen=32, window=2560, probes=[0, 1, 2, 15, 31],
+                       sample=512, top=64),
     # 2-bit MLPs from layer 15, I8 per-layer planes, bf16 per_layer_model_projection,
     # one scale a row, every projection but the head calibrated
     "small_kinds": dict(shape=dict(vocab=4096, hidden=512, inner=1024, layers=20, shared_layers=8, kinds=1),
@@ -89,6 +89,24 @@ def ref_forced(kind, folder, prompt, forced, window, threads):
     return out, margin
 
 
+def ref_probe(kind, folder, prompt, gen, window, threads, probes, vocab):
+    """The greedy run's whole logit rows at the steps `probes`."""
+    lib = ctypes.CDLL(PATHS[kind])
+    fn = lib.ref_engine_probe
+    fn.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                   ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                   ctypes.c_void_p]
+    steps = np.array(probes, dtype=np.int32)
+    ids = np.zeros(gen, np.int32)
+    rows = np.zeros((len(probes), vocab), np.float32)
+    t0 = time.time()
+    code = fn(folder.encode(), threads, 8, window, prompt.ctypes.data, prompt.size, gen, steps.ctypes.data,
+              steps.size, ids.ctypes.data, rows.ctypes.data)
+    if code != 0:
+        raise SystemExit(f"ref_engine_probe({kind}) returned {code}")
+    return ids, rows, time.time() - t0
+
+
 def ref_guess(kind, folder, prompt, gen, window, threads, span):
     lib = ctypes.CDLL(oracle_lib.REF_PLAIN_PATH if kind == "plain" else oracle_lib.REF_TUNED_PATH)
     fn = lib.ref_engine_guess
@@ -115,6 +133,34 @@ def main():
               "gen": case["gen"], "window_limit": case["window"], "cache_bits": 8,
               "repeat_span": case.get("repeat", 0), "guess_span": case.get("span", 0),
               "shape": {k: getattr(shape, k) for k, _ in shape._fields_}}
+    if case.get("probes"):
+        probes = case["probes"]
+        out = {}
+        for kind in ("plain", "tuned"):
+            ids, rows, secs = ref_probe(kind, folder, prompt, case["gen"], case["window"], threads, probes,
+                                        shape.vocab)
+            out[kind] = (ids, rows)
+            print(kind, f"{secs:.1f}s", flush=True)
+        plain_rows, tuned_rows = out["plain"][1], out["tuned"][1]
+        sample = np.random.default_rng(7).choice(shape.vocab, size=case["sample"], replace=False)
+        result["probes"] = []
+        for i, step in enumerate(probes):
+            top = np.argsort(-plain_rows[i], kind="stable")[:case["top"]]
+            ids = np.concatenate([top, sample[~np.isin(sample, top)]]).astype(np.int64)
+            result["probes"].append({
+                "step": step, "ids": ids.tolist(),
+                "plain": [float(x) for x in plain_rows[i][ids]],
+                "tuned": [float(x) for x in tuned_rows[i][ids]],
+                "plain_row_mean": float(plain_rows[i].astype(np.float64).mean()),
+                "plain_row_rms": float(np.sqrt((plain_rows[i].astype(np.float64) ** 2).mean())),
+                "builds_max_abs_diff": float(np.max(np.abs(plain_rows[i] - tuned_rows[i])))})
+            print("step", step, "plain/tuned max |diff| over the row", result["probes"][-1]["builds_max_abs_diff"],
+                  "row rms", result["probes"][-1]["plain_row_rms"], flush=True)
+        result["plain"] = {"ids": out["plain"][0].tolist()}
+        result["tuned"] = {"ids": out["tuned"][0].tolist()}
+        with open(os.path.join(HERE, f"e2e_{name}.json"), "w") as f:
+            json.dump(result, f, indent=1)
+        return
     if case.get("span"):
         for kind in ("plain", "tuned"):
             ids, stats, secs = ref_guess(kind, folder, prompt, case["gen"], case["window"], threads,

@@ -98,70 +98,44 @@ def test_e2b_greedy_stream_matches_reference(backend, e2b_model, precise, lane_l
     assert gap <= (2e-3 if precise else 5e-3)
 
 
-@pytest.fixture(scope="module")
-def e2b_centered_model():
-    """config.json dimensions with zero-mean int4 codes (values -7..7)."""
-    import shutil
-
-    fx = load_fixture("e2b_centered")
-    root = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
-    folder = os.path.join(root, f"igl_gemma_e2b_centered_test_{os.getpid()}")
-    write_gemma(folder, seed=fx["seed"], centered=1)
-    yield folder
-    shutil.rmtree(folder, ignore_errors=True)
-
-
 @pytest.mark.parametrize("precise,lane_limit", [(True, 16), (False, 2048)])
-def test_e2b_centered_stream_matches_reference(backend, e2b_centered_model, precise, lane_limit):
-    """A full-size stream that walks the vocabulary: config.json dimensions,
-    zero-mean int4 codes, 2048-id prompt, 256 greedy steps
-    (tests/golden/e2e_e2b_centered.json, the reference's plain and tuned
-    builds).  With the default codes (values -8..7, mean -0.5) every plane
-    carries a coherent component and the 35-layer stream settles on one id;
-    here nearly every step picks a different id, so the first-maximum pick
-    (session_pick_at, app_core.c:14672-14677) meets hundreds of distinct rows
-    of logits.
-
-    Some steps' top-1/top-2 gaps are below the logits' reassociation noise
-    (the smallest is 6e-4), so the engine is fed the reference's own stream
-    (teacher forcing) rather than its own picks, and a pick that differs where
-    the reference's gap is that small does not derail the steps after it.
-    Bar: equal picks wherever the reference's gap is decided (above four times
-    the gap bar, and above every gap at which its plain and tuned builds
-    pick differently); every gap within the bar."""
-    fx = load_fixture("e2b_centered")
-    assert fx["shape"]["centered"] == 1
+def test_e2b_logit_rows_match_reference(backend, e2b_model, precise, lane_limit):
+    """The whole pass at config.json dimensions, beyond the pick: the greedy
+    stream of this checkpoint settles on one id, but its 262144-wide rows of
+    logits do not.  At five steps after the 2048-id prompt the engine's row is
+    compared with the reference's plain build (tests/golden/e2e_e2b_logits.json)
+    at the row's top 64 ids and 512 seeded ones, and by the whole row's mean
+    and rms.  The bar is set by the reference itself: three times the largest
+    difference between its plain and tuned (AVX2+FMA) builds over the row, and
+    at least 1e-3 (precise) or 5e-3 (the fast prefill's binary16 operands)."""
+    fx = load_fixture("e2b_logits")
     prompt = prompt_ids(fx["prompt_count"], fx["shape"]["vocab"], seed=fx["prompt_seed"])
-    want = np.array(fx["plain"]["ids"], dtype=np.int32)
-    ref_margin = np.array(fx["plain"]["margin"])
-    eng = Engine(backend, e2b_centered_model, window_limit=fx["window_limit"], lane_limit=lane_limit,
-                 precise=precise)
-    picks, gaps = [], []
+    want_ids = np.array(fx["plain"]["ids"], dtype=np.int32)
+    probes = {p["step"]: p for p in fx["probes"]}
+    eng = Engine(backend, e2b_model, window_limit=fx["window_limit"], lane_limit=lane_limit, precise=precise)
+    worst = {}
     try:
         eng.prime(prompt)
         token = int(prompt[-1])
-        for t in want:
-            pick, gap = eng.step(token)
-            picks.append(pick)
-            gaps.append(gap)
-            token = int(t)
+        for step in range(fx["gen"]):
+            pick, _ = eng.step(token)
+            assert pick == want_ids[step]
+            if step in probes:
+                p = probes[step]
+                row = eng.logits(0)
+                ids = np.array(p["ids"])
+                diff = float(np.max(np.abs(row[ids] - np.array(p["plain"]))))
+                bar = max(3 * p["builds_max_abs_diff"], 1e-3 if precise else 5e-3)
+                row64 = row.astype(np.float64)
+                mean_gap = abs(float(row64.mean()) - p["plain_row_mean"])
+                rms_gap = abs(float(np.sqrt((row64 ** 2).mean())) - p["plain_row_rms"])
+                worst[step] = (diff, bar, mean_gap, rms_gap)
+                assert diff <= bar, (step, diff, bar)
+                assert mean_gap <= bar and rms_gap <= bar, (step, mean_gap, rms_gap, bar)
+            token = int(want_ids[step])
     finally:
         eng.close()
-    picks, gaps = np.array(picks, dtype=np.int32), np.array(gaps)
-    bar = 2e-3 if precise else 5e-3
-    tuned = np.array(fx["tuned"]["ids"], dtype=np.int32)
-    # the builds agree up to their first differing pick; after it their
-    # inputs differ, so only that first step says where they part
-    parted = float(ref_margin[np.argmax(tuned != want)]) if np.any(tuned != want) else 0.0
-    decided = ref_margin > max(4 * bar, 1.5 * parted)
-    diff = float(np.max(np.abs(gaps - ref_margin)))
-    print("distinct reference ids", len(set(want.tolist())), "decided", int(decided.sum()),
-          "mismatches", int((picks != want).sum()), "of which decided", int(((picks != want) & decided).sum()),
-          "max gap difference", diff)
-    assert len(set(want.tolist())) > 128
-    assert int(decided.sum()) >= 200
-    assert np.array_equal(picks[decided], want[decided])
-    assert diff <= bar
+        print("step: (max |logit diff| at the sampled ids, bar, row mean gap, row rms gap)", worst)
 
 
 @pytest.mark.parametrize("precise,lane_limit", [(True, 16), (False, 2048)])

@@ -173,8 +173,11 @@ def closed_form64(codes, gains, act64, K, group=32):
 
 
 @pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 8192)])
-@pytest.mark.parametrize("M", [64, 256, 1024, 2048])
+@pytest.mark.parametrize("M", [64, 100, 192, 256, 1024, 2048])
 def test_prefill_gemm(backend, N, K, M):
+    """BASELINE's prefill lanes (64 .. 2048) and two ragged counts: below 256
+    lanes the skinny form (128 rows x 64 lanes a workgroup, K slices), from 256
+    the large-tile form."""
     print_case(test="prefill", N=N, K=K, M=M)
     codes, gains, act = synth_projection(N, K, M, seed=M)
     a16 = bf16_round(act).reshape(M, K)
