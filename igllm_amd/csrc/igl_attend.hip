@@ -215,6 +215,23 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
       }
     }
   }
+  // PREP: the gains and turns of the thread's query dims, requested with the
+  // query itself (one round trip, not two): item i covers dims d0 .. d0 + 7 of
+  // its head, whose turn pairs j0 .. j0 + 7 are 16 consecutive floats.
+  constexpr int kHeadItems = HEAD / 8;
+  float4_t qgain[PREP ? kQItems : 1][2];
+  float4_t qturn[PREP ? kQItems : 1][4];
+  if (PREP) {
+#pragma unroll
+    for (int i = 0; i < kQItems; ++i) {
+      const int d0 = 8 * ((tid + 256 * i) % kHeadItems);
+      const int j0 = d0 < HALF ? d0 : d0 - HALF;
+      qgain[i][0] = *reinterpret_cast<const float4_t *>(a.q_gain + d0);
+      qgain[i][1] = *reinterpret_cast<const float4_t *>(a.q_gain + d0 + 4);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) qturn[i][v] = *reinterpret_cast<const float4_t *>(a.turn + 2 * j0 + 4 * v);
+    }
+  }
   // key row: position c0 + wave*PW + (n % PW), bytes QD*g .. QD*g + QD - 1
   const int tk = c0 + wave * PW + (n % PW);
   uint4_t kr[QD / 16];
@@ -242,7 +259,6 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
   if (PREP) {
     // Each head's items are 32 (HEAD 256) or 64 (HEAD 512) consecutive
     // threads; the pair (j, j + HALF) of a dim sits HALF / 8 items apart.
-    constexpr int kHeadItems = HEAD / 8;
 #pragma unroll
     for (int i = 0; i < kQItems; ++i) {
       const int item = tid + 256 * i;
@@ -254,8 +270,7 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
       for (int off = kHeadItems / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
       const float shrink = rms_shrink(ss, HEAD, a.eps);
       float own[8], other[8];
-      const float4_t g0 = *reinterpret_cast<const float4_t *>(a.q_gain + d0);
-      const float4_t g1 = *reinterpret_cast<const float4_t *>(a.q_gain + d0 + 4);
+      const float4_t g0 = qgain[i][0], g1 = qgain[i][1];
       const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -265,11 +280,10 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) other[e] = __shfl_xor(own[e], kHeadItems / 2);
       const bool low = d0 < HALF;
-      const int j0 = low ? d0 : d0 - HALF;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float c = a.turn[2 * (j0 + e)];
-        const float sn = a.turn[2 * (j0 + e) + 1];
+        const float c = qturn[i][e >> 1][2 * (e & 1)];
+        const float sn = qturn[i][e >> 1][2 * (e & 1) + 1];
         qf[i][e] = low ? own[e] * c - other[e] * sn : own[e] * c + other[e] * sn;
       }
     }
@@ -705,7 +719,8 @@ extern "C" hipError_t igl_launch_attend_prep(const uint8_t *key_store, const uin
   AttendArgs a;
   const int chunk = attend_chunk(place_bound, window, 1);
   const int chunks = attend_blocks(place_bound, window, 1);
-  if ((((uintptr_t)query) & 15u) || (((uintptr_t)q_gain) & 15u) || !place_dev || !turn)
+  if ((((uintptr_t)query) & 15u) || (((uintptr_t)q_gain) & 15u) || (((uintptr_t)turn) & 15u) ||
+      !place_dev || !turn)
     return hipErrorInvalidValue;
   if (k_raw && (!v_raw || !k_gain || !k_ring || !v_ring)) return hipErrorInvalidValue;
   a.key_store = key_store;

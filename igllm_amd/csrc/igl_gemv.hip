@@ -1331,9 +1331,13 @@ __device__ __forceinline__ void group_prologue(const GemvGroupArgs &a, const Pro
 
 // PRO: 0, or the elements a thread holds in the prologue (K <= 256 PRO).
 // GPT (PRO 0): the eight-element groups of x a thread stages, K <= 2048 GPT.
+// TPW: the four-row tiles a wave walks (KS 1 only): one workgroup then serves
+// 16 TPW rows, so TPW times fewer workgroups repeat the prologue and the
+// staging of x; a wave requests every tile's gains and codes up front.
 // Each row's sum is formed as gemv_q4_dot_kernel forms it.
-template <int MODE, int PRO, int GPT, int KS>
+template <int MODE, int PRO, int GPT, int KS, int TPW>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupArgs a) {
+  static_assert(TPW == 1 || KS == 1, "several tiles a wave only without a K split");
   constexpr int R = 4;
   constexpr int kTilesPerBlock = 4 / KS;
   constexpr int kItems = GPT;
@@ -1346,34 +1350,37 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tile = blockIdx.x * kTilesPerBlock + wave / KS;
+  const int tile0 = (blockIdx.x * kTilesPerBlock + wave / KS) * TPW;
   const int ks = wave % KS;
   const int units = a.K >> 5;
   const int u_raw = (units * ks) / KS + lane;
-  const bool has = tile < a.tiles && u_raw < (units * (ks + 1)) / KS;
+  const bool lane_has = u_raw < (units * (ks + 1)) / KS;
   const int u = min(u_raw, units - 1);
   uint4_t *dig = lds_grp;
   int *down = reinterpret_cast<int *>(lds_grp + kDigits * units);
 
-  // Row r of the tile: which plane, which row of it (tiles past the end
-  // reread the last row; their sums are dropped).
-  const int tile_c = min(tile, a.tiles - 1);
-  int plane[R], prow[R];
-  if (MODE == GEMV_GELU_PAIR) {
+  // Row r of tile i: which plane, which row of it (tiles past the end reread
+  // the last row; their sums are dropped).
+  int plane[TPW][R], prow[TPW][R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      plane[r] = r >> 1;
-      prow[r] = min(2 * tile_c + (r & 1), a.rows[0] - 1);
-    }
-  } else {
-    int seg = 0, first = 0;
-    const int row0 = tile_c * R;
-    if (a.segments > 1 && row0 >= a.rows[0]) { seg = 1; first = a.rows[0]; }
-    if (a.segments > 2 && row0 >= a.rows[0] + a.rows[1]) { seg = 2; first = a.rows[0] + a.rows[1]; }
+  for (int i = 0; i < TPW; ++i) {
+    const int tile_c = min(tile0 + i, a.tiles - 1);
+    if (MODE == GEMV_GELU_PAIR) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      plane[r] = seg;
-      prow[r] = min(row0 - first + r, a.rows[seg] - 1);
+      for (int r = 0; r < R; ++r) {
+        plane[i][r] = r >> 1;
+        prow[i][r] = min(2 * tile_c + (r & 1), a.rows[0] - 1);
+      }
+    } else {
+      int seg = 0, first = 0;
+      const int row0 = tile_c * R;
+      if (a.segments > 1 && row0 >= a.rows[0]) { seg = 1; first = a.rows[0]; }
+      if (a.segments > 2 && row0 >= a.rows[0] + a.rows[1]) { seg = 2; first = a.rows[0] + a.rows[1]; }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        plane[i][r] = seg;
+        prow[i][r] = min(row0 - first + r, a.rows[seg] - 1);
+      }
     }
   }
 
@@ -1389,19 +1396,23 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
     digit_loads<1, kItems, true>(held, a.act, 0, a.K);
   else
     digit_loads<1, kItems, false>(held, a.act, 0, a.K);
-  float s[R];
-  uint4_t w[R];
+  float s[TPW][R];
+  uint4_t w[TPW][R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int p = plane[r];
-    s[r] = a.gains[p][(size_t)prow[r] * (size_t)a.gain_stride[p] + ((unsigned)u >> a.group_shift)];
-  }
+  for (int i = 0; i < TPW; ++i)
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int p = plane[r];
-    w[r] = __builtin_nontemporal_load(
-        reinterpret_cast<const uint4_t *>(a.codes[p] + (size_t)prow[r] * (size_t)a.row_stride[p]) + u);
-  }
+    for (int r = 0; r < R; ++r) {
+      const int p = plane[i][r];
+      s[i][r] = a.gains[p][(size_t)prow[i][r] * (size_t)a.gain_stride[p] + ((unsigned)u >> a.group_shift)];
+    }
+#pragma unroll
+  for (int i = 0; i < TPW; ++i)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int p = plane[i][r];
+      w[i][r] = __builtin_nontemporal_load(
+          reinterpret_cast<const uint4_t *>(a.codes[p] + (size_t)prow[i][r] * (size_t)a.row_stride[p]) + u);
+    }
   if (PRO) {
     group_prologue<PRO ? PRO : 1>(a, pl, xs, pro_red);
     digit_store_lds<kDigits>(xs, a.K, dig, down);
@@ -1409,15 +1420,17 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
     digit_store<1, kItems, kDigits>(held, a.K, dig, down);
   }
 
-  float acc[R];
-  {
-    uint4_t dd[kDigits];
+  uint4_t dd[kDigits];
 #pragma unroll
-    for (int j = 0; j < kDigits; ++j) dd[j] = dig[j * units + u];
-    const int shift = down[u];
+  for (int j = 0; j < kDigits; ++j) dd[j] = dig[j * units + u];
+  const int shift = down[u];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int tile = tile0 + i;
+    float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const uint4_t c = w[r] ^ 0x88888888u;
+      const uint4_t c = w[i][r] ^ 0x88888888u;
       int t[kDigits];
 #pragma unroll
       for (int j = 0; j < kDigits; ++j) t[j] = 0;
@@ -1426,43 +1439,43 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
 #pragma unroll
         for (int j = 0; j < kDigits; ++j)
           t[j] = __builtin_amdgcn_sdot8((int)c[q], (int)dd[j][q], t[j], false);
-      const float gain = has ? s[r] : 0.0f;
+      const float gain = lane_has && tile < a.tiles ? s[i][r] : 0.0f;
       acc[r] = wave_sum_to_last(gain * __builtin_amdgcn_ldexpf(digit_sum<kDigits>(t), shift));
     }
-  }
 
-  if (KS > 1) {
-    if (lane == 63) {
+    if (KS > 1) {
+      if (lane == 63) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) red[wave][r] = acc[r];
+        for (int r = 0; r < R; ++r) red[wave][r] = acc[r];
+      }
+      __syncthreads();
+      if (ks != 0 || lane != 63) return;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float total = 0.0f;
+        for (int k = 0; k < KS; ++k) total += red[wave + k][r];
+        acc[r] = total;
+      }
+    } else if (lane != 63) {
+      continue;
     }
-    __syncthreads();
-    if (ks != 0 || lane != 63) return;
+    if (tile >= a.tiles) continue;
+    if (MODE == GEMV_GELU_PAIR) {
+      const int n0 = 2 * tile;
+      if (n0 < a.rows[0]) a.out[0][n0] = gelu_near(acc[0]) * acc[2];
+      if (n0 + 1 < a.rows[0]) a.out[0][n0 + 1] = gelu_near(acc[1]) * acc[3];
+    } else {
+      const int row0 = tile * R;
+      const int first = plane[i][0] == 0 ? 0 : plane[i][0] == 1 ? a.rows[0] : a.rows[0] + a.rows[1];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float total = 0.0f;
-      for (int k = 0; k < KS; ++k) total += red[wave + k][r];
-      acc[r] = total;
-    }
-  } else if (lane != 63) {
-    return;
-  }
-  if (tile >= a.tiles) return;
-  if (MODE == GEMV_GELU_PAIR) {
-    const int n0 = 2 * tile;
-    if (n0 < a.rows[0]) a.out[0][n0] = gelu_near(acc[0]) * acc[2];
-    if (n0 + 1 < a.rows[0]) a.out[0][n0 + 1] = gelu_near(acc[1]) * acc[3];
-  } else {
-    const int row0 = tile * R;
-    const int first = plane[0] == 0 ? 0 : plane[0] == 1 ? a.rows[0] : a.rows[0] + a.rows[1];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int n = row0 - first + r;
-      if (n >= a.rows[plane[0]]) break;
-      if (MODE == GEMV_GELU_MUL)
-        a.out[0][n] = gelu_near(acc[r]) * a.mul[n];
-      else
-        a.out[plane[0]][n] = acc[r];
+      for (int r = 0; r < R; ++r) {
+        const int n = row0 - first + r;
+        if (n >= a.rows[plane[i][0]]) break;
+        if (MODE == GEMV_GELU_MUL)
+          a.out[0][n] = gelu_near(acc[r]) * a.mul[n];
+        else
+          a.out[plane[i][0]][n] = acc[r];
+      }
     }
   }
 }
@@ -1990,19 +2003,26 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
   while (ksplit < 4 && (units > ksplit * kWave || (a.tiles * ksplit < 2048 && units / (ksplit * 2) >= 32)))
     ksplit *= 2;
   a.ksplit = ksplit;
-  const int tiles_per_block = 4 / ksplit;
+  // With the prologue, each workgroup repeats the residual update (four
+  // K-vectors read, two block sums): past four workgroups a CU, two tiles a
+  // wave halve that (measured: the 2 x 12288-row gate/up pair at K 1536, 11.5
+  // -> 9.7 us; at 6144 rows, and without the prologue, one tile is faster).
+  const int tpw = pro && ksplit == 1 && (a.tiles + 3) / 4 >= 1024 ? 2 : 1;
+  const int tiles_per_block = 4 / ksplit * tpw;
   dim3 grid((a.tiles + tiles_per_block - 1) / tiles_per_block);
   const size_t lds = gemv_dot_lds_bytes(1, units);  // at most 25 KiB (K <= 8192)
   // eight-element groups of x a thread stages without a prologue
   const int gpt = K <= 2048 ? 1 : K <= 4096 ? 2 : 4;
 #define IGL_GROUP_KS(M_, P_, G_)                                                                    \
   do {                                                                                              \
-    if (ksplit == 1)                                                                                \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
+    if (ksplit == 1 && tpw == 2 && P_ != 0)                                                         \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 1, 2>), grid, dim3(kGemvThreads), lds, stream, a); \
+    else if (ksplit == 1)                                                                           \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 1, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
     else if (ksplit == 2)                                                                           \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 2>), grid, dim3(kGemvThreads), lds, stream, a); \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 2, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
     else                                                                                            \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 4>), grid, dim3(kGemvThreads), lds, stream, a); \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 4, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
   } while (0)
 #define IGL_GROUP_LAUNCH(M_, P_)                                  \
   do {                                                            \
