@@ -39,6 +39,7 @@ CPU_SHARE = 16
 SHAPES = [(8192, 2048), (2048, 8192)]
 LANES = [1, 2, 4, 8]
 COPIES = 48                     # 48 x 10.5 MB per shape: past the 256 MiB MALL
+ATTEND_COPIES = 40              # 40 x 8 MiB of key/value rings: past the MALL
 # HBM bytes per dispatch of the decode GEMV (M=1, 8192x2048), from two rocprofv3
 # --pmc runs of `bench.py --kernel gemv` (profiles/gemv_q4_m1_8192x2048.md):
 # FETCH_SIZE 5179.6 KiB x 2.0 + WRITE_SIZE 32.0 KiB x 1.0, the factors a 256 MiB
@@ -58,7 +59,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decode leg")
     ap.add_argument("--kernel", choices=["gemv", "gemv8", "gemm", "attend", "copy", "head2", "real", "calib",
-                                         "readfloor"],
+                                         "readfloor", "decode"],
                     help="run one kernel's workload alone in a loop (for rocprofv3) and exit")
     ap.add_argument("--lanes", type=int, default=2048, help="--kernel gemm: the lane count M")
     ap.add_argument("--shape", type=int, default=0, choices=[0, 1],
@@ -183,21 +184,53 @@ def kernel_loop(be, name, reps, lanes=2048, shape=0):
                           "TFLOPs": round(2.0 * M * N * K / (us * 1e-6) / 1e12, 1)}))
         return
     if name == "attend":
-        L, head = 16384, 256
+        # int8 rings of 16384 positions, 40 copies (320 MB, past the MALL)
+        L, head, copies = 16384, 256, ATTEND_COPIES
         rng = np.random.default_rng(1)
-        kb = be.upload(rng.integers(0, 256, size=(L, head), dtype=np.uint8))
-        vb = be.upload(rng.integers(0, 256, size=(L, head), dtype=np.uint8))
+        rings = [(be.upload(rng.integers(0, 256, size=(L, head), dtype=np.uint8)),
+                  be.upload(rng.integers(0, 256, size=(L, head), dtype=np.uint8))) for _ in range(copies)]
         q = be.upload(rng.normal(size=(8, head)).astype(np.float32))
         o = be.alloc(8 * head * 4)
-        for _ in range(3):  # first launches load the code objects
-            be.attend_dev(kb, vb, 1, 4.0 / 127, 4.0 / 127, L, 1, 8, head, q, 0, L, 1.0 / 16, o)
+        for i in range(3):  # first launches load the code objects
+            be.attend_dev(rings[i][0], rings[i][1], 1, 4.0 / 127, 4.0 / 127, L, 1, 8, head, q, 0, L, 1.0 / 16, o)
         be.sync()
         be.mark()
-        for _ in range(reps):
+        for i in range(reps):
+            kb, vb = rings[i % copies]
             be.attend_dev(kb, vb, 1, 4.0 / 127, 4.0 / 127, L, 1, 8, head, q, 0, L, 1.0 / 16, o)
         be.mark()
         us = be.marks_ms() * 1e3 / reps
-        print(json.dumps({"kernel": "attend", "L": L, "avg_us": round(us, 2)}))
+        print(json.dumps({"kernel": "attend", "L": L, "copies": copies, "avg_us": round(us, 2)}))
+        return
+    if name == "decode":
+        decode_loop(be, reps)
+
+
+def decode_loop(be, steps):
+    """Decode steps alone, for kernel traces: the synthetic E2B checkpoint, a
+    2048-id prompt primed, then `steps` greedy steps replayed from the step
+    graph (the e2e leg's decode, without its timers)."""
+    import tempfile
+    from igllm_amd.engine import Engine, prompt_ids, write_gemma
+
+    root = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
+    folder = os.path.join(root, f"igl_gemma_e2b_{os.getpid()}")
+    try:
+        shape = write_gemma(folder, seed=0)
+        prompt = prompt_ids(2048, shape.vocab, seed=0)
+        eng = Engine(be, folder, window_limit=2048 + steps + 64, lane_limit=16, precise=True)
+        try:
+            eng.prime(prompt)
+            token = int(prompt[-1])
+            for _ in range(steps):
+                token, _ = eng.step(token)
+            be.sync()
+        finally:
+            eng.close()
+    finally:
+        import shutil
+        shutil.rmtree(folder, ignore_errors=True)
+    print(json.dumps({"kernel": "decode", "prompt": 2048, "steps": steps}))
 
 
 def cpu_e2e(folder, prompt, gen=8, prime=2048):
@@ -794,7 +827,7 @@ def main():
         be.detach(cp)
 
     # ---- decode attention, 8 q heads / 1 KV head / d=256, L=16384, int8 bytes.
-    L, head, rings = 16384, 256, 40
+    L, head, rings = 16384, 256, ATTEND_COPIES
     rng = np.random.default_rng(1)
     ring_bytes = L * head
     kb = be.alloc(ring_bytes * rings)

@@ -200,10 +200,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_q4_kernel(GemmArgs g) {
 // no registers held for loads in flight):
 //   * three stages of the step's 256 x 64 binary16 activations (two steps
 //     ahead), 16-byte chunks of a row XOR-swizzled by bits 1..3 of the row
-//     (no padding, no conflicts: a 16-byte LDS read serves 16 lanes a cycle
-//     from 64 banks, rows are 128 bytes so (row & 1) picks the banks' half,
-//     and the swizzle gives the 16 rows of a read 16 distinct slots; swizzled
-//     by the row's low three bits, rows r and r + 8 met in every read);
+//     (no padding; the 16 rows of a read land in 16 distinct 16-byte slots
+//     of the 64 banks.  Measured alone, these reads count the conflict
+//     counter's floor of four cycles per 64-lane 16-byte read, as the row's
+//     low three bits do; unswizzled, three times that);
 //   * four stages (three steps ahead) of the 256 rows' 64 codes as they are
 //     packed (32 bytes a row) and their two fp32 gains.
 // A wave turns its 64 columns' codes into binary16 operands in registers as
