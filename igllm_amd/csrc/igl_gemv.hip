@@ -1586,16 +1586,16 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
                                                  unit_c0 + 4 * c4);
     }
   }
-  // Activations: item (unit, lane m, group g) is x[m][32 u + 8 g .. + 7] (at
-  // most 8 a thread: 64 units x 8 lanes x 4 groups).
-  const int items = CU * a.M * 4;
+  // Activations: item i = 32 u + 4 m + g is x[m][32 u + 8 g .. + 7] (at most
+  // 8 a thread: 64 units x 8 lane slots x 4 groups).  Slots m >= M are
+  // skipped; their B columns are never read into an output that is stored.
+  const int items = CU * 32;
   float4_t xa[8], xb[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const int i = min(tid + 256 * k, items - 1);
-    const int um = i >> 2;
-    const int u = um / a.M;
-    const int m = um - u * a.M;
+    const int u = i >> 5;
+    const int m = min((i >> 2) & 7, a.M - 1);
     const float *src =
         a.act + (size_t)m * (size_t)a.act_stride + (size_t)(unit_c0 + u) * 32 + 8 * (i & 3);
     if (VEC) {
@@ -1648,9 +1648,9 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
     const int i = tid + 256 * k;
     if (i >= items) break;
     const int g = i & 3;
-    const int um = i >> 2;
-    const int u = um / a.M;
-    const int m = um - u * a.M;
+    const int u = i >> 5;
+    const int m = (i >> 2) & 7;
+    if (m >= a.M) continue;
     const float v[8] = {xa[k].x, xa[k].y, xa[k].z, xa[k].w, xb[k].x, xb[k].y, xb[k].z, xb[k].w};
     float peak = 0.0f;
 #pragma unroll
