@@ -241,50 +241,61 @@ constexpr int kBigLds = kBigStages * kBigA * 2 + kBigCodeStages * kBigCodeStage;
 // With level_step > 0 (a calibrated plane's prefill), each x is first its
 // quant_step level rint(x / level_step) clamped to [-128, 127]: an integer the
 // binary16 operand holds exactly (and so does a level / 16).
+// Rows a thread of act_half_kernel converts (its loads all issued first).
+constexpr int kHalfRows = 4;
+
 template <bool A_BF16>
 __global__ void act_half_kernel(const void *act, int act_stride, int M, int K, _Float16 *a16,
                                 float level_step) {
   const int k8 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
-  const int m = blockIdx.y;
-  if (k8 >= K || m >= M) return;
-  float x[8];
-  if (A_BF16) {
-    // rows are 16-byte aligned (act_stride % 8 == 0): one load for 8 values
-    const uint4_t raw = *reinterpret_cast<const uint4_t *>(
-        reinterpret_cast<const uint16_t *>(act) + (size_t)m * act_stride + k8);
+  const int m0 = blockIdx.y * kHalfRows;
+  if (k8 >= K) return;
+  float x[kHalfRows][8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      x[2 * i] = __builtin_bit_cast(float, raw[i] << 16);
-      x[2 * i + 1] = __builtin_bit_cast(float, raw[i] & 0xFFFF0000u);
-    }
-  } else {
-    const float4_t *src = reinterpret_cast<const float4_t *>(
-        reinterpret_cast<const float *>(act) + (size_t)m * act_stride + k8);
-    const float4_t lo = src[0], hi = src[1];
+  for (int r = 0; r < kHalfRows; ++r) {
+    const int m = min(m0 + r, M - 1);  // rows past M reread the last one, not stored
+    if (A_BF16) {
+      // rows are 16-byte aligned (act_stride % 8 == 0): one load for 8 values
+      const uint4_t raw = *reinterpret_cast<const uint4_t *>(
+          reinterpret_cast<const uint16_t *>(act) + (size_t)m * act_stride + k8);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      x[i] = lo[i];
-      x[4 + i] = hi[i];
-    }
-  }
-  if (level_step > 0.0f) {
+      for (int i = 0; i < 4; ++i) {
+        x[r][2 * i] = __builtin_bit_cast(float, raw[i] << 16);
+        x[r][2 * i + 1] = __builtin_bit_cast(float, raw[i] & 0xFFFF0000u);
+      }
+    } else {
+      const float4_t *src = reinterpret_cast<const float4_t *>(
+          reinterpret_cast<const float *>(act) + (size_t)m * act_stride + k8);
+      const float4_t lo = src[0], hi = src[1];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float level = __builtin_rintf(x[i] / level_step);
-      level = level < -128.0f ? -128.0f : level;
-      x[i] = level > 127.0f ? 127.0f : level;
+      for (int i = 0; i < 4; ++i) {
+        x[r][i] = lo[i];
+        x[r][4 + i] = hi[i];
+      }
     }
   }
   const _Float16 sixteenth = (_Float16)0.0625f;
-  half8_t h;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const bool up = i & 1;  // k = 1, 3 and their partners 5, 7
-    const _Float16 a = sat_half(x[i]), b = sat_half(x[i + 4]);
-    h[2 * i] = up ? a * sixteenth : a;
-    h[2 * i + 1] = up ? b * sixteenth : b;
+  for (int r = 0; r < kHalfRows; ++r) {
+    if (m0 + r >= M) break;
+    if (level_step > 0.0f) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float level = __builtin_rintf(x[r][i] / level_step);
+        level = level < -128.0f ? -128.0f : level;
+        x[r][i] = level > 127.0f ? 127.0f : level;
+      }
+    }
+    half8_t h;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool up = i & 1;  // k = 1, 3 and their partners 5, 7
+      const _Float16 a = sat_half(x[r][i]), b = sat_half(x[r][i + 4]);
+      h[2 * i] = up ? a * sixteenth : a;
+      h[2 * i + 1] = up ? b * sixteenth : b;
+    }
+    *reinterpret_cast<half8_t *>(a16 + (size_t)(m0 + r) * K + k8) = h;
   }
-  *reinterpret_cast<half8_t *>(a16 + (size_t)m * K + k8) = h;
 }
 
 struct GemmBigArgs {
@@ -811,7 +822,7 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
     const bool mid = gemm_is_mid(M, N, K);
     const int slices = mid ? gemm_mid_slices(M, N, K) : gemm_slices(M, N, K);
     float *part = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(work) + gemm_half_bytes(M, K));
-    dim3 cgrid((K / 8 + 255) / 256, M);
+    dim3 cgrid((K / 8 + 255) / 256, (M + kHalfRows - 1) / kHalfRows);
     if (act_bf16)
       hipLaunchKernelGGL((act_half_kernel<true>), cgrid, dim3(256), 0, stream, act, act_stride, M, K, a16, 0.0f);
     else
