@@ -208,8 +208,8 @@ def kernel_loop(be, name, reps, lanes=2048, shape=0):
 
 def decode_loop(be, steps):
     """Decode steps alone, for kernel traces: the synthetic E2B checkpoint, a
-    2048-id prompt primed, then `steps` greedy steps replayed from the step
-    graph (the e2e leg's decode, without its timers)."""
+    2048-id prompt primed, then `steps` greedy steps launched eagerly (the e2e
+    leg's decode without its timers or its step graph)."""
     import tempfile
     from igllm_amd.engine import Engine, prompt_ids, write_gemma
 
@@ -220,6 +220,10 @@ def decode_loop(be, steps):
         prompt = prompt_ids(2048, shape.vocab, seed=0)
         eng = Engine(be, folder, window_limit=2048 + steps + 64, lane_limit=16, precise=True)
         try:
+            # eager: the step's launches one by one, not its captured graph
+            # (rocprofv3's kernel trace of the graph launch has aborted in the
+            # profiler's interception)
+            eng.set_graph(False)
             eng.prime(prompt)
             token = int(prompt[-1])
             for _ in range(steps):
@@ -561,6 +565,103 @@ def cpu_baseline(budget_s=10.0):
     return allc
 
 
+def ref_tuned():
+    """The reference's AVX2+FMA build (oracle/_ref) when this host can run it,
+    else None."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as ol
+
+    flags = ""
+    try:
+        flags = open("/proc/cpuinfo").read()
+    except OSError:
+        pass
+    lib = ol.ref("tuned")
+    return lib if lib is not None and " avx2" in flags and " fma" in flags else None
+
+
+def cpu_attention(budget_s=3.0):
+    """The reference's own decode attention (ref_attend: attend_score_band and
+    attend_blend_band forked over its pool, AVX2+FMA build) on the bench's case:
+    one lane, 8 query heads on one key/value head of 256 dims, int8 rings of
+    16384 positions; the job's CPU share of threads, then one, each for about
+    `budget_s` seconds."""
+    import ctypes
+
+    lib = ref_tuned()
+    if lib is None:
+        return None
+    import oracle_lib as ol
+
+    L, head, scale = 16384, 256, 4.0 / 127
+    rng = np.random.default_rng(1)
+    kb = rng.integers(0, 256, size=(L, head), dtype=np.uint8)
+    vb = rng.integers(0, 256, size=(L, head), dtype=np.uint8)
+    q = rng.normal(size=(8, head)).astype(np.float32)
+    grid = np.arange(256, dtype=np.uint32).astype(np.uint8).view(np.int8).astype(np.float32) * np.float32(scale)
+    out = np.zeros((8, head), dtype=np.float32)
+    res = {}
+    for cores in (min(CPU_SHARE, os.cpu_count() or 1), 1):
+        desk = lib.ref_desk_open(cores, 64, 2048)
+        try:
+            calls, t0 = 0, time.perf_counter()
+            while True:
+                lib.ref_attend(desk, ol.p(kb), ol.p(vb), ol.p(grid), ol.p(grid), L, head, 0, ol.p(q), 0, 8,
+                               head, 0, L, ol.p(out))
+                calls += 1
+                if time.perf_counter() - t0 > budget_s:
+                    break
+            us = (time.perf_counter() - t0) * 1e6 / calls
+        finally:
+            lib.ref_desk_close(desk)
+        res[cores] = (us, calls)
+    cores = max(res)
+    return {"us": round(res[cores][0], 1), "GBps": round(2 * L * head / (res[cores][0] * 1e-6) / 1e9, 2),
+            "cores": cores, "one_thread_us": round(res[1][0], 1), "kind": "reference",
+            "sample": f"{res[cores][1]} and {res[1][1]} calls of ref_attend (app_core.c's score and blend "
+                      f"bands, AVX2+FMA build) at L={L}, int8 rings, {cores} threads and 1"}
+
+
+def cpu_prefill(budget_s=5.0):
+    """The reference's back_mat_mat (AVX2+FMA float path, its pool) on a
+    256-lane prefill of the 8192x2048 int4 plane: the job's CPU share of threads
+    and one, each for about `budget_s` seconds.  256 lanes, not 2048: the
+    reference takes the same 16-lane chunks either way, and 2048 lanes would
+    run past the bench's few minutes on one thread."""
+    import ctypes
+    from igllm_amd.backend import synth_projection
+
+    lib = ref_tuned()
+    if lib is None:
+        return None
+    import oracle_lib as ol
+
+    (N, K), M = SHAPES[0], 256
+    codes, gains, act = synth_projection(N, K, M, seed=0)
+    d = ol.plane_desc(codes, gains, K)
+    out = np.empty((M, N), dtype=np.float32)
+    res = {}
+    for cores in (min(CPU_SHARE, os.cpu_count() or 1), 1):
+        desk = lib.ref_desk_open(cores, 256, 8192)
+        try:
+            calls, t0 = 0, time.perf_counter()
+            while True:
+                lib.ref_desk_mat_mat(desk, ctypes.byref(d), ol.p(act), K, M, ol.p(out), N)
+                calls += 1
+                if time.perf_counter() - t0 > budget_s:
+                    break
+            s_each = (time.perf_counter() - t0) / calls
+        finally:
+            lib.ref_desk_close(desk)
+        res[cores] = (s_each, calls)
+    cores = max(res)
+    flops = 2.0 * M * N * K
+    return {"TFLOPs": round(flops / res[cores][0] / 1e12, 4), "lanes_per_s": round(M / res[cores][0], 1),
+            "cores": cores, "one_thread_TFLOPs": round(flops / res[1][0] / 1e12, 5), "kind": "reference",
+            "sample": f"{res[cores][1]} and {res[1][1]} calls of back_mat_mat (AVX2+FMA float build), "
+                      f"M={M} lanes of the {N}x{K} int4 plane, {cores} threads and 1"}
+
+
 def cpu_sweep(cores, budget_s):
     """`cores` threads of the reference's float back_mat_mat over the sweep for
     about `budget_s` seconds."""
@@ -898,6 +999,9 @@ def main():
     kinds = kinds_leg(be)
     e2e = None if args.no_e2e else e2e_decode(be, cpu=not args.no_cpu)
     cpu = None if args.no_cpu else cpu_baseline()
+    if not args.no_cpu:
+        attention["cpu_baseline"] = cpu_attention()
+        prefill["cpu_baseline"] = cpu_prefill()
 
     line = {
         "metric": "decode tok/s + int4 GEMV HBM GB/s (% of peak) + prefill GEMM % MFMA, 1 GPU",
