@@ -79,10 +79,12 @@ struct AttendArgs {
   // The decode step's heads prepared here (attend_split_kernel's PREP form):
   // `query` holds the query heads before their norm; q_gain their gain; turn
   // the (cos, sin) of the lane's position times each rotation step, HEAD / 2
-  // pairs.  With k_raw set, the workgroup whose chunk holds the lane's
-  // position also prepares its key and value heads (norm and gain and turn;
-  // norm) and writes their bytes into ring slot position % cache_span of
-  // k_ring / v_ring (the rings read here), code = e4m3(value / scale).
+  // pairs.  With k_raw set, the lane's own position gets a workgroup of its
+  // own after the chunks of the positions before it (attend_new_row): it
+  // prepares the key and value heads (norm and gain and turn; norm), writes
+  // their bytes into ring slot position % cache_span of k_ring / v_ring (the
+  // rings read here), code = e4m3(value / scale), and writes the position's
+  // partial; the chunk workgroups never read that slot.
   const float *q_gain;
   const float *turn;           // [HEAD / 2][2]
   const float *k_raw;
@@ -129,6 +131,150 @@ __device__ __forceinline__ float xsum32(float v) {
   return lo + hi;
 }
 
+// The decode step's new position, a workgroup of its own (PREP with k_raw):
+// the key and value heads prepared (norm, gain, turn; norm) and written to the
+// rings as e4m3 bytes, the 8 query heads prepared as every chunk prepares them,
+// and the position's partial: score_h = key_scale q_h . key(bytes) in fp32, peak
+// score_h, total 1, blend the value bytes times value_scale.  Off the path of
+// the chunk workgroups, which end before it.
+template <int HEAD>
+__device__ __forceinline__ void attend_new_row(const AttendArgs &a, int pos, int pc) {
+  constexpr int HALF = HEAD / 2;
+  constexpr int W = 4;
+  constexpr int kHeadItems = HEAD / 8;
+  constexpr int kQItems = kAttendGroup * HEAD / 8 / 256;
+  __shared__ double nr_red[2][W];
+  __shared__ __attribute__((aligned(16))) uint8_t nr_bytes[2][HEAD];
+  __shared__ float nr_score[kAttendGroup][256 / kHeadItems > 0 ? 256 / kHeadItems : 1];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  // every load first: the key/value pair of the thread (threads below HALF),
+  // then its query items with their gains and turns
+  float kx[2] = {0.0f, 0.0f}, vx[2] = {0.0f, 0.0f}, kg[2] = {0.0f, 0.0f}, kt[2] = {0.0f, 0.0f};
+  if (tid < HALF) {
+    kx[0] = a.k_raw[tid];
+    kx[1] = a.k_raw[tid + HALF];
+    vx[0] = a.v_raw[tid];
+    vx[1] = a.v_raw[tid + HALF];
+    kg[0] = a.k_gain[tid];
+    kg[1] = a.k_gain[tid + HALF];
+    kt[0] = a.turn[2 * tid];
+    kt[1] = a.turn[2 * tid + 1];
+  }
+  float qf[kQItems][8];
+  float4_t qgain[kQItems][2], qturn[kQItems][4];
+#pragma unroll
+  for (int i = 0; i < kQItems; ++i) {
+    const int item = tid + 256 * i;
+    const float4_t *q = reinterpret_cast<const float4_t *>(a.query + 8 * item);
+    const float4_t u = q[0], v = q[1];
+    qf[i][0] = u.x; qf[i][1] = u.y; qf[i][2] = u.z; qf[i][3] = u.w;
+    qf[i][4] = v.x; qf[i][5] = v.y; qf[i][6] = v.z; qf[i][7] = v.w;
+    const int d0 = 8 * (item % kHeadItems);
+    const int j0 = d0 < HALF ? d0 : d0 - HALF;
+    qgain[i][0] = *reinterpret_cast<const float4_t *>(a.q_gain + d0);
+    qgain[i][1] = *reinterpret_cast<const float4_t *>(a.q_gain + d0 + 4);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) qturn[i][w] = *reinterpret_cast<const float4_t *>(a.turn + 2 * j0 + 4 * w);
+  }
+  // key: norm, gain, turn; value: norm (session_attend 11504-11510)
+  {
+    double ks = (double)kx[0] * (double)kx[0] + (double)kx[1] * (double)kx[1];
+    double vs2 = (double)vx[0] * (double)vx[0] + (double)vx[1] * (double)vx[1];
+    ks = wave_sum_f64_to_last(ks);
+    vs2 = wave_sum_f64_to_last(vs2);
+    if (lane == 63) {
+      nr_red[0][wave] = ks;
+      nr_red[1][wave] = vs2;
+    }
+    __syncthreads();
+    double kt_sum = nr_red[0][0], vt_sum = nr_red[1][0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) {
+      kt_sum += nr_red[0][w];
+      vt_sum += nr_red[1][w];
+    }
+    if (tid < HALF) {
+      const float ksh = rms_shrink(kt_sum, HEAD, a.eps);
+      const float vsh = rms_shrink(vt_sum, HEAD, a.eps);
+      float lo = kx[0] * ksh, hi = kx[1] * ksh;
+      lo = lo * kg[0];
+      hi = hi * kg[1];
+      const float k0 = lo * kt[0] - hi * kt[1];
+      const float k1 = hi * kt[0] + lo * kt[1];
+      const uint8_t b0 = e4m3_code(k0 / a.k_code_scale), b1 = e4m3_code(k1 / a.k_code_scale);
+      const uint8_t c0b = e4m3_code(vx[0] * vsh / a.v_code_scale);
+      const uint8_t c1b = e4m3_code(vx[1] * vsh / a.v_code_scale);
+      const size_t row = (size_t)(pos % a.cache_span) * a.kv_width;
+      a.k_ring[row + tid] = b0;
+      a.k_ring[row + tid + HALF] = b1;
+      a.v_ring[row + tid] = c0b;
+      a.v_ring[row + tid + HALF] = c1b;
+      nr_bytes[0][tid] = b0;
+      nr_bytes[0][tid + HALF] = b1;
+      nr_bytes[1][tid] = c0b;
+      nr_bytes[1][tid + HALF] = c1b;
+    }
+  }
+  __syncthreads();
+  // the query heads as the chunks prepare them, then each item's share of
+  // its head's score against the decoded key bytes
+#pragma unroll
+  for (int i = 0; i < kQItems; ++i) {
+    const int item = tid + 256 * i;
+    const int h = item / kHeadItems;
+    const int d0 = 8 * (item % kHeadItems);
+    double ss = 0.0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += (double)qf[i][e] * (double)qf[i][e];
+#pragma unroll
+    for (int off = kHeadItems / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    const float shrink = rms_shrink(ss, HEAD, a.eps);
+    const float gg[8] = {qgain[i][0].x, qgain[i][0].y, qgain[i][0].z, qgain[i][0].w,
+                         qgain[i][1].x, qgain[i][1].y, qgain[i][1].z, qgain[i][1].w};
+    float own[8], other[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      own[e] = qf[i][e] * shrink;
+      own[e] = own[e] * gg[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) other[e] = __shfl_xor(own[e], kHeadItems / 2);
+    const bool low = d0 < HALF;
+    const uint2_t kb = *reinterpret_cast<const uint2_t *>(&nr_bytes[0][d0]);
+    const half8_t kd = decode8<0>(kb.x, kb.y);
+    float part = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float c = qturn[i][e >> 1][2 * (e & 1)];
+      const float sn = qturn[i][e >> 1][2 * (e & 1) + 1];
+      const float qv = low ? own[e] * c - other[e] * sn : own[e] * c + other[e] * sn;
+      part = __builtin_fmaf(qv, (float)kd[e], part);
+    }
+#pragma unroll
+    for (int off = kHeadItems / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
+    if (item % kHeadItems == 0) nr_score[h][0] = part * a.key_scale;
+  }
+  __syncthreads();
+  // the partial: every head blends the one value row with weight e^0 = 1
+  for (int i = tid; i < kAttendGroup * HEAD / 8; i += 256) {
+    const int h = i / (HEAD / 8);
+    const int d0 = 8 * (i % (HEAD / 8));
+    const uint2_t vb = *reinterpret_cast<const uint2_t *>(&nr_bytes[1][d0]);
+    const half8_t vd = decode8<0>(vb.x, vb.y);
+    float *dst = a.part_out + ((size_t)pc * a.head_count + h) * HEAD + d0;
+    *reinterpret_cast<float4_t *>(dst) = float4_t{(float)vd[0] * a.value_scale, (float)vd[1] * a.value_scale,
+                                                  (float)vd[2] * a.value_scale, (float)vd[3] * a.value_scale};
+    *reinterpret_cast<float4_t *>(dst + 4) = float4_t{(float)vd[4] * a.value_scale, (float)vd[5] * a.value_scale,
+                                                      (float)vd[6] * a.value_scale, (float)vd[7] * a.value_scale};
+  }
+  if (tid < kAttendGroup) {
+    a.part_peak[(size_t)pc * a.head_count + tid] = nr_score[tid][0];
+    a.part_total[(size_t)pc * a.head_count + tid] = 1.0f;
+  }
+}
+
 // The split form.  A workgroup of four waves takes a chunk of C positions
 // (32 or 64) of one lane.  The two products are split differently among the
 // waves, so that each wave's dependent chain is a quarter of the chunk's work:
@@ -172,26 +318,19 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
   const int block = blockIdx.x;
   const int lane_id = blockIdx.z;
   const int pos = (a.place_dev ? *a.place_dev : a.place0) + lane_id;
-  const int span_count = a.window > 0 ? min(pos + 1, a.window) : pos + 1;
-  const int place_start = pos - span_count + 1;
+  const int span_full = a.window > 0 ? min(pos + 1, a.window) : pos + 1;
+  const int place_start = pos - span_full + 1;
+  // PREP with k_raw: the lane's own position is the workgroup after the
+  // chunks, which cover the positions before it
+  const bool new_row = PREP && a.k_raw != nullptr;
+  const int span_count = new_row ? span_full - 1 : span_full;
   const int blocks_seen = (span_count + C - 1) / C;
-  if (block >= blocks_seen) return;  // past this lane's span: the whole workgroup
   const int pc = lane_id * a.chunks + block;
-  // PREP: this workgroup's chunk holds the lane's position, whose key and
-  // value rows it prepares (one key pair j, j + HALF and one value pair a
-  // thread, threads below HALF)
-  const bool row_here = PREP && a.k_raw != nullptr && block == blocks_seen - 1;
-  float kx[2] = {0.0f, 0.0f}, vx[2] = {0.0f, 0.0f}, kg[2] = {0.0f, 0.0f}, kt[2] = {0.0f, 0.0f};
-  if (row_here && tid < HALF) {
-    kx[0] = a.k_raw[tid];
-    kx[1] = a.k_raw[tid + HALF];
-    vx[0] = a.v_raw[tid];
-    vx[1] = a.v_raw[tid + HALF];
-    kg[0] = a.k_gain[tid];
-    kg[1] = a.k_gain[tid + HALF];
-    kt[0] = a.turn[2 * tid];
-    kt[1] = a.turn[2 * tid + 1];
+  if (new_row && block == blocks_seen) {
+    if (PREP) attend_new_row<HEAD>(a, pos, pc);
+    return;
   }
+  if (block >= blocks_seen) return;  // past this lane's span: the whole workgroup
   const size_t kv_off = (size_t)kv * HEAD;
   const int c0 = block * C;  // the chunk's first position (relative to place_start)
 
@@ -254,8 +393,6 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
         a.value_store + (size_t)slot * a.kv_width + kv_off + wave * DS + 16 * (lane % LPR)));
   }
 
-  __shared__ double kv_red[2][W];
-  __shared__ __attribute__((aligned(16))) uint8_t row_bytes[2][HEAD];
   if (PREP) {
     // Each head's items are 32 (HEAD 256) or 64 (HEAD 512) consecutive
     // threads; the pair (j, j + HALF) of a dim sits HALF / 8 items apart.
@@ -287,45 +424,6 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
         qf[i][e] = low ? own[e] * c - other[e] * sn : own[e] * c + other[e] * sn;
       }
     }
-    if (row_here) {
-      // key: norm, gain, turn; value: norm (session_attend 11504-11510)
-      double ks = (double)kx[0] * (double)kx[0] + (double)kx[1] * (double)kx[1];
-      double vs2 = (double)vx[0] * (double)vx[0] + (double)vx[1] * (double)vx[1];
-      ks = wave_sum_f64_to_last(ks);
-      vs2 = wave_sum_f64_to_last(vs2);
-      if (lane == 63) {
-        kv_red[0][wave] = ks;
-        kv_red[1][wave] = vs2;
-      }
-      __syncthreads();
-      double kt_sum = kv_red[0][0], vt_sum = kv_red[1][0];
-#pragma unroll
-      for (int w = 1; w < W; ++w) {
-        kt_sum += kv_red[0][w];
-        vt_sum += kv_red[1][w];
-      }
-      if (tid < HALF) {
-        const float ksh = rms_shrink(kt_sum, HEAD, a.eps);
-        const float vsh = rms_shrink(vt_sum, HEAD, a.eps);
-        float lo = kx[0] * ksh, hi = kx[1] * ksh;
-        lo = lo * kg[0];
-        hi = hi * kg[1];
-        const float k0 = lo * kt[0] - hi * kt[1];
-        const float k1 = hi * kt[0] + lo * kt[1];
-        const uint8_t b0 = e4m3_code(k0 / a.k_code_scale), b1 = e4m3_code(k1 / a.k_code_scale);
-        const uint8_t c0b = e4m3_code(vx[0] * vsh / a.v_code_scale);
-        const uint8_t c1b = e4m3_code(vx[1] * vsh / a.v_code_scale);
-        const size_t row = (size_t)(pos % a.cache_span) * a.kv_width + kv_off;
-        a.k_ring[row + tid] = b0;
-        a.k_ring[row + tid + HALF] = b1;
-        a.v_ring[row + tid] = c0b;
-        a.v_ring[row + tid + HALF] = c1b;
-        row_bytes[0][tid] = b0;
-        row_bytes[0][tid + HALF] = b1;
-        row_bytes[1][tid] = c0b;
-        row_bytes[1][tid + HALF] = c1b;
-      }
-    }
   }
 
   // query operands, x = hi + lo in binary16
@@ -344,11 +442,6 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
   }
   __syncthreads();
 
-  // the lane's own new key row (PREP): the bytes just written, not the stale ones loaded
-  if (row_here && tk == span_count - 1) {
-#pragma unroll
-    for (int q = 0; q < QD / 16; ++q) kr[q] = *reinterpret_cast<const uint4_t *>(&row_bytes[0][QD * g + 16 * q]);
-  }
   // ---- scores of the wave's PW positions for the 8 heads, all dims
   float sc[4];
   float m_w[4];
@@ -394,15 +487,6 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
       uint2_t *dst = reinterpret_cast<uint2_t *>(vw + (lane / LPR + RPI * i) * VP + 16 * (lane % LPR));
       dst[0] = uint2_t{vr[i][0], vr[i][1]};
       dst[1] = uint2_t{vr[i][2], vr[i][3]};
-    }
-    if (row_here) {
-      // the new value row's slice replaces the stale one staged above (the
-      // staging wrote whole 8-byte words; every lane of the wave is past it)
-      __builtin_amdgcn_wave_barrier();
-      const int r = span_count - 1 - c0;
-      if (lane < DS / 8)
-        *reinterpret_cast<uint2_t *>(vw + r * VP + 8 * lane) =
-            *reinterpret_cast<const uint2_t *>(&row_bytes[1][wave * DS + 8 * lane]);
     }
   }
   __syncthreads();
@@ -501,7 +585,7 @@ __global__ __launch_bounds__(256) void attend_fold_kernel(const float *part_out_
                                                           const float *part_total_all,
                                                           int chunk_slots, int chunk, int place0,
                                                           const int *place_dev, int window,
-                                                          int head_count, int head_size,
+                                                          int extra, int head_count, int head_size,
                                                           float *blend_all, int o_stride) {
   constexpr int SL = 256 / DIMS;
   __shared__ float red_m[SL];
@@ -511,7 +595,9 @@ __global__ __launch_bounds__(256) void attend_fold_kernel(const float *part_out_
   const int d = tid % DIMS, sl = tid / DIMS;
   const int pos = (place_dev ? *place_dev : place0) + lane_id;
   const int span = window > 0 ? min(pos + 1, window) : pos + 1;
-  const int chunks = (span + chunk - 1) / chunk;
+  // extra: the lane's own position has a partial of its own, after the
+  // chunks of the positions before it
+  const int chunks = extra ? (span - 1 + chunk - 1) / chunk + 1 : (span + chunk - 1) / chunk;
   const size_t base = (size_t)lane_id * chunk_slots;
   const size_t step = (size_t)head_count * head_size;
   const float *pout = part_out_all + base * step + (size_t)h * head_size + blockIdx.z * DIMS + d;
@@ -602,7 +688,7 @@ static void attend_launch_chunk(const AttendArgs &a, dim3 grid, int chunk, bool 
 
 static hipError_t attend_fold(const AttendArgs &a, int chunks, int chunk, int place0,
                               const int *place_dev, int window, int lanes, int head_size,
-                              float *blend_out, hipStream_t stream);
+                              float *blend_out, hipStream_t stream, int extra = 0);
 
 // `lanes` query lanes at positions place0 .. place0 + lanes - 1, each seeing
 // the last `window` positions up to its own (0: every position from 0).  Lane
@@ -666,7 +752,7 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
 // The fold of a launch's chunk partials into `blend_out`.
 static hipError_t attend_fold(const AttendArgs &a, int chunks, int chunk, int place0,
                               const int *place_dev, int window, int lanes, int head_size,
-                              float *blend_out, hipStream_t stream) {
+                              float *blend_out, hipStream_t stream, int extra) {
   const int head_count = a.head_count;
   const int q_stride = a.q_stride;
   // One lane: 16 dims a fold workgroup (the most workgroups); many lanes
@@ -678,7 +764,7 @@ static hipError_t attend_fold(const AttendArgs &a, int chunks, int chunk, int pl
   const dim3 fgrid(head_count, lanes, head_size / dims);
 #define IGL_FOLD(D, P)                                                                             \
   hipLaunchKernelGGL((attend_fold_kernel<D, P>), fgrid, dim3(256), 0, stream, a.part_out,         \
-                     a.part_peak, a.part_total, chunks, chunk, place0, place_dev, window,          \
+                     a.part_peak, a.part_total, chunks, chunk, place0, place_dev, window, extra,   \
                      head_count, head_size, blend_out, q_stride)
 #define IGL_FOLD_PER(D)                                                                            \
   switch (per) {                                                                                   \
@@ -718,7 +804,9 @@ extern "C" hipError_t igl_launch_attend_prep(const uint8_t *key_store, const uin
                                              hipStream_t stream) {
   AttendArgs a;
   const int chunk = attend_chunk(place_bound, window, 1);
-  const int chunks = attend_blocks(place_bound, window, 1);
+  // with k_raw, one slot more: the position's own partial (attend_new_row)
+  const int extra = k_raw ? 1 : 0;
+  const int chunks = attend_blocks(place_bound, window, 1) + extra;
   if ((((uintptr_t)query) & 15u) || (((uintptr_t)q_gain) & 15u) || (((uintptr_t)turn) & 15u) ||
       !place_dev || !turn)
     return hipErrorInvalidValue;
@@ -731,7 +819,7 @@ extern "C" hipError_t igl_launch_attend_prep(const uint8_t *key_store, const uin
   a.place_dev = place_dev;
   a.window = window;
   a.chunks = chunks;
-  a.final_out = chunks == 1 ? blend_out : nullptr;
+  a.final_out = chunks == 1 && !extra ? blend_out : nullptr;
   a.q_stride = kAttendGroup * head_size;
   a.query = query;
   a.key_scale = key_scale * 256.0f * score_scale;
@@ -762,8 +850,16 @@ extern "C" hipError_t igl_launch_attend_prep(const uint8_t *key_store, const uin
   else
     return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || chunks == 1) return e;
-  return attend_fold(a, chunks, chunk, place_bound, place_dev, window, 1, head_size, blend_out, stream);
+  if (e != hipSuccess || a.final_out) return e;
+  return attend_fold(a, chunks, chunk, place_bound, place_dev, window, 1, head_size, blend_out, stream,
+                     extra);
+}
+
+// Floats of workspace igl_launch_attend_prep needs for the same arguments
+// (with a key/value row to write: one partial slot more than the chunks).
+extern "C" size_t igl_attend_prep_work_floats(int place_bound, int window, int head_size, int writes_row) {
+  const size_t blocks = (size_t)attend_blocks(place_bound, window, 1) + (writes_row ? 1 : 0);
+  return blocks * (size_t)kAttendGroup * ((size_t)head_size + 2);
 }
 
 // Floats of workspace igl_launch_attend needs for the same arguments.
@@ -786,7 +882,9 @@ extern "C" size_t igl_attend_work_floats_limit(int span_limit, int lanes, int he
   const int b_short = attend_blocks(short_top - 1, 0, 1);
   const int b_long = attend_blocks(span_limit - 1, 0, 1);
   const size_t blocks = (size_t)(b_short > b_long ? b_short : b_long);
-  return (size_t)lanes * blocks * (size_t)head_count * ((size_t)head_size + 2);
+  // a one-lane decode step with its own position's slot needs blocks + 1
+  const size_t slots = (size_t)lanes * blocks > blocks + 1 ? (size_t)lanes * blocks : blocks + 1;
+  return slots * (size_t)head_count * ((size_t)head_size + 2);
 }
 
 // ---- the workspace of the entry that allocates nothing ---------------------

@@ -151,6 +151,8 @@ hipError_t igl_launch_attend_prep(const uint8_t *key_store, const uint8_t *value
                                   float score_scale, float *blend_out, float *work,
                                   hipStream_t stream);
 
+size_t igl_attend_prep_work_floats(int place_bound, int window, int head_size, int writes_row);
+
 /* The desk's HIP stream, for the engine's own launches (back_hip.c). */
 void *igl_desk_stream(igl_desk *desk);
 

@@ -21,10 +21,11 @@ def lib():
     from igllm_amd import native
 
     lib = native.load()
-    for name in ("igl_attend_work_floats", "igl_attend_work_floats_limit"):
+    for name in ("igl_attend_work_floats", "igl_attend_work_floats_limit", "igl_attend_prep_work_floats"):
         getattr(lib, name).restype = ctypes.c_size_t
     lib.igl_attend_work_floats.argtypes = [ctypes.c_int] * 5
     lib.igl_attend_work_floats_limit.argtypes = [ctypes.c_int] * 4
+    lib.igl_attend_prep_work_floats.argtypes = [ctypes.c_int] * 4
     return lib
 
 
@@ -53,3 +54,17 @@ def test_longest_span_alone_falls_short(lib):
     need = lib.igl_attend_work_floats(8192 - lanes, 0, lanes, HEADS, HEAD)
     assert need > max(one, many)
     assert need <= lib.igl_attend_work_floats_limit(W, lanes, HEADS, HEAD)
+
+
+@pytest.mark.parametrize("window_limit", [1, 33, 4097, 8192, 8193, 12000])
+@pytest.mark.parametrize("lane_limit", [1, 16, 2048])
+@pytest.mark.parametrize("head", [256, 512])
+def test_decode_step_fits_the_engine_allocation(lib, window_limit, lane_limit, head):
+    """The decode step's prepared attention writes one partial slot more than
+    its chunks (the new position's own); its graph is sized for the last
+    position, on full and sliding layers, with and without a row to write."""
+    have = lib.igl_attend_work_floats_limit(window_limit, lane_limit, HEADS, head)
+    for window in (0, 512):
+        for writes in (0, 1):
+            need = lib.igl_attend_prep_work_floats(window_limit - 1, window, head, writes)
+            assert need <= have, (window, writes, need, have)
