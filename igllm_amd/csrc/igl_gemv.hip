@@ -2657,14 +2657,17 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
   a.act_vec = ((((uintptr_t)act) & 15u) == 0 && (act_stride & 3) == 0) ? 1 : 0;
   // One to four lanes on the integer dot path (aligned activations, M K <=
   // 16384): eight-row tiles from 128 units up for one and two lanes, so the
-  // staging of x is shared by more rows; below that two-row tiles for one lane
-  // (twice the workgroups, half the loads a lane in flight: measured ~2%
-  // faster at 8192 x 2048 than four); enough waves on a row tile that each
-  // lane holds one unit (two past 256).
+  // staging of x is shared by more rows, and on tall planes (32768 rows and
+  // up: at least 1024 workgroups of 32 rows), where every workgroup's staging
+  // of x would otherwise be read as often as the weights (the 262144 x 1536
+  // head: 52 -> 41 us); below that two-row tiles for one lane (twice the
+  // workgroups, half the loads a lane in flight: measured ~2% faster at
+  // 8192 x 2048 than four, and eight rows 25% slower); enough waves on a row
+  // tile that each lane holds one unit (two past 256).
   if (a.act_vec && lanes <= 4 && lanes * K <= kDotMaxItems * kGemvThreads * 8 &&
       K / 32 <= 8 * kWave) {
     const int units = K / 32;
-    const int R = lanes <= 2 && units >= 128 ? 8 : lanes == 1 ? 2 : 4;
+    const int R = lanes <= 2 && (units >= 128 || N >= 32768) ? 8 : lanes == 1 ? 2 : 4;
     const int tiles = (N + R - 1) / R;
     const int upl = units > 4 * kWave ? 2 : 1;
     int ksplit = 1;
