@@ -304,8 +304,8 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
 
   __shared__ half8_t qs[2][kAttendGroup][HEAD / 8];
   __shared__ float ps[kAttendGroup][C];
-  __shared__ float wm[W][kAttendGroup];
-  __shared__ float wl[W][kAttendGroup];
+  __shared__ __attribute__((aligned(16))) float wm[W][kAttendGroup];
+  __shared__ __attribute__((aligned(16))) float wl[W][kAttendGroup];
   __shared__ __attribute__((aligned(16))) uint8_t vs[W][C * VP];
 
   const int tid = threadIdx.x;
@@ -333,6 +333,13 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
   if (block >= blocks_seen) return;  // past this lane's span: the whole workgroup
   const size_t kv_off = (size_t)kv * HEAD;
   const int c0 = block * C;  // the chunk's first position (relative to place_start)
+  // ring slot of relative position t: (place_start + t) % cache_span, from one
+  // uniform remainder (0 <= t < span <= cache_span, so one wrap at most)
+  const int ring0 = place_start % a.cache_span;
+  auto ring_slot = [&](int t) {
+    const int slot = ring0 + t;
+    return slot >= a.cache_span ? slot - a.cache_span : slot;
+  };
 
   // ---- loads, all issued before the first wait
   constexpr int kQTotal = kAttendGroup * HEAD / 8;
@@ -376,7 +383,7 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
   uint4_t kr[QD / 16];
   {
     const int t = min(tk, span_count - 1);
-    const int slot = (place_start + t) % a.cache_span;
+    const int slot = ring_slot(t);
     const uint4_t *row =
         reinterpret_cast<const uint4_t *>(a.key_store + (size_t)slot * a.kv_width + kv_off + QD * g);
 #pragma unroll
@@ -388,7 +395,7 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
 #pragma unroll
   for (int i = 0; i < VL; ++i) {
     const int t = min(c0 + lane / LPR + RPI * i, span_count - 1);
-    const int slot = (place_start + t) % a.cache_span;
+    const int slot = ring_slot(t);
     vr[i] = __builtin_nontemporal_load(reinterpret_cast<const uint4_t *>(
         a.value_store + (size_t)slot * a.kv_width + kv_off + wave * DS + 16 * (lane % LPR)));
   }
@@ -542,16 +549,25 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) o[t][r] = xsum32(o[t][r]);
   if (g >= 2) return;
+  // the waves' peaks and sums of heads 4g .. 4g + 3, read at once
+  float4_t pk[W], tl[W];
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    pk[w] = *reinterpret_cast<const float4_t *>(&wm[w][4 * g]);
+    tl[w] = *reinterpret_cast<const float4_t *>(&wl[w][4 * g]);
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int h = 4 * g + r;
-    float Mh = wm[0][h];
+    float Mh = pk[0][r];
 #pragma unroll
-    for (int w = 1; w < W; ++w) Mh = fmaxf(Mh, wm[w][h]);
+    for (int w = 1; w < W; ++w) Mh = fmaxf(Mh, pk[w][r]);
     float L = 0.0f;
 #pragma unroll
-    for (int w = 0; w < W; ++w)
-      if (wm[w][h] != -INFINITY) L += wl[w][h] * __expf(wm[w][h] - Mh);
+    for (int w = 0; w < W; ++w) {
+      const float e = pk[w][r] != -INFINITY ? __expf(pk[w][r] - Mh) : 0.0f;
+      L += tl[w][r] * e;
+    }
     float *dst;
     float mul;
     if (a.final_out) {

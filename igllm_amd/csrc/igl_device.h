@@ -65,17 +65,20 @@ __device__ __forceinline__ double lane_read_f64(double v, int lane) {
   return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
-// Sum of one double per thread over a workgroup of up to 16 waves, the same
+// Sum of one double per thread over a workgroup of WAVES waves, the same
 // total in every thread: DPP within each wave, then the wave sums in wave
 // order.  `red` holds one double a wave; the trailing barrier lets the caller
-// reuse it.
+// reuse it.  The wave count is a constant, not blockDim: blockDim comes from
+// the dispatch packet through a vector load, and the wait for it would also
+// wait for every load the kernel issued before it (a GEMV's weights).
+template <int WAVES = 4>
 __device__ __forceinline__ double block_sum_f64(double v, double *red) {
-  const int waves = (blockDim.x + 63) >> 6;
   v = wave_sum_f64_to_last(v);
   if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = v;
   __syncthreads();
   double total = red[0];
-  for (int w = 1; w < waves; ++w) total += red[w];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) total += red[w];
   __syncthreads();
   return total;
 }

@@ -12,15 +12,15 @@ namespace igl {
 // RMS norm of one vector per workgroup: sum of squares in double (the
 // reference accumulates in double, kern_norm_rms app_core.c:4667-4684), then
 // x * (mean + eps)^-1/2 * gain.
-__global__ void norm_rms_kernel(const float *in, const float *gain, int n, int stride, float eps,
-                                float *out) {
+__global__ __launch_bounds__(256) void norm_rms_kernel(const float *in, const float *gain, int n,
+                                                       int stride, float eps, float *out) {
   __shared__ double part[16];
   const float *x = in + (size_t)blockIdx.x * stride;
   float *y = out + (size_t)blockIdx.x * stride;
   double acc = 0.0;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) acc += (double)x[i] * (double)x[i];
+  for (int i = threadIdx.x; i < n; i += 256) acc += (double)x[i] * (double)x[i];
   const float shrink = rms_shrink(block_sum_f64(acc, part), n, eps);
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+  for (int i = threadIdx.x; i < n; i += 256) {
     const float v = x[i] * shrink;
     y[i] = gain ? v * gain[i] : v;
   }
