@@ -1745,9 +1745,34 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
   const int u_w0 = part * (NG * 4);
 
   // Staging loads go out first and unconditionally (indices past the end are
-  // clamped and their values dropped), then the code loads, so the block
-  // waits one round trip for its gains and activations while the codes are
-  // still in flight.
+  // clamped and their values dropped), then the code loads.  The activations
+  // go first: they come from the cache, the gains and codes from memory, and
+  // loads retire in order, so the B tiles are formed while the gains and
+  // codes are still in flight (gains first: 3.3 us into the launch under a
+  // full stream, against about 1 us for the activations).
+  // Activations: item i = 4 M u + 4 m + g is x[m][32 u + 8 g .. + 7] (at most
+  // 8 a thread: 64 units x 8 lanes x 4 groups).  B columns m >= M are never
+  // written; they only reach outputs that are not stored.  u = i / (4 M) by a
+  // multiply, exact for every i < 2048 and M <= 8.
+  const int per_u = 4 * a.M;
+  const int items = CU * per_u;
+  const uint32_t inv_u = (65536u + (uint32_t)per_u - 1u) / (uint32_t)per_u;
+  float4_t xa[8], xb[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int i = min(tid + 256 * k, items - 1);
+    const int u = (int)(((uint32_t)i * inv_u) >> 16);
+    const int m = (i - u * per_u) >> 2;
+    const float *src =
+        a.act + (size_t)m * (size_t)a.act_stride + (size_t)(unit_c0 + u) * 32 + 8 * (i & 3);
+    if (VEC) {
+      xa[k] = *reinterpret_cast<const float4_t *>(src);
+      xb[k] = *reinterpret_cast<const float4_t *>(src + 4);
+    } else {
+      xa[k] = float4_t{src[0], src[1], src[2], src[3]};
+      xb[k] = float4_t{src[4], src[5], src[6], src[7]};
+    }
+  }
   // Gains: float4 runs of each row's chunk (at most 4 a thread: 64 rows x 16).
   const int gain_runs = rows_b * (CU >> 2);
   float4_t gv[4];
@@ -1762,26 +1787,6 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
                                                  unit_c0 + 4 * c4);
     }
   }
-  // Activations: item i = 32 u + 4 m + g is x[m][32 u + 8 g .. + 7] (at most
-  // 8 a thread: 64 units x 8 lane slots x 4 groups).  Slots m >= M are
-  // skipped; their B columns are never read into an output that is stored.
-  const int items = CU * 32;
-  float4_t xa[8], xb[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int i = min(tid + 256 * k, items - 1);
-    const int u = i >> 5;
-    const int m = min((i >> 2) & 7, a.M - 1);
-    const float *src =
-        a.act + (size_t)m * (size_t)a.act_stride + (size_t)(unit_c0 + u) * 32 + 8 * (i & 3);
-    if (VEC) {
-      xa[k] = *reinterpret_cast<const float4_t *>(src);
-      xb[k] = *reinterpret_cast<const float4_t *>(src + 4);
-    } else {
-      xa[k] = float4_t{src[0], src[1], src[2], src[3]};
-      xb[k] = float4_t{src[4], src[5], src[6], src[7]};
-    }
-  }
 
   // Codes: lane (r, q) takes unit u_w0 + 4 g + q of its row.
   uint4_t w[NG];
@@ -1794,6 +1799,52 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
     for (int g = 0; g < NG; ++g) w[g] = __builtin_nontemporal_load(src + 4 * g);
   }
 
+  // Nothing below may sink a staging load past the code loads (a load used
+  // only under a branch is otherwise moved into it, and its wait then covers
+  // every code load).
+  asm volatile("" ::: "memory");
+
+  // B tiles; the four items of a (unit, lane) sit in one quad and agree on e.
+  // Past the items (a bound uniform over the workgroup) a thread's quads
+  // recompute the last item and store nothing.
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (256 * k >= items) break;
+    const int i_raw = tid + 256 * k;
+    const bool own = i_raw < items;
+    const int i = min(i_raw, items - 1);
+    const int u = (int)(((uint32_t)i * inv_u) >> 16);
+    const int rem = i - u * per_u;
+    const int g = rem & 3;
+    const int m = rem >> 2;
+    const float v[8] = {xa[k].x, xa[k].y, xa[k].z, xa[k].w, xb[k].x, xb[k].y, xb[k].z, xb[k].w};
+    float peak = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) peak = fmaxf(peak, fabsf(v[j]));
+    peak = fmaxf(peak, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, peak), 0xB1, 0xF, 0xF, false)));
+    peak = fmaxf(peak, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, peak), 0x4E, 0xF, 0xF, false)));
+    int e = 0;
+    if (peak > 0.0f && peak <= 3.4e38f) {
+      int power;
+      (void)frexpf(peak, &power);  // peak in [2^(power-1), 2^power)
+      e = min(max(15 - power, -126), 126);
+    }
+    const float up = __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
+    if (own && g == 0) sc[u * 8 + m] = __builtin_bit_cast(float, (uint32_t)(127 - e) << 23);
+    half8_t hi, lo;
+    constexpr int kOrder[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float s = v[kOrder[j]] * up;
+      const _Float16 h = (_Float16)s;
+      hi[j] = h;
+      lo[j] = (_Float16)(s - (float)h);
+    }
+    if (own) {
+      bt[(u * 4 + g) * 16 + m] = __builtin_bit_cast(uint4_t, hi);
+      bt[(u * 4 + g) * 16 + m + 8] = __builtin_bit_cast(uint4_t, lo);
+    }
+  }
   // Gains stored [unit][row].
   if (VEC) {
 #pragma unroll
@@ -1818,41 +1869,6 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
     }
   }
 
-  // B tiles; the four items of a (unit, lane) sit in one quad and agree on e.
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int i = tid + 256 * k;
-    if (i >= items) break;
-    const int g = i & 3;
-    const int u = i >> 5;
-    const int m = (i >> 2) & 7;
-    if (m >= a.M) continue;
-    const float v[8] = {xa[k].x, xa[k].y, xa[k].z, xa[k].w, xb[k].x, xb[k].y, xb[k].z, xb[k].w};
-    float peak = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) peak = fmaxf(peak, fabsf(v[j]));
-    peak = fmaxf(peak, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, peak), 0xB1, 0xF, 0xF, false)));
-    peak = fmaxf(peak, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, peak), 0x4E, 0xF, 0xF, false)));
-    int e = 0;
-    if (peak > 0.0f && peak <= 3.4e38f) {
-      int power;
-      (void)frexpf(peak, &power);  // peak in [2^(power-1), 2^power)
-      e = min(max(15 - power, -126), 126);
-    }
-    const float up = __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
-    if (g == 0) sc[u * 8 + m] = __builtin_bit_cast(float, (uint32_t)(127 - e) << 23);
-    half8_t hi, lo;
-    constexpr int kOrder[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float s = v[kOrder[j]] * up;
-      const _Float16 h = (_Float16)s;
-      hi[j] = h;
-      lo[j] = (_Float16)(s - (float)h);
-    }
-    bt[(u * 4 + g) * 16 + m] = __builtin_bit_cast(uint4_t, hi);
-    bt[(u * 4 + g) * 16 + m + 8] = __builtin_bit_cast(uint4_t, lo);
-  }
   __syncthreads();
 
   const uint32_t exp16 = 0x4C004C00u;
