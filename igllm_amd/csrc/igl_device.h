@@ -71,6 +71,18 @@ __device__ __forceinline__ double lane_read_f64(double v, int lane) {
 // reuse it.  The wave count is a constant, not blockDim: blockDim comes from
 // the dispatch packet through a vector load, and the wait for it would also
 // wait for every load the kernel issued before it (a GEMV's weights).
+// block_sum_f64 without the trailing barrier, for an LDS slot read once.
+template <int WAVES = 4>
+__device__ __forceinline__ double block_sum_f64_once(double v, double *red) {
+  v = wave_sum_f64_to_last(v);
+  if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double total = red[0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) total += red[w];
+  return total;
+}
+
 template <int WAVES = 4>
 __device__ __forceinline__ double block_sum_f64(double v, double *red) {
   v = wave_sum_f64_to_last(v);

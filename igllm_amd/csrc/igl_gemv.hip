@@ -1255,81 +1255,122 @@ struct GemvGroupArgs {
   int apply_scale;
   const float *norm_gain;
   float eps;
+  int pro_vec;            // every prologue vector (and state_out) 16-byte aligned
 };
 
-// The update above for K <= 256 HELD, into `xs` (K floats of LDS), in two
-// steps so that a kernel can issue the loads ahead of its weight loads.
-// Thread t holds elements t + 256 k, as norm_add_kernel does.  Every load is
-// issued: an absent vector reads state_in in its place and elements past K
-// reread element K - 1, and the values are then masked.
-template <int HELD>
+// The update above in the kernel's digit form (into `dig` / `down`, as
+// digit_store stages x), in two steps so that a kernel can issue the loads
+// ahead of its weight loads.  Thread t holds the eight-element groups
+// g = t + 256 j (j < PG) of every K-vector, so a group's x is formed in
+// registers and digitized there (the four groups of a unit sit in one quad):
+// nothing passes through LDS but the two block sums and the digits.  Every
+// load is issued: an absent vector reads state_in in its place, groups past
+// K / 8 reread the last one, and the values are then masked.  The element
+// operations are norm_add_kernel's; only the double sums of the two norms add
+// in another order (a thread's eight elements, then the waves).
+template <int PG>
 struct PrologueLoads {
-  float sv[HELD], lv[HELD], gv[HELD], nv[HELD];
+  float v[PG][4][8];  // state_in, lift, lift_gain, norm_gain
 };
 
-template <int HELD>
-__device__ __forceinline__ void prologue_loads(const GemvGroupArgs &a, PrologueLoads<HELD> &p) {
-  const float *lift = a.lift ? a.lift : a.state_in;
-  const float *lift_gain = a.lift ? a.lift_gain : a.state_in;
-  const float *norm_gain = a.norm_gain ? a.norm_gain : a.state_in;
+template <int PG>
+__device__ __forceinline__ void prologue_loads(const GemvGroupArgs &a, PrologueLoads<PG> &p) {
+  const float *src[4] = {a.state_in, a.lift ? a.lift : a.state_in,
+                         a.lift ? a.lift_gain : a.state_in,
+                         a.norm_gain ? a.norm_gain : a.state_in};
+  const int groups = a.K >> 3;
 #pragma unroll
-  for (int k = 0; k < HELD; ++k) {
-    const int i = min((int)threadIdx.x + 256 * k, a.K - 1);
-    p.sv[k] = a.state_in[i];
-    p.lv[k] = lift[i];
-    p.gv[k] = lift_gain[i];
-    p.nv[k] = norm_gain[i];
+  for (int j = 0; j < PG; ++j) {
+    const int g = min((int)threadIdx.x + 256 * j, groups - 1);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float *q = src[w] + 8 * g;
+      if (a.pro_vec) {
+        const float4_t lo = *reinterpret_cast<const float4_t *>(q);
+        const float4_t hi = *reinterpret_cast<const float4_t *>(q + 4);
+        p.v[j][w][0] = lo.x; p.v[j][w][1] = lo.y; p.v[j][w][2] = lo.z; p.v[j][w][3] = lo.w;
+        p.v[j][w][4] = hi.x; p.v[j][w][5] = hi.y; p.v[j][w][6] = hi.z; p.v[j][w][7] = hi.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p.v[j][w][e] = q[e];
+      }
+    }
   }
 }
 
-// Branch-free up to the stores (both reductions always run, absent vectors
-// are masked), so that the compiler keeps the loads where they were issued.
-template <int HELD>
-__device__ __forceinline__ void group_prologue(const GemvGroupArgs &a, const PrologueLoads<HELD> &p,
-                                               float *xs, double *red) {
-  constexpr int kHeld = HELD;
+// The two block sums use their own LDS slots (`red`, 2 x 4 doubles), so
+// neither needs a barrier after its reads; ends with the barrier after the
+// digit stores.
+template <int PG>
+__device__ __forceinline__ void group_prologue(const GemvGroupArgs &a, const PrologueLoads<PG> &p,
+                                               uint4_t *dig, int *down, double *red) {
   const int n = a.K;
+  const int groups = n >> 3;
+  const int units = n >> 5;
   const bool lift = a.lift != nullptr;
   const bool normed = a.norm_gain != nullptr;
-  float sv[kHeld], lv[kHeld], gv[kHeld], nv[kHeld];
+  float sv[PG][8], lv[PG][8], gv[PG][8], nv[PG][8];
 #pragma unroll
-  for (int k = 0; k < kHeld; ++k) {
-    const bool in = (int)threadIdx.x + 256 * k < n;
-    sv[k] = in ? p.sv[k] : 0.0f;
-    lv[k] = in && lift ? p.lv[k] : 0.0f;
-    gv[k] = in && lift ? p.gv[k] : 0.0f;
-    nv[k] = in && normed ? p.nv[k] : 0.0f;
+  for (int j = 0; j < PG; ++j) {
+    const bool in = (int)threadIdx.x + 256 * j < groups;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sv[j][e] = in ? p.v[j][0][e] : 0.0f;
+      lv[j][e] = in && lift ? p.v[j][1][e] : 0.0f;
+      gv[j][e] = in && lift ? p.v[j][2][e] : 0.0f;
+      nv[j][e] = in && normed ? p.v[j][3][e] : 0.0f;
+    }
   }
   double acc = 0.0;
 #pragma unroll
-  for (int k = 0; k < kHeld; ++k) acc += (double)lv[k] * (double)lv[k];
-  const float shrink = rms_shrink(block_sum_f64(acc, red), n, a.eps);
+  for (int j = 0; j < PG; ++j)
 #pragma unroll
-  for (int k = 0; k < kHeld; ++k) {
-    float sum = sv[k] + lv[k] * shrink * gv[k];
-    if (a.apply_scale) sum *= a.scale;
-    sv[k] = lift ? sum : sv[k];
-  }
+    for (int e = 0; e < 8; ++e) acc += (double)lv[j][e] * (double)lv[j][e];
+  const float shrink = rms_shrink(block_sum_f64_once(acc, red), n, a.eps);
+#pragma unroll
+  for (int j = 0; j < PG; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float sum = sv[j][e] + lv[j][e] * shrink * gv[j][e];
+      if (a.apply_scale) sum *= a.scale;
+      sv[j][e] = lift ? sum : sv[j][e];
+    }
   if (lift && blockIdx.x == 0) {
 #pragma unroll
-    for (int k = 0; k < kHeld; ++k) {
-      const int i = threadIdx.x + 256 * k;
-      if (i < n) a.state_out[i] = sv[k];
+    for (int j = 0; j < PG; ++j) {
+      const int g = threadIdx.x + 256 * j;
+      if (g < groups) {
+        float *q = a.state_out + 8 * g;
+        if (a.pro_vec) {
+          *reinterpret_cast<float4_t *>(q) = float4_t{sv[j][0], sv[j][1], sv[j][2], sv[j][3]};
+          *reinterpret_cast<float4_t *>(q + 4) = float4_t{sv[j][4], sv[j][5], sv[j][6], sv[j][7]};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) q[e] = sv[j][e];
+        }
+      }
     }
   }
   double acc2 = 0.0;
 #pragma unroll
-  for (int k = 0; k < kHeld; ++k) acc2 += (double)sv[k] * (double)sv[k];
-  const float shrink2 = rms_shrink(block_sum_f64(acc2, red), n, a.eps);
+  for (int j = 0; j < PG; ++j)
 #pragma unroll
-  for (int k = 0; k < kHeld; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    if (i < n) xs[i] = normed ? sv[k] * shrink2 * nv[k] : sv[k];
+    for (int e = 0; e < 8; ++e) acc2 += (double)sv[j][e] * (double)sv[j][e];
+  const float shrink2 = rms_shrink(block_sum_f64_once(acc2, red + 4), n, a.eps);
+#pragma unroll
+  for (int j = 0; j < PG; ++j) {
+    const int g = threadIdx.x + 256 * j;
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = normed ? sv[j][e] * shrink2 * nv[j][e] : sv[j][e];
+    // a unit's four groups are one quad, all in or all out (K % 32 == 0)
+    if (g < groups) digit_group_store<kDigits>(x, 0, g, units, dig, down);
   }
   __syncthreads();
 }
 
-// PRO: 0, or the elements a thread holds in the prologue (K <= 256 PRO).
+// PRO: 0, or the eight-element groups a thread holds in the prologue
+// (K <= 2048 PRO).
 // GPT (PRO 0): the eight-element groups of x a thread stages, K <= 2048 GPT.
 // TPW: the four-row tiles a wave walks (KS 1 only): one workgroup then serves
 // 16 TPW rows, so TPW times fewer workgroups repeat the prologue and the
@@ -1342,8 +1383,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
   constexpr int kTilesPerBlock = 4 / KS;
   constexpr int kItems = GPT;
   __shared__ float red[4][R];
-  __shared__ double pro_red[16];
-  __shared__ __attribute__((aligned(16))) float xs[PRO ? 256 * PRO : 4];
+  __shared__ double pro_red[8];
   // the digit form of x, sized at launch (gemv_dot_lds_bytes(1, K / 32)):
   // the LDS a workgroup holds bounds how many share a CU
   extern __shared__ uint4_t lds_grp[];
@@ -1423,8 +1463,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
           reinterpret_cast<const uint4_t *>(a.codes[p] + (size_t)prow[i][r] * (size_t)a.row_stride[p]) + u);
     }
   if (PRO) {
-    group_prologue<PRO ? PRO : 1>(a, pl, xs, pro_red);
-    digit_store_lds<kDigits>(xs, a.K, dig, down);
+    group_prologue<PRO ? PRO : 1>(a, pl, dig, down, pro_red);
   } else {
     digit_store<1, kItems, kDigits>(held, a.K, dig, down);
   }
@@ -2172,6 +2211,7 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
   a.apply_scale = pro ? pro->apply_scale : 0;
   a.norm_gain = pro ? pro->norm_gain : nullptr;
   a.eps = pro ? pro->eps : 0.0f;
+  a.pro_vec = 0;
   if ((mode == GEMV_GELU_PAIR && (segments != 2 || rows[0] != rows[1])) ||
       (mode == GEMV_GELU_MUL && (segments != 1 || !mul)))
     return hipErrorInvalidValue;
@@ -2206,6 +2246,7 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
                               (uintptr_t)(pro->lift_gain ? pro->lift_gain : pro->state_in) |
                               (uintptr_t)(pro->norm_gain ? pro->norm_gain : pro->state_in) |
                               (uintptr_t)(pro->state_out ? pro->state_out : pro->state_in)) & 15u) == 0;
+  a.pro_vec = vec16 ? 1 : 0;
   if (vec16 && units <= kWave && a.tiles <= kGroupWaveTiles) {
     a.ksplit = 1;
     if (mode == GEMV_SEGMENTS)
@@ -2243,21 +2284,19 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
     else if (gpt == 2) IGL_GROUP_KS(M_, P_, 2);                   \
     else IGL_GROUP_KS(M_, P_, 4);                                 \
   } while (0)
-  // registers the prologue holds: the fewest of 6, 8, 16 a thread that cover K
-  const int held = !pro ? 0 : K <= 6 * 256 ? 6 : K <= 8 * 256 ? 8 : 16;
-  switch (mode * 4 + (held == 0 ? 0 : held == 6 ? 1 : held == 8 ? 2 : 3)) {
+  // groups of eight the prologue holds a thread: 1 up to K 2048, 2 up to 4096
+  const int held = !pro ? 0 : K <= 2048 ? 1 : K <= 4096 ? 2 : -1;
+  if (held < 0) return hipErrorInvalidValue;
+  switch (mode * 3 + held) {
     case 0: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 0); break;
-    case 1: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 6); break;
-    case 2: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 8); break;
-    case 3: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 16); break;
-    case 4: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 0); break;
-    case 5: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 6); break;
-    case 6: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 8); break;
-    case 7: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 16); break;
-    case 8: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 0); break;
-    case 9: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 6); break;
-    case 10: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 8); break;
-    case 11: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 16); break;
+    case 1: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 1); break;
+    case 2: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 2); break;
+    case 3: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 0); break;
+    case 4: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 1); break;
+    case 5: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 2); break;
+    case 6: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 0); break;
+    case 7: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 1); break;
+    case 8: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 2); break;
     default: return hipErrorInvalidValue;
   }
 #undef IGL_GROUP_LAUNCH
