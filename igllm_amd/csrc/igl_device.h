@@ -58,13 +58,6 @@ __device__ __forceinline__ double wave_sum_f64_to_last(double v) {
   return v;
 }
 
-__device__ __forceinline__ double lane_read_f64(double v, int lane) {
-  const uint64_t bits = __builtin_bit_cast(uint64_t, v);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)bits, lane);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(bits >> 32), lane);
-  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
-
 // Sum of one double per thread over a workgroup of WAVES waves, the same
 // total in every thread: DPP within each wave, then the wave sums in wave
 // order.  `red` holds one double a wave; the trailing barrier lets the caller

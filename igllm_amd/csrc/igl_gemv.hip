@@ -1326,7 +1326,8 @@ __device__ __forceinline__ void group_prologue(const GemvGroupArgs &a, const Pro
   for (int j = 0; j < PG; ++j)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc += (double)lv[j][e] * (double)lv[j][e];
-  const float shrink = rms_shrink(block_sum_f64_once(acc, red), n, a.eps);
+  // (a uniform branch: without lift or norm_gain its sum is skipped)
+  const float shrink = lift ? rms_shrink(block_sum_f64_once(acc, red), n, a.eps) : 0.0f;
 #pragma unroll
   for (int j = 0; j < PG; ++j)
 #pragma unroll
@@ -1356,7 +1357,7 @@ __device__ __forceinline__ void group_prologue(const GemvGroupArgs &a, const Pro
   for (int j = 0; j < PG; ++j)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc2 += (double)sv[j][e] * (double)sv[j][e];
-  const float shrink2 = rms_shrink(block_sum_f64_once(acc2, red + 4), n, a.eps);
+  const float shrink2 = normed ? rms_shrink(block_sum_f64_once(acc2, red + 4), n, a.eps) : 0.0f;
 #pragma unroll
   for (int j = 0; j < PG; ++j) {
     const int g = threadIdx.x + 256 * j;
@@ -1528,172 +1529,6 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
   }
 }
 
-// The same launch for few row tiles (the per-layer-input gate's 64): one
-// wave a tile, and lane u holds unit u (32 elements) of every K-vector, so the
-// residual update, both norms and the digit form of x are formed in the
-// wave's registers: the sums are butterflies across the wave, a lane digitizes
-// its own unit (the staged form's digits exactly), and nothing passes through
-// LDS or waits at a barrier.  Every wave repeats the prologue's reads, so the
-// launch takes this form only for a few tiles.  Rows, digits and the row sums
-// are formed as gemv_q4_group_kernel forms them; only the double sums of the
-// two norms add in another order.  K / 32 <= 64, K-vectors 16-byte aligned.
-// The wave's total in every lane: the DPP sum into the last lane, read back
-// as a uniform value (no LDS permutes).
-__device__ __forceinline__ double wave_total_f64(double v) {
-  return lane_read_f64(wave_sum_f64_to_last(v), 63);
-}
-
-template <int MODE>
-__global__ __launch_bounds__(64) void gemv_q4_group_wave_kernel(GemvGroupArgs a) {
-  constexpr int R = 4;
-  using Form = DigitForm<kDigits>;
-  const int lane = threadIdx.x;
-  const int tile = blockIdx.x;
-  const int units = a.K >> 5;
-  const bool has = lane < units;
-  const int u = min(lane, units - 1);
-
-  int plane[R], prow[R];
-  if (MODE == GEMV_GELU_PAIR) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      plane[r] = r >> 1;
-      prow[r] = min(2 * tile + (r & 1), a.rows[0] - 1);
-    }
-  } else {
-    int seg = 0, first = 0;
-    const int row0 = tile * R;
-    if (a.segments > 1 && row0 >= a.rows[0]) { seg = 1; first = a.rows[0]; }
-    if (a.segments > 2 && row0 >= a.rows[0] + a.rows[1]) { seg = 2; first = a.rows[0] + a.rows[1]; }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      plane[r] = seg;
-      prow[r] = min(row0 - first + r, a.rows[seg] - 1);
-    }
-  }
-
-  // Every load first: the lane's unit of the four K-vectors (an absent vector
-  // reads state_in in its place, masked below), then gains, then codes.
-  const bool lift = a.lift != nullptr;
-  const bool normed = a.norm_gain != nullptr;
-  const float4_t *sp = reinterpret_cast<const float4_t *>(a.state_in + 32 * u);
-  const float4_t *lp = reinterpret_cast<const float4_t *>((lift ? a.lift : a.state_in) + 32 * u);
-  const float4_t *gp = reinterpret_cast<const float4_t *>((lift ? a.lift_gain : a.state_in) + 32 * u);
-  const float4_t *np = reinterpret_cast<const float4_t *>((normed ? a.norm_gain : a.state_in) + 32 * u);
-  float4_t sv[8], lv[8], gv[8], nv[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    sv[i] = sp[i];
-    lv[i] = lp[i];
-    gv[i] = gp[i];
-    nv[i] = np[i];
-  }
-  float s[R];
-  uint4_t w[R];
-  // GEMV_GELU_MUL: the multipliers of the tile's rows, requested now rather
-  // than after the sums (a round trip at the end of the chain)
-  float mulv[R];
-  if (MODE == GEMV_GELU_MUL) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) mulv[r] = a.mul[min(tile * R + r, a.rows[0] - 1)];
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int pl = plane[r];
-    s[r] = a.gains[pl][(size_t)prow[r] * (size_t)a.gain_stride[pl] + ((unsigned)u >> a.group_shift)];
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int pl = plane[r];
-    w[r] = __builtin_nontemporal_load(
-        reinterpret_cast<const uint4_t *>(a.codes[pl] + (size_t)prow[r] * (size_t)a.row_stride[pl]) + u);
-  }
-
-  float x[32];
-  double acc = 0.0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float l = has && lift ? lv[i][c] : 0.0f;
-      acc += (double)l * (double)l;
-    }
-  const float shrink = rms_shrink(wave_total_f64(acc), a.K, a.eps);
-  double acc2 = 0.0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float sv0 = has ? sv[i][c] : 0.0f;
-      const float lv0 = has && lift ? lv[i][c] : 0.0f;
-      const float gv0 = has && lift ? gv[i][c] : 0.0f;
-      float sum = sv0 + lv0 * shrink * gv0;
-      if (a.apply_scale) sum *= a.scale;
-      x[4 * i + c] = lift ? sum : sv0;
-      acc2 += (double)x[4 * i + c] * (double)x[4 * i + c];
-    }
-  if (lift && blockIdx.x == 0 && has) {
-    float4_t *so = reinterpret_cast<float4_t *>(a.state_out + 32 * u);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) so[i] = float4_t{x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]};
-  }
-  const float shrink2 = rms_shrink(wave_total_f64(acc2), a.K, a.eps);
-  float peak = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float nv0 = has && normed ? nv[i][c] : 0.0f;
-      x[4 * i + c] = normed ? x[4 * i + c] * shrink2 * nv0 : x[4 * i + c];
-      peak = fmaxf(peak, fabsf(x[4 * i + c]));
-    }
-  // the unit's digits: dword q of digit j holds elements 8 q .. 8 q + 7
-  const int E = __builtin_amdgcn_frexp_expf(peak);
-  uint4_t dd[kDigits];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const float e8[8] = {x[8 * q], x[8 * q + 1], x[8 * q + 2], x[8 * q + 3],
-                         x[8 * q + 4], x[8 * q + 5], x[8 * q + 6], x[8 * q + 7]};
-    uint32_t d[kDigits];
-    digits_of_eight<kDigits>(e8, Form::kP - E, d);
-#pragma unroll
-    for (int j = 0; j < kDigits; ++j) dd[j][q] = d[j];
-  }
-  const int shift = E - Form::kP;
-
-  float out[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const uint4_t c = w[r] ^ 0x88888888u;
-    int t[kDigits];
-#pragma unroll
-    for (int j = 0; j < kDigits; ++j) t[j] = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int j = 0; j < kDigits; ++j) t[j] = __builtin_amdgcn_sdot8((int)c[q], (int)dd[j][q], t[j], false);
-    const float gain = has ? s[r] : 0.0f;
-    out[r] = wave_sum_to_last(gain * __builtin_amdgcn_ldexpf(digit_sum<kDigits>(t), shift));
-  }
-  if (lane != 63) return;
-  if (MODE == GEMV_GELU_PAIR) {
-    const int n0 = 2 * tile;
-    if (n0 < a.rows[0]) a.out[0][n0] = gelu_near(out[0]) * out[2];
-    if (n0 + 1 < a.rows[0]) a.out[0][n0 + 1] = gelu_near(out[1]) * out[3];
-  } else {
-    const int row0 = tile * R;
-    const int first = plane[0] == 0 ? 0 : plane[0] == 1 ? a.rows[0] : a.rows[0] + a.rows[1];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int n = row0 - first + r;
-      if (n >= a.rows[plane[0]]) break;
-      if (MODE == GEMV_GELU_MUL)
-        a.out[0][n] = gelu_near(out[r]) * mulv[r];
-      else
-        a.out[plane[0]][n] = out[r];
-    }
-  }
-}
 
 // ---- the small-lane form on the matrix cores (1..8 lanes) -----------------
 //
@@ -2179,11 +2014,6 @@ extern "C" int igl_gemv_chunk_cols(int lanes, int K, int lds_limit) {
   return per * 32;
 }
 
-// Tiles up to which a prologue launch takes one wave a tile: every wave reads
-// the four K-vectors, so past this the repeated reads outweigh the barriers
-// saved (measured, K 1536: 64 tiles 5.1 against 5.6 us, 100 even, 128 slower).
-constexpr int kGroupWaveTiles = 64;
-
 // One activation row against `segments` planes of the same width and group
 // size (see gemv_q4_group_kernel for the modes).  Every plane but the last of
 // a GEMV_SEGMENTS launch has a multiple of four rows; a GEMV_GELU_PAIR launch
@@ -2240,23 +2070,12 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
   while (ksplit < 4 && (units > ksplit * kWave || (a.tiles * ksplit < 2048 && units / (ksplit * 2) >= 32)))
     ksplit *= 2;
   a.ksplit = ksplit;
-  // A few tiles with the prologue, K-vectors 16-byte aligned: one wave a
-  // tile, formed in registers (gemv_q4_group_wave_kernel).
+  // The prologue loads its K-vectors 16 bytes at a time where all are aligned.
   const bool vec16 = pro && ((((uintptr_t)pro->state_in) | (uintptr_t)(pro->lift ? pro->lift : pro->state_in) |
                               (uintptr_t)(pro->lift_gain ? pro->lift_gain : pro->state_in) |
                               (uintptr_t)(pro->norm_gain ? pro->norm_gain : pro->state_in) |
                               (uintptr_t)(pro->state_out ? pro->state_out : pro->state_in)) & 15u) == 0;
   a.pro_vec = vec16 ? 1 : 0;
-  if (vec16 && units <= kWave && a.tiles <= kGroupWaveTiles) {
-    a.ksplit = 1;
-    if (mode == GEMV_SEGMENTS)
-      hipLaunchKernelGGL((gemv_q4_group_wave_kernel<GEMV_SEGMENTS>), dim3(a.tiles), dim3(kWave), 0, stream, a);
-    else if (mode == GEMV_GELU_PAIR)
-      hipLaunchKernelGGL((gemv_q4_group_wave_kernel<GEMV_GELU_PAIR>), dim3(a.tiles), dim3(kWave), 0, stream, a);
-    else
-      hipLaunchKernelGGL((gemv_q4_group_wave_kernel<GEMV_GELU_MUL>), dim3(a.tiles), dim3(kWave), 0, stream, a);
-    return hipGetLastError();
-  }
   // With the prologue, each workgroup repeats the residual update (four
   // K-vectors read, two block sums): past four workgroups a CU, two tiles a
   // wave halve that (measured: the 2 x 12288-row gate/up pair at K 1536, 11.5
