@@ -1647,18 +1647,21 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
       xb[k] = float4_t{src[4], src[5], src[6], src[7]};
     }
   }
-  // Gains: float4 runs of each row's chunk (at most 4 a thread: 64 rows x 16).
-  const int gain_runs = rows_b * (CU >> 2);
-  float4_t gv[4];
+  // Gains (VEC): each wave loads the slice it reads, its tile's 16 rows over
+  // its part's 4 NG units, as float4 runs (lane i: row i % 16, run i / 16),
+  // and transposes it into LDS itself after the barrier, so the barrier waits
+  // only for the B tiles and the products start while gains and codes are
+  // still arriving.
+  constexpr int kRunsPerLane = (NG + 3) / 4;
+  float4_t gv[kRunsPerLane];
   if (VEC) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = min(tid + 256 * k, gain_runs - 1);
-      const int rr = i / (CU >> 2);
-      const int c4 = i - rr * (CU >> 2);
-      const int row = min(row_b0 + rr, a.N - 1);
+    for (int k = 0; k < kRunsPerLane; ++k) {
+      const int i = lane + 64 * k;
+      const int c4 = min(i >> 4, NG - 1);
+      const int row = min(row_b0 + 16 * t + (i & 15), a.N - 1);
       gv[k] = *reinterpret_cast<const float4_t *>(a.gains + (size_t)row * (size_t)a.gain_stride +
-                                                 unit_c0 + 4 * c4);
+                                                 unit_c0 + u_w0 + 4 * c4);
     }
   }
 
@@ -1719,21 +1722,9 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
       bt[(u * 4 + g) * 16 + m + 8] = __builtin_bit_cast(uint4_t, lo);
     }
   }
-  // Gains stored [unit][row].
-  if (VEC) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = tid + 256 * k;
-      if (i < gain_runs) {
-        const int rr = i / (CU >> 2);
-        const int u = 4 * (i - rr * (CU >> 2));
-        gs[(u + 0) * pitch + rr] = gv[k].x;
-        gs[(u + 1) * pitch + rr] = gv[k].y;
-        gs[(u + 2) * pitch + rr] = gv[k].z;
-        gs[(u + 3) * pitch + rr] = gv[k].w;
-      }
-    }
-  } else {
+  // Gains stored [unit][row]: here only without VEC (every thread over the
+  // whole block, before the barrier).
+  if (!VEC) {
     for (int i = tid; i < CU * rows_b; i += 256) {
       const int rr = i / CU;
       const int u = i - rr * CU;
@@ -1744,6 +1735,22 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
   }
 
   __syncthreads();
+  // VEC: the wave's own gain slice, written and then read by this wave only
+  // (LDS operations of one wave complete in order).
+  if (VEC) {
+#pragma unroll
+    for (int k = 0; k < kRunsPerLane; ++k) {
+      const int i = lane + 64 * k;
+      if ((i >> 4) < NG) {
+        const int rr = 16 * t + (i & 15);
+        const int u = u_w0 + 4 * (i >> 4);
+        gs[(u + 0) * pitch + rr] = gv[k].x;
+        gs[(u + 1) * pitch + rr] = gv[k].y;
+        gs[(u + 2) * pitch + rr] = gv[k].z;
+        gs[(u + 3) * pitch + rr] = gv[k].w;
+      }
+    }
+  }
 
   const uint32_t exp16 = 0x4C004C00u;
   const _Float16 lift = (_Float16)(16.0f + a.code_bias);
