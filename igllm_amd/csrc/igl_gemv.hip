@@ -2076,6 +2076,10 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
   int ksplit = 1;
   while (ksplit < 4 && (units > ksplit * kWave || (a.tiles * ksplit < 2048 && units / (ksplit * 2) >= 32)))
     ksplit *= 2;
+  // Few tiles (the per-layer-input gate's 64): four waves on each tile, a
+  // workgroup a tile, so more workgroups share the launch's chains (lab, K
+  // 1536 with the prologue: 4.70 -> 4.24 us; at 640 tiles it is slower).
+  if (a.tiles * 4 <= 256 && units >= 16) ksplit = 4;
   a.ksplit = ksplit;
   // The prologue loads its K-vectors 16 bytes at a time where all are aligned.
   const bool vec16 = pro && ((((uintptr_t)pro->state_in) | (uintptr_t)(pro->lift ? pro->lift : pro->state_in) |
