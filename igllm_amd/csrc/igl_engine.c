@@ -698,6 +698,23 @@ static int project_level_epi(igl_engine *e, const igl_plane *p, const float *act
   return IGL_OKAY;
 }
 
+/* One lane through a calibrated plane whose x is formed by a residual update
+ * in the launch's prologue (igl_launch_gemv_level_pro): x is also written to
+ * x_out (NULL: not kept) for the planes that read it next. */
+static int level_pro_fits(const igl_engine *e, const igl_plane *p) {
+  return p->form == IGL_PLANE_CODE && p->enter_gain > 0.0f && p->device &&
+         igl_gemv_level_fits(p->bit_count, p->col_count) && p->col_count == e->hidden &&
+         p->col_count <= 2048;
+}
+
+static int project_level_pro(igl_engine *e, const igl_plane *p, const igl_gemv_prologue *pro, float *x_out,
+                             float *out, int epi, const float *epi_in) {
+  const igl_code_view view = igl_plane_view(p, dev_codes(e, p), dev_gains(e, p));
+  RUN(igl_launch_gemv_level_pro(&view, p->enter_gain, p->leave_gain, pro, x_out, out, p->row_count,
+                                p->col_count, epi, epi_in, e->stream));
+  return IGL_OKAY;
+}
+
 static int norm_rows(igl_engine *e, const float *in, const float *gain, int n, int lanes, int stride,
                      float *out) {
   return igl_norm_rms_dev(e->desk, in, gain, n, lanes, stride, e->eps, out);
@@ -821,6 +838,17 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
     e->pending = 0;
     OKAY(group_run(e, &gq, &L->q, IGL_GEMV_SEGMENTS, NULL, NULL, &pro));
     state_flip(e);
+  } else if (lanes == 1 && e->pending && level_pro_fits(e, &L->q)) {
+    /* a calibrated query plane takes the update in its prologue and leaves
+     * the normed input in scrap for the key and value planes */
+    igl_gemv_prologue pro = state_update(e, e->lift, e->pending_gain, e->pending_scale, L->enter_norm);
+    e->pending = 0;
+    OKAY(project_level_pro(e, &L->q, &pro, e->scrap, e->q, IGL_LEVEL_EPI_NONE, NULL));
+    state_flip(e);
+    if (!L->shared) {
+      OKAY(project(e, &L->k, e->scrap, H, lanes, e->k, e->kv_stride));
+      OKAY(project(e, &L->v, e->scrap, H, lanes, e->v, e->kv_stride));
+    }
   } else {
     OKAY(settle(e, lanes, L->enter_norm));
     if (fused) {
@@ -855,9 +883,16 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
     OKAY(group_run(e, &gf, &L->gate, IGL_GEMV_GELU_PAIR, NULL, NULL, &pro));
     state_flip(e);
   } else {
-    RUN(igl_launch_norm_add(e->state, H, e->lift, H, L->after_attn, H, lanes, e->eps, 1.0f, 0,
-                            L->before_ff, e->scrap, H, st));
-    OKAY(project(e, &L->gate, e->scrap, H, lanes, e->gate, e->inner_max));
+    if (lanes == 1 && level_pro_fits(e, &L->gate)) {
+      /* a calibrated gate plane takes the update in its prologue */
+      igl_gemv_prologue pro = state_update(e, e->lift, L->after_attn, 1.0f, L->before_ff);
+      OKAY(project_level_pro(e, &L->gate, &pro, e->scrap, e->gate, IGL_LEVEL_EPI_NONE, NULL));
+      state_flip(e);
+    } else {
+      RUN(igl_launch_norm_add(e->state, H, e->lift, H, L->after_attn, H, lanes, e->eps, 1.0f, 0,
+                              L->before_ff, e->scrap, H, st));
+      OKAY(project(e, &L->gate, e->scrap, H, lanes, e->gate, e->inner_max));
+    }
     if (level_epi_fits(&L->up, e->scrap, lanes) && L->up.row_count == L->inner) {
       /* gate = gelu(gate) * up proj, in the up projection's store */
       OKAY(project_level_epi(e, &L->up, e->scrap, e->gate, IGL_LEVEL_EPI_GELU_RISE, e->gate));
@@ -871,6 +906,12 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
   if (fused) {
     igl_gemv_prologue pro = state_update(e, e->lift, L->after_ff, 1.0f, NULL);
     OKAY(group_run(e, &gp, &L->ple_gate, IGL_GEMV_GELU_MUL, NULL, slice, &pro));
+    state_flip(e);
+  } else if (lanes == 1 && level_pro_fits(e, &L->ple_gate) && L->ple_gate.row_count == e->ple) {
+    /* gate = gelu(per-layer gate proj of the updated state) * slice, the
+     * update in the projection's prologue */
+    igl_gemv_prologue pro = state_update(e, e->lift, L->after_ff, 1.0f, NULL);
+    OKAY(project_level_pro(e, &L->ple_gate, &pro, NULL, e->gate, IGL_LEVEL_EPI_GELU_MUL, slice));
     state_flip(e);
   } else {
     RUN(igl_launch_norm_add(e->state, H, e->lift, H, L->after_ff, H, lanes, e->eps, 1.0f, 0, NULL,

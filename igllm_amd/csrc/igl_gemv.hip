@@ -835,6 +835,19 @@ struct GemvLevelArgs {
   int epi;                // IGL_LEVEL_EPI_*: the elementwise step that follows, fused
   const float *epi_in;    // its other operand, lane m at epi_in + m * epi_stride
   int epi_stride;
+  // One lane (PRO): x is not read from `act` but formed by the residual
+  // update of GemvGroupArgs; workgroup 0 writes s to `state_out` and, with
+  // `x_out`, x itself there for the launches that read the same x next.
+  const float *state_in;
+  float *state_out;
+  const float *lift;
+  const float *lift_gain;
+  float scale;
+  int apply_scale;
+  const float *norm_gain;
+  float eps;
+  int pro_vec;            // the K-vectors, state_out and x_out 16-byte aligned
+  float *x_out;
 };
 
 __host__ __device__ constexpr size_t gemv_level_lds_bytes(int M, int units) {
@@ -863,8 +876,108 @@ __device__ __forceinline__ float grid_value(float v, float step) {
   return level * step;
 }
 
-template <int BITS, int M, int R, int UPL, int GPT>
+// The prologue's loads of one thread: its eight-element groups of state_in,
+// lift, lift_gain and norm_gain (an absent vector reads state_in in its place).
+template <int PG>
+struct PrologueLoads {
+  float v[PG][4][8];
+};
+
+__device__ __forceinline__ void store_eight(float *dst, const float (&v)[8], int vec) {
+  if (vec) {
+    *reinterpret_cast<float4_t *>(dst) = float4_t{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<float4_t *>(dst + 4) = float4_t{v[4], v[5], v[6], v[7]};
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dst[e] = v[e];
+  }
+}
+
+// The residual update and norms of the level form's one-lane prologue, in two
+// steps (loads ahead of the weights, then the arithmetic).  Thread t holds the
+// eight-element groups of digit_item (t + 256 j, a group past the end standing
+// for the same quarter of the last unit), so level_store_form stores x as it
+// stores loaded activations; only groups in range count in the two sums.  The
+// element operations are norm_add_kernel's.
+template <int PG>
+__device__ __forceinline__ void level_prologue_loads(const GemvLevelArgs &a, PrologueLoads<PG> &p) {
+  const float *src[4] = {a.state_in, a.lift ? a.lift : a.state_in,
+                         a.lift ? a.lift_gain : a.state_in,
+                         a.norm_gain ? a.norm_gain : a.state_in};
+  const int groups = a.K >> 3;
+#pragma unroll
+  for (int j = 0; j < PG; ++j) {
+    const int g = digit_item(j, groups);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float *q = src[w] + 8 * g;
+      if (a.pro_vec) {
+        const float4_t lo = *reinterpret_cast<const float4_t *>(q);
+        const float4_t hi = *reinterpret_cast<const float4_t *>(q + 4);
+        p.v[j][w][0] = lo.x; p.v[j][w][1] = lo.y; p.v[j][w][2] = lo.z; p.v[j][w][3] = lo.w;
+        p.v[j][w][4] = hi.x; p.v[j][w][5] = hi.y; p.v[j][w][6] = hi.z; p.v[j][w][7] = hi.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p.v[j][w][e] = q[e];
+      }
+    }
+  }
+}
+
+template <int PG>
+__device__ __forceinline__ void level_prologue(const GemvLevelArgs &a, const PrologueLoads<PG> &p,
+                                               DigitLoads<PG> &held, double *red) {
+  const int n = a.K;
+  const int groups = n >> 3;
+  const bool lift = a.lift != nullptr;
+  const bool normed = a.norm_gain != nullptr;
+  double acc = 0.0;
+#pragma unroll
+  for (int j = 0; j < PG; ++j) {
+    const bool in = (int)threadIdx.x + 256 * j < groups;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float l = in && lift ? p.v[j][1][e] : 0.0f;
+      acc += (double)l * (double)l;
+    }
+  }
+  // (a uniform branch: without lift or norm_gain its sum is skipped)
+  const float shrink = lift ? rms_shrink(block_sum_f64_once(acc, red), n, a.eps) : 0.0f;
+  float sv[PG][8];
+  double acc2 = 0.0;
+#pragma unroll
+  for (int j = 0; j < PG; ++j) {
+    const bool in = (int)threadIdx.x + 256 * j < groups;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float sum = p.v[j][0][e] + (lift ? p.v[j][1][e] : 0.0f) * shrink * (lift ? p.v[j][2][e] : 0.0f);
+      if (a.apply_scale) sum *= a.scale;
+      sv[j][e] = lift ? sum : p.v[j][0][e];
+      const float c = in ? sv[j][e] : 0.0f;
+      acc2 += (double)c * (double)c;
+    }
+  }
+  const float shrink2 = normed ? rms_shrink(block_sum_f64_once(acc2, red + 4), n, a.eps) : 0.0f;
+#pragma unroll
+  for (int j = 0; j < PG; ++j) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) held.x[j][e] = normed ? sv[j][e] * shrink2 * p.v[j][3][e] : sv[j][e];
+  }
+  if (blockIdx.x == 0) {
+#pragma unroll
+    for (int j = 0; j < PG; ++j) {
+      const int g = threadIdx.x + 256 * j;
+      if (g >= groups) continue;
+      if (lift) store_eight(a.state_out + 8 * g, sv[j], a.pro_vec);
+      if (a.x_out) store_eight(a.x_out + 8 * g, held.x[j], a.pro_vec);
+    }
+  }
+}
+
+// PRO: one lane whose x is formed by the prologue above (M == 1).
+template <int BITS, int M, int R, int UPL, int GPT, bool PRO = false>
 __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs a) {
+  static_assert(!PRO || M == 1, "the prologue forms one lane");
   constexpr int FORM = CodeForm<BITS>::kDigits;
   constexpr int kSub = BITS == 2 ? 2 : 1;
   extern __shared__ uint4_t lds_lv[];
@@ -891,7 +1004,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
   int *nanu = corr + M * units;
 
   DigitLoads<GPT> held;
-  {
+  PrologueLoads<PRO ? GPT : 1> pl;
+  __shared__ double pro_red[PRO ? 8 : 1];
+  if (PRO) {
+    level_prologue_loads<PRO ? GPT : 1>(a, pl);
+  } else {
     const int last = a.lanes - 1;
     const int per_lane = a.K >> 3;
 #pragma unroll
@@ -933,6 +1050,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
       w[j][r] = __builtin_nontemporal_load(reinterpret_cast<const uint4_t *>(a.codes + (size_t)row * (size_t)a.row_stride) + sl);
     }
   }
+  if constexpr (PRO) level_prologue<GPT>(a, pl, held, pro_red);
   level_store_form<M, GPT, FORM>(held, a.K, a.step, a.code_bias, lv, corr, nanu);
 
   // one gain a row: exact integer parts (a slot past the part or the row adds
@@ -1268,11 +1386,6 @@ struct GemvGroupArgs {
 // K / 8 reread the last one, and the values are then masked.  The element
 // operations are norm_add_kernel's; only the double sums of the two norms add
 // in another order (a thread's eight elements, then the waves).
-template <int PG>
-struct PrologueLoads {
-  float v[PG][4][8];  // state_in, lift, lift_gain, norm_gain
-};
-
 template <int PG>
 __device__ __forceinline__ void prologue_loads(const GemvGroupArgs &a, PrologueLoads<PG> &p) {
   const float *src[4] = {a.state_in, a.lift ? a.lift : a.state_in,
@@ -2300,6 +2413,12 @@ template <int BITS, int M, int UPL, int GPT>
 static hipError_t gemv_level_launch4(const GemvLevelArgs &a, dim3 grid, size_t lds, hipStream_t stream) {
   // one lane: two-row tiles, twice the workgroups (the export-kinds decode
   // measured 2.52 against 2.68 ms a token with four)
+  if constexpr (M == 1) {
+    if (a.state_in) {
+      hipLaunchKernelGGL((gemv_level_kernel<BITS, 1, 2, UPL, GPT, true>), grid, dim3(kGemvThreads), lds, stream, a);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL((gemv_level_kernel<BITS, M, (M == 1 ? 2 : 4), UPL, GPT>), grid, dim3(kGemvThreads), lds, stream,
                      a);
   return hipGetLastError();
@@ -2341,6 +2460,11 @@ static hipError_t gemv_level_launch_bits(const GemvLevelArgs &a, int M, int upl,
 
 }  // namespace igl
 
+static hipError_t igl_level_launch(GemvLevelArgs a, const igl_code_view *v, float step, float leave,
+                                   const float *act, int act_stride, int lanes, float *out,
+                                   int out_stride, int N, int K, int epi, const float *epi_in,
+                                   int epi_stride, hipStream_t stream);
+
 // Whether igl_launch_gemv_level takes this plane's shape.
 extern "C" int igl_gemv_level_fits(int bit_count, int K) {
   return (bit_count == 2 || bit_count == 4 || bit_count == 8) && K >= 32 && K % 32 == 0 && K <= 16384 &&
@@ -2365,12 +2489,58 @@ extern "C" hipError_t igl_launch_gemv_level_epi(const igl_code_view *v, float st
                                                 const float *act, int act_stride, int lanes, float *out,
                                                 int out_stride, int N, int K, int epi, const float *epi_in,
                                                 int epi_stride, hipStream_t stream) {
-  const int bits = v->bit_count;
-  if (!(step > 0.0f) || !igl_gemv_level_fits(bits, K) || (((uintptr_t)act) & 15u) ||
-      (lanes > 1 && (act_stride & 3)) || lanes < 1 || N < 1 || epi < IGL_LEVEL_EPI_NONE ||
-      epi > IGL_LEVEL_EPI_GELU_MUL || (epi != IGL_LEVEL_EPI_NONE && !epi_in))
+  GemvLevelArgs a;
+  a.state_in = a.lift = a.lift_gain = a.norm_gain = nullptr;
+  a.state_out = a.x_out = nullptr;
+  a.scale = 1.0f;
+  a.apply_scale = 0;
+  a.eps = 0.0f;
+  a.pro_vec = 0;
+  return igl_level_launch(a, v, step, leave, act, act_stride, lanes, out, out_stride, N, K, epi, epi_in,
+                          epi_stride, stream);
+}
+
+// One lane with the residual update of igl_launch_gemv_group as the
+// prologue (`pro`: state_in, lift and its gain, scale, norm_gain, eps), x
+// written to `x_out` as well where it is not NULL (the launches that read the
+// same x next), K at most 2048.  y and the fused elementwise step as
+// igl_launch_gemv_level_epi.
+extern "C" hipError_t igl_launch_gemv_level_pro(const igl_code_view *v, float step, float leave,
+                                                const igl_gemv_prologue *pro, float *x_out, float *out,
+                                                int N, int K, int epi, const float *epi_in,
+                                                hipStream_t stream) {
+  if (!pro || !pro->state_in || K > 2048 || (pro->lift && (!pro->lift_gain || !pro->state_out)) ||
+      pro->state_out == pro->state_in)
     return hipErrorInvalidValue;
   GemvLevelArgs a;
+  a.state_in = pro->state_in;
+  a.state_out = pro->state_out;
+  a.lift = pro->lift;
+  a.lift_gain = pro->lift_gain;
+  a.scale = pro->scale;
+  a.apply_scale = pro->apply_scale;
+  a.norm_gain = pro->norm_gain;
+  a.eps = pro->eps;
+  a.x_out = x_out;
+  a.pro_vec = ((((uintptr_t)a.state_in) | (uintptr_t)(a.lift ? a.lift : a.state_in) |
+                (uintptr_t)(a.lift_gain ? a.lift_gain : a.state_in) |
+                (uintptr_t)(a.norm_gain ? a.norm_gain : a.state_in) |
+                (uintptr_t)(a.state_out ? a.state_out : a.state_in) |
+                (uintptr_t)(x_out ? x_out : a.state_in)) & 15u) == 0;
+  return igl_level_launch(a, v, step, leave, nullptr, K, 1, out, N, N, K, epi, epi_in, 0, stream);
+}
+
+static hipError_t igl_level_launch(GemvLevelArgs a, const igl_code_view *v, float step, float leave,
+                                   const float *act, int act_stride, int lanes, float *out,
+                                   int out_stride, int N, int K, int epi, const float *epi_in,
+                                   int epi_stride, hipStream_t stream) {
+  const int bits = v->bit_count;
+  // activations come from `act` (16-byte aligned) unless the prologue forms them
+  if (!(step > 0.0f) || !igl_gemv_level_fits(bits, K) ||
+      (!a.state_in && (!act || (((uintptr_t)act) & 15u))) || (lanes > 1 && (act_stride & 3)) ||
+      lanes < 1 || N < 1 || epi < IGL_LEVEL_EPI_NONE || epi > IGL_LEVEL_EPI_GELU_MUL ||
+      (epi != IGL_LEVEL_EPI_NONE && !epi_in))
+    return hipErrorInvalidValue;
   a.epi = epi;
   a.epi_stride = epi_stride;
   a.codes = v->codes;
@@ -2402,7 +2572,7 @@ extern "C" hipError_t igl_launch_gemv_level_epi(const igl_code_view *v, float st
       ksplit *= 2;
     const int items = (M * (K >> 3) + kGemvThreads - 1) / kGemvThreads;
     const int gpt = items <= 1 ? 1 : items <= 2 ? 2 : items <= 4 ? 4 : 8;
-    a.act = act + (size_t)done * (size_t)act_stride;
+    a.act = act ? act + (size_t)done * (size_t)act_stride : nullptr;
     a.act_stride = act_stride;
     a.lanes = l;
     a.out = out + (size_t)done * (size_t)out_stride;

@@ -93,6 +93,12 @@ typedef struct igl_gemv_prologue {
   const float *norm_gain;
   float eps;
 } igl_gemv_prologue;
+/* One lane of a calibrated plane (igl_launch_gemv_level_epi) with the residual
+ * update of igl_launch_gemv_group as its prologue; x also to x_out (NULL:
+ * not kept); K <= 2048. */
+hipError_t igl_launch_gemv_level_pro(const igl_code_view *v, float step, float leave,
+                                     const igl_gemv_prologue *pro, float *x_out, float *out, int N,
+                                     int K, int epi, const float *epi_in, hipStream_t stream);
 hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_t *const *codes,
                                  const long long *row_stride, const float *const *gains,
                                  const int *gain_stride, const int *rows, float *const *out,
