@@ -2410,10 +2410,15 @@ extern "C" hipError_t igl_launch_gemv_codes(const igl_code_view *v, const float 
 namespace igl {
 
 template <int BITS, int M, int UPL, int GPT>
-static hipError_t gemv_level_launch4(const GemvLevelArgs &a, dim3 grid, size_t lds, hipStream_t stream) {
+static hipError_t gemv_level_launch4(const GemvLevelArgs &a, dim3 grid, size_t lds, hipStream_t stream,
+                                     int rows) {
   // one lane: two-row tiles, twice the workgroups (the export-kinds decode
-  // measured 2.52 against 2.68 ms a token with four)
+  // measured 2.52 against 2.68 ms a token with four); six on wide rows
   if constexpr (M == 1) {
+    if (rows == 6) {
+      hipLaunchKernelGGL((gemv_level_kernel<BITS, 1, 6, UPL, GPT>), grid, dim3(kGemvThreads), lds, stream, a);
+      return hipGetLastError();
+    }
     if (a.state_in) {
       hipLaunchKernelGGL((gemv_level_kernel<BITS, 1, 2, UPL, GPT, true>), grid, dim3(kGemvThreads), lds, stream, a);
       return hipGetLastError();
@@ -2426,23 +2431,23 @@ static hipError_t gemv_level_launch4(const GemvLevelArgs &a, dim3 grid, size_t l
 
 template <int BITS, int M>
 static hipError_t gemv_level_launch_m(const GemvLevelArgs &a, int upl, int gpt, dim3 grid, size_t lds,
-                                      hipStream_t stream) {
+                                      hipStream_t stream, int rows) {
   // more than 256 slots a row: one lane of 4-bit codes, one or two of 8-bit codes
   constexpr bool kTwoSlots = (M == 1 && BITS >= 4) || (M == 2 && BITS == 8);
   if (upl == 1) {
     switch (gpt) {
-      case 1: return gemv_level_launch4<BITS, M, 1, 1>(a, grid, lds, stream);
-      case 2: return gemv_level_launch4<BITS, M, 1, 2>(a, grid, lds, stream);
-      case 4: return gemv_level_launch4<BITS, M, 1, 4>(a, grid, lds, stream);
-      default: return gemv_level_launch4<BITS, M, 1, 8>(a, grid, lds, stream);
+      case 1: return gemv_level_launch4<BITS, M, 1, 1>(a, grid, lds, stream, rows);
+      case 2: return gemv_level_launch4<BITS, M, 1, 2>(a, grid, lds, stream, rows);
+      case 4: return gemv_level_launch4<BITS, M, 1, 4>(a, grid, lds, stream, rows);
+      default: return gemv_level_launch4<BITS, M, 1, 8>(a, grid, lds, stream, rows);
     }
   }
   if constexpr (kTwoSlots) {
     switch (gpt) {
-      case 1: return gemv_level_launch4<BITS, M, 2, 1>(a, grid, lds, stream);
-      case 2: return gemv_level_launch4<BITS, M, 2, 2>(a, grid, lds, stream);
-      case 4: return gemv_level_launch4<BITS, M, 2, 4>(a, grid, lds, stream);
-      default: return gemv_level_launch4<BITS, M, 2, 8>(a, grid, lds, stream);
+      case 1: return gemv_level_launch4<BITS, M, 2, 1>(a, grid, lds, stream, rows);
+      case 2: return gemv_level_launch4<BITS, M, 2, 2>(a, grid, lds, stream, rows);
+      case 4: return gemv_level_launch4<BITS, M, 2, 4>(a, grid, lds, stream, rows);
+      default: return gemv_level_launch4<BITS, M, 2, 8>(a, grid, lds, stream, rows);
     }
   }
   return hipErrorInvalidValue;
@@ -2450,11 +2455,11 @@ static hipError_t gemv_level_launch_m(const GemvLevelArgs &a, int upl, int gpt, 
 
 template <int BITS>
 static hipError_t gemv_level_launch_bits(const GemvLevelArgs &a, int M, int upl, int gpt, dim3 grid,
-                                         size_t lds, hipStream_t stream) {
+                                         size_t lds, hipStream_t stream, int rows) {
   switch (M) {
-    case 1: return gemv_level_launch_m<BITS, 1>(a, upl, gpt, grid, lds, stream);
-    case 2: return gemv_level_launch_m<BITS, 2>(a, upl, gpt, grid, lds, stream);
-    default: return gemv_level_launch_m<BITS, 4>(a, upl, gpt, grid, lds, stream);
+    case 1: return gemv_level_launch_m<BITS, 1>(a, upl, gpt, grid, lds, stream, rows);
+    case 2: return gemv_level_launch_m<BITS, 2>(a, upl, gpt, grid, lds, stream, rows);
+    default: return gemv_level_launch_m<BITS, 4>(a, upl, gpt, grid, lds, stream, rows);
   }
 }
 
@@ -2564,12 +2569,20 @@ static hipError_t igl_level_launch(GemvLevelArgs a, const igl_code_view *v, floa
     const int slots = (K * bits + 127) / 128;
     const int upl = slots > 4 * kWave ? 2 : 1;
     const int subs_log = upl == 1 && slots <= 16 ? 2 : upl == 1 && slots <= 32 ? 1 : 0;
-    const int rows_t = M == 1 ? 2 : 4;  // rows a sub-wave (the kernel's R)
-    const int tiles = (N + (rows_t << subs_log) - 1) / (rows_t << subs_log);
+    int rows_t = M == 1 ? 2 : 4;  // rows a sub-wave (the kernel's R)
+    int tiles = (N + (rows_t << subs_log) - 1) / (rows_t << subs_log);
     int ksplit = 1;
     while (subs_log == 0 && ksplit < 4 &&
            (slots > ksplit * kWave * upl || (tiles * ksplit < 2048 && slots / (ksplit * 2) >= 32 * upl)))
       ksplit *= 2;
+    // One lane on wide rows (four waves a tile): six-row tiles where two
+    // give a CU several workgroups that each stage all of x and six give every
+    // CU at most one (lab, 1536 rows: 2-bit K 12288 14.13 -> 10.34 us, 4-bit
+    // K 6144 8.08 -> 7.10 us; the same sums).
+    if (M == 1 && subs_log == 0 && ksplit == 4 && !a.state_in && (N + 1) / 2 > 256 && (N + 5) / 6 <= 256) {
+      rows_t = 6;
+      tiles = (N + 5) / 6;
+    }
     const int items = (M * (K >> 3) + kGemvThreads - 1) / kGemvThreads;
     const int gpt = items <= 1 ? 1 : items <= 2 ? 2 : items <= 4 ? 4 : 8;
     a.act = act ? act + (size_t)done * (size_t)act_stride : nullptr;
@@ -2583,9 +2596,9 @@ static hipError_t igl_level_launch(GemvLevelArgs a, const igl_code_view *v, floa
     const int per_block = 4 / ksplit;
     const dim3 grid((tiles + per_block - 1) / per_block);
     const size_t lds = gemv_level_lds_bytes(M, K / 32);
-    hipError_t e = bits == 2   ? gemv_level_launch_bits<2>(a, M, upl, gpt, grid, lds, stream)
-                   : bits == 4 ? gemv_level_launch_bits<4>(a, M, upl, gpt, grid, lds, stream)
-                               : gemv_level_launch_bits<8>(a, M, upl, gpt, grid, lds, stream);
+    hipError_t e = bits == 2   ? gemv_level_launch_bits<2>(a, M, upl, gpt, grid, lds, stream, rows_t)
+                   : bits == 4 ? gemv_level_launch_bits<4>(a, M, upl, gpt, grid, lds, stream, rows_t)
+                               : gemv_level_launch_bits<8>(a, M, upl, gpt, grid, lds, stream, rows_t);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
