@@ -523,8 +523,29 @@ __device__ __forceinline__ void digit_store_lds(const float *xs, int K, uint4_t 
 // 0..15 / 16..31); corr[m units + u] = the bias correction of the unit
 // (4-bit: 8 sum lo; 2-bit: code_bias sum L; 8-bit: 0); nanu[m units + u] != 0
 // where the unit holds a NaN (its level is no level; the lane's outputs are NaN).
+// x / step rounded to nearest, for rounding to a level: with inv = 1 / step
+// correctly rounded, q0 = x inv is within an ulp of the quotient, the residual
+// x - q0 step is exact (one fma), and q0 + residual inv rounds to the
+// correctly rounded quotient (Markstein's theorem on division by a correctly
+// rounded reciprocal and an fma correction).  Quotients of 256 and up (and
+// their overflow) skip the correction: the level clamps at -128 / 127 either
+// way.  A host check of 4e8 random and near-half-integer quotients found no
+// level that differs from rint(x / step).  The theorem needs inv normal and
+// the residual exact (no underflow): step in [2^-96, 2^96] gives both for
+// every quotient under 256, and level_recip returns 0 outside it, where the
+// caller divides instead.
+__device__ __forceinline__ float quot_near(float x, float step, float inv) {
+  const float q0 = x * inv;
+  const float r = __builtin_fmaf(-q0, step, x);
+  return __builtin_fabsf(q0) < 256.0f ? __builtin_fmaf(r, inv, q0) : q0;
+}
+
+__device__ __forceinline__ float level_recip(float step) {
+  return step >= 0x1p-96f && step <= 0x1p96f ? 1.0f / step : 0.0f;
+}
+
 template <int FORM>
-__device__ __forceinline__ void level_group_store(const float (&xin)[8], float step, int code_bias, int m,
+__device__ __forceinline__ void level_group_store(const float (&xin)[8], float step, float inv, int code_bias, int m,
                                                   int gg, int units, uint4_t *lv, int *corr, int *nanu) {
   const int u = gg >> 2, dw = gg & 3;
   float x[8];
@@ -542,11 +563,19 @@ __device__ __forceinline__ void level_group_store(const float (&xin)[8], float s
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = xin[e];
   }
+  float qt[8];
+  if (inv != 0.0f) {  // uniform: one step for the launch
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qt[e] = quot_near(x[e], step, inv);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qt[e] = x[e] / step;
+  }
   int L[8];
   int bad = 0;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    float q = __builtin_rintf(x[e] / step);
+    float q = __builtin_rintf(qt[e]);
     bad |= q != q;
     q = q < -128.0f ? -128.0f : q;
     q = q > 127.0f ? 127.0f : q;
@@ -607,11 +636,12 @@ __device__ __forceinline__ void level_store_form(const DigitLoads<GPT> &h, int K
                                                  uint4_t *lv, int *corr, int *nanu) {
   const int units = K >> 5;
   const int per_lane = K >> 3;
+  const float inv = level_recip(step);  // once a thread
 #pragma unroll
   for (int i = 0; i < GPT; ++i) {
     const int g = digit_item(i, M * per_lane);
     const int m = M == 1 ? 0 : g / per_lane;
-    level_group_store<FORM>(h.x[i], step, code_bias, m, g - m * per_lane, units, lv, corr, nanu);
+    level_group_store<FORM>(h.x[i], step, inv, code_bias, m, g - m * per_lane, units, lv, corr, nanu);
   }
   __syncthreads();
 }

@@ -2575,11 +2575,13 @@ static hipError_t igl_level_launch(GemvLevelArgs a, const igl_code_view *v, floa
     while (subs_log == 0 && ksplit < 4 &&
            (slots > ksplit * kWave * upl || (tiles * ksplit < 2048 && slots / (ksplit * 2) >= 32 * upl)))
       ksplit *= 2;
-    // One lane on wide rows (four waves a tile): six-row tiles where two
-    // give a CU several workgroups that each stage all of x and six give every
-    // CU at most one (lab, 1536 rows: 2-bit K 12288 14.13 -> 10.34 us, 4-bit
-    // K 6144 8.08 -> 7.10 us; the same sums).
-    if (M == 1 && subs_log == 0 && ksplit == 4 && !a.state_in && (N + 1) / 2 > 256 && (N + 5) / 6 <= 256) {
+    // One lane on wide rows (four waves a tile, 192 slots and up): six-row
+    // tiles where two give a CU several workgroups that each stage all of x
+    // and six give every CU at most one (lab, 1536 rows: 2-bit K 12288 14.13
+    // -> 10.34 us, 4-bit K 6144 8.08 -> 7.10 us; the same sums; at 128 slots,
+    // 4-bit K 4096, the decode step measured it slower, 6.2 -> 7.6 us).
+    if (M == 1 && subs_log == 0 && ksplit == 4 && slots >= 192 && !a.state_in && (N + 1) / 2 > 256 &&
+        (N + 5) / 6 <= 256) {
       rows_t = 6;
       tiles = (N + 5) / 6;
     }
