@@ -81,15 +81,11 @@ struct LevelArgs {
   int k_steps;            // steps of one slice (blockIdx.z)
 };
 
-// fl(y / leave) from leave_rcp = fl(1 / leave): q = fl(y * leave_rcp) is
-// within an ulp of the quotient, the fma gives the remainder y - q leave
-// exactly, and one more fma rounds q to the correctly rounded quotient
-// (Markstein's correction step).  Finite y only; others divide.
+// y / leave as rint needs it: quot_near (the correctly rounded quotient below
+// 256, the rest clamps alike, NaN stays NaN) from leave_rcp =
+// level_recip(leave); a leave outside that range (leave_rcp 0) divides.
 __device__ __forceinline__ float div_leave(float y, float leave, float leave_rcp) {
-  if (!(__builtin_fabsf(y) <= 3.0e38f)) return y / leave;
-  const float q = y * leave_rcp;
-  const float e = __builtin_fmaf(-q, leave, y);
-  return __builtin_fmaf(e, leave_rcp, q);
+  return leave_rcp != 0.0f ? quot_near(y, leave, leave_rcp) : y / leave;
 }
 
 // The leave grid (quant_step) on y = fl(gain * step) * part.
@@ -245,7 +241,7 @@ __global__ __launch_bounds__(kLvThreads) void gemm_level_kernel(LevelArgs g) {
   // fl(gain * step) of the lane's sixteen columns, loaded before any store
   // (the outputs could alias the gains as far as the compiler knows)
   float gs[4][4];
-  const float leave_rcp = g.leave > 0.0f ? 1.0f / g.leave : 0.0f;
+  const float leave_rcp = g.leave > 0.0f ? level_recip(g.leave) : 0.0f;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -295,7 +291,7 @@ __global__ void level_close_kernel(const int32_t *part, int slices, int M, int N
   if (n >= N) return;
   int32_t t = 0;
   for (int z = 0; z < slices; ++z) t += part[((size_t)z * M + m) * N + n];
-  const float leave_rcp = leave > 0.0f ? 1.0f / leave : 0.0f;
+  const float leave_rcp = leave > 0.0f ? level_recip(leave) : 0.0f;
   out[(size_t)m * out_stride + n] =
       nan_rows[m] ? __builtin_nanf("") : level_grid(gains[n] * step, t >> shift, leave, leave_rcp);
 }

@@ -169,6 +169,55 @@ def test_plane_lift_level_bitexact(backend, N, K, bits, flip, lanes):
     backend.detach(cp)
 
 
+NEAR_TIE_STEPS = [2.5 / 127, 2.0 ** -96, 2.0 ** 90, 2.0 ** -100, 2.0 ** 100]
+
+
+@pytest.mark.parametrize("step_in", NEAR_TIE_STEPS)
+@pytest.mark.parametrize("bits,lanes", [(4, 1), (2, 3), (4, 64)])
+def test_plane_lift_level_near_ties(backend, step_in, bits, lanes):
+    """Activations at and one ulp either side of every half-integer quotient of
+    the clamp range, with steps inside [2^-96, 2^96] (the reciprocal and fma
+    correction) and outside it (the kernels divide), and a leave grid scaled to
+    the products: the levels, the product and the leave grid equal the
+    oracle's level path to the bit (the fused GEMV below 64 lanes, the int8
+    MFMA GEMM and its close from 64)."""
+    from igllm_amd.backend import make_plane
+    from test_oracle import quant_step_closed
+
+    N, K = 512, 1536
+    print("case near-ties step=%g bits=%d lanes=%d" % (step_in, bits, lanes), flush=True)
+    r = np.random.default_rng(bits * 100 + lanes)
+    step = float(np.float32(step_in))
+    stride = ((K * bits + 7) // 8 + 15) // 16 * 16
+    codes = r.integers(0, 256, size=(N, stride), dtype=np.uint8)
+    gains = np.abs(r.normal(0, 0.02, size=(N, 1))).astype(np.float32)
+    k = r.integers(-140, 140, size=(lanes, K))
+    act = ((k + 0.5) * step).astype(np.float32)
+    nudge = r.integers(-1, 2, size=(lanes, K))
+    act = np.where(nudge > 0, np.nextafter(act, np.float32(np.inf)), act)
+    act = np.where(nudge < 0, np.nextafter(act, np.float32(-np.inf)), act).astype(np.float32)
+    act[:, ::7] = (r.normal(size=act[:, ::7].shape) * 60.0 * step).astype(np.float32)
+    cp = backend.attach(make_plane(codes, gains, K, group_size=K, bits=bits))
+    cp.plane.enter_gain = step
+    kw = dict(bits=bits, code_bias=1 << (bits - 1), code_flip=0)
+    want = ol.oracle_mat_mat_level(codes, gains, act, K, K, step, **kw)
+    dev_act = backend.upload(act)
+    out = backend.alloc(lanes * N * 4)
+    backend.plane_lift_dev(cp, dev_act, K, lanes, out, N)
+    backend.sync()
+    got = out.get(np.float32, lanes * N).reshape(lanes, N)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    leave = float(np.float32(np.sqrt(np.mean(want.astype(np.float64) ** 2)) / 40.0))
+    cp.plane.leave_gain = leave
+    backend.plane_lift_dev(cp, dev_act, K, lanes, out, N)
+    backend.sync()
+    got = out.get(np.float32, lanes * N).reshape(lanes, N)
+    assert np.array_equal(got.view(np.uint32), np.stack([quant_step_closed(y, leave) for y in want]).view(np.uint32))
+    dev_act.free()
+    out.free()
+    backend.detach(cp)
+
+
 def test_plane_lift_level_nan_lane(backend):
     """A NaN activation puts its lane's outputs at NaN and leaves the others on
     the grid.  (The reference sends the whole 16-lane chunk to the float path

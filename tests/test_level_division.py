@@ -1,10 +1,14 @@
-"""The leave grid's division (quant_step, app_core.c:1930-1940, as
-rint(y / leave)) is computed on the GPU as q = fl(y r), r = fl(1 / leave), then
-fl(q + fl(y - q leave) r) with two fused multiply-adds (div_leave in
-igl_gemm_level.hip).  This pins that sequence to the correctly rounded binary32
-quotient in exact rational arithmetic: near-ties at every half-integer quotient
-of the clamp range, random quotients, and leave values including all-ones
-mantissas, powers of two and the grids the tests use."""
+"""The grid divisions (quant_step, app_core.c:1930-1940, as rint(y / leave)
+and rint(x / step)) are computed on the GPU as q = fl(y r), r = fl(1 / leave),
+then fl(q + fl(y - q leave) r) with two fused multiply-adds (quot_near in
+igl_device.h: the fused GEMV's activation levels, and div_leave in
+igl_gemm_level.hip: the leave grid), for steps in [2^-96, 2^96] (level_recip;
+outside it the kernels divide), quotients under 256 (at and above it fl(y r)
+is kept, and the level clamps alike).  This pins that sequence to the
+correctly rounded binary32 quotient in exact rational arithmetic: near-ties at
+every half-integer quotient of the clamp range, random quotients, and leave
+values including all-ones mantissas, powers of two, both ends of the range
+and the grids the tests use."""
 from fractions import Fraction
 
 import numpy as np
@@ -80,3 +84,64 @@ def test_corrected_division_is_correctly_rounded():
             assert device_div(yf, leave) == rn32(yf / leave), (float(y), lv)
             checked += 1
     assert checked > 20000
+
+
+def quot_near(x: Fraction, step: Fraction):
+    """quot_near of igl_device.h in exact arithmetic, each operation rounded
+    once; returns (value, corrected)."""
+    inv = rn32(1 / step)
+    q0 = rn32(x * inv)
+    if abs(q0) >= 256:
+        return q0, False
+    r = rn32(x - q0 * step)
+    return rn32(r * inv + q0), True
+
+
+def clamp_level(q: float) -> float:
+    return min(max(float(np.rint(q)), -128.0), 127.0)
+
+
+def test_quot_near_range_ends():
+    """Steps at both ends of [2^-96, 2^96] (powers of two and all-ones
+    mantissas) and the usual grids: below 256 the corrected quotient is the
+    correctly rounded one; at and above it the level clamps as the quotient's."""
+    ones = float(np.nextafter(np.float32(2.0), np.float32(0.0)))  # 2 - 2^-23
+    steps = [2.0 ** -96, ones * 2.0 ** -96, 2.0 ** 96, ones * 2.0 ** 95, 2.5 / 127, 0.02, 3.0]
+    rng = np.random.default_rng(3)
+    checked = 0
+    for st in steps:
+        step = f32(st)
+        xs = []
+        for k in list(range(-131, 131, 3)) + [-129, -128, 126, 127, 255, 256]:
+            t = np.float32((k + 0.5) * float(step))
+            xs += [t, np.nextafter(t, np.float32(np.inf)), np.nextafter(t, np.float32(-np.inf))]
+        xs += list((rng.normal(size=200) * 90.0 * float(step)).astype(np.float32))
+        xs += list((rng.normal(size=40) * 5000.0 * float(step)).astype(np.float32))
+        for x in xs:
+            xf = Fraction(float(x))
+            if xf == 0:
+                continue
+            got, corrected = quot_near(xf, step)
+            want = rn32(xf / step)
+            if corrected:
+                assert got == want, (float(x), st)
+            else:
+                assert clamp_level(float(got)) == clamp_level(float(want)), (float(x), st)
+            checked += 1
+    assert checked > 3000
+
+
+def test_quot_near_specials_clamp_alike():
+    """Overflowing and non-finite quotients in binary32: fl(x r) overflows to
+    infinity (kept, as |q0| >= 256), NaN stays NaN, zero stays zero."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        for x, st in [(3.0e38, 0.01), (-3.0e38, 0.01), (np.inf, 0.5), (-np.inf, 0.5), (np.nan, 0.5), (0.0, 2.0 ** -96)]:
+            x, st = np.float32(x), np.float32(st)
+            inv = np.float32(1.0) / st
+            q0 = x * inv
+            want = x / st
+            if np.isnan(want):
+                assert np.isnan(q0)
+            else:
+                assert not abs(q0) < 256 or q0 == want
+                assert clamp_level(q0) == clamp_level(want)
