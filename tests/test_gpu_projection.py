@@ -95,6 +95,30 @@ def test_gemv_edges(backend, N, K, lanes, group):
     backend.detach(cp)
 
 
+def test_gemv_chunked_repeat(backend):
+    """K-chunked matrix-core launches (partials summed in chunk order by a
+    second launch): launches of different lane counts and planes (full and
+    ragged row blocks) interleaved, each repeated: every repeat is
+    bit-identical to the first and within the bar of the oracle."""
+    cases = [(2048, 8192, 4), (2048, 8192, 8), (40, 8192, 5), (2000, 8192, 3), (33, 12288, 8)]
+    planes, firsts = [], []
+    for N, K, lanes in cases:
+        print_case(test="chunked_repeat", N=N, K=K, lanes=lanes)
+        codes, gains, act = synth_projection(N, K, lanes, seed=N + lanes)
+        cp = backend.attach(make_plane(codes, gains, K))
+        planes.append((cp, act))
+        got = run_gemv_dev(backend, cp, act, lanes)
+        want = ol.oracle_mat_mat(codes, gains, act, K, threads=8)
+        assert rel_err(got, want) <= 1e-3
+        firsts.append(got)
+    for turn in range(3):
+        for (cp, act), first in zip(planes, firsts):
+            got = run_gemv_dev(backend, cp, act, act.shape[0])
+            assert np.array_equal(got.view(np.uint32), first.view(np.uint32)), f"repeat {turn}"
+    for cp, _ in planes:
+        backend.detach(cp)
+
+
 @pytest.mark.parametrize("lanes", [1, 3])
 def test_gemv_unaligned_activations(backend, lanes):
     """An activation stride that is not a multiple of four floats takes the

@@ -20,29 +20,34 @@ def desk():
 
 
 def test_replay_equals_eager(desk):
-    print("case replay gemv 8192x2048 M=1, 2048x8192 M=1, 8192x2048 M=4", flush=True)
+    print("case replay gemv 8192x2048 M=1, 2048x8192 M=1, 8192x2048 M=4, 2048x8192 M=4", flush=True)
     c1, g1, x1 = synth_projection(8192, 2048, 4, seed=0)
-    c2, g2, x2 = synth_projection(2048, 8192, 1, seed=1)
+    c2, g2, x2 = synth_projection(2048, 8192, 4, seed=1)
     p1 = desk.attach(make_plane(c1, g1, 2048))
     p2 = desk.attach(make_plane(c2, g2, 8192))
     a1 = desk.upload(x1[:1].copy())
     a4 = desk.upload(x1)
-    a2 = desk.upload(x2)
+    a2 = desk.upload(x2[:1].copy())
+    a24 = desk.upload(x2)
     o1, o2, o4 = desk.alloc(8192 * 4), desk.alloc(2048 * 4), desk.alloc(4 * 8192 * 4)
     e1, e2, e4 = desk.alloc(8192 * 4), desk.alloc(2048 * 4), desk.alloc(4 * 8192 * 4)
+    o24, e24 = desk.alloc(4 * 2048 * 4), desk.alloc(4 * 2048 * 4)
 
     def eager():
         desk.gemv_dev(p1, a1, 2048, 1, e1, 8192)
         desk.gemv_dev(p2, a2, 8192, 1, e2, 2048)
         desk.gemv_dev(p1, a4, 2048, 4, e4, 8192)
+        desk.gemv_dev(p2, a24, 8192, 4, e24, 2048)  # K-chunked: partials, then their sum
         desk.sync()
-        return (e1.get(np.float32, 8192), e2.get(np.float32, 2048), e4.get(np.float32, 4 * 8192))
+        return (e1.get(np.float32, 8192), e2.get(np.float32, 2048), e4.get(np.float32, 4 * 8192),
+                e24.get(np.float32, 4 * 2048))
 
     want = eager()  # also sizes every scratch buffer the entries use
     desk.record_begin()
     desk.gemv_dev(p1, a1, 2048, 1, o1, 8192)
     desk.gemv_dev(p2, a2, 8192, 1, o2, 2048)
     desk.gemv_dev(p1, a4, 2048, 4, o4, 8192)
+    desk.gemv_dev(p2, a24, 8192, 4, o24, 2048)
     replay = desk.record_end()
     try:
         rng = np.random.default_rng(7)
@@ -52,10 +57,12 @@ def test_replay_equals_eager(desk):
                 a1.put(rng.normal(size=(1, 2048)).astype(np.float32))
                 a2.put(rng.normal(size=(1, 8192)).astype(np.float32))
                 a4.put(rng.normal(size=(4, 2048)).astype(np.float32))
+                a24.put(rng.normal(size=(4, 8192)).astype(np.float32))
                 want = eager()
             desk.replay_run(replay)
             desk.sync()
-            got = (o1.get(np.float32, 8192), o2.get(np.float32, 2048), o4.get(np.float32, 4 * 8192))
+            got = (o1.get(np.float32, 8192), o2.get(np.float32, 2048), o4.get(np.float32, 4 * 8192),
+                   o24.get(np.float32, 4 * 2048))
             for g, w in zip(got, want):
                 assert np.array_equal(g, w), f"replay {turn} differs from the eager run"
     finally:
