@@ -304,12 +304,21 @@ __device__ __forceinline__ float digit_sum(const int (&t)[DIG]) {
 //                  codes into two dwords of nibbles;
 //   DIGITS_BYTE    8-bit codes: three base-256 digits, q + 0x808080, byte e
 //                  of a dword element e of its four, for v_dot4_i32_i8.
-// Every form fills six 16-byte slots a unit: uint4 dig[(m 6 + s) units + u].
-// Nibble forms: slot s = digit j, dword k = the k-th eight elements.  Byte
-// form: slot 2 j + h = digit j of elements 16 h .. 16 h + 15, four a dword.
+// Every form fills six 16-byte slots a unit, unit-major with a pitch of
+// seven: uint4 dig[(m units + u) kDigitPitch + s] (digit_slot).  Nibble forms:
+// slot s = digit j, dword k = the k-th eight elements.  Byte form: slot
+// 2 j + h = digit j of elements 16 h .. 16 h + 15, four a dword.
 // The pair form also stores qsum[m units + u] = sum_e q_e, which takes the
 // code bias out of a dot against unsigned codes: sum (c - b) q = sum c q - b qsum.
 enum { DIGITS_NIBBLE = 0, DIGITS_PAIRS = 1, DIGITS_BYTE = 2 };
+
+// A unit's digits sit together, so a quad stores them, and a lane reads them,
+// at constant offsets from one address; the seventh slot is padding that
+// spreads the 16 units a b128 read or a b32 store touches at once over every
+// bank (a unit 28 dwords on: 28 u mod 64 is a distinct multiple of 4 for u < 16).
+constexpr int kDigitPitch = 7;
+
+__host__ __device__ constexpr int digit_slot(int m, int u, int units) { return (m * units + u) * kDigitPitch; }
 
 template <int BITS>
 struct CodeForm {
@@ -391,14 +400,15 @@ __device__ __forceinline__ void digit_group_store_form(const float (&xin)[8], in
     bytes_of_four(v[4], v[5], v[6], v[7], hi);
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
-      uint32_t *slot = base + ((m * 6 + 2 * j + (dw >> 1)) * units + u) * 4 + 2 * (dw & 1);
+      uint32_t *slot = base + (digit_slot(m, u, units) + 2 * j + (dw >> 1)) * 4 + 2 * (dw & 1);
       *reinterpret_cast<uint2_t *>(slot) = uint2_t{lo[j], hi[j]};
     }
   } else {
     uint32_t d[6];
     digits_of_eight<6>(x, up, d);
+    uint32_t *slot = base + digit_slot(m, u, units) * 4 + dw;
 #pragma unroll
-    for (int j = 0; j < 6; ++j) base[((m * 6 + j) * units + u) * 4 + dw] = d[j];
+    for (int j = 0; j < 6; ++j) slot[4 * j] = d[j];
     if constexpr (FORM == DIGITS_PAIRS) {
       int s = 0;
 #pragma unroll
@@ -415,7 +425,7 @@ __device__ __forceinline__ void digit_group_store_form(const float (&xin)[8], in
 // Staging x in digit form, for a workgroup of 256 threads.  Eight-element
 // group g of lane m (g < K / 8) is thread (m K / 8 + g) % 256's item
 // (m K / 8 + g) / 256; a thread holds GPT items.  The LDS form: uint4
-// dig[(m DIG + j) units + u] holds digit j of unit u's four dwords of eight
+// dig[digit_slot(m, u, units) + j] holds digit j of unit u's four dwords of eight
 // elements, and down[m units + u] = E - P.  K % 32 == 0, so the four
 // groups of a unit sit in one quad of threads, and a quad is wholly inside
 // or wholly past the end.
@@ -475,8 +485,9 @@ __device__ __forceinline__ void digit_group_store(const float (&x)[8], int m, in
   digits_of_eight<DIG>(x, DigitForm<DIG>::kP - E, d);
   const int u = gg >> 2, dw = gg & 3;
   uint32_t *base = reinterpret_cast<uint32_t *>(dig);
+  uint32_t *slot = base + digit_slot(m, u, units) * 4 + dw;
 #pragma unroll
-  for (int j = 0; j < DIG; ++j) base[((m * DIG + j) * units + u) * 4 + dw] = d[j];
+  for (int j = 0; j < DIG; ++j) slot[4 * j] = d[j];
   if (dw == 0) down[m * units + u] = E - DigitForm<DIG>::kP;
 }
 

@@ -366,7 +366,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_reg_kernel(GemvArgs a) {
 constexpr int kDigits = 6;
 
 __host__ __device__ constexpr size_t gemv_dot_lds_bytes(int M, int units) {
-  return (size_t)M * units * (kDigits * 16 + 4);
+  return (size_t)M * units * (kDigitPitch * 16 + 4);
 }
 
 template <int M, int R, int UPL, int GPT>
@@ -385,7 +385,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
   const int u_end = (units * (ks + 1)) >> ks_log;
   const int u_first = ((units * ks) >> ks_log) + lane;
   uint4_t *dig = lds_dig;
-  int *down = reinterpret_cast<int *>(dig + M * kDigits * units);
+  int *down = reinterpret_cast<int *>(dig + M * kDigitPitch * units);
 
   // Activations first, then the weights, all unconditionally: rows and
   // units past the end reload valid ones and get gain 0, so the arithmetic
@@ -434,7 +434,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
 #pragma unroll
       for (int m = 0; m < M; ++m) {
 #pragma unroll
-        for (int j = 0; j < kDigits; ++j) dd[m][j] = dig[(m * kDigits + j) * units + u];
+        for (int j = 0; j < kDigits; ++j) dd[m][j] = dig[digit_slot(m, u, units) + j];
         shift[m] = down[m * units + u];
       }
 #pragma unroll
@@ -468,7 +468,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
       for (int m = 0; m < M; ++m) {
         uint4_t dd[kDigits];
 #pragma unroll
-        for (int j = 0; j < kDigits; ++j) dd[j] = dig[(m * kDigits + j) * units + u];
+        for (int j = 0; j < kDigits; ++j) dd[j] = dig[digit_slot(m, u, units) + j];
         const int shift = down[m * units + u];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -565,7 +565,7 @@ struct GemvCodeArgs {
 };
 
 __host__ __device__ constexpr size_t gemv_code_lds_bytes(int M, int units) {
-  return (size_t)M * units * (6 * 16 + 8);
+  return (size_t)M * units * (kDigitPitch * 16 + 8);
 }
 
 // Sum over each sub-wave of 64 >> subs_log lanes; the total lands in the
@@ -615,7 +615,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_code_dot_kernel(GemvCodeArg
   const int unit0 = col0 >> 5;
   const uint8_t *code0 = a.codes + (size_t)(col0 / 8) * BITS;
   uint4_t *dig = lds_dig;
-  int *down = reinterpret_cast<int *>(dig + M * 6 * units);
+  int *down = reinterpret_cast<int *>(dig + M * kDigitPitch * units);
   int *qsum = down + M * units;
 
   // Every load unconditional (clamped rows, slots and units), gains before
@@ -692,7 +692,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_code_dot_kernel(GemvCodeArg
         for (int m = 0; m < M; ++m) {
           uint4_t dd[6];
 #pragma unroll
-          for (int j = 0; j < 6; ++j) dd[j] = dig[(m * 6 + j) * units + u];
+          for (int j = 0; j < 6; ++j) dd[j] = dig[digit_slot(m, u, units) + j];
           const int shift = down[m * units + u];
 #pragma unroll
           for (int r = 0; r < R; ++r) {
@@ -715,7 +715,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_code_dot_kernel(GemvCodeArg
           for (int m = 0; m < M; ++m) {
             uint4_t dd[6];
 #pragma unroll
-            for (int j = 0; j < 6; ++j) dd[j] = dig[(m * 6 + j) * units + u];
+            for (int j = 0; j < 6; ++j) dd[j] = dig[digit_slot(m, u, units) + j];
             const int shift = down[m * units + u];
             const int bq = a.code_bias * qsum[m * units + u];
 #pragma unroll
@@ -741,7 +741,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_code_dot_kernel(GemvCodeArg
         for (int m = 0; m < M; ++m) {
           uint4_t dd[3];
 #pragma unroll
-          for (int j = 0; j < 3; ++j) dd[j] = dig[(m * 6 + 2 * j + hf) * units + u];
+          for (int j = 0; j < 3; ++j) dd[j] = dig[digit_slot(m, u, units) + 2 * j + hf];
           const int shift = down[m * units + u];
 #pragma unroll
           for (int r = 0; r < R; ++r) {
@@ -1511,7 +1511,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
   const bool lane_has = u_raw < (units * (ks + 1)) / KS;
   const int u = min(u_raw, units - 1);
   uint4_t *dig = lds_grp;
-  int *down = reinterpret_cast<int *>(lds_grp + kDigits * units);
+  int *down = reinterpret_cast<int *>(lds_grp + kDigitPitch * units);
 
   // Row r of tile i: which plane, which row of it (tiles past the end reread
   // the last row; their sums are dropped).
@@ -1584,7 +1584,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
 
   uint4_t dd[kDigits];
 #pragma unroll
-  for (int j = 0; j < kDigits; ++j) dd[j] = dig[j * units + u];
+  for (int j = 0; j < kDigits; ++j) dd[j] = dig[digit_slot(0, u, units) + j];
   const int shift = down[u];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
@@ -2207,7 +2207,7 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
   const int tpw = pro && ksplit == 1 && (a.tiles + 3) / 4 >= 1024 ? 2 : 1;
   const int tiles_per_block = 4 / ksplit * tpw;
   dim3 grid((a.tiles + tiles_per_block - 1) / tiles_per_block);
-  const size_t lds = gemv_dot_lds_bytes(1, units);  // at most 25 KiB (K <= 8192)
+  const size_t lds = gemv_dot_lds_bytes(1, units);  // at most 29 KiB (K <= 8192)
   // eight-element groups of x a thread stages without a prologue
   const int gpt = K <= 2048 ? 1 : K <= 4096 ? 2 : 4;
 #define IGL_GROUP_KS(M_, P_, G_)                                                                    \
