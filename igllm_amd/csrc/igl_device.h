@@ -582,45 +582,55 @@ __device__ __forceinline__ void level_group_store(const float (&xin)[8], float s
 #pragma unroll
     for (int e = 0; e < 8; ++e) qt[e] = x[e] / step;
   }
-  int L[8];
-  int bad = 0;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float q = __builtin_rintf(qt[e]);
-    bad |= q != q;
-    q = q < -128.0f ? -128.0f : q;
-    q = q > 127.0f ? 127.0f : q;
-    L[e] = q == q ? (int)q : 0;
-  }
+  // A NaN quotient (a NaN x) marks the unit; its bytes below are then any
+  // value, as the lane's outputs are NaN.
+  const int bad = (__builtin_isunordered(qt[0], qt[1]) || __builtin_isunordered(qt[2], qt[3]) ||
+                   __builtin_isunordered(qt[4], qt[5]) || __builtin_isunordered(qt[6], qt[7])) ? 1 : 0;
+  // B = L + 128 as bytes: rint, the two clamps as one med3, then an exact
+  // integer in [0, 255] into its byte (v_cvt_pk_u8_f32)
+  auto biased = [&](int e) { return __builtin_amdgcn_fmed3f(__builtin_rintf(qt[e]), -128.0f, 127.0f) + 128.0f; };
   uint32_t *base = reinterpret_cast<uint32_t *>(lv);
   int c = 0;
   if constexpr (FORM == DIGITS_BYTE) {
+    // elements 0..3 and 4..7, four a dword, as signed bytes L = B ^ 0x80
     uint32_t b0 = 0, b1 = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      b0 |= ((uint32_t)L[e] & 0xFFu) << (8 * e);
-      b1 |= ((uint32_t)L[e + 4] & 0xFFu) << (8 * e);
+      b0 = __builtin_amdgcn_cvt_pk_u8_f32(biased(e), e, b0);
+      b1 = __builtin_amdgcn_cvt_pk_u8_f32(biased(e + 4), e, b1);
     }
-    *reinterpret_cast<uint2_t *>(base + ((m * 2 + (dw >> 1)) * units + u) * 4 + 2 * (dw & 1)) = uint2_t{b0, b1};
+    *reinterpret_cast<uint2_t *>(base + ((m * 2 + (dw >> 1)) * units + u) * 4 + 2 * (dw & 1)) =
+        uint2_t{b0 ^ 0x80808080u, b1 ^ 0x80808080u};
   } else {
-    uint32_t lo = 0, hi = 0;
+    // even and odd elements' bytes: byte k of be / bo is element 2k / 2k + 1,
+    // so their low nibbles interleave into L & 15 (nibble e = element e) and
+    // their high nibbles into (L >> 4) + 8, a signed nibble once xor 8
+    uint32_t be = 0, bo = 0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      lo |= ((uint32_t)L[e] & 15u) << (4 * e);
-      hi |= ((uint32_t)(L[e] >> 4) & 15u) << (4 * e);
-      c += FORM == DIGITS_PAIRS ? L[e] : (L[e] & 15);
+    for (int k = 0; k < 4; ++k) {
+      be = __builtin_amdgcn_cvt_pk_u8_f32(biased(2 * k), k, be);
+      bo = __builtin_amdgcn_cvt_pk_u8_f32(biased(2 * k + 1), k, bo);
     }
+    const uint32_t lo = (be & 0x0F0F0F0Fu) | ((bo << 4) & 0xF0F0F0F0u);
+    const uint32_t hi = (((be >> 4) & 0x0F0F0F0Fu) | (bo & 0xF0F0F0F0u)) ^ 0x88888888u;
     base[((m * 2 + 0) * units + u) * 4 + dw] = lo;
     base[((m * 2 + 1) * units + u) * 4 + dw] = hi;
-    c *= FORM == DIGITS_PAIRS ? code_bias : 8;
+    if constexpr (FORM == DIGITS_PAIRS) {
+      // sum L = sum B - 8 * 128
+      const int sum_b = (int)__builtin_amdgcn_udot4(be, 0x01010101u, __builtin_amdgcn_udot4(bo, 0x01010101u, 0u, false), false);
+      c = (sum_b - 1024) * code_bias;
+    } else {
+      c = 8 * (int)__builtin_amdgcn_udot8(lo, 0x11111111u, 0u, false);  // 8 sum (L & 15)
+    }
   }
+  int bad_sum = bad;
   c += __builtin_amdgcn_update_dpp(0, c, 0xB1, 0xF, 0xF, true);
   c += __builtin_amdgcn_update_dpp(0, c, 0x4E, 0xF, 0xF, true);
-  bad += __builtin_amdgcn_update_dpp(0, bad, 0xB1, 0xF, 0xF, true);
-  bad += __builtin_amdgcn_update_dpp(0, bad, 0x4E, 0xF, 0xF, true);
+  bad_sum += __builtin_amdgcn_update_dpp(0, bad_sum, 0xB1, 0xF, 0xF, true);
+  bad_sum += __builtin_amdgcn_update_dpp(0, bad_sum, 0x4E, 0xF, 0xF, true);
   if (dw == 0) {
     corr[m * units + u] = c;
-    nanu[m * units + u] = bad;
+    nanu[m * units + u] = bad_sum;
   }
 }
 

@@ -1142,9 +1142,28 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
     }
 #pragma unroll
   for (int m = 0; m < M; ++m) bad[m] = sub_sum_to_last_int(bad[m], subs_log);
+  // One output (row r of the sub-wave's R, lane m): the row close as the
+  // reference's, fl(fl(gain step) fl(part)), NaN for a lane that held one,
+  // the leave grid, then the fused elementwise step.
+  auto close = [&](int r, int m, int it, float ft, int b) {
+    const int row = row0 + r;
+    if (row >= a.N || m >= a.lanes) return;
+    float y = one_group ? a.gains[(size_t)row * (size_t)a.gain_stride] * a.step * (float)it : ft;
+    if (b) y = __builtin_nanf("");
+    y = grid_value(y, a.leave);
+    // the reference's next step on this output (kern_gelu_gate): with the gate
+    // projection's output, gelu(gate) * y; with the per-layer input, gelu(y) * it
+    if (a.epi == IGL_LEVEL_EPI_GELU_RISE)
+      y = gelu_near(a.epi_in[(size_t)m * a.epi_stride + row]) * y;
+    else if (a.epi == IGL_LEVEL_EPI_GELU_MUL)
+      y = gelu_near(y) * a.epi_in[(size_t)m * a.epi_stride + row];
+    a.out[(size_t)m * a.out_stride + row] = y;
+  };
   const bool owner = sub_lane == (64 >> subs_log) - 1;
   if (ks_log > 0) {
-    // one tile a wave group (subs_log == 0): the waves' sums meet in LDS
+    // one tile a wave group (subs_log == 0): the waves' sums meet in LDS, and
+    // lane r M + m of the first wave closes output (r, m), adding the waves'
+    // parts in wave order
     if (owner) {
 #pragma unroll
       for (int m = 0; m < M; ++m) {
@@ -1157,46 +1176,26 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
       }
     }
     __syncthreads();
-    if (ks != 0) return;
+    if (ks != 0 || lane >= R * M) return;
+    const int r = lane / M;
+    const int m = lane - r * M;
+    int it = 0, b = 0;
+    float ft = 0.0f;
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      int b = 0;
-      for (int k = 0; k < (1 << ks_log); ++k) b += bred[wave + k][m];
-      bad[m] = b;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        int it = 0;
-        float ft = 0.0f;
-        for (int k = 0; k < (1 << ks_log); ++k) {
-          it += ired[wave + k][r][m];
-          ft += fred[wave + k][r][m];
-        }
-        ip[r][m] = it;
-        fp[r][m] = ft;
+    for (int k = 0; k < 4; ++k)
+      if (k < (1 << ks_log)) {
+        it += ired[wave + k][r][m];
+        ft += fred[wave + k][r][m];
+        b += bred[wave + k][m];
       }
-    }
+    close(r, m, it, ft, b);
+    return;
   }
   if (!owner) return;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int row = row0 + r;
-    if (row >= a.N) continue;
-    const float gain_step = one_group ? a.gains[(size_t)row * (size_t)a.gain_stride] * a.step : 0.0f;
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      if (m >= a.lanes) continue;
-      float y = one_group ? gain_step * (float)ip[r][m] : fp[r][m];
-      if (bad[m]) y = __builtin_nanf("");
-      y = grid_value(y, a.leave);
-      // the reference's next step on this output (kern_gelu_gate): with the gate
-      // projection's output, gelu(gate) * y; with the per-layer input, gelu(y) * it
-      if (a.epi == IGL_LEVEL_EPI_GELU_RISE)
-        y = gelu_near(a.epi_in[(size_t)m * a.epi_stride + row]) * y;
-      else if (a.epi == IGL_LEVEL_EPI_GELU_MUL)
-        y = gelu_near(y) * a.epi_in[(size_t)m * a.epi_stride + row];
-      a.out[(size_t)m * a.out_stride + row] = y;
-    }
-  }
+    for (int m = 0; m < M; ++m) close(r, m, ip[r][m], fp[r][m], bad[m]);
 }
 
 // ---- real planes: F32, F16 or BF16 rows -------------------------------------
