@@ -529,31 +529,40 @@ __device__ __forceinline__ void digit_store_lds(const float *xs, int K, uint4_t 
 // of eight: `lo` holds L & 15 (unsigned), `hi` holds L >> 4 (a signed
 // nibble), so L = 16 hi + lo and a dot against codes splits into one signed
 // and one unsigned v_dot8; the byte form stores L itself, four a dword.  The
-// element order is the digit form's (DIGITS_PAIRS for 2-bit codes).  LDS:
-// uint4 lv[(m 2 + s) units + u], s = 0 / 1 the lo / hi dwords (bytes: elements
-// 0..15 / 16..31); corr[m units + u] = the bias correction of the unit
+// element order is the digit form's (DIGITS_PAIRS for 2-bit codes).  LDS,
+// unit-major at a pitch of three slots (level_slot; the pad puts the 16 units
+// of one b128 read 12 dwords apart, a distinct 4-bank group each):
+// uint4 lv[level_slot(m, u, units) + s], s = 0 / 1 the lo / hi dwords (bytes:
+// elements 0..15 / 16..31); corr[m units + u] = the bias correction of the unit
 // (4-bit: 8 sum lo; 2-bit: code_bias sum L; 8-bit: 0); nanu[m units + u] != 0
 // where the unit holds a NaN (its level is no level; the lane's outputs are NaN).
 // x / step rounded to nearest, for rounding to a level: with inv = 1 / step
 // correctly rounded, q0 = x inv is within an ulp of the quotient, the residual
 // x - q0 step is exact (one fma), and q0 + residual inv rounds to the
 // correctly rounded quotient (Markstein's theorem on division by a correctly
-// rounded reciprocal and an fma correction).  Quotients of 256 and up (and
-// their overflow) skip the correction: the level clamps at -128 / 127 either
-// way.  A host check of 4e8 random and near-half-integer quotients found no
-// level that differs from rint(x / step).  The theorem needs inv normal and
-// the residual exact (no underflow): step in [2^-96, 2^96] gives both for
-// every quotient under 256, and level_recip returns 0 outside it, where the
-// caller divides instead.
+// rounded reciprocal and an fma correction).  q0 is first clamped to
+// [-256, 256] (one med3): below that the clamp changes nothing; past it the
+// level clamps at -128 / 127 whatever the correction gives, and the clamp
+// keeps an overflowed q0 (an infinity) out of the residual, where inf - inf
+// would turn it into a NaN; a NaN x stays NaN through the residual.  A host
+// check of 4e8 random and near-half-integer quotients found no level that
+// differs from rint(x / step).  The theorem needs inv normal and the residual
+// exact (no underflow): step in [2^-96, 2^96] gives both for every quotient
+// under 256, and level_recip returns 0 outside it, where the caller divides
+// instead.
 __device__ __forceinline__ float quot_near(float x, float step, float inv) {
-  const float q0 = x * inv;
+  const float q0 = __builtin_amdgcn_fmed3f(x * inv, -256.0f, 256.0f);
   const float r = __builtin_fmaf(-q0, step, x);
-  return __builtin_fabsf(q0) < 256.0f ? __builtin_fmaf(r, inv, q0) : q0;
+  return __builtin_fmaf(r, inv, q0);
 }
 
 __device__ __forceinline__ float level_recip(float step) {
   return step >= 0x1p-96f && step <= 0x1p96f ? 1.0f / step : 0.0f;
 }
+
+constexpr int kLevelPitch = 3;
+
+__host__ __device__ constexpr int level_slot(int m, int u, int units) { return (m * units + u) * kLevelPitch; }
 
 template <int FORM>
 __device__ __forceinline__ void level_group_store(const float (&xin)[8], float step, float inv, int code_bias, int m,
@@ -599,7 +608,7 @@ __device__ __forceinline__ void level_group_store(const float (&xin)[8], float s
       b0 = __builtin_amdgcn_cvt_pk_u8_f32(biased(e), e, b0);
       b1 = __builtin_amdgcn_cvt_pk_u8_f32(biased(e + 4), e, b1);
     }
-    *reinterpret_cast<uint2_t *>(base + ((m * 2 + (dw >> 1)) * units + u) * 4 + 2 * (dw & 1)) =
+    *reinterpret_cast<uint2_t *>(base + (level_slot(m, u, units) + (dw >> 1)) * 4 + 2 * (dw & 1)) =
         uint2_t{b0 ^ 0x80808080u, b1 ^ 0x80808080u};
   } else {
     // even and odd elements' bytes: byte k of be / bo is element 2k / 2k + 1,
@@ -613,8 +622,9 @@ __device__ __forceinline__ void level_group_store(const float (&xin)[8], float s
     }
     const uint32_t lo = (be & 0x0F0F0F0Fu) | ((bo << 4) & 0xF0F0F0F0u);
     const uint32_t hi = (((be >> 4) & 0x0F0F0F0Fu) | (bo & 0xF0F0F0F0u)) ^ 0x88888888u;
-    base[((m * 2 + 0) * units + u) * 4 + dw] = lo;
-    base[((m * 2 + 1) * units + u) * 4 + dw] = hi;
+    uint32_t *slot = base + level_slot(m, u, units) * 4 + dw;
+    slot[0] = lo;
+    slot[4] = hi;
     if constexpr (FORM == DIGITS_PAIRS) {
       // sum L = sum B - 8 * 128
       const int sum_b = (int)__builtin_amdgcn_udot4(be, 0x01010101u, __builtin_amdgcn_udot4(bo, 0x01010101u, 0u, false), false);

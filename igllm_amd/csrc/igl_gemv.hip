@@ -851,7 +851,7 @@ struct GemvLevelArgs {
 };
 
 __host__ __device__ constexpr size_t gemv_level_lds_bytes(int M, int units) {
-  return (size_t)M * units * (2 * 16 + 8);
+  return (size_t)M * units * (kLevelPitch * 16 + 8);
 }
 
 __device__ __forceinline__ int sub_sum_to_last_int(int v, int subs_log) {
@@ -1000,7 +1000,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
   const int s_end = (slots * (ks + 1)) >> ks_log;
   const int s_first = ((slots * ks) >> ks_log) + sub_lane;
   uint4_t *lv = lds_lv;
-  int *corr = reinterpret_cast<int *>(lv + M * 2 * units);
+  int *corr = reinterpret_cast<int *>(lv + M * kLevelPitch * units);
   int *nanu = corr + M * units;
 
   DigitLoads<GPT> held;
@@ -1083,10 +1083,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
         bad[m] |= live && nanu[m * units + u] != 0;
         uint4_t lo, hi;
         if constexpr (BITS == 8) {
-          lo = lv[(m * 2 + (sl & 1)) * units + u];
+          lo = lv[level_slot(m, u, units) + (sl & 1)];
         } else {
-          lo = lv[(m * 2 + 0) * units + u];
-          hi = lv[(m * 2 + 1) * units + u];
+          lo = lv[level_slot(m, u, units)];
+          hi = lv[level_slot(m, u, units) + 1];
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {

@@ -3,8 +3,8 @@ and rint(x / step)) are computed on the GPU as q = fl(y r), r = fl(1 / leave),
 then fl(q + fl(y - q leave) r) with two fused multiply-adds (quot_near in
 igl_device.h: the fused GEMV's activation levels, and div_leave in
 igl_gemm_level.hip: the leave grid), for steps in [2^-96, 2^96] (level_recip;
-outside it the kernels divide), quotients under 256 (at and above it fl(y r)
-is kept, and the level clamps alike).  This pins that sequence to the
+outside it the kernels divide), with fl(y r) first clamped to [-256, 256]
+(beyond it the level clamps alike).  This pins that sequence to the
 correctly rounded binary32 quotient in exact rational arithmetic: near-ties at
 every half-integer quotient of the clamp range, random quotients, and leave
 values including all-ones mantissas, powers of two, both ends of the range
@@ -88,13 +88,14 @@ def test_corrected_division_is_correctly_rounded():
 
 def quot_near(x: Fraction, step: Fraction):
     """quot_near of igl_device.h in exact arithmetic, each operation rounded
-    once; returns (value, corrected)."""
+    once; returns (value, corrected): corrected is False where q0 was clamped
+    (the quotient's magnitude is then at least 256)."""
     inv = rn32(1 / step)
     q0 = rn32(x * inv)
-    if abs(q0) >= 256:
-        return q0, False
+    clamped = abs(q0) > 256
+    q0 = max(min(q0, Fraction(256)), Fraction(-256))
     r = rn32(x - q0 * step)
-    return rn32(r * inv + q0), True
+    return rn32(r * inv + q0), not clamped
 
 
 def clamp_level(q: float) -> float:
@@ -131,17 +132,28 @@ def test_quot_near_range_ends():
     assert checked > 3000
 
 
+def device_quot_f32(x, st):
+    """quot_near in binary32 with numpy, each fma as a float64 product (exact
+    for two binary32 values) and sum rounded to binary32; only the clamped
+    levels of these special cases are compared."""
+    inv = np.float32(1.0) / st
+    q0 = np.float32(np.clip(np.float32(x * inv), -256.0, 256.0)) if not np.isnan(x * inv) else np.float32(256.0)
+    r = np.float32(np.float64(x) - np.float64(q0) * np.float64(st))
+    return np.float32(np.float64(r) * np.float64(inv) + np.float64(q0))
+
+
 def test_quot_near_specials_clamp_alike():
-    """Overflowing and non-finite quotients in binary32: fl(x r) overflows to
-    infinity (kept, as |q0| >= 256), NaN stays NaN, zero stays zero."""
+    """Overflowing and non-finite quotients in binary32: fl(x r) overflowing
+    to infinity is clamped to 256 and the result clamps to the same level as
+    the quotient; NaN stays NaN (whatever the clamp gives for it); zero stays
+    zero."""
     with np.errstate(over="ignore", invalid="ignore"):
-        for x, st in [(3.0e38, 0.01), (-3.0e38, 0.01), (np.inf, 0.5), (-np.inf, 0.5), (np.nan, 0.5), (0.0, 2.0 ** -96)]:
+        for x, st in [(3.0e38, 0.01), (-3.0e38, 0.01), (np.inf, 0.5), (-np.inf, 0.5), (np.nan, 0.5),
+                      (0.0, 2.0 ** -96), (300.0, 1.0), (-1000.0, 1.0), (255.75, 1.0), (-128.5, 1.0)]:
             x, st = np.float32(x), np.float32(st)
-            inv = np.float32(1.0) / st
-            q0 = x * inv
+            got = device_quot_f32(x, st)
             want = x / st
             if np.isnan(want):
-                assert np.isnan(q0)
+                assert np.isnan(got)
             else:
-                assert not abs(q0) < 256 or q0 == want
-                assert clamp_level(q0) == clamp_level(want)
+                assert clamp_level(got) == clamp_level(want), (float(x), float(st), float(got))
