@@ -564,7 +564,8 @@ constexpr int kLevelPitch = 3;
 
 __host__ __device__ constexpr int level_slot(int m, int u, int units) { return (m * units + u) * kLevelPitch; }
 
-template <int FORM>
+// NEAR: x / step by quot_near (inv = level_recip(step) != 0); else divided.
+template <int FORM, bool NEAR>
 __device__ __forceinline__ void level_group_store(const float (&xin)[8], float step, float inv, int code_bias, int m,
                                                   int gg, int units, uint4_t *lv, int *corr, int *nanu) {
   const int u = gg >> 2, dw = gg & 3;
@@ -584,13 +585,8 @@ __device__ __forceinline__ void level_group_store(const float (&xin)[8], float s
     for (int e = 0; e < 8; ++e) x[e] = xin[e];
   }
   float qt[8];
-  if (inv != 0.0f) {  // uniform: one step for the launch
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qt[e] = quot_near(x[e], step, inv);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qt[e] = x[e] / step;
-  }
+  for (int e = 0; e < 8; ++e) qt[e] = NEAR ? quot_near(x[e], step, inv) : x[e] / step;
   // A NaN quotient (a NaN x) marks the unit; its bytes below are then any
   // value, as the lane's outputs are NaN.
   const int bad = (__builtin_isunordered(qt[0], qt[1]) || __builtin_isunordered(qt[2], qt[3]) ||
@@ -668,11 +664,21 @@ __device__ __forceinline__ void level_store_form(const DigitLoads<GPT> &h, int K
   const int units = K >> 5;
   const int per_lane = K >> 3;
   const float inv = level_recip(step);  // once a thread
+  // one branch (uniform: one step for the launch), each arm straight-line
+  if (inv != 0.0f) {
 #pragma unroll
-  for (int i = 0; i < GPT; ++i) {
-    const int g = digit_item(i, M * per_lane);
-    const int m = M == 1 ? 0 : g / per_lane;
-    level_group_store<FORM>(h.x[i], step, inv, code_bias, m, g - m * per_lane, units, lv, corr, nanu);
+    for (int i = 0; i < GPT; ++i) {
+      const int g = digit_item(i, M * per_lane);
+      const int m = M == 1 ? 0 : g / per_lane;
+      level_group_store<FORM, true>(h.x[i], step, inv, code_bias, m, g - m * per_lane, units, lv, corr, nanu);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int g = digit_item(i, M * per_lane);
+      const int m = M == 1 ? 0 : g / per_lane;
+      level_group_store<FORM, false>(h.x[i], step, inv, code_bias, m, g - m * per_lane, units, lv, corr, nanu);
+    }
   }
   __syncthreads();
 }
