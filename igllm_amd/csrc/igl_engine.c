@@ -715,6 +715,23 @@ static int project_level_pro(igl_engine *e, const igl_plane *p, const igl_gemv_p
   return IGL_OKAY;
 }
 
+/* Gate and up planes that one pair launch takes: both calibrated one-lane
+ * prologue planes of the same kind, rows and enter step. */
+static int level_pair_fits(const igl_engine *e, const igl_plane *g, const igl_plane *u, int rows) {
+  return level_pro_fits(e, g) && level_pro_fits(e, u) && g->bit_count == u->bit_count &&
+         g->code_bias == u->code_bias && g->code_flip == u->code_flip && g->group_count == u->group_count &&
+         g->row_count == rows && u->row_count == rows && g->enter_gain == u->enter_gain;
+}
+
+static int project_level_pair(igl_engine *e, const igl_plane *g, const igl_plane *u,
+                              const igl_gemv_prologue *pro, float *out) {
+  const igl_code_view vg = igl_plane_view(g, dev_codes(e, g), dev_gains(e, g));
+  const igl_code_view vu = igl_plane_view(u, dev_codes(e, u), dev_gains(e, u));
+  RUN(igl_launch_gemv_level_pair(&vg, &vu, g->enter_gain, g->leave_gain, u->leave_gain, pro, out, g->row_count,
+                                 g->col_count, e->stream));
+  return IGL_OKAY;
+}
+
 static int norm_rows(igl_engine *e, const float *in, const float *gain, int n, int lanes, int stride,
                      float *out) {
   return igl_norm_rms_dev(e->desk, in, gain, n, lanes, stride, e->eps, out);
@@ -881,6 +898,11 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
   if (fused) {
     igl_gemv_prologue pro = state_update(e, e->lift, L->after_attn, 1.0f, L->before_ff);
     OKAY(group_run(e, &gf, &L->gate, IGL_GEMV_GELU_PAIR, NULL, NULL, &pro));
+    state_flip(e);
+  } else if (lanes == 1 && level_pair_fits(e, &L->gate, &L->up, L->inner)) {
+    /* calibrated gate and up planes in one launch, the update as its prologue */
+    igl_gemv_prologue pro = state_update(e, e->lift, L->after_attn, 1.0f, L->before_ff);
+    OKAY(project_level_pair(e, &L->gate, &L->up, &pro, e->gate));
     state_flip(e);
   } else {
     if (lanes == 1 && level_pro_fits(e, &L->gate)) {

@@ -848,6 +848,13 @@ struct GemvLevelArgs {
   float eps;
   int pro_vec;            // the K-vectors, state_out and x_out 16-byte aligned
   float *x_out;
+  // PAIR (one lane): the up projection beside the gate one (`codes`, `gains`,
+  // `leave`), the same kind, rows and enter step; out = gelu(gate) * up
+  const uint8_t *codes2;
+  long long row_stride2;
+  const float *gains2;
+  int gain_stride2;
+  float leave2;
 };
 
 __host__ __device__ constexpr size_t gemv_level_lds_bytes(int M, int units) {
@@ -975,9 +982,13 @@ __device__ __forceinline__ void level_prologue(const GemvLevelArgs &a, const Pro
 }
 
 // PRO: one lane whose x is formed by the prologue above (M == 1).
-template <int BITS, int M, int R, int UPL, int GPT, bool PRO = false>
+template <int BITS, int M, int R, int UPL, int GPT, bool PRO = false, bool PAIR = false>
 __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs a) {
   static_assert(!PRO || M == 1, "the prologue forms one lane");
+  static_assert(!PAIR || (M == 1 && R % 2 == 0), "a pair: one lane, rows of both planes");
+  // rows of one plane a sub-wave: a pair's tile holds RP gate rows, then the
+  // same RP rows of the up plane
+  constexpr int RP = PAIR ? R / 2 : R;
   constexpr int FORM = CodeForm<BITS>::kDigits;
   constexpr int kSub = BITS == 2 ? 2 : 1;
   extern __shared__ uint4_t lds_lv[];
@@ -994,7 +1005,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
   const int sub = lane >> (6 - subs_log);
   const int sub_lane = lane & ((64 >> subs_log) - 1);
   const int tile = blockIdx.x * (4 >> ks_log) + (wave >> ks_log);
-  const int row0 = tile * (R << subs_log) + sub * R;
+  const int row0 = tile * (RP << subs_log) + sub * RP;
   const int units = a.K >> 5;
   const int slots = (a.K * BITS + 127) >> 7;
   const int s_end = (slots * (ks + 1)) >> ks_log;
@@ -1035,9 +1046,12 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
       const int u = min(u_raw, units - 1);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const int row = min(row0 + r, a.N - 1);
-        const float g = a.gains[(size_t)row * (size_t)a.gain_stride + ((unsigned)u >> a.group_shift)];
-        s[j][r][h] = in && u_raw < units && row0 + r < a.N ? g : 0.0f;
+        const bool up = PAIR && r >= RP;
+        const int row = min(row0 + r % RP, a.N - 1);
+        const float *gp = up ? a.gains2 : a.gains;
+        const int gs = up ? a.gain_stride2 : a.gain_stride;
+        const float g = gp[(size_t)row * (size_t)gs + ((unsigned)u >> a.group_shift)];
+        s[j][r][h] = in && u_raw < units && row0 + r % RP < a.N ? g : 0.0f;
       }
     }
   }
@@ -1046,8 +1060,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
     const int sl = min(s_first + 64 * j, slots - 1);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int row = min(row0 + r, a.N - 1);
-      w[j][r] = __builtin_nontemporal_load(reinterpret_cast<const uint4_t *>(a.codes + (size_t)row * (size_t)a.row_stride) + sl);
+      const bool up = PAIR && r >= RP;
+      const int row = min(row0 + r % RP, a.N - 1);
+      const uint8_t *cp = up ? a.codes2 : a.codes;
+      const long long rs = up ? a.row_stride2 : a.row_stride;
+      w[j][r] = __builtin_nontemporal_load(reinterpret_cast<const uint4_t *>(cp + (size_t)row * (size_t)rs) + sl);
     }
   }
   if constexpr (PRO) level_prologue<GPT>(a, pl, held, pro_red);
@@ -1159,6 +1176,21 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
       y = gelu_near(y) * a.epi_in[(size_t)m * a.epi_stride + row];
     a.out[(size_t)m * a.out_stride + row] = y;
   };
+  // A pair's output (row r of the sub-wave's RP, the one lane): both row
+  // closes on their own leave grids, then kern_gelu_gate's gelu(gate) * up.
+  auto close_pair = [&](int r, int itg, float ftg, int itu, float ftu, int b) {
+    const int row = row0 + r;
+    if (row >= a.N) return;
+    float yg = one_group ? a.gains[(size_t)row * (size_t)a.gain_stride] * a.step * (float)itg : ftg;
+    float yu = one_group ? a.gains2[(size_t)row * (size_t)a.gain_stride2] * a.step * (float)itu : ftu;
+    if (b) {
+      yg = __builtin_nanf("");
+      yu = yg;
+    }
+    yg = grid_value(yg, a.leave);
+    yu = grid_value(yu, a.leave2);
+    a.out[row] = gelu_near(yg) * yu;
+  };
   const bool owner = sub_lane == (64 >> subs_log) - 1;
   if (ks_log > 0) {
     // one tile a wave group (subs_log == 0): the waves' sums meet in LDS, and
@@ -1176,6 +1208,22 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
       }
     }
     __syncthreads();
+    if constexpr (PAIR) {
+      if (ks != 0 || lane >= RP) return;
+      int itg = 0, itu = 0, b = 0;
+      float ftg = 0.0f, ftu = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (k < (1 << ks_log)) {
+          itg += ired[wave + k][lane][0];
+          ftg += fred[wave + k][lane][0];
+          itu += ired[wave + k][lane + RP][0];
+          ftu += fred[wave + k][lane + RP][0];
+          b += bred[wave + k][0];
+        }
+      close_pair(lane, itg, ftg, itu, ftu, b);
+      return;
+    }
     if (ks != 0 || lane >= R * M) return;
     const int r = lane / M;
     const int m = lane - r * M;
@@ -1192,6 +1240,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
     return;
   }
   if (!owner) return;
+  if constexpr (PAIR) {
+#pragma unroll
+    for (int r = 0; r < RP; ++r) close_pair(r, ip[r][0], fp[r][0], ip[r + RP][0], fp[r + RP][0], bad[0]);
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -2532,6 +2585,87 @@ extern "C" hipError_t igl_launch_gemv_level_pro(const igl_code_view *v, float st
                 (uintptr_t)(a.state_out ? a.state_out : a.state_in) |
                 (uintptr_t)(x_out ? x_out : a.state_in)) & 15u) == 0;
   return igl_level_launch(a, v, step, leave, nullptr, K, 1, out, N, N, K, epi, epi_in, 0, stream);
+}
+
+// Rows a sub-wave of a pair launch (half of them the gate plane's).
+constexpr int kLevelPairRows = 4;
+
+template <int BITS>
+static hipError_t gemv_level_pair_launch(const GemvLevelArgs &a, dim3 grid, size_t lds, hipStream_t stream) {
+  hipLaunchKernelGGL((gemv_level_kernel<BITS, 1, kLevelPairRows, 1, 1, true, true>), grid, dim3(kGemvThreads), lds,
+                     stream, a);
+  return hipGetLastError();
+}
+
+// The gate and up projections of one lane in one launch (kern_gelu_gate's
+// gelu(gate) * up into `out`), the residual update as the prologue: both
+// planes the same kind, rows and enter step, K <= 2048.
+extern "C" hipError_t igl_launch_gemv_level_pair(const igl_code_view *gate, const igl_code_view *up, float step,
+                                                 float leave_gate, float leave_up, const igl_gemv_prologue *pro,
+                                                 float *out, int N, int K, hipStream_t stream) {
+  const int bits = gate ? gate->bit_count : 0;
+  if (!gate || !up || !pro || !pro->state_in || !out || N < 1 || K > 2048 || !(step > 0.0f) ||
+      !igl_gemv_level_fits(bits, K) || up->bit_count != bits || up->code_bias != gate->code_bias ||
+      up->code_flip != gate->code_flip || up->group_shift != gate->group_shift ||
+      (pro->lift && (!pro->lift_gain || !pro->state_out)) || pro->state_out == pro->state_in)
+    return hipErrorInvalidValue;
+  GemvLevelArgs a{};
+  a.state_in = pro->state_in;
+  a.state_out = pro->state_out;
+  a.lift = pro->lift;
+  a.lift_gain = pro->lift_gain;
+  a.scale = pro->scale;
+  a.apply_scale = pro->apply_scale;
+  a.norm_gain = pro->norm_gain;
+  a.eps = pro->eps;
+  a.x_out = nullptr;
+  a.pro_vec = ((((uintptr_t)a.state_in) | (uintptr_t)(a.lift ? a.lift : a.state_in) |
+                (uintptr_t)(a.lift_gain ? a.lift_gain : a.state_in) |
+                (uintptr_t)(a.norm_gain ? a.norm_gain : a.state_in) |
+                (uintptr_t)(a.state_out ? a.state_out : a.state_in)) & 15u) == 0;
+  a.codes = gate->codes;
+  a.row_stride = gate->row_stride;
+  a.gains = gate->gains;
+  a.gain_stride = gate->gain_stride;
+  a.codes2 = up->codes;
+  a.row_stride2 = up->row_stride;
+  a.gains2 = up->gains;
+  a.gain_stride2 = up->gain_stride;
+  a.group_shift = gate->group_shift;
+  a.act = nullptr;
+  a.act_stride = K;
+  a.out = out;
+  a.out_stride = N;
+  a.lanes = 1;
+  a.N = N;
+  a.K = K;
+  a.code_bias = gate->code_bias;
+  a.step = step;
+  a.leave = leave_gate;
+  a.leave2 = leave_up;
+  a.epi = IGL_LEVEL_EPI_NONE;
+  a.epi_in = nullptr;
+  a.epi_stride = 0;
+  const uint32_t field = bits == 8 ? (uint32_t)((gate->code_flip ^ gate->code_bias) & 255)
+                                   : (uint32_t)(gate->code_flip & ((1 << bits) - 1));
+  a.code_xor = field * (bits == 2 ? 0x55555555u : bits == 4 ? 0x11111111u : 0x01010101u);
+  const int slots = (K * bits + 127) / 128;
+  if (slots > 4 * kWave) return hipErrorInvalidValue;
+  const int subs_log = slots <= 16 ? 2 : slots <= 32 ? 1 : 0;
+  const int rp = kLevelPairRows / 2;
+  const int tiles = (N + (rp << subs_log) - 1) / (rp << subs_log);
+  int ksplit = 1;
+  while (subs_log == 0 && ksplit < 4 &&
+         (slots > ksplit * kWave || (tiles * ksplit < 2048 && slots / (ksplit * 2) >= 32)))
+    ksplit *= 2;
+  a.ks_log = ksplit == 1 ? 0 : ksplit == 2 ? 1 : 2;
+  a.subs_log = subs_log;
+  const int per_block = 4 / ksplit;
+  const dim3 grid((tiles + per_block - 1) / per_block);
+  const size_t lds = gemv_level_lds_bytes(1, K / 32);
+  return bits == 2   ? gemv_level_pair_launch<2>(a, grid, lds, stream)
+         : bits == 4 ? gemv_level_pair_launch<4>(a, grid, lds, stream)
+                     : gemv_level_pair_launch<8>(a, grid, lds, stream);
 }
 
 static hipError_t igl_level_launch(GemvLevelArgs a, const igl_code_view *v, float step, float leave,

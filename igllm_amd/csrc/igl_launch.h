@@ -99,6 +99,13 @@ typedef struct igl_gemv_prologue {
 hipError_t igl_launch_gemv_level_pro(const igl_code_view *v, float step, float leave,
                                      const igl_gemv_prologue *pro, float *x_out, float *out, int N,
                                      int K, int epi, const float *epi_in, hipStream_t stream);
+/* The gate and up planes of one lane in one launch, out = gelu(gate) * up
+ * (each product on its own leave grid), the residual update as the prologue:
+ * both planes the same kind (bits, bias, flip, gain layout), N rows and enter
+ * step; K <= 2048. */
+hipError_t igl_launch_gemv_level_pair(const igl_code_view *gate, const igl_code_view *up, float step,
+                                      float leave_gate, float leave_up, const igl_gemv_prologue *pro,
+                                      float *out, int N, int K, hipStream_t stream);
 hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_t *const *codes,
                                  const long long *row_stride, const float *const *gains,
                                  const int *gain_stride, const int *rows, float *const *out,

@@ -1,6 +1,8 @@
 """GPU parity of the backend table's elementwise entries (norm_rms, soft_max,
 gelu_gate, rope_turn) through the table itself, against the oracle.
 Bar: 1e-5 relative to the vector's scale (1e-6 for softmax probabilities)."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -245,3 +247,85 @@ def test_plane_lift_level_nan_lane(backend):
     dev_act.free()
     out.free()
     backend.detach(cp)
+
+
+class _CodeView(ctypes.Structure):
+    _fields_ = [("codes", ctypes.c_void_p), ("row_stride", ctypes.c_longlong), ("gains", ctypes.c_void_p),
+                ("gain_stride", ctypes.c_int), ("group_shift", ctypes.c_int), ("bit_count", ctypes.c_int),
+                ("code_bias", ctypes.c_int), ("code_flip", ctypes.c_int)]
+
+
+class _Prologue(ctypes.Structure):
+    _fields_ = [("state_in", ctypes.c_void_p), ("state_out", ctypes.c_void_p), ("lift", ctypes.c_void_p),
+                ("lift_gain", ctypes.c_void_p), ("scale", ctypes.c_float), ("apply_scale", ctypes.c_int),
+                ("norm_gain", ctypes.c_void_p), ("eps", ctypes.c_float)]
+
+
+@pytest.mark.parametrize("bits,N,K", [(2, 12288, 1536), (4, 6144, 1536), (2, 1001, 1536), (8, 513, 2048),
+                                      (4, 77, 1024)])
+def test_level_pair_equals_two_launches(backend, bits, N, K):
+    """The calibrated gate and up planes of one lane in one launch
+    (igl_launch_gemv_level_pair: the residual update as its prologue, both
+    row closes on their own leave grids, then gelu(gate) * up) equals, to the
+    bit, the two launches it replaces: the gate plane with the prologue
+    (igl_launch_gemv_level_pro, x kept) and the up plane with gelu(gate) * up
+    fused in its store (igl_launch_gemv_level_epi); and both leave the same
+    updated state."""
+    print("case level pair bits=%d N=%d K=%d" % (bits, N, K), flush=True)
+    lib = backend.lib
+    for name, args in (("igl_launch_gemv_level_pro",
+                        [ctypes.c_void_p, ctypes.c_float, ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p,
+                         ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                         ctypes.c_void_p]),
+                       ("igl_launch_gemv_level_epi",
+                        [ctypes.c_void_p, ctypes.c_float, ctypes.c_float, ctypes.c_void_p, ctypes.c_int,
+                         ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                         ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]),
+                       ("igl_launch_gemv_level_pair",
+                        [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p])):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = args
+    lib.igl_desk_stream.restype = ctypes.c_void_p
+    lib.igl_desk_stream.argtypes = [ctypes.c_void_p]
+    stream = lib.igl_desk_stream(ctypes.byref(backend.desk))
+    r = np.random.default_rng(bits * 1000 + N)
+    row_bytes = K * bits // 8
+    bufs = []
+
+    def up_load(a):
+        b = backend.upload(np.ascontiguousarray(a))
+        bufs.append(b)
+        return b
+
+    planes = []
+    for _ in range(2):
+        codes = up_load(r.integers(0, 256, size=(N, row_bytes), dtype=np.uint8))
+        gains = up_load(np.abs(r.normal(0, 0.02, size=N)).astype(np.float32))
+        planes.append(_CodeView(codes.ptr, row_bytes, gains.ptr, 1, 31, bits, 1 << (bits - 1),
+                                128 if bits == 8 else 0))
+    state = up_load(r.normal(size=K).astype(np.float32))
+    lift = up_load(r.normal(size=K).astype(np.float32))
+    lift_gain = up_load(r.normal(1.0, 0.1, size=K).astype(np.float32))
+    norm_gain = up_load(r.normal(1.0, 0.1, size=K).astype(np.float32))
+    s_two, s_pair = backend.alloc(K * 4), backend.alloc(K * 4)
+    scrap, y_two, y_pair = backend.alloc(K * 4), backend.alloc(N * 4), backend.alloc(N * 4)
+    bufs += [s_two, s_pair, scrap, y_two, y_pair]
+    step, leave_g, leave_u = float(np.float32(0.04)), float(np.float32(0.03)), float(np.float32(0.05))
+    pro_two = _Prologue(state.ptr, s_two.ptr, lift.ptr, lift_gain.ptr, 1.0, 0, norm_gain.ptr, 1e-6)
+    pro_pair = _Prologue(state.ptr, s_pair.ptr, lift.ptr, lift_gain.ptr, 1.0, 0, norm_gain.ptr, 1e-6)
+    g, u = planes
+    assert lib.igl_launch_gemv_level_pro(ctypes.byref(g), step, leave_g, ctypes.byref(pro_two), scrap.ptr,
+                                         y_two.ptr, N, K, 0, None, stream) == 0
+    assert lib.igl_launch_gemv_level_epi(ctypes.byref(u), step, leave_u, scrap.ptr, K, 1, y_two.ptr, N, N, K,
+                                         1, y_two.ptr, N, stream) == 0
+    assert lib.igl_launch_gemv_level_pair(ctypes.byref(g), ctypes.byref(u), step, leave_g, leave_u,
+                                          ctypes.byref(pro_pair), y_pair.ptr, N, K, stream) == 0
+    backend.sync()
+    want, got = y_two.get(np.float32, N), y_pair.get(np.float32, N)
+    assert np.all(np.isfinite(want)) and np.any(want != 0)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(s_pair.get(np.float32, K).view(np.uint32), s_two.get(np.float32, K).view(np.uint32))
+    for b in bufs:
+        b.free()
