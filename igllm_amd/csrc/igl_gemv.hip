@@ -2587,7 +2587,9 @@ extern "C" hipError_t igl_launch_gemv_level_pro(const igl_code_view *v, float st
   return igl_level_launch(a, v, step, leave, nullptr, K, 1, out, N, N, K, epi, epi_in, 0, stream);
 }
 
-// Rows a sub-wave of a pair launch (half of them the gate plane's).
+// Rows a sub-wave of a pair launch (half of them the gate plane's): the
+// export-kinds decode measured 1.54 ms a token with four, 1.57 with two and
+// 1.59-1.60 with eight.
 constexpr int kLevelPairRows = 4;
 
 template <int BITS>
