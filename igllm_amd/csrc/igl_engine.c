@@ -732,6 +732,28 @@ static int project_level_pair(igl_engine *e, const igl_plane *g, const igl_plane
   return IGL_OKAY;
 }
 
+/* Planes that one segments launch takes with p: calibrated one-lane prologue
+ * planes of p's kind and enter step. */
+static int level_same_kind(const igl_engine *e, const igl_plane *p, const igl_plane *u) {
+  return level_pro_fits(e, u) && p->bit_count == u->bit_count && p->code_bias == u->code_bias &&
+         p->code_flip == u->code_flip && p->group_count == u->group_count && p->enter_gain == u->enter_gain;
+}
+
+static int project_level_segments(igl_engine *e, const igl_plane *const *p, int count, float *const *out,
+                                  const igl_gemv_prologue *pro) {
+  igl_code_view v[3];
+  int rows[3];
+  float leave[3];
+  for (int i = 0; i < count; ++i) {
+    v[i] = igl_plane_view(p[i], dev_codes(e, p[i]), dev_gains(e, p[i]));
+    rows[i] = p[i]->row_count;
+    leave[i] = p[i]->leave_gain;
+  }
+  RUN(igl_launch_gemv_level_segments(v, count, rows, out, leave, p[0]->enter_gain, pro, p[0]->col_count,
+                                     e->stream));
+  return IGL_OKAY;
+}
+
 static int norm_rows(igl_engine *e, const float *in, const float *gain, int n, int lanes, int stride,
                      float *out) {
   return igl_norm_rms_dev(e->desk, in, gain, n, lanes, stride, e->eps, out);
@@ -854,6 +876,16 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
     igl_gemv_prologue pro = state_update(e, e->lift, e->pending_gain, e->pending_scale, L->enter_norm);
     e->pending = 0;
     OKAY(group_run(e, &gq, &L->q, IGL_GEMV_SEGMENTS, NULL, NULL, &pro));
+    state_flip(e);
+  } else if (lanes == 1 && e->pending && level_pro_fits(e, &L->q) && !L->shared &&
+             level_same_kind(e, &L->q, &L->k) && level_same_kind(e, &L->q, &L->v)) {
+    /* calibrated query, key and value planes in one launch, the update as its
+     * prologue */
+    const igl_plane *qkv[3] = {&L->q, &L->k, &L->v};
+    float *outs[3] = {e->q, e->k, e->v};
+    igl_gemv_prologue pro = state_update(e, e->lift, e->pending_gain, e->pending_scale, L->enter_norm);
+    e->pending = 0;
+    OKAY(project_level_segments(e, qkv, 3, outs, &pro));
     state_flip(e);
   } else if (lanes == 1 && e->pending && level_pro_fits(e, &L->q)) {
     /* a calibrated query plane takes the update in its prologue and leaves

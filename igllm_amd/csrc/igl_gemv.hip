@@ -848,14 +848,28 @@ struct GemvLevelArgs {
   float eps;
   int pro_vec;            // the K-vectors, state_out and x_out 16-byte aligned
   float *x_out;
-  // PAIR (one lane): the up projection beside the gate one (`codes`, `gains`,
-  // `leave`), the same kind, rows and enter step; out = gelu(gate) * up
+  // FUSE (one lane, the same kind and enter step):
+  //   kLevelPair: the up projection (`*2`) beside the gate one, the same
+  //     rows; out = gelu(gate) * up;
+  //   kLevelSegments: the rows of up to three planes one after the other,
+  //     plane 2 from row first2, plane 3 from row first3 (N in all), each
+  //     on its own leave grid into its own output
   const uint8_t *codes2;
   long long row_stride2;
   const float *gains2;
   int gain_stride2;
   float leave2;
+  float *out2;
+  const uint8_t *codes3;
+  long long row_stride3;
+  const float *gains3;
+  int gain_stride3;
+  float leave3;
+  float *out3;
+  int first2, first3;
 };
+
+enum { kLevelOne = 0, kLevelPair = 1, kLevelSegments = 2 };
 
 __host__ __device__ constexpr size_t gemv_level_lds_bytes(int M, int units) {
   return (size_t)M * units * (kLevelPitch * 16 + 8);
@@ -982,10 +996,13 @@ __device__ __forceinline__ void level_prologue(const GemvLevelArgs &a, const Pro
 }
 
 // PRO: one lane whose x is formed by the prologue above (M == 1).
-template <int BITS, int M, int R, int UPL, int GPT, bool PRO = false, bool PAIR = false>
+template <int BITS, int M, int R, int UPL, int GPT, bool PRO = false, int FUSE = kLevelOne>
 __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs a) {
   static_assert(!PRO || M == 1, "the prologue forms one lane");
+  constexpr bool PAIR = FUSE == kLevelPair;
+  constexpr bool SEG = FUSE == kLevelSegments;
   static_assert(!PAIR || (M == 1 && R % 2 == 0), "a pair: one lane, rows of both planes");
+  static_assert(!SEG || M == 1, "segments: one lane");
   // rows of one plane a sub-wave: a pair's tile holds RP gate rows, then the
   // same RP rows of the up plane
   constexpr int RP = PAIR ? R / 2 : R;
@@ -1047,9 +1064,15 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const bool up = PAIR && r >= RP;
-        const int row = min(row0 + r % RP, a.N - 1);
+        int row = min(row0 + r % RP, a.N - 1);
         const float *gp = up ? a.gains2 : a.gains;
-        const int gs = up ? a.gain_stride2 : a.gain_stride;
+        int gs = up ? a.gain_stride2 : a.gain_stride;
+        if constexpr (SEG) {
+          const int sg = row >= a.first3 ? 2 : row >= a.first2 ? 1 : 0;
+          row -= sg == 2 ? a.first3 : sg == 1 ? a.first2 : 0;
+          gp = sg == 2 ? a.gains3 : sg == 1 ? a.gains2 : a.gains;
+          gs = sg == 2 ? a.gain_stride3 : sg == 1 ? a.gain_stride2 : a.gain_stride;
+        }
         const float g = gp[(size_t)row * (size_t)gs + ((unsigned)u >> a.group_shift)];
         s[j][r][h] = in && u_raw < units && row0 + r % RP < a.N ? g : 0.0f;
       }
@@ -1061,9 +1084,15 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const bool up = PAIR && r >= RP;
-      const int row = min(row0 + r % RP, a.N - 1);
+      int row = min(row0 + r % RP, a.N - 1);
       const uint8_t *cp = up ? a.codes2 : a.codes;
-      const long long rs = up ? a.row_stride2 : a.row_stride;
+      long long rs = up ? a.row_stride2 : a.row_stride;
+      if constexpr (SEG) {
+        const int sg = row >= a.first3 ? 2 : row >= a.first2 ? 1 : 0;
+        row -= sg == 2 ? a.first3 : sg == 1 ? a.first2 : 0;
+        cp = sg == 2 ? a.codes3 : sg == 1 ? a.codes2 : a.codes;
+        rs = sg == 2 ? a.row_stride3 : sg == 1 ? a.row_stride2 : a.row_stride;
+      }
       w[j][r] = __builtin_nontemporal_load(reinterpret_cast<const uint4_t *>(cp + (size_t)row * (size_t)rs) + sl);
     }
   }
@@ -1163,18 +1192,30 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_level_kernel(GemvLevelArgs 
   // reference's, fl(fl(gain step) fl(part)), NaN for a lane that held one,
   // the leave grid, then the fused elementwise step.
   auto close = [&](int r, int m, int it, float ft, int b) {
-    const int row = row0 + r;
+    int row = row0 + r;
     if (row >= a.N || m >= a.lanes) return;
-    float y = one_group ? a.gains[(size_t)row * (size_t)a.gain_stride] * a.step * (float)it : ft;
+    const float *gp = a.gains;
+    int gs = a.gain_stride;
+    float leave = a.leave;
+    float *out = a.out;
+    if constexpr (SEG) {
+      const int sg = row >= a.first3 ? 2 : row >= a.first2 ? 1 : 0;
+      row -= sg == 2 ? a.first3 : sg == 1 ? a.first2 : 0;
+      gp = sg == 2 ? a.gains3 : sg == 1 ? a.gains2 : a.gains;
+      gs = sg == 2 ? a.gain_stride3 : sg == 1 ? a.gain_stride2 : a.gain_stride;
+      leave = sg == 2 ? a.leave3 : sg == 1 ? a.leave2 : a.leave;
+      out = sg == 2 ? a.out3 : sg == 1 ? a.out2 : a.out;
+    }
+    float y = one_group ? gp[(size_t)row * (size_t)gs] * a.step * (float)it : ft;
     if (b) y = __builtin_nanf("");
-    y = grid_value(y, a.leave);
+    y = grid_value(y, leave);
     // the reference's next step on this output (kern_gelu_gate): with the gate
     // projection's output, gelu(gate) * y; with the per-layer input, gelu(y) * it
     if (a.epi == IGL_LEVEL_EPI_GELU_RISE)
       y = gelu_near(a.epi_in[(size_t)m * a.epi_stride + row]) * y;
     else if (a.epi == IGL_LEVEL_EPI_GELU_MUL)
       y = gelu_near(y) * a.epi_in[(size_t)m * a.epi_stride + row];
-    a.out[(size_t)m * a.out_stride + row] = y;
+    out[(size_t)m * a.out_stride + row] = y;
   };
   // A pair's output (row r of the sub-wave's RP, the one lane): both row
   // closes on their own leave grids, then kern_gelu_gate's gelu(gate) * up.
@@ -2594,9 +2635,107 @@ constexpr int kLevelPairRows = 4;
 
 template <int BITS>
 static hipError_t gemv_level_pair_launch(const GemvLevelArgs &a, dim3 grid, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((gemv_level_kernel<BITS, 1, kLevelPairRows, 1, 1, true, true>), grid, dim3(kGemvThreads), lds,
+  hipLaunchKernelGGL((gemv_level_kernel<BITS, 1, kLevelPairRows, 1, 1, true, kLevelPair>), grid, dim3(kGemvThreads),
+                     lds, stream, a);
+  return hipGetLastError();
+}
+
+template <int BITS>
+static hipError_t gemv_level_segments_launch(const GemvLevelArgs &a, dim3 grid, size_t lds, hipStream_t stream) {
+  hipLaunchKernelGGL((gemv_level_kernel<BITS, 1, 2, 1, 1, true, kLevelSegments>), grid, dim3(kGemvThreads), lds,
                      stream, a);
   return hipGetLastError();
+}
+
+// The residual update's prologue and its fields, shared by the fused level entries.
+static void level_prologue_args(GemvLevelArgs &a, const igl_gemv_prologue *pro) {
+  a.state_in = pro->state_in;
+  a.state_out = pro->state_out;
+  a.lift = pro->lift;
+  a.lift_gain = pro->lift_gain;
+  a.scale = pro->scale;
+  a.apply_scale = pro->apply_scale;
+  a.norm_gain = pro->norm_gain;
+  a.eps = pro->eps;
+  a.x_out = nullptr;
+  a.pro_vec = ((((uintptr_t)a.state_in) | (uintptr_t)(a.lift ? a.lift : a.state_in) |
+                (uintptr_t)(a.lift_gain ? a.lift_gain : a.state_in) |
+                (uintptr_t)(a.norm_gain ? a.norm_gain : a.state_in) |
+                (uintptr_t)(a.state_out ? a.state_out : a.state_in)) & 15u) == 0;
+}
+
+// Up to three calibrated planes of one lane that read the same input (a
+// layer's q, k and v) in one launch, the residual update as the prologue:
+// every plane the same kind and enter step, K <= 2048; plane s's rows into
+// out[s] on its own leave grid.
+extern "C" hipError_t igl_launch_gemv_level_segments(const igl_code_view *v, int segments, const int *rows,
+                                                     float *const *out, const float *leave, float step,
+                                                     const igl_gemv_prologue *pro, int K, hipStream_t stream) {
+  if (!v || segments < 1 || segments > 3 || !rows || !out || !leave || !pro || !pro->state_in || K > 2048 ||
+      !(step > 0.0f) || (pro->lift && (!pro->lift_gain || !pro->state_out)) || pro->state_out == pro->state_in)
+    return hipErrorInvalidValue;
+  const int bits = v[0].bit_count;
+  if (!igl_gemv_level_fits(bits, K)) return hipErrorInvalidValue;
+  int total = 0;
+  for (int i = 0; i < segments; ++i) {
+    if (rows[i] < 1 || !out[i] || v[i].bit_count != bits || v[i].code_bias != v[0].code_bias ||
+        v[i].code_flip != v[0].code_flip || v[i].group_shift != v[0].group_shift)
+      return hipErrorInvalidValue;
+    total += rows[i];
+  }
+  GemvLevelArgs a{};
+  level_prologue_args(a, pro);
+  const int last = segments - 1;
+  a.codes = v[0].codes;
+  a.row_stride = v[0].row_stride;
+  a.gains = v[0].gains;
+  a.gain_stride = v[0].gain_stride;
+  a.leave = leave[0];
+  a.out = out[0];
+  a.codes2 = v[min(1, last)].codes;
+  a.row_stride2 = v[min(1, last)].row_stride;
+  a.gains2 = v[min(1, last)].gains;
+  a.gain_stride2 = v[min(1, last)].gain_stride;
+  a.leave2 = leave[min(1, last)];
+  a.out2 = out[min(1, last)];
+  a.codes3 = v[last].codes;
+  a.row_stride3 = v[last].row_stride;
+  a.gains3 = v[last].gains;
+  a.gain_stride3 = v[last].gain_stride;
+  a.leave3 = leave[last];
+  a.out3 = out[last];
+  // planes past `segments` start past the last row
+  a.first2 = segments > 1 ? rows[0] : total;
+  a.first3 = segments > 2 ? rows[0] + rows[1] : total;
+  a.group_shift = v[0].group_shift;
+  a.act = nullptr;
+  a.act_stride = K;
+  a.out_stride = 0;
+  a.lanes = 1;
+  a.N = total;
+  a.K = K;
+  a.code_bias = v[0].code_bias;
+  a.step = step;
+  a.epi = IGL_LEVEL_EPI_NONE;
+  const uint32_t field = bits == 8 ? (uint32_t)((v[0].code_flip ^ v[0].code_bias) & 255)
+                                   : (uint32_t)(v[0].code_flip & ((1 << bits) - 1));
+  a.code_xor = field * (bits == 2 ? 0x55555555u : bits == 4 ? 0x11111111u : 0x01010101u);
+  const int slots = (K * bits + 127) / 128;
+  if (slots > 4 * kWave) return hipErrorInvalidValue;
+  const int subs_log = slots <= 16 ? 2 : slots <= 32 ? 1 : 0;
+  const int tiles = (total + (2 << subs_log) - 1) / (2 << subs_log);
+  int ksplit = 1;
+  while (subs_log == 0 && ksplit < 4 &&
+         (slots > ksplit * kWave || (tiles * ksplit < 2048 && slots / (ksplit * 2) >= 32)))
+    ksplit *= 2;
+  a.ks_log = ksplit == 1 ? 0 : ksplit == 2 ? 1 : 2;
+  a.subs_log = subs_log;
+  const int per_block = 4 / ksplit;
+  const dim3 grid((tiles + per_block - 1) / per_block);
+  const size_t lds = gemv_level_lds_bytes(1, K / 32);
+  return bits == 2   ? gemv_level_segments_launch<2>(a, grid, lds, stream)
+         : bits == 4 ? gemv_level_segments_launch<4>(a, grid, lds, stream)
+                     : gemv_level_segments_launch<8>(a, grid, lds, stream);
 }
 
 // The gate and up projections of one lane in one launch (kern_gelu_gate's
@@ -2612,19 +2751,7 @@ extern "C" hipError_t igl_launch_gemv_level_pair(const igl_code_view *gate, cons
       (pro->lift && (!pro->lift_gain || !pro->state_out)) || pro->state_out == pro->state_in)
     return hipErrorInvalidValue;
   GemvLevelArgs a{};
-  a.state_in = pro->state_in;
-  a.state_out = pro->state_out;
-  a.lift = pro->lift;
-  a.lift_gain = pro->lift_gain;
-  a.scale = pro->scale;
-  a.apply_scale = pro->apply_scale;
-  a.norm_gain = pro->norm_gain;
-  a.eps = pro->eps;
-  a.x_out = nullptr;
-  a.pro_vec = ((((uintptr_t)a.state_in) | (uintptr_t)(a.lift ? a.lift : a.state_in) |
-                (uintptr_t)(a.lift_gain ? a.lift_gain : a.state_in) |
-                (uintptr_t)(a.norm_gain ? a.norm_gain : a.state_in) |
-                (uintptr_t)(a.state_out ? a.state_out : a.state_in)) & 15u) == 0;
+  level_prologue_args(a, pro);
   a.codes = gate->codes;
   a.row_stride = gate->row_stride;
   a.gains = gate->gains;

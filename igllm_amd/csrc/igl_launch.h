@@ -106,6 +106,13 @@ hipError_t igl_launch_gemv_level_pro(const igl_code_view *v, float step, float l
 hipError_t igl_launch_gemv_level_pair(const igl_code_view *gate, const igl_code_view *up, float step,
                                       float leave_gate, float leave_up, const igl_gemv_prologue *pro,
                                       float *out, int N, int K, hipStream_t stream);
+/* Up to three calibrated planes of one lane that read the same input (a
+ * layer's q, k and v) in one launch, the residual update as the prologue:
+ * every plane the same kind and enter step, K <= 2048; plane s's rows[s]
+ * outputs into out[s], on its own leave grid leave[s]. */
+hipError_t igl_launch_gemv_level_segments(const igl_code_view *v, int segments, const int *rows,
+                                          float *const *out, const float *leave, float step,
+                                          const igl_gemv_prologue *pro, int K, hipStream_t stream);
 hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_t *const *codes,
                                  const long long *row_stride, const float *const *gains,
                                  const int *gain_stride, const int *rows, float *const *out,

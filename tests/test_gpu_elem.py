@@ -329,3 +329,79 @@ def test_level_pair_equals_two_launches(backend, bits, N, K):
     assert np.array_equal(s_pair.get(np.float32, K).view(np.uint32), s_two.get(np.float32, K).view(np.uint32))
     for b in bufs:
         b.free()
+
+
+@pytest.mark.parametrize("bits,rows,K", [(4, (2048, 256, 256), 1536), (4, (2048, 512, 512), 1536),
+                                         (2, (1001, 131, 130), 1536), (8, (256, 77), 2048), (4, (300,), 1024)])
+def test_level_segments_equal_separate_launches(backend, bits, rows, K):
+    """Up to three calibrated planes of one lane that read the same input (a
+    layer's q, k and v; igl_launch_gemv_level_segments: the residual update as
+    the prologue, each plane's rows on its own leave grid into its own output)
+    equal, to the bit, the launches they replace: the first plane with the
+    prologue (igl_launch_gemv_level_pro, x kept) and the others reading the
+    kept x (igl_launch_gemv_level_epi); odd row counts put plane boundaries
+    inside a row tile."""
+    print("case level segments bits=%d rows=%s K=%d" % (bits, rows, K), flush=True)
+    lib = backend.lib
+    for name, args in (("igl_launch_gemv_level_pro",
+                        [ctypes.c_void_p, ctypes.c_float, ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p,
+                         ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                         ctypes.c_void_p]),
+                       ("igl_launch_gemv_level_epi",
+                        [ctypes.c_void_p, ctypes.c_float, ctypes.c_float, ctypes.c_void_p, ctypes.c_int,
+                         ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                         ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]),
+                       ("igl_launch_gemv_level_segments",
+                        [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                         ctypes.c_float, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p])):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = args
+    lib.igl_desk_stream.restype = ctypes.c_void_p
+    lib.igl_desk_stream.argtypes = [ctypes.c_void_p]
+    stream = lib.igl_desk_stream(ctypes.byref(backend.desk))
+    r = np.random.default_rng(bits * 1000 + sum(rows))
+    row_bytes = K * bits // 8
+    bufs = []
+
+    def up_load(a):
+        b = backend.upload(np.ascontiguousarray(a))
+        bufs.append(b)
+        return b
+
+    n = len(rows)
+    views = (_CodeView * 3)()
+    for i, N in enumerate(rows):
+        codes = up_load(r.integers(0, 256, size=(N, row_bytes), dtype=np.uint8))
+        gains = up_load(np.abs(r.normal(0, 0.02, size=N)).astype(np.float32))
+        views[i] = _CodeView(codes.ptr, row_bytes, gains.ptr, 1, 31, bits, 1 << (bits - 1), 128 if bits == 8 else 0)
+    state = up_load(r.normal(size=K).astype(np.float32))
+    lift = up_load(r.normal(size=K).astype(np.float32))
+    lift_gain = up_load(r.normal(1.0, 0.1, size=K).astype(np.float32))
+    norm_gain = up_load(r.normal(1.0, 0.1, size=K).astype(np.float32))
+    s_one, s_seg, scrap = backend.alloc(K * 4), backend.alloc(K * 4), backend.alloc(K * 4)
+    y_one = [backend.alloc(N * 4) for N in rows]
+    y_seg = [backend.alloc(N * 4) for N in rows]
+    bufs += [s_one, s_seg, scrap] + y_one + y_seg
+    step = float(np.float32(0.04))
+    leaves = [float(np.float32(v)) for v in (0.03, 0.05, 0.0)[:n]]
+    pro_one = _Prologue(state.ptr, s_one.ptr, lift.ptr, lift_gain.ptr, 1.0, 0, norm_gain.ptr, 1e-6)
+    pro_seg = _Prologue(state.ptr, s_seg.ptr, lift.ptr, lift_gain.ptr, 1.0, 0, norm_gain.ptr, 1e-6)
+    assert lib.igl_launch_gemv_level_pro(ctypes.byref(views[0]), step, leaves[0], ctypes.byref(pro_one), scrap.ptr,
+                                         y_one[0].ptr, rows[0], K, 0, None, stream) == 0
+    for i in range(1, n):
+        assert lib.igl_launch_gemv_level_epi(ctypes.byref(views[i]), step, leaves[i], scrap.ptr, K, 1, y_one[i].ptr,
+                                             rows[i], rows[i], K, 0, None, 0, stream) == 0
+    rows_c = (ctypes.c_int * 3)(*rows)
+    outs_c = (ctypes.c_void_p * 3)(*[b.ptr for b in y_seg])
+    leave_c = (ctypes.c_float * 3)(*leaves)
+    assert lib.igl_launch_gemv_level_segments(views, n, rows_c, outs_c, leave_c, step, ctypes.byref(pro_seg), K,
+                                              stream) == 0
+    backend.sync()
+    for i, N in enumerate(rows):
+        want, got = y_one[i].get(np.float32, N), y_seg[i].get(np.float32, N)
+        assert np.all(np.isfinite(want)) and np.any(want != 0)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"plane {i}"
+    assert np.array_equal(s_seg.get(np.float32, K).view(np.uint32), s_one.get(np.float32, K).view(np.uint32))
+    for b in bufs:
+        b.free()
