@@ -204,7 +204,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_kernel(GemvArgs a) {
     const int r = lane / M;
     const int m = lane - r * M;
     float total = 0.0f;
-    for (int k = 0; k < a.ksplit; ++k) total += red[((wave + k) * R + r) * M + m];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k < a.ksplit) total += red[((wave + k) * R + r) * M + m];
     if (row0 + r < a.N) dst[(size_t)m * a.out_stride + row0 + r] = total;
   }
 }
@@ -350,7 +352,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_reg_kernel(GemvArgs a) {
     const int r = lane / M;
     const int m = lane - r * M;
     float total = 0.0f;
-    for (int k = 0; k < a.ksplit; ++k) total += red[wave + k][r][m];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k < a.ksplit) total += red[wave + k][r][m];
     if (row0 + r < a.N) a.out[(size_t)m * a.out_stride + row0 + r] = total;
   }
 }
@@ -513,7 +517,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
     const int r = lane / M;
     const int m = lane - r * M;
     float total = 0.0f;
-    for (int k = 0; k < (1 << ks_log); ++k) total += red[wave + k][r][m];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k < (1 << ks_log)) total += red[wave + k][r][m];
     if (row0 + r < a.N) a.out[(size_t)m * a.out_stride + row0 + r] = total;
   }
 }
@@ -787,7 +793,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_code_dot_kernel(GemvCodeArg
         const int r = lane / M;
         const int m = lane - r * M;
         float total = 0.0f;
-        for (int k = 0; k < (1 << ks_log); ++k) total += red[wave + k][r][m];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (k < (1 << ks_log)) total += red[wave + k][r][m];
         if (row0 + r < a.N && m < a.lanes) dst[(size_t)m * a.out_stride + row0 + r] = total;
       }
     }
