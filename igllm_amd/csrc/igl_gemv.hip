@@ -2837,7 +2837,7 @@ static hipError_t igl_level_launch(GemvLevelArgs a, const igl_code_view *v, floa
     const int l = lanes - done < most ? lanes - done : most;
     const int M = l <= 2 ? l : 4;
     const int slots = (K * bits + 127) / 128;
-    const int upl = slots > 4 * kWave ? 2 : 1;
+    int upl = slots > 4 * kWave ? 2 : 1;
     const int subs_log = upl == 1 && slots <= 16 ? 2 : upl == 1 && slots <= 32 ? 1 : 0;
     int rows_t = M == 1 ? 2 : 4;  // rows a sub-wave (the kernel's R)
     int tiles = (N + (rows_t << subs_log) - 1) / (rows_t << subs_log);
@@ -2854,6 +2854,15 @@ static hipError_t igl_level_launch(GemvLevelArgs a, const igl_code_view *v, floa
         (N + 5) / 6 <= 256) {
       rows_t = 6;
       tiles = (N + 5) / 6;
+    }
+    // One lane on a small plane (under 4096 rows, at most 128 slots; two
+    // slots a lane past 64, for the widths that have that form): one wave a
+    // two-row tile, no K split -- the integer-dot form's rule for the same
+    // shapes.
+    if (M == 1 && subs_log == 0 && !a.state_in && N < 4096 &&
+        (slots <= kWave || (bits >= 4 && slots <= 2 * kWave))) {
+      upl = slots > kWave ? 2 : 1;
+      ksplit = 1;
     }
     const int items = (M * (K >> 3) + kGemvThreads - 1) / kGemvThreads;
     const int gpt = items <= 1 ? 1 : items <= 2 ? 2 : items <= 4 ? 4 : 8;

@@ -124,6 +124,9 @@ LEVEL_KINDS = [
     # one lane on wide rows: six-row tiles, four waves a tile (the export-kinds
     # down projections, a ragged last tile, two slots a lane of 8-bit codes)
     (1536, 12288, 2, 0, 1), (1000, 6144, 4, 0, 1), (700, 6144, 8, 128, 1),
+    # one lane on small planes: one wave a two-row tile, no K split (two slots
+    # a lane for 8-bit codes at K 2048)
+    (1536, 2048, 4, 0, 1), (1000, 2048, 8, 128, 1), (257, 1536, 8, 128, 1),
     # from 64 lanes: the int8 MFMA GEMM (levels against codes as int8 operands)
     (2048, 1536, 4, 0, 64), (6144, 1536, 2, 0, 300), (256, 1536, 8, 128, 70), (1536, 256, 8, 128, 256),
     (1536, 6144, 2, 0, 100), (512, 2048, 4, 3, 64),
