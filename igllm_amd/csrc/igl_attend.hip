@@ -55,10 +55,11 @@ namespace igl {
 // Positions a chunk, by the longest span a launch covers: 32 up to
 // kAttendShortSpan (the most workgroups, the shortest chain each), 64 beyond
 // (half the partials: at 16384 positions 11.4 us against 13.0 us for 32).
-// Windowed spans of kAttendWideLanes lanes and more take 64 as well: a
+// Launches of kAttendWideLanes lanes and more take 64 whatever the span: a
 // prefill pass has workgroups enough, and half the partials to fold (the
-// 2047-lane fast prefill 46 700 -> 49 300 tok/s; one lane keeps 32: its
-// sliding window measured 6.8 against 7.3 us with 64).
+// 2047-lane fast prefill 46 700 -> 49 300 tok/s with it on windowed spans,
+// 52 400 with it on every span; one lane keeps 32: its sliding window
+// measured 6.8 against 7.3 us with 64).
 constexpr int kAttendShortSpan = 8192;
 constexpr int kAttendWideLanes = 64;
 constexpr int kAttendGroup = 8;                    // query heads per key/value head
@@ -683,7 +684,7 @@ static int attend_max_span(int place0, int window, int lanes) {
 }
 
 static int attend_chunk(int place0, int window, int lanes) {
-  if (window > 0 && lanes >= kAttendWideLanes) return 64;
+  if (lanes >= kAttendWideLanes) return 64;
   return attend_max_span(place0, window, lanes) <= kAttendShortSpan ? 32 : 64;
 }
 
@@ -896,7 +897,7 @@ extern "C" size_t igl_attend_work_floats(int place0, int window, int lanes, int 
 // count is not monotonic in the span: chunks are 32 positions up to
 // kAttendShortSpan and 64 beyond, so a span just under kAttendShortSpan has
 // more chunks than one just over it.  The largest count of each regime is
-// taken (windowed spans of many lanes take 64-position chunks: fewer).
+// taken (launches of many lanes take 64-position chunks: fewer).
 extern "C" size_t igl_attend_work_floats_limit(int span_limit, int lanes, int head_count,
                                                int head_size) {
   if (span_limit < 1 || lanes < 1) return 0;

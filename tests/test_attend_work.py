@@ -2,7 +2,7 @@
 
 The decode attention writes one partial per (lane, chunk, head).  Its chunk
 count is not monotonic in the span (32-position chunks up to 8192 positions,
-64-position chunks beyond, and for windowed spans of 64 lanes and more), so a
+64-position chunks beyond, and for every launch of 64 lanes and more), so a
 batch whose last position lands just under
 8192 needs more partials than a decode step at the last position of a longer
 window.  The engine sizes the buffer with igl_attend_work_floats_limit; this
