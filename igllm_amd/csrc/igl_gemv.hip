@@ -212,14 +212,25 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_kernel(GemvArgs a) {
 }
 
 // Sums the grid K-chunk partials in chunk order: out[m][n] = sum_c part[c][m][n].
+// Eight chunks' loads go out together, then their adds in order (chunks past
+// the count are skipped, not added as zeros): one memory round trip per eight
+// chunks instead of one per chunk.
 __global__ void gemv_chunk_sum_kernel(const float *part, int chunks, int M, int N, float *out,
                                       int out_stride) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= M * N) return;
   const int m = i / N;
   const int n = i - m * N;
+  const size_t step = (size_t)M * (size_t)N;  // part[c][m][n] = part[c * step + i]
   float total = 0.0f;
-  for (int c = 0; c < chunks; ++c) total += part[((size_t)c * M + m) * N + n];
+  for (int c0 = 0; c0 < chunks; c0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = c0 + j < chunks ? part[(size_t)(c0 + j) * step + i] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (c0 + j < chunks) total += v[j];
+  }
   out[(size_t)m * out_stride + n] = total;
 }
 
