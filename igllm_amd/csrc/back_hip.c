@@ -392,6 +392,8 @@ static int gemm_run(igl_desk *desk, const igl_plane *sheet, const void *act_dev,
   igl_desk_state *st = desk->state;
   const igl_device_plane *dp = sheet->device;
   const int align = act_bf16 ? 8 : 4;
+  /* bf16 activations are one exact binary16 term; fp32 ones two (hi + lo) */
+  const int terms = act_bf16 ? 1 : 2;
   int code;
   if ((code = check_lanes(sheet, act_dev, act_stride, lane_count, out_dev, out_stride)) != IGL_OKAY ||
       ((uintptr_t)act_dev & 15u) || (act_stride % align) ||
@@ -401,16 +403,16 @@ static int gemm_run(igl_desk *desk, const igl_plane *sheet, const void *act_dev,
     return code;
   }
   {
-    size_t bytes = igl_gemm_work_bytes(lane_count, sheet->row_count, sheet->col_count);
+    size_t bytes = igl_gemm_work_bytes(lane_count, sheet->row_count, sheet->col_count, terms);
     if (bytes && grow_dev(st, &st->gemm_dev, &st->gemm_floats, (bytes + 3) / 4) != IGL_OKAY)
       return IGL_FAIL_MEMORY;
   }
   return hip_check(st, igl_launch_gemm_q4(act_dev, act_bf16, act_stride, (const uint8_t *)dp->codes,
                                           (long long)sheet->row_stride, dp->gains,
                                           sheet->group_count, igl_plane_group_shift(sheet),
-                                          sheet->code_bias,
+                                          sheet->code_bias, NULL,
                                           out_dev, out_bf16, out_stride, lane_count,
-                                          sheet->row_count, sheet->col_count, st->gemm_dev,
+                                          sheet->row_count, sheet->col_count, terms, st->gemm_dev,
                                           NULL, st->stream));
 }
 
@@ -421,7 +423,8 @@ int igl_mat_mat_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev
   igl_desk_state *st = desk ? desk->state : NULL;
   int code;
   if (!st) return IGL_FAIL_STATE;
-  if (lane_count < IGL_GEMM_FLOOR || (sheet && !plane_is_q4(sheet)))
+  if (lane_count < IGL_GEMM_FLOOR || (sheet && !plane_is_q4(sheet)) ||
+      (sheet && !igl_gemm_fits(lane_count, sheet->row_count, sheet->col_count)))
     return igl_gemv_dev(desk, sheet, act_dev, act_stride, lane_count, out_dev, out_stride);
   if ((code = plane_supported(sheet)) != IGL_OKAY || !sheet->device) {
     code = code != IGL_OKAY ? code : IGL_FAIL_STATE;
@@ -441,7 +444,7 @@ int igl_gemm_bf16_dev(igl_desk *desk, const igl_plane *sheet, const uint16_t *ac
     desk_fail(st, code);
     return code;
   }
-  if (!plane_is_q4(sheet)) {
+  if (!plane_is_q4(sheet) || !igl_gemm_fits(lane_count, sheet->row_count, sheet->col_count)) {
     desk_fail(st, IGL_FAIL_SUPPORT);
     return IGL_FAIL_SUPPORT;
   }
@@ -493,11 +496,11 @@ static int lift_levels_gemm(igl_desk_state *st, const igl_plane *sheet, const fl
   const uint8_t *hi_plane = (const uint8_t *)sheet->device->codes;
   const uint8_t *lo_plane = NULL;
   long long row_stride = (long long)sheet->row_stride;
-  size_t work = igl_gemm_work_bytes(lanes, N, K);
+  size_t work = igl_gemm_work_bytes(lanes, N, K, 1);
   float *a_out = two ? NULL : out_dev;
   int a_stride = two ? N : out_stride;
   int code;
-  if (((two || !work) && grow_dev(st, &st->quant_dev, &st->quant_floats, (size_t)lanes * (size_t)K) != IGL_OKAY) ||
+  if ((two && grow_dev(st, &st->quant_dev, &st->quant_floats, (size_t)lanes * (size_t)K) != IGL_OKAY) ||
       (widen && grow_dev(st, &st->wide_dev, &st->wide_floats, (two ? 2 : 1) * plane_bytes / 4) != IGL_OKAY) ||
       (two && grow_dev(st, &st->lsum_dev, &st->lsum_floats, (size_t)lanes) != IGL_OKAY) ||
       (two && grow_dev(st, &st->prod_dev, &st->prod_floats, 2 * (size_t)lanes * (size_t)N) != IGL_OKAY) ||
@@ -520,26 +523,26 @@ static int lift_levels_gemm(igl_desk_state *st, const igl_plane *sheet, const fl
                                                     st->stream))) != IGL_OKAY)
       return code;
   }
-  if (!two && work) {
-    /* the large-tile form takes the levels and the row close in its own
-     * conversion and store */
+  if (!two) {
+    /* the GEMM takes the levels and the row close in its own conversion and
+     * store */
     const igl_gemm_close close = {sheet->device->gains, sheet->enter_gain, sheet->leave_gain};
     return hip_check(st, igl_launch_gemm_q4(act_dev, 0, act_stride, hi_plane, row_stride, st->ones_dev, 1, 31,
-                                            8, out_dev, 0, out_stride, lanes, N, K, st->gemm_dev, &close,
-                                            st->stream));
+                                            8, NULL, out_dev, 0, out_stride, lanes, N, K, 1, st->gemm_dev,
+                                            &close, st->stream));
   }
   if ((code = hip_check(st, igl_launch_quant_level(act_dev, act_stride, st->quant_dev, K, K, lanes,
                                                    sheet->enter_gain, two ? st->lsum_dev : NULL,
                                                    st->stream))) != IGL_OKAY)
     return code;
   if ((code = hip_check(st, igl_launch_gemm_q4(st->quant_dev, 0, K, hi_plane, row_stride, st->ones_dev, 1, 31,
-                                               8, a_out, 0, a_stride, lanes, N, K, st->gemm_dev, NULL,
-                                               st->stream))) != IGL_OKAY)
+                                               8, NULL, a_out, 0, a_stride, lanes, N, K, 1, st->gemm_dev,
+                                               NULL, st->stream))) != IGL_OKAY)
     return code;
   if (two &&
       (code = hip_check(st, igl_launch_gemm_q4(st->quant_dev, 0, K, lo_plane, row_stride, st->ones_dev, 1, 31,
-                                               8, st->prod_dev + (size_t)lanes * (size_t)N, 0, N, lanes,
-                                               N, K, st->gemm_dev, NULL, st->stream))) != IGL_OKAY)
+                                               8, NULL, st->prod_dev + (size_t)lanes * (size_t)N, 0, N, lanes,
+                                               N, K, 1, st->gemm_dev, NULL, st->stream))) != IGL_OKAY)
     return code;
   return hip_check(st, igl_launch_grid_close(a_out, two ? st->prod_dev + (size_t)lanes * (size_t)N : NULL,
                                              two ? st->lsum_dev : NULL, a_stride,
@@ -571,6 +574,8 @@ int igl_plane_lift_dev(igl_desk *desk, const igl_plane *sheet, const float *act_
   }
   if (sheet->enter_gain > 0.0f && sheet->form == IGL_PLANE_CODE && lane_count >= IGL_GEMM_FLOOR &&
       plane_supported(sheet) == IGL_OKAY && sheet->device && sheet->group_count == 1 &&
+      (igl_gemm_level_fits(sheet->bit_count, sheet->code_bias, sheet->col_count) ||
+       igl_gemm_fits(lane_count, sheet->row_count, sheet->col_count)) &&
       ((uintptr_t)act_dev & 15u) == 0 && (act_stride & 3) == 0)
     return lift_levels_gemm(st, sheet, act_dev, act_stride, lane_count, out_dev, out_stride);
   if (sheet->enter_gain > 0.0f) {

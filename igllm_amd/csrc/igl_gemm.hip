@@ -1,317 +1,204 @@
 // igl_gemm.hip - packed int4 projection for batched prefill (M >= 64 lanes),
-// gfx950 MFMA.
+// gfx950 MFMA, with the reference's float arithmetic.
 //
-// C[m][n] = sum_k A[m][k] * w[n][k],  w[n][k] = (c[n][k] - code_bias) * gain[n][k / group]
+// C[m][n] = sum_g gain[n][g] * sum_{k in g} x[m][k] * (c[n][k] - code_bias - zero[n][g])
 // with the codes read straight from the checkpoint's rows (two a byte, low
 // nibble first).  This is the reference's back_mat_mat (app_core.c:5247-5323)
-// for a lane count it would chunk by sixteen; the arithmetic is the same
-// product, evaluated as a dense contraction.
+// over kern_row_code / kern_row_code_many (3688-3706, 4075-4117) for a lane
+// count it would chunk by sixteen: a group's dot product, then its gain, in
+// fp32, group after group.
 //
-// Each workgroup owns a 128 x 128 tile of C and walks K in steps of 64 (two
-// 32-wide groups):
-//   * the int4 tile (128 rows x 32 bytes) is read with one 16-byte load a
-//     thread, dequantized in registers to binary16 (c - code_bias) * gain and
-//     written to LDS;
-//   * the activation tile (128 x 64) is read as bf16 or fp32, converted to
-//     binary16 and written to LDS;
-//   * four waves (2 x 2) each run a 64 x 64 block as 4 x 4
-//     v_mfma_f32_16x16x32_f16 tiles, fp32 accumulate.
-// binary16 rather than bf16 on both sides: a dequantized weight keeps eleven
-// significant bits instead of eight, and bf16 activations convert exactly to
-// binary16 over its normal range (|a| < 65504; larger values saturate).
+// Nothing on the way to the fp32 accumulators is rounded more coarsely than
+// the reference rounds:
+//   * the weight operand is c - bias - zero as an exact binary16 integer (one
+//     v_and_or_b32 puts a nibble in the mantissa of 1024.0, and subtracting
+//     1024 + bias + zero is exact); the gain is not folded into it;
+//   * the activations of a row are scaled by a power of two 2^t that puts the
+//     row's largest magnitude in [2^14, 2^15) and split into binary16 terms:
+//     a bf16 activation is exactly one term; an fp32 activation is hi + lo,
+//     24 bits but for the last rounding of lo (a relative 2^-22 at most);
+//   * one v_mfma_f32_16x16x32_f16 covers exactly one 32-code group, so its
+//     fp32 result is that group's dot product (every partial product exact),
+//     and one fp32 FMA adds gain * dot to the accumulator, as kern_row_code
+//     does;
+//   * the row's 2^-t is applied, exactly, at the store.
+// Planes with one gain a row accumulate all of K in the matrix cores and take
+// the gain once at the store (kern_row_code's single group).
+//
+// Tiling.  A workgroup of WN x WM x KS waves owns a TN x TM tile of C
+// (TN = 16 NB WN weight rows, TM = 16 MB WM lanes).  K advances through LDS
+// stages written only by the LDS DMA (global_load_lds: no registers hold loads
+// in flight); a stage holds KS consecutive 64-wide steps, and wave group ks of
+// the workgroup takes the ks-th: the K split happens inside the workgroup, and
+// the KS partial tiles are added in ks order through LDS at the end, so no
+// partial sums go to memory and the result does not depend on the tiling's
+// timing.  Small tile counts (few lanes, or few rows) take a deeper KS instead
+// of a K split across workgroups.
 #include "igl_device.h"
 #include "igl_launch.h"
 
 namespace igl {
 
-constexpr int kGemmBM = 128;
-constexpr int kGemmBN = 128;
-constexpr int kGemmBK = 64;
-constexpr int kGemmPitch = kGemmBK + 8;  // halves per LDS row (pad breaks bank aliasing)
-constexpr int kGemmThreads = 256;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
 
-struct GemmArgs {
-  const void *act;        // [M][act_stride] of bf16 (raw uint16) or fp32
-  int act_stride;
-  const uint8_t *codes;
-  long long row_stride;
-  const float *gains;
-  int gain_stride;
-  int group_shift;        // gain of unit u: u >> group_shift (31: one gain a row)
-  float code_bias;
-  void *out;              // [M][out_stride] of bf16 or fp32
-  int out_stride;
-  int M, N, K;
-};
+constexpr int kStepK = 64;  // k of one wave step: two 32-code groups
 
-__device__ __forceinline__ _Float16 sat_half(float v) {
-  v = fminf(fmaxf(v, -65504.0f), 65504.0f);
-  return (_Float16)v;
-}
-
-__device__ __forceinline__ float bf16_to_float(uint16_t raw) {
-  return __builtin_bit_cast(float, (uint32_t)raw << 16);
-}
-
-// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet): the conversion
-// instruction, two values at a time where a pair is stored together.
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+// Round-to-nearest-even fp32 -> bf16.
 __device__ __forceinline__ uint16_t float_to_bf16(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
-__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
-  bf16x2_t p;
-  p[0] = (__bf16)lo;
-  p[1] = (__bf16)hi;
-  return __builtin_bit_cast(uint32_t, p);
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
 }
 
-template <bool A_BF16, bool C_BF16>
-__global__ __launch_bounds__(kGemmThreads) void gemm_q4_kernel(GemmArgs g) {
-  __shared__ _Float16 As[kGemmBM * kGemmPitch];
-  __shared__ _Float16 Bs[kGemmBN * kGemmPitch];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1;  // wave row block (M)
-  const int wn = wave & 1;   // wave column block (N)
-  const int m0 = blockIdx.y * kGemmBM;
-  const int n0 = blockIdx.x * kGemmBN;
-
-  float4_t acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-  // Work assignment for the tile loads.
-  const int b_row = tid >> 1;        // 0..127: W row within the tile
-  const int b_half = tid & 1;        // which 32-code group of the 64-wide step
-  const int n_b = n0 + b_row;
-
-  for (int k0 = 0; k0 < g.K; k0 += kGemmBK) {
-    // ---- W tile: 16 bytes (one group of 32 codes) per thread.
-    {
-      const int kcol = k0 + b_half * 32;
-      _Float16 *dst = Bs + b_row * kGemmPitch + b_half * 32;
-      if (n_b < g.N && kcol < g.K) {
-        const uint4_t w = __builtin_nontemporal_load(reinterpret_cast<const uint4_t *>(
-            g.codes + (size_t)n_b * (size_t)g.row_stride + (size_t)(kcol >> 1)));
-        const float s = g.gains[(size_t)n_b * g.gain_stride + ((unsigned)(kcol >> 5) >> g.group_shift)];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          half8_t h;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float c = (float)((w[j] >> (4 * i)) & 15u);
-            h[i] = (_Float16)((c - g.code_bias) * s);
-          }
-          *reinterpret_cast<half8_t *>(dst + 8 * j) = h;
-        }
-      } else {
-        const half8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) *reinterpret_cast<half8_t *>(dst + 8 * j) = z;
-      }
-    }
-    // ---- A tile: 128 rows x 64 columns, 32 values per thread.
-    {
-      const int a_row = tid >> 1;
-      const int a_col = (tid & 1) * 32;
-      const int m = m0 + a_row;
-      _Float16 *dst = As + a_row * kGemmPitch + a_col;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        half8_t h;
-        const int kc = k0 + a_col + 8 * j;
-        if (m < g.M && kc < g.K) {
-          if (A_BF16) {
-            const uint4_t raw = *reinterpret_cast<const uint4_t *>(
-                reinterpret_cast<const uint16_t *>(g.act) + (size_t)m * g.act_stride + kc);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              h[2 * i] = sat_half(__builtin_bit_cast(float, raw[i] << 16));
-              h[2 * i + 1] = sat_half(__builtin_bit_cast(float, raw[i] & 0xFFFF0000u));
-            }
-          } else {
-            const float *src = reinterpret_cast<const float *>(g.act) + (size_t)m * g.act_stride + kc;
-            const float4_t lo = *reinterpret_cast<const float4_t *>(src);
-            const float4_t hi = *reinterpret_cast<const float4_t *>(src + 4);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              h[i] = sat_half(lo[i]);
-              h[4 + i] = sat_half(hi[i]);
-            }
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) h[i] = (_Float16)0.0f;
-        }
-        *reinterpret_cast<half8_t *>(dst + 8 * j) = h;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < kGemmBK; kk += 32) {
-      const int koff = kk + 8 * (lane >> 4);
-      half8_t af[4], bf[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const half8_t *>(As + (wm * 64 + i * 16 + (lane & 15)) * kGemmPitch + koff);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bf[j] = *reinterpret_cast<const half8_t *>(Bs + (wn * 64 + j * 16 + (lane & 15)) * kGemmPitch + koff);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    __syncthreads();
-  }
-
-  // D layout of a 16x16 tile: lane l holds rows 4*(l/16) + r, column l % 16.
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + wn * 64 + j * 16 + (lane & 15);
-      if (n >= g.N) continue;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
-        if (m >= g.M) continue;
-        if (C_BF16)
-          reinterpret_cast<uint16_t *>(g.out)[(size_t)m * g.out_stride + n] = float_to_bf16(acc[i][j][r]);
-        else
-          reinterpret_cast<float *>(g.out)[(size_t)m * g.out_stride + n] = acc[i][j][r];
-      }
-    }
-}
-
-// ---- the large-tile form ---------------------------------------------------
+// ---- activations -----------------------------------------------------------
 //
-// For M and N of 256 and up, K a multiple of 64.  The activations are first
-// converted once to a binary16 copy (act_half_kernel) in the operand order
-// the weights are decoded in (below), so the tile loop only moves them.
-//
-// A workgroup owns a 256 x 256 tile of C; its eight waves (2 x 4) each hold a
-// 128 x 64 block as 8 x 4 v_mfma_f32_16x16x32_f16 accumulators.  K advances
-// 64 a step through LDS stages that only the LDS DMA writes (global_load_lds:
-// no registers held for loads in flight):
-//   * three stages of the step's 256 x 64 binary16 activations (two steps
-//     ahead), 16-byte chunks of a row XOR-swizzled by bits 1..3 of the row
-//     (no padding; the 16 rows of a read land in 16 distinct 16-byte slots
-//     of the 64 banks.  Measured alone, these reads count the conflict
-//     counter's floor of four cycles per 64-lane 16-byte read, as the row's
-//     low three bits do; unswizzled, three times that);
-//   * four stages (three steps ahead) of the 256 rows' 64 codes as they are
-//     packed (32 bytes a row) and their two fp32 gains.
-// A wave turns its 64 columns' codes into binary16 operands in registers as
-// it consumes them: one v_and_or_b32 puts a nibble in the mantissa of 1024.0
-// (ulp 1: 1024 + c) or, four bits up, of 1024.0 with ulp 16 (1024 + 16 c), so
-// a dword of eight codes takes one shift; subtracting 1024 + bias (or
-// 1024 + 16 bias) is exact, and one multiply by the gain rounded to binary16
-// gives (c - bias) gain or 16 (c - bias) gain, rounded once.  The activation
-// copy holds x / 16 where the weight holds 16 (c - bias) gain, and each eight
-// consecutive k appear in the order 0 4 1 5 2 6 3 7 the pairs come in.
-// A wave's step runs 64 products in eight blocks of eight, reading the next
-// block's activations and decoding one of the next step's eight weight
-// operands beside each block.  The weights are the products' first operand,
-// so each accumulator holds C transposed: four consecutive columns of one row,
-// stored as one vector.
-//
-// Measured on this tile (M = 2048, 8192 x 2048): the same loop with only its
-// products (no decode, no activation reads, no DMA) takes ~70% of the whole
-// kernel, and the final 32 MB of output drains in ~15 us with every CU
-// finishing its one tile at once.
-constexpr int kBigM = 256;
-constexpr int kBigN = 256;
-constexpr int kBigK = 64;
-constexpr int kBigStages = 3;                 // activation stages (DMA two steps ahead)
-constexpr int kBigCodeStages = 4;             // code stages (decoded a step early)
-constexpr int kBigA = kBigM * kBigK;          // halves of a stage's activations
-constexpr int kBigB = kBigN * kBigK / 2;      // bytes of a stage's codes
-constexpr int kBigG = kBigN * kBigK / 32;     // floats of a stage's gains
-constexpr int kBigCodeStage = kBigB + kBigG * 4;
-constexpr int kBigLds = kBigStages * kBigA * 2 + kBigCodeStages * kBigCodeStage;
+// One workgroup a row: the row's largest magnitude fixes t, then every eight
+// consecutive k are written as binary16 operands in the order the weight
+// decoding produces them, positions 0 4 1 5 2 6 3 7, with k = 1, 5, 3, 7
+// (where the weight holds 16 (c - bias - zero)) divided by 16, in rows of Kp
+// (K padded with zeros to a whole number of steps).  hi =
+// binary16(x 2^t), lo = binary16(x 2^t - hi) (both of x 2^t / 16 at the
+// divided positions); inv[m] = 2^-t.
+// With level_step > 0 (a calibrated plane's prefill) each x is first its
+// quant_step level rint(x / level_step) clamped to [-128, 127] (quant_step,
+// app_core.c:1930-1940), an integer hi holds exactly.
+constexpr int kActThreads = 256;
 
-// a16 = binary16(a), saturating at +-65504, in the large-tile form's operand
-// order: within each eight k, positions 0 4 1 5 2 6 3 7, and k = 1, 5, 3, 7
-// divided by 16 (exact for every normal binary16).
-// With level_step > 0 (a calibrated plane's prefill), each x is first its
-// quant_step level rint(x / level_step) clamped to [-128, 127]: an integer the
-// binary16 operand holds exactly (and so does a level / 16).
-// Rows a thread of act_half_kernel converts (its loads all issued first).
-constexpr int kHalfRows = 4;
-
-template <bool A_BF16>
-__global__ void act_half_kernel(const void *act, int act_stride, int M, int K, _Float16 *a16,
-                                float level_step) {
-  const int k8 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
-  const int m0 = blockIdx.y * kHalfRows;
-  if (k8 >= K) return;
-  float x[kHalfRows][8];
-#pragma unroll
-  for (int r = 0; r < kHalfRows; ++r) {
-    const int m = min(m0 + r, M - 1);  // rows past M reread the last one, not stored
-    if (A_BF16) {
-      // rows are 16-byte aligned (act_stride % 8 == 0): one load for 8 values
-      const uint4_t raw = *reinterpret_cast<const uint4_t *>(
-          reinterpret_cast<const uint16_t *>(act) + (size_t)m * act_stride + k8);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[r][2 * i] = __builtin_bit_cast(float, raw[i] << 16);
-        x[r][2 * i + 1] = __builtin_bit_cast(float, raw[i] & 0xFFFF0000u);
-      }
-    } else {
-      const float4_t *src = reinterpret_cast<const float4_t *>(
-          reinterpret_cast<const float *>(act) + (size_t)m * act_stride + k8);
-      const float4_t lo = src[0], hi = src[1];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[r][i] = lo[i];
-        x[r][4 + i] = hi[i];
-      }
-    }
-  }
-  const _Float16 sixteenth = (_Float16)0.0625f;
-#pragma unroll
-  for (int r = 0; r < kHalfRows; ++r) {
-    if (m0 + r >= M) break;
-    if (level_step > 0.0f) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float level = __builtin_rintf(x[r][i] / level_step);
-        level = level < -128.0f ? -128.0f : level;
-        x[r][i] = level > 127.0f ? 127.0f : level;
-      }
-    }
-    half8_t h;
+template <bool IN_BF16>
+__device__ __forceinline__ void act_load8(const void *row, int k8, float (&x)[8]) {
+  if (IN_BF16) {
+    const uint4_t raw = *reinterpret_cast<const uint4_t *>(reinterpret_cast<const uint16_t *>(row) + k8);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const bool up = i & 1;  // k = 1, 3 and their partners 5, 7
-      const _Float16 a = sat_half(x[r][i]), b = sat_half(x[r][i + 4]);
-      h[2 * i] = up ? a * sixteenth : a;
-      h[2 * i + 1] = up ? b * sixteenth : b;
+      x[2 * i] = __builtin_bit_cast(float, raw[i] << 16);
+      x[2 * i + 1] = __builtin_bit_cast(float, raw[i] & 0xFFFF0000u);
     }
-    *reinterpret_cast<half8_t *>(a16 + (size_t)(m0 + r) * K + k8) = h;
+  } else {
+    const float4_t *src = reinterpret_cast<const float4_t *>(reinterpret_cast<const float *>(row) + k8);
+    const float4_t a = src[0], b = src[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = a[i];
+      x[4 + i] = b[i];
+    }
   }
 }
 
-struct GemmBigArgs {
-  const _Float16 *a16;    // [M][K], act_half_kernel's form
+__device__ __forceinline__ float level_of(float x, float step) {
+  float level = __builtin_rintf(x / step);
+  level = level < -128.0f ? -128.0f : level;
+  return level > 127.0f ? 127.0f : level;
+}
+
+// A row's values stay in registers between its peak and its conversion: at
+// most kActChunks chunks of eight a thread (rows up to 16384 wide in one
+// pass); wider rows read their values again for the conversion.
+constexpr int kActChunks = 8;
+
+template <bool IN_BF16, bool LO>
+__global__ __launch_bounds__(kActThreads) void act_scale_kernel(const void *act, int act_stride, int K,
+                                                                  int Kp, _Float16 *hi, _Float16 *lo,
+                                                                  float *inv, float level_step) {
+  __shared__ float red[kActThreads / 64];
+  const int m = blockIdx.x;
+  const int tid = threadIdx.x;
+  const void *row = IN_BF16 ? static_cast<const void *>(reinterpret_cast<const uint16_t *>(act) + (size_t)m * act_stride)
+                            : static_cast<const void *>(reinterpret_cast<const float *>(act) + (size_t)m * act_stride);
+  float held[kActChunks][8];
+  float peak = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kActChunks; ++c) {
+    const int k8 = (tid + c * kActThreads) * 8;
+    if (k8 < K) {
+      act_load8<IN_BF16>(row, k8, held[c]);
+      if (level_step > 0.0f) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) held[c][i] = level_of(held[c][i], level_step);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) peak = fmaxf(peak, fabsf(held[c][i]));
+    }
+  }
+  for (int k8 = (tid + kActChunks * kActThreads) * 8; k8 < K; k8 += kActThreads * 8) {
+    float x[8];
+    act_load8<IN_BF16>(row, k8, x);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) peak = fmaxf(peak, fabsf(level_step > 0.0f ? level_of(x[i], level_step) : x[i]));
+  }
+  peak = wave_max(peak);
+  if ((tid & 63) == 0) red[tid >> 6] = peak;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kActThreads / 64; ++w) peak = fmaxf(peak, red[w]);
+  // peak in [2^(e-1), 2^e): t = 15 - e puts it in [2^14, 2^15)
+  int t = 0;
+  if (peak > 0.0f && peak <= 3.402823466e38f) {
+    int e;
+    (void)frexpf(peak, &e);
+    t = 15 - e;
+    t = t < -126 ? -126 : (t > 126 ? 126 : t);
+  }
+  const float scale = ldexpf(1.0f, t);
+  if (tid == 0) inv[m] = ldexpf(1.0f, -t);
+  _Float16 *hrow = hi + (size_t)m * Kp;
+  _Float16 *lrow = LO ? lo + (size_t)m * Kp : nullptr;
+  auto store = [&](int k8, const float (&x)[8]) {
+    half8_t h, l;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      // operand slot 2 j + p holds k = j + 4 p, divided by 16 for odd j
+      const int j = i >> 1, p = i & 1;
+      const float v = x[j + 4 * p] * ((j & 1) ? scale * 0.0625f : scale);
+      const _Float16 vh = (_Float16)v;
+      h[i] = vh;
+      if (LO) l[i] = (_Float16)(v - (float)vh);
+    }
+    *reinterpret_cast<half8_t *>(hrow + k8) = h;
+    if (LO) *reinterpret_cast<half8_t *>(lrow + k8) = l;
+  };
+#pragma unroll
+  for (int c = 0; c < kActChunks; ++c) {
+    const int k8 = (tid + c * kActThreads) * 8;
+    if (k8 < K) store(k8, held[c]);
+  }
+  for (int k8 = (tid + kActChunks * kActThreads) * 8; k8 < K; k8 += kActThreads * 8) {
+    float x[8];
+    act_load8<IN_BF16>(row, k8, x);
+    if (level_step > 0.0f) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = level_of(x[i], level_step);
+    }
+    store(k8, x);
+  }
+  // the padding to a whole step: zeros, so the codes it meets add nothing
+  for (int k8 = K + tid * 8; k8 < Kp; k8 += kActThreads * 8) {
+    const half8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
+    *reinterpret_cast<half8_t *>(hrow + k8) = z;
+    if (LO) *reinterpret_cast<half8_t *>(lrow + k8) = z;
+  }
+}
+
+// ---- the product -----------------------------------------------------------
+
+struct GemmCodesArgs {
+  const _Float16 *a_hi;     // [M][K] act_scale_kernel's form
+  const _Float16 *a_lo;     // [M][K], two-term activations only
+  const float *row_inv;     // [M] 2^-t
   const uint8_t *codes;
   long long row_stride;
-  const float *gains;
+  const float *gains;       // [N][gain_stride]
   int gain_stride;
-  int group_shift;
-  float code_bias;
-  void *out;              // C, or with K slices fp32 partials [slice][M][N]
+  int group_shift;          // gain of 32-code unit u: u >> group_shift
+  const uint32_t *zero_pairs;  // [N][gain_stride] binary16 (1024 + b + z, 1024 + 16 (b + z))
+  uint32_t bias_pair;       // the same pair without zero points
+  void *out;                // [M][out_stride] bf16 or fp32
   int out_stride;
-  int M, N, K;            // K: the whole plane's columns
-  int k_steps;            // 64-wide steps of one K slice (blockIdx.z)
-  size_t slice_floats;    // floats between slices' partials (0: no split)
-  igl_gemm_close close;   // fp32 C only: C = grid(close.gains[n] step acc, leave)
+  int M, N, K;
+  int Kp;                   // K padded to whole steps: the activation rows' length
+  igl_gemm_close close;     // fp32 C only: C = grid(close.gains[n] step acc, leave)
 };
 
 // The row close of a calibrated plane's product on levels and unit gains:
@@ -328,584 +215,483 @@ __device__ __forceinline__ float close_value(const igl_gemm_close &c, int n, flo
   return y;
 }
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void global_void_t;
+constexpr int round_up(int v, int q) { return (v + q - 1) / q * q; }
 
-template <bool C_BF16>
-__global__ __launch_bounds__(512) void gemm_q4_big_kernel(GemmBigArgs g) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds_b[];
+// Waits until this wave's loads but the last N are in (vmcnt retires them in
+// issue order) and its LDS reads have landed.
+template <int N>
+__device__ __forceinline__ void wait_loads() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds six bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70);
+}
+
+// The stage layout of one form, in bytes.  Every array is padded to a whole
+// number of DMA instructions per wave (a lane past the data loads a valid
+// address into the padding), so every wave issues the same loads.
+template <int WN, int WM, int KS, int NB, int MB, int LIM, bool LO, bool ROWGAIN, bool ZERO>
+struct CodesForm {
+  static constexpr int W = WN * WM * KS;
+  static constexpr int THREADS = 64 * W;
+  static constexpr int TN = WN * NB * 16;
+  static constexpr int TM = WM * MB * 16;
+  static constexpr int A_PAD = round_up(KS * TM * 128, 1024 * W);
+  static constexpr int C_PAD = round_up(KS * TN * 32, 1024 * W);
+  static constexpr int G_PAD = ROWGAIN ? 0 : round_up(KS * 2 * TN * 4, 256 * W);
+  static constexpr int Z_PAD = ZERO ? round_up(KS * 2 * TN * 4, 256 * W) : 0;
+  static constexpr int L_OFF = A_PAD;
+  static constexpr int C_OFF = A_PAD * (LO ? 2 : 1);
+  static constexpr int G_OFF = C_OFF + C_PAD;
+  static constexpr int Z_OFF = G_OFF + G_PAD;
+  static constexpr int STAGE = Z_OFF + Z_PAD;
+  // three stages where they fit the form's LDS budget (LIM KiB: 160 for one
+  // workgroup a CU, 80 for two), else two
+  static constexpr int STAGES = 3 * STAGE <= LIM * 1024 ? 3 : 2;
+  static constexpr int RED = (KS - 1) * TN * TM * 4;
+  static constexpr int LDS = STAGES * STAGE > RED ? STAGES * STAGE : RED;
+  static constexpr int NA = A_PAD / (1024 * W);
+  static constexpr int NC = C_PAD / (1024 * W);
+  static constexpr int NG = G_PAD / (256 * W);
+  static constexpr int NZ = Z_PAD / (256 * W);
+  static constexpr int LOADS = NA * (LO ? 2 : 1) + NC + NG + NZ;
+  static_assert(LDS <= LIM * 1024, "LDS");
+  static_assert(LOADS * (STAGES - 2) < 64, "vmcnt");
+};
+
+template <int WN, int WM, int KS, int NB, int MB, int LIM, bool LO, bool ROWGAIN, bool ZERO, bool C_BF16>
+__global__ __launch_bounds__(64 * WN * WM * KS) void gemm_codes_kernel(GemmCodesArgs g) {
+  using F = CodesForm<WN, WM, KS, NB, MB, LIM, LO, ROWGAIN, ZERO>;
+  constexpr int W = F::W, TN = F::TN, TM = F::TM, STAGES = F::STAGES;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 2;      // 2 wave rows of 128
-  const int wn = wave & 3;       // 4 wave columns of 64
+  const int wn = wave % WN, wm = (wave / WN) % WM, ks = wave / (WN * WM);
   int tile_x, tile_y;
   xcd_tile(tile_x, tile_y);
-  const int m0 = tile_y * kBigM;
-  const int n0 = tile_x * kBigN;
-  const int steps = g.k_steps;
-  const int k_first = blockIdx.z * g.k_steps * kBigK;
-
-  // DMA sources (a lane's 16 bytes land at the wave's LDS address + 16 lane).
-  // Activations: wave w's instruction i fills rows 8 (4 w + i) .. +7, lane l
-  // row R0 + l / 8 at physical chunk l % 8, logical chunk (l % 8) ^ ((row >> 1) & 7).
-  const _Float16 *a_src[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 8 * (4 * wave + i) + (lane >> 3);
-    const int c = (lane & 7) ^ ((r >> 1) & 7);
-    a_src[i] = g.a16 + (size_t)min(m0 + r, g.M - 1) * g.K + k_first + 8 * c;
-  }
-  // codes: wave w fills rows 32 w .. +31, lane l row 32 w + l / 2, physical
-  // half l & 1, which holds logical half (l & 1) ^ (bit 3 of the row): rows
-  // n and n + 8 then read their eight bytes from different banks.  Gains
-  // (4 bytes a lane): the same rows, group l & 1.
-  const int br = min(n0 + 32 * wave + (lane >> 1), g.N - 1);
-  const uint8_t *b_src = g.codes + (size_t)br * (size_t)g.row_stride + k_first / 2 +
-                         16 * ((lane & 1) ^ ((lane >> 4) & 1));
-  const float *s_src = g.gains + (size_t)br * g.gain_stride;
-  const int s_first = k_first / 32;
-  const int s_grp = lane & 1;
-  // Activation stages first, then the code stages.
-  auto a_stage = [&](int step) { return lds_b + (step % kBigStages) * (kBigA * 2); };
-  auto b_stage = [&](int step) { return lds_b + kBigStages * kBigA * 2 + (step % kBigCodeStages) * kBigCodeStage; };
-  auto issue_a = [&](int step) {
-    uint8_t *st = a_stage(step);
-    const int k0 = step * kBigK;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds((global_void_t *)(a_src[i] + k0),
-                                       (lds_void_t *)(st + (4 * wave + i) * 1024), 16, 0, 0);
-  };
-  auto issue_b = [&](int step) {
-    uint8_t *st = b_stage(step);
-    const int k0 = step * kBigK;
-    __builtin_amdgcn_global_load_lds((global_void_t *)(b_src + k0 / 2), (lds_void_t *)(st + wave * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(
-        (global_void_t *)(s_src + (((unsigned)(s_first + k0 / 32 + s_grp)) >> g.group_shift)),
-        (lds_void_t *)(st + kBigB + wave * 256), 4, 0, 0);
-  };
-
-  float4_t acc[8][4];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const uint32_t exp10 = 0x64006400u;  // 1024.0 in both halves
-  const _Float16 lo_bias = (_Float16)(1024.0f + g.code_bias);
-  const _Float16 hi_bias = (_Float16)(1024.0f + 16.0f * g.code_bias);
-  const half2_t bias_lo = half2_t{lo_bias, lo_bias};
-  const half2_t bias_hi = half2_t{hi_bias, hi_bias};
-  const int gq = lane >> 4;     // lane group: k 16 gq .. 16 gq + 15 of a step
+  const int n0 = tile_x * TN, m0 = tile_y * TM;
+  const int steps = g.Kp / (kStepK * KS);
+  const int gq = lane >> 4;  // lane group: k 8 gq .. 8 gq + 7 of a 32-code group
   const int n = lane & 15;
 
-  // The codes of a step are read and decoded into binary16 operands a step
-  // ahead, eight fragments a step: one v_and_or_b32 puts a nibble pair in the
-  // mantissas of 1024.0 (ulp 1, or four bits up ulp 16); subtracting
-  // 1024 + bias (or 1024 + 16 bias) is exact; one multiply by the gain rounds
-  // once.  k-half q of lane group gq is k 16 gq + 8 q .. + 7: its activations
-  // are logical chunk 2 gq + q of the row, its codes dword q of the eight bytes.
-  auto read_codes = [&](const uint8_t *st, uint2_t (&braw)[4], half2_t (&bscale)[4]) {
-    const float *gs = reinterpret_cast<const float *>(st + kBigB);
+  // DMA sources at step 0.  Activations: 16-byte chunk f of a stage is step
+  // f / (8 TM), row (f / 8) % TM, physical chunk f % 8 holding logical chunk
+  // (f % 8) ^ ((row >> 1) & 7) (the 16 rows a read spans land in 16 distinct
+  // bank groups).  Codes: chunk f is step f / (2 TN), row (f / 2) % TN,
+  // physical half f % 2 holding group (f % 2) ^ (bit 3 of the row) (rows r and
+  // r + 8 read different banks).  Gains and zero pairs (4 bytes a lane): slot
+  // f is group f / TN of the stage (step (f / TN) / 2), row f % TN.
+  size_t a_off[F::NA];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = wn * 64 + 16 * j + n;
-      const int half = (gq >> 1) ^ ((n >> 3) & 1);
-      braw[j] = *reinterpret_cast<const uint2_t *>(st + row * 32 + 16 * half + 8 * (gq & 1));
-      const _Float16 sh = (_Float16)gs[row * 2 + (gq >> 1)];
-      bscale[j] = half2_t{sh, sh};
+  for (int u = 0; u < F::NA; ++u) {
+    const int f = 64 * (wave + W * u) + lane;
+    int kss = 0, row = 0, lc = 0;
+    if (f < KS * TM * 8) {
+      kss = f / (TM * 8);
+      row = (f / 8) % TM;
+      lc = (f & 7) ^ ((row >> 1) & 7);
     }
-  };
-  auto read_rows = [&](const uint8_t *st, int i, half8_t (&a)[2]) {
-    const _Float16 *as = reinterpret_cast<const _Float16 *>(st);
+    a_off[u] = (size_t)min(m0 + row, g.M - 1) * g.Kp + kss * kStepK + 8 * lc;
+  }
+  const uint8_t *c_row[F::NC];
+  int c_in[F::NC];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int r = wm * 128 + 16 * i + n;
-      const int p = (2 * gq + q) ^ ((r >> 1) & 7);
-      a[q] = *reinterpret_cast<const half8_t *>(as + r * kBigK + 8 * p);
+  for (int u = 0; u < F::NC; ++u) {
+    const int f = 64 * (wave + W * u) + lane;
+    int kss = 0, row = 0, lh = 0;
+    if (f < KS * TN * 2) {
+      kss = f / (TN * 2);
+      row = (f / 2) % TN;
+      lh = (f & 1) ^ ((row >> 3) & 1);
     }
+    c_row[u] = g.codes + (size_t)min(n0 + row, g.N - 1) * (size_t)g.row_stride;
+    c_in[u] = kss * (kStepK / 2) + 16 * lh;
+  }
+  const int row_bytes = g.K / 2;  // a group past K (padding) reads the row's first: its activations are 0
+  const unsigned last_unit = (unsigned)(g.K / 32 - 1);
+  const float *g_src[F::NG > 0 ? F::NG : 1];
+  int g_unit[F::NG > 0 ? F::NG : 1];
+#pragma unroll
+  for (int u = 0; u < F::NG; ++u) {
+    const int f = 64 * (wave + W * u) + lane;
+    int kq = 0, row = 0;
+    if (f < KS * 2 * TN) {
+      kq = f / TN;
+      row = f % TN;
+    }
+    g_src[u] = g.gains + (size_t)min(n0 + row, g.N - 1) * g.gain_stride;
+    g_unit[u] = kq;
+  }
+  const uint32_t *z_src[F::NZ > 0 ? F::NZ : 1];
+  int z_unit[F::NZ > 0 ? F::NZ : 1];
+#pragma unroll
+  for (int u = 0; u < F::NZ; ++u) {
+    const int f = 64 * (wave + W * u) + lane;
+    int kq = 0, row = 0;
+    if (f < KS * 2 * TN) {
+      kq = f / TN;
+      row = f % TN;
+    }
+    z_src[u] = g.zero_pairs + (size_t)min(n0 + row, g.N - 1) * g.gain_stride;
+    z_unit[u] = kq;
+  }
+  auto stage = [&](int s) { return lds + (s % STAGES) * F::STAGE; };
+  auto issue = [&](int s) {
+    uint8_t *st = stage(s);
+    const size_t k0 = (size_t)s * (kStepK * KS);
+#pragma unroll
+    for (int u = 0; u < F::NA; ++u)
+      __builtin_amdgcn_global_load_lds((global_void_t *)(g.a_hi + a_off[u] + k0),
+                                       (lds_void_t *)(st + 1024 * (wave + W * u)), 16, 0, 0);
+    if (LO) {
+#pragma unroll
+      for (int u = 0; u < F::NA; ++u)
+        __builtin_amdgcn_global_load_lds((global_void_t *)(g.a_lo + a_off[u] + k0),
+                                         (lds_void_t *)(st + F::L_OFF + 1024 * (wave + W * u)), 16, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < F::NC; ++u) {
+      const int b = c_in[u] + (int)(k0 / 2);
+      __builtin_amdgcn_global_load_lds((global_void_t *)(c_row[u] + (b < row_bytes ? b : 0)),
+                                       (lds_void_t *)(st + F::C_OFF + 1024 * (wave + W * u)), 16, 0, 0);
+    }
+    const unsigned unit0 = (unsigned)(k0 / 32);
+#pragma unroll
+    for (int u = 0; u < F::NG; ++u)
+      __builtin_amdgcn_global_load_lds(
+          (global_void_t *)(g_src[u] + (min(unit0 + (unsigned)g_unit[u], last_unit) >> g.group_shift)),
+          (lds_void_t *)(st + F::G_OFF + 256 * (wave + W * u)), 4, 0, 0);
+#pragma unroll
+    for (int u = 0; u < F::NZ; ++u)
+      __builtin_amdgcn_global_load_lds(
+          (global_void_t *)(z_src[u] + (min(unit0 + (unsigned)z_unit[u], last_unit) >> g.group_shift)),
+          (lds_void_t *)(st + F::Z_OFF + 256 * (wave + W * u)), 4, 0, 0);
   };
-  auto decode = [&](uint32_t d, half2_t scale) {
+
+  float4_t acc[MB][NB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t exp10 = 0x64006400u;  // 1024.0 in both halves
+  const half2_t pair_c = as_half2(g.bias_pair);
+  // A dword of eight codes k .. k + 7 as the binary16 operand
+  // (k, k+4, 16 k+1, 16 k+5, k+2, k+6, 16 k+3, 16 k+7) minus the bias pair.
+  auto decode = [&](uint32_t d, half2_t pair) {
+    const half2_t blo = half2_t{pair[0], pair[0]};
+    const half2_t bhi = half2_t{pair[1], pair[1]};
     const uint32_t e = d >> 8;
-    const half2_t p0 = (as_half2(and_or_b32(d, 0x000F000Fu, exp10)) - bias_lo) * scale;
-    const half2_t p1 = (as_half2(and_or_b32(d, 0x00F000F0u, exp10)) - bias_hi) * scale;
-    const half2_t p2 = (as_half2(and_or_b32(e, 0x000F000Fu, exp10)) - bias_lo) * scale;
-    const half2_t p3 = (as_half2(and_or_b32(e, 0x00F000F0u, exp10)) - bias_hi) * scale;
+    const half2_t p0 = as_half2(and_or_b32(d, 0x000F000Fu, exp10)) - blo;
+    const half2_t p1 = as_half2(and_or_b32(d, 0x00F000F0u, exp10)) - bhi;
+    const half2_t p2 = as_half2(and_or_b32(e, 0x000F000Fu, exp10)) - blo;
+    const half2_t p3 = as_half2(and_or_b32(e, 0x00F000F0u, exp10)) - bhi;
     return __builtin_bit_cast(half8_t, uint4_t{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
                                                __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)});
   };
-  // Waits until this wave's loads but the last `after` are in (vmcnt retires
-  // them in order) and its LDS reads have landed (the stages they read are
-  // refilled after the next barrier), then meets every wave at a bare barrier
-  // (a fence would also wait for the loads still in flight for later steps).
-  auto wait_meet = [&](int after) {
-    if (after >= 12)
-      __builtin_amdgcn_s_waitcnt(0x007C);  // vmcnt(12) lgkmcnt(0)
-    else if (after >= 6)
-      __builtin_amdgcn_s_waitcnt(0x0076);  // vmcnt(6) lgkmcnt(0)
-    else if (after >= 4)
-      __builtin_amdgcn_s_waitcnt(0x0074);  // vmcnt(4) lgkmcnt(0)
+
+  // Software pipeline: STAGES - 1 steps in flight.  Iteration s waits for
+  // step s (this wave's loads but those of the later steps already issued),
+  // meets every wave at a bare barrier (step s - 1's stage is then free; a
+  // fence would also wait for the later steps' loads), refills that stage
+  // with step s + STAGES - 1 and runs step s.
+  constexpr int AHEAD = STAGES - 1;
+  for (int t = 0; t < AHEAD && t < steps; ++t) issue(t);
+  for (int s = 0; s < steps; ++s) {
+    if (AHEAD >= 2 && s + 1 < steps)
+      wait_loads<F::LOADS * (AHEAD >= 2 ? 1 : 0)>();
     else
-      __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+      wait_loads<0>();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-  };
-
-  // Software pipeline.  Iteration s issues the activations of step s + 2 and
-  // the codes of step s + 3, and runs step s's 64 products in eight blocks of
-  // eight; between the blocks it reads step s's next row tile of activations
-  // (one block ahead) and decodes one of step s + 1's eight code fragments, so
-  // the decoding runs beside the matrix cores instead of between steps.  A
-  // wave's loads retire in issue order: before iteration s they are ...,
-  // [A s, B s+1], [A s+1, B s+2] (4 + 2 each), so A s and B s+1 are in when
-  // all but the last 4 [s+1 < steps] + 2 [s+2 < steps] are.
-  issue_b(0);
-  issue_a(0);
-  if (steps > 1) issue_b(1);
-  if (steps > 1) issue_a(1);
-  if (steps > 2) issue_b(2);
-  wait_meet((steps > 1 ? 10 : 0) + (steps > 2 ? 2 : 0) >= 12 ? 12 : 0);
-  half8_t bf[2][4];
-  {
-    uint2_t braw[4];
-    half2_t bscale[4];
-    read_codes(b_stage(0), braw, bscale);
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bf[q][j] = decode(braw[j][q], bscale[j]);
-  }
-  for (int s = 0; s < steps; ++s) {
-    wait_meet(4 * (s + 1 < steps) + 2 * (s + 2 < steps));
-    if (s + 2 < steps) issue_a(s + 2);
-    if (s + 3 < steps) issue_b(s + 3);
-    const bool more = s + 1 < steps;
-    const uint8_t *ast = a_stage(s);
-    half8_t bn[2][4];
-    uint2_t braw[4];
-    half2_t bscale[4];
-    read_codes(b_stage(more ? s + 1 : s), braw, bscale);
-    half8_t a_cur[2], a_next[2];
-    read_rows(ast, 0, a_cur);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (i + 1 < 8) read_rows(ast, i + 1, a_next);
-#pragma unroll
-      for (int q = 0; q < 2; ++q)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[q][j], a_cur[q], acc[i][j], 0, 0, 0);
-      bn[i >> 2][i & 3] = decode(braw[i & 3][i >> 2], bscale[i & 3]);
-      __builtin_amdgcn_sched_barrier(0);
-      a_cur[0] = a_next[0];
-      a_cur[1] = a_next[1];
-    }
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bf[q][j] = bn[q][j];
-  }
-
-  // The products take the codes as the first operand, so a 16x16 tile of D is
-  // C transposed: lane l holds row l % 16 of its row tile and the four
-  // consecutive columns 4 (l / 16) .. + 3, stored as one 8- or 16-byte vector.
-  float *part = reinterpret_cast<float *>(g.out) + blockIdx.z * g.slice_floats;
-  const bool vec_ok = g.slice_floats ? (g.N % 4 == 0)
-                                     : (g.out_stride % 4 == 0 &&
-                                        ((uintptr_t)g.out & (C_BF16 ? 7u : 15u)) == 0);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int m = m0 + wm * 128 + i * 16 + n;
-    if (m >= g.M) continue;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int nb = n0 + wn * 64 + j * 16 + 4 * gq;
-      float4_t v = acc[i][j];
-      if (!g.slice_floats && !C_BF16 && g.close.gains) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (nb + r < g.N) v[r] = close_value(g.close, nb + r, v[r]);
-      }
-      if (vec_ok && nb + 3 < g.N) {
-        if (g.slice_floats) {
-          *reinterpret_cast<float4_t *>(part + (size_t)m * g.N + nb) = v;
-        } else if (C_BF16) {
-          const uint32_t lo = bf16_pair(v[0], v[1]);
-          const uint32_t hi = bf16_pair(v[2], v[3]);
-          *reinterpret_cast<uint2_t *>(reinterpret_cast<uint16_t *>(g.out) + (size_t)m * g.out_stride + nb) =
-              uint2_t{lo, hi};
-        } else {
-          *reinterpret_cast<float4_t *>(reinterpret_cast<float *>(g.out) + (size_t)m * g.out_stride + nb) = v;
-        }
-        continue;
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int nn = nb + r;
-        if (nn >= g.N) continue;
-        if (g.slice_floats)
-          part[(size_t)m * g.N + nn] = v[r];
-        else if (C_BF16)
-          reinterpret_cast<uint16_t *>(g.out)[(size_t)m * g.out_stride + nn] = float_to_bf16(v[r]);
-        else
-          reinterpret_cast<float *>(g.out)[(size_t)m * g.out_stride + nn] = v[r];
-      }
-    }
-  }
-}
-
-// C = the K slices' partials added in slice order (four columns a thread).
-template <bool C_BF16>
-__global__ void gemm_slice_sum_kernel(const float *part, int slices, size_t slice_floats, int M,
-                                      int N, void *out, int out_stride, igl_gemm_close close) {
-  const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
-  const int m = blockIdx.y;
-  if (n >= N) return;
-  const float *src = part + (size_t)m * N + n;
-  float4_t t = *reinterpret_cast<const float4_t *>(src);
-  for (int z = 1; z < slices; ++z) t += *reinterpret_cast<const float4_t *>(src + z * slice_floats);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    if (n + e >= N) break;
-    if (C_BF16)
-      reinterpret_cast<uint16_t *>(out)[(size_t)m * out_stride + n + e] = float_to_bf16(t[e]);
-    else
-      reinterpret_cast<float *>(out)[(size_t)m * out_stride + n + e] =
-          close.gains ? close_value(close, n + e, t[e]) : t[e];
-  }
-}
-
-// ---- the skinny form (64 <= M < 256 lanes) --------------------------------
-//
-// Few lanes leave the product bound by the weight stream, which must be read
-// once: a workgroup of four waves owns 128 weight rows x 64 lanes and walks its
-// K slice in steps of 64, with the large-tile form's operand order, decoding
-// and DMA staging (three stages, issued two steps ahead; eight stages measured
-// slower: a CU's outstanding reads, not their latency, bound the stream).  Wave w decodes rows
-// 32 w .. 32 w + 31 and multiplies them by all 64 lanes (2 x 4 products of
-// 16 x 16 a k-half), so no row is decoded twice.  K slices (blockIdx.z) keep
-// at least 128 workgroups; their fp32 partials are added in slice order by
-// gemm_slice_sum_kernel.
-constexpr int kMidM = 64;
-constexpr int kMidN = 128;
-constexpr int kMidK = 64;
-constexpr int kMidStages = 3;
-constexpr int kMidAhead = kMidStages - 1;
-constexpr int kMidA = kMidM * kMidK;                  // halves of a stage's activations
-constexpr int kMidB = kMidN * kMidK / 2;              // bytes of a stage's codes
-constexpr int kMidG = kMidN * kMidK / 32;             // floats of a stage's gains
-constexpr int kMidStage = kMidA * 2 + kMidB + kMidG * 4;
-constexpr int kMidLds = kMidStages * kMidStage;
-
-template <bool C_BF16>
-__global__ __launch_bounds__(256) void gemm_q4_mid_kernel(GemmBigArgs g) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds_m[];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n0 = blockIdx.x * kMidN;
-  const int m0 = blockIdx.y * kMidM;
-  const int steps = g.k_steps;
-  const int k_first = blockIdx.z * g.k_steps * kMidK;
-
-  // DMA sources.  Activations: wave w's instruction i fills rows 8 (2 w + i)
-  // .. +7, lane l row R0 + l / 8 at physical chunk l % 8, logical chunk
-  // (l % 8) ^ ((row >> 1) & 7).  Codes: wave w fills rows 32 w .. +31, lane l row
-  // 32 w + l / 2, physical half l & 1 holding logical half (l & 1) ^ (bit 3 of
-  // the row).  Gains: the same rows, group l & 1.
-  const _Float16 *a_src[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = 8 * (2 * wave + i) + (lane >> 3);
-    const int c = (lane & 7) ^ ((r >> 1) & 7);
-    a_src[i] = g.a16 + (size_t)min(m0 + r, g.M - 1) * g.K + k_first + 8 * c;
-  }
-  const int br = min(n0 + 32 * wave + (lane >> 1), g.N - 1);
-  const uint8_t *b_src = g.codes + (size_t)br * (size_t)g.row_stride + k_first / 2 +
-                         16 * ((lane & 1) ^ ((lane >> 4) & 1));
-  const float *s_src = g.gains + (size_t)br * g.gain_stride;
-  const int s_first = k_first / 32;
-  const int s_grp = lane & 1;
-  auto stage = [&](int step) { return lds_m + (step % kMidStages) * kMidStage; };
-  auto issue = [&](int step) {
-    uint8_t *st = stage(step);
-    const int k0 = step * kMidK;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      __builtin_amdgcn_global_load_lds((global_void_t *)(a_src[i] + k0),
-                                       (lds_void_t *)(st + (2 * wave + i) * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((global_void_t *)(b_src + k0 / 2),
-                                     (lds_void_t *)(st + kMidA * 2 + wave * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(
-        (global_void_t *)(s_src + (((unsigned)(s_first + k0 / 32 + s_grp)) >> g.group_shift)),
-        (lds_void_t *)(st + kMidA * 2 + kMidB + wave * 256), 4, 0, 0);
-  };
-
-  float4_t acc[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const uint32_t exp10 = 0x64006400u;  // 1024.0 in both halves
-  const _Float16 lo_bias = (_Float16)(1024.0f + g.code_bias);
-  const _Float16 hi_bias = (_Float16)(1024.0f + 16.0f * g.code_bias);
-  const half2_t bias_lo = half2_t{lo_bias, lo_bias};
-  const half2_t bias_hi = half2_t{hi_bias, hi_bias};
-  const int gq = lane >> 4;
-  const int n = lane & 15;
-  auto decode = [&](uint32_t d, half2_t scale) {
-    const uint32_t e = d >> 8;
-    const half2_t p0 = (as_half2(and_or_b32(d, 0x000F000Fu, exp10)) - bias_lo) * scale;
-    const half2_t p1 = (as_half2(and_or_b32(d, 0x00F000F0u, exp10)) - bias_hi) * scale;
-    const half2_t p2 = (as_half2(and_or_b32(e, 0x000F000Fu, exp10)) - bias_lo) * scale;
-    const half2_t p3 = (as_half2(and_or_b32(e, 0x00F000F0u, exp10)) - bias_hi) * scale;
-    return __builtin_bit_cast(half8_t, uint4_t{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
-                                               __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)});
-  };
-
-  // A wave's loads retire in issue order, four a step: before iteration s
-  // steps s .. min(s + kMidAhead, steps) - 1 are in flight, so step s is in
-  // when all but the last 4 min(kMidAhead - 1, steps - s - 1) are.
-  for (int t = 0; t < kMidAhead && t < steps; ++t) issue(t);
-  for (int s = 0; s < steps; ++s) {
-    switch (min(kMidAhead - 1, steps - s - 1)) {  // vmcnt(4 n) lgkmcnt(0)
-      case 0: __builtin_amdgcn_s_waitcnt(0x0070); break;
-      case 1: __builtin_amdgcn_s_waitcnt(0x0074); break;
-      case 2: __builtin_amdgcn_s_waitcnt(0x0078); break;
-      case 3: __builtin_amdgcn_s_waitcnt(0x007C); break;
-      case 4: __builtin_amdgcn_s_waitcnt(0x4070); break;
-      case 5: __builtin_amdgcn_s_waitcnt(0x4074); break;
-      default: __builtin_amdgcn_s_waitcnt(0x4078); break;
-    }
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();  // every wave's DMA of step s is in; step s - 1's stage is free
-    asm volatile("" ::: "memory");
-    if (s + kMidAhead < steps) issue(s + kMidAhead);
+    if (s + AHEAD < steps) issue(s + AHEAD);
     const uint8_t *st = stage(s);
-    const _Float16 *as = reinterpret_cast<const _Float16 *>(st);
-    const uint8_t *cs = st + kMidA * 2;
-    const float *gs = reinterpret_cast<const float *>(cs + kMidB);
-    half8_t bf[2][2];
+    half8_t bf[NB][2];
+    float gain[NB][2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int row = 32 * wave + 16 * j + n;
-      const int half = (gq >> 1) ^ ((n >> 3) & 1);
-      const uint2_t raw = *reinterpret_cast<const uint2_t *>(cs + row * 32 + 16 * half + 8 * (gq & 1));
-      const _Float16 sh = (_Float16)gs[row * 2 + (gq >> 1)];
-      const half2_t sc = half2_t{sh, sh};
-      bf[0][j] = decode(raw[0], sc);
-      bf[1][j] = decode(raw[1], sc);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      half8_t a[2];
+    for (int j = 0; j < NB; ++j) {
+      const int row = wn * NB * 16 + 16 * j + n;
+      const int sw = (row >> 3) & 1;
+      const uint8_t *cr = st + F::C_OFF + (ks * TN + row) * 32 + 4 * gq;
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        const int r = 16 * i + n;
-        const int p = (2 * gq + q) ^ ((r >> 1) & 7);
-        a[q] = *reinterpret_cast<const half8_t *>(as + r * kMidK + 8 * p);
+        const uint32_t d = *reinterpret_cast<const uint32_t *>(cr + 16 * (q ^ sw));
+        const int slot = (ks * 2 + q) * TN + row;
+        half2_t pair = pair_c;
+        if (ZERO) pair = as_half2(*reinterpret_cast<const uint32_t *>(st + F::Z_OFF + 4 * slot));
+        bf[j][q] = decode(d, pair);
+        if (!ROWGAIN) gain[j][q] = *reinterpret_cast<const float *>(st + F::G_OFF + 4 * slot);
       }
+    }
+    // The step's MB x NB x 2 products as one chain of tasks (lane block i,
+    // row block j, group q): task t's product is issued, then the gain FMAs of
+    // task t - kLag, whose product has had kLag products' time to land, so the
+    // matrix cores and the FMAs overlap instead of each FMA waiting on its
+    // own product.  A lane block's activations are read from LDS one block
+    // ahead.
+    constexpr int T = MB * NB * 2;
+    constexpr int kLag = ROWGAIN ? 0 : 3;
+    half8_t ah[2][2], al[2][2];
+    auto read_acts = [&](int i, half8_t (&h)[2], half8_t (&l)[2]) {
+      const int arow = wm * MB * 16 + 16 * i + n;
 #pragma unroll
-      for (int q = 0; q < 2; ++q)
+      for (int q = 0; q < 2; ++q) {
+        const int pc = (4 * q + gq) ^ ((arow >> 1) & 7);
+        const int at = ((ks * TM + arow) * 64 + 8 * pc) * 2;
+        h[q] = *reinterpret_cast<const half8_t *>(st + at);
+        if (LO) l[q] = *reinterpret_cast<const half8_t *>(st + F::L_OFF + at);
+      }
+    };
+    read_acts(0, ah[0], al[0]);
+    float4_t part[kLag + 1];
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[q][j], a[q], acc[i][j], 0, 0, 0);
+    for (int t = 0; t < T + kLag; ++t) {
+      if (t < T) {
+        const int i = t / (NB * 2), j = (t / 2) % NB, q = t & 1;
+        if (j == 0 && q == 0 && i + 1 < MB) read_acts(i + 1, ah[(i + 1) & 1], al[(i + 1) & 1]);
+        const half8_t &a = ah[i & 1][q];
+        if (ROWGAIN) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bf[j][q], acc[i][j], 0, 0, 0);
+          if (LO) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i & 1][q], bf[j][q], acc[i][j], 0, 0, 0);
+        } else {
+          float4_t p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bf[j][q], float4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+          if (LO) p = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i & 1][q], bf[j][q], p, 0, 0, 0);
+          part[t % (kLag + 1)] = p;
+        }
+      }
+      if (!ROWGAIN && t >= kLag) {
+        const int u = t - kLag;
+        const int i = u / (NB * 2), j = (u / 2) % NB, q = u & 1;
+        const float4_t p = part[u % (kLag + 1)];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(gain[j][q], p[r], acc[i][j][r]);
+      }
+      // keep the chain's order (the scheduler would otherwise put each FMA
+      // right behind its own product)
+      if (!ROWGAIN) __builtin_amdgcn_sched_barrier(0);
     }
   }
 
-  // D is C transposed (as in the large-tile form): lane l holds lane row
-  // l % 16 of its tile and four consecutive weight rows 4 (l / 16) .. + 3.
-  float *part = reinterpret_cast<float *>(g.out) + blockIdx.z * g.slice_floats;
-  const bool vec_ok = g.slice_floats ? (g.N % 4 == 0)
-                                     : (g.out_stride % 4 == 0 &&
-                                        ((uintptr_t)g.out & (C_BF16 ? 7u : 15u)) == 0);
+  // The K split's partial tiles, added in ks order.
+  if (KS > 1) {
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(lds);
+    const int tile = wm * WN + wn;
+    if (ks > 0) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0 + 16 * i + n;
-    if (m >= g.M) continue;
+      for (int i = 0; i < MB; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int nb = n0 + 32 * wave + 16 * j + 4 * gq;
-      float4_t v = acc[i][j];
-      if (!g.slice_floats && !C_BF16 && g.close.gains) {
+        for (int j = 0; j < NB; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (nb + r < g.N) v[r] = close_value(g.close, nb + r, v[r]);
-      }
-      if (vec_ok && nb + 3 < g.N) {
-        if (g.slice_floats) {
-          *reinterpret_cast<float4_t *>(part + (size_t)m * g.N + nb) = v;
-        } else if (C_BF16) {
-          *reinterpret_cast<uint2_t *>(reinterpret_cast<uint16_t *>(g.out) + (size_t)m * g.out_stride + nb) =
-              uint2_t{bf16_pair(v[0], v[1]), bf16_pair(v[2], v[3])};
-        } else {
-          *reinterpret_cast<float4_t *>(reinterpret_cast<float *>(g.out) + (size_t)m * g.out_stride + nb) = v;
-        }
-        continue;
-      }
+          for (int r = 0; r < 4; ++r)
+            red[((((ks - 1) * WM * WN + tile) * MB * NB + i * NB + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int z = 1; z < KS; ++z)
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[i][j][r] += red[((((z - 1) * WM * WN + tile) * MB * NB + i * NB + j) * 4 + r) * 64 + lane];
+  }
+
+  // A 16 x 16 tile of D: lane l holds lanes (C rows) 4 (l / 16) .. + 3 of
+  // weight row (C column) l % 16.
+  float inv[MB][4];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) inv[i][r] = g.row_inv[min(m0 + wm * MB * 16 + 16 * i + 4 * gq + r, g.M - 1)];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int nn = n0 + wn * NB * 16 + 16 * j + n;
+    if (nn >= g.N) continue;
+    const float row_gain = ROWGAIN ? g.gains[(size_t)nn * g.gain_stride] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int nn = nb + r;
-        if (nn >= g.N) continue;
-        if (g.slice_floats)
-          part[(size_t)m * g.N + nn] = v[r];
-        else if (C_BF16)
-          reinterpret_cast<uint16_t *>(g.out)[(size_t)m * g.out_stride + nn] = float_to_bf16(v[r]);
-        else
-          reinterpret_cast<float *>(g.out)[(size_t)m * g.out_stride + nn] = v[r];
+        const int m = m0 + wm * MB * 16 + 16 * i + 4 * gq + r;
+        if (m >= g.M) continue;
+        float v = acc[i][j][r] * inv[i][r];
+        if (ROWGAIN) v = row_gain * v;
+        if (C_BF16) {
+          reinterpret_cast<uint16_t *>(g.out)[(size_t)m * g.out_stride + nn] = float_to_bf16(v);
+        } else {
+          if (g.close.gains) v = close_value(g.close, nn, v);
+          reinterpret_cast<float *>(g.out)[(size_t)m * g.out_stride + nn] = v;
+        }
       }
-    }
   }
+}
+
+// ---- forms and their choice -----------------------------------------------
+
+// (WN, WM, KS, NB, MB) of the forms, widest tile first.  A launch takes the
+// first form whose tiles fill the 256 CUs and whose K split divides K, else
+// the last that divides K.
+struct FormShape {
+  int wn, wm, ks, nb, mb, lim;
+};
+constexpr FormShape kForms[] = {
+    {4, 2, 1, 4, 8, 160},  // 256 x 256, eight waves
+    {2, 2, 2, 4, 4, 160},  // 128 x 128, eight waves, K split in two
+    {2, 1, 4, 2, 4, 160},  // 64 x 64, eight waves, K split in four
+    {1, 1, 8, 2, 4, 160},  // 32 x 64, eight waves, K split in eight
+    {1, 1, 8, 1, 4, 160},  // 16 x 64, eight waves, K split in eight
+};
+constexpr int kFormCount = sizeof(kForms) / sizeof(kForms[0]);
+// Two-term activations: the same forms with the K split capped where the
+// stages would not fit.
+constexpr FormShape kFormsLo[] = {
+    {4, 2, 1, 4, 4, 160},
+    {2, 2, 2, 4, 4, 160},
+    {2, 1, 4, 2, 4, 160},
+    {1, 1, 4, 2, 4, 160},
+    {1, 1, 4, 1, 4, 160},
+};
+
+static int choose_form(int M, int N, int K, int two_terms) {
+  const FormShape *forms = two_terms ? kFormsLo : kForms;
+  int last = -1;
+  for (int f = 0; f < kFormCount; ++f) {
+    const FormShape &s = forms[f];
+    if (s.ks > 1 ? K % (kStepK * s.ks) != 0 : K % 32 != 0) continue;
+    const long tn = 16L * s.nb * s.wn, tm = 16L * s.mb * s.wm;
+    const long tiles = ((N + tn - 1) / tn) * ((M + tm - 1) / tm);
+    last = f;
+    if (tiles >= 256) return f;
+  }
+  return last;
+}
+
+template <int WN, int WM, int KS, int NB, int MB, int LIM, bool LO, bool ROWGAIN, bool ZERO, bool C_BF16>
+static hipError_t launch_form(const GemmCodesArgs &a, hipStream_t stream) {
+  using F = CodesForm<WN, WM, KS, NB, MB, LIM, LO, ROWGAIN, ZERO>;
+  const void *fn =
+      reinterpret_cast<const void *>(&gemm_codes_kernel<WN, WM, KS, NB, MB, LIM, LO, ROWGAIN, ZERO, C_BF16>);
+  static bool granted = false;  // the dynamic LDS a kernel asks for is granted once
+  if (!granted) {
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, F::LDS);
+    if (e != hipSuccess) return e;
+    granted = true;
+  }
+  const dim3 grid((a.N + F::TN - 1) / F::TN, (a.M + F::TM - 1) / F::TM);
+  hipLaunchKernelGGL((gemm_codes_kernel<WN, WM, KS, NB, MB, LIM, LO, ROWGAIN, ZERO, C_BF16>), grid, dim3(F::THREADS),
+                     (size_t)F::LDS, stream, a);
+  return hipGetLastError();
+}
+
+template <int F, bool LO, bool ROWGAIN, bool ZERO, bool C_BF16>
+static hipError_t launch_shape(const GemmCodesArgs &a, hipStream_t stream) {
+  constexpr FormShape s = LO ? kFormsLo[F] : kForms[F];
+  return launch_form<s.wn, s.wm, s.ks, s.nb, s.mb, s.lim, LO, ROWGAIN, ZERO, C_BF16>(a, stream);
+}
+
+template <bool LO, bool ROWGAIN, bool ZERO, bool C_BF16>
+static hipError_t launch_pick(int form, const GemmCodesArgs &a, hipStream_t stream) {
+  switch (form) {
+    case 0: return launch_shape<0, LO, ROWGAIN, ZERO, C_BF16>(a, stream);
+    case 1: return launch_shape<1, LO, ROWGAIN, ZERO, C_BF16>(a, stream);
+    case 2: return launch_shape<2, LO, ROWGAIN, ZERO, C_BF16>(a, stream);
+    case 3: return launch_shape<3, LO, ROWGAIN, ZERO, C_BF16>(a, stream);
+    default: return launch_shape<4, LO, ROWGAIN, ZERO, C_BF16>(a, stream);
+  }
+}
+
+template <bool LO, bool ROWGAIN, bool ZERO>
+static hipError_t launch_out(int form, int out_bf16, const GemmCodesArgs &a, hipStream_t stream) {
+  return out_bf16 ? launch_pick<LO, ROWGAIN, ZERO, true>(form, a, stream)
+                  : launch_pick<LO, ROWGAIN, ZERO, false>(form, a, stream);
 }
 
 }  // namespace igl
 
 using namespace igl;
 
-// K slices of a large-tile launch: while the tiles fill fewer than 256
-// workgroups (one a CU) and every slice keeps four 64-wide steps, K is cut in
-// two again; N % 4 == 0 for the slice sum's four-column reads.
-static int gemm_slices(int M, int N, int K) {
-  const int tiles = ((M + kBigM - 1) / kBigM) * ((N + kBigN - 1) / kBigN);
-  int slices = 1;
-  while (slices < 8 && tiles * slices < 256 && N % 4 == 0 && K % (2 * slices * kBigK) == 0 &&
-         K / (2 * slices) >= 4 * kBigK)
-    slices *= 2;
-  return slices;
+static size_t half_bytes(int M, int K) { return ((size_t)M * (size_t)K * sizeof(_Float16) + 255) & ~(size_t)255; }
+
+// K padded to the chosen form's whole steps (only the forms without a K split
+// pad: by one 32-code group at most).
+static int padded_k(int K) { return (K + kStepK - 1) / kStepK * kStepK; }
+
+extern "C" int igl_gemm_fits(int M, int N, int K) { return M >= 1 && N >= 1 && K >= 32 && K % 32 == 0; }
+
+extern "C" size_t igl_gemm_work_bytes(int M, int N, int K, int act_terms) {
+  if (!igl_gemm_fits(M, N, K)) return 0;
+  return half_bytes(M, padded_k(K)) * (act_terms == 2 ? 2 : 1) + (((size_t)M * sizeof(float) + 255) & ~(size_t)255);
 }
 
-static size_t gemm_half_bytes(int M, int K) {
-  return ((size_t)M * (size_t)K * sizeof(_Float16) + 255) & ~(size_t)255;
+extern "C" int igl_gemm_form(int M, int N, int K, int act_terms) {
+  return igl_gemm_fits(M, N, K) ? choose_form(M, N, K, act_terms == 2) : -1;
 }
 
-// Bytes of workspace igl_launch_gemm_q4 needs for an M x N x K product (the
-// binary16 activations of the large-tile form, then any K slices' fp32
-// partials), 0 when it takes the small form.
-// K slices of a skinny-form launch: while the tiles fill fewer than 128
-// workgroups (the weight stream needs about half the CUs).
-static int gemm_mid_slices(int M, int N, int K) {
-  const int tiles = ((M + kMidM - 1) / kMidM) * ((N + kMidN - 1) / kMidN);
-  int slices = 1;
-  while (slices < 8 && tiles * slices < 128 && N % 4 == 0 && K % (2 * slices * kMidK) == 0 &&
-         K / (2 * slices) >= 4 * kMidK)
-    slices *= 2;
-  return slices;
-}
-
-static int gemm_is_mid(int M, int N, int K) {
-  return M >= 64 && M < kBigM && N >= kMidN && K % kMidK == 0;
-}
-
-extern "C" size_t igl_gemm_work_bytes(int M, int N, int K) {
-  if (gemm_is_mid(M, N, K)) {
-    const int slices = gemm_mid_slices(M, N, K);
-    return gemm_half_bytes(M, K) + (slices > 1 ? (size_t)slices * M * N * sizeof(float) : 0);
-  }
-  if (M < kBigM || N < kBigN || K % kBigK) return 0;
-  const int slices = gemm_slices(M, N, K);
-  return gemm_half_bytes(M, K) + (slices > 1 ? (size_t)slices * M * N * sizeof(float) : 0);
-}
-
-extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride,
-                                         const uint8_t *codes, long long row_stride,
-                                         const float *gains, int gain_stride, int group_shift,
-                                         int code_bias, void *out, int out_bf16, int out_stride,
-                                         int M, int N, int K, void *work,
-                                         const igl_gemm_close *close, hipStream_t stream) {
+extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride, const uint8_t *codes,
+                                         long long row_stride, const float *gains, int gain_stride,
+                                         int group_shift, int code_bias, const uint32_t *zero_pairs, void *out,
+                                         int out_bf16, int out_stride, int M, int N, int K, int act_terms,
+                                         void *work, const igl_gemm_close *close, hipStream_t stream) {
   const igl_gemm_close no_close = {nullptr, 0.0f, 0.0f};
   const igl_gemm_close cl = close ? *close : no_close;
-  if (cl.gains && (out_bf16 || act_bf16 || !igl_gemm_work_bytes(M, N, K) || !work))
-    return hipErrorInvalidValue;  // the close rides only on the large-tile form's fp32 C
-  if (igl_gemm_work_bytes(M, N, K) && work) {
-    _Float16 *a16 = reinterpret_cast<_Float16 *>(work);
-    const bool mid = gemm_is_mid(M, N, K);
-    const int slices = mid ? gemm_mid_slices(M, N, K) : gemm_slices(M, N, K);
-    float *part = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(work) + gemm_half_bytes(M, K));
-    dim3 cgrid((K / 8 + 255) / 256, (M + kHalfRows - 1) / kHalfRows);
-    if (act_bf16)
-      hipLaunchKernelGGL((act_half_kernel<true>), cgrid, dim3(256), 0, stream, act, act_stride, M, K, a16, 0.0f);
-    else
-      hipLaunchKernelGGL((act_half_kernel<false>), cgrid, dim3(256), 0, stream, act, act_stride, M, K, a16,
-                         cl.gains ? cl.step : 0.0f);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    GemmBigArgs b;
-    b.a16 = a16;
-    b.codes = codes;
-    b.row_stride = row_stride;
-    b.gains = gains;
-    b.gain_stride = gain_stride;
-    b.group_shift = group_shift;
-    b.code_bias = (float)code_bias;
-    b.out = slices > 1 ? static_cast<void *>(part) : out;
-    b.out_stride = out_stride;
-    b.M = M;
-    b.N = N;
-    b.K = K;
-    b.k_steps = K / kBigK / slices;
-    b.slice_floats = slices > 1 ? (size_t)M * N : 0;
-    b.close = cl;
-    // The dynamic LDS each form asks for is granted once per kernel.
-    static int granted[4];
-    const int use_bf16 = out_bf16 && (!mid || slices == 1);
-    const void *fn = mid ? (use_bf16 ? reinterpret_cast<const void *>(&gemm_q4_mid_kernel<true>)
-                                     : reinterpret_cast<const void *>(&gemm_q4_mid_kernel<false>))
-                         : (use_bf16 ? reinterpret_cast<const void *>(&gemm_q4_big_kernel<true>)
-                                     : reinterpret_cast<const void *>(&gemm_q4_big_kernel<false>));
-    const int lds = mid ? kMidLds : kBigLds;
-    const int which = 2 * mid + use_bf16;
-    if (!granted[which]) {
-      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-      if (e != hipSuccess) return e;
-      granted[which] = 1;
-    }
-    if (mid) {
-      const dim3 grid((N + kMidN - 1) / kMidN, (M + kMidM - 1) / kMidM, slices);
-      if (use_bf16)
-        hipLaunchKernelGGL((gemm_q4_mid_kernel<true>), grid, dim3(256), (size_t)lds, stream, b);
-      else
-        hipLaunchKernelGGL((gemm_q4_mid_kernel<false>), grid, dim3(256), (size_t)lds, stream, b);
-    } else {
-      const dim3 grid((N + kBigN - 1) / kBigN, (M + kBigM - 1) / kBigM, slices);
-      if (use_bf16)
-        hipLaunchKernelGGL((gemm_q4_big_kernel<true>), grid, dim3(512), (size_t)lds, stream, b);
-      else
-        hipLaunchKernelGGL((gemm_q4_big_kernel<false>), grid, dim3(512), (size_t)lds, stream, b);
-    }
-    e = hipGetLastError();
-    if (e != hipSuccess || slices == 1) return e;
-    dim3 sgrid((N / 4 + 255) / 256, M);
-    if (out_bf16)
-      hipLaunchKernelGGL((gemm_slice_sum_kernel<true>), sgrid, dim3(256), 0, stream, part, slices,
-                         b.slice_floats, M, N, out, out_stride, cl);
-    else
-      hipLaunchKernelGGL((gemm_slice_sum_kernel<false>), sgrid, dim3(256), 0, stream, part, slices,
-                         b.slice_floats, M, N, out, out_stride, cl);
-    return hipGetLastError();
-  }
-  GemmArgs g;
-  g.act = act;
-  g.act_stride = act_stride;
-  g.codes = codes;
-  g.row_stride = row_stride;
-  g.gains = gains;
-  g.gain_stride = gain_stride;
-  g.group_shift = group_shift;
-  g.code_bias = (float)code_bias;
-  g.out = out;
-  g.out_stride = out_stride;
-  g.M = M;
-  g.N = N;
-  g.K = K;
-  dim3 grid((N + kGemmBN - 1) / kGemmBN, (M + kGemmBM - 1) / kGemmBM);
-  if (act_bf16 && out_bf16)
-    hipLaunchKernelGGL((gemm_q4_kernel<true, true>), grid, dim3(kGemmThreads), 0, stream, g);
-  else if (act_bf16)
-    hipLaunchKernelGGL((gemm_q4_kernel<true, false>), grid, dim3(kGemmThreads), 0, stream, g);
-  else if (out_bf16)
-    hipLaunchKernelGGL((gemm_q4_kernel<false, true>), grid, dim3(kGemmThreads), 0, stream, g);
+  const bool lo = act_terms == 2;
+  if (!igl_gemm_fits(M, N, K) || !work || (act_terms != 1 && act_terms != 2) || (lo && act_bf16) ||
+      (cl.gains && (out_bf16 || act_bf16)) || ((uintptr_t)act & 15) || (act_stride % (act_bf16 ? 8 : 4)) ||
+      code_bias < 0 || code_bias > 15)
+    return hipErrorInvalidValue;
+  const int Kp = padded_k(K);
+  _Float16 *hi = reinterpret_cast<_Float16 *>(work);
+  _Float16 *lo_p = reinterpret_cast<_Float16 *>(reinterpret_cast<uint8_t *>(work) + half_bytes(M, Kp));
+  float *inv = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(work) + half_bytes(M, Kp) * (lo ? 2 : 1));
+  const float level_step = cl.gains ? cl.step : 0.0f;
+  if (act_bf16)
+    hipLaunchKernelGGL((act_scale_kernel<true, false>), dim3(M), dim3(kActThreads), 0, stream, act, act_stride, K,
+                       Kp, hi, lo_p, inv, level_step);
+  else if (lo)
+    hipLaunchKernelGGL((act_scale_kernel<false, true>), dim3(M), dim3(kActThreads), 0, stream, act, act_stride, K,
+                       Kp, hi, lo_p, inv, level_step);
   else
-    hipLaunchKernelGGL((gemm_q4_kernel<false, false>), grid, dim3(kGemmThreads), 0, stream, g);
-  return hipGetLastError();
+    hipLaunchKernelGGL((act_scale_kernel<false, false>), dim3(M), dim3(kActThreads), 0, stream, act, act_stride, K,
+                       Kp, hi, lo_p, inv, level_step);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  GemmCodesArgs a;
+  a.a_hi = hi;
+  a.a_lo = lo ? lo_p : nullptr;
+  a.row_inv = inv;
+  a.codes = codes;
+  a.row_stride = row_stride;
+  a.gains = gains;
+  a.gain_stride = gain_stride;
+  a.group_shift = group_shift;
+  a.zero_pairs = zero_pairs;
+  {
+    const _Float16 b_lo = (_Float16)(1024.0f + (float)code_bias);
+    const _Float16 b_hi = (_Float16)(1024.0f + 16.0f * (float)code_bias);
+    a.bias_pair = (uint32_t)__builtin_bit_cast(uint16_t, b_lo) | ((uint32_t)__builtin_bit_cast(uint16_t, b_hi) << 16);
+  }
+  a.out = out;
+  a.out_stride = out_stride;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.Kp = Kp;
+  a.close = cl;
+  const int form = choose_form(M, N, K, lo);
+  const bool rowgain = group_shift >= 31;
+  const bool zero = zero_pairs != nullptr;
+  if (lo) {
+    if (rowgain)
+      return zero ? launch_out<true, true, true>(form, out_bf16, a, stream)
+                  : launch_out<true, true, false>(form, out_bf16, a, stream);
+    return zero ? launch_out<true, false, true>(form, out_bf16, a, stream)
+                : launch_out<true, false, false>(form, out_bf16, a, stream);
+  }
+  if (rowgain)
+    return zero ? launch_out<false, true, true>(form, out_bf16, a, stream)
+                : launch_out<false, true, false>(form, out_bf16, a, stream);
+  return zero ? launch_out<false, false, true>(form, out_bf16, a, stream)
+              : launch_out<false, false, false>(form, out_bf16, a, stream);
 }

@@ -127,21 +127,29 @@ hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_stride, const 
 /* The row close of a calibrated plane's product taken on levels and unit gains:
  * C = quant_step(gains[n] * step * acc, leave) (fp32 C).  With `gains` set the
  * activations are also put on the grid of `step` (their levels) as they are
- * converted.  Only on the large-tile form with fp32 activations and output. */
+ * converted.  fp32 activations and output only. */
 typedef struct igl_gemm_close {
   const float *gains;
   float step;
   float leave;
 } igl_gemm_close;
 
-/* `work`: igl_gemm_work_bytes(M, N, K) bytes (NULL takes the small-tile form);
- * `close` NULL for a plain product. */
-size_t igl_gemm_work_bytes(int M, int N, int K);
+/* The prefill GEMM on 4-bit codes (code_bias 0..15, no flip): shapes it takes
+ * (K a multiple of 64), the workspace it needs, and the form it would pick
+ * (for tests and the bench).  `act_terms`: 1 takes each activation as one
+ * binary16 term after its row's power-of-two scale (exact for bf16
+ * activations and for levels), 2 as hi + lo (fp32 activations to a relative
+ * 2^-22).  `zero_pairs`: NULL, or per (row, group) the binary16 pair
+ * (1024 + code_bias + zero, 1024 + 16 (code_bias + zero)) as one word
+ * (igl_launch_zero_pairs). */
+int igl_gemm_fits(int M, int N, int K);
+size_t igl_gemm_work_bytes(int M, int N, int K, int act_terms);
+int igl_gemm_form(int M, int N, int K, int act_terms);
 hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride, const uint8_t *codes,
                               long long row_stride, const float *gains, int gain_stride,
-                              int group_shift, int code_bias, void *out, int out_bf16,
-                              int out_stride, int M, int N, int K, void *work,
-                              const igl_gemm_close *close, hipStream_t stream);
+                              int group_shift, int code_bias, const uint32_t *zero_pairs, void *out,
+                              int out_bf16, int out_stride, int M, int N, int K, int act_terms,
+                              void *work, const igl_gemm_close *close, hipStream_t stream);
 
 size_t igl_attend_work_floats(int place0, int window, int lanes, int head_count, int head_size);
 /* The device address of the fixed attention workspace on `device`

@@ -110,8 +110,8 @@ def test_plane_lift_dev(backend, lanes):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     ref = ol.oracle_mat_mat(codes, gains, entered, K, threads=8)
     floor = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
-    tol = 2e-3 if lanes >= 64 else 1e-5  # 64 lanes take the binary16-operand MFMA GEMM
-    assert np.max(np.abs(product - ref) / np.maximum(np.abs(ref), floor)) <= tol
+    # from 64 lanes the MFMA GEMM on hi + lo binary16 terms: as close as the GEMV
+    assert np.max(np.abs(product - ref) / np.maximum(np.abs(ref), floor)) <= 1e-5
     for b in (dev_act, out):
         b.free()
     backend.detach(cp)
