@@ -70,6 +70,7 @@ class CodePlane:
     plane: Plane
     codes: np.ndarray  # uint8 [N, row_stride]
     gains: np.ndarray  # float32 [N, G]
+    zeros: np.ndarray | None = None  # int8 [N, G] zero points, kept alive with the plane
 
     @property
     def N(self) -> int:
@@ -81,12 +82,18 @@ class CodePlane:
 
 
 def make_plane(codes: np.ndarray, gains: np.ndarray, K: int, group_size: int = 32,
-               code_bias: int | None = None, bits: int = 4, code_flip: int = 0) -> CodePlane:
+               code_bias: int | None = None, bits: int = 4, code_flip: int = 0,
+               zeros: np.ndarray | None = None) -> CodePlane:
     """A code plane over `codes` [N, row_stride] (bits-wide fields, low bits
     first) and F32 `gains` [N, groups]; code_bias defaults to 2^(bits-1), the
-    export's offset (plane_bind_gemma, app_core.c:7931-7935)."""
+    export's offset (plane_bind_gemma, app_core.c:7931-7935).  `zeros`: int8
+    zero points [N, groups] (plane_bind_part's bias_data, app_core.c:8053-8063),
+    or None for a symmetric plane."""
     codes = np.ascontiguousarray(codes, dtype=np.uint8)
     gains = np.ascontiguousarray(gains, dtype=np.float32)
+    if zeros is not None:
+        zeros = np.ascontiguousarray(zeros, dtype=np.int8)
+        assert zeros.shape == gains.shape
     N = codes.shape[0]
     p = Plane()
     p.form = native.IGL_PLANE_CODE
@@ -96,13 +103,13 @@ def make_plane(codes: np.ndarray, gains: np.ndarray, K: int, group_size: int = 3
     p.row_stride = codes.shape[1]
     p.gain_data = _ptr(gains)
     p.gain_type = native.IGL_STORE_F32
-    p.bias_data = None
+    p.bias_data = None if zeros is None else _ptr(zeros)
     p.bit_count = bits
     p.code_bias = (1 << (bits - 1)) if code_bias is None else code_bias
     p.code_flip = code_flip
     p.group_size = group_size
     p.group_count = gains.shape[1]
-    return CodePlane(p, codes, gains)
+    return CodePlane(p, codes, gains, zeros)
 
 
 def make_real_plane(rows: np.ndarray, real_type: int) -> CodePlane:

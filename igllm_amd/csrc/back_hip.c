@@ -25,6 +25,11 @@ struct igl_device_plane {
   const void  *codes;
   const float *gains;
   int          owned; /* allocated by igl_plane_attach */
+  /* zero points (bias_data), always owned: int8 [rows][groups] for the GEMV,
+   * and for 4-bit unflipped planes the GEMM's binary16 pairs
+   * (1024 + bias + zero, 1024 + 16 (bias + zero)) a word */
+  int8_t      *zeros;
+  uint32_t    *zero_pairs;
 };
 
 struct igl_desk_state {
@@ -192,7 +197,7 @@ static int plane_supported(const igl_plane *sheet) {
   if (!sheet || sheet->form != IGL_PLANE_CODE) return IGL_FAIL_SUPPORT;
   if (sheet->bit_count != 2 && sheet->bit_count != 4 && sheet->bit_count != 8) return IGL_FAIL_SUPPORT;
   if (sheet->code_bias != 1 << (sheet->bit_count - 1) || sheet->code_flip < 0 ||
-      sheet->code_flip >= 1 << sheet->bit_count || sheet->bias_data)
+      sheet->code_flip >= 1 << sheet->bit_count)
     return IGL_FAIL_SUPPORT;
   if (sheet->gain_type != IGL_STORE_F32) return IGL_FAIL_SUPPORT;
   if (sheet->row_count < 1 || sheet->col_count < 32 || (sheet->col_count & 31)) return IGL_FAIL_SUPPORT;
@@ -240,6 +245,49 @@ static int plane_reserve(igl_desk_state *st, const igl_plane *sheet) {
   return grow_out(st, out);
 }
 
+/* The plane's zero points on the device (none without bias_data): the int8
+ * table as it stands, and for 4-bit unflipped planes whose bias + zero stays
+ * in 0..63 the GEMM's binary16 subtrahends, 1024 + (bias + zero) and
+ * 1024 + 16 (bias + zero), exact integers in [1024, 2048) (exponent field 25:
+ * 0x6400 plus the integer). */
+static int attach_zeros(const igl_plane *sheet, igl_device_plane *dp) {
+  const size_t count = (size_t)sheet->row_count * (size_t)sheet->group_count;
+  uint32_t *pairs = NULL;
+  int pairs_ok = sheet->bit_count == 4 && sheet->code_flip == 0;
+  if (sheet->form != IGL_PLANE_CODE || !sheet->bias_data) return IGL_OKAY;
+  if (hipMalloc((void **)&dp->zeros, count) != hipSuccess) return IGL_FAIL_MEMORY;
+  if (hipMemcpy(dp->zeros, sheet->bias_data, count, hipMemcpyHostToDevice) != hipSuccess)
+    return IGL_FAIL_DEVICE;
+  for (size_t i = 0; i < count && pairs_ok; ++i) {
+    const int bz = sheet->code_bias + sheet->bias_data[i];
+    if (bz < 0 || bz > 63) pairs_ok = 0;
+  }
+  if (!pairs_ok) return IGL_OKAY;
+  pairs = (uint32_t *)malloc(count * sizeof(uint32_t));
+  if (!pairs) return IGL_FAIL_MEMORY;
+  for (size_t i = 0; i < count; ++i) {
+    const uint32_t bz = (uint32_t)(sheet->code_bias + sheet->bias_data[i]);
+    pairs[i] = (0x6400u + bz) | ((0x6400u + 16u * bz) << 16);
+  }
+  if (hipMalloc((void **)&dp->zero_pairs, count * sizeof(uint32_t)) != hipSuccess) {
+    free(pairs);
+    return IGL_FAIL_MEMORY;
+  }
+  if (hipMemcpy(dp->zero_pairs, pairs, count * sizeof(uint32_t), hipMemcpyHostToDevice) != hipSuccess) {
+    free(pairs);
+    return IGL_FAIL_DEVICE;
+  }
+  free(pairs);
+  return IGL_OKAY;
+}
+
+static void free_zeros(igl_device_plane *dp) {
+  if (dp->zeros) (void)hipFree(dp->zeros);
+  if (dp->zero_pairs) (void)hipFree(dp->zero_pairs);
+  dp->zeros = NULL;
+  dp->zero_pairs = NULL;
+}
+
 int igl_plane_attach(igl_desk *desk, igl_plane *sheet) {
   igl_desk_state *st = desk ? desk->state : NULL;
   igl_device_plane *dp;
@@ -281,7 +329,8 @@ int igl_plane_attach(igl_desk *desk, igl_plane *sheet) {
   dp->codes = codes;
   dp->gains = (const float *)gains;
   dp->owned = 1;
-  if ((code = plane_reserve(st, sheet)) != IGL_OKAY) {
+  if ((code = attach_zeros(sheet, dp)) != IGL_OKAY || (code = plane_reserve(st, sheet)) != IGL_OKAY) {
+    free_zeros(dp);
     (void)hipFree(codes);
     (void)hipFree(gains);
     free(dp);
@@ -305,7 +354,8 @@ int igl_plane_bind_dev(igl_desk *desk, igl_plane *sheet, const void *code_dev, c
   dp->codes = code_dev;
   dp->gains = gain_dev;
   dp->owned = 0;
-  if ((code = plane_reserve(st, sheet)) != IGL_OKAY) {
+  if ((code = attach_zeros(sheet, dp)) != IGL_OKAY || (code = plane_reserve(st, sheet)) != IGL_OKAY) {
+    free_zeros(dp);
     free(dp);
     return code;
   }
@@ -322,6 +372,7 @@ void igl_plane_detach(igl_desk *desk, igl_plane *sheet) {
     (void)hipFree((void *)dp->codes);
     (void)hipFree((void *)dp->gains);
   }
+  free_zeros(dp);
   free(dp);
   sheet->device = NULL;
 }
@@ -356,6 +407,15 @@ int igl_gemv_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev, i
     return IGL_FAIL_STATE;
   }
   dp = sheet->device;
+  if (dp->zeros) {
+    igl_code_view view = igl_plane_view(sheet, dp->codes, dp->gains);
+    if (((uintptr_t)act_dev & 15u) || (lane_count > 1 && (act_stride & 3))) {
+      desk_fail(st, IGL_FAIL_ARGUMENT);
+      return IGL_FAIL_ARGUMENT;
+    }
+    return hip_check(st, igl_launch_gemv_zero(&view, dp->zeros, act_dev, act_stride, lane_count, out_dev,
+                                              out_stride, sheet->row_count, sheet->col_count, st->stream));
+  }
   if (sheet->form == IGL_PLANE_REAL) {
     if (((uintptr_t)act_dev & 15u) || (lane_count > 1 && (act_stride & 3))) {
       desk_fail(st, IGL_FAIL_ARGUMENT);
@@ -410,7 +470,7 @@ static int gemm_run(igl_desk *desk, const igl_plane *sheet, const void *act_dev,
   return hip_check(st, igl_launch_gemm_q4(act_dev, act_bf16, act_stride, (const uint8_t *)dp->codes,
                                           (long long)sheet->row_stride, dp->gains,
                                           sheet->group_count, igl_plane_group_shift(sheet),
-                                          sheet->code_bias, NULL,
+                                          sheet->code_bias, dp->zero_pairs,
                                           out_dev, out_bf16, out_stride, lane_count,
                                           sheet->row_count, sheet->col_count, terms, st->gemm_dev,
                                           NULL, st->stream));
@@ -424,7 +484,8 @@ int igl_mat_mat_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev
   int code;
   if (!st) return IGL_FAIL_STATE;
   if (lane_count < IGL_GEMM_FLOOR || (sheet && !plane_is_q4(sheet)) ||
-      (sheet && !igl_gemm_fits(lane_count, sheet->row_count, sheet->col_count)))
+      (sheet && !igl_gemm_fits(lane_count, sheet->row_count, sheet->col_count)) ||
+      (sheet && sheet->device && sheet->device->zeros && !sheet->device->zero_pairs))
     return igl_gemv_dev(desk, sheet, act_dev, act_stride, lane_count, out_dev, out_stride);
   if ((code = plane_supported(sheet)) != IGL_OKAY || !sheet->device) {
     code = code != IGL_OKAY ? code : IGL_FAIL_STATE;
@@ -444,7 +505,8 @@ int igl_gemm_bf16_dev(igl_desk *desk, const igl_plane *sheet, const uint16_t *ac
     desk_fail(st, code);
     return code;
   }
-  if (!plane_is_q4(sheet) || !igl_gemm_fits(lane_count, sheet->row_count, sheet->col_count)) {
+  if (!plane_is_q4(sheet) || !igl_gemm_fits(lane_count, sheet->row_count, sheet->col_count) ||
+      (sheet->device->zeros && !sheet->device->zero_pairs)) {
     desk_fail(st, IGL_FAIL_SUPPORT);
     return IGL_FAIL_SUPPORT;
   }
@@ -564,7 +626,7 @@ int igl_plane_lift_dev(igl_desk *desk, const igl_plane *sheet, const float *act_
    * activation grid, entry and leave grids fused, the reference's level path
    * (exact integer sums) rather than the float path on quant_step values. */
   if (sheet->enter_gain > 0.0f && sheet->form == IGL_PLANE_CODE && lane_count < IGL_GEMM_FLOOR &&
-      plane_supported(sheet) == IGL_OKAY && sheet->device &&
+      plane_supported(sheet) == IGL_OKAY && sheet->device && !sheet->device->zeros &&
       igl_gemv_level_fits(sheet->bit_count, sheet->col_count) && ((uintptr_t)act_dev & 15u) == 0 &&
       (lane_count == 1 || (act_stride & 3) == 0)) {
     igl_code_view view = igl_plane_view(sheet, sheet->device->codes, sheet->device->gains);
@@ -573,7 +635,7 @@ int igl_plane_lift_dev(igl_desk *desk, const igl_plane *sheet, const float *act_
                                                sheet->row_count, sheet->col_count, st->stream));
   }
   if (sheet->enter_gain > 0.0f && sheet->form == IGL_PLANE_CODE && lane_count >= IGL_GEMM_FLOOR &&
-      plane_supported(sheet) == IGL_OKAY && sheet->device && sheet->group_count == 1 &&
+      plane_supported(sheet) == IGL_OKAY && sheet->device && !sheet->device->zeros && sheet->group_count == 1 &&
       (igl_gemm_level_fits(sheet->bit_count, sheet->code_bias, sheet->col_count) ||
        igl_gemm_fits(lane_count, sheet->row_count, sheet->col_count)) &&
       ((uintptr_t)act_dev & 15u) == 0 && (act_stride & 3) == 0)

@@ -47,7 +47,7 @@
 
 typedef struct eng_tensor {
   char      name[160];
-  int       dtype;     /* 0 U8, 1 F32, 2 I8, 3 BF16, -1 other */
+  int       dtype;     /* 0 U8, 1 F32, 2 I8, 3 BF16, 4 I32, -1 other */
   int       rank;
   long long shape[3];
   size_t    begin, end;
@@ -227,6 +227,7 @@ static int parse_header(igl_engine *e, const char *h, size_t len) {
                  : strncmp(v, "\"F32\"", 5) == 0  ? 1
                  : strncmp(v, "\"I8\"", 4) == 0   ? 2
                  : strncmp(v, "\"BF16\"", 6) == 0 ? 3
+                 : strncmp(v, "\"I32\"", 5) == 0  ? 4
                                                   : -1;
       v = member(obj, obj_end, "shape");
       if (!v || *v != '[') return IGL_FAIL_FORMAT;
@@ -283,6 +284,15 @@ static float read_scalar(const igl_engine *e, const char *name, float spare) {
  *   `input_activation_scale` / `output_activation_scale`, where present, are
  *   the plane's enter and leave grids (7946-7953);
  *   a BF16 or F32 `weight` [rows, col_hint] with no scale is a real plane. */
+static int bind_packed(igl_engine *e, const char *stem, const eng_tensor *w, igl_plane *out);
+
+/* The tensor whose first dimension is a projection's row count: `weight`, or
+ * the compressed-tensors pack's `weight_packed`. */
+static const eng_tensor *plane_tensor(const igl_engine *e, const char *stem) {
+  const eng_tensor *t = find_stem(e, stem, "weight");
+  return t ? t : find_stem(e, stem, "weight_packed");
+}
+
 static int bind_plane(igl_engine *e, const char *stem, int col_hint, igl_plane *out) {
   static const int widths[] = {8, 4, 2};
   const eng_tensor *w = find_stem(e, stem, "embedding_quantized");
@@ -293,7 +303,10 @@ static int bind_plane(igl_engine *e, const char *stem, int col_hint, igl_plane *
     w = find_stem(e, stem, "weight");
     s = find_stem(e, stem, "weight_scale");
   }
-  if (!w) return IGL_FAIL_MISSING;
+  if (!w) {
+    const eng_tensor *packed = find_stem(e, stem, "weight_packed");
+    return packed ? bind_packed(e, stem, packed, out) : IGL_FAIL_MISSING;
+  }
   memset(out, 0, sizeof(*out));
   if (!s && (w->dtype == 1 || w->dtype == 3)) {
     if (w->rank != 2 || w->shape[1] != col_hint) return IGL_FAIL_FORMAT;
@@ -333,6 +346,91 @@ static int bind_plane(igl_engine *e, const char *stem, int col_hint, igl_plane *
   out->leave_gain = read_scalar(e, name, 0.0f);
   return igl_plane_bind_dev(e->desk, out, e->payload_dev + w->begin,
                             (const float *)(e->payload_dev + s->begin));
+}
+
+void igl_zero_unpack(const uint32_t *words, int groups, int rows, int bits, int8_t *out) {
+  const uint32_t mask = bits >= 32 ? 0xFFFFFFFFu : (1u << bits) - 1u;
+  for (int n = 0; n < rows; ++n) {
+    const size_t first = (size_t)n * (size_t)bits;  /* the row's first bit in its group's column */
+    const size_t word = first >> 5;
+    const int shift = (int)(first & 31u);
+    for (int g = 0; g < groups; ++g) {
+      uint64_t window = words[word * (size_t)groups + (size_t)g];
+      if (shift + bits > 32) window |= (uint64_t)words[(word + 1) * (size_t)groups + (size_t)g] << 32;
+      out[(size_t)n * (size_t)groups + (size_t)g] =
+          (int8_t)((int)((window >> shift) & mask) - (1 << (bits - 1)));
+    }
+  }
+}
+
+/* A plane in the compressed-tensors pack (plane_bind_part's packed branch,
+ * app_core.c:8015-8065), bound in place on the device copy of the payload:
+ * `weight_packed` I32 [rows, words] holds each row as a dense little-endian
+ * bit stream (the same stream a U8 row holds, in whole 32-bit words); the
+ * input width is the last entry of `weight_shape`; the bit width is the one
+ * that makes ceil(cols * bits / 32) come out to `words`; `weight_scale` F32
+ * [rows, G] has group_size ceil(cols / G); codes are stored value + 2^(bits-1)
+ * with no flip; an optional `weight_zero_point` I32 [ceil(rows * bits / 32), G]
+ * packs each group's zero points along the rows (zero_read 7855-7866), here
+ * unpacked once into the plane's bias_data (owned: own_block). */
+static int bind_packed(igl_engine *e, const char *stem, const eng_tensor *w, igl_plane *out) {
+  const eng_tensor *s = find_stem(e, stem, "weight_scale");
+  const eng_tensor *shape = find_stem(e, stem, "weight_shape");
+  const eng_tensor *zero = find_stem(e, stem, "weight_zero_point");
+  char name[320];
+  int bits = 0, cols, groups, words, rows;
+  memset(out, 0, sizeof(*out));
+  if (!s) return IGL_FAIL_MISSING;
+  if (w->dtype != 4 || w->rank != 2 || s->dtype != 1 || s->rank < 1 || s->rank > 2) return IGL_FAIL_SUPPORT;
+  if (!shape || shape->dtype != 4 || shape->rank != 1 || shape->shape[0] < 2) return IGL_FAIL_FORMAT;
+  {
+    int32_t last;
+    memcpy(&last, (const uint8_t *)e->map + e->payload_at + shape->begin + 4 * (shape->shape[0] - 1), 4);
+    cols = last;
+  }
+  rows = (int)w->shape[0];
+  words = (int)w->shape[1];
+  for (int b = 1; b <= 8 && !bits; ++b)
+    if (((long long)cols * b + 31) / 32 == words) bits = b;
+  groups = s->rank == 2 ? (int)s->shape[1] : 1;
+  if (!bits || cols < 1 || groups < 1 || s->shape[0] != rows) return IGL_FAIL_FORMAT;
+  out->form = IGL_PLANE_CODE;
+  out->row_count = rows;
+  out->col_count = cols;
+  out->code_data = (const uint8_t *)e->map + e->payload_at + w->begin;
+  out->row_stride = (size_t)words * 4u;
+  out->gain_data = (const uint8_t *)e->map + e->payload_at + s->begin;
+  out->gain_type = IGL_STORE_F32;
+  out->bit_count = bits;
+  out->code_bias = 1 << (bits - 1);
+  out->code_flip = 0;
+  out->group_count = groups;
+  out->group_size = (cols + groups - 1) / groups;
+  if (zero) {
+    int8_t *table;
+    if (zero->dtype != 4 || zero->rank != 2 || zero->shape[1] != groups ||
+        zero->shape[0] != ((long long)rows * bits + 31) / 32)
+      return IGL_FAIL_FORMAT;
+    table = (int8_t *)malloc((size_t)rows * (size_t)groups);
+    if (!table) return IGL_FAIL_MEMORY;
+    igl_zero_unpack((const uint32_t *)((const uint8_t *)e->map + e->payload_at + zero->begin), groups, rows, bits,
+                    table);
+    out->bias_data = table;
+    out->own_block = table;
+  }
+  snprintf(name, sizeof(name), "%s.input_activation_scale", stem);
+  out->enter_gain = read_scalar(e, name, 0.0f);
+  snprintf(name, sizeof(name), "%s.output_activation_scale", stem);
+  out->leave_gain = read_scalar(e, name, 0.0f);
+  return igl_plane_bind_dev(e->desk, out, e->payload_dev + w->begin, (const float *)(e->payload_dev + s->begin));
+}
+
+/* Detaches a plane and frees what the binder unpacked for it. */
+static void drop_plane(igl_engine *e, igl_plane *p) {
+  igl_plane_detach(e->desk, p);
+  free(p->own_block);
+  p->own_block = NULL;
+  p->bias_data = NULL;
 }
 
 static const float *bind_vector(igl_engine *e, const char *stem, int n) {
@@ -478,6 +576,12 @@ int igl_engine_open(igl_engine **out, igl_desk *desk, const char *folder, int wi
       (code = bind_plane(e, STEM("%sembed_tokens_per_layer", prefix), e->layers * e->ple, &e->ple_embed)) != IGL_OKAY ||
       (code = bind_plane(e, STEM("%sper_layer_model_projection", prefix), e->hidden, &e->ple_lift)) != IGL_OKAY)
     goto fail;
+  /* the embedding gathers decode rows without zero points (the exports keep
+   * the embeddings symmetric or float) */
+  if (e->embed.bias_data || e->ple_embed.bias_data) {
+    code = IGL_FAIL_SUPPORT;
+    goto fail;
+  }
   if (bind_plane(e, "lm_head", e->hidden, &e->head) != IGL_OKAY &&
       bind_plane(e, STEM("%slm_head", prefix), e->hidden, &e->head) != IGL_OKAY)
     e->head = e->embed;
@@ -506,11 +610,11 @@ int igl_engine_open(igl_engine **out, igl_desk *desk, const char *folder, int wi
           if (e->layer[j].full == L->full) last = j;
         L->keep = e->share_count > 0 && last == i;
       }
-      t = find_tensor(e, STEM("%slayers.%d.self_attn.q_proj.weight", prefix, i));
+      t = plane_tensor(e, STEM("%slayers.%d.self_attn.q_proj", prefix, i));
       if (!t) { code = IGL_FAIL_MISSING; goto fail; }
       L->head_size = (int)t->shape[0] / e->heads;
       if (L->head_size != 256 && L->head_size != 512) { code = IGL_FAIL_SUPPORT; goto fail; }
-      t = find_tensor(e, STEM("%slayers.%d.mlp.gate_proj.weight", prefix, i));
+      t = plane_tensor(e, STEM("%slayers.%d.mlp.gate_proj", prefix, i));
       if (!t) { code = IGL_FAIL_MISSING; goto fail; }
       L->inner = (int)t->shape[0];
       if (L->inner > e->inner_max) e->inner_max = L->inner;
@@ -622,15 +726,18 @@ void igl_engine_close(igl_engine *e) {
   for (int i = 0; i < e->layers && i < ENG_LAYER_LIMIT; ++i) {
     eng_layer *L = &e->layer[i];
     igl_plane *pl[] = {&L->q, &L->k, &L->v, &L->o, &L->gate, &L->up, &L->down, &L->ple_gate, &L->ple_proj};
-    for (size_t j = 0; j < sizeof(pl) / sizeof(pl[0]); ++j) igl_plane_detach(e->desk, pl[j]);
+    for (size_t j = 0; j < sizeof(pl) / sizeof(pl[0]); ++j) drop_plane(e, pl[j]);
     if (L->k_store) (void)hipFree(L->k_store);
     if (L->v_store) (void)hipFree(L->v_store);
   }
-  if (e->head.device == e->embed.device) e->head.device = NULL;
-  igl_plane_detach(e->desk, &e->embed);
-  igl_plane_detach(e->desk, &e->ple_embed);
-  igl_plane_detach(e->desk, &e->ple_lift);
-  igl_plane_detach(e->desk, &e->head);
+  if (e->head.device == e->embed.device) {
+    e->head.device = NULL;
+    e->head.own_block = NULL;
+  }
+  drop_plane(e, &e->embed);
+  drop_plane(e, &e->ple_embed);
+  drop_plane(e, &e->ple_lift);
+  drop_plane(e, &e->head);
   if (e->graph_ready) (void)hipGraphExecDestroy(e->graph);
   {
     void *bufs[] = {e->payload_dev, e->ctl_dev, e->attend_work, e->state_buf[0],
@@ -686,7 +793,7 @@ static int project(igl_engine *e, const igl_plane *p, const float *act, int act_
  * fused into the store: the same kernel and the same arithmetic, one launch
  * fewer.  0 where that route does not take the plane. */
 static int level_epi_fits(const igl_plane *p, const float *act, int lanes) {
-  return lanes == 1 && p->form == IGL_PLANE_CODE && p->enter_gain > 0.0f && p->device &&
+  return lanes == 1 && p->form == IGL_PLANE_CODE && p->enter_gain > 0.0f && p->device && !p->bias_data &&
          igl_gemv_level_fits(p->bit_count, p->col_count) && ((uintptr_t)act & 15u) == 0;
 }
 
@@ -702,7 +809,7 @@ static int project_level_epi(igl_engine *e, const igl_plane *p, const float *act
  * in the launch's prologue (igl_launch_gemv_level_pro): x is also written to
  * x_out (NULL: not kept) for the planes that read it next. */
 static int level_pro_fits(const igl_engine *e, const igl_plane *p) {
-  return p->form == IGL_PLANE_CODE && p->enter_gain > 0.0f && p->device &&
+  return p->form == IGL_PLANE_CODE && p->enter_gain > 0.0f && p->device && !p->bias_data &&
          igl_gemv_level_fits(p->bit_count, p->col_count) && p->col_count == e->hidden &&
          p->col_count <= 2048;
 }
@@ -786,7 +893,7 @@ static int group_fits(const eng_group *g, const igl_plane *const *p, int mode) {
     if (p[i]->col_count != p[0]->col_count || p[i]->group_size != p[0]->group_size ||
         p[i]->group_count != p[0]->group_count || p[i]->code_bias != p[0]->code_bias ||
         p[i]->bit_count != 4 || p[i]->code_flip != 0 || p[i]->col_count > 8192 ||
-        p[i]->enter_gain > 0.0f || p[i]->leave_gain > 0.0f)
+        p[i]->enter_gain > 0.0f || p[i]->leave_gain > 0.0f || p[i]->bias_data)
       return 0;
     if (mode == IGL_GEMV_SEGMENTS && i + 1 < g->count && p[i]->row_count % 4) return 0;
   }

@@ -32,18 +32,23 @@
 
 typedef struct gemma_tensor {
   char   name[160];
-  int    dtype;       /* 0 = U8, 1 = F32, 2 = I8, 3 = BF16 */
+  int    dtype;       /* 0 = U8, 1 = F32, 2 = I8, 3 = BF16, 4 = I32 */
   int    rank;
   long long shape[2];
   size_t offset;      /* within the payload */
   size_t bytes;
   int    fill;        /* 0 codes, 1 scales, 2 norm gain, 3 layer scalar, 4 cache scale,
                          5 the constant `value`, 6 scales value * U(0.75, 1.25), 7 bf16 N(0, value),
-                         8 scales value * U(0.99, 1.01), 9 2-bit codes of mean value 0 */
+                         8 scales value * U(0.99, 1.01), 9 2-bit codes of mean value 0,
+                         10 zero points packed along rows (`value` bits, `rows` rows),
+                         11 the I32 pair `rows`, `cols`,
+                         12 codes centred on each group's zero point (`value` bits,
+                            `rows` x `cols`) */
   float  value;
+  long long rows, cols;
 } gemma_tensor;
 
-static const char *const k_dtype_name[] = {"U8", "F32", "I8", "BF16"};
+static const char *const k_dtype_name[] = {"U8", "F32", "I8", "BF16", "I32"};
 
 typedef struct gemma_list {
   gemma_tensor item[GEMMA_TENSOR_LIMIT];
@@ -91,7 +96,7 @@ static int add_tensor(gemma_list *list, const char *name, int dtype, int rank, l
   t->rank = rank;
   t->shape[0] = d0;
   t->shape[1] = d1;
-  t->bytes = elems * (dtype == 1 ? 4u : dtype == 3 ? 2u : 1u);
+  t->bytes = elems * (dtype == 1 || dtype == 4 ? 4u : dtype == 3 ? 2u : 1u);
   t->offset = list->payload;
   t->fill = fill;
   list->payload += (t->bytes + GEMMA_ALIGN - 1) / GEMMA_ALIGN * GEMMA_ALIGN;
@@ -135,6 +140,35 @@ static int add_plane_kind(gemma_list *list, const char *stem, long long rows, lo
   return IGL_OKAY;
 }
 
+/* A plane in the compressed-tensors pack (plane_bind_part's packed branch,
+ * app_core.c:8015-8065): `weight_packed` I32 [rows, cols * bits / 32] (the
+ * same dense little-endian rows, codes value + 2^(bits-1)), `weight_scale` F32
+ * [rows, cols / 32] (group 32), `weight_shape` I32 [rows, cols] and
+ * `weight_zero_point` I32 [ceil(rows * bits / 32), cols / 32], each group's
+ * zero points packed along the rows (zero_read, 7855-7866). */
+static int add_plane_packed(gemma_list *list, const char *stem, long long rows, long long cols, int bits,
+                            float gain_std) {
+  char name[200];
+  int code;
+  snprintf(name, sizeof(name), "%s.weight_packed", stem);
+  if ((code = add_tensor(list, name, 4, 2, rows, cols * bits / 32, 12)) != IGL_OKAY) return code;
+  list->item[list->count - 1].value = (float)bits;
+  list->item[list->count - 1].rows = rows;
+  list->item[list->count - 1].cols = cols;
+  snprintf(name, sizeof(name), "%s.weight_scale", stem);
+  if ((code = add_tensor(list, name, 1, 2, rows, cols / 32, 6)) != IGL_OKAY) return code;
+  list->item[list->count - 1].value = gain_std;
+  snprintf(name, sizeof(name), "%s.weight_shape", stem);
+  if ((code = add_tensor(list, name, 4, 1, 2, 0, 11)) != IGL_OKAY) return code;
+  list->item[list->count - 1].rows = rows;
+  list->item[list->count - 1].cols = cols;
+  snprintf(name, sizeof(name), "%s.weight_zero_point", stem);
+  if ((code = add_tensor(list, name, 4, 2, (rows * bits + 31) / 32, cols / 32, 10)) != IGL_OKAY) return code;
+  list->item[list->count - 1].value = (float)bits;
+  list->item[list->count - 1].rows = rows;
+  return IGL_OKAY;
+}
+
 static int add_vector(gemma_list *list, const char *stem, long long n, int fill) {
   char name[200];
   snprintf(name, sizeof(name), "%s.weight", stem);
@@ -150,7 +184,7 @@ static int igl_gemma_layout(const igl_gemma_shape *s, gemma_list *list) {
   memset(list, 0, sizeof(*list));
   if (s->hidden % 32 || s->inner % 32 || s->ple_size % 32 || s->head_dim % 32 || s->full_head_dim % 32)
     return IGL_FAIL_ARGUMENT;
-  if (s->kinds) {
+  if (s->kinds == 1) {
     /* the export's kinds: 2-bit embedding (the head, tied), 4-bit per-layer
      * embedding with a scale column per layer, bf16 per_layer_model_projection */
     /* the tied head's rows: 2-bit values average -0.5, so scales that differ
@@ -183,9 +217,17 @@ static int igl_gemma_layout(const igl_gemma_shape *s, gemma_list *list) {
     const int mlp_bits = i < 15 ? 4 : 2;
     const float mlp_std = mlp_bits == 4 ? 0.02f : 0.05f;
 #define L(fmt) (snprintf(stem, sizeof(stem), P "layers.%d." fmt, i), stem)
-#define PLANE(name, rows, cols, bits, i8, std, enter, leave)                                       \
-  (s->kinds ? add_plane_kind(list, L(name), rows, cols, 0, bits, i8, 1, std, enter, leave)         \
-            : add_plane(list, L(name), rows, cols, 0))
+    /* the compressed-tensors pack: 4-bit attention, MLPs of the first half
+     * 4-bit and the rest 2-bit, 8-bit per-layer planes, every one with zero
+     * points */
+    const int pack_mlp = i < s->layers / 2 ? 4 : 2;
+#define PLANE(name, rows, cols, bits, i8, std, enter, leave)                                                  \
+  (s->kinds == 1   ? add_plane_kind(list, L(name), rows, cols, 0, bits, i8, 1, std, enter, leave)            \
+   : s->kinds == 2 ? add_plane_packed(list, L(name), rows, cols,                                             \
+                                      (bits) == 8 ? 8 : strstr(name, "mlp.") ? pack_mlp : 4,                 \
+                                      (bits) == 8 ? 0.0012f : strstr(name, "mlp.") && pack_mlp == 2 ? 0.05f  \
+                                                                                               : 0.02f)    \
+                   : add_plane(list, L(name), rows, cols, 0))
     code |= PLANE("self_attn.q_proj", (long long)s->heads * hd, s->hidden, 4, 0, 0.02f, 0.04f, 0.04f);
     if (!shared) {
       code |= PLANE("self_attn.k_proj", (long long)s->kv_heads * hd, s->hidden, 4, 0, 0.02f, 0.04f, 0.04f);
@@ -214,7 +256,7 @@ static int igl_gemma_layout(const igl_gemma_shape *s, gemma_list *list) {
 #undef L
     if (code) return IGL_FAIL_SUPPORT;
   }
-  if (!s->kinds && add_plane(list, "lm_head", s->vocab, s->hidden, 0)) return IGL_FAIL_SUPPORT;
+  if (s->kinds != 1 && add_plane(list, "lm_head", s->vocab, s->hidden, 0)) return IGL_FAIL_SUPPORT;
   return IGL_OKAY;
 }
 
@@ -294,6 +336,69 @@ static void fill_codes2(igl_rng *rng, uint8_t *dst, size_t count) {
       dst[i] = v;
     }
   }
+}
+
+/* The zero point of row r, group g of a packed plane: -1 throughout.  Zero
+ * points that vary from row to row or group to group give each its own mean
+ * weight (c - bias - zero averages -0.5 - zero on uniform codes) and make
+ * this random model's stream chaotic under the byte cache: the reference's
+ * own SSE2 and AVX2 builds then part within a few steps.  Varying zero points
+ * are the projection tests' business. */
+static int zero_of(long long r, long long g) {
+  (void)r;
+  (void)g;
+  return -1;
+}
+
+/* Zero points of a packed plane, I32 [words][groups]: each word of group g
+ * holds rows 32/bits w .. + 32/bits - 1, `bits` each, low bits first, stored
+ * value + 2^(bits-1); rows past the plane hold 0. */
+static void fill_zeros(uint32_t *dst, long long words, long long groups, long long rows, int bits) {
+  const int per = 32 / bits;
+  const int bias = 1 << (bits - 1);
+  for (long long w = 0; w < words; ++w)
+    for (long long g = 0; g < groups; ++g) {
+      uint32_t word = 0;
+      for (int r = 0; r < per; ++r) {
+        const int z = w * per + r < rows ? zero_of(w * per + r, g) : 0;
+        word |= (uint32_t)(z + bias) << (bits * r);
+      }
+      dst[w * groups + g] = word;
+    }
+}
+
+/* Codes of a packed plane, rows of cols * bits / 8 bytes, low bits first:
+ * c = 2^(bits-1) + zero + d, one field of a draw a code: 4 and 8 bits d
+ * uniform over -2^(bits-1) .. 2^(bits-1) - 1 (the symmetric planes' values,
+ * moved by the zero point; a code below 0 wraps to the top), 2 bits
+ * d = -1, 0, 0, 1. */
+static void fill_codes_centred(igl_rng *rng, uint8_t *dst, long long rows, long long cols, int bits) {
+  const int field = bits == 2 ? 2 : bits == 4 ? 4 : 8;
+  const int per_draw = 64 / field;
+  const size_t row_bytes = (size_t)(cols * bits / 8);
+  uint64_t draw = 0;
+  int left = 0;
+  memset(dst, 0, (size_t)rows * row_bytes);
+  for (long long r = 0; r < rows; ++r)
+    for (long long k = 0; k < cols; ++k) {
+      int v, d;
+      if (!left) {
+        draw = igl_rng_next(rng);
+        left = per_draw;
+      }
+      v = (int)(draw & ((1u << field) - 1u));
+      draw >>= field;
+      --left;
+      if (bits == 2) d = v == 0 ? -1 : v == 3 ? 1 : 0;
+      else if (bits == 4) d = v - 8;
+      else d = v - 128;
+      if ((1 << (bits - 1)) + zero_of(r, k / 32) + d < 0) d += 1 << bits;
+      {
+        const uint32_t c = (uint32_t)((1 << (bits - 1)) + zero_of(r, k / 32) + d);
+        const size_t bit = (size_t)k * (size_t)bits;
+        dst[(size_t)r * row_bytes + bit / 8] |= (uint8_t)(c << (bit % 8));
+      }
+    }
 }
 
 /* Fills `count` bytes of codes: 16 nibbles a draw, low nibble first. */
@@ -383,6 +488,15 @@ int igl_gemma_write(const char *folder, const igl_gemma_shape *shape, uint64_t s
           fill_codes(&rng, buf, take);
         } else if (x->fill == 9) {
           fill_codes2(&rng, buf, take);
+        } else if (x->fill == 10) {
+          if (x->bytes > buf_cap) { code = IGL_FAIL_SUPPORT; goto done; }
+          fill_zeros((uint32_t *)buf, x->shape[0], x->shape[1], x->rows, (int)x->value);
+        } else if (x->fill == 12) {
+          if (x->bytes > buf_cap) { code = IGL_FAIL_SUPPORT; goto done; }
+          fill_codes_centred(&rng, buf, x->rows, x->cols, (int)x->value);
+        } else if (x->fill == 11) {
+          const int32_t pair[2] = {(int32_t)x->rows, (int32_t)x->cols};
+          memcpy(buf, pair, sizeof(pair));
         } else {
           float *v = (float *)buf;
           size_t n = take / 4;

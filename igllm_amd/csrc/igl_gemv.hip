@@ -2161,6 +2161,96 @@ static hipError_t gemv_mfma_dispatch(const GemvMfmaArgs &a, const GemvMfmaPlan &
   }
 }
 
+// ---- planes with zero points -----------------------------------------------
+//
+// An asymmetric plane carries a zero point a row and group (plane_bind_part's
+// weight_zero_point, unpacked by zero_read, app_core.c:7855-7866, 8053-8063).
+// It is multiplied in kern_row_code's own form (app_core.c:3688-3706): for
+// each group of a row,
+//     y += gain * (dot - (code_bias + zero) * sum),
+// dot = sum x_k (c_k ^ flip) over the group's codes and sum = sum x_k, in fp32.
+// A wave takes one row; its lanes take the row's 32-code units in turn (a
+// group of 32 2^s codes closes as its 2^s units, each on the group's gain and
+// zero: the same terms, associated differently) and their partials meet in
+// DPP sums.  A plain fp32 form: zero points are a storage format of the
+// compressed-tensors export, not of the shipped Gemma one, and this kernel
+// does not carry a headline workload.
+struct GemvZeroArgs {
+  const uint8_t *codes;
+  long long row_stride;
+  const float *gains;     // [N][gain_stride]
+  const int8_t *zeros;    // [N][gain_stride]
+  int gain_stride;
+  int group_shift;
+  int code_bias;
+  uint32_t code_flip;
+  const float *act;       // 16-byte aligned, act_stride % 4 == 0
+  int act_stride;
+  int lanes;              // <= M: lanes past it reread the last one and are not stored
+  float *out;
+  int out_stride;
+  int N, K;
+};
+
+template <int BITS, int M>
+__global__ __launch_bounds__(kGemvThreads) void gemv_zero_kernel(GemvZeroArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * (kGemvThreads / 64) + (threadIdx.x >> 6);
+  if (row >= a.N) return;  // a whole wave
+  const int units = a.K >> 5;
+  const uint8_t *crow = a.codes + (size_t)row * (size_t)a.row_stride;
+  float acc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+  for (int u = lane; u < units; u += 64) {
+    uint32_t w[BITS];
+#pragma unroll
+    for (int i = 0; i < BITS; ++i) w[i] = reinterpret_cast<const uint32_t *>(crow + (size_t)u * BITS * 4)[i];
+    const size_t slot = (size_t)row * (size_t)a.gain_stride + ((unsigned)u >> a.group_shift);
+    const float gain = a.gains[slot];
+    const float bias = (float)(a.code_bias + (int)a.zeros[slot]);
+    float c[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k)
+      c[k] = (float)(((w[(k * BITS) >> 5] >> ((k * BITS) & 31)) & ((1u << BITS) - 1u)) ^ a.code_flip);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float4_t *x = reinterpret_cast<const float4_t *>(a.act + (size_t)min(m, a.lanes - 1) * a.act_stride +
+                                                             32 * (size_t)u);
+      float dot = 0.0f, sum = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float4_t v = x[q];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          dot = __builtin_fmaf(v[e], c[4 * q + e], dot);
+          sum += v[e];
+        }
+      }
+      acc[m] = __builtin_fmaf(gain, __builtin_fmaf(-bias, sum, dot), acc[m]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const float v = wave_sum_to_last(acc[m]);
+    if (lane == 63 && m < a.lanes) a.out[(size_t)m * a.out_stride + row] = v;
+  }
+}
+
+template <int BITS>
+static hipError_t gemv_zero_launch_bits(const GemvZeroArgs &a, hipStream_t stream) {
+  const dim3 grid((a.N + kGemvThreads / 64 - 1) / (kGemvThreads / 64));
+  if (a.lanes <= 1)
+    hipLaunchKernelGGL((gemv_zero_kernel<BITS, 1>), grid, dim3(kGemvThreads), 0, stream, a);
+  else if (a.lanes <= 2)
+    hipLaunchKernelGGL((gemv_zero_kernel<BITS, 2>), grid, dim3(kGemvThreads), 0, stream, a);
+  else if (a.lanes <= 4)
+    hipLaunchKernelGGL((gemv_zero_kernel<BITS, 4>), grid, dim3(kGemvThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((gemv_zero_kernel<BITS, 8>), grid, dim3(kGemvThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
 template <int M, int R, int UPL, int GPT>
 static hipError_t gemv_dot_launch_gpt(const GemvArgs &a, hipStream_t stream) {
   const int tiles = (a.N + R - 1) / R;
@@ -3150,4 +3240,36 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
   hipLaunchKernelGGL(gemv_chunk_sum_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, part,
                      chunks, lanes, N, out, out_stride);
   return hipGetLastError();
+}
+
+extern "C" hipError_t igl_launch_gemv_zero(const igl_code_view *v, const int8_t *zeros, const float *act,
+                                           int act_stride, int lanes, float *out, int out_stride, int N, int K,
+                                           hipStream_t stream) {
+  const int bits = v->bit_count;
+  if ((bits != 2 && bits != 4 && bits != 8) || K % 32 || !zeros || (((uintptr_t)act) & 15u) ||
+      (lanes > 1 && (act_stride & 3)) || (v->row_stride & 7) || N < 1 || lanes < 1)
+    return hipErrorInvalidValue;
+  GemvZeroArgs a;
+  a.codes = v->codes;
+  a.row_stride = v->row_stride;
+  a.gains = v->gains;
+  a.zeros = zeros;
+  a.gain_stride = v->gain_stride;
+  a.group_shift = v->group_shift;
+  a.code_bias = v->code_bias;
+  a.code_flip = (uint32_t)v->code_flip;
+  a.act_stride = act_stride;
+  a.out_stride = out_stride;
+  a.N = N;
+  a.K = K;
+  for (int done = 0; done < lanes; done += 8) {
+    a.act = act + (size_t)done * (size_t)act_stride;
+    a.out = out + (size_t)done * (size_t)out_stride;
+    a.lanes = lanes - done < 8 ? lanes - done : 8;
+    const hipError_t e = bits == 2   ? gemv_zero_launch_bits<2>(a, stream)
+                         : bits == 4 ? gemv_zero_launch_bits<4>(a, stream)
+                                     : gemv_zero_launch_bits<8>(a, stream);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }

@@ -52,6 +52,11 @@ static inline igl_code_view igl_plane_view(const igl_plane *sheet, const void *c
 }
 
 size_t igl_gemv_code_part_floats(int bit_count, int lanes, int N, int K);
+/* A plane with zero points (`zeros` [N][gain_stride], int8): kern_row_code's
+ * form, gain * (dot - (code_bias + zero) * sum) a group, any lane count. */
+hipError_t igl_launch_gemv_zero(const igl_code_view *v, const int8_t *zeros, const float *act,
+                                int act_stride, int lanes, float *out, int out_stride, int N, int K,
+                                hipStream_t stream);
 hipError_t igl_launch_gemv_codes(const igl_code_view *v, const float *act, int act_stride,
                                  int lanes, float *out, int out_stride, int N, int K,
                                  float *part, hipStream_t stream);

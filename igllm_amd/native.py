@@ -126,6 +126,7 @@ SIGNATURES = {
     "igl_gemma_shape_e2b": (None, [ctypes.POINTER(GemmaShape)]),
     "igl_gemma_full_layer": (_I, [ctypes.POINTER(GemmaShape), _I]),
     "igl_gemma_write": (_I, [ctypes.c_char_p, ctypes.POINTER(GemmaShape), ctypes.c_uint64]),
+    "igl_zero_unpack": (None, [_P, _I, _I, _I, _P]),
     "igl_engine_open": (_I, [ctypes.POINTER(_P), ctypes.POINTER(Desk), ctypes.c_char_p, _I, _I, _I]),
     "igl_engine_close": (None, [_P]),
     "igl_engine_prime": (_I, [_P, _P, _I]),

@@ -129,8 +129,12 @@ const char *igl_code_text(int code);
 /* Copies a plane's bytes (and gains) to the device unchanged and sets
  * `sheet->device`.  Supported code planes: 2, 4 or 8-bit codes with
  * code_bias 2^(bits-1) and any code_flip (the export's signed I8 planes flip
- * 128), F32 gains, no zero points, group_size a power-of-two multiple of 32 or
+ * 128), F32 gains, optional int8 zero points (bias_data [rows][groups], as
+ * plane_bind_part unpacks weight_zero_point, app_core.c:8053-8063; copied to
+ * the device with the plane), group_size a power-of-two multiple of 32 or
  * one group a row, col_count a multiple of 32, row_stride a multiple of 16.
+ * A row_stride of whole 32-bit words is the compressed-tensors weight_packed
+ * layout (8015-8065): the same dense bit stream. 
  * Supported real planes (plane_bind_part's `weight` of a float type,
  * app_core.c:7985-7998): F32, F16 or BF16 rows, col_count a multiple of 8.
  * Anything else is IGL_FAIL_SUPPORT. */
@@ -287,7 +291,9 @@ typedef struct igl_gemma_shape {
   int   vocab, hidden, inner, layers, heads, kv_heads, head_dim, full_head_dim;
   int   window, ple_size, shared_layers, double_wide, full_every, max_positions;
   int   cache_scales;  /* write k/v_cache_scale so a byte cache is used */
-  int   kinds;         /* 0: int4 group-32 planes everywhere; 1: the export's own kinds */
+  int   kinds;         /* 0: int4 group-32 planes everywhere; 1: the export's own kinds;
+                          2: the layer projections in the compressed-tensors pack
+                          (I32 weight_packed, weight_shape, weight_zero_point) */
   float norm_eps, logit_cap, rope_local, rope_global, partial_rotary;
 } igl_gemma_shape;
 
@@ -299,6 +305,13 @@ int  igl_gemma_full_layer(const igl_gemma_shape *shape, int layer);
 /* Writes config.json, tokenizer.json and model.safetensors (int4 group-32
  * planes in the export's U8 + F32-scale layout) into `folder`, seeded. */
 int  igl_gemma_write(const char *folder, const igl_gemma_shape *shape, uint64_t seed);
+
+/* zero_read (app_core.c:7855-7866) over a whole plane: `words` is a
+ * weight_zero_point tensor, I32 [ceil(rows * bits / 32)][groups], each group's
+ * zero points packed along the rows, low bits first, stored value +
+ * 2^(bits-1); `out` receives them as int8 [rows][groups] (the plane's
+ * bias_data, as plane_bind_part fills it, 8053-8063). */
+void igl_zero_unpack(const uint32_t *words, int groups, int rows, int bits, int8_t *out);
 
 /* ---- a device-resident decode session ------------------------------------- */
 

@@ -59,6 +59,13 @@ uint32_t ref_pack_read(const uint8_t *code_data, size_t element_index, int bit_c
   return pack_read(code_data, element_index, bit_count);
 }
 
+/* zero_read (app_core.c:7855-7866): a row's zero point in a weight_zero_point
+ * tensor packed along rows. */
+int ref_zero_read(const uint32_t *word_list, int group_count, int group_index, int row_index,
+                  int bit_count) {
+  return zero_read(word_list, group_count, group_index, row_index, bit_count);
+}
+
 void ref_plane_row(const ref_plane_desc *desc, int row_index, float *row_out) {
   plane sheet;
   ref_plane_fill(desc, &sheet);

@@ -9,6 +9,7 @@ by oracle/Makefile), run on this repository's seeded synthetic checkpoint.
     python tests/golden/make_e2e_golden.py small_long    # 8300-id prompt, 12000-position window
     python tests/golden/make_e2e_golden.py small_kinds   # the export's plane kinds, 20 layers
     python tests/golden/make_e2e_golden.py e2b_logits    # config.json dimensions, whole logit rows
+    python tests/golden/make_e2e_golden.py small_packed  # I32-packed planes with zero points
 
 For each, the checkpoint is written with igl_gemma_write (seed 0) into a
 scratch folder, the prompt is drawn by igllm_amd.engine.prompt_ids, and the
@@ -52,6 +53,10 @@ CASES = {
     # one scale a row, every projection but the head calibrated
     "small_kinds": dict(shape=dict(vocab=4096, hidden=512, inner=1024, layers=20, shared_layers=8, kinds=1),
                         prompt=600, gen=128, window=1024),
+    # the compressed-tensors pack: weight_packed I32 + weight_shape + weight_zero_point
+    # on every layer projection (4-bit, 2-bit MLPs from the middle layer, 8-bit
+    # per-layer planes), zero points on all of them
+    "small_packed": dict(shape=dict(SMALL, kinds=2), prompt=600, gen=128, window=1024, seed=1),
 }
 
 PATHS = {"plain": oracle_lib.REF_PLAIN_PATH, "tuned": oracle_lib.REF_TUNED_PATH,
@@ -127,9 +132,9 @@ def main():
     case = CASES[name]
     threads = int(os.environ.get("IGL_THREADS", os.cpu_count() or 4))
     folder = os.path.join(tempfile.gettempdir(), f"igl_gemma_{name}")
-    shape = write_gemma(folder, seed=0, **case["shape"])
+    shape = write_gemma(folder, seed=case.get("seed", 0), **case["shape"])
     prompt = prompt_ids(case["prompt"], shape.vocab, seed=0, repeat_span=case.get("repeat", 0))
-    result = {"case": name, "seed": 0, "prompt_seed": 0, "prompt_count": case["prompt"],
+    result = {"case": name, "seed": case.get("seed", 0), "prompt_seed": 0, "prompt_count": case["prompt"],
               "gen": case["gen"], "window_limit": case["window"], "cache_bits": 8,
               "repeat_span": case.get("repeat", 0), "guess_span": case.get("span", 0),
               "shape": {k: getattr(shape, k) for k, _ in shape._fields_}}
@@ -179,7 +184,7 @@ def main():
         print("agree", result["streams_agree"], "guess == greedy", result["guess_equals_greedy"])
         return
     kinds = ("plain", "tuned")
-    if case["shape"].get("kinds") and oracle_lib.ref("level") is not None:
+    if case["shape"].get("kinds") == 1 and oracle_lib.ref("level") is not None:
         kinds += ("level",)
     for kind in kinds:
         ids, margin, secs = ref_stream(kind, folder, prompt, case["gen"], case["window"], threads)

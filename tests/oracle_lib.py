@@ -71,6 +71,7 @@ ORACLE_SIGS = {
 REF_SIGS = {
     "ref_flavor": (ctypes.c_char_p, []),
     "ref_pack_read": (ctypes.c_uint32, [_P, _Z, _I]),
+    "ref_zero_read": (_I, [_P, _I, _I, _I, _I]),
     "ref_plane_row": (None, [ctypes.POINTER(PlaneDesc), _I, _P]),
     "ref_desk_open": (_P, [_I, _I, _I]),
     "ref_desk_close": (None, [_P]),

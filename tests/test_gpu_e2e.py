@@ -329,3 +329,54 @@ def test_kinds_greedy_and_forced_match_reference(backend, kinds_model, lane_limi
           "max gap difference", float(np.max(np.abs(gaps - fgap))))
     assert np.array_equal(picks[decided], fwant[decided])
     assert np.max(np.abs(gaps - fgap)) <= 1.5 * spread
+
+
+@pytest.fixture(scope="module")
+def packed_model():
+    fx = load_fixture("small_packed")
+    folder = os.path.join(tempfile.gettempdir(), f"igl_gemma_packed_{os.getpid()}")
+    write_gemma(folder, seed=fx["seed"], **dict(SMALL, kinds=2))
+    return folder, fx
+
+
+@pytest.mark.parametrize("precise,lane_limit", [(True, 16), (False, 64), (False, 600)])
+def test_packed_zero_point_stream_matches_reference(backend, packed_model, precise, lane_limit):
+    """A checkpoint whose layer projections are in the compressed-tensors pack
+    (plane_bind_part's packed branch, app_core.c:8015-8065): weight_packed I32
+    rows, weight_shape, and weight_zero_point (zero_read, 7855-7866) on every
+    one of them; 4-bit attention and early MLPs, 2-bit later MLPs, 8-bit
+    per-layer planes (tests/golden/e2e_small_packed.json, the reference's
+    plain and tuned builds agreeing).  The engine binds them in place and
+    multiplies on the zero-point GEMV and, from 64 lanes, the GEMM.  Greedy
+    stream equal with gaps within 2e-3; the forced walk (seed 1): every pick
+    equal, gaps within three times the largest gap difference between the
+    reference's own plain and tuned builds on it (and at least 2e-3), the bar
+    the logit-row test takes."""
+    folder, fx = packed_model
+    prompt = prompt_ids(fx["prompt_count"], fx["shape"]["vocab"], seed=fx["prompt_seed"])
+    forced = prompt_ids(fx["gen"], fx["shape"]["vocab"], seed=fx["forced_seed"])
+    eng = Engine(backend, folder, window_limit=fx["window_limit"], lane_limit=lane_limit, precise=precise)
+    try:
+        ids, margins = eng.greedy(prompt, fx["gen"])
+        eng.reset()
+        eng.prime(prompt)
+        picks, gaps = [], []
+        token = int(prompt[-1])
+        for t in forced:
+            pick, gap = eng.step(token)
+            picks.append(pick)
+            gaps.append(gap)
+            token = int(t)
+    finally:
+        eng.close()
+    want = np.array(fx["plain"]["ids"], dtype=np.int32)
+    gap = float(np.max(np.abs(margins - np.array(fx["plain"]["margin"]))))
+    fgap = float(np.max(np.abs(np.array(gaps) - np.array(fx["plain"]["forced_margin"]))))
+    print("greedy max gap difference", gap, "forced max gap difference", fgap,
+          "forced distinct picks", len(set(picks)))
+    assert np.array_equal(ids, want)
+    assert gap <= 2e-3
+    spread = float(np.max(np.abs(np.array(fx["plain"]["forced_margin"]) - np.array(fx["tuned"]["forced_margin"]))))
+    print("reference builds' forced gap spread", spread)
+    assert np.array_equal(np.array(picks), np.array(fx["plain"]["forced_ids"]))
+    assert fgap <= max(2e-3, 3 * spread)

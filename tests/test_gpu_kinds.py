@@ -199,3 +199,63 @@ def test_real_table_entries(backend):
     # one lane takes the whole row in one K-chunk, eight lanes two: not bit-equal
     assert rel_err(backend.mat_vec(cp, act[0])[None], want[:1]) <= 1e-3
     backend.detach(cp)
+
+
+# ---- zero points (the compressed-tensors pack's weight_zero_point) ----------
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("N,K,group,lanes", [
+    (1536, 512, 32, 1), (2048, 512, 32, 3), (512, 2048, 128, 8), (300, 1536, 1536, 2),
+    (1024, 512, 32, 16), (512, 1024, 32, 64), (1536, 512, 32, 300), (70, 96, 32, 65),
+])
+def test_zero_point_planes(backend, bits, N, K, group, lanes):
+    """Planes with a zero point a row and group, every value of the code
+    range's signed half, against the oracle (kern_row_code's
+    gain (dot - (bias + zero) sum), pinned to the reference's plain build):
+    below 64 lanes the zero-point GEMV, from 64 lanes 4-bit planes take the
+    MFMA GEMM with the zero folded into the weight operand's subtrahend and
+    2/8-bit planes the GEMV; both routes through igl_mat_mat_dev and, for
+    the GEMV, igl_gemv_dev."""
+    print_case(test="zero_points", bits=bits, N=N, K=K, group=group, lanes=lanes)
+    r = np.random.default_rng(bits * 1000 + N + lanes)
+    codes, gains, act = synth_kind(N, K, bits, group, lanes, seed=bits + N + lanes)
+    half = 1 << (bits - 1)
+    zeros = r.integers(-half, half, size=gains.shape).astype(np.int8)
+    cp = backend.attach(make_plane(codes, gains, K, group_size=group, bits=bits, zeros=zeros))
+    want = ol.oracle_mat_mat(codes, gains, act, K, group, threads=8, bits=bits, code_bias=half,
+                             zeros=zeros)
+    got = run_dev(backend, cp, act, lanes, path="mat_mat")
+    err = rel_err(got, want)
+    print("rel_err mat_mat", err)
+    assert err <= 1e-3
+    got = run_dev(backend, cp, act, lanes, path="gemv")
+    err = rel_err(got, want)
+    print("rel_err gemv", err)
+    assert err <= 1e-3
+    backend.detach(cp)
+
+
+def test_zero_point_bf16_gemm(backend):
+    """bf16 prefill on a 4-bit zero-point plane: the GEMM's bf16 output within
+    its rounding of the float64 closed form."""
+    N, K, M = 1024, 2048, 256
+    r = np.random.default_rng(77)
+    codes, gains, act = synth_kind(N, K, 4, 32, M, seed=77)
+    zeros = r.integers(-8, 8, size=gains.shape).astype(np.int8)
+    cp = backend.attach(make_plane(codes, gains, K, bits=4, zeros=zeros))
+    u = act.view(np.uint32).astype(np.uint64)
+    a16 = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    a32 = (a16.astype(np.uint32) << 16).view(np.float32)
+    dev_a = backend.upload(a16)
+    dev_c = backend.alloc(M * N * 2)
+    backend.gemm_bf16_dev(cp, dev_a, K, M, dev_c, N)
+    backend.sync()
+    got = (dev_c.get(np.uint16, M * N).astype(np.uint32) << 16).view(np.float32).reshape(M, N).astype(np.float64)
+    nib = np.stack([codes[:, :K // 2] & 15, codes[:, :K // 2] >> 4], axis=-1).reshape(N, K).astype(np.float64)
+    w = (nib - 8 - np.repeat(zeros.astype(np.float64), 32, axis=1)) * np.repeat(gains.astype(np.float64), 32, axis=1)
+    want = a32.astype(np.float64) @ w.T
+    rms = float(np.sqrt(np.mean(want ** 2)))
+    assert float((np.abs(got - want) - (2.0 ** -8 * np.abs(want) + 1e-4 * rms)).max()) <= 0.0
+    dev_a.free()
+    dev_c.free()
+    backend.detach(cp)

@@ -228,6 +228,79 @@ def test_shipped_kinds_bitexact_vs_reference(ref_plain, N, K, group, bits, flip,
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+# ---- zero points (asymmetric planes) -------------------------------------------
+
+ZERO_CASES = [(70, 128, 32, 4, 1), (70, 256, 32, 4, 5), (40, 1536, 128, 4, 3), (33, 256, 32, 2, 2),
+              (33, 512, 64, 2, 1), (24, 256, 32, 8, 4), (24, 512, 512, 8, 1), (70, 130, 48, 4, 19)]
+
+
+def zero_inputs(N, K, group, bits, lanes, seed=11):
+    r = np.random.default_rng(seed)
+    stride = (K * bits + 7) // 8
+    codes = r.integers(0, 256, size=(N, stride), dtype=np.uint8)
+    G = (K + group - 1) // group
+    gains = np.abs(r.normal(0, 0.02, size=(N, G))).astype(np.float32)
+    half = 1 << (bits - 1)
+    zeros = r.integers(-half, half, size=(N, G)).astype(np.int8)
+    act = r.normal(size=(lanes, K)).astype(np.float32)
+    return codes, gains, zeros, act
+
+
+def zero_closed(codes, gains, zeros, act, K, group, bits, sign=1):
+    """sum_g s[n,g] sum_{k in g} (c - bias - zero[n,g]) x in float64 (sign=-1
+    plants the slip of adding the zero point instead)."""
+    N = codes.shape[0]
+    fields = np.unpackbits(codes, axis=1, bitorder="little")[:, :K * bits].reshape(N, K, bits)
+    c = (fields.astype(np.int64) << np.arange(bits)).sum(axis=2).astype(np.float64)
+    z = np.repeat(zeros.astype(np.float64), group, axis=1)[:, :K]
+    w = (c - (1 << (bits - 1)) - sign * z) * np.repeat(gains.astype(np.float64), group, axis=1)[:, :K]
+    return act.astype(np.float64) @ w.T
+
+
+@pytest.mark.parametrize("N,K,group,bits,lanes", ZERO_CASES)
+def test_zero_points_closed_form(N, K, group, bits, lanes):
+    """plane_row's (code - bias - zero) gain (app_core.c:1849-1852) summed in
+    float64; a restatement that added the zero point misses it."""
+    codes, gains, zeros, act = zero_inputs(N, K, group, bits, lanes)
+    kw = dict(bits=bits, code_bias=1 << (bits - 1), zeros=zeros)
+    got = ol.oracle_mat_mat(codes, gains, act, K, group, threads=2, **kw)
+    want = zero_closed(codes, gains, zeros, act, K, group, bits)
+    scale = np.sqrt(np.mean(want ** 2))
+    assert np.max(np.abs(got - want)) <= 2e-6 * scale * math.sqrt(K / 32) + 1e-7
+    wrong = zero_closed(codes, gains, zeros, act, K, group, bits, sign=-1)
+    assert np.max(np.abs(wrong - want)) > 1e-2 * scale
+
+
+@pytest.mark.parametrize("N,K,group,bits,lanes", ZERO_CASES)
+def test_zero_points_bitexact_vs_reference(ref_plain, N, K, group, bits, lanes):
+    """With zero points the oracle and the reference's own back_mat_mat (plain
+    build, kern_row_code / kern_row_code_many: (bias + zero) sum per group)
+    agree to the bit."""
+    codes, gains, zeros, act = zero_inputs(N, K, group, bits, lanes)
+    kw = dict(bits=bits, code_bias=1 << (bits - 1), zeros=zeros)
+    got = ol.oracle_mat_mat(codes, gains, act, K, group, threads=2, **kw)
+    want = ol.ref_mat_mat(ref_plain, codes, gains, act, K, group, threads=2, **kw)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits,rows,groups", [(2, 70, 3), (4, 33, 5), (8, 24, 2), (4, 8, 1), (3, 50, 4)])
+def test_zero_unpack_matches_reference_zero_read(ref_plain, bits, rows, groups):
+    """The engine's loader unpacks weight_zero_point (I32, each group's zero
+    points packed along the rows) as the reference's zero_read
+    (app_core.c:7855-7866) reads it, row by row and group by group; 3-bit
+    fields straddle words."""
+    from igllm_amd import native
+
+    r = np.random.default_rng(bits * 100 + rows)
+    words = r.integers(0, 1 << 32, size=((rows * bits + 31) // 32 + 1, groups), dtype=np.uint64).astype(np.uint32)
+    out = np.zeros((rows, groups), dtype=np.int8)
+    native.load().igl_zero_unpack(ol.p(words), groups, rows, bits, ol.p(out))
+    want = np.array([[ref_plain.ref_zero_read(ol.p(words), groups, g, n, bits) for g in range(groups)]
+                     for n in range(rows)])
+    assert np.array_equal(out.astype(np.int64), want)
+    assert want.min() >= -(1 << (bits - 1)) and want.max() < (1 << (bits - 1))
+
+
 # ---- calibrated planes: the integer level path --------------------------------
 
 LEVEL_CASES = [
