@@ -170,30 +170,27 @@ static void dropin_release(void) {
   igl_back_close(&dropin.gpu);
 }
 
-/* The reference engine's greedy run (its prime, then `gen_count` steps with
- * the first-maximum pick, session_pick_at app_core.c:14672-14677) with the
- * backend table on device `device`.  calls_out[0..5]: the entries' call
- * counts; calls_out[6]: products on planes the load did not attach.  Returns 0,
- * the reference's app_code, or the backend's igl_code. */
-int dropin_engine_greedy(const char *folder, int device, int thread_count, int cache_bits,
-                         int window_limit, const int32_t *prompt, int prompt_count, int gen_count,
-                         int32_t *out_ids, float *margin_out, long *calls_out) {
+/* Loads the checkpoint with the reference's own model_load, opens the GPU
+ * desk sized as back_open sizes the CPU one (app_core.c:12585; 16 lanes, the
+ * session's batch, KERN_LANE_LIMIT), attaches the text stack, points the
+ * model's table at the forwarders and opens the reference's session. */
+static int dropin_open(const char *folder, int device, int thread_count, int cache_bits, int window_limit,
+                       app_model **model_out, app_session **session_out) {
   app_setup setup = app_setup_plain();
   app_model *model = NULL;
-  app_session *session = NULL;
   int code;
-  int32_t id;
   memset(&dropin, 0, sizeof(dropin));
+  *model_out = NULL;
+  *session_out = NULL;
   setup.thread_count = thread_count;
   setup.cache_bits = cache_bits;
   setup.window_limit = window_limit;
   code = (int)model_load(folder, &setup, &model);
   if (code != APP_OKAY) return code;
-  /* the GPU desk sized as back_open sizes the CPU one (app_core.c:12585);
-   * 16 lanes, the session's batch (KERN_LANE_LIMIT) */
+  *model_out = model;
   code = igl_back_open(&dropin.gpu, device, model->desk.sum_limit, 65536, KERN_LANE_LIMIT);
   if (code == IGL_OKAY) code = dropin_attach_model(model);
-  if (code != IGL_OKAY) goto done;
+  if (code != IGL_OKAY) return code;
   model->desk.name_text = dropin.gpu.name_text;
   model->desk.mat_vec = fwd_mat_vec;
   model->desk.mat_mat = fwd_mat_mat;
@@ -201,33 +198,18 @@ int dropin_engine_greedy(const char *folder, int device, int thread_count, int c
   model->desk.soft_max = fwd_soft_max;
   model->desk.gelu_gate = fwd_gelu_gate;
   model->desk.rope_turn = fwd_rope_turn;
-  code = (int)session_open(model, &session);
-  if (code != APP_OKAY) goto done;
-  code = (int)session_prime(session, prompt, prompt_count);
-  if (code == APP_OKAY) code = igl_desk_error_take(&dropin.gpu);
-  id = prompt[prompt_count - 1];
-  for (int step = 0; code == APP_OKAY && step < gen_count; ++step) {
-    const float *logits = session_step(session, id);
-    int vocab = model_vocab_count(model), best = 0;
-    float second = -FLT_MAX;
-    if (!logits) {
-      code = APP_FAIL_STATE;
-      break;
-    }
-    if ((code = igl_desk_error_take(&dropin.gpu)) != IGL_OKAY) break;
-    if (dropin.misses) {
-      code = IGL_FAIL_STATE;
-      break;
-    }
-    for (int v = 1; v < vocab; ++v)
-      if (logits[v] > logits[best]) best = v;
-    for (int v = 0; v < vocab; ++v)
-      if (v != best && logits[v] > second) second = logits[v];
-    out_ids[step] = best;
-    if (margin_out) margin_out[step] = logits[best] - second;
-    id = best;
-  }
-done:
+  return (int)session_open(model, session_out);
+}
+
+/* The backend's sticky error, then any product on a plane the load did not
+ * attach. */
+static int dropin_check(void) {
+  int code = igl_desk_error_take(&dropin.gpu);
+  if (code == IGL_OKAY && dropin.misses) code = IGL_FAIL_STATE;
+  return code;
+}
+
+static void dropin_close(app_model *model, app_session *session, long *calls_out) {
   if (calls_out) {
     for (int i = 0; i < 6; ++i) calls_out[i] = dropin.calls[i];
     calls_out[6] = dropin.misses;
@@ -235,5 +217,123 @@ done:
   if (session) session_close(session);
   dropin_release();
   model_free(model);
+}
+
+/* The first maximum of a row (session_pick_at's greedy rule,
+ * app_core.c:14672-14677) and its gap to the runner-up. */
+static int32_t dropin_top(const float *logits, int vocab, float *gap_out) {
+  int best = 0;
+  float second = -FLT_MAX;
+  for (int v = 1; v < vocab; ++v)
+    if (logits[v] > logits[best]) best = v;
+  for (int v = 0; v < vocab; ++v)
+    if (v != best && logits[v] > second) second = logits[v];
+  if (gap_out) *gap_out = logits[best] - second;
+  return best;
+}
+
+/* The reference engine's greedy run (its prime, then `gen_count` steps with
+ * the first-maximum pick) with the backend table on device `device`.
+ * calls_out[0..5]: the entries' call counts; calls_out[6]: products on planes
+ * the load did not attach.  Returns 0, the reference's app_code, or the
+ * backend's igl_code. */
+int dropin_engine_greedy(const char *folder, int device, int thread_count, int cache_bits,
+                         int window_limit, const int32_t *prompt, int prompt_count, int gen_count,
+                         int32_t *out_ids, float *margin_out, long *calls_out) {
+  app_model *model = NULL;
+  app_session *session = NULL;
+  int32_t id;
+  int code = dropin_open(folder, device, thread_count, cache_bits, window_limit, &model, &session);
+  if (code == APP_OKAY) code = (int)session_prime(session, prompt, prompt_count);
+  if (code == APP_OKAY) code = dropin_check();
+  id = prompt[prompt_count - 1];
+  for (int step = 0; code == APP_OKAY && step < gen_count; ++step) {
+    const float *logits = session_step(session, id);
+    if (!logits) {
+      code = APP_FAIL_STATE;
+      break;
+    }
+    if ((code = dropin_check()) != IGL_OKAY) break;
+    id = dropin_top(logits, model_vocab_count(model), margin_out ? margin_out + step : NULL);
+    out_ids[step] = id;
+  }
+  dropin_close(model, session, calls_out);
+  return code;
+}
+
+/* The CLI's greedy --guess loop (main_answer_guess, app_main.c:520-598,
+ * without the stop-id check) on the reference engine with the backend table
+ * on the GPU: the reference's scout proposes up to span - 1 ids
+ * (scout_draw), its session_guess runs the block (a batch of up to `span`
+ * lanes through the table's mat_mat), the argmax rows keep the agreed prefix
+ * plus the next id, session_guess_keep commits them; with nothing proposed,
+ * an ordinary step.  stats_out: rounds, ids proposed, ids taken. */
+int dropin_engine_guess(const char *folder, int device, int thread_count, int cache_bits, int window_limit,
+                        const int32_t *prompt, int prompt_count, int gen_count, int span, int32_t *out_ids,
+                        long *stats_out, long *calls_out) {
+  app_model *model = NULL;
+  app_session *session = NULL;
+  app_scout *scout = NULL;
+  int32_t block[16];
+  int32_t id_value = prompt[prompt_count - 1];
+  int made = 0, vocab = 0;
+  long rounds = 0, drawn = 0, taken = 0;
+  int code = dropin_open(folder, device, thread_count, cache_bits, window_limit, &model, &session);
+  if (code == APP_OKAY) code = (int)scout_open(&scout);
+  if (code == APP_OKAY) code = (int)session_prime(session, prompt, prompt_count);
+  if (code == APP_OKAY) code = dropin_check();
+  if (code == APP_OKAY) code = (int)scout_note(scout, prompt, prompt_count);
+  if (code == APP_OKAY) {
+    vocab = model_vocab_count(model);
+    if (span > session_guess_limit(session)) span = session_guess_limit(session);
+    if (span > 16) span = 16;
+    if (span < 1) span = 1;
+  }
+  while (code == APP_OKAY && made < gen_count) {
+    int want = span - 1, count, take = 0;
+    const float *rows;
+    int32_t after;
+    if (want > gen_count - made - 1) want = gen_count - made - 1;
+    if (want < 0) want = 0;
+    block[0] = id_value;
+    count = 1 + scout_draw(scout, block + 1, want);
+    rounds += 1;
+    if (count == 1) {
+      const float *logits = session_step(session, id_value);
+      if (!logits) {
+        code = APP_FAIL_STATE;
+        break;
+      }
+      if ((code = dropin_check()) != IGL_OKAY) break;
+      id_value = dropin_top(logits, vocab, NULL);
+      out_ids[made++] = id_value;
+      code = (int)scout_note(scout, &id_value, 1);
+      continue;
+    }
+    rows = session_guess(session, block, count);
+    if (!rows) {
+      code = APP_FAIL_STATE;
+      break;
+    }
+    if ((code = dropin_check()) != IGL_OKAY) break;
+    drawn += count - 1;
+    while (take + 1 < count && dropin_top(rows + (size_t)take * (size_t)vocab, vocab, NULL) == block[take + 1])
+      take += 1;
+    after = dropin_top(rows + (size_t)take * (size_t)vocab, vocab, NULL);
+    taken += take;
+    for (int slot = 0; slot <= take && made < gen_count; ++slot) {
+      id_value = slot < take ? block[slot + 1] : after;
+      out_ids[made++] = id_value;
+      if (scout_note(scout, &id_value, 1) != APP_OKAY) code = APP_FAIL_MEMORY;
+    }
+    if (code == APP_OKAY) code = (int)session_guess_keep(session, take + 1);
+  }
+  if (stats_out) {
+    stats_out[0] = rounds;
+    stats_out[1] = drawn;
+    stats_out[2] = taken;
+  }
+  if (scout) scout_close(scout);
+  dropin_close(model, session, calls_out);
   return code;
 }
