@@ -134,7 +134,7 @@ const char *igl_code_text(int code);
  * the device with the plane), group_size a power-of-two multiple of 32 or
  * one group a row, col_count a multiple of 32, row_stride a multiple of 16.
  * A row_stride of whole 32-bit words is the compressed-tensors weight_packed
- * layout (8015-8065): the same dense bit stream. 
+ * layout (8015-8065): the same dense bit stream.
  * Supported real planes (plane_bind_part's `weight` of a float type,
  * app_core.c:7985-7998): F32, F16 or BF16 rows, col_count a multiple of 8.
  * Anything else is IGL_FAIL_SUPPORT. */
