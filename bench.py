@@ -40,11 +40,46 @@ SHAPES = [(8192, 2048), (2048, 8192)]
 LANES = [1, 2, 4, 8]
 COPIES = 48                     # 48 x 10.5 MB per shape: past the 256 MiB MALL
 ATTEND_COPIES = 40              # 40 x 8 MiB of key/value rings: past the MALL
-# HBM bytes per dispatch of the decode GEMV (M=1, 8192x2048), from two rocprofv3
-# --pmc runs of `bench.py --kernel gemv` (profiles/gemv_q4_m1_8192x2048.md):
-# FETCH_SIZE 5179.6 KiB x 2.0 + WRITE_SIZE 32.0 KiB x 1.0, the factors a 256 MiB
-# device copy gives (profiles/copy_256mib_calibration.md).
-GEMV_M1_TRAFFIC_BYTES = int((5179.6 * 2.0 + 32.0) * 1024)
+# The roofline's profile figures come from the committed rocprofv3 summaries:
+# the decode GEMV's (M=1, 8192x2048) kernel-trace duration and its FETCH_SIZE /
+# WRITE_SIZE per dispatch, scaled by the factors a 256 MiB device copy gives.
+GEMV_M1_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4_m1_8192x2048.md")
+COPY_PROFILE = os.path.join(ROOT, "profiles", "copy_256mib_calibration.md")
+GEMV_M1_KERNEL = "gemv_q4_dot_kernel<1, 2, 1, 1>"
+
+
+def profile_rows(path, kernel):
+    """The table rows of a profile summary whose kernel cell names `kernel`:
+    [(cells...), ...] in file order (the kernel-trace row, then the counters')."""
+    rows = []
+    with open(path) as f:
+        for line in f:
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if line.startswith("|") and len(cells) > 1 and kernel in cells[0]:
+                rows.append(cells)
+    return rows
+
+
+def gemv_m1_profile(algo_bytes):
+    """roofline.traffic and the rocprof duration of the decode GEMV, from the
+    committed profiles: traffic = FETCH_SIZE x f + WRITE_SIZE x w KiB, where
+    the copy of a known 256 MiB gives f = 262144 / its FETCH_SIZE and w =
+    262144 / its WRITE_SIZE."""
+    try:
+        copy = profile_rows(COPY_PROFILE, "__amd_rocclr_copyBuffer")
+        gemv = profile_rows(GEMV_M1_PROFILE, GEMV_M1_KERNEL)
+        f = 262144.0 / round(float(copy[-1][1]))
+        w = 262144.0 / float(copy[-1][2])
+        fetch, write = float(gemv[-1][1]), float(gemv[-1][2])
+        avg_ns = float(gemv[0][2])
+    except (OSError, IndexError, ValueError, ZeroDivisionError):
+        return None
+    traffic = int(round((fetch * f + write * w) * 1024))
+    return {"traffic": traffic, "fetch_kib": fetch, "write_kib": write, "fetch_factor": round(f, 4),
+            "write_factor": round(w, 4), "rocprof_avg_launch_us": round(avg_ns / 1e3, 3),
+            "rocprof_frac": round(algo_bytes / (avg_ns * 1e-9) / 1e9 / HBM_PEAK_GBPS, 4),
+            "source": "profiles/gemv_q4_m1_8192x2048.md (kernel trace avg ns; FETCH_SIZE, WRITE_SIZE KiB a "
+                      "dispatch) scaled by profiles/copy_256mib_calibration.md"}
 
 
 def gemv_bytes(N, K, M, group=32):
@@ -819,6 +854,7 @@ def main():
     be.mark()
     gemv_enq_us = be.marks_ms() * 1e3 / launches
     gemv_algo = gemv_bytes(N, K, 1)
+    prof = gemv_m1_profile(gemv_algo)
 
     # ---- the read floor: a kernel that only reads the same bytes once (16-byte
     # loads, two a thread), over as many rotated buffers, launched the same way.
@@ -861,9 +897,11 @@ def main():
             for i in range(100):
                 be.gemv_dev(rr.planes[i % COPIES], acts[(N, K, M)], K, M, outs[(N, K, M)], N)
             be.mark()
-            us = be.marks_ms() * 1e3 / 100
+            enq_us = be.marks_ms() * 1e3 / 100
+            us = replayed(lambda i: be.gemv_dev(rr.planes[i % COPIES], acts[(N, K, M)], K, M, outs[(N, K, M)], N))
             sweep[f"{N}x{K}_M{M}"] = {"us": round(us, 3),
-                                      "GBps": round(gemv_bytes(N, K, M) / (us * 1e-6) / 1e9, 1)}
+                                      "GBps": round(gemv_bytes(N, K, M) / (us * 1e-6) / 1e9, 1),
+                                      "enqueued_us": round(enq_us, 3)}
 
     # ---- prefill GEMM, bf16 in/out, M in {64, 256, 1024, 2048} lanes (both
     # shapes; BASELINE's prefill config), timed replayed (the GEMM launches
@@ -1025,7 +1063,8 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "gemv_q4_dot_kernel<1, 2, 1, 1> 8192x2048 M=1",
                      "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": GEMV_M1_TRAFFIC_BYTES,
+                     "traffic": prof["traffic"] if prof else None,
+                     "profile": prof,
                      "algorithmic_bytes": gemv_algo, "avg_launch_us": round(gemv_us, 3),
                      "avg_launch_us_enqueued": round(gemv_enq_us, 3),
                      "timing": f"{launches} launches on rotated copies recorded once and replayed, HIP events "

@@ -82,6 +82,9 @@ struct igl_desk_state {
   int recording;
   int record_error;  /* the first failure while recording (error_take keeps it) */
   int replays_live;
+  /* counts the workspace reallocations: a graph captured by a caller outside
+   * the recording API is stale once it changes (igl_desk_generation) */
+  unsigned generation;
 };
 
 struct igl_replay {
@@ -150,6 +153,7 @@ static int grow_dev(igl_desk_state *st, float **buf, size_t *have, size_t floats
   if (*buf) (void)hipFree(*buf);
   *buf = (float *)fresh;
   *have = floats;
+  st->generation += 1;
   return IGL_OKAY;
 }
 
@@ -167,6 +171,7 @@ static int grow_out(igl_desk_state *st, size_t floats) {
   st->out_dev = (float *)dev;
   st->out_pin = (float *)pin;
   st->out_floats = floats;
+  st->generation += 1;
   return IGL_OKAY;
 fail:
   if (dev) (void)hipFree(dev);
@@ -477,6 +482,11 @@ static int gemm_run(igl_desk *desk, const igl_plane *sheet, const void *act_dev,
 }
 
 int igl_gemm_lane_floor(void) { return IGL_GEMM_FLOOR; }
+
+unsigned igl_desk_generation(igl_desk *desk) {
+  const igl_desk_state *st = desk ? desk->state : NULL;
+  return st ? st->generation : 0u;
+}
 
 int igl_mat_mat_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev, int act_stride,
                     int lane_count, float *out_dev, int out_stride) {

@@ -108,6 +108,13 @@ struct igl_engine {
   igl_step_io *io;    /* pinned: what the step reads and writes on the host */
   int graph_on, graph_ready, graph_tried;
   hipGraphExec_t graph;
+  /* a speculative block of `count` lanes as one captured graph per count
+   * (blocks below the GEMM's lane floor, whose launches use only buffers
+   * fixed at open and attach): ctl_host[0 .. count] is copied to ctl_dev */
+  int32_t *ctl_host;  /* pinned: the block's position and ids */
+  unsigned graph_gen; /* the desk's workspace generation the graphs were captured at */
+  hipGraphExec_t guess_graph[ENG_GUESS_LIMIT + 1];
+  unsigned char guess_ready[ENG_GUESS_LIMIT + 1], guess_tried[ENG_GUESS_LIMIT + 1];
 };
 
 /* ---- a little JSON, enough for config.json and a safetensors header ------ */
@@ -703,6 +710,8 @@ int igl_engine_open(igl_engine **out, igl_desk *desk, const char *folder, int wi
     e->state = e->state_buf[0];
     if (hipHostMalloc((void **)&e->io, sizeof(igl_step_io), hipHostMallocDefault) != hipSuccess ||
         hipHostMalloc((void **)&e->pairs_host, 2 * (size_t)e->guess_limit * sizeof(int32_t),
+                      hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc((void **)&e->ctl_host, (1 + (size_t)e->guess_limit) * sizeof(int32_t),
                       hipHostMallocDefault) != hipSuccess) {
       code = IGL_FAIL_MEMORY;
       goto fail;
@@ -739,6 +748,8 @@ void igl_engine_close(igl_engine *e) {
   drop_plane(e, &e->ple_lift);
   drop_plane(e, &e->head);
   if (e->graph_ready) (void)hipGraphExecDestroy(e->graph);
+  for (int c = 0; c <= ENG_GUESS_LIMIT; ++c)
+    if (e->guess_ready[c]) (void)hipGraphExecDestroy(e->guess_graph[c]);
   {
     void *bufs[] = {e->payload_dev, e->ctl_dev, e->attend_work, e->state_buf[0],
                     e->state_buf[1], e->scrap, e->lift, e->q,
@@ -750,6 +761,7 @@ void igl_engine_close(igl_engine *e) {
   }
   if (e->io) (void)hipHostFree(e->io);
   if (e->pairs_host) (void)hipHostFree(e->pairs_host);
+  if (e->ctl_host) (void)hipHostFree(e->ctl_host);
   if (e->map) munmap(e->map, e->map_bytes);
   free(e->tensor);
   free(e);
@@ -1177,6 +1189,21 @@ static int step_body(igl_engine *e) {
   return IGL_OKAY;
 }
 
+/* Drops every captured graph if the desk has reallocated a workspace since
+ * the captures (a larger batch through a path that grows one): the graphs
+ * would launch on freed addresses.  They are captured again on next use. */
+static void graphs_check(igl_engine *e) {
+  const unsigned gen = igl_desk_generation(e->desk);
+  if (gen == e->graph_gen) return;
+  if (e->graph_ready) (void)hipGraphExecDestroy(e->graph);
+  e->graph_ready = e->graph_tried = 0;
+  for (int c = 0; c <= ENG_GUESS_LIMIT; ++c) {
+    if (e->guess_ready[c]) (void)hipGraphExecDestroy(e->guess_graph[c]);
+    e->guess_ready[c] = e->guess_tried[c] = 0;
+  }
+  e->graph_gen = gen;
+}
+
 static int capture_step(igl_engine *e) {
   hipGraph_t graph = NULL;
   int code;
@@ -1201,13 +1228,15 @@ int igl_engine_step(igl_engine *e, int32_t id, int32_t *pick_out, float *margin_
   e->io->id = id;
   e->io->pick = -1;
   e->io->margin = 0.0f;
+  graphs_check(e);
   /* the first step runs as it is enqueued (every kernel's first launch
    * happens outside a capture); later ones replay its capture */
   if (e->graph_on && !e->graph_ready && !e->graph_tried) {
-    e->graph_tried = 1;
     OKAY(step_body(e));
     RUN(hipStreamSynchronize(e->stream));
     OKAY(igl_desk_error_take(e->desk));
+    graphs_check(e);  /* the run may have grown a workspace */
+    e->graph_tried = 1;
     OKAY(capture_step(e));
   } else if (e->graph_on && e->graph_ready) {
     RUN(hipGraphLaunch(e->graph, e->stream));
@@ -1237,20 +1266,72 @@ int igl_engine_set_graph(igl_engine *e, int on) {
  * block overwrites are past every window a later position can reach, and a
  * full-depth ring only gains rows past the kept positions, which later
  * steps overwrite before any query reads them. */
+/* One block of `count` lanes as a captured graph replays it: the position
+ * and ids in from ctl_host, the pass with the attention grid sized for
+ * `bound` (the position is read on the device), every lane's pick and margin
+ * out to pairs_host. */
+static int guess_body(igl_engine *e, int count, int bound) {
+  RUN(hipMemcpyAsync(e->ctl_dev, e->ctl_host, (1 + (size_t)count) * sizeof(int32_t), hipMemcpyHostToDevice,
+                     e->stream));
+  OKAY(run_pass(e, bound, count, 2));
+  RUN(igl_launch_pick(e->logits, e->vocab, (size_t)e->vocab, count, e->pick_work, e->pick_dev,
+                      e->stream));
+  RUN(hipMemcpyAsync(e->pairs_host, e->pick_dev, 2 * (size_t)count * sizeof(int32_t),
+                     hipMemcpyDeviceToHost, e->stream));
+  return IGL_OKAY;
+}
+
+static int capture_guess(igl_engine *e, int count) {
+  hipGraph_t graph = NULL;
+  int code;
+  hipError_t end;
+  if (hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
+    return IGL_FAIL_DEVICE;
+  code = guess_body(e, count, e->window_limit - count);
+  end = hipStreamEndCapture(e->stream, &graph);
+  if (code == IGL_OKAY && end != hipSuccess) code = IGL_FAIL_DEVICE;
+  if (code == IGL_OKAY && hipGraphInstantiate(&e->guess_graph[count], graph, NULL, NULL, 0) != hipSuccess)
+    code = IGL_FAIL_DEVICE;
+  if (graph) (void)hipGraphDestroy(graph);
+  if (code == IGL_OKAY) e->guess_ready[count] = 1;
+  return code;
+}
+
+/* session_guess (app_core.c:12139-12203): ids[0] is the next input and
+ * ids[1 ..] the proposed continuation; one pass over all of them, with the
+ * greedy pick (and its top-1/top-2 gap) of every lane's row of logits.  The
+ * cache keeps the block's rows until igl_engine_keep.  Nothing needs saving
+ * first: a sliding ring here is window + lane_limit rows deep, so the rows a
+ * block overwrites are past every window a later position can reach, and a
+ * full-depth ring only gains rows past the kept positions, which later
+ * steps overwrite before any query reads them.
+ *
+ * With graphs on, a block of fewer lanes than the GEMM's floor replays one
+ * graph captured for its lane count (the first block of each count runs as
+ * enqueued, with the same grid, then is captured): every projection of such a
+ * block is a GEMV, whose launches use only the workspace reserved at attach,
+ * so no captured address can move.  Larger blocks run as enqueued. */
 int igl_engine_guess(igl_engine *e, const int32_t *ids, int count, int32_t *picks_out,
                      float *margins_out) {
   if (!e || !ids || count < 1 || count > e->guess_limit) return IGL_FAIL_ARGUMENT;
   if (e->guess_count || e->fill + count > e->window_limit) return IGL_FAIL_STATE;
   for (int l = 0; l < count; ++l)
     if (ids[l] < 0 || ids[l] >= e->embed.row_count) return IGL_FAIL_ARGUMENT;
-  RUN(igl_launch_put_int(e->ctl_dev, e->fill, e->stream));
-  RUN(hipMemcpyAsync(e->ids_dev, ids, (size_t)count * sizeof(int32_t), hipMemcpyHostToDevice,
-                     e->stream));
-  OKAY(run_pass(e, e->fill, count, 2));
-  RUN(igl_launch_pick(e->logits, e->vocab, (size_t)e->vocab, count, e->pick_work, e->pick_dev,
-                      e->stream));
-  RUN(hipMemcpyAsync(e->pairs_host, e->pick_dev, 2 * (size_t)count * sizeof(int32_t),
-                     hipMemcpyDeviceToHost, e->stream));
+  e->ctl_host[0] = e->fill;
+  memcpy(e->ctl_host + 1, ids, (size_t)count * sizeof(int32_t));
+  graphs_check(e);
+  if (e->graph_on && count < igl_gemm_lane_floor() && e->guess_ready[count]) {
+    RUN(hipGraphLaunch(e->guess_graph[count], e->stream));
+  } else if (e->graph_on && count < igl_gemm_lane_floor() && !e->guess_tried[count]) {
+    OKAY(guess_body(e, count, e->window_limit - count));
+    RUN(hipStreamSynchronize(e->stream));
+    OKAY(igl_desk_error_take(e->desk));
+    graphs_check(e);  /* the run may have grown a workspace */
+    e->guess_tried[count] = 1;
+    OKAY(capture_guess(e, count));
+  } else {
+    OKAY(guess_body(e, count, e->fill));
+  }
   RUN(hipStreamSynchronize(e->stream));
   OKAY(igl_desk_error_take(e->desk));
   for (int l = 0; l < count; ++l) {

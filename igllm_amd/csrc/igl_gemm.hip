@@ -540,8 +540,10 @@ constexpr FormShape kForms[] = {
     {4, 2, 1, 4, 8, 160},  // 256 x 256, eight waves
     {2, 2, 2, 4, 4, 160},  // 128 x 128, eight waves, K split in two
     {2, 1, 4, 2, 4, 160},  // 64 x 64, eight waves, K split in four
-    {1, 1, 8, 2, 4, 160},  // 32 x 64, eight waves, K split in eight
-    {1, 1, 8, 1, 4, 160},  // 16 x 64, eight waves, K split in eight
+    {1, 1, 4, 2, 4, 160},  // 32 x 64, four waves, K split in four (three stages fit:
+                           // 8192 x 2048 at 64 lanes 19.8 -> 15.5 us against eight)
+    {1, 1, 8, 1, 4, 160},  // 16 x 64, eight waves, K split in eight (2048 x 8192 at 64
+                           // lanes: 26.5 us, against 29.0 split in four)
 };
 constexpr int kFormCount = sizeof(kForms) / sizeof(kForms[0]);
 // Two-term activations: the same forms with the K split capped where the

@@ -188,6 +188,10 @@ size_t igl_attend_prep_work_floats(int place_bound, int window, int head_size, i
 
 /* The desk's HIP stream, for the engine's own launches (back_hip.c). */
 void *igl_desk_stream(igl_desk *desk);
+/* Changes whenever the desk reallocates a workspace: a graph captured over
+ * desk launches outside igl_record_begin / igl_record_end is stale once it
+ * differs from the value at capture. */
+unsigned igl_desk_generation(igl_desk *desk);
 
 /* session kernels (igl_session.hip) */
 hipError_t igl_launch_gather_rows(const igl_code_view *v, int cols, int rows, const int32_t *ids,

@@ -256,6 +256,51 @@ def test_small_guess_stream_matches_reference(backend, small_model, graph):
     assert len(gaps) == fx["gen"] and gap <= 2e-3
 
 
+def test_guess_graphs_replay_the_enqueued_blocks(backend, small_model):
+    """A block replayed from its lane count's captured graph gives the picks and
+    margins the same block gives enqueued, at every position it is replayed at,
+    and after the desk reallocates a workspace (a 256-lane product grows the
+    GEMM's) the engine captures again instead of replaying onto freed memory.
+    The graph's attention grid is sized for the window's end, so its fold may
+    sum the same partials in another grouping: margins to 1e-5, picks equal."""
+    from igllm_amd.backend import make_plane, synth_projection
+
+    folder, fx = small_model
+    prompt = prompt_ids(600, fx["shape"]["vocab"], seed=5)
+    eng = Engine(backend, folder, window_limit=2048, lane_limit=16, precise=True)
+    rng = np.random.default_rng(3)
+    counts = [1, 2, 3, 5, 2, 16, 3, 1, 5, 4]
+    try:
+        eng.prime(prompt)
+        token = int(prompt[-1])
+        for rnd in range(3):
+            if rnd == 2:
+                # a product large enough to grow the desk's GEMM workspace
+                codes, gains, _ = synth_projection(512, 512, 1, seed=9)
+                cp = backend.attach(make_plane(codes, gains, 512))
+                act = backend.upload(rng.normal(size=256 * 512).astype(np.float32))
+                out = backend.alloc(256 * 512 * 4)
+                backend.mat_mat_dev(cp, act, 512, 256, out, 512)
+                backend.sync()
+                act.free()
+                out.free()
+                backend.detach(cp)
+            for c in counts:
+                block = np.concatenate([[token], rng.integers(3, fx["shape"]["vocab"], size=c - 1)]).astype(np.int32)
+                eng.set_graph(False)
+                want_picks, want_gaps = eng.guess(block)
+                eng.keep(0)
+                eng.set_graph(True)
+                picks, gaps = eng.guess(block)
+                assert np.array_equal(picks, want_picks), (rnd, c)
+                assert np.allclose(gaps, want_gaps, rtol=1e-5, atol=1e-6), (rnd, c, gaps, want_gaps)
+                keep = 1 + c // 2
+                eng.keep(keep)
+                token = int(picks[keep - 1])
+    finally:
+        eng.close()
+
+
 # ---- the export's plane kinds ------------------------------------------------
 
 KINDS_SHAPE = dict(vocab=4096, hidden=512, inner=1024, layers=20, shared_layers=8, kinds=1)

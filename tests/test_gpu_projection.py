@@ -98,9 +98,10 @@ def test_gemv_edges(backend, N, K, lanes, group):
 
 def test_gemv_chunked_repeat(backend):
     """K-chunked matrix-core launches (partials summed in chunk order by a
-    second launch): launches of different lane counts and planes (full and
-    ragged row blocks) interleaved, each repeated: every repeat is
-    bit-identical to the first and within the bar of the oracle."""
+    second launch): launches of different lane counts and planes (full and ragged row blocks)
+    interleaved, each repeated, then all of them recorded once and replayed
+    three times: every repeat and every replay is bit-identical to the first
+    and within the bar of the oracle."""
     cases = [(2048, 8192, 4), (2048, 8192, 8), (40, 8192, 5), (2000, 8192, 3), (33, 12288, 8)]
     planes, firsts = [], []
     for N, K, lanes in cases:
@@ -116,6 +117,27 @@ def test_gemv_chunked_repeat(backend):
         for (cp, act), first in zip(planes, firsts):
             got = run_gemv_dev(backend, cp, act, act.shape[0])
             assert np.array_equal(got.view(np.uint32), first.view(np.uint32)), f"repeat {turn}"
+    bufs = []
+    for cp, act in planes:
+        bufs.append((backend.upload(act), backend.alloc(act.shape[0] * cp.N * 4)))
+    backend.record_begin()
+    for (cp, act), (a, o) in zip(planes, bufs):
+        backend.gemv_dev(cp, a, cp.K, act.shape[0], o, cp.N)
+    handle = backend.record_end()
+    try:
+        for turn in range(3):
+            for _, o in bufs:
+                o.put(np.zeros(o.nbytes // 4, np.float32))
+            backend.replay_run(handle)
+            backend.sync()
+            for (cp, act), (a, o), first in zip(planes, bufs, firsts):
+                got = o.get(np.float32, act.shape[0] * cp.N).reshape(act.shape[0], cp.N)
+                assert np.array_equal(got.view(np.uint32), first.view(np.uint32)), f"replay {turn}"
+    finally:
+        backend.replay_free(handle)
+    for a, o in bufs:
+        a.free()
+        o.free()
     for cp, _ in planes:
         backend.detach(cp)
 
