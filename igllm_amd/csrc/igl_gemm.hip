@@ -505,19 +505,26 @@ __global__ __launch_bounds__(64 * WN * WM * KS) void gemm_codes_kernel(GemmCodes
   for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) inv[i][r] = g.row_inv[min(m0 + wm * MB * 16 + 16 * i + 4 * gq + r, g.M - 1)];
+  // Row by row: the wave's NB stores of one output row go out back to back,
+  // so each row's NB x 16 contiguous outputs reach the L2 together (with the
+  // row blocks outermost, a 256 x 256 tile's bf16 rows were written a quarter
+  // line at a time, far apart: 2.5x the output bytes in WRITE_SIZE).
+  float row_gain[NB];
 #pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    const int nn = n0 + wn * NB * 16 + 16 * j + n;
-    if (nn >= g.N) continue;
-    const float row_gain = ROWGAIN ? g.gains[(size_t)nn * g.gain_stride] : 1.0f;
+  for (int j = 0; j < NB; ++j)
+    row_gain[j] = ROWGAIN ? g.gains[(size_t)min(n0 + wn * NB * 16 + 16 * j + n, g.N - 1) * g.gain_stride] : 1.0f;
 #pragma unroll
-    for (int i = 0; i < MB; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * MB * 16 + 16 * i + 4 * gq + r;
-        if (m >= g.M) continue;
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + wm * MB * 16 + 16 * i + 4 * gq + r;
+      if (m >= g.M) continue;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int nn = n0 + wn * NB * 16 + 16 * j + n;
+        if (nn >= g.N) continue;
         float v = acc[i][j][r] * inv[i][r];
-        if (ROWGAIN) v = row_gain * v;
+        if (ROWGAIN) v = row_gain[j] * v;
         if (C_BF16) {
           reinterpret_cast<uint16_t *>(g.out)[(size_t)m * g.out_stride + nn] = float_to_bf16(v);
         } else {
@@ -525,7 +532,7 @@ __global__ __launch_bounds__(64 * WN * WM * KS) void gemm_codes_kernel(GemmCodes
           reinterpret_cast<float *>(g.out)[(size_t)m * g.out_stride + nn] = v;
         }
       }
-  }
+    }
 }
 
 // ---- forms and their choice -----------------------------------------------
