@@ -99,3 +99,46 @@ def test_cache_lay_bitexact(backend, fmt):
     assert np.array_equal(got, want)
     dr.free()
     store.free()
+
+
+class _At:
+    """A device address inside a buffer (an unaligned query)."""
+
+    def __init__(self, buf, offset):
+        self.ptr = buf.ptr + offset
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("kv", [1, 2])
+@pytest.mark.parametrize("span,aligned", [(33, True), (64, True), (300, False), (511, True), (512, False)])
+def test_attend_short_span_kv_heads(backend, fmt, kv, span, aligned):
+    """One lane over 2-16 chunks of 32 positions (the sliding-window layers'
+    spans), with one and two key/value heads, 16-byte aligned and unaligned
+    queries, at a ring offset that wraps."""
+    head = 256
+    cache_span = 640
+    start = 600  # slots (600 + t) % 640: the span wraps
+    r = np.random.default_rng(span + 7 * kv + fmt)
+    scale = (4.0 / 448.0) if fmt == 0 else (4.0 / 127.0)
+    k = np.clip(r.normal(size=(cache_span, kv * head)), -4, 4).astype(np.float32)
+    v = np.clip(r.normal(size=(cache_span, kv * head)), -4, 4).astype(np.float32)
+    q = r.normal(size=(HEADS * kv, head)).astype(np.float32)
+    kb, vb = ol.encode(k, scale, fmt), ol.encode(v, scale, fmt)
+    print("case short span", "fmt", fmt, "kv", kv, "span", span, "aligned", aligned, flush=True)
+    dk, dv = backend.upload(kb), backend.upload(vb)
+    qbuf = backend.alloc(q.nbytes + 16)
+    off = 0 if aligned else 4
+    qbuf.put(q, off)
+    do = backend.alloc(q.nbytes)
+    backend.attend_dev(dk, dv, fmt, scale, scale, cache_span, kv, HEADS, head, _At(qbuf, off), start, span,
+                       1.0 / 16.0, do)
+    backend.sync()
+    got = do.get(np.float32, q.size).reshape(q.shape)
+    for b in (dk, dv, qbuf, do):
+        b.free()
+    grid = ol.grid8(scale) if fmt == 0 else ol.grid_i8(scale)
+    for j in range(kv):
+        want = ol.oracle_attend(kb, vb, grid, grid, cache_span, kv * head, j, q[HEADS * j:HEADS * (j + 1)],
+                                0, HEADS, head, start, span, 1.0 / 16.0)
+        err = float(np.max(np.abs(got[HEADS * j:HEADS * (j + 1)] - want)))
+        assert err <= 1e-3 * float(np.max(np.abs(want))) + 1e-5, (j, err)
