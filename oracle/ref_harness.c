@@ -405,6 +405,51 @@ int ref_engine_guess(const char *folder, int thread_count, int cache_bits, int w
   return (int)code;
 }
 
+/* Fixed speculative blocks after a prompt: block b is ids[first .. first +
+ * counts[b]) (first the sum of the earlier counts), run by session_guess
+ * (app_core.c:12139-12203) with every lane's pick (first maximum) and
+ * top-1/top-2 gap recorded, then session_guess_keep (12205-12223) of keeps[b]
+ * lanes.  Multi-lane blocks over inputs a random model's greedy stream never
+ * takes. */
+int ref_engine_blocks(const char *folder, int thread_count, int cache_bits, int window_limit,
+                      const int32_t *prompt, int prompt_count, const int32_t *ids, const int *counts,
+                      const int *keeps, int block_count, int32_t *picks_out, float *margins_out) {
+  app_setup setup = app_setup_plain();
+  app_model *model = NULL;
+  app_session *session = NULL;
+  app_code code;
+  int first = 0, vocab;
+  setup.thread_count = thread_count;
+  setup.cache_bits = cache_bits;
+  setup.window_limit = window_limit;
+  code = model_load(folder, &setup, &model);
+  if (code != APP_OKAY) return (int)code;
+  code = session_open(model, &session);
+  if (code == APP_OKAY) code = session_prime(session, prompt, prompt_count);
+  vocab = model_vocab_count(model);
+  for (int b = 0; code == APP_OKAY && b < block_count; ++b) {
+    const float *rows = session_guess(session, ids + first, counts[b]);
+    if (!rows) {
+      code = APP_FAIL_STATE;
+      break;
+    }
+    for (int l = 0; l < counts[b]; ++l) {
+      const float *logits = rows + (size_t)l * (size_t)vocab;
+      int best = ref_top(logits, vocab);
+      float second = -FLT_MAX;
+      for (int v = 0; v < vocab; ++v)
+        if (v != best && logits[v] > second) second = logits[v];
+      picks_out[first + l] = best;
+      margins_out[first + l] = logits[best] - second;
+    }
+    code = session_guess_keep(session, keeps[b]);
+    first += counts[b];
+  }
+  if (session) session_close(session);
+  model_free(model);
+  return (int)code;
+}
+
 /* One lane's grouped decode attention through the reference's own two jobs
  * (attend_score_band / attend_blend_band, app_core.c:11296-11365), forked over
  * the desk's pool exactly as session_attend_group forks them (11415-11453).

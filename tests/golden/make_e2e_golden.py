@@ -10,6 +10,7 @@ by oracle/Makefile), run on this repository's seeded synthetic checkpoint.
     python tests/golden/make_e2e_golden.py small_kinds   # the export's plane kinds, 20 layers
     python tests/golden/make_e2e_golden.py e2b_logits    # config.json dimensions, whole logit rows
     python tests/golden/make_e2e_golden.py small_packed  # I32-packed planes with zero points
+    python tests/golden/make_e2e_golden.py e2b_blocks    # config.json dimensions, fixed guess blocks
 
 For each, the checkpoint is written with igl_gemma_write (seed 0) into a
 scratch folder, the prompt is drawn by igllm_amd.engine.prompt_ids, and the
@@ -57,6 +58,11 @@ CASES = {
     # on every layer projection (4-bit, 2-bit MLPs from the middle layer, 8-bit
     # per-layer planes), zero points on all of them
     "small_packed": dict(shape=dict(SMALL, kinds=2), prompt=600, gen=128, window=1024, seed=1),
+    # config.json dimensions: fixed speculative blocks of 1-5 lanes of random
+    # ids (seed 2) after the prompt, each kept in part; every lane's pick and
+    # gap (the greedy stream there is one id; these walk many inputs)
+    "e2b_blocks": dict(shape={}, prompt=2048, gen=0, window=2560,
+                       counts=[2, 3, 5, 4, 2, 5, 1, 3, 4, 2, 5, 3], keeps=[1, 2, 5, 1, 2, 3, 1, 3, 2, 1, 4, 3]),
 }
 
 PATHS = {"plain": oracle_lib.REF_PLAIN_PATH, "tuned": oracle_lib.REF_TUNED_PATH,
@@ -127,6 +133,24 @@ def ref_guess(kind, folder, prompt, gen, window, threads, span):
     return out, stats, time.time() - t0
 
 
+def ref_blocks(kind, folder, prompt, ids, counts, keeps, window, threads):
+    lib = ctypes.CDLL(PATHS[kind])
+    fn = lib.ref_engine_blocks
+    fn.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                   ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                   ctypes.c_void_p]
+    c = np.array(counts, np.int32)
+    k = np.array(keeps, np.int32)
+    picks = np.zeros(ids.size, np.int32)
+    margin = np.zeros(ids.size, np.float32)
+    t0 = time.time()
+    code = fn(folder.encode(), threads, 8, window, prompt.ctypes.data, prompt.size, ids.ctypes.data, c.ctypes.data,
+              k.ctypes.data, c.size, picks.ctypes.data, margin.ctypes.data)
+    if code != 0:
+        raise SystemExit(f"ref_engine_blocks({kind}) returned {code}")
+    return picks, margin, time.time() - t0
+
+
 def main():
     name = sys.argv[1] if len(sys.argv) > 1 else "small"
     case = CASES[name]
@@ -138,6 +162,22 @@ def main():
               "gen": case["gen"], "window_limit": case["window"], "cache_bits": 8,
               "repeat_span": case.get("repeat", 0), "guess_span": case.get("span", 0),
               "shape": {k: getattr(shape, k) for k, _ in shape._fields_}}
+    if case.get("counts"):
+        counts, keeps = case["counts"], case["keeps"]
+        ids = prompt_ids(sum(counts), shape.vocab, seed=2)
+        result.update({"block_seed": 2, "counts": counts, "keeps": keeps, "block_ids": ids.tolist()})
+        for kind in ("plain", "tuned"):
+            picks, margin, secs = ref_blocks(kind, folder, prompt, ids, counts, keeps, case["window"], threads)
+            result[kind] = {"picks": picks.tolist(), "margin": [float(m) for m in margin], "seconds": secs}
+            print(kind, f"{secs:.1f}s", "distinct picks", len(set(picks.tolist())), "min margin",
+                  float(margin.min()), flush=True)
+        result["builds_max_margin_diff"] = float(np.max(np.abs(np.array(result["plain"]["margin"]) -
+                                                              np.array(result["tuned"]["margin"]))))
+        result["picks_agree"] = result["plain"]["picks"] == result["tuned"]["picks"]
+        with open(os.path.join(HERE, f"e2e_{name}.json"), "w") as f:
+            json.dump(result, f, indent=1)
+        print("picks agree", result["picks_agree"], "builds' margin spread", result["builds_max_margin_diff"])
+        return
     if case.get("probes"):
         probes = case["probes"]
         out = {}

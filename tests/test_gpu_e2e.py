@@ -256,6 +256,42 @@ def test_small_guess_stream_matches_reference(backend, small_model, graph):
     assert len(gaps) == fx["gen"] and gap <= 2e-3
 
 
+@pytest.mark.parametrize("precise,lane_limit,graph", [(True, 16, True), (True, 16, False), (False, 2048, True)])
+def test_e2b_fixed_blocks_match_reference(backend, e2b_model, precise, lane_limit, graph):
+    """config.json dimensions, the 2048-id prompt, then twelve fixed
+    speculative blocks of 1-5 lanes of random ids, each kept in part
+    (tests/golden/e2e_e2b_blocks.json: the reference's session_guess /
+    session_guess_keep on the same blocks).  Every lane's pick equals the
+    reference's and its top-1/top-2 gap is within max(2e-3, 3 x the spread
+    between the reference's two builds).  The greedy stream at this size is
+    one id; these blocks run multi-lane passes (graph-replayed below the GEMM
+    floor, or enqueued) over inputs it never takes."""
+    fx = load_fixture("e2b_blocks")
+    prompt = prompt_ids(fx["prompt_count"], fx["shape"]["vocab"], seed=fx["prompt_seed"])
+    ids = np.array(fx["block_ids"], dtype=np.int32)
+    eng = Engine(backend, e2b_model, window_limit=fx["window_limit"], lane_limit=lane_limit, precise=precise)
+    picks, gaps = [], []
+    try:
+        eng.set_graph(graph)
+        eng.prime(prompt)
+        first = 0
+        for count, keep in zip(fx["counts"], fx["keeps"]):
+            p, g = eng.guess(ids[first:first + count])
+            picks += p.tolist()
+            gaps += g.tolist()
+            eng.keep(keep)
+            first += count
+        fill = eng.fill
+    finally:
+        eng.close()
+    assert fill == fx["prompt_count"] - 1 + sum(fx["keeps"])
+    bar = max(2e-3, 3 * fx["builds_max_margin_diff"])
+    gap = float(np.max(np.abs(np.array(gaps) - np.array(fx["plain"]["margin"]))))
+    print("max gap difference", gap, "bar", bar)
+    assert picks == fx["plain"]["picks"]
+    assert gap <= bar
+
+
 def test_guess_graphs_replay_the_enqueued_blocks(backend, small_model):
     """A block replayed from its lane count's captured graph gives the picks and
     margins the same block gives enqueued, at every position it is replayed at,
