@@ -19,6 +19,7 @@
 #include "igl_launch.h"
 
 #define IGL_GEMV_LANES 8  /* lanes one GEMV launch carries */
+#define IGL_GEMV_Q4_LANES 16 /* lanes one 4-bit GEMV launch carries (the matrix-core form) */
 #define IGL_GEMM_FLOOR 64 /* lanes from which mat_mat takes the MFMA GEMM */
 
 struct igl_device_plane {
@@ -236,7 +237,7 @@ static size_t plane_part_floats(const igl_desk_state *st, const igl_plane *sheet
   if (!plane_is_q4(sheet))
     return igl_gemv_code_part_floats(sheet->bit_count, IGL_GEMV_LANES, sheet->row_count,
                                      sheet->col_count);
-  for (int lanes = 1; lanes <= IGL_GEMV_LANES; ++lanes) {
+  for (int lanes = 1; lanes <= IGL_GEMV_Q4_LANES; ++lanes) {
     size_t need = igl_gemv_part_floats(lanes, sheet->row_count, sheet->col_count, st->lds_limit);
     if (need > most) most = need;
   }
@@ -440,8 +441,8 @@ int igl_gemv_dev(igl_desk *desk, const igl_plane *sheet, const float *act_dev, i
                                                out_stride, sheet->row_count, sheet->col_count,
                                                st->part_dev, st->stream));
   }
-  for (done = 0; done < lane_count; done += IGL_GEMV_LANES) {
-    int lanes = lane_count - done < IGL_GEMV_LANES ? lane_count - done : IGL_GEMV_LANES;
+  for (done = 0; done < lane_count; done += IGL_GEMV_Q4_LANES) {
+    int lanes = lane_count - done < IGL_GEMV_Q4_LANES ? lane_count - done : IGL_GEMV_Q4_LANES;
     hipError_t e = igl_launch_gemv_q4(
         (const uint8_t *)dp->codes, (long long)sheet->row_stride, dp->gains, sheet->group_count,
         igl_plane_group_shift(sheet), sheet->code_bias, act_dev + (size_t)done * (size_t)act_stride,

@@ -1755,7 +1755,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
 }
 
 
-// ---- the small-lane form on the matrix cores (1..8 lanes) -----------------
+// ---- the small-lane form on the matrix cores (1..16 lanes) ----------------
 //
 // One v_mfma_f32_16x16x32_f16 per (16 rows, unit):
 //   * A (16 rows x 32 codes) is c - code_bias, exact in binary16.  A lane
@@ -1763,14 +1763,19 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
 //     16-lane groups of a wave and a 4 x 4 exchange of dwords between the
 //     groups (two permlane32 and two permlane16 swaps) leaves in group q the
 //     q-th eight codes of each unit, the layout the instruction reads.
-//   * B (32 codes x 16 columns): column m < 8 is lane m's activations times
-//     2^e rounded to binary16 (the high part), column m + 8 the remainder
-//     rounded again (the low part), so hi + lo carries x to 22 bits.  e is
-//     chosen per (unit, lane) to put the unit's largest |x| in [2^14, 2^15):
-//     neither part overflows, and the low part stays normal.
-//   * D columns m and m + 8 hold 2^e sum (c - bias) x_hi and ... x_lo, each a
-//     sum of exact products in fp32; 2^-e and the gain multiply them into
-//     the fp32 accumulator, and row_shr:8 adds the pair at the end.
+//   * B (32 codes x 16 columns): up to 8 lanes (narrow), column m < 8 is
+//     lane m's activations times 2^e rounded to binary16 (the high part),
+//     column m + 8 the remainder rounded again (the low part), so hi + lo
+//     carries x to 22 bits; 9 to 16 lanes (WIDE), column m is lane m in two
+//     B tiles, the high parts and the low parts.  e is chosen per (unit,
+//     lane) to put the unit's largest |x| in [2^14, 2^15): neither part
+//     overflows, and the low part stays normal.
+//   * narrow: D columns m and m + 8 hold 2^e sum (c - bias) x_hi and ... x_lo,
+//     each a sum of exact products in fp32; 2^-e and the gain multiply them
+//     into the fp32 accumulator, and row_shr:8 adds the pair at the end.
+//     WIDE: the low tile's product accumulates onto the high tile's, so D
+//     column m holds 2^e sum (c - bias) (x_hi + x_lo) for lane m; the weights
+//     are read and converted once for all 16 lanes.
 // A workgroup owns `tiles_per_block` 16-row tiles over a chunk of
 // `chunk_units` units; its four waves split that as tiles x K-parts and build
 // the chunk's B tiles and gains in LDS once while their code loads are in
@@ -1818,18 +1823,22 @@ __device__ __forceinline__ half8_t codes_less_bias(uint32_t d, uint32_t exp16, h
 
 constexpr int kMfmaGains = 4;  // pad of the gain rows in LDS (keeps 16-byte reads aligned)
 
-template <int NG, bool VEC>
+template <int NG, bool VEC, bool WIDE>
 __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
+  // lanes a B column holds, the tiles a k-chunk has, activation items a thread
+  constexpr int kCols = WIDE ? 16 : 8;
+  constexpr int kTerms = WIDE ? 2 : 1;
+  constexpr int kIt = WIDE ? 16 : 8;
   extern __shared__ uint4_t lds_u4[];
   const int RTB = a.tiles_per_block;
   const int parts = 4 / RTB;
   const int CU = a.chunk_units;
   const int rows_b = RTB * 16;
   const int pitch = rows_b + kMfmaGains;
-  uint4_t *bt = lds_u4;                                       // [CU][4 groups][16 columns]
-  float *gs = reinterpret_cast<float *>(bt + CU * 64);        // [CU][pitch]
-  float *sc = gs + CU * pitch;                                // [CU][8]
-  float *red = sc + CU * 8;                                   // [parts][RTB][16][8]
+  uint4_t *bt = lds_u4;                                       // [CU][4 groups][terms][16 columns]
+  float *gs = reinterpret_cast<float *>(bt + CU * 64 * kTerms);  // [CU][pitch]
+  float *sc = gs + CU * pitch;                                // [CU][kCols]
+  float *red = sc + CU * kCols;                               // [parts][RTB][16][kCols]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1850,17 +1859,18 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
   // codes are still in flight (gains first: 3.3 us into the launch under a
   // full stream, against about 1 us for the activations).
   // Activations: item i = 4 M u + 4 m + g is x[m][32 u + 8 g .. + 7] (at most
-  // 8 a thread: 64 units x 8 lanes x 4 groups).  B columns m >= M are never
+  // kIt a thread: 64 units x 16 lanes x 4 groups).  B columns m >= M are never
   // written; they only reach outputs that are not stored.  u = i / (4 M) by a
-  // multiply, exact for every i < 2048 and M <= 8.
+  // multiply, exact for every i < 4096 and M <= 16 (the 2^21 reciprocal's
+  // excess, i / 2^21 < 1 / 512, stays under 1 / (4 M)).
   const int per_u = 4 * a.M;
   const int items = CU * per_u;
-  const uint32_t inv_u = (65536u + (uint32_t)per_u - 1u) / (uint32_t)per_u;
-  float4_t xa[8], xb[8];
+  const uint32_t inv_u = ((1u << 21) + (uint32_t)per_u - 1u) / (uint32_t)per_u;
+  float4_t xa[kIt], xb[kIt];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
+  for (int k = 0; k < kIt; ++k) {
     const int i = min(tid + 256 * k, items - 1);
-    const int u = (int)(((uint32_t)i * inv_u) >> 16);
+    const int u = (int)(((uint32_t)i * inv_u) >> 21);
     const int m = (i - u * per_u) >> 2;
     const float *src =
         a.act + (size_t)m * (size_t)a.act_stride + (size_t)(unit_c0 + u) * 32 + 8 * (i & 3);
@@ -1910,12 +1920,12 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
   // Past the items (a bound uniform over the workgroup) a thread's quads
   // recompute the last item and store nothing.
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
+  for (int k = 0; k < kIt; ++k) {
     if (256 * k >= items) break;
     const int i_raw = tid + 256 * k;
     const bool own = i_raw < items;
     const int i = min(i_raw, items - 1);
-    const int u = (int)(((uint32_t)i * inv_u) >> 16);
+    const int u = (int)(((uint32_t)i * inv_u) >> 21);
     const int rem = i - u * per_u;
     const int g = rem & 3;
     const int m = rem >> 2;
@@ -1932,7 +1942,7 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
       e = min(max(15 - power, -126), 126);
     }
     const float up = __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
-    if (own && g == 0) sc[u * 8 + m] = __builtin_bit_cast(float, (uint32_t)(127 - e) << 23);
+    if (own && g == 0) sc[u * kCols + m] = __builtin_bit_cast(float, (uint32_t)(127 - e) << 23);
     half8_t hi, lo;
     constexpr int kOrder[8] = {0, 4, 1, 5, 2, 6, 3, 7};
 #pragma unroll
@@ -1943,8 +1953,13 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
       lo[j] = (_Float16)(s - (float)h);
     }
     if (own) {
-      bt[(u * 4 + g) * 16 + m] = __builtin_bit_cast(uint4_t, hi);
-      bt[(u * 4 + g) * 16 + m + 8] = __builtin_bit_cast(uint4_t, lo);
+      if (WIDE) {
+        bt[((u * 4 + g) * 2 + 0) * 16 + m] = __builtin_bit_cast(uint4_t, hi);
+        bt[((u * 4 + g) * 2 + 1) * 16 + m] = __builtin_bit_cast(uint4_t, lo);
+      } else {
+        bt[(u * 4 + g) * 16 + m] = __builtin_bit_cast(uint4_t, hi);
+        bt[(u * 4 + g) * 16 + m + 8] = __builtin_bit_cast(uint4_t, lo);
+      }
     }
   }
   // Gains stored [unit][row]: here only without VEC (every thread over the
@@ -1980,20 +1995,25 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
   const uint32_t exp16 = 0x4C004C00u;
   const _Float16 lift = (_Float16)(16.0f + a.code_bias);
   const half2_t shift = half2_t{lift, lift};
-  const int m_col = r & 7;
+  // narrow: lanes r and r - 8 hold one lane's high and low columns, one scale
+  const int m_col = WIDE ? r : (r & 7);
   float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
   // A group is four units: its B tiles, gains and scales are read from LDS
   // one group ahead, its four products issue back to back, then the gains.
+  // B tile of unit u for this lane (k-chunk q, column r): narrow one, WIDE
+  // the high and the low parts.
+  auto b_at = [&](int u, int term) { return WIDE ? bt[u * 128 + q * 32 + term * 16 + r] : bt[u * 64 + lane]; };
   const float *gbase = gs + 16 * t + 4 * q;
-  uint4_t bq[2][4];
+  uint4_t bq[2][4][kTerms];
   float4_t gq[2][4];
   float sq[2][4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int u = u_w0 + j;
-    bq[0][j] = bt[u * 64 + lane];
+#pragma unroll
+    for (int e = 0; e < kTerms; ++e) bq[0][j][e] = b_at(u, e);
     gq[0][j] = *reinterpret_cast<const float4_t *>(gbase + u * pitch);
-    sq[0][j] = sc[u * 8 + m_col];
+    sq[0][j] = sc[u * kCols + m_col];
   }
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
@@ -2002,19 +2022,24 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int u = u_w0 + 4 * (g + 1) + j;
-        bq[cur ^ 1][j] = bt[u * 64 + lane];
+#pragma unroll
+        for (int e = 0; e < kTerms; ++e) bq[cur ^ 1][j][e] = b_at(u, e);
         gq[cur ^ 1][j] = *reinterpret_cast<const float4_t *>(gbase + u * pitch);
-        sq[cur ^ 1][j] = sc[u * 8 + m_col];
+        sq[cur ^ 1][j] = sc[u * kCols + m_col];
       }
     }
     uint32_t d[4] = {w[g].x, w[g].y, w[g].z, w[g].w};
     lane_group_exchange(d[0], d[1], d[2], d[3]);
     float4_t D[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      D[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_less_bias(d[j], exp16, shift),
-                                                    __builtin_bit_cast(half8_t, bq[cur][j]),
+    for (int j = 0; j < 4; ++j) {
+      const half8_t c = codes_less_bias(d[j], exp16, shift);
+      D[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(c, __builtin_bit_cast(half8_t, bq[cur][j][0]),
                                                     float4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+      if (WIDE)
+        D[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(c, __builtin_bit_cast(half8_t, bq[cur][j][kTerms - 1]), D[j],
+                                                      0, 0, 0);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float s = sq[cur][j];
@@ -2024,14 +2049,16 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
       acc.w = __builtin_fmaf(gq[cur][j].w * s, D[j].w, acc.w);
     }
   }
-  // Low columns into their high partners: lane r >= 8 holds lane m = r - 8.
-  acc.x += dpp_move<0x118>(acc.x);
-  acc.y += dpp_move<0x118>(acc.y);
-  acc.z += dpp_move<0x118>(acc.z);
-  acc.w += dpp_move<0x118>(acc.w);
-
-  const int m = r - 8;
-  const bool owner = r >= 8 && m < a.M;
+  // narrow: low columns into their high partners (lane r >= 8 holds lane
+  // m = r - 8); WIDE: lane r holds lane m = r whole.
+  if (!WIDE) {
+    acc.x += dpp_move<0x118>(acc.x);
+    acc.y += dpp_move<0x118>(acc.y);
+    acc.z += dpp_move<0x118>(acc.z);
+    acc.w += dpp_move<0x118>(acc.w);
+  }
+  const int m = WIDE ? r : r - 8;
+  const bool owner = (WIDE || r >= 8) && m < a.M;
   float *dst;
   int dst_stride;
   if (gridDim.y > 1) {
@@ -2053,11 +2080,11 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
     return;
   }
   if (owner) {
-    float *slot = red + ((part * RTB + t) * 16 + 4 * q) * 8 + m;
+    float *slot = red + ((part * RTB + t) * 16 + 4 * q) * kCols + m;
     slot[0] = acc.x;
-    slot[8] = acc.y;
-    slot[16] = acc.z;
-    slot[24] = acc.w;
+    slot[kCols] = acc.y;
+    slot[2 * kCols] = acc.z;
+    slot[3 * kCols] = acc.w;
   }
   __syncthreads();
   if (part == 0 && owner) {
@@ -2065,7 +2092,7 @@ __global__ __launch_bounds__(256) void gemv_q4_mfma_kernel(GemvMfmaArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float total = 0.0f;
-      for (int k = 0; k < parts; ++k) total += red[((k * RTB + t) * 16 + 4 * q + i) * 8 + m];
+      for (int k = 0; k < parts; ++k) total += red[((k * RTB + t) * 16 + 4 * q + i) * kCols + m];
       if (row0 + i < a.N) o[row0 + i] = total;
     }
   }
@@ -2078,7 +2105,7 @@ struct GemvMfmaPlan {
 };
 
 static int gemv_mfma_plan(int lanes, int N, int K, GemvMfmaPlan *plan) {
-  if (lanes < 1 || lanes > 8 || K % 128 || N < 1) return 0;
+  if (lanes < 1 || lanes > 16 || K % 128 || N < 1) return 0;
   const int units = K / 32;
   const int groups = units / 4;
   const int tiles = (N + 15) / 16;
@@ -2107,36 +2134,49 @@ static int gemv_mfma_plan(int lanes, int N, int K, GemvMfmaPlan *plan) {
     plan->chunks = kb;
     plan->groups_per_wave = groups / kb;
   }
+  // past 8 lanes a wave holds twice the B tiles: more than 8 groups a wave
+  // would spill, and such planes take launches of 8 lanes instead
+  if (lanes > 8 && plan->groups_per_wave > 8) return 0;
   return plan->groups_per_wave >= 1 && plan->groups_per_wave <= 16;
 }
 
-static size_t gemv_mfma_lds(const GemvMfmaPlan &p) {
+// LDS of a launch: the B tiles (one or, past 8 lanes, two a k-chunk), the
+// gains, the scales and the reduction across K-parts.
+static size_t gemv_mfma_lds(const GemvMfmaPlan &p, int lanes) {
   const int rows_b = p.tiles_per_block * 16;
-  return (size_t)p.chunk_units * 1024 + (size_t)p.chunk_units * (rows_b + kMfmaGains) * 4 +
-         (size_t)p.chunk_units * 32 + (size_t)4 * 16 * 8 * 4;
+  const size_t cols = lanes > 8 ? 16 : 8;
+  return (size_t)p.chunk_units * 1024 * (lanes > 8 ? 2 : 1) + (size_t)p.chunk_units * (rows_b + kMfmaGains) * 4 +
+         (size_t)p.chunk_units * cols * 4 + (size_t)4 * 16 * cols * 4;
 }
 
-template <int NG, bool VEC>
+template <int NG, bool VEC, bool WIDE>
 static hipError_t gemv_mfma_launch_form(const GemvMfmaArgs &a, const GemvMfmaPlan &p,
                                         hipStream_t stream) {
-  const size_t lds = gemv_mfma_lds(p);
+  const size_t lds = gemv_mfma_lds(p, a.M);
   static size_t lds_granted = 65536;  // launches above 64 KiB ask once
   if (lds > lds_granted) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q4_mfma_kernel<NG, VEC>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q4_mfma_kernel<NG, VEC, WIDE>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     lds_granted = lds;
   }
   const int tiles = (a.N + 15) / 16;
   dim3 grid((tiles + p.tiles_per_block - 1) / p.tiles_per_block, p.chunks);
-  hipLaunchKernelGGL((gemv_q4_mfma_kernel<NG, VEC>), grid, dim3(256), lds, stream, a);
+  hipLaunchKernelGGL((gemv_q4_mfma_kernel<NG, VEC, WIDE>), grid, dim3(256), lds, stream, a);
   return hipGetLastError();
 }
 
 template <int NG>
 static hipError_t gemv_mfma_launch(const GemvMfmaArgs &a, const GemvMfmaPlan &p, hipStream_t stream) {
-  return a.act_vec && a.gain_vec ? gemv_mfma_launch_form<NG, true>(a, p, stream)
-                                 : gemv_mfma_launch_form<NG, false>(a, p, stream);
+  const bool vec = a.act_vec && a.gain_vec;
+  if (a.M > 8) {
+    if (NG > 8) return hipErrorInvalidValue;  // the plan refuses it
+    constexpr int kNG = NG > 8 ? 8 : NG;
+    return vec ? gemv_mfma_launch_form<kNG, true, true>(a, p, stream)
+               : gemv_mfma_launch_form<kNG, false, true>(a, p, stream);
+  }
+  return vec ? gemv_mfma_launch_form<NG, true, false>(a, p, stream)
+             : gemv_mfma_launch_form<NG, false, false>(a, p, stream);
 }
 
 static hipError_t gemv_mfma_dispatch(const GemvMfmaArgs &a, const GemvMfmaPlan &p, hipStream_t stream) {
@@ -3077,6 +3117,8 @@ extern "C" hipError_t igl_launch_gemv_real(const void *rows, int real_type, cons
 // writes (0 when it needs none).
 extern "C" size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit) {
   GemvMfmaPlan plan;
+  // past 8 lanes without the matrix-core form: launches of 8 lanes in turn
+  if (lanes > 8 && !gemv_mfma_plan(lanes, N, K, &plan)) return igl_gemv_part_floats(8, N, K, lds_limit);
   if (lanes >= 3 && gemv_mfma_plan(lanes, N, K, &plan))
     return plan.chunks > 1 ? (size_t)plan.chunks * (size_t)lanes * (size_t)N : 0;
   if (lanes <= 2 && K / 32 <= 8 * kWave) return 0;
@@ -3085,7 +3127,7 @@ extern "C" size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit) {
   return chunks > 1 ? chunks * (size_t)lanes * (size_t)N : 0;
 }
 
-// Launches y = W x for 1..8 lanes.  `part` must hold chunks * lanes * N floats
+// Launches y = W x for 1..16 lanes (past 16: chunks of 8).  `part` must hold chunks * lanes * N floats
 // when the plane needs more than one K-chunk, and may be NULL otherwise;
 // `lds_limit` is the device's LDS bytes per workgroup.
 extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_stride,
@@ -3093,6 +3135,22 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
                                          int code_bias, const float *act, int act_stride,
                                          int lanes, float *out, int out_stride, int N, int K,
                                          float *part, int lds_limit, hipStream_t stream) {
+  // 9 to 16 lanes: one matrix-core launch where the form applies, else
+  // launches of 8 lanes in turn
+  if (lanes > 8) {
+    GemvMfmaPlan probe;
+    if (lanes > 16 || !gemv_mfma_plan(lanes, N, K, &probe)) {
+      for (int done = 0; done < lanes; done += 8) {
+        const int n = lanes - done < 8 ? lanes - done : 8;
+        const hipError_t e = igl_launch_gemv_q4(codes, row_stride, gains, gain_stride, group_shift, code_bias,
+                                                act + (size_t)done * (size_t)act_stride, act_stride, n,
+                                                out + (size_t)done * (size_t)out_stride, out_stride, N, K, part,
+                                                lds_limit, stream);
+        if (e != hipSuccess) return e;
+      }
+      return hipSuccess;
+    }
+  }
   GemvArgs a;
   a.codes = codes;
   a.row_stride = row_stride;

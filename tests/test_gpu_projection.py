@@ -61,7 +61,7 @@ def test_decode_gemv_config0(backend):
 
 
 @pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 8192)])
-@pytest.mark.parametrize("lanes", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("lanes", [1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 16])
 def test_small_lane_sweep(backend, N, K, lanes):
     print_case(test="sweep", N=N, K=K, lanes=lanes)
     codes, gains, act = synth_projection(N, K, lanes, seed=lanes)
