@@ -94,7 +94,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decode leg")
     ap.add_argument("--kernel", choices=["gemv", "gemv8", "gemm", "attend", "copy", "head2", "real", "calib",
-                                         "readfloor", "decode"],
+                                         "readfloor", "decode", "guess"],
                     help="run one kernel's workload alone in a loop (for rocprofv3) and exit")
     ap.add_argument("--lanes", type=int, default=2048, help="--kernel gemm: the lane count M")
     ap.add_argument("--shape", type=int, default=0, choices=[0, 1],
@@ -239,6 +239,9 @@ def kernel_loop(be, name, reps, lanes=2048, shape=0):
         return
     if name == "decode":
         decode_loop(be, reps)
+        return
+    if name == "guess":
+        guess_loop_blocks(be, reps)
 
 
 def decode_loop(be, steps):
@@ -270,6 +273,36 @@ def decode_loop(be, steps):
         import shutil
         shutil.rmtree(folder, ignore_errors=True)
     print(json.dumps({"kernel": "decode", "prompt": 2048, "steps": steps}))
+
+
+def guess_loop_blocks(be, blocks, lanes=2):
+    """Speculative blocks alone, for kernel traces: the synthetic E2B
+    checkpoint, a 2048-id prompt primed, then `blocks` blocks of `lanes` ids
+    (the next input and a proposal) launched eagerly and not kept: the
+    --guess leg's 2-lane round without its step graph."""
+    import tempfile
+    from igllm_amd.engine import Engine, prompt_ids, write_gemma
+
+    root = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
+    folder = os.path.join(root, f"igl_gemma_e2b_{os.getpid()}")
+    try:
+        shape = write_gemma(folder, seed=0)
+        prompt = prompt_ids(2048, shape.vocab, seed=0)
+        eng = Engine(be, folder, window_limit=2048 + 64, lane_limit=16, precise=True)
+        try:
+            eng.set_graph(False)
+            eng.prime(prompt)
+            block = np.full(lanes, int(prompt[-1]), np.int32)
+            for _ in range(blocks):
+                eng.guess(block)
+                eng.keep(0)
+            be.sync()
+        finally:
+            eng.close()
+    finally:
+        import shutil
+        shutil.rmtree(folder, ignore_errors=True)
+    print(json.dumps({"kernel": "guess", "prompt": 2048, "blocks": blocks, "lanes": lanes}))
 
 
 def cpu_e2e(folder, prompt, gen=8, prime=2048):
