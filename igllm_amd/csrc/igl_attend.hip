@@ -63,6 +63,7 @@ namespace igl {
 constexpr int kAttendShortSpan = 8192;
 constexpr int kAttendWideLanes = 64;
 constexpr int kAttendGroup = 8;                    // query heads per key/value head
+constexpr int kAttendPrepLanes = 4;                // lanes of one prepared launch
 
 struct AttendArgs {
   const uint8_t *key_store;    // [cache_span][kv_width]
@@ -82,18 +83,22 @@ struct AttendArgs {
   float *part_peak;            // [chunks][head_count]
   float *part_total;           // [chunks][head_count]
   int head_count;
-  // The decode step's heads prepared here (attend_split_kernel's PREP form):
-  // `query` holds the query heads before their norm; q_gain their gain; turn
-  // the (cos, sin) of the lane's position times each rotation step, HEAD / 2
-  // pairs.  With k_raw set, the lane's own position gets a workgroup of its
-  // own after the chunks of the positions before it (attend_new_row): it
-  // prepares the key and value heads (norm and gain and turn; norm), writes
-  // their bytes into ring slot position % cache_span of k_ring / v_ring (the
-  // rings read here), code = e4m3(value / scale), and writes the position's
-  // partial; the chunk workgroups never read that slot.
+  // The heads of a decode step or a small block prepared here
+  // (attend_split_kernel's PREP form): `query` holds the query heads before
+  // their norm; q_gain their gain; turn, lane by lane, the (cos, sin) of the
+  // lane's position times each rotation step, HEAD / 2 pairs.  With k_raw
+  // set, the block's new positions place .. place + l (lane l's, and the
+  // lanes' before it) get a workgroup of lane l's own after the chunks of the
+  // positions before the block (attend_fresh_rows): it prepares their key and
+  // value heads (norm and gain and turn; norm), writes lane l's bytes into
+  // ring slot (place + l) % cache_span of k_ring / v_ring (the rings read
+  // here), code = e4m3(value / scale), and writes the partial of those
+  // positions; the chunk workgroups never read those slots.
   const float *q_gain;
-  const float *turn;           // [HEAD / 2][2]
-  const float *k_raw;
+  const float *turn;           // [lanes][HEAD / 2][2]
+  int turn_stride;             // floats between lanes of turn
+  const float *k_raw;          // [lanes][kv_raw_stride], as v_raw
+  int kv_raw_stride;
   const float *v_raw;
   const float *k_gain;
   uint8_t *k_ring;
@@ -137,43 +142,63 @@ __device__ __forceinline__ float xsum32(float v) {
   return lo + hi;
 }
 
-// The decode step's new position, a workgroup of its own (PREP with k_raw):
-// the key and value heads prepared (norm, gain, turn; norm) and written to the
-// rings as e4m3 bytes, the 8 query heads prepared as every chunk prepares them,
-// and the position's partial: score_h = key_scale q_h . key(bytes) in fp32, peak
-// score_h, total 1, blend the value bytes times value_scale.  Off the path of
-// the chunk workgroups, which end before it.
+// The block's new positions seen by lane l, pos0 .. pos0 + l, a workgroup of
+// the lane's own (PREP with k_raw): the key and value heads of each new
+// position prepared (norm, gain, turn; norm), lane l writing only its own
+// position's bytes to the rings (lanes before it write theirs, from the same
+// arithmetic on the same inputs); the lane's 8 query heads prepared as every
+// chunk prepares them; and one partial over those l + 1 positions: score_h,j
+// = key_scale q_h . key_j(bytes) in fp32, peak_h = max_j score_h,j, total_h =
+// sum_j e^(score_h,j - peak_h), blend_h = sum_j e^(score_h,j - peak_h)
+// value_j(bytes) value_scale (one position: peak = its score, total 1, blend
+// its value).  Off the path of the chunk workgroups, which end before it.
 template <int HEAD>
-__device__ __forceinline__ void attend_new_row(const AttendArgs &a, int pos, int pc) {
+__device__ __forceinline__ void attend_fresh_rows(const AttendArgs &a, int pos0, int l, int pc) {
   constexpr int HALF = HEAD / 2;
   constexpr int W = 4;
+  constexpr int F = kAttendPrepLanes;
   constexpr int kHeadItems = HEAD / 8;
   constexpr int kQItems = kAttendGroup * HEAD / 8 / 256;
-  __shared__ double nr_red[2][W];
-  __shared__ __attribute__((aligned(16))) uint8_t nr_bytes[2][HEAD];
-  __shared__ float nr_score[kAttendGroup][256 / kHeadItems > 0 ? 256 / kHeadItems : 1];
+  __shared__ double nr_red[F][2][W];
+  __shared__ __attribute__((aligned(16))) uint8_t nr_bytes[F][2][HEAD];
+  __shared__ float nr_score[kAttendGroup][F];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  // every load first: the key/value pair of the thread (threads below HALF),
-  // then its query items with their gains and turns
-  float kx[2] = {0.0f, 0.0f}, vx[2] = {0.0f, 0.0f}, kg[2] = {0.0f, 0.0f}, kt[2] = {0.0f, 0.0f};
+  const int rows = l + 1;  // uniform, at most F
+  // every load first: the key/value pairs of the thread (threads below
+  // HALF) of each new position, then its query items with their gains and
+  // turns
+  float kx[F][2], vx[F][2], kt[F][2], kg[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < F; ++j) {
+    kx[j][0] = kx[j][1] = vx[j][0] = vx[j][1] = kt[j][0] = kt[j][1] = 0.0f;
+  }
   if (tid < HALF) {
-    kx[0] = a.k_raw[tid];
-    kx[1] = a.k_raw[tid + HALF];
-    vx[0] = a.v_raw[tid];
-    vx[1] = a.v_raw[tid + HALF];
     kg[0] = a.k_gain[tid];
     kg[1] = a.k_gain[tid + HALF];
-    kt[0] = a.turn[2 * tid];
-    kt[1] = a.turn[2 * tid + 1];
+#pragma unroll
+    for (int j = 0; j < F; ++j) {
+      if (j < rows) {
+        const float *kr = a.k_raw + (size_t)j * a.kv_raw_stride;
+        const float *vr = a.v_raw + (size_t)j * a.kv_raw_stride;
+        const float *tr = a.turn + (size_t)j * a.turn_stride;
+        kx[j][0] = kr[tid];
+        kx[j][1] = kr[tid + HALF];
+        vx[j][0] = vr[tid];
+        vx[j][1] = vr[tid + HALF];
+        kt[j][0] = tr[2 * tid];
+        kt[j][1] = tr[2 * tid + 1];
+      }
+    }
   }
   float qf[kQItems][8];
   float4_t qgain[kQItems][2], qturn[kQItems][4];
+  const float *own_turn = a.turn + (size_t)l * a.turn_stride;
 #pragma unroll
   for (int i = 0; i < kQItems; ++i) {
     const int item = tid + 256 * i;
-    const float4_t *q = reinterpret_cast<const float4_t *>(a.query + 8 * item);
+    const float4_t *q = reinterpret_cast<const float4_t *>(a.query + (size_t)l * a.q_stride + 8 * item);
     const float4_t u = q[0], v = q[1];
     qf[i][0] = u.x; qf[i][1] = u.y; qf[i][2] = u.z; qf[i][3] = u.w;
     qf[i][4] = v.x; qf[i][5] = v.y; qf[i][6] = v.z; qf[i][7] = v.w;
@@ -182,50 +207,63 @@ __device__ __forceinline__ void attend_new_row(const AttendArgs &a, int pos, int
     qgain[i][0] = *reinterpret_cast<const float4_t *>(a.q_gain + d0);
     qgain[i][1] = *reinterpret_cast<const float4_t *>(a.q_gain + d0 + 4);
 #pragma unroll
-    for (int w = 0; w < 4; ++w) qturn[i][w] = *reinterpret_cast<const float4_t *>(a.turn + 2 * j0 + 4 * w);
+    for (int w = 0; w < 4; ++w) qturn[i][w] = *reinterpret_cast<const float4_t *>(own_turn + 2 * j0 + 4 * w);
   }
-  // key: norm, gain, turn; value: norm (session_attend 11504-11510)
+  // keys: norm, gain, turn; values: norm (session_attend 11504-11510), every
+  // new position's sums behind one barrier
   {
-    double ks = (double)kx[0] * (double)kx[0] + (double)kx[1] * (double)kx[1];
-    double vs2 = (double)vx[0] * (double)vx[0] + (double)vx[1] * (double)vx[1];
-    ks = wave_sum_f64_to_last(ks);
-    vs2 = wave_sum_f64_to_last(vs2);
-    if (lane == 63) {
-      nr_red[0][wave] = ks;
-      nr_red[1][wave] = vs2;
+#pragma unroll
+    for (int j = 0; j < F; ++j) {
+      if (j < rows) {
+        double ks = (double)kx[j][0] * (double)kx[j][0] + (double)kx[j][1] * (double)kx[j][1];
+        double vs2 = (double)vx[j][0] * (double)vx[j][0] + (double)vx[j][1] * (double)vx[j][1];
+        ks = wave_sum_f64_to_last(ks);
+        vs2 = wave_sum_f64_to_last(vs2);
+        if (lane == 63) {
+          nr_red[j][0][wave] = ks;
+          nr_red[j][1][wave] = vs2;
+        }
+      }
     }
     __syncthreads();
-    double kt_sum = nr_red[0][0], vt_sum = nr_red[1][0];
 #pragma unroll
-    for (int w = 1; w < W; ++w) {
-      kt_sum += nr_red[0][w];
-      vt_sum += nr_red[1][w];
-    }
-    if (tid < HALF) {
-      const float ksh = rms_shrink(kt_sum, HEAD, a.eps);
-      const float vsh = rms_shrink(vt_sum, HEAD, a.eps);
-      float lo = kx[0] * ksh, hi = kx[1] * ksh;
-      lo = lo * kg[0];
-      hi = hi * kg[1];
-      const float k0 = lo * kt[0] - hi * kt[1];
-      const float k1 = hi * kt[0] + lo * kt[1];
-      const uint8_t b0 = e4m3_code(k0 / a.k_code_scale), b1 = e4m3_code(k1 / a.k_code_scale);
-      const uint8_t c0b = e4m3_code(vx[0] * vsh / a.v_code_scale);
-      const uint8_t c1b = e4m3_code(vx[1] * vsh / a.v_code_scale);
-      const size_t row = (size_t)(pos % a.cache_span) * a.kv_width;
-      a.k_ring[row + tid] = b0;
-      a.k_ring[row + tid + HALF] = b1;
-      a.v_ring[row + tid] = c0b;
-      a.v_ring[row + tid + HALF] = c1b;
-      nr_bytes[0][tid] = b0;
-      nr_bytes[0][tid + HALF] = b1;
-      nr_bytes[1][tid] = c0b;
-      nr_bytes[1][tid + HALF] = c1b;
+    for (int j = 0; j < F; ++j) {
+      if (j < rows) {
+        double kt_sum = nr_red[j][0][0], vt_sum = nr_red[j][1][0];
+#pragma unroll
+        for (int w = 1; w < W; ++w) {
+          kt_sum += nr_red[j][0][w];
+          vt_sum += nr_red[j][1][w];
+        }
+        if (tid < HALF) {
+          const float ksh = rms_shrink(kt_sum, HEAD, a.eps);
+          const float vsh = rms_shrink(vt_sum, HEAD, a.eps);
+          float lo = kx[j][0] * ksh, hi = kx[j][1] * ksh;
+          lo = lo * kg[0];
+          hi = hi * kg[1];
+          const float k0 = lo * kt[j][0] - hi * kt[j][1];
+          const float k1 = hi * kt[j][0] + lo * kt[j][1];
+          const uint8_t b0 = e4m3_code(k0 / a.k_code_scale), b1 = e4m3_code(k1 / a.k_code_scale);
+          const uint8_t c0b = e4m3_code(vx[j][0] * vsh / a.v_code_scale);
+          const uint8_t c1b = e4m3_code(vx[j][1] * vsh / a.v_code_scale);
+          if (j == l) {
+            const size_t row = (size_t)((pos0 + l) % a.cache_span) * a.kv_width;
+            a.k_ring[row + tid] = b0;
+            a.k_ring[row + tid + HALF] = b1;
+            a.v_ring[row + tid] = c0b;
+            a.v_ring[row + tid + HALF] = c1b;
+          }
+          nr_bytes[j][0][tid] = b0;
+          nr_bytes[j][0][tid + HALF] = b1;
+          nr_bytes[j][1][tid] = c0b;
+          nr_bytes[j][1][tid + HALF] = c1b;
+        }
+      }
     }
   }
   __syncthreads();
   // the query heads as the chunks prepare them, then each item's share of
-  // its head's score against the decoded key bytes
+  // its head's score against each new position's decoded key bytes
 #pragma unroll
   for (int i = 0; i < kQItems; ++i) {
     const int item = tid + 256 * i;
@@ -248,36 +286,53 @@ __device__ __forceinline__ void attend_new_row(const AttendArgs &a, int pos, int
 #pragma unroll
     for (int e = 0; e < 8; ++e) other[e] = __shfl_xor(own[e], kHeadItems / 2);
     const bool low = d0 < HALF;
-    const uint2_t kb = *reinterpret_cast<const uint2_t *>(&nr_bytes[0][d0]);
-    const half8_t kd = decode8<0>(kb.x, kb.y);
-    float part = 0.0f;
+    float qv[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float c = qturn[i][e >> 1][2 * (e & 1)];
       const float sn = qturn[i][e >> 1][2 * (e & 1) + 1];
-      const float qv = low ? own[e] * c - other[e] * sn : own[e] * c + other[e] * sn;
-      part = __builtin_fmaf(qv, (float)kd[e], part);
+      qv[e] = low ? own[e] * c - other[e] * sn : own[e] * c + other[e] * sn;
     }
 #pragma unroll
-    for (int off = kHeadItems / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
-    if (item % kHeadItems == 0) nr_score[h][0] = part * a.key_scale;
+    for (int j = 0; j < F; ++j) {
+      if (j < rows) {
+        const uint2_t kb = *reinterpret_cast<const uint2_t *>(&nr_bytes[j][0][d0]);
+        const half8_t kd = decode8<0>(kb.x, kb.y);
+        float part = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part = __builtin_fmaf(qv[e], (float)kd[e], part);
+#pragma unroll
+        for (int off = kHeadItems / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
+        if (item % kHeadItems == 0) nr_score[h][j] = part * a.key_scale;
+      }
+    }
   }
   __syncthreads();
-  // the partial: every head blends the one value row with weight e^0 = 1
+  // the partial: each head blends the new value rows, weighted against its peak
   for (int i = tid; i < kAttendGroup * HEAD / 8; i += 256) {
     const int h = i / (HEAD / 8);
     const int d0 = 8 * (i % (HEAD / 8));
-    const uint2_t vb = *reinterpret_cast<const uint2_t *>(&nr_bytes[1][d0]);
-    const half8_t vd = decode8<0>(vb.x, vb.y);
+    float peak = nr_score[h][0];
+    for (int j = 1; j < rows; ++j) peak = fmaxf(peak, nr_score[h][j]);
+    float o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < rows; ++j) {
+      const float wgt = __expf(nr_score[h][j] - peak);
+      const uint2_t vb = *reinterpret_cast<const uint2_t *>(&nr_bytes[j][1][d0]);
+      const half8_t vd = decode8<0>(vb.x, vb.y);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += wgt * ((float)vd[e] * a.value_scale);
+    }
     float *dst = a.part_out + ((size_t)pc * a.head_count + h) * HEAD + d0;
-    *reinterpret_cast<float4_t *>(dst) = float4_t{(float)vd[0] * a.value_scale, (float)vd[1] * a.value_scale,
-                                                  (float)vd[2] * a.value_scale, (float)vd[3] * a.value_scale};
-    *reinterpret_cast<float4_t *>(dst + 4) = float4_t{(float)vd[4] * a.value_scale, (float)vd[5] * a.value_scale,
-                                                      (float)vd[6] * a.value_scale, (float)vd[7] * a.value_scale};
+    *reinterpret_cast<float4_t *>(dst) = float4_t{o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<float4_t *>(dst + 4) = float4_t{o[4], o[5], o[6], o[7]};
   }
   if (tid < kAttendGroup) {
-    a.part_peak[(size_t)pc * a.head_count + tid] = nr_score[tid][0];
-    a.part_total[(size_t)pc * a.head_count + tid] = 1.0f;
+    float peak = nr_score[tid][0];
+    for (int j = 1; j < rows; ++j) peak = fmaxf(peak, nr_score[tid][j]);
+    float total = 0.0f;
+    for (int j = 0; j < rows; ++j) total += __expf(nr_score[tid][j] - peak);
+    a.part_peak[(size_t)pc * a.head_count + tid] = peak;
+    a.part_total[(size_t)pc * a.head_count + tid] = total;
   }
 }
 
@@ -323,17 +378,19 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
   const int head0 = kv * kAttendGroup;
   const int block = blockIdx.x;
   const int lane_id = blockIdx.z;
-  const int pos = (a.place_dev ? *a.place_dev : a.place0) + lane_id;
+  const int pos0 = a.place_dev ? *a.place_dev : a.place0;
+  const int pos = pos0 + lane_id;
   const int span_full = a.window > 0 ? min(pos + 1, a.window) : pos + 1;
   const int place_start = pos - span_full + 1;
-  // PREP with k_raw: the lane's own position is the workgroup after the
-  // chunks, which cover the positions before it
+  // PREP with k_raw: the block's new positions up to the lane's own are the
+  // workgroup after the chunks, which cover the positions before the block
+  // (lane_id + 1 <= kAttendPrepLanes is inside every window)
   const bool new_row = PREP && a.k_raw != nullptr;
-  const int span_count = new_row ? span_full - 1 : span_full;
+  const int span_count = new_row ? span_full - (lane_id + 1) : span_full;
   const int blocks_seen = (span_count + C - 1) / C;
   const int pc = lane_id * a.chunks + block;
   if (new_row && block == blocks_seen) {
-    if (PREP) attend_new_row<HEAD>(a, pos, pc);
+    if (PREP) attend_fresh_rows<HEAD>(a, pos0, lane_id, pc);
     return;
   }
   if (block >= blocks_seen) return;  // past this lane's span: the whole workgroup
@@ -381,7 +438,8 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
       qgain[i][0] = *reinterpret_cast<const float4_t *>(a.q_gain + d0);
       qgain[i][1] = *reinterpret_cast<const float4_t *>(a.q_gain + d0 + 4);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) qturn[i][v] = *reinterpret_cast<const float4_t *>(a.turn + 2 * j0 + 4 * v);
+      for (int v = 0; v < 4; ++v)
+        qturn[i][v] = *reinterpret_cast<const float4_t *>(a.turn + (size_t)lane_id * a.turn_stride + 2 * j0 + 4 * v);
     }
   }
   // key row: position c0 + wave*PW + (n % PW), bytes QD*g .. QD*g + QD - 1
@@ -617,9 +675,10 @@ __global__ __launch_bounds__(256) void attend_fold_kernel(const float *part_out_
   const int d = tid % DIMS, sl = tid / DIMS;
   const int pos = (place_dev ? *place_dev : place0) + lane_id;
   const int span = window > 0 ? min(pos + 1, window) : pos + 1;
-  // extra: the lane's own position has a partial of its own, after the
-  // chunks of the positions before it
-  const int chunks = extra ? (span - 1 + chunk - 1) / chunk + 1 : (span + chunk - 1) / chunk;
+  // extra: the block's new positions up to the lane's own have a partial of
+  // their own, after the chunks of the positions before the block
+  const int fresh = extra ? lane_id + 1 : 0;
+  const int chunks = (span - fresh + chunk - 1) / chunk + (extra ? 1 : 0);
   const size_t base = (size_t)lane_id * chunk_slots;
   const size_t step = (size_t)head_count * head_size;
   const float *pout = part_out_all + base * step + (size_t)h * head_size + blockIdx.z * DIMS + d;
@@ -808,32 +867,46 @@ static hipError_t attend_fold(const AttendArgs &a, int chunks, int chunk, int pl
   return hipGetLastError();
 }
 
-// The decode step's attention with the heads prepared in the same launch
-// (attend_split_kernel's PREP form): one lane at the position in *place_dev
-// (place_bound its upper bound, which sizes the grid), e4m3 rings, one
-// key/value head.  query: the query heads before their norm, 16-byte aligned;
-// turn: (cos, sin) pairs of the position times each step, head_size / 2 of
-// them; k_raw, v_raw, k_gain: the key and value heads before their norms and
-// the key gain, whose bytes go to ring slot position % cache_span (NULL for a
-// layer that reads another layer's rings and writes none).
+// The attention of a decode step or a small block with the heads prepared in
+// the same launch (attend_split_kernel's PREP form): 1 to kAttendPrepLanes
+// lanes, lane 0 at the position in *place_dev (place_bound its upper bound,
+// which sizes the grid), e4m3 rings, one key/value head.  query: the query
+// heads before their norm, 16-byte aligned, lanes q_stride floats apart (a
+// multiple of 4; the blend out the same); turn: lane by lane, turn_stride
+// floats apart (a multiple of 4), the (cos, sin) pairs of the lane's position
+// times each step, head_size / 2 of them; k_raw, v_raw, k_gain: the key and
+// value heads before their norms, lanes kv_stride floats apart, and the key
+// gain, whose bytes go to ring slot position % cache_span (NULL for a layer
+// that reads another layer's rings and writes none).
 extern "C" hipError_t igl_launch_attend_prep(const uint8_t *key_store, const uint8_t *value_store,
                                              float key_scale, float value_scale, int cache_span,
-                                             int head_size, const float *query, const float *q_gain,
-                                             const float *turn, const float *k_raw,
-                                             const float *v_raw, const float *k_gain,
+                                             int head_size, int lanes, const float *query,
+                                             int q_stride, const float *q_gain, const float *turn,
+                                             int turn_stride, const float *k_raw,
+                                             const float *v_raw, int kv_stride, const float *k_gain,
                                              uint8_t *k_ring, uint8_t *v_ring, float eps,
                                              int place_bound, const int *place_dev, int window,
                                              float score_scale, float *blend_out, float *work,
                                              hipStream_t stream) {
   AttendArgs a;
-  const int chunk = attend_chunk(place_bound, window, 1);
-  // with k_raw, one slot more: the position's own partial (attend_new_row)
+  if (lanes < 1 || lanes > kAttendPrepLanes) return hipErrorInvalidValue;
+  const int chunk = attend_chunk(place_bound, window, lanes);
+  // with k_raw, one slot more a lane: the partial of the block's new positions
   const int extra = k_raw ? 1 : 0;
-  const int chunks = attend_blocks(place_bound, window, 1) + extra;
+  const int chunks = attend_blocks(place_bound, window, lanes) + extra;
   if ((((uintptr_t)query) & 15u) || (((uintptr_t)q_gain) & 15u) || (((uintptr_t)turn) & 15u) ||
       !place_dev || !turn)
     return hipErrorInvalidValue;
+  if (lanes > 1 && (q_stride < kAttendGroup * head_size || (q_stride & 3) || turn_stride < head_size ||
+                    (turn_stride & 3) || (k_raw && kv_stride < head_size)))
+    return hipErrorInvalidValue;
   if (k_raw && (!v_raw || !k_gain || !k_ring || !v_ring)) return hipErrorInvalidValue;
+  // the new positions of the block sit inside every lane's window and the
+  // ring holds them beside every older position a lane reads
+  if (window > 0 && lanes > window) return hipErrorInvalidValue;
+  if (k_raw && cache_span < (window > 0 ? window : place_bound + 1) + lanes - 1 &&
+      cache_span < place_bound + lanes)
+    return hipErrorInvalidValue;
   a.key_store = key_store;
   a.value_store = value_store;
   a.kv_width = head_size;
@@ -843,17 +916,19 @@ extern "C" hipError_t igl_launch_attend_prep(const uint8_t *key_store, const uin
   a.window = window;
   a.chunks = chunks;
   a.final_out = chunks == 1 && !extra ? blend_out : nullptr;
-  a.q_stride = kAttendGroup * head_size;
+  a.q_stride = lanes > 1 ? q_stride : kAttendGroup * head_size;
   a.query = query;
   a.key_scale = key_scale * 256.0f * score_scale;
   a.value_scale = value_scale * 256.0f;
   a.head_count = kAttendGroup;
   a.part_out = work;
-  a.part_peak = work + (size_t)chunks * kAttendGroup * head_size;
-  a.part_total = a.part_peak + (size_t)chunks * kAttendGroup;
+  a.part_peak = work + (size_t)lanes * chunks * kAttendGroup * head_size;
+  a.part_total = a.part_peak + (size_t)lanes * chunks * kAttendGroup;
   a.q_gain = q_gain;
   a.turn = turn;
+  a.turn_stride = lanes > 1 ? turn_stride : 0;
   a.k_raw = k_raw;
+  a.kv_raw_stride = lanes > 1 ? kv_stride : 0;
   a.v_raw = v_raw;
   a.k_gain = k_gain;
   a.k_ring = k_ring;
@@ -861,7 +936,7 @@ extern "C" hipError_t igl_launch_attend_prep(const uint8_t *key_store, const uin
   a.k_code_scale = key_scale;
   a.v_code_scale = value_scale;
   a.eps = eps;
-  const dim3 grid(chunks, 1, 1);
+  const dim3 grid(chunks, 1, lanes);
   if (head_size == 256 && chunk == 32)
     hipLaunchKernelGGL((attend_split_kernel<256, 0, 32, true, true>), grid, dim3(256), 0, stream, a);
   else if (head_size == 256)
@@ -874,15 +949,16 @@ extern "C" hipError_t igl_launch_attend_prep(const uint8_t *key_store, const uin
     return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.final_out) return e;
-  return attend_fold(a, chunks, chunk, place_bound, place_dev, window, 1, head_size, blend_out, stream,
+  return attend_fold(a, chunks, chunk, place_bound, place_dev, window, lanes, head_size, blend_out, stream,
                      extra);
 }
 
 // Floats of workspace igl_launch_attend_prep needs for the same arguments
-// (with a key/value row to write: one partial slot more than the chunks).
-extern "C" size_t igl_attend_prep_work_floats(int place_bound, int window, int head_size, int writes_row) {
-  const size_t blocks = (size_t)attend_blocks(place_bound, window, 1) + (writes_row ? 1 : 0);
-  return blocks * (size_t)kAttendGroup * ((size_t)head_size + 2);
+// (with key/value rows to write: one partial slot a lane more than the chunks).
+extern "C" size_t igl_attend_prep_work_floats(int place_bound, int window, int head_size, int lanes,
+                                              int writes_row) {
+  const size_t blocks = (size_t)attend_blocks(place_bound, window, lanes) + (writes_row ? 1 : 0);
+  return (size_t)lanes * blocks * (size_t)kAttendGroup * ((size_t)head_size + 2);
 }
 
 // Floats of workspace igl_launch_attend needs for the same arguments.
@@ -905,8 +981,10 @@ extern "C" size_t igl_attend_work_floats_limit(int span_limit, int lanes, int he
   const int b_short = attend_blocks(short_top - 1, 0, 1);
   const int b_long = attend_blocks(span_limit - 1, 0, 1);
   const size_t blocks = (size_t)(b_short > b_long ? b_short : b_long);
-  // a one-lane decode step with its own position's slot needs blocks + 1
-  const size_t slots = (size_t)lanes * blocks > blocks + 1 ? (size_t)lanes * blocks : blocks + 1;
+  // a prepared launch of up to kAttendPrepLanes lanes (a decode step, a small
+  // block) needs blocks + 1 slots a lane: its new positions' partial
+  const size_t prep = (size_t)(lanes < kAttendPrepLanes ? lanes : kAttendPrepLanes) * (blocks + 1);
+  const size_t slots = (size_t)lanes * blocks > prep ? (size_t)lanes * blocks : prep;
   return slots * (size_t)head_count * ((size_t)head_size + 2);
 }
 

@@ -43,6 +43,9 @@
  * sized by this and not by the prime's lane limit.  The reference's blocks
  * carry at most KERN_LANE_LIMIT = 16 (app_core.c:1980). */
 #define ENG_GUESS_LIMIT 64
+/* lanes a pass runs with the grouped projections and the prepared attention
+ * (a decode step, a small speculative block) */
+#define ENG_SMALL_LANES 4
 #define ENG_TENSOR_LIMIT 4096
 
 typedef struct eng_tensor {
@@ -77,7 +80,7 @@ struct igl_engine {
   int window_limit, lane_limit, guess_limit, fill, precise;
   int turns[2], halves[2];
   float *steps_dev[2];
-  float *turn_dev[2];  /* a one-lane pass's rotation row of each kind: [half][cos, sin] */
+  float *turn_dev[2];  /* a small pass's rotation rows of each kind: [lane][half][cos, sin] */
   /* the checkpoint */
   void   *map;
   size_t  map_bytes;
@@ -463,7 +466,7 @@ static int rope_table(igl_engine *e, int kind, int head_size, double theta, doub
   e->turns[kind] = turns;
   e->halves[kind] = half;
   if (hipMalloc((void **)&e->steps_dev[kind], (size_t)half * sizeof(float)) != hipSuccess ||
-      hipMalloc((void **)&e->turn_dev[kind], (size_t)half * 2 * sizeof(float)) != hipSuccess ||
+      hipMalloc((void **)&e->turn_dev[kind], (size_t)ENG_SMALL_LANES * half * 2 * sizeof(float)) != hipSuccess ||
       hipMemcpy(e->steps_dev[kind], steps, (size_t)half * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
     free(steps);
     return IGL_FAIL_DEVICE;
@@ -886,15 +889,17 @@ typedef struct eng_group {
   const float *gains[3];
   int gain_stride[3], rows[3];
   float *out[3];
+  int out_stride[3];
 } eng_group;
 
-static void group_add(igl_engine *e, eng_group *g, const igl_plane *p, float *out) {
+static void group_add(igl_engine *e, eng_group *g, const igl_plane *p, float *out, int out_stride) {
   g->codes[g->count] = dev_codes(e, p);
   g->row_stride[g->count] = (long long)p->row_stride;
   g->gains[g->count] = dev_gains(e, p);
   g->gain_stride[g->count] = p->group_count;
   g->rows[g->count] = p->row_count;
   g->out[g->count] = out;
+  g->out_stride[g->count] = out_stride;
   g->count++;
 }
 
@@ -912,11 +917,12 @@ static int group_fits(const eng_group *g, const igl_plane *const *p, int mode) {
   return mode != IGL_GEMV_GELU_PAIR || p[0]->row_count == p[1]->row_count;
 }
 
-static int group_run(igl_engine *e, const eng_group *g, const igl_plane *first, int mode,
-                     const float *act, const float *mul, const igl_gemv_prologue *pro) {
-  RUN(igl_launch_gemv_group(mode, g->count, g->codes, g->row_stride, g->gains, g->gain_stride,
-                            g->rows, g->out, igl_plane_group_shift(first), first->code_bias, act,
-                            first->col_count, mul, pro, e->stream));
+static int group_run(igl_engine *e, const eng_group *g, const igl_plane *first, int mode, int lanes,
+                     const float *act, const float *mul, int mul_stride, const igl_gemv_prologue *pro) {
+  RUN(igl_launch_gemv_group(mode, lanes, g->count, g->codes, g->row_stride, g->gains, g->gain_stride,
+                            g->rows, g->out, g->out_stride, igl_plane_group_shift(first),
+                            first->code_bias, act, e->hidden, first->col_count, mul, mul_stride, pro,
+                            e->stream));
   return IGL_OKAY;
 }
 
@@ -925,6 +931,7 @@ static int group_run(igl_engine *e, const eng_group *g, const igl_plane *first, 
 static igl_gemv_prologue state_update(igl_engine *e, const float *lift, const float *lift_gain,
                                       float scale, const float *norm_gain) {
   igl_gemv_prologue pro;
+  pro.lane_stride = e->hidden;
   pro.state_in = e->state;
   pro.state_out = e->state_buf[e->cur ^ 1];
   pro.lift = lift;
@@ -959,12 +966,12 @@ static int settle(igl_engine *e, int lanes, const float *next_norm) {
  * 11637-11743 with session_attend 11455-11580.
  *
  * A batch runs every residual update as its own launch, with scrap holding
- * the next sub-block's normed input.  One lane (a decode step) folds each
- * update into the prologue of the grouped launch that consumes it - the
- * post-attention update into the gate/up launch, the post-feed-forward one
- * into the per-layer-input gate, and this layer's last (per-layer-input)
- * update into the next layer's query/key/value launch - so a layer is eight
- * launches. */
+ * the next sub-block's normed input.  One to four lanes (a decode step, a
+ * speculative block) fold each update into the prologue of the grouped
+ * launch that consumes it - the post-attention update into the gate/up
+ * launch, the post-feed-forward one into the per-layer-input gate, and this
+ * layer's last (per-layer-input) update into the next layer's
+ * query/key/value launch - so a layer is eight launches for one lane. */
 static int run_layer(igl_engine *e, int li, int bound, int lanes) {
   eng_layer *L = &e->layer[li];
   const eng_layer *S = &e->layer[L->source];
@@ -978,15 +985,17 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
   const float *slice = e->ple_room + (size_t)li * e->ple;
   int fused;
 
-  group_add(e, &gq, &L->q, e->q);
+  group_add(e, &gq, &L->q, e->q, e->q_stride);
   if (!L->shared) {
-    group_add(e, &gq, &L->k, e->k);
-    group_add(e, &gq, &L->v, e->v);
+    group_add(e, &gq, &L->k, e->k, e->kv_stride);
+    group_add(e, &gq, &L->v, e->v, e->kv_stride);
   }
-  group_add(e, &gf, &L->gate, e->gate);
-  group_add(e, &gf, &L->up, e->rise);
-  group_add(e, &gp, &L->ple_gate, e->gate);
-  fused = lanes == 1 && H <= 4096 && group_fits(&gq, pq, IGL_GEMV_SEGMENTS) &&
+  group_add(e, &gf, &L->gate, e->gate, e->inner_max);
+  group_add(e, &gf, &L->up, e->rise, e->inner_max);
+  group_add(e, &gp, &L->ple_gate, e->gate, e->inner_max);
+  /* the grouped launches take one lane up to hidden 4096, two to four up to 2048 */
+  fused = lanes <= ENG_SMALL_LANES && H <= (lanes == 1 ? 4096 : 2048) &&
+          group_fits(&gq, pq, IGL_GEMV_SEGMENTS) &&
           group_fits(&gf, pf, IGL_GEMV_GELU_PAIR) && group_fits(&gp, pp, IGL_GEMV_GELU_MUL) &&
           L->q.col_count == H && L->gate.col_count == H && L->ple_gate.col_count == H;
 
@@ -994,7 +1003,7 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
   if (fused && e->pending) {
     igl_gemv_prologue pro = state_update(e, e->lift, e->pending_gain, e->pending_scale, L->enter_norm);
     e->pending = 0;
-    OKAY(group_run(e, &gq, &L->q, IGL_GEMV_SEGMENTS, NULL, NULL, &pro));
+    OKAY(group_run(e, &gq, &L->q, IGL_GEMV_SEGMENTS, lanes, NULL, NULL, 0, &pro));
     state_flip(e);
   } else if (lanes == 1 && e->pending && level_pro_fits(e, &L->q) && !L->shared &&
              level_same_kind(e, &L->q, &L->k) && level_same_kind(e, &L->q, &L->v)) {
@@ -1020,7 +1029,7 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
   } else {
     OKAY(settle(e, lanes, L->enter_norm));
     if (fused) {
-      OKAY(group_run(e, &gq, &L->q, IGL_GEMV_SEGMENTS, e->scrap, NULL, NULL));
+      OKAY(group_run(e, &gq, &L->q, IGL_GEMV_SEGMENTS, lanes, e->scrap, NULL, 0, NULL));
     } else {
       OKAY(project(e, &L->q, e->scrap, H, lanes, e->q, e->q_stride));
       if (!L->shared) {
@@ -1029,13 +1038,15 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
       }
     }
   }
-  if (lanes == 1) {
-    /* one lane: the heads' norms and turns and the new ring row in the
-     * attention launch (the pass's rotation rows are already on device) */
-    RUN(igl_launch_attend_prep(S->k_store, S->v_store, S->k_scale, S->v_scale, S->cache_span, hs, e->q,
-                               L->q_norm, e->turn_dev[kind], L->shared ? NULL : e->k, e->v, L->k_norm,
-                               L->k_store, L->v_store, e->eps, bound, e->ctl_dev, L->full ? 0 : e->window,
-                               1.0f, e->blend, e->attend_work, st));
+  if (lanes <= ENG_SMALL_LANES) {
+    /* a decode step or a small block: the heads' norms and turns and the new
+     * ring rows in the attention launch (the pass's rotation rows are
+     * already on device) */
+    RUN(igl_launch_attend_prep(S->k_store, S->v_store, S->k_scale, S->v_scale, S->cache_span, hs, lanes,
+                               e->q, e->q_stride, L->q_norm, e->turn_dev[kind], 2 * e->halves[kind],
+                               L->shared ? NULL : e->k, e->v, e->kv_stride, L->k_norm, L->k_store,
+                               L->v_store, e->eps, bound, e->ctl_dev, L->full ? 0 : e->window, 1.0f,
+                               e->blend, e->attend_work, st));
   } else {
     RUN(igl_launch_qkv_prep(e->q, e->q_stride, L->shared ? NULL : e->k, e->v, e->kv_stride, e->heads,
                             hs, lanes, L->q_norm, L->k_norm, e->eps, e->steps_dev[kind], e->ctl_dev,
@@ -1048,7 +1059,7 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
   /* state += norm(o) * after_attn; gate = gelu(gate proj) * up proj of norm(state) * before_ff */
   if (fused) {
     igl_gemv_prologue pro = state_update(e, e->lift, L->after_attn, 1.0f, L->before_ff);
-    OKAY(group_run(e, &gf, &L->gate, IGL_GEMV_GELU_PAIR, NULL, NULL, &pro));
+    OKAY(group_run(e, &gf, &L->gate, IGL_GEMV_GELU_PAIR, lanes, NULL, NULL, 0, &pro));
     state_flip(e);
   } else if (lanes == 1 && level_pair_fits(e, &L->gate, &L->up, L->inner)) {
     /* calibrated gate and up planes in one launch, the update as its prologue */
@@ -1078,7 +1089,7 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
   /* state += norm(down) * after_ff; gate = gelu(per-layer gate proj of state) * slice */
   if (fused) {
     igl_gemv_prologue pro = state_update(e, e->lift, L->after_ff, 1.0f, NULL);
-    OKAY(group_run(e, &gp, &L->ple_gate, IGL_GEMV_GELU_MUL, NULL, slice, &pro));
+    OKAY(group_run(e, &gp, &L->ple_gate, IGL_GEMV_GELU_MUL, lanes, NULL, slice, e->ple_stride, &pro));
     state_flip(e);
   } else if (lanes == 1 && level_pro_fits(e, &L->ple_gate) && L->ple_gate.row_count == e->ple) {
     /* gate = gelu(per-layer gate proj of the updated state) * slice, the
@@ -1135,9 +1146,9 @@ static int run_pass(igl_engine *e, int bound, int lanes, int logits) {
                            (float)(1.0 / sqrt(2.0)), st));
   }
   OKAY(norm_rows(e, e->state, e->layer[0].enter_norm, H, lanes, H, e->scrap));
-  if (lanes == 1)
+  if (lanes <= ENG_SMALL_LANES)
     RUN(igl_launch_turn_row(e->steps_dev[0], e->steps_dev[0] ? e->halves[0] : 0, e->steps_dev[1],
-                            e->steps_dev[1] ? e->halves[1] : 0, e->ctl_dev, e->turn_dev[0],
+                            e->steps_dev[1] ? e->halves[1] : 0, e->ctl_dev, lanes, e->turn_dev[0],
                             e->turn_dev[1], st));
   for (int li = 0; li < e->layers; ++li) OKAY(run_layer(e, li, bound, lanes));
   if (logits == 1 && lanes == 1) {

@@ -1439,20 +1439,21 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_real_kernel(GemvRealArgs a)
         if (m < a.lanes) dst[(size_t)m * a.out_stride + row0 + r] = acc[r][m];
 }
 
-// ---- one activation row against several planes in one launch (decode) -----
+// ---- a few activation rows against several planes in one launch (decode) ---
 //
-// The register form for one lane and four rows a wave, over up to three planes
-// that read the same activations (the query, key and value projections; the
-// gate and up projections), with the epilogue the decode step applies next:
+// The integer-dot form for one to four lanes and four rows a wave, over up to
+// three planes that read the same activations (the query, key and value
+// projections; the gate and up projections), with the epilogue the decode
+// step (one lane) or a speculative block (two to four) applies next:
 //   GEMV_SEGMENTS  the planes' rows one after another, each stored as it is;
 //   GEMV_GELU_PAIR planes 0 and 1 have the same rows: a wave takes rows n, n+1
 //                  of both and stores gelu(plane 0) * plane 1 (kern_gelu_gate,
 //                  app_core.c:5105-5190);
 //   GEMV_GELU_MUL  one plane, stored as gelu(y[n]) * mul[n] (the per-layer
 //                  input gate, session_layer 11718-11723).
-// Each row's sum is formed as gemv_q4_reg_kernel forms it; with the same
-// K-split the results are those of separate launches followed by the
-// elementwise kernel, bit for bit.
+// Each row's sum is formed as gemv_q4_dot_kernel forms it with one unit a
+// lane; with the same K-split the results are those of separate launches
+// followed by the elementwise kernel, bit for bit.
 enum { GEMV_SEGMENTS = 0, GEMV_GELU_PAIR = 1, GEMV_GELU_MUL = 2 };
 
 struct GemvGroupArgs {
@@ -1462,21 +1463,26 @@ struct GemvGroupArgs {
   int gain_stride[3];
   int rows[3];            // rows of each plane
   float *out[3];          // GEMV_SEGMENTS: one output row per plane; otherwise out[0]
+  int out_stride[3];      // floats between lanes of out[s]
   int segments;
   int tiles;              // four-row tiles over all planes
   int group_shift;
   const float *act;
-  int act_vec;
+  int act_stride;         // floats between lanes of act
+  int act_vec;            // act 16-byte aligned and act_stride % 4 == 0
   int K;
   int ksplit;
   float unit_bias;
   const float *mul;       // GEMV_GELU_MUL
+  int mul_stride;         // floats between lanes of mul
   // The residual update in front of the product (with `state_in` set): the
   // activations are not read from `act` but formed in every workgroup as
   //   s = (state_in + norm(lift) * lift_gain) * scale   (lift NULL: s = state_in)
   //   x = norm(s) * norm_gain                           (norm_gain NULL: x = s)
-  // with the float operations of norm_add_kernel; workgroup 0 writes s to
-  // `state_out`, which must not alias `state_in`.
+  // with the float operations of norm_add_kernel, lane by lane; workgroup 0
+  // writes s to `state_out`, which must not alias `state_in`.  Lanes of
+  // state_in, state_out and lift lie `lane_stride` floats apart.
+  int lane_stride;
   const float *state_in;
   float *state_out;
   const float *lift;
@@ -1491,126 +1497,187 @@ struct GemvGroupArgs {
 // The update above in the kernel's digit form (into `dig` / `down`, as
 // digit_store stages x), in two steps so that a kernel can issue the loads
 // ahead of its weight loads.  Thread t holds the eight-element groups
-// g = t + 256 j (j < PG) of every K-vector, so a group's x is formed in
-// registers and digitized there (the four groups of a unit sit in one quad):
-// nothing passes through LDS but the two block sums and the digits.  Every
-// load is issued: an absent vector reads state_in in its place, groups past
-// K / 8 reread the last one, and the values are then masked.  The element
-// operations are norm_add_kernel's; only the double sums of the two norms add
-// in another order (a thread's eight elements, then the waves).
-template <int PG>
-__device__ __forceinline__ void prologue_loads(const GemvGroupArgs &a, PrologueLoads<PG> &p) {
-  const float *src[4] = {a.state_in, a.lift ? a.lift : a.state_in,
-                         a.lift ? a.lift_gain : a.state_in,
-                         a.norm_gain ? a.norm_gain : a.state_in};
+// g = t + 256 j (j < PG) of every K-vector of every lane, so a group's x is
+// formed in registers and digitized there (the four groups of a unit sit in
+// one quad): nothing passes through LDS but the block sums and the digits.
+// Every load is issued: an absent vector reads state_in in its place, groups
+// past K / 8 reread the last one, and the values are then masked.  The
+// element operations are norm_add_kernel's, in another order (a thread's
+// eight elements, then the waves).
+template <int PG, int M>
+struct GroupProLoads {
+  float s[PG][M][8];  // state_in, lane by lane
+  float l[PG][M][8];  // lift, lane by lane
+  float g[PG][8];     // lift_gain
+  float n[PG][8];     // norm_gain
+};
+
+__device__ __forceinline__ void load_eight(float (&v)[8], const float *q, int vec) {
+  if (vec) {
+    const float4_t lo = *reinterpret_cast<const float4_t *>(q);
+    const float4_t hi = *reinterpret_cast<const float4_t *>(q + 4);
+    v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+    v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = q[e];
+  }
+}
+
+template <int PG, int M>
+__device__ __forceinline__ void prologue_loads(const GemvGroupArgs &a, GroupProLoads<PG, M> &p) {
+  const bool lift = a.lift != nullptr;
+  const float *lift_src = lift ? a.lift : a.state_in;
+  const float *gain_src = lift ? a.lift_gain : a.state_in;
+  const float *norm_src = a.norm_gain ? a.norm_gain : a.state_in;
+  const size_t lift_stride = lift ? (size_t)a.lane_stride : 0;
   const int groups = a.K >> 3;
 #pragma unroll
   for (int j = 0; j < PG; ++j) {
     const int g = min((int)threadIdx.x + 256 * j, groups - 1);
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float *q = src[w] + 8 * g;
-      if (a.pro_vec) {
-        const float4_t lo = *reinterpret_cast<const float4_t *>(q);
-        const float4_t hi = *reinterpret_cast<const float4_t *>(q + 4);
-        p.v[j][w][0] = lo.x; p.v[j][w][1] = lo.y; p.v[j][w][2] = lo.z; p.v[j][w][3] = lo.w;
-        p.v[j][w][4] = hi.x; p.v[j][w][5] = hi.y; p.v[j][w][6] = hi.z; p.v[j][w][7] = hi.w;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) p.v[j][w][e] = q[e];
-      }
+    for (int m = 0; m < M; ++m) {
+      load_eight(p.s[j][m], a.state_in + (size_t)m * (size_t)a.lane_stride + 8 * g, a.pro_vec);
+      load_eight(p.l[j][m], lift_src + (size_t)m * lift_stride + 8 * g, a.pro_vec);
     }
+    load_eight(p.g[j], gain_src + 8 * g, a.pro_vec);
+    load_eight(p.n[j], norm_src + 8 * g, a.pro_vec);
   }
 }
 
-// The two block sums use their own LDS slots (`red`, 2 x 4 doubles), so
-// neither needs a barrier after its reads; ends with the barrier after the
-// digit stores.
-template <int PG>
-__device__ __forceinline__ void group_prologue(const GemvGroupArgs &a, const PrologueLoads<PG> &p,
+// M sums of one double per thread over a workgroup of four waves behind one
+// barrier, each formed as block_sum_f64_once forms it (DPP within each wave,
+// then the wave sums in wave order); `red` holds 4 M doubles, each read once.
+template <int M>
+__device__ __forceinline__ void block_sums_f64_once(double (&v)[M], double *red) {
+#pragma unroll
+  for (int m = 0; m < M; ++m) v[m] = wave_sum_f64_to_last(v[m]);
+  if ((threadIdx.x & 63) == 63) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) red[4 * m + (threadIdx.x >> 6)] = v[m];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    double total = red[4 * m];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) total += red[4 * m + w];
+    v[m] = total;
+  }
+}
+
+// The two rounds of block sums use their own LDS slots (`red`, 2 x 4 M
+// doubles), so neither needs a barrier after its reads; ends with the barrier
+// after the digit stores.
+template <int PG, int M>
+__device__ __forceinline__ void group_prologue(const GemvGroupArgs &a, GroupProLoads<PG, M> &p,
                                                uint4_t *dig, int *down, double *red) {
   const int n = a.K;
   const int groups = n >> 3;
   const int units = n >> 5;
   const bool lift = a.lift != nullptr;
   const bool normed = a.norm_gain != nullptr;
-  float sv[PG][8], lv[PG][8], gv[PG][8], nv[PG][8];
 #pragma unroll
   for (int j = 0; j < PG; ++j) {
     const bool in = (int)threadIdx.x + 256 * j < groups;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      sv[j][e] = in ? p.v[j][0][e] : 0.0f;
-      lv[j][e] = in && lift ? p.v[j][1][e] : 0.0f;
-      gv[j][e] = in && lift ? p.v[j][2][e] : 0.0f;
-      nv[j][e] = in && normed ? p.v[j][3][e] : 0.0f;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        p.s[j][m][e] = in ? p.s[j][m][e] : 0.0f;
+        p.l[j][m][e] = in && lift ? p.l[j][m][e] : 0.0f;
+      }
+      p.g[j][e] = in && lift ? p.g[j][e] : 0.0f;
+      p.n[j][e] = in && normed ? p.n[j][e] : 0.0f;
     }
   }
-  double acc = 0.0;
+  // (uniform branches: without lift or norm_gain their sums are skipped)
+  float shrink[M];
+  if (lift) {
+    double acc[M];
 #pragma unroll
-  for (int j = 0; j < PG; ++j)
+    for (int m = 0; m < M; ++m) {
+      acc[m] = 0.0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += (double)lv[j][e] * (double)lv[j][e];
-  // (a uniform branch: without lift or norm_gain its sum is skipped)
-  const float shrink = lift ? rms_shrink(block_sum_f64_once(acc, red), n, a.eps) : 0.0f;
+      for (int j = 0; j < PG; ++j)
 #pragma unroll
-  for (int j = 0; j < PG; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float sum = sv[j][e] + lv[j][e] * shrink * gv[j][e];
-      if (a.apply_scale) sum *= a.scale;
-      sv[j][e] = lift ? sum : sv[j][e];
+        for (int e = 0; e < 8; ++e) acc[m] += (double)p.l[j][m][e] * (double)p.l[j][m][e];
     }
-  if (lift && blockIdx.x == 0) {
+    block_sums_f64_once<M>(acc, red);
 #pragma unroll
-    for (int j = 0; j < PG; ++j) {
-      const int g = threadIdx.x + 256 * j;
-      if (g < groups) {
-        float *q = a.state_out + 8 * g;
-        if (a.pro_vec) {
-          *reinterpret_cast<float4_t *>(q) = float4_t{sv[j][0], sv[j][1], sv[j][2], sv[j][3]};
-          *reinterpret_cast<float4_t *>(q + 4) = float4_t{sv[j][4], sv[j][5], sv[j][6], sv[j][7]};
-        } else {
+    for (int m = 0; m < M; ++m) shrink[m] = rms_shrink(acc[m], n, a.eps);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) q[e] = sv[j][e];
+    for (int j = 0; j < PG; ++j)
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float sum = p.s[j][m][e] + p.l[j][m][e] * shrink[m] * p.g[j][e];
+          if (a.apply_scale) sum *= a.scale;
+          p.s[j][m][e] = sum;
+        }
+    if (blockIdx.x == 0) {
+#pragma unroll
+      for (int j = 0; j < PG; ++j) {
+        const int g = threadIdx.x + 256 * j;
+        if (g < groups) {
+#pragma unroll
+          for (int m = 0; m < M; ++m)
+            store_eight(a.state_out + (size_t)m * (size_t)a.lane_stride + 8 * g, p.s[j][m], a.pro_vec);
         }
       }
     }
   }
-  double acc2 = 0.0;
+  float shrink2[M];
+  if (normed) {
+    double acc2[M];
 #pragma unroll
-  for (int j = 0; j < PG; ++j)
+    for (int m = 0; m < M; ++m) {
+      acc2[m] = 0.0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc2 += (double)sv[j][e] * (double)sv[j][e];
-  const float shrink2 = normed ? rms_shrink(block_sum_f64_once(acc2, red + 4), n, a.eps) : 0.0f;
+      for (int j = 0; j < PG; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc2[m] += (double)p.s[j][m][e] * (double)p.s[j][m][e];
+    }
+    block_sums_f64_once<M>(acc2, red + 4 * M);
+#pragma unroll
+    for (int m = 0; m < M; ++m) shrink2[m] = rms_shrink(acc2[m], n, a.eps);
+  }
 #pragma unroll
   for (int j = 0; j < PG; ++j) {
     const int g = threadIdx.x + 256 * j;
-    float x[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = normed ? sv[j][e] * shrink2 * nv[j][e] : sv[j][e];
-    // a unit's four groups are one quad, all in or all out (K % 32 == 0)
-    if (g < groups) digit_group_store<kDigits>(x, 0, g, units, dig, down);
+    for (int m = 0; m < M; ++m) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = normed ? p.s[j][m][e] * shrink2[m] * p.n[j][e] : p.s[j][m][e];
+      // a unit's four groups are one quad, all in or all out (K % 32 == 0)
+      if (g < groups) digit_group_store<kDigits>(x, m, g, units, dig, down);
+    }
   }
   __syncthreads();
 }
 
+// M: the lanes (1 to 4), lane m's activations, outputs and multipliers
+// `act_stride`, `out_stride[s]`, `mul_stride` floats after lane m - 1's.
 // PRO: 0, or the eight-element groups a thread holds in the prologue
-// (K <= 2048 PRO).
-// GPT (PRO 0): the eight-element groups of x a thread stages, K <= 2048 GPT.
-// TPW: the four-row tiles a wave walks (KS 1 only): one workgroup then serves
-// 16 TPW rows, so TPW times fewer workgroups repeat the prologue and the
-// staging of x; a wave requests every tile's gains and codes up front.
+// (K <= 2048 PRO; one for several lanes).
+// GPT (PRO 0): the eight-element groups of x a thread stages, M K <= 2048 GPT.
+// TPW: the four-row tiles a wave walks (KS 1, one or two lanes): one
+// workgroup then serves 16 TPW rows, so TPW times fewer workgroups repeat the
+// prologue and the staging of x; a wave requests every tile's gains and codes
+// up front.
 // Each row's sum is formed as gemv_q4_dot_kernel forms it.
-template <int MODE, int PRO, int GPT, int KS, int TPW>
+template <int MODE, int M, int PRO, int GPT, int KS, int TPW>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupArgs a) {
   static_assert(TPW == 1 || KS == 1, "several tiles a wave only without a K split");
+  static_assert(TPW == 1 || M <= 2, "several tiles a wave only for one or two lanes");
   constexpr int R = 4;
   constexpr int kTilesPerBlock = 4 / KS;
   constexpr int kItems = GPT;
-  __shared__ float red[4][R];
-  __shared__ double pro_red[8];
-  // the digit form of x, sized at launch (gemv_dot_lds_bytes(1, K / 32)):
+  __shared__ float red[4][R][M];
+  __shared__ double pro_red[8 * M];
+  // the digit form of x, sized at launch (gemv_dot_lds_bytes(M, K / 32)):
   // the LDS a workgroup holds bounds how many share a CU
   extern __shared__ uint4_t lds_grp[];
   const int tid = threadIdx.x;
@@ -1623,7 +1690,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
   const bool lane_has = u_raw < (units * (ks + 1)) / KS;
   const int u = min(u_raw, units - 1);
   uint4_t *dig = lds_grp;
-  int *down = reinterpret_cast<int *>(lds_grp + kDigitPitch * units);
+  int *down = reinterpret_cast<int *>(lds_grp + M * kDigitPitch * units);
 
   // Row r of tile i: which plane, which row of it (tiles past the end reread
   // the last row; their sums are dropped).
@@ -1654,24 +1721,27 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
   // weights, gains before codes: vmcnt retires loads in order, so the block
   // forms x while the weights are in flight, and each row waits only for its
   // own codes.
-  PrologueLoads<PRO ? PRO : 1> pl;
+  GroupProLoads<PRO ? PRO : 1, M> pl;
   DigitLoads<kItems> held;
   if (PRO)
-    prologue_loads<PRO ? PRO : 1>(a, pl);
+    prologue_loads<PRO ? PRO : 1, M>(a, pl);
   else if (a.act_vec)
-    digit_loads<1, kItems, true>(held, a.act, 0, a.K);
+    digit_loads<M, kItems, true>(held, a.act, a.act_stride, a.K);
   else
-    digit_loads<1, kItems, false>(held, a.act, 0, a.K);
+    digit_loads<M, kItems, false>(held, a.act, a.act_stride, a.K);
   float s[TPW][R];
   uint4_t w[TPW][R];
   // GEMV_GELU_MUL: the multipliers of the tiles' rows, requested now rather
   // than after the sums (a round trip at the end of the chain)
-  float mulv[TPW][R];
+  float mulv[TPW][R][M];
   if (MODE == GEMV_GELU_MUL) {
 #pragma unroll
     for (int i = 0; i < TPW; ++i)
 #pragma unroll
-      for (int r = 0; r < R; ++r) mulv[i][r] = a.mul[min((tile0 + i) * R + r, a.rows[0] - 1)];
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+          mulv[i][r][m] = a.mul[(size_t)m * (size_t)a.mul_stride + min((tile0 + i) * R + r, a.rows[0] - 1)];
   }
 #pragma unroll
   for (int i = 0; i < TPW; ++i)
@@ -1689,66 +1759,100 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
           reinterpret_cast<const uint4_t *>(a.codes[p] + (size_t)prow[i][r] * (size_t)a.row_stride[p]) + u);
     }
   if (PRO) {
-    group_prologue<PRO ? PRO : 1>(a, pl, dig, down, pro_red);
+    group_prologue<PRO ? PRO : 1, M>(a, pl, dig, down, pro_red);
   } else {
-    digit_store<1, kItems, kDigits>(held, a.K, dig, down);
+    digit_store<M, kItems, kDigits>(held, a.K, dig, down);
   }
 
-  uint4_t dd[kDigits];
+  // up to two lanes' digits held across the tiles; more, one lane's at a time
+  constexpr int kHeld = M <= 2 ? M : 1;
+  uint4_t dd[kHeld][kDigits];
+  int shift[kHeld];
+  if (M <= 2) {
 #pragma unroll
-  for (int j = 0; j < kDigits; ++j) dd[j] = dig[digit_slot(0, u, units) + j];
-  const int shift = down[u];
+    for (int m = 0; m < kHeld; ++m) {
+#pragma unroll
+      for (int j = 0; j < kDigits; ++j) dd[m][j] = dig[digit_slot(m, u, units) + j];
+      shift[m] = down[m * units + u];
+    }
+  }
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
     const int tile = tile0 + i;
-    float acc[R];
+    float acc[R][M];
+    uint4_t c[R];
+    float gain[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const uint4_t c = w[i][r] ^ 0x88888888u;
-      int t[kDigits];
+      c[r] = w[i][r] ^ 0x88888888u;
+      gain[r] = lane_has && tile < a.tiles ? s[i][r] : 0.0f;
+    }
 #pragma unroll
-      for (int j = 0; j < kDigits; ++j) t[j] = 0;
+    for (int m = 0; m < M; ++m) {
+      const int hm = M <= 2 ? m : 0;
+      if (M > 2) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+        for (int j = 0; j < kDigits; ++j) dd[0][j] = dig[digit_slot(m, u, units) + j];
+        shift[0] = down[m * units + u];
+      }
 #pragma unroll
-        for (int j = 0; j < kDigits; ++j)
-          t[j] = __builtin_amdgcn_sdot8((int)c[q], (int)dd[j][q], t[j], false);
-      const float gain = lane_has && tile < a.tiles ? s[i][r] : 0.0f;
-      acc[r] = wave_sum_to_last(gain * __builtin_amdgcn_ldexpf(digit_sum<kDigits>(t), shift));
+      for (int r = 0; r < R; ++r) {
+        int t[kDigits];
+#pragma unroll
+        for (int j = 0; j < kDigits; ++j) t[j] = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int j = 0; j < kDigits; ++j)
+            t[j] = __builtin_amdgcn_sdot8((int)c[r][q], (int)dd[hm][j][q], t[j], false);
+        acc[r][m] = wave_sum_to_last(gain[r] * __builtin_amdgcn_ldexpf(digit_sum<kDigits>(t), shift[hm]));
+      }
     }
 
     if (KS > 1) {
       if (lane == 63) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) red[wave][r] = acc[r];
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int m = 0; m < M; ++m) red[wave][r][m] = acc[r][m];
       }
       __syncthreads();
       if (ks != 0 || lane != 63) return;
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float total = 0.0f;
-        for (int k = 0; k < KS; ++k) total += red[wave + k][r];
-        acc[r] = total;
-      }
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          float total = 0.0f;
+          for (int k = 0; k < KS; ++k) total += red[wave + k][r][m];
+          acc[r][m] = total;
+        }
     } else if (lane != 63) {
       continue;
     }
     if (tile >= a.tiles) continue;
     if (MODE == GEMV_GELU_PAIR) {
       const int n0 = 2 * tile;
-      if (n0 < a.rows[0]) a.out[0][n0] = gelu_near(acc[0]) * acc[2];
-      if (n0 + 1 < a.rows[0]) a.out[0][n0 + 1] = gelu_near(acc[1]) * acc[3];
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float *o = a.out[0] + (size_t)m * (size_t)a.out_stride[0];
+        if (n0 < a.rows[0]) o[n0] = gelu_near(acc[0][m]) * acc[2][m];
+        if (n0 + 1 < a.rows[0]) o[n0 + 1] = gelu_near(acc[1][m]) * acc[3][m];
+      }
     } else {
+      const int p0 = plane[i][0];
       const int row0 = tile * R;
-      const int first = plane[i][0] == 0 ? 0 : plane[i][0] == 1 ? a.rows[0] : a.rows[0] + a.rows[1];
+      const int first = p0 == 0 ? 0 : p0 == 1 ? a.rows[0] : a.rows[0] + a.rows[1];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int n = row0 - first + r;
-        if (n >= a.rows[plane[i][0]]) break;
-        if (MODE == GEMV_GELU_MUL)
-          a.out[0][n] = gelu_near(acc[r]) * mulv[i][r];
-        else
-          a.out[plane[i][0]][n] = acc[r];
+        if (n >= a.rows[p0]) break;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          if (MODE == GEMV_GELU_MUL)
+            a.out[0][(size_t)m * (size_t)a.out_stride[0] + n] = gelu_near(acc[r][m]) * mulv[i][r][m];
+          else
+            a.out[p0][(size_t)m * (size_t)a.out_stride[p0] + n] = acc[r][m];
+        }
       }
     }
   }
@@ -2308,21 +2412,26 @@ static hipError_t gemv_dot_launch_gpt(const GemvArgs &a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Items a thread stages: M K / 8 groups over 256 threads, at most 8.
+// Items a thread stages: M K / 8 groups over 256 threads, at most 8 (12 for
+// two lanes).
 constexpr int kDotMaxItems = 8;
 
 // The integer-dot form with 16-byte aligned activations and M K <= 16384 (a
-// thread stages at most eight groups of eight); `a.ksplit` a power of two.
+// thread stages at most eight groups of eight), or two lanes up to K 12288
+// (twelve); `a.ksplit` a power of two.
 template <int M, int R, int UPL>
 static hipError_t gemv_dot_launch(GemvArgs a, hipStream_t stream) {
   const int items = (M * (a.K >> 3) + kGemvThreads - 1) / kGemvThreads;
   if (!a.act_vec) return hipErrorInvalidValue;
   a.ks_log = a.ksplit == 1 ? 0 : a.ksplit == 2 ? 1 : a.ksplit == 4 ? 2 : -1;
   if (a.ks_log < 0) return hipErrorInvalidValue;
+  // every unit of K has a lane: the row tile's waves times UPL units a lane
+  if (a.ksplit * kWave * UPL < (a.K >> 5)) return hipErrorInvalidValue;
   if (items <= 1) return gemv_dot_launch_gpt<M, R, UPL, 1>(a, stream);
   if (items <= 2) return gemv_dot_launch_gpt<M, R, UPL, 2>(a, stream);
   if (items <= 4) return gemv_dot_launch_gpt<M, R, UPL, 4>(a, stream);
   if (items <= kDotMaxItems) return gemv_dot_launch_gpt<M, R, UPL, kDotMaxItems>(a, stream);
+  if (M == 2 && items <= 12) return gemv_dot_launch_gpt<M, R, UPL, 12>(a, stream);
   return hipErrorInvalidValue;
 }
 
@@ -2376,25 +2485,32 @@ extern "C" int igl_gemv_chunk_cols(int lanes, int K, int lds_limit) {
   return per * 32;
 }
 
-// One activation row against `segments` planes of the same width and group
-// size (see gemv_q4_group_kernel for the modes).  Every plane but the last of
-// a GEMV_SEGMENTS launch has a multiple of four rows; a GEMV_GELU_PAIR launch
-// takes two planes of equal rows.  K / 32 must fit the waves of a row tile
-// (K <= 8192).
-extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_t *const *codes,
+// One to four activation rows (lanes) against `segments` planes of the same
+// width and group size (see gemv_q4_group_kernel for the modes).  Every plane
+// but the last of a GEMV_SEGMENTS launch has a multiple of four rows; a
+// GEMV_GELU_PAIR launch takes two planes of equal rows.  K / 32 must fit the
+// waves of a row tile (K <= 8192, lanes x K <= 8192 without the prologue);
+// several lanes take the prologue up to K 2048, and without it only
+// GEMV_SEGMENTS.
+extern "C" hipError_t igl_launch_gemv_group(int mode, int lanes, int segments, const uint8_t *const *codes,
                                             const long long *row_stride,
                                             const float *const *gains, const int *gain_stride,
-                                            const int *rows, float *const *out, int group_shift,
-                                            int code_bias, const float *act, int K,
-                                            const float *mul, const igl_gemv_prologue *pro,
-                                            hipStream_t stream) {
+                                            const int *rows, float *const *out, const int *out_stride,
+                                            int group_shift, int code_bias, const float *act,
+                                            int act_stride, int K, const float *mul, int mul_stride,
+                                            const igl_gemv_prologue *pro, hipStream_t stream) {
   GemvGroupArgs a;
   const int units = K / 32;
-  if (segments < 1 || segments > 3 || K % 32 || units > 4 * kWave || group_shift < 0)
+  if (lanes < 1 || lanes > 4 || segments < 1 || segments > 3 || K % 32 || units > 4 * kWave ||
+      group_shift < 0)
     return hipErrorInvalidValue;
   if (pro && (K > 4096 || !pro->state_in || (pro->lift && (!pro->state_out || !pro->lift_gain ||
                                                             pro->state_out == pro->state_in))))
     return hipErrorInvalidValue;
+  if (lanes > 1 && (pro ? K > 2048 || pro->lane_stride < K : mode != GEMV_SEGMENTS || act_stride < K))
+    return hipErrorInvalidValue;
+  if (!pro && lanes * K > 8192) return hipErrorInvalidValue;
+  a.lane_stride = pro ? pro->lane_stride : 0;
   a.state_in = pro ? pro->state_in : nullptr;
   a.state_out = pro ? pro->state_out : nullptr;
   a.lift = pro ? pro->lift : nullptr;
@@ -2412,22 +2528,29 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
     const int live = s < segments;
     if (live && (rows[s] < 1 || (mode == GEMV_SEGMENTS && s + 1 < segments && rows[s] % 4)))
       return hipErrorInvalidValue;
+    // lanes of one plane's output must not overlap (GEMV_GELU_PAIR writes out[0] only)
+    if (live && lanes > 1 && (mode == GEMV_SEGMENTS || s == 0) && out_stride[s] < rows[s])
+      return hipErrorInvalidValue;
     a.codes[s] = live ? codes[s] : nullptr;
     a.row_stride[s] = live ? row_stride[s] : 0;
     a.gains[s] = live ? gains[s] : nullptr;
     a.gain_stride[s] = live ? gain_stride[s] : 0;
     a.rows[s] = live ? rows[s] : 0;
     a.out[s] = live ? out[s] : nullptr;
+    a.out_stride[s] = live && lanes > 1 ? out_stride[s] : 0;
     total += a.rows[s];
   }
+  if (mode == GEMV_GELU_MUL && lanes > 1 && mul_stride < rows[0]) return hipErrorInvalidValue;
   a.segments = segments;
   a.tiles = mode == GEMV_GELU_PAIR ? (rows[0] + 1) / 2 : (total + 3) / 4;
   a.group_shift = group_shift;
   a.act = act;
-  a.act_vec = (((uintptr_t)act) & 15u) == 0 ? 1 : 0;
+  a.act_stride = lanes > 1 ? act_stride : 0;
+  a.act_vec = ((((uintptr_t)act) & 15u) == 0 && (a.act_stride & 3) == 0) ? 1 : 0;
   a.K = K;
   a.unit_bias = 16.0f + (float)code_bias;
   a.mul = mul;
+  a.mul_stride = lanes > 1 ? mul_stride : 0;
   int ksplit = 1;
   while (ksplit < 4 && (units > ksplit * kWave || (a.tiles * ksplit < 2048 && units / (ksplit * 2) >= 32)))
     ksplit *= 2;
@@ -2440,49 +2563,73 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_
   const bool vec16 = pro && ((((uintptr_t)pro->state_in) | (uintptr_t)(pro->lift ? pro->lift : pro->state_in) |
                               (uintptr_t)(pro->lift_gain ? pro->lift_gain : pro->state_in) |
                               (uintptr_t)(pro->norm_gain ? pro->norm_gain : pro->state_in) |
-                              (uintptr_t)(pro->state_out ? pro->state_out : pro->state_in)) & 15u) == 0;
+                              (uintptr_t)(pro->state_out ? pro->state_out : pro->state_in) |
+                              (uintptr_t)a.lane_stride * sizeof(float)) & 15u) == 0;
   a.pro_vec = vec16 ? 1 : 0;
   // With the prologue, each workgroup repeats the residual update (four
   // K-vectors read, two block sums): past four workgroups a CU, two tiles a
-  // wave halve that (measured: the 2 x 12288-row gate/up pair at K 1536, 11.5
-  // -> 9.7 us; at 6144 rows, and without the prologue, one tile is faster).
-  const int tpw = pro && ksplit == 1 && (a.tiles + 3) / 4 >= 1024 ? 2 : 1;
+  // wave halve that for one and two lanes (measured: the 2 x 12288-row
+  // gate/up pair at K 1536, one lane 11.5 -> 9.7 us, a two-lane block 23 us
+  // faster over its 20 such launches; at 6144 rows, and without the
+  // prologue, one tile is faster).
+  const int tpw = lanes <= 2 && pro && ksplit == 1 && (a.tiles + 3) / 4 >= 1024 ? 2 : 1;
   const int tiles_per_block = 4 / ksplit * tpw;
   dim3 grid((a.tiles + tiles_per_block - 1) / tiles_per_block);
-  const size_t lds = gemv_dot_lds_bytes(1, units);  // at most 29 KiB (K <= 8192)
+  const size_t lds = gemv_dot_lds_bytes(lanes, units);  // at most 29 KiB (lanes x K <= 8192)
   // eight-element groups of x a thread stages without a prologue
-  const int gpt = K <= 2048 ? 1 : K <= 4096 ? 2 : 4;
-#define IGL_GROUP_KS(M_, P_, G_)                                                                    \
-  do {                                                                                              \
-    if (ksplit == 1 && tpw == 2 && P_ != 0)                                                         \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 1, 2>), grid, dim3(kGemvThreads), lds, stream, a); \
-    else if (ksplit == 1)                                                                           \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 1, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
-    else if (ksplit == 2)                                                                           \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 2, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
-    else                                                                                            \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 4, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
+  const int items = (lanes * K / 8 + kGemvThreads - 1) / kGemvThreads;
+  const int gpt = items <= 1 ? 1 : items <= 2 ? 2 : 4;
+#define IGL_GROUP_KS(M_, L_, P_, G_)                                                                   \
+  do {                                                                                                 \
+    if (L_ <= 2 && ksplit == 1 && tpw == 2 && P_ != 0)                                                 \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, L_, P_, G_, 1, (L_ <= 2 ? 2 : 1)>), grid,            \
+                         dim3(kGemvThreads), lds, stream, a);                                          \
+    else if (ksplit == 1)                                                                              \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, L_, P_, G_, 1, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
+    else if (ksplit == 2)                                                                              \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, L_, P_, G_, 2, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
+    else                                                                                               \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, L_, P_, G_, 4, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
   } while (0)
-#define IGL_GROUP_LAUNCH(M_, P_)                                  \
-  do {                                                            \
-    if (P_ != 0 || gpt == 1) IGL_GROUP_KS(M_, P_, 1);             \
-    else if (gpt == 2) IGL_GROUP_KS(M_, P_, 2);                   \
-    else IGL_GROUP_KS(M_, P_, 4);                                 \
+#define IGL_GROUP_LAUNCH(M_, L_, P_)                                  \
+  do {                                                                \
+    if (P_ != 0 || gpt == 1) IGL_GROUP_KS(M_, L_, P_, 1);             \
+    else if (gpt == 2) IGL_GROUP_KS(M_, L_, P_, 2);                   \
+    else IGL_GROUP_KS(M_, L_, P_, 4);                                 \
   } while (0)
   // groups of eight the prologue holds a thread: 1 up to K 2048, 2 up to 4096
   const int held = !pro ? 0 : K <= 2048 ? 1 : K <= 4096 ? 2 : -1;
   if (held < 0) return hipErrorInvalidValue;
-  switch (mode * 3 + held) {
-    case 0: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 0); break;
-    case 1: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 1); break;
-    case 2: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 2); break;
-    case 3: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 0); break;
-    case 4: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 1); break;
-    case 5: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 2); break;
-    case 6: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 0); break;
-    case 7: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 1); break;
-    case 8: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 2); break;
-    default: return hipErrorInvalidValue;
+  if (lanes == 1) {
+    switch (mode * 3 + held) {
+      case 0: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 1, 0); break;
+      case 1: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 1, 1); break;
+      case 2: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 1, 2); break;
+      case 3: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 1, 0); break;
+      case 4: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 1, 1); break;
+      case 5: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 1, 2); break;
+      case 6: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 1, 0); break;
+      case 7: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 1, 1); break;
+      case 8: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 1, 2); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    // several lanes: the prologue holds one group a lane (K <= 2048), and
+    // without it only the query/key/value segments read x
+#define IGL_GROUP_LANES(L_)                                                         \
+  do {                                                                              \
+    switch (mode * 3 + held) {                                                      \
+      case 0: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, L_, 0); break;                        \
+      case 1: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, L_, 1); break;                        \
+      case 4: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, L_, 1); break;                       \
+      case 7: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, L_, 1); break;                        \
+      default: return hipErrorInvalidValue;                                         \
+    }                                                                               \
+  } while (0)
+    if (lanes == 2) IGL_GROUP_LANES(2);
+    else if (lanes == 3) IGL_GROUP_LANES(3);
+    else IGL_GROUP_LANES(4);
+#undef IGL_GROUP_LANES
   }
 #undef IGL_GROUP_LAUNCH
 #undef IGL_GROUP_KS
@@ -3164,7 +3311,9 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
   a.unit_bias = 16.0f + (float)code_bias;
   a.act_vec = ((((uintptr_t)act) & 15u) == 0 && (act_stride & 3) == 0) ? 1 : 0;
   // One to four lanes on the integer dot path (aligned activations, M K <=
-  // 16384): eight-row tiles from 128 units up for one and two lanes, so the
+  // 16384, or two lanes up to K 12288: the 1536 x 12288 down projection of
+  // a two-lane speculative block, 11.4 -> 8.3 us against the float form,
+  // and the matrix-core form's 10.9): eight-row tiles from 128 units up for one and two lanes, so the
   // staging of x is shared by more rows, and on tall planes (32768 rows and
   // up: at least 1024 workgroups of 32 rows), where every workgroup's staging
   // of x would otherwise be read as often as the weights (the 262144 x 1536
@@ -3172,25 +3321,29 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
   // workgroups, half the loads a lane in flight: measured ~2% faster at
   // 8192 x 2048 than four, and eight rows 25% slower); enough waves on a row
   // tile that each lane holds one unit (two past 256).
-  if (a.act_vec && lanes <= 4 && lanes * K <= kDotMaxItems * kGemvThreads * 8 &&
+  if (a.act_vec && lanes <= 4 &&
+      (lanes * K <= kDotMaxItems * kGemvThreads * 8 || (lanes == 2 && K <= 12288)) &&
       K / 32 <= 8 * kWave) {
     const int units = K / 32;
     int R = lanes <= 2 && (units >= 128 || N >= 32768) ? 8 : lanes == 1 ? 2 : 4;
-    // One lane on wide rows: six-row tiles where eight leave CUs without a
-    // workgroup and six give every CU at most one (1536 x 12288: 192 -> 256
-    // workgroups, 7.77 -> 6.94 us; 1536 x 6144 4.36 -> 4.27 us; the same sums).
-    if (lanes == 1 && R == 8 && N < 32768 && (N + 7) / 8 < 256 && (N + 5) / 6 <= 256) R = 6;
+    // One or two lanes on wide rows: six-row tiles where eight leave CUs
+    // without a workgroup and six give every CU at most one (1536 x 12288:
+    // 192 -> 256 workgroups, one lane 7.77 -> 6.94 us, two lanes 10.57 ->
+    // 9.46 us; 1536 x 6144 4.36 -> 4.27 us and 6.74 -> 6.10 us; the same sums).
+    if (lanes <= 2 && R == 8 && N < 32768 && (N + 7) / 8 < 256 && (N + 5) / 6 <= 256) R = 6;
     const int tiles = (N + R - 1) / R;
     int upl = units > 4 * kWave ? 2 : 1;
     int ksplit = 1;
     while (ksplit < 4 && (units > ksplit * kWave * upl ||
                           (tiles * ksplit < 2048 && units / (ksplit * 2) >= 32 * upl)))
       ksplit *= 2;
-    // One lane on a small plane (under 4096 rows, at most 128 units): two-row
-    // tiles, one wave a tile, two units a lane past 64 -- fewer workgroups
-    // than the split above gives, and faster (lab: 1536 x 2048 2.95 -> 2.61
-    // us, the same sums; 1536 x 4096 3.49 -> 2.97 us).
-    if (lanes == 1 && N < 4096 && units <= 2 * kWave) {
+    // One or two lanes on a small plane (under 4096 rows, at most 128
+    // units): two-row tiles, one wave a tile, two units a lane past 64 --
+    // fewer workgroups than the split above gives, and faster (lab, one lane:
+    // 1536 x 2048 2.95 -> 2.61 us, the same sums; 1536 x 4096 3.49 -> 2.97
+    // us; two lanes: 1536 x 4096 5.22 -> 3.85 us, 1536 x 2048 3.43 -> 3.14,
+    // 1536 x 256 3.10 -> 2.60).
+    if (lanes <= 2 && N < 4096 && units <= 2 * kWave) {
       R = 2;
       upl = units > kWave ? 2 : 1;
       ksplit = 1;
@@ -3205,7 +3358,11 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
         if (R == 4) return gemv_dot_launch<1, 4, 1>(a, stream);
         if (R == 6) return upl == 2 ? gemv_dot_launch<1, 6, 2>(a, stream) : gemv_dot_launch<1, 6, 1>(a, stream);
         return upl == 2 ? gemv_dot_launch<1, 8, 2>(a, stream) : gemv_dot_launch<1, 8, 1>(a, stream);
-      case 2: return R == 4 ? gemv_dot_launch<2, 4, 1>(a, stream) : gemv_dot_launch<2, 8, 1>(a, stream);
+      case 2:
+        if (R == 6) return upl == 2 ? gemv_dot_launch<2, 6, 2>(a, stream) : gemv_dot_launch<2, 6, 1>(a, stream);
+        if (R == 2) return upl == 2 ? gemv_dot_launch<2, 2, 2>(a, stream) : gemv_dot_launch<2, 2, 1>(a, stream);
+        if (R == 4) return upl == 2 ? gemv_dot_launch<2, 4, 2>(a, stream) : gemv_dot_launch<2, 4, 1>(a, stream);
+        return upl == 2 ? gemv_dot_launch<2, 8, 2>(a, stream) : gemv_dot_launch<2, 8, 1>(a, stream);
       case 3: return gemv_dot_launch<3, 4, 1>(a, stream);
       default: return gemv_dot_launch<4, 4, 1>(a, stream);
     }

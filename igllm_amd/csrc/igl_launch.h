@@ -87,8 +87,11 @@ size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit);
 /* The residual update a grouped launch can form in front of its product, in
  * place of reading `act`: s = (state_in + norm(lift) * lift_gain) * scale
  * (lift NULL: s = state_in), written to state_out by one workgroup; the
- * activations are norm(s) * norm_gain (norm_gain NULL: s).  K <= 4096. */
+ * activations are norm(s) * norm_gain (norm_gain NULL: s).  K <= 4096.
+ * Lanes of state_in, state_out and lift lie lane_stride floats apart (read
+ * by igl_launch_gemv_group with several lanes only). */
 typedef struct igl_gemv_prologue {
+  int lane_stride;
   const float *state_in;
   float *state_out;
   const float *lift;
@@ -118,12 +121,15 @@ hipError_t igl_launch_gemv_level_pair(const igl_code_view *gate, const igl_code_
 hipError_t igl_launch_gemv_level_segments(const igl_code_view *v, int segments, const int *rows,
                                           float *const *out, const float *leave, float step,
                                           const igl_gemv_prologue *pro, int K, hipStream_t stream);
-hipError_t igl_launch_gemv_group(int mode, int segments, const uint8_t *const *codes,
+/* One to four lanes against up to three 4-bit planes that read the same
+ * activations, in one launch with the mode's epilogue; lane m of act, out[s]
+ * and mul lies m act_stride, m out_stride[s], m mul_stride floats in. */
+hipError_t igl_launch_gemv_group(int mode, int lanes, int segments, const uint8_t *const *codes,
                                  const long long *row_stride, const float *const *gains,
                                  const int *gain_stride, const int *rows, float *const *out,
-                                 int group_shift, int code_bias, const float *act, int K,
-                                 const float *mul, const igl_gemv_prologue *pro,
-                                 hipStream_t stream);
+                                 const int *out_stride, int group_shift, int code_bias,
+                                 const float *act, int act_stride, int K, const float *mul,
+                                 int mul_stride, const igl_gemv_prologue *pro, hipStream_t stream);
 hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_stride, const float *gains,
                               int gain_stride, int group_shift, int code_bias, const float *act,
                               int act_stride, int lanes, float *out, int out_stride, int N, int K,
@@ -172,19 +178,23 @@ hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t *value_stor
                              int lanes, float score_scale, float *blend_out, float *work,
                              hipStream_t stream);
 
-/* The decode step's attention with the query, key and value heads prepared in
- * the same launch (norms, gains, turns, the new ring row): one lane, e4m3 rings,
- * one key/value head; k_raw NULL for a layer that writes no row. */
+/* The attention of a decode step or a small block (1 to 4 lanes) with the
+ * query, key and value heads prepared in the same launch (norms, gains, turns,
+ * the new ring rows): e4m3 rings, one key/value head; lane l's query, turn row
+ * and raw key/value heads q_stride, turn_stride and kv_stride floats after
+ * lane l - 1's; k_raw NULL for a layer that writes no row. */
 hipError_t igl_launch_attend_prep(const uint8_t *key_store, const uint8_t *value_store,
                                   float key_scale, float value_scale, int cache_span,
-                                  int head_size, const float *query, const float *q_gain,
-                                  const float *turn, const float *k_raw, const float *v_raw,
+                                  int head_size, int lanes, const float *query, int q_stride,
+                                  const float *q_gain, const float *turn, int turn_stride,
+                                  const float *k_raw, const float *v_raw, int kv_stride,
                                   const float *k_gain, uint8_t *k_ring, uint8_t *v_ring,
                                   float eps, int place_bound, const int *place_dev, int window,
                                   float score_scale, float *blend_out, float *work,
                                   hipStream_t stream);
 
-size_t igl_attend_prep_work_floats(int place_bound, int window, int head_size, int writes_row);
+size_t igl_attend_prep_work_floats(int place_bound, int window, int head_size, int lanes,
+                                   int writes_row);
 
 /* The desk's HIP stream, for the engine's own launches (back_hip.c). */
 void *igl_desk_stream(igl_desk *desk);
@@ -204,10 +214,10 @@ hipError_t igl_launch_head_prep(float *v, int lane_stride, int heads, int head_s
                                 const float *gain, float eps, const float *step, int turn,
                                 int place_first, hipStream_t stream);
 hipError_t igl_launch_put_int(int32_t *dst, int value, hipStream_t stream);
-/* (cos, sin) of the position in *place_dev times each step of both kinds of
- * layer, as float pairs [half][2]. */
+/* (cos, sin) of the positions *place_dev .. *place_dev + lanes - 1 times each
+ * step of both kinds of layer, as float pairs [lanes][half][2]. */
 hipError_t igl_launch_turn_row(const float *step0, int half0, const float *step1, int half1,
-                               const int *place_dev, float *turn0, float *turn1,
+                               const int *place_dev, int lanes, float *turn0, float *turn1,
                                hipStream_t stream);
 hipError_t igl_launch_qkv_prep(float *q, int q_stride, const float *k, const float *v,
                                int kv_stride, int heads, int head_size, int lanes,

@@ -380,29 +380,32 @@ extern "C" hipError_t igl_launch_put_int(int32_t *dst, int value, hipStream_t st
   return hipGetLastError();
 }
 
-// The rotation row of one position, for each kind of layer: turn[j] =
+// The rotation rows of a pass's positions, for each kind of layer: turn[j] =
 // ((float)cos(p * step[j]), (float)sin(p * step[j])) in double, as head_turn
-// forms them (the reference's cos_room / sin_room at that position), p read
-// from place_dev.  Computed once a decode step for every layer's attention.
+// forms them (the reference's cos_room / sin_room at that position), p =
+// *place_dev + lane, one workgroup a lane.  Computed once a decode step (or a
+// small block) for every layer's attention.
 __global__ __launch_bounds__(256) void turn_row_kernel(const float *step0, int half0,
                                                        const float *step1, int half1,
                                                        const int *place_dev, float *turn0,
                                                        float *turn1) {
-  const double place = (double)*place_dev;
+  const int lane = blockIdx.x;
+  const double place = (double)(*place_dev + lane);
   for (int j = threadIdx.x; j < half0 + half1; j += blockDim.x) {
     const bool first = j < half0;
     const int i = first ? j : j - half0;
     const double angle = place * (double)(first ? step0 : step1)[i];
-    float *t = first ? turn0 : turn1;
+    float *t = first ? turn0 + (size_t)lane * 2 * half0 : turn1 + (size_t)lane * 2 * half1;
     t[2 * i] = (float)cos(angle);
     t[2 * i + 1] = (float)sin(angle);
   }
 }
 
 extern "C" hipError_t igl_launch_turn_row(const float *step0, int half0, const float *step1,
-                                          int half1, const int *place_dev, float *turn0,
+                                          int half1, const int *place_dev, int lanes, float *turn0,
                                           float *turn1, hipStream_t stream) {
-  hipLaunchKernelGGL(turn_row_kernel, dim3(1), dim3(256), 0, stream, step0, half0, step1, half1,
+  if (lanes < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(turn_row_kernel, dim3(lanes), dim3(256), 0, stream, step0, half0, step1, half1,
                      place_dev, turn0, turn1);
   return hipGetLastError();
 }

@@ -380,14 +380,18 @@ static void check_view(const char *what, const igl_code_view *v, int K, int N) {
   check_plane(what, v->codes, v->row_stride, K, v->bit_count, v->gains, v->gain_stride, N);
 }
 
-static void check_pro(const char *what, const igl_gemv_prologue *pro, int K) {
+/* lanes of state_in, state_out and lift lie lane_stride floats apart */
+static void check_pro_lanes(const char *what, const igl_gemv_prologue *pro, int K, int lanes) {
   if (!pro) return;
-  check_range(what, "pro.state_in", pro->state_in, (size_t)K * sizeof(float));
-  if (pro->state_out) check_range(what, "pro.state_out", pro->state_out, (size_t)K * sizeof(float));
-  if (pro->lift) check_range(what, "pro.lift", pro->lift, (size_t)K * sizeof(float));
+  const size_t lane_bytes = ((size_t)(lanes - 1) * (size_t)pro->lane_stride + (size_t)K) * sizeof(float);
+  check_range(what, "pro.state_in", pro->state_in, lane_bytes);
+  if (pro->state_out) check_range(what, "pro.state_out", pro->state_out, lane_bytes);
+  if (pro->lift) check_range(what, "pro.lift", pro->lift, lane_bytes);
   if (pro->lift_gain) check_range(what, "pro.lift_gain", pro->lift_gain, (size_t)K * sizeof(float));
   if (pro->norm_gain) check_range(what, "pro.norm_gain", pro->norm_gain, (size_t)K * sizeof(float));
 }
+
+static void check_pro(const char *what, const igl_gemv_prologue *pro, int K) { check_pro_lanes(what, pro, K, 1); }
 
 hipError_t R(igl_launch_gemv_q4)(const uint8_t *, long long, const float *, int, int, int, const float *, int, int,
                                  float *, int, int, int, float *, int, hipStream_t);
@@ -509,24 +513,27 @@ hipError_t W(igl_launch_gemv_level_segments)(const igl_code_view *v, int segment
   return R(igl_launch_gemv_level_segments)(v, segments, rows, out, leave, step, pro, K, stream);
 }
 
-hipError_t R(igl_launch_gemv_group)(int, int, const uint8_t *const *, const long long *, const float *const *,
-                                    const int *, const int *, float *const *, int, int, const float *, int,
-                                    const float *, const igl_gemv_prologue *, hipStream_t);
-hipError_t W(igl_launch_gemv_group)(int mode, int segments, const uint8_t *const *codes, const long long *row_stride,
-                                    const float *const *gains, const int *gain_stride, const int *rows,
-                                    float *const *out, int group_shift, int code_bias, const float *act, int K,
-                                    const float *mul, const igl_gemv_prologue *pro, hipStream_t stream) {
+hipError_t R(igl_launch_gemv_group)(int, int, int, const uint8_t *const *, const long long *, const float *const *,
+                                    const int *, const int *, float *const *, const int *, int, int, const float *,
+                                    int, int, const float *, int, const igl_gemv_prologue *, hipStream_t);
+hipError_t W(igl_launch_gemv_group)(int mode, int lanes, int segments, const uint8_t *const *codes,
+                                    const long long *row_stride, const float *const *gains, const int *gain_stride,
+                                    const int *rows, float *const *out, const int *out_stride, int group_shift,
+                                    int code_bias, const float *act, int act_stride, int K, const float *mul,
+                                    int mul_stride, const igl_gemv_prologue *pro, hipStream_t stream) {
   const char *w = "igl_launch_gemv_group";
+  const size_t before = (size_t)(lanes - 1);
   for (int s = 0; s < segments; ++s) {
     check_plane(w, codes[s], row_stride[s], K, 4, gains[s], gain_stride[s], rows[s]);
     /* GELU_PAIR writes gelu(gate) * up once, into out[0] */
-    if (mode != IGL_GEMV_GELU_PAIR || s == 0) check_range(w, "out[s]", out[s], (size_t)rows[s] * 4);
+    if (mode != IGL_GEMV_GELU_PAIR || s == 0)
+      check_range(w, "out[s]", out[s], (before * (size_t)out_stride[s] + (size_t)rows[s]) * 4);
   }
-  if (pro) check_pro(w, pro, K);
-  else check_range(w, "act", act, (size_t)K * 4);
-  if (mode == IGL_GEMV_GELU_MUL) check_range(w, "mul", mul, (size_t)rows[0] * 4);
-  return R(igl_launch_gemv_group)(mode, segments, codes, row_stride, gains, gain_stride, rows, out, group_shift,
-                                  code_bias, act, K, mul, pro, stream);
+  if (pro) check_pro_lanes(w, pro, K, lanes);
+  else check_range(w, "act", act, (before * (size_t)act_stride + (size_t)K) * 4);
+  if (mode == IGL_GEMV_GELU_MUL) check_range(w, "mul", mul, (before * (size_t)mul_stride + (size_t)rows[0]) * 4);
+  return R(igl_launch_gemv_group)(mode, lanes, segments, codes, row_stride, gains, gain_stride, rows, out, out_stride,
+                                  group_shift, code_bias, act, act_stride, K, mul, mul_stride, pro, stream);
 }
 
 hipError_t R(igl_launch_gemm_q4)(const void *, int, int, const uint8_t *, long long, const float *, int, int, int,
@@ -585,35 +592,38 @@ hipError_t W(igl_launch_attend)(const uint8_t *key_store, const uint8_t *value_s
                               blend_out, work, stream);
 }
 
-hipError_t R(igl_launch_attend_prep)(const uint8_t *, const uint8_t *, float, float, int, int, const float *,
-                                     const float *, const float *, const float *, const float *, const float *,
-                                     uint8_t *, uint8_t *, float, int, const int *, int, float, float *, float *,
-                                     hipStream_t);
+hipError_t R(igl_launch_attend_prep)(const uint8_t *, const uint8_t *, float, float, int, int, int, const float *, int,
+                                     const float *, const float *, int, const float *, const float *, int,
+                                     const float *, uint8_t *, uint8_t *, float, int, const int *, int, float, float *,
+                                     float *, hipStream_t);
 hipError_t W(igl_launch_attend_prep)(const uint8_t *key_store, const uint8_t *value_store, float key_scale,
-                                     float value_scale, int cache_span, int head_size, const float *query,
-                                     const float *q_gain, const float *turn, const float *k_raw, const float *v_raw,
-                                     const float *k_gain, uint8_t *k_ring, uint8_t *v_ring, float eps,
-                                     int place_bound, const int *place_dev, int window, float score_scale,
-                                     float *blend_out, float *work, hipStream_t stream) {
+                                     float value_scale, int cache_span, int head_size, int lanes, const float *query,
+                                     int q_stride, const float *q_gain, const float *turn, int turn_stride,
+                                     const float *k_raw, const float *v_raw, int kv_stride, const float *k_gain,
+                                     uint8_t *k_ring, uint8_t *v_ring, float eps, int place_bound,
+                                     const int *place_dev, int window, float score_scale, float *blend_out,
+                                     float *work, hipStream_t stream) {
   const char *w = "igl_launch_attend_prep";
+  const size_t qs = lanes > 1 ? (size_t)q_stride : 8 * (size_t)head_size;
   check_range(w, "key_store", key_store, (size_t)cache_span * (size_t)head_size);
   check_range(w, "value_store", value_store, (size_t)cache_span * (size_t)head_size);
-  check_range(w, "query", query, 8 * (size_t)head_size * 4);
+  check_range(w, "query", query, rows_bytes(lanes, qs, 8 * (size_t)head_size, 4));
   check_range(w, "q_gain", q_gain, (size_t)head_size * 4);
-  check_range(w, "turn", turn, (size_t)head_size * 4); /* head_size / 2 (cos, sin) pairs */
+  /* head_size / 2 (cos, sin) pairs a lane */
+  check_range(w, "turn", turn, rows_bytes(lanes, (size_t)turn_stride, (size_t)head_size, 4));
   check_range(w, "place_dev", place_dev, 4);
   if (k_raw) {
-    check_range(w, "k_raw", k_raw, (size_t)head_size * 4);
-    check_range(w, "v_raw", v_raw, (size_t)head_size * 4);
+    check_range(w, "k_raw", k_raw, rows_bytes(lanes, (size_t)kv_stride, (size_t)head_size, 4));
+    check_range(w, "v_raw", v_raw, rows_bytes(lanes, (size_t)kv_stride, (size_t)head_size, 4));
     check_range(w, "k_gain", k_gain, (size_t)head_size * 4);
     check_range(w, "k_ring", k_ring, (size_t)cache_span * (size_t)head_size);
     check_range(w, "v_ring", v_ring, (size_t)cache_span * (size_t)head_size);
   }
-  check_range(w, "blend_out", blend_out, 8 * (size_t)head_size * 4);
-  check_range(w, "work", work, igl_attend_prep_work_floats(place_bound, window, head_size, k_raw != NULL) * 4);
-  return R(igl_launch_attend_prep)(key_store, value_store, key_scale, value_scale, cache_span, head_size, query,
-                                   q_gain, turn, k_raw, v_raw, k_gain, k_ring, v_ring, eps, place_bound, place_dev,
-                                   window, score_scale, blend_out, work, stream);
+  check_range(w, "blend_out", blend_out, rows_bytes(lanes, qs, 8 * (size_t)head_size, 4));
+  check_range(w, "work", work, igl_attend_prep_work_floats(place_bound, window, head_size, lanes, k_raw != NULL) * 4);
+  return R(igl_launch_attend_prep)(key_store, value_store, key_scale, value_scale, cache_span, head_size, lanes, query,
+                                   q_stride, q_gain, turn, turn_stride, k_raw, v_raw, kv_stride, k_gain, k_ring,
+                                   v_ring, eps, place_bound, place_dev, window, score_scale, blend_out, work, stream);
 }
 
 hipError_t R(igl_launch_gather_rows)(const igl_code_view *, int, int, const int32_t *, int, float, float *, int,
@@ -647,20 +657,21 @@ hipError_t W(igl_launch_put_int)(int32_t *dst, int value, hipStream_t stream) {
   return R(igl_launch_put_int)(dst, value, stream);
 }
 
-hipError_t R(igl_launch_turn_row)(const float *, int, const float *, int, const int *, float *, float *, hipStream_t);
+hipError_t R(igl_launch_turn_row)(const float *, int, const float *, int, const int *, int, float *, float *,
+                                  hipStream_t);
 hipError_t W(igl_launch_turn_row)(const float *step0, int half0, const float *step1, int half1, const int *place_dev,
-                                  float *turn0, float *turn1, hipStream_t stream) {
+                                  int lanes, float *turn0, float *turn1, hipStream_t stream) {
   const char *w = "igl_launch_turn_row";
   if (step0) {
     check_range(w, "step0", step0, (size_t)half0 * 4);
-    check_range(w, "turn0", turn0, (size_t)half0 * 8);
+    check_range(w, "turn0", turn0, (size_t)lanes * (size_t)half0 * 8);
   }
   if (step1) {
     check_range(w, "step1", step1, (size_t)half1 * 4);
-    check_range(w, "turn1", turn1, (size_t)half1 * 8);
+    check_range(w, "turn1", turn1, (size_t)lanes * (size_t)half1 * 8);
   }
   check_range(w, "place_dev", place_dev, 4);
-  return R(igl_launch_turn_row)(step0, half0, step1, half1, place_dev, turn0, turn1, stream);
+  return R(igl_launch_turn_row)(step0, half0, step1, half1, place_dev, lanes, turn0, turn1, stream);
 }
 
 hipError_t R(igl_launch_qkv_prep)(float *, int, const float *, const float *, int, int, int, int, const float *,

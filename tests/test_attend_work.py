@@ -26,7 +26,7 @@ def lib():
         getattr(lib, name).restype = ctypes.c_size_t
     lib.igl_attend_work_floats.argtypes = [ctypes.c_int] * 5
     lib.igl_attend_work_floats_limit.argtypes = [ctypes.c_int] * 4
-    lib.igl_attend_prep_work_floats.argtypes = [ctypes.c_int] * 4
+    lib.igl_attend_prep_work_floats.argtypes = [ctypes.c_int] * 5
     return lib
 
 
@@ -61,11 +61,17 @@ def test_longest_span_alone_falls_short(lib):
 @pytest.mark.parametrize("lane_limit", [1, 16, 2048])
 @pytest.mark.parametrize("head", [256, 512])
 def test_decode_step_fits_the_engine_allocation(lib, window_limit, lane_limit, head):
-    """The decode step's prepared attention writes one partial slot more than
-    its chunks (the new position's own); its graph is sized for the last
-    position, on full and sliding layers, with and without a row to write."""
+    """The prepared attention of a decode step or a small block (up to four
+    lanes) writes one partial slot a lane more than its chunks (the new
+    positions' own); its graph is sized for the last positions, on full and
+    sliding layers, with and without rows to write, and an eager pass or a
+    prime's tail launches it at every position before that."""
     have = lib.igl_attend_work_floats_limit(window_limit, lane_limit, HEADS, head)
-    for window in (0, 512):
-        for writes in (0, 1):
-            need = lib.igl_attend_prep_work_floats(window_limit - 1, window, head, writes)
-            assert need <= have, (window, writes, need, have)
+    for lanes in range(1, min(4, lane_limit, window_limit) + 1):
+        for window in (0, 512):
+            for writes in (0, 1):
+                for bound in sorted({window_limit - lanes, max(0, 8192 - lanes), max(0, window_limit // 2)}):
+                    if bound > window_limit - lanes:
+                        continue
+                    need = lib.igl_attend_prep_work_floats(bound, window, head, lanes, writes)
+                    assert need <= have, (lanes, window, writes, bound, need, have)

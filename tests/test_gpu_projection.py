@@ -78,13 +78,17 @@ def test_small_lane_sweep(backend, N, K, lanes):
     (70, 128, 1, 32), (130, 96, 3, 32), (1, 32, 1, 32), (257, 1536, 2, 32), (64, 12288, 1, 32),
     (33, 12288, 8, 32), (100, 2048, 8, 64), (100, 4096, 4, 128), (512, 256, 16, 32),
     (300, 6144, 12, 32), (40, 8192, 5, 32), (1536, 12288, 1, 32), (1000, 6144, 1, 32),
-    (1536, 4096, 1, 32), (999, 2048, 1, 32),
+    (1536, 4096, 1, 32), (999, 2048, 1, 32), (1536, 12288, 2, 32), (37, 9216, 2, 32),
+    (1536, 4096, 2, 32), (999, 2048, 2, 32), (1537, 256, 2, 32), (1000, 6144, 2, 32),
 ])
 def test_gemv_edges(backend, N, K, lanes, group):
     """Ragged rows, narrow and odd unit counts, K-chunked launches, wider groups,
-    lane counts past one launch; one lane on wide rows in six-row tiles (the
-    decode step's 1536 x 12288 down projection, and a ragged last tile); one
-    lane on small planes, one wave a tile, two units a lane past 64."""
+    lane counts past one launch; one or two lanes on wide rows in six-row
+    tiles (the 1536 x 12288 down projection of a decode step or a two-lane
+    block, and a ragged last tile); one
+    or two lanes on small planes, one wave a tile, two units a lane past 64;
+    two lanes past K 8192 (twelve staged groups a thread, two units a
+    lane)."""
     print_case(test="gemv_edges", N=N, K=K, lanes=lanes, group=group)
     codes, gains, act = synth_projection(N, K, lanes, seed=N + K, group_size=group)
     cp = backend.attach(make_plane(codes, gains, K, group_size=group))
