@@ -839,7 +839,7 @@ static hipError_t attend_fold(const AttendArgs &a, int chunks, int chunk, int pl
   const int q_stride = a.q_stride;
   // One lane: 16 dims a fold workgroup (the most workgroups); many lanes
   // (a prime or a block): 64.  Chunks a thread loads: enough for one pass.
-  const int dims = lanes == 1 ? 16 : 64;
+  const int dims = lanes <= kAttendPrepLanes ? 16 : 64;
   const int slices = 256 / dims;
   int per = 1;
   while (per < 32 && per * slices < chunks) per *= 2;

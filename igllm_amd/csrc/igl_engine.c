@@ -100,6 +100,9 @@ struct igl_engine {
   int cur, pending;
   const float *pending_gain;
   float pending_scale;
+  /* the first layer's input norm, left by run_pass to that layer's first
+   * launch (a grouped launch's prologue forms it, others norm into scrap) */
+  int enter_pending;
   float *attend_work;
   size_t attend_floats;
   int q_stride, kv_stride, inner_max, ple_stride;
@@ -1026,8 +1029,17 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
       OKAY(project(e, &L->k, e->scrap, H, lanes, e->k, e->kv_stride));
       OKAY(project(e, &L->v, e->scrap, H, lanes, e->v, e->kv_stride));
     }
+  } else if (fused && e->enter_pending) {
+    /* the first layer: its input norm in the prologue, the state as it is */
+    igl_gemv_prologue pro = state_update(e, NULL, NULL, 1.0f, L->enter_norm);
+    e->enter_pending = 0;
+    OKAY(group_run(e, &gq, &L->q, IGL_GEMV_SEGMENTS, lanes, NULL, NULL, 0, &pro));
   } else {
     OKAY(settle(e, lanes, L->enter_norm));
+    if (e->enter_pending) {
+      OKAY(norm_rows(e, e->state, L->enter_norm, H, lanes, H, e->scrap));
+      e->enter_pending = 0;
+    }
     if (fused) {
       OKAY(group_run(e, &gq, &L->q, IGL_GEMV_SEGMENTS, lanes, e->scrap, NULL, 0, NULL));
     } else {
@@ -1145,22 +1157,21 @@ static int run_pass(igl_engine *e, int bound, int lanes, int logits) {
                            e->ple, e->layers, lanes, e->eps, (float)(1.0 / sqrt((double)H)),
                            (float)(1.0 / sqrt(2.0)), st));
   }
-  OKAY(norm_rows(e, e->state, e->layer[0].enter_norm, H, lanes, H, e->scrap));
+  e->enter_pending = 1;
   if (lanes <= ENG_SMALL_LANES)
     RUN(igl_launch_turn_row(e->steps_dev[0], e->steps_dev[0] ? e->halves[0] : 0, e->steps_dev[1],
                             e->steps_dev[1] ? e->halves[1] : 0, e->ctl_dev, lanes, e->turn_dev[0],
                             e->turn_dev[1], st));
   for (int li = 0; li < e->layers; ++li) OKAY(run_layer(e, li, bound, lanes));
-  if (logits == 1 && lanes == 1) {
-    /* the last update with the final norm in one launch */
-    OKAY(settle(e, lanes, e->final_norm));
-  } else {
-    OKAY(settle(e, lanes, NULL));
-  }
+  /* the last update with the final norm in one launch when the head reads
+   * every lane */
+  const int head_all = logits == 2 || (logits == 1 && lanes == 1);
+  const int settled = e->pending;
+  OKAY(settle(e, lanes, head_all ? e->final_norm : NULL));
   if (logits) {
     const int from = logits == 2 ? 0 : lanes - 1;
     const int span = lanes - from;
-    if (!(logits == 1 && lanes == 1))
+    if (!(head_all && settled))
       OKAY(norm_rows(e, e->state + (size_t)from * H, e->final_norm, H, span, H, e->scrap));
     OKAY(project(e, &e->head, e->scrap, H, span, e->logits, e->vocab));
     if (e->cap > 0.0f) RUN(igl_launch_logit_cap(e->logits, (size_t)span * e->vocab, e->cap, st));
