@@ -89,9 +89,9 @@ size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit);
  * (lift NULL: s = state_in), written to state_out by one workgroup; the
  * activations are norm(s) * norm_gain (norm_gain NULL: s).  K <= 4096.
  * Lanes of state_in, state_out and lift lie lane_stride floats apart (read
- * by igl_launch_gemv_group with several lanes only). */
+ * by igl_launch_gemv_group with several lanes only).  Callers outside C
+ * mirror this layout field for field. */
 typedef struct igl_gemv_prologue {
-  int lane_stride;
   const float *state_in;
   float *state_out;
   const float *lift;
@@ -100,6 +100,7 @@ typedef struct igl_gemv_prologue {
   int apply_scale;
   const float *norm_gain;
   float eps;
+  int lane_stride;
 } igl_gemv_prologue;
 /* One lane of a calibrated plane (igl_launch_gemv_level_epi) with the residual
  * update of igl_launch_gemv_group as its prologue; x also to x_out (NULL:

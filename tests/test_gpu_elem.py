@@ -6,6 +6,7 @@ import ctypes
 import numpy as np
 import pytest
 
+import launch_structs
 import oracle_lib as ol
 
 pytestmark = pytest.mark.gpu
@@ -252,16 +253,8 @@ def test_plane_lift_level_nan_lane(backend):
     backend.detach(cp)
 
 
-class _CodeView(ctypes.Structure):
-    _fields_ = [("codes", ctypes.c_void_p), ("row_stride", ctypes.c_longlong), ("gains", ctypes.c_void_p),
-                ("gain_stride", ctypes.c_int), ("group_shift", ctypes.c_int), ("bit_count", ctypes.c_int),
-                ("code_bias", ctypes.c_int), ("code_flip", ctypes.c_int)]
-
-
-class _Prologue(ctypes.Structure):
-    _fields_ = [("state_in", ctypes.c_void_p), ("state_out", ctypes.c_void_p), ("lift", ctypes.c_void_p),
-                ("lift_gain", ctypes.c_void_p), ("scale", ctypes.c_float), ("apply_scale", ctypes.c_int),
-                ("norm_gain", ctypes.c_void_p), ("eps", ctypes.c_float)]
+_CodeView = launch_structs.CodeView
+_Prologue = launch_structs.Prologue
 
 
 @pytest.mark.parametrize("bits,N,K", [(2, 12288, 1536), (4, 6144, 1536), (2, 1001, 1536), (8, 513, 2048),
