@@ -996,8 +996,8 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
   group_add(e, &gf, &L->gate, e->gate, e->inner_max);
   group_add(e, &gf, &L->up, e->rise, e->inner_max);
   group_add(e, &gp, &L->ple_gate, e->gate, e->inner_max);
-  /* the grouped launches take one lane up to hidden 4096, two to four up to 2048 */
-  fused = lanes <= ENG_SMALL_LANES && H <= (lanes == 1 ? 4096 : 2048) &&
+  /* the grouped launches take one to four lanes up to hidden 4096 */
+  fused = lanes <= ENG_SMALL_LANES && H <= 4096 &&
           group_fits(&gq, pq, IGL_GEMV_SEGMENTS) &&
           group_fits(&gf, pf, IGL_GEMV_GELU_PAIR) && group_fits(&gp, pp, IGL_GEMV_GELU_MUL) &&
           L->q.col_count == H && L->gate.col_count == H && L->ple_gate.col_count == H;

@@ -47,6 +47,7 @@ struct GemvArgs {
   int ks_log;             // log2(ksplit)
   float unit_bias;        // 16 + code_bias
   int act_vec;            // activations 16-byte aligned with act_stride % 4 == 0
+  int lane_rows;          // > 1 (one-lane dot form): grid row blockIdx.y is lane blockIdx.y
 };
 
 constexpr int kGemvThreads = 256;
@@ -388,6 +389,8 @@ template <int M, int R, int UPL, int GPT>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
   extern __shared__ uint4_t lds_dig[];
   __shared__ float red[4][R][M];
+  // lane_rows: grid row blockIdx.y is lane blockIdx.y of the launch
+  const size_t lane0 = M == 1 && a.lane_rows > 1 ? blockIdx.y : 0;
   // wave-uniform indices in scalar registers; ksplit a power of two
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -406,7 +409,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
   // units past the end reload valid ones and get gain 0, so the arithmetic
   // needs no branch either (tail rows of a tile are computed, never stored).
   DigitLoads<GPT> held;
-  digit_loads<M, GPT, true>(held, a.act, a.act_stride, a.K);
+  digit_loads<M, GPT, true>(held, a.act + lane0 * (size_t)a.act_stride, a.act_stride, a.K);
   // Gains before codes, and each row's codes in row order: the row loop
   // below waits for one row at a time.
   uint4_t w[UPL][R];
@@ -513,7 +516,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
       for (int r = 0; r < R; ++r)
         if (row0 + r < a.N)
 #pragma unroll
-          for (int m = 0; m < M; ++m) a.out[(size_t)m * a.out_stride + row0 + r] = acc[r][m];
+          for (int m = 0; m < M; ++m) a.out[(lane0 + (size_t)m) * a.out_stride + row0 + r] = acc[r][m];
     }
     return;
   }
@@ -531,7 +534,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
 #pragma unroll
     for (int k = 0; k < 4; ++k)
       if (k < (1 << ks_log)) total += red[wave + k][r][m];
-    if (row0 + r < a.N) a.out[(size_t)m * a.out_stride + row0 + r] = total;
+    if (row0 + r < a.N) a.out[(lane0 + (size_t)m) * a.out_stride + row0 + r] = total;
   }
 }
 
@@ -1441,10 +1444,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_real_kernel(GemvRealArgs a)
 
 // ---- a few activation rows against several planes in one launch (decode) ---
 //
-// The integer-dot form for one to four lanes and four rows a wave, over up to
-// three planes that read the same activations (the query, key and value
+// The integer-dot form for one lane and four rows a wave, over up to three
+// planes that read the same activations (the query, key and value
 // projections; the gate and up projections), with the epilogue the decode
-// step (one lane) or a speculative block (two to four) applies next:
+// step applies next:
 //   GEMV_SEGMENTS  the planes' rows one after another, each stored as it is;
 //   GEMV_GELU_PAIR planes 0 and 1 have the same rows: a wave takes rows n, n+1
 //                  of both and stores gelu(plane 0) * plane 1 (kern_gelu_gate,
@@ -1453,7 +1456,12 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_real_kernel(GemvRealArgs a)
 //                  input gate, session_layer 11718-11723).
 // Each row's sum is formed as gemv_q4_dot_kernel forms it with one unit a
 // lane; with the same K-split the results are those of separate launches
-// followed by the elementwise kernel, bit for bit.
+// followed by the elementwise kernel, bit for bit.  Two to four lanes (a
+// speculative block) run as that many rows of workgroups (blockIdx.y = lane,
+// `lane_rows`): every lane's arithmetic is the one-lane step's, and each row
+// reads the planes again, the repeats served by the L2 and the MALL (a
+// two-lane block 1.75 -> 1.64 ms against a form that holds both lanes in
+// each wave, whose sums cost twice the dot instructions a row).
 enum { GEMV_SEGMENTS = 0, GEMV_GELU_PAIR = 1, GEMV_GELU_MUL = 2 };
 
 struct GemvGroupArgs {
@@ -1475,11 +1483,12 @@ struct GemvGroupArgs {
   float unit_bias;
   const float *mul;       // GEMV_GELU_MUL
   int mul_stride;         // floats between lanes of mul
+  int lane_rows;          // lanes, one a row of workgroups (blockIdx.y)
   // The residual update in front of the product (with `state_in` set): the
   // activations are not read from `act` but formed in every workgroup as
   //   s = (state_in + norm(lift) * lift_gain) * scale   (lift NULL: s = state_in)
   //   x = norm(s) * norm_gain                           (norm_gain NULL: x = s)
-  // with the float operations of norm_add_kernel, lane by lane; workgroup 0
+  // with the float operations of norm_add_kernel; workgroup 0 of each lane
   // writes s to `state_out`, which must not alias `state_in`.  Lanes of
   // state_in, state_out and lift lie `lane_stride` floats apart.
   int lane_stride;
@@ -1497,187 +1506,127 @@ struct GemvGroupArgs {
 // The update above in the kernel's digit form (into `dig` / `down`, as
 // digit_store stages x), in two steps so that a kernel can issue the loads
 // ahead of its weight loads.  Thread t holds the eight-element groups
-// g = t + 256 j (j < PG) of every K-vector of every lane, so a group's x is
-// formed in registers and digitized there (the four groups of a unit sit in
-// one quad): nothing passes through LDS but the block sums and the digits.
-// Every load is issued: an absent vector reads state_in in its place, groups
-// past K / 8 reread the last one, and the values are then masked.  The
-// element operations are norm_add_kernel's, in another order (a thread's
-// eight elements, then the waves).
-template <int PG, int M>
-struct GroupProLoads {
-  float s[PG][M][8];  // state_in, lane by lane
-  float l[PG][M][8];  // lift, lane by lane
-  float g[PG][8];     // lift_gain
-  float n[PG][8];     // norm_gain
-};
-
-__device__ __forceinline__ void load_eight(float (&v)[8], const float *q, int vec) {
-  if (vec) {
-    const float4_t lo = *reinterpret_cast<const float4_t *>(q);
-    const float4_t hi = *reinterpret_cast<const float4_t *>(q + 4);
-    v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
-    v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = q[e];
-  }
-}
-
-template <int PG, int M>
-__device__ __forceinline__ void prologue_loads(const GemvGroupArgs &a, GroupProLoads<PG, M> &p) {
-  const bool lift = a.lift != nullptr;
-  const float *lift_src = lift ? a.lift : a.state_in;
-  const float *gain_src = lift ? a.lift_gain : a.state_in;
-  const float *norm_src = a.norm_gain ? a.norm_gain : a.state_in;
-  const size_t lift_stride = lift ? (size_t)a.lane_stride : 0;
+// g = t + 256 j (j < PG) of every K-vector, so a group's x is formed in
+// registers and digitized there (the four groups of a unit sit in one quad):
+// nothing passes through LDS but the two block sums and the digits.  Every
+// load is issued: an absent vector reads state_in in its place, groups past
+// K / 8 reread the last one, and the values are then masked.  The element
+// operations are norm_add_kernel's; only the double sums of the two norms add
+// in another order (a thread's eight elements, then the waves).
+template <int PG>
+__device__ __forceinline__ void prologue_loads(const GemvGroupArgs &a, PrologueLoads<PG> &p, int lane0) {
+  const size_t off = (size_t)lane0 * (size_t)a.lane_stride;  // the workgroup row's lane
+  const float *state = a.state_in + off;
+  const float *src[4] = {state, a.lift ? a.lift + off : state, a.lift ? a.lift_gain : state,
+                         a.norm_gain ? a.norm_gain : state};
   const int groups = a.K >> 3;
 #pragma unroll
   for (int j = 0; j < PG; ++j) {
     const int g = min((int)threadIdx.x + 256 * j, groups - 1);
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      load_eight(p.s[j][m], a.state_in + (size_t)m * (size_t)a.lane_stride + 8 * g, a.pro_vec);
-      load_eight(p.l[j][m], lift_src + (size_t)m * lift_stride + 8 * g, a.pro_vec);
+    for (int w = 0; w < 4; ++w) {
+      const float *q = src[w] + 8 * g;
+      if (a.pro_vec) {
+        const float4_t lo = *reinterpret_cast<const float4_t *>(q);
+        const float4_t hi = *reinterpret_cast<const float4_t *>(q + 4);
+        p.v[j][w][0] = lo.x; p.v[j][w][1] = lo.y; p.v[j][w][2] = lo.z; p.v[j][w][3] = lo.w;
+        p.v[j][w][4] = hi.x; p.v[j][w][5] = hi.y; p.v[j][w][6] = hi.z; p.v[j][w][7] = hi.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p.v[j][w][e] = q[e];
+      }
     }
-    load_eight(p.g[j], gain_src + 8 * g, a.pro_vec);
-    load_eight(p.n[j], norm_src + 8 * g, a.pro_vec);
   }
 }
 
-// M sums of one double per thread over a workgroup of four waves behind one
-// barrier, each formed as block_sum_f64_once forms it (DPP within each wave,
-// then the wave sums in wave order); `red` holds 4 M doubles, each read once.
-template <int M>
-__device__ __forceinline__ void block_sums_f64_once(double (&v)[M], double *red) {
-#pragma unroll
-  for (int m = 0; m < M; ++m) v[m] = wave_sum_f64_to_last(v[m]);
-  if ((threadIdx.x & 63) == 63) {
-#pragma unroll
-    for (int m = 0; m < M; ++m) red[4 * m + (threadIdx.x >> 6)] = v[m];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    double total = red[4 * m];
-#pragma unroll
-    for (int w = 1; w < 4; ++w) total += red[4 * m + w];
-    v[m] = total;
-  }
-}
-
-// The two rounds of block sums use their own LDS slots (`red`, 2 x 4 M
-// doubles), so neither needs a barrier after its reads; ends with the barrier
-// after the digit stores.
-template <int PG, int M>
-__device__ __forceinline__ void group_prologue(const GemvGroupArgs &a, GroupProLoads<PG, M> &p,
-                                               uint4_t *dig, int *down, double *red) {
+// The two block sums use their own LDS slots (`red`, 2 x 4 doubles), so
+// neither needs a barrier after its reads; ends with the barrier after the
+// digit stores.
+template <int PG>
+__device__ __forceinline__ void group_prologue(const GemvGroupArgs &a, const PrologueLoads<PG> &p,
+                                               uint4_t *dig, int *down, double *red, int lane0) {
   const int n = a.K;
   const int groups = n >> 3;
   const int units = n >> 5;
   const bool lift = a.lift != nullptr;
   const bool normed = a.norm_gain != nullptr;
+  float sv[PG][8], lv[PG][8], gv[PG][8], nv[PG][8];
 #pragma unroll
   for (int j = 0; j < PG; ++j) {
     const bool in = (int)threadIdx.x + 256 * j < groups;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        p.s[j][m][e] = in ? p.s[j][m][e] : 0.0f;
-        p.l[j][m][e] = in && lift ? p.l[j][m][e] : 0.0f;
-      }
-      p.g[j][e] = in && lift ? p.g[j][e] : 0.0f;
-      p.n[j][e] = in && normed ? p.n[j][e] : 0.0f;
+      sv[j][e] = in ? p.v[j][0][e] : 0.0f;
+      lv[j][e] = in && lift ? p.v[j][1][e] : 0.0f;
+      gv[j][e] = in && lift ? p.v[j][2][e] : 0.0f;
+      nv[j][e] = in && normed ? p.v[j][3][e] : 0.0f;
     }
   }
-  // (uniform branches: without lift or norm_gain their sums are skipped)
-  float shrink[M];
-  if (lift) {
-    double acc[M];
+  double acc = 0.0;
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      acc[m] = 0.0;
+  for (int j = 0; j < PG; ++j)
 #pragma unroll
-      for (int j = 0; j < PG; ++j)
+    for (int e = 0; e < 8; ++e) acc += (double)lv[j][e] * (double)lv[j][e];
+  // (a uniform branch: without lift or norm_gain its sum is skipped)
+  const float shrink = lift ? rms_shrink(block_sum_f64_once(acc, red), n, a.eps) : 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[m] += (double)p.l[j][m][e] * (double)p.l[j][m][e];
+  for (int j = 0; j < PG; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float sum = sv[j][e] + lv[j][e] * shrink * gv[j][e];
+      if (a.apply_scale) sum *= a.scale;
+      sv[j][e] = lift ? sum : sv[j][e];
     }
-    block_sums_f64_once<M>(acc, red);
+  if (lift && blockIdx.x == 0) {
 #pragma unroll
-    for (int m = 0; m < M; ++m) shrink[m] = rms_shrink(acc[m], n, a.eps);
+    for (int j = 0; j < PG; ++j) {
+      const int g = threadIdx.x + 256 * j;
+      if (g < groups) {
+        float *q = a.state_out + (size_t)lane0 * (size_t)a.lane_stride + 8 * g;
+        if (a.pro_vec) {
+          *reinterpret_cast<float4_t *>(q) = float4_t{sv[j][0], sv[j][1], sv[j][2], sv[j][3]};
+          *reinterpret_cast<float4_t *>(q + 4) = float4_t{sv[j][4], sv[j][5], sv[j][6], sv[j][7]};
+        } else {
 #pragma unroll
-    for (int j = 0; j < PG; ++j)
-#pragma unroll
-      for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float sum = p.s[j][m][e] + p.l[j][m][e] * shrink[m] * p.g[j][e];
-          if (a.apply_scale) sum *= a.scale;
-          p.s[j][m][e] = sum;
-        }
-    if (blockIdx.x == 0) {
-#pragma unroll
-      for (int j = 0; j < PG; ++j) {
-        const int g = threadIdx.x + 256 * j;
-        if (g < groups) {
-#pragma unroll
-          for (int m = 0; m < M; ++m)
-            store_eight(a.state_out + (size_t)m * (size_t)a.lane_stride + 8 * g, p.s[j][m], a.pro_vec);
+          for (int e = 0; e < 8; ++e) q[e] = sv[j][e];
         }
       }
     }
   }
-  float shrink2[M];
-  if (normed) {
-    double acc2[M];
+  double acc2 = 0.0;
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      acc2[m] = 0.0;
+  for (int j = 0; j < PG; ++j)
 #pragma unroll
-      for (int j = 0; j < PG; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc2[m] += (double)p.s[j][m][e] * (double)p.s[j][m][e];
-    }
-    block_sums_f64_once<M>(acc2, red + 4 * M);
-#pragma unroll
-    for (int m = 0; m < M; ++m) shrink2[m] = rms_shrink(acc2[m], n, a.eps);
-  }
+    for (int e = 0; e < 8; ++e) acc2 += (double)sv[j][e] * (double)sv[j][e];
+  const float shrink2 = normed ? rms_shrink(block_sum_f64_once(acc2, red + 4), n, a.eps) : 0.0f;
 #pragma unroll
   for (int j = 0; j < PG; ++j) {
     const int g = threadIdx.x + 256 * j;
+    float x[8];
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      float x[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = normed ? p.s[j][m][e] * shrink2[m] * p.n[j][e] : p.s[j][m][e];
-      // a unit's four groups are one quad, all in or all out (K % 32 == 0)
-      if (g < groups) digit_group_store<kDigits>(x, m, g, units, dig, down);
-    }
+    for (int e = 0; e < 8; ++e) x[e] = normed ? sv[j][e] * shrink2 * nv[j][e] : sv[j][e];
+    // a unit's four groups are one quad, all in or all out (K % 32 == 0)
+    if (g < groups) digit_group_store<kDigits>(x, 0, g, units, dig, down);
   }
   __syncthreads();
 }
 
-// M: the lanes (1 to 4), lane m's activations, outputs and multipliers
-// `act_stride`, `out_stride[s]`, `mul_stride` floats after lane m - 1's.
 // PRO: 0, or the eight-element groups a thread holds in the prologue
-// (K <= 2048 PRO; one for several lanes).
-// GPT (PRO 0): the eight-element groups of x a thread stages, M K <= 2048 GPT.
-// TPW: the four-row tiles a wave walks (KS 1, one or two lanes): one
-// workgroup then serves 16 TPW rows, so TPW times fewer workgroups repeat the
-// prologue and the staging of x; a wave requests every tile's gains and codes
-// up front.
+// (K <= 2048 PRO).
+// GPT (PRO 0): the eight-element groups of x a thread stages, K <= 2048 GPT.
+// TPW: the four-row tiles a wave walks (KS 1 only): one workgroup then serves
+// 16 TPW rows, so TPW times fewer workgroups repeat the prologue and the
+// staging of x; a wave requests every tile's gains and codes up front.
 // Each row's sum is formed as gemv_q4_dot_kernel forms it.
-template <int MODE, int M, int PRO, int GPT, int KS, int TPW>
+template <int MODE, int PRO, int GPT, int KS, int TPW>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupArgs a) {
   static_assert(TPW == 1 || KS == 1, "several tiles a wave only without a K split");
-  static_assert(TPW == 1 || M <= 2, "several tiles a wave only for one or two lanes");
   constexpr int R = 4;
   constexpr int kTilesPerBlock = 4 / KS;
   constexpr int kItems = GPT;
-  __shared__ float red[4][R][M];
-  __shared__ double pro_red[8 * M];
-  // the digit form of x, sized at launch (gemv_dot_lds_bytes(M, K / 32)):
+  __shared__ float red[4][R];
+  __shared__ double pro_red[8];
+  // the digit form of x, sized at launch (gemv_dot_lds_bytes(1, K / 32)):
   // the LDS a workgroup holds bounds how many share a CU
   extern __shared__ uint4_t lds_grp[];
   const int tid = threadIdx.x;
@@ -1685,12 +1634,15 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tile0 = (blockIdx.x * kTilesPerBlock + wave / KS) * TPW;
   const int ks = wave % KS;
+  // the lane of this row of workgroups (the arguments stay as passed: a
+  // written copy would live in scratch)
+  const int lane0 = a.lane_rows > 1 ? (int)blockIdx.y : 0;
   const int units = a.K >> 5;
   const int u_raw = (units * ks) / KS + lane;
   const bool lane_has = u_raw < (units * (ks + 1)) / KS;
   const int u = min(u_raw, units - 1);
   uint4_t *dig = lds_grp;
-  int *down = reinterpret_cast<int *>(lds_grp + M * kDigitPitch * units);
+  int *down = reinterpret_cast<int *>(lds_grp + kDigitPitch * units);
 
   // Row r of tile i: which plane, which row of it (tiles past the end reread
   // the last row; their sums are dropped).
@@ -1721,27 +1673,25 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
   // weights, gains before codes: vmcnt retires loads in order, so the block
   // forms x while the weights are in flight, and each row waits only for its
   // own codes.
-  GroupProLoads<PRO ? PRO : 1, M> pl;
+  PrologueLoads<PRO ? PRO : 1> pl;
   DigitLoads<kItems> held;
   if (PRO)
-    prologue_loads<PRO ? PRO : 1, M>(a, pl);
+    prologue_loads<PRO ? PRO : 1>(a, pl, lane0);
   else if (a.act_vec)
-    digit_loads<M, kItems, true>(held, a.act, a.act_stride, a.K);
+    digit_loads<1, kItems, true>(held, a.act + (size_t)lane0 * (size_t)a.act_stride, 0, a.K);
   else
-    digit_loads<M, kItems, false>(held, a.act, a.act_stride, a.K);
+    digit_loads<1, kItems, false>(held, a.act + (size_t)lane0 * (size_t)a.act_stride, 0, a.K);
   float s[TPW][R];
   uint4_t w[TPW][R];
   // GEMV_GELU_MUL: the multipliers of the tiles' rows, requested now rather
   // than after the sums (a round trip at the end of the chain)
-  float mulv[TPW][R][M];
+  float mulv[TPW][R];
   if (MODE == GEMV_GELU_MUL) {
 #pragma unroll
     for (int i = 0; i < TPW; ++i)
 #pragma unroll
       for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < M; ++m)
-          mulv[i][r][m] = a.mul[(size_t)m * (size_t)a.mul_stride + min((tile0 + i) * R + r, a.rows[0] - 1)];
+        mulv[i][r] = a.mul[(size_t)lane0 * (size_t)a.mul_stride + min((tile0 + i) * R + r, a.rows[0] - 1)];
   }
 #pragma unroll
   for (int i = 0; i < TPW; ++i)
@@ -1759,100 +1709,67 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q4_group_kernel(GemvGroupAr
           reinterpret_cast<const uint4_t *>(a.codes[p] + (size_t)prow[i][r] * (size_t)a.row_stride[p]) + u);
     }
   if (PRO) {
-    group_prologue<PRO ? PRO : 1, M>(a, pl, dig, down, pro_red);
+    group_prologue<PRO ? PRO : 1>(a, pl, dig, down, pro_red, lane0);
   } else {
-    digit_store<M, kItems, kDigits>(held, a.K, dig, down);
+    digit_store<1, kItems, kDigits>(held, a.K, dig, down);
   }
 
-  // up to two lanes' digits held across the tiles; more, one lane's at a time
-  constexpr int kHeld = M <= 2 ? M : 1;
-  uint4_t dd[kHeld][kDigits];
-  int shift[kHeld];
-  if (M <= 2) {
+  uint4_t dd[kDigits];
 #pragma unroll
-    for (int m = 0; m < kHeld; ++m) {
-#pragma unroll
-      for (int j = 0; j < kDigits; ++j) dd[m][j] = dig[digit_slot(m, u, units) + j];
-      shift[m] = down[m * units + u];
-    }
-  }
+  for (int j = 0; j < kDigits; ++j) dd[j] = dig[digit_slot(0, u, units) + j];
+  const int shift = down[u];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
     const int tile = tile0 + i;
-    float acc[R][M];
-    uint4_t c[R];
-    float gain[R];
+    float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      c[r] = w[i][r] ^ 0x88888888u;
-      gain[r] = lane_has && tile < a.tiles ? s[i][r] : 0.0f;
-    }
+      const uint4_t c = w[i][r] ^ 0x88888888u;
+      int t[kDigits];
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const int hm = M <= 2 ? m : 0;
-      if (M > 2) {
+      for (int j = 0; j < kDigits; ++j) t[j] = 0;
 #pragma unroll
-        for (int j = 0; j < kDigits; ++j) dd[0][j] = dig[digit_slot(m, u, units) + j];
-        shift[0] = down[m * units + u];
-      }
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        int t[kDigits];
-#pragma unroll
-        for (int j = 0; j < kDigits; ++j) t[j] = 0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int j = 0; j < kDigits; ++j)
-            t[j] = __builtin_amdgcn_sdot8((int)c[r][q], (int)dd[hm][j][q], t[j], false);
-        acc[r][m] = wave_sum_to_last(gain[r] * __builtin_amdgcn_ldexpf(digit_sum<kDigits>(t), shift[hm]));
-      }
+        for (int j = 0; j < kDigits; ++j)
+          t[j] = __builtin_amdgcn_sdot8((int)c[q], (int)dd[j][q], t[j], false);
+      const float gain = lane_has && tile < a.tiles ? s[i][r] : 0.0f;
+      acc[r] = wave_sum_to_last(gain * __builtin_amdgcn_ldexpf(digit_sum<kDigits>(t), shift));
     }
 
     if (KS > 1) {
       if (lane == 63) {
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int m = 0; m < M; ++m) red[wave][r][m] = acc[r][m];
+        for (int r = 0; r < R; ++r) red[wave][r] = acc[r];
       }
       __syncthreads();
       if (ks != 0 || lane != 63) return;
 #pragma unroll
-      for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-          float total = 0.0f;
-          for (int k = 0; k < KS; ++k) total += red[wave + k][r][m];
-          acc[r][m] = total;
-        }
+      for (int r = 0; r < R; ++r) {
+        float total = 0.0f;
+        for (int k = 0; k < KS; ++k) total += red[wave + k][r];
+        acc[r] = total;
+      }
     } else if (lane != 63) {
       continue;
     }
     if (tile >= a.tiles) continue;
     if (MODE == GEMV_GELU_PAIR) {
       const int n0 = 2 * tile;
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        float *o = a.out[0] + (size_t)m * (size_t)a.out_stride[0];
-        if (n0 < a.rows[0]) o[n0] = gelu_near(acc[0][m]) * acc[2][m];
-        if (n0 + 1 < a.rows[0]) o[n0 + 1] = gelu_near(acc[1][m]) * acc[3][m];
-      }
+      float *o = a.out[0] + (size_t)lane0 * (size_t)a.out_stride[0];
+      if (n0 < a.rows[0]) o[n0] = gelu_near(acc[0]) * acc[2];
+      if (n0 + 1 < a.rows[0]) o[n0 + 1] = gelu_near(acc[1]) * acc[3];
     } else {
-      const int p0 = plane[i][0];
       const int row0 = tile * R;
-      const int first = p0 == 0 ? 0 : p0 == 1 ? a.rows[0] : a.rows[0] + a.rows[1];
+      const int first = plane[i][0] == 0 ? 0 : plane[i][0] == 1 ? a.rows[0] : a.rows[0] + a.rows[1];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int n = row0 - first + r;
-        if (n >= a.rows[p0]) break;
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-          if (MODE == GEMV_GELU_MUL)
-            a.out[0][(size_t)m * (size_t)a.out_stride[0] + n] = gelu_near(acc[r][m]) * mulv[i][r][m];
-          else
-            a.out[p0][(size_t)m * (size_t)a.out_stride[p0] + n] = acc[r][m];
-        }
+        if (n >= a.rows[plane[i][0]]) break;
+        if (MODE == GEMV_GELU_MUL)
+          a.out[0][(size_t)lane0 * (size_t)a.out_stride[0] + n] = gelu_near(acc[r]) * mulv[i][r];
+        else
+          a.out[plane[i][0]][(size_t)lane0 * (size_t)a.out_stride[plane[i][0]] + n] = acc[r];
       }
     }
   }
@@ -2399,7 +2316,7 @@ template <int M, int R, int UPL, int GPT>
 static hipError_t gemv_dot_launch_gpt(const GemvArgs &a, hipStream_t stream) {
   const int tiles = (a.N + R - 1) / R;
   const int tiles_per_block = 4 / a.ksplit;
-  dim3 grid((tiles + tiles_per_block - 1) / tiles_per_block);
+  dim3 grid((tiles + tiles_per_block - 1) / tiles_per_block, M == 1 && a.lane_rows > 1 ? a.lane_rows : 1);
   const size_t lds = gemv_dot_lds_bytes(M, a.K >> 5);
   static size_t lds_granted = 65536;  // launches above 64 KiB ask once
   if (lds > lds_granted) {
@@ -2431,7 +2348,8 @@ static hipError_t gemv_dot_launch(GemvArgs a, hipStream_t stream) {
   if (items <= 2) return gemv_dot_launch_gpt<M, R, UPL, 2>(a, stream);
   if (items <= 4) return gemv_dot_launch_gpt<M, R, UPL, 4>(a, stream);
   if (items <= kDotMaxItems) return gemv_dot_launch_gpt<M, R, UPL, kDotMaxItems>(a, stream);
-  if (M == 2 && items <= 12) return gemv_dot_launch_gpt<M, R, UPL, 12>(a, stream);
+  if constexpr (M == 2)
+    if (items <= 12) return gemv_dot_launch_gpt<M, R, UPL, 12>(a, stream);
   return hipErrorInvalidValue;
 }
 
@@ -2486,12 +2404,12 @@ extern "C" int igl_gemv_chunk_cols(int lanes, int K, int lds_limit) {
 }
 
 // One to four activation rows (lanes) against `segments` planes of the same
-// width and group size (see gemv_q4_group_kernel for the modes).  Every plane
-// but the last of a GEMV_SEGMENTS launch has a multiple of four rows; a
+// width and group size (see gemv_q4_group_kernel for the modes; lane l of
+// act, out[s], mul and the prologue's vectors lies l act_stride, l
+// out_stride[s], l mul_stride, l lane_stride floats in).  Every plane but the
+// last of a GEMV_SEGMENTS launch has a multiple of four rows; a
 // GEMV_GELU_PAIR launch takes two planes of equal rows.  K / 32 must fit the
-// waves of a row tile (K <= 8192, lanes x K <= 8192 without the prologue);
-// several lanes take the prologue up to K 2048, and without it only
-// GEMV_SEGMENTS.
+// waves of a row tile (K <= 8192).
 extern "C" hipError_t igl_launch_gemv_group(int mode, int lanes, int segments, const uint8_t *const *codes,
                                             const long long *row_stride,
                                             const float *const *gains, const int *gain_stride,
@@ -2499,18 +2417,20 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int lanes, int segments, c
                                             int group_shift, int code_bias, const float *act,
                                             int act_stride, int K, const float *mul, int mul_stride,
                                             const igl_gemv_prologue *pro, hipStream_t stream) {
-  GemvGroupArgs a;
+  GemvGroupArgs a{};
   const int units = K / 32;
   if (lanes < 1 || lanes > 4 || segments < 1 || segments > 3 || K % 32 || units > 4 * kWave ||
       group_shift < 0)
     return hipErrorInvalidValue;
+  // lanes past the first: their strides keep them apart
+  if (lanes > 1 && (pro ? pro->lane_stride < K : act_stride < K)) return hipErrorInvalidValue;
+  a.lane_rows = lanes;
+  a.lane_stride = pro && lanes > 1 ? pro->lane_stride : 0;
+  a.act_stride = lanes > 1 ? act_stride : 0;
+  a.mul_stride = lanes > 1 ? mul_stride : 0;
   if (pro && (K > 4096 || !pro->state_in || (pro->lift && (!pro->state_out || !pro->lift_gain ||
                                                             pro->state_out == pro->state_in))))
     return hipErrorInvalidValue;
-  if (lanes > 1 && (pro ? K > 2048 || pro->lane_stride < K : mode != GEMV_SEGMENTS || act_stride < K))
-    return hipErrorInvalidValue;
-  if (!pro && lanes * K > 8192) return hipErrorInvalidValue;
-  a.lane_stride = pro ? pro->lane_stride : 0;
   a.state_in = pro ? pro->state_in : nullptr;
   a.state_out = pro ? pro->state_out : nullptr;
   a.lift = pro ? pro->lift : nullptr;
@@ -2528,29 +2448,27 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int lanes, int segments, c
     const int live = s < segments;
     if (live && (rows[s] < 1 || (mode == GEMV_SEGMENTS && s + 1 < segments && rows[s] % 4)))
       return hipErrorInvalidValue;
-    // lanes of one plane's output must not overlap (GEMV_GELU_PAIR writes out[0] only)
-    if (live && lanes > 1 && (mode == GEMV_SEGMENTS || s == 0) && out_stride[s] < rows[s])
-      return hipErrorInvalidValue;
     a.codes[s] = live ? codes[s] : nullptr;
     a.row_stride[s] = live ? row_stride[s] : 0;
     a.gains[s] = live ? gains[s] : nullptr;
     a.gain_stride[s] = live ? gain_stride[s] : 0;
     a.rows[s] = live ? rows[s] : 0;
     a.out[s] = live ? out[s] : nullptr;
+    // lanes of one plane's output must not overlap (GEMV_GELU_PAIR writes out[0] only)
+    if (live && lanes > 1 && (mode != GEMV_GELU_PAIR || s == 0) && out_stride[s] < rows[s])
+      return hipErrorInvalidValue;
     a.out_stride[s] = live && lanes > 1 ? out_stride[s] : 0;
     total += a.rows[s];
   }
-  if (mode == GEMV_GELU_MUL && lanes > 1 && mul_stride < rows[0]) return hipErrorInvalidValue;
   a.segments = segments;
   a.tiles = mode == GEMV_GELU_PAIR ? (rows[0] + 1) / 2 : (total + 3) / 4;
   a.group_shift = group_shift;
   a.act = act;
-  a.act_stride = lanes > 1 ? act_stride : 0;
   a.act_vec = ((((uintptr_t)act) & 15u) == 0 && (a.act_stride & 3) == 0) ? 1 : 0;
   a.K = K;
   a.unit_bias = 16.0f + (float)code_bias;
   a.mul = mul;
-  a.mul_stride = lanes > 1 ? mul_stride : 0;
+  if (mode == GEMV_GELU_MUL && lanes > 1 && mul_stride < rows[0]) return hipErrorInvalidValue;
   int ksplit = 1;
   while (ksplit < 4 && (units > ksplit * kWave || (a.tiles * ksplit < 2048 && units / (ksplit * 2) >= 32)))
     ksplit *= 2;
@@ -2568,68 +2486,45 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int lanes, int segments, c
   a.pro_vec = vec16 ? 1 : 0;
   // With the prologue, each workgroup repeats the residual update (four
   // K-vectors read, two block sums): past four workgroups a CU, two tiles a
-  // wave halve that for one and two lanes (measured: the 2 x 12288-row
-  // gate/up pair at K 1536, one lane 11.5 -> 9.7 us, a two-lane block 23 us
-  // faster over its 20 such launches; at 6144 rows, and without the
-  // prologue, one tile is faster).
-  const int tpw = lanes <= 2 && pro && ksplit == 1 && (a.tiles + 3) / 4 >= 1024 ? 2 : 1;
+  // wave halve that (measured: the 2 x 12288-row gate/up pair at K 1536, 11.5
+  // -> 9.7 us; at 6144 rows, and without the prologue, one tile is faster).
+  const int tpw = pro && ksplit == 1 && (a.tiles + 3) / 4 >= 1024 ? 2 : 1;
   const int tiles_per_block = 4 / ksplit * tpw;
-  dim3 grid((a.tiles + tiles_per_block - 1) / tiles_per_block);
-  const size_t lds = gemv_dot_lds_bytes(lanes, units);  // at most 29 KiB (lanes x K <= 8192)
+  dim3 grid((a.tiles + tiles_per_block - 1) / tiles_per_block, lanes);
+  const size_t lds = gemv_dot_lds_bytes(1, units);  // at most 29 KiB (K <= 8192)
   // eight-element groups of x a thread stages without a prologue
-  const int items = (lanes * K / 8 + kGemvThreads - 1) / kGemvThreads;
-  const int gpt = items <= 1 ? 1 : items <= 2 ? 2 : 4;
-#define IGL_GROUP_KS(M_, L_, P_, G_)                                                                   \
-  do {                                                                                                 \
-    if (L_ <= 2 && ksplit == 1 && tpw == 2 && P_ != 0)                                                 \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, L_, P_, G_, 1, (L_ <= 2 ? 2 : 1)>), grid,            \
-                         dim3(kGemvThreads), lds, stream, a);                                          \
-    else if (ksplit == 1)                                                                              \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, L_, P_, G_, 1, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
-    else if (ksplit == 2)                                                                              \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, L_, P_, G_, 2, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
-    else                                                                                               \
-      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, L_, P_, G_, 4, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
+  const int gpt = K <= 2048 ? 1 : K <= 4096 ? 2 : 4;
+#define IGL_GROUP_KS(M_, P_, G_)                                                                    \
+  do {                                                                                              \
+    if (ksplit == 1 && tpw == 2 && P_ != 0)                                                         \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 1, 2>), grid, dim3(kGemvThreads), lds, stream, a); \
+    else if (ksplit == 1)                                                                           \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 1, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
+    else if (ksplit == 2)                                                                           \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 2, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
+    else                                                                                            \
+      hipLaunchKernelGGL((gemv_q4_group_kernel<M_, P_, G_, 4, 1>), grid, dim3(kGemvThreads), lds, stream, a); \
   } while (0)
-#define IGL_GROUP_LAUNCH(M_, L_, P_)                                  \
-  do {                                                                \
-    if (P_ != 0 || gpt == 1) IGL_GROUP_KS(M_, L_, P_, 1);             \
-    else if (gpt == 2) IGL_GROUP_KS(M_, L_, P_, 2);                   \
-    else IGL_GROUP_KS(M_, L_, P_, 4);                                 \
+#define IGL_GROUP_LAUNCH(M_, P_)                                  \
+  do {                                                            \
+    if (P_ != 0 || gpt == 1) IGL_GROUP_KS(M_, P_, 1);             \
+    else if (gpt == 2) IGL_GROUP_KS(M_, P_, 2);                   \
+    else IGL_GROUP_KS(M_, P_, 4);                                 \
   } while (0)
   // groups of eight the prologue holds a thread: 1 up to K 2048, 2 up to 4096
   const int held = !pro ? 0 : K <= 2048 ? 1 : K <= 4096 ? 2 : -1;
   if (held < 0) return hipErrorInvalidValue;
-  if (lanes == 1) {
-    switch (mode * 3 + held) {
-      case 0: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 1, 0); break;
-      case 1: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 1, 1); break;
-      case 2: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 1, 2); break;
-      case 3: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 1, 0); break;
-      case 4: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 1, 1); break;
-      case 5: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 1, 2); break;
-      case 6: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 1, 0); break;
-      case 7: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 1, 1); break;
-      case 8: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 1, 2); break;
-      default: return hipErrorInvalidValue;
-    }
-  } else {
-    // several lanes: the prologue holds one group a lane (K <= 2048), and
-    // without it only the query/key/value segments read x
-#define IGL_GROUP_LANES(L_)                                                         \
-  do {                                                                              \
-    switch (mode * 3 + held) {                                                      \
-      case 0: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, L_, 0); break;                        \
-      case 1: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, L_, 1); break;                        \
-      case 4: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, L_, 1); break;                       \
-      case 7: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, L_, 1); break;                        \
-      default: return hipErrorInvalidValue;                                         \
-    }                                                                               \
-  } while (0)
-    if (lanes == 2) IGL_GROUP_LANES(2);
-    else if (lanes == 3) IGL_GROUP_LANES(3);
-    else IGL_GROUP_LANES(4);
-#undef IGL_GROUP_LANES
+  switch (mode * 3 + held) {
+    case 0: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 0); break;
+    case 1: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 1); break;
+    case 2: IGL_GROUP_LAUNCH(GEMV_SEGMENTS, 2); break;
+    case 3: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 0); break;
+    case 4: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 1); break;
+    case 5: IGL_GROUP_LAUNCH(GEMV_GELU_PAIR, 2); break;
+    case 6: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 0); break;
+    case 7: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 1); break;
+    case 8: IGL_GROUP_LAUNCH(GEMV_GELU_MUL, 2); break;
+    default: return hipErrorInvalidValue;
   }
 #undef IGL_GROUP_LAUNCH
 #undef IGL_GROUP_KS
@@ -3274,6 +3169,14 @@ extern "C" size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit) {
   return chunks > 1 ? chunks * (size_t)lanes * (size_t)N : 0;
 }
 
+// Whether two to four lanes of an N x K plane run as one-lane grids side by
+// side rather than in one multi-lane form: below 32768 rows (the head's
+// 262144 x 1536 plane, read once a lane, would double its HBM bytes).
+static bool gemv_lane_rows_pay(int lanes, int N, int K) {
+  (void)K;
+  return lanes >= 2 && lanes <= 4 && N < 32768;
+}
+
 // Launches y = W x for 1..16 lanes (past 16: chunks of 8).  `part` must hold chunks * lanes * N floats
 // when the plane needs more than one K-chunk, and may be NULL otherwise;
 // `lds_limit` is the device's LDS bytes per workgroup.
@@ -3298,7 +3201,7 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
       return hipSuccess;
     }
   }
-  GemvArgs a;
+  GemvArgs a{};
   a.codes = codes;
   a.row_stride = row_stride;
   a.gains = gains;
@@ -3321,16 +3224,23 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
   // workgroups, half the loads a lane in flight: measured ~2% faster at
   // 8192 x 2048 than four, and eight rows 25% slower); enough waves on a row
   // tile that each lane holds one unit (two past 256).
+  //
+  // Two to four lanes of a plane under 32768 rows run as that many one-lane
+  // grids side by side (lane_rows): the arithmetic of a lane is the one-lane
+  // form's, the plane is read once a lane (the repeats from the L2 and the
+  // MALL), and each workgroup stages one lane of x.
+  const int form = gemv_lane_rows_pay(lanes, N, K) ? 1 : lanes;  // lanes of the kernel's form
   if (a.act_vec && lanes <= 4 &&
-      (lanes * K <= kDotMaxItems * kGemvThreads * 8 || (lanes == 2 && K <= 12288)) &&
+      (form * K <= kDotMaxItems * kGemvThreads * 8 || (form == 2 && K <= 12288)) &&
       K / 32 <= 8 * kWave) {
     const int units = K / 32;
-    int R = lanes <= 2 && (units >= 128 || N >= 32768) ? 8 : lanes == 1 ? 2 : 4;
+    a.lane_rows = form == 1 ? lanes : 1;
+    int R = form <= 2 && (units >= 128 || N >= 32768) ? 8 : form == 1 ? 2 : 4;
     // One or two lanes on wide rows: six-row tiles where eight leave CUs
     // without a workgroup and six give every CU at most one (1536 x 12288:
     // 192 -> 256 workgroups, one lane 7.77 -> 6.94 us, two lanes 10.57 ->
     // 9.46 us; 1536 x 6144 4.36 -> 4.27 us and 6.74 -> 6.10 us; the same sums).
-    if (lanes <= 2 && R == 8 && N < 32768 && (N + 7) / 8 < 256 && (N + 5) / 6 <= 256) R = 6;
+    if (form <= 2 && R == 8 && N < 32768 && (N + 7) / 8 < 256 && (N + 5) / 6 <= 256) R = 6;
     const int tiles = (N + R - 1) / R;
     int upl = units > 4 * kWave ? 2 : 1;
     int ksplit = 1;
@@ -3343,7 +3253,7 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
     // 1536 x 2048 2.95 -> 2.61 us, the same sums; 1536 x 4096 3.49 -> 2.97
     // us; two lanes: 1536 x 4096 5.22 -> 3.85 us, 1536 x 2048 3.43 -> 3.14,
     // 1536 x 256 3.10 -> 2.60).
-    if (lanes <= 2 && N < 4096 && units <= 2 * kWave) {
+    if (form <= 2 && N < 4096 && units <= 2 * kWave) {
       R = 2;
       upl = units > kWave ? 2 : 1;
       ksplit = 1;
@@ -3352,7 +3262,7 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
     a.chunk_cols = K;
     a.out = out;
     a.out_stride = out_stride;
-    switch (lanes) {
+    switch (form) {
       case 1:
         if (R == 2) return upl == 2 ? gemv_dot_launch<1, 2, 2>(a, stream) : gemv_dot_launch<1, 2, 1>(a, stream);
         if (R == 4) return gemv_dot_launch<1, 4, 1>(a, stream);
