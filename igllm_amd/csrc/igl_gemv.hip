@@ -3170,11 +3170,16 @@ extern "C" size_t igl_gemv_part_floats(int lanes, int N, int K, int lds_limit) {
 }
 
 // Whether two to four lanes of an N x K plane run as one-lane grids side by
-// side rather than in one multi-lane form: below 32768 rows (the head's
-// 262144 x 1536 plane, read once a lane, would double its HBM bytes).
+// side rather than in one multi-lane form.  Measured (replayed, us, lanes 2 /
+// 3 / 4, one-lane grids against the form): 1536 x 2048 2.87 / 3.03 / 3.11
+// against 3.11 / 4.44 / 4.93, 1536 x 6144 5.21 / 6.66 / 7.76 against 6.08 /
+// 8.55 / 8.64, 4096 x 2048 3.86 / 4.50 / 5.14 against 4.69 / 6.38 / 7.09;
+// but 8192 x 2048 5.47 / 7.17 / 8.52 against 5.17 / 6.23 / 7.09, and past
+// about 40M lane-codes the repeated reads cost more than the form (1536 x
+// 12288: 9.07 / 11.58 / 15.03 against 9.42 / 11.31 / 11.40; 2048 x 8192 four
+// lanes 9.24 against 8.52).  The head's 262144 rows never split.
 static bool gemv_lane_rows_pay(int lanes, int N, int K) {
-  (void)K;
-  return lanes >= 2 && lanes <= 4 && N < 32768;
+  return lanes >= 2 && lanes <= 4 && N <= 4096 && (long long)lanes * N * K <= 40LL * 1024 * 1024;
 }
 
 // Launches y = W x for 1..16 lanes (past 16: chunks of 8).  `part` must hold chunks * lanes * N floats
@@ -3225,10 +3230,10 @@ extern "C" hipError_t igl_launch_gemv_q4(const uint8_t *codes, long long row_str
   // 8192 x 2048 than four, and eight rows 25% slower); enough waves on a row
   // tile that each lane holds one unit (two past 256).
   //
-  // Two to four lanes of a plane under 32768 rows run as that many one-lane
-  // grids side by side (lane_rows): the arithmetic of a lane is the one-lane
-  // form's, the plane is read once a lane (the repeats from the L2 and the
-  // MALL), and each workgroup stages one lane of x.
+  // Two to four lanes of a small plane run as that many one-lane grids side
+  // by side (lane_rows, gemv_lane_rows_pay): the arithmetic of a lane is the
+  // one-lane form's, the plane is read once a lane (the repeats from the L2
+  // and the MALL), and each workgroup stages one lane of x.
   const int form = gemv_lane_rows_pay(lanes, N, K) ? 1 : lanes;  // lanes of the kernel's form
   if (a.act_vec && lanes <= 4 &&
       (form * K <= kDotMaxItems * kGemvThreads * 8 || (form == 2 && K <= 12288)) &&
