@@ -1131,7 +1131,8 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
 
 /* session_pass (11843-11975) for `lanes` ids already in ids_dev, lane 0 at
  * the position in ctl_dev[0] (at most `bound`); with `logits`, the head runs
- * on the last lane (1) or every lane (2). */
+ * on the last lane (1) or every lane (2), its logits not yet capped: the pick
+ * that follows every such pass caps them in place as it reads them. */
 static int run_pass(igl_engine *e, int bound, int lanes, int logits) {
   hipStream_t st = e->stream;
   const int H = e->hidden;
@@ -1174,7 +1175,6 @@ static int run_pass(igl_engine *e, int bound, int lanes, int logits) {
     if (!(head_all && settled))
       OKAY(norm_rows(e, e->state + (size_t)from * H, e->final_norm, H, span, H, e->scrap));
     OKAY(project(e, &e->head, e->scrap, H, span, e->logits, e->vocab));
-    if (e->cap > 0.0f) RUN(igl_launch_logit_cap(e->logits, (size_t)span * e->vocab, e->cap, st));
   }
   return IGL_OKAY;
 }
@@ -1204,7 +1204,7 @@ static int step_body(igl_engine *e) {
   RUN(hipMemcpyAsync(e->ctl_dev, &e->io->place, 2 * sizeof(int32_t), hipMemcpyHostToDevice,
                      e->stream));
   OKAY(run_pass(e, e->window_limit - 1, 1, 1));
-  RUN(igl_launch_pick(e->logits, e->vocab, (size_t)e->vocab, 1, e->pick_work, e->pick_dev,
+  RUN(igl_launch_pick(e->logits, e->vocab, (size_t)e->vocab, 1, e->cap, e->pick_work, e->pick_dev,
                       e->stream));
   RUN(hipMemcpyAsync(&e->io->pick, e->pick_dev, 2 * sizeof(int32_t), hipMemcpyDeviceToHost,
                      e->stream));
@@ -1296,7 +1296,7 @@ static int guess_body(igl_engine *e, int count, int bound) {
   RUN(hipMemcpyAsync(e->ctl_dev, e->ctl_host, (1 + (size_t)count) * sizeof(int32_t), hipMemcpyHostToDevice,
                      e->stream));
   OKAY(run_pass(e, bound, count, 2));
-  RUN(igl_launch_pick(e->logits, e->vocab, (size_t)e->vocab, count, e->pick_work, e->pick_dev,
+  RUN(igl_launch_pick(e->logits, e->vocab, (size_t)e->vocab, count, e->cap, e->pick_work, e->pick_dev,
                       e->stream));
   RUN(hipMemcpyAsync(e->pairs_host, e->pick_dev, 2 * (size_t)count * sizeof(int32_t),
                      hipMemcpyDeviceToHost, e->stream));

@@ -241,9 +241,10 @@ hipError_t igl_launch_gelu_gate_rows(float *gate, int gate_stride, const float *
 hipError_t igl_launch_cache_lay_rows(const float *rows, int row_stride, int width, float scale,
                                      uint8_t *store, int span, int place_first, int lanes,
                                      hipStream_t stream);
-hipError_t igl_launch_logit_cap(float *v, size_t n, float cap, hipStream_t stream);
 size_t igl_pick_work_bytes(int lanes);
-hipError_t igl_launch_pick(const float *v, int n, size_t stride, int lanes, void *work,
+/* The greedy pick of `lanes` rows of n logits, `stride` floats apart; with
+ * cap > 0 the rows are first capped in place (the final logit softcap). */
+hipError_t igl_launch_pick(float *v, int n, size_t stride, int lanes, float cap, void *work,
                            int32_t *pairs, hipStream_t stream);
 
 hipError_t igl_launch_quant_step(const float *src, int src_stride, float *dst, int dst_stride,

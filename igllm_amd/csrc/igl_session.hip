@@ -264,17 +264,6 @@ __global__ void cache_lay_rows_kernel(const float *rows, int row_stride, int wid
   store[slot * width + i] = e4m3_code(rows[(size_t)lane * row_stride + i] / scale);
 }
 
-// cap * (1 - 2 / (e^(2y) + 1)), y = x / cap clamped to +-10 (kern_logit_cap_one, 5009-5014).
-__global__ void logit_cap_kernel(float *v, size_t n, float cap) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const float back = 1.0f / cap;
-  float y = v[i] * back;
-  if (y > 10.0f) y = 10.0f;
-  if (y < -10.0f) y = -10.0f;
-  v[i] = cap * (1.0f - 2.0f / (exp_near(y + y) + 1.0f));
-}
-
 // Greedy pick: the first index of the largest logit (session_pick_at
 // 14672-14677), and the gap to the second largest value.  Stage one: per-block
 // (best, index, second); stage two in one block.
@@ -298,15 +287,27 @@ __device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
   return r;
 }
 
-// One lane of logits a grid row (blockIdx.y), `stride` floats apart.
-__global__ __launch_bounds__(256) void pick_stage_kernel(const float *v, int n, size_t stride,
+// One lane of logits a grid row (blockIdx.y), `stride` floats apart.  With
+// cap > 0 each logit is first capped, cap * (1 - 2 / (e^(2y) + 1)) with y =
+// x / cap clamped to +-10 (kern_logit_cap_one, 5009-5014), and written back,
+// so the row holds the capped logits the pick reads.
+__global__ __launch_bounds__(256) void pick_stage_kernel(float *v, int n, size_t stride, float cap,
                                                          Top2 *part) {
   __shared__ Top2 red[256];
   v += (size_t)blockIdx.y * stride;
   part += (size_t)blockIdx.y * gridDim.x;
   Top2 t{-INFINITY, 0x7FFFFFFF, -INFINITY};
+  const float back = cap > 0.0f ? 1.0f / cap : 0.0f;
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-    Top2 one{v[i], i, -INFINITY};
+    float x = v[i];
+    if (cap > 0.0f) {
+      float y = x * back;
+      if (y > 10.0f) y = 10.0f;
+      if (y < -10.0f) y = -10.0f;
+      x = cap * (1.0f - 2.0f / (exp_near(y + y) + 1.0f));
+      v[i] = x;
+    }
+    Top2 one{x, i, -INFINITY};
     t = top2_merge(t, one);
   }
   red[threadIdx.x] = t;
@@ -473,20 +474,15 @@ extern "C" hipError_t igl_launch_cache_lay_rows(const float *rows, int row_strid
   return hipGetLastError();
 }
 
-extern "C" hipError_t igl_launch_logit_cap(float *v, size_t n, float cap, hipStream_t stream) {
-  hipLaunchKernelGGL(logit_cap_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, v, n, cap);
-  return hipGetLastError();
-}
-
 // Workspace for `lanes` lanes of igl_launch_pick.
 extern "C" size_t igl_pick_work_bytes(int lanes) { return sizeof(Top2) * kPickBlocks * (size_t)lanes; }
 
 // The greedy pick of `lanes` rows of n logits, `stride` floats apart, into
 // pairs[2 l] (index) and pairs[2 l + 1] (the top-1/top-2 gap's float bits).
-extern "C" hipError_t igl_launch_pick(const float *v, int n, size_t stride, int lanes, void *work,
+extern "C" hipError_t igl_launch_pick(float *v, int n, size_t stride, int lanes, float cap, void *work,
                                       int32_t *pairs, hipStream_t stream) {
   hipLaunchKernelGGL(pick_stage_kernel, dim3(kPickBlocks, lanes), dim3(256), 0, stream, v, n,
-                     stride, reinterpret_cast<Top2 *>(work));
+                     stride, cap, reinterpret_cast<Top2 *>(work));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(pick_final_kernel, dim3(lanes), dim3(256), 0, stream,

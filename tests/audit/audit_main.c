@@ -122,7 +122,7 @@ static int run_planted(void) {
     return 2;
   (void)igl_launch_gelu_mul(gate, n, ple, n, n, lanes, NULL);
   (void)igl_launch_add_rows(ple + n, n, ple, n, n, lanes, 1.0f, 0, NULL);    /* past the end */
-  (void)igl_launch_pick(logits, n / 2, (size_t)n / 2, 2, work, pairs, NULL);
+  (void)igl_launch_pick(logits, n / 2, (size_t)n / 2, 2, 0.0f, work, pairs, NULL);
   hipFree(gate);
   hipFree(ple);
   hipFree(logits);

@@ -742,19 +742,13 @@ hipError_t W(igl_launch_gelu_gate_rows)(float *gate, int gate_stride, const floa
   return R(igl_launch_gelu_gate_rows)(gate, gate_stride, rise, rise_stride, n, lanes, stream);
 }
 
-hipError_t R(igl_launch_logit_cap)(float *, size_t, float, hipStream_t);
-hipError_t W(igl_launch_logit_cap)(float *v, size_t n, float cap, hipStream_t stream) {
-  check_range("igl_launch_logit_cap", "v", v, n * 4);
-  return R(igl_launch_logit_cap)(v, n, cap, stream);
-}
-
-hipError_t R(igl_launch_pick)(const float *, int, size_t, int, void *, int32_t *, hipStream_t);
-hipError_t W(igl_launch_pick)(const float *v, int n, size_t stride, int lanes, void *work, int32_t *pairs,
+hipError_t R(igl_launch_pick)(float *, int, size_t, int, float, void *, int32_t *, hipStream_t);
+hipError_t W(igl_launch_pick)(float *v, int n, size_t stride, int lanes, float cap, void *work, int32_t *pairs,
                               hipStream_t stream) {
   check_range("igl_launch_pick", "v", v, rows_bytes(lanes, stride, (size_t)n, 4));
   check_range("igl_launch_pick", "work", work, igl_pick_work_bytes(lanes));
   check_range("igl_launch_pick", "pairs", pairs, (size_t)lanes * 8);
-  return R(igl_launch_pick)(v, n, stride, lanes, work, pairs, stream);
+  return R(igl_launch_pick)(v, n, stride, lanes, cap, work, pairs, stream);
 }
 
 hipError_t R(igl_launch_norm_rms)(const float *, const float *, int, int, int, float, float *, hipStream_t);
