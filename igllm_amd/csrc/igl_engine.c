@@ -43,9 +43,13 @@
  * sized by this and not by the prime's lane limit.  The reference's blocks
  * carry at most KERN_LANE_LIMIT = 16 (app_core.c:1980). */
 #define ENG_GUESS_LIMIT 64
-/* lanes a pass runs with the grouped projections and the prepared attention
- * (a decode step, a small speculative block) */
+/* lanes a pass runs with the prepared attention (a decode step, a small
+ * speculative block) */
 #define ENG_SMALL_LANES 4
+/* lanes a pass runs with the grouped projections, one row of workgroups a
+ * lane (blocks of 5, 6 and 8 lanes: 3.12 / 3.16 / 3.31 -> 2.54 / 2.69 / 3.04
+ * ms against separate projections and updates) */
+#define ENG_GROUP_LANES 8
 #define ENG_TENSOR_LIMIT 4096
 
 typedef struct eng_tensor {
@@ -969,7 +973,7 @@ static int settle(igl_engine *e, int lanes, const float *next_norm) {
  * 11637-11743 with session_attend 11455-11580.
  *
  * A batch runs every residual update as its own launch, with scrap holding
- * the next sub-block's normed input.  One to four lanes (a decode step, a
+ * the next sub-block's normed input.  One to eight lanes (a decode step, a
  * speculative block) fold each update into the prologue of the grouped
  * launch that consumes it - the post-attention update into the gate/up
  * launch, the post-feed-forward one into the per-layer-input gate, and this
@@ -996,8 +1000,8 @@ static int run_layer(igl_engine *e, int li, int bound, int lanes) {
   group_add(e, &gf, &L->gate, e->gate, e->inner_max);
   group_add(e, &gf, &L->up, e->rise, e->inner_max);
   group_add(e, &gp, &L->ple_gate, e->gate, e->inner_max);
-  /* the grouped launches take one to four lanes up to hidden 4096 */
-  fused = lanes <= ENG_SMALL_LANES && H <= 4096 &&
+  /* the grouped launches take one to eight lanes up to hidden 4096 */
+  fused = lanes <= ENG_GROUP_LANES && H <= 4096 &&
           group_fits(&gq, pq, IGL_GEMV_SEGMENTS) &&
           group_fits(&gf, pf, IGL_GEMV_GELU_PAIR) && group_fits(&gp, pp, IGL_GEMV_GELU_MUL) &&
           L->q.col_count == H && L->gate.col_count == H && L->ple_gate.col_count == H;

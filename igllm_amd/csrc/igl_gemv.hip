@@ -1456,7 +1456,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_real_kernel(GemvRealArgs a)
 //                  input gate, session_layer 11718-11723).
 // Each row's sum is formed as gemv_q4_dot_kernel forms it with one unit a
 // lane; with the same K-split the results are those of separate launches
-// followed by the elementwise kernel, bit for bit.  Two to four lanes (a
+// followed by the elementwise kernel, bit for bit.  Two to eight lanes (a
 // speculative block) run as that many rows of workgroups (blockIdx.y = lane,
 // `lane_rows`): every lane's arithmetic is the one-lane step's, and each row
 // reads the planes again, the repeats served by the L2 and the MALL (a
@@ -2403,7 +2403,7 @@ extern "C" int igl_gemv_chunk_cols(int lanes, int K, int lds_limit) {
   return per * 32;
 }
 
-// One to four activation rows (lanes) against `segments` planes of the same
+// One to eight activation rows (lanes) against `segments` planes of the same
 // width and group size (see gemv_q4_group_kernel for the modes; lane l of
 // act, out[s], mul and the prologue's vectors lies l act_stride, l
 // out_stride[s], l mul_stride, l lane_stride floats in).  Every plane but the
@@ -2419,7 +2419,7 @@ extern "C" hipError_t igl_launch_gemv_group(int mode, int lanes, int segments, c
                                             const igl_gemv_prologue *pro, hipStream_t stream) {
   GemvGroupArgs a{};
   const int units = K / 32;
-  if (lanes < 1 || lanes > 4 || segments < 1 || segments > 3 || K % 32 || units > 4 * kWave ||
+  if (lanes < 1 || lanes > 8 || segments < 1 || segments > 3 || K % 32 || units > 4 * kWave ||
       group_shift < 0)
     return hipErrorInvalidValue;
   // lanes past the first: their strides keep them apart

@@ -122,7 +122,7 @@ hipError_t igl_launch_gemv_level_pair(const igl_code_view *gate, const igl_code_
 hipError_t igl_launch_gemv_level_segments(const igl_code_view *v, int segments, const int *rows,
                                           float *const *out, const float *leave, float step,
                                           const igl_gemv_prologue *pro, int K, hipStream_t stream);
-/* One to four lanes against up to three 4-bit planes that read the same
+/* One to eight lanes against up to three 4-bit planes that read the same
  * activations, in one launch with the mode's epilogue; lane m of act, out[s]
  * and mul lies m act_stride, m out_stride[s], m mul_stride floats in. */
 hipError_t igl_launch_gemv_group(int mode, int lanes, int segments, const uint8_t *const *codes,

@@ -1,6 +1,6 @@
 """Lanes as rows of one-lane workgroups (`lane_rows`): a launch of two to four
-lanes whose form runs every lane as the one-lane launch gives each lane that
-launch's outputs to the bit.  Checked on the integer-dot GEMV (planes where
+lanes whose form runs every lane as the one-lane launch (up to eight for the
+grouped launches) gives each lane that launch's outputs to the bit.  Checked on the integer-dot GEMV (planes where
 gemv_lane_rows_pay takes the rows) and on the grouped decode launches
 (igl_launch_gemv_group: q/k/v segments, gate/up with gelu * up and the
 residual-update prologue, the per-layer-input gate with gelu * mul), against
@@ -62,6 +62,8 @@ def _bind(lib):
     (GEMV_GELU_PAIR, (6144, 6144), 1536, 4, True),
     (GEMV_GELU_MUL, (256,), 1536, 3, True),              # the per-layer-input gate, K split four ways
     (GEMV_SEGMENTS, (4096, 512, 512), 2048, 4, True),
+    (GEMV_GELU_PAIR, (6144, 6144), 1536, 8, True),       # a block of eight lanes
+    (GEMV_GELU_MUL, (256,), 1536, 6, True),
 ])
 def test_group_lane_rows_equal_one_lane(backend, mode, rows, K, lanes, pro):
     print("case group lane rows mode=%d rows=%s K=%d lanes=%d pro=%d" % (mode, rows, K, lanes, pro), flush=True)
