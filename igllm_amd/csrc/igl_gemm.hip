@@ -30,10 +30,11 @@
 // stages written only by the LDS DMA (global_load_lds: no registers hold loads
 // in flight); a stage holds KS consecutive 64-wide steps, and wave group ks of
 // the workgroup takes the ks-th: the K split happens inside the workgroup, and
-// the KS partial tiles are added in ks order through LDS at the end, so no
-// partial sums go to memory and the result does not depend on the tiling's
-// timing.  Small tile counts (few lanes, or few rows) take a deeper KS instead
-// of a K split across workgroups.
+// the KS partial tiles are added in ks order through LDS at the end, so the
+// result does not depend on the tiling's timing.  Small tile counts (few
+// lanes, or few rows) take a deeper KS; on long rows (K >= 4096) they also
+// split K across workgroups (grid z = slice), each slice's fp32 product going
+// to the work area and one launch adding the slices in slice order.
 #include "igl_device.h"
 #include "igl_launch.h"
 
@@ -198,6 +199,8 @@ struct GemmCodesArgs {
   int out_stride;
   int M, N, K;
   int Kp;                   // K padded to whole steps: the activation rows' length
+  int slice_k;              // k a workgroup covers: Kp, or K / gridDim.z with K split across workgroups
+  long long slice_stride;   // fp32 C only: floats between the partial products of K slices z and z + 1
   igl_gemm_close close;     // fp32 C only: C = grid(close.gains[n] step acc, leave)
 };
 
@@ -269,7 +272,8 @@ __global__ __launch_bounds__(64 * WN * WM * KS) void gemm_codes_kernel(GemmCodes
   int tile_x, tile_y;
   xcd_tile(tile_x, tile_y);
   const int n0 = tile_x * TN, m0 = tile_y * TM;
-  const int steps = g.Kp / (kStepK * KS);
+  const int steps = g.slice_k / (kStepK * KS);
+  const int kbase = (int)blockIdx.z * g.slice_k;
   const int gq = lane >> 4;  // lane group: k 8 gq .. 8 gq + 7 of a 32-code group
   const int n = lane & 15;
 
@@ -337,7 +341,7 @@ __global__ __launch_bounds__(64 * WN * WM * KS) void gemm_codes_kernel(GemmCodes
   auto stage = [&](int s) { return lds + (s % STAGES) * F::STAGE; };
   auto issue = [&](int s) {
     uint8_t *st = stage(s);
-    const size_t k0 = (size_t)s * (kStepK * KS);
+    const size_t k0 = (size_t)kbase + (size_t)s * (kStepK * KS);
 #pragma unroll
     for (int u = 0; u < F::NA; ++u)
       __builtin_amdgcn_global_load_lds((global_void_t *)(g.a_hi + a_off[u] + k0),
@@ -529,10 +533,37 @@ __global__ __launch_bounds__(64 * WN * WM * KS) void gemm_codes_kernel(GemmCodes
           reinterpret_cast<uint16_t *>(g.out)[(size_t)m * g.out_stride + nn] = float_to_bf16(v);
         } else {
           if (g.close.gains) v = close_value(g.close, nn, v);
-          reinterpret_cast<float *>(g.out)[(size_t)m * g.out_stride + nn] = v;
+          reinterpret_cast<float *>(g.out)[(size_t)blockIdx.z * g.slice_stride + (size_t)m * g.out_stride + nn] = v;
         }
       }
     }
+}
+
+// ---- K slices ---------------------------------------------------------------
+//
+// With K split across workgroups each slice's product (already scaled by the
+// row's 2^-t, an exact power of two) is an fp32 tile of its own; one thread an
+// output adds the S slices in slice order (all S loads issued first) and
+// converts once.  The order is fixed, so the result does not depend on timing.
+constexpr int kFoldThreads = 256;
+
+template <int S>
+__global__ __launch_bounds__(kFoldThreads) void gemm_slice_fold_kernel(const float *part, long long slice_stride,
+                                                                       int M, int N, void *out, int out_bf16,
+                                                                       int out_stride) {
+  const size_t i = (size_t)blockIdx.x * kFoldThreads + threadIdx.x;
+  if (i >= (size_t)M * (size_t)N) return;
+  float v[S];
+#pragma unroll
+  for (int z = 0; z < S; ++z) v[z] = part[(size_t)z * slice_stride + i];
+  float sum = v[0];
+#pragma unroll
+  for (int z = 1; z < S; ++z) sum += v[z];
+  const size_t m = i / (size_t)N, n = i % (size_t)N;
+  if (out_bf16)
+    reinterpret_cast<uint16_t *>(out)[m * (size_t)out_stride + n] = float_to_bf16(sum);
+  else
+    reinterpret_cast<float *>(out)[m * (size_t)out_stride + n] = sum;
 }
 
 // ---- forms and their choice -----------------------------------------------
@@ -553,6 +584,7 @@ constexpr FormShape kForms[] = {
                            // lanes: 26.5 us, against 29.0 split in four)
 };
 constexpr int kFormCount = sizeof(kForms) / sizeof(kForms[0]);
+constexpr int kSplitForm = 2;  // the form a K split across workgroups takes
 // Two-term activations: the same forms with the K split capped where the
 // stages would not fit.
 constexpr FormShape kFormsLo[] = {
@@ -577,6 +609,42 @@ static int choose_form(int M, int N, int K, int two_terms) {
   return last;
 }
 
+struct GemmPlan {
+  int form;
+  int slices;  // K split across workgroups: 1, or 2 .. 16 slices folded by gemm_slice_fold_kernel
+};
+
+// Long rows (K >= 4096) where the walk above ends at a form narrower than
+// 64 x 64 (a few hundred lanes or less) take the 64 x 64 form instead, with K
+// split across workgroups into S = 1, 2, 4 or 8 slices: each workgroup then
+// stages K / S of its lanes' activations instead of all of K, for S fp32
+// partial tiles written and folded.  S is the most slices whose workgroups
+// still run in one round on the 256 CUs (one a CU at this form's LDS): a
+// second round, or more partials, cost more than the shorter K saves (1536 x
+// 6144 at 128 lanes: 48 tiles, 19.4 us in four slices, 25.7 in eight; at 512
+// lanes 36.7 unsplit, 43.8 in two).  Replayed, us, bf16 / fp32 activations,
+// the walk's form against the split:
+//   2048 x 8192:  64 lanes 25.0 / 39.9 -> 18.9 / 22.1 (S 8), 128 lanes 26.6 /
+//                 43.0 -> 22.8 / 27.3 (S 4), 256 lanes 38.1 / 55.1 -> 30.9 /
+//                 39.7 (S 2)
+//   1536 x 6144:  64 lanes 20.7 / 32.7 -> 16.5 / 18.2, 256 lanes 36.5 / 62.5
+//                 -> 26.9 / 33.2, 512 lanes 53.7 / 77.2 -> 36.7 / 47.4 (S 1)
+//   1536 x 12288: 64 lanes 37.2 / 61.9 -> 21.3 / 25.6, 256 lanes 66.2 / 114.7
+//                 -> 39.9 / 52.3
+// Rows of 2048 (8192 x 2048) were slower split at every lane count tried
+// (64-256): the partials cost more than the shorter staging saves.
+static GemmPlan choose_plan(int M, int N, int K, int two_terms, bool close) {
+  GemmPlan p{choose_form(M, N, K, two_terms), 1};
+  if (close || K < 4096 || p.form < kSplitForm) return p;
+  const FormShape &s = (two_terms ? kFormsLo : kForms)[kSplitForm];
+  if (K % (kStepK * s.ks)) return p;
+  const long tiles = (long)((N + 16 * s.nb * s.wn - 1) / (16 * s.nb * s.wn)) *
+                     (long)((M + 16 * s.mb * s.wm - 1) / (16 * s.mb * s.wm));
+  int slices = 1;
+  while (slices < 8 && tiles * 2 * slices <= 256 && K % (2 * slices * kStepK * s.ks) == 0) slices *= 2;
+  return GemmPlan{kSplitForm, slices};
+}
+
 template <int WN, int WM, int KS, int NB, int MB, int LIM, bool LO, bool ROWGAIN, bool ZERO, bool C_BF16>
 static hipError_t launch_form(const GemmCodesArgs &a, hipStream_t stream) {
   using F = CodesForm<WN, WM, KS, NB, MB, LIM, LO, ROWGAIN, ZERO>;
@@ -588,7 +656,7 @@ static hipError_t launch_form(const GemmCodesArgs &a, hipStream_t stream) {
     if (e != hipSuccess) return e;
     granted = true;
   }
-  const dim3 grid((a.N + F::TN - 1) / F::TN, (a.M + F::TM - 1) / F::TM);
+  const dim3 grid((a.N + F::TN - 1) / F::TN, (a.M + F::TM - 1) / F::TM, a.Kp / a.slice_k);
   hipLaunchKernelGGL((gemm_codes_kernel<WN, WM, KS, NB, MB, LIM, LO, ROWGAIN, ZERO, C_BF16>), grid, dim3(F::THREADS),
                      (size_t)F::LDS, stream, a);
   return hipGetLastError();
@@ -629,13 +697,25 @@ static int padded_k(int K) { return (K + kStepK - 1) / kStepK * kStepK; }
 
 extern "C" int igl_gemm_fits(int M, int N, int K) { return M >= 1 && N >= 1 && K >= 32 && K % 32 == 0; }
 
+static size_t inv_bytes(int M) { return ((size_t)M * sizeof(float) + 255) & ~(size_t)255; }
+
+// The K slices' fp32 partial products, [slices][M][N].
+static size_t slice_bytes(const GemmPlan &p, int M, int N) {
+  return p.slices > 1 ? ((size_t)p.slices * (size_t)M * (size_t)N * sizeof(float) + 255) & ~(size_t)255 : 0;
+}
+
 extern "C" size_t igl_gemm_work_bytes(int M, int N, int K, int act_terms) {
   if (!igl_gemm_fits(M, N, K)) return 0;
-  return half_bytes(M, padded_k(K)) * (act_terms == 2 ? 2 : 1) + (((size_t)M * sizeof(float) + 255) & ~(size_t)255);
+  return half_bytes(M, padded_k(K)) * (act_terms == 2 ? 2 : 1) + inv_bytes(M) +
+         slice_bytes(choose_plan(M, N, K, act_terms == 2, false), M, N);
 }
 
 extern "C" int igl_gemm_form(int M, int N, int K, int act_terms) {
-  return igl_gemm_fits(M, N, K) ? choose_form(M, N, K, act_terms == 2) : -1;
+  return igl_gemm_fits(M, N, K) ? choose_plan(M, N, K, act_terms == 2, false).form : -1;
+}
+
+extern "C" int igl_gemm_slices(int M, int N, int K, int act_terms) {
+  return igl_gemm_fits(M, N, K) ? choose_plan(M, N, K, act_terms == 2, false).slices : 0;
 }
 
 extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride, const uint8_t *codes,
@@ -687,20 +767,58 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
   a.N = N;
   a.K = K;
   a.Kp = Kp;
+  a.slice_k = Kp;
+  a.slice_stride = 0;
   a.close = cl;
-  const int form = choose_form(M, N, K, lo);
+  const GemmPlan plan = choose_plan(M, N, K, lo, cl.gains != nullptr);
+  const int form = plan.form;
+  int c_bf16 = out_bf16;
+  float *part = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(work) + half_bytes(M, Kp) * (lo ? 2 : 1) +
+                                          inv_bytes(M));
+  if (plan.slices > 1) {
+    // each slice's fp32 product into the work area; the fold writes C
+    a.slice_k = K / plan.slices;
+    a.slice_stride = (long long)M * (long long)N;
+    a.out = part;
+    a.out_stride = N;
+    c_bf16 = 0;
+  }
   const bool rowgain = group_shift >= 31;
   const bool zero = zero_pairs != nullptr;
   if (lo) {
     if (rowgain)
-      return zero ? launch_out<true, true, true>(form, out_bf16, a, stream)
-                  : launch_out<true, true, false>(form, out_bf16, a, stream);
-    return zero ? launch_out<true, false, true>(form, out_bf16, a, stream)
-                : launch_out<true, false, false>(form, out_bf16, a, stream);
+      e = zero ? launch_out<true, true, true>(form, c_bf16, a, stream)
+               : launch_out<true, true, false>(form, c_bf16, a, stream);
+    else
+      e = zero ? launch_out<true, false, true>(form, c_bf16, a, stream)
+               : launch_out<true, false, false>(form, c_bf16, a, stream);
+  } else if (rowgain) {
+    e = zero ? launch_out<false, true, true>(form, c_bf16, a, stream)
+             : launch_out<false, true, false>(form, c_bf16, a, stream);
+  } else {
+    e = zero ? launch_out<false, false, true>(form, c_bf16, a, stream)
+             : launch_out<false, false, false>(form, c_bf16, a, stream);
   }
-  if (rowgain)
-    return zero ? launch_out<false, true, true>(form, out_bf16, a, stream)
-                : launch_out<false, true, false>(form, out_bf16, a, stream);
-  return zero ? launch_out<false, false, true>(form, out_bf16, a, stream)
-              : launch_out<false, false, false>(form, out_bf16, a, stream);
+  if (e != hipSuccess || plan.slices == 1) return e;
+  const size_t count = (size_t)M * (size_t)N;
+  const dim3 fold_grid((unsigned)((count + kFoldThreads - 1) / kFoldThreads));
+  switch (plan.slices) {
+    case 2:
+      hipLaunchKernelGGL(gemm_slice_fold_kernel<2>, fold_grid, dim3(kFoldThreads), 0, stream, part,
+                         a.slice_stride, M, N, out, out_bf16, out_stride);
+      break;
+    case 4:
+      hipLaunchKernelGGL(gemm_slice_fold_kernel<4>, fold_grid, dim3(kFoldThreads), 0, stream, part,
+                         a.slice_stride, M, N, out, out_bf16, out_stride);
+      break;
+    case 8:
+      hipLaunchKernelGGL(gemm_slice_fold_kernel<8>, fold_grid, dim3(kFoldThreads), 0, stream, part,
+                         a.slice_stride, M, N, out, out_bf16, out_stride);
+      break;
+    default:
+      hipLaunchKernelGGL(gemm_slice_fold_kernel<16>, fold_grid, dim3(kFoldThreads), 0, stream, part,
+                         a.slice_stride, M, N, out, out_bf16, out_stride);
+      break;
+  }
+  return hipGetLastError();
 }

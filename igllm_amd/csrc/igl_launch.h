@@ -157,6 +157,7 @@ typedef struct igl_gemm_close {
 int igl_gemm_fits(int M, int N, int K);
 size_t igl_gemm_work_bytes(int M, int N, int K, int act_terms);
 int igl_gemm_form(int M, int N, int K, int act_terms);
+int igl_gemm_slices(int M, int N, int K, int act_terms);
 hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_stride, const uint8_t *codes,
                               long long row_stride, const float *gains, int gain_stride,
                               int group_shift, int code_bias, const uint32_t *zero_pairs, void *out,

@@ -405,6 +405,76 @@ def test_gemm_repeat_bitwise(backend):
         backend.detach(cp)
 
 
+def gemm_slices(backend, M, N, K, terms):
+    """How many K slices the GEMM launcher splits K into across workgroups
+    (1: none)."""
+    fn = backend.lib.igl_gemm_slices
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int] * 4
+    return fn(M, N, K, terms)
+
+
+# (M, N, K, group, zero points): long rows at a few hundred lanes or less,
+# whose K the launcher splits across workgroups into 2, 4 and 8 slices, with
+# ragged tiles in M and N, groups of 64 codes, one gain a row, and zero points.
+SLICE_CASES = [(64, 2048, 8192, 32, False), (100, 1000, 4096, 32, False), (192, 2048, 8192, 32, False),
+               (70, 4000, 4096, 64, False), (96, 512, 16384, 16384, False), (128, 1536, 6144, 32, True)]
+
+
+@pytest.mark.parametrize("terms", [1, 2])
+def test_gemm_k_slices(backend, terms):
+    """K split across workgroups: each slice's fp32 product (row scale
+    applied, exactly) written apart and the slices added in slice order by a
+    second launch.  bf16 activations (one term) against the float64 closed
+    form at the bf16 output's rounding, fp32 ones (two terms) against the
+    oracle at 1e-3; each case repeated bit-identical; 2, 4 and 8 slices all
+    reached."""
+    seen = set()
+    for M, N, K, group, zero in SLICE_CASES:
+        slices = gemm_slices(backend, M, N, K, terms)
+        seen.add(slices)
+        print_case(test="k_slices", M=M, N=N, K=K, group=group, zero=zero, terms=terms, slices=slices)
+        codes, gains, act = synth_projection(N, K, M, seed=M + K + group, group_size=group)
+        zeros = None
+        if zero:
+            zeros = np.random.default_rng(M + N).integers(-8, 8, size=gains.shape).astype(np.int8)
+        cp = backend.attach(make_plane(codes, gains, K, group_size=group, zeros=zeros))
+        if terms == 1:
+            a16 = bf16_round(act).reshape(M, K)
+            dev_a = backend.upload(a16)
+            dev_c = backend.alloc(M * N * 2)
+            runs = []
+            for _ in range(2):
+                backend.gemm_bf16_dev(cp, dev_a, K, M, dev_c, N)
+                backend.sync()
+                runs.append(dev_c.get(np.uint16, M * N))
+            assert np.array_equal(runs[0], runs[1])
+            got = bf16_to_f32(runs[0]).reshape(M, N).astype(np.float64)
+            nib = np.stack([codes & 15, codes >> 4], axis=-1).reshape(N, -1)[:, :K].astype(np.float64)
+            sub = 8.0 if zeros is None else 8.0 + np.repeat(zeros.astype(np.float64), group, axis=1)[:, :K]
+            w = (nib - sub) * np.repeat(gains.astype(np.float64), group, axis=1)[:, :K]
+            want = bf16_to_f32(a16).astype(np.float64) @ w.T
+            rms = math.sqrt(float(np.mean(want ** 2)))
+            excess = np.abs(got - want) - (2.0 ** -8 * np.abs(want) + 1e-4 * rms)
+            same = float(np.mean(got == bf16_to_f32(bf16_round(want.astype(np.float32)))))
+            print("max_excess", float(excess.max()), "bf16(y) share", same)
+            assert float(excess.max()) <= 0.0
+            assert same >= 0.999
+            dev_a.free()
+            dev_c.free()
+        else:
+            got = run_gemv_dev(backend, cp, act, M, path="mat_mat")
+            again = run_gemv_dev(backend, cp, act, M, path="mat_mat")
+            assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+            kw = {} if zeros is None else {"zeros": zeros}
+            want = ol.oracle_mat_mat(codes, gains, act, K, group, threads=8, **kw)
+            err = rel_err(got, want)
+            print("rel_err", err)
+            assert err <= 1e-3
+        backend.detach(cp)
+    assert {2, 4, 8} <= seen
+
+
 def test_mat_mat_many_lanes_takes_gemm(backend):
     """fp32 activations with >= 64 lanes go to the MFMA GEMM through mat_mat_dev."""
     N, K, M = 384, 1024, 96
