@@ -542,28 +542,46 @@ __global__ __launch_bounds__(64 * WN * WM * KS) void gemm_codes_kernel(GemmCodes
 // ---- K slices ---------------------------------------------------------------
 //
 // With K split across workgroups each slice's product (already scaled by the
-// row's 2^-t, an exact power of two) is an fp32 tile of its own; one thread an
-// output adds the S slices in slice order (all S loads issued first) and
-// converts once.  The order is fixed, so the result does not depend on timing.
+// row's 2^-t, an exact power of two) is an fp32 tile of its own; a thread
+// takes V consecutive outputs of a row (V = 4, 16-byte loads, where N is a
+// multiple of 4), adds the S slices in slice order (all S loads issued first)
+// and converts once.  The order is fixed, so the result does not depend on
+// timing.
 constexpr int kFoldThreads = 256;
 
-template <int S>
+template <int S, int V>
 __global__ __launch_bounds__(kFoldThreads) void gemm_slice_fold_kernel(const float *part, long long slice_stride,
                                                                        int M, int N, void *out, int out_bf16,
                                                                        int out_stride) {
-  const size_t i = (size_t)blockIdx.x * kFoldThreads + threadIdx.x;
+  const size_t i = ((size_t)blockIdx.x * kFoldThreads + threadIdx.x) * V;
   if (i >= (size_t)M * (size_t)N) return;
-  float v[S];
+  typedef float vec_t __attribute__((ext_vector_type(V)));
+  vec_t v[S];
 #pragma unroll
-  for (int z = 0; z < S; ++z) v[z] = part[(size_t)z * slice_stride + i];
-  float sum = v[0];
+  for (int z = 0; z < S; ++z) v[z] = *reinterpret_cast<const vec_t *>(part + (size_t)z * slice_stride + i);
+  vec_t sum = v[0];
 #pragma unroll
   for (int z = 1; z < S; ++z) sum += v[z];
   const size_t m = i / (size_t)N, n = i % (size_t)N;
-  if (out_bf16)
-    reinterpret_cast<uint16_t *>(out)[m * (size_t)out_stride + n] = float_to_bf16(sum);
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    if (out_bf16)
+      reinterpret_cast<uint16_t *>(out)[m * (size_t)out_stride + n + e] = float_to_bf16(sum[e]);
+    else
+      reinterpret_cast<float *>(out)[m * (size_t)out_stride + n + e] = sum[e];
+  }
+}
+
+template <int S>
+static void launch_fold(const float *part, long long slice_stride, int M, int N, void *out, int out_bf16,
+                        int out_stride, hipStream_t stream) {
+  const size_t count = (size_t)M * (size_t)N;
+  if (N % 4 == 0)
+    hipLaunchKernelGGL((gemm_slice_fold_kernel<S, 4>), dim3((unsigned)((count / 4 + kFoldThreads - 1) / kFoldThreads)),
+                       dim3(kFoldThreads), 0, stream, part, slice_stride, M, N, out, out_bf16, out_stride);
   else
-    reinterpret_cast<float *>(out)[m * (size_t)out_stride + n] = sum;
+    hipLaunchKernelGGL((gemm_slice_fold_kernel<S, 1>), dim3((unsigned)((count + kFoldThreads - 1) / kFoldThreads)),
+                       dim3(kFoldThreads), 0, stream, part, slice_stride, M, N, out, out_bf16, out_stride);
 }
 
 // ---- forms and their choice -----------------------------------------------
@@ -800,25 +818,11 @@ extern "C" hipError_t igl_launch_gemm_q4(const void *act, int act_bf16, int act_
              : launch_out<false, false, false>(form, c_bf16, a, stream);
   }
   if (e != hipSuccess || plan.slices == 1) return e;
-  const size_t count = (size_t)M * (size_t)N;
-  const dim3 fold_grid((unsigned)((count + kFoldThreads - 1) / kFoldThreads));
   switch (plan.slices) {
-    case 2:
-      hipLaunchKernelGGL(gemm_slice_fold_kernel<2>, fold_grid, dim3(kFoldThreads), 0, stream, part,
-                         a.slice_stride, M, N, out, out_bf16, out_stride);
-      break;
-    case 4:
-      hipLaunchKernelGGL(gemm_slice_fold_kernel<4>, fold_grid, dim3(kFoldThreads), 0, stream, part,
-                         a.slice_stride, M, N, out, out_bf16, out_stride);
-      break;
-    case 8:
-      hipLaunchKernelGGL(gemm_slice_fold_kernel<8>, fold_grid, dim3(kFoldThreads), 0, stream, part,
-                         a.slice_stride, M, N, out, out_bf16, out_stride);
-      break;
-    default:
-      hipLaunchKernelGGL(gemm_slice_fold_kernel<16>, fold_grid, dim3(kFoldThreads), 0, stream, part,
-                         a.slice_stride, M, N, out, out_bf16, out_stride);
-      break;
+    case 2: launch_fold<2>(part, a.slice_stride, M, N, out, out_bf16, out_stride, stream); break;
+    case 4: launch_fold<4>(part, a.slice_stride, M, N, out, out_bf16, out_stride, stream); break;
+    case 8: launch_fold<8>(part, a.slice_stride, M, N, out, out_bf16, out_stride, stream); break;
+    default: return hipErrorInvalidValue;  // choose_plan takes 1, 2, 4 or 8 slices
   }
   return hipGetLastError();
 }
