@@ -586,9 +586,8 @@ static void launch_fold(const float *part, long long slice_stride, int M, int N,
 
 // ---- forms and their choice -----------------------------------------------
 
-// (WN, WM, KS, NB, MB) of the forms, widest tile first.  A launch takes the
-// first form whose tiles fill the 256 CUs and whose K split divides K, else
-// the last that divides K.
+// (WN, WM, KS, NB, MB) of the forms, widest tile first; choose_form below
+// says which a launch takes.
 struct FormShape {
   int wn, wm, ks, nb, mb, lim;
 };
@@ -600,8 +599,9 @@ constexpr FormShape kForms[] = {
                            // 8192 x 2048 at 64 lanes 19.8 -> 15.5 us against eight)
     {1, 1, 8, 1, 4, 160},  // 16 x 64, eight waves, K split in eight (2048 x 8192 at 64
                            // lanes: 26.5 us, against 29.0 split in four)
+    {2, 1, 2, 2, 4, 80},   // 64 x 64, four waves, K split in two, two workgroups a CU
 };
-constexpr int kFormCount = sizeof(kForms) / sizeof(kForms[0]);
+constexpr int kPairForm = 5;   // 64 x 64 tiles, two workgroups a CU
 constexpr int kSplitForm = 2;  // the form a K split across workgroups takes
 // Two-term activations: the same forms with the K split capped where the
 // stages would not fit.
@@ -611,20 +611,44 @@ constexpr FormShape kFormsLo[] = {
     {2, 1, 4, 2, 4, 160},
     {1, 1, 4, 2, 4, 160},
     {1, 1, 4, 1, 4, 160},
+    {2, 1, 2, 2, 4, 80},
 };
 
+// A launch takes, of the forms whose K split divides K:
+//   * the 256 x 256 or 128 x 128 form where its tiles fill the 256 CUs;
+//   * else, where the 64 x 64 tiles exceed one round of 256 (one workgroup a
+//     CU at 126 KB of stages), the same tiles in four-wave workgroups, two a
+//     CU at 74-75 KB;
+//   * else, of the 64 x 64, 32 x 64 and 16 x 64 forms, the one with the most
+//     tiles one round holds.
+// Against the widest form that filled the CUs (the choice before), replayed,
+// us, bf16 / fp32 activations: 8192 x 2048 at 256 lanes 30.2 / 41.5 -> 27.2 /
+// 35.1 (two a CU); 6144 x 1536 at 128 lanes 22.5 / 30.0 -> 15.0 / 18.7 (64 x 64,
+// 192 tiles, not 32 x 64 at 384), at 256 lanes 25.3 / 31.9 -> 21.7 / 26.7;
+// 12288 x 1536 at 64 lanes 22.4 / 29.8 -> 14.8 / 18.3.  The 128 x 128 form on
+// fewer tiles than CUs lost to the two-a-CU form (6144 x 1536 at 256 lanes,
+// 96 tiles: 28.5 against 21.7 us).
 static int choose_form(int M, int N, int K, int two_terms) {
   const FormShape *forms = two_terms ? kFormsLo : kForms;
-  int last = -1;
-  for (int f = 0; f < kFormCount; ++f) {
-    const FormShape &s = forms[f];
-    if (s.ks > 1 ? K % (kStepK * s.ks) != 0 : K % 32 != 0) continue;
-    const long tn = 16L * s.nb * s.wn, tm = 16L * s.mb * s.wm;
-    const long tiles = ((N + tn - 1) / tn) * ((M + tm - 1) / tm);
-    last = f;
-    if (tiles >= 256) return f;
+  auto divides = [&](int f) { return forms[f].ks > 1 ? K % (kStepK * forms[f].ks) == 0 : K % 32 == 0; };
+  auto tiles = [&](int f) {
+    const long tn = 16L * forms[f].nb * forms[f].wn, tm = 16L * forms[f].mb * forms[f].wm;
+    return ((N + tn - 1) / tn) * ((M + tm - 1) / tm);
+  };
+  for (int f = 0; f < 2; ++f)
+    if (divides(f) && tiles(f) >= 256) return f;
+  if (divides(kPairForm) && tiles(kPairForm) > 256) return kPairForm;
+  int best = -1;
+  for (int f = 2; f < 5; ++f) {
+    if (!divides(f)) continue;
+    const bool one_round = tiles(f) <= 256;
+    if (best < 0 || (one_round && tiles(f) > tiles(best)) || (!one_round && tiles(best) > 256 && tiles(f) < tiles(best)))
+      best = f;
   }
-  return last;
+  if (best >= 0) return best;
+  // K a multiple of 128 but not of 256 takes the two-a-CU form; other K (a
+  // multiple of 32) the 256 x 256 form, which pads K to whole steps
+  return divides(kPairForm) ? kPairForm : 0;
 }
 
 struct GemmPlan {
@@ -632,9 +656,10 @@ struct GemmPlan {
   int slices;  // K split across workgroups: 1, or 2 .. 16 slices folded by gemm_slice_fold_kernel
 };
 
-// Long rows (K >= 4096) where the walk above ends at a form narrower than
-// 64 x 64 (a few hundred lanes or less) take the 64 x 64 form instead, with K
-// split across workgroups into S = 1, 2, 4 or 8 slices: each workgroup then
+// Long rows (K >= 4096) where choose_form ends past the 128 x 128 form take the
+// 64 x 64 form in eight-wave workgroups (at 1024 lanes of 2048 x 8192 the
+// two-a-CU form was no faster: 79.0 against 77.0 us), with K split across
+// workgroups into S = 1, 2, 4 or 8 slices: each workgroup then
 // stages K / S of its lanes' activations instead of all of K, for S fp32
 // partial tiles written and folded.  S is the most slices whose workgroups
 // still run in one round on the 256 CUs (one a CU at this form's LDS): a
@@ -693,7 +718,8 @@ static hipError_t launch_pick(int form, const GemmCodesArgs &a, hipStream_t stre
     case 1: return launch_shape<1, LO, ROWGAIN, ZERO, C_BF16>(a, stream);
     case 2: return launch_shape<2, LO, ROWGAIN, ZERO, C_BF16>(a, stream);
     case 3: return launch_shape<3, LO, ROWGAIN, ZERO, C_BF16>(a, stream);
-    default: return launch_shape<4, LO, ROWGAIN, ZERO, C_BF16>(a, stream);
+    case 4: return launch_shape<4, LO, ROWGAIN, ZERO, C_BF16>(a, stream);
+    default: return launch_shape<5, LO, ROWGAIN, ZERO, C_BF16>(a, stream);
   }
 }
 

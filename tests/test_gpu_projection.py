@@ -233,8 +233,9 @@ def closed_form64_groups(codes, gains, act64, K, group):
 
 
 def gemm_form(backend, M, N, K, terms):
-    """The tiling form the GEMM launcher picks (0: 256 x 128 tiles .. 4: 16 x 64
-    tiles with an eight-way K split inside the workgroup)."""
+    """The tiling form the GEMM launcher picks (0: 256 x 256 tiles .. 4: 16 x 64
+    tiles with an eight-way K split inside the workgroup; 5: 64 x 64 tiles in
+    four-wave workgroups, two a CU)."""
     fn = backend.lib.igl_gemm_form
     fn.restype = ctypes.c_int
     fn.argtypes = [ctypes.c_int] * 4
@@ -295,9 +296,11 @@ def test_mat_mat_gemm_fp32(backend, N, K, M):
 
 
 # (M, N, K): cases that reach each tiling form, plus ragged tiles in M and N,
-# and K an odd number of 32-code groups (padded to a whole step with zeros).
+# K an odd number of 32-code groups (padded to a whole step with zeros), and K
+# a multiple of 128 but not 256 (the two-a-CU form's K split only).
 FORM_CASES = [(1024, 8192, 256), (2048, 2048, 512), (256, 4096, 1024), (64, 8192, 1024),
-              (64, 2048, 2048), (100, 1000, 1536), (333, 777, 192), (70, 300, 1056), (128, 256, 96)]
+              (64, 2048, 2048), (100, 1000, 1536), (333, 777, 192), (70, 300, 1056), (128, 256, 96),
+              (300, 5000, 384), (64, 1024, 640)]
 
 
 @pytest.mark.parametrize("terms", [1, 2])
@@ -332,7 +335,7 @@ def test_gemm_forms(backend, terms):
             print("rel_err", err)
             assert err <= 1e-3
         backend.detach(cp)
-    assert seen == {0, 1, 2, 3, 4}
+    assert seen == {0, 1, 2, 3, 4, 5}
 
 
 @pytest.mark.parametrize("case", ["zeros", "tiny", "huge", "rows", "mixed"])
