@@ -385,12 +385,15 @@ __host__ __device__ constexpr size_t gemv_dot_lds_bytes(int M, int units) {
   return (size_t)M * units * (kDigitPitch * 16 + 4);
 }
 
-template <int M, int R, int UPL, int GPT>
+// LR (one lane only): lanes as workgroup rows, grid row blockIdx.y being lane
+// blockIdx.y of the launch; a template constant, so the decode step's own
+// one-lane launches carry no offset arithmetic (1-2% of their time).
+template <int M, int R, int UPL, int GPT, bool LR = false>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q4_dot_kernel(GemvArgs a) {
+  static_assert(!LR || M == 1, "lanes as rows run the one-lane form");
   extern __shared__ uint4_t lds_dig[];
   __shared__ float red[4][R][M];
-  // lane_rows: grid row blockIdx.y is lane blockIdx.y of the launch
-  const size_t lane0 = M == 1 && a.lane_rows > 1 ? blockIdx.y : 0;
+  const size_t lane0 = LR ? blockIdx.y : 0;
   // wave-uniform indices in scalar registers; ksplit a power of two
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -2312,21 +2315,28 @@ static hipError_t gemv_zero_launch_bits(const GemvZeroArgs &a, hipStream_t strea
   return hipGetLastError();
 }
 
-template <int M, int R, int UPL, int GPT>
-static hipError_t gemv_dot_launch_gpt(const GemvArgs &a, hipStream_t stream) {
+template <int M, int R, int UPL, int GPT, bool LR>
+static hipError_t gemv_dot_launch_rows(const GemvArgs &a, hipStream_t stream) {
   const int tiles = (a.N + R - 1) / R;
   const int tiles_per_block = 4 / a.ksplit;
-  dim3 grid((tiles + tiles_per_block - 1) / tiles_per_block, M == 1 && a.lane_rows > 1 ? a.lane_rows : 1);
+  dim3 grid((tiles + tiles_per_block - 1) / tiles_per_block, LR ? a.lane_rows : 1);
   const size_t lds = gemv_dot_lds_bytes(M, a.K >> 5);
   static size_t lds_granted = 65536;  // launches above 64 KiB ask once
   if (lds > lds_granted) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q4_dot_kernel<M, R, UPL, GPT>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q4_dot_kernel<M, R, UPL, GPT, LR>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     lds_granted = lds;
   }
-  hipLaunchKernelGGL((gemv_q4_dot_kernel<M, R, UPL, GPT>), grid, dim3(kGemvThreads), lds, stream, a);
+  hipLaunchKernelGGL((gemv_q4_dot_kernel<M, R, UPL, GPT, LR>), grid, dim3(kGemvThreads), lds, stream, a);
   return hipGetLastError();
+}
+
+template <int M, int R, int UPL, int GPT>
+static hipError_t gemv_dot_launch_gpt(const GemvArgs &a, hipStream_t stream) {
+  if constexpr (M == 1)
+    if (a.lane_rows > 1) return gemv_dot_launch_rows<M, R, UPL, GPT, true>(a, stream);
+  return gemv_dot_launch_rows<M, R, UPL, GPT, false>(a, stream);
 }
 
 // Items a thread stages: M K / 8 groups over 256 threads, at most 8 (12 for
