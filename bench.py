@@ -45,7 +45,7 @@ ATTEND_COPIES = 40              # 40 x 8 MiB of key/value rings: past the MALL
 # WRITE_SIZE per dispatch, scaled by the factors a 256 MiB device copy gives.
 GEMV_M1_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4_m1_8192x2048.md")
 COPY_PROFILE = os.path.join(ROOT, "profiles", "copy_256mib_calibration.md")
-GEMV_M1_KERNEL = "gemv_q4_dot_kernel<1, 2, 1, 1>"
+GEMV_M1_KERNEL = "gemv_q4_dot_kernel<1, 2, 1, 1, false>"
 
 
 def profile_rows(path, kernel):
@@ -1093,7 +1093,7 @@ def main():
                                "M in {1,2,4,8}, fp32 activations, weights rotated over "
                                f"{COPIES} copies per shape",
                    "step_bytes": step_bytes},
-        "roofline": {"bound": "hbm", "kernel": "gemv_q4_dot_kernel<1, 2, 1, 1> 8192x2048 M=1",
+        "roofline": {"bound": "hbm", "kernel": "gemv_q4_dot_kernel<1, 2, 1, 1, false> 8192x2048 M=1",
                      "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": prof["traffic"] if prof else None,
