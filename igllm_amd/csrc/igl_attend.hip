@@ -652,6 +652,261 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
   }
 }
 
+// Wide launches (a prefill pass of kAttendWideLanes lanes or more): one
+// workgroup a lane and key/value head walks the lane's chunks of 64 positions
+// in order, each chunk's scores and blend computed as attend_split_kernel
+// computes them, and merges them into a running peak, total and blend in
+// registers (the online form of attend_fold_kernel's fold), so no partial goes
+// to memory and no fold launch follows.  The lanes give the launch its
+// workgroups, and the workgroups a CU holds (two at 512-dim heads, four at
+// 256) hide each other's loads: requesting the next chunk's bytes ahead in
+// registers instead held one a CU and was slower (2047 lanes, 2048 positions,
+// 512-dim heads: 955 against 667 us; a 512 window of 256-dim heads: 146
+// against 114 us).
+template <int HEAD, int FMT, bool QVEC>
+__global__ __launch_bounds__(256) void attend_rows_kernel(AttendArgs a) {
+  constexpr int C = 64;               // positions a chunk
+  constexpr int W = 4;                // waves
+  constexpr int PW = C / W;           // positions a wave scores
+  constexpr int DS = HEAD / W;        // dims a wave blends: 64 or 128
+  constexpr int S = HEAD / 32;        // k-steps of the score product
+  constexpr int QD = HEAD / 4;        // bytes of a key row one lane group reads
+  constexpr int QUADS = DS / 64;      // 64-dim groups of a wave's blend
+  constexpr int KS = C / 32;          // k-steps of the blend
+  constexpr int VP = DS + 8;          // staged value row pitch in bytes
+  constexpr int LPR = DS / 16;        // lanes that load one value row
+  constexpr int RPI = 64 / LPR;       // value rows one load instruction covers
+  constexpr int VL = C / RPI;         // value loads a lane issues
+
+  __shared__ half8_t qs[2][kAttendGroup][HEAD / 8];
+  __shared__ float ps[kAttendGroup][C];
+  __shared__ __attribute__((aligned(16))) float wm[W][kAttendGroup];
+  __shared__ __attribute__((aligned(16))) float wl[W][kAttendGroup];
+  __shared__ __attribute__((aligned(16))) uint8_t vs[W][C * VP];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int kv = blockIdx.y;
+  const int head0 = kv * kAttendGroup;
+  const int lane_id = blockIdx.z;
+  const int pos0 = a.place_dev ? *a.place_dev : a.place0;
+  const int pos = pos0 + lane_id;
+  const int span = a.window > 0 ? min(pos + 1, a.window) : pos + 1;
+  const int place_start = pos - span + 1;
+  const int blocks = (span + C - 1) / C;
+  const size_t kv_off = (size_t)kv * HEAD;
+  const int ring0 = place_start % a.cache_span;
+  auto ring_slot = [&](int t) {
+    const int slot = ring0 + t;
+    return slot >= a.cache_span ? slot - a.cache_span : slot;
+  };
+  // key row of chunk b: position b C + wave PW + n, bytes QD g .. QD g + QD - 1;
+  // value rows: lane / LPR + RPI i, dims wave DS + 16 (lane % LPR) .. + 15
+  auto load_keys = [&](int b, uint4_t (&kr)[QD / 16]) {
+    const int t = min(b * C + wave * PW + n, span - 1);
+    const uint4_t *row =
+        reinterpret_cast<const uint4_t *>(a.key_store + (size_t)ring_slot(t) * a.kv_width + kv_off + QD * g);
+#pragma unroll
+    for (int q = 0; q < QD / 16; ++q) kr[q] = __builtin_nontemporal_load(row + q);
+  };
+  auto load_values = [&](int b, uint4_t (&vr)[VL]) {
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      const int t = min(b * C + lane / LPR + RPI * i, span - 1);
+      vr[i] = __builtin_nontemporal_load(reinterpret_cast<const uint4_t *>(
+          a.value_store + (size_t)ring_slot(t) * a.kv_width + kv_off + wave * DS + 16 * (lane % LPR)));
+    }
+  };
+
+  // ---- the query, once: x = hi + lo in binary16
+  constexpr int kQItems = kAttendGroup * HEAD / 8 / 256;
+  {
+    float qf[kQItems][8];
+    const float *qb = a.query + (size_t)lane_id * a.q_stride + (size_t)head0 * HEAD;
+#pragma unroll
+    for (int i = 0; i < kQItems; ++i) {
+      const float *q = qb + 8 * (tid + 256 * i);
+      if (QVEC) {
+        const float4_t u = *reinterpret_cast<const float4_t *>(q);
+        const float4_t v = *reinterpret_cast<const float4_t *>(q + 4);
+        qf[i][0] = u.x; qf[i][1] = u.y; qf[i][2] = u.z; qf[i][3] = u.w;
+        qf[i][4] = v.x; qf[i][5] = v.y; qf[i][6] = v.z; qf[i][7] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[i][e] = q[e];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kQItems; ++i) {
+      half8_t hi8, lo8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const _Float16 hi = (_Float16)qf[i][e];
+        hi8[e] = hi;
+        lo8[e] = (_Float16)(qf[i][e] - (float)hi);
+      }
+      const int item = tid + 256 * i;
+      qs[0][item / (HEAD / 8)][item % (HEAD / 8)] = hi8;
+      qs[1][item / (HEAD / 8)][item % (HEAD / 8)] = lo8;
+    }
+  }
+
+  // running peak, total and blend of heads 4g + r (lanes g < 2), dims
+  // wave DS + 64 qd + 4 n + t
+  float run_m[4], run_l[4];
+  float4_t run_o[4 * QUADS];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    run_m[r] = -INFINITY;
+    run_l[r] = 0.0f;
+  }
+#pragma unroll
+  for (int t = 0; t < 4 * QUADS; ++t) run_o[t] = float4_t{0, 0, 0, 0};
+
+  uint4_t kr[QD / 16], vr[VL];
+  const int hh = n & 7;
+  for (int b = 0; b < blocks; ++b) {
+    __syncthreads();  // the query in LDS; the chunk before done with ps, wm, wl, vs
+    const int c0 = b * C;
+    // requested after the barrier: before it, 709 against 667 us (2047 lanes,
+    // 2048 positions, 512-dim heads)
+    load_keys(b, kr);
+    load_values(b, vr);
+    // scores of the wave's PW positions for the 8 heads, all dims
+    float sc[4], m_w[4];
+    {
+      float4_t sacc = float4_t{0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const half8_t qa = qs[n >> 3][n & 7][QD * g / 8 + s];
+        const uint4_t w = kr[s >> 1];
+        const half8_t kb = (s & 1) ? decode8<FMT>(w[2], w[3]) : decode8<FMT>(w[0], w[1]);
+        sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, kb, sacc, 0, 0, 0);
+      }
+      const bool valid = c0 + wave * PW + n < span;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float v = xsum32(sacc[r]);
+        sc[r] = valid ? v * a.key_scale : -INFINITY;
+        m_w[r] = row16_max(sc[r]);
+      }
+    }
+    {
+      float l_w[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = m_w[r] != -INFINITY && sc[r] != -INFINITY ? __expf(sc[r] - m_w[r]) : 0.0f;
+        l_w[r] = row16_sum(p);
+        if (g < 2) ps[4 * g + r][wave * PW + n] = p;
+      }
+      if (g < 2 && n == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          wm[wave][4 * g + r] = m_w[r];
+          wl[wave][4 * g + r] = l_w[r];
+        }
+      }
+    }
+    {
+      uint8_t *vw = vs[wave];
+#pragma unroll
+      for (int i = 0; i < VL; ++i) {
+        uint2_t *dst = reinterpret_cast<uint2_t *>(vw + (lane / LPR + RPI * i) * VP + 16 * (lane % LPR));
+        dst[0] = uint2_t{vr[i][0], vr[i][1]};
+        dst[1] = uint2_t{vr[i][2], vr[i][3]};
+      }
+    }
+    __syncthreads();
+    // blend of the wave's dims over the chunk, against the chunk's peak M
+    float M = wm[0][hh];
+#pragma unroll
+    for (int w = 1; w < W; ++w) M = fmaxf(M, wm[w][hh]);
+    float4_t o[4 * QUADS];
+#pragma unroll
+    for (int t = 0; t < 4 * QUADS; ++t) o[t] = float4_t{0, 0, 0, 0};
+    const uint8_t *vw = vs[wave];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int p0 = 32 * ks + 8 * g;
+      const float mw = wm[p0 / PW][hh];
+      const float f = mw != -INFINITY ? __expf(mw - M) : 0.0f;
+      half8_t pa;
+      {
+        const float *src = &ps[hh][p0];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float v = src[e] * f;
+          const _Float16 hi = (_Float16)v;
+          pa[e] = n >= 8 ? (_Float16)(v - (float)hi) : hi;
+        }
+      }
+#pragma unroll
+      for (int qd = 0; qd < QUADS; ++qd) {
+        uint32_t dw[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          dw[e] = *reinterpret_cast<const uint32_t *>(vw + (p0 + e) * VP + 64 * qd + 4 * n);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          uint32_t w[4];
+          const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + t) << 16) | (uint32_t)t;
+#pragma unroll
+          for (int pr = 0; pr < 4; ++pr)
+            w[pr] = decode_pair<FMT>(__builtin_amdgcn_perm(dw[2 * pr + 1], dw[2 * pr], sel));
+          o[4 * qd + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, __builtin_bit_cast(half8_t, w),
+                                                                 o[4 * qd + t], 0, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 4 * QUADS; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[t][r] = xsum32(o[t][r]);
+    // merge the chunk (peak Mh, total L, blend o) into the running state
+    if (g < 2) {
+      float4_t pk[W], tl[W];
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        pk[w] = *reinterpret_cast<const float4_t *>(&wm[w][4 * g]);
+        tl[w] = *reinterpret_cast<const float4_t *>(&wl[w][4 * g]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float Mh = pk[0][r];
+#pragma unroll
+        for (int w = 1; w < W; ++w) Mh = fmaxf(Mh, pk[w][r]);
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          const float e = pk[w][r] != -INFINITY ? __expf(pk[w][r] - Mh) : 0.0f;
+          L += tl[w][r] * e;
+        }
+        const float Mn = fmaxf(run_m[r], Mh);
+        const float keep = run_m[r] != -INFINITY ? __expf(run_m[r] - Mn) : 0.0f;
+        const float take = Mh != -INFINITY ? __expf(Mh - Mn) : 0.0f;
+        run_l[r] = run_l[r] * keep + L * take;
+#pragma unroll
+        for (int t = 0; t < 4 * QUADS; ++t) run_o[t][r] = run_o[t][r] * keep + o[t][r] * take;
+        run_m[r] = Mn;
+      }
+    }
+  }
+  if (g >= 2) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * g + r;
+    const float mul = run_l[r] > 0.0f ? a.value_scale * (1.0f / run_l[r]) : 0.0f;
+    float *dst = a.final_out + (size_t)lane_id * a.q_stride + (size_t)(head0 + h) * HEAD + wave * DS + 4 * n;
+#pragma unroll
+    for (int qd = 0; qd < QUADS; ++qd)
+      *reinterpret_cast<float4_t *>(dst + 64 * qd) = float4_t{run_o[4 * qd][r] * mul, run_o[4 * qd + 1][r] * mul,
+                                                              run_o[4 * qd + 2][r] * mul, run_o[4 * qd + 3][r] * mul};
+  }
+}
+
 // Folds chunk partials in one memory round trip.  A workgroup per (head, lane,
 // DIMS dims) of 256 threads: thread (d, s) loads, for up to PER chunks
 // c = s, s + 256/DIMS, ..., its dim's partial and the chunk's peak and total
@@ -761,6 +1016,14 @@ static void attend_launch(const AttendArgs &a, dim3 grid, bool qvec, hipStream_t
 }
 
 template <int HEAD, int FMT>
+static void attend_launch_rows(const AttendArgs &a, dim3 grid, bool qvec, hipStream_t stream) {
+  if (qvec)
+    hipLaunchKernelGGL((attend_rows_kernel<HEAD, FMT, true>), grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((attend_rows_kernel<HEAD, FMT, false>), grid, dim3(256), 0, stream, a);
+}
+
+template <int HEAD, int FMT>
 static void attend_launch_chunk(const AttendArgs &a, dim3 grid, int chunk, bool qvec, hipStream_t stream) {
   if (chunk == 32)
     attend_launch<HEAD, FMT, 32>(a, grid, qvec, stream);
@@ -815,6 +1078,22 @@ extern "C" hipError_t igl_launch_attend(const uint8_t *key_store, const uint8_t 
   a.k_code_scale = a.v_code_scale = a.eps = 0.0f;
   dim3 grid(chunks, kv_count, lanes);
   const bool qvec = (((uintptr_t)query) & 15u) == 0 && (q_stride & 3) == 0;
+  if (lanes >= kAttendWideLanes && chunks > 1) {
+    // a prefill pass: one workgroup a lane walks its chunks, no partials
+    a.final_out = blend_out;
+    const dim3 rows(1, kv_count, lanes);
+    if (head_size == 256 && fmt == 0)
+      attend_launch_rows<256, 0>(a, rows, qvec, stream);
+    else if (head_size == 256 && fmt == 1)
+      attend_launch_rows<256, 1>(a, rows, qvec, stream);
+    else if (head_size == 512 && fmt == 0)
+      attend_launch_rows<512, 0>(a, rows, qvec, stream);
+    else if (head_size == 512 && fmt == 1)
+      attend_launch_rows<512, 1>(a, rows, qvec, stream);
+    else
+      return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   if (head_size == 256 && fmt == 0)
     attend_launch_chunk<256, 0>(a, grid, chunk, qvec, stream);
   else if (head_size == 256 && fmt == 1)
