@@ -658,13 +658,14 @@ __global__ __launch_bounds__(256) void attend_split_kernel(AttendArgs a) {
 // computes them, and merges them into a running peak, total and blend in
 // registers (the online form of attend_fold_kernel's fold), so no partial goes
 // to memory and no fold launch follows.  The lanes give the launch its
-// workgroups, and the workgroups a CU holds (two at 512-dim heads, four at
-// 256) hide each other's loads: requesting the next chunk's bytes ahead in
-// registers instead held one a CU and was slower (2047 lanes, 2048 positions,
-// 512-dim heads: 955 against 667 us; a 512 window of 256-dim heads: 146
-// against 114 us).
+// workgroups, and the workgroups a CU holds hide each other's loads: three
+// at 512-dim heads (the registers capped for it, as many as their LDS
+// allows), four at 256.  Requesting the next chunk's bytes ahead in registers
+// instead held one a CU and was slower (2047 lanes, 2048 positions, 512-dim
+// heads: 955 against 667 us at two a CU, 596 at three; a 512 window of
+// 256-dim heads: 146 against 114, 109).
 template <int HEAD, int FMT, bool QVEC>
-__global__ __launch_bounds__(256) void attend_rows_kernel(AttendArgs a) {
+__global__ __launch_bounds__(256, 3) void attend_rows_kernel(AttendArgs a) {
   constexpr int C = 64;               // positions a chunk
   constexpr int W = 4;                // waves
   constexpr int PW = C / W;           // positions a wave scores
