@@ -692,7 +692,9 @@ __global__ __launch_bounds__(256, 3) void attend_rows_kernel(AttendArgs a) {
   const int n = lane & 15;
   const int kv = blockIdx.y;
   const int head0 = kv * kAttendGroup;
-  const int lane_id = blockIdx.z;
+  // the last lanes, with the most chunks, first: the workgroups are handed
+  // out in grid order, and the long ones would otherwise start last
+  const int lane_id = (int)gridDim.z - 1 - (int)blockIdx.z;
   const int pos0 = a.place_dev ? *a.place_dev : a.place0;
   const int pos = pos0 + lane_id;
   const int span = a.window > 0 ? min(pos + 1, a.window) : pos + 1;
