@@ -1247,6 +1247,9 @@ extern "C" size_t igl_attend_prep_work_floats(int place_bound, int window, int h
 extern "C" size_t igl_attend_work_floats(int place0, int window, int lanes, int head_count,
                                          int head_size) {
   const size_t blocks = (size_t)attend_blocks(place0, window, lanes);
+  // a wide launch of more than one chunk merges its chunks in registers
+  // (attend_rows_kernel): no partials
+  if (lanes >= kAttendWideLanes && blocks > 1) return 0;
   return (size_t)lanes * blocks * (size_t)head_count * ((size_t)head_size + 2);
 }
 
@@ -1255,7 +1258,9 @@ extern "C" size_t igl_attend_work_floats(int place0, int window, int lanes, int 
 // count is not monotonic in the span: chunks are 32 positions up to
 // kAttendShortSpan and 64 beyond, so a span just under kAttendShortSpan has
 // more chunks than one just over it.  The largest count of each regime is
-// taken (launches of many lanes take 64-position chunks: fewer).
+// taken.  Launches of kAttendWideLanes lanes and more keep no partials (one
+// chunk: the blend written directly; more: merged in registers), so the most
+// lanes that keep partials is kAttendWideLanes - 1.
 extern "C" size_t igl_attend_work_floats_limit(int span_limit, int lanes, int head_count,
                                                int head_size) {
   if (span_limit < 1 || lanes < 1) return 0;
@@ -1263,10 +1268,11 @@ extern "C" size_t igl_attend_work_floats_limit(int span_limit, int lanes, int he
   const int b_short = attend_blocks(short_top - 1, 0, 1);
   const int b_long = attend_blocks(span_limit - 1, 0, 1);
   const size_t blocks = (size_t)(b_short > b_long ? b_short : b_long);
+  const size_t narrow = (size_t)(lanes < kAttendWideLanes ? lanes : kAttendWideLanes - 1);
   // a prepared launch of up to kAttendPrepLanes lanes (a decode step, a small
   // block) needs blocks + 1 slots a lane: its new positions' partial
   const size_t prep = (size_t)(lanes < kAttendPrepLanes ? lanes : kAttendPrepLanes) * (blocks + 1);
-  const size_t slots = (size_t)lanes * blocks > prep ? (size_t)lanes * blocks : prep;
+  const size_t slots = narrow * blocks > prep ? narrow * blocks : prep;
   return slots * (size_t)head_count * ((size_t)head_size + 2);
 }
 
