@@ -93,8 +93,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decode leg")
-    ap.add_argument("--kernel", choices=["gemv", "gemv8", "gemm", "attend", "copy", "head2", "real", "calib",
-                                         "readfloor", "decode", "guess"],
+    ap.add_argument("--kernel", choices=["gemv", "gemv8", "gemm", "attend", "attend_rows", "copy", "head2", "real",
+                                         "calib", "readfloor", "decode", "guess"],
                     help="run one kernel's workload alone in a loop (for rocprofv3) and exit")
     ap.add_argument("--lanes", type=int, default=2048, help="--kernel gemm: the lane count M")
     ap.add_argument("--shape", type=int, default=0, choices=[0, 1],
@@ -106,7 +106,9 @@ def kernel_loop(be, name, reps, lanes=2048, shape=0):
     """One kernel's workload alone, for counter runs: the decode GEMV (M=1,
     8192x2048, rotated copies), the M=8 GEMV, the prefill GEMM (M lanes, either
     shape; M=2048 on 8192x2048 by default), the
-    L=16384 attention, a 256 MiB device copy that calibrates FETCH_SIZE and
+    L=16384 attention, the prefill attention (2047 lanes over a 2048-position
+    ring of 512-dim heads, then a 512-position window of 256-dim heads, e4m3,
+    alternating), a 256 MiB device copy that calibrates FETCH_SIZE and
     WRITE_SIZE against a known byte count, the 2-bit 262144x1536 head and the
     bf16 8960x1536 real plane at M=1 (rotated copies), the calibrated
     prefill (M=2048, 8192x2048 4-bit, one gain a row), or the read floor (the
@@ -236,6 +238,33 @@ def kernel_loop(be, name, reps, lanes=2048, shape=0):
         be.mark()
         us = be.marks_ms() * 1e3 / reps
         print(json.dumps({"kernel": "attend", "L": L, "copies": copies, "avg_us": round(us, 2)}))
+        return
+    if name == "attend_rows":
+        lanes, rng = 2047, np.random.default_rng(2)
+        cases = []
+        for window, head in ((0, 512), (512, 256)):
+            span = window + lanes if window else lanes + 1
+            kb = be.upload(rng.integers(0, 120, size=(span, head), dtype=np.uint8))
+            vb = be.upload(rng.integers(0, 120, size=(span, head), dtype=np.uint8))
+            q = be.upload(rng.normal(size=(lanes, 8 * head)).astype(np.float32))
+            o = be.alloc(lanes * 8 * head * 4)
+            cases.append((window, head, span, kb, vb, q, o))
+
+        def launch(c):
+            window, head, span, kb, vb, q, o = c
+            code = be.lib.igl_attend_lanes_dev(ctypes.byref(be.desk), kb.ptr, vb.ptr, 0, 0.02, 0.02, span, 1, 8,
+                                               head, q.ptr, 8 * head, 1, window, lanes, 1.0 / 16, o.ptr)
+            if code != 0:
+                raise RuntimeError("igl_attend_lanes_dev failed: %d" % code)
+        for c in cases:
+            launch(c)
+        be.sync()
+        be.mark()
+        for i in range(reps):
+            launch(cases[i % 2])
+        be.mark()
+        us = be.marks_ms() * 1e3 / reps
+        print(json.dumps({"kernel": "attend_rows", "lanes": lanes, "avg_us_per_launch": round(us, 2)}))
         return
     if name == "decode":
         decode_loop(be, reps)
