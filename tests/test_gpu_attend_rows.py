@@ -38,16 +38,18 @@ def _bind(lib):
     return fn
 
 
-@pytest.mark.parametrize("lanes,window,place0,head,fmt,kv_count", [
-    (64, 0, 65, 512, 0, 1),       # a global layer, two and three chunks
-    (100, 0, 37, 256, 1, 1),      # int8 ring, ragged last chunk
-    (300, 512, 1000, 256, 0, 1),  # a sliding layer, windows cut mid-chunk
-    (130, 512, 2000, 256, 0, 2),  # two key/value heads, the ring wrapped
-    (257, 0, 1500, 512, 0, 1),    # a global layer at 1500-1756 positions
+@pytest.mark.parametrize("lanes,window,place0,head,fmt,kv_count,pad", [
+    (64, 0, 65, 512, 0, 1, 0),       # a global layer, two and three chunks
+    (100, 0, 37, 256, 1, 1, 0),      # int8 ring, ragged last chunk
+    (300, 512, 1000, 256, 0, 1, 0),  # a sliding layer, windows cut mid-chunk
+    (130, 512, 2000, 256, 0, 2, 0),  # two key/value heads, the ring wrapped
+    (257, 0, 1500, 512, 0, 1, 0),    # a global layer at 1500-1756 positions
+    (300, 512, 100, 256, 0, 1, 0),   # a sliding layer whose first spans are shorter than the window
+    (96, 0, 200, 256, 1, 1, 1),      # lanes one float off 16-byte alignment (scalar query loads)
 ])
-def test_wide_attention(backend, lanes, window, place0, head, fmt, kv_count):
-    print("case wide attention lanes=%d window=%d place0=%d head=%d fmt=%d kv=%d" % (
-        lanes, window, place0, head, fmt, kv_count), flush=True)
+def test_wide_attention(backend, lanes, window, place0, head, fmt, kv_count, pad):
+    print("case wide attention lanes=%d window=%d place0=%d head=%d fmt=%d kv=%d pad=%d" % (
+        lanes, window, place0, head, fmt, kv_count, pad), flush=True)
     lib = backend.lib
     fn = _bind(lib)
     stream = lib.igl_desk_stream(ctypes.byref(backend.desk))
@@ -60,12 +62,14 @@ def test_wide_attention(backend, lanes, window, place0, head, fmt, kv_count):
                         (1.0 if fmt == 1 else 0.05), scale, fmt)
     v_bytes = ol.encode(np.clip(r.normal(size=(cache_span, kv_width)), -4, 4).astype(np.float32) *
                         (1.0 if fmt == 1 else 0.05), scale, fmt)
-    q_stride = kv_count * HEADS * head
+    q_stride = kv_count * HEADS * head + pad
     query = r.normal(size=(lanes, q_stride)).astype(np.float32)
     score_scale = 1.0 / 16.0
     dk, dv, dq = backend.upload(k_bytes), backend.upload(v_bytes), backend.upload(query)
     wide = backend.alloc(lanes * q_stride * 4)
     narrow = backend.alloc(lanes * q_stride * 4)
+    for b in (wide, narrow):  # the pad columns compare equal
+        b.put(np.zeros(lanes * q_stride, np.float32))
     work_floats = max([lib.igl_attend_work_floats(place0 + at, window, min(NARROW, lanes - at), kv_count * HEADS,
                                                   head) for at in range(0, lanes, NARROW)] + [1])
     work = backend.alloc(work_floats * 4)
